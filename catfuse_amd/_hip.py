@@ -1,0 +1,99 @@
+"""ctypes binding of the gfx950 C-ABI library ``_lib/libcatfuse_amd.so``.
+
+Every entry point takes raw device pointers, int64 sizes and the HIP stream
+(torch's current stream), returns a ``hipError_t`` as int, never allocates
+and never synchronises.  A non-zero return raises ``RuntimeError``.  There is
+no CPU or PyTorch fallback: if the library is missing the import of any
+kernel wrapper raises, so a GPU run cannot silently take another path.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import c_double, c_float, c_int, c_int64, c_void_p, c_char_p
+
+import torch
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libcatfuse_amd.so")
+
+# name -> argtypes (all return c_int unless listed in _RESTYPES)
+_P = c_void_p
+_I = c_int64
+_SIGNATURES = {
+    "cf_version": [],
+    "cf_error_string": [c_int],
+    "cf_probe_mfma_layout": [_P, _P, _P, _P],
+    "cf_lif_multistep": [_P, _P, _P, _P, c_int, _P, _P, c_int, _P, _I, _I, _I, _I,
+                         c_double, c_double, c_double, c_int, c_int, _P],
+    "cf_avgpool2x2_lif": [_P, _P, _P, c_int, _P, _I, _I, _I, _I,
+                          c_double, c_double, c_double, c_int, c_int, _P],
+    "cf_pack_input": [_P, _I, _I, _I, _I, _I, _P, _P, c_int, c_float, _P, _P, _P],
+    "cf_route_from_nnz": [_P, _I, c_double, _P, _P],
+    "cf_zero_counter": [_P, _P],
+    "cf_prescan_tiles": [_P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P],
+    "cf_pack_conv_weights": [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P],
+    "cf_conv_mfma": [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I, c_double,
+                     _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
+                     c_int, c_double, c_double, c_double, c_int, c_int, _P],
+    "cf_conv_direct": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
+                       _I, _I, _I, c_int, c_double, c_double, c_double, c_int, c_int, _P],
+}
+_RESTYPES = {"cf_error_string": c_char_p}
+
+_lib = None
+
+
+class _Lib:
+    def __init__(self, handle):
+        self._h = handle
+        for name, args in _SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.argtypes = args
+            fn.restype = _RESTYPES.get(name, c_int)
+            setattr(self, name, fn)
+
+
+def library_path() -> str:
+    return _LIB_PATH
+
+
+def lib() -> _Lib:
+    """Load (once) and return the bound library; raises if it is not built."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(
+                f"catfuse_amd HIP library not found at {_LIB_PATH}; build it with "
+                "`python -m catfuse_amd.build` (hipcc --offload-arch=gfx950)")
+        _lib = _Lib(ctypes.CDLL(_LIB_PATH, mode=ctypes.RTLD_LOCAL))
+    return _lib
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != 0:
+        msg = lib().cf_error_string(rc)
+        msg = msg.decode() if isinstance(msg, bytes) else str(msg)
+        raise RuntimeError(f"catfuse_amd {what} failed: hipError {rc} ({msg})")
+
+
+def ptr(t) -> int | None:
+    """Device pointer of a tensor (None passes a null pointer)."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def stream(device=None) -> int:
+    """hipStream_t of torch's current stream on the tensor's device."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_gpu_tensor(t: torch.Tensor, name: str, dtype=torch.float32) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor")
+    if not t.is_cuda:
+        raise RuntimeError(f"{name} must be a GPU tensor (catfuse_amd has no CPU path)")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise RuntimeError(f"{name} must be contiguous")

@@ -1,0 +1,70 @@
+// Shared device helpers for the catfuse_amd gfx950 kernels.
+//
+// Numerics contract (all kernels): built with -ffp-contract=off and
+// correctly-rounded fp32 division, so the LIF recurrence below rounds every
+// operation exactly as SpikingJelly's eval-mode multi-step torch path does
+// on the CPU (see lif_charge / lif_fire_reset).
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#define CF_API extern "C" __attribute__((visibility("default")))
+
+// Route words written on the device by the pack/route kernels and read by
+// the conv kernels.  Values mirror catfuse's SpatialBackend decision:
+//   ZERO   <=> count_nonzero(x) == 0                      (StaticZero)
+//   SPARSE <=> 1 - nnz/numel > 0.7 (evaluated in double)  (SparseFlow)
+//   DENSE  otherwise                                       (DenseKeep)
+enum { CF_ROUTE_ZERO = 0, CF_ROUTE_SPARSE = 1, CF_ROUTE_DENSE = 2 };
+
+// Status word bits (sticky, device side; read by catfuse_amd.runtime).
+enum {
+  CF_STATUS_INEXACT_FP16 = 1u,   // an input assumed fp16-exact was not
+};
+
+// LIF parameters passed by value to every kernel with a LIF epilogue.
+struct LifParams {
+  float tau;
+  float v_th;
+  float v_reset;     // ignored when hard == 0 (soft reset)
+  float decay_coef;  // (float)(1 - 1/tau) computed in double on the host;
+                     // used only by the soft-reset, no-decay-input charge
+  int hard;          // 1: hard reset to v_reset; 0: soft reset v -= v_th
+  int decay_input;   // 1: v += (x - (v - v_reset)) / tau
+};
+
+// Charge step, SpikingJelly eval-mode op order.
+//   hard, decay_input    : v = v + (x - (v - v_reset)) / tau
+//   hard, no decay_input : v = v - (v - v_reset) / tau + x
+//   soft, decay_input    : v = v + (x - v) / tau
+//   soft, no decay_input : v = v * (1 - 1/tau) + x
+__device__ __forceinline__ float lif_charge(float v, float x, const LifParams& p) {
+  if (p.hard) {
+    if (p.decay_input) return v + (x - (v - p.v_reset)) / p.tau;
+    return (v - (v - p.v_reset) / p.tau) + x;
+  }
+  if (p.decay_input) return v + (x - v) / p.tau;
+  return v * p.decay_coef + x;
+}
+
+// Fire + reset.  Returns the spike (0/1) and updates v in place.
+//   hard: v = v_reset * s + (1 - s) * v
+//   soft: v = v - s * v_th
+__device__ __forceinline__ float lif_fire_reset(float& v, const LifParams& p) {
+  const float s = (v >= p.v_th) ? 1.0f : 0.0f;
+  if (p.hard) v = p.v_reset * s + (1.0f - s) * v;
+  else v = v - s * p.v_th;
+  return s;
+}
+
+__device__ __forceinline__ float lif_initial_v(const LifParams& p) {
+  return p.hard ? p.v_reset : 0.0f;
+}
+
+// Host: LIF parameter block from SpikingJelly-level (double) parameters.
+LifParams cf_make_lif_params(double tau, double v_th, double v_reset, int hard, int decay_input);
+
+// Number of dispatches one grid dimension may hold.
+static inline unsigned cf_blocks(int64_t n, int per_block) {
+  return (unsigned)((n + per_block - 1) / per_block);
+}

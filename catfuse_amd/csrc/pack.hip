@@ -1,0 +1,138 @@
+// Input staging for the MFMA conv path, plus the per-pixel half of the
+// SparseFlow prescan and the StaticZero/SparseFlow/DenseKeep route count.
+//
+// One pass over the fp32 NCHW boundary tensor x[NB][C][H][W] produces:
+//   xp   fp16 NHWC x[NB][H][W][Cp] (channels C..Cp-1 zero) — MFMA B operand
+//   act  uint32 [NB][H][W]: bit g set iff |x[c]| > thr for some c in
+//        channel group g (channels g*GS .. g*GS+GS-1)
+//   nnz  += count_nonzero(x)   (64-bit device counter)
+//   status |= CF_STATUS_INEXACT_FP16 if some x is not exactly representable
+//        in fp16 (the MFMA path multiplies fp16 x by split fp32 weights, so
+//        exactness of x is what keeps the contraction fp32-faithful)
+// The group-OR per pixel is the channel reduction of the reference prescan
+// (catfuse/sparseflow/prescan.py:32-45 _groupwise_amax_last_dim, then
+// `> threshold` at :184); the spatial (receptive field, tile) reduction is in
+// prescan.hip.  HBM traffic: 4 B read + 2 B (xp) + 4/C B (act) per element.
+#include "cf_common.h"
+
+namespace {
+
+constexpr int PX = 64;   // pixels per block
+constexpr int CC = 32;   // channels per chunk
+
+__global__ __launch_bounds__(256) void pack_kernel(
+    const float* __restrict__ x, int64_t C, int64_t HW, int64_t Cp,
+    _Float16* __restrict__ xp, uint32_t* __restrict__ act, int gs, float thr,
+    unsigned long long* __restrict__ nnz, uint32_t* __restrict__ status) {
+  __shared__ _Float16 tile[CC][PX + 2];
+  __shared__ uint32_t bits_sh[4][PX];
+  __shared__ unsigned int cnt_sh;
+  __shared__ unsigned int inexact_sh;
+  const int tid = threadIdx.x;
+  const int64_t n = blockIdx.y;
+  const int64_t hw0 = (int64_t)blockIdx.x * PX;
+  const int px = tid % PX;       // pixel handled in the load phase
+  const int cs = tid / PX;       // 0..3 channel sub-lane in the load phase
+  const bool pvalid = (hw0 + px) < HW;
+  if (tid == 0) { cnt_sh = 0; inexact_sh = 0; }
+  uint32_t mybits = 0;
+  unsigned int mycnt = 0;
+  bool myinexact = false;
+  const float* xn = x + n * C * HW + hw0 + px;
+  __syncthreads();
+  for (int64_t c0 = 0; c0 < Cp; c0 += CC) {
+#pragma unroll
+    for (int i = 0; i < CC / 4; ++i) {
+      const int cl = cs + 4 * i;
+      const int64_t c = c0 + cl;
+      float v = 0.0f;
+      if (pvalid && c < C) v = xn[c * HW];
+      const _Float16 h = (_Float16)v;
+      myinexact |= ((float)h != v);
+      mycnt += (v != 0.0f) ? 1u : 0u;
+      if (fabsf(v) > thr && c < C) mybits |= 1u << (unsigned)(c / gs);
+      tile[cl][px] = h;
+    }
+    __syncthreads();
+    if (xp) {
+      // write phase: 4 threads per pixel, 8 channels (16 B) each
+      const int wp = tid / 4, part = tid % 4;
+      if (hw0 + wp < HW) {
+        _Float16 o[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = tile[part * 8 + j][wp];
+        *reinterpret_cast<uint4*>(xp + ((n * HW + hw0 + wp) * Cp + c0 + part * 8)) =
+            *reinterpret_cast<const uint4*>(o);
+      }
+    }
+    __syncthreads();
+  }
+  if (act) {
+    bits_sh[cs][px] = mybits;
+    __syncthreads();
+    if (tid < PX && pvalid)
+      act[n * HW + hw0 + tid] = bits_sh[0][tid] | bits_sh[1][tid] | bits_sh[2][tid] | bits_sh[3][tid];
+  }
+  if (nnz) {
+    // wave-level reduction, then one shared atomic per wave
+    unsigned int c = mycnt;
+    for (int off = 32; off > 0; off >>= 1) c += __shfl_xor(c, off, 64);
+    if ((tid & 63) == 0) atomicAdd(&cnt_sh, c);
+  }
+  if (myinexact) atomicOr(&inexact_sh, 1u);
+  __syncthreads();
+  if (tid == 0) {
+    if (nnz && cnt_sh) atomicAdd(nnz, (unsigned long long)cnt_sh);
+    if (status && inexact_sh) atomicOr(status, (uint32_t)CF_STATUS_INEXACT_FP16);
+  }
+}
+
+__global__ void route_kernel(const unsigned long long* __restrict__ nnz, int64_t numel,
+                             double sparse_threshold, int32_t* __restrict__ route) {
+  if (threadIdx.x == 0 && blockIdx.x == 0) {
+    const unsigned long long k = *nnz;
+    int r;
+    if (k == 0) r = CF_ROUTE_ZERO;
+    else if (1.0 - (double)k / (double)numel > sparse_threshold) r = CF_ROUTE_SPARSE;
+    else r = CF_ROUTE_DENSE;
+    *route = r;
+  }
+}
+
+__global__ void zero_u64(unsigned long long* p) { *p = 0ull; }
+
+}  // namespace
+
+CF_API int cf_pack_input(const float* x, int64_t NB, int64_t C, int64_t H, int64_t W,
+                         int64_t Cp, void* xp, uint32_t* act, int group_size, float threshold,
+                         unsigned long long* nnz, uint32_t* status, void* stream) {
+  if (!x || NB < 0 || C <= 0 || H <= 0 || W <= 0) return (int)hipErrorInvalidValue;
+  if (xp && (Cp < C || Cp % CC != 0)) return (int)hipErrorInvalidValue;
+  if (!xp) Cp = ((C + CC - 1) / CC) * CC;
+  if (act && (group_size <= 0 || (C + group_size - 1) / group_size > 32)) return (int)hipErrorInvalidValue;
+  if (group_size <= 0) group_size = 32;
+  if (NB == 0) return 0;
+  if (NB > 65535) return (int)hipErrorInvalidValue;
+  const int64_t HW = H * W;
+  dim3 grid(cf_blocks(HW, PX), (unsigned)NB);
+  hipLaunchKernelGGL(pack_kernel, grid, dim3(256), 0, (hipStream_t)stream, x, C, HW, Cp,
+                     (_Float16*)xp, act, group_size, threshold, nnz, status);
+  return (int)hipGetLastError();
+}
+
+// Route word from the nonzero count, exactly the host formula of
+// catfuse/sparseflow/ops/st_fusion_conv_bn_lif.py:510-524 evaluated in double.
+CF_API int cf_route_from_nnz(const unsigned long long* nnz, int64_t numel,
+                             double sparse_threshold, int32_t* route, void* stream) {
+  if (!nnz || !route || numel <= 0) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(route_kernel, dim3(1), dim3(64), 0, (hipStream_t)stream, nnz, numel,
+                     sparse_threshold, route);
+  return (int)hipGetLastError();
+}
+
+// Clears a 64-bit device counter with a kernel (graph-capture safe: no memset node).
+CF_API int cf_zero_counter(unsigned long long* p, void* stream) {
+  if (!p) return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(zero_u64, dim3(1), dim3(1), 0, (hipStream_t)stream, p);
+  return (int)hipGetLastError();
+}

@@ -1,0 +1,339 @@
+"""Launch layer: torch tensors in, gfx950 C-ABI calls out.
+
+Each function validates shapes/dtypes/devices on the host, allocates its
+outputs with torch (device memory plumbing) and launches on torch's current
+HIP stream.  Nothing here computes on the CPU and nothing falls back: a
+missing library or a non-GPU tensor raises.
+
+`ConvLIFRunner` owns the per-layer device state of a fused Conv->BN->LIF:
+packed fp16 hi/lo weights, the folded epilogue affine, the fp16 NHWC staging
+buffer, prescan buffers and the nonzero counter.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from catfuse_amd import _hip
+from catfuse_amd._hip import check, ptr, require_gpu_tensor
+
+EPI_LIF, EPI_Z = 0, 1
+ROUTE_ZERO, ROUTE_SPARSE, ROUTE_DENSE = 0, 1, 2
+STATUS_INEXACT_FP16 = 1
+
+_status_words: dict = {}
+
+
+def status_word(device) -> torch.Tensor:
+    """Per-device sticky status word (int32[1]) OR-ed by the pack kernel."""
+    dev = torch.device(device)
+    key = dev.index if dev.index is not None else torch.cuda.current_device()
+    t = _status_words.get(key)
+    if t is None:
+        t = torch.zeros(1, dtype=torch.int32, device=torch.device("cuda", key))
+        _status_words[key] = t
+    return t
+
+
+def read_status(device=None) -> int:
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    return int(status_word(dev).item())
+
+
+def clear_status(device=None) -> None:
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else device
+    status_word(dev).zero_()
+
+
+def _lif_args(tau, v_threshold, v_reset, decay_input):
+    hard = v_reset is not None
+    return (float(tau), float(v_threshold), float(v_reset) if hard else 0.0, int(hard),
+            int(bool(decay_input)))
+
+
+# ---------------------------------------------------------------------------
+# LIF family
+# ---------------------------------------------------------------------------
+
+def lif_multistep(z: torch.Tensor, v_in: Optional[torch.Tensor] = None, *, tau=2.0,
+                  v_threshold=1.0, v_reset=0.0, decay_input=True, mode=0,
+                  z2: Optional[torch.Tensor] = None, scale: Optional[torch.Tensor] = None,
+                  shift: Optional[torch.Tensor] = None, channels: int = 1, hw: int = 1,
+                  spike_dtype=torch.float32, want_v_out: bool = True):
+    """z [T, ...] -> (spikes [T, ...], v_out [...] or None) on the GPU."""
+    require_gpu_tensor(z, "z")
+    T = z.shape[0]
+    N = z[0].numel() if T > 0 else 0
+    if z2 is not None:
+        require_gpu_tensor(z2, "z2")
+        if z2.shape != z.shape:
+            raise ValueError(f"z2 shape {tuple(z2.shape)} != z shape {tuple(z.shape)}")
+    for name, t in (("scale", scale), ("shift", shift)):
+        if t is not None:
+            require_gpu_tensor(t, name)
+            if t.numel() != channels:
+                raise ValueError(f"{name} has {t.numel()} entries, expected {channels}")
+    if v_in is not None:
+        require_gpu_tensor(v_in, "v_in")
+        if v_in.numel() != N:
+            raise ValueError(f"v_in has {v_in.numel()} elements, expected {N}")
+    if mode in (1, 2, 4) and (N % (channels * hw) != 0):
+        raise ValueError("N must be a multiple of channels*hw for per-channel modes")
+    sd = {torch.float32: 0, torch.uint8: 1}.get(spike_dtype)
+    if sd is None:
+        raise TypeError("spike_dtype must be float32 or uint8")
+    spikes = torch.empty(z.shape, dtype=spike_dtype, device=z.device)
+    v_out = torch.empty(z.shape[1:], dtype=torch.float32, device=z.device) if want_v_out else None
+    rc = _hip.lib().cf_lif_multistep(ptr(z), ptr(z2), ptr(scale), ptr(shift), int(mode), ptr(v_in),
+                                     ptr(spikes), sd, ptr(v_out), T, N, int(channels), int(hw),
+                                     *_lif_args(tau, v_threshold, v_reset, decay_input),
+                                     _hip.stream(z.device))
+    check(rc, "cf_lif_multistep")
+    return spikes, v_out
+
+
+def avgpool2x2_lif(x: torch.Tensor, v_in: Optional[torch.Tensor] = None, *, tau=2.0,
+                   v_threshold=1.0, v_reset=0.0, decay_input=True, spike_dtype=torch.float32):
+    """x [T, B, C, H, W] -> (spikes [T, B, C, H//2, W//2], v_out)."""
+    require_gpu_tensor(x, "x")
+    if x.dim() != 5:
+        raise ValueError("x must be [T, B, C, H, W]")
+    T, B, C, H, W = x.shape
+    if H < 2 or W < 2:
+        raise ValueError("AvgPool2x2 needs H, W >= 2")
+    Ho, Wo = H // 2, W // 2
+    if v_in is not None:
+        require_gpu_tensor(v_in, "v_in")
+        if v_in.numel() != B * C * Ho * Wo:
+            raise ValueError("v_in has the wrong size")
+    sd = {torch.float32: 0, torch.uint8: 1}[spike_dtype]
+    spikes = torch.empty((T, B, C, Ho, Wo), dtype=spike_dtype, device=x.device)
+    v_out = torch.empty((B, C, Ho, Wo), dtype=torch.float32, device=x.device)
+    rc = _hip.lib().cf_avgpool2x2_lif(ptr(x), ptr(v_in), ptr(spikes), sd, ptr(v_out), T, B * C, H,
+                                      W, *_lif_args(tau, v_threshold, v_reset, decay_input),
+                                      _hip.stream(x.device))
+    check(rc, "cf_avgpool2x2_lif")
+    return spikes, v_out
+
+
+# ---------------------------------------------------------------------------
+# Prescan
+# ---------------------------------------------------------------------------
+
+def pad32(c: int) -> int:
+    return ((c + 31) // 32) * 32
+
+
+def pack_input(x4: torch.Tensor, *, cp: Optional[int] = None, want_xp=True, group_size=0,
+               threshold=1e-6, nnz: Optional[torch.Tensor] = None, act_out=None, xp_out=None,
+               status: Optional[torch.Tensor] = None):
+    """x4 [NB, C, H, W] fp32 -> (xp fp16 [NB, H, W, Cp] | None, act int32 [NB, H, W] | None)."""
+    require_gpu_tensor(x4, "x")
+    NB, C, H, W = x4.shape
+    cp = pad32(C) if cp is None else cp
+    xp = None
+    if want_xp:
+        xp = xp_out if xp_out is not None else torch.empty((NB, H, W, cp), dtype=torch.float16,
+                                                          device=x4.device)
+        if xp.shape != (NB, H, W, cp) or xp.dtype != torch.float16:
+            raise ValueError("xp_out has the wrong shape/dtype")
+    act = None
+    if group_size > 0:
+        act = act_out if act_out is not None else torch.empty((NB, H, W), dtype=torch.int32,
+                                                              device=x4.device)
+    rc = _hip.lib().cf_pack_input(ptr(x4), NB, C, H, W, cp, ptr(xp), ptr(act), int(group_size),
+                                  float(threshold), ptr(nnz), ptr(status), _hip.stream(x4.device))
+    check(rc, "cf_pack_input")
+    return xp, act
+
+
+def prescan_tiles(act: torch.Tensor, H: int, W: int, H_out: int, W_out: int, kernel_size: int,
+                  stride: int, padding: int, block_h: int, block_w: int, num_groups: int,
+                  ag_mask_out=None, tile_class_out=None):
+    NB = act.shape[0]
+    GH, GW = -(-H_out // block_h), -(-W_out // block_w)
+    n = NB * GH * GW
+    ag = ag_mask_out if ag_mask_out is not None else torch.empty(n, dtype=torch.int32,
+                                                                 device=act.device)
+    tc = tile_class_out if tile_class_out is not None else torch.empty(n, dtype=torch.int32,
+                                                                      device=act.device)
+    if ag.numel() < n or tc.numel() < n:
+        raise ValueError("prescan output buffers are too small")
+    rc = _hip.lib().cf_prescan_tiles(ptr(act), NB, H, W, H_out, W_out, kernel_size, stride,
+                                     padding, block_h, block_w, num_groups, ptr(ag), ptr(tc),
+                                     _hip.stream(act.device))
+    check(rc, "cf_prescan_tiles")
+    return tc[:n], ag[:n]
+
+
+def zero_counter(c: torch.Tensor) -> None:
+    check(_hip.lib().cf_zero_counter(ptr(c), _hip.stream(c.device)), "cf_zero_counter")
+
+
+def route_from_nnz(nnz: torch.Tensor, numel: int, sparse_threshold: float,
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    r = out if out is not None else torch.empty(1, dtype=torch.int32, device=nnz.device)
+    check(_hip.lib().cf_route_from_nnz(ptr(nnz), int(numel), float(sparse_threshold), ptr(r),
+                                       _hip.stream(nnz.device)), "cf_route_from_nnz")
+    return r
+
+
+# ---------------------------------------------------------------------------
+# Conv -> BN -> LIF
+# ---------------------------------------------------------------------------
+
+class ConvLIFRunner:
+    """Device state + launches for one fused Conv -> (BN) -> LIF layer.
+
+    weight [Cout, Cin, KH, KW] fp32; bn_scale/bn_shift [Cout] (folded eval
+    BN, optional); bias [Cout] (optional).  Call `refresh()` after changing
+    any of them.
+    """
+
+    def __init__(self, weight, bn_scale, bn_shift, bias, stride, padding, tau, v_threshold,
+                 v_reset, decay_input):
+        self.weight = weight
+        self.bn_scale = bn_scale
+        self.bn_shift = bn_shift
+        self.bias = bias
+        self.stride = int(stride)
+        self.padding = int(padding)
+        self.lif = _lif_args(tau, v_threshold, v_reset, decay_input)
+        self.Cout, self.Cin, self.KH, self.KW = (int(s) for s in weight.shape)
+        self.Cp = pad32(self.Cin)
+        self.Coutp = ((self.Cout + 63) // 64) * 64
+        self._packed_key = None
+        self.w_packed = self.alpha = self.beta = None
+        self.alpha_direct = self.beta_direct = None
+        self._ws = {}
+
+    def refresh(self):
+        self._packed_key = None
+
+    def _ensure_packed(self, device):
+        key = (device, self.weight.data_ptr(), getattr(self.weight, "_version", 0),
+               None if self.bn_scale is None else (self.bn_scale.data_ptr(), self.bn_scale._version),
+               None if self.bn_shift is None else (self.bn_shift.data_ptr(), self.bn_shift._version),
+               None if self.bias is None else (self.bias.data_ptr(), self.bias._version))
+        if key == self._packed_key:
+            return
+        w = self.weight.detach().float().contiguous()
+        bs = None if self.bn_scale is None else self.bn_scale.detach().float().contiguous()
+        bh = None if self.bn_shift is None else self.bn_shift.detach().float().contiguous()
+        bi = None if self.bias is None else self.bias.detach().float().contiguous()
+        for name, t in (("weight", w), ("bn_scale", bs), ("bn_shift", bh), ("bias", bi)):
+            if t is not None:
+                require_gpu_tensor(t, name)
+        st = _hip.stream(device)
+        self.w_packed = torch.empty((2, self.Coutp, self.KH * self.KW, self.Cp),
+                                    dtype=torch.float16, device=device)
+        self.alpha = torch.empty(self.Coutp, dtype=torch.float32, device=device)
+        self.beta = torch.empty(self.Coutp, dtype=torch.float32, device=device)
+        check(_hip.lib().cf_pack_conv_weights(ptr(w), self.Cout, self.Cin, self.KH, self.KW,
+                                              self.Coutp, self.Cp, ptr(bs), ptr(bh), ptr(bi),
+                                              ptr(self.w_packed), ptr(self.alpha),
+                                              ptr(self.beta), st), "cf_pack_conv_weights")
+        self.alpha_direct = torch.empty(self.Coutp, dtype=torch.float32, device=device)
+        self.beta_direct = torch.empty(self.Coutp, dtype=torch.float32, device=device)
+        check(_hip.lib().cf_pack_conv_weights(ptr(w), self.Cout, self.Cin, self.KH, self.KW,
+                                              self.Coutp, self.Cp, ptr(bs), ptr(bh), ptr(bi),
+                                              None, ptr(self.alpha_direct),
+                                              ptr(self.beta_direct), st), "cf_pack_conv_weights")
+        self._w_f32 = w
+        self._packed_key = key
+
+    def out_hw(self, H, W):
+        return ((H + 2 * self.padding - self.KH) // self.stride + 1,
+                (W + 2 * self.padding - self.KW) // self.stride + 1)
+
+    def workspace(self, key, shape, dtype, device):
+        t = self._ws.get(key)
+        if t is None or t.shape != torch.Size(shape) or t.dtype != dtype or t.device != device:
+            t = torch.empty(shape, dtype=dtype, device=device)
+            self._ws[key] = t
+        return t
+
+    def run_mfma(self, x: torch.Tensor, v_in=None, *, epilogue=EPI_LIF, want_v_out=True,
+                 identity=None, sparse=None, sparse_threshold=0.7, static_zero=True):
+        """x [T, B, Cin, H, W] fp32 (values exact in fp16).  sparse: None for
+        flat dense tiles, or a dict with block_h, block_w, group_size to run
+        the prescan and SparseFlow chunk skipping.  Returns (out, v_out)."""
+        require_gpu_tensor(x, "x")
+        T, B, C, H, W = x.shape
+        if C != self.Cin:
+            raise ValueError(f"expected {self.Cin} input channels, got {C}")
+        dev = x.device
+        self._ensure_packed(dev)
+        Ho, Wo = self.out_hw(H, W)
+        st = status_word(dev)
+        nnz = None
+        if static_zero or sparse is not None:
+            nnz = self.workspace("nnz", (1,), torch.int64, dev)
+            zero_counter(nnz)
+        gs = sparse["group_size"] if sparse is not None else 0
+        xp = self.workspace("xp", (T * B, H, W, self.Cp), torch.float16, dev)
+        act = (self.workspace("act", (T * B, H, W), torch.int32, dev) if sparse is not None
+               else None)
+        pack_input(x.reshape(T * B, C, H, W), cp=self.Cp, group_size=gs, nnz=nnz, act_out=act,
+                   xp_out=xp, status=st)
+        ag = None
+        th = tw = 0
+        if sparse is not None:
+            th, tw = sparse["block_h"], sparse["block_w"]
+            GH, GW = -(-Ho // th), -(-Wo // tw)
+            n = T * B * GH * GW
+            ag_buf = self.workspace("ag", (n,), torch.int32, dev)
+            tc_buf = self.workspace("tc", (n,), torch.int32, dev)
+            G = -(-self.Cin // gs)
+            prescan_tiles(act, H, W, Ho, Wo, self.KH, self.stride, self.padding, th, tw, G,
+                          ag_buf, tc_buf)
+            ag = ag_buf
+        if identity is not None:
+            require_gpu_tensor(identity, "identity")
+            if identity.shape != (T, B, self.Cout, Ho, Wo):
+                raise ValueError("identity shape mismatch")
+        if v_in is not None:
+            require_gpu_tensor(v_in, "v_in")
+            if v_in.numel() != B * self.Cout * Ho * Wo:
+                raise ValueError("v_in has the wrong size")
+        out = torch.empty((T, B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
+        v_out = (torch.empty((B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
+                 if (epilogue == EPI_LIF and want_v_out) else None)
+        rc = _hip.lib().cf_conv_mfma(
+            ptr(xp), ptr(self.w_packed), ptr(self.alpha), ptr(self.beta), ptr(v_in), ptr(v_out),
+            ptr(out), ptr(identity), ptr(ag), ptr(nnz), x.numel(), float(sparse_threshold),
+            T, B, self.Cp, self.Cout, self.Coutp, H, W, Ho, Wo, self.KH, self.KW, self.stride,
+            self.padding, B, th, tw, gs, int(epilogue), *self.lif, _hip.stream(dev))
+        check(rc, "cf_conv_mfma")
+        self.last_nnz = nnz
+        self.last_tiles = None if ag is None else (tc_buf, ag)
+        return out, v_out
+
+    def run_direct(self, x: torch.Tensor, v_in=None, *, epilogue=EPI_LIF, want_v_out=True):
+        """Analog-input path (fp32 VALU).  x may have a stride-0 time axis
+        (direct encoding), in which case the conv is evaluated once."""
+        if not x.is_cuda or x.dtype != torch.float32:
+            raise RuntimeError("x must be a float32 GPU tensor")
+        T, B, C, H, W = x.shape
+        dev = x.device
+        self._ensure_packed(dev)
+        if x.stride(0) == 0 and x[0].is_contiguous():
+            tstride = 0
+            xb = x[0]
+        else:
+            x = x.contiguous()
+            tstride = B
+            xb = x
+        Ho, Wo = self.out_hw(H, W)
+        if v_in is not None:
+            require_gpu_tensor(v_in, "v_in")
+        out = torch.empty((T, B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
+        v_out = (torch.empty((B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
+                 if (epilogue == EPI_LIF and want_v_out) else None)
+        rc = _hip.lib().cf_conv_direct(
+            ptr(xb), ptr(self._w_f32), ptr(self.alpha_direct), ptr(self.beta_direct), ptr(v_in),
+            ptr(v_out), ptr(out), T, B, C, self.Cout, H, W, Ho, Wo, self.KH, self.KW,
+            self.stride, self.padding, tstride, int(epilogue), *self.lif, _hip.stream(dev))
+        check(rc, "cf_conv_direct")
+        return out, v_out

@@ -1,0 +1,363 @@
+"""Minimal SpikingJelly-compatible modules and model builders.
+
+SpikingJelly (the reference's model zoo, pinned at 0.0.0.0.14) is not
+installed in this environment.  This module provides the subset of its
+``activation_based`` API that CATFuse-SF consumes, with the same attribute
+names, so ``catfuse_amd.optimize`` can be exercised on the same module trees
+SpikingJelly builds:
+
+* ``LIFNode`` (tau, decay_input, v_threshold, v_reset, step_mode, v, reset())
+  running SpikingJelly's eval-mode multi-step recurrence in torch;
+* multi-step layer wrappers ``Conv2d``, ``BatchNorm2d``, ``MaxPool2d``,
+  ``AvgPool2d``, ``AdaptiveAvgPool2d``, ``Linear``, ``Flatten`` (``[T, B, ...]``
+  inputs are flattened to ``[T*B, ...]`` as SpikingJelly's
+  ``SeqToANNContainer`` does);
+* ``functional.reset_net`` / ``functional.set_step_mode``;
+* ``sew_resnet18`` (BasicBlock with conv{1,2}/bn{1,2}/sn{1,2}/downsample/
+  downsample_sn/cnf, forward as catfuse/patterns.py:676-689 describes) and
+  ``spiking_vgg11_bn`` with AvgPool->LIF at the pools.
+
+These modules are the *unfused input* to the optimizer (the model the user
+would have built with SpikingJelly); the fused path never calls them.  When
+the real SpikingJelly is importable, ``catfuse_amd.substitute`` accepts its
+modules as well (duck-typed on class name and attributes).
+"""
+from __future__ import annotations
+
+import math
+from types import SimpleNamespace
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+
+class MemoryModule(nn.Module):
+    """Stateful module with ``reset()`` and a ``step_mode`` ('s' or 'm')."""
+
+    def __init__(self):
+        super().__init__()
+        self.step_mode = "s"
+
+    def reset(self):
+        pass
+
+
+class LIFNode(MemoryModule):
+    """Leaky integrate-and-fire neuron, SpikingJelly semantics (eval path).
+
+    Multi-step charge/fire/reset per step t (SpikingJelly 0.0.0.0.14
+    ``LIFNode.jit_eval_multi_step_forward_*``):
+      hard reset, decay_input : v = v + (x - (v - v_reset)) / tau
+      hard reset, no decay    : v = v - (v - v_reset) / tau + x
+      soft reset, decay_input : v = v + (x - v) / tau
+      soft reset, no decay    : v = v * (1 - 1/tau) + x
+      spike = (v >= v_threshold)
+      hard: v = v_reset * spike + (1 - spike) * v ;  soft: v = v - spike * v_threshold
+    """
+
+    def __init__(self, tau: float = 2.0, decay_input: bool = True, v_threshold: float = 1.0,
+                 v_reset=0.0, surrogate_function=None, detach_reset: bool = False,
+                 step_mode: str = "s", backend: str = "torch", store_v_seq: bool = False):
+        super().__init__()
+        self.tau = float(tau)
+        self.decay_input = bool(decay_input)
+        self.v_threshold = float(v_threshold)
+        self.v_reset = None if v_reset is None else float(v_reset)
+        self.surrogate_function = surrogate_function
+        self.detach_reset = detach_reset
+        self.step_mode = step_mode
+        self.backend = backend
+        self.store_v_seq = store_v_seq
+        self.v = 0.0 if self.v_reset is None else self.v_reset
+
+    def reset(self):
+        self.v = 0.0 if self.v_reset is None else self.v_reset
+
+    def _charge(self, v, x):
+        if self.v_reset is not None:
+            if self.decay_input:
+                return v + (x - (v - self.v_reset)) / self.tau
+            return v - (v - self.v_reset) / self.tau + x
+        if self.decay_input:
+            return v + (x - v) / self.tau
+        return v * (1.0 - 1.0 / self.tau) + x
+
+    def _fire_reset(self, v):
+        spike = (v >= self.v_threshold).to(v.dtype)
+        if self.v_reset is not None:
+            v = self.v_reset * spike + (1.0 - spike) * v
+        else:
+            v = v - spike * self.v_threshold
+        return spike, v
+
+    def _init_v(self, x):
+        if not isinstance(self.v, torch.Tensor) or self.v.shape != x.shape or self.v.device != x.device:
+            fill = float(self.v) if not isinstance(self.v, torch.Tensor) else (
+                0.0 if self.v_reset is None else self.v_reset)
+            self.v = torch.full_like(x, fill)
+
+    def forward(self, x):
+        if self.step_mode == "m":
+            self._init_v(x[0])
+            v = self.v
+            out = torch.empty_like(x)
+            for t in range(x.shape[0]):
+                v = self._charge(v, x[t])
+                out[t], v = self._fire_reset(v)
+            self.v = v
+            return out
+        self._init_v(x)
+        v = self._charge(self.v, x)
+        s, self.v = self._fire_reset(v)
+        return s
+
+    def extra_repr(self):
+        return (f"v_threshold={self.v_threshold}, v_reset={self.v_reset}, tau={self.tau}, "
+                f"decay_input={self.decay_input}, step_mode={self.step_mode}")
+
+
+class _SeqMixin:
+    """Flatten [T, B, ...] -> [T*B, ...] around a per-sample module in 'm' mode."""
+
+    def _seq(self, fn, x):
+        if getattr(self, "step_mode", "s") == "m":
+            T, B = x.shape[0], x.shape[1]
+            y = fn(x.flatten(0, 1))
+            return y.reshape(T, B, *y.shape[1:])
+        return fn(x)
+
+
+class Conv2d(nn.Conv2d, _SeqMixin):
+    def __init__(self, *args, step_mode: str = "s", **kw):
+        super().__init__(*args, **kw)
+        self.step_mode = step_mode
+
+    def forward(self, x):
+        return self._seq(super().forward, x)
+
+
+class BatchNorm2d(nn.BatchNorm2d, _SeqMixin):
+    def __init__(self, *args, step_mode: str = "s", **kw):
+        super().__init__(*args, **kw)
+        self.step_mode = step_mode
+
+    def forward(self, x):
+        return self._seq(super().forward, x)
+
+
+class MaxPool2d(nn.MaxPool2d, _SeqMixin):
+    def __init__(self, *args, step_mode: str = "s", **kw):
+        super().__init__(*args, **kw)
+        self.step_mode = step_mode
+
+    def forward(self, x):
+        return self._seq(super().forward, x)
+
+
+class AvgPool2d(nn.AvgPool2d, _SeqMixin):
+    def __init__(self, *args, step_mode: str = "s", **kw):
+        super().__init__(*args, **kw)
+        self.step_mode = step_mode
+
+    def forward(self, x):
+        return self._seq(super().forward, x)
+
+
+class AdaptiveAvgPool2d(nn.AdaptiveAvgPool2d, _SeqMixin):
+    def __init__(self, *args, step_mode: str = "s", **kw):
+        super().__init__(*args, **kw)
+        self.step_mode = step_mode
+
+    def forward(self, x):
+        return self._seq(super().forward, x)
+
+
+class Linear(nn.Linear):
+    def __init__(self, *args, step_mode: str = "s", **kw):
+        super().__init__(*args, **kw)
+        self.step_mode = step_mode
+
+
+class Flatten(nn.Flatten):
+    """Flatten all dims after the batch dims ([T, B, ...] -> [T, B, F] in 'm')."""
+
+    def __init__(self, start_dim: int = 1, end_dim: int = -1, step_mode: str = "s"):
+        super().__init__(start_dim, end_dim)
+        self.step_mode = step_mode
+
+    def forward(self, x):
+        if self.step_mode == "m":
+            return torch.flatten(x, 2)
+        return super().forward(x)
+
+
+def _reset_net(net: nn.Module):
+    for m in net.modules():
+        if hasattr(m, "reset") and callable(m.reset):
+            m.reset()
+
+
+def _set_step_mode(net: nn.Module, step_mode: str):
+    for m in net.modules():
+        if hasattr(m, "step_mode"):
+            m.step_mode = step_mode
+
+
+functional = SimpleNamespace(reset_net=_reset_net, set_step_mode=_set_step_mode)
+neuron = SimpleNamespace(LIFNode=LIFNode)
+layer = SimpleNamespace(Conv2d=Conv2d, BatchNorm2d=BatchNorm2d, MaxPool2d=MaxPool2d,
+                        AvgPool2d=AvgPool2d, AdaptiveAvgPool2d=AdaptiveAvgPool2d,
+                        Linear=Linear, Flatten=Flatten)
+
+
+# ---------------------------------------------------------------------------
+# SEW-ResNet (connect function applied after both LIFs)
+# ---------------------------------------------------------------------------
+
+def sew_function(x, y, cnf: str):
+    if cnf == "ADD":
+        return x + y
+    if cnf == "AND":
+        return x * y
+    if cnf == "IAND":
+        return x * (1.0 - y)
+    raise NotImplementedError(cnf)
+
+
+class BasicBlock(nn.Module):
+    """SEW-ResNet BasicBlock (attribute names as SpikingJelly's sew_resnet)."""
+    expansion = 1
+
+    def __init__(self, inplanes, planes, stride=1, downsample=None, cnf: str = "ADD",
+                 spiking_neuron=LIFNode, **kwargs):
+        super().__init__()
+        self.conv1 = Conv2d(inplanes, planes, 3, stride, 1, bias=False)
+        self.bn1 = BatchNorm2d(planes)
+        self.sn1 = spiking_neuron(**kwargs)
+        self.conv2 = Conv2d(planes, planes, 3, 1, 1, bias=False)
+        self.bn2 = BatchNorm2d(planes)
+        self.sn2 = spiking_neuron(**kwargs)
+        self.downsample = downsample
+        if downsample is not None:
+            self.downsample_sn = spiking_neuron(**kwargs)
+        self.stride = stride
+        self.cnf = cnf
+
+    def forward(self, x):
+        identity = x
+        out = self.sn1(self.bn1(self.conv1(x)))
+        out = self.sn2(self.bn2(self.conv2(out)))
+        if self.downsample is not None:
+            identity = self.downsample_sn(self.downsample(x))
+        return sew_function(identity, out, self.cnf)
+
+
+class SEWResNet(nn.Module):
+    def __init__(self, layers=(2, 2, 2, 2), num_classes=1000, cnf="ADD", spiking_neuron=LIFNode,
+                 **kwargs):
+        super().__init__()
+        self.inplanes = 64
+        self.conv1 = Conv2d(3, 64, 7, 2, 3, bias=False)
+        self.bn1 = BatchNorm2d(64)
+        self.sn1 = spiking_neuron(**kwargs)
+        self.maxpool = MaxPool2d(3, 2, 1)
+        self.layer1 = self._make_layer(64, layers[0], 1, cnf, spiking_neuron, kwargs)
+        self.layer2 = self._make_layer(128, layers[1], 2, cnf, spiking_neuron, kwargs)
+        self.layer3 = self._make_layer(256, layers[2], 2, cnf, spiking_neuron, kwargs)
+        self.layer4 = self._make_layer(512, layers[3], 2, cnf, spiking_neuron, kwargs)
+        self.avgpool = AdaptiveAvgPool2d((1, 1))
+        self.fc = Linear(512, num_classes)
+        for m in self.modules():
+            if isinstance(m, nn.Conv2d):
+                nn.init.kaiming_normal_(m.weight, mode="fan_out", nonlinearity="relu")
+
+    def _make_layer(self, planes, blocks, stride, cnf, sn, kwargs):
+        downsample = None
+        if stride != 1 or self.inplanes != planes:
+            downsample = nn.Sequential(Conv2d(self.inplanes, planes, 1, stride, bias=False),
+                                       BatchNorm2d(planes))
+        layers = [BasicBlock(self.inplanes, planes, stride, downsample, cnf, sn, **kwargs)]
+        self.inplanes = planes
+        for _ in range(1, blocks):
+            layers.append(BasicBlock(self.inplanes, planes, 1, None, cnf, sn, **kwargs))
+        return nn.Sequential(*layers)
+
+    def forward(self, x):
+        x = self.maxpool(self.sn1(self.bn1(self.conv1(x))))
+        x = self.layer4(self.layer3(self.layer2(self.layer1(x))))
+        x = self.avgpool(x)
+        x = torch.flatten(x, 2) if self.avgpool.step_mode == "m" else torch.flatten(x, 1)
+        return self.fc(x)
+
+
+def sew_resnet18(num_classes=1000, cnf="ADD", spiking_neuron=LIFNode, **kwargs):
+    return SEWResNet((2, 2, 2, 2), num_classes, cnf, spiking_neuron, **kwargs)
+
+
+# ---------------------------------------------------------------------------
+# Spiking VGG-11-BN with AvgPool -> LIF at the pools
+# ---------------------------------------------------------------------------
+
+VGG11_CFG = (64, "M", 128, "M", 256, 256, "M", 512, 512, "M", 512, 512, "M")
+
+
+class SpikingVGG(nn.Module):
+    """features: Conv-BN-LIF per conv, except that the conv before a pool is
+    followed by Conv-BN-AvgPool(2)-LIF; classifier: Linear-LIF, Linear-LIF,
+    Linear (CIFAR-size input, 32x32 -> 1x1 after five pools)."""
+
+    def __init__(self, cfg=VGG11_CFG, num_classes=10, spiking_neuron=LIFNode, **kwargs):
+        super().__init__()
+        mods, cin = [], 3
+        for i, c in enumerate(cfg):
+            if c == "M":
+                continue
+            pool_next = i + 1 < len(cfg) and cfg[i + 1] == "M"
+            mods += [Conv2d(cin, c, 3, 1, 1, bias=False), BatchNorm2d(c)]
+            if pool_next:
+                mods.append(AvgPool2d(2, 2))
+            mods.append(spiking_neuron(**kwargs))
+            cin = c
+        self.features = nn.Sequential(*mods)
+        self.flatten = Flatten()
+        self.classifier = nn.Sequential(
+            Linear(512, 4096), spiking_neuron(**kwargs),
+            Linear(4096, 4096), spiking_neuron(**kwargs),
+            Linear(4096, num_classes))
+        for m in self.modules():
+            if isinstance(m, nn.Conv2d):
+                nn.init.kaiming_normal_(m.weight, mode="fan_out", nonlinearity="relu")
+
+    def forward(self, x):
+        return self.classifier(self.flatten(self.features(x)))
+
+
+def spiking_vgg11_bn(num_classes=10, spiking_neuron=LIFNode, **kwargs):
+    return SpikingVGG(VGG11_CFG, num_classes, spiking_neuron, **kwargs)
+
+
+def randomize_bn(model: nn.Module, generator: torch.Generator) -> None:
+    """BN running statistics and affine parameters as the benchmark configs
+    specify: running_mean ~ N(0, 0.1), running_var ~ U(0.5, 1.5),
+    gamma ~ U(0.8, 1.2), beta ~ N(0, 0.1)."""
+    with torch.no_grad():
+        for m in model.modules():
+            if isinstance(m, nn.BatchNorm2d):
+                C = m.num_features
+                m.running_mean.copy_(torch.randn(C, generator=generator) * 0.1)
+                m.running_var.copy_(torch.rand(C, generator=generator) + 0.5)
+                m.weight.copy_(torch.rand(C, generator=generator) * 0.4 + 0.8)
+                m.bias.copy_(torch.randn(C, generator=generator) * 0.1)
+
+
+def kaiming_init(model: nn.Module, generator: torch.Generator) -> None:
+    """Seeded kaiming-normal conv/linear weights (fan_out, relu gain)."""
+    with torch.no_grad():
+        for m in model.modules():
+            if isinstance(m, (nn.Conv2d, nn.Linear)):
+                fan_out = m.weight.shape[0] * (m.weight[0][0].numel() if m.weight.dim() > 2 else 1)
+                std = math.sqrt(2.0 / fan_out)
+                m.weight.copy_(torch.randn(m.weight.shape, generator=generator) * std)
+                if m.bias is not None:
+                    m.bias.zero_()

@@ -1,0 +1,156 @@
+/* catfuse_amd — C-ABI of the gfx950 HIP kernels behind the CATFuse-SF
+ * spatio-temporal fused SNN inference path.
+ *
+ * Conventions for every entry point:
+ *   - device pointers are raw HIP device addresses; "nullable" pointers may
+ *     be NULL;
+ *   - sizes are int64, LIF parameters are passed as the SpikingJelly-level
+ *     doubles (rounded to fp32 inside exactly as torch rounds a Python float
+ *     against an fp32 tensor);
+ *   - `stream` is a hipStream_t; every call is asynchronous on it, never
+ *     allocates, never synchronises;
+ *   - the return value is a hipError_t (0 = success; hipErrorInvalidValue
+ *     for rejected arguments, checked on the host before any launch).
+ * Tensor layouts: "NCHW" = [T][B][C][H][W] fp32 boundary tensors (the
+ * layout SpikingJelly multi-step modules exchange); "NHWC16" = fp16
+ * [images][H][W][Cp] staging of conv inputs.
+ *
+ * Each declaration names the reference interface it replaces
+ * (paths relative to the hpcyhr/CATFuse source tree).
+ */
+#ifndef CATFUSE_AMD_H
+#define CATFUSE_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Route words written by cf_route_from_nnz. */
+#define CF_ROUTE_ZERO 0   /* StaticZero: count_nonzero(x) == 0          */
+#define CF_ROUTE_SPARSE 1 /* SparseFlow: 1 - nnz/numel > threshold      */
+#define CF_ROUTE_DENSE 2  /* DenseKeep                                  */
+
+/* Status bits OR-ed into the device status word by cf_pack_input. */
+#define CF_STATUS_INEXACT_FP16 1u
+
+int cf_version(void);
+const char* cf_error_string(int code);
+
+/* Multi-step LIF over T steps with the membrane potential kept on chip.
+ * Replaces catfuse/sparseflow/lif_seq_kernel.py:51-90 lif_sequential
+ * (mode 0), catfuse/kernels/partial_fusion_conv_bn_lif_impl.py:157-189
+ * _launch_bn_lif_state_carry (mode 1),
+ * catfuse/kernels/partial_fusion_conv_bn_add_lif_impl.py:125-158 (mode 2),
+ * catfuse/kernels/add_lif.py:112-151 triton_add_lif_blocked (mode 3),
+ * benchmarks/add_bn_lif_min.py:131-226 run_fusion (mode 4).
+ *   input current per step and neuron n (channel c = (n / HW) % C):
+ *     0: z          1: z*scale[c] + shift[c]       2: (z*scale[c] + shift[c]) + z2
+ *     3: z + z2     4: (z + z2)*scale[c] + shift[c]
+ *   z, z2: [T][N] fp32; v_in, v_out: [N] fp32 (nullable; NULL v_in starts at
+ *   v_reset for hard reset, 0 for soft); spike: [T][N] fp32 (spike_dtype 0)
+ *   or uint8 (spike_dtype 1).  hard_reset = 0 means soft reset (v_reset
+ *   None in SpikingJelly). */
+int cf_lif_multistep(const float* z, const float* z2, const float* scale, const float* shift,
+                     int mode, const float* v_in, void* spike, int spike_dtype, float* v_out,
+                     int64_t T, int64_t N, int64_t C, int64_t HW, double tau, double v_th,
+                     double v_reset, int hard_reset, int decay_input, void* stream);
+
+/* AvgPool2d(2,2) -> LIF over T steps.  Replaces
+ * catfuse/kernels/avgpool_lif.py:61-190 (avgpool_lif_block_kernel /
+ * triton_avgpool_lif_blocked).  x: [T][NC][H][W]; spike: [T][NC][H/2][W/2];
+ * v_in/v_out: [NC][H/2][W/2] (nullable). */
+int cf_avgpool2x2_lif(const float* x, const float* v_in, void* spike, int spike_dtype,
+                      float* v_out, int64_t T, int64_t NC, int64_t H, int64_t W, double tau,
+                      double v_th, double v_reset, int hard_reset, int decay_input, void* stream);
+
+/* One pass over a conv input x [NB][C][H][W] fp32: fp16 NHWC staging
+ * (xp: [NB][H][W][Cp], Cp % 32 == 0, nullable), per-pixel channel-group
+ * activity bits (act: uint32 [NB][H][W], bit g <=> some |x| > threshold in
+ * channels [g*group_size, (g+1)*group_size), nullable), nonzero count
+ * (nnz += count_nonzero(x), nullable) and exactness status (nullable).
+ * Replaces the channel half of catfuse/sparseflow/prescan.py:32-54,153-189
+ * and the count_nonzero of
+ * catfuse/sparseflow/ops/st_fusion_conv_bn_lif.py:512-514. */
+int cf_pack_input(const float* x, int64_t NB, int64_t C, int64_t H, int64_t W, int64_t Cp,
+                  void* xp, uint32_t* act, int group_size, float threshold,
+                  unsigned long long* nnz, uint32_t* status, void* stream);
+
+/* route = ZERO if nnz == 0, SPARSE if 1 - nnz/numel > sparse_threshold (in
+ * double), else DENSE.  Replaces the host decision at
+ * catfuse/sparseflow/ops/st_fusion_conv_bn_lif.py:510-524. */
+int cf_route_from_nnz(const unsigned long long* nnz, int64_t numel, double sparse_threshold,
+                      int32_t* route, void* stream);
+
+/* *p = 0 by a one-thread kernel (graph-capture safe). */
+int cf_zero_counter(unsigned long long* p, void* stream);
+
+/* Prescan tile reduction: ag_mask / tile_class int32 [NB*GH*GW] from the
+ * activity bits of cf_pack_input, GH = ceil(Ho/block_h), GW =
+ * ceil(Wo/block_w).  Replaces catfuse/sparseflow/fast_prescan_v2.py:92-137
+ * fast_spike_prescan_2d_v2 and prescan.py:153-189 _prescan_2d_impl
+ * (bit-exact contract: same masks and classes). */
+int cf_prescan_tiles(const uint32_t* act, int64_t NB, int64_t H, int64_t W, int64_t Ho,
+                     int64_t Wo, int64_t kernel_size, int64_t stride, int64_t padding,
+                     int64_t block_h, int64_t block_w, int64_t num_groups, int32_t* ag_mask,
+                     int32_t* tile_class, void* stream);
+
+/* Conv weight staging for cf_conv_mfma: fp32 w [Cout][Cin][KH][KW] ->
+ * fp16 hi/lo limbs [2][Coutp][KH*KW][Cp] with a per-channel power-of-two
+ * prescale, plus the folded epilogue affine alpha/beta [Coutp]
+ * (alpha = bn_scale / prescale, beta = bn_shift + bias*bn_scale; bn_* and
+ * bias nullable).  With w_packed == NULL only alpha/beta are written (no
+ * prescale), the form cf_conv_direct consumes.  Replaces the weight caches
+ * of catfuse/implementations/dense_keep.py:73-95 (_ensure_fold) and
+ * catfuse/implementations/sparse_flow.py:92-99 (_ensure_w_cl). */
+int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, int64_t KW,
+                         int64_t Coutp, int64_t Cp, const float* bn_scale, const float* bn_shift,
+                         const float* bias, void* w_packed, float* alpha, float* beta,
+                         void* stream);
+
+/* Fused Conv -> BN -> LIF (epilogue 0) or Conv -> BN -> z (epilogue 1) on
+ * the matrix cores, all T steps in one launch.
+ *   x: NHWC16 [T*x_img_tstride + B][H][W][Cp] from cf_pack_input;
+ *   out: NCHW [T][B][Cout][Ho][Wo] spikes (plus identity when non-NULL,
+ *   the SEW ADD of catfuse/patterns.py:676-689) or z;
+ *   v_in/v_out: [B][Cout][Ho][Wo] (nullable);
+ *   tile_h/tile_w > 0 selects rectangular pixel tiles aligned with the
+ *   prescan tiles (tile_h*tile_w in {64,128}) and enables SparseFlow chunk
+ *   skipping from ag_mask ([T][B*GH*GW]) when nnz is non-NULL; tile_h = 0
+ *   selects flat pixel tiles (dense).  nnz non-NULL also enables the
+ *   StaticZero route.  All routes give bit-identical results.
+ * Replaces catfuse/implementations/dense_keep.py:97-155 (DenseKeep.forward),
+ * catfuse/implementations/sparse_flow.py:186-270 (SparseFlow.forward ->
+ * catfuse/sparseflow/streamfuse_kernel.py:32-187), and
+ * catfuse/sparseflow/fused_conv_bn_lif_kernel.py:342-539. */
+int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha, const float* beta,
+                 const float* v_in, float* v_out, float* out, const float* identity,
+                 const int32_t* ag_mask, const unsigned long long* nnz, int64_t numel,
+                 double sparse_threshold, int64_t T, int64_t B, int64_t Cp, int64_t Cout,
+                 int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo, int64_t KH,
+                 int64_t KW, int64_t stride, int64_t pad, int64_t x_img_tstride, int64_t tile_h,
+                 int64_t tile_w, int64_t group_size, int epilogue, double tau, double v_th,
+                 double v_reset, int hard_reset, int decay_input, void* stream);
+
+/* Fused Conv -> BN -> LIF / z in fp32 (VALU) for analog inputs
+ * x [T*x_img_tstride + B][Cin][H][W]; x_img_tstride == 0 evaluates the
+ * convolution once for a time-repeated (direct-encoded) input.  Replaces
+ * catfuse/implementations/dense_keep.py:97-155 for the network stem. */
+int cf_conv_direct(const float* x, const float* w, const float* alpha, const float* beta,
+                   const float* v_in, float* v_out, float* out, int64_t T, int64_t B,
+                   int64_t Cin, int64_t Cout, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
+                   int64_t KH, int64_t KW, int64_t stride, int64_t pad, int64_t x_img_tstride,
+                   int epilogue, double tau, double v_th, double v_reset, int hard_reset,
+                   int decay_input, void* stream);
+
+/* Diagnostic: one wave computes D(32x32 fp32) = A(32x16 fp16) * B(16x32
+ * fp16) through the matrix-core lane mapping cf_conv_mfma relies on.
+ * No reference counterpart (layout self-test). */
+int cf_probe_mfma_layout(const void* A, const void* B, float* D, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* CATFUSE_AMD_H */

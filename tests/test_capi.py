@@ -1,0 +1,74 @@
+"""C-ABI checks that need no GPU: the library loads, exports every entry
+point include/catfuse_amd.h declares, and rejects malformed arguments on
+the host (before any launch) with hipErrorInvalidValue."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "catfuse_amd.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:int|const char\*)\s+(cf_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    for s in ("cf_lif_multistep", "cf_conv_mfma", "cf_prescan_tiles", "cf_pack_input",
+              "cf_conv_direct", "cf_avgpool2x2_lif", "cf_route_from_nnz"):
+        assert s in syms
+
+
+def test_library_exports_every_declared_symbol():
+    from catfuse_amd import _hip
+    path = _hip.library_path()
+    assert os.path.exists(path), "build the library first (python -m catfuse_amd.build)"
+    lib = ctypes.CDLL(path)
+    missing = [s for s in declared_symbols() if not hasattr(lib, s)]
+    assert not missing, f"not exported: {missing}"
+    # and the Python binding covers them all
+    assert set(declared_symbols()) <= set(_hip._SIGNATURES)
+
+
+def test_version():
+    from catfuse_amd import _hip
+    assert _hip.lib().cf_version() >= 100
+
+
+INVALID = 1  # hipErrorInvalidValue
+
+
+def test_host_side_argument_validation():
+    from catfuse_amd import _hip
+    L = _hip.lib()
+    # null input / bad mode
+    assert L.cf_lif_multistep(None, None, None, None, 0, None, None, 0, None, 4, 16, 1, 1,
+                              2.0, 1.0, 0.0, 1, 1, None) == INVALID
+    assert L.cf_lif_multistep(1, None, None, None, 9, None, 1, 0, None, 4, 16, 1, 1,
+                              2.0, 1.0, 0.0, 1, 1, None) == INVALID
+    # add modes need z2, affine modes need scale/shift
+    assert L.cf_lif_multistep(1, None, None, None, 3, None, 1, 0, None, 4, 16, 1, 1,
+                              2.0, 1.0, 0.0, 1, 1, None) == INVALID
+    assert L.cf_lif_multistep(1, None, None, None, 1, None, 1, 0, None, 4, 16, 1, 1,
+                              2.0, 1.0, 0.0, 1, 1, None) == INVALID
+    # conv: Cp not a multiple of 32
+    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, None, None, 0, 0.7,
+                          4, 2, 48, 64, 64, 8, 8, 8, 8, 3, 3, 1, 1, 2, 0, 0, 0,
+                          0, 2.0, 1.0, 0.0, 1, 1, None) == INVALID
+    # conv: inconsistent output size
+    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, None, None, 0, 0.7,
+                          4, 2, 64, 64, 64, 8, 8, 7, 8, 3, 3, 1, 1, 2, 0, 0, 0,
+                          0, 2.0, 1.0, 0.0, 1, 1, None) == INVALID
+    # conv: rect tile must hold 64 or 128 pixels
+    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, None, None, 0, 0.7,
+                          4, 2, 64, 64, 64, 8, 8, 8, 8, 3, 3, 1, 1, 2, 4, 4, 16,
+                          0, 2.0, 1.0, 0.0, 1, 1, None) == INVALID
+    # prescan: more than 32 groups
+    assert L.cf_prescan_tiles(1, 1, 8, 8, 8, 8, 3, 1, 1, 8, 8, 33, 1, 1, None) == INVALID
+    # pack: groups must fit 32 bits
+    assert L.cf_pack_input(1, 1, 1024, 4, 4, 1024, None, 1, 16, 1e-6, None, None,
+                           None) == INVALID

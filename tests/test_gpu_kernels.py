@@ -1,0 +1,298 @@
+"""Kernel-level parity of the gfx950 HIP path against the CPU oracle.
+
+Element-wise LIF tails, prescan masks/classes, route words and nonzero
+counts are compared bit-exactly; fused Conv->BN->LIF layers use the LIF
+tolerance in tests/parity.py.  SparseFlow and DenseKeep routes of the same
+conv are compared bit-exactly with each other.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from parity import lif_parity
+
+pytestmark = pytest.mark.gpu
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+# ---------------------------------------------------------------------------
+# matrix-core layout
+# ---------------------------------------------------------------------------
+
+def test_mfma_layout_probe(cuda):
+    from catfuse_amd import _hip
+    g = _gen(0)
+    A = torch.randint(-8, 9, (32, 16), generator=g).to(torch.float16)
+    B = torch.randint(-8, 9, (16, 32), generator=g).to(torch.float16)
+    Ad, Bd = A.to(cuda), B.to(cuda)
+    D = torch.zeros(32, 32, dtype=torch.float32, device=cuda)
+    _hip.check(_hip.lib().cf_probe_mfma_layout(Ad.data_ptr(), Bd.data_ptr(), D.data_ptr(),
+                                               _hip.stream(cuda)))
+    torch.cuda.synchronize()
+    np.testing.assert_array_equal(D.cpu().numpy(), (A.float() @ B.float()).numpy())
+
+
+# ---------------------------------------------------------------------------
+# LIF family: bit-exact
+# ---------------------------------------------------------------------------
+
+LIF_VARIANTS = [
+    dict(tau=2.0, v_threshold=1.0, v_reset=0.0, decay_input=True),
+    dict(tau=3.0, v_threshold=1.0, v_reset=0.0, decay_input=True),
+    dict(tau=2.0, v_threshold=0.5, v_reset=None, decay_input=True),
+    dict(tau=1.7, v_threshold=1.0, v_reset=0.0, decay_input=False),
+    dict(tau=2.5, v_threshold=1.0, v_reset=None, decay_input=False),
+    dict(tau=2.0, v_threshold=1.0, v_reset=-0.2, decay_input=True),
+]
+
+
+@pytest.mark.parametrize("variant", range(len(LIF_VARIANTS)))
+@pytest.mark.parametrize("mode", [0, 1, 2, 3, 4])
+@pytest.mark.parametrize("shape", [(4, 2, 16, 7, 9), (4, 3, 8, 8, 8)])
+def test_lif_multistep_bit_exact(cuda, variant, mode, shape):
+    from catfuse_amd import runtime
+    p = LIF_VARIANTS[variant]
+    T, B, C, H, W = shape
+    g = _gen(100 * variant + mode)
+    z = torch.randn(shape, generator=g) * 1.2
+    z2 = torch.randn(shape, generator=g) * 0.5
+    sc = torch.rand(C, generator=g) + 0.5
+    sh = torch.randn(C, generator=g) * 0.2
+    v0 = torch.randn(B, C, H, W, generator=g) * 0.4
+    s_ref, v_ref, _ = oracle.lif_multistep(z, v0, mode=mode, z2=z2, scale=sc, shift=sh, C=C,
+                                           HW=H * W, **p)
+    s, v = runtime.lif_multistep(z.to(cuda), v0.to(cuda), mode=mode, z2=z2.to(cuda),
+                                 scale=sc.to(cuda), shift=sh.to(cuda), channels=C, hw=H * W, **p)
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(v.cpu().numpy(), v_ref)
+
+
+def test_lif_uint8_spikes_and_default_v(cuda):
+    from catfuse_amd import runtime
+    z = torch.randn(5, 1000, generator=_gen(5)) * 2
+    s_ref, v_ref, _ = oracle.lif_multistep(z)
+    s, v = runtime.lif_multistep(z.to(cuda), None, spike_dtype=torch.uint8)
+    assert s.dtype == torch.uint8
+    np.testing.assert_array_equal(s.cpu().numpy().astype(np.float32), s_ref)
+    np.testing.assert_array_equal(v.cpu().numpy(), v_ref)
+
+
+def test_lif_sequential_api(cuda):
+    from catfuse_amd.sparseflow.lif_seq_kernel import lif_sequential
+    z = torch.randn(4, 2, 3, 5, 5, generator=_gen(9))
+    v0 = torch.zeros(2, 3, 5, 5)
+    s, v = lif_sequential(z.to(cuda), v0.to(cuda), tau=2.0, v_threshold=1.0, v_reset=0.0)
+    s_ref, v_ref, _ = oracle.lif_multistep(z, v0)
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(v.cpu().numpy(), v_ref)
+
+
+@pytest.mark.parametrize("shape", [(4, 2, 8, 16, 16), (3, 1, 5, 7, 9)])
+def test_avgpool2x2_lif_bit_exact(cuda, shape):
+    from catfuse_amd import runtime
+    g = _gen(11)
+    x = torch.rand(shape, generator=g) * 3
+    T, B, C, H, W = shape
+    z = torch.nn.functional.avg_pool2d(x.flatten(0, 1), 2, 2)
+    z = z.reshape(T, B, C, H // 2, W // 2)
+    s_ref, v_ref, _ = oracle.lif_multistep(z)
+    s, v = runtime.avgpool2x2_lif(x.to(cuda))
+    np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(v.cpu().numpy(), v_ref)
+
+
+# ---------------------------------------------------------------------------
+# pack + prescan + route: bit-exact
+# ---------------------------------------------------------------------------
+
+PRESCAN_SHAPES = [
+    # N, C, H, W, k, s, p
+    (8, 64, 32, 32, 3, 1, 1),
+    (4, 256, 14, 14, 3, 1, 1),
+    (2, 64, 56, 56, 3, 1, 1),
+    (2, 40, 9, 11, 3, 1, 1),
+    (2, 128, 28, 28, 3, 2, 1),
+    (3, 64, 14, 14, 1, 2, 0),
+    (2, 1024, 8, 8, 1, 1, 0),
+]
+
+
+@pytest.mark.parametrize("shape", PRESCAN_SHAPES)
+@pytest.mark.parametrize("rate", [0.0, 0.001, 0.05, 0.5])
+def test_pack_prescan_bit_exact(cuda, shape, rate):
+    from catfuse_amd import runtime
+    N, C, H, W, k, s, p = shape
+    x = (torch.rand(N, C, H, W, generator=_gen(int(rate * 1000) + C)) < rate).float()
+    Ho, Wo = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+    bh, bw = oracle.select_tile_sizes(Ho, Wo)
+    gs = oracle.choose_group_size(C)
+    G = -(-C // gs)
+    xd = x.to(cuda)
+    nnz = torch.zeros(1, dtype=torch.int64, device=cuda)
+    st = torch.zeros(1, dtype=torch.int32, device=cuda)
+    xp, act = runtime.pack_input(xd, group_size=gs, nnz=nnz, status=st)
+    tc, ag = runtime.prescan_tiles(act, H, W, Ho, Wo, k, s, p, bh, bw, G)
+    tc_ref, ag_ref = oracle.prescan2d(x, Ho, Wo, k, s, p, bh, bw, gs)
+    np.testing.assert_array_equal(ag.cpu().numpy(), ag_ref)
+    np.testing.assert_array_equal(tc.cpu().numpy(), tc_ref)
+    assert int(nnz.item()) == int(np.count_nonzero(x.numpy()))
+    assert int(st.item()) == 0
+    cp = runtime.pad32(C)
+    ref_xp = torch.zeros(N, H, W, cp, dtype=torch.float16)
+    ref_xp[..., :C] = x.permute(0, 2, 3, 1).half()
+    assert torch.equal(xp.cpu(), ref_xp)
+    route = runtime.route_from_nnz(nnz, x.numel(), 0.7)
+    assert int(route.item()) == oracle.route(x)
+
+
+def test_pack_flags_inexact_inputs(cuda):
+    from catfuse_amd import runtime
+    st = torch.zeros(1, dtype=torch.int32, device=cuda)
+    x = torch.full((1, 32, 4, 4), 0.5, device=cuda)
+    runtime.pack_input(x, status=st)
+    assert int(st.item()) == 0
+    x[0, 3, 1, 1] = 0.1  # not representable in fp16
+    runtime.pack_input(x, status=st)
+    assert int(st.item()) == runtime.STATUS_INEXACT_FP16
+
+
+def test_fast_spike_prescan_api(cuda):
+    from catfuse_amd.sparseflow.prescan import fast_spike_prescan_2d_v2
+    x = (torch.rand(4, 256, 14, 14, generator=_gen(3)) < 0.02).float()
+    tc, ag = fast_spike_prescan_2d_v2(x.to(cuda), 14, 14, kernel_size=3, stride=1, padding=1,
+                                      block_h=8, block_w=8, group_size_c=32)
+    tc_ref, ag_ref = oracle.prescan2d(x, 14, 14, 3, 1, 1, 8, 8, 32)
+    np.testing.assert_array_equal(tc.cpu().numpy(), tc_ref)
+    np.testing.assert_array_equal(ag.cpu().numpy(), ag_ref)
+
+
+# ---------------------------------------------------------------------------
+# fused conv -> BN -> LIF
+# ---------------------------------------------------------------------------
+
+def _bn(C, g):
+    bn = torch.nn.BatchNorm2d(C).eval()
+    with torch.no_grad():
+        bn.running_mean.copy_(torch.randn(C, generator=g) * 0.1)
+        bn.running_var.copy_(torch.rand(C, generator=g) + 0.5)
+        bn.weight.copy_(torch.rand(C, generator=g) * 0.4 + 0.8)
+        bn.bias.copy_(torch.randn(C, generator=g) * 0.1)
+    return bn
+
+
+def _layer(Cin, Cout, k, s, p, seed, bias=False, lif=None):
+    from catfuse_amd import snn
+    g = _gen(seed)
+    conv = torch.nn.Conv2d(Cin, Cout, k, s, p, bias=bias)
+    with torch.no_grad():
+        conv.weight.copy_(torch.randn(conv.weight.shape, generator=g) *
+                          (2.0 / (Cin * k * k)) ** 0.5)
+        if bias:
+            conv.bias.copy_(torch.randn(Cout, generator=g) * 0.1)
+    bn = _bn(Cout, g)
+    return conv, bn, (lif or snn.LIFNode(tau=2.0, v_threshold=1.0, v_reset=0.0))
+
+
+def _runner(conv, bn, lif, dev):
+    from catfuse_amd import runtime
+    sc, sh = oracle.bn_fold(bn.weight, bn.bias, bn.running_mean, bn.running_var, bn.eps)
+    return runtime.ConvLIFRunner(conv.weight.detach().to(dev), sc.to(dev), sh.to(dev),
+                                 None if conv.bias is None else conv.bias.detach().to(dev),
+                                 conv.stride[0], conv.padding[0], lif.tau, lif.v_threshold,
+                                 lif.v_reset, lif.decay_input)
+
+
+CONV_CASES = [
+    # name, T, B, Cin, Cout, H, W, k, s, p, rate
+    ("C0", 4, 8, 64, 64, 32, 32, 3, 1, 1, 0.15),
+    ("C1", 4, 4, 256, 256, 14, 14, 3, 1, 1, 0.05),
+    ("l4", 4, 4, 512, 512, 7, 7, 3, 1, 1, 0.2),
+    ("s2", 2, 2, 64, 128, 28, 28, 3, 2, 1, 0.3),
+    ("ds", 2, 2, 128, 256, 28, 28, 1, 2, 0, 0.3),
+    ("odd", 3, 2, 40, 96, 9, 11, 3, 1, 1, 0.4),
+    ("t1", 1, 2, 64, 64, 16, 16, 3, 1, 1, 0.5),
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES, ids=[c[0] for c in CONV_CASES])
+def test_conv_bn_lif_mfma_parity(cuda, case):
+    name, T, B, Cin, Cout, H, W, k, s, p, rate = case
+    conv, bn, lif = _layer(Cin, Cout, k, s, p, seed=hash(name) % 997)
+    x = (torch.rand(T, B, Cin, H, W, generator=_gen(1)) < rate).float()
+    s_ref, v_ref, h_ref = oracle.conv_bn_lif(x, conv, bn, lif)
+    r = _runner(conv, bn, lif, cuda)
+    spk, v = r.run_mfma(x.to(cuda))
+    lif_parity(spk.cpu().numpy(), v.cpu().numpy(), s_ref, v_ref, h_ref, what=name)
+    # z itself against the oracle's fp64 conv + fp32 BN
+    z, _ = r.run_mfma(x.to(cuda), epilogue=1)
+    zr = oracle.batch_norm(oracle.conv2d(x.flatten(0, 1), conv.weight, None, s, p), bn)
+    np.testing.assert_allclose(z.cpu().numpy().reshape(zr.shape), zr.numpy(), rtol=2e-5,
+                               atol=2e-5)
+
+
+@pytest.mark.parametrize("rate", [0.0, 0.01, 0.05, 0.2, 0.5])
+@pytest.mark.parametrize("pattern", ["iid", "block"])
+def test_sparse_route_bitwise_equals_dense(cuda, rate, pattern):
+    T, B, C, H, W = 4, 4, 256, 14, 14
+    conv, bn, lif = _layer(C, C, 3, 1, 1, seed=5)
+    g = _gen(int(rate * 100) + (7 if pattern == "block" else 0))
+    x = (torch.rand(T, B, C, H, W, generator=g) < rate).float()
+    if pattern == "block":
+        keep = (torch.rand(T, B, C, 2, 2, generator=g) >= 0.7).float()
+        keep = keep.repeat_interleave(8, 3).repeat_interleave(8, 4)[..., :H, :W]
+        x = x * keep
+    r = _runner(conv, bn, lif, cuda)
+    xd = x.to(cuda)
+    v0 = (torch.rand(B, C, H, W, generator=g) * 0.5).to(cuda)
+    s_dense, v_dense = r.run_mfma(xd, v0, static_zero=False)
+    s_sparse, v_sparse = r.run_mfma(xd, v0, sparse=dict(block_h=8, block_w=8, group_size=32))
+    s_sz, v_sz = r.run_mfma(xd, v0, static_zero=True)
+    for s2, v2 in ((s_sparse, v_sparse), (s_sz, v_sz)):
+        assert torch.equal(s2, s_dense)
+        assert torch.equal(v2, v_dense)
+    s_ref, v_ref, h_ref = oracle.conv_bn_lif(x, conv, bn, lif, v_in=v0.cpu())
+    lif_parity(s_dense.cpu().numpy(), v_dense.cpu().numpy(), s_ref, v_ref, h_ref,
+               what=f"C1 {pattern} {rate}")
+
+
+def test_static_zero_route_equals_bias_only(cuda):
+    T, B, C, H, W = 4, 2, 64, 8, 8
+    conv, bn, lif = _layer(C, C, 3, 1, 1, seed=8)
+    r = _runner(conv, bn, lif, cuda)
+    x = torch.zeros(T, B, C, H, W, device=cuda)
+    spk, v = r.run_mfma(x, sparse=dict(block_h=8, block_w=8, group_size=16))
+    sc, sh = oracle.bn_fold(bn.weight, bn.bias, bn.running_mean, bn.running_var, bn.eps)
+    z = sh.view(1, 1, C, 1, 1).expand(T, B, C, H, W)
+    s_ref, v_ref, _ = oracle.lif_multistep(z)
+    np.testing.assert_array_equal(spk.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(v.cpu().numpy(), v_ref)
+
+
+def test_conv_bias_and_sew_identity(cuda):
+    T, B, Cin, Cout, H, W = 2, 2, 64, 64, 12, 12
+    conv, bn, lif = _layer(Cin, Cout, 3, 1, 1, seed=13, bias=True)
+    x = (torch.rand(T, B, Cin, H, W, generator=_gen(2)) < 0.3).float()
+    ident = (torch.rand(T, B, Cout, H, W, generator=_gen(3)) < 0.5).float()
+    r = _runner(conv, bn, lif, cuda)
+    spk, v = r.run_mfma(x.to(cuda))
+    out, _ = r.run_mfma(x.to(cuda), identity=ident.to(cuda))
+    assert torch.equal(out.cpu(), ident + spk.cpu())
+    s_ref, v_ref, h_ref = oracle.conv_bn_lif(x, conv, bn, lif)
+    lif_parity(spk.cpu().numpy(), v.cpu().numpy(), s_ref, v_ref, h_ref, what="bias")
+
+
+@pytest.mark.parametrize("dedupe", [True, False])
+def test_conv_direct_stem_parity(cuda, dedupe):
+    T, B, H, W = 4, 2, 64, 64
+    conv, bn, lif = _layer(3, 64, 7, 2, 3, seed=21)
+    img = torch.randn(B, 3, H, W, generator=_gen(4))
+    x = img.unsqueeze(0).expand(T, B, 3, H, W)
+    xd = img.to(cuda).unsqueeze(0).expand(T, B, 3, H, W) if dedupe else x.contiguous().to(cuda)
+    r = _runner(conv, bn, lif, cuda)
+    spk, v = r.run_direct(xd)
+    s_ref, v_ref, h_ref = oracle.conv_bn_lif(x.contiguous(), conv, bn, lif)
+    lif_parity(spk.cpu().numpy(), v.cpu().numpy(), s_ref, v_ref, h_ref, what="stem")

@@ -1,0 +1,229 @@
+"""Pins the CPU oracle (oracle/) with checks that do not restate its code:
+hand-derived closed-form LIF sequences, an independent torch evaluation of
+SpikingJelly's op sequence, two independent prescan formulations plus their
+closed-form special cases, and a brute-force convolution."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+
+# ---------------------------------------------------------------------------
+# LIF: closed forms (derived by hand, SpikingJelly semantics)
+# ---------------------------------------------------------------------------
+
+def test_lif_constant_input_closed_form():
+    # tau=2, v_th=1, hard reset 0, decay_input: v1 = 1.5/2 = 0.75;
+    # v2 = 0.75 + (1.5 - 0.75)/2 = 1.125 -> spike, reset to 0; period 2.
+    z = np.full((6, 1), 1.5, np.float32)
+    s, v, h = oracle.lif_multistep(z)
+    assert s[:, 0].tolist() == [0, 1, 0, 1, 0, 1]
+    assert h[:, 0].tolist() == [0.75, 1.125, 0.75, 1.125, 0.75, 1.125]
+    assert v[0] == 0.0
+
+
+def test_lif_zero_input_decays_by_half():
+    v0 = np.array([0.8, -0.4, 0.0], np.float32)
+    s, v, h = oracle.lif_multistep(np.zeros((3, 3), np.float32), v_in=v0)
+    assert not s.any()
+    np.testing.assert_array_equal(h[0], v0 / 2)
+    np.testing.assert_array_equal(v, v0 / 8)
+
+
+def test_lif_threshold_is_inclusive():
+    # v = 0 + (2 - 0)/2 = 1.0 exactly -> fires (v >= v_th)
+    s, v, _ = oracle.lif_multistep(np.array([[2.0]], np.float32))
+    assert s[0, 0] == 1.0 and v[0] == 0.0
+
+
+def test_lif_soft_reset_subtracts_threshold():
+    # soft reset: v1 = 3/2 = 1.5 -> spike, v = 0.5; v2 = 0.5 + (0 - 0.5)/2 = 0.25
+    z = np.array([[3.0], [0.0]], np.float32)
+    s, v, h = oracle.lif_multistep(z, v_reset=None)
+    assert s[:, 0].tolist() == [1.0, 0.0]
+    assert h[:, 0].tolist() == [1.5, 0.25]
+    assert v[0] == 0.25
+
+
+def test_lif_no_decay_input():
+    # decay_input=False, hard reset: v = v - (v - 0)/2 + x; x=0.6: 0.6, 0.9, 1.05 -> spike
+    z = np.full((3, 1), 0.6, np.float32)
+    s, v, h = oracle.lif_multistep(z, decay_input=False)
+    np.testing.assert_allclose(h[:, 0], [0.6, 0.9, 1.05], rtol=1e-6)
+    assert s[:, 0].tolist() == [0.0, 0.0, 1.0]
+
+
+def test_lif_nonzero_reset_value():
+    # hard reset to -0.5: v1 = -0.5 + (4 - (-0.5 + 0.5))/2 = 1.5 -> spike -> v = -0.5
+    s, v, h = oracle.lif_multistep(np.array([[4.0]], np.float32), v_reset=-0.5)
+    assert h[0, 0] == 1.5 and s[0, 0] == 1.0 and v[0] == -0.5
+
+
+def _torch_sj_reference(z, v, tau, vth, vreset, decay):
+    """SpikingJelly's eval recurrence evaluated with torch fp32 CPU ops."""
+    out = []
+    for t in range(z.shape[0]):
+        x = z[t]
+        if vreset is not None:
+            v = v + (x - (v - vreset)) / tau if decay else v - (v - vreset) / tau + x
+        else:
+            v = v + (x - v) / tau if decay else v * (1.0 - 1.0 / tau) + x
+        s = (v >= vth).to(torch.float32)
+        v = vreset * s + (1.0 - s) * v if vreset is not None else v - s * vth
+        out.append(s)
+    return torch.stack(out), v
+
+
+@pytest.mark.parametrize("tau,vreset,decay", [(2.0, 0.0, True), (3.0, 0.0, True),
+                                              (2.0, None, True), (1.7, 0.0, False),
+                                              (2.5, None, False), (2.0, -0.2, True)])
+def test_lif_matches_torch_fp32_evaluation(tau, vreset, decay):
+    g = torch.Generator().manual_seed(7)
+    z = torch.randn(6, 4000, generator=g) * 0.9
+    v0 = torch.randn(4000, generator=g) * 0.3
+    s_ref, v_ref = _torch_sj_reference(z, v0.clone(), tau, 1.0, vreset, decay)
+    s, v, _ = oracle.lif_multistep(z, v_in=v0, tau=tau, v_reset=vreset, decay_input=decay)
+    np.testing.assert_array_equal(s, s_ref.numpy())
+    np.testing.assert_array_equal(v, v_ref.numpy())
+
+
+def test_lif_modes_input_current():
+    g = torch.Generator().manual_seed(1)
+    T, C, HW = 3, 4, 5
+    z = torch.randn(T, 2 * C * HW, generator=g)
+    z2 = torch.randn(T, 2 * C * HW, generator=g)
+    sc = torch.rand(C, generator=g) + 0.5
+    sh = torch.randn(C, generator=g)
+    c = (torch.arange(2 * C * HW) // HW) % C
+    expect = {
+        1: z * sc[c] + sh[c],
+        2: (z * sc[c] + sh[c]) + z2,
+        3: z + z2,
+        4: (z + z2) * sc[c] + sh[c],
+    }
+    for mode, x in expect.items():
+        s, v, h = oracle.lif_multistep(z, mode=mode, z2=z2, scale=sc, shift=sh, C=C, HW=HW)
+        s0, v0, h0 = oracle.lif_multistep(x)
+        np.testing.assert_array_equal(h, h0)
+        np.testing.assert_array_equal(s, s0)
+
+
+# ---------------------------------------------------------------------------
+# Prescan: two independent formulations + closed forms
+# ---------------------------------------------------------------------------
+
+PRESCAN_CASES = [
+    # N, C, H, W, k, s, p
+    (2, 64, 32, 32, 3, 1, 1),
+    (1, 256, 14, 14, 3, 1, 1),
+    (2, 32, 56, 56, 3, 1, 1),
+    (1, 40, 9, 11, 3, 1, 1),
+    (1, 64, 16, 16, 3, 2, 1),
+    (2, 48, 12, 12, 1, 2, 0),
+    (1, 128, 8, 8, 1, 1, 0),
+]
+
+
+@pytest.mark.parametrize("case", PRESCAN_CASES)
+@pytest.mark.parametrize("rate", [0.0, 0.002, 0.05, 0.5])
+def test_prescan_bruteforce_equals_maxpool_cascade(case, rate):
+    N, C, H, W, k, s, p = case
+    g = torch.Generator().manual_seed(hash((case, rate)) % 1000)
+    x = (torch.rand(N, C, H, W, generator=g) < rate).float()
+    Ho, Wo = (H + 2 * p - k) // s + 1, (W + 2 * p - k) // s + 1
+    bh, bw = oracle.select_tile_sizes(Ho, Wo)
+    gs = oracle.choose_group_size(C)
+    a = oracle.prescan2d(x, Ho, Wo, k, s, p, bh, bw, gs)
+    b = oracle.prescan2d_maxpool(x, Ho, Wo, k, s, p, bh, bw, gs)
+    np.testing.assert_array_equal(a[0], b[0])
+    np.testing.assert_array_equal(a[1], b[1])
+
+
+def test_prescan_closed_forms():
+    N, C, H, W = 1, 64, 16, 16
+    gs = oracle.choose_group_size(C)          # 16 -> 4 groups
+    assert gs == 16
+    zero = np.zeros((N, C, H, W), np.float32)
+    tc, ag = oracle.prescan2d(zero, H, W, 3, 1, 1, 8, 8, gs)
+    assert (tc == 0).all() and (ag == 0).all()
+    ones = np.ones((N, C, H, W), np.float32)
+    tc, ag = oracle.prescan2d(ones, H, W, 3, 1, 1, 8, 8, gs)
+    assert (tc == 2).all() and (ag == 0b1111).all()
+    # one spike at channel 37 (group 2), pixel (7, 8): the 3x3 RF of output
+    # pixels (6..8, 7..9) touches tiles (0,0)? no: oh in 6..8 -> gh 0 (6,7) and
+    # gh 1 (8); ow in 7..9 -> gw 0 (7) and gw 1 (8, 9) -> all four tiles.
+    one = np.zeros((N, C, H, W), np.float32)
+    one[0, 37, 7, 8] = 1.0
+    tc, ag = oracle.prescan2d(one, H, W, 3, 1, 1, 8, 8, gs)
+    assert ag.tolist() == [4, 4, 4, 4] and tc.tolist() == [1, 1, 1, 1]
+    # at pixel (3, 3) only tile (0, 0) sees it
+    one[:] = 0
+    one[0, 5, 3, 3] = 1.0
+    tc, ag = oracle.prescan2d(one, H, W, 3, 1, 1, 8, 8, gs)
+    assert ag.tolist() == [1, 0, 0, 0]
+    # threshold: |x| must exceed 1e-6 strictly; negative values count
+    one[0, 5, 3, 3] = -2e-6
+    assert oracle.prescan2d(one, H, W, 3, 1, 1, 8, 8, gs)[1][0] == 1
+    one[0, 5, 3, 3] = 1e-6
+    assert oracle.prescan2d(one, H, W, 3, 1, 1, 8, 8, gs)[1][0] == 0
+
+
+def test_prescan_32_groups_sign_bit():
+    C = 1024  # gs 32 -> 32 groups -> bit 31 is the int32 sign bit
+    assert oracle.choose_group_size(C) == 32
+    x = np.zeros((1, C, 8, 8), np.float32)
+    x[0, C - 1, 0, 0] = 1
+    tc, ag = oracle.prescan2d(x, 8, 8, 1, 1, 0, 8, 8, 32)
+    assert ag[0] == np.int32(-2 ** 31)
+    tc2, ag2 = oracle.prescan2d_maxpool(x, 8, 8, 1, 1, 0, 8, 8, 32)
+    assert ag2[0] == ag[0]
+
+
+def test_geometry_helpers():
+    assert [oracle.choose_group_size(c) for c in (3, 64, 128, 129, 256, 512, 1024, 2048)] == \
+        [16, 16, 16, 32, 32, 32, 32, 64]
+    assert oracle.select_tile_sizes(56, 56) == (8, 16)
+    assert oracle.select_tile_sizes(55, 57) == (8, 8)    # 3135 pixels < 3136
+    assert oracle.select_tile_sizes(14, 14) == (8, 8)
+
+
+def test_route_decision():
+    assert oracle.route(np.zeros(100, np.float32)) == 0
+    x = np.zeros(1000, np.float32)
+    x[:300] = 1   # sparsity 0.7 -> not > 0.7 -> dense
+    assert oracle.route(x) == 2
+    x[299] = 0    # sparsity 0.701 -> sparse
+    assert oracle.route(x) == 1
+
+
+# ---------------------------------------------------------------------------
+# Conv / BN
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("shape", [(2, 3, 9, 9, 5, 3, 1, 1), (1, 4, 8, 10, 6, 1, 2, 0),
+                                   (1, 3, 15, 15, 4, 7, 2, 3)])
+def test_conv_library_equals_bruteforce(shape):
+    N, Cin, H, W, Cout, k, s, p = shape
+    g = torch.Generator().manual_seed(3)
+    x = torch.randn(N, Cin, H, W, generator=g)
+    w = torch.randn(Cout, Cin, k, k, generator=g)
+    a = oracle.conv2d(x, w, stride=s, padding=p).numpy()
+    b = oracle.conv2d_bruteforce(x, w, stride=s, padding=p)
+    np.testing.assert_allclose(a, b, rtol=1e-6, atol=1e-6)
+
+
+def test_bn_fold_matches_torch_batch_norm():
+    g = torch.Generator().manual_seed(4)
+    C = 16
+    bn = torch.nn.BatchNorm2d(C).eval()
+    with torch.no_grad():
+        bn.running_mean.copy_(torch.randn(C, generator=g) * 0.1)
+        bn.running_var.copy_(torch.rand(C, generator=g) + 0.5)
+        bn.weight.copy_(torch.rand(C, generator=g) * 0.4 + 0.8)
+        bn.bias.copy_(torch.randn(C, generator=g) * 0.1)
+    z = torch.randn(2, C, 5, 5, generator=g)
+    sc, sh = oracle.bn_fold(bn.weight, bn.bias, bn.running_mean, bn.running_var, bn.eps)
+    folded = z * sc.view(1, -1, 1, 1) + sh.view(1, -1, 1, 1)
+    np.testing.assert_allclose(folded.numpy(), oracle.batch_norm(z, bn).numpy(), rtol=1e-5,
+                               atol=1e-6)
