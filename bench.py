@@ -1,0 +1,224 @@
+"""Benchmark: SEW-ResNet18 (ADD, LIF tau=2, v_th=1, hard reset) T=4, B=32,
+3x224x224 direct-encoded input, fused by catfuse_amd.optimize on one MI355X.
+
+One step = one full forward of the fused network over the batch (all T
+steps, stem to logits) on synthetic inputs resident in HBM, with a
+functional.reset_net before it.  Prints ONE JSON line (rank 0):
+  value      = images/s = B / (seconds per step)
+  roofline   = dominant kernel (the MFMA conv) achieved dense-equivalent
+               TFLOP/s vs the 2.5 PFLOP/s fp16 dense MFMA peak, timed live
+               with HIP events on the launch stream during the timed steps
+  lif_tails  = standalone LIF-family kernels' achieved HBM GB/s vs 8 TB/s
+  cpu_baseline = the CPU oracle (SpikingJelly-equivalent PyTorch/C
+               multi-step path, fp32) on a bounded sample of the same
+               workload on this host's cores
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "SEW-ResNet18 T=4 images/s on 1 MI355X; fused-LIF HBM GB/s vs peak"
+PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
+PEAK_HBM_GBPS = 8000.0
+
+
+def build_model(num_classes=1000, seed=0):
+    import torch
+    from catfuse_amd import snn
+    g = torch.Generator().manual_seed(seed)
+    m = snn.sew_resnet18(num_classes=num_classes, cnf="ADD", tau=2.0, v_threshold=1.0,
+                         v_reset=0.0)
+    snn.functional.set_step_mode(m, "m")
+    snn.kaiming_init(m, g)
+    snn.randomize_bn(m, g)
+    return m.eval()
+
+
+def traffic_from_profiles():
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 PMC summary (profiles/conv_mfma_sew_resnet18_traffic.json), or
+    None when it has not been collected."""
+    p = os.path.join(ROOT, "profiles", "conv_mfma_sew_resnet18_traffic.json")
+    if not os.path.exists(p):
+        return None
+    try:
+        return json.load(open(p)).get("hbm_bytes_per_launch")
+    except Exception:
+        return None
+
+
+def measure_tails(dev, reps=20):
+    """Standalone LIF-family kernels at SEW-RN18 / C1 shapes; GB/s from the
+    algorithmic bytes of each launch and its HIP-event duration."""
+    import torch
+    from catfuse_amd import runtime
+    out = []
+    g = torch.Generator(device=dev).manual_seed(0)
+    cases = [
+        ("lif", (4, 32, 64, 56, 56), 0),        # C3 layer1 tail: (8T+8)N
+        ("bn_lif", (4, 32, 64, 56, 56), 1),
+        ("add_lif", (4, 32, 64, 56, 56), 3),    # (12T+8)N
+        ("lif", (4, 32, 256, 14, 14), 0),       # C1 tail
+    ]
+    for name, shape, mode in cases:
+        T, B, C, H, W = shape
+        z = torch.randn(shape, device=dev, generator=g)
+        z2 = torch.randn(shape, device=dev, generator=g) if mode in (2, 3, 4) else None
+        sc = torch.rand(C, device=dev, generator=g) + 0.5
+        sh = torch.randn(C, device=dev, generator=g) * 0.1
+        v0 = torch.zeros(B, C, H, W, device=dev)
+        for _ in range(3):
+            runtime.lif_multistep(z, v0, mode=mode, z2=z2, scale=sc, shift=sh, channels=C, hw=H * W)
+        timer = runtime.KernelTimer()
+        runtime.set_timer(timer)
+        for _ in range(reps):
+            runtime.lif_multistep(z, v0, mode=mode, z2=z2, scale=sc, shift=sh, channels=C, hw=H * W)
+        runtime.set_timer(None)
+        s = next(iter(timer.summary().values()))
+        gbps = s["bytes"] / (s["ms_total"] * 1e-3) / 1e9
+        out.append({"kernel": f"cf_lif_multistep/{name}", "shape": list(shape),
+                    "bytes_per_launch": s["bytes"] // s["launches"],
+                    "us_per_launch": round(s["ms_avg"] * 1e3, 2), "GB/s": round(gbps, 1),
+                    "frac": round(gbps / PEAK_HBM_GBPS, 4)})
+        del z, z2
+    x = torch.rand((4, 32, 128, 32, 32), device=dev, generator=g)
+    for _ in range(3):
+        runtime.avgpool2x2_lif(x)
+    timer = runtime.KernelTimer()
+    runtime.set_timer(timer)
+    for _ in range(reps):
+        runtime.avgpool2x2_lif(x)
+    runtime.set_timer(None)
+    s = next(iter(timer.summary().values()))
+    gbps = s["bytes"] / (s["ms_total"] * 1e-3) / 1e9
+    out.append({"kernel": "cf_avgpool2x2_lif", "shape": [4, 32, 128, 32, 32],
+                "bytes_per_launch": s["bytes"] // s["launches"],
+                "us_per_launch": round(s["ms_avg"] * 1e3, 2), "GB/s": round(gbps, 1),
+                "frac": round(gbps / PEAK_HBM_GBPS, 4)})
+    return out
+
+
+def cpu_baseline(model, T, image, budget_s=12.0):
+    """Oracle forward (fp32 torch CPU conv + eval BN + C LIF, SpikingJelly
+    multi-step semantics) on this host: 1 warm-up image, then batches of 2
+    images until about budget_s seconds have been timed."""
+    import torch
+    import oracle
+    threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(1)
+    x1 = torch.randn(1, 3, image, image, generator=g)
+    oracle.sew_resnet_forward(model, x1.unsqueeze(0).expand(T, 1, 3, image, image),
+                              conv_dtype=torch.float32)
+    x2 = torch.randn(2, 3, image, image, generator=g)
+    xs = x2.unsqueeze(0).expand(T, 2, 3, image, image)
+    imgs, t_total = 0, 0.0
+    while t_total < budget_s:
+        t0 = time.perf_counter()
+        oracle.sew_resnet_forward(model, xs, conv_dtype=torch.float32)
+        t_total += time.perf_counter() - t0
+        imgs += 2
+    return {"value": round(imgs / t_total, 3), "unit": "images/s", "cores": threads,
+            "kind": "port",
+            "sample": f"{imgs} images of 3x{image}x{image}, T={T}, in batches of 2 "
+                      f"({t_total:.1f} s), after 1 warm-up image"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--batch", type=int, default=32)
+    ap.add_argument("--image", type=int, default=224)
+    ap.add_argument("--T", type=int, default=4)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-tails", action="store_true")
+    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: every GPU box in this setup has a single "
+              "MI355X; run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    import catfuse_amd
+    from catfuse_amd import runtime, snn
+
+    dev = torch.device("cuda", 0)
+    T, B, HW = args.T, args.batch, args.image
+    model = build_model()
+    fused, stats = catfuse_amd.optimize(model, device=dev, T=T)
+    fused.eval()
+    g = torch.Generator(device=dev).manual_seed(0)
+    img = torch.randn(B, 3, HW, HW, device=dev, generator=g)
+    x = img.unsqueeze(0).expand(T, B, 3, HW, HW)      # direct encoding, resident in HBM
+
+    with torch.no_grad():
+        for _ in range(args.warmup):
+            snn.functional.reset_net(fused)
+            fused(x)
+        torch.cuda.synchronize()
+        catfuse_amd.check_status(dev)
+
+        timer = runtime.KernelTimer()
+        runtime.set_timer(timer)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            snn.functional.reset_net(fused)
+            y = fused(x)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        runtime.set_timer(None)
+    kern = timer.summary()
+    ms = (t1 - t0) * 1e3 / args.steps
+    ips = B / (ms * 1e-3)
+
+    conv = kern.get("conv_mfma", {})
+    conv_sp = kern.get("conv_mfma_sparse", {})
+    tot_ms = conv.get("ms_total", 0) + conv_sp.get("ms_total", 0)
+    tot_fl = conv.get("flops", 0) + conv_sp.get("flops", 0)
+    launches = conv.get("launches", 0) + conv_sp.get("launches", 0)
+    achieved = tot_fl / (tot_ms * 1e-3) / 1e12 if tot_ms else 0.0
+    roofline = {"kernel": "conv_mfma_kernel (fused Conv-BN-LIF, all launches)",
+                "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+                "traffic": traffic_from_profiles(),
+                "flops_per_launch_avg": tot_fl // max(1, launches),
+                "us_per_launch_avg": round(tot_ms * 1e3 / max(1, launches), 2),
+                "launches_per_step": launches // args.steps}
+    per_kernel = {k: {"launches_per_step": v["launches"] // args.steps,
+                      "ms_per_step": round(v["ms_total"] / args.steps, 4)}
+                  for k, v in kern.items()}
+
+    result = {
+        "metric": METRIC, "value": round(ips, 2), "unit": "images/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32 (conv: fp16 hi/lo split weights x fp16-exact spikes on MFMA, fp32 acc)",
+        "data": "synthetic (seeded N(0,1) images, random kaiming weights, config BN stats)",
+        "config": {"workload": "sew_resnet18_adds_T4_B32_224", "T": T, "batch": B,
+                   "image": [3, HW, HW], "encoding": "direct (input repeated over T)",
+                   "fused_lif_nodes": stats["fused_lif_nodes"],
+                   "total_lif_nodes": stats["total_lif_nodes"]},
+        "roofline": roofline,
+        "kernels": per_kernel,
+    }
+    if not args.no_tails:
+        result["lif_tails"] = measure_tails(dev)
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(model, T, HW, args.cpu_budget)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,43 @@
+"""catfuse_amd — MI355X-native CATFuse-SF: spatio-temporal fused SNN inference.
+
+Drop-in surface of the reference package `catfuse` (hpcyhr/CATFuse):
+``optimize(model, device, policy, T, use_sparseflow) -> (model, stats)``,
+``substitute``, ``substitute_sf``, the pattern modules, ``StateBuffer``,
+the ``Implementation`` plug-in point, ``policy`` and ``hardware``.  All
+tensor math of the fused patterns runs in hand-written gfx950 HIP kernels
+behind the C-ABI in include/catfuse_amd.h (library: catfuse_amd/_lib).
+"""
+from __future__ import annotations
+
+__version__ = "0.1.0"
+
+
+def optimize(model, device="cuda:0", policy=None, T=16, use_sparseflow=True,
+             fuse_sew_add=True):
+    """Substitute the SpikingJelly model's fusible subgraphs with gfx950
+    patterns.  `policy` may be a HardwareProfile for the static routing
+    table (default: the reference's V100 table shape); `device`, when not
+    None, is where the fused model is placed."""
+    from catfuse_amd.substitute import substitute, substitute_sf
+    if use_sparseflow:
+        fused, stats = substitute_sf(model, T=T, fuse_sew_add=fuse_sew_add, hwprof=policy)
+    else:
+        fused, stats = substitute(model)
+    if device is not None:
+        import torch
+        if torch.cuda.is_available():
+            fused = fused.to(device)
+    return fused, stats
+
+
+def check_status(device=None) -> None:
+    """Raise if any fused layer received an input that its fp16 MFMA path
+    could not represent exactly (sticky device flag; synchronises)."""
+    from catfuse_amd import runtime
+    st = runtime.read_status(device)
+    if st & runtime.STATUS_INEXACT_FP16:
+        raise RuntimeError("catfuse_amd: a fused layer on the fp16 MFMA path received inputs "
+                           "that are not exactly representable in fp16")
+
+
+__all__ = ["optimize", "check_status", "__version__"]

@@ -41,6 +41,10 @@ constexpr int KC = 32;        // channels per K step
 constexpr int LDK = KC + 8;   // padded LDS row (halves)
 
 enum { EPI_LIF = 0, EPI_Z = 1 };
+// identity_mode: where a non-NULL identity tensor enters the epilogue.
+//   ID_ADD_SPIKE: out = identity + spike   (SEW ADD after the LIF)
+//   ID_ADD_Z    : z = BN(conv) + identity  (spiking ResNet: BN -> Add -> LIF)
+enum { ID_ADD_SPIKE = 1, ID_ADD_Z = 2 };
 
 struct ConvArgs {
   const _Float16* x;
@@ -51,6 +55,7 @@ struct ConvArgs {
   float* v_out;
   float* out;
   const float* identity;
+  int identity_mode;
   const int32_t* ag_mask;
   const unsigned long long* nnz;
   int64_t numel;
@@ -278,14 +283,15 @@ __global__ __launch_bounds__(256, (conv_min_blocks<BM, BN, EPI>())) void conv_mf
         for (int nb = 0; nb < NB; ++nb) {
           if (e_img[nb] < 0) continue;
           const size_t o = ((size_t)(t * a.B + e_img[nb]) * a.Cout + co) * HoWo + e_off[nb];
-          const float z = acc[mb][nb][r] * al + be;
+          float z = acc[mb][nb][r] * al + be;
+          if (a.identity && a.identity_mode == ID_ADD_Z) z = z + a.identity[o];
           if (EPI == EPI_Z) {
             a.out[o] = z;
           } else {
             float vv = lif_charge(v[mb][nb][r], z, a.lif);
             float sp = lif_fire_reset(vv, a.lif);
             v[mb][nb][r] = vv;
-            a.out[o] = a.identity ? a.identity[o] + sp : sp;
+            a.out[o] = (a.identity && a.identity_mode == ID_ADD_SPIKE) ? a.identity[o] + sp : sp;
           }
         }
       }
@@ -394,7 +400,7 @@ CF_API int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64
 
 CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
                         const float* beta, const float* v_in, float* v_out, float* out,
-                        const float* identity, const int32_t* ag_mask,
+                        const float* identity, int identity_mode, const int32_t* ag_mask,
                         const unsigned long long* nnz, int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
                         int64_t W, int64_t Ho, int64_t Wo, int64_t KH, int64_t KW, int64_t stride,
@@ -407,6 +413,8 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
       stride <= 0 || pad < 0 || x_img_tstride < 0)
     return (int)hipErrorInvalidValue;
   if (epilogue != EPI_LIF && epilogue != EPI_Z) return (int)hipErrorInvalidValue;
+  if (identity && identity_mode != ID_ADD_SPIKE && identity_mode != ID_ADD_Z)
+    return (int)hipErrorInvalidValue;
   if (Ho != (H + 2 * pad - KH) / stride + 1 || Wo != (W + 2 * pad - KW) / stride + 1)
     return (int)hipErrorInvalidValue;
   const bool rect = tile_h > 0 && tile_w > 0;
@@ -423,7 +431,7 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
   a.x = (const _Float16*)x;
   a.w = (const _Float16*)w_packed;
   a.alpha = alpha; a.beta = beta; a.v_in = v_in; a.v_out = v_out; a.out = out;
-  a.identity = identity; a.ag_mask = ag_mask; a.nnz = nnz; a.numel = numel;
+  a.identity = identity; a.identity_mode = identity_mode; a.ag_mask = ag_mask; a.nnz = nnz; a.numel = numel;
   a.sparse_thr = sparse_threshold;
   a.T = (int)T; a.B = (int)B; a.Cp = (int)Cp; a.Cout = (int)Cout; a.Coutp = (int)Coutp;
   a.H = (int)H; a.W = (int)W; a.Ho = (int)Ho; a.Wo = (int)Wo; a.KH = (int)KH; a.KW = (int)KW;

@@ -1,0 +1,88 @@
+"""SparseFlow: prescan + sparse fused Conv -> BN -> LIF, routed on the device.
+
+Realises TimeBlock(K) ∘ StreamFuse(Conv, LIF) ∘ StateCarry(LIF)
+(catfuse/implementations/sparse_flow.py:56-448) on gfx950:
+
+1. cf_pack_input stages x as fp16 NHWC, ORs channel-group activity bits per
+   pixel and counts nonzeros (one pass over x);
+2. cf_prescan_tiles reduces the bits over each output tile's receptive
+   field (tile geometry and group size exactly as the reference's
+   _select_tile_sizes / choose_group_size);
+3. cf_conv_mfma in rectangular-tile mode reads the nonzero count and
+   decides the route itself — nnz == 0: StaticZero (no K loop, z = bias);
+   sparsity > threshold: skip every 32-channel K chunk whose group bits are
+   clear for the tile; otherwise dense — then applies BN and the LIF in its
+   epilogue.  No host synchronisation; every route gives bit-identical
+   results (skipped chunks contribute exact zeros).
+"""
+from __future__ import annotations
+
+import torch
+
+from catfuse_amd.hardware import runtime_profile
+from catfuse_amd.implementations._hip_conv import HipConvImplementation
+from catfuse_amd.implementations.stream_fuse import fused_decomposition, fused_io_cost
+from catfuse_amd.sparseflow.sparse_helpers import _select_tile_sizes, choose_group_size
+
+
+class SparseFlow(HipConvImplementation):
+    name = "SparseFlow"
+
+    def __init__(self, sparsity_threshold: float = None):
+        super().__init__()
+        self.sparsity_threshold = (runtime_profile().sf_sparsity_threshold
+                                   if sparsity_threshold is None else float(sparsity_threshold))
+
+    def geometry(self, spec, H_in, W_in):
+        Ho, Wo = spec.output_hw(H_in, W_in)
+        bh, bw = _select_tile_sizes(Ho, Wo)
+        return dict(block_h=bh, block_w=bw, group_size=choose_group_size(spec.in_channels))
+
+    def forward(self, x, spec, params, state):
+        self.check_input(x, spec)
+        B = x.shape[1]
+        Ho, Wo = spec.output_hw(x.shape[3], x.shape[4])
+        r = self.runner(spec, params, x.device)
+        v_in = state.peek((B, spec.out_channels, Ho, Wo), x.device)
+        if self.input_is_analog(x):
+            spikes, v_out = r.run_direct(x, v_in)
+        else:
+            spikes, v_out = r.run_mfma(x.contiguous(), v_in,
+                                       sparse=self.geometry(spec, x.shape[3], x.shape[4]),
+                                       sparse_threshold=self.sparsity_threshold)
+        state.set(v_out)
+        return spikes
+
+    def last_route(self) -> int:
+        """Route of the most recent forward (0 ZERO, 1 SPARSE, 2 DENSE); reads
+        the device counter, so it synchronises."""
+        from catfuse_amd import runtime
+        r = self._runner
+        if r is None or getattr(r, "last_nnz", None) is None:
+            return -1
+        numel = r._ws["xp"].shape[0] * r._ws["xp"].shape[1] * r._ws["xp"].shape[2] * r.Cin
+        word = runtime.route_from_nnz(r.last_nnz, numel, self.sparsity_threshold)
+        return int(word.item())
+
+    def last_tiles(self):
+        """(tile_class, ag_mask) of the most recent forward (device tensors)."""
+        r = self._runner
+        return None if r is None else r.last_tiles
+
+    def forward_with_k(self, x, spec, params, state, K=None):
+        T = x.shape[0]
+        K = T if K is None else max(1, min(int(K), int(T)))
+        if K >= T:
+            return self.forward(x, spec, params, state)
+        return torch.cat([self.forward(x[s:s + K].contiguous(), spec, params, state)
+                          for s in range(0, T, K)], dim=0)
+
+    def analytic_io_cost(self, spec, T, B, H_in, W_in, K=None, *, dtype_bytes=4):
+        return fused_io_cost(spec, T, B, H_in, W_in, K, dtype_bytes, "SparseFlow")
+
+    def schedule_decomposition(self, spec, T, K=None):
+        return fused_decomposition(T, K, "SparseFlow")
+
+    def __repr__(self):
+        return (f"SparseFlow(hip, threshold={self.sparsity_threshold}, "
+                f"packed={'yes' if self._runner is not None else 'no'})")

@@ -1,0 +1,637 @@
+"""Fused pattern modules (drop-in replacements for SpikingJelly subgraphs).
+
+Mirrors catfuse/patterns.py:52-1063: every pattern takes SpikingJelly
+multi-step tensors [T, B, ...] (fp32, on the GPU), owns its parameters and a
+StateBuffer for the membrane potential, resets through `reset()` (so
+`functional.reset_net` clears it), and is built from the original modules
+with `from_sj_modules(...)` / `from_sj_block(...)`.  The math runs in the
+gfx950 kernels through an Implementation (StreamFuse on MI355X by default,
+DenseKeep available) or a direct kernel launcher.
+
+Differences from the reference that are deliberate (the reference's
+behaviour diverges from SpikingJelly there):
+  * the conv bias of PartialFusionConvBNLIF and the Linear bias of
+    FusedLinearLIF are kept (catfuse/patterns.py:299,326-331,594-595 drop them);
+  * the first state of every pattern is SpikingJelly's (v_reset for hard
+    reset, 0 for soft), also when v_reset != 0;
+  * CTFSEWBasicBlock with cnf='ADD' computes identity + spikes in the second
+    conv's epilogue instead of a separate elementwise add.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from catfuse_amd.hardware import runtime_profile
+from catfuse_amd.implementations import ConvLIFParams, ConvLIFSpec, DenseKeep, StreamFuse
+from catfuse_amd.runtime import (EPI_Z, ID_ADD_SPIKE, ID_ADD_Z, ConvLIFRunner, avgpool2x2_lif,
+                                 lif_multistep)
+from catfuse_amd.state import StateBuffer
+
+try:  # SpikingJelly's MemoryModule when available, so reset_net recognises us
+    from spikingjelly.activation_based.base import MemoryModule as _BaseModule  # type: ignore
+except Exception:  # pragma: no cover - SpikingJelly absent
+    from catfuse_amd.snn import MemoryModule as _BaseModule
+
+
+# ---------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------
+
+def _first(v):
+    return v[0] if isinstance(v, (tuple, list)) else v
+
+
+def conv_geometry(conv):
+    return int(_first(conv.kernel_size)), int(_first(conv.stride)), int(_first(conv.padding))
+
+
+def lif_params(lif):
+    v_reset = getattr(lif, "v_reset", 0.0)
+    return dict(tau=float(getattr(lif, "tau", 2.0)),
+                v_threshold=float(getattr(lif, "v_threshold", 1.0)),
+                v_reset=None if v_reset is None else float(v_reset),
+                decay_input=bool(getattr(lif, "decay_input", True)))
+
+
+def fold_bn(weight, bias, running_mean, running_var, eps):
+    """scale = gamma / sqrt(var + eps), shift = beta - mean * scale (eval BN)."""
+    inv_std = 1.0 / torch.sqrt(running_var + eps)
+    scale = inv_std if weight is None else weight * inv_std
+    shift = -running_mean * scale if bias is None else bias - running_mean * scale
+    return scale.detach(), shift.detach()
+
+
+def _dense_impl():
+    return DenseKeep() if runtime_profile().dense_impl == "DenseKeep" else StreamFuse()
+
+
+def sew_function(identity, out, cnf):
+    if cnf == "ADD":
+        return identity + out
+    if cnf == "AND":
+        return identity * out
+    if cnf == "IAND":
+        return identity * (1.0 - out)
+    raise NotImplementedError(f"Unknown cnf: {cnf}")
+
+
+# ---------------------------------------------------------------------------
+# base
+# ---------------------------------------------------------------------------
+
+class CTFPattern(_BaseModule):
+    """Base of all fused patterns: StateBuffer registration and reset."""
+
+    policy_row: Optional[int] = None
+
+    def __init__(self):
+        super().__init__()
+        self._catfuse_states: list = []
+        self.step_mode = "m"
+
+    def _register_state(self, state) -> None:
+        if not isinstance(state, StateBuffer):
+            raise TypeError(f"_register_state expects a StateBuffer, got {type(state).__name__}")
+        if getattr(self, "_catfuse_states", None) is None:
+            self._catfuse_states = []
+        self._catfuse_states.append(state)
+
+    def forward(self, x):
+        raise NotImplementedError
+
+    @classmethod
+    def from_sj_modules(cls, *sj_modules, **kwargs):
+        raise NotImplementedError
+
+    def reset(self):
+        for s in getattr(self, "_catfuse_states", []):
+            s.reset()
+
+    def single_step_forward(self, x):
+        return self.forward(x)
+
+    def multi_step_forward(self, x_seq):
+        return self.forward(x_seq)
+
+
+class _ConvPattern(CTFPattern):
+    """Shared parts of the Conv -> (BN) -> LIF patterns."""
+
+    def _setup(self, in_channels, out_channels, kernel_size, stride, padding, tau, v_threshold,
+               v_reset, decay_input, has_bn, bn_eps, conv_bias):
+        self.in_channels, self.out_channels = int(in_channels), int(out_channels)
+        self.kernel_size, self.stride, self.padding = int(kernel_size), int(stride), int(padding)
+        self.tau, self.v_threshold = float(tau), float(v_threshold)
+        self.v_reset = None if v_reset is None else float(v_reset)
+        self.decay_input = bool(decay_input)
+        self.bn_eps = float(bn_eps)
+        self.weight = nn.Parameter(torch.empty(out_channels, in_channels, kernel_size, kernel_size))
+        nn.init.kaiming_normal_(self.weight)
+        self.conv_bias = nn.Parameter(torch.zeros(out_channels)) if conv_bias else None
+        self.state = StateBuffer()
+        self._register_state(self.state)
+        self.spec = ConvLIFSpec(self.in_channels, self.out_channels, self.kernel_size, self.stride,
+                                self.padding, has_conv_bias=bool(conv_bias), has_bn=has_bn,
+                                tau=self.tau, v_threshold=self.v_threshold, v_reset=self.v_reset,
+                                decay_input=self.decay_input, bn_eps=self.bn_eps)
+        self._params = None
+        self._params_key = None
+
+    def _bn_tensors(self):
+        return None
+
+    def _ensure_params(self) -> ConvLIFParams:
+        bn = self._bn_tensors()
+        key = (id(self.weight), self.weight._version,
+               None if self.conv_bias is None else (id(self.conv_bias), self.conv_bias._version),
+               None if bn is None else tuple((id(t), t._version) for t in bn if t is not None))
+        if self._params_key == key and self._params is not None:
+            return self._params
+        with torch.no_grad():
+            if bn is not None:
+                scale, shift = fold_bn(bn[0], bn[1], bn[2], bn[3], self.bn_eps)
+            else:
+                scale = shift = None
+        self._params = ConvLIFParams(self.weight, self.conv_bias, scale, shift)
+        self._params_key = key
+        return self._params
+
+    def _run(self, impl, x, **kw):
+        if x.ndim == 4:
+            return impl.forward(x.unsqueeze(0), self.spec, self._ensure_params(), self.state,
+                                **kw).squeeze(0)
+        return impl.forward(x, self.spec, self._ensure_params(), self.state, **kw)
+
+    def extra_repr(self):
+        return (f"{self.in_channels}, {self.out_channels}, kernel_size={self.kernel_size}, "
+                f"stride={self.stride}, padding={self.padding}, tau={self.tau}, "
+                f"v_th={self.v_threshold}, v_reset={self.v_reset}")
+
+
+class PartialFusionConvLIF(_ConvPattern):
+    """Conv -> LIF (no BN)."""
+
+    policy_row = 1
+
+    def __init__(self, in_channels, out_channels, kernel_size, stride=1, padding=0, tau=2.0,
+                 v_threshold=1.0, v_reset=0.0, decay_input=True, bias=False):
+        super().__init__()
+        self._setup(in_channels, out_channels, kernel_size, stride, padding, tau, v_threshold,
+                    v_reset, decay_input, has_bn=False, bn_eps=1e-5, conv_bias=bias)
+        self._impl = _dense_impl()
+
+    def forward(self, x):
+        return self._run(self._impl, x)
+
+    @classmethod
+    def from_sj_modules(cls, sj_conv, sj_lif):
+        k, s, p = conv_geometry(sj_conv)
+        inst = cls(sj_conv.in_channels, sj_conv.out_channels, k, s, p,
+                   bias=sj_conv.bias is not None, **lif_params(sj_lif))
+        with torch.no_grad():
+            inst.weight.copy_(sj_conv.weight)
+            if sj_conv.bias is not None:
+                inst.conv_bias.copy_(sj_conv.bias)
+        return inst.to(sj_conv.weight.device)
+
+
+class PartialFusionConvBNLIF(_ConvPattern):
+    """Conv -> BN (eval, folded) -> LIF."""
+
+    policy_row = 2
+
+    def __init__(self, in_channels, out_channels, kernel_size, stride=1, padding=0, tau=2.0,
+                 v_threshold=1.0, v_reset=0.0, bn_eps=1e-5, decay_input=True, bias=False):
+        super().__init__()
+        self._setup(in_channels, out_channels, kernel_size, stride, padding, tau, v_threshold,
+                    v_reset, decay_input, has_bn=True, bn_eps=bn_eps, conv_bias=bias)
+        self.bn_weight = nn.Parameter(torch.ones(out_channels))
+        self.bn_bias = nn.Parameter(torch.zeros(out_channels))
+        self.register_buffer("running_mean", torch.zeros(out_channels))
+        self.register_buffer("running_var", torch.ones(out_channels))
+        self._impl = _dense_impl()
+
+    def _bn_tensors(self):
+        return (self.bn_weight, self.bn_bias, self.running_mean, self.running_var)
+
+    def forward(self, x, sew_identity=None):
+        if sew_identity is not None:
+            return self._run(self._impl, x, identity=sew_identity, identity_mode=ID_ADD_SPIKE)
+        return self._run(self._impl, x)
+
+    def supports_sew_identity(self):
+        return isinstance(self._impl, StreamFuse)
+
+    def _copy_bn(self, sj_bn):
+        with torch.no_grad():
+            if sj_bn.weight is not None:
+                self.bn_weight.copy_(sj_bn.weight)
+            if sj_bn.bias is not None:
+                self.bn_bias.copy_(sj_bn.bias)
+            self.running_mean.copy_(sj_bn.running_mean)
+            self.running_var.copy_(sj_bn.running_var)
+
+    @classmethod
+    def from_sj_modules(cls, sj_conv, sj_bn, sj_lif):
+        k, s, p = conv_geometry(sj_conv)
+        inst = cls(sj_conv.in_channels, sj_conv.out_channels, k, s, p, bn_eps=sj_bn.eps,
+                   bias=sj_conv.bias is not None, **lif_params(sj_lif))
+        with torch.no_grad():
+            inst.weight.copy_(sj_conv.weight)
+            if sj_conv.bias is not None:
+                inst.conv_bias.copy_(sj_conv.bias)
+        inst._copy_bn(sj_bn)
+        return inst.to(sj_conv.weight.device)
+
+
+class PartialFusionConvBNAddLIF(PartialFusionConvBNLIF):
+    """Conv -> BN -> (+ identity) -> LIF, the second half of a spiking-ResNet
+    block; identity is added to z inside the conv epilogue."""
+
+    policy_row = 9
+
+    def __init__(self, *args, **kw):
+        super().__init__(*args, **kw)
+        self._impl = StreamFuse()
+
+    def forward(self, x, identity):
+        return self._run(self._impl, x, identity=identity.contiguous(), identity_mode=ID_ADD_Z)
+
+
+class PartialFusionConvBNAvgPoolLIF(PartialFusionConvBNLIF):
+    """Conv -> BN -> AvgPool2d(2, 2) -> LIF: the conv writes z (MFMA, BN in
+    the epilogue), the pooled LIF runs in one streaming kernel."""
+
+    policy_row = "ConvBNAvgPoolLIF"
+
+    def forward(self, x):
+        squeeze = x.ndim == 4
+        if squeeze:
+            x = x.unsqueeze(0)
+        params = self._ensure_params()
+        impl = self._impl
+        r = impl.runner(self.spec, params, x.device)
+        if impl.input_is_analog(x):
+            z, _ = r.run_direct(x, epilogue=EPI_Z)
+        else:
+            z, _ = r.run_mfma(x.contiguous(), epilogue=EPI_Z, static_zero=True)
+        T, B, C, H, W = z.shape
+        v_in = self.state.peek((B, C, H // 2, W // 2), z.device)
+        s, v = avgpool2x2_lif(z, v_in, tau=self.tau, v_threshold=self.v_threshold,
+                              v_reset=self.v_reset, decay_input=self.decay_input)
+        self.state.set(v)
+        return s.squeeze(0) if squeeze else s
+
+    @classmethod
+    def from_sj_modules(cls, sj_conv, sj_bn, sj_pool, sj_lif):
+        inst = super().from_sj_modules(sj_conv, sj_bn, sj_lif)
+        ks, st = _first(sj_pool.kernel_size), _first(sj_pool.stride or sj_pool.kernel_size)
+        if ks != 2 or st != 2 or _first(getattr(sj_pool, "padding", 0)) != 0:
+            raise ValueError("only AvgPool2d(2, 2) is fused")
+        return inst
+
+
+# ---------------------------------------------------------------------------
+# Linear -> LIF
+# ---------------------------------------------------------------------------
+
+class FusedLinearLIF(CTFPattern):
+    """Linear (+bias) -> LIF on [T, B, I]; the linear runs on the matrix
+    cores as a 1x1 convolution over B one-pixel images, the LIF in its
+    epilogue."""
+
+    policy_row = 4
+
+    def __init__(self, in_features, out_features, tau=2.0, v_threshold=1.0, v_reset=0.0,
+                 decay_input=True, bias=True):
+        super().__init__()
+        self.in_features, self.out_features = int(in_features), int(out_features)
+        self.tau, self.v_threshold = float(tau), float(v_threshold)
+        self.v_reset = None if v_reset is None else float(v_reset)
+        self.decay_input = bool(decay_input)
+        self.weight_io = nn.Parameter(torch.empty(in_features, out_features))
+        nn.init.kaiming_normal_(self.weight_io.T)
+        self.bias = nn.Parameter(torch.zeros(out_features)) if bias else None
+        self.state = StateBuffer()
+        self._register_state(self.state)
+        self.spec = ConvLIFSpec(self.in_features, self.out_features, 1, 1, 0,
+                                has_conv_bias=bool(bias), has_bn=False, tau=self.tau,
+                                v_threshold=self.v_threshold, v_reset=self.v_reset,
+                                decay_input=self.decay_input)
+        self._impl = StreamFuse()
+        self._params = None
+        self._params_key = None
+
+    def _ensure_params(self):
+        key = (id(self.weight_io), self.weight_io._version,
+               None if self.bias is None else (id(self.bias), self.bias._version))
+        if self._params_key != key:
+            w = self.weight_io.detach().t().contiguous().view(self.out_features, self.in_features, 1, 1)
+            self._params = ConvLIFParams(w, self.bias, None, None)
+            self._params_key = key
+        return self._params
+
+    def forward(self, x):
+        squeeze = x.ndim == 2
+        if squeeze:
+            x = x.unsqueeze(0)
+        T, B, I = x.shape
+        y = self._impl.forward(x.reshape(T, B, I, 1, 1), self.spec, self._ensure_params(),
+                               self.state)
+        y = y.reshape(T, B, self.out_features)
+        return y.squeeze(0) if squeeze else y
+
+    @classmethod
+    def from_sj_modules(cls, sj_linear, sj_lif):
+        inst = cls(sj_linear.in_features, sj_linear.out_features,
+                   bias=sj_linear.bias is not None, **lif_params(sj_lif))
+        with torch.no_grad():
+            inst.weight_io.copy_(sj_linear.weight.t())
+            if sj_linear.bias is not None:
+                inst.bias.copy_(sj_linear.bias)
+        return inst.to(sj_linear.weight.device)
+
+
+# ---------------------------------------------------------------------------
+# streaming tails: Add -> LIF, Add -> BN -> LIF, AvgPool -> LIF
+# ---------------------------------------------------------------------------
+
+class _TailPattern(CTFPattern):
+    def _lif_setup(self, tau, v_threshold, v_reset, decay_input):
+        self.tau, self.v_threshold = float(tau), float(v_threshold)
+        self.v_reset = None if v_reset is None else float(v_reset)
+        self.decay_input = bool(decay_input)
+        self.state = StateBuffer()
+        self._register_state(self.state)
+
+    def _lif(self, z, **kw):
+        v_in = self.state.peek(z.shape[1:], z.device)
+        s, v = lif_multistep(z, v_in, tau=self.tau, v_threshold=self.v_threshold,
+                             v_reset=self.v_reset, decay_input=self.decay_input, **kw)
+        self.state.set(v)
+        return s
+
+
+class FusedAddLIF(_TailPattern):
+    """a + x -> LIF (catfuse/kernels/add_lif.py:63-151)."""
+
+    policy_row = 5
+
+    def __init__(self, tau=2.0, v_threshold=1.0, v_reset=0.0, decay_input=True):
+        super().__init__()
+        self._lif_setup(tau, v_threshold, v_reset, decay_input)
+
+    def forward(self, a, x):
+        return self._lif(a.contiguous(), mode=3, z2=x.contiguous())
+
+    @classmethod
+    def from_sj_modules(cls, sj_lif):
+        return cls(**lif_params(sj_lif))
+
+
+class FusedAddBNLIF(_TailPattern):
+    """(a + x) -> BN (eval) -> LIF (benchmarks/add_bn_lif_min.py:72-226)."""
+
+    policy_row = 6
+
+    def __init__(self, num_features, tau=2.0, v_threshold=1.0, v_reset=0.0, bn_eps=1e-5,
+                 decay_input=True):
+        super().__init__()
+        self._lif_setup(tau, v_threshold, v_reset, decay_input)
+        self.num_features = int(num_features)
+        self.bn_eps = float(bn_eps)
+        self.bn_weight = nn.Parameter(torch.ones(num_features))
+        self.bn_bias = nn.Parameter(torch.zeros(num_features))
+        self.register_buffer("running_mean", torch.zeros(num_features))
+        self.register_buffer("running_var", torch.ones(num_features))
+
+    def forward(self, a, x):
+        scale, shift = fold_bn(self.bn_weight, self.bn_bias, self.running_mean, self.running_var,
+                               self.bn_eps)
+        T, B, C = a.shape[:3]
+        hw = a[0, 0, 0].numel()
+        return self._lif(a.contiguous(), mode=4, z2=x.contiguous(), scale=scale.contiguous(),
+                         shift=shift.contiguous(), channels=C, hw=hw)
+
+    @classmethod
+    def from_sj_modules(cls, sj_bn, sj_lif):
+        inst = cls(sj_bn.num_features, bn_eps=sj_bn.eps, **lif_params(sj_lif))
+        with torch.no_grad():
+            inst.bn_weight.copy_(sj_bn.weight)
+            inst.bn_bias.copy_(sj_bn.bias)
+            inst.running_mean.copy_(sj_bn.running_mean)
+            inst.running_var.copy_(sj_bn.running_var)
+        return inst.to(sj_bn.running_mean.device)
+
+
+class FusedAvgPoolLIF(_TailPattern):
+    """AvgPool2d(2, 2) -> LIF (catfuse/kernels/avgpool_lif.py:61-190)."""
+
+    policy_row = 7
+
+    def __init__(self, tau=2.0, v_threshold=1.0, v_reset=0.0, decay_input=True):
+        super().__init__()
+        self._lif_setup(tau, v_threshold, v_reset, decay_input)
+
+    def forward(self, x):
+        T, B, C, H, W = x.shape
+        v_in = self.state.peek((B, C, H // 2, W // 2), x.device)
+        s, v = avgpool2x2_lif(x.contiguous(), v_in, tau=self.tau, v_threshold=self.v_threshold,
+                              v_reset=self.v_reset, decay_input=self.decay_input)
+        self.state.set(v)
+        return s
+
+    @classmethod
+    def from_sj_modules(cls, sj_pool, sj_lif):
+        if _first(sj_pool.kernel_size) != 2 or _first(sj_pool.stride or 2) != 2:
+            raise ValueError("only AvgPool2d(2, 2) is fused")
+        return cls(**lif_params(sj_lif))
+
+
+# ---------------------------------------------------------------------------
+# blocks
+# ---------------------------------------------------------------------------
+
+def _conv_bn_lif_from(conv, bn, lif, K=None):
+    """STFusionConvBNLIF for 3x3/s1 layers in the SparseFlow regime is chosen
+    by substitute_sf; blocks built here use the dense pattern."""
+    return PartialFusionConvBNLIF.from_sj_modules(conv, bn, lif)
+
+
+class CTFSEWBasicBlock(CTFPattern):
+    """SEW-ResNet BasicBlock: out = sew(identity, LIF(BN(conv2(LIF(BN(conv1 x))))))
+    with identity = downsample_sn(downsample(x)) or x; for cnf='ADD' the add
+    is done in conv2's epilogue."""
+
+    def __init__(self, fused_first, fused_second, fused_downsample, cnf):
+        super().__init__()
+        self.fused_first = fused_first
+        self.fused_second = fused_second
+        self.fused_downsample = fused_downsample
+        self.cnf = cnf
+
+    def forward(self, x):
+        out = self.fused_first(x)
+        identity = self.fused_downsample(x) if self.fused_downsample is not None else x
+        second = self.fused_second
+        if (self.cnf == "ADD" and getattr(second, "supports_sew_identity", lambda: False)()
+                and identity.shape[:2] == out.shape[:2]):
+            return second(out, sew_identity=identity.contiguous())
+        return sew_function(identity, second(out), self.cnf)
+
+    @classmethod
+    def from_sj_block(cls, sj_block):
+        first = _conv_bn_lif_from(sj_block.conv1, sj_block.bn1, sj_block.sn1)
+        second = _conv_bn_lif_from(sj_block.conv2, sj_block.bn2, sj_block.sn2)
+        ds = None
+        if sj_block.downsample is not None:
+            ds = PartialFusionConvBNLIF.from_sj_modules(sj_block.downsample[0],
+                                                        sj_block.downsample[1],
+                                                        sj_block.downsample_sn)
+        return cls(first, second, ds, sj_block.cnf)
+
+
+class _DownsampleConvBN(nn.Module):
+    """Conv -> BN without LIF (spiking-ResNet shortcut), z from the MFMA conv."""
+
+    def __init__(self, weight, bn_scale, bn_bias, stride, padding):
+        super().__init__()
+        self.weight = nn.Parameter(weight.detach().clone())
+        self.register_buffer("bn_scale", bn_scale.detach().clone())
+        self.register_buffer("bn_bias", bn_bias.detach().clone())
+        self.stride, self.padding = int(stride), int(padding)
+        self._runner = None
+        self._key = None
+
+    def forward(self, x):
+        key = (id(self.weight), self.weight._version, id(self.bn_scale), id(self.bn_bias))
+        if self._key != key:
+            self._runner = ConvLIFRunner(self.weight, self.bn_scale, self.bn_bias, None,
+                                         self.stride, self.padding, 2.0, 1.0, 0.0, True)
+            self._key = key
+        z, _ = self._runner.run_mfma(x.contiguous(), epilogue=EPI_Z, static_zero=True)
+        return z
+
+
+class CTFSpikingBasicBlock(CTFPattern):
+    """Spiking-ResNet BasicBlock: LIF(BN(conv2(LIF(BN(conv1 x)))) + identity),
+    identity = BN(conv_ds(x)) or x (no LIF on the shortcut)."""
+
+    def __init__(self, fused_first, fused_second_add, downsample_conv_weight, downsample_bn_scale,
+                 downsample_bn_bias, downsample_stride, downsample_padding):
+        super().__init__()
+        self.fused_first = fused_first
+        self.fused_second_add = fused_second_add
+        self.has_downsample = downsample_conv_weight is not None
+        self.downsample = (_DownsampleConvBN(downsample_conv_weight, downsample_bn_scale,
+                                             downsample_bn_bias, downsample_stride,
+                                             downsample_padding)
+                           if self.has_downsample else None)
+
+    def forward(self, x):
+        out = self.fused_first(x)
+        identity = self.downsample(x) if self.has_downsample else x
+        return self.fused_second_add(out, identity)
+
+    @classmethod
+    def from_sj_block(cls, sj_block):
+        first = PartialFusionConvBNLIF.from_sj_modules(sj_block.conv1, sj_block.bn1, sj_block.sn1)
+        second = PartialFusionConvBNAddLIF.from_sj_modules(sj_block.conv2, sj_block.bn2,
+                                                           sj_block.sn2)
+        if sj_block.downsample is None:
+            return cls(first, second, None, None, None, 0, 0)
+        c, b = sj_block.downsample[0], sj_block.downsample[1]
+        sc, sh = fold_bn(b.weight, b.bias, b.running_mean, b.running_var, b.eps)
+        k, s, p = conv_geometry(c)
+        return cls(first, second, c.weight.data, sc, sh, s, p)
+
+
+class CTFSEWBottleneck(CTFPattern):
+    """SEW-ResNet Bottleneck: three Conv-BN-LIF stages + SEW connect."""
+
+    def __init__(self, fused_first, fused_middle, fused_last, fused_downsample, cnf):
+        super().__init__()
+        self.fused_first = fused_first
+        self.fused_middle = fused_middle
+        self.fused_last = fused_last
+        self.fused_downsample = fused_downsample
+        self.cnf = cnf
+
+    def forward(self, x):
+        out = self.fused_middle(self.fused_first(x))
+        identity = self.fused_downsample(x) if self.fused_downsample is not None else x
+        if self.cnf == "ADD" and self.fused_last.supports_sew_identity():
+            return self.fused_last(out, sew_identity=identity.contiguous())
+        return sew_function(identity, self.fused_last(out), self.cnf)
+
+    @classmethod
+    def from_sj_block(cls, b):
+        mk = PartialFusionConvBNLIF.from_sj_modules
+        ds = None
+        if b.downsample is not None:
+            ds = mk(b.downsample[0], b.downsample[1], b.downsample_sn)
+        return cls(mk(b.conv1, b.bn1, b.sn1), mk(b.conv2, b.bn2, b.sn2), mk(b.conv3, b.bn3, b.sn3),
+                   ds, b.cnf)
+
+
+class CTFSpikingBottleneck(CTFPattern):
+    """Spiking-ResNet Bottleneck: LIF(BN(conv3(...)) + identity) last."""
+
+    def __init__(self, fused_first, fused_middle, fused_last_add, downsample_conv_weight,
+                 downsample_bn_scale, downsample_bn_bias, downsample_stride, downsample_padding):
+        super().__init__()
+        self.fused_first = fused_first
+        self.fused_middle = fused_middle
+        self.fused_last_add = fused_last_add
+        self.has_downsample = downsample_conv_weight is not None
+        self.downsample = (_DownsampleConvBN(downsample_conv_weight, downsample_bn_scale,
+                                             downsample_bn_bias, downsample_stride,
+                                             downsample_padding)
+                           if self.has_downsample else None)
+
+    def forward(self, x):
+        out = self.fused_middle(self.fused_first(x))
+        identity = self.downsample(x) if self.has_downsample else x
+        return self.fused_last_add(out, identity)
+
+    @classmethod
+    def from_sj_block(cls, b):
+        mk = PartialFusionConvBNLIF.from_sj_modules
+        last = PartialFusionConvBNAddLIF.from_sj_modules(b.conv3, b.bn3, b.sn3)
+        if b.downsample is None:
+            return cls(mk(b.conv1, b.bn1, b.sn1), mk(b.conv2, b.bn2, b.sn2), last,
+                       None, None, None, 0, 0)
+        c, bn = b.downsample[0], b.downsample[1]
+        sc, sh = fold_bn(bn.weight, bn.bias, bn.running_mean, bn.running_var, bn.eps)
+        k, s, p = conv_geometry(c)
+        return cls(mk(b.conv1, b.bn1, b.sn1), mk(b.conv2, b.bn2, b.sn2), last, c.weight.data,
+                   sc, sh, s, p)
+
+
+PATTERN_REGISTRY = {
+    "PartialFusionConvLIF": PartialFusionConvLIF,
+    "PartialFusionConvBNLIF": PartialFusionConvBNLIF,
+    "PartialFusionConvBNAddLIF": PartialFusionConvBNAddLIF,
+    "PartialFusionConvBNAvgPoolLIF": PartialFusionConvBNAvgPoolLIF,
+    "FusedLinearLIF": FusedLinearLIF,
+    "FusedAddLIF": FusedAddLIF,
+    "FusedAddBNLIF": FusedAddBNLIF,
+    "FusedAvgPoolLIF": FusedAvgPoolLIF,
+    "CTFSEWBasicBlock": CTFSEWBasicBlock,
+    "CTFSpikingBasicBlock": CTFSpikingBasicBlock,
+    "CTFSEWBottleneck": CTFSEWBottleneck,
+    "CTFSpikingBottleneck": CTFSpikingBottleneck,
+}
+
+from catfuse_amd.sparseflow.ops.st_fusion_conv_bn_lif import STFusionConvBNLIF  # noqa: E402
+
+PATTERN_REGISTRY["STFusionConvBNLIF"] = STFusionConvBNLIF
+
+__all__ = ["CTFPattern", "PartialFusionConvLIF", "PartialFusionConvBNLIF",
+           "PartialFusionConvBNAddLIF", "PartialFusionConvBNAvgPoolLIF", "FusedLinearLIF",
+           "FusedAddLIF", "FusedAddBNLIF", "FusedAvgPoolLIF", "CTFSEWBasicBlock",
+           "CTFSpikingBasicBlock", "CTFSEWBottleneck", "CTFSpikingBottleneck",
+           "STFusionConvBNLIF", "PATTERN_REGISTRY", "fold_bn", "lif_params", "conv_geometry"]

@@ -19,10 +19,63 @@ from catfuse_amd import _hip
 from catfuse_amd._hip import check, ptr, require_gpu_tensor
 
 EPI_LIF, EPI_Z = 0, 1
+ID_ADD_SPIKE, ID_ADD_Z = 1, 2
 ROUTE_ZERO, ROUTE_SPARSE, ROUTE_DENSE = 0, 1, 2
 STATUS_INEXACT_FP16 = 1
 
 _status_words: dict = {}
+
+
+class KernelTimer:
+    """Optional live timing of kernel launches with HIP events recorded on
+    the launch stream (torch's current stream, which every wrapper here
+    launches on).  Each record carries the launch's algorithmic work (FLOPs
+    and/or bytes) so callers can report achieved rates per kernel."""
+
+    def __init__(self):
+        self.records = []   # (name, start_event, end_event, flops, bytes)
+
+    def start(self):
+        ev = torch.cuda.Event(enable_timing=True)
+        ev.record()
+        return ev
+
+    def stop(self, name, ev0, flops=0, nbytes=0):
+        ev1 = torch.cuda.Event(enable_timing=True)
+        ev1.record()
+        self.records.append((name, ev0, ev1, int(flops), int(nbytes)))
+
+    def summary(self):
+        """{name: dict(launches, ms_total, ms_avg, flops, bytes)} (synchronises)."""
+        torch.cuda.synchronize()
+        out = {}
+        for name, e0, e1, fl, nb in self.records:
+            d = out.setdefault(name, dict(launches=0, ms_total=0.0, flops=0, bytes=0))
+            d["launches"] += 1
+            d["ms_total"] += e0.elapsed_time(e1)
+            d["flops"] += fl
+            d["bytes"] += nb
+        for d in out.values():
+            d["ms_avg"] = d["ms_total"] / max(1, d["launches"])
+        return out
+
+
+_timer = None
+
+
+def set_timer(timer):
+    """Install (or remove with None) the process-wide KernelTimer."""
+    global _timer
+    _timer = timer
+
+
+def _t0():
+    return _timer.start() if _timer is not None else None
+
+
+def _t1(name, ev0, flops=0, nbytes=0):
+    if ev0 is not None:
+        _timer.stop(name, ev0, flops, nbytes)
 
 
 def status_word(device) -> torch.Tensor:
@@ -85,11 +138,15 @@ def lif_multistep(z: torch.Tensor, v_in: Optional[torch.Tensor] = None, *, tau=2
         raise TypeError("spike_dtype must be float32 or uint8")
     spikes = torch.empty(z.shape, dtype=spike_dtype, device=z.device)
     v_out = torch.empty(z.shape[1:], dtype=torch.float32, device=z.device) if want_v_out else None
+    ev = _t0()
     rc = _hip.lib().cf_lif_multistep(ptr(z), ptr(z2), ptr(scale), ptr(shift), int(mode), ptr(v_in),
                                      ptr(spikes), sd, ptr(v_out), T, N, int(channels), int(hw),
                                      *_lif_args(tau, v_threshold, v_reset, decay_input),
                                      _hip.stream(z.device))
     check(rc, "cf_lif_multistep")
+    nbytes = T * N * (4 + (4 if z2 is not None else 0) + spikes.element_size()) + \
+        4 * N * ((v_in is not None) + (v_out is not None))
+    _t1(f"lif_multistep_mode{mode}", ev, nbytes=nbytes)
     return spikes, v_out
 
 
@@ -110,10 +167,14 @@ def avgpool2x2_lif(x: torch.Tensor, v_in: Optional[torch.Tensor] = None, *, tau=
     sd = {torch.float32: 0, torch.uint8: 1}[spike_dtype]
     spikes = torch.empty((T, B, C, Ho, Wo), dtype=spike_dtype, device=x.device)
     v_out = torch.empty((B, C, Ho, Wo), dtype=torch.float32, device=x.device)
+    ev = _t0()
     rc = _hip.lib().cf_avgpool2x2_lif(ptr(x), ptr(v_in), ptr(spikes), sd, ptr(v_out), T, B * C, H,
                                       W, *_lif_args(tau, v_threshold, v_reset, decay_input),
                                       _hip.stream(x.device))
     check(rc, "cf_avgpool2x2_lif")
+    n_out = B * C * Ho * Wo
+    _t1("avgpool2x2_lif", ev, nbytes=T * n_out * (16 + spikes.element_size()) +
+        4 * n_out * (1 + (v_in is not None)))
     return spikes, v_out
 
 
@@ -142,9 +203,12 @@ def pack_input(x4: torch.Tensor, *, cp: Optional[int] = None, want_xp=True, grou
     if group_size > 0:
         act = act_out if act_out is not None else torch.empty((NB, H, W), dtype=torch.int32,
                                                               device=x4.device)
+    ev = _t0()
     rc = _hip.lib().cf_pack_input(ptr(x4), NB, C, H, W, cp, ptr(xp), ptr(act), int(group_size),
                                   float(threshold), ptr(nnz), ptr(status), _hip.stream(x4.device))
     check(rc, "cf_pack_input")
+    _t1("pack_input", ev, nbytes=4 * NB * C * H * W + (2 * NB * H * W * cp if xp is not None else 0)
+        + (4 * NB * H * W if act is not None else 0))
     return xp, act
 
 
@@ -160,10 +224,12 @@ def prescan_tiles(act: torch.Tensor, H: int, W: int, H_out: int, W_out: int, ker
                                                                       device=act.device)
     if ag.numel() < n or tc.numel() < n:
         raise ValueError("prescan output buffers are too small")
+    ev = _t0()
     rc = _hip.lib().cf_prescan_tiles(ptr(act), NB, H, W, H_out, W_out, kernel_size, stride,
                                      padding, block_h, block_w, num_groups, ptr(ag), ptr(tc),
                                      _hip.stream(act.device))
     check(rc, "cf_prescan_tiles")
+    _t1("prescan_tiles", ev, nbytes=4 * NB * H * W + 8 * n)
     return tc[:n], ag[:n]
 
 
@@ -255,7 +321,8 @@ class ConvLIFRunner:
         return t
 
     def run_mfma(self, x: torch.Tensor, v_in=None, *, epilogue=EPI_LIF, want_v_out=True,
-                 identity=None, sparse=None, sparse_threshold=0.7, static_zero=True):
+                 identity=None, identity_mode=ID_ADD_SPIKE, sparse=None, sparse_threshold=0.7,
+                 static_zero=True):
         """x [T, B, Cin, H, W] fp32 (values exact in fp16).  sparse: None for
         flat dense tiles, or a dict with block_h, block_w, group_size to run
         the prescan and SparseFlow chunk skipping.  Returns (out, v_out)."""
@@ -300,12 +367,16 @@ class ConvLIFRunner:
         out = torch.empty((T, B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
         v_out = (torch.empty((B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
                  if (epilogue == EPI_LIF and want_v_out) else None)
+        ev = _t0()
         rc = _hip.lib().cf_conv_mfma(
             ptr(xp), ptr(self.w_packed), ptr(self.alpha), ptr(self.beta), ptr(v_in), ptr(v_out),
-            ptr(out), ptr(identity), ptr(ag), ptr(nnz), x.numel(), float(sparse_threshold),
-            T, B, self.Cp, self.Cout, self.Coutp, H, W, Ho, Wo, self.KH, self.KW, self.stride,
-            self.padding, B, th, tw, gs, int(epilogue), *self.lif, _hip.stream(dev))
+            ptr(out), ptr(identity), int(identity_mode), ptr(ag), ptr(nnz), x.numel(),
+            float(sparse_threshold), T, B, self.Cp, self.Cout, self.Coutp, H, W, Ho, Wo, self.KH,
+            self.KW, self.stride, self.padding, B, th, tw, gs, int(epilogue), *self.lif,
+            _hip.stream(dev))
         check(rc, "cf_conv_mfma")
+        _t1("conv_mfma" + ("_sparse" if sparse is not None else ""), ev,
+            flops=2 * T * B * Ho * Wo * self.Cout * self.Cin * self.KH * self.KW)
         self.last_nnz = nnz
         self.last_tiles = None if ag is None else (tc_buf, ag)
         return out, v_out
@@ -331,9 +402,12 @@ class ConvLIFRunner:
         out = torch.empty((T, B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
         v_out = (torch.empty((B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
                  if (epilogue == EPI_LIF and want_v_out) else None)
+        ev = _t0()
         rc = _hip.lib().cf_conv_direct(
             ptr(xb), ptr(self._w_f32), ptr(self.alpha_direct), ptr(self.beta_direct), ptr(v_in),
             ptr(v_out), ptr(out), T, B, C, self.Cout, H, W, Ho, Wo, self.KH, self.KW,
             self.stride, self.padding, tstride, int(epilogue), *self.lif, _hip.stream(dev))
         check(rc, "cf_conv_direct")
+        _t1("conv_direct", ev, flops=2 * (1 if tstride == 0 else T) * B * Ho * Wo * self.Cout *
+            C * self.KH * self.KW)
         return out, v_out

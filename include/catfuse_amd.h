@@ -112,8 +112,11 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
 /* Fused Conv -> BN -> LIF (epilogue 0) or Conv -> BN -> z (epilogue 1) on
  * the matrix cores, all T steps in one launch.
  *   x: NHWC16 [T*x_img_tstride + B][H][W][Cp] from cf_pack_input;
- *   out: NCHW [T][B][Cout][Ho][Wo] spikes (plus identity when non-NULL,
- *   the SEW ADD of catfuse/patterns.py:676-689) or z;
+ *   out: NCHW [T][B][Cout][Ho][Wo] spikes or z;
+ *   identity (nullable, NCHW like out): identity_mode 1 adds it to the
+ *   spikes (SEW ADD, catfuse/patterns.py:672-737), identity_mode 2 adds it
+ *   to z before the LIF (BN -> Add -> LIF,
+ *   catfuse/kernels/partial_fusion_conv_bn_add_lif_impl.py:76-123);
  *   v_in/v_out: [B][Cout][Ho][Wo] (nullable);
  *   tile_h/tile_w > 0 selects rectangular pixel tiles aligned with the
  *   prescan tiles (tile_h*tile_w in {64,128}) and enables SparseFlow chunk
@@ -126,7 +129,7 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
  * catfuse/sparseflow/fused_conv_bn_lif_kernel.py:342-539. */
 int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha, const float* beta,
                  const float* v_in, float* v_out, float* out, const float* identity,
-                 const int32_t* ag_mask, const unsigned long long* nnz, int64_t numel,
+                 int identity_mode, const int32_t* ag_mask, const unsigned long long* nnz, int64_t numel,
                  double sparse_threshold, int64_t T, int64_t B, int64_t Cp, int64_t Cout,
                  int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo, int64_t KH,
                  int64_t KW, int64_t stride, int64_t pad, int64_t x_img_tstride, int64_t tile_h,

@@ -1,0 +1,192 @@
+"""Host-side logic of the drop-in API (no GPU): policy table KATs, hardware
+profiles, IOCost known answers (tests/stage4_verify.py:120-124,181,247 and
+the analytic columns of experiments/results/k_sweep.csv, kept as a fixture),
+the schedule verifier cases (tests/stage5_verify.py:155-231), StateBuffer,
+and the substitution structure/routing stats on the model builders."""
+import csv
+import math
+import os
+
+import pytest
+import torch
+
+from catfuse_amd import hardware, policy, snn
+from catfuse_amd.implementations import (ConvLIFSpec, DenseKeep, ScheduleDecomposition,
+                                         ScheduleTransform, SparseFlow, StreamFuse)
+from catfuse_amd.state import StateBuffer
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+def test_policy_kats():
+    row = policy.get_policy("Conv3x3_BN_LIF", C_in=64, C_out=64, H=56, W=56)
+    assert row.spatial_backend == policy.SpatialBackend.DENSE_KEEP
+    row2 = policy.get_policy("Conv3x3_BN_LIF", C_in=512, C_out=512, H=7, W=7)
+    assert row2.spatial_backend == policy.SpatialBackend.SPARSE_FLOW
+    assert row2.K == 8
+    assert policy.get_policy("Linear_LIF", T=4).K == 4
+    assert policy.classify_shape_regime(64, 64, 56, 56, 1) == "memory_bound"
+    assert policy.classify_shape_regime(192, 192, 40, 40) == "compute_bound"
+    assert policy.classify_shape_regime(192, 192, 20, 20) == "memory_bound"
+    assert policy.optimal_K(16, "compute_bound") == 4
+    assert policy.optimal_K(4, "memory_bound") == 4
+    assert abs(policy.io_ratio_partial_fusion(4) - 3.5 / 7) < 1e-12
+    assert abs(policy.io_ratio_full_fusion(8) - 1.25 / 5) < 1e-12
+    # unknown pattern -> conservative partial fusion with K = min(4, T)
+    r = policy.get_policy("Conv5x5_BN_LIF", C_in=64, H=8, W=8, T=2)
+    assert (r.K, r.spatial_backend) == (2, policy.SpatialBackend.DENSE_KEEP)
+
+
+def test_hardware_profiles():
+    assert hardware.DEFAULT is hardware.V100_PCIE_32GB
+    assert hardware.MI355X.gcn_arch == "gfx950"
+    assert hardware.MI355X.hbm_bandwidth_gbps == 8000.0
+    assert hardware.A100_40GB.sm_capability == 80
+    p = hardware.detect_hardware()
+    assert isinstance(p, hardware.HardwareProfile)
+
+
+SPEC = ConvLIFSpec(256, 256, 3, 1, 1, has_conv_bias=False, has_bn=True, tau=2.0,
+                   v_threshold=1.0, v_reset=0.0)
+
+
+def test_iocost_dense_keep_kat():
+    c = DenseKeep().analytic_io_cost(SPEC, T=4, B=2, H_in=8, W_in=8, dtype_bytes=4)
+    assert (c.x_load, c.w_load, c.z_io, c.v_io, c.spike_write) == \
+        (524_288, 2_359_296, 1_048_576, 262_144, 524_288)
+    assert c.total == 524_288 + 2_359_296 + 1_048_576 + 262_144 + 524_288
+    assert c.num_blocks == 1
+
+
+@pytest.mark.parametrize("impl_cls", [SparseFlow, StreamFuse])
+def test_iocost_fused_kat(impl_cls):
+    impl = impl_cls()
+    hwc = 8 * 8 * 256
+    for K in (1, 2, 4):
+        c = impl.analytic_io_cost(SPEC, T=4, B=2, H_in=8, W_in=8, K=K)
+        nb = math.ceil(4 / K)
+        assert c.z_io == 0 and c.v_io == 2 * nb * 2 * hwc * 4 and c.num_blocks == nb
+    dk = DenseKeep().analytic_io_cost(SPEC, 4, 2, 8, 8)
+    sf = impl.analytic_io_cost(SPEC, 4, 2, 8, 8, K=4)
+    assert abs(sf.intermediate_io / dk.intermediate_io - 1.0 / 5) < 1e-12   # 1/(T+1)
+
+
+def test_iocost_matches_k_sweep_fixture():
+    rows = list(csv.DictReader(open(os.path.join(GOLDEN, "k_sweep_analytic.csv"))))
+    assert len(rows) >= 16
+    for r in rows:
+        T, B, Cin, Cout, H, W, K = (int(r[k]) for k in ("T", "B", "Cin", "Cout", "H", "W", "K"))
+        spec = ConvLIFSpec(Cin, Cout, 3, 1, 1, False, True, 2.0, 1.0, 0.0)
+        impl = DenseKeep() if r["impl"] == "DenseKeep" else SparseFlow()
+        c = impl.analytic_io_cost(spec, T=T, B=B, H_in=H, W_in=W, K=K)
+        got = (c.num_blocks, c.x_load, c.w_load, c.z_io, c.v_io, c.spike_write,
+               c.intermediate_io, c.total)
+        want = tuple(int(r[k]) for k in ("num_blocks", "analytic_x_load", "analytic_w_load",
+                                         "analytic_z_io", "analytic_v_io",
+                                         "analytic_spike_write", "analytic_intermediate_io",
+                                         "analytic_total"))
+        assert got == want, (r["config"], r["impl"], K)
+
+
+def test_schedule_decompositions_verify():
+    for impl in (DenseKeep(), SparseFlow(), StreamFuse()):
+        for K in (1, 2, 4):
+            ok, errs = impl.schedule_decomposition(SPEC, T=4, K=K).verify()
+            assert ok, errs
+    assert DenseKeep().schedule_decomposition(SPEC, 4).form == "form_1"
+    assert str(SparseFlow().schedule_decomposition(SPEC, 4, 2)) == \
+        "TimeBlock(K=2) ∘ StreamFuse(Conv, LIF) ∘ StateCarry(LIF)"
+
+
+@pytest.mark.parametrize("transforms,marker", [
+    ((ScheduleTransform.BatchFold("LIF"), ScheduleTransform.TimeBlock(4)), "BatchFold(LIF) ILLEGAL"),
+    ((ScheduleTransform.StreamFuse("LIF", "Conv"), ScheduleTransform.TimeBlock(4)),
+     "StreamFuse(LIF, Conv) ILLEGAL"),
+    ((ScheduleTransform.StateCarry("Conv"), ScheduleTransform.TimeBlock(4)), "StateCarry(Conv) ILLEGAL"),
+    ((ScheduleTransform.BatchFold("Conv"),), "Missing TimeBlock"),
+    ((ScheduleTransform.StreamFuse("Conv", "LIF"), ScheduleTransform.TimeBlock(4)),
+     "without StateCarry(LIF)"),
+    ((ScheduleTransform.TimeBlock(0),), "K >= 1"),
+    ((ScheduleTransform.BatchFold("Attention"), ScheduleTransform.TimeBlock(4)),
+     "BatchFold(Attention) ILLEGAL"),
+])
+def test_schedule_verifier_rejects(transforms, marker):
+    ok, errs = ScheduleDecomposition(transforms=transforms, form="custom").verify()
+    assert not ok and any(marker in e for e in errs), errs
+
+
+def test_state_buffer_lifecycle():
+    s = StateBuffer()
+    assert not s.is_initialized and s.peek((2, 3), "cpu") is None
+    v = s.get((2, 3), "cpu")
+    assert v.shape == (2, 3) and (v == 0).all()
+    assert s.get((2, 3), "cpu") is v
+    assert s.get((3, 3), "cpu") is not v
+    s.set(torch.ones(3, 3, requires_grad=True))
+    assert not s.tensor.requires_grad and s.peek((3, 3), "cpu") is not None
+    s.reset()
+    assert s.tensor is None
+
+
+def _sew18():
+    g = torch.Generator().manual_seed(0)
+    m = snn.sew_resnet18(num_classes=10, cnf="ADD")
+    snn.functional.set_step_mode(m, "m")
+    snn.kaiming_init(m, g)
+    snn.randomize_bn(m, g)
+    return m.eval()
+
+
+def test_substitute_sf_sew_resnet18_routing():
+    import catfuse_amd
+    from catfuse_amd.patterns import CTFSEWBasicBlock, PartialFusionConvBNLIF, STFusionConvBNLIF
+    m = _sew18()
+    fused, stats = catfuse_amd.optimize(m, device=None, T=4)
+    assert stats["total_lif_nodes"] == 20 and stats["fused_lif_nodes"] == 20
+    assert stats["coverage_pct"] == 100.0
+    sf = sorted(r["name"] for r in stats["routing"] if r["pattern"] == "STFusionConvBNLIF")
+    assert sf == ["layer3.0.conv2", "layer3.1.conv1", "layer3.1.conv2", "layer4.0.conv2",
+                  "layer4.1.conv1", "layer4.1.conv2"]
+    labels = {r["name"]: r["backend"] for r in stats["routing"]}
+    assert labels["layer4.0.conv1"] == "DenseKeep"   # stride 2: built and labelled dense
+    assert sum(1 for b in labels.values() if b == "SparseFlow") == 6
+    assert isinstance(fused.conv1, PartialFusionConvBNLIF)
+    assert isinstance(fused.layer3[1].fused_second, STFusionConvBNLIF)
+    assert all(isinstance(b, CTFSEWBasicBlock) for l in (fused.layer1, fused.layer2, fused.layer3,
+                                                         fused.layer4) for b in l)
+    # the original model is untouched
+    assert type(m.layer1[0].sn1).__name__ == "LIFNode"
+
+
+def test_substitute_block_level():
+    import catfuse_amd
+    fused, stats = catfuse_amd.optimize(_sew18(), device=None, use_sparseflow=False)
+    assert stats["patterns_matched"]["CTFSEWBasicBlock"] == 8
+    assert stats["fused_lif_nodes"] == 19   # stem LIF is not inside a block/Sequential
+
+
+def test_root_sequential_is_rewritten():
+    import catfuse_amd
+    from catfuse_amd.patterns import CTFPattern
+    m = torch.nn.Sequential(snn.Conv2d(8, 8, 3, 1, 1, bias=False), snn.BatchNorm2d(8),
+                            snn.LIFNode(), snn.Linear(8, 4), snn.LIFNode())
+    for use_sf in (True, False):
+        fused, stats = catfuse_amd.optimize(m, device=None, T=4, use_sparseflow=use_sf)
+        assert stats["fused_lif_nodes"] == 2, stats
+        assert isinstance(fused, torch.nn.Sequential) and len(fused) == 2
+        assert all(isinstance(c, CTFPattern) for c in fused)
+
+
+def test_substitute_sf_vgg11():
+    import catfuse_amd
+    g = torch.Generator().manual_seed(0)
+    m = snn.spiking_vgg11_bn(num_classes=10)
+    snn.functional.set_step_mode(m, "m")
+    snn.kaiming_init(m, g)
+    snn.randomize_bn(m, g)
+    fused, stats = catfuse_amd.optimize(m.eval(), device=None, T=4)
+    pm = stats["patterns_matched"]
+    assert pm["PartialFusionConvBNAvgPoolLIF"] == 5
+    assert pm["FusedLinearLIF"] == 2
+    assert pm.get("PartialFusionConvBNLIF", 0) + pm.get("STFusionConvBNLIF", 0) == 3
+    assert stats["fused_lif_nodes"] == stats["total_lif_nodes"] == 10

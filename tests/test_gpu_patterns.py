@@ -1,0 +1,321 @@
+"""Drop-in pattern layer and whole networks on the GPU against the oracle.
+
+Network parity is checked layer by layer: every fused layer's recorded GPU
+input is fed to the oracle with the original SpikingJelly-style modules, so
+a rare near-threshold flip in one layer does not cascade into the next
+layer's comparison.  Implementations of one layer (DenseKeep, StreamFuse,
+SparseFlow, TimeBlock K-chunking) are compared bit-exactly with each other.
+"""
+import numpy as np
+import pytest
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+import oracle
+from parity import lif_parity
+
+pytestmark = pytest.mark.gpu
+
+
+def _gen(s):
+    return torch.Generator().manual_seed(s)
+
+
+def _init(model, seed=0):
+    from catfuse_amd import snn
+    g = _gen(seed)
+    snn.functional.set_step_mode(model, "m")
+    snn.kaiming_init(model, g)
+    snn.randomize_bn(model, g)
+    return model.eval()
+
+
+def _triple(Cin, Cout, k, s, p, seed=0, bias=False):
+    from catfuse_amd import snn
+    m = nn.Sequential(snn.Conv2d(Cin, Cout, k, s, p, bias=bias), snn.BatchNorm2d(Cout),
+                      snn.LIFNode(tau=2.0, v_threshold=1.0, v_reset=0.0))
+    _init(m, seed)
+    if bias:
+        with torch.no_grad():
+            m[0].bias.copy_(torch.randn(Cout, generator=_gen(seed + 1)) * 0.1)
+    return m
+
+
+# ---------------------------------------------------------------------------
+# single patterns
+# ---------------------------------------------------------------------------
+
+def test_partial_fusion_conv_bn_lif_c0(cuda):
+    from catfuse_amd.patterns import PartialFusionConvBNLIF
+    m = _triple(64, 64, 3, 1, 1, seed=1)
+    x = (torch.rand(4, 8, 64, 32, 32, generator=_gen(0)) < 0.15).float()
+    pat = PartialFusionConvBNLIF.from_sj_modules(*m).to(cuda)
+    out = pat(x.to(cuda))
+    s_ref, v_ref, h_ref = oracle.conv_bn_lif(x, *m)
+    lif_parity(out.cpu().numpy(), pat.state.tensor.cpu().numpy(), s_ref, v_ref, h_ref, what="C0")
+    pat.reset()
+    assert pat.state.tensor is None
+    out2 = pat(x.to(cuda))
+    assert torch.equal(out, out2)
+
+
+@pytest.mark.parametrize("rate", [0.0, 0.01, 0.05, 0.2, 0.5])
+def test_stfusion_c1_all_impls_bitwise(cuda, rate):
+    from catfuse_amd.implementations import DenseKeep, StreamFuse
+    from catfuse_amd.patterns import STFusionConvBNLIF
+    m = _triple(256, 256, 3, 1, 1, seed=2)
+    x = (torch.rand(4, 8, 256, 14, 14, generator=_gen(int(rate * 100))) < rate).float().to(cuda)
+    st = STFusionConvBNLIF.from_sj_modules(*m).to(cuda)
+    out_dev = st(x)
+    v_dev = st.state.tensor.clone()
+    ref = {}
+    for name, impl in (("DenseKeep", DenseKeep()), ("StreamFuse", StreamFuse())):
+        st.reset()
+        o = impl.forward(x, st.spec, st._ensure_params(), st.state)
+        ref[name] = (o, st.state.tensor.clone())
+    for name, (o, v) in ref.items():
+        assert torch.equal(o, out_dev), name
+        assert torch.equal(v, v_dev), name
+    expect_route = oracle.route(x.cpu())
+    assert st.last_route() == expect_route
+    st_host = STFusionConvBNLIF.from_sj_modules(*m, routing="host").to(cuda)
+    assert torch.equal(st_host(x), out_dev)
+    s_ref, v_ref, h_ref = oracle.conv_bn_lif(x.cpu(), *m)
+    lif_parity(out_dev.cpu().numpy(), v_dev.cpu().numpy(), s_ref, v_ref, h_ref, what="C1")
+
+
+@pytest.mark.parametrize("K", [1, 2, 3, 4])
+def test_timeblock_state_carry_bitwise(cuda, K):
+    from catfuse_amd.patterns import STFusionConvBNLIF
+    m = _triple(256, 256, 3, 1, 1, seed=3)
+    x = (torch.rand(4, 2, 256, 8, 8, generator=_gen(5)) < 0.1).float().to(cuda)
+    st = STFusionConvBNLIF.from_sj_modules(*m).to(cuda)
+    full = st(x)
+    v_full = st.state.tensor.clone()
+    st.reset()
+    chunked = st.forward_with_k(x, K)
+    assert torch.equal(chunked, full)
+    assert torch.equal(st.state.tensor, v_full)
+    # consecutive forward calls carry v exactly like one longer sequence
+    st.reset()
+    a = st(x[:2].contiguous())
+    b = st(x[2:].contiguous())
+    assert torch.equal(torch.cat([a, b]), full)
+
+
+def test_conv_bias_kept(cuda):
+    from catfuse_amd.patterns import PartialFusionConvBNLIF
+    m = _triple(32, 64, 3, 1, 1, seed=4, bias=True)
+    x = (torch.rand(2, 2, 32, 10, 10, generator=_gen(1)) < 0.3).float()
+    pat = PartialFusionConvBNLIF.from_sj_modules(*m).to(cuda)
+    out = pat(x.to(cuda))
+    s_ref, v_ref, h_ref = oracle.conv_bn_lif(x, *m)
+    lif_parity(out.cpu().numpy(), pat.state.tensor.cpu().numpy(), s_ref, v_ref, h_ref, what="bias")
+
+
+def test_fused_linear_lif(cuda):
+    from catfuse_amd import snn
+    from catfuse_amd.patterns import FusedLinearLIF
+    lin = snn.Linear(512, 256)
+    lif = snn.LIFNode()
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(256, 512, generator=_gen(2)) * (2 / 512) ** 0.5 * 2)
+        lin.bias.copy_(torch.randn(256, generator=_gen(3)) * 0.1)
+    x = (torch.rand(4, 16, 512, generator=_gen(4)) < 0.3).float()
+    pat = FusedLinearLIF.from_sj_modules(lin, lif).to(cuda)
+    out = pat(x.to(cuda))
+    z = F.linear(x.double(), lin.weight.double(), lin.bias.double()).float()
+    s_ref, v_ref, h_ref = oracle.lif_multistep(z)
+    lif_parity(out.cpu().numpy(), pat.state.tensor.cpu().numpy(), s_ref, v_ref, h_ref,
+               what="linear")
+
+
+def test_tail_patterns_bit_exact(cuda):
+    from catfuse_amd import snn
+    from catfuse_amd.patterns import FusedAddBNLIF, FusedAddLIF, FusedAvgPoolLIF
+    g = _gen(6)
+    a = torch.randn(4, 2, 8, 6, 6, generator=g)
+    b = torch.randn(4, 2, 8, 6, 6, generator=g)
+    lif = snn.LIFNode()
+    out = FusedAddLIF.from_sj_modules(lif)(a.to(cuda), b.to(cuda))
+    np.testing.assert_array_equal(out.cpu().numpy(), oracle.lif_multistep(a + b)[0])
+    bn = snn.BatchNorm2d(8)
+    _init(nn.Sequential(bn), 7)
+    pat = FusedAddBNLIF.from_sj_modules(bn, lif).to(cuda)
+    out = pat(a.to(cuda), b.to(cuda))
+    sc = pat.bn_weight * (1.0 / torch.sqrt(pat.running_var + pat.bn_eps))
+    sh = pat.bn_bias - pat.running_mean * sc
+    ref = oracle.lif_multistep(a, mode=4, z2=b, scale=sc.cpu(), shift=sh.cpu(), C=8, HW=36)[0]
+    np.testing.assert_array_equal(out.cpu().numpy(), ref)
+    x = torch.rand(4, 2, 8, 6, 6, generator=g) * 3
+    out = FusedAvgPoolLIF.from_sj_modules(snn.AvgPool2d(2, 2), lif)(x.to(cuda))
+    z = F.avg_pool2d(x.flatten(0, 1), 2).reshape(4, 2, 8, 3, 3)
+    np.testing.assert_array_equal(out.cpu().numpy(), oracle.lif_multistep(z)[0])
+
+
+def test_functional_kernel_api(cuda):
+    from catfuse_amd import kernels
+    m = _triple(64, 64, 3, 1, 1, seed=9)
+    conv, bn, lif = m
+    x = (torch.rand(4, 2, 64, 12, 12, generator=_gen(9)) < 0.2).float()
+    out = kernels.partial_fusion_conv_bn_lif(
+        x.to(cuda), conv.weight.detach().to(cuda), bn.weight.detach().to(cuda),
+        bn.bias.detach().to(cuda), bn.running_mean.to(cuda), bn.running_var.to(cuda), bn.eps)
+    s_ref, v_ref, h_ref = oracle.conv_bn_lif(x, conv, bn, lif)
+    lif_parity(out.cpu().numpy(), None, s_ref, None, h_ref, what="functional")
+    s, v = kernels.add_lif(x.to(cuda), x.to(cuda))
+    np.testing.assert_array_equal(s.cpu().numpy(), oracle.lif_multistep(x + x)[0])
+
+
+# ---------------------------------------------------------------------------
+# networks
+# ---------------------------------------------------------------------------
+
+def _hook_layers(pairs):
+    """pairs: [(fused_module, (conv, bn, lif), kind)] -> records list."""
+    recs, handles = [], []
+    for fm, orig, kind in pairs:
+        def hook(mod, args, kwargs, out, orig=orig, kind=kind):
+            recs.append((kind, orig, args[0].detach().cpu(), kwargs.get("sew_identity"),
+                         out.detach().cpu()))
+        handles.append(fm.register_forward_hook(hook, with_kwargs=True))
+    return recs, handles
+
+
+def _check_records(recs):
+    flips = 0
+    for kind, orig, x, ident, out in recs:
+        if kind == "conv":
+            s_ref, _, h_ref = oracle.conv_bn_lif(x, *orig)
+        elif kind == "conv_pool":
+            conv, bn, pool, lif = orig
+            T, B = x.shape[:2]
+            z = oracle.batch_norm(oracle.conv2d(x.flatten(0, 1), conv.weight, conv.bias,
+                                                conv.stride[0], conv.padding[0]), bn)
+            z = F.avg_pool2d(z, 2, 2)
+            s_ref, _, h_ref = oracle.lif_multistep(z.reshape(T, B, *z.shape[1:]))
+        else:  # linear
+            lin, lif = orig
+            z = F.linear(x.double(), lin.weight.detach().double(),
+                         None if lin.bias is None else lin.bias.detach().double()).float()
+            s_ref, _, h_ref = oracle.lif_multistep(z)
+        spikes = out - ident.cpu() if ident is not None else out
+        flips += lif_parity(spikes.numpy(), None, s_ref, None, h_ref, what=str(kind))
+    return flips
+
+
+def _sew_pairs(m, fused):
+    pairs = [(fused.conv1, (m.conv1, m.bn1, m.sn1), "conv")]
+    for li in range(1, 5):
+        for mb, fb in zip(getattr(m, f"layer{li}"), getattr(fused, f"layer{li}")):
+            pairs.append((fb.fused_first, (mb.conv1, mb.bn1, mb.sn1), "conv"))
+            pairs.append((fb.fused_second, (mb.conv2, mb.bn2, mb.sn2), "conv"))
+            if mb.downsample is not None:
+                pairs.append((fb.fused_downsample, (mb.downsample[0], mb.downsample[1],
+                                                    mb.downsample_sn), "conv"))
+    return pairs
+
+
+@pytest.mark.parametrize("hw", [64, 96])
+def test_sew_resnet18_per_layer_and_logits(cuda, hw):
+    import catfuse_amd
+    from catfuse_amd import snn
+    m = _init(snn.sew_resnet18(num_classes=100, cnf="ADD"), seed=11)
+    T, B = 4, 2
+    img = torch.randn(B, 3, hw, hw, generator=_gen(12))
+    fused, stats = catfuse_amd.optimize(m, T=T)
+    recs, handles = _hook_layers(_sew_pairs(m, fused))
+    with torch.no_grad():
+        y = fused(img.to(cuda).unsqueeze(0).expand(T, B, 3, hw, hw))
+    torch.cuda.synchronize()
+    for h in handles:
+        h.remove()
+    catfuse_amd.check_status()
+    assert len(recs) == 20
+    flips = _check_records(recs)
+    y_ref = oracle.sew_resnet_forward(m, img.unsqueeze(0).expand(T, B, 3, hw, hw))
+    if flips == 0:
+        np.testing.assert_allclose(y.cpu().numpy(), y_ref.numpy(), rtol=1e-4, atol=1e-4)
+    assert (y.cpu().argmax(-1) == y_ref.argmax(-1)).float().mean() >= 0.9
+    snn.functional.reset_net(fused)
+    with torch.no_grad():
+        y2 = fused(img.to(cuda).unsqueeze(0).expand(T, B, 3, hw, hw))
+    assert torch.equal(y, y2)
+
+
+def test_vgg11_per_layer(cuda):
+    import catfuse_amd
+    from catfuse_amd import snn
+    from catfuse_amd.patterns import FusedLinearLIF
+    m = _init(snn.spiking_vgg11_bn(num_classes=10), seed=21)
+    fused, stats = catfuse_amd.optimize(m, T=4)
+    orig = list(m.features)
+    groups, i = [], 0
+    while i < len(orig):
+        if isinstance(orig[i + 2], nn.AvgPool2d):
+            groups.append((tuple(orig[i:i + 4]), "conv_pool"))
+            i += 4
+        else:
+            groups.append((tuple(orig[i:i + 3]), "conv"))
+            i += 3
+    pairs = [(f, o, k) for f, (o, k) in zip(fused.features, groups)]
+    lin = [c for c in fused.classifier if isinstance(c, FusedLinearLIF)]
+    pairs += [(lin[0], (m.classifier[0], m.classifier[1]), "linear"),
+              (lin[1], (m.classifier[2], m.classifier[3]), "linear")]
+    recs, handles = _hook_layers(pairs)
+    x = torch.randn(4, 3, 3, 32, 32, generator=_gen(22))
+    with torch.no_grad():
+        fused(x.to(cuda))
+    torch.cuda.synchronize()
+    for h in handles:
+        h.remove()
+    assert len(recs) == 10
+    _check_records(recs)
+
+
+class _SpikingBasicBlock(nn.Module):
+    """Standard spiking-ResNet BasicBlock (no cnf): LIF(BN(conv2(.)) + identity)."""
+
+    def __init__(self, cin, cout, stride):
+        super().__init__()
+        from catfuse_amd import snn
+        self.conv1 = snn.Conv2d(cin, cout, 3, stride, 1, bias=False)
+        self.bn1 = snn.BatchNorm2d(cout)
+        self.sn1 = snn.LIFNode()
+        self.conv2 = snn.Conv2d(cout, cout, 3, 1, 1, bias=False)
+        self.bn2 = snn.BatchNorm2d(cout)
+        self.sn2 = snn.LIFNode()
+        self.downsample = None
+        if stride != 1 or cin != cout:
+            self.downsample = nn.Sequential(snn.Conv2d(cin, cout, 1, stride, bias=False),
+                                            snn.BatchNorm2d(cout))
+
+    def forward(self, x):
+        out = self.sn1(self.bn1(self.conv1(x)))
+        out = self.bn2(self.conv2(out))
+        identity = x if self.downsample is None else self.downsample(x)
+        return self.sn2(out + identity)
+
+
+_SpikingBasicBlock.__name__ = "BasicBlock"
+
+
+def test_spiking_basic_block_bn_add_lif(cuda):
+    import catfuse_amd
+    blk = _init(nn.Sequential(_SpikingBasicBlock(64, 128, 2)), seed=31)
+    x = (torch.rand(4, 2, 64, 16, 16, generator=_gen(32)) < 0.3).float()
+    fused, stats = catfuse_amd.optimize(blk, use_sparseflow=False)
+    assert stats["patterns_matched"].get("CTFSpikingBasicBlock") == 1
+    with torch.no_grad():
+        out = fused(x.to(cuda))
+    b = blk[0]
+    s1, _, _ = oracle.conv_bn_lif(x, b.conv1, b.bn1, b.sn1)
+    T, B = 4, 2
+    s1 = torch.from_numpy(s1)
+    z2 = oracle.batch_norm(oracle.conv2d(s1.flatten(0, 1), b.conv2.weight, None, 1, 1), b.bn2)
+    zi = oracle.batch_norm(oracle.conv2d(x.flatten(0, 1), b.downsample[0].weight, None, 2, 0),
+                           b.downsample[1])
+    z = (z2 + zi).reshape(T, B, *z2.shape[1:])
+    s_ref, v_ref, h_ref = oracle.lif_multistep(z)
+    lif_parity(out.cpu().numpy(), None, s_ref, None, h_ref, what="spiking block")
