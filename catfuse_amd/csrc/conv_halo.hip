@@ -1,0 +1,342 @@
+// Fused 3x3 Conv -> BN -> LIF on the matrix cores with the input halo staged
+// in LDS and the time axis inside the tile.
+//
+// Workgroup tile: BM output channels x (TH x TW) output pixels of one image,
+// for a block of up to TB = 4 time steps at once.  For every 32-channel
+// chunk the workgroup stages the input halo of its tile for all time steps
+// of the block in LDS ([t][RH][RW][32 ch], fp16, RH = (TH-1)*S + 3), then
+// runs the 9 taps from LDS: each weight fragment (fp16 hi/lo limbs, loaded
+// once per tap from L2, one tap ahead) feeds the MFMAs of every time step.
+// Activations are therefore read from L2 once per chunk instead of once per
+// tap, and weights once per tap instead of once per tap and time step.
+// When the K loop of a time block is complete the epilogue applies BN and
+// the LIF for t = 0..TB-1 in order, with v in VGPRs across time blocks.
+//
+// Tiles are the SparseFlow prescan tiles (8x8 / 8x16), so the same kernel
+// serves the SparseFlow route: a chunk is skipped for time step t when the
+// tile's group bits for t are clear, and a chunk inactive at every step of
+// the block is not even staged.  Routes are decided on the device from the
+// nonzero count and are bit-identical (skipped chunks contribute zeros,
+// and the accumulation order of the remaining ones is unchanged).
+//
+// Accumulation order per output element: chunk-major, then tap, then the
+// two 16-channel halves, hi limb then lo limb.
+#include "cf_common.h"
+
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int KC = 32;       // channels per chunk
+constexpr int LDK = KC + 8;  // padded halo pixel (halves)
+constexpr int TB = 4;        // time steps per block
+
+enum { EPI_LIF = 0, EPI_Z = 1 };
+enum { ID_ADD_SPIKE = 1, ID_ADD_Z = 2 };
+
+struct HaloArgs {
+  const _Float16* x;        // [T*B][H][W][Cp]
+  const _Float16* w;        // [2][Coutp][9][Cp]
+  const float* alpha;
+  const float* beta;
+  const float* v_in;
+  float* v_out;
+  float* out;               // [T][B][Cout][Ho][Wo]
+  const float* identity;
+  int identity_mode;
+  const int32_t* ag_mask;   // [T][B*GH*GW]
+  const unsigned long long* nnz;
+  int64_t numel;
+  double sparse_thr;
+  int T, B, Cp, Cout, Coutp, H, W, Ho, Wo, pad;
+  int GH, GW;
+  int gs;
+  LifParams lif;
+};
+
+__device__ __forceinline__ int halo_route(const unsigned long long* nnz, int64_t numel,
+                                          double thr) {
+  if (!nnz) return CF_ROUTE_DENSE;
+  const unsigned long long k = *nnz;
+  if (k == 0) return CF_ROUTE_ZERO;
+  return (1.0 - (double)k / (double)numel > thr) ? CF_ROUTE_SPARSE : CF_ROUTE_DENSE;
+}
+
+// 128-channel tiles keep 4 x 32 accumulator registers per time block plus
+// double-buffered weight fragments: they get the full 512-register budget.
+template <int BM, int TH, int TW, int S>
+constexpr int halo_min_blocks() { return (BM >= 128 || S == 2 || TH * TW >= 128) ? 1 : 2; }
+
+template <int BM, int TH, int TW, int S, int EPI>
+__global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S>())) void conv_halo_kernel(
+    HaloArgs a) {
+  constexpr int BN = TH * TW;
+  constexpr int WM = BM / 2, WN = BN / 2, MT = WM / 32, NT = WN / 32;
+  constexpr int RH = (TH - 1) * S + 3, RW = (TW - 1) * S + 3;
+  constexpr int HALO_PIX = RH * RW;
+  constexpr int UNITS = TB * HALO_PIX * 4;  // 16-byte units per chunk
+  static_assert(MT >= 1 && NT >= 1, "tile too small");
+  __shared__ __attribute__((aligned(16))) _Float16 halo[TB * HALO_PIX * LDK];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int tile = blockIdx.x;
+  const int gw = tile % a.GW, gh = (tile / a.GW) % a.GH, b = tile / (a.GW * a.GH);
+  const int oh0 = gh * TH, ow0 = gw * TW;
+  const int ih0 = oh0 * S - a.pad, iw0 = ow0 * S - a.pad;
+  const int cout0 = blockIdx.y * BM;
+  const int HoWo = a.Ho * a.Wo;
+  const int nch = a.Cp / KC;
+  const int ntiles = a.B * a.GH * a.GW;
+
+  // Pixels this lane owns in the accumulator layout (column lane%32 of each N tile).
+  int n_base[NT], e_off[NT];
+  bool n_ok[NT];
+#pragma unroll
+  for (int nt = 0; nt < NT; ++nt) {
+    const int n = wn * WN + nt * 32 + (lane & 31);
+    const int py = n / TW, px = n % TW;
+    n_base[nt] = (py * S) * RW + px * S;
+    n_ok[nt] = (oh0 + py) < a.Ho && (ow0 + px) < a.Wo;
+    e_off[nt] = (oh0 + py) * a.Wo + (ow0 + px);
+  }
+  const int kof = (lane >> 5) * 8;
+
+  float v[MT][NT][16];
+  if (EPI == EPI_LIF) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int co = cout0 + wm * WM + mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          float v0 = lif_initial_v(a.lif);
+          if (a.v_in && co < a.Cout && n_ok[nt])
+            v0 = a.v_in[((size_t)b * a.Cout + co) * HoWo + e_off[nt]];
+          v[mt][nt][r] = v0;
+        }
+      }
+  }
+
+  const int route = halo_route(a.nnz, a.numel, a.sparse_thr);
+
+  // Weight fragment addresses: row (cout) per M tile, k offset per lane.
+  const _Float16* wrow[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+    wrow[mt] = a.w + ((size_t)(cout0 + wm * WM + mt * 32 + (lane & 31)) * 9) * a.Cp + kof;
+  const size_t limb_stride = (size_t)a.Coutp * 9 * a.Cp;
+
+  for (int tb0 = 0; tb0 < a.T; tb0 += TB) {
+    const int nsteps = min(TB, a.T - tb0);
+    uint32_t mask[TB];
+#pragma unroll
+    for (int t = 0; t < TB; ++t) {
+      uint32_t m = 0u;
+      if (t < nsteps) {
+        if (route == CF_ROUTE_DENSE) m = 0xffffffffu;
+        else if (route == CF_ROUTE_SPARSE)
+          m = (uint32_t)a.ag_mask[(size_t)(tb0 + t) * ntiles + tile];
+      }
+      mask[t] = m;
+    }
+    f16v acc[TB][MT][NT];
+#pragma unroll
+    for (int t = 0; t < TB; ++t)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[t][mt][nt][r] = 0.0f;
+
+    for (int ch = 0; ch < nch; ++ch) {
+      // groups covered by this chunk
+      const int g0 = (ch * KC) / a.gs, g1 = (ch * KC + KC - 1) / a.gs;
+      uint32_t gbits = 0u;
+      for (int g = g0; g <= g1 && g < 32; ++g) gbits |= 1u << g;
+      bool act[TB];
+      bool any = false;
+#pragma unroll
+      for (int t = 0; t < TB; ++t) {
+        act[t] = (mask[t] & gbits) != 0u;
+        any |= act[t];
+      }
+      if (!any) continue;  // uniform: same mask for the whole workgroup
+
+      __syncthreads();  // previous chunk's halo reads are complete
+      const int c0 = ch * KC;
+      for (int u = tid; u < UNITS; u += 256) {
+        const int part = u & 3;
+        const int pix = (u >> 2) % HALO_PIX;
+        const int t = (u >> 2) / HALO_PIX;
+        const int ry = pix / RW, rx = pix % RW;
+        const int ih = ih0 + ry, iw = iw0 + rx;
+        u32x4 val = (u32x4)(0u);
+        if (t < nsteps && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W)
+          val = *reinterpret_cast<const u32x4*>(
+              a.x + ((((size_t)(tb0 + t) * a.B + b) * a.H + ih) * a.W + iw) * a.Cp + c0 + part * 8);
+        *reinterpret_cast<u32x4*>(&halo[(t * HALO_PIX + pix) * LDK + part * 8]) = val;
+      }
+      __syncthreads();
+
+      h8 ah[2][MT][2], al[2][MT][2];  // [buffer][mt][ks]
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const _Float16* p = wrow[mt] + c0 + ks * 16;
+          ah[0][mt][ks] = *reinterpret_cast<const h8*>(p);
+          al[0][mt][ks] = *reinterpret_cast<const h8*>(p + limb_stride);
+        }
+#pragma unroll
+      for (int tap = 0; tap < 9; ++tap) {
+        const int cur = tap & 1;
+        if (tap + 1 < 9) {
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+              const _Float16* p = wrow[mt] + (size_t)(tap + 1) * a.Cp + c0 + ks * 16;
+              ah[cur ^ 1][mt][ks] = *reinterpret_cast<const h8*>(p);
+              al[cur ^ 1][mt][ks] = *reinterpret_cast<const h8*>(p + limb_stride);
+            }
+        }
+        const int tap_off = (tap / 3) * RW + (tap % 3);
+#pragma unroll
+        for (int t = 0; t < TB; ++t) {
+          if (!act[t]) continue;
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks) {
+            h8 bb[NT];
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+              bb[nt] = *reinterpret_cast<const h8*>(
+                  &halo[(t * HALO_PIX + n_base[nt] + tap_off) * LDK + ks * 16 + kof]);
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+              for (int nt = 0; nt < NT; ++nt) {
+                acc[t][mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[cur][mt][ks], bb[nt],
+                                                                        acc[t][mt][nt], 0, 0, 0);
+                acc[t][mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[cur][mt][ks], bb[nt],
+                                                                        acc[t][mt][nt], 0, 0, 0);
+              }
+          }
+        }
+      }
+    }
+
+    // Epilogue over the time block.
+#pragma unroll
+    for (int t = 0; t < TB; ++t) {
+      if (t >= nsteps) break;
+      const int tt = tb0 + t;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int co = cout0 + wm * WM + mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          if (co >= a.Cout) continue;
+          const float al_ = a.alpha[co], be = a.beta[co];
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            if (!n_ok[nt]) continue;
+            const size_t o = ((size_t)(tt * a.B + b) * a.Cout + co) * HoWo + e_off[nt];
+            float z = acc[t][mt][nt][r] * al_ + be;
+            if (a.identity && a.identity_mode == ID_ADD_Z) z = z + a.identity[o];
+            if (EPI == EPI_Z) {
+              a.out[o] = z;
+            } else {
+              float vv = lif_charge(v[mt][nt][r], z, a.lif);
+              const float sp = lif_fire_reset(vv, a.lif);
+              v[mt][nt][r] = vv;
+              a.out[o] = (a.identity && a.identity_mode == ID_ADD_SPIKE) ? a.identity[o] + sp : sp;
+            }
+          }
+        }
+    }
+  }
+
+  if (EPI == EPI_LIF && a.v_out) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int co = cout0 + wm * WM + mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          if (co < a.Cout && n_ok[nt])
+            a.v_out[((size_t)b * a.Cout + co) * HoWo + e_off[nt]] = v[mt][nt][r];
+      }
+  }
+}
+
+template <int BM, int TH, int TW, int S>
+hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
+  dim3 grid((unsigned)(a.B * a.GH * a.GW), (unsigned)(a.Coutp / BM));
+  if (epi == EPI_Z)
+    hipLaunchKernelGGL((conv_halo_kernel<BM, TH, TW, S, EPI_Z>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((conv_halo_kernel<BM, TH, TW, S, EPI_LIF>), grid, dim3(256), 0, st, a);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// 3x3 convolutions (stride 1 or 2, any padding) with halo staging; the
+// caller picks the tile (tile_h x tile_w in {8x8, 8x16}; 8x16 only with
+// stride 1).  Arguments as cf_conv_mfma.
+CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
+                        const float* beta, const float* v_in, float* v_out, float* out,
+                        const float* identity, int identity_mode, const int32_t* ag_mask,
+                        const unsigned long long* nnz, int64_t numel, double sparse_threshold,
+                        int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
+                        int64_t W, int64_t Ho, int64_t Wo, int64_t stride, int64_t pad,
+                        int64_t tile_h, int64_t tile_w, int64_t group_size, int epilogue,
+                        double tau, double v_th, double v_reset, int hard_reset, int decay_input,
+                        void* stream) {
+  if (!x || !w_packed || !alpha || !beta || !out) return (int)hipErrorInvalidValue;
+  if (T <= 0 || B <= 0 || Cp <= 0 || Cp % KC != 0 || Cp / KC > 64 || Cout <= 0 ||
+      Coutp < Cout || Coutp % 64 != 0 || H <= 0 || W <= 0 || pad < 0 || pad > 2)
+    return (int)hipErrorInvalidValue;
+  if (stride != 1 && stride != 2) return (int)hipErrorInvalidValue;
+  if (Ho != (H + 2 * pad - 3) / stride + 1 || Wo != (W + 2 * pad - 3) / stride + 1 || Ho <= 0 ||
+      Wo <= 0)
+    return (int)hipErrorInvalidValue;
+  if (epilogue != EPI_LIF && epilogue != EPI_Z) return (int)hipErrorInvalidValue;
+  if (identity && identity_mode != ID_ADD_SPIKE && identity_mode != ID_ADD_Z)
+    return (int)hipErrorInvalidValue;
+  if (!((tile_h == 8 && tile_w == 8) || (tile_h == 8 && tile_w == 16 && stride == 1)))
+    return (int)hipErrorInvalidValue;
+  if (ag_mask && (group_size <= 0 || (Cp + group_size - 1) / group_size > 32))
+    return (int)hipErrorInvalidValue;
+  if (B * Ho * Wo > INT32_MAX || T * B * H * W > ((int64_t)1 << 40)) return (int)hipErrorInvalidValue;
+  HaloArgs a;
+  a.x = (const _Float16*)x; a.w = (const _Float16*)w_packed; a.alpha = alpha; a.beta = beta;
+  a.v_in = v_in; a.v_out = v_out; a.out = out; a.identity = identity;
+  a.identity_mode = identity_mode; a.ag_mask = ag_mask;
+  // Without masks the SparseFlow route cannot be taken: pass the count only
+  // when masks exist (StaticZero is still detected through nnz == 0 below).
+  a.nnz = nnz; a.numel = numel;
+  a.sparse_thr = ag_mask ? sparse_threshold : 2.0;  // 2.0: sparsity never exceeds it
+  a.T = (int)T; a.B = (int)B; a.Cp = (int)Cp; a.Cout = (int)Cout; a.Coutp = (int)Coutp;
+  a.H = (int)H; a.W = (int)W; a.Ho = (int)Ho; a.Wo = (int)Wo; a.pad = (int)pad;
+  a.GH = (int)((Ho + tile_h - 1) / tile_h);
+  a.GW = (int)((Wo + tile_w - 1) / tile_w);
+  a.gs = group_size > 0 ? (int)group_size : 32;
+  a.lif = cf_make_lif_params(tau, v_th, v_reset, hard_reset, decay_input);
+  hipStream_t st = (hipStream_t)stream;
+  const bool bm128 = (Coutp % 128 == 0);
+  hipError_t e;
+  if (stride == 1 && tile_w == 16)
+    e = launch_halo<64, 8, 16, 1>(a, epilogue, st);  // 64-channel tiles (register budget)
+  else if (stride == 1)
+    e = bm128 ? launch_halo<128, 8, 8, 1>(a, epilogue, st) : launch_halo<64, 8, 8, 1>(a, epilogue, st);
+  else
+    e = bm128 ? launch_halo<128, 8, 8, 2>(a, epilogue, st) : launch_halo<64, 8, 8, 2>(a, epilogue, st);
+  return (int)e;
+}

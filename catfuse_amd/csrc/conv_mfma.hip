@@ -398,6 +398,16 @@ CF_API int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64
   return (int)hipGetLastError();
 }
 
+CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
+                        const float* beta, const float* v_in, float* v_out, float* out,
+                        const float* identity, int identity_mode, const int32_t* ag_mask,
+                        const unsigned long long* nnz, int64_t numel, double sparse_threshold,
+                        int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
+                        int64_t W, int64_t Ho, int64_t Wo, int64_t stride, int64_t pad,
+                        int64_t tile_h, int64_t tile_w, int64_t group_size, int epilogue,
+                        double tau, double v_th, double v_reset, int hard_reset, int decay_input,
+                        void* stream);
+
 CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
                         const float* beta, const float* v_in, float* v_out, float* out,
                         const float* identity, int identity_mode, const int32_t* ag_mask,
@@ -418,6 +428,19 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
   if (Ho != (H + 2 * pad - KH) / stride + 1 || Wo != (W + 2 * pad - KW) / stride + 1)
     return (int)hipErrorInvalidValue;
   const bool rect = tile_h > 0 && tile_w > 0;
+  // 3x3 convolutions (stride 1/2, pad <= 2, one time-major input) always take
+  // the halo-staged kernel, whatever the route or epilogue, so every
+  // implementation of a layer accumulates in the same order.
+  const bool halo_ok = KH == 3 && KW == 3 && (stride == 1 || stride == 2) && pad <= 2 &&
+                       Cp / KC <= 64 && x_img_tstride == B &&
+                       (!rect || (tile_h == 8 && (tile_w == 8 || (tile_w == 16 && stride == 1))));
+  if (halo_ok) {
+    const int64_t th = 8, tw = rect ? tile_w : 8;
+    return cf_conv_halo(x, w_packed, alpha, beta, v_in, v_out, out, identity, identity_mode,
+                        rect ? ag_mask : nullptr, nnz, numel, sparse_threshold, T, B, Cp, Cout,
+                        Coutp, H, W, Ho, Wo, stride, pad, th, tw, rect ? group_size : 0,
+                        epilogue, tau, v_th, v_reset, hard_reset, decay_input, stream);
+  }
   if (rect) {
     if (!(tile_h * tile_w == 64 || tile_h * tile_w == 128)) return (int)hipErrorInvalidValue;
     if (Cp / KC > 64 || group_size <= 0 || (Cp + group_size - 1) / group_size > 32)

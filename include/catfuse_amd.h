@@ -136,6 +136,22 @@ int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha, const 
                  int64_t tile_w, int64_t group_size, int epilogue, double tau, double v_th,
                  double v_reset, int hard_reset, int decay_input, void* stream);
 
+/* 3x3 Conv (stride 1 or 2) -> BN -> LIF / z with the input halo of each
+ * (tile_h x tile_w) output tile staged in LDS once per 32-channel chunk and
+ * up to 4 time steps accumulated per tile (weights fetched once per tap for
+ * all of them).  cf_conv_mfma forwards every 3x3 layer here (tile 8x8 when
+ * tile_h = 0), so all routes and epilogues of a layer accumulate in the same
+ * order.  Tiles: 8x8, or 8x16 with stride 1.  Other arguments as
+ * cf_conv_mfma.  Replaces the same reference interfaces as cf_conv_mfma. */
+int cf_conv_halo(const void* x, const void* w_packed, const float* alpha, const float* beta,
+                 const float* v_in, float* v_out, float* out, const float* identity,
+                 int identity_mode, const int32_t* ag_mask, const unsigned long long* nnz,
+                 int64_t numel, double sparse_threshold, int64_t T, int64_t B, int64_t Cp,
+                 int64_t Cout, int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
+                 int64_t stride, int64_t pad, int64_t tile_h, int64_t tile_w,
+                 int64_t group_size, int epilogue, double tau, double v_th, double v_reset,
+                 int hard_reset, int decay_input, void* stream);
+
 /* Fused Conv -> BN -> LIF / z in fp32 (VALU) for analog inputs
  * x [T*x_img_tstride + B][Cin][H][W]; x_img_tstride == 0 evaluates the
  * convolution once for a time-repeated (direct-encoded) input.  Replaces

@@ -215,6 +215,8 @@ CONV_CASES = [
     ("ds", 2, 2, 128, 256, 28, 28, 1, 2, 0, 0.3),
     ("odd", 3, 2, 40, 96, 9, 11, 3, 1, 1, 0.4),
     ("t1", 1, 2, 64, 64, 16, 16, 3, 1, 1, 0.5),
+    ("t6", 6, 2, 64, 128, 12, 12, 3, 1, 1, 0.3),
+    ("t9s2", 9, 1, 32, 64, 15, 15, 3, 2, 1, 0.3),
 ]
 
 
@@ -257,6 +259,20 @@ def test_sparse_route_bitwise_equals_dense(cuda, rate, pattern):
     s_ref, v_ref, h_ref = oracle.conv_bn_lif(x, conv, bn, lif, v_in=v0.cpu())
     lif_parity(s_dense.cpu().numpy(), v_dense.cpu().numpy(), s_ref, v_ref, h_ref,
                what=f"C1 {pattern} {rate}")
+
+
+@pytest.mark.parametrize("rate", [0.0, 0.02, 0.3])
+def test_sparse_8x16_tiles_bitwise_equals_dense(cuda, rate):
+    T, B, C, H, W = 4, 2, 64, 56, 56      # 3136 px -> 8x16 prescan tiles
+    conv, bn, lif = _layer(C, 64, 3, 1, 1, seed=6)
+    x = (torch.rand(T, B, C, H, W, generator=_gen(int(rate * 100) + 1)) < rate).float()
+    r = _runner(conv, bn, lif, cuda)
+    xd = x.to(cuda)
+    s_dense, v_dense = r.run_mfma(xd, static_zero=False)
+    s_sparse, v_sparse = r.run_mfma(xd, sparse=dict(block_h=8, block_w=16, group_size=16))
+    assert torch.equal(s_sparse, s_dense) and torch.equal(v_sparse, v_dense)
+    s_ref, v_ref, h_ref = oracle.conv_bn_lif(x, conv, bn, lif)
+    lif_parity(s_dense.cpu().numpy(), v_dense.cpu().numpy(), s_ref, v_ref, h_ref, what="56x56")
 
 
 def test_static_zero_route_equals_bias_only(cuda):
