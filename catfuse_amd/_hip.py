@@ -32,13 +32,13 @@ _SIGNATURES = {
     "cf_zero_counter": [_P, _P],
     "cf_prescan_tiles": [_P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P],
     "cf_pack_conv_weights": [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P],
-    "cf_conv_mfma": [_P, _P, _P, _P, _P, _P, _P, _P, c_int, _P, _P, _I, c_double,
+    "cf_conv_mfma": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, c_int, _P, _P, _I, c_double,
                      _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                      c_int, c_double, c_double, c_double, c_int, c_int, _P],
-    "cf_conv_halo": [_P, _P, _P, _P, _P, _P, _P, _P, c_int, _P, _P, _I, c_double,
-                     _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
+    "cf_conv_halo": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, c_int, _P, _P, _I, c_double,
+                     _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                      c_int, c_double, c_double, c_double, c_int, c_int, _P],
-    "cf_conv_direct": [_P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
+    "cf_conv_direct": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                        _I, _I, _I, c_int, c_double, c_double, c_double, c_int, c_int, _P],
 }
 _RESTYPES = {"cf_error_string": c_char_p}

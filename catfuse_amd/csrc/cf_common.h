@@ -64,6 +64,13 @@ __device__ __forceinline__ float lif_initial_v(const LifParams& p) {
 // Host: LIF parameter block from SpikingJelly-level (double) parameters.
 LifParams cf_make_lif_params(double tau, double v_th, double v_reset, int hard, int decay_input);
 
+// fp16 NHWC copy of a boundary output element, read by the next fused conv
+// instead of re-packing the fp32 tensor: nhwc[(img*HoWo + pix)*cp + co].
+__device__ __forceinline__ void store_nhwc(_Float16* nhwc, int cp, size_t img, int HoWo, int pix,
+                                           int co, float val) {
+  nhwc[((size_t)img * HoWo + pix) * cp + co] = (_Float16)val;
+}
+
 // Number of dispatches one grid dimension may hold.
 static inline unsigned cf_blocks(int64_t n, int per_block) {
   return (unsigned)((n + per_block - 1) / per_block);

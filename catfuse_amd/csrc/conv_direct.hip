@@ -27,6 +27,8 @@ struct DirectArgs {
   const float* v_in;
   float* v_out;
   float* out;  // [T][B][Cout][Ho][Wo]
+  _Float16* out_nhwc;  // [T*B][Ho][Wo][cp_out] or null
+  int cp_out;
   int T, B, Cin, Cout, H, W, Ho, Wo, KH, KW, stride, pad, x_img_tstride;
   LifParams lif;
 };
@@ -78,14 +80,20 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(DirectArgs a) {
       const int co = co0 + j;
       const float z = acc[j] * a.alpha[co] + a.beta[co];
       const size_t o = ((size_t)(t * a.B + b) * a.Cout + co) * HoWo + p;
+      float ov;
       if (EPI == EPI_Z) {
-        a.out[o] = z;
+        ov = z;
       } else {
         float vv = lif_charge(v[j], z, a.lif);
-        a.out[o] = lif_fire_reset(vv, a.lif);
+        ov = lif_fire_reset(vv, a.lif);
         v[j] = vv;
       }
+      a.out[o] = ov;
+      if (a.out_nhwc) store_nhwc(a.out_nhwc, a.cp_out, (size_t)t * a.B + b, HoWo, p, co, ov);
     }
+    if (a.out_nhwc && co0 + COB == a.Cout)
+      for (int co = a.Cout; co < a.cp_out; ++co)
+        store_nhwc(a.out_nhwc, a.cp_out, (size_t)t * a.B + b, HoWo, p, co, 0.0f);
   }
   if (EPI == EPI_LIF && a.v_out) {
 #pragma unroll
@@ -104,7 +112,8 @@ hipError_t launch_direct(const DirectArgs& a, int epi, hipStream_t st) {
 }  // namespace
 
 CF_API int cf_conv_direct(const float* x, const float* w, const float* alpha, const float* beta,
-                          const float* v_in, float* v_out, float* out, int64_t T, int64_t B,
+                          const float* v_in, float* v_out, float* out, void* out_nhwc,
+                          int64_t cp_out, int64_t T, int64_t B,
                           int64_t Cin, int64_t Cout, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
                           int64_t KH, int64_t KW, int64_t stride, int64_t pad,
                           int64_t x_img_tstride, int epilogue, double tau, double v_th,
@@ -119,6 +128,8 @@ CF_API int cf_conv_direct(const float* x, const float* w, const float* alpha, co
   if (epilogue != EPI_LIF && epilogue != EPI_Z) return (int)hipErrorInvalidValue;
   DirectArgs a;
   a.x = x; a.w = w; a.alpha = alpha; a.beta = beta; a.v_in = v_in; a.v_out = v_out; a.out = out;
+  a.out_nhwc = (_Float16*)out_nhwc; a.cp_out = (int)cp_out;
+  if (out_nhwc && cp_out < Cout) return (int)hipErrorInvalidValue;
   a.T = (int)T; a.B = (int)B; a.Cin = (int)Cin; a.Cout = (int)Cout; a.H = (int)H; a.W = (int)W;
   a.Ho = (int)Ho; a.Wo = (int)Wo; a.KH = (int)KH; a.KW = (int)KW; a.stride = (int)stride;
   a.pad = (int)pad; a.x_img_tstride = (int)x_img_tstride;

@@ -23,6 +23,8 @@
 // two 16-channel halves, hi limb then lo limb.
 #include "cf_common.h"
 
+#include <stdlib.h>
+
 namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
@@ -44,6 +46,8 @@ struct HaloArgs {
   const float* v_in;
   float* v_out;
   float* out;               // [T][B][Cout][Ho][Wo]
+  _Float16* out_nhwc;       // [T*B][Ho][Wo][cp_out] or null
+  int cp_out;
   const float* identity;
   int identity_mode;
   const int32_t* ag_mask;   // [T][B*GH*GW]
@@ -66,17 +70,27 @@ __device__ __forceinline__ int halo_route(const unsigned long long* nnz, int64_t
 
 // 128-channel tiles keep 4 x 32 accumulator registers per time block plus
 // double-buffered weight fragments: they get the full 512-register budget.
-template <int BM, int TH, int TW, int S>
-constexpr int halo_min_blocks() { return (BM >= 128 || S == 2 || TH * TW >= 128) ? 1 : 2; }
+template <int BM, int TH, int TW, int S, int K>
+constexpr int halo_min_blocks() {
+  return (BM >= 128 || (S == 2 && K == 3) || TH * TW >= 128) ? 1 : 2;
+}
 
-template <int BM, int TH, int TW, int S, int EPI>
-__global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S>())) void conv_halo_kernel(
+// K: filter size (3, or 1 for pointwise convolutions, whose strided input
+// samples are staged densely: RH = TH, RW = TW).
+template <int BM, int TH, int TW, int S, int K, int EPI>
+__global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>())) void conv_halo_kernel(
     HaloArgs a) {
   constexpr int BN = TH * TW;
   constexpr int WM = BM / 2, WN = BN / 2, MT = WM / 32, NT = WN / 32;
-  constexpr int RH = (TH - 1) * S + 3, RW = (TW - 1) * S + 3;
+  constexpr int RH = K == 1 ? TH : (TH - 1) * S + K, RW = K == 1 ? TW : (TW - 1) * S + K;
+  constexpr int SS = K == 1 ? S : 1;  // input step between staged pixels
+  constexpr int KK = K * K;
   constexpr int HALO_PIX = RH * RW;
   constexpr int UNITS = TB * HALO_PIX * 4;  // 16-byte units per chunk
+  constexpr int PER = (UNITS + 255) / 256;  // staging units per thread
+  // Overlap the next chunk's halo loads with this chunk's taps when the
+  // staging registers are few (stride 1, 8x8 tiles: 7 units per thread).
+  constexpr bool PREFETCH = (S == 1 || K == 1) && TH * TW == 64;
   static_assert(MT >= 1 && NT >= 1, "tile too small");
   __shared__ __attribute__((aligned(16))) _Float16 halo[TB * HALO_PIX * LDK];
 
@@ -98,7 +112,7 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S>())) void conv_
   for (int nt = 0; nt < NT; ++nt) {
     const int n = wn * WN + nt * 32 + (lane & 31);
     const int py = n / TW, px = n % TW;
-    n_base[nt] = (py * S) * RW + px * S;
+    n_base[nt] = K == 1 ? py * RW + px : (py * S) * RW + px * S;
     n_ok[nt] = (oh0 + py) < a.Ho && (ow0 + px) < a.Wo;
     e_off[nt] = (oh0 + py) * a.Wo + (ow0 + px);
   }
@@ -127,8 +141,8 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S>())) void conv_
   const _Float16* wrow[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
-    wrow[mt] = a.w + ((size_t)(cout0 + wm * WM + mt * 32 + (lane & 31)) * 9) * a.Cp + kof;
-  const size_t limb_stride = (size_t)a.Coutp * 9 * a.Cp;
+    wrow[mt] = a.w + ((size_t)(cout0 + wm * WM + mt * 32 + (lane & 31)) * KK) * a.Cp + kof;
+  const size_t limb_stride = (size_t)a.Coutp * KK * a.Cp;
 
   for (int tb0 = 0; tb0 < a.T; tb0 += TB) {
     const int nsteps = min(TB, a.T - tb0);
@@ -153,36 +167,81 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S>())) void conv_
 #pragma unroll
           for (int r = 0; r < 16; ++r) acc[t][mt][nt][r] = 0.0f;
 
-    for (int ch = 0; ch < nch; ++ch) {
-      // groups covered by this chunk
+    // Chunks active at some step of the block, in order (uniform across the
+    // workgroup: every thread evaluates the same masks).
+    auto chunk_act = [&](int ch, bool (&act)[TB]) -> bool {
       const int g0 = (ch * KC) / a.gs, g1 = (ch * KC + KC - 1) / a.gs;
       uint32_t gbits = 0u;
       for (int g = g0; g <= g1 && g < 32; ++g) gbits |= 1u << g;
-      bool act[TB];
       bool any = false;
 #pragma unroll
       for (int t = 0; t < TB; ++t) {
         act[t] = (mask[t] & gbits) != 0u;
         any |= act[t];
       }
-      if (!any) continue;  // uniform: same mask for the whole workgroup
-
-      __syncthreads();  // previous chunk's halo reads are complete
+      return any;
+    };
+    auto next_chunk = [&](int ch) -> int {
+      bool tmp[TB];
+      for (int c = ch + 1; c < nch; ++c)
+        if (chunk_act(c, tmp)) return c;
+      return nch;
+    };
+    // Halo staging through registers: all loads of a chunk are issued
+    // before any LDS store, and the next chunk's loads are in flight while
+    // the current chunk's taps run.
+    constexpr int NSTG = PREFETCH ? PER : (PER < 8 ? PER : 8);
+    u32x4 stg[NSTG];
+    auto halo_load = [&](int ch, int i0, u32x4 (&st)[NSTG]) {
       const int c0 = ch * KC;
-      for (int u = tid; u < UNITS; u += 256) {
+#pragma unroll
+      for (int i = 0; i < NSTG; ++i) {
+        const int u = tid + 256 * (i0 + i);
         const int part = u & 3;
         const int pix = (u >> 2) % HALO_PIX;
         const int t = (u >> 2) / HALO_PIX;
         const int ry = pix / RW, rx = pix % RW;
-        const int ih = ih0 + ry, iw = iw0 + rx;
-        u32x4 val = (u32x4)(0u);
-        if (t < nsteps && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W)
-          val = *reinterpret_cast<const u32x4*>(
-              a.x + ((((size_t)(tb0 + t) * a.B + b) * a.H + ih) * a.W + iw) * a.Cp + c0 + part * 8);
-        *reinterpret_cast<u32x4*>(&halo[(t * HALO_PIX + pix) * LDK + part * 8]) = val;
+        const int ih = ih0 + ry * SS, iw = iw0 + rx * SS;
+        const bool ok = u < UNITS && t < nsteps && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W;
+        const size_t off =
+            ok ? ((((size_t)(tb0 + t) * a.B + b) * a.H + ih) * a.W + iw) * a.Cp + c0 + part * 8 : 0;
+        const u32x4 val = *reinterpret_cast<const u32x4*>(a.x + off);
+        st[i] = ok ? val : (u32x4)(0u);
       }
-      __syncthreads();
+    };
+    auto halo_store = [&](int i0, const u32x4 (&st)[NSTG]) {
+#pragma unroll
+      for (int i = 0; i < NSTG; ++i) {
+        const int u = tid + 256 * (i0 + i);
+        if (u < UNITS) {
+          const int part = u & 3;
+          const int pix = (u >> 2) % HALO_PIX;
+          const int t = (u >> 2) / HALO_PIX;
+          *reinterpret_cast<u32x4*>(&halo[(t * HALO_PIX + pix) * LDK + part * 8]) = st[i];
+        }
+      }
+    };
 
+    // Whole-chunk staging in groups of NSTG units (loads of a group are all
+    // issued before its stores).
+    auto halo_stage = [&](int ch) {
+      for (int i0 = 0; i0 < PER; i0 += NSTG) {
+        halo_load(ch, i0, stg);
+        halo_store(i0, stg);
+      }
+    };
+    int ch = next_chunk(-1);
+    if (ch < nch) {
+      __syncthreads();  // previous time block's halo reads are complete
+      halo_stage(ch);
+      __syncthreads();
+    }
+    while (ch < nch) {
+      bool act[TB];
+      chunk_act(ch, act);
+      const int nx = next_chunk(ch);
+      if (PREFETCH && nx < nch) halo_load(nx, 0, stg);
+      const int c0 = ch * KC;
       h8 ah[2][MT][2], al[2][MT][2];  // [buffer][mt][ks]
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
@@ -193,9 +252,9 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S>())) void conv_
           al[0][mt][ks] = *reinterpret_cast<const h8*>(p + limb_stride);
         }
 #pragma unroll
-      for (int tap = 0; tap < 9; ++tap) {
+      for (int tap = 0; tap < KK; ++tap) {
         const int cur = tap & 1;
-        if (tap + 1 < 9) {
+        if (tap + 1 < KK) {
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
@@ -205,7 +264,7 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S>())) void conv_
               al[cur ^ 1][mt][ks] = *reinterpret_cast<const h8*>(p + limb_stride);
             }
         }
-        const int tap_off = (tap / 3) * RW + (tap % 3);
+        const int tap_off = (tap / K) * RW + (tap % K);
 #pragma unroll
         for (int t = 0; t < TB; ++t) {
           if (!act[t]) continue;
@@ -228,6 +287,13 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S>())) void conv_
           }
         }
       }
+      if (nx < nch) {
+        __syncthreads();  // all taps of this chunk have read the halo
+        if (PREFETCH) halo_store(0, stg);
+        else halo_stage(nx);
+        __syncthreads();
+      }
+      ch = nx;
     }
 
     // Epilogue over the time block.
@@ -240,7 +306,13 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S>())) void conv_
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int co = cout0 + wm * WM + mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          if (co >= a.Cout) continue;
+          if (co >= a.Cout) {
+            if (a.out_nhwc && co < a.cp_out)
+#pragma unroll
+              for (int nt = 0; nt < NT; ++nt)
+                if (n_ok[nt]) store_nhwc(a.out_nhwc, a.cp_out, (size_t)tt * a.B + b, HoWo, e_off[nt], co, 0.0f);
+            continue;
+          }
           const float al_ = a.alpha[co], be = a.beta[co];
 #pragma unroll
           for (int nt = 0; nt < NT; ++nt) {
@@ -248,14 +320,17 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S>())) void conv_
             const size_t o = ((size_t)(tt * a.B + b) * a.Cout + co) * HoWo + e_off[nt];
             float z = acc[t][mt][nt][r] * al_ + be;
             if (a.identity && a.identity_mode == ID_ADD_Z) z = z + a.identity[o];
+            float ov;
             if (EPI == EPI_Z) {
-              a.out[o] = z;
+              ov = z;
             } else {
               float vv = lif_charge(v[mt][nt][r], z, a.lif);
               const float sp = lif_fire_reset(vv, a.lif);
               v[mt][nt][r] = vv;
-              a.out[o] = (a.identity && a.identity_mode == ID_ADD_SPIKE) ? a.identity[o] + sp : sp;
+              ov = (a.identity && a.identity_mode == ID_ADD_SPIKE) ? a.identity[o] + sp : sp;
             }
+            a.out[o] = ov;
+            if (a.out_nhwc) store_nhwc(a.out_nhwc, a.cp_out, (size_t)tt * a.B + b, HoWo, e_off[nt], co, ov);
           }
         }
     }
@@ -275,13 +350,13 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S>())) void conv_
   }
 }
 
-template <int BM, int TH, int TW, int S>
+template <int BM, int TH, int TW, int S, int K = 3>
 hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
   dim3 grid((unsigned)(a.B * a.GH * a.GW), (unsigned)(a.Coutp / BM));
   if (epi == EPI_Z)
-    hipLaunchKernelGGL((conv_halo_kernel<BM, TH, TW, S, EPI_Z>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((conv_halo_kernel<BM, TH, TW, S, K, EPI_Z>), grid, dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((conv_halo_kernel<BM, TH, TW, S, EPI_LIF>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((conv_halo_kernel<BM, TH, TW, S, K, EPI_LIF>), grid, dim3(256), 0, st, a);
   return hipGetLastError();
 }
 
@@ -292,25 +367,28 @@ hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
 // stride 1).  Arguments as cf_conv_mfma.
 CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
                         const float* beta, const float* v_in, float* v_out, float* out,
+                        void* out_nhwc, int64_t cp_out,
                         const float* identity, int identity_mode, const int32_t* ag_mask,
                         const unsigned long long* nnz, int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
-                        int64_t W, int64_t Ho, int64_t Wo, int64_t stride, int64_t pad,
-                        int64_t tile_h, int64_t tile_w, int64_t group_size, int epilogue,
-                        double tau, double v_th, double v_reset, int hard_reset, int decay_input,
-                        void* stream) {
+                        int64_t W, int64_t Ho, int64_t Wo, int64_t ksize, int64_t stride,
+                        int64_t pad, int64_t tile_h, int64_t tile_w, int64_t group_size,
+                        int epilogue, double tau, double v_th, double v_reset, int hard_reset,
+                        int decay_input, void* stream) {
   if (!x || !w_packed || !alpha || !beta || !out) return (int)hipErrorInvalidValue;
+  if (ksize != 1 && ksize != 3) return (int)hipErrorInvalidValue;
+  if (out_nhwc && (cp_out < Cout || cp_out > Coutp)) return (int)hipErrorInvalidValue;
   if (T <= 0 || B <= 0 || Cp <= 0 || Cp % KC != 0 || Cp / KC > 64 || Cout <= 0 ||
       Coutp < Cout || Coutp % 64 != 0 || H <= 0 || W <= 0 || pad < 0 || pad > 2)
     return (int)hipErrorInvalidValue;
   if (stride != 1 && stride != 2) return (int)hipErrorInvalidValue;
-  if (Ho != (H + 2 * pad - 3) / stride + 1 || Wo != (W + 2 * pad - 3) / stride + 1 || Ho <= 0 ||
+  if (Ho != (H + 2 * pad - ksize) / stride + 1 || Wo != (W + 2 * pad - ksize) / stride + 1 || Ho <= 0 ||
       Wo <= 0)
     return (int)hipErrorInvalidValue;
   if (epilogue != EPI_LIF && epilogue != EPI_Z) return (int)hipErrorInvalidValue;
   if (identity && identity_mode != ID_ADD_SPIKE && identity_mode != ID_ADD_Z)
     return (int)hipErrorInvalidValue;
-  if (!((tile_h == 8 && tile_w == 8) || (tile_h == 8 && tile_w == 16 && stride == 1)))
+  if (!((tile_h == 8 && tile_w == 8) || (tile_h == 8 && tile_w == 16 && stride == 1 && ksize == 3)))
     return (int)hipErrorInvalidValue;
   if (ag_mask && (group_size <= 0 || (Cp + group_size - 1) / group_size > 32))
     return (int)hipErrorInvalidValue;
@@ -318,6 +396,7 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
   HaloArgs a;
   a.x = (const _Float16*)x; a.w = (const _Float16*)w_packed; a.alpha = alpha; a.beta = beta;
   a.v_in = v_in; a.v_out = v_out; a.out = out; a.identity = identity;
+  a.out_nhwc = (_Float16*)out_nhwc; a.cp_out = (int)cp_out;
   a.identity_mode = identity_mode; a.ag_mask = ag_mask;
   // Without masks the SparseFlow route cannot be taken: pass the count only
   // when masks exist (StaticZero is still detected through nnz == 0 below).
@@ -330,9 +409,19 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
   a.gs = group_size > 0 ? (int)group_size : 32;
   a.lif = cf_make_lif_params(tau, v_th, v_reset, hard_reset, decay_input);
   hipStream_t st = (hipStream_t)stream;
-  const bool bm128 = (Coutp % 128 == 0);
+  // 64-channel tiles: measured faster on every SEW-ResNet18 layer than
+  // 128-channel ones (which hold one workgroup per CU slot).
+  // CATFUSE_HALO_BM=128 selects 128-channel tiles (tuning).
+  bool bm128 = false;
+  if (const char* e = getenv("CATFUSE_HALO_BM")) {
+    if (atoi(e) == 128) bm128 = (Coutp % 128 == 0);
+    else if (atoi(e) == 64) bm128 = false;
+  }
   hipError_t e;
-  if (stride == 1 && tile_w == 16)
+  if (ksize == 1)
+    e = stride == 1 ? launch_halo<64, 8, 8, 1, 1>(a, epilogue, st)
+                    : launch_halo<64, 8, 8, 2, 1>(a, epilogue, st);
+  else if (stride == 1 && tile_w == 16)
     e = launch_halo<64, 8, 16, 1>(a, epilogue, st);  // 64-channel tiles (register budget)
   else if (stride == 1)
     e = bm128 ? launch_halo<128, 8, 8, 1>(a, epilogue, st) : launch_halo<64, 8, 8, 1>(a, epilogue, st);

@@ -54,6 +54,8 @@ struct ConvArgs {
   const float* v_in;
   float* v_out;
   float* out;
+  _Float16* out_nhwc;
+  int cp_out;
   const float* identity;
   int identity_mode;
   const int32_t* ag_mask;
@@ -277,7 +279,14 @@ __global__ __launch_bounds__(256, (conv_min_blocks<BM, BN, EPI>())) void conv_mf
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int co = cout0 + wm * WM + mb * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (co >= a.Cout) continue;
+        if (co >= a.Cout) {
+          if (a.out_nhwc && co < a.cp_out)
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+              if (e_img[nb] >= 0)
+                store_nhwc(a.out_nhwc, a.cp_out, (size_t)t * a.B + e_img[nb], HoWo, e_off[nb], co, 0.0f);
+          continue;
+        }
         const float al = a.alpha[co], be = a.beta[co];
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
@@ -285,14 +294,18 @@ __global__ __launch_bounds__(256, (conv_min_blocks<BM, BN, EPI>())) void conv_mf
           const size_t o = ((size_t)(t * a.B + e_img[nb]) * a.Cout + co) * HoWo + e_off[nb];
           float z = acc[mb][nb][r] * al + be;
           if (a.identity && a.identity_mode == ID_ADD_Z) z = z + a.identity[o];
+          float ov;
           if (EPI == EPI_Z) {
-            a.out[o] = z;
+            ov = z;
           } else {
             float vv = lif_charge(v[mb][nb][r], z, a.lif);
             float sp = lif_fire_reset(vv, a.lif);
             v[mb][nb][r] = vv;
-            a.out[o] = (a.identity && a.identity_mode == ID_ADD_SPIKE) ? a.identity[o] + sp : sp;
+            ov = (a.identity && a.identity_mode == ID_ADD_SPIKE) ? a.identity[o] + sp : sp;
           }
+          a.out[o] = ov;
+          if (a.out_nhwc)
+            store_nhwc(a.out_nhwc, a.cp_out, (size_t)t * a.B + e_img[nb], HoWo, e_off[nb], co, ov);
         }
       }
   }
@@ -400,16 +413,18 @@ CF_API int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64
 
 CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
                         const float* beta, const float* v_in, float* v_out, float* out,
+                        void* out_nhwc, int64_t cp_out,
                         const float* identity, int identity_mode, const int32_t* ag_mask,
                         const unsigned long long* nnz, int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
-                        int64_t W, int64_t Ho, int64_t Wo, int64_t stride, int64_t pad,
-                        int64_t tile_h, int64_t tile_w, int64_t group_size, int epilogue,
-                        double tau, double v_th, double v_reset, int hard_reset, int decay_input,
-                        void* stream);
+                        int64_t W, int64_t Ho, int64_t Wo, int64_t ksize, int64_t stride,
+                        int64_t pad, int64_t tile_h, int64_t tile_w, int64_t group_size,
+                        int epilogue, double tau, double v_th, double v_reset, int hard_reset,
+                        int decay_input, void* stream);
 
 CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
                         const float* beta, const float* v_in, float* v_out, float* out,
+                        void* out_nhwc, int64_t cp_out,
                         const float* identity, int identity_mode, const int32_t* ag_mask,
                         const unsigned long long* nnz, int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
@@ -425,20 +440,26 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
   if (epilogue != EPI_LIF && epilogue != EPI_Z) return (int)hipErrorInvalidValue;
   if (identity && identity_mode != ID_ADD_SPIKE && identity_mode != ID_ADD_Z)
     return (int)hipErrorInvalidValue;
+  if (out_nhwc && (cp_out < Cout || cp_out > Coutp)) return (int)hipErrorInvalidValue;
   if (Ho != (H + 2 * pad - KH) / stride + 1 || Wo != (W + 2 * pad - KW) / stride + 1)
     return (int)hipErrorInvalidValue;
   const bool rect = tile_h > 0 && tile_w > 0;
-  // 3x3 convolutions (stride 1/2, pad <= 2, one time-major input) always take
-  // the halo-staged kernel, whatever the route or epilogue, so every
-  // implementation of a layer accumulates in the same order.
-  const bool halo_ok = KH == 3 && KW == 3 && (stride == 1 || stride == 2) && pad <= 2 &&
-                       Cp / KC <= 64 && x_img_tstride == B &&
-                       (!rect || (tile_h == 8 && (tile_w == 8 || (tile_w == 16 && stride == 1))));
+  // 3x3 convolutions and 1x1 convolutions over feature maps of at least
+  // 4x4 (stride 1/2, pad <= 2, one time-major input) always take the
+  // halo-staged kernel, whatever the route or epilogue, so every
+  // implementation of a layer accumulates in the same order.  The choice
+  // depends on the layer shape only.
+  const bool k_ok = (KH == 3 && KW == 3) || (KH == 1 && KW == 1 && Ho >= 4 && Wo >= 4);
+  const bool halo_ok = k_ok && (stride == 1 || stride == 2) && pad <= 2 && Cp / KC <= 64 &&
+                       x_img_tstride == B &&
+                       (!rect || (tile_h == 8 && (tile_w == 8 ||
+                                                  (tile_w == 16 && stride == 1 && KH == 3))));
   if (halo_ok) {
     const int64_t th = 8, tw = rect ? tile_w : 8;
-    return cf_conv_halo(x, w_packed, alpha, beta, v_in, v_out, out, identity, identity_mode,
+    return cf_conv_halo(x, w_packed, alpha, beta, v_in, v_out, out, out_nhwc, cp_out, identity,
+                        identity_mode,
                         rect ? ag_mask : nullptr, nnz, numel, sparse_threshold, T, B, Cp, Cout,
-                        Coutp, H, W, Ho, Wo, stride, pad, th, tw, rect ? group_size : 0,
+                        Coutp, H, W, Ho, Wo, KH, stride, pad, th, tw, rect ? group_size : 0,
                         epilogue, tau, v_th, v_reset, hard_reset, decay_input, stream);
   }
   if (rect) {
@@ -454,6 +475,7 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
   a.x = (const _Float16*)x;
   a.w = (const _Float16*)w_packed;
   a.alpha = alpha; a.beta = beta; a.v_in = v_in; a.v_out = v_out; a.out = out;
+  a.out_nhwc = (_Float16*)out_nhwc; a.cp_out = (int)cp_out;
   a.identity = identity; a.identity_mode = identity_mode; a.ag_mask = ag_mask; a.nnz = nnz; a.numel = numel;
   a.sparse_thr = sparse_threshold;
   a.T = (int)T; a.B = (int)B; a.Cp = (int)Cp; a.Cout = (int)Cout; a.Coutp = (int)Coutp;

@@ -186,6 +186,24 @@ def pad32(c: int) -> int:
     return ((c + 31) // 32) * 32
 
 
+def attach_shadow(out: torch.Tensor, nhwc: torch.Tensor) -> None:
+    """Record the fp16 NHWC copy a fused conv wrote next to its fp32 output,
+    tagged with the output's version counter (any in-place change of `out`
+    invalidates it)."""
+    out._cf_nhwc = (nhwc, out._version)
+
+
+def shadow_of(x: torch.Tensor, shape) -> Optional[torch.Tensor]:
+    """The current fp16 NHWC copy of x with the given shape, or None."""
+    sh = getattr(x, "_cf_nhwc", None)
+    if sh is None:
+        return None
+    t, ver = sh
+    if ver != x._version or tuple(t.shape) != tuple(shape) or t.device != x.device:
+        return None
+    return t
+
+
 def pack_input(x4: torch.Tensor, *, cp: Optional[int] = None, want_xp=True, group_size=0,
                threshold=1e-6, nnz: Optional[torch.Tensor] = None, act_out=None, xp_out=None,
                status: Optional[torch.Tensor] = None):
@@ -322,10 +340,13 @@ class ConvLIFRunner:
 
     def run_mfma(self, x: torch.Tensor, v_in=None, *, epilogue=EPI_LIF, want_v_out=True,
                  identity=None, identity_mode=ID_ADD_SPIKE, sparse=None, sparse_threshold=0.7,
-                 static_zero=True):
+                 static_zero=True, emit_nhwc=True):
         """x [T, B, Cin, H, W] fp32 (values exact in fp16).  sparse: None for
-        flat dense tiles, or a dict with block_h, block_w, group_size to run
-        the prescan and SparseFlow chunk skipping.  Returns (out, v_out)."""
+        the dense route only, or a dict with block_h, block_w, group_size to
+        run the prescan and SparseFlow chunk skipping.  If x carries a current
+        fp16 NHWC copy (written by the producing fused conv) the pack pass is
+        skipped (and with it the StaticZero count); with emit_nhwc the output
+        carries its own copy for the next layer.  Returns (out, v_out)."""
         require_gpu_tensor(x, "x")
         T, B, C, H, W = x.shape
         if C != self.Cin:
@@ -333,17 +354,19 @@ class ConvLIFRunner:
         dev = x.device
         self._ensure_packed(dev)
         Ho, Wo = self.out_hw(H, W)
-        st = status_word(dev)
-        nnz = None
-        if static_zero or sparse is not None:
-            nnz = self.workspace("nnz", (1,), torch.int64, dev)
-            zero_counter(nnz)
         gs = sparse["group_size"] if sparse is not None else 0
-        xp = self.workspace("xp", (T * B, H, W, self.Cp), torch.float16, dev)
-        act = (self.workspace("act", (T * B, H, W), torch.int32, dev) if sparse is not None
-               else None)
-        pack_input(x.reshape(T * B, C, H, W), cp=self.Cp, group_size=gs, nnz=nnz, act_out=act,
-                   xp_out=xp, status=st)
+        xp = shadow_of(x, (T * B, H, W, self.Cp)) if sparse is None else None
+        nnz = act = None
+        if xp is None:
+            st = status_word(dev)
+            if static_zero or sparse is not None:
+                nnz = self.workspace("nnz", (1,), torch.int64, dev)
+                zero_counter(nnz)
+            xp = self.workspace("xp", (T * B, H, W, self.Cp), torch.float16, dev)
+            act = (self.workspace("act", (T * B, H, W), torch.int32, dev) if sparse is not None
+                   else None)
+            pack_input(x.reshape(T * B, C, H, W), cp=self.Cp, group_size=gs, nnz=nnz,
+                       act_out=act, xp_out=xp, status=st)
         ag = None
         th = tw = 0
         if sparse is not None:
@@ -367,10 +390,14 @@ class ConvLIFRunner:
         out = torch.empty((T, B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
         v_out = (torch.empty((B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
                  if (epilogue == EPI_LIF and want_v_out) else None)
+        cp_out = pad32(self.Cout)
+        nhwc = (torch.empty((T * B, Ho, Wo, cp_out), dtype=torch.float16, device=dev)
+                if (emit_nhwc and epilogue == EPI_LIF) else None)
         ev = _t0()
         rc = _hip.lib().cf_conv_mfma(
             ptr(xp), ptr(self.w_packed), ptr(self.alpha), ptr(self.beta), ptr(v_in), ptr(v_out),
-            ptr(out), ptr(identity), int(identity_mode), ptr(ag), ptr(nnz), x.numel(),
+            ptr(out), ptr(nhwc), cp_out, ptr(identity), int(identity_mode), ptr(ag), ptr(nnz),
+            x.numel(),
             float(sparse_threshold), T, B, self.Cp, self.Cout, self.Coutp, H, W, Ho, Wo, self.KH,
             self.KW, self.stride, self.padding, B, th, tw, gs, int(epilogue), *self.lif,
             _hip.stream(dev))
@@ -379,9 +406,12 @@ class ConvLIFRunner:
             flops=2 * T * B * Ho * Wo * self.Cout * self.Cin * self.KH * self.KW)
         self.last_nnz = nnz
         self.last_tiles = None if ag is None else (tc_buf, ag)
+        if nhwc is not None:
+            attach_shadow(out, nhwc)
         return out, v_out
 
-    def run_direct(self, x: torch.Tensor, v_in=None, *, epilogue=EPI_LIF, want_v_out=True):
+    def run_direct(self, x: torch.Tensor, v_in=None, *, epilogue=EPI_LIF, want_v_out=True,
+                   emit_nhwc=True):
         """Analog-input path (fp32 VALU).  x may have a stride-0 time axis
         (direct encoding), in which case the conv is evaluated once."""
         if not x.is_cuda or x.dtype != torch.float32:
@@ -402,12 +432,18 @@ class ConvLIFRunner:
         out = torch.empty((T, B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
         v_out = (torch.empty((B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
                  if (epilogue == EPI_LIF and want_v_out) else None)
+        cp_out = pad32(self.Cout)
+        nhwc = (torch.empty((T * B, Ho, Wo, cp_out), dtype=torch.float16, device=dev)
+                if (emit_nhwc and epilogue == EPI_LIF) else None)
         ev = _t0()
         rc = _hip.lib().cf_conv_direct(
             ptr(xb), ptr(self._w_f32), ptr(self.alpha_direct), ptr(self.beta_direct), ptr(v_in),
-            ptr(v_out), ptr(out), T, B, C, self.Cout, H, W, Ho, Wo, self.KH, self.KW,
-            self.stride, self.padding, tstride, int(epilogue), *self.lif, _hip.stream(dev))
+            ptr(v_out), ptr(out), ptr(nhwc), cp_out, T, B, C, self.Cout, H, W, Ho, Wo, self.KH,
+            self.KW, self.stride, self.padding, tstride, int(epilogue), *self.lif,
+            _hip.stream(dev))
         check(rc, "cf_conv_direct")
         _t1("conv_direct", ev, flops=2 * (1 if tstride == 0 else T) * B * Ho * Wo * self.Cout *
             C * self.KH * self.KW)
+        if nhwc is not None:
+            attach_shadow(out, nhwc)
         return out, v_out

@@ -113,6 +113,9 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
  * the matrix cores, all T steps in one launch.
  *   x: NHWC16 [T*x_img_tstride + B][H][W][Cp] from cf_pack_input;
  *   out: NCHW [T][B][Cout][Ho][Wo] spikes or z;
+ *   out_nhwc (nullable): the same values as fp16 NHWC [T*B][Ho][Wo][cp_out]
+ *   (Cout <= cp_out <= Coutp, channels >= Cout zero) — the staging layout
+ *   the next fused conv reads, so it needs no separate pack pass;
  *   identity (nullable, NCHW like out): identity_mode 1 adds it to the
  *   spikes (SEW ADD, catfuse/patterns.py:672-737), identity_mode 2 adds it
  *   to z before the LIF (BN -> Add -> LIF,
@@ -128,27 +131,28 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
  * catfuse/sparseflow/streamfuse_kernel.py:32-187), and
  * catfuse/sparseflow/fused_conv_bn_lif_kernel.py:342-539. */
 int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha, const float* beta,
-                 const float* v_in, float* v_out, float* out, const float* identity,
-                 int identity_mode, const int32_t* ag_mask, const unsigned long long* nnz, int64_t numel,
+                 const float* v_in, float* v_out, float* out, void* out_nhwc, int64_t cp_out,
+                 const float* identity, int identity_mode, const int32_t* ag_mask, const unsigned long long* nnz, int64_t numel,
                  double sparse_threshold, int64_t T, int64_t B, int64_t Cp, int64_t Cout,
                  int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo, int64_t KH,
                  int64_t KW, int64_t stride, int64_t pad, int64_t x_img_tstride, int64_t tile_h,
                  int64_t tile_w, int64_t group_size, int epilogue, double tau, double v_th,
                  double v_reset, int hard_reset, int decay_input, void* stream);
 
-/* 3x3 Conv (stride 1 or 2) -> BN -> LIF / z with the input halo of each
+/* 3x3 or 1x1 Conv (stride 1 or 2) -> BN -> LIF / z with the input halo of each
  * (tile_h x tile_w) output tile staged in LDS once per 32-channel chunk and
  * up to 4 time steps accumulated per tile (weights fetched once per tap for
- * all of them).  cf_conv_mfma forwards every 3x3 layer here (tile 8x8 when
- * tile_h = 0), so all routes and epilogues of a layer accumulate in the same
- * order.  Tiles: 8x8, or 8x16 with stride 1.  Other arguments as
+ * all of them).  cf_conv_mfma forwards every 3x3 layer and every 1x1 layer
+ * with Ho, Wo >= 4 here (tile 8x8 when tile_h = 0), so all routes and
+ * epilogues of a layer accumulate in the same order.  ksize: 1 or 3.
+ * Tiles: 8x8, or 8x16 with stride 1 and ksize 3.  Other arguments as
  * cf_conv_mfma.  Replaces the same reference interfaces as cf_conv_mfma. */
 int cf_conv_halo(const void* x, const void* w_packed, const float* alpha, const float* beta,
-                 const float* v_in, float* v_out, float* out, const float* identity,
-                 int identity_mode, const int32_t* ag_mask, const unsigned long long* nnz,
+                 const float* v_in, float* v_out, float* out, void* out_nhwc, int64_t cp_out,
+                 const float* identity, int identity_mode, const int32_t* ag_mask, const unsigned long long* nnz,
                  int64_t numel, double sparse_threshold, int64_t T, int64_t B, int64_t Cp,
                  int64_t Cout, int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
-                 int64_t stride, int64_t pad, int64_t tile_h, int64_t tile_w,
+                 int64_t ksize, int64_t stride, int64_t pad, int64_t tile_h, int64_t tile_w,
                  int64_t group_size, int epilogue, double tau, double v_th, double v_reset,
                  int hard_reset, int decay_input, void* stream);
 
@@ -157,7 +161,8 @@ int cf_conv_halo(const void* x, const void* w_packed, const float* alpha, const 
  * convolution once for a time-repeated (direct-encoded) input.  Replaces
  * catfuse/implementations/dense_keep.py:97-155 for the network stem. */
 int cf_conv_direct(const float* x, const float* w, const float* alpha, const float* beta,
-                   const float* v_in, float* v_out, float* out, int64_t T, int64_t B,
+                   const float* v_in, float* v_out, float* out, void* out_nhwc, int64_t cp_out,
+                   int64_t T, int64_t B,
                    int64_t Cin, int64_t Cout, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
                    int64_t KH, int64_t KW, int64_t stride, int64_t pad, int64_t x_img_tstride,
                    int epilogue, double tau, double v_th, double v_reset, int hard_reset,

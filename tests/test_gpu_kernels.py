@@ -312,3 +312,35 @@ def test_conv_direct_stem_parity(cuda, dedupe):
     spk, v = r.run_direct(xd)
     s_ref, v_ref, h_ref = oracle.conv_bn_lif(x.contiguous(), conv, bn, lif)
     lif_parity(spk.cpu().numpy(), v.cpu().numpy(), s_ref, v_ref, h_ref, what="stem")
+
+
+def test_nhwc_shadow_handoff_bitwise_and_invalidated(cuda):
+    """A fused conv's output carries an fp16 NHWC copy that the next fused
+    conv reads instead of re-packing; results are bit-identical, and an
+    in-place change of the fp32 output invalidates the copy."""
+    from catfuse_amd import runtime
+    c1, b1, l1 = _layer(64, 64, 3, 1, 1, seed=41)
+    c2, b2, l2 = _layer(64, 96, 1, 2, 0, seed=42)
+    r1, r2 = _runner(c1, b1, l1, cuda), _runner(c2, b2, l2, cuda)
+    x = (torch.rand(4, 2, 64, 16, 16, generator=_gen(43)) < 0.3).float().to(cuda)
+    y1, _ = r1.run_mfma(x)
+    assert runtime.shadow_of(y1, (8, 16, 16, 64)) is not None
+    ref_xp = torch.zeros(8, 16, 16, 64, dtype=torch.float16, device=cuda)
+    ref_xp[..., :64] = y1.reshape(8, 64, 16, 16).permute(0, 2, 3, 1).half()
+    assert torch.equal(runtime.shadow_of(y1, (8, 16, 16, 64)), ref_xp)
+    y2_shadow, v2a = r2.run_mfma(y1)
+    y2_pack, v2b = r2.run_mfma(y1.clone())          # clone: no shadow -> pack pass
+    assert torch.equal(y2_shadow, y2_pack) and torch.equal(v2a, v2b)
+    y1.mul_(0.0)                                      # in-place change
+    assert runtime.shadow_of(y1, (8, 16, 16, 64)) is None
+    y2_zero, _ = r2.run_mfma(y1)
+    y2_ref, _ = r2.run_mfma(torch.zeros_like(y1))
+    assert torch.equal(y2_zero, y2_ref)
+    # direct (analog) conv emits a copy with zero-padded channels
+    c3, b3, l3 = _layer(3, 40, 3, 1, 1, seed=44)
+    r3 = _runner(c3, b3, l3, cuda)
+    img = torch.randn(4, 2, 3, 8, 8, generator=_gen(45)).to(cuda)
+    y3, _ = r3.run_direct(img)
+    sh = runtime.shadow_of(y3, (8, 8, 8, 64))
+    assert sh is not None and not sh[..., 40:].any()
+    assert torch.equal(sh[..., :40], y3.reshape(8, 40, 8, 8).permute(0, 2, 3, 1).half())
