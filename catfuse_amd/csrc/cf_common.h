@@ -29,9 +29,18 @@ struct LifParams {
   float v_reset;     // ignored when hard == 0 (soft reset)
   float decay_coef;  // (float)(1 - 1/tau) computed in double on the host;
                      // used only by the soft-reset, no-decay-input charge
+  float inv_tau;     // 1/tau, exact when tau_pow2 is set
+  int tau_pow2;      // tau = +-2^k with 1/tau a normal float: x / tau and
+                     // x * inv_tau round the same real number, so the
+                     // multiply gives the division's bits
   int hard;          // 1: hard reset to v_reset; 0: soft reset v -= v_th
   int decay_input;   // 1: v += (x - (v - v_reset)) / tau
 };
+
+// x / tau, IEEE-rounded (the multiply form only where it is bit-identical).
+__device__ __forceinline__ float lif_div_tau(float x, const LifParams& p) {
+  return p.tau_pow2 ? x * p.inv_tau : x / p.tau;
+}
 
 // Charge step, SpikingJelly eval-mode op order.
 //   hard, decay_input    : v = v + (x - (v - v_reset)) / tau
@@ -40,10 +49,10 @@ struct LifParams {
 //   soft, no decay_input : v = v * (1 - 1/tau) + x
 __device__ __forceinline__ float lif_charge(float v, float x, const LifParams& p) {
   if (p.hard) {
-    if (p.decay_input) return v + (x - (v - p.v_reset)) / p.tau;
-    return (v - (v - p.v_reset) / p.tau) + x;
+    if (p.decay_input) return v + lif_div_tau(x - (v - p.v_reset), p);
+    return (v - lif_div_tau(v - p.v_reset, p)) + x;
   }
-  if (p.decay_input) return v + (x - v) / p.tau;
+  if (p.decay_input) return v + lif_div_tau(x - v, p);
   return v * p.decay_coef + x;
 }
 

@@ -29,7 +29,27 @@ namespace {
 
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+// Sixteen zero bytes in device memory: out-of-range halo units load from
+// here, so a loaded register never needs a select that would force the
+// wave to wait for the load before the taps run.
+__device__ __attribute__((aligned(16))) u32x4 g_halo_zero;
+
+// Returns x unchanged, hidden from the optimiser: per-element addresses
+// derived from it are recomputed where they are used instead of being kept
+// live (in registers or scratch) across the K loop.
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+template <typename P>
+__device__ __forceinline__ P* opaque_ptr(P* p) {
+  asm volatile("" : "+s"(p));
+  return p;
+}
 
 constexpr int KC = 32;       // channels per chunk
 constexpr int LDK = KC + 8;  // padded halo pixel (halves)
@@ -68,11 +88,14 @@ __device__ __forceinline__ int halo_route(const unsigned long long* nnz, int64_t
   return (1.0 - (double)k / (double)numel > thr) ? CF_ROUTE_SPARSE : CF_ROUTE_DENSE;
 }
 
-// 128-channel tiles keep 4 x 32 accumulator registers per time block plus
-// double-buffered weight fragments: they get the full 512-register budget.
+// Workgroups per CU the register budget is sized for.  128-channel or
+// 128-pixel tiles keep 4 x 32 accumulator registers per time block and get
+// the full 512-register budget (stride-2 3x3 tiles are held to one
+// workgroup per CU by their 92 KB halo anyway); 64 x 64 tiles fit in 168
+// registers, three workgroups per CU.
 template <int BM, int TH, int TW, int S, int K>
 constexpr int halo_min_blocks() {
-  return (BM >= 128 || (S == 2 && K == 3) || TH * TW >= 128) ? 1 : 2;
+  return (BM >= 128 || (S == 2 && K == 3) || TH * TW >= 128) ? 1 : 3;
 }
 
 // K: filter size (3, or 1 for pointwise convolutions, whose strided input
@@ -88,9 +111,6 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>())) void co
   constexpr int HALO_PIX = RH * RW;
   constexpr int UNITS = TB * HALO_PIX * 4;  // 16-byte units per chunk
   constexpr int PER = (UNITS + 255) / 256;  // staging units per thread
-  // Overlap the next chunk's halo loads with this chunk's taps when the
-  // staging registers are few (stride 1, 8x8 tiles: 7 units per thread).
-  constexpr bool PREFETCH = (S == 1 || K == 1) && TH * TW == 64;
   static_assert(MT >= 1 && NT >= 1, "tile too small");
   __shared__ __attribute__((aligned(16))) _Float16 halo[TB * HALO_PIX * LDK];
 
@@ -118,18 +138,23 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>())) void co
   }
   const int kof = (lane >> 5) * 8;
 
+  // Output channel of accumulator register r in M tile mt is
+  // co_lane + mt * 32 + 8 * (r / 4) + r % 4.  Element indices are 32-bit
+  // (the host checks that every output tensor has fewer than 2^31 elements).
+  const int co_lane = cout0 + wm * WM + 4 * (lane >> 5);
   float v[MT][NT][16];
   if (EPI == EPI_LIF) {
+    const int col = opaque(co_lane);
+    const int vb = (b * a.Cout + col) * HoWo;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int co = cout0 + wm * WM + mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int dc = mt * 32 + 8 * (r >> 2) + (r & 3);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           float v0 = lif_initial_v(a.lif);
-          if (a.v_in && co < a.Cout && n_ok[nt])
-            v0 = a.v_in[((size_t)b * a.Cout + co) * HoWo + e_off[nt]];
+          if (a.v_in && col + dc < a.Cout && n_ok[nt]) v0 = a.v_in[vb + dc * HoWo + e_off[nt]];
           v[mt][nt][r] = v0;
         }
       }
@@ -187,32 +212,34 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>())) void co
         if (chunk_act(c, tmp)) return c;
       return nch;
     };
-    // Halo staging through registers: all loads of a chunk are issued
-    // before any LDS store, and the next chunk's loads are in flight while
-    // the current chunk's taps run.
-    constexpr int NSTG = PREFETCH ? PER : (PER < 8 ? PER : 8);
+    // Halo staging through registers in groups of NSTG 16-byte units: all
+    // loads of a group are issued before its LDS stores.  (No register
+    // prefetch of the next chunk during the taps: vector memory loads retire
+    // in order, so the taps' weight loads would wait for it anyway.)
+    constexpr int NSTG = PER < 8 ? PER : 8;
     u32x4 stg[NSTG];
     auto halo_load = [&](int ch, int i0, u32x4 (&st)[NSTG]) {
       const int c0 = ch * KC;
 #pragma unroll
       for (int i = 0; i < NSTG; ++i) {
-        const int u = tid + 256 * (i0 + i);
+        const int u = opaque(tid) + 256 * (i0 + i);
         const int part = u & 3;
         const int pix = (u >> 2) % HALO_PIX;
         const int t = (u >> 2) / HALO_PIX;
         const int ry = pix / RW, rx = pix % RW;
         const int ih = ih0 + ry * SS, iw = iw0 + rx * SS;
         const bool ok = u < UNITS && t < nsteps && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W;
-        const size_t off =
-            ok ? ((((size_t)(tb0 + t) * a.B + b) * a.H + ih) * a.W + iw) * a.Cp + c0 + part * 8 : 0;
-        const u32x4 val = *reinterpret_cast<const u32x4*>(a.x + off);
-        st[i] = ok ? val : (u32x4)(0u);
+        const u32x4* src =
+            ok ? reinterpret_cast<const u32x4*>(
+                     a.x + ((((size_t)(tb0 + t) * a.B + b) * a.H + ih) * a.W + iw) * a.Cp + c0 + part * 8)
+               : &g_halo_zero;
+        st[i] = *src;
       }
     };
     auto halo_store = [&](int i0, const u32x4 (&st)[NSTG]) {
 #pragma unroll
       for (int i = 0; i < NSTG; ++i) {
-        const int u = tid + 256 * (i0 + i);
+        const int u = opaque(tid) + 256 * (i0 + i);
         if (u < UNITS) {
           const int part = u & 3;
           const int pix = (u >> 2) % HALO_PIX;
@@ -230,8 +257,23 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>())) void co
         halo_store(i0, stg);
       }
     };
+    // Weight fragments: [buffer][mt][ks], hi and lo limbs.  Tap 0 of a chunk
+    // is loaded into buffer 0 before the chunk's halo is staged (loads
+    // retire in order, so it is ready when the taps start).
+    h8 ah[2][MT][2], al[2][MT][2];
+    auto load_tap0 = [&](int chunk) {
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const _Float16* p = wrow[mt] + chunk * KC + ks * 16;
+          ah[0][mt][ks] = *reinterpret_cast<const h8*>(p);
+          al[0][mt][ks] = *reinterpret_cast<const h8*>(p + limb_stride);
+        }
+    };
     int ch = next_chunk(-1);
     if (ch < nch) {
+      load_tap0(ch);
       __syncthreads();  // previous time block's halo reads are complete
       halo_stage(ch);
       __syncthreads();
@@ -240,20 +282,24 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>())) void co
       bool act[TB];
       chunk_act(ch, act);
       const int nx = next_chunk(ch);
-      if (PREFETCH && nx < nch) halo_load(nx, 0, stg);
       const int c0 = ch * KC;
-      h8 ah[2][MT][2], al[2][MT][2];  // [buffer][mt][ks]
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const _Float16* p = wrow[mt] + c0 + ks * 16;
-          ah[0][mt][ks] = *reinterpret_cast<const h8*>(p);
-          al[0][mt][ks] = *reinterpret_cast<const h8*>(p + limb_stride);
-        }
 #pragma unroll
       for (int tap = 0; tap < KK; ++tap) {
         const int cur = tap & 1;
+        const int tap_off = (tap / K) * RW + (tap % K);
+        // All B fragments of the tap are read, unconditionally and before
+        // its first MFMA, so the LDS latency is paid once per tap (reads for
+        // steps this chunk skips are harmless and keep the reads free of
+        // branches, which would otherwise serialise them).
+        h8 bb[TB][2][NT];
+#pragma unroll
+        for (int t = 0; t < TB; ++t)
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int nt = 0; nt < NT; ++nt)
+              bb[t][ks][nt] = *reinterpret_cast<const h8*>(
+                  &halo[(t * HALO_PIX + n_base[nt] + tap_off) * LDK + ks * 16 + kof]);
         if (tap + 1 < KK) {
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt)
@@ -264,88 +310,114 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>())) void co
               al[cur ^ 1][mt][ks] = *reinterpret_cast<const h8*>(p + limb_stride);
             }
         }
-        const int tap_off = (tap / K) * RW + (tap % K);
 #pragma unroll
         for (int t = 0; t < TB; ++t) {
           if (!act[t]) continue;
 #pragma unroll
-          for (int ks = 0; ks < 2; ++ks) {
-            h8 bb[NT];
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
-              bb[nt] = *reinterpret_cast<const h8*>(
-                  &halo[(t * HALO_PIX + n_base[nt] + tap_off) * LDK + ks * 16 + kof]);
+          for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
               for (int nt = 0; nt < NT; ++nt) {
-                acc[t][mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[cur][mt][ks], bb[nt],
-                                                                        acc[t][mt][nt], 0, 0, 0);
-                acc[t][mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[cur][mt][ks], bb[nt],
-                                                                        acc[t][mt][nt], 0, 0, 0);
+                acc[t][mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                    ah[cur][mt][ks], bb[t][ks][nt], acc[t][mt][nt], 0, 0, 0);
+                acc[t][mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                    al[cur][mt][ks], bb[t][ks][nt], acc[t][mt][nt], 0, 0, 0);
               }
-          }
         }
+        // Later taps' reads stay below this tap's MFMAs (register budget).
+        __builtin_amdgcn_sched_barrier(0);
       }
       if (nx < nch) {
+        load_tap0(nx);
         __syncthreads();  // all taps of this chunk have read the halo
-        if (PREFETCH) halo_store(0, stg);
-        else halo_stage(nx);
+        halo_stage(nx);
         __syncthreads();
       }
       ch = nx;
     }
 
-    // Epilogue over the time block.
+    // Epilogue over the time block.  The fp16 NHWC copy of each step's
+    // output tile is staged in LDS (the halo buffer is free here) and written
+    // as 16-byte chunks: one 2*BM-byte run per pixel.
+    constexpr int OLD = BM + 8;  // staged row (halves) per pixel
+    static_assert(BN * OLD <= TB * HALO_PIX * LDK, "output staging exceeds the halo buffer");
+    _Float16* ostage = halo;
+    __syncthreads();  // last chunk's halo reads are complete
 #pragma unroll
     for (int t = 0; t < TB; ++t) {
       if (t >= nsteps) break;
       const int tt = tb0 + t;
+      const int col = opaque(co_lane);
+      const int ob = ((tt * a.B + b) * a.Cout + col) * HoWo;
+      // BN coefficients are re-read per step (L1 hits) rather than hoisted
+      // into 2 x 16 registers that would stay live across the K loop.
+      const float* alpha = opaque_ptr(a.alpha);
+      const float* beta = opaque_ptr(a.beta);
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int co = cout0 + wm * WM + mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-          if (co >= a.Cout) {
-            if (a.out_nhwc && co < a.cp_out)
-#pragma unroll
-              for (int nt = 0; nt < NT; ++nt)
-                if (n_ok[nt]) store_nhwc(a.out_nhwc, a.cp_out, (size_t)tt * a.B + b, HoWo, e_off[nt], co, 0.0f);
-            continue;
-          }
-          const float al_ = a.alpha[co], be = a.beta[co];
+        for (int r4 = 0; r4 < 4; ++r4) {
+          // Registers 4*r4 .. 4*r4+3 hold four consecutive output channels.
+          const int colb = wm * WM + mt * 32 + 8 * r4 + 4 * (lane >> 5);
 #pragma unroll
           for (int nt = 0; nt < NT; ++nt) {
-            if (!n_ok[nt]) continue;
-            const size_t o = ((size_t)(tt * a.B + b) * a.Cout + co) * HoWo + e_off[nt];
-            float z = acc[t][mt][nt][r] * al_ + be;
-            if (a.identity && a.identity_mode == ID_ADD_Z) z = z + a.identity[o];
-            float ov;
-            if (EPI == EPI_Z) {
-              ov = z;
-            } else {
-              float vv = lif_charge(v[mt][nt][r], z, a.lif);
-              const float sp = lif_fire_reset(vv, a.lif);
-              v[mt][nt][r] = vv;
-              ov = (a.identity && a.identity_mode == ID_ADD_SPIKE) ? a.identity[o] + sp : sp;
+            h4 pk;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int r = 4 * r4 + j;
+              const int dc = mt * 32 + 8 * r4 + j;
+              const int co = col + dc;
+              float ov = 0.0f;
+              if (co < a.Cout && n_ok[nt]) {
+                const int o = ob + dc * HoWo + e_off[nt];
+                float z = acc[t][mt][nt][r] * alpha[co] + beta[co];
+                if (a.identity && a.identity_mode == ID_ADD_Z) z = z + a.identity[o];
+                if (EPI == EPI_Z) {
+                  ov = z;
+                } else {
+                  float vv = lif_charge(v[mt][nt][r], z, a.lif);
+                  const float sp = lif_fire_reset(vv, a.lif);
+                  v[mt][nt][r] = vv;
+                  ov = (a.identity && a.identity_mode == ID_ADD_SPIKE) ? a.identity[o] + sp : sp;
+                }
+                if (a.out) a.out[o] = ov;
+              }
+              pk[j] = (_Float16)ov;
             }
-            a.out[o] = ov;
-            if (a.out_nhwc) store_nhwc(a.out_nhwc, a.cp_out, (size_t)tt * a.B + b, HoWo, e_off[nt], co, ov);
+            if (a.out_nhwc)
+              *reinterpret_cast<h4*>(&ostage[(wn * WN + nt * 32 + (lane & 31)) * OLD + colb]) = pk;
           }
         }
+      if (a.out_nhwc) {
+        __syncthreads();
+        constexpr int CH8 = BM / 8;  // 16-byte chunks per pixel
+        for (int c = tid; c < BN * CH8; c += 256) {
+          const int px = c / CH8, part = c % CH8;
+          const int py = px / TW, pxx = px % TW;
+          const int co8 = cout0 + part * 8;
+          if (oh0 + py < a.Ho && ow0 + pxx < a.Wo && co8 < a.cp_out) {
+            const size_t pix = (size_t)(oh0 + py) * a.Wo + (ow0 + pxx);
+            *reinterpret_cast<u32x4*>(a.out_nhwc + (((size_t)tt * a.B + b) * HoWo + pix) * a.cp_out + co8) =
+                *reinterpret_cast<const u32x4*>(&ostage[px * OLD + part * 8]);
+          }
+        }
+        __syncthreads();
+      }
     }
   }
 
   if (EPI == EPI_LIF && a.v_out) {
+    const int col = opaque(co_lane);
+    const int vb = (b * a.Cout + col) * HoWo;
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int co = cout0 + wm * WM + mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int dc = mt * 32 + 8 * (r >> 2) + (r & 3);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt)
-          if (co < a.Cout && n_ok[nt])
-            a.v_out[((size_t)b * a.Cout + co) * HoWo + e_off[nt]] = v[mt][nt][r];
+          if (col + dc < a.Cout && n_ok[nt]) a.v_out[vb + dc * HoWo + e_off[nt]] = v[mt][nt][r];
       }
   }
 }
@@ -375,7 +447,7 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
                         int64_t pad, int64_t tile_h, int64_t tile_w, int64_t group_size,
                         int epilogue, double tau, double v_th, double v_reset, int hard_reset,
                         int decay_input, void* stream) {
-  if (!x || !w_packed || !alpha || !beta || !out) return (int)hipErrorInvalidValue;
+  if (!x || !w_packed || !alpha || !beta || (!out && !out_nhwc)) return (int)hipErrorInvalidValue;
   if (ksize != 1 && ksize != 3) return (int)hipErrorInvalidValue;
   if (out_nhwc && (cp_out < Cout || cp_out > Coutp)) return (int)hipErrorInvalidValue;
   if (T <= 0 || B <= 0 || Cp <= 0 || Cp % KC != 0 || Cp / KC > 64 || Cout <= 0 ||
@@ -392,7 +464,8 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
     return (int)hipErrorInvalidValue;
   if (ag_mask && (group_size <= 0 || (Cp + group_size - 1) / group_size > 32))
     return (int)hipErrorInvalidValue;
-  if (B * Ho * Wo > INT32_MAX || T * B * H * W > ((int64_t)1 << 40)) return (int)hipErrorInvalidValue;
+  if (T * B * Cout * Ho * Wo > INT32_MAX || T * B * H * W > ((int64_t)1 << 40))
+    return (int)hipErrorInvalidValue;
   HaloArgs a;
   a.x = (const _Float16*)x; a.w = (const _Float16*)w_packed; a.alpha = alpha; a.beta = beta;
   a.v_in = v_in; a.v_out = v_out; a.out = out; a.identity = identity;

@@ -303,7 +303,7 @@ __global__ __launch_bounds__(256, (conv_min_blocks<BM, BN, EPI>())) void conv_mf
             v[mb][nb][r] = vv;
             ov = (a.identity && a.identity_mode == ID_ADD_SPIKE) ? a.identity[o] + sp : sp;
           }
-          a.out[o] = ov;
+          if (a.out) a.out[o] = ov;
           if (a.out_nhwc)
             store_nhwc(a.out_nhwc, a.cp_out, (size_t)t * a.B + e_img[nb], HoWo, e_off[nb], co, ov);
         }
@@ -432,7 +432,7 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
                         int64_t pad, int64_t x_img_tstride, int64_t tile_h, int64_t tile_w,
                         int64_t group_size, int epilogue, double tau, double v_th,
                         double v_reset, int hard_reset, int decay_input, void* stream) {
-  if (!x || !w_packed || !alpha || !beta || !out) return (int)hipErrorInvalidValue;
+  if (!x || !w_packed || !alpha || !beta || (!out && !out_nhwc)) return (int)hipErrorInvalidValue;
   if (T <= 0 || B <= 0 || Cp <= 0 || Cp % KC != 0 || Cout <= 0 || Coutp < Cout ||
       Coutp % 64 != 0 || H <= 0 || W <= 0 || Ho <= 0 || Wo <= 0 || KH <= 0 || KW <= 0 ||
       stride <= 0 || pad < 0 || x_img_tstride < 0)
@@ -451,7 +451,7 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
   // depends on the layer shape only.
   const bool k_ok = (KH == 3 && KW == 3) || (KH == 1 && KW == 1 && Ho >= 4 && Wo >= 4);
   const bool halo_ok = k_ok && (stride == 1 || stride == 2) && pad <= 2 && Cp / KC <= 64 &&
-                       x_img_tstride == B &&
+                       x_img_tstride == B && T * B * Cout * Ho * Wo <= INT32_MAX &&
                        (!rect || (tile_h == 8 && (tile_w == 8 ||
                                                   (tile_w == 16 && stride == 1 && KH == 3))));
   if (halo_ok) {

@@ -17,6 +17,7 @@
 // The LIF op order follows SpikingJelly (lif_charge in cf_common.h), not the
 // reference's Triton reformulation v*DECAY + z*RT (lif_seq_kernel.py:37).
 #include "cf_common.h"
+#include <math.h>
 
 namespace {
 
@@ -158,6 +159,10 @@ LifParams cf_make_lif_params(double tau, double v_th, double v_reset, int hard, 
   p.v_th = (float)v_th;
   p.v_reset = hard ? (float)v_reset : 0.0f;
   p.decay_coef = (float)(1.0 - 1.0 / tau);
+  int e2 = 0;
+  const double m = frexp((double)p.tau, &e2);  // |tau| = |m| * 2^e2, |m| in [0.5, 1)
+  p.tau_pow2 = (m == 0.5 || m == -0.5) && e2 - 1 >= -125 && e2 - 1 <= 126 ? 1 : 0;
+  p.inv_tau = p.tau_pow2 ? (float)(1.0 / (double)p.tau) : 0.0f;
   p.hard = hard ? 1 : 0;
   p.decay_input = decay_input ? 1 : 0;
   return p;

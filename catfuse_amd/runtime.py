@@ -411,7 +411,7 @@ class ConvLIFRunner:
         return out, v_out
 
     def run_direct(self, x: torch.Tensor, v_in=None, *, epilogue=EPI_LIF, want_v_out=True,
-                   emit_nhwc=True):
+                   emit_nhwc=False):
         """Analog-input path (fp32 VALU).  x may have a stride-0 time axis
         (direct encoding), in which case the conv is evaluated once."""
         if not x.is_cuda or x.dtype != torch.float32:

@@ -340,7 +340,7 @@ def test_nhwc_shadow_handoff_bitwise_and_invalidated(cuda):
     c3, b3, l3 = _layer(3, 40, 3, 1, 1, seed=44)
     r3 = _runner(c3, b3, l3, cuda)
     img = torch.randn(4, 2, 3, 8, 8, generator=_gen(45)).to(cuda)
-    y3, _ = r3.run_direct(img)
+    y3, _ = r3.run_direct(img, emit_nhwc=True)
     sh = runtime.shadow_of(y3, (8, 8, 8, 64))
     assert sh is not None and not sh[..., 40:].any()
     assert torch.equal(sh[..., :40], y3.reshape(8, 40, 8, 8).permute(0, 2, 3, 1).half())
