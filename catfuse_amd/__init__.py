@@ -13,14 +13,16 @@ __version__ = "0.1.0"
 
 
 def optimize(model, device="cuda:0", policy=None, T=16, use_sparseflow=True,
-             fuse_sew_add=True):
+             fuse_sew_add=True, fuse_stem=True):
     """Substitute the SpikingJelly model's fusible subgraphs with gfx950
     patterns.  `policy` may be a HardwareProfile for the static routing
     table (default: the reference's V100 table shape); `device`, when not
-    None, is where the fused model is placed."""
+    None, is where the fused model is placed.  `fuse_stem` also folds a
+    ResNet stem's MaxPool2d(3, 2, 1) into its Conv-BN-LIF kernel."""
     from catfuse_amd.substitute import substitute, substitute_sf
     if use_sparseflow:
-        fused, stats = substitute_sf(model, T=T, fuse_sew_add=fuse_sew_add, hwprof=policy)
+        fused, stats = substitute_sf(model, T=T, fuse_sew_add=fuse_sew_add, hwprof=policy,
+                                     fuse_stem=fuse_stem)
     else:
         fused, stats = substitute(model)
     if device is not None:
@@ -38,6 +40,9 @@ def check_status(device=None) -> None:
     if st & runtime.STATUS_INEXACT_FP16:
         raise RuntimeError("catfuse_amd: a fused layer on the fp16 MFMA path received inputs "
                            "that are not exactly representable in fp16")
+    if st & runtime.STATUS_FP16_RANGE:
+        raise RuntimeError("catfuse_amd: the fused stem received image values outside the "
+                           "fp16 range (|x| > 65504 or not finite)")
 
 
 __all__ = ["optimize", "check_status", "__version__"]

@@ -20,6 +20,8 @@ enum { CF_ROUTE_ZERO = 0, CF_ROUTE_SPARSE = 1, CF_ROUTE_DENSE = 2 };
 // Status word bits (sticky, device side; read by catfuse_amd.runtime).
 enum {
   CF_STATUS_INEXACT_FP16 = 1u,   // an input assumed fp16-exact was not
+  CF_STATUS_FP16_RANGE = 2u,     // an analog input split into fp16 limbs was
+                                 // outside the fp16 range (or not finite)
 };
 
 // LIF parameters passed by value to every kernel with a LIF epilogue.

@@ -1,0 +1,339 @@
+// Fused network stem: Conv(KH x KW, stride 2) -> BN -> LIF -> MaxPool(3, 2, 1)
+// on the matrix cores, for an analog image that is repeated over T (direct
+// encoding: the convolution is evaluated once per image and its z feeds all
+// T LIF steps, which is exact because z is the same at every step).
+//
+// Replaces, for the SEW/Spiking-ResNet stem, the reference's DenseKeep
+// conv1 -> bn1 -> sn1 (catfuse/implementations/dense_keep.py:97-155 through
+// catfuse/patterns.py:237-387) followed by SpikingJelly's MaxPool2d, which
+// the reference leaves unfused.  The maxpool of spikes is a bitwise OR of
+// the spike trains in the window, so it is exact.
+//
+// Precision: the image is split into fp16 limbs x = xh + xl (xl = x - xh
+// rounded to fp16) and the weights into w*s = wh + wl (s a power of two per
+// channel, undone in alpha).  Each output accumulates, in fp32 on the
+// MFMA, wh*xh + wl*xh + wh*xl over the filter rows; the dropped wl*xl term
+// is below 2^-22 |w x| per product.
+//
+// Workgroup: one 8 x 8 tile of pooled pixels of one image and 64 output
+// channels.  It computes the 17 x 17 conv outputs under the tile's pooling
+// windows (the border row/column is recomputed by the neighbouring tile),
+// runs the LIF over T for each, keeps the spike train of each conv output as
+// a T-bit word in LDS, ORs the words over each 3 x 3 window and writes the
+// pooled spikes (fp32 NCHW and/or the fp16 NHWC copy the next fused conv
+// reads).  v_out holds the final membrane of the conv outputs each tile owns.
+//
+// K layout: for filter row kh the 32 k-values are kw * 4 + c (kw < 8,
+// c < 4), so one 16-byte LDS read gives a lane two neighbouring input pixels
+// of all channels.  Staged input: [limb][row][col][4] fp16.
+#include "cf_common.h"
+
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int PT = 8;                   // pooled tile edge
+constexpr int PR = 2 * PT + 1;          // conv outputs per tile edge (17)
+constexpr int NPIX = PR * PR;           // 289
+constexpr int NTILE = (NPIX + 31) / 32; // 10 MFMA column tiles
+constexpr int CS = 2;                   // conv stride
+constexpr int MAXKH = 7;
+constexpr int KROW = 32;                // k-values per filter row
+constexpr int RH = (PR - 1) * CS + MAXKH;  // 39 staged input rows
+constexpr int RW = (PR - 1) * CS + 8;      // 40 staged input columns
+constexpr int BMS = 64;                 // output channels per workgroup
+constexpr int SLD = BMS + 2;            // spike-word row stride (odd dword count for u16)
+
+struct StemArgs {
+  const float* x;        // [B][Cin][H][W]
+  const _Float16* w;     // [2][Coutp][KH][32]
+  const float* alpha;
+  const float* beta;
+  const float* v_in;     // [B][Cout][Hc][Wc] or null
+  float* v_out;          // [B][Cout][Hc][Wc] or null
+  float* out;            // [T][B][Cout][Hp][Wp] or null
+  _Float16* out_nhwc;    // [T*B][Hp][Wp][cp_out] or null
+  int cp_out;
+  uint32_t* status;
+  int T, B, Cin, Cout, Coutp, H, W, KH, pad, Hc, Wc, Hp, Wp, GHp, GWp;
+  LifParams lif;
+};
+
+template <typename SW>
+__global__ __launch_bounds__(256, sizeof(SW) == 2 ? 2 : 1) void conv_stem_kernel(StemArgs a) {
+  __shared__ __attribute__((aligned(16))) _Float16 xs[2][RH * RW * 4];
+  __shared__ SW spk[NPIX * SLD];
+  __shared__ SW pooled[PT * PT * SLD];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int mt = wave >> 1, nsel = wave & 1;
+  const int tile = blockIdx.x;
+  const int gw = tile % a.GWp, gh = (tile / a.GWp) % a.GHp, b = tile / (a.GWp * a.GHp);
+  const int ph0 = gh * PT, pw0 = gw * PT;
+  const int y0 = 2 * ph0 - 1, x0 = 2 * pw0 - 1;  // conv output at local (0, 0)
+  const int cout0 = blockIdx.y * BMS;
+
+  // Weight fragments of this wave's 32 output channels, all filter rows.
+  h8 wh[MAXKH][2], wl[MAXKH][2];
+  {
+    const int co = cout0 + mt * 32 + (lane & 31);
+    const _Float16* p0 = a.w + (size_t)co * a.KH * KROW + 8 * (lane >> 5);
+    const size_t limb = (size_t)a.Coutp * a.KH * KROW;
+#pragma unroll
+    for (int kh = 0; kh < MAXKH; ++kh)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if (kh < a.KH) {
+          wh[kh][ks] = *reinterpret_cast<const h8*>(p0 + kh * KROW + ks * 16);
+          wl[kh][ks] = *reinterpret_cast<const h8*>(p0 + limb + kh * KROW + ks * 16);
+        } else {
+          wh[kh][ks] = (h8)(_Float16)0.0f;
+          wl[kh][ks] = (h8)(_Float16)0.0f;
+        }
+      }
+  }
+
+  // Stage the input rows/columns under the tile, split into fp16 limbs.
+  {
+    const int ih0 = y0 * CS - a.pad, iw0 = x0 * CS - a.pad;
+    bool overflow = false;
+    for (int p = tid; p < RH * RW; p += 256) {
+      const int ry = p / RW, rx = p % RW;
+      const int ih = ih0 + ry, iw = iw0 + rx;
+      const bool in = ih >= 0 && ih < a.H && iw >= 0 && iw < a.W;
+      h4 hi, lo;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        float v = 0.0f;
+        if (in && c < a.Cin) v = a.x[(((size_t)b * a.Cin + c) * a.H + ih) * a.W + iw];
+        overflow |= !(fabsf(v) <= 65504.0f);
+        const _Float16 h = (_Float16)v;
+        hi[c] = h;
+        lo[c] = (_Float16)(v - (float)h);
+      }
+      *reinterpret_cast<h4*>(&xs[0][p * 4]) = hi;
+      *reinterpret_cast<h4*>(&xs[1][p * 4]) = lo;
+    }
+    if (overflow && a.status) atomicOr(a.status, (uint32_t)CF_STATUS_FP16_RANGE);
+  }
+  __syncthreads();
+
+  // Conv outputs: 10 column tiles x 2 channel tiles over 4 waves; wave
+  // (mt, nsel) takes channel tile mt and column tiles nsel, nsel + 2, ...
+  const int kof2 = 2 * (lane >> 5);  // first kw of this lane's 8 k-values (+4 per ks)
+  for (int nt = nsel; nt < NTILE; nt += 2) {
+    const int n = nt * 32 + (lane & 31);
+    const int nc = n < NPIX ? n : NPIX - 1;  // keeps dead lanes' reads inside the tile
+    const int ly = nc / PR, lx = nc % PR;
+    const int y = y0 + ly, x = x0 + lx;
+    const bool valid = n < NPIX && y >= 0 && y < a.Hc && x >= 0 && x < a.Wc;
+    const int base = ((CS * ly) * RW + CS * lx + kof2) * 4;
+    f16v acc;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+#pragma unroll
+    for (int kh = 0; kh < MAXKH; ++kh) {
+      if (kh >= a.KH) break;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int off = base + (kh * RW + 4 * ks) * 4;
+        const h8 xh = *reinterpret_cast<const h8*>(&xs[0][off]);
+        const h8 xl = *reinterpret_cast<const h8*>(&xs[1][off]);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wh[kh][ks], xh, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wl[kh][ks], xh, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wh[kh][ks], xl, acc, 0, 0, 0);
+      }
+    }
+    // Epilogue: BN, LIF over T with a constant z, spike train -> LDS.
+    const bool own = valid && ly >= 1 && lx >= 1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int cl = mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+      const int co = cout0 + cl;
+      SW bits = 0;
+      if (valid && co < a.Cout) {
+        const float z = acc[r] * a.alpha[co] + a.beta[co];
+        const size_t vi = (((size_t)b * a.Cout + co) * a.Hc + y) * a.Wc + x;
+        float v = a.v_in ? a.v_in[vi] : lif_initial_v(a.lif);
+        for (int t = 0; t < a.T; ++t) {
+          v = lif_charge(v, z, a.lif);
+          if (lif_fire_reset(v, a.lif) != 0.0f) bits |= (SW)((SW)1 << t);
+        }
+        if (own && a.v_out) a.v_out[vi] = v;
+      }
+      if (n < NPIX) spk[n * SLD + cl] = bits;
+    }
+  }
+  __syncthreads();
+
+  // MaxPool(3, 2, 1) of spikes = OR of the spike words in the window (rows
+  // and columns outside the conv output hold zero words, and every window
+  // has a valid position).
+  for (int i = tid; i < PT * PT * BMS; i += 256) {
+    const int cl = i % BMS, pp = i / BMS;
+    const int py = pp / PT, px = pp % PT;
+    SW o = 0;
+#pragma unroll
+    for (int dy = 0; dy < 3; ++dy)
+#pragma unroll
+      for (int dx = 0; dx < 3; ++dx) o |= spk[((2 * py + dy) * PR + 2 * px + dx) * SLD + cl];
+    pooled[pp * SLD + cl] = o;
+  }
+  __syncthreads();
+
+  const int HpWp = a.Hp * a.Wp;
+  if (a.out) {
+    // fp32 NCHW: a thread writes 4 neighbouring pooled pixels of one row.
+    const bool vec = (a.Wp & 3) == 0;
+    for (int i = tid; i < BMS * PT * 2; i += 256) {
+      const int hx = i & 1, py = (i >> 1) % PT, cl = i / (2 * PT);
+      const int co = cout0 + cl, oh = ph0 + py, ow = pw0 + 4 * hx;
+      if (co >= a.Cout || oh >= a.Hp) continue;
+      SW wd[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) wd[q] = pooled[(py * PT + 4 * hx + q) * SLD + cl];
+      for (int t = 0; t < a.T; ++t) {
+        float* dst = a.out + (((size_t)t * a.B + b) * a.Cout + co) * HpWp + (size_t)oh * a.Wp + ow;
+        if (vec && ow + 3 < a.Wp) {
+          float4 f;
+          f.x = (float)((wd[0] >> t) & 1);
+          f.y = (float)((wd[1] >> t) & 1);
+          f.z = (float)((wd[2] >> t) & 1);
+          f.w = (float)((wd[3] >> t) & 1);
+          *reinterpret_cast<float4*>(dst) = f;
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (ow + q < a.Wp) dst[q] = (float)((wd[q] >> t) & 1);
+        }
+      }
+    }
+  }
+  if (a.out_nhwc) {
+    // fp16 NHWC: 16 bytes = 8 channels of one pooled pixel per store.
+    for (int i = tid; i < PT * PT * (BMS / 8); i += 256) {
+      const int c8 = i % (BMS / 8), pp = i / (BMS / 8);
+      const int py = pp / PT, px = pp % PT;
+      const int oh = ph0 + py, ow = pw0 + px, co8 = cout0 + 8 * c8;
+      if (oh >= a.Hp || ow >= a.Wp || co8 >= a.cp_out) continue;
+      SW wd[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) wd[j] = pooled[pp * SLD + 8 * c8 + j];
+      for (int t = 0; t < a.T; ++t) {
+        h8 hv;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hv[j] = (_Float16)(float)((wd[j] >> t) & 1);
+        *reinterpret_cast<h8*>(a.out_nhwc +
+                               (((size_t)t * a.B + b) * HpWp + (size_t)oh * a.Wp + ow) * a.cp_out +
+                               co8) = hv;
+      }
+    }
+  }
+}
+
+// Stem weight packing: fp32 [Cout][Cin][KH][KW] -> fp16 hi/lo
+// [2][Coutp][KH][32] with k = kw * 4 + c (zero beyond KW, Cin), the
+// per-channel power-of-two prescale s_c that keeps |w s| < 2^14, and
+//   alpha = bn_scale / s_c,  beta = bn_shift + bias * bn_scale.
+__global__ __launch_bounds__(256) void pack_stem_weights_kernel(
+    const float* __restrict__ w, int Cout, int Cin, int KH, int KW,
+    const float* __restrict__ bn_scale, const float* __restrict__ bn_shift,
+    const float* __restrict__ bias, _Float16* __restrict__ wp, int Coutp,
+    float* __restrict__ alpha, float* __restrict__ beta) {
+  __shared__ float red[256];
+  const int co = blockIdx.x, tid = threadIdx.x;
+  const int K = Cin * KH * KW;
+  const bool real = co < Cout;
+  float m = 0.0f;
+  if (real)
+    for (int k = tid; k < K; k += 256) m = fmaxf(m, fabsf(w[(size_t)co * K + k]));
+  red[tid] = m;
+  __syncthreads();
+  for (int s = 128; s > 0; s >>= 1) {
+    if (tid < s) red[tid] = fmaxf(red[tid], red[tid + s]);
+    __syncthreads();
+  }
+  m = red[0];
+  float sc = 1.0f, inv = 1.0f;
+  if (m > 0.0f) {
+    int e;
+    frexpf(m, &e);  // m < 2^e
+    int sh = 14 - e;
+    if (sh > 100) sh = 100;
+    if (sh < -100) sh = -100;
+    sc = ldexpf(1.0f, sh);
+    inv = ldexpf(1.0f, -sh);
+  }
+  for (int i = tid; i < KH * KROW; i += 256) {
+    const int kh = i / KROW, k = i % KROW, kw = k / 4, c = k % 4;
+    float ws = 0.0f;
+    if (real && kw < KW && c < Cin) ws = w[(((size_t)co * Cin + c) * KH + kh) * KW + kw] * sc;
+    const _Float16 hi = (_Float16)ws;
+    const _Float16 lo = (_Float16)(ws - (float)hi);
+    wp[((size_t)co * KH + kh) * KROW + k] = hi;
+    wp[(((size_t)Coutp + co) * KH + kh) * KROW + k] = lo;
+  }
+  if (tid == 0) {
+    const float bs = (real && bn_scale) ? bn_scale[co] : 1.0f;
+    const float bh = (real && bn_shift) ? bn_shift[co] : 0.0f;
+    const float bi = (real && bias) ? bias[co] : 0.0f;
+    alpha[co] = real ? bs * inv : 0.0f;
+    beta[co] = real ? (bias ? bh + bi * bs : bh) : 0.0f;
+  }
+}
+
+}  // namespace
+
+CF_API int cf_pack_stem_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, int64_t KW,
+                                int64_t Coutp, const float* bn_scale, const float* bn_shift,
+                                const float* bias, void* w_stem, float* alpha, float* beta,
+                                void* stream) {
+  if (!w || !w_stem || !alpha || !beta || Cout <= 0 || Cin <= 0 || Cin > 4 || KH <= 0 ||
+      KH > MAXKH || KW <= 0 || KW > 8 || Coutp < Cout || Coutp % BMS != 0)
+    return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(pack_stem_weights_kernel, dim3((unsigned)Coutp), dim3(256), 0,
+                     (hipStream_t)stream, w, (int)Cout, (int)Cin, (int)KH, (int)KW, bn_scale,
+                     bn_shift, bias, (_Float16*)w_stem, (int)Coutp, alpha, beta);
+  return (int)hipGetLastError();
+}
+
+CF_API int cf_conv_stem_lif_maxpool(const float* x, const void* w_stem, const float* alpha,
+                                    const float* beta, const float* v_in, float* v_out,
+                                    float* out, void* out_nhwc, int64_t cp_out, uint32_t* status,
+                                    int64_t T, int64_t B, int64_t Cin, int64_t Cout, int64_t Coutp,
+                                    int64_t H, int64_t W, int64_t KH, int64_t KW, int64_t stride,
+                                    int64_t pad, int64_t pool_k, int64_t pool_stride,
+                                    int64_t pool_pad, double tau, double v_th, double v_reset,
+                                    int hard_reset, int decay_input, void* stream) {
+  if (!x || !w_stem || !alpha || !beta || (!out && !out_nhwc)) return (int)hipErrorInvalidValue;
+  if (T <= 0 || T > 32 || B <= 0 || Cin <= 0 || Cin > 4 || Cout <= 0 || Coutp < Cout ||
+      Coutp % BMS != 0 || H <= 0 || W <= 0 || KH <= 0 || KH > MAXKH || KW <= 0 || KW > 8 ||
+      stride != CS || pad < 0)
+    return (int)hipErrorInvalidValue;
+  if (pool_k != 3 || pool_stride != 2 || pool_pad != 1) return (int)hipErrorInvalidValue;
+  if (out_nhwc && (cp_out < Cout || cp_out > Coutp || cp_out % 8 != 0))
+    return (int)hipErrorInvalidValue;
+  const int64_t Hc = (H + 2 * pad - KH) / CS + 1, Wc = (W + 2 * pad - KW) / CS + 1;
+  if (Hc <= 0 || Wc <= 0) return (int)hipErrorInvalidValue;
+  const int64_t Hp = (Hc + 2 - 3) / 2 + 1, Wp = (Wc + 2 - 3) / 2 + 1;
+  const int64_t GHp = (Hp + PT - 1) / PT, GWp = (Wp + PT - 1) / PT;
+  if (B * GHp * GWp > INT32_MAX || T * B * Cout * Hp * Wp > ((int64_t)1 << 40))
+    return (int)hipErrorInvalidValue;
+  StemArgs a;
+  a.x = x; a.w = (const _Float16*)w_stem; a.alpha = alpha; a.beta = beta;
+  a.v_in = v_in; a.v_out = v_out; a.out = out; a.out_nhwc = (_Float16*)out_nhwc;
+  a.cp_out = (int)cp_out; a.status = status;
+  a.T = (int)T; a.B = (int)B; a.Cin = (int)Cin; a.Cout = (int)Cout; a.Coutp = (int)Coutp;
+  a.H = (int)H; a.W = (int)W; a.KH = (int)KH; a.pad = (int)pad;
+  a.Hc = (int)Hc; a.Wc = (int)Wc; a.Hp = (int)Hp; a.Wp = (int)Wp;
+  a.GHp = (int)GHp; a.GWp = (int)GWp;
+  a.lif = cf_make_lif_params(tau, v_th, v_reset, hard_reset, decay_input);
+  dim3 grid((unsigned)(B * GHp * GWp), (unsigned)(Coutp / BMS));
+  hipStream_t st = (hipStream_t)stream;
+  if (T <= 16) hipLaunchKernelGGL(conv_stem_kernel<uint16_t>, grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(conv_stem_kernel<uint32_t>, grid, dim3(256), 0, st, a);
+  return (int)hipGetLastError();
+}

@@ -294,6 +294,64 @@ class PartialFusionConvBNAvgPoolLIF(PartialFusionConvBNLIF):
         return inst
 
 
+class PartialFusionConvBNLIFMaxPool(PartialFusionConvBNLIF):
+    """Conv -> BN -> LIF -> MaxPool2d(3, 2, 1): the SEW/Spiking-ResNet stem.
+
+    No counterpart in the reference, which fuses conv1/bn1/sn1
+    (catfuse/patterns.py:237-387) and leaves SpikingJelly's MaxPool2d after
+    it.  For a direct-encoded image (the same frame at every step, a stride-0
+    time axis) the whole chain is one gfx950 kernel
+    (cf_conv_stem_lif_maxpool): the conv runs once per image on the matrix
+    cores, the LIF over T, and the max of spikes is the OR of their trains.
+    Any other input takes the Conv->BN->LIF kernels followed by the pool.
+    The state is the conv-resolution membrane, as SpikingJelly's sn1 keeps."""
+
+    policy_row = "ConvBNLIFMaxPool"
+
+    def __init__(self, *args, pool=(3, 2, 1), **kw):
+        super().__init__(*args, **kw)
+        self.pool = tuple(int(p) for p in pool)
+
+    def forward(self, x):
+        squeeze = x.ndim == 4
+        if squeeze:
+            x = x.unsqueeze(0)
+        self._impl.check_input(x, self.spec)
+        params = self._ensure_params()
+        r = self._impl.runner(self.spec, params, x.device)
+        if r.stem_supported(x, self.pool) and self._impl.input_is_analog(x):
+            B = x.shape[1]
+            Hc, Wc = r.out_hw(x.shape[3], x.shape[4])
+            v_in = self.state.peek((B, self.out_channels, Hc, Wc), x.device)
+            s, v = r.run_stem_pool(x, v_in)
+            self.state.set(v)
+        else:
+            y = self._run(self._impl, x)
+            T, B = y.shape[:2]
+            k, st, pd = self.pool
+            s = torch.nn.functional.max_pool2d(y.flatten(0, 1), k, st, pd)
+            s = s.reshape(T, B, *s.shape[1:])
+        return s.squeeze(0) if squeeze else s
+
+    @classmethod
+    def from_sj_modules(cls, sj_conv, sj_bn, sj_lif, sj_pool):
+        ks = _first(sj_pool.kernel_size)
+        st = _first(sj_pool.stride if sj_pool.stride is not None else sj_pool.kernel_size)
+        pd = _first(getattr(sj_pool, "padding", 0))
+        if (ks, st, pd) != (3, 2, 1) or _first(getattr(sj_pool, "dilation", 1)) != 1 or \
+                getattr(sj_pool, "ceil_mode", False):
+            raise ValueError("only MaxPool2d(3, 2, 1) is fused")
+        k, s, p = conv_geometry(sj_conv)
+        inst = cls(sj_conv.in_channels, sj_conv.out_channels, k, s, p, bn_eps=sj_bn.eps,
+                   bias=sj_conv.bias is not None, pool=(ks, st, pd), **lif_params(sj_lif))
+        with torch.no_grad():
+            inst.weight.copy_(sj_conv.weight)
+            if sj_conv.bias is not None:
+                inst.conv_bias.copy_(sj_conv.bias)
+        inst._copy_bn(sj_bn)
+        return inst.to(sj_conv.weight.device)
+
+
 # ---------------------------------------------------------------------------
 # Linear -> LIF
 # ---------------------------------------------------------------------------
@@ -616,6 +674,7 @@ PATTERN_REGISTRY = {
     "PartialFusionConvBNLIF": PartialFusionConvBNLIF,
     "PartialFusionConvBNAddLIF": PartialFusionConvBNAddLIF,
     "PartialFusionConvBNAvgPoolLIF": PartialFusionConvBNAvgPoolLIF,
+    "PartialFusionConvBNLIFMaxPool": PartialFusionConvBNLIFMaxPool,
     "FusedLinearLIF": FusedLinearLIF,
     "FusedAddLIF": FusedAddLIF,
     "FusedAddBNLIF": FusedAddBNLIF,
@@ -631,7 +690,8 @@ from catfuse_amd.sparseflow.ops.st_fusion_conv_bn_lif import STFusionConvBNLIF  
 PATTERN_REGISTRY["STFusionConvBNLIF"] = STFusionConvBNLIF
 
 __all__ = ["CTFPattern", "PartialFusionConvLIF", "PartialFusionConvBNLIF",
-           "PartialFusionConvBNAddLIF", "PartialFusionConvBNAvgPoolLIF", "FusedLinearLIF",
+           "PartialFusionConvBNAddLIF", "PartialFusionConvBNAvgPoolLIF",
+           "PartialFusionConvBNLIFMaxPool", "FusedLinearLIF",
            "FusedAddLIF", "FusedAddBNLIF", "FusedAvgPoolLIF", "CTFSEWBasicBlock",
            "CTFSpikingBasicBlock", "CTFSEWBottleneck", "CTFSpikingBottleneck",
            "STFusionConvBNLIF", "PATTERN_REGISTRY", "fold_bn", "lif_params", "conv_geometry"]

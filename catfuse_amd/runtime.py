@@ -22,6 +22,7 @@ EPI_LIF, EPI_Z = 0, 1
 ID_ADD_SPIKE, ID_ADD_Z = 1, 2
 ROUTE_ZERO, ROUTE_SPARSE, ROUTE_DENSE = 0, 1, 2
 STATUS_INEXACT_FP16 = 1
+STATUS_FP16_RANGE = 2
 
 _status_words: dict = {}
 
@@ -294,12 +295,18 @@ class ConvLIFRunner:
 
     def refresh(self):
         self._packed_key = None
+        self._stem_key = None
+
+    def _param_key(self, device):
+        return (device, self.weight.data_ptr(), getattr(self.weight, "_version", 0),
+                None if self.bn_scale is None else (self.bn_scale.data_ptr(),
+                                                    self.bn_scale._version),
+                None if self.bn_shift is None else (self.bn_shift.data_ptr(),
+                                                    self.bn_shift._version),
+                None if self.bias is None else (self.bias.data_ptr(), self.bias._version))
 
     def _ensure_packed(self, device):
-        key = (device, self.weight.data_ptr(), getattr(self.weight, "_version", 0),
-               None if self.bn_scale is None else (self.bn_scale.data_ptr(), self.bn_scale._version),
-               None if self.bn_shift is None else (self.bn_shift.data_ptr(), self.bn_shift._version),
-               None if self.bias is None else (self.bias.data_ptr(), self.bias._version))
+        key = self._param_key(device)
         if key == self._packed_key:
             return
         w = self.weight.detach().float().contiguous()
@@ -444,6 +451,73 @@ class ConvLIFRunner:
         check(rc, "cf_conv_direct")
         _t1("conv_direct", ev, flops=2 * (1 if tstride == 0 else T) * B * Ho * Wo * self.Cout *
             C * self.KH * self.KW)
+        if nhwc is not None:
+            attach_shadow(out, nhwc)
+        return out, v_out
+
+    # -- fused stem: Conv -> BN -> LIF -> MaxPool(3, 2, 1) -------------------
+
+    def stem_supported(self, x: torch.Tensor, pool) -> bool:
+        """cf_conv_stem_lif_maxpool covers a direct-encoded image (stride-0
+        time axis, or T = 1), at most 4 input channels, filters up to 7 x 8, conv
+        stride 2, T <= 32 and MaxPool2d(3, 2, 1)."""
+        return (x.dim() == 5 and (x.stride(0) == 0 or x.shape[0] == 1) and x[0].is_contiguous()
+                and x.dtype == torch.float32 and self.Cin <= 4 and self.KH <= 7
+                and self.KW <= 8 and self.stride == 2 and 1 <= x.shape[0] <= 32
+                and tuple(int(p) for p in pool) == (3, 2, 1))
+
+    def _ensure_stem_packed(self, device):
+        key = ("stem",) + self._param_key(device)
+        if key == getattr(self, "_stem_key", None):
+            return
+        w = self.weight.detach().float().contiguous()
+        bs = None if self.bn_scale is None else self.bn_scale.detach().float().contiguous()
+        bh = None if self.bn_shift is None else self.bn_shift.detach().float().contiguous()
+        bi = None if self.bias is None else self.bias.detach().float().contiguous()
+        for name, t in (("weight", w), ("bn_scale", bs), ("bn_shift", bh), ("bias", bi)):
+            if t is not None:
+                require_gpu_tensor(t, name)
+        self.w_stem = torch.empty((2, self.Coutp, self.KH, 32), dtype=torch.float16,
+                                  device=device)
+        self.alpha_stem = torch.empty(self.Coutp, dtype=torch.float32, device=device)
+        self.beta_stem = torch.empty(self.Coutp, dtype=torch.float32, device=device)
+        check(_hip.lib().cf_pack_stem_weights(ptr(w), self.Cout, self.Cin, self.KH, self.KW,
+                                              self.Coutp, ptr(bs), ptr(bh), ptr(bi),
+                                              ptr(self.w_stem), ptr(self.alpha_stem),
+                                              ptr(self.beta_stem), _hip.stream(device)),
+              "cf_pack_stem_weights")
+        self._stem_key = key
+
+    def run_stem_pool(self, x: torch.Tensor, v_in=None, *, want_v_out=True, emit_nhwc=True):
+        """x [T, B, Cin, H, W] with a stride-0 time axis.  Returns the pooled
+        spikes [T, B, Cout, Hp, Wp] (carrying the fp16 NHWC copy when
+        emit_nhwc) and the conv-resolution membrane [B, Cout, Hc, Wc]."""
+        if not self.stem_supported(x, (3, 2, 1)):
+            raise ValueError("input/layer not covered by the fused stem kernel")
+        T, B, C, H, W = x.shape
+        dev = x.device
+        require_gpu_tensor(x[0], "x")
+        self._ensure_stem_packed(dev)
+        Hc, Wc = self.out_hw(H, W)
+        Hp, Wp = (Hc - 1) // 2 + 1, (Wc - 1) // 2 + 1
+        if v_in is not None:
+            require_gpu_tensor(v_in, "v_in")
+            if v_in.numel() != B * self.Cout * Hc * Wc:
+                raise ValueError("v_in has the wrong size")
+        out = torch.empty((T, B, self.Cout, Hp, Wp), dtype=torch.float32, device=dev)
+        v_out = (torch.empty((B, self.Cout, Hc, Wc), dtype=torch.float32, device=dev)
+                 if want_v_out else None)
+        cp_out = pad32(self.Cout)
+        nhwc = (torch.empty((T * B, Hp, Wp, cp_out), dtype=torch.float16, device=dev)
+                if emit_nhwc else None)
+        ev = _t0()
+        rc = _hip.lib().cf_conv_stem_lif_maxpool(
+            ptr(x[0]), ptr(self.w_stem), ptr(self.alpha_stem), ptr(self.beta_stem), ptr(v_in),
+            ptr(v_out), ptr(out), ptr(nhwc), cp_out, ptr(status_word(dev)), T, B, C, self.Cout,
+            self.Coutp, H, W, self.KH, self.KW, self.stride, self.padding, 3, 2, 1, *self.lif,
+            _hip.stream(dev))
+        check(rc, "cf_conv_stem_lif_maxpool")
+        _t1("conv_stem", ev, flops=2 * B * Hc * Wc * self.Cout * C * self.KH * self.KW)
         if nhwc is not None:
             attach_shadow(out, nhwc)
         return out, v_out

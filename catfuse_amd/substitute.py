@@ -29,7 +29,8 @@ import torch.nn as nn
 from catfuse_amd.patterns import (CTFSEWBasicBlock, CTFSEWBottleneck, CTFSpikingBasicBlock,
                                   CTFSpikingBottleneck, FusedAvgPoolLIF, FusedLinearLIF,
                                   PartialFusionConvBNAvgPoolLIF, PartialFusionConvBNLIF,
-                                  PartialFusionConvLIF, STFusionConvBNLIF, conv_geometry)
+                                  PartialFusionConvBNLIFMaxPool, PartialFusionConvLIF,
+                                  STFusionConvBNLIF, conv_geometry)
 from catfuse_amd.policy import SpatialBackend, get_policy
 
 
@@ -52,6 +53,24 @@ def _is_avgpool2(m) -> bool:
     s = m.stride if isinstance(m.stride, int) else (m.stride[0] if m.stride else k)
     p = m.padding if isinstance(m.padding, int) else m.padding[0]
     return k == 2 and s == 2 and p == 0
+
+
+def _is_maxpool_321(m) -> bool:
+    if not isinstance(m, nn.MaxPool2d):
+        return False
+    one = lambda v: v if isinstance(v, int) else v[0]  # noqa: E731
+    st = m.stride if m.stride is not None else m.kernel_size
+    return ((one(m.kernel_size), one(st), one(m.padding), one(m.dilation)) == (3, 2, 1, 1)
+            and not m.ceil_mode)
+
+
+def _is_resnet_stem_owner(m) -> bool:
+    """SpikingJelly's SEWResNet / SpikingResNet (or the catfuse_amd.snn
+    stand-ins), whose forward applies conv1 -> bn1 -> sn1 -> maxpool in that
+    order and uses maxpool nowhere else."""
+    return (type(m).__name__ in ("SEWResNet", "SpikingResNet")
+            and _is_sj_conv2d(getattr(m, "conv1", None)) and _is_sj_bn2d(getattr(m, "bn1", None))
+            and _is_lif(getattr(m, "sn1", None)) and _is_maxpool_321(getattr(m, "maxpool", None)))
 
 
 def _is_lif(m) -> bool:
@@ -243,7 +262,7 @@ def _strip_root(name: str) -> str:
 
 
 def substitute_sf(sj_model, T=16, verbose=False, force_sparse=False, fuse_sew_add=True,
-                  hwprof=None):
+                  hwprof=None, fuse_stem=True):
     holder = _Root(copy.deepcopy(sj_model))
     model = holder
     stats = {"total_lif_nodes": _count_lif(model), "fused_lif_nodes": 0, "patterns_matched": {},
@@ -260,6 +279,21 @@ def substitute_sf(sj_model, T=16, verbose=False, force_sparse=False, fuse_sew_ad
         if verbose:
             print(f"  [substitute_sf] {name}: {entry['pattern']} ({entry['shape']}, "
                   f"backend={entry['backend']}, K={entry['K']})")
+
+    # Phase 0: ResNet stem conv1 / bn1 / sn1 / maxpool as one fused kernel
+    # (no counterpart in the reference, which leaves the maxpool unfused).
+    for pname, pmod in list(model.named_modules()):
+        if not (fuse_stem and _is_resnet_stem_owner(pmod)) or id(pmod.sn1) in done:
+            continue
+        c, b, l = pmod.conv1, pmod.bn1, pmod.sn1
+        fused = PartialFusionConvBNLIFMaxPool.from_sj_modules(c, b, l, pmod.maxpool)
+        pmod.conv1 = fused
+        pmod.bn1, pmod.sn1, pmod.maxpool = nn.Identity(), nn.Identity(), nn.Identity()
+        k, st, _ = conv_geometry(c)
+        record(f"{pname}.conv1" if pname else "conv1", fused,
+               {"pattern": "PartialFusionConvBNLIFMaxPool",
+                "shape": f"{c.in_channels}->{c.out_channels}, k={k}, s={st}, maxpool 3/2/1",
+                "backend": SpatialBackend.DENSE_KEEP, "K": T}, l)
 
     # Phase 1a: conv{i} / bn{i} / sn{i}
     for pname, pmod in list(model.named_modules()):

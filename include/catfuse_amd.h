@@ -168,6 +168,36 @@ int cf_conv_direct(const float* x, const float* w, const float* alpha, const flo
                    int epilogue, double tau, double v_th, double v_reset, int hard_reset,
                    int decay_input, void* stream);
 
+/* Stem weight packing for cf_conv_stem_lif_maxpool: fp32 [Cout][Cin][KH][KW]
+ * (Cin <= 4, KH <= 7, KW <= 8) -> fp16 hi/lo limbs [2][Coutp][KH][32] with
+ * k = kw*4 + c, a per-channel power-of-two prescale, and the folded
+ * epilogue alpha/beta [Coutp] (BN scale/shift, conv bias).  Replaces the
+ * weight handling of catfuse/implementations/dense_keep.py:73-95 for the
+ * stem. */
+int cf_pack_stem_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, int64_t KW,
+                         int64_t Coutp, const float* bn_scale, const float* bn_shift,
+                         const float* bias, void* w_stem, float* alpha, float* beta,
+                         void* stream);
+
+/* Fused stem Conv(stride 2) -> BN -> LIF -> MaxPool2d(3, 2, 1) on the matrix
+ * cores for a direct-encoded image x [B][Cin][H][W] (the same frame at all T
+ * <= 32 steps: the conv runs once, its z feeds every LIF step).  The image
+ * is split into fp16 hi/lo limbs; products wh*xh + wl*xh + wh*xl accumulate
+ * in fp32.  Outputs the pooled spikes out [T][B][Cout][Hp][Wp] and/or their
+ * fp16 NHWC copy [T*B][Hp][Wp][cp_out]; v_in/v_out [B][Cout][Hc][Wc] hold
+ * the conv-resolution membrane.  status |= 2 if |x| > 65504 or not finite.
+ * Replaces catfuse/implementations/dense_keep.py:97-155 (conv1/bn1/sn1 via
+ * catfuse/patterns.py:237-387) plus the unfused SpikingJelly MaxPool2d that
+ * follows it in the ResNet stem. */
+int cf_conv_stem_lif_maxpool(const float* x, const void* w_stem, const float* alpha,
+                             const float* beta, const float* v_in, float* v_out, float* out,
+                             void* out_nhwc, int64_t cp_out, uint32_t* status, int64_t T,
+                             int64_t B, int64_t Cin, int64_t Cout, int64_t Coutp, int64_t H,
+                             int64_t W, int64_t KH, int64_t KW, int64_t stride, int64_t pad,
+                             int64_t pool_k, int64_t pool_stride, int64_t pool_pad, double tau,
+                             double v_th, double v_reset, int hard_reset, int decay_input,
+                             void* stream);
+
 /* Diagnostic: one wave computes D(32x32 fp32) = A(32x16 fp16) * B(16x32
  * fp16) through the matrix-core lane mapping cf_conv_mfma relies on.
  * No reference counterpart (layout self-test). */

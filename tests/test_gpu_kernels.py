@@ -10,7 +10,7 @@ import pytest
 import torch
 
 import oracle
-from parity import lif_parity
+from parity import lif_parity, membrane_parity, pooled_parity
 
 pytestmark = pytest.mark.gpu
 
@@ -312,6 +312,63 @@ def test_conv_direct_stem_parity(cuda, dedupe):
     spk, v = r.run_direct(xd)
     s_ref, v_ref, h_ref = oracle.conv_bn_lif(x.contiguous(), conv, bn, lif)
     lif_parity(spk.cpu().numpy(), v.cpu().numpy(), s_ref, v_ref, h_ref, what="stem")
+
+
+STEM_CASES = [
+    # name, T, B, H, W, Cout, lif, continue_state
+    ("rn_stem", 4, 2, 64, 64, 64, None, False),
+    ("odd", 4, 2, 70, 58, 40, None, False),
+    ("t20_state", 20, 1, 48, 48, 64, None, True),
+    ("t1_c128", 1, 3, 32, 32, 128, None, False),
+    ("soft_nodecay", 6, 2, 40, 40, 64, dict(tau=1.7, v_threshold=0.6, v_reset=None,
+                                            decay_input=False), False),
+]
+
+
+@pytest.mark.parametrize("case", STEM_CASES, ids=[c[0] for c in STEM_CASES])
+def test_conv_stem_lif_maxpool_parity(cuda, case):
+    """Fused stem (Conv 7x7/2 -> BN -> LIF -> MaxPool 3/2/1, direct encoding)
+    against the oracle's conv (fp64) -> BN -> LIF, max-pooled on the CPU;
+    the fp16 NHWC copy equals the fp32 output; channels past Cout are zero."""
+    from catfuse_amd import runtime, snn
+    name, T, B, H, W, Cout, lifp, cont = case
+    lif = snn.LIFNode(**lifp) if lifp else None
+    conv, bn, lif = _layer(3, Cout, 7, 2, 3, seed=61, lif=lif)
+    img = torch.randn(B, 3, H, W, generator=_gen(62))
+    r = _runner(conv, bn, lif, cuda)
+    x = img.to(cuda).unsqueeze(0).expand(T, B, 3, H, W)
+    assert r.stem_supported(x, (3, 2, 1))
+    v_in = None
+    if cont:  # continue from the state a first call leaves (same v_in for both)
+        _, v_in = r.run_stem_pool(x)
+    v_in_ref = None if v_in is None else v_in.cpu()
+    runtime.clear_status(cuda)
+    out, v = r.run_stem_pool(x, v_in)
+    torch.cuda.synchronize()
+    assert runtime.read_status(cuda) == 0
+    s_ref, v_ref, h_ref = oracle.conv_bn_lif(x.cpu().contiguous(), conv, bn, lif,
+                                              v_in=v_in_ref)
+    vth = lif.v_threshold
+    pooled_parity(out.cpu().numpy(), s_ref, h_ref, v_th=vth, what=name)
+    membrane_parity(v.cpu().numpy(), v_ref, h_ref, v_th=vth, what=name)
+    Hp, Wp = out.shape[3], out.shape[4]
+    cp = runtime.pad32(Cout)
+    sh = runtime.shadow_of(out, (T * B, Hp, Wp, cp))
+    assert sh is not None and not sh[..., Cout:].any()
+    assert torch.equal(sh[..., :Cout].float(), out.reshape(T * B, Cout, Hp, Wp).permute(0, 2, 3, 1))
+
+
+def test_conv_stem_range_flag(cuda):
+    """An image value outside fp16's range raises the sticky status bit."""
+    from catfuse_amd import runtime
+    conv, bn, lif = _layer(3, 64, 7, 2, 3, seed=63)
+    r = _runner(conv, bn, lif, cuda)
+    img = torch.randn(1, 3, 32, 32)
+    img[0, 1, 5, 7] = 1e6
+    runtime.clear_status(cuda)
+    r.run_stem_pool(img.to(cuda).unsqueeze(0).expand(2, 1, 3, 32, 32))
+    assert runtime.read_status(cuda) & runtime.STATUS_FP16_RANGE
+    runtime.clear_status(cuda)
 
 
 def test_nhwc_shadow_handoff_bitwise_and_invalidated(cuda):

@@ -13,7 +13,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 import oracle
-from parity import lif_parity
+from parity import lif_parity, pooled_parity
 
 pytestmark = pytest.mark.gpu
 
@@ -58,6 +58,34 @@ def test_partial_fusion_conv_bn_lif_c0(cuda):
     assert pat.state.tensor is None
     out2 = pat(x.to(cuda))
     assert torch.equal(out, out2)
+
+
+def test_stem_maxpool_pattern_direct_and_fallback(cuda):
+    """PartialFusionConvBNLIFMaxPool: the fused stem kernel for a direct-
+    encoded image, the Conv-BN-LIF kernels + pool for distinct frames; both
+    against the oracle, and state carried across calls."""
+    from catfuse_amd import snn
+    from catfuse_amd.patterns import PartialFusionConvBNLIFMaxPool
+    m = _triple(3, 64, 7, 2, 3, seed=8)
+    pool = snn.MaxPool2d(3, 2, 1)
+    pat = PartialFusionConvBNLIFMaxPool.from_sj_modules(*m, pool).to(cuda)
+    T, B = 4, 2
+    img = torch.randn(B, 3, 40, 36, generator=_gen(9))
+    x = img.unsqueeze(0).expand(T, B, 3, 40, 36)
+    out = pat(img.to(cuda).unsqueeze(0).expand(T, B, 3, 40, 36))
+    s_ref, v_ref, h_ref = oracle.conv_bn_lif(x.contiguous(), *m)
+    pooled_parity(out.cpu().numpy(), s_ref, h_ref, what="direct")
+    v1 = pat.state.tensor.clone()
+    # second call continues from v1 (no reset), like SpikingJelly's sn1
+    out2 = pat(img.to(cuda).unsqueeze(0).expand(T, B, 3, 40, 36))
+    s2, _, h2 = oracle.conv_bn_lif(x.contiguous(), *m, v_in=v1.cpu())
+    pooled_parity(out2.cpu().numpy(), s2, h2, what="continued")
+    # distinct frames: fallback path
+    pat.reset()
+    xs = torch.randn(T, B, 3, 40, 36, generator=_gen(10))
+    out3 = pat(xs.to(cuda))
+    s3, _, h3 = oracle.conv_bn_lif(xs, *m)
+    pooled_parity(out3.cpu().numpy(), s3, h3, what="fallback")
 
 
 @pytest.mark.parametrize("rate", [0.0, 0.01, 0.05, 0.2, 0.5])
@@ -186,6 +214,13 @@ def _hook_layers(pairs):
 def _check_records(recs):
     flips = 0
     for kind, orig, x, ident, out in recs:
+        if kind == "conv_maxpool":
+            conv, bn, lif, pool = orig
+            s_ref, _, h_ref = oracle.conv_bn_lif(x.contiguous(), conv, bn, lif)
+            flips += pooled_parity(out.numpy(), s_ref, h_ref,
+                                   pool=(pool.kernel_size, pool.stride, pool.padding),
+                                   v_th=lif.v_threshold, what=kind)
+            continue
         if kind == "conv":
             s_ref, _, h_ref = oracle.conv_bn_lif(x, *orig)
         elif kind == "conv_pool":
@@ -206,7 +241,7 @@ def _check_records(recs):
 
 
 def _sew_pairs(m, fused):
-    pairs = [(fused.conv1, (m.conv1, m.bn1, m.sn1), "conv")]
+    pairs = [(fused.conv1, (m.conv1, m.bn1, m.sn1, m.maxpool), "conv_maxpool")]
     for li in range(1, 5):
         for mb, fb in zip(getattr(m, f"layer{li}"), getattr(fused, f"layer{li}")):
             pairs.append((fb.fused_first, (mb.conv1, mb.bn1, mb.sn1), "conv"))
