@@ -68,6 +68,44 @@ __device__ __forceinline__ float lif_fire_reset(float& v, const LifParams& p) {
   return s;
 }
 
+// LIF specialisations picked on the host.  LM_GENERIC takes the parameter
+// branches above at run time; LM_HARD_DECAY_P2 is SpikingJelly's default
+// LIFNode (hard reset, decay_input, tau a power of two) with the same
+// operations in the same order and no branches.
+// LM_HARD0_DECAY_P2 is the same with v_reset == +0.0 (SpikingJelly's
+// default), where v - v_reset == v exactly.
+enum { LM_GENERIC = 0, LM_HARD_DECAY_P2 = 1, LM_HARD0_DECAY_P2 = 2 };
+
+__host__ __device__ inline int cf_lif_mode(const LifParams& p) {
+  if (!(p.hard && p.decay_input && p.tau_pow2)) return LM_GENERIC;
+  // +0.0 exactly (not -0.0): v - (+0) == v for every v, signed zeros included
+  return __builtin_bit_cast(uint32_t, p.v_reset) == 0u ? LM_HARD0_DECAY_P2 : LM_HARD_DECAY_P2;
+}
+
+template <int LM>
+__device__ __forceinline__ float lif_charge_m(float v, float x, const LifParams& p) {
+  if constexpr (LM == LM_HARD0_DECAY_P2) return v + (x - v) * p.inv_tau;
+  else if constexpr (LM == LM_HARD_DECAY_P2) return v + (x - (v - p.v_reset)) * p.inv_tau;
+  else return lif_charge(v, x, p);
+}
+
+// Fire + reset returning the spike as a bool.  The hard reset
+// v_reset * s + (1 - s) * v is evaluated as fma(m, v, c) with m = 1 - s and
+// c = v_reset * s selected from {v_reset, 0 * v_reset}: both products are
+// exact (s, m are 0 or 1), so the fma's single rounding is the add's.
+template <int LM>
+__device__ __forceinline__ bool lif_fire_reset_bit(float& v, const LifParams& p) {
+  if constexpr (LM == LM_HARD0_DECAY_P2 || LM == LM_HARD_DECAY_P2) {
+    const bool f = v >= p.v_th;
+    const float m = f ? 0.0f : 1.0f;
+    const float c = LM == LM_HARD0_DECAY_P2 ? 0.0f : (f ? p.v_reset : 0.0f * p.v_reset);
+    v = __builtin_fmaf(m, v, c);
+    return f;
+  } else {
+    return lif_fire_reset(v, p) != 0.0f;
+  }
+}
+
 __device__ __forceinline__ float lif_initial_v(const LifParams& p) {
   return p.hard ? p.v_reset : 0.0f;
 }

@@ -15,8 +15,8 @@
 // MFMA, wh*xh + wl*xh + wh*xl over the filter rows; the dropped wl*xl term
 // is below 2^-22 |w x| per product.
 //
-// Workgroup: one 8 x 8 tile of pooled pixels of one image and 64 output
-// channels.  It computes the 17 x 17 conv outputs under the tile's pooling
+// Workgroup: one 8 x 7 tile of pooled pixels of one image and 64 output
+// channels.  It computes the 17 x 15 conv outputs under the tile's pooling
 // windows (the border row/column is recomputed by the neighbouring tile),
 // runs the LIF over T for each, keeps the spike train of each conv output as
 // a T-bit word in LDS, ORs the words over each 3 x 3 window and writes the
@@ -35,17 +35,26 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int PT = 8;                   // pooled tile edge
-constexpr int PR = 2 * PT + 1;          // conv outputs per tile edge (17)
-constexpr int NPIX = PR * PR;           // 289
-constexpr int NTILE = (NPIX + 31) / 32; // 10 MFMA column tiles
-constexpr int CS = 2;                   // conv stride
+// Pooled tile 8 x 7: its pooling windows cover 17 x 15 = 255 conv outputs,
+// eight MFMA column tiles with a single idle lane.
+constexpr int PTH = 8, PTW = 7;            // pooled tile
+constexpr int PRH = 2 * PTH + 1;           // conv output rows under the tile (17)
+constexpr int PRW = 2 * PTW + 1;           // conv output columns (15)
+constexpr int NPIX = PRH * PRW;            // 255
+constexpr int NTILE = (NPIX + 31) / 32;    // 8 MFMA column tiles
+constexpr int CS = 2;                      // conv stride
 constexpr int MAXKH = 7;
-constexpr int KROW = 32;                // k-values per filter row
-constexpr int RH = (PR - 1) * CS + MAXKH;  // 39 staged input rows
-constexpr int RW = (PR - 1) * CS + 8;      // 40 staged input columns
-constexpr int BMS = 64;                 // output channels per workgroup
-constexpr int SLD = BMS + 2;            // spike-word row stride (odd dword count for u16)
+constexpr int KROW = 32;                   // k-values per filter row
+constexpr int RH = (PRH - 1) * CS + MAXKH; // 39 staged input rows
+constexpr int RW = (PRW - 1) * CS + 8;     // 36 staged input columns
+constexpr int BMS = 64;                    // output channels per workgroup
+
+// Spike-word row stride (in words) per conv output: an odd number of dwords,
+// so the 32 pixels of a column tile land in distinct LDS banks.
+template <typename SW>
+constexpr int spike_ld() {
+  return sizeof(SW) == 1 ? BMS + 4 : (sizeof(SW) == 2 ? BMS + 2 : BMS + 1);
+}
 
 struct StemArgs {
   const float* x;        // [B][Cin][H][W]
@@ -62,17 +71,18 @@ struct StemArgs {
   LifParams lif;
 };
 
-template <typename SW>
-__global__ __launch_bounds__(256, sizeof(SW) == 2 ? 2 : 1) void conv_stem_kernel(StemArgs a) {
+template <typename SW, int LM>
+__global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 2 : 1) void conv_stem_kernel(StemArgs a) {
+  constexpr int SLD = spike_ld<SW>();
   __shared__ __attribute__((aligned(16))) _Float16 xs[2][RH * RW * 4];
   __shared__ SW spk[NPIX * SLD];
-  __shared__ SW pooled[PT * PT * SLD];
+  __shared__ SW pooled[PTH * PTW * SLD];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int mt = wave >> 1, nsel = wave & 1;
   const int tile = blockIdx.x;
   const int gw = tile % a.GWp, gh = (tile / a.GWp) % a.GHp, b = tile / (a.GWp * a.GHp);
-  const int ph0 = gh * PT, pw0 = gw * PT;
+  const int ph0 = gh * PTH, pw0 = gw * PTW;
   const int y0 = 2 * ph0 - 1, x0 = 2 * pw0 - 1;  // conv output at local (0, 0)
   const int cout0 = blockIdx.y * BMS;
 
@@ -97,25 +107,40 @@ __global__ __launch_bounds__(256, sizeof(SW) == 2 ? 2 : 1) void conv_stem_kernel
   }
 
   // Stage the input rows/columns under the tile, split into fp16 limbs.
+  // All loads of the thread are issued before the first conversion.
   {
+    constexpr int NP = (RH * RW + 255) / 256;  // positions per thread
     const int ih0 = y0 * CS - a.pad, iw0 = x0 * CS - a.pad;
-    bool overflow = false;
-    for (int p = tid; p < RH * RW; p += 256) {
+    const size_t plane = (size_t)a.H * a.W;
+    const float* xb = a.x + (size_t)b * a.Cin * plane;
+    float xv[NP][4];
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int p = tid + 256 * i;
       const int ry = p / RW, rx = p % RW;
       const int ih = ih0 + ry, iw = iw0 + rx;
-      const bool in = ih >= 0 && ih < a.H && iw >= 0 && iw < a.W;
+      const bool in = p < RH * RW && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W;
+      const float* src = xb + (size_t)ih * a.W + iw;
+#pragma unroll
+      for (int c = 0; c < 4; ++c) xv[i][c] = (in && c < a.Cin) ? src[c * plane] : 0.0f;
+    }
+    bool overflow = false;
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      const int p = tid + 256 * i;
       h4 hi, lo;
 #pragma unroll
       for (int c = 0; c < 4; ++c) {
-        float v = 0.0f;
-        if (in && c < a.Cin) v = a.x[(((size_t)b * a.Cin + c) * a.H + ih) * a.W + iw];
+        const float v = xv[i][c];
         overflow |= !(fabsf(v) <= 65504.0f);
         const _Float16 h = (_Float16)v;
         hi[c] = h;
         lo[c] = (_Float16)(v - (float)h);
       }
-      *reinterpret_cast<h4*>(&xs[0][p * 4]) = hi;
-      *reinterpret_cast<h4*>(&xs[1][p * 4]) = lo;
+      if (p < RH * RW) {
+        *reinterpret_cast<h4*>(&xs[0][p * 4]) = hi;
+        *reinterpret_cast<h4*>(&xs[1][p * 4]) = lo;
+      }
     }
     if (overflow && a.status) atomicOr(a.status, (uint32_t)CF_STATUS_FP16_RANGE);
   }
@@ -124,108 +149,131 @@ __global__ __launch_bounds__(256, sizeof(SW) == 2 ? 2 : 1) void conv_stem_kernel
   // Conv outputs: 10 column tiles x 2 channel tiles over 4 waves; wave
   // (mt, nsel) takes channel tile mt and column tiles nsel, nsel + 2, ...
   const int kof2 = 2 * (lane >> 5);  // first kw of this lane's 8 k-values (+4 per ks)
-  for (int nt = nsel; nt < NTILE; nt += 2) {
+  const int cl0 = mt * 32 + 4 * (lane >> 5);  // channel of register r: cl0 + 8 * (r / 4) + r % 4
+  const size_t vplane = (size_t)a.Hc * a.Wc;
+
+  // Epilogue of one column tile: BN, then the LIF over T with a constant z,
+  // the 16 elements of the lane stepped together; spike trains -> LDS.
+  auto epilogue = [&](int nt, const f16v& acc) {
     const int n = nt * 32 + (lane & 31);
-    const int nc = n < NPIX ? n : NPIX - 1;  // keeps dead lanes' reads inside the tile
-    const int ly = nc / PR, lx = nc % PR;
+    const int nc = n < NPIX ? n : NPIX - 1;
+    const int ly = nc / PRW, lx = nc % PRW;
     const int y = y0 + ly, x = x0 + lx;
     const bool valid = n < NPIX && y >= 0 && y < a.Hc && x >= 0 && x < a.Wc;
-    const int base = ((CS * ly) * RW + CS * lx + kof2) * 4;
-    f16v acc;
+    const bool own = valid && ly >= 1 && lx >= 1;
+    const size_t vb = (((size_t)b * a.Cout + cout0 + cl0) * a.Hc + y) * a.Wc + x;
+    float zr[16], vr[16];
+    uint32_t bits[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.0f;
+    for (int r = 0; r < 16; ++r) {
+      const int dc = 8 * (r >> 2) + (r & 3);
+      const int co = cout0 + cl0 + dc;
+      const bool ok = valid && co < a.Cout;
+      zr[r] = ok ? acc[r] * a.alpha[co] + a.beta[co] : 0.0f;
+      vr[r] = (ok && a.v_in) ? a.v_in[vb + dc * vplane] : lif_initial_v(a.lif);
+      bits[r] = 0u;
+    }
+    for (int t = 0; t < a.T; ++t) {
+      const uint32_t tbit = 1u << t;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        vr[r] = lif_charge_m<LM>(vr[r], zr[r], a.lif);
+        bits[r] |= lif_fire_reset_bit<LM>(vr[r], a.lif) ? tbit : 0u;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int dc = 8 * (r >> 2) + (r & 3);
+      const bool ok = valid && cout0 + cl0 + dc < a.Cout;
+      if (ok && own && a.v_out) a.v_out[vb + dc * vplane] = vr[r];
+      if (n < NPIX) spk[n * SLD + cl0 + dc] = ok ? (SW)bits[r] : (SW)0;
+    }
+  };
+  auto tile_base = [&](int nt) {
+    const int n = nt * 32 + (lane & 31);
+    const int nc = n < NPIX ? n : NPIX - 1;  // keeps dead lanes' reads inside the tile
+    return ((CS * (nc / PRW)) * RW + CS * (nc % PRW) + kof2) * 4;
+  };
+
+  // Column tiles nsel, nsel + 2, ... of this wave, two at a time so that two
+  // independent accumulation chains share the matrix core.  Accumulation
+  // order per output: filter row, 16-k half, then wh*xh, wl*xh, wh*xl.
+  for (int nt = nsel; nt < NTILE; nt += 4) {
+    const bool two = nt + 2 < NTILE;
+    const int base0 = tile_base(nt), base1 = tile_base(two ? nt + 2 : nt);
+    f16v acc0, acc1;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      acc0[r] = 0.0f;
+      acc1[r] = 0.0f;
+    }
 #pragma unroll
     for (int kh = 0; kh < MAXKH; ++kh) {
       if (kh >= a.KH) break;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const int off = base + (kh * RW + 4 * ks) * 4;
-        const h8 xh = *reinterpret_cast<const h8*>(&xs[0][off]);
-        const h8 xl = *reinterpret_cast<const h8*>(&xs[1][off]);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wh[kh][ks], xh, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wl[kh][ks], xh, acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(wh[kh][ks], xl, acc, 0, 0, 0);
+        const int o = (kh * RW + 4 * ks) * 4;
+        const h8 xh0 = *reinterpret_cast<const h8*>(&xs[0][base0 + o]);
+        const h8 xl0 = *reinterpret_cast<const h8*>(&xs[1][base0 + o]);
+        const h8 xh1 = *reinterpret_cast<const h8*>(&xs[0][base1 + o]);
+        const h8 xl1 = *reinterpret_cast<const h8*>(&xs[1][base1 + o]);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wh[kh][ks], xh0, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wh[kh][ks], xh1, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wl[kh][ks], xh0, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wl[kh][ks], xh1, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wh[kh][ks], xl0, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wh[kh][ks], xl1, acc1, 0, 0, 0);
       }
     }
-    // Epilogue: BN, LIF over T with a constant z, spike train -> LDS.
-    const bool own = valid && ly >= 1 && lx >= 1;
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int cl = mt * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-      const int co = cout0 + cl;
-      SW bits = 0;
-      if (valid && co < a.Cout) {
-        const float z = acc[r] * a.alpha[co] + a.beta[co];
-        const size_t vi = (((size_t)b * a.Cout + co) * a.Hc + y) * a.Wc + x;
-        float v = a.v_in ? a.v_in[vi] : lif_initial_v(a.lif);
-        for (int t = 0; t < a.T; ++t) {
-          v = lif_charge(v, z, a.lif);
-          if (lif_fire_reset(v, a.lif) != 0.0f) bits |= (SW)((SW)1 << t);
-        }
-        if (own && a.v_out) a.v_out[vi] = v;
-      }
-      if (n < NPIX) spk[n * SLD + cl] = bits;
-    }
+    epilogue(nt, acc0);
+    if (two) epilogue(nt + 2, acc1);
   }
   __syncthreads();
 
   // MaxPool(3, 2, 1) of spikes = OR of the spike words in the window (rows
   // and columns outside the conv output hold zero words, and every window
   // has a valid position).
-  for (int i = tid; i < PT * PT * BMS; i += 256) {
+  constexpr int NPOOL = PTH * PTW;
+  for (int i = tid; i < NPOOL * BMS; i += 256) {
     const int cl = i % BMS, pp = i / BMS;
-    const int py = pp / PT, px = pp % PT;
+    const int py = pp / PTW, px = pp % PTW;
     SW o = 0;
 #pragma unroll
     for (int dy = 0; dy < 3; ++dy)
 #pragma unroll
-      for (int dx = 0; dx < 3; ++dx) o |= spk[((2 * py + dy) * PR + 2 * px + dx) * SLD + cl];
+      for (int dx = 0; dx < 3; ++dx) o |= spk[((2 * py + dy) * PRW + 2 * px + dx) * SLD + cl];
     pooled[pp * SLD + cl] = o;
   }
   __syncthreads();
 
   const int HpWp = a.Hp * a.Wp;
   if (a.out) {
-    // fp32 NCHW: a thread writes 4 neighbouring pooled pixels of one row.
-    const bool vec = (a.Wp & 3) == 0;
-    for (int i = tid; i < BMS * PT * 2; i += 256) {
-      const int hx = i & 1, py = (i >> 1) % PT, cl = i / (2 * PT);
-      const int co = cout0 + cl, oh = ph0 + py, ow = pw0 + 4 * hx;
-      if (co >= a.Cout || oh >= a.Hp) continue;
-      SW wd[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) wd[q] = pooled[(py * PT + 4 * hx + q) * SLD + cl];
-      for (int t = 0; t < a.T; ++t) {
-        float* dst = a.out + (((size_t)t * a.B + b) * a.Cout + co) * HpWp + (size_t)oh * a.Wp + ow;
-        if (vec && ow + 3 < a.Wp) {
-          float4 f;
-          f.x = (float)((wd[0] >> t) & 1);
-          f.y = (float)((wd[1] >> t) & 1);
-          f.z = (float)((wd[2] >> t) & 1);
-          f.w = (float)((wd[3] >> t) & 1);
-          *reinterpret_cast<float4*>(dst) = f;
-        } else {
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (ow + q < a.Wp) dst[q] = (float)((wd[q] >> t) & 1);
-        }
-      }
+    // fp32 NCHW: consecutive threads write consecutive pooled pixels of a row.
+    for (int i = tid; i < BMS * NPOOL; i += 256) {
+      const int pp = i % NPOOL, cl = i / NPOOL;
+      const int py = pp / PTW, px = pp % PTW;
+      const int co = cout0 + cl, oh = ph0 + py, ow = pw0 + px;
+      if (co >= a.Cout || oh >= a.Hp || ow >= a.Wp) continue;
+      const uint32_t wd = pooled[pp * SLD + cl];
+      float* dst = a.out + ((size_t)b * a.Cout + co) * HpWp + (size_t)oh * a.Wp + ow;
+      const size_t tstep = (size_t)a.B * a.Cout * HpWp;
+      for (int t = 0; t < a.T; ++t) dst[t * tstep] = (float)((wd >> t) & 1u);
     }
   }
   if (a.out_nhwc) {
     // fp16 NHWC: 16 bytes = 8 channels of one pooled pixel per store.
-    for (int i = tid; i < PT * PT * (BMS / 8); i += 256) {
+    for (int i = tid; i < NPOOL * (BMS / 8); i += 256) {
       const int c8 = i % (BMS / 8), pp = i / (BMS / 8);
-      const int py = pp / PT, px = pp % PT;
+      const int py = pp / PTW, px = pp % PTW;
       const int oh = ph0 + py, ow = pw0 + px, co8 = cout0 + 8 * c8;
       if (oh >= a.Hp || ow >= a.Wp || co8 >= a.cp_out) continue;
-      SW wd[8];
+      uint32_t wd[8];
 #pragma unroll
       for (int j = 0; j < 8; ++j) wd[j] = pooled[pp * SLD + 8 * c8 + j];
       for (int t = 0; t < a.T; ++t) {
         h8 hv;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) hv[j] = (_Float16)(float)((wd[j] >> t) & 1);
+        for (int j = 0; j < 8; ++j) hv[j] = ((wd[j] >> t) & 1u) ? (_Float16)1.0f : (_Float16)0.0f;
         *reinterpret_cast<h8*>(a.out_nhwc +
                                (((size_t)t * a.B + b) * HpWp + (size_t)oh * a.Wp + ow) * a.cp_out +
                                co8) = hv;
@@ -285,6 +333,16 @@ __global__ __launch_bounds__(256) void pack_stem_weights_kernel(
   }
 }
 
+template <typename SW>
+void launch_stem(const StemArgs& a, int lm, dim3 grid, hipStream_t st) {
+  if (lm == LM_HARD0_DECAY_P2)
+    hipLaunchKernelGGL((conv_stem_kernel<SW, LM_HARD0_DECAY_P2>), grid, dim3(256), 0, st, a);
+  else if (lm == LM_HARD_DECAY_P2)
+    hipLaunchKernelGGL((conv_stem_kernel<SW, LM_HARD_DECAY_P2>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((conv_stem_kernel<SW, LM_GENERIC>), grid, dim3(256), 0, st, a);
+}
+
 }  // namespace
 
 CF_API int cf_pack_stem_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, int64_t KW,
@@ -319,7 +377,7 @@ CF_API int cf_conv_stem_lif_maxpool(const float* x, const void* w_stem, const fl
   const int64_t Hc = (H + 2 * pad - KH) / CS + 1, Wc = (W + 2 * pad - KW) / CS + 1;
   if (Hc <= 0 || Wc <= 0) return (int)hipErrorInvalidValue;
   const int64_t Hp = (Hc + 2 - 3) / 2 + 1, Wp = (Wc + 2 - 3) / 2 + 1;
-  const int64_t GHp = (Hp + PT - 1) / PT, GWp = (Wp + PT - 1) / PT;
+  const int64_t GHp = (Hp + PTH - 1) / PTH, GWp = (Wp + PTW - 1) / PTW;
   if (B * GHp * GWp > INT32_MAX || T * B * Cout * Hp * Wp > ((int64_t)1 << 40))
     return (int)hipErrorInvalidValue;
   StemArgs a;
@@ -333,7 +391,9 @@ CF_API int cf_conv_stem_lif_maxpool(const float* x, const void* w_stem, const fl
   a.lif = cf_make_lif_params(tau, v_th, v_reset, hard_reset, decay_input);
   dim3 grid((unsigned)(B * GHp * GWp), (unsigned)(Coutp / BMS));
   hipStream_t st = (hipStream_t)stream;
-  if (T <= 16) hipLaunchKernelGGL(conv_stem_kernel<uint16_t>, grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL(conv_stem_kernel<uint32_t>, grid, dim3(256), 0, st, a);
+  const int lm = cf_lif_mode(a.lif);
+  if (T <= 8) launch_stem<uint8_t>(a, lm, grid, st);
+  else if (T <= 16) launch_stem<uint16_t>(a, lm, grid, st);
+  else launch_stem<uint32_t>(a, lm, grid, st);
   return (int)hipGetLastError();
 }

@@ -36,7 +36,7 @@ template <typename S> __device__ __forceinline__ S to_spike(float s);
 template <> __device__ __forceinline__ float to_spike<float>(float s) { return s; }
 template <> __device__ __forceinline__ uint8_t to_spike<uint8_t>(float s) { return (uint8_t)s; }
 
-template <int MODE, typename S>
+template <int MODE, typename S, int LM>
 __global__ __launch_bounds__(256) void lif_stream_vec4(
     const float* __restrict__ z, const float* __restrict__ z2,
     const float* __restrict__ scale, const float* __restrict__ shift,
@@ -77,8 +77,8 @@ __global__ __launch_bounds__(256) void lif_stream_vec4(
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const float x = input_current<MODE>(zi[j], z2i[j], sc[j], sh[j]);
-      v[j] = lif_charge(v[j], x, p);
-      s[j] = lif_fire_reset(v[j], p);
+      v[j] = lif_charge_m<LM>(v[j], x, p);
+      s[j] = lif_fire_reset_bit<LM>(v[j], p) ? 1.0f : 0.0f;
     }
     if constexpr (sizeof(S) == 4) {
       *reinterpret_cast<float4*>(spike + off) = make_float4(s[0], s[1], s[2], s[3]);
@@ -91,7 +91,7 @@ __global__ __launch_bounds__(256) void lif_stream_vec4(
   if (v_out) *reinterpret_cast<float4*>(v_out + n0) = make_float4(v[0], v[1], v[2], v[3]);
 }
 
-template <int MODE, typename S>
+template <int MODE, typename S, int LM>
 __global__ __launch_bounds__(256) void lif_stream_scalar(
     const float* __restrict__ z, const float* __restrict__ z2,
     const float* __restrict__ scale, const float* __restrict__ shift,
@@ -110,28 +110,45 @@ __global__ __launch_bounds__(256) void lif_stream_scalar(
     const int64_t off = (int64_t)t * N + n;
     const float b = (MODE == M_BN_ADD || MODE == M_ADD || MODE == M_ADD_BN) ? z2[off] : 0.0f;
     const float x = input_current<MODE>(z[off], b, sc, sh);
-    v = lif_charge(v, x, p);
-    spike[off] = to_spike<S>(lif_fire_reset(v, p));
+    v = lif_charge_m<LM>(v, x, p);
+    spike[off] = to_spike<S>(lif_fire_reset_bit<LM>(v, p) ? 1.0f : 0.0f);
   }
   if (v_out) v_out[n] = v;
+}
+
+template <int MODE, typename S, int LM>
+hipError_t launch_lif_m(const float* z, const float* z2, const float* scale, const float* shift,
+                        const float* v_in, S* spike, float* v_out, int T, int64_t N, int C,
+                        int64_t HW, const LifParams& p, hipStream_t st) {
+  const bool aligned = ((uintptr_t)z % 16 == 0) && (!z2 || (uintptr_t)z2 % 16 == 0) &&
+                       ((uintptr_t)spike % (4 * sizeof(S)) == 0) &&
+                       (!v_in || (uintptr_t)v_in % 16 == 0) &&
+                       (!v_out || (uintptr_t)v_out % 16 == 0);
+  if (N % 4 == 0 && aligned) {
+    hipLaunchKernelGGL((lif_stream_vec4<MODE, S, LM>), dim3(cf_blocks(N / 4, 256)), dim3(256), 0,
+                       st, z, z2, scale, shift, v_in, spike, v_out, T, N, C, HW, p);
+  } else {
+    hipLaunchKernelGGL((lif_stream_scalar<MODE, S, LM>), dim3(cf_blocks(N, 256)), dim3(256), 0,
+                       st, z, z2, scale, shift, v_in, spike, v_out, T, N, C, HW, p);
+  }
+  return hipGetLastError();
 }
 
 template <int MODE, typename S>
 hipError_t launch_lif(const float* z, const float* z2, const float* scale, const float* shift,
                       const float* v_in, S* spike, float* v_out, int T, int64_t N, int C,
                       int64_t HW, const LifParams& p, hipStream_t st) {
-  const bool aligned = ((uintptr_t)z % 16 == 0) && (!z2 || (uintptr_t)z2 % 16 == 0) &&
-                       ((uintptr_t)spike % (4 * sizeof(S)) == 0) &&
-                       (!v_in || (uintptr_t)v_in % 16 == 0) &&
-                       (!v_out || (uintptr_t)v_out % 16 == 0);
-  if (N % 4 == 0 && aligned) {
-    hipLaunchKernelGGL((lif_stream_vec4<MODE, S>), dim3(cf_blocks(N / 4, 256)), dim3(256), 0, st,
-                       z, z2, scale, shift, v_in, spike, v_out, T, N, C, HW, p);
-  } else {
-    hipLaunchKernelGGL((lif_stream_scalar<MODE, S>), dim3(cf_blocks(N, 256)), dim3(256), 0, st,
-                       z, z2, scale, shift, v_in, spike, v_out, T, N, C, HW, p);
+  switch (cf_lif_mode(p)) {
+    case LM_HARD0_DECAY_P2:
+      return launch_lif_m<MODE, S, LM_HARD0_DECAY_P2>(z, z2, scale, shift, v_in, spike, v_out, T,
+                                                      N, C, HW, p, st);
+    case LM_HARD_DECAY_P2:
+      return launch_lif_m<MODE, S, LM_HARD_DECAY_P2>(z, z2, scale, shift, v_in, spike, v_out, T,
+                                                     N, C, HW, p, st);
+    default:
+      return launch_lif_m<MODE, S, LM_GENERIC>(z, z2, scale, shift, v_in, spike, v_out, T, N, C,
+                                               HW, p, st);
   }
-  return hipGetLastError();
 }
 
 template <typename S>

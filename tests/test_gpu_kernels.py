@@ -322,6 +322,10 @@ STEM_CASES = [
     ("t1_c128", 1, 3, 32, 32, 128, None, False),
     ("soft_nodecay", 6, 2, 40, 40, 64, dict(tau=1.7, v_threshold=0.6, v_reset=None,
                                             decay_input=False), False),
+    ("vreset", 4, 2, 48, 48, 64, dict(tau=2.0, v_threshold=1.0, v_reset=-0.2,
+                                      decay_input=True), True),
+    ("tau4_t12", 12, 1, 40, 40, 64, dict(tau=4.0, v_threshold=0.8, v_reset=0.0,
+                                         decay_input=True), False),
 ]
 
 
