@@ -52,7 +52,10 @@ __device__ __forceinline__ P* opaque_ptr(P* p) {
 }
 
 constexpr int KC = 32;       // channels per chunk
-constexpr int LDK = KC + 8;  // padded halo pixel (halves)
+#ifndef CF_HALO_LDK
+#define CF_HALO_LDK (KC + 8)
+#endif
+constexpr int LDK = CF_HALO_LDK;  // padded halo pixel (halves)
 constexpr int TB = 4;        // time steps per block
 
 enum { EPI_LIF = 0, EPI_Z = 1 };
@@ -69,6 +72,8 @@ struct HaloArgs {
   _Float16* out_nhwc;       // [T*B][Ho][Wo][cp_out] or null
   int cp_out;
   const float* identity;
+  const _Float16* identity_nhwc;  // [T*B][Ho][Wo][cp_id] spike-valued identity, or null
+  int cp_id;
   int identity_mode;
   const int32_t* ag_mask;   // [T][B*GH*GW]
   const unsigned long long* nnz;
@@ -98,11 +103,25 @@ constexpr int halo_min_blocks() {
   return (BM >= 128 || (S == 2 && K == 3) || TH * TW >= 128) ? 1 : 3;
 }
 
+// Producer-wave variants (64 x 64 tiles, stride-1 3x3 or 1x1): a fifth wave
+// stages the next chunk's halo into the second of two LDS buffers while the
+// four MFMA waves run the current chunk, so the staging latency is hidden
+// and the MFMA waves' own vector memory queue holds only weight loads.
+#ifndef CF_HALO_PRODUCER
+#define CF_HALO_PRODUCER 0
+#endif
+template <int BM, int TH, int TW, int S, int K>
+constexpr bool halo_producer() {
+  return CF_HALO_PRODUCER && BM == 64 && TH * TW == 64 && (K == 1 || S == 1);
+}
+
 // K: filter size (3, or 1 for pointwise convolutions, whose strided input
 // samples are staged densely: RH = TH, RW = TW).
-template <int BM, int TH, int TW, int S, int K, int EPI>
-__global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>())) void conv_halo_kernel(
-    HaloArgs a) {
+// LM: LIF specialisation (cf_lif_mode) of the EPI_LIF epilogue.
+template <int BM, int TH, int TW, int S, int K, int EPI, int LM,
+          bool PROD = halo_producer<BM, TH, TW, S, K>()>
+__global__ __launch_bounds__((PROD ? 320 : 256), (PROD ? 3 : halo_min_blocks<BM, TH, TW, S, K>()))
+void conv_halo_kernel(HaloArgs a) {
   constexpr int BN = TH * TW;
   constexpr int WM = BM / 2, WN = BN / 2, MT = WM / 32, NT = WN / 32;
   constexpr int RH = K == 1 ? TH : (TH - 1) * S + K, RW = K == 1 ? TW : (TW - 1) * S + K;
@@ -112,9 +131,20 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>())) void co
   constexpr int UNITS = TB * HALO_PIX * 4;  // 16-byte units per chunk
   constexpr int PER = (UNITS + 255) / 256;  // staging units per thread
   static_assert(MT >= 1 && NT >= 1, "tile too small");
-  __shared__ __attribute__((aligned(16))) _Float16 halo[TB * HALO_PIX * LDK];
+  constexpr int NTHR = PROD ? 320 : 256;
+  constexpr int TBR = PROD ? 2 : TB;  // time steps per batch of B-fragment reads
+  // LDS halo pixel: 4 x 16-byte channel parts + 16 bytes of padding (LDK
+  // halves).  The producer's direct-to-LDS loads write 64 lanes x 16 bytes
+  // contiguously, so it loads 5 units per pixel (the fifth reads zeros).
+  constexpr int PUNITS = TB * HALO_PIX * 5;
+  constexpr int PPER = (PUNITS + 63) / 64;  // producer load instructions per chunk
+  constexpr int HBUF = PROD ? (TB * HALO_PIX * LDK > PPER * 512 ? TB * HALO_PIX * LDK : PPER * 512)
+                            : TB * HALO_PIX * LDK;  // one halo buffer (halves)
+  auto halo_idx = [](int P, int part) { return P * LDK + (part << 3); };
+  __shared__ __attribute__((aligned(16))) _Float16 halo[(PROD ? 2 : 1) * HBUF];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const bool producer = PROD && wave == 4;  // stages halos; no MFMA work
   const int wm = wave >> 1, wn = wave & 1;
   const int tile = blockIdx.x;
   const int gw = tile % a.GW, gh = (tile / a.GW) % a.GH, b = tile / (a.GW * a.GH);
@@ -143,7 +173,7 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>())) void co
   // (the host checks that every output tensor has fewer than 2^31 elements).
   const int co_lane = cout0 + wm * WM + 4 * (lane >> 5);
   float v[MT][NT][16];
-  if (EPI == EPI_LIF) {
+  if (EPI == EPI_LIF && !producer) {
     const int col = opaque(co_lane);
     const int vb = (b * a.Cout + col) * HoWo;
 #pragma unroll
@@ -206,6 +236,13 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>())) void co
       }
       return any;
     };
+    // act[t] for a lane-dependent t (no dynamic register indexing).
+    auto act_at = [](const bool (&act)[TB], int t) {
+      bool r = false;
+#pragma unroll
+      for (int i = 0; i < TB; ++i) r = r || (t == i && act[i]);
+      return r;
+    };
     auto next_chunk = [&](int ch) -> int {
       bool tmp[TB];
       for (int c = ch + 1; c < nch; ++c)
@@ -220,6 +257,8 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>())) void co
     u32x4 stg[NSTG];
     auto halo_load = [&](int ch, int i0, u32x4 (&st)[NSTG]) {
       const int c0 = ch * KC;
+      bool act[TB];
+      chunk_act(ch, act);
 #pragma unroll
       for (int i = 0; i < NSTG; ++i) {
         const int u = opaque(tid) + 256 * (i0 + i);
@@ -228,7 +267,8 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>())) void co
         const int t = (u >> 2) / HALO_PIX;
         const int ry = pix / RW, rx = pix % RW;
         const int ih = ih0 + ry * SS, iw = iw0 + rx * SS;
-        const bool ok = u < UNITS && t < nsteps && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W;
+        const bool ok = u < UNITS && t < nsteps && act_at(act, t) && ih >= 0 && ih < a.H &&
+                        iw >= 0 && iw < a.W;
         const u32x4* src =
             ok ? reinterpret_cast<const u32x4*>(
                      a.x + ((((size_t)(tb0 + t) * a.B + b) * a.H + ih) * a.W + iw) * a.Cp + c0 + part * 8)
@@ -257,6 +297,31 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>())) void co
         halo_store(i0, stg);
       }
     };
+    // Producer wave: a whole chunk into buffer `buf` with direct-to-LDS
+    // loads (no registers): instruction j fills 16-byte LDS units
+    // 64 j .. 64 j + 63, lane i unit 64 j + i = 5 P + part (part 4 is the
+    // pixel's padding).  All loads are in flight before the one wait.
+    auto prod_stage = [&](int ch, _Float16* buf) {
+      const int c0 = ch * KC;
+      bool act[TB];
+      chunk_act(ch, act);
+#pragma unroll 4
+      for (int j = 0; j < PPER; ++j) {
+        const int u = 64 * j + opaque(lane);
+        const int P = u / 5, part = u % 5;  // LDS pixel (t, pix), 16-byte part
+        const int pix = P % HALO_PIX, t = P / HALO_PIX;
+        const int ry = pix / RW, rx = pix % RW;
+        const int ih = ih0 + ry * SS, iw = iw0 + rx * SS;
+        const bool ok = part < 4 && t < nsteps && act_at(act, t) && ih >= 0 && ih < a.H &&
+                        iw >= 0 && iw < a.W;
+        const void* src =
+            ok ? static_cast<const void*>(a.x + ((((size_t)(tb0 + t) * a.B + b) * a.H + ih) * a.W +
+                                                 iw) * a.Cp + c0 + part * 8)
+               : static_cast<const void*>(&g_halo_zero);
+        __builtin_amdgcn_global_load_lds(src, buf + 512 * j, 16, 0, 0);
+      }
+      __builtin_amdgcn_s_waitcnt(0);  // all of this wave's loads have landed in LDS
+    };
     // Weight fragments: [buffer][mt][ks], hi and lo limbs.  Tap 0 of a chunk
     // is loaded into buffer 0 before the chunk's halo is staged (loads
     // retire in order, so it is ready when the taps start).
@@ -271,128 +336,181 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>())) void co
           al[0][mt][ks] = *reinterpret_cast<const h8*>(p + limb_stride);
         }
     };
-    int ch = next_chunk(-1);
-    if (ch < nch) {
-      load_tap0(ch);
-      __syncthreads();  // previous time block's halo reads are complete
-      halo_stage(ch);
-      __syncthreads();
-    }
-    while (ch < nch) {
-      bool act[TB];
-      chunk_act(ch, act);
-      const int nx = next_chunk(ch);
+    // The K loop of one chunk from halo buffer hb (MFMA waves only).
+    // The K loop of one chunk: no per-step branches.  A step the chunk is
+    // inactive at (SparseFlow) was staged as zeros, and adding the exact
+    // zero products leaves the accumulator's bits unchanged (it starts at
+    // +0 and is never -0), so this equals skipping the step.
+    auto run_taps = [&](int ch, const _Float16* hb) {
       const int c0 = ch * KC;
 #pragma unroll
       for (int tap = 0; tap < KK; ++tap) {
         const int cur = tap & 1;
         const int tap_off = (tap / K) * RW + (tap % K);
-        // All B fragments of the tap are read, unconditionally and before
-        // its first MFMA, so the LDS latency is paid once per tap (reads for
-        // steps this chunk skips are harmless and keep the reads free of
-        // branches, which would otherwise serialise them).
-        h8 bb[TB][2][NT];
+        // B fragments are read TBR steps at a time, unconditionally and
+        // before those steps' MFMAs (reads for steps this chunk skips are
+        // harmless and keep the reads free of branches, which would
+        // otherwise serialise them).
 #pragma unroll
-        for (int t = 0; t < TB; ++t)
+        for (int th = 0; th < TB; th += TBR) {
+          h8 bb[TBR][2][NT];
 #pragma unroll
-          for (int ks = 0; ks < 2; ++ks)
+          for (int tr = 0; tr < TBR; ++tr)
 #pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
-              bb[t][ks][nt] = *reinterpret_cast<const h8*>(
-                  &halo[(t * HALO_PIX + n_base[nt] + tap_off) * LDK + ks * 16 + kof]);
-        if (tap + 1 < KK) {
+            for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-              const _Float16* p = wrow[mt] + (size_t)(tap + 1) * a.Cp + c0 + ks * 16;
-              ah[cur ^ 1][mt][ks] = *reinterpret_cast<const h8*>(p);
-              al[cur ^ 1][mt][ks] = *reinterpret_cast<const h8*>(p + limb_stride);
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < TB; ++t) {
-          if (!act[t]) continue;
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks)
+              for (int nt = 0; nt < NT; ++nt)
+                bb[tr][ks][nt] = *reinterpret_cast<const h8*>(
+                    &hb[halo_idx((th + tr) * HALO_PIX + n_base[nt] + tap_off, 2 * ks + (lane >> 5))]);
+          if (th == 0 && tap + 1 < KK) {
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-              for (int nt = 0; nt < NT; ++nt) {
-                acc[t][mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                    ah[cur][mt][ks], bb[t][ks][nt], acc[t][mt][nt], 0, 0, 0);
-                acc[t][mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                    al[cur][mt][ks], bb[t][ks][nt], acc[t][mt][nt], 0, 0, 0);
+              for (int ks = 0; ks < 2; ++ks) {
+                const _Float16* p = wrow[mt] + (size_t)(tap + 1) * a.Cp + c0 + ks * 16;
+                ah[cur ^ 1][mt][ks] = *reinterpret_cast<const h8*>(p);
+                al[cur ^ 1][mt][ks] = *reinterpret_cast<const h8*>(p + limb_stride);
+              }
+            // Issue the next tap's weight loads before this tap's MFMAs.
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          // Consecutive MFMAs go to different accumulators (time steps, tiles)
+          // so none waits for the previous one's result; each accumulator
+          // still sums ks 0 hi, ks 0 lo, ks 1 hi, ks 1 lo in that order.
+#pragma unroll
+          for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+            for (int limb = 0; limb < 2; ++limb)
+#pragma unroll
+              for (int tr = 0; tr < TBR; ++tr) {
+                const int t = th + tr;
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                  for (int nt = 0; nt < NT; ++nt)
+                    acc[t][mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                        limb ? al[cur][mt][ks] : ah[cur][mt][ks], bb[tr][ks][nt], acc[t][mt][nt],
+                        0, 0, 0);
               }
         }
         // Later taps' reads stay below this tap's MFMAs (register budget).
         __builtin_amdgcn_sched_barrier(0);
       }
-      if (nx < nch) {
-        load_tap0(nx);
-        __syncthreads();  // all taps of this chunk have read the halo
-        halo_stage(nx);
+    };
+
+    int ch = next_chunk(-1);
+    if constexpr (PROD) {
+      // One barrier per chunk: after it the MFMA waves take chunk k from
+      // buffer k % 2 while the producer fills buffer (k + 1) % 2, which the
+      // MFMA waves finished reading before the barrier.
+      if (ch < nch) {
+        if (producer) prod_stage(ch, halo);
+        else load_tap0(ch);
         __syncthreads();
       }
-      ch = nx;
+      int k = 0;
+      while (ch < nch) {
+        const int nx = next_chunk(ch);
+        if (producer) {
+          if (nx < nch) prod_stage(nx, halo + ((k + 1) & 1) * HBUF);
+        } else {
+          run_taps(ch, halo + (k & 1) * HBUF);
+          if (nx < nch) load_tap0(nx);
+        }
+        __syncthreads();
+        ch = nx;
+        ++k;
+      }
+    } else {
+      if (ch < nch) {
+        load_tap0(ch);
+        __syncthreads();  // previous time block's halo reads are complete
+        halo_stage(ch);
+        __syncthreads();
+      }
+      while (ch < nch) {
+        const int nx = next_chunk(ch);
+        run_taps(ch, halo);
+        if (nx < nch) {
+          load_tap0(nx);
+          __syncthreads();  // all taps of this chunk have read the halo
+          halo_stage(nx);
+          __syncthreads();
+        }
+        ch = nx;
+      }
     }
 
     // Epilogue over the time block.  The fp16 NHWC copy of each step's
     // output tile is staged in LDS (the halo buffer is free here) and written
-    // as 16-byte chunks: one 2*BM-byte run per pixel.
+    // as 16-byte chunks: one 2*BM-byte run per pixel.  A spike-valued
+    // identity (SEW ADD) is read from its fp16 NHWC copy when there is one:
+    // four consecutive channels of a pixel per 8-byte load, exact for the
+    // integer values it holds.
     constexpr int OLD = BM + 8;  // staged row (halves) per pixel
-    static_assert(BN * OLD <= TB * HALO_PIX * LDK, "output staging exceeds the halo buffer");
+    static_assert(BN * OLD <= HBUF, "output staging exceeds the halo buffer");
     _Float16* ostage = halo;
-    __syncthreads();  // last chunk's halo reads are complete
+    if (!PROD) __syncthreads();  // last chunk's halo reads are complete
 #pragma unroll
     for (int t = 0; t < TB; ++t) {
       if (t >= nsteps) break;
       const int tt = tb0 + t;
-      const int col = opaque(co_lane);
-      const int ob = ((tt * a.B + b) * a.Cout + col) * HoWo;
-      // BN coefficients are re-read per step (L1 hits) rather than hoisted
-      // into 2 x 16 registers that would stay live across the K loop.
-      const float* alpha = opaque_ptr(a.alpha);
-      const float* beta = opaque_ptr(a.beta);
+      if (!producer) {
+        const int col = opaque(co_lane);
+        const int ob = ((tt * a.B + b) * a.Cout + col) * HoWo;
+        // BN coefficients are re-read per step (L1 hits) rather than hoisted
+        // into 2 x 16 registers that would stay live across the K loop.
+        const float* alpha = opaque_ptr(a.alpha);
+        const float* beta = opaque_ptr(a.beta);
+        const _Float16* idn = a.identity_nhwc;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+        for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          // Registers 4*r4 .. 4*r4+3 hold four consecutive output channels.
-          const int colb = wm * WM + mt * 32 + 8 * r4 + 4 * (lane >> 5);
+          for (int r4 = 0; r4 < 4; ++r4) {
+            // Registers 4*r4 .. 4*r4+3 hold four consecutive output channels.
+            const int colb = wm * WM + mt * 32 + 8 * r4 + 4 * (lane >> 5);
 #pragma unroll
-          for (int nt = 0; nt < NT; ++nt) {
-            h4 pk;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const int r = 4 * r4 + j;
-              const int dc = mt * 32 + 8 * r4 + j;
-              const int co = col + dc;
-              float ov = 0.0f;
-              if (co < a.Cout && n_ok[nt]) {
-                const int o = ob + dc * HoWo + e_off[nt];
-                float z = acc[t][mt][nt][r] * alpha[co] + beta[co];
-                if (a.identity && a.identity_mode == ID_ADD_Z) z = z + a.identity[o];
-                if (EPI == EPI_Z) {
-                  ov = z;
-                } else {
-                  float vv = lif_charge(v[mt][nt][r], z, a.lif);
-                  const float sp = lif_fire_reset(vv, a.lif);
-                  v[mt][nt][r] = vv;
-                  ov = (a.identity && a.identity_mode == ID_ADD_SPIKE) ? a.identity[o] + sp : sp;
-                }
-                if (a.out) a.out[o] = ov;
+            for (int nt = 0; nt < NT; ++nt) {
+              h4 idh = {};
+              if (idn) {
+                const int pix = n_ok[nt] ? e_off[nt] : 0;
+                idh = *reinterpret_cast<const h4*>(
+                    idn + ((size_t)(tt * a.B + b) * HoWo + pix) * a.cp_id + col + mt * 32 + 8 * r4);
               }
-              pk[j] = (_Float16)ov;
+              h4 pk;
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const int r = 4 * r4 + j;
+                const int dc = mt * 32 + 8 * r4 + j;
+                const int co = col + dc;
+                float ov = 0.0f;
+                if (co < a.Cout && n_ok[nt]) {
+                  const int o = ob + dc * HoWo + e_off[nt];
+                  float z = acc[t][mt][nt][r] * alpha[co] + beta[co];
+                  if (a.identity && a.identity_mode == ID_ADD_Z) z = z + a.identity[o];
+                  if (EPI == EPI_Z) {
+                    ov = z;
+                  } else {
+                    float vv = lif_charge_m<LM>(v[mt][nt][r], z, a.lif);
+                    const float sp = lif_fire_reset_bit<LM>(vv, a.lif) ? 1.0f : 0.0f;
+                    v[mt][nt][r] = vv;
+                    if (idn) ov = (float)idh[j] + sp;
+                    else if (a.identity && a.identity_mode == ID_ADD_SPIKE) ov = a.identity[o] + sp;
+                    else ov = sp;
+                  }
+                  if (a.out) a.out[o] = ov;
+                }
+                pk[j] = (_Float16)ov;
+              }
+              if (a.out_nhwc)
+                *reinterpret_cast<h4*>(&ostage[(wn * WN + nt * 32 + (lane & 31)) * OLD + colb]) = pk;
             }
-            if (a.out_nhwc)
-              *reinterpret_cast<h4*>(&ostage[(wn * WN + nt * 32 + (lane & 31)) * OLD + colb]) = pk;
           }
-        }
+      }
       if (a.out_nhwc) {
         __syncthreads();
         constexpr int CH8 = BM / 8;  // 16-byte chunks per pixel
-        for (int c = tid; c < BN * CH8; c += 256) {
+        for (int c = tid; c < BN * CH8; c += NTHR) {
           const int px = c / CH8, part = c % CH8;
           const int py = px / TW, pxx = px % TW;
           const int co8 = cout0 + part * 8;
@@ -407,7 +525,7 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>())) void co
     }
   }
 
-  if (EPI == EPI_LIF && a.v_out) {
+  if (EPI == EPI_LIF && a.v_out && !producer) {
     const int col = opaque(co_lane);
     const int vb = (b * a.Cout + col) * HoWo;
 #pragma unroll
@@ -425,10 +543,24 @@ __global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>())) void co
 template <int BM, int TH, int TW, int S, int K = 3>
 hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
   dim3 grid((unsigned)(a.B * a.GH * a.GW), (unsigned)(a.Coutp / BM));
-  if (epi == EPI_Z)
-    hipLaunchKernelGGL((conv_halo_kernel<BM, TH, TW, S, K, EPI_Z>), grid, dim3(256), 0, st, a);
-  else
-    hipLaunchKernelGGL((conv_halo_kernel<BM, TH, TW, S, K, EPI_LIF>), grid, dim3(256), 0, st, a);
+  const dim3 block(halo_producer<BM, TH, TW, S, K>() ? 320 : 256);
+  if (epi == EPI_Z) {
+    hipLaunchKernelGGL((conv_halo_kernel<BM, TH, TW, S, K, EPI_Z, LM_GENERIC>), grid, block, 0, st, a);
+  } else {
+    switch (cf_lif_mode(a.lif)) {
+      case LM_HARD0_DECAY_P2:
+        hipLaunchKernelGGL((conv_halo_kernel<BM, TH, TW, S, K, EPI_LIF, LM_HARD0_DECAY_P2>), grid,
+                           block, 0, st, a);
+        break;
+      case LM_HARD_DECAY_P2:
+        hipLaunchKernelGGL((conv_halo_kernel<BM, TH, TW, S, K, EPI_LIF, LM_HARD_DECAY_P2>), grid,
+                           block, 0, st, a);
+        break;
+      default:
+        hipLaunchKernelGGL((conv_halo_kernel<BM, TH, TW, S, K, EPI_LIF, LM_GENERIC>), grid, block,
+                           0, st, a);
+    }
+  }
   return hipGetLastError();
 }
 
@@ -440,7 +572,8 @@ hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
 CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
                         const float* beta, const float* v_in, float* v_out, float* out,
                         void* out_nhwc, int64_t cp_out,
-                        const float* identity, int identity_mode, const int32_t* ag_mask,
+                        const float* identity, const void* identity_nhwc, int64_t cp_id,
+                        int identity_mode, const int32_t* ag_mask,
                         const unsigned long long* nnz, int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
                         int64_t W, int64_t Ho, int64_t Wo, int64_t ksize, int64_t stride,
@@ -460,6 +593,8 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
   if (epilogue != EPI_LIF && epilogue != EPI_Z) return (int)hipErrorInvalidValue;
   if (identity && identity_mode != ID_ADD_SPIKE && identity_mode != ID_ADD_Z)
     return (int)hipErrorInvalidValue;
+  if (identity_nhwc && (identity_mode != ID_ADD_SPIKE || cp_id < Cout || cp_id % 4 != 0))
+    return (int)hipErrorInvalidValue;
   if (!((tile_h == 8 && tile_w == 8) || (tile_h == 8 && tile_w == 16 && stride == 1 && ksize == 3)))
     return (int)hipErrorInvalidValue;
   if (ag_mask && (group_size <= 0 || (Cp + group_size - 1) / group_size > 32))
@@ -469,6 +604,7 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
   HaloArgs a;
   a.x = (const _Float16*)x; a.w = (const _Float16*)w_packed; a.alpha = alpha; a.beta = beta;
   a.v_in = v_in; a.v_out = v_out; a.out = out; a.identity = identity;
+  a.identity_nhwc = (const _Float16*)identity_nhwc; a.cp_id = (int)cp_id;
   a.out_nhwc = (_Float16*)out_nhwc; a.cp_out = (int)cp_out;
   a.identity_mode = identity_mode; a.ag_mask = ag_mask;
   // Without masks the SparseFlow route cannot be taken: pass the count only

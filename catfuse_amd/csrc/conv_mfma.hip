@@ -57,6 +57,8 @@ struct ConvArgs {
   _Float16* out_nhwc;
   int cp_out;
   const float* identity;
+  const _Float16* identity_nhwc;  // spike-valued identity as fp16 NHWC, or null
+  int cp_id;
   int identity_mode;
   const int32_t* ag_mask;
   const unsigned long long* nnz;
@@ -301,7 +303,11 @@ __global__ __launch_bounds__(256, (conv_min_blocks<BM, BN, EPI>())) void conv_mf
             float vv = lif_charge(v[mb][nb][r], z, a.lif);
             float sp = lif_fire_reset(vv, a.lif);
             v[mb][nb][r] = vv;
-            ov = (a.identity && a.identity_mode == ID_ADD_SPIKE) ? a.identity[o] + sp : sp;
+            if (a.identity_nhwc)
+              ov = (float)a.identity_nhwc[((size_t)t * a.B + e_img[nb]) * HoWo * a.cp_id +
+                                          (size_t)e_off[nb] * a.cp_id + co] + sp;
+            else
+              ov = (a.identity && a.identity_mode == ID_ADD_SPIKE) ? a.identity[o] + sp : sp;
           }
           if (a.out) a.out[o] = ov;
           if (a.out_nhwc)
@@ -414,7 +420,8 @@ CF_API int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64
 CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
                         const float* beta, const float* v_in, float* v_out, float* out,
                         void* out_nhwc, int64_t cp_out,
-                        const float* identity, int identity_mode, const int32_t* ag_mask,
+                        const float* identity, const void* identity_nhwc, int64_t cp_id,
+                        int identity_mode, const int32_t* ag_mask,
                         const unsigned long long* nnz, int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
                         int64_t W, int64_t Ho, int64_t Wo, int64_t ksize, int64_t stride,
@@ -425,7 +432,8 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
 CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
                         const float* beta, const float* v_in, float* v_out, float* out,
                         void* out_nhwc, int64_t cp_out,
-                        const float* identity, int identity_mode, const int32_t* ag_mask,
+                        const float* identity, const void* identity_nhwc, int64_t cp_id,
+                        int identity_mode, const int32_t* ag_mask,
                         const unsigned long long* nnz, int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
                         int64_t W, int64_t Ho, int64_t Wo, int64_t KH, int64_t KW, int64_t stride,
@@ -439,6 +447,8 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
     return (int)hipErrorInvalidValue;
   if (epilogue != EPI_LIF && epilogue != EPI_Z) return (int)hipErrorInvalidValue;
   if (identity && identity_mode != ID_ADD_SPIKE && identity_mode != ID_ADD_Z)
+    return (int)hipErrorInvalidValue;
+  if (identity_nhwc && (identity_mode != ID_ADD_SPIKE || cp_id < Cout || cp_id % 4 != 0))
     return (int)hipErrorInvalidValue;
   if (out_nhwc && (cp_out < Cout || cp_out > Coutp)) return (int)hipErrorInvalidValue;
   if (Ho != (H + 2 * pad - KH) / stride + 1 || Wo != (W + 2 * pad - KW) / stride + 1)
@@ -457,7 +467,7 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
   if (halo_ok) {
     const int64_t th = 8, tw = rect ? tile_w : 8;
     return cf_conv_halo(x, w_packed, alpha, beta, v_in, v_out, out, out_nhwc, cp_out, identity,
-                        identity_mode,
+                        identity_nhwc, cp_id, identity_mode,
                         rect ? ag_mask : nullptr, nnz, numel, sparse_threshold, T, B, Cp, Cout,
                         Coutp, H, W, Ho, Wo, KH, stride, pad, th, tw, rect ? group_size : 0,
                         epilogue, tau, v_th, v_reset, hard_reset, decay_input, stream);
@@ -477,6 +487,7 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
   a.alpha = alpha; a.beta = beta; a.v_in = v_in; a.v_out = v_out; a.out = out;
   a.out_nhwc = (_Float16*)out_nhwc; a.cp_out = (int)cp_out;
   a.identity = identity; a.identity_mode = identity_mode; a.ag_mask = ag_mask; a.nnz = nnz; a.numel = numel;
+  a.identity_nhwc = (const _Float16*)identity_nhwc; a.cp_id = (int)cp_id;
   a.sparse_thr = sparse_threshold;
   a.T = (int)T; a.B = (int)B; a.Cp = (int)Cp; a.Cout = (int)Cout; a.Coutp = (int)Coutp;
   a.H = (int)H; a.W = (int)W; a.Ho = (int)Ho; a.Wo = (int)Wo; a.KH = (int)KH; a.KW = (int)KW;

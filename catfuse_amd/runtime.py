@@ -386,10 +386,14 @@ class ConvLIFRunner:
             prescan_tiles(act, H, W, Ho, Wo, self.KH, self.stride, self.padding, th, tw, G,
                           ag_buf, tc_buf)
             ag = ag_buf
+        id_nhwc = None
         if identity is not None:
             require_gpu_tensor(identity, "identity")
             if identity.shape != (T, B, self.Cout, Ho, Wo):
                 raise ValueError("identity shape mismatch")
+            if identity_mode == ID_ADD_SPIKE:
+                # spike-valued identity: read its fp16 NHWC copy when current
+                id_nhwc = shadow_of(identity, (T * B, Ho, Wo, pad32(self.Cout)))
         if v_in is not None:
             require_gpu_tensor(v_in, "v_in")
             if v_in.numel() != B * self.Cout * Ho * Wo:
@@ -403,7 +407,8 @@ class ConvLIFRunner:
         ev = _t0()
         rc = _hip.lib().cf_conv_mfma(
             ptr(xp), ptr(self.w_packed), ptr(self.alpha), ptr(self.beta), ptr(v_in), ptr(v_out),
-            ptr(out), ptr(nhwc), cp_out, ptr(identity), int(identity_mode), ptr(ag), ptr(nnz),
+            ptr(out), ptr(nhwc), cp_out, ptr(identity), ptr(id_nhwc), pad32(self.Cout),
+            int(identity_mode), ptr(ag), ptr(nnz),
             x.numel(),
             float(sparse_threshold), T, B, self.Cp, self.Cout, self.Coutp, H, W, Ho, Wo, self.KH,
             self.KW, self.stride, self.padding, B, th, tw, gs, int(epilogue), *self.lif,

@@ -120,6 +120,9 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
  *   spikes (SEW ADD, catfuse/patterns.py:672-737), identity_mode 2 adds it
  *   to z before the LIF (BN -> Add -> LIF,
  *   catfuse/kernels/partial_fusion_conv_bn_add_lif_impl.py:76-123);
+ *   identity_nhwc (nullable, mode 1 only): the same identity as fp16 NHWC
+ *   [T*B][Ho][Wo][cp_id] (cp_id >= Cout, a multiple of 4), read instead of
+ *   the NCHW one (exact for the integer values a SEW ADD identity holds);
  *   v_in/v_out: [B][Cout][Ho][Wo] (nullable);
  *   tile_h/tile_w > 0 selects rectangular pixel tiles aligned with the
  *   prescan tiles (tile_h*tile_w in {64,128}) and enables SparseFlow chunk
@@ -132,8 +135,10 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
  * catfuse/sparseflow/fused_conv_bn_lif_kernel.py:342-539. */
 int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha, const float* beta,
                  const float* v_in, float* v_out, float* out, void* out_nhwc, int64_t cp_out,
-                 const float* identity, int identity_mode, const int32_t* ag_mask, const unsigned long long* nnz, int64_t numel,
-                 double sparse_threshold, int64_t T, int64_t B, int64_t Cp, int64_t Cout,
+                 const float* identity, const void* identity_nhwc, int64_t cp_id,
+                 int identity_mode, const int32_t* ag_mask, const unsigned long long* nnz,
+                 int64_t numel, double sparse_threshold, int64_t T, int64_t B, int64_t Cp,
+                 int64_t Cout,
                  int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo, int64_t KH,
                  int64_t KW, int64_t stride, int64_t pad, int64_t x_img_tstride, int64_t tile_h,
                  int64_t tile_w, int64_t group_size, int epilogue, double tau, double v_th,
@@ -149,7 +154,8 @@ int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha, const 
  * cf_conv_mfma.  Replaces the same reference interfaces as cf_conv_mfma. */
 int cf_conv_halo(const void* x, const void* w_packed, const float* alpha, const float* beta,
                  const float* v_in, float* v_out, float* out, void* out_nhwc, int64_t cp_out,
-                 const float* identity, int identity_mode, const int32_t* ag_mask, const unsigned long long* nnz,
+                 const float* identity, const void* identity_nhwc, int64_t cp_id,
+                 int identity_mode, const int32_t* ag_mask, const unsigned long long* nnz,
                  int64_t numel, double sparse_threshold, int64_t T, int64_t B, int64_t Cp,
                  int64_t Cout, int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
                  int64_t ksize, int64_t stride, int64_t pad, int64_t tile_h, int64_t tile_w,

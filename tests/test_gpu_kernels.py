@@ -299,6 +299,19 @@ def test_conv_bias_and_sew_identity(cuda):
     assert torch.equal(out.cpu(), ident + spk.cpu())
     s_ref, v_ref, h_ref = oracle.conv_bn_lif(x, conv, bn, lif)
     lif_parity(spk.cpu().numpy(), v.cpu().numpy(), s_ref, v_ref, h_ref, what="bias")
+    # an identity produced by a fused conv carries an fp16 NHWC copy, which
+    # the epilogue reads instead of the NCHW tensor: same bits; the copy of
+    # a SEW sum (values 0, 1, 2) is exact
+    from catfuse_amd import runtime
+    r2 = _runner(*_layer(Cin, Cout, 3, 1, 1, seed=14), cuda)
+    ident2, _ = r2.run_mfma(x.to(cuda))
+    ident3, _ = r2.run_mfma(x.to(cuda), identity=ident2)
+    assert runtime.shadow_of(ident3, (T * B, H, W, 64)) is not None
+    for idt in (ident2, ident3):
+        with_copy, v1 = r.run_mfma(x.to(cuda), identity=idt)
+        without, v2 = r.run_mfma(x.to(cuda), identity=idt.clone())
+        assert torch.equal(with_copy, without) and torch.equal(v1, v2)
+        assert torch.equal(with_copy, idt + spk)
 
 
 @pytest.mark.parametrize("dedupe", [True, False])
