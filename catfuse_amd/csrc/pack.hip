@@ -87,6 +87,45 @@ __global__ __launch_bounds__(256) void pack_kernel(
   }
 }
 
+// The same activity bits and nonzero count from an fp16 NHWC copy that a
+// fused conv already wrote (xp[NPIX][Cp], channels >= C zero), so a
+// SparseFlow layer whose input carries one needs no fp32 pass.  One thread
+// per pixel; group sizes are multiples of 8, so the 8 channels of a 16-byte
+// load share one group.
+__global__ __launch_bounds__(256) void scan_nhwc_kernel(
+    const _Float16* __restrict__ xp, int64_t npix, int Cp, int C, uint32_t* __restrict__ act,
+    int gs, float thr, unsigned long long* __restrict__ nnz) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  __shared__ unsigned int cnt_sh;
+  const int tid = threadIdx.x;
+  const int64_t p = (int64_t)blockIdx.x * 256 + tid;
+  if (tid == 0) cnt_sh = 0;
+  __syncthreads();
+  uint32_t bits = 0;
+  unsigned int cnt = 0;
+  if (p < npix) {
+    const _Float16* src = xp + p * Cp;
+    for (int c0 = 0; c0 < Cp; c0 += 8) {
+      const h8 hv = *reinterpret_cast<const h8*>(src + c0);
+      bool any = false;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float v = (float)hv[j];
+        cnt += (v != 0.0f) ? 1u : 0u;
+        any |= fabsf(v) > thr && c0 + j < C;
+      }
+      if (any) bits |= 1u << (unsigned)(c0 / gs);
+    }
+    if (act) act[p] = bits;
+  }
+  if (nnz) {
+    for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+    if ((tid & 63) == 0) atomicAdd(&cnt_sh, cnt);
+    __syncthreads();
+    if (tid == 0 && cnt_sh) atomicAdd(nnz, (unsigned long long)cnt_sh);
+  }
+}
+
 __global__ void route_kernel(const unsigned long long* __restrict__ nnz, int64_t numel,
                              double sparse_threshold, int32_t* __restrict__ route) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
@@ -117,6 +156,22 @@ CF_API int cf_pack_input(const float* x, int64_t NB, int64_t C, int64_t H, int64
   dim3 grid(cf_blocks(HW, PX), (unsigned)NB);
   hipLaunchKernelGGL(pack_kernel, grid, dim3(256), 0, (hipStream_t)stream, x, C, HW, Cp,
                      (_Float16*)xp, act, group_size, threshold, nnz, status);
+  return (int)hipGetLastError();
+}
+
+CF_API int cf_scan_nhwc(const void* xp, int64_t NB, int64_t H, int64_t W, int64_t Cp, int64_t C,
+                        uint32_t* act, int group_size, float threshold, unsigned long long* nnz,
+                        void* stream) {
+  if (!xp || NB < 0 || H <= 0 || W <= 0 || C <= 0 || Cp < C || Cp % 8 != 0)
+    return (int)hipErrorInvalidValue;
+  if (act && (group_size <= 0 || group_size % 8 != 0 || (C + group_size - 1) / group_size > 32))
+    return (int)hipErrorInvalidValue;
+  if (group_size <= 0) group_size = 32;
+  const int64_t npix = NB * H * W;
+  if (npix == 0) return 0;
+  hipLaunchKernelGGL(scan_nhwc_kernel, dim3(cf_blocks(npix, 256)), dim3(256), 0,
+                     (hipStream_t)stream, (const _Float16*)xp, npix, (int)Cp, (int)C, act,
+                     group_size, threshold, nnz);
   return (int)hipGetLastError();
 }
 

@@ -231,6 +231,22 @@ def pack_input(x4: torch.Tensor, *, cp: Optional[int] = None, want_xp=True, grou
     return xp, act
 
 
+def scan_nhwc(xp: torch.Tensor, C: int, *, group_size: int, threshold=1e-6,
+              nnz: Optional[torch.Tensor] = None, act_out=None):
+    """xp fp16 NHWC [NB, H, W, Cp] (a fused conv's output copy) -> act int32
+    [NB, H, W] with cf_pack_input's bits, and the nonzero count into nnz."""
+    require_gpu_tensor(xp, "xp", dtype=torch.float16)
+    NB, H, W, cp = xp.shape
+    act = act_out if act_out is not None else torch.empty((NB, H, W), dtype=torch.int32,
+                                                          device=xp.device)
+    ev = _t0()
+    rc = _hip.lib().cf_scan_nhwc(ptr(xp), NB, H, W, cp, C, ptr(act), int(group_size),
+                                 float(threshold), ptr(nnz), _hip.stream(xp.device))
+    check(rc, "cf_scan_nhwc")
+    _t1("scan_nhwc", ev, nbytes=2 * NB * H * W * cp + 4 * NB * H * W)
+    return act
+
+
 def prescan_tiles(act: torch.Tensor, H: int, W: int, H_out: int, W_out: int, kernel_size: int,
                   stride: int, padding: int, block_h: int, block_w: int, num_groups: int,
                   ag_mask_out=None, tile_class_out=None):
@@ -352,7 +368,8 @@ class ConvLIFRunner:
         the dense route only, or a dict with block_h, block_w, group_size to
         run the prescan and SparseFlow chunk skipping.  If x carries a current
         fp16 NHWC copy (written by the producing fused conv) the pack pass is
-        skipped (and with it the StaticZero count); with emit_nhwc the output
+        skipped: a SparseFlow layer scans the copy for its activity bits and
+        count, a dense one takes the dense route; with emit_nhwc the output
         carries its own copy for the next layer.  Returns (out, v_out)."""
         require_gpu_tensor(x, "x")
         T, B, C, H, W = x.shape
@@ -362,9 +379,16 @@ class ConvLIFRunner:
         self._ensure_packed(dev)
         Ho, Wo = self.out_hw(H, W)
         gs = sparse["group_size"] if sparse is not None else 0
-        xp = shadow_of(x, (T * B, H, W, self.Cp)) if sparse is None else None
+        xp = shadow_of(x, (T * B, H, W, self.Cp))
         nnz = act = None
-        if xp is None:
+        if xp is not None and sparse is not None:
+            # SparseFlow on an input that carries its fp16 NHWC copy: the
+            # activity bits and the nonzero count come from the copy
+            nnz = self.workspace("nnz", (1,), torch.int64, dev)
+            zero_counter(nnz)
+            act = scan_nhwc(xp, C, group_size=gs, nnz=nnz,
+                            act_out=self.workspace("act", (T * B, H, W), torch.int32, dev))
+        elif xp is None:
             st = status_word(dev)
             if static_zero or sparse is not None:
                 nnz = self.workspace("nnz", (1,), torch.int64, dev)

@@ -77,6 +77,17 @@ int cf_pack_input(const float* x, int64_t NB, int64_t C, int64_t H, int64_t W, i
                   void* xp, uint32_t* act, int group_size, float threshold,
                   unsigned long long* nnz, uint32_t* status, void* stream);
 
+/* Activity bits and nonzero count of cf_pack_input (same definitions, same
+ * act layout) from an fp16 NHWC tensor xp [NB][H][W][Cp] that a fused conv
+ * wrote as its output copy (channels >= C zero), for a SparseFlow layer whose
+ * input carries one: no fp32 pass.  group_size must be a multiple of 8.
+ * Replaces, like cf_pack_input, the channel reduction of
+ * catfuse/sparseflow/prescan.py:32-45,184 and the count of
+ * catfuse/sparseflow/ops/st_fusion_conv_bn_lif.py:510-524. */
+int cf_scan_nhwc(const void* xp, int64_t NB, int64_t H, int64_t W, int64_t Cp, int64_t C,
+                 uint32_t* act, int group_size, float threshold, unsigned long long* nnz,
+                 void* stream);
+
 /* route = ZERO if nnz == 0, SPARSE if 1 - nnz/numel > sparse_threshold (in
  * double), else DENSE.  Replaces the host decision at
  * catfuse/sparseflow/ops/st_fusion_conv_bn_lif.py:510-524. */

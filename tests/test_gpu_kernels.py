@@ -388,6 +388,43 @@ def test_conv_stem_range_flag(cuda):
     runtime.clear_status(cuda)
 
 
+@pytest.mark.parametrize("C,gs", [(64, 16), (96, 16), (256, 32), (40, 16)])
+def test_scan_nhwc_matches_pack(cuda, C, gs):
+    """cf_scan_nhwc on the fp16 NHWC copy gives cf_pack_input's activity bits
+    and nonzero count, bit for bit (values include ones, twos and tiny ones)."""
+    from catfuse_amd import runtime
+    g = _gen(C)
+    x = (torch.rand(6, C, 9, 11, generator=g) < 0.2).float()
+    x += (torch.rand(x.shape, generator=g) < 0.05).float()
+    x[0, 0, 0, 0] = 2.0 ** -21  # below the 1e-6 activity threshold, still nonzero
+    xd = x.to(cuda)
+    n1 = torch.zeros(1, dtype=torch.int64, device=cuda)
+    n2 = torch.zeros(1, dtype=torch.int64, device=cuda)
+    xp, act = runtime.pack_input(xd, cp=runtime.pad32(C), group_size=gs, nnz=n1)
+    act2 = runtime.scan_nhwc(xp, C, group_size=gs, nnz=n2)
+    torch.cuda.synchronize()
+    assert torch.equal(act, act2)
+    assert int(n1.item()) == int(n2.item()) == int((x != 0).sum())
+
+
+def test_sparseflow_on_nhwc_copy_bitwise(cuda):
+    """A SparseFlow layer fed an input that carries its NHWC copy (activity
+    from cf_scan_nhwc) equals the same layer fed a plain tensor (cf_pack_input)."""
+    from catfuse_amd.sparseflow.sparse_helpers import choose_group_size
+    c1, b1, l1 = _layer(64, 64, 3, 1, 1, seed=51)
+    c2, b2, l2 = _layer(64, 128, 3, 1, 1, seed=52)
+    r1, r2 = _runner(c1, b1, l1, cuda), _runner(c2, b2, l2, cuda)
+    x = (torch.rand(4, 2, 64, 16, 16, generator=_gen(53)) < 0.1).float().to(cuda)
+    y1, _ = r1.run_mfma(x)
+    geom = dict(block_h=8, block_w=8, group_size=choose_group_size(64))
+    a, va = r2.run_mfma(y1, sparse=geom, sparse_threshold=0.5)
+    tiles_a = [t.clone() for t in r2.last_tiles]
+    b_, vb = r2.run_mfma(y1.clone(), sparse=geom, sparse_threshold=0.5)
+    assert torch.equal(a, b_) and torch.equal(va, vb)
+    for ta, tb in zip(tiles_a, r2.last_tiles):
+        assert torch.equal(ta, tb)
+
+
 def test_nhwc_shadow_handoff_bitwise_and_invalidated(cuda):
     """A fused conv's output carries an fp16 NHWC copy that the next fused
     conv reads instead of re-packing; results are bit-identical, and an
