@@ -29,6 +29,7 @@ _SIGNATURES = {
                           c_double, c_double, c_double, c_int, c_int, _P],
     "cf_pack_input": [_P, _I, _I, _I, _I, _I, _P, _P, c_int, c_float, _P, _P, _P],
     "cf_scan_nhwc": [_P, _I, _I, _I, _I, _I, _P, c_int, c_float, _P, _P],
+    "cf_nhwc_to_nchw": [_P, _P, _I, _I, _I, _I, _I, _P],
     "cf_route_from_nnz": [_P, _I, c_double, _P, _P],
     "cf_zero_counter": [_P, _P],
     "cf_prescan_tiles": [_P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P],
@@ -85,9 +86,13 @@ def check(rc: int, what: str = "") -> None:
 
 
 def ptr(t) -> int | None:
-    """Device pointer of a tensor (None passes a null pointer)."""
+    """Device pointer of a tensor (None passes a null pointer).  A fused
+    layer's output still held only as its NHWC copy is filled first."""
     if t is None:
         return None
+    m = getattr(t, "cf_materialize", None)
+    if m is not None:
+        m()
     return t.data_ptr()
 
 

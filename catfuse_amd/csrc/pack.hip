@@ -126,6 +126,38 @@ __global__ __launch_bounds__(256) void scan_nhwc_kernel(
   }
 }
 
+// fp16 NHWC [NB][HW][cp] -> fp32 NCHW [NB][C][HW]: materialises the fp32
+// view of a fused conv output that was kept only as its NHWC copy.  A block
+// moves 64 pixels x 32 channels through LDS (reads: 64-byte runs per pixel;
+// writes: 256-byte runs per channel).
+__global__ __launch_bounds__(256) void nhwc_to_nchw_kernel(
+    const _Float16* __restrict__ xp, float* __restrict__ out, int64_t C, int64_t HW, int64_t cp) {
+  __shared__ float tile[CC][PX + 1];
+  const int tid = threadIdx.x;
+  const int64_t n = blockIdx.z;
+  const int64_t hw0 = (int64_t)blockIdx.x * PX;
+  const int64_t c0 = (int64_t)blockIdx.y * CC;
+  {
+    // read: 4 threads per pixel, 8 channels (16 bytes) each
+    const int px = tid / 4, part = tid % 4;
+    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    h8 v = {};
+    if (hw0 + px < HW && c0 + part * 8 < cp)
+      v = *reinterpret_cast<const h8*>(xp + ((n * HW + hw0 + px) * cp + c0 + part * 8));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) tile[part * 8 + j][px] = (float)v[j];
+  }
+  __syncthreads();
+  // write: 64 consecutive pixels of one channel per 64 threads
+  const int px = tid % PX;
+#pragma unroll
+  for (int i = 0; i < CC / 4; ++i) {
+    const int cl = tid / PX + 4 * i;
+    const int64_t c = c0 + cl;
+    if (c < C && hw0 + px < HW) out[(n * C + c) * HW + hw0 + px] = tile[cl][px];
+  }
+}
+
 __global__ void route_kernel(const unsigned long long* __restrict__ nnz, int64_t numel,
                              double sparse_threshold, int32_t* __restrict__ route) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
@@ -172,6 +204,18 @@ CF_API int cf_scan_nhwc(const void* xp, int64_t NB, int64_t H, int64_t W, int64_
   hipLaunchKernelGGL(scan_nhwc_kernel, dim3(cf_blocks(npix, 256)), dim3(256), 0,
                      (hipStream_t)stream, (const _Float16*)xp, npix, (int)Cp, (int)C, act,
                      group_size, threshold, nnz);
+  return (int)hipGetLastError();
+}
+
+CF_API int cf_nhwc_to_nchw(const void* xp, float* out, int64_t NB, int64_t C, int64_t H,
+                           int64_t W, int64_t cp, void* stream) {
+  if (!xp || !out || NB < 0 || C <= 0 || H <= 0 || W <= 0 || cp < C || cp % 8 != 0 || NB > 65535)
+    return (int)hipErrorInvalidValue;
+  if (NB == 0) return 0;
+  const int64_t HW = H * W;
+  dim3 grid(cf_blocks(HW, PX), (unsigned)((C + CC - 1) / CC), (unsigned)NB);
+  hipLaunchKernelGGL(nhwc_to_nchw_kernel, grid, dim3(256), 0, (hipStream_t)stream,
+                     (const _Float16*)xp, out, C, HW, cp);
   return (int)hipGetLastError();
 }
 

@@ -187,6 +187,82 @@ def pad32(c: int) -> int:
     return ((c + 31) // 32) * 32
 
 
+# ---------------------------------------------------------------------------
+# fp32 outputs kept as their fp16 NHWC copy until first read
+# ---------------------------------------------------------------------------
+
+def _metadata_functions():
+    T = torch.Tensor
+    props = ("shape", "dtype", "device", "is_cuda", "ndim", "_version", "requires_grad",
+             "layout", "is_sparse", "is_quantized", "is_meta", "grad_fn", "names")
+    fns = {getattr(T, p).__get__ for p in props if hasattr(T, p)}
+    fns |= {T.dim, T.size, T.stride, T.numel, T.nelement, T.is_contiguous, T.storage_offset,
+            T.element_size, T.is_floating_point, T.get_device, T.__len__}
+    return fns
+
+
+_METADATA = None
+
+
+class NHWCSpikes(torch.Tensor):
+    """An fp32 NCHW [T, B, C, H, W] output of a fused layer whose values were
+    written only as the fp16 NHWC copy the next fused layer reads.  The fp32
+    storage is filled (cf_nhwc_to_nchw) the first time anything other than a
+    metadata query touches the tensor, so code outside the fused chain sees
+    an ordinary tensor with the right values; fused layers that take the copy
+    never pay for the fp32 form.  Results of torch operations are plain
+    tensors."""
+
+    @staticmethod
+    def __new__(cls, base: torch.Tensor, nhwc: torch.Tensor):
+        t = base.as_subclass(cls)
+        t._cf_pending = True
+        t._cf_nhwc = (nhwc, base._version)
+        return t
+
+    def cf_materialize(self) -> None:
+        if not self.__dict__.get("_cf_pending", False):
+            return
+        self._cf_pending = False
+        with torch._C.DisableTorchFunctionSubclass():
+            nhwc = self._cf_nhwc[0]
+            T, B, C, H, W = self.shape
+            check(_hip.lib().cf_nhwc_to_nchw(nhwc.data_ptr(), self.data_ptr(), T * B, C, H, W,
+                                             nhwc.shape[-1], _hip.stream(self.device)),
+                  "cf_nhwc_to_nchw")
+
+    @classmethod
+    def __torch_function__(cls, func, types, args=(), kwargs=None):
+        global _METADATA
+        if _METADATA is None:
+            _METADATA = _metadata_functions()
+        kwargs = kwargs or {}
+        self_ok = func is torch.Tensor.contiguous and args and args[0].is_contiguous()
+        if not self_ok and func not in _METADATA:
+            for a in _tensors_in(args, kwargs):
+                if isinstance(a, NHWCSpikes):
+                    a.cf_materialize()
+        with torch._C.DisableTorchFunctionSubclass():
+            return func(*args, **kwargs)
+
+
+def _tensors_in(args, kwargs):
+    stack = list(args) + list(kwargs.values())
+    while stack:
+        a = stack.pop()
+        if isinstance(a, torch.Tensor):
+            yield a
+        elif isinstance(a, (list, tuple)):
+            stack.extend(a)
+        elif isinstance(a, dict):
+            stack.extend(a.values())
+
+
+def lazy_output(shape, nhwc: torch.Tensor, device) -> NHWCSpikes:
+    """Uninitialised fp32 storage of `shape` that fills itself from `nhwc`."""
+    return NHWCSpikes(torch.empty(shape, dtype=torch.float32, device=device), nhwc)
+
+
 def attach_shadow(out: torch.Tensor, nhwc: torch.Tensor) -> None:
     """Record the fp16 NHWC copy a fused conv wrote next to its fp32 output,
     tagged with the output's version counter (any in-place change of `out`
@@ -422,17 +498,23 @@ class ConvLIFRunner:
             require_gpu_tensor(v_in, "v_in")
             if v_in.numel() != B * self.Cout * Ho * Wo:
                 raise ValueError("v_in has the wrong size")
-        out = torch.empty((T, B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
         v_out = (torch.empty((B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
                  if (epilogue == EPI_LIF and want_v_out) else None)
         cp_out = pad32(self.Cout)
         nhwc = (torch.empty((T * B, Ho, Wo, cp_out), dtype=torch.float16, device=dev)
                 if (emit_nhwc and epilogue == EPI_LIF) else None)
+        if nhwc is not None:
+            # spikes: written as the NHWC copy only; fp32 on first outside read
+            out = lazy_output((T, B, self.Cout, Ho, Wo), nhwc, dev)
+            out_ptr = None
+        else:
+            out = torch.empty((T, B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
+            out_ptr = ptr(out)
         ev = _t0()
         rc = _hip.lib().cf_conv_mfma(
             ptr(xp), ptr(self.w_packed), ptr(self.alpha), ptr(self.beta), ptr(v_in), ptr(v_out),
-            ptr(out), ptr(nhwc), cp_out, ptr(identity), ptr(id_nhwc), pad32(self.Cout),
-            int(identity_mode), ptr(ag), ptr(nnz),
+            out_ptr, ptr(nhwc), cp_out, None if id_nhwc is not None else ptr(identity),
+            ptr(id_nhwc), pad32(self.Cout), int(identity_mode), ptr(ag), ptr(nnz),
             x.numel(),
             float(sparse_threshold), T, B, self.Cp, self.Cout, self.Coutp, H, W, Ho, Wo, self.KH,
             self.KW, self.stride, self.padding, B, th, tw, gs, int(epilogue), *self.lif,
@@ -442,8 +524,6 @@ class ConvLIFRunner:
             flops=2 * T * B * Ho * Wo * self.Cout * self.Cin * self.KH * self.KW)
         self.last_nnz = nnz
         self.last_tiles = None if ag is None else (tc_buf, ag)
-        if nhwc is not None:
-            attach_shadow(out, nhwc)
         return out, v_out
 
     def run_direct(self, x: torch.Tensor, v_in=None, *, epilogue=EPI_LIF, want_v_out=True,
@@ -533,20 +613,23 @@ class ConvLIFRunner:
             require_gpu_tensor(v_in, "v_in")
             if v_in.numel() != B * self.Cout * Hc * Wc:
                 raise ValueError("v_in has the wrong size")
-        out = torch.empty((T, B, self.Cout, Hp, Wp), dtype=torch.float32, device=dev)
         v_out = (torch.empty((B, self.Cout, Hc, Wc), dtype=torch.float32, device=dev)
                  if want_v_out else None)
         cp_out = pad32(self.Cout)
-        nhwc = (torch.empty((T * B, Hp, Wp, cp_out), dtype=torch.float16, device=dev)
-                if emit_nhwc else None)
+        if emit_nhwc:
+            nhwc = torch.empty((T * B, Hp, Wp, cp_out), dtype=torch.float16, device=dev)
+            out = lazy_output((T, B, self.Cout, Hp, Wp), nhwc, dev)
+            out_ptr = None
+        else:
+            nhwc = None
+            out = torch.empty((T, B, self.Cout, Hp, Wp), dtype=torch.float32, device=dev)
+            out_ptr = ptr(out)
         ev = _t0()
         rc = _hip.lib().cf_conv_stem_lif_maxpool(
             ptr(x[0]), ptr(self.w_stem), ptr(self.alpha_stem), ptr(self.beta_stem), ptr(v_in),
-            ptr(v_out), ptr(out), ptr(nhwc), cp_out, ptr(status_word(dev)), T, B, C, self.Cout,
+            ptr(v_out), out_ptr, ptr(nhwc), cp_out, ptr(status_word(dev)), T, B, C, self.Cout,
             self.Coutp, H, W, self.KH, self.KW, self.stride, self.padding, 3, 2, 1, *self.lif,
             _hip.stream(dev))
         check(rc, "cf_conv_stem_lif_maxpool")
         _t1("conv_stem", ev, flops=2 * B * Hc * Wc * self.Cout * C * self.KH * self.KW)
-        if nhwc is not None:
-            attach_shadow(out, nhwc)
         return out, v_out

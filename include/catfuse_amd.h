@@ -88,6 +88,14 @@ int cf_scan_nhwc(const void* xp, int64_t NB, int64_t H, int64_t W, int64_t Cp, i
                  uint32_t* act, int group_size, float threshold, unsigned long long* nnz,
                  void* stream);
 
+/* fp16 NHWC xp [NB][H][W][cp] -> fp32 NCHW out [NB][C][H][W]: the fp32 form
+ * of a fused conv output kept only as its NHWC copy, produced when a module
+ * outside the fused chain first reads it.  No counterpart in the reference
+ * (whose fused layers always write fp32 spikes, e.g.
+ * catfuse/implementations/sparse_flow.py:236-238). */
+int cf_nhwc_to_nchw(const void* xp, float* out, int64_t NB, int64_t C, int64_t H, int64_t W,
+                    int64_t cp, void* stream);
+
 /* route = ZERO if nnz == 0, SPARSE if 1 - nnz/numel > sparse_threshold (in
  * double), else DENSE.  Replaces the host decision at
  * catfuse/sparseflow/ops/st_fusion_conv_bn_lif.py:510-524. */

@@ -425,6 +425,26 @@ def test_sparseflow_on_nhwc_copy_bitwise(cuda):
         assert torch.equal(ta, tb)
 
 
+def test_lazy_fp32_output_matches_written_fp32(cuda):
+    """A fused conv that emits its NHWC copy returns an NHWCSpikes tensor
+    whose fp32 values appear on first read and equal the fp32 the kernel
+    writes when asked to; torch results on it are plain tensors."""
+    from catfuse_amd import runtime
+    c1, b1, l1 = _layer(64, 96, 3, 1, 1, seed=71)
+    r1 = _runner(c1, b1, l1, cuda)
+    x = (torch.rand(4, 2, 64, 12, 10, generator=_gen(72)) < 0.3).float().to(cuda)
+    lazy, v1 = r1.run_mfma(x)
+    eager, v2 = r1.run_mfma(x, emit_nhwc=False)
+    assert isinstance(lazy, runtime.NHWCSpikes) and lazy._cf_pending
+    assert runtime.shadow_of(lazy, (8, 12, 10, 96)) is not None
+    assert lazy._cf_pending  # metadata queries and the copy lookup do not fill it
+    s = lazy * 1.0
+    assert not lazy._cf_pending and type(s) is torch.Tensor
+    assert torch.equal(lazy, eager) and torch.equal(v1, v2)
+    lazy2, _ = r1.run_mfma(x)
+    assert torch.equal(lazy2.detach().cpu(), eager.cpu())
+
+
 def test_nhwc_shadow_handoff_bitwise_and_invalidated(cuda):
     """A fused conv's output carries an fp16 NHWC copy that the next fused
     conv reads instead of re-packing; results are bit-identical, and an
