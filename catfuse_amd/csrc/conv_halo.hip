@@ -2,7 +2,7 @@
 // in LDS and the time axis inside the tile.
 //
 // Workgroup tile: BM output channels x (TH x TW) output pixels of one image,
-// for a block of up to TB = 4 time steps at once.  For every 32-channel
+// for a block of up to TB = 4 time steps at once (2 for stride-2 3x3).  For every 32-channel
 // chunk the workgroup stages the input halo of its tile for all time steps
 // of the block in LDS ([t][RH][RW][32 ch], fp16, RH = (TH-1)*S + 3), then
 // runs the 9 taps from LDS: each weight fragment (fp16 hi/lo limbs, loaded
@@ -56,7 +56,12 @@ constexpr int KC = 32;       // channels per chunk
 #define CF_HALO_LDK (KC + 8)
 #endif
 constexpr int LDK = CF_HALO_LDK;  // padded halo pixel (halves)
-constexpr int TB = 4;        // time steps per block
+// Time steps per block: 4, or 2 for stride-2 3x3 tiles, whose 17 x 17 input
+// halo would otherwise hold a workgroup per CU on LDS alone.
+template <int S, int K>
+constexpr int halo_tb() {
+  return (S == 2 && K == 3) ? 2 : 4;
+}
 
 enum { EPI_LIF = 0, EPI_Z = 1 };
 enum { ID_ADD_SPIKE = 1, ID_ADD_Z = 2 };
@@ -95,12 +100,11 @@ __device__ __forceinline__ int halo_route(const unsigned long long* nnz, int64_t
 
 // Workgroups per CU the register budget is sized for.  128-channel or
 // 128-pixel tiles keep 4 x 32 accumulator registers per time block and get
-// the full 512-register budget (stride-2 3x3 tiles are held to one
-// workgroup per CU by their 92 KB halo anyway); 64 x 64 tiles fit in 168
-// registers, three workgroups per CU.
+// the full 512-register budget; 64 x 64 tiles fit in 168 registers, three
+// workgroups per CU.
 template <int BM, int TH, int TW, int S, int K>
 constexpr int halo_min_blocks() {
-  return (BM >= 128 || (S == 2 && K == 3) || TH * TW >= 128) ? 1 : 3;
+  return (BM >= 128 || TH * TW >= 128) ? 1 : 3;
 }
 
 // Producer-wave variants (64 x 64 tiles, stride-1 3x3 or 1x1): a fifth wave
@@ -128,6 +132,7 @@ void conv_halo_kernel(HaloArgs a) {
   constexpr int SS = K == 1 ? S : 1;  // input step between staged pixels
   constexpr int KK = K * K;
   constexpr int HALO_PIX = RH * RW;
+  constexpr int TB = halo_tb<S, K>();
   constexpr int UNITS = TB * HALO_PIX * 4;  // 16-byte units per chunk
   constexpr int PER = (UNITS + 255) / 256;  // staging units per thread
   static_assert(MT >= 1 && NT >= 1, "tile too small");
