@@ -5,7 +5,8 @@ One step = one full forward of the fused network over the batch (all T
 steps, stem to logits) on synthetic inputs resident in HBM, with a
 functional.reset_net before it.  Prints ONE JSON line (rank 0):
   value      = images/s = B / (seconds per step)
-  roofline   = dominant kernel (the MFMA conv) achieved dense-equivalent
+  roofline   = dominant kernel (the MFMA conv, conv_halo_kernel behind
+               cf_conv_mfma) achieved dense-equivalent
                TFLOP/s vs the 2.5 PFLOP/s fp16 dense MFMA peak, timed live
                with HIP events on the launch stream during the timed steps
   lif_tails  = standalone LIF-family kernels' achieved HBM GB/s vs 8 TB/s
@@ -189,7 +190,7 @@ def main():
     tot_fl = conv.get("flops", 0) + conv_sp.get("flops", 0)
     launches = conv.get("launches", 0) + conv_sp.get("launches", 0)
     achieved = tot_fl / (tot_ms * 1e-3) / 1e12 if tot_ms else 0.0
-    roofline = {"kernel": "conv_mfma_kernel (fused Conv-BN-LIF, all launches)",
+    roofline = {"kernel": "conv_halo_kernel (cf_conv_mfma fused Conv-BN-LIF, all launches)",
                 "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
                 "traffic": traffic_from_profiles(),
