@@ -24,6 +24,17 @@ enum {
                                  // outside the fp16 range (or not finite)
 };
 
+// Packed conv weights (cf_pack_conv_weights) are stored fragment-major: for
+// each limb, 32-row output-channel tile, tap and 16-channel K step, the
+// 32 x 16 A operand of one v_mfma_f32_32x32x16_f16 as 64 lanes x 8 halves
+// (lane l holds row l % 32, channels 8 * (l / 32) .. + 7), so a wave loads a
+// fragment with one fully coalesced 1 KB access.  Element (limb, co, tap, c):
+__host__ __device__ inline size_t cf_wfrag_index(int limb, int co, int tap, int c, int Coutp,
+                                                 int KHW, int Cp) {
+  const size_t frag = (((size_t)limb * (Coutp / 32) + co / 32) * KHW + tap) * (Cp / 16) + c / 16;
+  return (frag * 64 + (co % 32) + 32 * ((c % 16) / 8)) * 8 + (c % 8);
+}
+
 // LIF parameters passed by value to every kernel with a LIF epilogue.
 struct LifParams {
   float tau;

@@ -6,7 +6,8 @@
 // chunk the workgroup stages the input halo of its tile for all time steps
 // of the block in LDS ([t][RH][RW][32 ch], fp16, RH = (TH-1)*S + 3), then
 // runs the 9 taps from LDS: each weight fragment (fp16 hi/lo limbs, loaded
-// once per tap from L2, one tap ahead) feeds the MFMAs of every time step.
+// once per tap from L2 as one coalesced 1 KB access, one tap ahead) feeds
+// the MFMAs of every time step.
 // Activations are therefore read from L2 once per chunk instead of once per
 // tap, and weights once per tap instead of once per tap and time step.
 // When the K loop of a time block is complete the epilogue applies BN and
@@ -24,6 +25,8 @@
 #include "cf_common.h"
 
 #include <stdlib.h>
+
+#include <type_traits>
 
 namespace {
 
@@ -68,7 +71,7 @@ enum { ID_ADD_SPIKE = 1, ID_ADD_Z = 2 };
 
 struct HaloArgs {
   const _Float16* x;        // [T*B][H][W][Cp]
-  const _Float16* w;        // [2][Coutp][9][Cp]
+  const _Float16* w;        // fragment-major limbs (cf_wfrag_index)
   const float* alpha;
   const float* beta;
   const float* v_in;
@@ -107,24 +110,11 @@ constexpr int halo_min_blocks() {
   return (BM >= 128 || TH * TW >= 128) ? 1 : 3;
 }
 
-// Producer-wave variants (64 x 64 tiles, stride-1 3x3 or 1x1): a fifth wave
-// stages the next chunk's halo into the second of two LDS buffers while the
-// four MFMA waves run the current chunk, so the staging latency is hidden
-// and the MFMA waves' own vector memory queue holds only weight loads.
-#ifndef CF_HALO_PRODUCER
-#define CF_HALO_PRODUCER 0
-#endif
-template <int BM, int TH, int TW, int S, int K>
-constexpr bool halo_producer() {
-  return CF_HALO_PRODUCER && BM == 64 && TH * TW == 64 && (K == 1 || S == 1);
-}
-
 // K: filter size (3, or 1 for pointwise convolutions, whose strided input
 // samples are staged densely: RH = TH, RW = TW).
 // LM: LIF specialisation (cf_lif_mode) of the EPI_LIF epilogue.
-template <int BM, int TH, int TW, int S, int K, int EPI, int LM,
-          bool PROD = halo_producer<BM, TH, TW, S, K>()>
-__global__ __launch_bounds__((PROD ? 320 : 256), (PROD ? 3 : halo_min_blocks<BM, TH, TW, S, K>()))
+template <int BM, int TH, int TW, int S, int K, int EPI, int LM>
+__global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>()))
 void conv_halo_kernel(HaloArgs a) {
   constexpr int BN = TH * TW;
   constexpr int WM = BM / 2, WN = BN / 2, MT = WM / 32, NT = WN / 32;
@@ -136,20 +126,19 @@ void conv_halo_kernel(HaloArgs a) {
   constexpr int UNITS = TB * HALO_PIX * 4;  // 16-byte units per chunk
   constexpr int PER = (UNITS + 255) / 256;  // staging units per thread
   static_assert(MT >= 1 && NT >= 1, "tile too small");
-  constexpr int NTHR = PROD ? 320 : 256;
-  constexpr int TBR = PROD ? 2 : TB;  // time steps per batch of B-fragment reads
-  // LDS halo pixel: 4 x 16-byte channel parts + 16 bytes of padding (LDK
-  // halves).  The producer's direct-to-LDS loads write 64 lanes x 16 bytes
-  // contiguously, so it loads 5 units per pixel (the fifth reads zeros).
-  constexpr int PUNITS = TB * HALO_PIX * 5;
-  constexpr int PPER = (PUNITS + 63) / 64;  // producer load instructions per chunk
-  constexpr int HBUF = PROD ? (TB * HALO_PIX * LDK > PPER * 512 ? TB * HALO_PIX * LDK : PPER * 512)
-                            : TB * HALO_PIX * LDK;  // one halo buffer (halves)
+  constexpr int HBUF = TB * HALO_PIX * LDK;  // halo buffer (halves)
+  // Output staging of the epilogue (in the halo buffer): one step's tile as
+  // BN pixels x (BM + 8) halves; two buffers when they fit, so one barrier
+  // per step separates a step's LDS writes from its copy-out.
+  constexpr int OLD = BM + 8;
+  constexpr int OSTEP = BN * OLD;
+  constexpr int NOBUF = 2 * OSTEP <= HBUF ? 2 : 1;
+  static_assert(OSTEP <= HBUF, "output staging exceeds the halo buffer");
   auto halo_idx = [](int P, int part) { return P * LDK + (part << 3); };
-  __shared__ __attribute__((aligned(16))) _Float16 halo[(PROD ? 2 : 1) * HBUF];
+  __shared__ __attribute__((aligned(16))) _Float16 halo[HBUF];
+  __shared__ __attribute__((aligned(16))) float bn_s[2][BM];  // alpha, beta of the tile
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const bool producer = PROD && wave == 4;  // stages halos; no MFMA work
   const int wm = wave >> 1, wn = wave & 1;
   const int tile = blockIdx.x;
   const int gw = tile % a.GW, gh = (tile / a.GW) % a.GH, b = tile / (a.GW * a.GH);
@@ -159,6 +148,10 @@ void conv_halo_kernel(HaloArgs a) {
   const int HoWo = a.Ho * a.Wo;
   const int nch = a.Cp / KC;
   const int ntiles = a.B * a.GH * a.GW;
+  if (tid < BM) {  // alpha/beta hold Coutp entries
+    bn_s[0][tid] = a.alpha[cout0 + tid];
+    bn_s[1][tid] = a.beta[cout0 + tid];
+  }
 
   // Pixels this lane owns in the accumulator layout (column lane%32 of each N tile).
   int n_base[NT], e_off[NT];
@@ -171,14 +164,14 @@ void conv_halo_kernel(HaloArgs a) {
     n_ok[nt] = (oh0 + py) < a.Ho && (ow0 + px) < a.Wo;
     e_off[nt] = (oh0 + py) * a.Wo + (ow0 + px);
   }
-  const int kof = (lane >> 5) * 8;
 
   // Output channel of accumulator register r in M tile mt is
   // co_lane + mt * 32 + 8 * (r / 4) + r % 4.  Element indices are 32-bit
   // (the host checks that every output tensor has fewer than 2^31 elements).
   const int co_lane = cout0 + wm * WM + 4 * (lane >> 5);
+  const bool full_c = cout0 + BM <= a.Cout;  // every channel of the tile is real
   float v[MT][NT][16];
-  if (EPI == EPI_LIF && !producer) {
+  if (EPI == EPI_LIF) {
     const int col = opaque(co_lane);
     const int vb = (b * a.Cout + col) * HoWo;
 #pragma unroll
@@ -197,11 +190,15 @@ void conv_halo_kernel(HaloArgs a) {
 
   const int route = halo_route(a.nnz, a.numel, a.sparse_thr);
 
-  // Weight fragment addresses: row (cout) per M tile, k offset per lane.
-  const _Float16* wrow[MT];
+  // Weight fragments (fragment-major packing): this lane's 16 bytes of the
+  // fragment (M tile mt, tap, 16-channel step k16) are at
+  // wbase[mt] + (tap * Cp/16 + k16) * 512 halves; the lo limb follows the hi
+  // limb at limb_stride.
+  const int k16s = a.Cp / 16;
+  const _Float16* wbase[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt)
-    wrow[mt] = a.w + ((size_t)(cout0 + wm * WM + mt * 32 + (lane & 31)) * KK) * a.Cp + kof;
+    wbase[mt] = a.w + (size_t)((cout0 + wm * WM + mt * 32) / 32) * KK * k16s * 512 + lane * 8;
   const size_t limb_stride = (size_t)a.Coutp * KK * a.Cp;
 
   for (int tb0 = 0; tb0 < a.T; tb0 += TB) {
@@ -293,39 +290,11 @@ void conv_halo_kernel(HaloArgs a) {
         }
       }
     };
-
-    // Whole-chunk staging in groups of NSTG units (loads of a group are all
-    // issued before its stores).
     auto halo_stage = [&](int ch) {
       for (int i0 = 0; i0 < PER; i0 += NSTG) {
         halo_load(ch, i0, stg);
         halo_store(i0, stg);
       }
-    };
-    // Producer wave: a whole chunk into buffer `buf` with direct-to-LDS
-    // loads (no registers): instruction j fills 16-byte LDS units
-    // 64 j .. 64 j + 63, lane i unit 64 j + i = 5 P + part (part 4 is the
-    // pixel's padding).  All loads are in flight before the one wait.
-    auto prod_stage = [&](int ch, _Float16* buf) {
-      const int c0 = ch * KC;
-      bool act[TB];
-      chunk_act(ch, act);
-#pragma unroll 4
-      for (int j = 0; j < PPER; ++j) {
-        const int u = 64 * j + opaque(lane);
-        const int P = u / 5, part = u % 5;  // LDS pixel (t, pix), 16-byte part
-        const int pix = P % HALO_PIX, t = P / HALO_PIX;
-        const int ry = pix / RW, rx = pix % RW;
-        const int ih = ih0 + ry * SS, iw = iw0 + rx * SS;
-        const bool ok = part < 4 && t < nsteps && act_at(act, t) && ih >= 0 && ih < a.H &&
-                        iw >= 0 && iw < a.W;
-        const void* src =
-            ok ? static_cast<const void*>(a.x + ((((size_t)(tb0 + t) * a.B + b) * a.H + ih) * a.W +
-                                                 iw) * a.Cp + c0 + part * 8)
-               : static_cast<const void*>(&g_halo_zero);
-        __builtin_amdgcn_global_load_lds(src, buf + 512 * j, 16, 0, 0);
-      }
-      __builtin_amdgcn_s_waitcnt(0);  // all of this wave's loads have landed in LDS
     };
     // Weight fragments: [buffer][mt][ks], hi and lo limbs.  Tap 0 of a chunk
     // is loaded into buffer 0 before the chunk's halo is staged (loads
@@ -336,219 +305,198 @@ void conv_halo_kernel(HaloArgs a) {
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          const _Float16* p = wrow[mt] + chunk * KC + ks * 16;
+          const _Float16* p = wbase[mt] + (size_t)(chunk * 2 + ks) * 512;
           ah[0][mt][ks] = *reinterpret_cast<const h8*>(p);
           al[0][mt][ks] = *reinterpret_cast<const h8*>(p + limb_stride);
         }
     };
-    // The K loop of one chunk from halo buffer hb (MFMA waves only).
     // The K loop of one chunk: no per-step branches.  A step the chunk is
     // inactive at (SparseFlow) was staged as zeros, and adding the exact
     // zero products leaves the accumulator's bits unchanged (it starts at
     // +0 and is never -0), so this equals skipping the step.
-    auto run_taps = [&](int ch, const _Float16* hb) {
-      const int c0 = ch * KC;
+    auto run_taps = [&](int ch) {
 #pragma unroll
       for (int tap = 0; tap < KK; ++tap) {
         const int cur = tap & 1;
         const int tap_off = (tap / K) * RW + (tap % K);
-        // B fragments are read TBR steps at a time, unconditionally and
-        // before those steps' MFMAs (reads for steps this chunk skips are
-        // harmless and keep the reads free of branches, which would
-        // otherwise serialise them).
+        // B fragments of all TB steps are read before the tap's MFMAs,
+        // unconditionally (reads for steps this chunk skips are harmless and
+        // keep the reads free of branches, which would serialise them).
+        h8 bb[TB][2][NT];
 #pragma unroll
-        for (int th = 0; th < TB; th += TBR) {
-          h8 bb[TBR][2][NT];
-#pragma unroll
-          for (int tr = 0; tr < TBR; ++tr)
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-              for (int nt = 0; nt < NT; ++nt)
-                bb[tr][ks][nt] = *reinterpret_cast<const h8*>(
-                    &hb[halo_idx((th + tr) * HALO_PIX + n_base[nt] + tap_off, 2 * ks + (lane >> 5))]);
-          if (th == 0 && tap + 1 < KK) {
-#pragma unroll
-            for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-              for (int ks = 0; ks < 2; ++ks) {
-                const _Float16* p = wrow[mt] + (size_t)(tap + 1) * a.Cp + c0 + ks * 16;
-                ah[cur ^ 1][mt][ks] = *reinterpret_cast<const h8*>(p);
-                al[cur ^ 1][mt][ks] = *reinterpret_cast<const h8*>(p + limb_stride);
-              }
-            // Issue the next tap's weight loads before this tap's MFMAs.
-            __builtin_amdgcn_sched_barrier(0);
-          }
-          // Consecutive MFMAs go to different accumulators (time steps, tiles)
-          // so none waits for the previous one's result; each accumulator
-          // still sums ks 0 hi, ks 0 lo, ks 1 hi, ks 1 lo in that order.
+        for (int t = 0; t < TB; ++t)
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-            for (int limb = 0; limb < 2; ++limb)
+            for (int nt = 0; nt < NT; ++nt)
+              bb[t][ks][nt] = *reinterpret_cast<const h8*>(
+                  &halo[halo_idx(t * HALO_PIX + n_base[nt] + tap_off, 2 * ks + (lane >> 5))]);
+        if (tap + 1 < KK) {
 #pragma unroll
-              for (int tr = 0; tr < TBR; ++tr) {
-                const int t = th + tr;
+          for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                  for (int nt = 0; nt < NT; ++nt)
-                    acc[t][mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                        limb ? al[cur][mt][ks] : ah[cur][mt][ks], bb[tr][ks][nt], acc[t][mt][nt],
-                        0, 0, 0);
-              }
+            for (int ks = 0; ks < 2; ++ks) {
+              const _Float16* p = wbase[mt] + (size_t)((tap + 1) * k16s + ch * 2 + ks) * 512;
+              ah[cur ^ 1][mt][ks] = *reinterpret_cast<const h8*>(p);
+              al[cur ^ 1][mt][ks] = *reinterpret_cast<const h8*>(p + limb_stride);
+            }
+          // Issue the next tap's weight loads before this tap's MFMAs.
+          __builtin_amdgcn_sched_barrier(0);
         }
+        // Consecutive MFMAs go to different accumulators (time steps, tiles)
+        // so none waits for the previous one's result; each accumulator
+        // still sums ks 0 hi, ks 0 lo, ks 1 hi, ks 1 lo in that order.
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int limb = 0; limb < 2; ++limb)
+#pragma unroll
+            for (int t = 0; t < TB; ++t)
+#pragma unroll
+              for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int nt = 0; nt < NT; ++nt)
+                  acc[t][mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                      limb ? al[cur][mt][ks] : ah[cur][mt][ks], bb[t][ks][nt], acc[t][mt][nt],
+                      0, 0, 0);
         // Later taps' reads stay below this tap's MFMAs (register budget).
         __builtin_amdgcn_sched_barrier(0);
       }
     };
 
     int ch = next_chunk(-1);
-    if constexpr (PROD) {
-      // One barrier per chunk: after it the MFMA waves take chunk k from
-      // buffer k % 2 while the producer fills buffer (k + 1) % 2, which the
-      // MFMA waves finished reading before the barrier.
-      if (ch < nch) {
-        if (producer) prod_stage(ch, halo);
-        else load_tap0(ch);
+    if (ch < nch) {
+      load_tap0(ch);
+      __syncthreads();  // previous time block's LDS reads are complete
+      halo_stage(ch);
+      __syncthreads();
+    }
+    while (ch < nch) {
+      const int nx = next_chunk(ch);
+      run_taps(ch);
+      if (nx < nch) {
+        load_tap0(nx);
+        __syncthreads();  // all taps of this chunk have read the halo
+        halo_stage(nx);
         __syncthreads();
       }
-      int k = 0;
-      while (ch < nch) {
-        const int nx = next_chunk(ch);
-        if (producer) {
-          if (nx < nch) prod_stage(nx, halo + ((k + 1) & 1) * HBUF);
-        } else {
-          run_taps(ch, halo + (k & 1) * HBUF);
-          if (nx < nch) load_tap0(nx);
-        }
-        __syncthreads();
-        ch = nx;
-        ++k;
-      }
-    } else {
-      if (ch < nch) {
-        load_tap0(ch);
-        __syncthreads();  // previous time block's halo reads are complete
-        halo_stage(ch);
-        __syncthreads();
-      }
-      while (ch < nch) {
-        const int nx = next_chunk(ch);
-        run_taps(ch, halo);
-        if (nx < nch) {
-          load_tap0(nx);
-          __syncthreads();  // all taps of this chunk have read the halo
-          halo_stage(nx);
-          __syncthreads();
-        }
-        ch = nx;
-      }
+      ch = nx;
     }
 
-    // Epilogue over the time block.  The fp16 NHWC copy of each step's
-    // output tile is staged in LDS (the halo buffer is free here) and written
-    // as 16-byte chunks: one 2*BM-byte run per pixel.  A spike-valued
-    // identity (SEW ADD) is read from its fp16 NHWC copy when there is one:
-    // four consecutive channels of a pixel per 8-byte load, exact for the
-    // integer values it holds.
-    constexpr int OLD = BM + 8;  // staged row (halves) per pixel
-    static_assert(BN * OLD <= HBUF, "output staging exceeds the halo buffer");
-    _Float16* ostage = halo;
-    if (!PROD) __syncthreads();  // last chunk's halo reads are complete
+    // Epilogue over the time block: BN, (identity), LIF, then the fp16 NHWC
+    // copy of the step's output tile, staged in LDS (the halo buffer is free
+    // here) and written as 16-byte chunks, one 2*BM-byte run per pixel.  A
+    // spike-valued identity (SEW ADD) is read from its fp16 NHWC copy when
+    // there is one: four consecutive channels of a pixel per 8-byte load,
+    // exact for the integer values it holds.  The lean path (no fp32 output,
+    // no fp32 identity, every channel real) has no per-element branches:
+    // out-of-range pixels are computed from zero halo and never stored.
+    __syncthreads();  // the last chunk's halo reads are complete
+    const bool lean = EPI == EPI_LIF && !a.out && !a.identity && full_c;
+    auto epi_step = [&](auto lean_c, int t) {
+      constexpr bool LEAN = decltype(lean_c)::value;
+      const int tt = tb0 + t;
+      _Float16* ostage = halo + (t % NOBUF) * OSTEP;
+      const int col = opaque(co_lane);
+      const int ob = ((tt * a.B + b) * a.Cout + col) * HoWo;
+      const _Float16* idn = a.identity_nhwc;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          // Registers 4*r4 .. 4*r4+3 hold four consecutive output channels.
+          const int colb = wm * WM + mt * 32 + 8 * r4 + 4 * (lane >> 5);
+          const float4 al4 = *reinterpret_cast<const float4*>(&bn_s[0][colb]);
+          const float4 be4 = *reinterpret_cast<const float4*>(&bn_s[1][colb]);
+          const float alv[4] = {al4.x, al4.y, al4.z, al4.w};
+          const float bev[4] = {be4.x, be4.y, be4.z, be4.w};
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            h4 idh = {};
+            if (idn) {
+              const int pix = n_ok[nt] ? e_off[nt] : 0;
+              idh = *reinterpret_cast<const h4*>(
+                  idn + ((size_t)(tt * a.B + b) * HoWo + pix) * a.cp_id + col + mt * 32 + 8 * r4);
+            }
+            h4 pk;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int r = 4 * r4 + j;
+              float z = acc[t][mt][nt][r] * alv[j] + bev[j];
+              float ov;
+              if constexpr (LEAN) {
+                float vv = lif_charge_m<LM>(v[mt][nt][r], z, a.lif);
+                const float sp = lif_fire_reset_bit<LM>(vv, a.lif) ? 1.0f : 0.0f;
+                v[mt][nt][r] = vv;
+                ov = idn ? (float)idh[j] + sp : sp;
+              } else {
+                const int dc = mt * 32 + 8 * r4 + j;
+                const bool ok = col + dc < a.Cout && n_ok[nt];
+                const int o = ob + dc * HoWo + e_off[nt];
+                if (ok && a.identity && a.identity_mode == ID_ADD_Z) z = z + a.identity[o];
+                if (EPI == EPI_Z) {
+                  ov = z;
+                } else {
+                  float vv = lif_charge_m<LM>(v[mt][nt][r], z, a.lif);
+                  const float sp = lif_fire_reset_bit<LM>(vv, a.lif) ? 1.0f : 0.0f;
+                  v[mt][nt][r] = vv;
+                  if (idn) ov = (float)idh[j] + sp;
+                  else if (ok && a.identity && a.identity_mode == ID_ADD_SPIKE) ov = a.identity[o] + sp;
+                  else ov = sp;
+                }
+                if (ok && a.out) a.out[o] = ov;
+              }
+              pk[j] = (_Float16)ov;
+            }
+            *reinterpret_cast<h4*>(&ostage[(wn * WN + nt * 32 + (lane & 31)) * OLD + colb]) = pk;
+          }
+        }
+    };
 #pragma unroll
     for (int t = 0; t < TB; ++t) {
       if (t >= nsteps) break;
-      const int tt = tb0 + t;
-      if (!producer) {
-        const int col = opaque(co_lane);
-        const int ob = ((tt * a.B + b) * a.Cout + col) * HoWo;
-        // BN coefficients are re-read per step (L1 hits) rather than hoisted
-        // into 2 x 16 registers that would stay live across the K loop.
-        const float* alpha = opaque_ptr(a.alpha);
-        const float* beta = opaque_ptr(a.beta);
-        const _Float16* idn = a.identity_nhwc;
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int r4 = 0; r4 < 4; ++r4) {
-            // Registers 4*r4 .. 4*r4+3 hold four consecutive output channels.
-            const int colb = wm * WM + mt * 32 + 8 * r4 + 4 * (lane >> 5);
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt) {
-              h4 idh = {};
-              if (idn) {
-                const int pix = n_ok[nt] ? e_off[nt] : 0;
-                idh = *reinterpret_cast<const h4*>(
-                    idn + ((size_t)(tt * a.B + b) * HoWo + pix) * a.cp_id + col + mt * 32 + 8 * r4);
-              }
-              h4 pk;
-#pragma unroll
-              for (int j = 0; j < 4; ++j) {
-                const int r = 4 * r4 + j;
-                const int dc = mt * 32 + 8 * r4 + j;
-                const int co = col + dc;
-                float ov = 0.0f;
-                if (co < a.Cout && n_ok[nt]) {
-                  const int o = ob + dc * HoWo + e_off[nt];
-                  float z = acc[t][mt][nt][r] * alpha[co] + beta[co];
-                  if (a.identity && a.identity_mode == ID_ADD_Z) z = z + a.identity[o];
-                  if (EPI == EPI_Z) {
-                    ov = z;
-                  } else {
-                    float vv = lif_charge_m<LM>(v[mt][nt][r], z, a.lif);
-                    const float sp = lif_fire_reset_bit<LM>(vv, a.lif) ? 1.0f : 0.0f;
-                    v[mt][nt][r] = vv;
-                    if (idn) ov = (float)idh[j] + sp;
-                    else if (a.identity && a.identity_mode == ID_ADD_SPIKE) ov = a.identity[o] + sp;
-                    else ov = sp;
-                  }
-                  if (a.out) a.out[o] = ov;
-                }
-                pk[j] = (_Float16)ov;
-              }
-              if (a.out_nhwc)
-                *reinterpret_cast<h4*>(&ostage[(wn * WN + nt * 32 + (lane & 31)) * OLD + colb]) = pk;
-            }
-          }
-      }
+      if (NOBUF == 1 && t > 0) __syncthreads();  // the previous step's copy-out is complete
+      if (lean) epi_step(std::true_type{}, t);
+      else epi_step(std::false_type{}, t);
       if (a.out_nhwc) {
-        __syncthreads();
+        __syncthreads();  // the step's tile is staged
+        const _Float16* ostage = halo + (t % NOBUF) * OSTEP;
         constexpr int CH8 = BM / 8;  // 16-byte chunks per pixel
-        for (int c = tid; c < BN * CH8; c += NTHR) {
+        for (int c = tid; c < BN * CH8; c += 256) {
           const int px = c / CH8, part = c % CH8;
           const int py = px / TW, pxx = px % TW;
           const int co8 = cout0 + part * 8;
           if (oh0 + py < a.Ho && ow0 + pxx < a.Wo && co8 < a.cp_out) {
             const size_t pix = (size_t)(oh0 + py) * a.Wo + (ow0 + pxx);
-            *reinterpret_cast<u32x4*>(a.out_nhwc + (((size_t)tt * a.B + b) * HoWo + pix) * a.cp_out + co8) =
+            *reinterpret_cast<u32x4*>(a.out_nhwc + (((size_t)(tb0 + t) * a.B + b) * HoWo + pix) * a.cp_out + co8) =
                 *reinterpret_cast<const u32x4*>(&ostage[px * OLD + part * 8]);
           }
         }
-        __syncthreads();
       }
     }
   }
 
-  if (EPI == EPI_LIF && a.v_out && !producer) {
+  if (EPI == EPI_LIF && a.v_out) {
     const int col = opaque(co_lane);
     const int vb = (b * a.Cout + col) * HoWo;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+    for (int nt = 0; nt < NT; ++nt) {
+      if (!n_ok[nt]) continue;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int dc = mt * 32 + 8 * (r >> 2) + (r & 3);
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-          if (col + dc < a.Cout && n_ok[nt]) a.v_out[vb + dc * HoWo + e_off[nt]] = v[mt][nt][r];
-      }
+        for (int r = 0; r < 16; ++r) {
+          const int dc = mt * 32 + 8 * (r >> 2) + (r & 3);
+          if (full_c || col + dc < a.Cout) a.v_out[vb + dc * HoWo + e_off[nt]] = v[mt][nt][r];
+        }
+    }
   }
 }
 
 template <int BM, int TH, int TW, int S, int K = 3>
 hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
   dim3 grid((unsigned)(a.B * a.GH * a.GW), (unsigned)(a.Coutp / BM));
-  const dim3 block(halo_producer<BM, TH, TW, S, K>() ? 320 : 256);
+  const dim3 block(256);
   if (epi == EPI_Z) {
     hipLaunchKernelGGL((conv_halo_kernel<BM, TH, TW, S, K, EPI_Z, LM_GENERIC>), grid, block, 0, st, a);
   } else {

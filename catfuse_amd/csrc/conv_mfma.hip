@@ -5,7 +5,7 @@
 //
 // * A operand (weights): fp32 weights split into two fp16 limbs
 //   w*s_c = hi + lo (s_c a per-output-channel power of two that keeps
-//   |w*s_c| < 2^14), packed [limb][Coutp][KH*KW][Cp].  Both limbs are
+//   |w*s_c| < 2^14), packed fragment-major (cf_wfrag_index).  Both limbs are
 //   multiplied into the same fp32 accumulator, so the contraction carries
 //   ~22 significant weight bits (fp32-faithful up to accumulation order).
 // * B operand (activations): fp16 NHWC [img][H][W][Cp] from pack.hip.  Spikes
@@ -153,7 +153,7 @@ __global__ __launch_bounds__(256, (conv_min_blocks<BM, BN, EPI>())) void conv_mf
       const int u = tid + 256 * i;
       const int limb = u / (BM * 4), row = (u >> 2) % BM, part = u & 3;
       ar[i] = *reinterpret_cast<const u32x4*>(
-          a.w + (((size_t)limb * a.Coutp + cout0 + row) * KHW + tap) * a.Cp + c0 + part * 8);
+          a.w + cf_wfrag_index(limb, cout0 + row, tap, c0 + part * 8, a.Coutp, KHW, a.Cp));
     }
     const int img_base = t * a.x_img_tstride;
 #pragma unroll
@@ -331,7 +331,7 @@ __global__ __launch_bounds__(256, (conv_min_blocks<BM, BN, EPI>())) void conv_mf
 }
 
 // ---------------------------------------------------------------------------
-// Weight packing: fp32 [Cout][Cin][KH][KW] -> fp16 hi/lo [2][Coutp][KH*KW][Cp]
+// Weight packing: fp32 [Cout][Cin][KH][KW] -> fp16 hi/lo limbs (cf_wfrag_index)
 // with per-channel power-of-two prescale, and the folded epilogue affine
 //   alpha = bn_scale / s_c,   beta = bn_shift + bias * bn_scale.
 // With w_packed == nullptr only alpha/beta are produced (s_c = 1).
@@ -366,15 +366,15 @@ __global__ __launch_bounds__(256) void pack_weights_kernel(
     inv = ldexpf(1.0f, -sh);
   }
   if (wp) {
-    // packed index: ((limb*Coutp + co)*KHW + tap)*Cp + c
+    // fragment-major layout (cf_wfrag_index)
     for (int i = tid; i < KHW * Cp; i += 256) {
       const int tap = i / Cp, c = i % Cp;
       float ws = 0.0f;
       if (real && c < Cin) ws = w[((size_t)co * Cin + c) * KHW + tap] * sc;
       const _Float16 hi = (_Float16)ws;
       const _Float16 lo = (_Float16)(ws - (float)hi);
-      wp[((size_t)co * KHW + tap) * Cp + c] = hi;
-      wp[(((size_t)Coutp + co) * KHW + tap) * Cp + c] = lo;
+      wp[cf_wfrag_index(0, co, tap, c, Coutp, KHW, Cp)] = hi;
+      wp[cf_wfrag_index(1, co, tap, c, Coutp, KHW, Cp)] = lo;
     }
   }
   if (tid == 0) {

@@ -116,8 +116,9 @@ int cf_prescan_tiles(const uint32_t* act, int64_t NB, int64_t H, int64_t W, int6
                      int32_t* tile_class, void* stream);
 
 /* Conv weight staging for cf_conv_mfma: fp32 w [Cout][Cin][KH][KW] ->
- * fp16 hi/lo limbs [2][Coutp][KH*KW][Cp] with a per-channel power-of-two
- * prescale, plus the folded epilogue affine alpha/beta [Coutp]
+ * fp16 hi/lo limbs with a per-channel power-of-two prescale (2*Coutp*KH*KW*Cp
+ * halves, fragment-major: per limb, 32-channel tile, tap and 16-channel K
+ * step one 64-lane x 8-half MFMA A fragment), plus the folded epilogue affine alpha/beta [Coutp]
  * (alpha = bn_scale / prescale, beta = bn_shift + bias*bn_scale; bn_* and
  * bias nullable).  With w_packed == NULL only alpha/beta are written (no
  * prescale), the form cf_conv_direct consumes.  Replaces the weight caches
