@@ -1,24 +1,24 @@
-// Fused 3x3 Conv -> BN -> LIF on the matrix cores with the input halo staged
-// in LDS and the time axis inside the tile.
+// Fused 3x3 (and 1x1) Conv -> BN -> LIF on the matrix cores with the input
+// halo staged in LDS and the time axis inside the tile.
 //
-// Workgroup tile: BM output channels x (TH x TW) output pixels of one image,
-// for a block of up to TB = 4 time steps at once (2 for stride-2 3x3).  For every 32-channel
-// chunk the workgroup stages the input halo of its tile for all time steps
-// of the block in LDS ([t][RH][RW][32 ch], fp16, RH = (TH-1)*S + 3), then
-// runs the 9 taps from LDS: each weight fragment (fp16 hi/lo limbs, loaded
-// once per tap from L2 as one coalesced 1 KB access, one tap ahead) feeds
-// the MFMAs of every time step.
-// Activations are therefore read from L2 once per chunk instead of once per
-// tap, and weights once per tap instead of once per tap and time step.
-// When the K loop of a time block is complete the epilogue applies BN and
-// the LIF for t = 0..TB-1 in order, with v in VGPRs across time blocks.
+// Workgroup tile: BM = 64 output channels x (TH x TW) output pixels of one
+// image, for a block of up to TB = 4 time steps at once (2 for stride-2 3x3).
+// One K step = one 32-channel chunk of one time block: the input halo of the
+// tile for the block's steps is copied to LDS ([t][row][col][32 ch], fp16)
+// by direct global->LDS loads, then the KK taps run from LDS: each weight
+// fragment (fp16 hi/lo limbs, one coalesced 1 KB load per fragment from L2,
+// one tap ahead) feeds the MFMAs of every time step.  Two halo buffers: the
+// loads of the next K step are spread over the current step's taps, so the
+// matrix cores do not wait for the staging.  When the K loop of a time block
+// is complete the epilogue applies BN and the LIF for its steps in order,
+// with v in VGPRs across time blocks.
 //
 // Tiles are the SparseFlow prescan tiles (8x8 / 8x16), so the same kernel
-// serves the SparseFlow route: a chunk is skipped for time step t when the
-// tile's group bits for t are clear, and a chunk inactive at every step of
-// the block is not even staged.  Routes are decided on the device from the
-// nonzero count and are bit-identical (skipped chunks contribute zeros,
-// and the accumulation order of the remaining ones is unchanged).
+// serves the SparseFlow route: a chunk inactive at every step of a block is
+// skipped, and a step a chunk is inactive at is staged as zeros.  Routes are
+// decided on the device from the nonzero count and are bit-identical
+// (skipped or zero chunks add exact zeros, and the accumulation order of the
+// remaining ones is unchanged).
 //
 // Accumulation order per output element: chunk-major, then tap, then the
 // two 16-channel halves, hi limb then lo limb.
@@ -54,17 +54,63 @@ __device__ __forceinline__ P* opaque_ptr(P* p) {
   return p;
 }
 
-constexpr int KC = 32;       // channels per chunk
-#ifndef CF_HALO_LDK
-#define CF_HALO_LDK (KC + 8)
-#endif
-constexpr int LDK = CF_HALO_LDK;  // padded halo pixel (halves)
-// Time steps per block: 4, or 2 for stride-2 3x3 tiles, whose 17 x 17 input
-// halo would otherwise hold a workgroup per CU on LDS alone.
+constexpr int KC = 32;  // channels per chunk: four 16-byte parts per staged pixel
+
+// One direct global -> LDS load (global_load_lds_dwordx4): lane l copies
+// 16 bytes from its src to LDS byte address lds + 16 l (lds wave-uniform).
+// Issued through inline assembly so that the compiler does not track it:
+// its own load counting then never waits for these copies (it only waits
+// for loads it issued, which in-order completion makes safe: a copy issued
+// after a load never delays the wait for that load).  The kernel waits for
+// the copies itself (s_waitcnt vmcnt(0) and a barrier) before reading them.
+__device__ __forceinline__ void lds_copy16(const void* src, unsigned lds) {
+  asm volatile(
+      "s_mov_b32 m0, %1\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %0, off"
+      :
+      : "v"(src), "s"(lds)
+      : "memory", "m0");
+}
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// Time steps per block: 4, or 2 for stride-2 3x3 tiles (17 x 17 input halo).
 template <int S, int K>
 constexpr int halo_tb() {
   return (S == 2 && K == 3) ? 2 : 4;
 }
+
+// Staged halo geometry and LDS layout: [t][RH][RW] pixels of 64 bytes (32
+// channels), the pixel's four 16-byte parts stored in the order
+// part ^ swz(row, col).  The taps' B-fragment reads (ds_read_b128) are served
+// 16 lanes at a time from 64 four-byte banks (16 sixteen-byte slots): lanes
+// 0-7 read one part of 8 consecutive output pixels, lanes 8-15 the same
+// pixels one output row down.  The XOR spreads these 16 reads over 16
+// distinct slots for every tap and time step (checked exhaustively for each
+// configuration used).  Stride-2 3x3 halos store their columns
+// de-interleaved (even columns, then odd ones), so that consecutive output
+// pixels read consecutive staged pixels at every tap.
+template <int S, int K, int TH, int TW>
+struct HaloGeom {
+  static constexpr int RH = K == 1 ? TH : (TH - 1) * S + K;
+  static constexpr int RW = K == 1 ? TW : (TW - 1) * S + K;
+  static constexpr int SS = K == 1 ? S : 1;  // input step between staged pixels
+  static constexpr bool DEINT = K == 3 && S == 2;
+  static constexpr int HALF = (RW + 1) / 2;
+  // staged column of halo column rx
+  __device__ static constexpr int col(int rx) {
+    return DEINT ? ((rx & 1) ? HALF + (rx >> 1) : (rx >> 1)) : rx;
+  }
+  // halo column of staged column c
+  __device__ static constexpr int inv_col(int c) {
+    return DEINT ? (c < HALF ? 2 * c : 2 * (c - HALF) + 1) : c;
+  }
+  __device__ static constexpr int swz(int ry, int c) {
+    return K == 1 ? (((c >> 2) ^ (2 * ry)) & 3) : (TW == 16 ? ((c >> 2) & 3) : ((c >> 1) & 3));
+  }
+};
 
 enum { EPI_LIF = 0, EPI_Z = 1 };
 enum { ID_ADD_SPIKE = 1, ID_ADD_Z = 2 };
@@ -101,45 +147,48 @@ __device__ __forceinline__ int halo_route(const unsigned long long* nnz, int64_t
   return (1.0 - (double)k / (double)numel > thr) ? CF_ROUTE_SPARSE : CF_ROUTE_DENSE;
 }
 
-// Workgroups per CU the register budget is sized for.  128-channel or
-// 128-pixel tiles keep 4 x 32 accumulator registers per time block and get
-// the full 512-register budget; 64 x 64 tiles fit in 168 registers, three
-// workgroups per CU.
-template <int BM, int TH, int TW, int S, int K>
+// Workgroups per CU the kernel is sized for: 64 x 64 tiles fit in 168
+// registers (three per CU); 64 x 128 tiles keep twice the accumulators and
+// get the full register budget.
+template <int TH, int TW>
 constexpr int halo_min_blocks() {
-  return (BM >= 128 || TH * TW >= 128) ? 1 : 3;
+  return TH * TW >= 128 ? 1 : 3;
 }
 
 // K: filter size (3, or 1 for pointwise convolutions, whose strided input
 // samples are staged densely: RH = TH, RW = TW).
 // LM: LIF specialisation (cf_lif_mode) of the EPI_LIF epilogue.
-template <int BM, int TH, int TW, int S, int K, int EPI, int LM>
-__global__ __launch_bounds__(256, (halo_min_blocks<BM, TH, TW, S, K>()))
+template <int TH, int TW, int S, int K, int EPI, int LM>
+__global__ __launch_bounds__(256, (halo_min_blocks<TH, TW>()))
 void conv_halo_kernel(HaloArgs a) {
+  using G = HaloGeom<S, K, TH, TW>;
+  constexpr int BM = 64;
   constexpr int BN = TH * TW;
-  constexpr int WM = BM / 2, WN = BN / 2, MT = WM / 32, NT = WN / 32;
-  constexpr int RH = K == 1 ? TH : (TH - 1) * S + K, RW = K == 1 ? TW : (TW - 1) * S + K;
-  constexpr int SS = K == 1 ? S : 1;  // input step between staged pixels
+  constexpr int WM = BM / 2, WN = BN / 2, NT = WN / 32;
+  constexpr int RH = G::RH, RW = G::RW, SS = G::SS;
   constexpr int KK = K * K;
-  constexpr int HALO_PIX = RH * RW;
   constexpr int TB = halo_tb<S, K>();
-  constexpr int UNITS = TB * HALO_PIX * 4;  // 16-byte units per chunk
-  constexpr int PER = (UNITS + 255) / 256;  // staging units per thread
-  static_assert(MT >= 1 && NT >= 1, "tile too small");
-  constexpr int HBUF = TB * HALO_PIX * LDK;  // halo buffer (halves)
-  // Output staging of the epilogue (in the halo buffer): one step's tile as
-  // BN pixels x (BM + 8) halves; two buffers when they fit, so one barrier
-  // per step separates a step's LDS writes from its copy-out.
+  constexpr int TSTR = RH * RW * KC;           // staged time step (halves)
+  constexpr int NU = TB * RH * RW * 4;         // 16-byte units per staged chunk
+  constexpr int NB = (NU + 63) / 64;           // 64-unit blocks (one direct load each)
+  constexpr int HB = NB * 64 * 8;              // one halo buffer (halves), whole blocks
+  constexpr int NPF = (NB + 3) / 4;            // direct loads per thread per chunk
+  constexpr int TBR = TB > 2 ? 2 : TB;         // time steps per batch of B-fragment reads
+  // Output staging of the epilogue (in the halo buffer consumed last): one
+  // step's tile as BN pixels x (BM + 8) halves; two of them when they fit, so
+  // one barrier per step separates a step's LDS writes from its copy-out.
   constexpr int OLD = BM + 8;
   constexpr int OSTEP = BN * OLD;
-  constexpr int NOBUF = 2 * OSTEP <= HBUF ? 2 : 1;
-  static_assert(OSTEP <= HBUF, "output staging exceeds the halo buffer");
-  auto halo_idx = [](int P, int part) { return P * LDK + (part << 3); };
-  __shared__ __attribute__((aligned(16))) _Float16 halo[HBUF];
+  constexpr int NOBUF = 2 * OSTEP <= HB ? 2 : 1;
+  static_assert(OSTEP <= HB, "output staging exceeds a halo buffer");
+  static_assert(NT >= 1, "tile too small");
+  __shared__ __attribute__((aligned(16))) _Float16 halo[2 * HB];
   __shared__ __attribute__((aligned(16))) float bn_s[2][BM];  // alpha, beta of the tile
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers
   const int wm = wave >> 1, wn = wave & 1;
+  const int hi = lane >> 5;
   const int tile = blockIdx.x;
   const int gw = tile % a.GW, gh = (tile / a.GW) % a.GH, b = tile / (a.GW * a.GH);
   const int oh0 = gh * TH, ow0 = gw * TW;
@@ -153,196 +202,174 @@ void conv_halo_kernel(HaloArgs a) {
     bn_s[1][tid] = a.beta[cout0 + tid];
   }
 
-  // Pixels this lane owns in the accumulator layout (column lane%32 of each N tile).
-  int n_base[NT], e_off[NT];
+  // Pixels this lane owns in the accumulator layout (column lane%32 of each
+  // N tile).  Its B fragment reads: staged pixel of tap (0, 0) (rd_pix,
+  // halves within a staged step) and the part swizzle of each kw (2 bits per
+  // kw in rd_swz); the kh rows and time steps are constant offsets.
+  int e_off[NT];
   bool n_ok[NT];
+  int rd_pix[NT], rd_swz[NT];
 #pragma unroll
   for (int nt = 0; nt < NT; ++nt) {
     const int n = wn * WN + nt * 32 + (lane & 31);
     const int py = n / TW, px = n % TW;
-    n_base[nt] = K == 1 ? py * RW + px : (py * S) * RW + px * S;
     n_ok[nt] = (oh0 + py) < a.Ho && (ow0 + px) < a.Wo;
     e_off[nt] = (oh0 + py) * a.Wo + (ow0 + px);
+    const int ry = K == 1 ? py : py * S, rx = K == 1 ? px : px * S;
+    rd_pix[nt] = (ry * RW + G::col(rx)) * KC;
+    int sw = 0;
+#pragma unroll
+    for (int kw = 0; kw < K; ++kw) sw |= G::swz(ry, G::col(rx + kw)) << (2 * kw);
+    rd_swz[nt] = sw;
   }
+  auto rd_addr = [&](int nt, int kw, int ks) {
+    const int sw = (rd_swz[nt] >> (2 * kw)) & 3;
+    return rd_pix[nt] + (G::col(kw) - G::col(0)) * KC + (((2 * ks + hi) ^ sw) << 3);
+  };
 
-  // Output channel of accumulator register r in M tile mt is
-  // co_lane + mt * 32 + 8 * (r / 4) + r % 4.  Element indices are 32-bit
-  // (the host checks that every output tensor has fewer than 2^31 elements).
-  const int co_lane = cout0 + wm * WM + 4 * (lane >> 5);
+  // Output channel of accumulator register r is co_lane + 8 * (r / 4) + r % 4.
+  // Element indices are 32-bit (the host checks that every output tensor has
+  // fewer than 2^31 elements).
+  const int co_lane = cout0 + wm * WM + 4 * hi;
   const bool full_c = cout0 + BM <= a.Cout;  // every channel of the tile is real
-  float v[MT][NT][16];
-  if (EPI == EPI_LIF) {
-    const int col = opaque(co_lane);
-    const int vb = (b * a.Cout + col) * HoWo;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int dc = mt * 32 + 8 * (r >> 2) + (r & 3);
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          float v0 = lif_initial_v(a.lif);
-          if (a.v_in && col + dc < a.Cout && n_ok[nt]) v0 = a.v_in[vb + dc * HoWo + e_off[nt]];
-          v[mt][nt][r] = v0;
-        }
-      }
-  }
 
   const int route = halo_route(a.nnz, a.numel, a.sparse_thr);
+  // Group bits active at time step tt (uniform across the workgroup).
+  auto step_mask = [&](int tt) -> uint32_t {
+    if (tt >= a.T || route == CF_ROUTE_ZERO) return 0u;
+    if (route == CF_ROUTE_DENSE) return 0xffffffffu;
+    return (uint32_t)a.ag_mask[(size_t)tt * ntiles + tile];
+  };
+  auto chunk_bits = [&](int ch) -> uint32_t {
+    const int g0 = (ch * KC) / a.gs, g1 = (ch * KC + KC - 1) / a.gs;
+    uint32_t gb = 0u;
+    for (int g = g0; g <= g1 && g < 32; ++g) gb |= 1u << g;
+    return gb;
+  };
+  // Steps (bit t) of the block starting at tbs that chunk ch is active at.
+  auto chunk_act = [&](int tbs, int ch) -> uint32_t {
+    const uint32_t gb = chunk_bits(ch);
+    uint32_t m = 0u;
+#pragma unroll
+    for (int t = 0; t < TB; ++t) m |= ((step_mask(tbs + t) & gb) != 0u ? 1u : 0u) << t;
+    return m;
+  };
+  // The K step after (tbs, ch): the next active chunk of the block, else the
+  // first active chunk of a later block (tbs' = T when there is none), and
+  // its step activity.
+  auto next_step = [&](int tbs, int ch, int& ntb, int& nc, uint32_t& nact) {
+    for (int tb = tbs; tb < a.T; tb += TB) {
+      for (int c = (tb == tbs ? ch + 1 : 0); c < nch; ++c) {
+        const uint32_t m = chunk_act(tb, c);
+        if (m) {
+          ntb = tb;
+          nc = c;
+          nact = m;
+          return;
+        }
+      }
+    }
+    ntb = a.T;
+    nc = 0;
+    nact = 0u;
+  };
+  // Direct loads i0 .. i1-1 (of NPF) of this thread for K step (tbs, ch)
+  // with step activity act into halo buffer hb: load i of wave w fills the
+  // 64-unit block 4 i + w (wrapped into 0 .. NB-1: a wrapped load repeats
+  // another one, writing the same bytes), lane l unit 64 * block + l.  Units
+  // of steps the chunk is inactive at, of pixels outside the image, and past
+  // the last unit (the buffer's tail) load zeros.  No branches: the
+  // compiler's load counting stays exact, so the taps wait only for their
+  // own weights.  The unit indices are laundered so that the address
+  // arithmetic stays where the load is issued.
+  const size_t img_stride = (size_t)a.H * a.W * a.Cp;  // halves per staged image
+  const _Float16* zero_page = opaque_ptr(reinterpret_cast<const _Float16*>(&g_halo_zero));
+  auto stage_loads = [&](int tbs, int ch, uint32_t act, _Float16* hb, int i0, int i1) {
+    const int nst = tbs < a.T ? min(TB, a.T - tbs) : 0;  // 0: every unit loads zeros
+    const _Float16* xb = a.x + (size_t)(tbs * a.B + b) * img_stride + ch * KC;
+#pragma unroll
+    for (int i = i0; i < i1; ++i) {
+      int blk = 4 * i + wave;
+      if (4 * NPF > NB && blk >= NB) blk -= NB;
+      const int l = opaque(lane);
+      const int U = blk * 64 + l;
+      const int slot = l & 3, pix = blk * 16 + (l >> 2);
+      const int c = pix % RW, ry = (pix / RW) % RH, t = pix / (RW * RH);
+      const int rx = G::inv_col(c);
+      const int part = slot ^ G::swz(ry, c);
+      const int ih = ih0 + ry * SS, iw = iw0 + rx * SS;
+      // bitwise tests: no branches around the address arithmetic
+      const bool ok = (U < NU) & (t < nst) & (((act >> t) & 1u) != 0u) & (ih >= 0) & (ih < a.H) &
+                      (iw >= 0) & (iw < a.W);
+      const _Float16* src = xb + (size_t)t * a.B * img_stride +
+                            (unsigned)((ih * a.W + iw) * a.Cp + part * 8);
+      lds_copy16(ok ? src : zero_page, __builtin_amdgcn_readfirstlane(lds_addr(hb + blk * 512)));
+    }
+  };
 
   // Weight fragments (fragment-major packing): this lane's 16 bytes of the
-  // fragment (M tile mt, tap, 16-channel step k16) are at
-  // wbase[mt] + (tap * Cp/16 + k16) * 512 halves; the lo limb follows the hi
-  // limb at limb_stride.
+  // fragment (tap, 16-channel step k16) of its 32-channel M tile are at
+  // wbase + (tap * Cp/16 + k16) * 512 halves; the lo limb follows the hi limb
+  // at limb_stride.  Two register buffers, alternating with a running tap
+  // count that continues across K steps.
   const int k16s = a.Cp / 16;
-  const _Float16* wbase[MT];
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-    wbase[mt] = a.w + (size_t)((cout0 + wm * WM + mt * 32) / 32) * KK * k16s * 512 + lane * 8;
+  const _Float16* wbase = a.w + (size_t)((cout0 + wm * WM) / 32) * KK * k16s * 512 + lane * 8;
   const size_t limb_stride = (size_t)a.Coutp * KK * a.Cp;
-
-  for (int tb0 = 0; tb0 < a.T; tb0 += TB) {
-    const int nsteps = min(TB, a.T - tb0);
-    uint32_t mask[TB];
+  h8 ah[2][2], al[2][2];
+  auto load_w = [&](int buf, int tap, int ch) {
 #pragma unroll
-    for (int t = 0; t < TB; ++t) {
-      uint32_t m = 0u;
-      if (t < nsteps) {
-        if (route == CF_ROUTE_DENSE) m = 0xffffffffu;
-        else if (route == CF_ROUTE_SPARSE)
-          m = (uint32_t)a.ag_mask[(size_t)(tb0 + t) * ntiles + tile];
-      }
-      mask[t] = m;
+    for (int ks = 0; ks < 2; ++ks) {
+      const _Float16* p = wbase + (size_t)(tap * k16s + ch * 2 + ks) * 512;
+      ah[buf][ks] = *reinterpret_cast<const h8*>(p);
+      al[buf][ks] = *reinterpret_cast<const h8*>(p + limb_stride);
     }
-    f16v acc[TB][MT][NT];
-#pragma unroll
-    for (int t = 0; t < TB; ++t)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-#pragma unroll
-          for (int r = 0; r < 16; ++r) acc[t][mt][nt][r] = 0.0f;
+  };
 
-    // Chunks active at some step of the block, in order (uniform across the
-    // workgroup: every thread evaluates the same masks).
-    auto chunk_act = [&](int ch, bool (&act)[TB]) -> bool {
-      const int g0 = (ch * KC) / a.gs, g1 = (ch * KC + KC - 1) / a.gs;
-      uint32_t gbits = 0u;
-      for (int g = g0; g <= g1 && g < 32; ++g) gbits |= 1u << g;
-      bool any = false;
+  f16v acc[TB][NT];
+  // The taps of K step ch from halo buffer hb: tap j uses weight buffer
+  // j & 1 and loads the weights of the next tap (at the last tap: the next
+  // K step's tap 0, moved to buffer 0 after the taps), then the direct loads
+  // of the next K step (ntb, nc) into the other halo buffer hb_next, spread
+  // over taps 0 .. KK-2.  Every load is issued unconditionally (a next step
+  // in a later time block stages zeros here, its weights are reloaded
+  // before the epilogue), and hb and hb_next are restrict-qualified: the
+  // compiler's load counting then stays exact, and a tap waits for its own
+  // weights only, not for every outstanding load.  No
+  // per-step branches: a step the chunk is inactive at was staged as zeros,
+  // and adding the exact zero products leaves the accumulator's bits
+  // unchanged (it starts at +0 and is never -0), so this equals skipping it.
+  auto run_taps = [&](const _Float16* __restrict__ hb, _Float16* __restrict__ hb_next, int ch,
+                      int ntb, int nc, uint32_t nact, int wblk) {
+    const int stb = ntb == wblk ? ntb : a.T;  // a.T: stage zeros
 #pragma unroll
-      for (int t = 0; t < TB; ++t) {
-        act[t] = (mask[t] & gbits) != 0u;
-        any |= act[t];
-      }
-      return any;
-    };
-    // act[t] for a lane-dependent t (no dynamic register indexing).
-    auto act_at = [](const bool (&act)[TB], int t) {
-      bool r = false;
+    for (int tap = 0; tap < KK; ++tap) {
+      const int cur = tap & 1;
+      const int kh = tap / K, kw = tap % K;
+      // B fragments are read TBR steps at a time, unconditionally (reads of
+      // steps this chunk skips hold zeros), each batch before its MFMAs.
 #pragma unroll
-      for (int i = 0; i < TB; ++i) r = r || (t == i && act[i]);
-      return r;
-    };
-    auto next_chunk = [&](int ch) -> int {
-      bool tmp[TB];
-      for (int c = ch + 1; c < nch; ++c)
-        if (chunk_act(c, tmp)) return c;
-      return nch;
-    };
-    // Halo staging through registers in groups of NSTG 16-byte units: all
-    // loads of a group are issued before its LDS stores.  (No register
-    // prefetch of the next chunk during the taps: vector memory loads retire
-    // in order, so the taps' weight loads would wait for it anyway.)
-    constexpr int NSTG = PER < 8 ? PER : 8;
-    u32x4 stg[NSTG];
-    auto halo_load = [&](int ch, int i0, u32x4 (&st)[NSTG]) {
-      const int c0 = ch * KC;
-      bool act[TB];
-      chunk_act(ch, act);
+      for (int th = 0; th < TB; th += TBR) {
+        h8 bb[TBR][2][NT];
 #pragma unroll
-      for (int i = 0; i < NSTG; ++i) {
-        const int u = opaque(tid) + 256 * (i0 + i);
-        const int part = u & 3;
-        const int pix = (u >> 2) % HALO_PIX;
-        const int t = (u >> 2) / HALO_PIX;
-        const int ry = pix / RW, rx = pix % RW;
-        const int ih = ih0 + ry * SS, iw = iw0 + rx * SS;
-        const bool ok = u < UNITS && t < nsteps && act_at(act, t) && ih >= 0 && ih < a.H &&
-                        iw >= 0 && iw < a.W;
-        const u32x4* src =
-            ok ? reinterpret_cast<const u32x4*>(
-                     a.x + ((((size_t)(tb0 + t) * a.B + b) * a.H + ih) * a.W + iw) * a.Cp + c0 + part * 8)
-               : &g_halo_zero;
-        st[i] = *src;
-      }
-    };
-    auto halo_store = [&](int i0, const u32x4 (&st)[NSTG]) {
-#pragma unroll
-      for (int i = 0; i < NSTG; ++i) {
-        const int u = opaque(tid) + 256 * (i0 + i);
-        if (u < UNITS) {
-          const int part = u & 3;
-          const int pix = (u >> 2) % HALO_PIX;
-          const int t = (u >> 2) / HALO_PIX;
-          *reinterpret_cast<u32x4*>(&halo[(t * HALO_PIX + pix) * LDK + part * 8]) = st[i];
-        }
-      }
-    };
-    auto halo_stage = [&](int ch) {
-      for (int i0 = 0; i0 < PER; i0 += NSTG) {
-        halo_load(ch, i0, stg);
-        halo_store(i0, stg);
-      }
-    };
-    // Weight fragments: [buffer][mt][ks], hi and lo limbs.  Tap 0 of a chunk
-    // is loaded into buffer 0 before the chunk's halo is staged (loads
-    // retire in order, so it is ready when the taps start).
-    h8 ah[2][MT][2], al[2][MT][2];
-    auto load_tap0 = [&](int chunk) {
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-          const _Float16* p = wbase[mt] + (size_t)(chunk * 2 + ks) * 512;
-          ah[0][mt][ks] = *reinterpret_cast<const h8*>(p);
-          al[0][mt][ks] = *reinterpret_cast<const h8*>(p + limb_stride);
-        }
-    };
-    // The K loop of one chunk: no per-step branches.  A step the chunk is
-    // inactive at (SparseFlow) was staged as zeros, and adding the exact
-    // zero products leaves the accumulator's bits unchanged (it starts at
-    // +0 and is never -0), so this equals skipping the step.
-    auto run_taps = [&](int ch) {
-#pragma unroll
-      for (int tap = 0; tap < KK; ++tap) {
-        const int cur = tap & 1;
-        const int tap_off = (tap / K) * RW + (tap % K);
-        // B fragments of all TB steps are read before the tap's MFMAs,
-        // unconditionally (reads for steps this chunk skips are harmless and
-        // keep the reads free of branches, which would serialise them).
-        h8 bb[TB][2][NT];
-#pragma unroll
-        for (int t = 0; t < TB; ++t)
+        for (int tr = 0; tr < TBR; ++tr)
 #pragma unroll
           for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
             for (int nt = 0; nt < NT; ++nt)
-              bb[t][ks][nt] = *reinterpret_cast<const h8*>(
-                  &halo[halo_idx(t * HALO_PIX + n_base[nt] + tap_off, 2 * ks + (lane >> 5))]);
-        if (tap + 1 < KK) {
-#pragma unroll
-          for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-            for (int ks = 0; ks < 2; ++ks) {
-              const _Float16* p = wbase[mt] + (size_t)((tap + 1) * k16s + ch * 2 + ks) * 512;
-              ah[cur ^ 1][mt][ks] = *reinterpret_cast<const h8*>(p);
-              al[cur ^ 1][mt][ks] = *reinterpret_cast<const h8*>(p + limb_stride);
-            }
-          // Issue the next tap's weight loads before this tap's MFMAs.
-          __builtin_amdgcn_sched_barrier(0);
+              bb[tr][ks][nt] = *reinterpret_cast<const h8*>(
+                  &hb[(th + tr) * TSTR + kh * RW * KC + rd_addr(nt, kw, ks)]);
+        if (th == 0) {
+          if (tap + 1 < KK) load_w(cur ^ 1, tap + 1, ch);
+          else load_w(cur ^ 1, 0, nc);
+          if (KK == 1) {
+            stage_loads(stb, nc, nact, hb_next, 0, NPF);
+          } else if (tap + 1 < KK) {
+            const int i0 = (tap * NPF) / (KK - 1), i1 = ((tap + 1) * NPF) / (KK - 1);
+            if (i1 > i0) stage_loads(stb, nc, nact, hb_next, i0, i1);
+          }
         }
+        // Issue the loads before these MFMAs.
+        __builtin_amdgcn_sched_barrier(0);
         // Consecutive MFMAs go to different accumulators (time steps, tiles)
         // so none waits for the previous one's result; each accumulator
         // still sums ks 0 hi, ks 0 lo, ks 1 hi, ks 1 lo in that order.
@@ -351,106 +378,159 @@ void conv_halo_kernel(HaloArgs a) {
 #pragma unroll
           for (int limb = 0; limb < 2; ++limb)
 #pragma unroll
-            for (int t = 0; t < TB; ++t)
+            for (int tr = 0; tr < TBR; ++tr)
 #pragma unroll
-              for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-                for (int nt = 0; nt < NT; ++nt)
-                  acc[t][mt][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                      limb ? al[cur][mt][ks] : ah[cur][mt][ks], bb[t][ks][nt], acc[t][mt][nt],
-                      0, 0, 0);
-        // Later taps' reads stay below this tap's MFMAs (register budget).
+              for (int nt = 0; nt < NT; ++nt)
+                acc[th + tr][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                    limb ? al[cur][ks] : ah[cur][ks], bb[tr][ks][nt], acc[th + tr][nt], 0, 0, 0);
+        // Later reads stay below these MFMAs (register budget).
         __builtin_amdgcn_sched_barrier(0);
       }
-    };
-
-    int ch = next_chunk(-1);
-    if (ch < nch) {
-      load_tap0(ch);
-      __syncthreads();  // previous time block's LDS reads are complete
-      halo_stage(ch);
-      __syncthreads();
     }
-    while (ch < nch) {
-      const int nx = next_chunk(ch);
-      run_taps(ch);
-      if (nx < nch) {
-        load_tap0(nx);
-        __syncthreads();  // all taps of this chunk have read the halo
-        halo_stage(nx);
-        __syncthreads();
+    if (KK & 1) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        ah[0][ks] = ah[1][ks];
+        al[0][ks] = al[1][ks];
       }
-      ch = nx;
+    }
+  };
+
+  // First K step: staged and its tap-0 weights loaded before the loop.
+  int s_tb, s_ch;
+  uint32_t s_act;
+  next_step(0, -1, s_tb, s_ch, s_act);
+  int pf_tb = s_tb;  // block of the K step already staged into buffer 0
+  if (s_tb < a.T) {
+    load_w(0, 0, s_ch);
+    stage_loads(s_tb, s_ch, s_act, halo, 0, NPF);
+  }
+
+  for (int tb0 = 0; tb0 < a.T; tb0 += TB) {
+    const int nsteps = min(TB, a.T - tb0);
+#pragma unroll
+    for (int t = 0; t < TB; ++t)
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[t][nt][r] = 0.0f;
+
+    // The block's K steps alternate halo buffers, starting with buffer 0.
+    int buf = 0;
+    while (s_tb == tb0) {
+      int ntb, nc;
+      uint32_t nact;
+      next_step(s_tb, s_ch, ntb, nc, nact);
+      // This step's halo has landed (each wave waits for its own direct
+      // loads, the barrier for everyone's); every wave has finished reading
+      // the other buffer, which the taps below refill.
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      run_taps(halo + buf * HB, halo + (buf ^ 1) * HB, s_ch, ntb, nc, nact, tb0);
+      buf ^= 1;
+      s_tb = ntb;
+      s_ch = nc;
+      s_act = nact;
     }
 
     // Epilogue over the time block: BN, (identity), LIF, then the fp16 NHWC
-    // copy of the step's output tile, staged in LDS (the halo buffer is free
-    // here) and written as 16-byte chunks, one 2*BM-byte run per pixel.  A
-    // spike-valued identity (SEW ADD) is read from its fp16 NHWC copy when
-    // there is one: four consecutive channels of a pixel per 8-byte load,
-    // exact for the integer values it holds.  The lean path (no fp32 output,
-    // no fp32 identity, every channel real) has no per-element branches:
-    // out-of-range pixels are computed from zero halo and never stored.
-    __syncthreads();  // the last chunk's halo reads are complete
+    // copy of the step's output tile, staged in LDS (the halo buffer consumed
+    // last; the next K step's loads go to the other one) and written as
+    // 16-byte chunks, one 2*BM-byte run per pixel.  A spike-valued identity
+    // (SEW ADD) is read from its fp16 NHWC copy when there is one: four
+    // consecutive channels of a pixel per 8-byte load, exact for the integer
+    // values it holds.  The lean path (no fp32 output, no fp32 identity,
+    // every channel real) has no per-element branches: out-of-range pixels
+    // are computed from zero halo and never stored.
+    // The last taps' reads are complete, and so are the direct loads they
+    // issued (zeros into the buffer the output is staged in below).
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    // The next block's first K step: tap-0 weights and halo (into buffer 0)
+    // in flight during the epilogue, which stages its output in buffer 1.
+    if (s_tb < a.T && s_tb != pf_tb) {
+      load_w(0, 0, s_ch);
+      stage_loads(s_tb, s_ch, s_act, halo, 0, NPF);
+      pf_tb = s_tb;
+    }
+    _Float16* obuf = halo + HB;
+    // Membrane potentials of this lane's elements live in registers during
+    // the epilogue only: from v_in (or the initial value) for the first time
+    // block, from v_out (written at the end of the previous block's epilogue
+    // by this same lane) for later ones.
+    float v[NT][16];
+    if (EPI == EPI_LIF) {
+      const int col = opaque(co_lane);
+      const int vb = (b * a.Cout + col) * HoWo;
+      const float* vsrc = tb0 == 0 ? a.v_in : a.v_out;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dc = 8 * (r >> 2) + (r & 3);
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt) {
+          float v0 = lif_initial_v(a.lif);
+          if (vsrc && (full_c || col + dc < a.Cout) && n_ok[nt]) v0 = vsrc[vb + dc * HoWo + e_off[nt]];
+          v[nt][r] = v0;
+        }
+      }
+    }
     const bool lean = EPI == EPI_LIF && !a.out && !a.identity && full_c;
     auto epi_step = [&](auto lean_c, int t) {
       constexpr bool LEAN = decltype(lean_c)::value;
       const int tt = tb0 + t;
-      _Float16* ostage = halo + (t % NOBUF) * OSTEP;
+      _Float16* ostage = obuf + (t % NOBUF) * OSTEP;
       const int col = opaque(co_lane);
       const int ob = ((tt * a.B + b) * a.Cout + col) * HoWo;
       const _Float16* idn = a.identity_nhwc;
 #pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int r4 = 0; r4 < 4; ++r4) {
+        // Registers 4*r4 .. 4*r4+3 hold four consecutive output channels.
+        const int colb = wm * WM + 8 * r4 + 4 * hi;
+        const float4 al4 = *reinterpret_cast<const float4*>(&bn_s[0][colb]);
+        const float4 be4 = *reinterpret_cast<const float4*>(&bn_s[1][colb]);
+        const float alv[4] = {al4.x, al4.y, al4.z, al4.w};
+        const float bev[4] = {be4.x, be4.y, be4.z, be4.w};
 #pragma unroll
-        for (int r4 = 0; r4 < 4; ++r4) {
-          // Registers 4*r4 .. 4*r4+3 hold four consecutive output channels.
-          const int colb = wm * WM + mt * 32 + 8 * r4 + 4 * (lane >> 5);
-          const float4 al4 = *reinterpret_cast<const float4*>(&bn_s[0][colb]);
-          const float4 be4 = *reinterpret_cast<const float4*>(&bn_s[1][colb]);
-          const float alv[4] = {al4.x, al4.y, al4.z, al4.w};
-          const float bev[4] = {be4.x, be4.y, be4.z, be4.w};
-#pragma unroll
-          for (int nt = 0; nt < NT; ++nt) {
-            h4 idh = {};
-            if (idn) {
-              const int pix = n_ok[nt] ? e_off[nt] : 0;
-              idh = *reinterpret_cast<const h4*>(
-                  idn + ((size_t)(tt * a.B + b) * HoWo + pix) * a.cp_id + col + mt * 32 + 8 * r4);
-            }
-            h4 pk;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              const int r = 4 * r4 + j;
-              float z = acc[t][mt][nt][r] * alv[j] + bev[j];
-              float ov;
-              if constexpr (LEAN) {
-                float vv = lif_charge_m<LM>(v[mt][nt][r], z, a.lif);
-                const float sp = lif_fire_reset_bit<LM>(vv, a.lif) ? 1.0f : 0.0f;
-                v[mt][nt][r] = vv;
-                ov = idn ? (float)idh[j] + sp : sp;
-              } else {
-                const int dc = mt * 32 + 8 * r4 + j;
-                const bool ok = col + dc < a.Cout && n_ok[nt];
-                const int o = ob + dc * HoWo + e_off[nt];
-                if (ok && a.identity && a.identity_mode == ID_ADD_Z) z = z + a.identity[o];
-                if (EPI == EPI_Z) {
-                  ov = z;
-                } else {
-                  float vv = lif_charge_m<LM>(v[mt][nt][r], z, a.lif);
-                  const float sp = lif_fire_reset_bit<LM>(vv, a.lif) ? 1.0f : 0.0f;
-                  v[mt][nt][r] = vv;
-                  if (idn) ov = (float)idh[j] + sp;
-                  else if (ok && a.identity && a.identity_mode == ID_ADD_SPIKE) ov = a.identity[o] + sp;
-                  else ov = sp;
-                }
-                if (ok && a.out) a.out[o] = ov;
-              }
-              pk[j] = (_Float16)ov;
-            }
-            *reinterpret_cast<h4*>(&ostage[(wn * WN + nt * 32 + (lane & 31)) * OLD + colb]) = pk;
+        for (int nt = 0; nt < NT; ++nt) {
+          h4 idh = {};
+          if (idn) {
+            const int pix = n_ok[nt] ? e_off[nt] : 0;
+            idh = *reinterpret_cast<const h4*>(
+                idn + ((size_t)(tt * a.B + b) * HoWo + pix) * a.cp_id + col + 8 * r4);
           }
+          h4 pk;
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            const int r = 4 * r4 + j;
+            float z = acc[t][nt][r] * alv[j] + bev[j];
+            float ov;
+            if constexpr (LEAN) {
+              float vv = lif_charge_m<LM>(v[nt][r], z, a.lif);
+              const float sp = lif_fire_reset_bit<LM>(vv, a.lif) ? 1.0f : 0.0f;
+              v[nt][r] = vv;
+              ov = idn ? (float)idh[j] + sp : sp;
+            } else {
+              const int dc = 8 * r4 + j;
+              const bool ok = col + dc < a.Cout && n_ok[nt];
+              const int o = ob + dc * HoWo + e_off[nt];
+              if (ok && a.identity && a.identity_mode == ID_ADD_Z) z = z + a.identity[o];
+              if (EPI == EPI_Z) {
+                ov = z;
+              } else {
+                float vv = lif_charge_m<LM>(v[nt][r], z, a.lif);
+                const float sp = lif_fire_reset_bit<LM>(vv, a.lif) ? 1.0f : 0.0f;
+                v[nt][r] = vv;
+                if (idn) ov = (float)idh[j] + sp;
+                else if (ok && a.identity && a.identity_mode == ID_ADD_SPIKE) ov = a.identity[o] + sp;
+                else ov = sp;
+              }
+              if (ok && a.out) a.out[o] = ov;
+            }
+            pk[j] = (_Float16)ov;
+          }
+          *reinterpret_cast<h4*>(&ostage[(wn * WN + nt * 32 + (lane & 31)) * OLD + colb]) = pk;
         }
+      }
     };
 #pragma unroll
     for (int t = 0; t < TB; ++t) {
@@ -460,7 +540,7 @@ void conv_halo_kernel(HaloArgs a) {
       else epi_step(std::false_type{}, t);
       if (a.out_nhwc) {
         __syncthreads();  // the step's tile is staged
-        const _Float16* ostage = halo + (t % NOBUF) * OSTEP;
+        const _Float16* ostage = obuf + (t % NOBUF) * OSTEP;
         constexpr int CH8 = BM / 8;  // 16-byte chunks per pixel
         for (int c = tid; c < BN * CH8; c += 256) {
           const int px = c / CH8, part = c % CH8;
@@ -474,44 +554,43 @@ void conv_halo_kernel(HaloArgs a) {
         }
       }
     }
-  }
-
-  if (EPI == EPI_LIF && a.v_out) {
-    const int col = opaque(co_lane);
-    const int vb = (b * a.Cout + col) * HoWo;
+    // The block's final membrane potentials (the layer's state after the last block).
+    if (EPI == EPI_LIF && a.v_out) {
+      const int col = opaque(co_lane);
+      const int vb = (b * a.Cout + col) * HoWo;
 #pragma unroll
-    for (int nt = 0; nt < NT; ++nt) {
-      if (!n_ok[nt]) continue;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt)
+      for (int nt = 0; nt < NT; ++nt) {
+        if (!n_ok[nt]) continue;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int dc = mt * 32 + 8 * (r >> 2) + (r & 3);
-          if (full_c || col + dc < a.Cout) a.v_out[vb + dc * HoWo + e_off[nt]] = v[mt][nt][r];
+          const int dc = 8 * (r >> 2) + (r & 3);
+          if (full_c || col + dc < a.Cout) a.v_out[vb + dc * HoWo + e_off[nt]] = v[nt][r];
         }
+      }
     }
   }
+
 }
 
-template <int BM, int TH, int TW, int S, int K = 3>
+template <int TH, int TW, int S, int K = 3>
 hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
-  dim3 grid((unsigned)(a.B * a.GH * a.GW), (unsigned)(a.Coutp / BM));
+  dim3 grid((unsigned)(a.B * a.GH * a.GW), (unsigned)(a.Coutp / 64));
   const dim3 block(256);
   if (epi == EPI_Z) {
-    hipLaunchKernelGGL((conv_halo_kernel<BM, TH, TW, S, K, EPI_Z, LM_GENERIC>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_Z, LM_GENERIC>), grid, block, 0, st, a);
   } else {
     switch (cf_lif_mode(a.lif)) {
       case LM_HARD0_DECAY_P2:
-        hipLaunchKernelGGL((conv_halo_kernel<BM, TH, TW, S, K, EPI_LIF, LM_HARD0_DECAY_P2>), grid,
-                           block, 0, st, a);
+        hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LM_HARD0_DECAY_P2>), grid, block,
+                           0, st, a);
         break;
       case LM_HARD_DECAY_P2:
-        hipLaunchKernelGGL((conv_halo_kernel<BM, TH, TW, S, K, EPI_LIF, LM_HARD_DECAY_P2>), grid,
-                           block, 0, st, a);
+        hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LM_HARD_DECAY_P2>), grid, block,
+                           0, st, a);
         break;
       default:
-        hipLaunchKernelGGL((conv_halo_kernel<BM, TH, TW, S, K, EPI_LIF, LM_GENERIC>), grid, block,
-                           0, st, a);
+        hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LM_GENERIC>), grid, block, 0, st,
+                           a);
     }
   }
   return hipGetLastError();
@@ -552,8 +631,12 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
     return (int)hipErrorInvalidValue;
   if (ag_mask && (group_size <= 0 || (Cp + group_size - 1) / group_size > 32))
     return (int)hipErrorInvalidValue;
-  if (T * B * Cout * Ho * Wo > INT32_MAX || T * B * H * W > ((int64_t)1 << 40))
+  if (T * B * Cout * Ho * Wo > INT32_MAX || T * B * H * W > ((int64_t)1 << 40) ||
+      H * W * Cp > INT32_MAX)
     return (int)hipErrorInvalidValue;
+  // The membrane state passes from one time block to the next through v_out.
+  const int tb = (stride == 2 && ksize == 3) ? halo_tb<2, 3>() : halo_tb<1, 3>();
+  if (epilogue == EPI_LIF && !v_out && T > tb) return (int)hipErrorInvalidValue;
   HaloArgs a;
   a.x = (const _Float16*)x; a.w = (const _Float16*)w_packed; a.alpha = alpha; a.beta = beta;
   a.v_in = v_in; a.v_out = v_out; a.out = out; a.identity = identity;
@@ -571,23 +654,14 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
   a.gs = group_size > 0 ? (int)group_size : 32;
   a.lif = cf_make_lif_params(tau, v_th, v_reset, hard_reset, decay_input);
   hipStream_t st = (hipStream_t)stream;
-  // 64-channel tiles: measured faster on every SEW-ResNet18 layer than
-  // 128-channel ones (which hold one workgroup per CU slot).
-  // CATFUSE_HALO_BM=128 selects 128-channel tiles (tuning).
-  bool bm128 = false;
-  if (const char* e = getenv("CATFUSE_HALO_BM")) {
-    if (atoi(e) == 128) bm128 = (Coutp % 128 == 0);
-    else if (atoi(e) == 64) bm128 = false;
-  }
   hipError_t e;
   if (ksize == 1)
-    e = stride == 1 ? launch_halo<64, 8, 8, 1, 1>(a, epilogue, st)
-                    : launch_halo<64, 8, 8, 2, 1>(a, epilogue, st);
+    e = stride == 1 ? launch_halo<8, 8, 1, 1>(a, epilogue, st) : launch_halo<8, 8, 2, 1>(a, epilogue, st);
   else if (stride == 1 && tile_w == 16)
-    e = launch_halo<64, 8, 16, 1>(a, epilogue, st);  // 64-channel tiles (register budget)
+    e = launch_halo<8, 16, 1>(a, epilogue, st);
   else if (stride == 1)
-    e = bm128 ? launch_halo<128, 8, 8, 1>(a, epilogue, st) : launch_halo<64, 8, 8, 1>(a, epilogue, st);
+    e = launch_halo<8, 8, 1>(a, epilogue, st);
   else
-    e = bm128 ? launch_halo<128, 8, 8, 2>(a, epilogue, st) : launch_halo<64, 8, 8, 2>(a, epilogue, st);
+    e = launch_halo<8, 8, 2>(a, epilogue, st);
   return (int)e;
 }

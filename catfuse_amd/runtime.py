@@ -498,8 +498,10 @@ class ConvLIFRunner:
             require_gpu_tensor(v_in, "v_in")
             if v_in.numel() != B * self.Cout * Ho * Wo:
                 raise ValueError("v_in has the wrong size")
+        # the halo kernel carries the membrane state between its time blocks
+        # (2 or 4 steps) through v_out, so it gets one whenever T > 2
         v_out = (torch.empty((B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
-                 if (epilogue == EPI_LIF and want_v_out) else None)
+                 if (epilogue == EPI_LIF and (want_v_out or T > 2)) else None)
         cp_out = pad32(self.Cout)
         nhwc = (torch.empty((T * B, Ho, Wo, cp_out), dtype=torch.float16, device=dev)
                 if (emit_nhwc and epilogue == EPI_LIF) else None)
@@ -524,7 +526,7 @@ class ConvLIFRunner:
             flops=2 * T * B * Ho * Wo * self.Cout * self.Cin * self.KH * self.KW)
         self.last_nnz = nnz
         self.last_tiles = None if ag is None else (tc_buf, ag)
-        return out, v_out
+        return out, (v_out if want_v_out else None)
 
     def run_direct(self, x: torch.Tensor, v_in=None, *, epilogue=EPI_LIF, want_v_out=True,
                    emit_nhwc=False):
@@ -546,8 +548,10 @@ class ConvLIFRunner:
         if v_in is not None:
             require_gpu_tensor(v_in, "v_in")
         out = torch.empty((T, B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
+        # the halo kernel carries the membrane state between its time blocks
+        # (2 or 4 steps) through v_out, so it gets one whenever T > 2
         v_out = (torch.empty((B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
-                 if (epilogue == EPI_LIF and want_v_out) else None)
+                 if (epilogue == EPI_LIF and (want_v_out or T > 2)) else None)
         cp_out = pad32(self.Cout)
         nhwc = (torch.empty((T * B, Ho, Wo, cp_out), dtype=torch.float16, device=dev)
                 if (emit_nhwc and epilogue == EPI_LIF) else None)

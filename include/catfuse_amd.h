@@ -143,7 +143,9 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
  *   identity_nhwc (nullable, mode 1 only): the same identity as fp16 NHWC
  *   [T*B][Ho][Wo][cp_id] (cp_id >= Cout, a multiple of 4), read instead of
  *   the NCHW one (exact for the integer values a SEW ADD identity holds);
- *   v_in/v_out: [B][Cout][Ho][Wo] (nullable);
+ *   v_in/v_out: [B][Cout][Ho][Wo] (nullable, except that layers taking the
+ *   halo kernel (cf_conv_halo) need v_out for the LIF epilogue when T > 2:
+ *   the state passes between its time blocks through it);
  *   tile_h/tile_w > 0 selects rectangular pixel tiles aligned with the
  *   prescan tiles (tile_h*tile_w in {64,128}) and enables SparseFlow chunk
  *   skipping from ag_mask ([T][B*GH*GW]) when nnz is non-NULL; tile_h = 0

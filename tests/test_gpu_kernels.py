@@ -275,6 +275,31 @@ def test_sparse_8x16_tiles_bitwise_equals_dense(cuda, rate):
     lif_parity(s_dense.cpu().numpy(), v_dense.cpu().numpy(), s_ref, v_ref, h_ref, what="56x56")
 
 
+@pytest.mark.parametrize("stride,T", [(1, 7), (2, 5)])
+def test_sparse_route_multiblock_bitwise(cuda, stride, T):
+    # several time blocks per tile (4 steps, 2 for stride 2): the state
+    # passes between blocks through v_out, the staging of the next block's
+    # first chunk overlaps the current block's taps
+    B, C, H, W = 2, 96, 16, 16
+    conv, bn, lif = _layer(C, 64, 3, stride, 1, seed=11 + stride)
+    g = _gen(31 + T)
+    x = (torch.rand(T, B, C, H, W, generator=g) < 0.05).float()
+    x[:, :, 32:64] = 0.0                       # a chunk inactive everywhere
+    x[1] = 0.0                                 # a step with no input at all
+    r = _runner(conv, bn, lif, cuda)
+    xd = x.to(cuda)
+    Ho = (H + 2 - 3) // stride + 1
+    v0 = (torch.rand(B, 64, Ho, Ho, generator=g) * 0.5).to(cuda)
+    s_dense, v_dense = r.run_mfma(xd, v0, static_zero=False)
+    s_sparse, v_sparse = r.run_mfma(xd, v0, sparse=dict(block_h=8, block_w=8, group_size=32))
+    assert torch.equal(s_sparse, s_dense) and torch.equal(v_sparse, v_dense)
+    s_nov, v_nov = r.run_mfma(xd, v0, want_v_out=False)
+    assert v_nov is None and torch.equal(s_nov, s_dense)
+    s_ref, v_ref, h_ref = oracle.conv_bn_lif(x, conv, bn, lif, v_in=v0.cpu())
+    lif_parity(s_dense.cpu().numpy(), v_dense.cpu().numpy(), s_ref, v_ref, h_ref,
+               what=f"multiblock s{stride} T{T}")
+
+
 def test_static_zero_route_equals_bias_only(cuda):
     T, B, C, H, W = 4, 2, 64, 8, 8
     conv, bn, lif = _layer(C, C, 3, 1, 1, seed=8)
