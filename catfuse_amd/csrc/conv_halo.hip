@@ -158,7 +158,9 @@ constexpr int halo_min_blocks() {
 // K: filter size (3, or 1 for pointwise convolutions, whose strided input
 // samples are staged densely: RH = TH, RW = TW).
 // LM: LIF specialisation (cf_lif_mode) of the EPI_LIF epilogue.
-template <int TH, int TW, int S, int K, int EPI, int LM>
+// LEAN: the EPI_LIF epilogue without fp32 output or fp32 identity, every
+// output channel real (Cout a multiple of 64): no per-element branches.
+template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN>
 __global__ __launch_bounds__(256, (halo_min_blocks<TH, TW>()))
 void conv_halo_kernel(HaloArgs a) {
   using G = HaloGeom<S, K, TH, TW>;
@@ -284,26 +286,77 @@ void conv_halo_kernel(HaloArgs a) {
   // arithmetic stays where the load is issued.
   const size_t img_stride = (size_t)a.H * a.W * a.Cp;  // halves per staged image
   const _Float16* zero_page = opaque_ptr(reinterpret_cast<const _Float16*>(&g_halo_zero));
-  auto stage_loads = [&](int tbs, int ch, uint32_t act, _Float16* hb, int i0, int i1) {
+  // This thread's unit of direct load i is the same for every K step of the
+  // tile: its source offset (halves, from the tile's top-left input pixel of
+  // time step 0 of the block; 32-bit, checked on the host), whether the
+  // pixel lies inside the image (bit i of cp_inb) and its time step within
+  // the block (bits 2i.. of cp_t).  Per K step only the block, the chunk and
+  // the step activity change.
+  const _Float16* xtile = a.x + (ptrdiff_t)((ptrdiff_t)ih0 * a.W + iw0) * a.Cp;
+  // Unit of direct load i of this thread: 64-unit block 4 i + w of wave w
+  // (wrapped into 0 .. NB-1: a wrapped load repeats another one, writing
+  // the same bytes), lane l unit 64 * block + l.  Its source offset (halves,
+  // from the tile's top-left input pixel of time step 0 of the block;
+  // 32-bit, checked on the host), whether the pixel lies inside the image,
+  // and its time step within the block.
+  auto unit_of = [&](int i, int& off, bool& inb, int& t) {
+    int blk = 4 * i + wave;
+    if (4 * NPF > NB && blk >= NB) blk -= NB;
+    const int l = opaque(lane);
+    const int U = blk * 64 + l;
+    const int slot = l & 3, pix = blk * 16 + (l >> 2);
+    const int c = pix % RW, ry = (pix / RW) % RH;
+    t = min(pix / (RW * RH), TB - 1);
+    const int rx = G::inv_col(c);
+    const int part = slot ^ G::swz(ry, c);
+    const int ih = ih0 + ry * SS, iw = iw0 + rx * SS;
+    inb = (U < NU) & (ih >= 0) & (ih < a.H) & (iw >= 0) & (iw < a.W);
+    off = t * a.B * (int)img_stride + ((ry * SS) * a.W + rx * SS) * a.Cp + part * 8;
+    return blk;
+  };
+  // The units are the same for every K step of the tile; each time block
+  // keeps them in registers for its taps (cp_off, bit i of cp_inb, bits
+  // 2i.. of cp_t), so a K step's loads cost a few instructions each.
+  int cp_off[NPF];
+  uint32_t cp_inb = 0u, cp_t = 0u;
+  auto units_precompute = [&]() {
+    cp_inb = 0u;
+    cp_t = 0u;
+#pragma unroll
+    for (int i = 0; i < NPF; ++i) {
+      bool inb;
+      int t;
+      unit_of(i, cp_off[i], inb, t);
+      cp_inb |= (inb ? 1u : 0u) << i;
+      cp_t |= (uint32_t)t << (2 * i);
+    }
+  };
+  // Direct loads i0 .. i1-1 (of NPF) of this thread for K step (tbs, ch)
+  // with step activity act into halo buffer hb.  Units of steps the chunk is
+  // inactive at, of pixels outside the image, and past the last unit (the
+  // buffer's tail) load zeros.  No branches.  PRE: from the precomputed
+  // units (inside a block's K loop), else computed here.
+  auto stage_loads = [&](auto pre_c, int tbs, int ch, uint32_t act, _Float16* hb, int i0, int i1) {
+    constexpr bool PRE = decltype(pre_c)::value;
     const int nst = tbs < a.T ? min(TB, a.T - tbs) : 0;  // 0: every unit loads zeros
-    const _Float16* xb = a.x + (size_t)(tbs * a.B + b) * img_stride + ch * KC;
+    const uint32_t live = act & ((1u << nst) - 1u);    // steps to load, bit t
+    const _Float16* xb = xtile + (size_t)(tbs * a.B + b) * img_stride + ch * KC;
 #pragma unroll
     for (int i = i0; i < i1; ++i) {
-      int blk = 4 * i + wave;
-      if (4 * NPF > NB && blk >= NB) blk -= NB;
-      const int l = opaque(lane);
-      const int U = blk * 64 + l;
-      const int slot = l & 3, pix = blk * 16 + (l >> 2);
-      const int c = pix % RW, ry = (pix / RW) % RH, t = pix / (RW * RH);
-      const int rx = G::inv_col(c);
-      const int part = slot ^ G::swz(ry, c);
-      const int ih = ih0 + ry * SS, iw = iw0 + rx * SS;
-      // bitwise tests: no branches around the address arithmetic
-      const bool ok = (U < NU) & (t < nst) & (((act >> t) & 1u) != 0u) & (ih >= 0) & (ih < a.H) &
-                      (iw >= 0) & (iw < a.W);
-      const _Float16* src = xb + (size_t)t * a.B * img_stride +
-                            (unsigned)((ih * a.W + iw) * a.Cp + part * 8);
-      lds_copy16(ok ? src : zero_page, __builtin_amdgcn_readfirstlane(lds_addr(hb + blk * 512)));
+      int off, t, blk;
+      bool inb;
+      if constexpr (PRE) {
+        blk = 4 * i + wave;
+        if (4 * NPF > NB && blk >= NB) blk -= NB;
+        off = cp_off[i];
+        inb = ((cp_inb >> i) & 1u) != 0u;
+        t = (cp_t >> (2 * i)) & 3u;
+      } else {
+        blk = unit_of(i, off, inb, t);
+      }
+      const bool ok = inb & (((live >> t) & 1u) != 0u);
+      lds_copy16(ok ? xb + off : zero_page,
+                 __builtin_amdgcn_readfirstlane(lds_addr(hb + blk * 512)));
     }
   };
 
@@ -362,10 +415,10 @@ void conv_halo_kernel(HaloArgs a) {
           if (tap + 1 < KK) load_w(cur ^ 1, tap + 1, ch);
           else load_w(cur ^ 1, 0, nc);
           if (KK == 1) {
-            stage_loads(stb, nc, nact, hb_next, 0, NPF);
+            stage_loads(std::true_type{}, stb, nc, nact, hb_next, 0, NPF);
           } else if (tap + 1 < KK) {
             const int i0 = (tap * NPF) / (KK - 1), i1 = ((tap + 1) * NPF) / (KK - 1);
-            if (i1 > i0) stage_loads(stb, nc, nact, hb_next, i0, i1);
+            if (i1 > i0) stage_loads(std::true_type{}, stb, nc, nact, hb_next, i0, i1);
           }
         }
         // Issue the loads before these MFMAs.
@@ -403,7 +456,7 @@ void conv_halo_kernel(HaloArgs a) {
   int pf_tb = s_tb;  // block of the K step already staged into buffer 0
   if (s_tb < a.T) {
     load_w(0, 0, s_ch);
-    stage_loads(s_tb, s_ch, s_act, halo, 0, NPF);
+    stage_loads(std::false_type{}, s_tb, s_ch, s_act, halo, 0, NPF);
   }
 
   for (int tb0 = 0; tb0 < a.T; tb0 += TB) {
@@ -416,6 +469,9 @@ void conv_halo_kernel(HaloArgs a) {
         for (int r = 0; r < 16; ++r) acc[t][nt][r] = 0.0f;
 
     // The block's K steps alternate halo buffers, starting with buffer 0.
+    // (The units are recomputed per block, unconditionally, so that they are
+    // not live across the epilogue.)
+    units_precompute();
     int buf = 0;
     while (s_tb == tb0) {
       int ntb, nc;
@@ -450,38 +506,43 @@ void conv_halo_kernel(HaloArgs a) {
     // in flight during the epilogue, which stages its output in buffer 1.
     if (s_tb < a.T && s_tb != pf_tb) {
       load_w(0, 0, s_ch);
-      stage_loads(s_tb, s_ch, s_act, halo, 0, NPF);
+      stage_loads(std::false_type{}, s_tb, s_ch, s_act, halo, 0, NPF);
       pf_tb = s_tb;
     }
     _Float16* obuf = halo + HB;
+    // Addresses below are a workgroup-uniform 64-bit base (scalar registers)
+    // plus a 32-bit per-lane offset.  Lane-constant parts: its channel
+    // column (col), its pixel (e_off, 0 for pixels outside the output).
+    const int col = opaque(co_lane);
+    int epix[NT];
+#pragma unroll
+    for (int nt = 0; nt < NT; ++nt) epix[nt] = n_ok[nt] ? e_off[nt] : 0;
     // Membrane potentials of this lane's elements live in registers during
     // the epilogue only: from v_in (or the initial value) for the first time
     // block, from v_out (written at the end of the previous block's epilogue
     // by this same lane) for later ones.
     float v[NT][16];
     if (EPI == EPI_LIF) {
-      const int col = opaque(co_lane);
-      const int vb = (b * a.Cout + col) * HoWo;
       const float* vsrc = tb0 == 0 ? a.v_in : a.v_out;
+      const float* vbase = vsrc ? vsrc + (size_t)b * a.Cout * HoWo : nullptr;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int dc = 8 * (r >> 2) + (r & 3);
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           float v0 = lif_initial_v(a.lif);
-          if (vsrc && (full_c || col + dc < a.Cout) && n_ok[nt]) v0 = vsrc[vb + dc * HoWo + e_off[nt]];
+          if (vbase && (full_c || col + dc < a.Cout) && n_ok[nt])
+            v0 = vbase[(unsigned)((col + dc) * HoWo + e_off[nt])];
           v[nt][r] = v0;
         }
       }
     }
-    const bool lean = EPI == EPI_LIF && !a.out && !a.identity && full_c;
-    auto epi_step = [&](auto lean_c, int t) {
-      constexpr bool LEAN = decltype(lean_c)::value;
+    auto epi_step = [&](int t) {
       const int tt = tb0 + t;
+      const int img = tt * a.B + b;
       _Float16* ostage = obuf + (t % NOBUF) * OSTEP;
-      const int col = opaque(co_lane);
-      const int ob = ((tt * a.B + b) * a.Cout + col) * HoWo;
       const _Float16* idn = a.identity_nhwc;
+      const _Float16* idbase = idn ? idn + (size_t)img * HoWo * a.cp_id : nullptr;
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         // Registers 4*r4 .. 4*r4+3 hold four consecutive output channels.
@@ -493,23 +554,29 @@ void conv_halo_kernel(HaloArgs a) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           h4 idh = {};
-          if (idn) {
-            const int pix = n_ok[nt] ? e_off[nt] : 0;
-            idh = *reinterpret_cast<const h4*>(
-                idn + ((size_t)(tt * a.B + b) * HoWo + pix) * a.cp_id + col + 8 * r4);
-          }
+          if (idbase)
+            idh = *reinterpret_cast<const h4*>(idbase + (unsigned)(epix[nt] * a.cp_id + col + 8 * r4));
           h4 pk;
+          if constexpr (LEAN) {
+            // Spikes as halves; identity + spike in packed fp16 (exact: both
+            // are small integers).  idh is +0 without an identity.
+            h4 sph;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const int r = 4 * r4 + j;
-            float z = acc[t][nt][r] * alv[j] + bev[j];
-            float ov;
-            if constexpr (LEAN) {
+            for (int j = 0; j < 4; ++j) {
+              const int r = 4 * r4 + j;
+              const float z = __builtin_fmaf(acc[t][nt][r], alv[j], bev[j]);
               float vv = lif_charge_m<LM>(v[nt][r], z, a.lif);
-              const float sp = lif_fire_reset_bit<LM>(vv, a.lif) ? 1.0f : 0.0f;
+              sph[j] = lif_fire_reset_bit<LM>(vv, a.lif) ? (_Float16)1.0f : (_Float16)0.0f;
               v[nt][r] = vv;
-              ov = idn ? (float)idh[j] + sp : sp;
-            } else {
+            }
+            pk = idh + sph;
+          } else {
+            const int ob = ((tt * a.B + b) * a.Cout + col) * HoWo;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int r = 4 * r4 + j;
+              float z = __builtin_fmaf(acc[t][nt][r], alv[j], bev[j]);
+              float ov;
               const int dc = 8 * r4 + j;
               const bool ok = col + dc < a.Cout && n_ok[nt];
               const int o = ob + dc * HoWo + e_off[nt];
@@ -525,46 +592,47 @@ void conv_halo_kernel(HaloArgs a) {
                 else ov = sp;
               }
               if (ok && a.out) a.out[o] = ov;
+              pk[j] = (_Float16)ov;
             }
-            pk[j] = (_Float16)ov;
           }
           *reinterpret_cast<h4*>(&ostage[(wn * WN + nt * 32 + (lane & 31)) * OLD + colb]) = pk;
         }
       }
     };
+    // Copy-out of a staged step: BN * BM/8 sixteen-byte chunks, CPI per thread.
+    constexpr int CH8 = BM / 8;  // 16-byte chunks per pixel
+    constexpr int CPI = (BN * CH8 + 255) / 256;
 #pragma unroll
     for (int t = 0; t < TB; ++t) {
       if (t >= nsteps) break;
       if (NOBUF == 1 && t > 0) __syncthreads();  // the previous step's copy-out is complete
-      if (lean) epi_step(std::true_type{}, t);
-      else epi_step(std::false_type{}, t);
+      epi_step(t);
       if (a.out_nhwc) {
         __syncthreads();  // the step's tile is staged
         const _Float16* ostage = obuf + (t % NOBUF) * OSTEP;
-        constexpr int CH8 = BM / 8;  // 16-byte chunks per pixel
-        for (int c = tid; c < BN * CH8; c += 256) {
+        _Float16* obase = a.out_nhwc + (size_t)((tb0 + t) * a.B + b) * HoWo * a.cp_out;
+#pragma unroll
+        for (int i = 0; i < CPI; ++i) {
+          const int c = opaque(tid) + 256 * i;
           const int px = c / CH8, part = c % CH8;
           const int py = px / TW, pxx = px % TW;
           const int co8 = cout0 + part * 8;
-          if (oh0 + py < a.Ho && ow0 + pxx < a.Wo && co8 < a.cp_out) {
-            const size_t pix = (size_t)(oh0 + py) * a.Wo + (ow0 + pxx);
-            *reinterpret_cast<u32x4*>(a.out_nhwc + (((size_t)(tb0 + t) * a.B + b) * HoWo + pix) * a.cp_out + co8) =
+          if ((c < BN * CH8) & (oh0 + py < a.Ho) & (ow0 + pxx < a.Wo) & (co8 < a.cp_out))
+            *reinterpret_cast<u32x4*>(obase + (unsigned)(((oh0 + py) * a.Wo + ow0 + pxx) * a.cp_out + co8)) =
                 *reinterpret_cast<const u32x4*>(&ostage[px * OLD + part * 8]);
-          }
         }
       }
     }
     // The block's final membrane potentials (the layer's state after the last block).
     if (EPI == EPI_LIF && a.v_out) {
-      const int col = opaque(co_lane);
-      const int vb = (b * a.Cout + col) * HoWo;
+      float* vbase = a.v_out + (size_t)b * a.Cout * HoWo;
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
         if (!n_ok[nt]) continue;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int dc = 8 * (r >> 2) + (r & 3);
-          if (full_c || col + dc < a.Cout) a.v_out[vb + dc * HoWo + e_off[nt]] = v[nt][r];
+          if (full_c || col + dc < a.Cout) vbase[(unsigned)((col + dc) * HoWo + e_off[nt])] = v[nt][r];
         }
       }
     }
@@ -576,21 +644,26 @@ template <int TH, int TW, int S, int K = 3>
 hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
   dim3 grid((unsigned)(a.B * a.GH * a.GW), (unsigned)(a.Coutp / 64));
   const dim3 block(256);
+  const bool lean = epi == EPI_LIF && !a.out && !a.identity && a.Cout % 64 == 0;
   if (epi == EPI_Z) {
-    hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_Z, LM_GENERIC>), grid, block, 0, st, a);
+    hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_Z, LM_GENERIC, false>), grid, block, 0,
+                       st, a);
+  } else if (!lean) {
+    hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LM_GENERIC, false>), grid, block, 0,
+                       st, a);
   } else {
     switch (cf_lif_mode(a.lif)) {
       case LM_HARD0_DECAY_P2:
-        hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LM_HARD0_DECAY_P2>), grid, block,
-                           0, st, a);
+        hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LM_HARD0_DECAY_P2, true>), grid,
+                           block, 0, st, a);
         break;
       case LM_HARD_DECAY_P2:
-        hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LM_HARD_DECAY_P2>), grid, block,
-                           0, st, a);
+        hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LM_HARD_DECAY_P2, true>), grid,
+                           block, 0, st, a);
         break;
       default:
-        hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LM_GENERIC>), grid, block, 0, st,
-                           a);
+        hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LM_GENERIC, true>), grid, block,
+                           0, st, a);
     }
   }
   return hipGetLastError();
@@ -631,8 +704,10 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
     return (int)hipErrorInvalidValue;
   if (ag_mask && (group_size <= 0 || (Cp + group_size - 1) / group_size > 32))
     return (int)hipErrorInvalidValue;
+  // 32-bit element indices of the outputs, and 32-bit offsets of a tile's
+  // input within one time block (4 steps)
   if (T * B * Cout * Ho * Wo > INT32_MAX || T * B * H * W > ((int64_t)1 << 40) ||
-      H * W * Cp > INT32_MAX)
+      4 * B * H * W * Cp > INT32_MAX)
     return (int)hipErrorInvalidValue;
   // The membrane state passes from one time block to the next through v_out.
   const int tb = (stride == 2 && ksize == 3) ? halo_tb<2, 3>() : halo_tb<1, 3>();

@@ -294,7 +294,7 @@ __global__ __launch_bounds__(256, (conv_min_blocks<BM, BN, EPI>())) void conv_mf
         for (int nb = 0; nb < NB; ++nb) {
           if (e_img[nb] < 0) continue;
           const size_t o = ((size_t)(t * a.B + e_img[nb]) * a.Cout + co) * HoWo + e_off[nb];
-          float z = acc[mb][nb][r] * al + be;
+          float z = __builtin_fmaf(acc[mb][nb][r], al, be);  // BN (one rounding, as the halo kernel)
           if (a.identity && a.identity_mode == ID_ADD_Z) z = z + a.identity[o];
           float ov;
           if (EPI == EPI_Z) {
