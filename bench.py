@@ -3,12 +3,17 @@
 
 One step = one full forward of the fused network over the batch (all T
 steps, stem to logits) on synthetic inputs resident in HBM, with a
-functional.reset_net before it.  Prints ONE JSON line (rank 0):
+functional.reset_net before it: by default a replay of the HIP graph that
+catfuse_amd.graph.capture records for reset_net + forward (the batch is
+copied into the graph's input first, inside the timed step; the replay's
+output is checked against the eager forward's); --eager times the eager
+launches instead.  Prints ONE JSON line (rank 0):
   value      = images/s = B / (seconds per step)
   roofline   = dominant kernel (the MFMA conv, conv_halo_kernel behind
                cf_conv_mfma) achieved dense-equivalent
-               TFLOP/s vs the 2.5 PFLOP/s fp16 dense MFMA peak, timed live
-               with HIP events on the launch stream during the timed steps
+               TFLOP/s vs the 2.5 PFLOP/s fp16 dense MFMA peak, timed with
+               HIP events on the launch stream around every launch of an
+               eager pass over the same steps (the kernels the graph replays)
   lif_tails  = standalone LIF-family kernels' achieved HBM GB/s vs 8 TB/s
   cpu_baseline = the CPU oracle (SpikingJelly-equivalent PyTorch/C
                multi-step path, fp32) on a bounded sample of the same
@@ -144,6 +149,8 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-tails", action="store_true")
     ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--eager", action="store_true",
+                    help="time eager launches instead of the captured HIP graph")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: every GPU box in this setup has a single "
@@ -152,6 +159,7 @@ def main():
 
     import torch
     import catfuse_amd
+    from catfuse_amd import graph as cf_graph
     from catfuse_amd import runtime, snn
 
     dev = torch.device("cuda", 0)
@@ -170,6 +178,8 @@ def main():
         torch.cuda.synchronize()
         catfuse_amd.check_status(dev)
 
+        # Eager pass with HIP events around every launch (per-kernel times
+        # for the roofline; the same kernels the graph replays).
         timer = runtime.KernelTimer()
         runtime.set_timer(timer)
         torch.cuda.synchronize()
@@ -180,8 +190,30 @@ def main():
         torch.cuda.synchronize()
         t1 = time.perf_counter()
         runtime.set_timer(None)
+        ms_eager = (t1 - t0) * 1e3 / args.steps
+        ms = ms_eager
+        mode = "eager"
+        if not args.eager:
+            # One step = copy the batch into the captured input + replay of
+            # reset_net + the whole fused forward (HIP graph).
+            graphed = cf_graph.capture(fused, x)
+            y_ref = y.clone()
+            for _ in range(args.warmup):
+                graphed(img)
+            torch.cuda.synchronize()
+            if not torch.equal(graphed(img), y_ref):
+                print("graph replay differs from the eager forward", file=sys.stderr)
+                sys.exit(1)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                y = graphed(img)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            ms = (t1 - t0) * 1e3 / args.steps
+            mode = "hip_graph"
+        catfuse_amd.check_status(dev)
     kern = timer.summary()
-    ms = (t1 - t0) * 1e3 / args.steps
     ips = B / (ms * 1e-3)
 
     conv = kern.get("conv_mfma", {})
@@ -204,6 +236,7 @@ def main():
     result = {
         "metric": METRIC, "value": round(ips, 2), "unit": "images/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "mode": mode, "eager_ms_per_step": round(ms_eager, 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp32 (conv: fp16 hi/lo split weights x fp16-exact spikes on MFMA, fp32 acc)",
         "data": "synthetic (seeded N(0,1) images, random kaiming weights, config BN stats)",

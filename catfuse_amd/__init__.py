@@ -45,4 +45,12 @@ def check_status(device=None) -> None:
                            "fp16 range (|x| > 65504 or not finite)")
 
 
-__all__ = ["optimize", "check_status", "__version__"]
+def capture(model, example, reset=True, warmup=2):
+    """HIP-graph replay of ``reset_net(model); model(example)`` (see
+    catfuse_amd.graph): returns a callable that copies its input into the
+    captured input buffer and replays the whole fused forward."""
+    from catfuse_amd import graph
+    return graph.capture(model, example, reset=reset, warmup=warmup)
+
+
+__all__ = ["optimize", "check_status", "capture", "__version__"]
