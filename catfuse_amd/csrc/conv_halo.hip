@@ -130,7 +130,7 @@ struct HaloArgs {
   int cp_id;
   int identity_mode;
   const int32_t* ag_mask;   // [T][B*GH*GW]
-  const unsigned long long* nnz;
+  unsigned long long* nnz;    // counter block (cf_nnz_release)
   int64_t numel;
   double sparse_thr;
   int T, B, Cp, Cout, Coutp, H, W, Ho, Wo, pad;
@@ -191,11 +191,21 @@ void conv_halo_kernel(HaloArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers
   const int wm = wave >> 1, wn = wave & 1;
   const int hi = lane >> 5;
-  const int tile = blockIdx.x;
+  // XCD-aware work order: workgroup L runs on XCD L % 8 (dispatch is
+  // round-robin over the 8 XCDs), and the XCD's workgroups take a contiguous
+  // range of work items, tile-major with the tile's 64-channel output blocks
+  // adjacent.  The blocks of a tile (which stage the same input halo) and
+  // neighbouring tiles (whose halos overlap) then run together on one XCD and
+  // share its L2.
+  const int nwork = a.B * a.GH * a.GW * (a.Coutp / BM);
+  const int L = blockIdx.x, xcd = L & 7, j = L >> 3;
+  const int work = xcd * (nwork >> 3) + min(xcd, nwork & 7) + j;
+  const int ncb = a.Coutp / BM;
+  const int tile = work / ncb;
   const int gw = tile % a.GW, gh = (tile / a.GW) % a.GH, b = tile / (a.GW * a.GH);
   const int oh0 = gh * TH, ow0 = gw * TW;
   const int ih0 = oh0 * S - a.pad, iw0 = ow0 * S - a.pad;
-  const int cout0 = blockIdx.y * BM;
+  const int cout0 = (work - tile * ncb) * BM;
   const int HoWo = a.Ho * a.Wo;
   const int nch = a.Cp / KC;
   const int ntiles = a.B * a.GH * a.GW;
@@ -637,12 +647,13 @@ void conv_halo_kernel(HaloArgs a) {
       }
     }
   }
+  cf_nnz_release(a.nnz, gridDim.x);
 
 }
 
 template <int TH, int TW, int S, int K = 3>
 hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
-  dim3 grid((unsigned)(a.B * a.GH * a.GW), (unsigned)(a.Coutp / 64));
+  dim3 grid((unsigned)(a.B * a.GH * a.GW * (a.Coutp / 64)));
   const dim3 block(256);
   const bool lean = epi == EPI_LIF && !a.out && !a.identity && a.Cout % 64 == 0;
   if (epi == EPI_Z) {
@@ -679,7 +690,7 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
                         void* out_nhwc, int64_t cp_out,
                         const float* identity, const void* identity_nhwc, int64_t cp_id,
                         int identity_mode, const int32_t* ag_mask,
-                        const unsigned long long* nnz, int64_t numel, double sparse_threshold,
+                        unsigned long long* nnz, int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
                         int64_t W, int64_t Ho, int64_t Wo, int64_t ksize, int64_t stride,
                         int64_t pad, int64_t tile_h, int64_t tile_w, int64_t group_size,
@@ -707,7 +718,8 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
   // 32-bit element indices of the outputs, and 32-bit offsets of a tile's
   // input within one time block (4 steps)
   if (T * B * Cout * Ho * Wo > INT32_MAX || T * B * H * W > ((int64_t)1 << 40) ||
-      4 * B * H * W * Cp > INT32_MAX)
+      4 * B * H * W * Cp > INT32_MAX ||
+      B * ((Ho + tile_h - 1) / tile_h) * ((Wo + tile_w - 1) / tile_w) * (Coutp / 64) * 256 > INT32_MAX)
     return (int)hipErrorInvalidValue;
   // The membrane state passes from one time block to the next through v_out.
   const int tb = (stride == 2 && ksize == 3) ? halo_tb<2, 3>() : halo_tb<1, 3>();

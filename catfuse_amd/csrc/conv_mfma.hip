@@ -61,7 +61,7 @@ struct ConvArgs {
   int cp_id;
   int identity_mode;
   const int32_t* ag_mask;
-  const unsigned long long* nnz;
+  unsigned long long* nnz;    // counter block (cf_nnz_release)
   int64_t numel;
   double sparse_thr;
   int T, B, Cp, Cout, Coutp, H, W, Ho, Wo, KH, KW, stride, pad;
@@ -328,6 +328,7 @@ __global__ __launch_bounds__(256, (conv_min_blocks<BM, BN, EPI>())) void conv_mf
             a.v_out[((size_t)e_img[nb] * a.Cout + co) * HoWo + e_off[nb]] = v[mb][nb][r];
         }
   }
+  cf_nnz_release(a.nnz, gridDim.x * gridDim.y);
 }
 
 // ---------------------------------------------------------------------------
@@ -422,7 +423,7 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
                         void* out_nhwc, int64_t cp_out,
                         const float* identity, const void* identity_nhwc, int64_t cp_id,
                         int identity_mode, const int32_t* ag_mask,
-                        const unsigned long long* nnz, int64_t numel, double sparse_threshold,
+                        unsigned long long* nnz, int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
                         int64_t W, int64_t Ho, int64_t Wo, int64_t ksize, int64_t stride,
                         int64_t pad, int64_t tile_h, int64_t tile_w, int64_t group_size,
@@ -434,7 +435,7 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
                         void* out_nhwc, int64_t cp_out,
                         const float* identity, const void* identity_nhwc, int64_t cp_id,
                         int identity_mode, const int32_t* ag_mask,
-                        const unsigned long long* nnz, int64_t numel, double sparse_threshold,
+                        unsigned long long* nnz, int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
                         int64_t W, int64_t Ho, int64_t Wo, int64_t KH, int64_t KW, int64_t stride,
                         int64_t pad, int64_t x_img_tstride, int64_t tile_h, int64_t tile_w,

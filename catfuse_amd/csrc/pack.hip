@@ -89,34 +89,44 @@ __global__ __launch_bounds__(256) void pack_kernel(
 
 // The same activity bits and nonzero count from an fp16 NHWC copy that a
 // fused conv already wrote (xp[NPIX][Cp], channels >= C zero), so a
-// SparseFlow layer whose input carries one needs no fp32 pass.  One thread
-// per pixel; group sizes are multiples of 8, so the 8 channels of a 16-byte
-// load share one group.
+// SparseFlow layer whose input carries one needs no fp32 pass.  Sixteen
+// lanes per pixel, each reading 16-byte chunks c8 = lane, lane + 16, ... (a
+// pixel's channels are one contiguous run, so a 16-lane group reads 256
+// contiguous bytes per load); group sizes are multiples of 8, so the 8
+// channels of a chunk share one group, and the pixel's bits are OR-reduced
+// over its 16 lanes.  Grid-stride over pixels; one atomic per block for the
+// count.
 __global__ __launch_bounds__(256) void scan_nhwc_kernel(
     const _Float16* __restrict__ xp, int64_t npix, int Cp, int C, uint32_t* __restrict__ act,
     int gs, float thr, unsigned long long* __restrict__ nnz) {
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   __shared__ unsigned int cnt_sh;
-  const int tid = threadIdx.x;
-  const int64_t p = (int64_t)blockIdx.x * 256 + tid;
+  const int tid = threadIdx.x, sub = tid & 15;
   if (tid == 0) cnt_sh = 0;
   __syncthreads();
-  uint32_t bits = 0;
   unsigned int cnt = 0;
-  if (p < npix) {
-    const _Float16* src = xp + p * Cp;
-    for (int c0 = 0; c0 < Cp; c0 += 8) {
-      const h8 hv = *reinterpret_cast<const h8*>(src + c0);
-      bool any = false;
+  const int nc8 = Cp / 8;
+  for (int64_t p0 = (int64_t)blockIdx.x * 16; p0 < npix; p0 += (int64_t)gridDim.x * 16) {
+    const int64_t p = p0 + (tid >> 4);
+    uint32_t bits = 0;
+    if (p < npix) {
+      const _Float16* src = xp + p * Cp;
+      for (int c8 = sub; c8 < nc8; c8 += 16) {
+        const h8 hv = *reinterpret_cast<const h8*>(src + c8 * 8);
+        bool any = false;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float v = (float)hv[j];
-        cnt += (v != 0.0f) ? 1u : 0u;
-        any |= fabsf(v) > thr && c0 + j < C;
+        for (int j = 0; j < 8; ++j) {
+          const float v = (float)hv[j];
+          cnt += (v != 0.0f) ? 1u : 0u;
+          any |= fabsf(v) > thr && c8 * 8 + j < C;
+        }
+        if (any) bits |= 1u << (unsigned)((c8 * 8) / gs);
       }
-      if (any) bits |= 1u << (unsigned)(c0 / gs);
     }
-    if (act) act[p] = bits;
+    // the 16 lanes of a pixel share p, so this reduction stays in bounds
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) bits |= __shfl_xor(bits, off, 16);
+    if (act && p < npix && sub == 0) act[p] = bits;
   }
   if (nnz) {
     for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
@@ -201,7 +211,8 @@ CF_API int cf_scan_nhwc(const void* xp, int64_t NB, int64_t H, int64_t W, int64_
   if (group_size <= 0) group_size = 32;
   const int64_t npix = NB * H * W;
   if (npix == 0) return 0;
-  hipLaunchKernelGGL(scan_nhwc_kernel, dim3(cf_blocks(npix, 256)), dim3(256), 0,
+  const int64_t nblk = (npix + 15) / 16;
+  hipLaunchKernelGGL(scan_nhwc_kernel, dim3((unsigned)(nblk < 1024 ? nblk : 1024)), dim3(256), 0,
                      (hipStream_t)stream, (const _Float16*)xp, npix, (int)Cp, (int)C, act,
                      group_size, threshold, nnz);
   return (int)hipGetLastError();

@@ -437,6 +437,16 @@ class ConvLIFRunner:
             self._ws[key] = t
         return t
 
+    def counter(self, device):
+        """The layer's nonzero-count block (3 x u64: count, completion tally,
+        last count).  Zeroed once when created; afterwards the conv that
+        consumes the count leaves it cleared for the next producer pass."""
+        t = self._ws.get("nnz")
+        if t is None or t.device != device:
+            t = torch.zeros((3,), dtype=torch.int64, device=device)
+            self._ws["nnz"] = t
+        return t
+
     def run_mfma(self, x: torch.Tensor, v_in=None, *, epilogue=EPI_LIF, want_v_out=True,
                  identity=None, identity_mode=ID_ADD_SPIKE, sparse=None, sparse_threshold=0.7,
                  static_zero=True, emit_nhwc=True):
@@ -460,15 +470,13 @@ class ConvLIFRunner:
         if xp is not None and sparse is not None:
             # SparseFlow on an input that carries its fp16 NHWC copy: the
             # activity bits and the nonzero count come from the copy
-            nnz = self.workspace("nnz", (1,), torch.int64, dev)
-            zero_counter(nnz)
+            nnz = self.counter(dev)
             act = scan_nhwc(xp, C, group_size=gs, nnz=nnz,
                             act_out=self.workspace("act", (T * B, H, W), torch.int32, dev))
         elif xp is None:
             st = status_word(dev)
             if static_zero or sparse is not None:
-                nnz = self.workspace("nnz", (1,), torch.int64, dev)
-                zero_counter(nnz)
+                nnz = self.counter(dev)
             xp = self.workspace("xp", (T * B, H, W, self.Cp), torch.float16, dev)
             act = (self.workspace("act", (T * B, H, W), torch.int32, dev) if sparse is not None
                    else None)
@@ -524,7 +532,7 @@ class ConvLIFRunner:
         check(rc, "cf_conv_mfma")
         _t1("conv_mfma" + ("_sparse" if sparse is not None else ""), ev,
             flops=2 * T * B * Ho * Wo * self.Cout * self.Cin * self.KH * self.KW)
-        self.last_nnz = nnz
+        self.last_nnz = None if nnz is None else nnz[2:3]  # the count of this input
         self.last_tiles = None if ag is None else (tc_buf, ag)
         return out, (v_out if want_v_out else None)
 

@@ -149,7 +149,11 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
  *   tile_h/tile_w > 0 selects rectangular pixel tiles aligned with the
  *   prescan tiles (tile_h*tile_w in {64,128}) and enables SparseFlow chunk
  *   skipping from ag_mask ([T][B*GH*GW]) when nnz is non-NULL; tile_h = 0
- *   selects flat pixel tiles (dense).  nnz non-NULL also enables the
+ *   selects flat pixel tiles (dense).  nnz (nullable) is a block of three
+ *   u64: [0] the input's nonzero count (accumulated by cf_pack_input /
+ *   cf_scan_nhwc), [1] a completion tally that must be 0 at launch, [2]
+ *   receives the count; the launch's last workgroup clears [0] and [1], so
+ *   the next producer pass needs no clearing launch.  nnz non-NULL also enables the
  *   StaticZero route.  All routes give bit-identical results.
  * Replaces catfuse/implementations/dense_keep.py:97-155 (DenseKeep.forward),
  * catfuse/implementations/sparse_flow.py:186-270 (SparseFlow.forward ->
@@ -158,7 +162,7 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
 int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha, const float* beta,
                  const float* v_in, float* v_out, float* out, void* out_nhwc, int64_t cp_out,
                  const float* identity, const void* identity_nhwc, int64_t cp_id,
-                 int identity_mode, const int32_t* ag_mask, const unsigned long long* nnz,
+                 int identity_mode, const int32_t* ag_mask, unsigned long long* nnz,
                  int64_t numel, double sparse_threshold, int64_t T, int64_t B, int64_t Cp,
                  int64_t Cout,
                  int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo, int64_t KH,
@@ -177,7 +181,7 @@ int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha, const 
 int cf_conv_halo(const void* x, const void* w_packed, const float* alpha, const float* beta,
                  const float* v_in, float* v_out, float* out, void* out_nhwc, int64_t cp_out,
                  const float* identity, const void* identity_nhwc, int64_t cp_id,
-                 int identity_mode, const int32_t* ag_mask, const unsigned long long* nnz,
+                 int identity_mode, const int32_t* ag_mask, unsigned long long* nnz,
                  int64_t numel, double sparse_threshold, int64_t T, int64_t B, int64_t Cp,
                  int64_t Cout, int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
                  int64_t ksize, int64_t stride, int64_t pad, int64_t tile_h, int64_t tile_w,

@@ -88,6 +88,28 @@ def test_stem_maxpool_pattern_direct_and_fallback(cuda):
     pooled_parity(out3.cpu().numpy(), s3, h3, what="fallback")
 
 
+def test_route_counter_clears_between_calls(cuda):
+    # the nonzero count is cleared by the conv that consumes it: a sequence of
+    # calls with different sparsity must route each input on its own count,
+    # both from an fp32 input (pack pass) and from a fused layer's NHWC copy
+    # (scan pass)
+    from catfuse_amd.patterns import STFusionConvBNLIF
+    m = _triple(256, 256, 3, 1, 1, seed=4)
+    st = STFusionConvBNLIF.from_sj_modules(*m).to(cuda)
+    prod = STFusionConvBNLIF.from_sj_modules(*m).to(cuda)
+    for rate in (0.0, 0.5, 0.0, 0.01, 0.5, 0.01, 0.0):
+        x = (torch.rand(4, 2, 256, 14, 14, generator=_gen(int(rate * 1000) + 7)) < rate).float()
+        st.reset()
+        st(x.to(cuda))
+        assert st.last_route() == oracle.route(x), f"fp32 input, rate {rate}"
+        # an input carried as a fused layer's NHWC copy
+        prod.reset()
+        y = prod(x.to(cuda) * 4.0)
+        st.reset()
+        st(y)
+        assert st.last_route() == oracle.route(y.cpu()), f"NHWC input, rate {rate}"
+
+
 @pytest.mark.parametrize("rate", [0.0, 0.01, 0.05, 0.2, 0.5])
 def test_stfusion_c1_all_impls_bitwise(cuda, rate):
     from catfuse_amd.implementations import DenseKeep, StreamFuse
