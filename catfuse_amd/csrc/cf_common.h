@@ -127,22 +127,23 @@ __device__ __forceinline__ float lif_initial_v(const LifParams& p) {
 //   [1] completion tally of the conv's workgroups;
 //   [2] the count of the conv's input, kept for inspection.
 // The conv's last workgroup to finish moves [0] to [2] and clears [0] and
-// [1]: every workgroup has read [0] before it counts itself complete, so the
-// next producer pass starts from zero with no separate clearing launch.
-// Called by every thread of the workgroup at the end of the kernel.
+// [1]: every workgroup has read [0] (and routed on it) before it counts
+// itself complete, so the next producer pass starts from zero with no
+// separate clearing launch.  No fences: nothing in this kernel reads [0]
+// after the tally is complete, and the kernel boundary orders the clearing
+// before the next pass.  (A release fence at agent scope would write back
+// the L2 of the workgroup's XCD.)  Called by every thread of the workgroup at
+// the end of the kernel.
 __device__ __forceinline__ void cf_nnz_release(unsigned long long* nnz, unsigned nwg) {
   if (!nnz) return;
   __syncthreads();
   if (threadIdx.x == 0) {
-    __threadfence();
     const unsigned long long prev = atomicAdd(&nnz[1], 1ull);
     if (prev == (unsigned long long)nwg - 1ull) {
-      __threadfence();
       const unsigned long long k = atomicAdd(&nnz[0], 0ull);
       nnz[2] = k;
       nnz[0] = 0ull;
       nnz[1] = 0ull;
-      __threadfence();
     }
   }
 }
