@@ -50,9 +50,9 @@ def build_model(num_classes=1000, seed=0):
 
 def traffic_from_profiles():
     """HBM bytes per launch of the dominant kernel from the committed
-    rocprofv3 PMC summary (profiles/conv_mfma_sew_resnet18_traffic.json), or
+    rocprofv3 PMC summary (profiles/conv_halo_sew_resnet18_traffic.json), or
     None when it has not been collected."""
-    p = os.path.join(ROOT, "profiles", "conv_mfma_sew_resnet18_traffic.json")
+    p = os.path.join(ROOT, "profiles", "conv_halo_sew_resnet18_traffic.json")
     if not os.path.exists(p):
         return None
     try:
