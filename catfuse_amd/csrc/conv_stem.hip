@@ -75,16 +75,25 @@ template <typename SW, int LM>
 __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 2 : 1) void conv_stem_kernel(StemArgs a) {
   constexpr int SLD = spike_ld<SW>();
   __shared__ __attribute__((aligned(16))) _Float16 xs[2][RH * RW * 4];
-  __shared__ SW spk[NPIX * SLD];
-  __shared__ SW pooled[PTH * PTW * SLD];
+  __shared__ __attribute__((aligned(16))) SW spk[NPIX * SLD];
+  __shared__ __attribute__((aligned(16))) SW pooled[PTH * PTW * SLD];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int mt = wave >> 1, nsel = wave & 1;
-  const int tile = blockIdx.x;
+  // XCD-aware work order (workgroup L runs on XCD L % 8; each XCD takes a
+  // contiguous range of work items, tile-major with the 64-channel blocks
+  // adjacent): horizontally neighbouring tiles, whose 56-byte segments of
+  // the fp32 state rows share cache lines and whose input patches overlap,
+  // run on the same XCD and meet in its L2.
+  const int ncb = a.Coutp / BMS;
+  const int nwork = a.B * a.GHp * a.GWp * ncb;
+  const int L = blockIdx.x, xcd = L & 7;
+  const int work = xcd * (nwork >> 3) + min(xcd, nwork & 7) + (L >> 3);
+  const int tile = work / ncb;
   const int gw = tile % a.GWp, gh = (tile / a.GWp) % a.GHp, b = tile / (a.GWp * a.GHp);
   const int ph0 = gh * PTH, pw0 = gw * PTW;
   const int y0 = 2 * ph0 - 1, x0 = 2 * pw0 - 1;  // conv output at local (0, 0)
-  const int cout0 = blockIdx.y * BMS;
+  const int cout0 = (work - tile * ncb) * BMS;
 
   // Weight fragments of this wave's 32 output channels, all filter rows.
   h8 wh[MAXKH][2], wl[MAXKH][2];
@@ -152,8 +161,24 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 2 : 1) void conv_stem_kernel
   const int cl0 = mt * 32 + 4 * (lane >> 5);  // channel of register r: cl0 + 8 * (r / 4) + r % 4
   const size_t vplane = (size_t)a.Hc * a.Wc;
 
+  // BN coefficients of this lane's 16 channels (registers 4*q .. 4*q+3 hold
+  // channels cl0 + 8q .. + 3), loaded once.
+  float alr[16], ber[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int co = cout0 + cl0 + 8 * (r >> 2) + (r & 3);  // < Coutp: alpha/beta are padded
+    alr[r] = a.alpha[co];
+    ber[r] = a.beta[co];
+  }
+  // Membrane-state planes of this image: a uniform 64-bit base and 32-bit
+  // per-element offsets.
+  const float* vin_b = a.v_in ? a.v_in + (size_t)b * a.Cout * vplane : nullptr;
+  float* vout_b = a.v_out ? a.v_out + (size_t)b * a.Cout * vplane : nullptr;
+  const bool full_c = cout0 + BMS <= a.Cout;
+
   // Epilogue of one column tile: BN, then the LIF over T with a constant z,
-  // the 16 elements of the lane stepped together; spike trains -> LDS.
+  // the 16 elements of the lane stepped together; spike trains -> LDS (four
+  // consecutive channels' words per store).
   auto epilogue = [&](int nt, const f16v& acc) {
     const int n = nt * 32 + (lane & 31);
     const int nc = n < NPIX ? n : NPIX - 1;
@@ -161,17 +186,21 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 2 : 1) void conv_stem_kernel
     const int y = y0 + ly, x = x0 + lx;
     const bool valid = n < NPIX && y >= 0 && y < a.Hc && x >= 0 && x < a.Wc;
     const bool own = valid && ly >= 1 && lx >= 1;
-    const size_t vb = (((size_t)b * a.Cout + cout0 + cl0) * a.Hc + y) * a.Wc + x;
+    const unsigned vo = (unsigned)(((cout0 + cl0) * a.Hc + y) * a.Wc + x);
     float zr[16], vr[16];
     uint32_t bits[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      const int dc = 8 * (r >> 2) + (r & 3);
-      const int co = cout0 + cl0 + dc;
-      const bool ok = valid && co < a.Cout;
-      zr[r] = ok ? acc[r] * a.alpha[co] + a.beta[co] : 0.0f;
-      vr[r] = (ok && a.v_in) ? a.v_in[vb + dc * vplane] : lif_initial_v(a.lif);
+      zr[r] = __builtin_fmaf(acc[r], alr[r], ber[r]);
+      vr[r] = lif_initial_v(a.lif);
       bits[r] = 0u;
+    }
+    if (vin_b && valid) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dc = 8 * (r >> 2) + (r & 3);
+        if (full_c || cout0 + cl0 + dc < a.Cout) vr[r] = vin_b[vo + dc * (unsigned)vplane];
+      }
     }
     for (int t = 0; t < a.T; ++t) {
       const uint32_t tbit = 1u << t;
@@ -181,12 +210,37 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 2 : 1) void conv_stem_kernel
         bits[r] |= lif_fire_reset_bit<LM>(vr[r], a.lif) ? tbit : 0u;
       }
     }
+    if (vout_b && own) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int dc = 8 * (r >> 2) + (r & 3);
-      const bool ok = valid && cout0 + cl0 + dc < a.Cout;
-      if (ok && own && a.v_out) a.v_out[vb + dc * vplane] = vr[r];
-      if (n < NPIX) spk[n * SLD + cl0 + dc] = ok ? (SW)bits[r] : (SW)0;
+      for (int r = 0; r < 16; ++r) {
+        const int dc = 8 * (r >> 2) + (r & 3);
+        if (full_c || cout0 + cl0 + dc < a.Cout) vout_b[vo + dc * (unsigned)vplane] = vr[r];
+      }
+    }
+    if (n < NPIX) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        // channels cl0 + 8q .. + 3; channels >= Cout and invalid outputs
+        // hold zero words
+        SW w4[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int dc = 8 * q + j;
+          const bool ok = valid && (full_c || cout0 + cl0 + dc < a.Cout);
+          w4[j] = ok ? (SW)bits[4 * q + j] : (SW)0;
+        }
+        SW* dst = &spk[n * SLD + cl0 + 8 * q];
+        if constexpr (sizeof(SW) == 1) {
+          *reinterpret_cast<uint32_t*>(dst) = (uint32_t)w4[0] | ((uint32_t)w4[1] << 8) |
+                                              ((uint32_t)w4[2] << 16) | ((uint32_t)w4[3] << 24);
+        } else if constexpr (sizeof(SW) == 2) {
+          *reinterpret_cast<uint32_t*>(dst) = (uint32_t)w4[0] | ((uint32_t)w4[1] << 16);
+          *reinterpret_cast<uint32_t*>(dst + 2) = (uint32_t)w4[2] | ((uint32_t)w4[3] << 16);
+        } else {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) dst[j] = w4[j];
+        }
+      }
     }
   };
   auto tile_base = [&](int nt) {
@@ -234,15 +288,32 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 2 : 1) void conv_stem_kernel
   // and columns outside the conv output hold zero words, and every window
   // has a valid position).
   constexpr int NPOOL = PTH * PTW;
-  for (int i = tid; i < NPOOL * BMS; i += 256) {
-    const int cl = i % BMS, pp = i / BMS;
-    const int py = pp / PTW, px = pp % PTW;
-    SW o = 0;
+  if constexpr (sizeof(SW) <= 2) {
+    // four (uint8) or two (uint16) channels' words per 32-bit LDS access
+    constexpr int CPW = 4 / sizeof(SW);  // channels per word access
+    for (int i = tid; i < NPOOL * (BMS / CPW); i += 256) {
+      const int cg = i % (BMS / CPW), pp = i / (BMS / CPW);
+      const int py = pp / PTW, px = pp % PTW;
+      uint32_t o = 0u;
 #pragma unroll
-    for (int dy = 0; dy < 3; ++dy)
+      for (int dy = 0; dy < 3; ++dy)
 #pragma unroll
-      for (int dx = 0; dx < 3; ++dx) o |= spk[((2 * py + dy) * PRW + 2 * px + dx) * SLD + cl];
-    pooled[pp * SLD + cl] = o;
+        for (int dx = 0; dx < 3; ++dx)
+          o |= *reinterpret_cast<const uint32_t*>(
+              &spk[((2 * py + dy) * PRW + 2 * px + dx) * SLD + cg * CPW]);
+      *reinterpret_cast<uint32_t*>(&pooled[pp * SLD + cg * CPW]) = o;
+    }
+  } else {
+    for (int i = tid; i < NPOOL * BMS; i += 256) {
+      const int cl = i % BMS, pp = i / BMS;
+      const int py = pp / PTW, px = pp % PTW;
+      SW o = 0;
+#pragma unroll
+      for (int dy = 0; dy < 3; ++dy)
+#pragma unroll
+        for (int dx = 0; dx < 3; ++dx) o |= spk[((2 * py + dy) * PRW + 2 * px + dx) * SLD + cl];
+      pooled[pp * SLD + cl] = o;
+    }
   }
   __syncthreads();
 
@@ -389,7 +460,7 @@ CF_API int cf_conv_stem_lif_maxpool(const float* x, const void* w_stem, const fl
   a.Hc = (int)Hc; a.Wc = (int)Wc; a.Hp = (int)Hp; a.Wp = (int)Wp;
   a.GHp = (int)GHp; a.GWp = (int)GWp;
   a.lif = cf_make_lif_params(tau, v_th, v_reset, hard_reset, decay_input);
-  dim3 grid((unsigned)(B * GHp * GWp), (unsigned)(Coutp / BMS));
+  dim3 grid((unsigned)(B * GHp * GWp * (Coutp / BMS)));
   hipStream_t st = (hipStream_t)stream;
   const int lm = cf_lif_mode(a.lif);
   if (T <= 8) launch_stem<uint8_t>(a, lm, grid, st);
