@@ -136,6 +136,7 @@ struct HaloArgs {
   int T, B, Cp, Cout, Coutp, H, W, Ho, Wo, pad;
   int GH, GW;
   int gs;
+  int gs_shift;             // log2(gs) when gs is a power of two, else -1
   LifParams lif;
 };
 
@@ -252,14 +253,26 @@ void conv_halo_kernel(HaloArgs a) {
     if (route == CF_ROUTE_DENSE) return 0xffffffffu;
     return (uint32_t)a.ag_mask[(size_t)tt * ntiles + tile];
   };
+  // Group bits of chunk ch: groups g0 .. g1 its 32 channels fall in.
   auto chunk_bits = [&](int ch) -> uint32_t {
-    const int g0 = (ch * KC) / a.gs, g1 = (ch * KC + KC - 1) / a.gs;
-    uint32_t gb = 0u;
-    for (int g = g0; g <= g1 && g < 32; ++g) gb |= 1u << g;
-    return gb;
+    int g0, g1;
+    if (a.gs_shift >= 0) {
+      g0 = (ch * KC) >> a.gs_shift;
+      g1 = (ch * KC + KC - 1) >> a.gs_shift;
+    } else {
+      g0 = (ch * KC) / a.gs;
+      g1 = (ch * KC + KC - 1) / a.gs;
+    }
+    if (g0 > 31) return 0u;
+    const uint32_t hi = g1 >= 31 ? 0xffffffffu : ((2u << g1) - 1u);
+    return hi & ~((1u << g0) - 1u);
   };
-  // Steps (bit t) of the block starting at tbs that chunk ch is active at.
+  // Steps (bit t) of the block starting at tbs (< T) that chunk ch is
+  // active at: every step on the dense route, none on the zero route.
   auto chunk_act = [&](int tbs, int ch) -> uint32_t {
+    const int nst = min(TB, a.T - tbs);
+    if (route == CF_ROUTE_DENSE) return (1u << nst) - 1u;
+    if (route == CF_ROUTE_ZERO) return 0u;
     const uint32_t gb = chunk_bits(ch);
     uint32_t m = 0u;
 #pragma unroll
@@ -268,8 +281,20 @@ void conv_halo_kernel(HaloArgs a) {
   };
   // The K step after (tbs, ch): the next active chunk of the block, else the
   // first active chunk of a later block (tbs' = T when there is none), and
-  // its step activity.
+  // its step activity.  On the dense route every chunk of every block is a
+  // step, in order.
   auto next_step = [&](int tbs, int ch, int& ntb, int& nc, uint32_t& nact) {
+    if (route == CF_ROUTE_DENSE) {
+      if (ch + 1 < nch) {
+        ntb = tbs;
+        nc = ch + 1;
+      } else {
+        ntb = tbs + TB < a.T ? tbs + TB : a.T;
+        nc = 0;
+      }
+      nact = ntb < a.T ? (1u << min(TB, a.T - ntb)) - 1u : 0u;
+      return;
+    }
     for (int tb = tbs; tb < a.T; tb += TB) {
       for (int c = (tb == tbs ? ch + 1 : 0); c < nch; ++c) {
         const uint32_t m = chunk_act(tb, c);
@@ -285,15 +310,6 @@ void conv_halo_kernel(HaloArgs a) {
     nc = 0;
     nact = 0u;
   };
-  // Direct loads i0 .. i1-1 (of NPF) of this thread for K step (tbs, ch)
-  // with step activity act into halo buffer hb: load i of wave w fills the
-  // 64-unit block 4 i + w (wrapped into 0 .. NB-1: a wrapped load repeats
-  // another one, writing the same bytes), lane l unit 64 * block + l.  Units
-  // of steps the chunk is inactive at, of pixels outside the image, and past
-  // the last unit (the buffer's tail) load zeros.  No branches: the
-  // compiler's load counting stays exact, so the taps wait only for their
-  // own weights.  The unit indices are laundered so that the address
-  // arithmetic stays where the load is issued.
   const size_t img_stride = (size_t)a.H * a.W * a.Cp;  // halves per staged image
   const _Float16* zero_page = opaque_ptr(reinterpret_cast<const _Float16*>(&g_halo_zero));
   // This thread's unit of direct load i is the same for every K step of the
@@ -514,9 +530,13 @@ void conv_halo_kernel(HaloArgs a) {
     __syncthreads();
     // The next block's first K step: tap-0 weights and halo (into buffer 0)
     // in flight during the epilogue, which stages its output in buffer 1.
+    // (Two-step blocks, where a forward of 4 steps always has a next block,
+    // reuse the units computed for this block: they are the same for every
+    // block.  Four-step blocks compute them here, which keeps the units out of
+    // the registers live across their K loop.)
     if (s_tb < a.T && s_tb != pf_tb) {
       load_w(0, 0, s_ch);
-      stage_loads(std::false_type{}, s_tb, s_ch, s_act, halo, 0, NPF);
+      stage_loads(std::integral_constant<bool, (TB == 2)>{}, s_tb, s_ch, s_act, halo, 0, NPF);
       pf_tb = s_tb;
     }
     _Float16* obuf = halo + HB;
@@ -739,6 +759,7 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
   a.GH = (int)((Ho + tile_h - 1) / tile_h);
   a.GW = (int)((Wo + tile_w - 1) / tile_w);
   a.gs = group_size > 0 ? (int)group_size : 32;
+  a.gs_shift = (a.gs & (a.gs - 1)) == 0 ? __builtin_ctz((unsigned)a.gs) : -1;
   a.lif = cf_make_lif_params(tau, v_th, v_reset, hard_reset, decay_input);
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
