@@ -161,7 +161,9 @@ constexpr int halo_min_blocks() {
 // LM: LIF specialisation (cf_lif_mode) of the EPI_LIF epilogue.
 // LEAN: the EPI_LIF epilogue without fp32 output or fp32 identity, every
 // output channel real (Cout a multiple of 64): no per-element branches.
-template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN>
+// ONEB: T fits one time block (T <= TB): the block loop runs once, so the
+// K-loop state is dead in the epilogue (fewer live registers).
+template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB>
 __global__ __launch_bounds__(256, (halo_min_blocks<TH, TW>()))
 void conv_halo_kernel(HaloArgs a) {
   using G = HaloGeom<S, K, TH, TW>;
@@ -485,7 +487,7 @@ void conv_halo_kernel(HaloArgs a) {
     stage_loads(std::false_type{}, s_tb, s_ch, s_act, halo, 0, NPF);
   }
 
-  for (int tb0 = 0; tb0 < a.T; tb0 += TB) {
+  for (int tb0 = 0; tb0 < (ONEB ? 1 : a.T); tb0 += TB) {
     const int nsteps = min(TB, a.T - tb0);
 #pragma unroll
     for (int t = 0; t < TB; ++t)
@@ -676,26 +678,28 @@ hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
   dim3 grid((unsigned)(a.B * a.GH * a.GW * (a.Coutp / 64)));
   const dim3 block(256);
   const bool lean = epi == EPI_LIF && !a.out && !a.identity && a.Cout % 64 == 0;
+  const bool oneb = a.T <= halo_tb<S, K>();
   if (epi == EPI_Z) {
-    hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_Z, LM_GENERIC, false>), grid, block, 0,
-                       st, a);
+    hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_Z, LM_GENERIC, false, false>), grid,
+                       block, 0, st, a);
   } else if (!lean) {
-    hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LM_GENERIC, false>), grid, block, 0,
-                       st, a);
+    hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LM_GENERIC, false, false>), grid,
+                       block, 0, st, a);
   } else {
-    switch (cf_lif_mode(a.lif)) {
-      case LM_HARD0_DECAY_P2:
-        hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LM_HARD0_DECAY_P2, true>), grid,
-                           block, 0, st, a);
-        break;
-      case LM_HARD_DECAY_P2:
-        hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LM_HARD_DECAY_P2, true>), grid,
-                           block, 0, st, a);
-        break;
-      default:
-        hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LM_GENERIC, true>), grid, block,
-                           0, st, a);
+    const int lm = cf_lif_mode(a.lif);
+#define CF_HALO_LEAN(LMV, OB)                                                                   \
+  hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LMV, true, OB>), grid, block, 0, st, \
+                     a)
+    if (lm == LM_HARD0_DECAY_P2) {
+      if (oneb) CF_HALO_LEAN(LM_HARD0_DECAY_P2, true);
+      else CF_HALO_LEAN(LM_HARD0_DECAY_P2, false);
+    } else if (lm == LM_HARD_DECAY_P2) {
+      if (oneb) CF_HALO_LEAN(LM_HARD_DECAY_P2, true);
+      else CF_HALO_LEAN(LM_HARD_DECAY_P2, false);
+    } else {
+      CF_HALO_LEAN(LM_GENERIC, false);
     }
+#undef CF_HALO_LEAN
   }
   return hipGetLastError();
 }
