@@ -121,31 +121,45 @@ __device__ __forceinline__ float lif_initial_v(const LifParams& p) {
   return p.hard ? p.v_reset : 0.0f;
 }
 
-// Nonzero-count block of a SparseFlow / StaticZero layer: three u64,
-//   [0] count accumulated by the producer pass (pack / scan), read by every
-//       workgroup of the conv to pick its route;
-//   [1] completion tally of the conv's workgroups;
-//   [2] the count of the conv's input, kept for inspection.
-// The conv's last workgroup to finish moves [0] to [2] and clears [0] and
-// [1]: every workgroup has read [0] (and routed on it) before it counts
-// itself complete, so the next producer pass starts from zero with no
-// separate clearing launch.  No fences: nothing in this kernel reads [0]
-// after the tally is complete, and the kernel boundary orders the clearing
-// before the next pass.  (A release fence at agent scope would write back
-// the L2 of the workgroup's XCD.)  Called by every thread of the workgroup at
-// the end of the kernel.
-__device__ __forceinline__ void cf_nnz_release(unsigned long long* nnz, unsigned nwg) {
-  if (!nnz) return;
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned long long prev = atomicAdd(&nnz[1], 1ull);
-    if (prev == (unsigned long long)nwg - 1ull) {
-      const unsigned long long k = atomicAdd(&nnz[0], 0ull);
-      nnz[2] = k;
-      nnz[0] = 0ull;
-      nnz[1] = 0ull;
-    }
+// Count block of a producer pass (cf_pack_input, cf_scan_nhwc, a fused conv
+// writing its output): two u64,
+//   [0] the pass accumulator, (sum of workgroup counts) << CF_TALLY_BITS |
+//       completed workgroups; zero between passes;
+//   [1] the count of the last completed pass, read by the kernels that
+//       consume the pass's output (later in stream order).
+// Each workgroup adds its count and its completion with one atomic; the
+// workgroup that completes the pass (tally nwg - 1) stores the total in [1]
+// and clears [0], so the next pass starts from zero with no clearing launch.
+// One atomic carries both the count and the completion, so nothing orders
+// two updates and no fence is needed (an agent-scope release fence would
+// write back the L2 of the workgroup's XCD); the kernel boundary orders the
+// stores before the readers.  A pass has fewer than 2^24 workgroups (the
+// launchers check) and counts below 2^40.
+constexpr int CF_TALLY_BITS = 24;
+constexpr unsigned long long CF_MAX_COUNT_WG = 1ull << CF_TALLY_BITS;
+
+// Called by one thread of every workgroup of the pass, once its count is final.
+__device__ __forceinline__ void cf_count_publish(unsigned long long* blk, unsigned long long cnt,
+                                                 unsigned nwg) {
+  const unsigned long long prev = atomicAdd(&blk[0], (cnt << CF_TALLY_BITS) | 1ull);
+  if ((prev & (CF_MAX_COUNT_WG - 1ull)) == (unsigned long long)nwg - 1ull) {
+    blk[1] = (prev >> CF_TALLY_BITS) + cnt;
+    blk[0] = 0ull;
   }
+}
+
+// Workgroup "any" of a per-thread predicate (256-thread workgroups): one
+// wave vote per wave, combined through four LDS words after a barrier.
+__device__ __forceinline__ bool cf_wg_any(bool pred, unsigned* sh4) {
+  const bool w = __any(pred ? 1 : 0) != 0;
+  if ((threadIdx.x & 63) == 0) sh4[threadIdx.x >> 6] = w ? 1u : 0u;
+  __syncthreads();
+  return (sh4[0] | sh4[1] | sh4[2] | sh4[3]) != 0u;
+}
+
+// The published count of a block (a pass of an earlier kernel).
+__device__ __forceinline__ unsigned long long cf_count_read(const unsigned long long* blk) {
+  return blk[1];
 }
 
 // Host: LIF parameter block from SpikingJelly-level (double) parameters.

@@ -34,6 +34,18 @@ typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef float f16v __attribute__((ext_vector_type(16)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
+
+// Raw buffer resource over [base, base + bytes) (gfx9 word 3).  Buffer
+// loads outside the range return zeros and buffer stores outside it are
+// dropped by the hardware, so the lean epilogue issues every load and store
+// unconditionally (a fixed count per step, which lets the compiler wait for
+// exactly the loads it needs instead of draining earlier stores).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t halo_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+constexpr uint32_t HALO_OOB = 0x80000000u;  // an offset beyond every range used here
 
 // Sixteen zero bytes in device memory: out-of-range halo units load from
 // here, so a loaded register never needs a select that would force the
@@ -130,7 +142,9 @@ struct HaloArgs {
   int cp_id;
   int identity_mode;
   const int32_t* ag_mask;   // [T][B*GH*GW]
-  unsigned long long* nnz;    // counter block (cf_nnz_release)
+  const unsigned long long* nnz;  // count block of the input (cf_count_read), or null
+  unsigned long long* nz_out;     // count block of the output: workgroups that wrote a
+                                  // nonzero value (cf_count_publish), or null
   int64_t numel;
   double sparse_thr;
   int T, B, Cp, Cout, Coutp, H, W, Ho, Wo, pad;
@@ -143,7 +157,7 @@ struct HaloArgs {
 __device__ __forceinline__ int halo_route(const unsigned long long* nnz, int64_t numel,
                                           double thr) {
   if (!nnz) return CF_ROUTE_DENSE;
-  const unsigned long long k = *nnz;
+  const unsigned long long k = cf_count_read(nnz);
   if (k == 0) return CF_ROUTE_ZERO;
   return (1.0 - (double)k / (double)numel > thr) ? CF_ROUTE_SPARSE : CF_ROUTE_DENSE;
 }
@@ -189,6 +203,7 @@ void conv_halo_kernel(HaloArgs a) {
   static_assert(NT >= 1, "tile too small");
   __shared__ __attribute__((aligned(16))) _Float16 halo[2 * HB];
   __shared__ __attribute__((aligned(16))) float bn_s[2][BM];  // alpha, beta of the tile
+  __shared__ unsigned any_sh[4];  // per-wave votes of the output count
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers
@@ -249,6 +264,7 @@ void conv_halo_kernel(HaloArgs a) {
   const bool full_c = cout0 + BM <= a.Cout;  // every channel of the tile is real
 
   const int route = halo_route(a.nnz, a.numel, a.sparse_thr);
+  uint32_t anyw = 0u;  // OR of the bits of the output values this thread stores
   // Group bits active at time step tt (uniform across the workgroup).
   auto step_mask = [&](int tt) -> uint32_t {
     if (tt >= a.T || route == CF_ROUTE_ZERO) return 0u;
@@ -569,12 +585,33 @@ void conv_halo_kernel(HaloArgs a) {
         }
       }
     }
+    // Lean path: the identity of step t is loaded into idq[t & 1] while step
+    // t - 1 is computed, before that step's stores (zeros without an
+    // identity or beyond the block: an empty range).
+    h4 idq[LEAN ? 2 : 1][NT][4];
+    auto id_load = [&](int t) {
+      const bool have = a.identity_nhwc && t < nsteps;
+      const _Float16* base =
+          have ? a.identity_nhwc + (size_t)((tb0 + t) * a.B + b) * HoWo * a.cp_id : a.identity_nhwc;
+      const __amdgpu_buffer_rsrc_t rid = halo_rsrc(base, have ? (uint32_t)(HoWo * a.cp_id * 2) : 0u);
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          idq[t & 1][nt][r4] = __builtin_bit_cast(
+              h4, __builtin_amdgcn_raw_buffer_load_b64(
+                      rid, (unsigned)((epix[nt] * a.cp_id + col + 8 * r4) * 2), 0, 0));
+    };
+    if constexpr (LEAN) id_load(0);
     auto epi_step = [&](int t) {
       const int tt = tb0 + t;
       const int img = tt * a.B + b;
       _Float16* ostage = obuf + (t % NOBUF) * OSTEP;
       const _Float16* idn = a.identity_nhwc;
       const _Float16* idbase = idn ? idn + (size_t)img * HoWo * a.cp_id : nullptr;
+      if constexpr (LEAN) {
+        if (t + 1 < TB) id_load(t + 1);
+      }
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
         // Registers 4*r4 .. 4*r4+3 hold four consecutive output channels.
@@ -586,8 +623,12 @@ void conv_halo_kernel(HaloArgs a) {
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           h4 idh = {};
-          if (idbase)
-            idh = *reinterpret_cast<const h4*>(idbase + (unsigned)(epix[nt] * a.cp_id + col + 8 * r4));
+          if constexpr (LEAN) {
+            idh = idq[t & 1][nt][r4];
+          } else {
+            if (idbase)
+              idh = *reinterpret_cast<const h4*>(idbase + (unsigned)(epix[nt] * a.cp_id + col + 8 * r4));
+          }
           h4 pk;
           if constexpr (LEAN) {
             // Spikes as halves; identity + spike in packed fp16 (exact: both
@@ -602,6 +643,10 @@ void conv_halo_kernel(HaloArgs a) {
               v[nt][r] = vv;
             }
             pk = idh + sph;
+            if (a.nz_out) {
+              const u32x2 pw = __builtin_bit_cast(u32x2, pk);
+              anyw |= n_ok[nt] ? (pw[0] | pw[1]) : 0u;
+            }
           } else {
             const int ob = ((tt * a.B + b) * a.Cout + col) * HoWo;
 #pragma unroll
@@ -623,6 +668,7 @@ void conv_halo_kernel(HaloArgs a) {
                 else if (ok && a.identity && a.identity_mode == ID_ADD_SPIKE) ov = a.identity[o] + sp;
                 else ov = sp;
               }
+              if (ok && a.nz_out) anyw |= __float_as_uint(ov);
               if (ok && a.out) a.out[o] = ov;
               pk[j] = (_Float16)ov;
             }
@@ -636,27 +682,58 @@ void conv_halo_kernel(HaloArgs a) {
     constexpr int CPI = (BN * CH8 + 255) / 256;
 #pragma unroll
     for (int t = 0; t < TB; ++t) {
-      if (t >= nsteps) break;
+      if (t > 0 && t >= nsteps) break;  // every block has a first step
       if (NOBUF == 1 && t > 0) __syncthreads();  // the previous step's copy-out is complete
       epi_step(t);
       if (a.out_nhwc) {
         __syncthreads();  // the step's tile is staged
         const _Float16* ostage = obuf + (t % NOBUF) * OSTEP;
         _Float16* obase = a.out_nhwc + (size_t)((tb0 + t) * a.B + b) * HoWo * a.cp_out;
+        if constexpr (LEAN) {
+          // every chunk index is below BN * CH8 and every channel real; the
+          // hardware drops pixels outside the output
+          static_assert(BN * CH8 % 256 == 0, "lean copy-out assumes whole passes");
+          const __amdgpu_buffer_rsrc_t ro = halo_rsrc(obase, (uint32_t)(HoWo * a.cp_out * 2));
 #pragma unroll
-        for (int i = 0; i < CPI; ++i) {
-          const int c = opaque(tid) + 256 * i;
-          const int px = c / CH8, part = c % CH8;
-          const int py = px / TW, pxx = px % TW;
-          const int co8 = cout0 + part * 8;
-          if ((c < BN * CH8) & (oh0 + py < a.Ho) & (ow0 + pxx < a.Wo) & (co8 < a.cp_out))
-            *reinterpret_cast<u32x4*>(obase + (unsigned)(((oh0 + py) * a.Wo + ow0 + pxx) * a.cp_out + co8)) =
-                *reinterpret_cast<const u32x4*>(&ostage[px * OLD + part * 8]);
+          for (int i = 0; i < CPI; ++i) {
+            const int c = opaque(tid) + 256 * i;
+            const int px = c / CH8, part = c % CH8;
+            const int py = px / TW, pxx = px % TW;
+            const bool ok = (oh0 + py < a.Ho) & (ow0 + pxx < a.Wo);
+            const uint32_t off =
+                ok ? (uint32_t)((((oh0 + py) * a.Wo + ow0 + pxx) * a.cp_out + cout0 + part * 8) * 2)
+                   : HALO_OOB;
+            __builtin_amdgcn_raw_buffer_store_b128(
+                *reinterpret_cast<const u32x4*>(&ostage[px * OLD + part * 8]), ro, off, 0, 0);
+          }
+        } else {
+#pragma unroll
+          for (int i = 0; i < CPI; ++i) {
+            const int c = opaque(tid) + 256 * i;
+            const int px = c / CH8, part = c % CH8;
+            const int py = px / TW, pxx = px % TW;
+            const int co8 = cout0 + part * 8;
+            if ((c < BN * CH8) & (oh0 + py < a.Ho) & (ow0 + pxx < a.Wo) & (co8 < a.cp_out))
+              *reinterpret_cast<u32x4*>(obase + (unsigned)(((oh0 + py) * a.Wo + ow0 + pxx) * a.cp_out + co8)) =
+                  *reinterpret_cast<const u32x4*>(&ostage[px * OLD + part * 8]);
+          }
         }
       }
     }
     // The block's final membrane potentials (the layer's state after the last block).
-    if (EPI == EPI_LIF && a.v_out) {
+    if (LEAN && a.v_out) {
+      // every channel of a lean tile is real; pixels outside the output are dropped
+      const __amdgpu_buffer_rsrc_t rv =
+          halo_rsrc(a.v_out + (size_t)b * a.Cout * HoWo, (uint32_t)(a.Cout * HoWo * 4));
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dc = 8 * (r >> 2) + (r & 3);
+          const uint32_t off = n_ok[nt] ? (uint32_t)(((col + dc) * HoWo + e_off[nt]) * 4) : HALO_OOB;
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[nt][r]), rv, off, 0, 0);
+        }
+    } else if (EPI == EPI_LIF && a.v_out) {
       float* vbase = a.v_out + (size_t)b * a.Cout * HoWo;
 #pragma unroll
       for (int nt = 0; nt < NT; ++nt) {
@@ -669,7 +746,13 @@ void conv_halo_kernel(HaloArgs a) {
       }
     }
   }
-  cf_nnz_release(a.nnz, gridDim.x);
+  if (a.nz_out) {
+    // magnitude bits only (-0.0 counts as zero): two halves per word on the
+    // lean path, one fp32 value otherwise
+    const uint32_t mag = LEAN ? 0x7fff7fffu : 0x7fffffffu;
+    const bool any = cf_wg_any((anyw & mag) != 0u, any_sh);
+    if (threadIdx.x == 0) cf_count_publish(a.nz_out, any ? 1ull : 0ull, gridDim.x);
+  }
 
 }
 
@@ -714,7 +797,8 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
                         void* out_nhwc, int64_t cp_out,
                         const float* identity, const void* identity_nhwc, int64_t cp_id,
                         int identity_mode, const int32_t* ag_mask,
-                        unsigned long long* nnz, int64_t numel, double sparse_threshold,
+                        const unsigned long long* nnz, unsigned long long* nz_out,
+                        int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
                         int64_t W, int64_t Ho, int64_t Wo, int64_t ksize, int64_t stride,
                         int64_t pad, int64_t tile_h, int64_t tile_w, int64_t group_size,
@@ -745,6 +829,7 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
       4 * B * H * W * Cp > INT32_MAX ||
       B * ((Ho + tile_h - 1) / tile_h) * ((Wo + tile_w - 1) / tile_w) * (Coutp / 64) * 256 > INT32_MAX)
     return (int)hipErrorInvalidValue;
+  // (the grid is below 2^23 workgroups, within a count block's tally)
   // The membrane state passes from one time block to the next through v_out.
   const int tb = (stride == 2 && ksize == 3) ? halo_tb<2, 3>() : halo_tb<1, 3>();
   if (epilogue == EPI_LIF && !v_out && T > tb) return (int)hipErrorInvalidValue;
@@ -756,7 +841,7 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
   a.identity_mode = identity_mode; a.ag_mask = ag_mask;
   // Without masks the SparseFlow route cannot be taken: pass the count only
   // when masks exist (StaticZero is still detected through nnz == 0 below).
-  a.nnz = nnz; a.numel = numel;
+  a.nnz = nnz; a.nz_out = nz_out; a.numel = numel;
   a.sparse_thr = ag_mask ? sparse_threshold : 2.0;  // 2.0: sparsity never exceeds it
   a.T = (int)T; a.B = (int)B; a.Cp = (int)Cp; a.Cout = (int)Cout; a.Coutp = (int)Coutp;
   a.H = (int)H; a.W = (int)W; a.Ho = (int)Ho; a.Wo = (int)Wo; a.pad = (int)pad;

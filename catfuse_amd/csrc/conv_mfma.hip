@@ -61,7 +61,9 @@ struct ConvArgs {
   int cp_id;
   int identity_mode;
   const int32_t* ag_mask;
-  unsigned long long* nnz;    // counter block (cf_nnz_release)
+  const unsigned long long* nnz;  // count block of the input (cf_count_read), or null
+  unsigned long long* nz_out;     // count block of the output: workgroups that wrote a
+                                  // nonzero value (cf_count_publish), or null
   int64_t numel;
   double sparse_thr;
   int T, B, Cp, Cout, Coutp, H, W, Ho, Wo, KH, KW, stride, pad;
@@ -75,7 +77,7 @@ struct ConvArgs {
 __device__ __forceinline__ int device_route(const unsigned long long* nnz, int64_t numel,
                                             double thr) {
   if (!nnz) return CF_ROUTE_DENSE;
-  const unsigned long long k = *nnz;
+  const unsigned long long k = cf_count_read(nnz);
   if (k == 0) return CF_ROUTE_ZERO;
   return (1.0 - (double)k / (double)numel > thr) ? CF_ROUTE_SPARSE : CF_ROUTE_DENSE;
 }
@@ -224,6 +226,7 @@ __global__ __launch_bounds__(256, (conv_min_blocks<BM, BN, EPI>())) void conv_mf
 
   const int route = device_route(a.nnz, a.numel, a.sparse_thr);
   const int ntiles_t = a.n_ptiles;
+  uint32_t anyw = 0u;  // OR of the bits of every output value this thread writes
 
   for (int t = 0; t < a.T; ++t) {
     int nact;
@@ -309,6 +312,7 @@ __global__ __launch_bounds__(256, (conv_min_blocks<BM, BN, EPI>())) void conv_mf
             else
               ov = (a.identity && a.identity_mode == ID_ADD_SPIKE) ? a.identity[o] + sp : sp;
           }
+          anyw |= __float_as_uint(ov);
           if (a.out) a.out[o] = ov;
           if (a.out_nhwc)
             store_nhwc(a.out_nhwc, a.cp_out, (size_t)t * a.B + e_img[nb], HoWo, e_off[nb], co, ov);
@@ -328,7 +332,12 @@ __global__ __launch_bounds__(256, (conv_min_blocks<BM, BN, EPI>())) void conv_mf
             a.v_out[((size_t)e_img[nb] * a.Cout + co) * HoWo + e_off[nb]] = v[mb][nb][r];
         }
   }
-  cf_nnz_release(a.nnz, gridDim.x * gridDim.y);
+  if (a.nz_out) {
+    // magnitude bits only: -0.0 counts as zero
+    __shared__ unsigned any_sh[4];
+    const bool any = cf_wg_any((anyw & 0x7fffffffu) != 0u, any_sh);
+    if (tid == 0) cf_count_publish(a.nz_out, any ? 1ull : 0ull, gridDim.x * gridDim.y);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -423,7 +432,8 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
                         void* out_nhwc, int64_t cp_out,
                         const float* identity, const void* identity_nhwc, int64_t cp_id,
                         int identity_mode, const int32_t* ag_mask,
-                        unsigned long long* nnz, int64_t numel, double sparse_threshold,
+                        const unsigned long long* nnz, unsigned long long* nz_out,
+                        int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
                         int64_t W, int64_t Ho, int64_t Wo, int64_t ksize, int64_t stride,
                         int64_t pad, int64_t tile_h, int64_t tile_w, int64_t group_size,
@@ -435,7 +445,8 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
                         void* out_nhwc, int64_t cp_out,
                         const float* identity, const void* identity_nhwc, int64_t cp_id,
                         int identity_mode, const int32_t* ag_mask,
-                        unsigned long long* nnz, int64_t numel, double sparse_threshold,
+                        const unsigned long long* nnz, unsigned long long* nz_out,
+                        int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
                         int64_t W, int64_t Ho, int64_t Wo, int64_t KH, int64_t KW, int64_t stride,
                         int64_t pad, int64_t x_img_tstride, int64_t tile_h, int64_t tile_w,
@@ -469,7 +480,7 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
     const int64_t th = 8, tw = rect ? tile_w : 8;
     return cf_conv_halo(x, w_packed, alpha, beta, v_in, v_out, out, out_nhwc, cp_out, identity,
                         identity_nhwc, cp_id, identity_mode,
-                        rect ? ag_mask : nullptr, nnz, numel, sparse_threshold, T, B, Cp, Cout,
+                        rect ? ag_mask : nullptr, nnz, nz_out, numel, sparse_threshold, T, B, Cp, Cout,
                         Coutp, H, W, Ho, Wo, KH, stride, pad, th, tw, rect ? group_size : 0,
                         epilogue, tau, v_th, v_reset, hard_reset, decay_input, stream);
   }
@@ -487,7 +498,7 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
   a.w = (const _Float16*)w_packed;
   a.alpha = alpha; a.beta = beta; a.v_in = v_in; a.v_out = v_out; a.out = out;
   a.out_nhwc = (_Float16*)out_nhwc; a.cp_out = (int)cp_out;
-  a.identity = identity; a.identity_mode = identity_mode; a.ag_mask = ag_mask; a.nnz = nnz; a.numel = numel;
+  a.identity = identity; a.identity_mode = identity_mode; a.ag_mask = ag_mask; a.nnz = nnz; a.nz_out = nz_out; a.numel = numel;
   a.identity_nhwc = (const _Float16*)identity_nhwc; a.cp_id = (int)cp_id;
   a.sparse_thr = sparse_threshold;
   a.T = (int)T; a.B = (int)B; a.Cp = (int)Cp; a.Cout = (int)Cout; a.Coutp = (int)Coutp;
@@ -508,6 +519,8 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
     BNsel = 128;
     n_ptiles = (int)((B * Ho * Wo + BNsel - 1) / BNsel);
   }
+  if (nz_out && (unsigned long long)n_ptiles * (Coutp / 64) >= CF_MAX_COUNT_WG)
+    return (int)hipErrorInvalidValue;
   a.n_ptiles = n_ptiles;
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;

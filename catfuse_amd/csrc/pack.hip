@@ -5,7 +5,7 @@
 //   xp   fp16 NHWC x[NB][H][W][Cp] (channels C..Cp-1 zero) — MFMA B operand
 //   act  uint32 [NB][H][W]: bit g set iff |x[c]| > thr for some c in
 //        channel group g (channels g*GS .. g*GS+GS-1)
-//   nnz  += count_nonzero(x)   (64-bit device counter)
+//   nnz  count_nonzero(x), published in a count block (cf_count_publish)
 //   status |= CF_STATUS_INEXACT_FP16 if some x is not exactly representable
 //        in fp16 (the MFMA path multiplies fp16 x by split fp32 weights, so
 //        exactness of x is what keeps the contraction fp32-faithful)
@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void pack_kernel(
   if (myinexact) atomicOr(&inexact_sh, 1u);
   __syncthreads();
   if (tid == 0) {
-    if (nnz && cnt_sh) atomicAdd(nnz, (unsigned long long)cnt_sh);
+    if (nnz) cf_count_publish(nnz, cnt_sh, gridDim.x * gridDim.y);
     if (status && inexact_sh) atomicOr(status, (uint32_t)CF_STATUS_INEXACT_FP16);
   }
 }
@@ -94,8 +94,8 @@ __global__ __launch_bounds__(256) void pack_kernel(
 // pixel's channels are one contiguous run, so a 16-lane group reads 256
 // contiguous bytes per load); group sizes are multiples of 8, so the 8
 // channels of a chunk share one group, and the pixel's bits are OR-reduced
-// over its 16 lanes.  Grid-stride over pixels; one atomic per block for the
-// count.
+// over its 16 lanes.  Grid-stride over pixels; the count is published with
+// one atomic per block.
 __global__ __launch_bounds__(256) void scan_nhwc_kernel(
     const _Float16* __restrict__ xp, int64_t npix, int Cp, int C, uint32_t* __restrict__ act,
     int gs, float thr, unsigned long long* __restrict__ nnz) {
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(256) void scan_nhwc_kernel(
     for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
     if ((tid & 63) == 0) atomicAdd(&cnt_sh, cnt);
     __syncthreads();
-    if (tid == 0 && cnt_sh) atomicAdd(nnz, (unsigned long long)cnt_sh);
+    if (tid == 0) cf_count_publish(nnz, cnt_sh, gridDim.x);
   }
 }
 
@@ -171,7 +171,7 @@ __global__ __launch_bounds__(256) void nhwc_to_nchw_kernel(
 __global__ void route_kernel(const unsigned long long* __restrict__ nnz, int64_t numel,
                              double sparse_threshold, int32_t* __restrict__ route) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
-    const unsigned long long k = *nnz;
+    const unsigned long long k = cf_count_read(nnz);
     int r;
     if (k == 0) r = CF_ROUTE_ZERO;
     else if (1.0 - (double)k / (double)numel > sparse_threshold) r = CF_ROUTE_SPARSE;
@@ -196,6 +196,7 @@ CF_API int cf_pack_input(const float* x, int64_t NB, int64_t C, int64_t H, int64
   if (NB > 65535) return (int)hipErrorInvalidValue;
   const int64_t HW = H * W;
   dim3 grid(cf_blocks(HW, PX), (unsigned)NB);
+  if (nnz && (unsigned long long)grid.x * grid.y >= CF_MAX_COUNT_WG) return (int)hipErrorInvalidValue;
   hipLaunchKernelGGL(pack_kernel, grid, dim3(256), 0, (hipStream_t)stream, x, C, HW, Cp,
                      (_Float16*)xp, act, group_size, threshold, nnz, status);
   return (int)hipGetLastError();

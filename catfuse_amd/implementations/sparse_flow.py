@@ -60,8 +60,7 @@ class SparseFlow(HipConvImplementation):
         r = self._runner
         if r is None or getattr(r, "last_nnz", None) is None:
             return -1
-        numel = r._ws["xp"].shape[0] * r._ws["xp"].shape[1] * r._ws["xp"].shape[2] * r.Cin
-        word = runtime.route_from_nnz(r.last_nnz, numel, self.sparsity_threshold)
+        word = runtime.route_from_nnz(r.last_nnz, r.last_numel, self.sparsity_threshold)
         return int(word.item())
 
     def last_tiles(self):

@@ -281,11 +281,47 @@ def shadow_of(x: torch.Tensor, shape) -> Optional[torch.Tensor]:
     return t
 
 
+def count_block(device) -> torch.Tensor:
+    """A count block (two int64): [0] the accumulator of a producer pass, zero
+    between passes; [1] the count the last completed pass published.  The
+    producer kernels (cf_pack_input, cf_scan_nhwc, a fused conv writing its
+    output) clear [0] themselves, so a block is zeroed once, here."""
+    return torch.zeros(2, dtype=torch.int64, device=device)
+
+
+def _require_block(blk: Optional[torch.Tensor]) -> None:
+    if blk is not None and (blk.dtype != torch.int64 or blk.numel() < 2
+                            or not blk.is_contiguous() or not blk.is_cuda):
+        raise ValueError("a count block is a contiguous int64 GPU tensor of two elements")
+
+
+def attach_count(out: torch.Tensor, blk: torch.Tensor, gen_cell: list) -> None:
+    """Record the count block a fused conv published for its output (the
+    number of its workgroups that wrote a nonzero value: zero iff the output
+    is all zero).  gen_cell is the producing layer's call counter: a later
+    call of the same layer republishes the block, which then no longer
+    describes this output."""
+    out._cf_count = (blk, gen_cell, gen_cell[0], out._version)
+
+
+def count_of(x: torch.Tensor) -> Optional[torch.Tensor]:
+    """The count block describing x's current values, or None."""
+    c = getattr(x, "_cf_count", None)
+    if c is None:
+        return None
+    blk, cell, gen, ver = c
+    if ver != x._version or cell[0] != gen or blk.device != x.device:
+        return None
+    return blk
+
+
 def pack_input(x4: torch.Tensor, *, cp: Optional[int] = None, want_xp=True, group_size=0,
                threshold=1e-6, nnz: Optional[torch.Tensor] = None, act_out=None, xp_out=None,
                status: Optional[torch.Tensor] = None):
-    """x4 [NB, C, H, W] fp32 -> (xp fp16 [NB, H, W, Cp] | None, act int32 [NB, H, W] | None)."""
+    """x4 [NB, C, H, W] fp32 -> (xp fp16 [NB, H, W, Cp] | None, act int32 [NB, H, W] | None);
+    count_nonzero(x4) is published in the count block nnz (count_block) when given."""
     require_gpu_tensor(x4, "x")
+    _require_block(nnz)
     NB, C, H, W = x4.shape
     cp = pad32(C) if cp is None else cp
     xp = None
@@ -310,8 +346,10 @@ def pack_input(x4: torch.Tensor, *, cp: Optional[int] = None, want_xp=True, grou
 def scan_nhwc(xp: torch.Tensor, C: int, *, group_size: int, threshold=1e-6,
               nnz: Optional[torch.Tensor] = None, act_out=None):
     """xp fp16 NHWC [NB, H, W, Cp] (a fused conv's output copy) -> act int32
-    [NB, H, W] with cf_pack_input's bits, and the nonzero count into nnz."""
+    [NB, H, W] with cf_pack_input's bits; the nonzero count is published in
+    the count block nnz when given."""
     require_gpu_tensor(xp, "xp", dtype=torch.float16)
+    _require_block(nnz)
     NB, H, W, cp = xp.shape
     act = act_out if act_out is not None else torch.empty((NB, H, W), dtype=torch.int32,
                                                           device=xp.device)
@@ -350,6 +388,8 @@ def zero_counter(c: torch.Tensor) -> None:
 
 def route_from_nnz(nnz: torch.Tensor, numel: int, sparse_threshold: float,
                    out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Route word (int32 device tensor) from the count block nnz."""
+    _require_block(nnz)
     r = out if out is not None else torch.empty(1, dtype=torch.int32, device=nnz.device)
     check(_hip.lib().cf_route_from_nnz(ptr(nnz), int(numel), float(sparse_threshold), ptr(r),
                                        _hip.stream(nnz.device)), "cf_route_from_nnz")
@@ -384,6 +424,7 @@ class ConvLIFRunner:
         self.w_packed = self.alpha = self.beta = None
         self.alpha_direct = self.beta_direct = None
         self._ws = {}
+        self._gen = [0]  # calls that published the output count block
 
     def refresh(self):
         self._packed_key = None
@@ -438,13 +479,22 @@ class ConvLIFRunner:
         return t
 
     def counter(self, device):
-        """The layer's nonzero-count block (3 x u64: count, completion tally,
-        last count).  Zeroed once when created; afterwards the conv that
-        consumes the count leaves it cleared for the next producer pass."""
+        """Count block of the layer's input when the layer counts it itself
+        (cf_pack_input / cf_scan_nhwc publish into it; see count_block)."""
         t = self._ws.get("nnz")
         if t is None or t.device != device:
-            t = torch.zeros((3,), dtype=torch.int64, device=device)
+            t = count_block(device)
             self._ws["nnz"] = t
+        return t
+
+    def out_counter(self, device):
+        """Count block the conv publishes for its output (workgroups that wrote
+        a nonzero value), read by the next fused layer to take the StaticZero
+        route without a counting pass."""
+        t = self._ws.get("nz_out")
+        if t is None or t.device != device:
+            t = count_block(device)
+            self._ws["nz_out"] = t
         return t
 
     def run_mfma(self, x: torch.Tensor, v_in=None, *, epilogue=EPI_LIF, want_v_out=True,
@@ -456,7 +506,9 @@ class ConvLIFRunner:
         fp16 NHWC copy (written by the producing fused conv) the pack pass is
         skipped: a SparseFlow layer scans the copy for its activity bits and
         count, a dense one takes the dense route; with emit_nhwc the output
-        carries its own copy for the next layer.  Returns (out, v_out)."""
+        carries its own copy for the next layer, and the count block of its
+        output (attach_count): a dense layer whose input carries one takes
+        the StaticZero route on an all-zero input.  Returns (out, v_out)."""
         require_gpu_tensor(x, "x")
         T, B, C, H, W = x.shape
         if C != self.Cin:
@@ -473,7 +525,11 @@ class ConvLIFRunner:
             nnz = self.counter(dev)
             act = scan_nhwc(xp, C, group_size=gs, nnz=nnz,
                             act_out=self.workspace("act", (T * B, H, W), torch.int32, dev))
-        elif xp is None:
+        elif xp is not None:
+            # dense route on an NHWC input: the producer's count block (if it
+            # still describes x) enables StaticZero
+            nnz = count_of(x) if static_zero else None
+        else:
             st = status_word(dev)
             if static_zero or sparse is not None:
                 nnz = self.counter(dev)
@@ -513,10 +569,14 @@ class ConvLIFRunner:
         cp_out = pad32(self.Cout)
         nhwc = (torch.empty((T * B, Ho, Wo, cp_out), dtype=torch.float16, device=dev)
                 if (emit_nhwc and epilogue == EPI_LIF) else None)
+        nz_out = None
         if nhwc is not None:
             # spikes: written as the NHWC copy only; fp32 on first outside read
             out = lazy_output((T, B, self.Cout, Ho, Wo), nhwc, dev)
             out_ptr = None
+            nz_out = self.out_counter(dev)
+            self._gen[0] += 1
+            attach_count(out, nz_out, self._gen)
         else:
             out = torch.empty((T, B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
             out_ptr = ptr(out)
@@ -524,7 +584,7 @@ class ConvLIFRunner:
         rc = _hip.lib().cf_conv_mfma(
             ptr(xp), ptr(self.w_packed), ptr(self.alpha), ptr(self.beta), ptr(v_in), ptr(v_out),
             out_ptr, ptr(nhwc), cp_out, None if id_nhwc is not None else ptr(identity),
-            ptr(id_nhwc), pad32(self.Cout), int(identity_mode), ptr(ag), ptr(nnz),
+            ptr(id_nhwc), pad32(self.Cout), int(identity_mode), ptr(ag), ptr(nnz), ptr(nz_out),
             x.numel(),
             float(sparse_threshold), T, B, self.Cp, self.Cout, self.Coutp, H, W, Ho, Wo, self.KH,
             self.KW, self.stride, self.padding, B, th, tw, gs, int(epilogue), *self.lif,
@@ -532,7 +592,8 @@ class ConvLIFRunner:
         check(rc, "cf_conv_mfma")
         _t1("conv_mfma" + ("_sparse" if sparse is not None else ""), ev,
             flops=2 * T * B * Ho * Wo * self.Cout * self.Cin * self.KH * self.KW)
-        self.last_nnz = None if nnz is None else nnz[2:3]  # the count of this input
+        self.last_nnz = nnz  # count block of this input (None: not counted)
+        self.last_numel = x.numel()
         self.last_tiles = None if ag is None else (tc_buf, ag)
         return out, (v_out if want_v_out else None)
 

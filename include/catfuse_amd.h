@@ -32,6 +32,17 @@ extern "C" {
 #define CF_ROUTE_SPARSE 1 /* SparseFlow: 1 - nnz/numel > threshold      */
 #define CF_ROUTE_DENSE 2  /* DenseKeep                                  */
 
+/* Count blocks: two uint64 in device memory, [0] the accumulator of a
+ * producer pass (zero between passes), [1] the count the last completed pass
+ * published.  Producer passes (cf_pack_input, cf_scan_nhwc, and cf_conv_mfma /
+ * cf_conv_halo through nz_out) add into [0] with one atomic per workgroup; the
+ * workgroup that completes the pass stores the total in [1] and clears [0].
+ * The owner zeroes a block once; passes publishing into one block must not
+ * overlap (stream order).  Readers (the routing of cf_conv_mfma / cf_conv_halo,
+ * cf_route_from_nnz) read [1] in later launches.  Replaces the host-side
+ * count_nonzero(x).item() of
+ * catfuse/sparseflow/ops/st_fusion_conv_bn_lif.py:512-514. */
+
 /* Status bits OR-ed into the device status word by cf_pack_input. */
 #define CF_STATUS_INEXACT_FP16 1u
 
@@ -69,7 +80,8 @@ int cf_avgpool2x2_lif(const float* x, const float* v_in, void* spike, int spike_
  * (xp: [NB][H][W][Cp], Cp % 32 == 0, nullable), per-pixel channel-group
  * activity bits (act: uint32 [NB][H][W], bit g <=> some |x| > threshold in
  * channels [g*group_size, (g+1)*group_size), nullable), nonzero count
- * (nnz += count_nonzero(x), nullable) and exactness status (nullable).
+ * (count_nonzero(x) published in the count block nnz, nullable; see
+ * "Count blocks" below) and exactness status (nullable).
  * Replaces the channel half of catfuse/sparseflow/prescan.py:32-54,153-189
  * and the count_nonzero of
  * catfuse/sparseflow/ops/st_fusion_conv_bn_lif.py:512-514. */
@@ -96,8 +108,8 @@ int cf_scan_nhwc(const void* xp, int64_t NB, int64_t H, int64_t W, int64_t Cp, i
 int cf_nhwc_to_nchw(const void* xp, float* out, int64_t NB, int64_t C, int64_t H, int64_t W,
                     int64_t cp, void* stream);
 
-/* route = ZERO if nnz == 0, SPARSE if 1 - nnz/numel > sparse_threshold (in
- * double), else DENSE.  Replaces the host decision at
+/* route = ZERO if the count block's published count k (nnz[1]) is 0, SPARSE
+ * if 1 - k/numel > sparse_threshold (in double), else DENSE.  Replaces the host decision at
  * catfuse/sparseflow/ops/st_fusion_conv_bn_lif.py:510-524. */
 int cf_route_from_nnz(const unsigned long long* nnz, int64_t numel, double sparse_threshold,
                       int32_t* route, void* stream);
@@ -149,12 +161,15 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
  *   tile_h/tile_w > 0 selects rectangular pixel tiles aligned with the
  *   prescan tiles (tile_h*tile_w in {64,128}) and enables SparseFlow chunk
  *   skipping from ag_mask ([T][B*GH*GW]) when nnz is non-NULL; tile_h = 0
- *   selects flat pixel tiles (dense).  nnz (nullable) is a block of three
- *   u64: [0] the input's nonzero count (accumulated by cf_pack_input /
- *   cf_scan_nhwc), [1] a completion tally that must be 0 at launch, [2]
- *   receives the count; the launch's last workgroup clears [0] and [1], so
- *   the next producer pass needs no clearing launch.  nnz non-NULL also enables the
- *   StaticZero route.  All routes give bit-identical results.
+ *   selects flat pixel tiles (dense).  nnz (nullable, read only) is the
+ *   count block of the input: its published count k (exact, from
+ *   cf_pack_input / cf_scan_nhwc, or the producing conv's nz_out) routes
+ *   the launch: k == 0 StaticZero (no K loop), SparseFlow when ag_mask is
+ *   given and 1 - k/numel > sparse_threshold, dense otherwise.  nz_out
+ *   (nullable) is the count block the launch publishes for its output: the
+ *   number of workgroups that stored a nonzero value (0 iff the output is
+ *   all zero), so the next fused conv can route on it without a counting
+ *   pass.  All routes give bit-identical results.
  * Replaces catfuse/implementations/dense_keep.py:97-155 (DenseKeep.forward),
  * catfuse/implementations/sparse_flow.py:186-270 (SparseFlow.forward ->
  * catfuse/sparseflow/streamfuse_kernel.py:32-187), and
@@ -162,10 +177,9 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
 int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha, const float* beta,
                  const float* v_in, float* v_out, float* out, void* out_nhwc, int64_t cp_out,
                  const float* identity, const void* identity_nhwc, int64_t cp_id,
-                 int identity_mode, const int32_t* ag_mask, unsigned long long* nnz,
-                 int64_t numel, double sparse_threshold, int64_t T, int64_t B, int64_t Cp,
-                 int64_t Cout,
-                 int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo, int64_t KH,
+                 int identity_mode, const int32_t* ag_mask, const unsigned long long* nnz,
+                 unsigned long long* nz_out, int64_t numel, double sparse_threshold, int64_t T,
+                 int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo, int64_t KH,
                  int64_t KW, int64_t stride, int64_t pad, int64_t x_img_tstride, int64_t tile_h,
                  int64_t tile_w, int64_t group_size, int epilogue, double tau, double v_th,
                  double v_reset, int hard_reset, int decay_input, void* stream);
@@ -181,9 +195,9 @@ int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha, const 
 int cf_conv_halo(const void* x, const void* w_packed, const float* alpha, const float* beta,
                  const float* v_in, float* v_out, float* out, void* out_nhwc, int64_t cp_out,
                  const float* identity, const void* identity_nhwc, int64_t cp_id,
-                 int identity_mode, const int32_t* ag_mask, unsigned long long* nnz,
-                 int64_t numel, double sparse_threshold, int64_t T, int64_t B, int64_t Cp,
-                 int64_t Cout, int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
+                 int identity_mode, const int32_t* ag_mask, const unsigned long long* nnz,
+                 unsigned long long* nz_out, int64_t numel, double sparse_threshold, int64_t T,
+                 int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
                  int64_t ksize, int64_t stride, int64_t pad, int64_t tile_h, int64_t tile_w,
                  int64_t group_size, int epilogue, double tau, double v_th, double v_reset,
                  int hard_reset, int decay_input, void* stream);

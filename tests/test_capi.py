@@ -56,15 +56,15 @@ def test_host_side_argument_validation():
     assert L.cf_lif_multistep(1, None, None, None, 1, None, 1, 0, None, 4, 16, 1, 1,
                               2.0, 1.0, 0.0, 1, 1, None) == INVALID
     # conv: Cp not a multiple of 32
-    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, 0, 0.7,
+    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, None, 0, 0.7,
                           4, 2, 48, 64, 64, 8, 8, 8, 8, 3, 3, 1, 1, 2, 0, 0, 0,
                           0, 2.0, 1.0, 0.0, 1, 1, None) == INVALID
     # conv: inconsistent output size
-    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, 0, 0.7,
+    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, None, 0, 0.7,
                           4, 2, 64, 64, 64, 8, 8, 7, 8, 3, 3, 1, 1, 2, 0, 0, 0,
                           0, 2.0, 1.0, 0.0, 1, 1, None) == INVALID
     # conv: rect tile must hold 64 or 128 pixels
-    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, 0, 0.7,
+    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, None, 0, 0.7,
                           4, 2, 64, 64, 64, 8, 8, 8, 8, 3, 3, 1, 1, 2, 4, 4, 16,
                           0, 2.0, 1.0, 0.0, 1, 1, None) == INVALID
     # prescan: more than 32 groups

@@ -132,14 +132,15 @@ def test_pack_prescan_bit_exact(cuda, shape, rate):
     gs = oracle.choose_group_size(C)
     G = -(-C // gs)
     xd = x.to(cuda)
-    nnz = torch.zeros(1, dtype=torch.int64, device=cuda)
+    nnz = runtime.count_block(cuda)
     st = torch.zeros(1, dtype=torch.int32, device=cuda)
     xp, act = runtime.pack_input(xd, group_size=gs, nnz=nnz, status=st)
     tc, ag = runtime.prescan_tiles(act, H, W, Ho, Wo, k, s, p, bh, bw, G)
     tc_ref, ag_ref = oracle.prescan2d(x, Ho, Wo, k, s, p, bh, bw, gs)
     np.testing.assert_array_equal(ag.cpu().numpy(), ag_ref)
     np.testing.assert_array_equal(tc.cpu().numpy(), tc_ref)
-    assert int(nnz.item()) == int(np.count_nonzero(x.numpy()))
+    assert int(nnz[1].item()) == int(np.count_nonzero(x.numpy()))
+    assert int(nnz[0].item()) == 0  # the pass left its accumulator cleared
     assert int(st.item()) == 0
     cp = runtime.pad32(C)
     ref_xp = torch.zeros(N, H, W, cp, dtype=torch.float16)
@@ -234,6 +235,58 @@ def test_conv_bn_lif_mfma_parity(cuda, case):
     zr = oracle.batch_norm(oracle.conv2d(x.flatten(0, 1), conv.weight, None, s, p), bn)
     np.testing.assert_allclose(z.cpu().numpy().reshape(zr.shape), zr.numpy(), rtol=2e-5,
                                atol=2e-5)
+
+
+OUTPUT_COUNT_CASES = [
+    # name, Cin, Cmid, Cout, k1, k2, s2, p2, H, producer SparseFlow tile width
+    ("halo", 64, 64, 64, 3, 3, 1, 1, 16, 0),
+    ("halo_s2", 32, 64, 128, 3, 3, 2, 1, 16, 0),
+    ("ds", 32, 64, 128, 3, 1, 2, 0, 16, 0),
+    ("flat", 32, 64, 64, 5, 5, 1, 2, 12, 0),
+    ("tile8x16", 32, 64, 64, 3, 3, 1, 1, 56, 16),
+]
+
+
+@pytest.mark.parametrize("case", OUTPUT_COUNT_CASES, ids=[c[0] for c in OUTPUT_COUNT_CASES])
+def test_output_count_routes_next_layer(cuda, case):
+    """A fused conv publishes a count block for its output (zero iff every
+    output value is zero); the next fused conv reads it from its input and
+    takes the StaticZero route on an all-zero input, bit-identical to the
+    dense route.  A later call of the producer invalidates the block for the
+    earlier output."""
+    from catfuse_amd import runtime
+    name, Cin, Cmid, Cout, k1, k2, s2, p2, H, tw1 = case
+    T, B = 4, 2
+    conv1, bn1, lif1 = _layer(Cin, Cmid, k1, 1, k1 // 2, seed=61)
+    conv2, bn2, lif2 = _layer(Cmid, Cout, k2, s2, p2, seed=62)
+    r1 = _runner(conv1, bn1, lif1, cuda)
+    r2 = _runner(conv2, bn2, lif2, cuda)
+    sp1 = dict(block_h=8, block_w=tw1, group_size=16) if tw1 else None
+    g = _gen(63)
+    seen_zero = seen_nonzero = False
+    for rate in (0.0, 0.4, 0.0, 0.02):
+        x = (torch.rand(T, B, Cin, H, H, generator=g) < rate).float().to(cuda)
+        y1, _ = r1.run_mfma(x, sparse=sp1)
+        blk = runtime.count_of(y1)
+        assert blk is not None
+        n1 = int(blk[1].item())
+        assert int(blk[0].item()) == 0
+        dense_y1 = y1.clone()  # the fp32 values, as a plain tensor
+        all_zero = int(torch.count_nonzero(dense_y1)) == 0
+        assert (n1 == 0) == all_zero, f"{name} rate {rate}: count {n1}"
+        seen_zero |= all_zero
+        seen_nonzero |= not all_zero
+        y2, v2 = r2.run_mfma(y1)
+        assert r2.last_nnz is blk
+        y2d, v2d = r2.run_mfma(y1, static_zero=False)
+        assert r2.last_nnz is None
+        assert torch.equal(y2, y2d) and torch.equal(v2, v2d), f"{name} rate {rate}"
+        y2p, v2p = r2.run_mfma(dense_y1)  # plain fp32 input: counted by the pack pass
+        assert torch.equal(y2p, y2d) and torch.equal(v2p, v2d)
+    assert seen_zero and seen_nonzero
+    ya, _ = r1.run_mfma(x, sparse=sp1)
+    yb, _ = r1.run_mfma(x, sparse=sp1)
+    assert runtime.count_of(ya) is None and runtime.count_of(yb) is not None
 
 
 @pytest.mark.parametrize("rate", [0.0, 0.01, 0.05, 0.2, 0.5])
@@ -423,13 +476,15 @@ def test_scan_nhwc_matches_pack(cuda, C, gs):
     x += (torch.rand(x.shape, generator=g) < 0.05).float()
     x[0, 0, 0, 0] = 2.0 ** -21  # below the 1e-6 activity threshold, still nonzero
     xd = x.to(cuda)
-    n1 = torch.zeros(1, dtype=torch.int64, device=cuda)
-    n2 = torch.zeros(1, dtype=torch.int64, device=cuda)
-    xp, act = runtime.pack_input(xd, cp=runtime.pad32(C), group_size=gs, nnz=n1)
-    act2 = runtime.scan_nhwc(xp, C, group_size=gs, nnz=n2)
-    torch.cuda.synchronize()
-    assert torch.equal(act, act2)
-    assert int(n1.item()) == int(n2.item()) == int((x != 0).sum())
+    n1 = runtime.count_block(cuda)
+    n2 = runtime.count_block(cuda)
+    for _ in range(2):  # a second pass republishes the same count
+        xp, act = runtime.pack_input(xd, cp=runtime.pad32(C), group_size=gs, nnz=n1)
+        act2 = runtime.scan_nhwc(xp, C, group_size=gs, nnz=n2)
+        torch.cuda.synchronize()
+        assert torch.equal(act, act2)
+        assert int(n1[1].item()) == int(n2[1].item()) == int((x != 0).sum())
+        assert int(n1[0].item()) == int(n2[0].item()) == 0
 
 
 def test_sparseflow_on_nhwc_copy_bitwise(cuda):

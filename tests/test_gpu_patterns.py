@@ -89,8 +89,9 @@ def test_stem_maxpool_pattern_direct_and_fallback(cuda):
 
 
 def test_route_counter_clears_between_calls(cuda):
-    # the nonzero count is cleared by the conv that consumes it: a sequence of
-    # calls with different sparsity must route each input on its own count,
+    # each counting pass publishes its count and leaves its accumulator
+    # cleared: a sequence of calls with different sparsity must route each
+    # input on its own count,
     # both from an fp32 input (pack pass) and from a fused layer's NHWC copy
     # (scan pass)
     from catfuse_amd.patterns import STFusionConvBNLIF
