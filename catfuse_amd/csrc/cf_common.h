@@ -122,28 +122,46 @@ __device__ __forceinline__ float lif_initial_v(const LifParams& p) {
 }
 
 // Count block of a producer pass (cf_pack_input, cf_scan_nhwc, a fused conv
-// writing its output): two u64,
-//   [0] the pass accumulator, (sum of workgroup counts) << CF_TALLY_BITS |
-//       completed workgroups; zero between passes;
+// writing its output): CF_COUNT_BLOCK_WORDS u64,
+//   [0] the pass accumulator, (sum of counts) << CF_TALLY_BITS | completed
+//       groups; zero between passes;
 //   [1] the count of the last completed pass, read by the kernels that
-//       consume the pass's output (later in stream order).
-// Each workgroup adds its count and its completion with one atomic; the
-// workgroup that completes the pass (tally nwg - 1) stores the total in [1]
-// and clears [0], so the next pass starts from zero with no clearing launch.
-// One atomic carries both the count and the completion, so nothing orders
-// two updates and no fence is needed (an agent-scope release fence would
-// write back the L2 of the workgroup's XCD); the kernel boundary orders the
-// stores before the readers.  A pass has fewer than 2^24 workgroups (the
-// launchers check) and counts below 2^40.
+//       consume the pass's output (later in stream order);
+//   [16 * (g + 1)] the accumulator of workgroup group g (workgroups whose
+//       linear index is g modulo CF_COUNT_GROUPS), same packing, zero
+//       between passes; each on a 128-byte line of its own.
+// A workgroup adds its count and its completion to its group word with one
+// atomic; the workgroup that completes its group adds the group's total and
+// one group completion to [0] and clears the group word; the one that
+// completes [0] stores the pass total in [1] and clears [0].  So the next
+// pass starts from zero with no clearing launch, one atomic carries each
+// count together with its completion (nothing orders two updates, so no
+// fence is needed; an agent-scope release fence would write back the L2 of
+// the workgroup's XCD), and the same-address atomics of a pass are spread
+// over CF_COUNT_GROUPS words (at ~10 ns per same-address atomic, a single
+// word costs ~10 us for a thousand workgroups finishing together).  A pass
+// has fewer than 2^24 workgroups (the launchers check) and counts below 2^40.
 constexpr int CF_TALLY_BITS = 24;
 constexpr unsigned long long CF_MAX_COUNT_WG = 1ull << CF_TALLY_BITS;
+constexpr unsigned CF_COUNT_GROUPS = 16;
+constexpr unsigned CF_COUNT_BLOCK_WORDS = 16 * (CF_COUNT_GROUPS + 1);
 
-// Called by one thread of every workgroup of the pass, once its count is final.
+// Called by one thread of every workgroup of the pass, once its count is
+// final; wg is the workgroup's linear index, nwg the pass's workgroup count.
 __device__ __forceinline__ void cf_count_publish(unsigned long long* blk, unsigned long long cnt,
-                                                 unsigned nwg) {
-  const unsigned long long prev = atomicAdd(&blk[0], (cnt << CF_TALLY_BITS) | 1ull);
-  if ((prev & (CF_MAX_COUNT_WG - 1ull)) == (unsigned long long)nwg - 1ull) {
-    blk[1] = (prev >> CF_TALLY_BITS) + cnt;
+                                                 unsigned wg, unsigned nwg) {
+  constexpr unsigned long long TALLY = CF_MAX_COUNT_WG - 1ull;
+  const unsigned g = wg % CF_COUNT_GROUPS;
+  const unsigned ngroups = nwg < CF_COUNT_GROUPS ? nwg : CF_COUNT_GROUPS;
+  const unsigned in_group = (nwg - g + CF_COUNT_GROUPS - 1) / CF_COUNT_GROUPS;
+  unsigned long long* gw = blk + 16 * (g + 1);
+  const unsigned long long prev = atomicAdd(gw, (cnt << CF_TALLY_BITS) | 1ull);
+  if ((prev & TALLY) != (unsigned long long)in_group - 1ull) return;
+  const unsigned long long gtot = (prev >> CF_TALLY_BITS) + cnt;
+  *gw = 0ull;
+  const unsigned long long prev0 = atomicAdd(&blk[0], (gtot << CF_TALLY_BITS) | 1ull);
+  if ((prev0 & TALLY) == (unsigned long long)ngroups - 1ull) {
+    blk[1] = (prev0 >> CF_TALLY_BITS) + gtot;
     blk[0] = 0ull;
   }
 }

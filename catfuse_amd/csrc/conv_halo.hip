@@ -751,7 +751,7 @@ void conv_halo_kernel(HaloArgs a) {
     // lean path, one fp32 value otherwise
     const uint32_t mag = LEAN ? 0x7fff7fffu : 0x7fffffffu;
     const bool any = cf_wg_any((anyw & mag) != 0u, any_sh);
-    if (threadIdx.x == 0) cf_count_publish(a.nz_out, any ? 1ull : 0ull, gridDim.x);
+    if (threadIdx.x == 0) cf_count_publish(a.nz_out, any ? 1ull : 0ull, blockIdx.x, gridDim.x);
   }
 
 }

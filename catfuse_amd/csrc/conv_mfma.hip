@@ -336,7 +336,8 @@ __global__ __launch_bounds__(256, (conv_min_blocks<BM, BN, EPI>())) void conv_mf
     // magnitude bits only: -0.0 counts as zero
     __shared__ unsigned any_sh[4];
     const bool any = cf_wg_any((anyw & 0x7fffffffu) != 0u, any_sh);
-    if (tid == 0) cf_count_publish(a.nz_out, any ? 1ull : 0ull, gridDim.x * gridDim.y);
+    if (tid == 0) cf_count_publish(a.nz_out, any ? 1ull : 0ull, blockIdx.x + gridDim.x * blockIdx.y,
+                                  gridDim.x * gridDim.y);
   }
 }
 

@@ -82,7 +82,7 @@ __global__ __launch_bounds__(256) void pack_kernel(
   if (myinexact) atomicOr(&inexact_sh, 1u);
   __syncthreads();
   if (tid == 0) {
-    if (nnz) cf_count_publish(nnz, cnt_sh, gridDim.x * gridDim.y);
+    if (nnz) cf_count_publish(nnz, cnt_sh, blockIdx.x + gridDim.x * blockIdx.y, gridDim.x * gridDim.y);
     if (status && inexact_sh) atomicOr(status, (uint32_t)CF_STATUS_INEXACT_FP16);
   }
 }
@@ -132,7 +132,7 @@ __global__ __launch_bounds__(256) void scan_nhwc_kernel(
     for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
     if ((tid & 63) == 0) atomicAdd(&cnt_sh, cnt);
     __syncthreads();
-    if (tid == 0) cf_count_publish(nnz, cnt_sh, gridDim.x);
+    if (tid == 0) cf_count_publish(nnz, cnt_sh, blockIdx.x, gridDim.x);
   }
 }
 
@@ -213,7 +213,7 @@ CF_API int cf_scan_nhwc(const void* xp, int64_t NB, int64_t H, int64_t W, int64_
   const int64_t npix = NB * H * W;
   if (npix == 0) return 0;
   const int64_t nblk = (npix + 15) / 16;
-  hipLaunchKernelGGL(scan_nhwc_kernel, dim3((unsigned)(nblk < 1024 ? nblk : 1024)), dim3(256), 0,
+  hipLaunchKernelGGL(scan_nhwc_kernel, dim3((unsigned)(nblk < 512 ? nblk : 512)), dim3(256), 0,
                      (hipStream_t)stream, (const _Float16*)xp, npix, (int)Cp, (int)C, act,
                      group_size, threshold, nnz);
   return (int)hipGetLastError();

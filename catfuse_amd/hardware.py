@@ -58,15 +58,19 @@ A100_80GB = replace(A100_40GB, arch_name="A100 80GB", hbm_bandwidth_gbps=2039.0)
 
 # AMD Instinct MI355X (CDNA4, gfx950): 256 CUs in 8 XCDs, 288 GB HBM3E at
 # ~8 TB/s, 256 MB Infinity Cache, ~2.5 PFLOP/s dense fp16 MFMA.  The
-# SparseFlow route threshold is the measured SF/DK crossover of the gfx950
-# kernels (see DESIGN.md for the sweep); the static regime thresholds keep
+# SparseFlow route threshold is the measured crossover of the gfx950 kernels
+# (catfuse_amd.sparseflow.crossover): at every measured input sparsity of
+# config C1 (i.i.d., per-channel and all-channel 8x8 block patterns, rates
+# 0.001-0.5) the fused dense conv beat the forced SparseFlow route (scan +
+# prescan + chunk skipping), so the threshold is 1.0 (never taken); all-zero
+# inputs take StaticZero on every route.  The static regime thresholds keep
 # the reference's table shape.
 MI355X = HardwareProfile(
     arch_name="AMD Instinct MI355X", sm_version=(9, 5), hbm_bandwidth_gbps=8000.0,
     l2_size_mb=32.0, sm_count=256, sf_threshold_C=256, sf_threshold_H=14,
     default_K_memory_bound=8, default_K_compute_bound=4,
     notes="gfx950; fused StreamFuse conv as the dense path, device-side routing.",
-    gcn_arch="gfx950", peak_fp16_tflops=2500.0, sf_sparsity_threshold=0.7,
+    gcn_arch="gfx950", peak_fp16_tflops=2500.0, sf_sparsity_threshold=1.0,
     dense_impl="StreamFuse")
 
 DEFAULT = V100_PCIE_32GB

@@ -14,6 +14,12 @@ Realises TimeBlock(K) ∘ StreamFuse(Conv, LIF) ∘ StateCarry(LIF)
    clear for the tile; otherwise dense — then applies BN and the LIF in its
    epilogue.  No host synchronisation; every route gives bit-identical
    results (skipped chunks contribute exact zeros).
+
+Steps 1-2 and the sparse route run only when the threshold is below 1.  The
+MI355X profile's threshold is 1.0: on gfx950 no measured input sparsity made
+the SparseFlow route faster than the fused dense conv (the sweep of
+catfuse_amd.sparseflow.crossover), so the layer then runs the dense fused
+conv, with StaticZero decided from the input's count block.
 """
 from __future__ import annotations
 
@@ -38,6 +44,12 @@ class SparseFlow(HipConvImplementation):
         bh, bw = _select_tile_sizes(Ho, Wo)
         return dict(block_h=bh, block_w=bw, group_size=choose_group_size(spec.in_channels))
 
+    def route_geometry(self, spec, H_in, W_in):
+        """Prescan geometry for the conv, or None when the threshold (>= 1)
+        can never select the SparseFlow route: no activity scan or prescan
+        then, only the StaticZero check."""
+        return self.geometry(spec, H_in, W_in) if self.sparsity_threshold < 1.0 else None
+
     def forward(self, x, spec, params, state):
         self.check_input(x, spec)
         B = x.shape[1]
@@ -47,8 +59,8 @@ class SparseFlow(HipConvImplementation):
         if self.input_is_analog(x):
             spikes, v_out = r.run_direct(x, v_in)
         else:
-            spikes, v_out = r.run_mfma(x.contiguous(), v_in,
-                                       sparse=self.geometry(spec, x.shape[3], x.shape[4]),
+            sparse = self.route_geometry(spec, x.shape[3], x.shape[4])
+            spikes, v_out = r.run_mfma(x.contiguous(), v_in, sparse=sparse,
                                        sparse_threshold=self.sparsity_threshold)
         state.set(v_out)
         return spikes

@@ -281,18 +281,24 @@ def shadow_of(x: torch.Tensor, shape) -> Optional[torch.Tensor]:
     return t
 
 
+COUNT_BLOCK_WORDS = 272  # CF_COUNT_BLOCK_WORDS of the C-ABI
+
+
 def count_block(device) -> torch.Tensor:
-    """A count block (two int64): [0] the accumulator of a producer pass, zero
-    between passes; [1] the count the last completed pass published.  The
-    producer kernels (cf_pack_input, cf_scan_nhwc, a fused conv writing its
-    output) clear [0] themselves, so a block is zeroed once, here."""
-    return torch.zeros(2, dtype=torch.int64, device=device)
+    """A count block (COUNT_BLOCK_WORDS int64): [0] the accumulator of a
+    producer pass, zero between passes; [1] the count the last completed
+    pass published; then per-group accumulators that spread the pass's
+    atomics.  The producer kernels (cf_pack_input, cf_scan_nhwc, a fused conv
+    writing its output) clear the accumulators themselves, so a block is
+    zeroed once, here."""
+    return torch.zeros(COUNT_BLOCK_WORDS, dtype=torch.int64, device=device)
 
 
 def _require_block(blk: Optional[torch.Tensor]) -> None:
-    if blk is not None and (blk.dtype != torch.int64 or blk.numel() < 2
+    if blk is not None and (blk.dtype != torch.int64 or blk.numel() < COUNT_BLOCK_WORDS
                             or not blk.is_contiguous() or not blk.is_cuda):
-        raise ValueError("a count block is a contiguous int64 GPU tensor of two elements")
+        raise ValueError(f"a count block is a contiguous int64 GPU tensor of "
+                         f"{COUNT_BLOCK_WORDS} elements (count_block)")
 
 
 def attach_count(out: torch.Tensor, blk: torch.Tensor, gen_cell: list) -> None:

@@ -42,7 +42,7 @@ class STFusionConvBNLIF(CTFPattern):
                  bn_scale: Optional[torch.Tensor] = None, bn_bias: Optional[torch.Tensor] = None,
                  tau: float = 2.0, v_threshold: float = 1.0, v_reset: Optional[float] = 0.0,
                  decay_input: bool = True, K: int = 4, threshold: float = 1e-6,
-                 routing: str = "device"):
+                 routing: str = "device", sparsity_threshold: Optional[float] = None):
         super().__init__()
         self.in_channels, self.out_channels = int(in_channels), int(out_channels)
         self.kernel_size, self.stride, self.padding = int(kernel_size), int(stride), int(padding)
@@ -74,7 +74,9 @@ class STFusionConvBNLIF(CTFPattern):
                                 decay_input=self.decay_input)
         prof = runtime_profile()
         self._impl_dense = DenseKeep() if prof.dense_impl == "DenseKeep" else StreamFuse()
-        self._impl_sparse = SparseFlow()
+        # sparsity above which the SparseFlow route is taken: the profile's
+        # measured value unless given (0.7 reproduces the reference's routing)
+        self._impl_sparse = SparseFlow(sparsity_threshold)
         self._params = None
         self._params_key = None
         self.route_counts = {"StaticZero": 0, "SparseFlow": 0, "DenseKeep": 0}
@@ -125,9 +127,9 @@ class STFusionConvBNLIF(CTFPattern):
                 spikes, v_out = r.run_direct(x, v_in)
                 spikes = identity + spikes
             else:
+                sparse = impl.route_geometry(self.spec, x.shape[3], x.shape[4])
                 spikes, v_out = r.run_mfma(x.contiguous(), v_in, identity=identity.contiguous(),
-                                           identity_mode=ID_ADD_SPIKE,
-                                           sparse=impl.geometry(self.spec, x.shape[3], x.shape[4]),
+                                           identity_mode=ID_ADD_SPIKE, sparse=sparse,
                                            sparse_threshold=impl.sparsity_threshold)
             self.state.set(v_out)
             return spikes
@@ -144,13 +146,15 @@ class STFusionConvBNLIF(CTFPattern):
 
     @classmethod
     def from_sj_modules(cls, conv: nn.Conv2d, bn: nn.BatchNorm2d, lif, K: int = 4,
-                        threshold: float = 1e-6, routing: str = "device"):
+                        threshold: float = 1e-6, routing: str = "device",
+                        sparsity_threshold: Optional[float] = None):
         bn.eval()
         scale, offset = _fold_bn_params(bn)
         lp = lif_params(lif)
         m = cls(conv.in_channels, conv.out_channels, int(_first(conv.kernel_size)),
                 int(_first(conv.stride)), int(_first(conv.padding)), bias=conv.bias is not None,
-                bn_scale=scale, bn_bias=offset, K=K, threshold=threshold, routing=routing, **lp)
+                bn_scale=scale, bn_bias=offset, K=K, threshold=threshold, routing=routing,
+                sparsity_threshold=sparsity_threshold, **lp)
         with torch.no_grad():
             m.weight.copy_(conv.weight)
             if conv.bias is not None:

@@ -32,16 +32,20 @@ extern "C" {
 #define CF_ROUTE_SPARSE 1 /* SparseFlow: 1 - nnz/numel > threshold      */
 #define CF_ROUTE_DENSE 2  /* DenseKeep                                  */
 
-/* Count blocks: two uint64 in device memory, [0] the accumulator of a
- * producer pass (zero between passes), [1] the count the last completed pass
- * published.  Producer passes (cf_pack_input, cf_scan_nhwc, and cf_conv_mfma /
- * cf_conv_halo through nz_out) add into [0] with one atomic per workgroup; the
- * workgroup that completes the pass stores the total in [1] and clears [0].
+/* Count blocks: CF_COUNT_BLOCK_WORDS uint64 in device memory, [0] the
+ * accumulator of a producer pass (zero between passes), [1] the count the
+ * last completed pass published, [16*(g+1)] for g < 16 the accumulators of
+ * the pass's workgroup groups (zero between passes).  Producer passes
+ * (cf_pack_input, cf_scan_nhwc, and cf_conv_mfma / cf_conv_halo through
+ * nz_out) add into their group word with one atomic per workgroup; the
+ * workgroup completing a group adds the group total to [0], and the one
+ * completing [0] stores the pass total in [1]; each clears what it completed.
  * The owner zeroes a block once; passes publishing into one block must not
- * overlap (stream order).  Readers (the routing of cf_conv_mfma / cf_conv_halo,
- * cf_route_from_nnz) read [1] in later launches.  Replaces the host-side
- * count_nonzero(x).item() of
+ * overlap (stream order).  Readers (the routing of cf_conv_mfma /
+ * cf_conv_halo, cf_route_from_nnz) read [1] in later launches.  Replaces the
+ * host-side count_nonzero(x).item() of
  * catfuse/sparseflow/ops/st_fusion_conv_bn_lif.py:512-514. */
+#define CF_COUNT_BLOCK_WORDS 272
 
 /* Status bits OR-ed into the device status word by cf_pack_input. */
 #define CF_STATUS_INEXACT_FP16 1u

@@ -190,3 +190,29 @@ def test_substitute_sf_vgg11():
     assert pm["FusedLinearLIF"] == 2
     assert pm.get("PartialFusionConvBNLIF", 0) + pm.get("STFusionConvBNLIF", 0) == 3
     assert stats["fused_lif_nodes"] == stats["total_lif_nodes"] == 10
+
+
+def test_crossover_inputs_and_decision():
+    """The crossover sweep's input patterns and its decision rule (CPU)."""
+    from catfuse_amd.sparseflow import crossover as xo
+    shape = (2, 3, 16, 14, 14)
+    x = xo.c1_input(0.5, "iid", shape, seed=1)
+    assert x.shape == shape and set(x.unique().tolist()) <= {0.0, 1.0}
+    # spatial: a zeroed 8x8 block is zero in every channel
+    xs = xo.c1_input(1.0, "spatial", shape, seed=2)
+    blocks = xs[..., :8, :8].amax(dim=(3, 4))           # [T, B, C]
+    assert torch.equal(blocks.amax(dim=2, keepdim=True).expand_as(blocks), blocks)
+    # block: zeroed per channel, about 30% of the blocks survive
+    xb = xo.c1_input(1.0, "block", (4, 8, 64, 16, 16), seed=3)
+    frac = float(xb.mean())
+    assert 0.2 < frac < 0.4
+    with pytest.raises(ValueError):
+        xo.c1_input(0.1, "checker", shape)
+    rows = [dict(pattern="iid", rate=r, density=r, SparseFlow=sf, StreamFuse=10.0,
+                 DenseKeep=12.0, auto=10.0)
+            for r, sf in ((0.0, 1.0), (0.01, 9.0), (0.1, 11.0), (0.5, 13.0))]
+    # rate 0 (StaticZero) never counts as a SparseFlow win
+    assert xo.crossover(rows) == {"iid": pytest.approx(0.99)}
+    rows[1]["SparseFlow"] = 10.5
+    assert xo.crossover(rows) == {"iid": None}
+    assert "| iid | 0.01 |" in xo.format_table(rows)

@@ -23,6 +23,15 @@ def test_header_declares_entry_points():
         assert s in syms
 
 
+def test_count_block_size_matches_header():
+    from catfuse_amd import runtime
+    m = re.search(r"#define CF_COUNT_BLOCK_WORDS (\d+)", open(HEADER).read())
+    assert m and int(m.group(1)) == runtime.COUNT_BLOCK_WORDS
+    src = open(os.path.join(ROOT, "catfuse_amd", "csrc", "cf_common.h")).read()
+    groups = int(re.search(r"CF_COUNT_GROUPS = (\d+);", src).group(1))
+    assert 16 * (groups + 1) == runtime.COUNT_BLOCK_WORDS
+
+
 def test_library_exports_every_declared_symbol():
     from catfuse_amd import _hip
     path = _hip.library_path()

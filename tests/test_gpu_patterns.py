@@ -96,8 +96,9 @@ def test_route_counter_clears_between_calls(cuda):
     # (scan pass)
     from catfuse_amd.patterns import STFusionConvBNLIF
     m = _triple(256, 256, 3, 1, 1, seed=4)
-    st = STFusionConvBNLIF.from_sj_modules(*m).to(cuda)
-    prod = STFusionConvBNLIF.from_sj_modules(*m).to(cuda)
+    # the reference's routing threshold: every route is exercised
+    st = STFusionConvBNLIF.from_sj_modules(*m, sparsity_threshold=0.7).to(cuda)
+    prod = STFusionConvBNLIF.from_sj_modules(*m, sparsity_threshold=0.7).to(cuda)
     for rate in (0.0, 0.5, 0.0, 0.01, 0.5, 0.01, 0.0):
         x = (torch.rand(4, 2, 256, 14, 14, generator=_gen(int(rate * 1000) + 7)) < rate).float()
         st.reset()
@@ -117,9 +118,15 @@ def test_stfusion_c1_all_impls_bitwise(cuda, rate):
     from catfuse_amd.patterns import STFusionConvBNLIF
     m = _triple(256, 256, 3, 1, 1, seed=2)
     x = (torch.rand(4, 8, 256, 14, 14, generator=_gen(int(rate * 100))) < rate).float().to(cuda)
-    st = STFusionConvBNLIF.from_sj_modules(*m).to(cuda)
+    st = STFusionConvBNLIF.from_sj_modules(*m, sparsity_threshold=0.7).to(cuda)
     out_dev = st(x)
     v_dev = st.state.tensor.clone()
+    # the MI355X profile's threshold (no SparseFlow route): same bits, no prescan
+    st_prof = STFusionConvBNLIF.from_sj_modules(*m).to(cuda)
+    assert torch.equal(st_prof(x), out_dev)
+    assert torch.equal(st_prof.state.tensor, v_dev)
+    assert st_prof._impl_sparse.last_tiles() is None
+    assert st_prof.last_route() == (0 if rate == 0.0 else 2)
     ref = {}
     for name, impl in (("DenseKeep", DenseKeep()), ("StreamFuse", StreamFuse())):
         st.reset()
@@ -130,7 +137,8 @@ def test_stfusion_c1_all_impls_bitwise(cuda, rate):
         assert torch.equal(v, v_dev), name
     expect_route = oracle.route(x.cpu())
     assert st.last_route() == expect_route
-    st_host = STFusionConvBNLIF.from_sj_modules(*m, routing="host").to(cuda)
+    st_host = STFusionConvBNLIF.from_sj_modules(*m, routing="host",
+                                                sparsity_threshold=0.7).to(cuda)
     assert torch.equal(st_host(x), out_dev)
     s_ref, v_ref, h_ref = oracle.conv_bn_lif(x.cpu(), *m)
     lif_parity(out_dev.cpu().numpy(), v_dev.cpu().numpy(), s_ref, v_ref, h_ref, what="C1")
