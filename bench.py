@@ -10,10 +10,13 @@ output is checked against the eager forward's); --eager times the eager
 launches instead.  Prints ONE JSON line (rank 0):
   value      = images/s = B / (seconds per step)
   roofline   = dominant kernel (the MFMA conv, conv_halo_kernel behind
-               cf_conv_mfma) achieved dense-equivalent
-               TFLOP/s vs the 2.5 PFLOP/s fp16 dense MFMA peak, timed with
-               HIP events on the launch stream around every launch of an
-               eager pass over the same steps (the kernels the graph replays)
+               cf_conv_mfma) achieved TFLOP/s over its launches that ran the
+               MFMA K loop (dense route) vs the 2.5 PFLOP/s fp16 dense MFMA
+               peak, timed with HIP events on the launch stream around every
+               launch of an eager pass over the same steps (the kernels the
+               graph replays); the launches that took the StaticZero route
+               (all-zero input: no K loop) are reported apart, as output
+               bytes written per second vs the 8 TB/s HBM peak
   lif_tails  = standalone LIF-family kernels' achieved HBM GB/s vs 8 TB/s
   cpu_baseline = the CPU oracle (SpikingJelly-equivalent PyTorch/C
                multi-step path, fp32) on a bounded sample of the same
@@ -216,19 +219,37 @@ def main():
     kern = timer.summary()
     ips = B / (ms * 1e-3)
 
-    conv = kern.get("conv_mfma", {})
-    conv_sp = kern.get("conv_mfma_sparse", {})
-    tot_ms = conv.get("ms_total", 0) + conv_sp.get("ms_total", 0)
-    tot_fl = conv.get("flops", 0) + conv_sp.get("flops", 0)
-    launches = conv.get("launches", 0) + conv_sp.get("launches", 0)
+    def agg(names):
+        ds = [kern.get(n, {}) for n in names]
+        return (sum(d.get("ms_total", 0.0) for d in ds), sum(d.get("flops", 0) for d in ds),
+                sum(d.get("bytes", 0) for d in ds), sum(d.get("launches", 0) for d in ds))
+
+    tot_ms, tot_fl, _, launches = agg(["conv_mfma", "conv_mfma_sparse"])
+    z_ms, _, z_bytes, z_launches = agg(["conv_mfma_staticzero", "conv_mfma_sparse_staticzero"])
     achieved = tot_fl / (tot_ms * 1e-3) / 1e12 if tot_ms else 0.0
-    roofline = {"kernel": "conv_halo_kernel (cf_conv_mfma fused Conv-BN-LIF, all launches)",
+    roofline = {"kernel": "conv_halo_kernel (cf_conv_mfma fused Conv-BN-LIF), launches that run "
+                          "the MFMA K loop",
                 "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
                 "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
                 "traffic": traffic_from_profiles(),
                 "flops_per_launch_avg": tot_fl // max(1, launches),
                 "us_per_launch_avg": round(tot_ms * 1e3 / max(1, launches), 2),
                 "launches_per_step": launches // args.steps}
+    z_gbps = z_bytes / (z_ms * 1e-3) / 1e9 if z_ms else 0.0
+    # route of each conv launch of one forward, in launch order (D: MFMA K
+    # loop, Z: StaticZero), decided on the device and read back here
+    conv_recs = [r for r in timer.records if r[0].startswith("conv_mfma")]
+    per_fwd = len(conv_recs) // max(1, args.steps)
+    route_seq = "".join("Z" if (r[5] is not None and r[5].is_zero()) else "D"
+                        for r in conv_recs[:per_fwd])
+    staticzero = {"kernel": "conv_halo_kernel on the StaticZero route (all-zero input: BN bias "
+                            "-> LIF, no K loop)",
+                  "bound": "hbm", "launches_per_step": z_launches // args.steps,
+                  "us_per_launch_avg": round(z_ms * 1e3 / max(1, z_launches), 2),
+                  "bytes_per_launch_avg": z_bytes // max(1, z_launches),
+                  "achieved": round(z_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                  "frac": round(z_gbps / PEAK_HBM_GBPS, 4),
+                  "conv_route_sequence": route_seq}
     per_kernel = {k: {"launches_per_step": v["launches"] // args.steps,
                       "ms_per_step": round(v["ms_total"] / args.steps, 4)}
                   for k, v in kern.items()}
@@ -245,6 +266,7 @@ def main():
                    "fused_lif_nodes": stats["fused_lif_nodes"],
                    "total_lif_nodes": stats["total_lif_nodes"]},
         "roofline": roofline,
+        "staticzero_convs": staticzero,
         "kernels": per_kernel,
     }
     if not args.no_tails:

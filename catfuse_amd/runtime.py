@@ -34,23 +34,28 @@ class KernelTimer:
     and/or bytes) so callers can report achieved rates per kernel."""
 
     def __init__(self):
-        self.records = []   # (name, start_event, end_event, flops, bytes)
+        self.records = []   # (name, start_event, end_event, flops, bytes, route probe)
 
     def start(self):
         ev = torch.cuda.Event(enable_timing=True)
         ev.record()
         return ev
 
-    def stop(self, name, ev0, flops=0, nbytes=0):
+    def stop(self, name, ev0, flops=0, nbytes=0, route=None):
         ev1 = torch.cuda.Event(enable_timing=True)
         ev1.record()
-        self.records.append((name, ev0, ev1, int(flops), int(nbytes)))
+        self.records.append((name, ev0, ev1, int(flops), int(nbytes), route))
 
     def summary(self):
-        """{name: dict(launches, ms_total, ms_avg, flops, bytes)} (synchronises)."""
+        """{name: dict(launches, ms_total, ms_avg, flops, bytes)} (synchronises).
+        A conv launch that took the StaticZero route (read from its input's
+        count block when the summary is made) is listed under
+        name + "_staticzero" with no FLOPs and its output bytes."""
         torch.cuda.synchronize()
         out = {}
-        for name, e0, e1, fl, nb in self.records:
+        for name, e0, e1, fl, nb, route in self.records:
+            if route is not None and route.is_zero():
+                name, fl, nb = name + "_staticzero", 0, route.zero_bytes
             d = out.setdefault(name, dict(launches=0, ms_total=0.0, flops=0, bytes=0))
             d["launches"] += 1
             d["ms_total"] += e0.elapsed_time(e1)
@@ -74,9 +79,22 @@ def _t0():
     return _timer.start() if _timer is not None else None
 
 
-def _t1(name, ev0, flops=0, nbytes=0):
+def _t1(name, ev0, flops=0, nbytes=0, route=None):
     if ev0 is not None:
-        _timer.stop(name, ev0, flops, nbytes)
+        _timer.stop(name, ev0, flops, nbytes, route)
+
+
+class _RouteProbe:
+    """The StaticZero decision of a conv launch, read back from the input's
+    count block (published count zero) after the launches complete."""
+    __slots__ = ("blk", "zero_bytes")
+
+    def __init__(self, blk, zero_bytes):
+        self.blk = blk
+        self.zero_bytes = int(zero_bytes)
+
+    def is_zero(self) -> bool:
+        return int(self.blk[1].item()) == 0
 
 
 def status_word(device) -> torch.Tensor:
@@ -596,8 +614,12 @@ class ConvLIFRunner:
             self.KW, self.stride, self.padding, B, th, tw, gs, int(epilogue), *self.lif,
             _hip.stream(dev))
         check(rc, "cf_conv_mfma")
+        out_bytes = (2 * T * B * Ho * Wo * cp_out if nhwc is not None else 0) \
+            + (4 * T * B * Ho * Wo * self.Cout if out_ptr is not None else 0) \
+            + (4 * B * Ho * Wo * self.Cout if v_out is not None else 0)
         _t1("conv_mfma" + ("_sparse" if sparse is not None else ""), ev,
-            flops=2 * T * B * Ho * Wo * self.Cout * self.Cin * self.KH * self.KW)
+            flops=2 * T * B * Ho * Wo * self.Cout * self.Cin * self.KH * self.KW,
+            route=None if nnz is None else _RouteProbe(nnz, out_bytes))
         self.last_nnz = nnz  # count block of this input (None: not counted)
         self.last_numel = x.numel()
         self.last_tiles = None if ag is None else (tc_buf, ag)
