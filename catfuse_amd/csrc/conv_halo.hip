@@ -265,6 +265,89 @@ void conv_halo_kernel(HaloArgs a) {
 
   const int route = halo_route(a.nnz, a.numel, a.sparse_thr);
   uint32_t anyw = 0u;  // OR of the bits of the output values this thread stores
+  // The output's count block: workgroups that stored a nonzero value.
+  auto publish_count = [&]() {
+    if (a.nz_out) {
+      // magnitude bits only (-0.0 counts as zero): two halves per word on the
+      // lean path, one fp32 value otherwise
+      const uint32_t mag = LEAN ? 0x7fff7fffu : 0x7fffffffu;
+      const bool any = cf_wg_any((anyw & mag) != 0u, any_sh);
+      if (threadIdx.x == 0) cf_count_publish(a.nz_out, any ? 1ull : 0ull, blockIdx.x, gridDim.x);
+    }
+  };
+
+  // StaticZero from the initial membrane state (no v_in): z is the BN bias
+  // of the channel at every pixel, so all pixels of a channel follow one
+  // membrane trajectory.  The lean path runs the LIF once per channel over
+  // all T steps (the operations of the per-element epilogue below, on the
+  // same values, so the same bits), keeps each step's spikes as a row of BM
+  // halves in LDS, and writes the tile from the rows: identity + spikes per
+  // 16-byte chunk (packed fp16 adds, as below), then the final potential at
+  // every pixel.  No K loop, no per-element LIF.
+  if constexpr (LEAN && EPI == EPI_LIF) {
+    if (route == CF_ROUTE_ZERO && a.v_in == nullptr && (a.T + 2) * BM <= 2 * HB) {
+      _Float16* srow = halo;                                       // [T][BM] spikes
+      float* vrow = reinterpret_cast<float*>(halo + a.T * BM);     // [BM] final v
+      if (tid < BM) {  // the thread that loaded this channel's alpha/beta
+        const float z = __builtin_fmaf(0.0f, bn_s[0][tid], bn_s[1][tid]);
+        float v = lif_initial_v(a.lif);
+        for (int t = 0; t < a.T; ++t) {
+          float vv = lif_charge_m<LM>(v, z, a.lif);
+          srow[t * BM + tid] = lif_fire_reset_bit<LM>(vv, a.lif) ? (_Float16)1.0f : (_Float16)0.0f;
+          v = vv;
+        }
+        vrow[tid] = v;
+      }
+      __syncthreads();
+      constexpr int CH8Z = BM / 8;                       // 16-byte chunks per pixel
+      constexpr int CPIZ = BN * CH8Z / 256;              // chunks per thread per step
+      static_assert(BN * CH8Z % 256 == 0, "whole copy-out passes");
+      const bool have_id = a.identity_nhwc != nullptr;
+      for (int t = 0; t < a.T; ++t) {
+        const size_t img = (size_t)t * a.B + b;
+        const __amdgpu_buffer_rsrc_t ro =
+            halo_rsrc(a.out_nhwc + img * HoWo * a.cp_out, (uint32_t)(HoWo * a.cp_out * 2));
+        const __amdgpu_buffer_rsrc_t ri =
+            halo_rsrc(have_id ? a.identity_nhwc + img * HoWo * a.cp_id : a.identity_nhwc,
+                      have_id ? (uint32_t)(HoWo * a.cp_id * 2) : 0u);
+#pragma unroll
+        for (int i = 0; i < CPIZ; ++i) {
+          const int c = tid + 256 * i;
+          const int px = c / CH8Z, part = c % CH8Z;
+          const int py = px / TW, pxx = px % TW;
+          const bool ok = (oh0 + py < a.Ho) & (ow0 + pxx < a.Wo);
+          const int pix = (oh0 + py) * a.Wo + ow0 + pxx;
+          const h8 sp = *reinterpret_cast<const h8*>(&srow[t * BM + part * 8]);
+          const h8 idv = __builtin_bit_cast(
+              h8, __builtin_amdgcn_raw_buffer_load_b128(
+                      ri, ok ? (uint32_t)((pix * a.cp_id + cout0 + part * 8) * 2) : HALO_OOB, 0, 0));
+          const u32x4 sum = __builtin_bit_cast(u32x4, idv + sp);
+          anyw |= ok ? (sum[0] | sum[1] | sum[2] | sum[3]) : 0u;
+          __builtin_amdgcn_raw_buffer_store_b128(
+              sum, ro, ok ? (uint32_t)((pix * a.cp_out + cout0 + part * 8) * 2) : HALO_OOB, 0, 0);
+        }
+      }
+      if (a.v_out) {
+        // pixel p of the tile, channels cg * VPT .. + VPT - 1 of the block
+        constexpr int VPT = BM * BN / 256;
+        const int p = tid % BN, cg = tid / BN;
+        const int py = p / TW, pxx = p % TW;
+        const bool ok = (oh0 + py < a.Ho) & (ow0 + pxx < a.Wo);
+        const int pix = (oh0 + py) * a.Wo + ow0 + pxx;
+        const __amdgpu_buffer_rsrc_t rv =
+            halo_rsrc(a.v_out + (size_t)b * a.Cout * HoWo, (uint32_t)(a.Cout * HoWo * 4));
+#pragma unroll
+        for (int k = 0; k < VPT; ++k) {
+          const int c = cg * VPT + k;
+          __builtin_amdgcn_raw_buffer_store_b32(
+              __float_as_uint(vrow[c]), rv, ok ? (uint32_t)(((cout0 + c) * HoWo + pix) * 4) : HALO_OOB,
+              0, 0);
+        }
+      }
+      publish_count();
+      return;
+    }
+  }
   // Group bits active at time step tt (uniform across the workgroup).
   auto step_mask = [&](int tt) -> uint32_t {
     if (tt >= a.T || route == CF_ROUTE_ZERO) return 0u;
@@ -746,14 +829,7 @@ void conv_halo_kernel(HaloArgs a) {
       }
     }
   }
-  if (a.nz_out) {
-    // magnitude bits only (-0.0 counts as zero): two halves per word on the
-    // lean path, one fp32 value otherwise
-    const uint32_t mag = LEAN ? 0x7fff7fffu : 0x7fffffffu;
-    const bool any = cf_wg_any((anyw & mag) != 0u, any_sh);
-    if (threadIdx.x == 0) cf_count_publish(a.nz_out, any ? 1ull : 0ull, blockIdx.x, gridDim.x);
-  }
-
+  publish_count();
 }
 
 template <int TH, int TW, int S, int K = 3>

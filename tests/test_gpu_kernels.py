@@ -289,6 +289,57 @@ def test_output_count_routes_next_layer(cuda, case):
     assert runtime.count_of(ya) is None and runtime.count_of(yb) is not None
 
 
+STATICZERO_CASES = [
+    # name, Cin, Cout, k, s, p, H, T, SparseFlow tile width (0: dense tiles)
+    ("s1", 64, 64, 3, 1, 1, 12, 4, 0),
+    ("s1_T6", 64, 64, 3, 1, 1, 12, 6, 0),
+    ("s2", 64, 128, 3, 2, 1, 16, 4, 0),
+    ("ds", 64, 128, 1, 2, 0, 16, 4, 0),
+    ("tile8x16", 32, 64, 3, 1, 1, 56, 4, 16),
+]
+
+
+@pytest.mark.parametrize("case", STATICZERO_CASES, ids=[c[0] for c in STATICZERO_CASES])
+def test_staticzero_epilogues_bitwise(cuda, case):
+    """An all-zero input takes StaticZero; from the initial state (no v_in)
+    the lean kernel runs the LIF once per channel and writes the tile from
+    per-step spike rows.  It equals the per-element StaticZero epilogue (v_in
+    given) and the dense route bit for bit, with and without a SEW identity
+    (read from its fp16 NHWC copy), including the final membrane potential."""
+    from catfuse_amd import runtime
+    name, Cin, Cout, k, s, p, H, T, tw = case
+    B = 2
+    conv, bn, lif = _layer(Cin, Cout, k, s, p, seed=71)
+    with torch.no_grad():
+        bn.bias[::3] += 1.5      # channels whose constant drive spikes
+        bn.bias[1::5] -= 0.7
+    r = _runner(conv, bn, lif, cuda)
+    Ho = (H + 2 * p - k) // s + 1
+    x = torch.zeros(T, B, Cin, H, H, device=cuda)
+    g = _gen(72)
+    idv = ((torch.rand(T, B, Cout, Ho, Ho, generator=g) < 0.3).float()
+           * torch.randint(1, 3, (T, B, Cout, Ho, Ho), generator=g).float())
+    id_nhwc = torch.zeros(T * B, Ho, Ho, runtime.pad32(Cout), dtype=torch.float16)
+    id_nhwc[..., :Cout] = idv.reshape(T * B, Cout, Ho, Ho).permute(0, 2, 3, 1).half()
+    identity = runtime.lazy_output((T, B, Cout, Ho, Ho), id_nhwc.to(cuda), cuda)
+    sp = dict(block_h=8, block_w=tw, group_size=16) if tw else None
+    v0 = torch.zeros(B, Cout, Ho, Ho, device=cuda)  # the initial state, given explicitly
+    for ident in (None, identity):
+        runs = [r.run_mfma(x, sparse=sp, identity=ident),             # uniform StaticZero
+                r.run_mfma(x, v0, sparse=sp, identity=ident),         # per-element StaticZero
+                r.run_mfma(x, identity=ident, static_zero=False)]     # dense route
+        outs = [(y.clone(), v.clone()) for y, v in runs]
+        for y, v in outs[1:]:
+            assert torch.equal(y, outs[0][0]), f"{name}: spikes"
+            assert torch.equal(v, outs[0][1]), f"{name}: membrane"
+        y0 = outs[0][0].cpu()
+        assert bool((y0 - (0 if ident is None else idv)).abs().max() <= 1.0)
+        assert bool(y0.any())    # the biased channels spike
+    s_ref, v_ref, h_ref = oracle.conv_bn_lif(x.cpu(), conv, bn, lif)
+    lif_parity(outs[0][0].cpu().numpy() - idv.numpy(), outs[0][1].cpu().numpy(), s_ref, v_ref,
+               h_ref, what=name)
+
+
 @pytest.mark.parametrize("rate", [0.0, 0.01, 0.05, 0.2, 0.5])
 @pytest.mark.parametrize("pattern", ["iid", "block"])
 def test_sparse_route_bitwise_equals_dense(cuda, rate, pattern):
