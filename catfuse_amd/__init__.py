@@ -13,16 +13,17 @@ __version__ = "0.1.0"
 
 
 def optimize(model, device="cuda:0", policy=None, T=16, use_sparseflow=True,
-             fuse_sew_add=True, fuse_stem=True):
+             fuse_sew_add=True, fuse_stem=True, fuse_head=True):
     """Substitute the SpikingJelly model's fusible subgraphs with gfx950
     patterns.  `policy` may be a HardwareProfile for the static routing
     table (default: the reference's V100 table shape); `device`, when not
     None, is where the fused model is placed.  `fuse_stem` also folds a
-    ResNet stem's MaxPool2d(3, 2, 1) into its Conv-BN-LIF kernel."""
+    ResNet stem's MaxPool2d(3, 2, 1) into its Conv-BN-LIF kernel; `fuse_head`
+    lets a global average pool read the last fused conv's fp16 NHWC copy."""
     from catfuse_amd.substitute import substitute, substitute_sf
     if use_sparseflow:
         fused, stats = substitute_sf(model, T=T, fuse_sew_add=fuse_sew_add, hwprof=policy,
-                                     fuse_stem=fuse_stem)
+                                     fuse_stem=fuse_stem, fuse_head=fuse_head)
     else:
         fused, stats = substitute(model)
     if device is not None:

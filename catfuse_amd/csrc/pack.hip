@@ -168,6 +168,31 @@ __global__ __launch_bounds__(256) void nhwc_to_nchw_kernel(
   }
 }
 
+// Global average pool of an fp16 NHWC copy xp [NB][HW][cp]: out[n][c] =
+// (sum over the HW pixels of xp[n][p][c]) * factor, factor = float(1)/HW --
+// torch's mean on the GPU (an fp32 sum, then a multiply by float(1)/count).
+// The copies this reads hold integers (spikes, SEW sums), whose fp32 sum is
+// exact in any order.  Block (n, 512-channel slice); a thread sums two
+// adjacent channels (one 4-byte load per pixel, 1 KB per pixel per block).
+__global__ __launch_bounds__(256) void global_avgpool_nhwc_kernel(
+    const _Float16* __restrict__ xp, float* __restrict__ out, int64_t HW, int C, int cp,
+    float factor) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const int64_t n = blockIdx.x;
+  const int c = (int)blockIdx.y * 512 + 2 * (int)threadIdx.x;
+  if (c >= C) return;
+  const _Float16* src = xp + n * HW * cp + c;
+  float s0 = 0.0f, s1 = 0.0f;
+#pragma unroll 7
+  for (int64_t p = 0; p < HW; ++p) {
+    const h2 v = *reinterpret_cast<const h2*>(src + p * cp);
+    s0 += (float)v[0];
+    s1 += (float)v[1];
+  }
+  out[n * C + c] = s0 * factor;
+  if (c + 1 < C) out[n * C + c + 1] = s1 * factor;
+}
+
 __global__ void route_kernel(const unsigned long long* __restrict__ nnz, int64_t numel,
                              double sparse_threshold, int32_t* __restrict__ route) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
@@ -228,6 +253,19 @@ CF_API int cf_nhwc_to_nchw(const void* xp, float* out, int64_t NB, int64_t C, in
   dim3 grid(cf_blocks(HW, PX), (unsigned)((C + CC - 1) / CC), (unsigned)NB);
   hipLaunchKernelGGL(nhwc_to_nchw_kernel, grid, dim3(256), 0, (hipStream_t)stream,
                      (const _Float16*)xp, out, C, HW, cp);
+  return (int)hipGetLastError();
+}
+
+CF_API int cf_global_avgpool_nhwc(const void* xp, float* out, int64_t NB, int64_t HW, int64_t C,
+                                  int64_t cp, void* stream) {
+  if (!xp || !out || NB < 0 || HW <= 0 || C <= 0 || cp < C || cp % 8 != 0 || NB > INT32_MAX ||
+      NB * HW * cp > ((int64_t)1 << 40))
+    return (int)hipErrorInvalidValue;
+  if (NB == 0) return 0;
+  const float factor = 1.0f / (float)HW;
+  hipLaunchKernelGGL(global_avgpool_nhwc_kernel, dim3((unsigned)NB, (unsigned)((C + 511) / 512)),
+                     dim3(256), 0, (hipStream_t)stream, (const _Float16*)xp, out, HW, (int)C,
+                     (int)cp, factor);
   return (int)hipGetLastError();
 }
 

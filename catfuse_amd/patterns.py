@@ -27,7 +27,7 @@ import torch.nn as nn
 from catfuse_amd.hardware import runtime_profile
 from catfuse_amd.implementations import ConvLIFParams, ConvLIFSpec, DenseKeep, StreamFuse
 from catfuse_amd.runtime import (EPI_Z, ID_ADD_SPIKE, ID_ADD_Z, ConvLIFRunner, avgpool2x2_lif,
-                                 lif_multistep)
+                                 global_avgpool_nhwc, lif_multistep, pad32, shadow_of)
 from catfuse_amd.state import StateBuffer
 
 try:  # SpikingJelly's MemoryModule when available, so reset_net recognises us
@@ -509,6 +509,41 @@ class FusedAvgPoolLIF(_TailPattern):
         return cls(**lif_params(sj_lif))
 
 
+class FusedGlobalAvgPool(nn.Module):
+    """AdaptiveAvgPool2d((1, 1)) of a network head that reads the fp16 NHWC
+    copy a fused conv wrote (cf_global_avgpool_nhwc) instead of first
+    materialising the fp32 feature map.  No counterpart in the reference,
+    whose fused layers hand the head (SpikingJelly's layer.AdaptiveAvgPool2d)
+    an fp32 tensor.  Values: torch's GPU mean (fp32 sum over H x W, times
+    float(1)/(H*W)); the copy's values are integers, so the sum is exact and
+    the result bit-identical.  Inputs without a current copy go through
+    torch's adaptive_avg_pool2d (counted in `fallback_calls`).
+    step_mode 'm': x [T, B, C, H, W] -> [T, B, C, 1, 1]; 's': [N, C, H, W] ->
+    [N, C, 1, 1]."""
+
+    def __init__(self, step_mode: str = "s"):
+        super().__init__()
+        self.step_mode = step_mode
+        self.fallback_calls = 0
+
+    def forward(self, x):
+        lead = x.shape[:-3]
+        C, H, W = x.shape[-3:]
+        nb = 1
+        for d in lead:
+            nb *= int(d)
+        xp = shadow_of(x, (nb, H, W, pad32(C))) if x.is_cuda else None
+        if xp is not None:
+            return global_avgpool_nhwc(xp, C).view(*lead, C, 1, 1)
+        self.fallback_calls += 1
+        y = nn.functional.adaptive_avg_pool2d(x.reshape(nb, C, H, W), 1)
+        return y.view(*lead, C, 1, 1)
+
+    @classmethod
+    def from_sj_modules(cls, pool):
+        return cls(getattr(pool, "step_mode", "s"))
+
+
 # ---------------------------------------------------------------------------
 # blocks
 # ---------------------------------------------------------------------------
@@ -692,6 +727,7 @@ PATTERN_REGISTRY["STFusionConvBNLIF"] = STFusionConvBNLIF
 __all__ = ["CTFPattern", "PartialFusionConvLIF", "PartialFusionConvBNLIF",
            "PartialFusionConvBNAddLIF", "PartialFusionConvBNAvgPoolLIF",
            "PartialFusionConvBNLIFMaxPool", "FusedLinearLIF",
-           "FusedAddLIF", "FusedAddBNLIF", "FusedAvgPoolLIF", "CTFSEWBasicBlock",
+           "FusedAddLIF", "FusedAddBNLIF", "FusedAvgPoolLIF", "FusedGlobalAvgPool",
+           "CTFSEWBasicBlock",
            "CTFSpikingBasicBlock", "CTFSEWBottleneck", "CTFSpikingBottleneck",
            "STFusionConvBNLIF", "PATTERN_REGISTRY", "fold_bn", "lif_params", "conv_geometry"]

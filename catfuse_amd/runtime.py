@@ -385,6 +385,19 @@ def scan_nhwc(xp: torch.Tensor, C: int, *, group_size: int, threshold=1e-6,
     return act
 
 
+def global_avgpool_nhwc(xp: torch.Tensor, C: int, out: Optional[torch.Tensor] = None):
+    """xp fp16 NHWC [NB, H, W, cp] -> fp32 [NB, C]: the mean over H, W
+    (AdaptiveAvgPool2d((1, 1)) of the fp32 tensor the copy stands for)."""
+    require_gpu_tensor(xp, "xp", dtype=torch.float16)
+    NB, H, W, cp = xp.shape
+    y = out if out is not None else torch.empty((NB, C), dtype=torch.float32, device=xp.device)
+    ev = _t0()
+    check(_hip.lib().cf_global_avgpool_nhwc(ptr(xp), ptr(y), NB, H * W, C, cp,
+                                            _hip.stream(xp.device)), "cf_global_avgpool_nhwc")
+    _t1("global_avgpool_nhwc", ev, nbytes=2 * NB * H * W * C + 4 * NB * C)
+    return y
+
+
 def prescan_tiles(act: torch.Tensor, H: int, W: int, H_out: int, W_out: int, kernel_size: int,
                   stride: int, padding: int, block_h: int, block_w: int, num_groups: int,
                   ag_mask_out=None, tile_class_out=None):

@@ -27,7 +27,8 @@ import warnings
 import torch.nn as nn
 
 from catfuse_amd.patterns import (CTFSEWBasicBlock, CTFSEWBottleneck, CTFSpikingBasicBlock,
-                                  CTFSpikingBottleneck, FusedAvgPoolLIF, FusedLinearLIF,
+                                  CTFSpikingBottleneck, FusedAvgPoolLIF, FusedGlobalAvgPool,
+                                  FusedLinearLIF,
                                   PartialFusionConvBNAvgPoolLIF, PartialFusionConvBNLIF,
                                   PartialFusionConvBNLIFMaxPool, PartialFusionConvLIF,
                                   STFusionConvBNLIF, conv_geometry)
@@ -262,7 +263,7 @@ def _strip_root(name: str) -> str:
 
 
 def substitute_sf(sj_model, T=16, verbose=False, force_sparse=False, fuse_sew_add=True,
-                  hwprof=None, fuse_stem=True):
+                  hwprof=None, fuse_stem=True, fuse_head=True):
     holder = _Root(copy.deepcopy(sj_model))
     model = holder
     stats = {"total_lif_nodes": _count_lif(model), "fused_lif_nodes": 0, "patterns_matched": {},
@@ -417,8 +418,25 @@ def substitute_sf(sj_model, T=16, verbose=False, force_sparse=False, fuse_sew_ad
     if fuse_sew_add:
         _wrap_sew_blocks(model)
 
+    # Phase 3: a global average pool in the head reads the last fused conv's
+    # fp16 NHWC copy (no counterpart in the reference, which leaves the head
+    # to SpikingJelly).
+    if fuse_head:
+        for pname, pmod in list(model.named_modules()):
+            for name, ch in list(pmod.named_children()):
+                if _is_global_avgpool(ch):
+                    setattr(pmod, name, FusedGlobalAvgPool.from_sj_modules(ch))
+                    _bump(stats, "FusedGlobalAvgPool")
+
     stats["coverage_pct"] = 100.0 * stats["fused_lif_nodes"] / max(stats["total_lif_nodes"], 1)
     return holder.root, stats
+
+
+def _is_global_avgpool(m) -> bool:
+    if not isinstance(m, nn.AdaptiveAvgPool2d):
+        return False
+    o = m.output_size
+    return o == 1 or tuple(o if isinstance(o, (tuple, list)) else (o, o)) == (1, 1)
 
 
 def _fused_conv(m):

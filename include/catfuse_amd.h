@@ -112,6 +112,16 @@ int cf_scan_nhwc(const void* xp, int64_t NB, int64_t H, int64_t W, int64_t Cp, i
 int cf_nhwc_to_nchw(const void* xp, float* out, int64_t NB, int64_t C, int64_t H, int64_t W,
                     int64_t cp, void* stream);
 
+/* Global average pool of an fp16 NHWC copy xp [NB][HW][cp] (channels >= C
+ * zero): out [NB][C] fp32 = (sum over the HW pixels) * float(1)/HW, which is
+ * torch's GPU mean (AdaptiveAvgPool2d((1, 1)) = mean over H, W) bit for bit
+ * for the integer values a fused conv's copy holds.  No counterpart in the
+ * reference (the network head after the fused layers is SpikingJelly's
+ * layer.AdaptiveAvgPool2d); it reads the copy instead of materialising the
+ * fp32 feature map. */
+int cf_global_avgpool_nhwc(const void* xp, float* out, int64_t NB, int64_t HW, int64_t C,
+                           int64_t cp, void* stream);
+
 /* route = ZERO if the count block's published count k (nnz[1]) is 0, SPARSE
  * if 1 - k/numel > sparse_threshold (in double), else DENSE.  Replaces the host decision at
  * catfuse/sparseflow/ops/st_fusion_conv_bn_lif.py:510-524. */

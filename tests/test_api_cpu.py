@@ -154,6 +154,10 @@ def test_substitute_sf_sew_resnet18_routing():
     assert isinstance(fused.layer3[1].fused_second, STFusionConvBNLIF)
     assert all(isinstance(b, CTFSEWBasicBlock) for l in (fused.layer1, fused.layer2, fused.layer3,
                                                          fused.layer4) for b in l)
+    # the head's global average pool reads the fused output's NHWC copy
+    from catfuse_amd.patterns import FusedGlobalAvgPool
+    assert isinstance(fused.avgpool, FusedGlobalAvgPool) and fused.avgpool.step_mode == "m"
+    assert stats["patterns_matched"]["FusedGlobalAvgPool"] == 1
     # the original model is untouched
     assert type(m.layer1[0].sn1).__name__ == "LIFNode"
 
@@ -216,3 +220,17 @@ def test_crossover_inputs_and_decision():
     rows[1]["SparseFlow"] = 10.5
     assert xo.crossover(rows) == {"iid": None}
     assert "| iid | 0.01 |" in xo.format_table(rows)
+
+
+def test_fused_global_avgpool_fallback_cpu():
+    """Without an NHWC copy (here: a CPU tensor) the pattern is torch's
+    adaptive_avg_pool2d, in both step modes."""
+    from catfuse_amd.patterns import FusedGlobalAvgPool
+    x = torch.randn(3, 2, 5, 7, 6, generator=torch.Generator().manual_seed(4))
+    pm = FusedGlobalAvgPool("m")
+    y = pm(x)
+    ref = torch.nn.functional.adaptive_avg_pool2d(x.flatten(0, 1), 1).view(3, 2, 5, 1, 1)
+    assert torch.equal(y, ref) and pm.fallback_calls == 1
+    ps = FusedGlobalAvgPool.from_sj_modules(snn.AdaptiveAvgPool2d((1, 1)))
+    assert ps.step_mode == "s"
+    assert torch.equal(ps(x[0]), torch.nn.functional.adaptive_avg_pool2d(x[0], 1))

@@ -310,6 +310,27 @@ def test_sew_resnet18_per_layer_and_logits(cuda, hw):
     assert torch.equal(y, y2)
 
 
+def test_fused_global_avgpool_nhwc_bitwise(cuda):
+    """The head's global average pool on a fused layer's output (read from its
+    fp16 NHWC copy) equals torch's GPU adaptive_avg_pool2d of the fp32 tensor
+    bit for bit, without materialising it."""
+    from catfuse_amd import runtime
+    from catfuse_amd.patterns import FusedGlobalAvgPool
+    T, B, C, H, W = 4, 3, 80, 7, 9
+    g = _gen(31)
+    v = ((torch.rand(T, B, C, H, W, generator=g) < 0.4).float()
+         * torch.randint(1, 4, (T, B, C, H, W), generator=g).float())
+    cp = runtime.pad32(C)
+    nhwc = torch.zeros(T * B, H, W, cp, dtype=torch.float16)
+    nhwc[..., :C] = v.reshape(T * B, C, H, W).permute(0, 2, 3, 1).half()
+    x = runtime.lazy_output((T, B, C, H, W), nhwc.to(cuda), cuda)
+    pool = FusedGlobalAvgPool("m")
+    y = pool(x)
+    assert pool.fallback_calls == 0 and x.__dict__.get("_cf_pending", False)  # not materialised
+    ref = torch.nn.functional.adaptive_avg_pool2d(v.to(cuda).flatten(0, 1), 1).view(T, B, C, 1, 1)
+    assert torch.equal(y, ref)
+
+
 def test_vgg11_per_layer(cuda):
     import catfuse_amd
     from catfuse_amd import snn
