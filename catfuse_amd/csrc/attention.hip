@@ -1,0 +1,212 @@
+// Spiking self-attention core with its LIF (Spikformer SSA: Q K^T V * scale,
+// then attn_lif), on the matrix cores.
+//
+// Reference: models/spikformer_github.py:139-160 (SSA.forward: q, k, v are
+// spike tensors [T, B, heads, N, dh]; attn = (q @ k^T) * scale; y = attn @ v;
+// attn_lif over T).  There is no softmax, so for binary Q, K, V the product
+// is evaluated as Q (K^T V):
+//   KV = K^T V   dh x dh integers <= N: exact as fp32 sums, then as fp16
+//                (N <= 2048) for the second product;
+//   Y  = Q KV    N x dh integers <= N * dh: exact in the fp32 accumulators;
+//   z  = Y * scale, one rounding; the LIF over T with v in registers.
+// The reference's fp32 evaluation rounds attn and every partial sum of
+// attn @ v; this one rounds once, so z differs from it by rounding only.
+//
+// Layouts (token-major, the fp16 NHWC copies of the fused linears): q, k, v
+// are fp16 [T*B][N][pitch] with head h at channels off + h*dh .. + dh - 1
+// (off = qoff, koff, voff; one concatenated QKV tensor or three tensors);
+// out is fp16 [T*B][N][cp_out] with head h at channels h*dh ..; v_in / v_out
+// fp32 [B][N][heads*dh].  One workgroup per (b, head), all T steps; dh = 32.
+#include "cf_common.h"
+
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int DH = 32;          // head dim (one MFMA tile edge)
+constexpr int NMAX = 256;       // tokens per image this kernel stages (LDS)
+
+struct AttnArgs {
+  const _Float16* q;
+  const _Float16* k;
+  const _Float16* v;
+  int qoff, koff, voff, pitch;
+  _Float16* out;
+  int cp_out;
+  const float* v_in;
+  float* v_out;
+  unsigned long long* nz_out;
+  int T, B, N, heads;
+  float scale;
+  LifParams lif;
+};
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t attn_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+
+template <int LM>
+__global__ __launch_bounds__(256) void spike_attention_kernel(AttnArgs a) {
+  // K and V of the current step, transposed ([d][n], n padded to a
+  // multiple of 16 with zeros) so each MFMA operand is one 16-byte read.
+  __shared__ __attribute__((aligned(16))) _Float16 kT[DH][NMAX];
+  __shared__ __attribute__((aligned(16))) _Float16 vT[DH][NMAX];
+  __shared__ __attribute__((aligned(16))) float kvp[4][DH][DH + 1];  // per-wave partial K^T V
+  __shared__ __attribute__((aligned(16))) _Float16 kvT[DH][DH];      // (K^T V)^T as fp16
+  __shared__ unsigned any_sh[4];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hi = lane >> 5, col = lane & 31;
+  const int b = blockIdx.x / a.heads, h = blockIdx.x % a.heads;
+  const int N = a.N, C = a.heads * DH;
+  const int NP = (N + 15) & ~15;            // K-dim of K^T V, padded
+  const int nks = NP / 16;                  // its 16-deep MFMA steps
+  const int ntile = (N + 31) / 32;          // 32-token row tiles of Y
+  // row tiles of this wave: wave, wave + 4
+  constexpr int MAXT = NMAX / 32 / 4;       // row tiles per wave at most
+  float v[MAXT][16];
+  uint32_t anyw = 0u;
+
+  // initial membrane potentials
+#pragma unroll
+  for (int i = 0; i < MAXT; ++i) {
+    const int tile = wave + 4 * i;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int n = tile * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
+      float v0 = lif_initial_v(a.lif);
+      if (a.v_in && tile < ntile && n < N) v0 = a.v_in[((size_t)b * N + n) * C + h * DH + col];
+      v[i][r] = v0;
+    }
+  }
+
+  for (int t = 0; t < a.T; ++t) {
+    const size_t img = (size_t)t * a.B + b;
+    const _Float16* qb = a.q + img * N * a.pitch + a.qoff + h * DH;
+    const _Float16* kb = a.k + img * N * a.pitch + a.koff + h * DH;
+    const _Float16* vb = a.v + img * N * a.pitch + a.voff + h * DH;
+    __syncthreads();  // the previous step's reads of kT / vT / kvT are complete
+    // stage K, V transposed: unit u = (token n, 8-channel part c)
+    for (int u = tid; u < NP * 4; u += 256) {
+      const int n = u >> 2, c = (u & 3) * 8;
+      h8 kx = {}, vx = {};
+      if (n < N) {
+        kx = *reinterpret_cast<const h8*>(kb + (size_t)n * a.pitch + c);
+        vx = *reinterpret_cast<const h8*>(vb + (size_t)n * a.pitch + c);
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        kT[c + j][n] = kx[j];
+        vT[c + j][n] = vx[j];
+      }
+    }
+    __syncthreads();
+    // K^T V: wave w accumulates the K steps w, w + 4, ...
+    {
+      f32x16 acc = {};
+      for (int s = wave; s < nks; s += 4) {
+        const int n0 = s * 16 + 8 * hi;
+        const h8 av = *reinterpret_cast<const h8*>(&kT[col][n0]);   // A[i = col][n]
+        const h8 bv = *reinterpret_cast<const h8*>(&vT[col][n0]);   // B[n][j = col]
+        acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, bv, acc, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) kvp[wave][8 * (r >> 2) + 4 * hi + (r & 3)][col] = acc[r];
+    }
+    __syncthreads();
+    // sum the partials (integers: exact in any order) and keep (K^T V)^T in
+    // fp16 (entries <= N, exact): kvT[j][i] = KV[i][j]
+    for (int e = tid; e < DH * DH; e += 256) {
+      const int i = e >> 5, j = e & 31;
+      const float s = kvp[0][i][j] + kvp[1][i][j] + kvp[2][i][j] + kvp[3][i][j];
+      kvT[j][i] = (_Float16)s;
+    }
+    __syncthreads();
+    // Y = Q KV per 32-token row tile; B operand: KV[i][j = col] for i in the step
+    const h8 kv0 = *reinterpret_cast<const h8*>(&kvT[col][8 * hi]);
+    const h8 kv1 = *reinterpret_cast<const h8*>(&kvT[col][16 + 8 * hi]);
+    const __amdgpu_buffer_rsrc_t rq = attn_rsrc(qb, (uint32_t)(((size_t)(N - 1) * a.pitch + DH) * 2));
+    _Float16* ob = a.out + img * N * a.cp_out + h * DH;
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+      const int tile = wave + 4 * i;
+      if (tile >= ntile) break;
+      const int n = tile * 32 + col;   // A row of this lane
+      // rows beyond N read zeros (out of the buffer's range)
+      const uint32_t qo = n < N ? (uint32_t)(((size_t)n * a.pitch) * 2) : 0x80000000u;
+      const h8 q0 = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rq, qo + 16 * hi, 0, 0));
+      const h8 q1 = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rq, qo + 32 + 16 * hi, 0, 0));
+      f32x16 y = {};
+      y = __builtin_amdgcn_mfma_f32_32x32x16_f16(q0, kv0, y, 0, 0, 0);
+      y = __builtin_amdgcn_mfma_f32_32x32x16_f16(q1, kv1, y, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int nr = tile * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
+        const float z = y[r] * a.scale;
+        float vv = lif_charge_m<LM>(v[i][r], z, a.lif);
+        const bool f = lif_fire_reset_bit<LM>(vv, a.lif);
+        v[i][r] = vv;
+        if (nr < N) {
+          ob[(size_t)nr * a.cp_out + col] = f ? (_Float16)1.0f : (_Float16)0.0f;
+          anyw |= f ? 1u : 0u;
+        }
+      }
+    }
+  }
+  if (a.v_out) {
+#pragma unroll
+    for (int i = 0; i < MAXT; ++i) {
+      const int tile = wave + 4 * i;
+      if (tile >= ntile) break;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int n = tile * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
+        if (n < N) a.v_out[((size_t)b * N + n) * C + h * DH + col] = v[i][r];
+      }
+    }
+  }
+  if (a.nz_out) {
+    const bool any = cf_wg_any(anyw != 0u, any_sh);
+    if (tid == 0) cf_count_publish(a.nz_out, any ? 1ull : 0ull, blockIdx.x, gridDim.x);
+  }
+}
+
+}  // namespace
+
+CF_API int cf_spike_attention_lif(const void* q, const void* k, const void* v, int64_t qoff,
+                                  int64_t koff, int64_t voff, int64_t pitch, void* out,
+                                  int64_t cp_out, const float* v_in, float* v_out,
+                                  unsigned long long* nz_out, int64_t T, int64_t B, int64_t N,
+                                  int64_t heads, int64_t head_dim, double scale, double tau,
+                                  double v_th, double v_reset, int hard_reset, int decay_input,
+                                  void* stream) {
+  if (!q || !k || !v || !out || T <= 0 || B <= 0 || N <= 0 || heads <= 0) return (int)hipErrorInvalidValue;
+  if (head_dim != DH || N > NMAX) return (int)hipErrorInvalidValue;
+  const int64_t C = heads * head_dim;
+  if (pitch % 8 != 0 || qoff % 8 != 0 || koff % 8 != 0 || voff % 8 != 0 || qoff < 0 ||
+      koff < 0 || voff < 0 || qoff + C > pitch || koff + C > pitch || voff + C > pitch ||
+      cp_out < C || T * B * N * pitch > ((int64_t)1 << 40) || B * heads >= (int64_t)CF_MAX_COUNT_WG ||
+      (int64_t)(N - 1) * pitch * 2 + 64 > INT32_MAX)
+    return (int)hipErrorInvalidValue;
+  AttnArgs a;
+  a.q = (const _Float16*)q; a.k = (const _Float16*)k; a.v = (const _Float16*)v;
+  a.qoff = (int)qoff; a.koff = (int)koff; a.voff = (int)voff; a.pitch = (int)pitch;
+  a.out = (_Float16*)out; a.cp_out = (int)cp_out; a.v_in = v_in; a.v_out = v_out;
+  a.nz_out = nz_out; a.T = (int)T; a.B = (int)B; a.N = (int)N; a.heads = (int)heads;
+  a.scale = (float)scale;
+  a.lif = cf_make_lif_params(tau, v_th, v_reset, hard_reset, decay_input);
+  const dim3 grid((unsigned)(B * heads)), block(256);
+  const int lm = cf_lif_mode(a.lif);
+  hipStream_t st = (hipStream_t)stream;
+  if (lm == LM_HARD0_DECAY_P2)
+    hipLaunchKernelGGL(spike_attention_kernel<LM_HARD0_DECAY_P2>, grid, block, 0, st, a);
+  else if (lm == LM_HARD_DECAY_P2)
+    hipLaunchKernelGGL(spike_attention_kernel<LM_HARD_DECAY_P2>, grid, block, 0, st, a);
+  else
+    hipLaunchKernelGGL(spike_attention_kernel<LM_GENERIC>, grid, block, 0, st, a);
+  return (int)hipGetLastError();
+}

@@ -193,6 +193,60 @@ __global__ __launch_bounds__(256) void global_avgpool_nhwc_kernel(
   if (c + 1 < C) out[n * C + c + 1] = s1 * factor;
 }
 
+// Token-major fp32 [NB][P][C] (a transformer's [T, B, N, C] activations)
+// -> its fp16 copy [NB][P][cp] (channels C..cp-1 zero), the nonzero count
+// (published in a count block) and the exactness status: the staging of a
+// fused linear's input, which the matrix-core kernels read as an NHWC image
+// of P pixels.  One 8-channel chunk per thread and pass (grid-stride).
+__global__ __launch_bounds__(256) void pack_tokens_kernel(
+    const float* __restrict__ x, int64_t rows, int C, int cp, _Float16* __restrict__ xp,
+    unsigned long long* __restrict__ nnz, uint32_t* __restrict__ status) {
+  __shared__ unsigned int cnt_sh;
+  __shared__ unsigned int inexact_sh;
+  if (threadIdx.x == 0) { cnt_sh = 0; inexact_sh = 0; }
+  __syncthreads();
+  const int nc8 = cp / 8;
+  unsigned int cnt = 0;
+  bool inexact = false;
+  for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < rows * nc8;
+       u += (int64_t)gridDim.x * 256) {
+    const int64_t r = u / nc8;
+    const int c0 = (int)(u % nc8) * 8;
+    _Float16 o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float v = (c0 + j < C) ? x[r * C + c0 + j] : 0.0f;
+      const _Float16 hv = (_Float16)v;
+      inexact |= ((float)hv != v);
+      cnt += (v != 0.0f) ? 1u : 0u;
+      o[j] = hv;
+    }
+    *reinterpret_cast<uint4*>(xp + r * cp + c0) = *reinterpret_cast<const uint4*>(o);
+  }
+  if (nnz) {
+    for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
+    if ((threadIdx.x & 63) == 0) atomicAdd(&cnt_sh, cnt);
+  }
+  if (inexact) atomicOr(&inexact_sh, 1u);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    if (nnz) cf_count_publish(nnz, cnt_sh, blockIdx.x, gridDim.x);
+    if (status && inexact_sh) atomicOr(status, (uint32_t)CF_STATUS_INEXACT_FP16);
+  }
+}
+
+// fp16 [NB][P][cp] -> fp32 [NB][P][C]: the fp32 form of a token-major fused
+// output kept only as its fp16 copy.
+__global__ __launch_bounds__(256) void tokens_to_f32_kernel(
+    const _Float16* __restrict__ xp, float* __restrict__ out, int64_t rows, int C, int cp) {
+  for (int64_t e = (int64_t)blockIdx.x * 256 + threadIdx.x; e < rows * C;
+       e += (int64_t)gridDim.x * 256) {
+    const int64_t r = e / C;
+    const int c = (int)(e % C);
+    out[e] = (float)xp[r * cp + c];
+  }
+}
+
 __global__ void route_kernel(const unsigned long long* __restrict__ nnz, int64_t numel,
                              double sparse_threshold, int32_t* __restrict__ route) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
@@ -266,6 +320,30 @@ CF_API int cf_global_avgpool_nhwc(const void* xp, float* out, int64_t NB, int64_
   hipLaunchKernelGGL(global_avgpool_nhwc_kernel, dim3((unsigned)NB, (unsigned)((C + 511) / 512)),
                      dim3(256), 0, (hipStream_t)stream, (const _Float16*)xp, out, HW, (int)C,
                      (int)cp, factor);
+  return (int)hipGetLastError();
+}
+
+CF_API int cf_pack_tokens(const float* x, int64_t rows, int64_t C, int64_t cp, void* xp,
+                          unsigned long long* nnz, uint32_t* status, void* stream) {
+  if (!x || !xp || rows < 0 || C <= 0 || cp < C || cp % 8 != 0 || rows * cp > ((int64_t)1 << 40))
+    return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  const int64_t units = rows * (cp / 8);
+  const unsigned grid = (unsigned)((units + 255) / 256 < 2048 ? (units + 255) / 256 : 2048);
+  hipLaunchKernelGGL(pack_tokens_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, x, rows,
+                     (int)C, (int)cp, (_Float16*)xp, nnz, status);
+  return (int)hipGetLastError();
+}
+
+CF_API int cf_tokens_to_f32(const void* xp, float* out, int64_t rows, int64_t C, int64_t cp,
+                            void* stream) {
+  if (!xp || !out || rows < 0 || C <= 0 || cp < C || rows * cp > ((int64_t)1 << 40))
+    return (int)hipErrorInvalidValue;
+  if (rows == 0) return 0;
+  const int64_t n = rows * C;
+  const unsigned grid = (unsigned)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
+  hipLaunchKernelGGL(tokens_to_f32_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                     (const _Float16*)xp, out, rows, (int)C, (int)cp);
   return (int)hipGetLastError();
 }
 

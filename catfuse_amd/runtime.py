@@ -232,9 +232,10 @@ class NHWCSpikes(torch.Tensor):
     tensors."""
 
     @staticmethod
-    def __new__(cls, base: torch.Tensor, nhwc: torch.Tensor):
+    def __new__(cls, base: torch.Tensor, nhwc: torch.Tensor, tokens: bool = False):
         t = base.as_subclass(cls)
         t._cf_pending = True
+        t._cf_tokens = tokens
         t._cf_nhwc = (nhwc, base._version)
         return t
 
@@ -244,9 +245,17 @@ class NHWCSpikes(torch.Tensor):
         self._cf_pending = False
         with torch._C.DisableTorchFunctionSubclass():
             nhwc = self._cf_nhwc[0]
+            cp = nhwc.shape[-1]
+            if self.__dict__.get("_cf_tokens", False):
+                # token-major [..., N, C]: a cast of the copy, dropping padding
+                C = self.shape[-1]
+                check(_hip.lib().cf_tokens_to_f32(nhwc.data_ptr(), self.data_ptr(),
+                                                  self.numel() // C, C, cp,
+                                                  _hip.stream(self.device)), "cf_tokens_to_f32")
+                return
             T, B, C, H, W = self.shape
             check(_hip.lib().cf_nhwc_to_nchw(nhwc.data_ptr(), self.data_ptr(), T * B, C, H, W,
-                                             nhwc.shape[-1], _hip.stream(self.device)),
+                                             cp, _hip.stream(self.device)),
                   "cf_nhwc_to_nchw")
 
     @classmethod
@@ -279,6 +288,44 @@ def _tensors_in(args, kwargs):
 def lazy_output(shape, nhwc: torch.Tensor, device) -> NHWCSpikes:
     """Uninitialised fp32 storage of `shape` that fills itself from `nhwc`."""
     return NHWCSpikes(torch.empty(shape, dtype=torch.float32, device=device), nhwc)
+
+
+def lazy_tokens(shape, copy: torch.Tensor, device) -> NHWCSpikes:
+    """Token-major fp32 [..., N, C] output whose values live in its fp16
+    copy (any shape with rows * cp elements, e.g. a conv's NHWC
+    [T*B, H, W, cp] with H*W = N); filled from the copy on first outside read."""
+    return NHWCSpikes(torch.empty(shape, dtype=torch.float32, device=device), copy, tokens=True)
+
+
+def token_shadow(x: torch.Tensor, cp: int) -> Optional[torch.Tensor]:
+    """The current fp16 copy of a token-major x [..., N, C] as [rows, cp]
+    (rows = x.numel() / C), or None."""
+    sh = getattr(x, "_cf_nhwc", None)
+    if sh is None:
+        return None
+    t, ver = sh
+    rows = x.numel() // x.shape[-1]
+    if (ver != x._version or t.device != x.device or t.shape[-1] != cp
+            or t.numel() != rows * cp):
+        return None
+    return t.reshape(rows, cp)
+
+
+def pack_tokens(x: torch.Tensor, cp: int, nnz: Optional[torch.Tensor] = None,
+                out: Optional[torch.Tensor] = None, status: Optional[torch.Tensor] = None):
+    """Token-major fp32 x [..., C] -> its fp16 copy [rows, cp] (channels
+    >= C zero); count_nonzero(x) published into nnz when given."""
+    require_gpu_tensor(x, "x")
+    _require_block(nnz)
+    x = x.contiguous()
+    C = x.shape[-1]
+    rows = x.numel() // C
+    xp = out if out is not None else torch.empty((rows, cp), dtype=torch.float16, device=x.device)
+    ev = _t0()
+    check(_hip.lib().cf_pack_tokens(ptr(x), rows, C, cp, ptr(xp), ptr(nnz), ptr(status),
+                                    _hip.stream(x.device)), "cf_pack_tokens")
+    _t1("pack_tokens", ev, nbytes=4 * rows * C + 2 * rows * cp)
+    return xp
 
 
 def attach_shadow(out: torch.Tensor, nhwc: torch.Tensor) -> None:
@@ -396,6 +443,42 @@ def global_avgpool_nhwc(xp: torch.Tensor, C: int, out: Optional[torch.Tensor] = 
                                             _hip.stream(xp.device)), "cf_global_avgpool_nhwc")
     _t1("global_avgpool_nhwc", ev, nbytes=2 * NB * H * W * C + 4 * NB * C)
     return y
+
+
+def spike_attention_lif(qkv: torch.Tensor, T: int, B: int, N: int, heads: int, offsets,
+                        scale: float, tau=2.0, v_threshold=1.0, v_reset=0.0, decay_input=True,
+                        v_in: Optional[torch.Tensor] = None, want_v_out=True,
+                        nz_out: Optional[torch.Tensor] = None):
+    """Spikformer's SSA core on the fp16 token copy qkv [T*B*N, pitch] that
+    holds Q, K, V at channel offsets (qoff, koff, voff) (head h at
+    off + 32h ..): LIF_T(((Q K^T) V) * scale) per head, evaluated as
+    Q (K^T V) on the matrix cores.  Returns (TokenSpikes [T, B, N, heads*32],
+    v_out [B, N, heads*32] or None)."""
+    require_gpu_tensor(qkv, "qkv", dtype=torch.float16)
+    _require_block(nz_out)
+    dev = qkv.device
+    pitch = qkv.shape[-1]
+    C = heads * 32
+    cp = pad32(C)
+    if qkv.numel() != T * B * N * pitch:
+        raise ValueError("qkv does not hold T * B * N tokens")
+    if v_in is not None:
+        require_gpu_tensor(v_in, "v_in")
+        if v_in.numel() != B * N * C:
+            raise ValueError("v_in has the wrong size")
+    copy = torch.empty((T * B * N, cp), dtype=torch.float16, device=dev)
+    v_out = torch.empty((B, N, C), dtype=torch.float32, device=dev) if want_v_out else None
+    qoff, koff, voff = (int(o) for o in offsets)
+    ev = _t0()
+    check(_hip.lib().cf_spike_attention_lif(
+        ptr(qkv), ptr(qkv), ptr(qkv), qoff, koff, voff, pitch, ptr(copy), cp, ptr(v_in),
+        ptr(v_out), ptr(nz_out), T, B, N, heads, 32, float(scale),
+        *_lif_args(tau, v_threshold, v_reset, decay_input), _hip.stream(dev)),
+        "cf_spike_attention_lif")
+    _t1("spike_attention", ev, flops=4 * T * B * heads * N * 32 * 32,
+        nbytes=2 * T * B * N * 3 * C + 2 * T * B * N * cp)
+    out = lazy_tokens((T, B, N, C), copy, dev)
+    return out, v_out
 
 
 def prescan_tiles(act: torch.Tensor, H: int, W: int, H_out: int, W_out: int, kernel_size: int,
@@ -595,6 +678,21 @@ class ConvLIFRunner:
             if identity_mode == ID_ADD_SPIKE:
                 # spike-valued identity: read its fp16 NHWC copy when current
                 id_nhwc = shadow_of(identity, (T * B, Ho, Wo, pad32(self.Cout)))
+        out, v_out = self._launch(
+            xp, T, B, H, W, Ho, Wo, x.numel(), nnz, ag, th, tw, gs, v_in, epilogue, want_v_out,
+            None if id_nhwc is not None else identity, id_nhwc, identity_mode, sparse_threshold,
+            emit_nhwc, lambda nhwc: lazy_output((T, B, self.Cout, Ho, Wo), nhwc, dev),
+            "conv_mfma" + ("_sparse" if sparse is not None else ""))
+        self.last_tiles = None if ag is None else (tc_buf, ag)
+        return out, v_out
+
+    def _launch(self, xp, T, B, H, W, Ho, Wo, numel, nnz, ag, th, tw, gs, v_in, epilogue,
+                want_v_out, identity, id_nhwc, identity_mode, sparse_threshold, emit_nhwc,
+                make_lazy, timer_name):
+        """One cf_conv_mfma launch on the staged fp16 NHWC input xp; the
+        output is make_lazy(nhwc copy) when emitting the copy (with its count
+        block attached), else an fp32 NCHW tensor.  Returns (out, v_out)."""
+        dev = xp.device
         if v_in is not None:
             require_gpu_tensor(v_in, "v_in")
             if v_in.numel() != B * self.Cout * Ho * Wo:
@@ -609,7 +707,7 @@ class ConvLIFRunner:
         nz_out = None
         if nhwc is not None:
             # spikes: written as the NHWC copy only; fp32 on first outside read
-            out = lazy_output((T, B, self.Cout, Ho, Wo), nhwc, dev)
+            out = make_lazy(nhwc)
             out_ptr = None
             nz_out = self.out_counter(dev)
             self._gen[0] += 1
@@ -620,9 +718,8 @@ class ConvLIFRunner:
         ev = _t0()
         rc = _hip.lib().cf_conv_mfma(
             ptr(xp), ptr(self.w_packed), ptr(self.alpha), ptr(self.beta), ptr(v_in), ptr(v_out),
-            out_ptr, ptr(nhwc), cp_out, None if id_nhwc is not None else ptr(identity),
-            ptr(id_nhwc), pad32(self.Cout), int(identity_mode), ptr(ag), ptr(nnz), ptr(nz_out),
-            x.numel(),
+            out_ptr, ptr(nhwc), cp_out, ptr(identity), ptr(id_nhwc), pad32(self.Cout),
+            int(identity_mode), ptr(ag), ptr(nnz), ptr(nz_out), numel,
             float(sparse_threshold), T, B, self.Cp, self.Cout, self.Coutp, H, W, Ho, Wo, self.KH,
             self.KW, self.stride, self.padding, B, th, tw, gs, int(epilogue), *self.lif,
             _hip.stream(dev))
@@ -630,13 +727,61 @@ class ConvLIFRunner:
         out_bytes = (2 * T * B * Ho * Wo * cp_out if nhwc is not None else 0) \
             + (4 * T * B * Ho * Wo * self.Cout if out_ptr is not None else 0) \
             + (4 * B * Ho * Wo * self.Cout if v_out is not None else 0)
-        _t1("conv_mfma" + ("_sparse" if sparse is not None else ""), ev,
-            flops=2 * T * B * Ho * Wo * self.Cout * self.Cin * self.KH * self.KW,
+        _t1(timer_name, ev, flops=2 * T * B * Ho * Wo * self.Cout * self.Cin * self.KH * self.KW,
             route=None if nnz is None else _RouteProbe(nnz, out_bytes))
         self.last_nnz = nnz  # count block of this input (None: not counted)
-        self.last_numel = x.numel()
-        self.last_tiles = None if ag is None else (tc_buf, ag)
+        self.last_numel = numel
         return out, (v_out if want_v_out else None)
+
+    def run_tokens(self, x: torch.Tensor, v_in=None, *, identity=None, want_v_out=True,
+                   static_zero=True, grid=None):
+        """Linear -> (BN) -> LIF over token-major x [T, B, N, Cin] (a 1x1 conv
+        over each image's N tokens as a grid of pixels, grid = (H, W) with
+        H * W = N; default the square root when N is a square of at least 16,
+        else (N, 1)).  x's fp16 copy (a fused token layer's output) is read
+        directly, otherwise x is packed.  identity [T, B, N, Cout] is added to
+        the spikes (a residual), read from its fp16 copy (packed if it has
+        none; its values must be fp16-exact).  Returns (lazy fp32 tokens
+        [T, B, N, Cout], v_out [B, Cout, N] or None)."""
+        require_gpu_tensor(x, "x")
+        if self.KH != 1 or self.KW != 1 or self.stride != 1 or self.padding != 0:
+            raise ValueError("run_tokens needs a 1x1 kernel with stride 1 and no padding")
+        T, B, N, C = x.shape
+        if C != self.Cin:
+            raise ValueError(f"expected {self.Cin} input channels, got {C}")
+        dev = x.device
+        self._ensure_packed(dev)
+        if grid is None:
+            r = int(round(N ** 0.5))
+            grid = (r, r) if (r * r == N and r >= 4) else (N, 1)
+        H, W = grid
+        if H * W != N:
+            raise ValueError("token grid does not match N")
+        xp = token_shadow(x, self.Cp)
+        nnz = None
+        if xp is not None:
+            nnz = count_of(x) if static_zero else None
+        else:
+            nnz = self.counter(dev) if static_zero else None
+            xp = pack_tokens(x, self.Cp, nnz=nnz, status=status_word(dev),
+                             out=self.workspace("xp", (T * B * N, self.Cp), torch.float16, dev))
+        id_cp = pad32(self.Cout)
+        id_copy = None
+        if identity is not None:
+            require_gpu_tensor(identity, "identity")
+            if tuple(identity.shape) != (T, B, N, self.Cout):
+                raise ValueError("identity shape mismatch")
+            id_copy = token_shadow(identity, id_cp)
+            if id_copy is None:
+                id_copy = pack_tokens(identity, id_cp, status=status_word(dev),
+                                      out=self.workspace("idp", (T * B * N, id_cp),
+                                                         torch.float16, dev))
+        out, v_out = self._launch(
+            xp.view(T * B, H, W, self.Cp), T, B, H, W, H, W, x.numel(), nnz, None, 0, 0, 0,
+            v_in, EPI_LIF, want_v_out, None,
+            None if id_copy is None else id_copy.view(T * B, H, W, id_cp), ID_ADD_SPIKE, 2.0,
+            True, lambda nhwc: lazy_tokens((T, B, N, self.Cout), nhwc, dev), "linear_tokens")
+        return out, (None if v_out is None else v_out.view(B, self.Cout, N))
 
     def run_direct(self, x: torch.Tensor, v_in=None, *, epilogue=EPI_LIF, want_v_out=True,
                    emit_nhwc=False):

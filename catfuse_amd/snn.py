@@ -337,13 +337,158 @@ def spiking_vgg11_bn(num_classes=10, spiking_neuron=LIFNode, **kwargs):
     return SpikingVGG(VGG11_CFG, num_classes, spiking_neuron, **kwargs)
 
 
+# ---------------------------------------------------------------------------
+# Spikformer (the structure and module names of the reference's
+# models/spikformer_github.py:59-330, multi-step: every LIF runs over T)
+# ---------------------------------------------------------------------------
+
+def _linear_bn_lif(x, linear, bn, lif):
+    """[T, B, N, C] -> Linear on the last dim -> BatchNorm1d over it -> LIF
+    over T (models/spikformer_github.py:126-137)."""
+    t, b, n, _ = x.shape
+    y = linear(x.flatten(0, 1))
+    y = bn(y.transpose(-1, -2)).transpose(-1, -2)
+    return lif(y.reshape(t, b, n, -1).contiguous())
+
+
+class SpikformerMLP(nn.Module):
+    def __init__(self, dim, hidden_dim, v_threshold=1.0):
+        super().__init__()
+        self.fc1 = nn.Linear(dim, hidden_dim)
+        self.fc1_bn = nn.BatchNorm1d(hidden_dim)
+        self.fc1_lif = LIFNode(tau=2.0, v_threshold=v_threshold, step_mode="m")
+        self.fc2 = nn.Linear(hidden_dim, dim)
+        self.fc2_bn = nn.BatchNorm1d(dim)
+        self.fc2_lif = LIFNode(tau=2.0, v_threshold=v_threshold, step_mode="m")
+        self.hidden_dim, self.dim = hidden_dim, dim
+
+    def forward(self, x):
+        return _linear_bn_lif(_linear_bn_lif(x, self.fc1, self.fc1_bn, self.fc1_lif),
+                              self.fc2, self.fc2_bn, self.fc2_lif)
+
+
+class SpikformerSSA(nn.Module):
+    """Spiking self-attention: LIF(BN(Linear)) for q, k, v; ((q k^T) * scale) v
+    per head; attn_lif; LIF(BN(proj)) (models/spikformer_github.py:94-160)."""
+
+    def __init__(self, dim, num_heads, v_threshold=1.0, scale=None):
+        super().__init__()
+        self.dim, self.num_heads = dim, num_heads
+        self.head_dim = dim // num_heads
+        self.scale = self.head_dim ** -0.5 if scale is None else float(scale)
+        for name in ("q", "k", "v"):
+            setattr(self, name, nn.Linear(dim, dim))
+            setattr(self, name + "_bn", nn.BatchNorm1d(dim))
+            setattr(self, name + "_lif", LIFNode(tau=2.0, v_threshold=v_threshold, step_mode="m"))
+        self.attn_lif = LIFNode(tau=2.0, v_threshold=v_threshold, step_mode="m")
+        self.proj = nn.Linear(dim, dim)
+        self.proj_bn = nn.BatchNorm1d(dim)
+        self.proj_lif = LIFNode(tau=2.0, v_threshold=v_threshold, step_mode="m")
+
+    def forward(self, x):
+        t, b, n, c = x.shape
+        hd = (t, b, n, self.num_heads, self.head_dim)
+        q = _linear_bn_lif(x, self.q, self.q_bn, self.q_lif).reshape(hd).permute(0, 1, 3, 2, 4)
+        k = _linear_bn_lif(x, self.k, self.k_bn, self.k_lif).reshape(hd).permute(0, 1, 3, 2, 4)
+        v = _linear_bn_lif(x, self.v, self.v_bn, self.v_lif).reshape(hd).permute(0, 1, 3, 2, 4)
+        attn = torch.matmul(q, k.transpose(-2, -1).contiguous()) * self.scale
+        y = torch.matmul(attn, v.contiguous())
+        y = self.attn_lif(y.transpose(2, 3).reshape(t, b, n, c).contiguous())
+        return _linear_bn_lif(y, self.proj, self.proj_bn, self.proj_lif)
+
+
+class SpikformerBlock(nn.Module):
+    def __init__(self, dim, num_heads, mlp_ratio=4.0, v_threshold=1.0, scale=None):
+        super().__init__()
+        self.attn = SpikformerSSA(dim, num_heads, v_threshold, scale)
+        self.mlp = SpikformerMLP(dim, int(dim * mlp_ratio), v_threshold)
+
+    def forward(self, x):
+        x = x + self.attn(x)
+        return x + self.mlp(x)
+
+
+class SpikformerSPS(nn.Module):
+    """Spiking patch splitting: four Conv3x3-BN-LIF stages (embed/8, /4, /2,
+    embed channels) with MaxPool2d(3, 2, 1) after the stages in `pools`
+    (the reference's CIFAR variant pools after stages 2 and 3; four pools
+    give the 14 x 14 tokens of a 224 x 224 image), then the relative
+    position Conv-BN-LIF added to its input, as tokens [T, B, N, C]
+    (models/spikformer_github.py:175-245)."""
+
+    def __init__(self, in_channels, embed_dim, v_threshold=1.0, pools=(2, 3)):
+        super().__init__()
+        chans = [in_channels, embed_dim // 8, embed_dim // 4, embed_dim // 2, embed_dim]
+        for i in range(4):
+            setattr(self, f"conv{i}", nn.Conv2d(chans[i], chans[i + 1], 3, 1, 1, bias=False))
+            setattr(self, f"bn{i}", nn.BatchNorm2d(chans[i + 1]))
+            setattr(self, f"lif{i}", LIFNode(tau=2.0, v_threshold=v_threshold, step_mode="m"))
+            setattr(self, f"pool{i}", nn.MaxPool2d(3, 2, 1) if i in pools else None)
+        self.rpe_conv = nn.Conv2d(embed_dim, embed_dim, 3, 1, 1, bias=False)
+        self.rpe_bn = nn.BatchNorm2d(embed_dim)
+        self.rpe_lif = LIFNode(tau=2.0, v_threshold=v_threshold, step_mode="m")
+
+    def forward(self, x):
+        t, b = x.shape[:2]
+        y = x
+        for i in range(4):
+            conv, bn, lif = getattr(self, f"conv{i}"), getattr(self, f"bn{i}"), getattr(self, f"lif{i}")
+            z = bn(conv(y.flatten(0, 1)))
+            y = lif(z.reshape(t, b, *z.shape[1:]).contiguous())
+            pool = getattr(self, f"pool{i}")
+            if pool is not None:
+                p = pool(y.flatten(0, 1))
+                y = p.reshape(t, b, *p.shape[1:])
+        z = self.rpe_bn(self.rpe_conv(y.flatten(0, 1)))
+        y = self.rpe_lif(z.reshape(t, b, *z.shape[1:]).contiguous()) + y
+        return y.flatten(-2).transpose(-1, -2).contiguous()
+
+
+class Spikformer(nn.Module):
+    """models/spikformer_github.py:248-330: SPS, `depth` blocks, token
+    average, pre-head LIF, linear head; x [T, B, C, H, W] (or [B, C, H, W],
+    repeated over T) -> [T, B, num_classes]."""
+
+    def __init__(self, img_size=224, in_channels=3, num_classes=1000, embed_dim=384,
+                 num_heads=12, mlp_ratio=4.0, depth=8, T=4, v_threshold=1.0, pools=(0, 1, 2, 3),
+                 scale=None):
+        super().__init__()
+        self.T = int(T)
+        self.num_classes = int(num_classes)
+        self.patch_embed = SpikformerSPS(in_channels, embed_dim, v_threshold, pools)
+        self.blocks = nn.ModuleList([SpikformerBlock(embed_dim, num_heads, mlp_ratio,
+                                                     v_threshold, scale) for _ in range(depth)])
+        self.pre_head_lif = LIFNode(tau=2.0, v_threshold=v_threshold, step_mode="m")
+        self.head = nn.Linear(embed_dim, num_classes)
+
+    def forward_features(self, x):
+        y = self.patch_embed(x)
+        for blk in self.blocks:
+            y = blk(y)
+        return y.mean(dim=2)
+
+    def forward(self, x):
+        if x.dim() == 4:
+            x = x.unsqueeze(0).expand(self.T, *x.shape)
+        return self.head(self.pre_head_lif(self.forward_features(x)))
+
+
+def spikformer_8_384(num_classes=1000, img_size=224, T=4, **kwargs):
+    """Config C4: 8 blocks, dim 384, 12 heads (head dim 32), MLP 1536; four
+    SPS pools give 14 x 14 = 196 tokens at 224 x 224; attention scale 0.125
+    as the config states (the reference module uses head_dim ** -0.5)."""
+    kwargs.setdefault("scale", 0.125)
+    return Spikformer(img_size=img_size, num_classes=num_classes, embed_dim=384, num_heads=12,
+                      mlp_ratio=4.0, depth=8, T=T, **kwargs)
+
+
 def randomize_bn(model: nn.Module, generator: torch.Generator) -> None:
     """BN running statistics and affine parameters as the benchmark configs
     specify: running_mean ~ N(0, 0.1), running_var ~ U(0.5, 1.5),
     gamma ~ U(0.8, 1.2), beta ~ N(0, 0.1)."""
     with torch.no_grad():
         for m in model.modules():
-            if isinstance(m, nn.BatchNorm2d):
+            if isinstance(m, (nn.BatchNorm1d, nn.BatchNorm2d)):
                 C = m.num_features
                 m.running_mean.copy_(torch.randn(C, generator=generator) * 0.1)
                 m.running_var.copy_(torch.rand(C, generator=generator) + 0.5)

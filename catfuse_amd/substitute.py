@@ -26,6 +26,8 @@ import warnings
 
 import torch.nn as nn
 
+from catfuse_amd.transformer import (CTFSpikformerBlock, CTFSpikformerSPS, is_spikformer_block,
+                                     is_spikformer_sps)
 from catfuse_amd.patterns import (CTFSEWBasicBlock, CTFSEWBottleneck, CTFSpikingBasicBlock,
                                   CTFSpikingBottleneck, FusedAvgPoolLIF, FusedGlobalAvgPool,
                                   FusedLinearLIF,
@@ -280,6 +282,47 @@ def substitute_sf(sj_model, T=16, verbose=False, force_sparse=False, fuse_sew_ad
         if verbose:
             print(f"  [substitute_sf] {name}: {entry['pattern']} ({entry['shape']}, "
                   f"backend={entry['backend']}, K={entry['K']})")
+
+    # Phase 0a: spiking transformer blocks and patch splitting (Spikformer):
+    # Linear -> BN1d -> LIF layers and the attention core fused (the
+    # reference leaves them unfused, substitute.py:559-567).
+    for pname, pmod in list(model.named_modules()):
+        for name, ch in list(pmod.named_children()):
+            full = f"{pname}.{name}" if pname else name
+            if is_spikformer_block(ch) and id(ch.attn.q_lif) not in done:
+                fused = CTFSpikformerBlock.from_sj_block(ch)
+                setattr(pmod, name, fused)
+                a, m = ch.attn, ch.mlp
+                d, hid = a.q.in_features, m.fc1.out_features
+                record(full + ".attn.qkv", fused, {"pattern": "FusedLinearBNLIF",
+                       "shape": f"{d}->3x{d} (q, k, v)", "backend": "StreamFuse", "K": T},
+                       a.q_lif)
+                for lif in (a.k_lif, a.v_lif):
+                    done.add(id(lif))
+                    stats["fused_lif_nodes"] += 1
+                record(full + ".attn.core", fused, {"pattern": "SpikeAttentionLIF",
+                       "shape": f"{a.num_heads} heads x 32, scale {a.scale:g}",
+                       "backend": "StreamFuse", "K": T}, a.attn_lif)
+                record(full + ".attn.proj", fused, {"pattern": "FusedLinearBNLIF",
+                       "shape": f"{d}->{d} + residual", "backend": "StreamFuse", "K": T},
+                       a.proj_lif)
+                record(full + ".mlp.fc1", fused, {"pattern": "FusedLinearBNLIF",
+                       "shape": f"{d}->{hid}", "backend": "StreamFuse", "K": T}, m.fc1_lif)
+                record(full + ".mlp.fc2", fused, {"pattern": "FusedLinearBNLIF",
+                       "shape": f"{hid}->{d} + residual", "backend": "StreamFuse", "K": T},
+                       m.fc2_lif)
+            elif is_spikformer_sps(ch) and id(ch.lif0) not in done:
+                fused = CTFSpikformerSPS.from_sj_module(ch)
+                setattr(pmod, name, fused)
+                for i in range(4):
+                    c = getattr(ch, f"conv{i}")
+                    record(f"{full}.conv{i}", fused, {"pattern": "PartialFusionConvBNLIF",
+                           "shape": f"{c.in_channels}->{c.out_channels}, k=3, s=1",
+                           "backend": SpatialBackend.DENSE_KEEP, "K": T}, getattr(ch, f"lif{i}"))
+                c = ch.rpe_conv
+                record(f"{full}.rpe_conv", fused, {"pattern": "PartialFusionConvBNLIF",
+                       "shape": f"{c.in_channels}->{c.out_channels}, k=3, s=1 + input",
+                       "backend": SpatialBackend.DENSE_KEEP, "K": T}, ch.rpe_lif)
 
     # Phase 0: ResNet stem conv1 / bn1 / sn1 / maxpool as one fused kernel
     # (no counterpart in the reference, which leaves the maxpool unfused).

@@ -1,0 +1,267 @@
+"""Fused patterns for spiking transformers (Spikformer, config C4).
+
+Reference: models/spikformer_github.py (SPS 175-245, SSA 94-160, MLP 59-92,
+Block 163-173).  The reference's substitution leaves Linear -> BatchNorm1d ->
+LIF unfused (catfuse/substitute.py:559-567) and runs the attention products
+in torch; here every Linear -> BN1d -> LIF is one matrix-core launch with BN
+folded into the epilogue affine and the LIF (and a residual add) in the
+epilogue, Q, K and V share one launch (their weights concatenated), and the
+attention core is one launch per layer (cf_spike_attention_lif).
+
+Token tensors [T, B, N, C] stay token-major: a fused layer keeps its output
+only as the fp16 copy [T*B*N, cp] (the next fused layer reads it as an NHWC
+image of the N tokens) and returns a lazy fp32 tensor that fills itself on
+first outside use.  Membrane states live in the kernels' layouts:
+Linear layers [B, C, N], the attention LIF [B, N, C].
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from catfuse_amd.patterns import (CTFPattern, PartialFusionConvBNLIF, fold_bn, lif_params)
+from catfuse_amd.runtime import (ConvLIFRunner, count_of, lazy_tokens, pad32, shadow_of,
+                                 spike_attention_lif, token_shadow)
+from catfuse_amd.state import StateBuffer
+
+
+class FusedLinearBNLIF(CTFPattern):
+    """Linear (+bias) -> BatchNorm1d (eval, over the feature dim) -> LIF on
+    token tensors x [T, B, N, I] (or [T, B, I]) -> spikes [T, B, N, O]
+    (models/spikformer_github.py:126-137).  forward(x, identity) adds a
+    residual [T, B, N, O] to the spikes in the same epilogue (the
+    `x + f(x)` of a Spikformer block)."""
+
+    def __init__(self, in_features, out_features, bias=True, has_bn=True, bn_eps=1e-5,
+                 tau=2.0, v_threshold=1.0, v_reset=0.0, decay_input=True):
+        super().__init__()
+        self.in_features, self.out_features = int(in_features), int(out_features)
+        self.tau, self.v_threshold = float(tau), float(v_threshold)
+        self.v_reset = None if v_reset is None else float(v_reset)
+        self.decay_input = bool(decay_input)
+        self.bn_eps = float(bn_eps)
+        self.weight = nn.Parameter(torch.empty(out_features, in_features))
+        nn.init.kaiming_normal_(self.weight)
+        self.bias = nn.Parameter(torch.zeros(out_features)) if bias else None
+        if has_bn:
+            self.bn_weight = nn.Parameter(torch.ones(out_features))
+            self.bn_bias = nn.Parameter(torch.zeros(out_features))
+            self.register_buffer("running_mean", torch.zeros(out_features))
+            self.register_buffer("running_var", torch.ones(out_features))
+        else:
+            self.bn_weight = self.bn_bias = None
+            self.register_buffer("running_mean", None)
+            self.register_buffer("running_var", None)
+        self.state = StateBuffer()
+        self._register_state(self.state)
+        self._runner = None
+        self._runner_key = None
+
+    def _param_tensors(self):
+        return [t for t in (self.weight, self.bias, self.bn_weight, self.bn_bias,
+                            self.running_mean, self.running_var) if t is not None]
+
+    def runner(self) -> ConvLIFRunner:
+        key = tuple((id(t), t._version, t.device) for t in self._param_tensors())
+        if key != self._runner_key:
+            with torch.no_grad():
+                scale = shift = None
+                if self.bn_weight is not None:
+                    scale, shift = fold_bn(self.bn_weight, self.bn_bias, self.running_mean,
+                                           self.running_var, self.bn_eps)
+                w = self.weight.detach().contiguous().view(self.out_features,
+                                                           self.in_features, 1, 1)
+                self._runner = ConvLIFRunner(w, scale, shift,
+                                             None if self.bias is None else self.bias.detach(),
+                                             1, 0, self.tau, self.v_threshold, self.v_reset,
+                                             self.decay_input)
+            self._runner_key = key
+        return self._runner
+
+    def forward(self, x, identity=None):
+        squeeze = x.ndim == 3
+        if squeeze:
+            x = x.unsqueeze(2)
+            identity = None if identity is None else identity.unsqueeze(2)
+        T, B, N, _ = x.shape
+        v_in = self.state.peek((B, self.out_features, N), x.device)
+        y, v = self.runner().run_tokens(x, v_in, identity=identity)
+        self.state.set(v)
+        return y.squeeze(2) if squeeze else y
+
+    @classmethod
+    def from_sj_modules(cls, linear, bn, lif):
+        inst = cls(linear.in_features, linear.out_features, bias=linear.bias is not None,
+                   has_bn=bn is not None, bn_eps=bn.eps if bn is not None else 1e-5,
+                   **lif_params(lif))
+        with torch.no_grad():
+            inst.weight.copy_(linear.weight)
+            if linear.bias is not None:
+                inst.bias.copy_(linear.bias)
+            if bn is not None:
+                inst.bn_weight.copy_(bn.weight)
+                inst.bn_bias.copy_(bn.bias)
+                inst.running_mean.copy_(bn.running_mean)
+                inst.running_var.copy_(bn.running_var)
+        return inst.to(linear.weight.device)
+
+    @classmethod
+    def concatenated(cls, triples):
+        """One layer computing several Linear -> BN1d -> LIF triples that
+        share their input and neuron parameters (Q, K and V): output
+        features in the order given."""
+        lins = [t[0] for t in triples]
+        lps = [lif_params(t[2]) for t in triples]
+        if any(lp != lps[0] for lp in lps):
+            raise ValueError("concatenated layers need equal LIF parameters")
+        eps = {t[1].eps for t in triples}
+        if len(eps) != 1 or any(t[1] is None for t in triples):
+            raise ValueError("concatenated layers need BatchNorm1d with one eps")
+        I = lins[0].in_features
+        O = sum(l.out_features for l in lins)
+        has_bias = all(l.bias is not None for l in lins)
+        inst = cls(I, O, bias=has_bias, has_bn=True, bn_eps=eps.pop(), **lps[0])
+        with torch.no_grad():
+            inst.weight.copy_(torch.cat([l.weight for l in lins], 0))
+            if has_bias:
+                inst.bias.copy_(torch.cat([l.bias for l in lins], 0))
+            for name, attr in (("bn_weight", "weight"), ("bn_bias", "bias"),
+                               ("running_mean", "running_mean"), ("running_var", "running_var")):
+                getattr(inst, name).copy_(torch.cat([getattr(t[1], attr) for t in triples], 0))
+        return inst.to(lins[0].weight.device)
+
+
+class CTFSpikformerSSA(CTFPattern):
+    """Spiking self-attention: fused QKV Linear-BN1d-LIF (one launch), the
+    attention core with attn_lif (one launch), fused proj Linear-BN1d-LIF
+    (+ the block's residual)."""
+
+    def __init__(self, dim, num_heads, scale, qkv: FusedLinearBNLIF, proj: FusedLinearBNLIF,
+                 attn_lif_params: dict):
+        super().__init__()
+        if dim != 32 * num_heads:
+            raise ValueError("the fused attention needs a head dim of 32")
+        self.dim, self.num_heads, self.scale = int(dim), int(num_heads), float(scale)
+        self.qkv = qkv
+        self.proj = proj
+        self.attn_lif = dict(attn_lif_params)
+        self.attn_state = StateBuffer()
+        self._register_state(self.attn_state)
+
+    def forward(self, x, residual=None):
+        T, B, N, C = x.shape
+        qkv = self.qkv(x)
+        copy = token_shadow(qkv, pad32(3 * C))
+        lp = self.attn_lif
+        v_in = self.attn_state.peek((B, N, C), x.device)
+        a, v = spike_attention_lif(copy, T, B, N, self.num_heads, (0, C, 2 * C), self.scale,
+                                   tau=lp["tau"], v_threshold=lp["v_threshold"],
+                                   v_reset=lp["v_reset"], decay_input=lp["decay_input"],
+                                   v_in=v_in)
+        self.attn_state.set(v)
+        return self.proj(a, identity=residual)
+
+    @classmethod
+    def from_sj_module(cls, ssa):
+        qkv = FusedLinearBNLIF.concatenated([(ssa.q, ssa.q_bn, ssa.q_lif),
+                                             (ssa.k, ssa.k_bn, ssa.k_lif),
+                                             (ssa.v, ssa.v_bn, ssa.v_lif)])
+        proj = FusedLinearBNLIF.from_sj_modules(ssa.proj, ssa.proj_bn, ssa.proj_lif)
+        return cls(ssa.dim, ssa.num_heads, ssa.scale, qkv, proj, lif_params(ssa.attn_lif))
+
+
+class CTFSpikformerMLP(CTFPattern):
+    def __init__(self, fc1: FusedLinearBNLIF, fc2: FusedLinearBNLIF):
+        super().__init__()
+        self.fc1, self.fc2 = fc1, fc2
+
+    def forward(self, x, residual=None):
+        return self.fc2(self.fc1(x), identity=residual)
+
+    @classmethod
+    def from_sj_module(cls, mlp):
+        return cls(FusedLinearBNLIF.from_sj_modules(mlp.fc1, mlp.fc1_bn, mlp.fc1_lif),
+                   FusedLinearBNLIF.from_sj_modules(mlp.fc2, mlp.fc2_bn, mlp.fc2_lif))
+
+
+class CTFSpikformerBlock(CTFPattern):
+    """x + SSA(x), then x + MLP(x), the adds in proj's and fc2's epilogues
+    (models/spikformer_github.py:163-173)."""
+
+    def __init__(self, attn: CTFSpikformerSSA, mlp: CTFSpikformerMLP):
+        super().__init__()
+        self.attn, self.mlp = attn, mlp
+
+    def forward(self, x):
+        x = self.attn(x, residual=x)
+        return self.mlp(x, residual=x)
+
+    @classmethod
+    def from_sj_block(cls, block):
+        return cls(CTFSpikformerSSA.from_sj_module(block.attn),
+                   CTFSpikformerMLP.from_sj_module(block.mlp))
+
+
+class CTFSpikformerSPS(CTFPattern):
+    """Spiking patch splitting: fused Conv-BN-LIF stages (MaxPool2d(3, 2, 1)
+    after the pooled ones, on the materialised spikes), then the relative
+    position Conv-BN-LIF with its input added in the epilogue; the result's
+    NHWC copy is the token copy [T*B*N, C] of the output tokens [T, B, N, C]
+    (models/spikformer_github.py:175-245)."""
+
+    def __init__(self, stages, pools, rpe):
+        super().__init__()
+        self.stages = nn.ModuleList(stages)
+        self.pools = nn.ModuleList([p if p is not None else nn.Identity() for p in pools])
+        self._pooled = [p is not None for p in pools]
+        self.rpe = rpe
+
+    def forward(self, x):
+        T, B = x.shape[:2]
+        y = x
+        for stage, pool, pooled in zip(self.stages, self.pools, self._pooled):
+            y = stage(y)
+            if pooled:
+                p = nn.functional.max_pool2d(y.flatten(0, 1), pool.kernel_size, pool.stride,
+                                             pool.padding)
+                y = p.reshape(T, B, *p.shape[1:])
+        r = self.rpe(y, sew_identity=y)
+        C, H, W = r.shape[2:]
+        copy = shadow_of(r, (T * B, H, W, pad32(C)))
+        if copy is None:
+            return r.flatten(-2).transpose(-1, -2).contiguous()
+        tok = lazy_tokens((T, B, H * W, C), copy, r.device)
+        if count_of(r) is not None:
+            # the same values: the rpe conv's count block describes the tokens
+            tok._cf_count = r._cf_count[:3] + (tok._version,)
+        return tok
+
+    @classmethod
+    def from_sj_module(cls, sps):
+        stages, pools = [], []
+        for i in range(4):
+            conv, bn, lif = (getattr(sps, f"{n}{i}") for n in ("conv", "bn", "lif"))
+            stages.append(PartialFusionConvBNLIF.from_sj_modules(conv, bn, lif))
+            pools.append(getattr(sps, f"pool{i}", None))
+        rpe = PartialFusionConvBNLIF.from_sj_modules(sps.rpe_conv, sps.rpe_bn, sps.rpe_lif)
+        return cls(stages, pools, rpe)
+
+
+def is_spikformer_block(m) -> bool:
+    attn, mlp = getattr(m, "attn", None), getattr(m, "mlp", None)
+    return (attn is not None and mlp is not None
+            and all(hasattr(attn, n) for n in ("q", "q_bn", "q_lif", "k", "v", "attn_lif",
+                                              "proj", "proj_bn", "proj_lif", "num_heads", "scale"))
+            and all(hasattr(mlp, n) for n in ("fc1", "fc1_bn", "fc1_lif", "fc2", "fc2_bn",
+                                             "fc2_lif")))
+
+
+def is_spikformer_sps(m) -> bool:
+    return all(hasattr(m, n) for n in ("conv0", "bn0", "lif0", "conv3", "bn3", "lif3",
+                                       "rpe_conv", "rpe_bn", "rpe_lif"))
+
+
+__all__ = ["FusedLinearBNLIF", "CTFSpikformerSSA", "CTFSpikformerMLP", "CTFSpikformerBlock",
+           "CTFSpikformerSPS", "is_spikformer_block", "is_spikformer_sps"]

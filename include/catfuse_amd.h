@@ -122,6 +122,40 @@ int cf_nhwc_to_nchw(const void* xp, float* out, int64_t NB, int64_t C, int64_t H
 int cf_global_avgpool_nhwc(const void* xp, float* out, int64_t NB, int64_t HW, int64_t C,
                            int64_t cp, void* stream);
 
+/* Token-major fp32 x [rows][C] (a transformer's [T, B, N, C] activations)
+ * -> its fp16 copy xp [rows][cp] (cp >= C, cp % 8 == 0, channels >= C zero),
+ * count_nonzero(x) published in the count block nnz (nullable) and the
+ * exactness status (nullable): the staging of a fused Linear's input, read
+ * by cf_conv_mfma as an NHWC image of the N tokens.  Replaces the fp32 input
+ * of the Linear layers of models/spikformer_github.py:77-92,126-137 (the
+ * reference leaves Linear -> BN1d -> LIF unfused, substitute.py:559-567). */
+int cf_pack_tokens(const float* x, int64_t rows, int64_t C, int64_t cp, void* xp,
+                   unsigned long long* nnz, uint32_t* status, void* stream);
+
+/* fp16 token copy xp [rows][cp] -> fp32 out [rows][C]: the fp32 form of a
+ * fused token layer's output kept only as its copy.  No counterpart. */
+int cf_tokens_to_f32(const void* xp, float* out, int64_t rows, int64_t C, int64_t cp,
+                     void* stream);
+
+/* Spikformer spiking self-attention core + its LIF over T, on the matrix
+ * cores: per (t, b, head) z = ((Q K^T) V) * scale with binary Q, K, V of
+ * N tokens x head_dim (= 32) channels, evaluated exactly as Q (K^T V) in
+ * integers and rounded once by the scale; then LIF_T(z) -> spikes.  Q, K, V
+ * are fp16 token copies [T*B][N][pitch] with head h at channel
+ * off + 32h (off = qoff / koff / voff; q, k, v may be one concatenated QKV
+ * tensor); out fp16 [T*B][N][cp_out] (head h at channel 32h); v_in / v_out
+ * fp32 [B][N][heads*32] (nullable); nz_out (nullable): count block of the
+ * output (workgroups with a spike).  N <= 256.  Replaces the SSA core of
+ * models/spikformer_github.py:139-160 (q @ k^T * scale, @ v, attn_lif) and
+ * the reference's spike-matmul kernels (sparseflow/sparse_bmm_kernel.py:40-358,
+ * sparse_attention_kernel.py:24-118). */
+int cf_spike_attention_lif(const void* q, const void* k, const void* v, int64_t qoff,
+                           int64_t koff, int64_t voff, int64_t pitch, void* out, int64_t cp_out,
+                           const float* v_in, float* v_out, unsigned long long* nz_out,
+                           int64_t T, int64_t B, int64_t N, int64_t heads, int64_t head_dim,
+                           double scale, double tau, double v_th, double v_reset, int hard_reset,
+                           int decay_input, void* stream);
+
 /* route = ZERO if the count block's published count k (nnz[1]) is 0, SPARSE
  * if 1 - k/numel > sparse_threshold (in double), else DENSE.  Replaces the host decision at
  * catfuse/sparseflow/ops/st_fusion_conv_bn_lif.py:510-524. */

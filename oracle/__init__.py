@@ -25,6 +25,12 @@ What it restates (reference = hpcyhr/CATFuse, SpikingJelly 0.0.0.0.14):
   ``select_tile_sizes`` (sparse_conv2d_kernel.py:80-84).
 * network forwards ``sew_resnet_forward`` / ``vgg_forward`` — module-by-
   module SpikingJelly semantics with the ops above.
+* spiking transformer: ``linear_bn_lif`` (float64 linear, torch eval BN,
+  C LIF; pinned against ``conv_bn_lif`` with a 1x1 conv over the token grid,
+  an independent formulation), ``spike_attention_lif`` (float64 torch
+  matmuls in the reference's order; pinned against
+  ``spike_attention_bruteforce``, the definition in Python loops, and the
+  integer identity (Q K^T) V = Q (K^T V)) and ``spikformer_forward``.
 """
 from __future__ import annotations
 
@@ -283,3 +289,103 @@ def sew_resnet_forward(model, x_seq, conv_dtype=torch.float64, record=None):
     b = model.fc.bias.detach().cpu().double() if model.fc.bias is not None else None
     y = F.linear(x.double(), w, b)
     return y.float()
+
+
+# ---------------------------------------------------------------------------
+# Spiking transformer (Spikformer, config C4)
+# ---------------------------------------------------------------------------
+
+def linear_bn_lif(x_seq, linear, bn, lif, v_in=None):
+    """Linear -> BatchNorm1d (eval, over the feature dim) -> LIF on token
+    tensors [T, B, N, I] (models/spikformer_github.py:126-137): the linear in
+    float64 rounded to fp32, torch's eval batch norm, C LIF over T.
+    Returns (spikes, v_final, h) as numpy fp32, [T, B, N, O] / [B, N, O]."""
+    x = torch.as_tensor(_f32(x_seq))
+    O = linear.out_features
+    w = linear.weight.detach().cpu().double()
+    b = None if linear.bias is None else linear.bias.detach().cpu().double()
+    z = F.linear(x.double(), w, b).float()
+    if bn is not None:
+        z = batch_norm(z.reshape(-1, O), bn).reshape(z.shape)
+    return lif_multistep(z, v_in, **lif_params_of(lif))
+
+
+def spike_attention_lif(q, k, v, heads, scale, lif, v_in=None):
+    """Spikformer's attention core in float64: per head
+    ((q k^T) * scale) v, then LIF over T (models/spikformer_github.py:150-156).
+    q, k, v: [T, B, N, C] spikes.  Returns (spikes, v_final, h), numpy fp32."""
+    q, k, v = (torch.as_tensor(_f32(a)).double() for a in (q, k, v))
+    T, B, N, C = q.shape
+    dh = C // heads
+
+    def split(a):
+        return a.reshape(T, B, N, heads, dh).permute(0, 1, 3, 2, 4)
+    attn = torch.matmul(split(q), split(k).transpose(-1, -2)) * scale
+    y = torch.matmul(attn, split(v)).permute(0, 1, 3, 2, 4).reshape(T, B, N, C).float()
+    return lif_multistep(y, v_in, **lif_params_of(lif))
+
+
+def spike_attention_bruteforce(q, k, v, heads, scale):
+    """The attention product from the definition with Python loops (tiny
+    inputs): y[t, b, n, h*dh + j] = sum_m (sum_i q[n, i] k[m, i]) * scale * v[m, j]."""
+    q, k, v = (np.asarray(_f32(a), dtype=np.float64) for a in (q, k, v))
+    T, B, N, C = q.shape
+    dh = C // heads
+    y = np.zeros((T, B, N, C))
+    for t in range(T):
+        for b in range(B):
+            for h in range(heads):
+                sl = slice(h * dh, (h + 1) * dh)
+                for n in range(N):
+                    for m in range(N):
+                        a = float(np.dot(q[t, b, n, sl], k[t, b, m, sl])) * scale
+                        y[t, b, n, sl] += a * v[t, b, m, sl]
+    return y
+
+
+def spikformer_forward(model, x_seq, conv_dtype=torch.float64, record=None):
+    """Spikformer forward on CPU in SpikingJelly multi-step semantics
+    (models/spikformer_github.py:175-330 with every LIF over T): SPS stages
+    Conv-BN-LIF (+ MaxPool), rpe Conv-BN-LIF + its input, tokens; blocks
+    x + SSA(x), x + MLP(x); token mean, pre-head LIF, head (float64).
+    `record`, if a dict, receives (input, spikes) per fused layer."""
+    T, B = x_seq.shape[:2]
+    sps = model.patch_embed
+
+    def rec(name, x, s):
+        if record is not None:
+            record[name] = (x, s)
+        return s
+
+    y = torch.as_tensor(_f32(x_seq))
+    for i in range(4):
+        s, _, _ = conv_bn_lif(y, getattr(sps, f"conv{i}"), getattr(sps, f"bn{i}"),
+                              getattr(sps, f"lif{i}"), conv_dtype=conv_dtype)
+        s = rec(f"patch_embed.conv{i}", y, torch.from_numpy(s))
+        pool = getattr(sps, f"pool{i}", None)
+        if pool is not None:
+            p = F.max_pool2d(s.flatten(0, 1), pool.kernel_size, pool.stride, pool.padding)
+            s = p.reshape(T, B, *p.shape[1:])
+        y = s
+    r, _, _ = conv_bn_lif(y, sps.rpe_conv, sps.rpe_bn, sps.rpe_lif, conv_dtype=conv_dtype)
+    r = rec("patch_embed.rpe_conv", y, torch.from_numpy(r) + y)
+    x = r.flatten(-2).transpose(-1, -2).contiguous()
+    for bi, blk in enumerate(model.blocks):
+        a, m = blk.attn, blk.mlp
+        p = f"blocks.{bi}"
+        qkv = [torch.from_numpy(linear_bn_lif(x, getattr(a, n), getattr(a, n + "_bn"),
+                                              getattr(a, n + "_lif"))[0]) for n in ("q", "k", "v")]
+        rec(p + ".attn.qkv", x, torch.cat(qkv, -1))
+        att = torch.from_numpy(spike_attention_lif(*qkv, a.num_heads, a.scale, a.attn_lif)[0])
+        rec(p + ".attn.core", torch.cat(qkv, -1), att)
+        pr = torch.from_numpy(linear_bn_lif(att, a.proj, a.proj_bn, a.proj_lif)[0])
+        x = rec(p + ".attn.proj", att, x + pr)
+        h = torch.from_numpy(linear_bn_lif(x, m.fc1, m.fc1_bn, m.fc1_lif)[0])
+        rec(p + ".mlp.fc1", x, h)
+        o = torch.from_numpy(linear_bn_lif(h, m.fc2, m.fc2_bn, m.fc2_lif)[0])
+        x = rec(p + ".mlp.fc2", h, x + o)
+    f = x.mean(dim=2)
+    s = torch.from_numpy(lif_multistep(f, None, **lif_params_of(model.pre_head_lif))[0])
+    w = model.head.weight.detach().cpu().double()
+    b = None if model.head.bias is None else model.head.bias.detach().cpu().double()
+    return F.linear(s.double(), w, b).float()

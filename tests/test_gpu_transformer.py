@@ -1,0 +1,195 @@
+"""Spiking transformer path (Spikformer, config C4) against the CPU oracle.
+
+Fused Linear -> BN1d -> LIF layers and the attention core under the LIF
+tolerance of tests/parity.py (bit-exact where the arithmetic is exact: the
+attention with scale 0.125 and binary Q, K, V); the concatenated QKV layer
+bit for bit against three separate layers; a small Spikformer layer by layer
+on the inputs each fused layer actually received, and its logits.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from parity import lif_parity
+
+pytestmark = pytest.mark.gpu
+
+
+def _gen(seed):
+    return torch.Generator().manual_seed(seed)
+
+
+def _triple(I, O, seed, v_threshold=1.0):
+    from catfuse_amd import snn
+    g = _gen(seed)
+    lin = torch.nn.Linear(I, O)
+    bn = torch.nn.BatchNorm1d(O).eval()
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(O, I, generator=g) * (2.0 / I) ** 0.5 * 1.5)
+        lin.bias.copy_(torch.randn(O, generator=g) * 0.1)
+        bn.running_mean.copy_(torch.randn(O, generator=g) * 0.1)
+        bn.running_var.copy_(torch.rand(O, generator=g) + 0.5)
+        bn.weight.copy_(torch.rand(O, generator=g) * 0.4 + 0.8)
+        bn.bias.copy_(torch.randn(O, generator=g) * 0.1)
+    return lin, bn, snn.LIFNode(step_mode="m", v_threshold=v_threshold)
+
+
+LINEAR_CASES = [
+    # name, T, B, N, I, O  (N = 196: 14 x 14 token grid, halo kernel; N = 10:
+    # flat tiles; N = 0: [T, B, I] input)
+    ("grid14", 4, 2, 196, 64, 96),
+    ("n10", 3, 2, 10, 96, 64),
+    ("vec", 4, 3, 0, 128, 64),
+    ("wide", 2, 2, 64, 384, 384),
+]
+
+
+@pytest.mark.parametrize("case", LINEAR_CASES, ids=[c[0] for c in LINEAR_CASES])
+def test_fused_linear_bn_lif_parity(cuda, case):
+    from catfuse_amd.transformer import FusedLinearBNLIF
+    name, T, B, N, I, O = case
+    lin, bn, lif = _triple(I, O, seed=hash(name) % 97)
+    shape = (T, B, N, I) if N else (T, B, I)
+    x = (torch.rand(shape, generator=_gen(1)) < 0.3).float()
+    f = FusedLinearBNLIF.from_sj_modules(lin, bn, lif).to(cuda)
+    y = f(x.to(cuda))
+    xs = x if N else x.unsqueeze(2)
+    s_ref, v_ref, h_ref = oracle.linear_bn_lif(xs, lin, bn, lif)
+    v = f.state.tensor.transpose(1, 2).cpu().numpy()   # state [B, O, N] -> [B, N, O]
+    yo = y.cpu().numpy() if N else y.unsqueeze(2).cpu().numpy()
+    lif_parity(yo, v, s_ref, v_ref, h_ref, what=name)
+    # residual added in the epilogue (integer-valued, read from a packed copy)
+    idv = ((torch.rand(s_ref.shape, generator=_gen(2)) < 0.5).float()
+           * torch.randint(1, 3, s_ref.shape, generator=_gen(3)).float())
+    f.reset()
+    y2 = f(x.to(cuda), identity=(idv if N else idv.squeeze(2)).to(cuda))
+    y2o = y2.cpu() if N else y2.unsqueeze(2).cpu()
+    lif_parity((y2o - idv).numpy(), None, s_ref, None, h_ref, what=name + "+residual")
+    # a second call carries the state like one longer sequence
+    f.reset()
+    a = f(x[:T // 2].to(cuda))
+    b = f(x[T // 2:].to(cuda))
+    assert torch.equal(torch.cat([a, b]).cpu(), y.cpu())
+
+
+def test_concatenated_qkv_bitwise(cuda):
+    from catfuse_amd.transformer import FusedLinearBNLIF
+    triples = [_triple(128, 128, seed=s) for s in (5, 6, 7)]
+    x = (torch.rand(4, 2, 196, 128, generator=_gen(8)) < 0.25).float().to(cuda)
+    cat = FusedLinearBNLIF.concatenated(triples).to(cuda)
+    y = cat(x)
+    for i, t in enumerate(triples):
+        f = FusedLinearBNLIF.from_sj_modules(*t).to(cuda)
+        assert torch.equal(f(x), y[..., 128 * i:128 * (i + 1)])
+
+
+@pytest.mark.parametrize("N,heads,T,scale", [(196, 2, 4, 0.125), (64, 3, 6, 0.125),
+                                             (256, 1, 2, 0.125), (196, 2, 4, 32 ** -0.5),
+                                             (37, 2, 3, 0.125)])
+def test_spike_attention_parity(cuda, N, heads, T, scale):
+    from catfuse_amd import runtime, snn
+    B, C = 2, 32 * heads
+    g = _gen(N + heads)
+    q, k, v = ((torch.rand(T, B, N, C, generator=g) < r).float() for r in (0.3, 0.2, 0.25))
+    lif = snn.LIFNode(step_mode="m", v_threshold=4.0)
+    copy = runtime.pack_tokens(torch.cat([q, k, v], -1).to(cuda), 3 * C)
+    out, v_out = runtime.spike_attention_lif(copy, T, B, N, heads, (0, C, 2 * C), scale,
+                                             v_threshold=4.0)
+    s_ref, v_ref, h_ref = oracle.spike_attention_lif(q, k, v, heads, scale, lif)
+    if scale == 0.125:
+        # integers times a power of two: every value exact on both sides
+        np.testing.assert_array_equal(out.cpu().numpy(), s_ref)
+        np.testing.assert_array_equal(v_out.cpu().numpy(), v_ref)
+    else:
+        lif_parity(out.cpu().numpy(), v_out.cpu().numpy(), s_ref, v_ref, h_ref,
+                   v_th=4.0, what="attention")
+    assert s_ref.any() and not s_ref.all()
+    # v_in carried: the second half of the sequence from the first half's state
+    out1, v1 = runtime.spike_attention_lif(
+        runtime.pack_tokens(torch.cat([q, k, v], -1)[: T // 2].to(cuda), 3 * C), T // 2, B, N,
+        heads, (0, C, 2 * C), scale, v_threshold=4.0)
+    out2, _ = runtime.spike_attention_lif(
+        runtime.pack_tokens(torch.cat([q, k, v], -1)[T // 2:].to(cuda), 3 * C), T - T // 2, B,
+        N, heads, (0, C, 2 * C), scale, v_threshold=4.0, v_in=v1)
+    assert torch.equal(torch.cat([out1, out2]).cpu(), out.cpu())
+
+
+def _small_spikformer(seed=41):
+    from catfuse_amd import snn
+    m = snn.Spikformer(img_size=32, num_classes=10, embed_dim=64, num_heads=2, depth=2, T=4,
+                       pools=(2, 3), v_threshold=1.0)
+    g = _gen(seed)
+    snn.kaiming_init(m, g)
+    snn.randomize_bn(m, g)
+    with torch.no_grad():   # keep every layer active: a stronger drive than kaiming's
+        for blk in m.blocks:
+            for lin in (blk.attn.q, blk.attn.k, blk.attn.v, blk.attn.proj, blk.mlp.fc1,
+                        blk.mlp.fc2):
+                lin.weight.mul_(3.0)
+        sps = m.patch_embed
+        for conv in [getattr(sps, f"conv{i}") for i in range(4)] + [sps.rpe_conv]:
+            conv.weight.mul_(3.0)
+    return m.eval()
+
+
+def test_spikformer_layers_and_logits(cuda):
+    import catfuse_amd
+    from catfuse_amd.transformer import FusedLinearBNLIF
+    m = _small_spikformer()
+    fused, stats = catfuse_amd.optimize(m, T=4)
+    assert stats["fused_lif_nodes"] == stats["total_lif_nodes"] - 1   # pre_head_lif
+    # per fused Linear-BN1d-LIF layer: the oracle on the input it received
+    recs = []
+    origs = {}
+    for bi, (fb, ob) in enumerate(zip(fused.blocks, m.blocks)):
+        a, mm = ob.attn, ob.mlp
+        origs[id(fb.attn.qkv)] = [(a.q, a.q_bn, a.q_lif), (a.k, a.k_bn, a.k_lif),
+                                  (a.v, a.v_bn, a.v_lif)]
+        origs[id(fb.attn.proj)] = [(a.proj, a.proj_bn, a.proj_lif)]
+        origs[id(fb.mlp.fc1)] = [(mm.fc1, mm.fc1_bn, mm.fc1_lif)]
+        origs[id(fb.mlp.fc2)] = [(mm.fc2, mm.fc2_bn, mm.fc2_lif)]
+    handles = []
+    for mod in fused.modules():
+        if isinstance(mod, FusedLinearBNLIF):
+            def hook(md, args, kwargs, out):
+                ident = kwargs.get("identity")
+                recs.append((id(md), args[0].detach().cpu(),
+                             None if ident is None else ident.detach().cpu(), out.detach().cpu()))
+            handles.append(mod.register_forward_hook(hook, with_kwargs=True))
+    img = torch.randn(2, 3, 32, 32, generator=_gen(42))
+    x = img.unsqueeze(0).expand(4, 2, 3, 32, 32)
+    with torch.no_grad():
+        y = fused(x.to(cuda))
+    torch.cuda.synchronize()
+    for h in handles:
+        h.remove()
+    catfuse_amd.check_status()
+    assert len(recs) == 8
+    flips = 0
+    by_id = {}
+    for mid, xin, ident, out in recs:
+        s_ref = np.concatenate([oracle.linear_bn_lif(xin, *t)[0] for t in origs[mid]], -1)
+        h_ref = np.concatenate([oracle.linear_bn_lif(xin, *t)[2] for t in origs[mid]], -1)
+        spikes = out - ident if ident is not None else out
+        flips += lif_parity(spikes.numpy(), None, s_ref, None, h_ref, what="linear")
+        by_id[mid] = (xin, out)
+    # the attention core on the Q, K, V its block produced
+    for fb, ob in zip(fused.blocks, m.blocks):
+        qkv_in, qkv = by_id[id(fb.attn.qkv)]
+        att, _ = by_id[id(fb.attn.proj)]
+        C = ob.attn.dim
+        s_ref, _, h_ref = oracle.spike_attention_lif(qkv[..., :C], qkv[..., C:2 * C],
+                                                     qkv[..., 2 * C:], ob.attn.num_heads,
+                                                     ob.attn.scale, ob.attn.attn_lif)
+        flips += lif_parity(att.numpy(), None, s_ref, None, h_ref, what="attention")
+    activity = [float(out.abs().sum()) for _, _, _, out in recs]
+    assert min(activity) > 0, "a layer's output is all zero: the test would not exercise it"
+    y_ref = oracle.spikformer_forward(m, x)
+    if flips == 0:
+        np.testing.assert_allclose(y.cpu().numpy(), y_ref.numpy(), rtol=1e-4, atol=1e-4)
+    snn_reset = catfuse_amd.snn.functional.reset_net
+    snn_reset(fused)
+    with torch.no_grad():
+        y2 = fused(x.to(cuda))
+    assert torch.equal(y, y2)

@@ -227,3 +227,65 @@ def test_bn_fold_matches_torch_batch_norm():
     folded = z * sc.view(1, -1, 1, 1) + sh.view(1, -1, 1, 1)
     np.testing.assert_allclose(folded.numpy(), oracle.batch_norm(z, bn).numpy(), rtol=1e-5,
                                atol=1e-6)
+
+
+# ---------------------------------------------------------------------------
+# spiking transformer restatements
+# ---------------------------------------------------------------------------
+
+def _lin_bn(I, O, seed):
+    g = torch.Generator().manual_seed(seed)
+    lin = torch.nn.Linear(I, O)
+    bn = torch.nn.BatchNorm1d(O).eval()
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(O, I, generator=g) * (2.0 / I) ** 0.5)
+        lin.bias.copy_(torch.randn(O, generator=g) * 0.1)
+        bn.running_mean.copy_(torch.randn(O, generator=g) * 0.1)
+        bn.running_var.copy_(torch.rand(O, generator=g) + 0.5)
+        bn.weight.copy_(torch.rand(O, generator=g) * 0.4 + 0.8)
+        bn.bias.copy_(torch.randn(O, generator=g) * 0.1)
+    return lin, bn
+
+
+def test_linear_bn_lif_equals_1x1_conv_formulation():
+    """Linear -> BN1d -> LIF over tokens equals Conv1x1 -> BN2d -> LIF over
+    the token grid (an independent formulation through conv_bn_lif), bit for
+    bit: both take the float64 product rounded to fp32 and torch's eval BN."""
+    from catfuse_amd import snn
+    T, B, Hg, Wg, I, O = 3, 2, 3, 4, 24, 40
+    lin, bn1 = _lin_bn(I, O, seed=1)
+    lif = snn.LIFNode(step_mode="m")
+    x = (torch.rand(T, B, Hg * Wg, I, generator=torch.Generator().manual_seed(2)) < 0.3).float()
+    s1, v1, h1 = oracle.linear_bn_lif(x, lin, bn1, lif)
+    conv = torch.nn.Conv2d(I, O, 1, bias=True)
+    bn2 = torch.nn.BatchNorm2d(O).eval()
+    with torch.no_grad():
+        conv.weight.copy_(lin.weight.view(O, I, 1, 1))
+        conv.bias.copy_(lin.bias)
+        for n in ("weight", "bias", "running_mean", "running_var"):
+            getattr(bn2, n).copy_(getattr(bn1, n))
+    xc = x.reshape(T, B, Hg, Wg, I).permute(0, 1, 4, 2, 3)
+    s2, v2, h2 = oracle.conv_bn_lif(xc, conv, bn2, lif)
+    to_tok = lambda a: np.moveaxis(a, -3, -1).reshape(*a.shape[:-3], Hg * Wg, O)
+    np.testing.assert_array_equal(s1, to_tok(s2))
+    np.testing.assert_array_equal(h1, to_tok(h2))
+    np.testing.assert_array_equal(v1, to_tok(v2))
+
+
+def test_spike_attention_oracle_pins():
+    """The float64 attention equals the definition in loops, and the integer
+    identity (Q K^T) V = Q (K^T V) holds (the reordering the kernel uses)."""
+    from catfuse_amd import snn
+    g = torch.Generator().manual_seed(3)
+    T, B, N, heads = 2, 2, 7, 2
+    q, k, v = ((torch.rand(T, B, N, 64, generator=g) < 0.4).float() for _ in range(3))
+    for scale in (0.125, 32 ** -0.5):
+        y = oracle.spike_attention_bruteforce(q, k, v, heads, scale)
+        lif = snn.LIFNode(step_mode="m", v_threshold=2.0)
+        s, vf, h = oracle.spike_attention_lif(q, k, v, heads, scale, lif)
+        # the charge of the first step from v = 0 with tau = 2 is z / 2
+        np.testing.assert_allclose(h[0], (y[0] * 0.5).astype(np.float32), rtol=1e-6)
+        s_ref, _, _ = oracle.lif_multistep(torch.from_numpy(y).float(), None, v_threshold=2.0)
+        np.testing.assert_array_equal(s, s_ref)
+    qi, ki, vi = (a.reshape(T, B, N, heads, 32).permute(0, 1, 3, 2, 4).long() for a in (q, k, v))
+    assert torch.equal((qi @ ki.transpose(-1, -2)) @ vi, qi @ (ki.transpose(-1, -2) @ vi))
