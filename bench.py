@@ -39,10 +39,16 @@ PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
 PEAK_HBM_GBPS = 8000.0
 
 
-def build_model(num_classes=1000, seed=0):
+def build_model(num_classes=1000, seed=0, workload="sew_resnet18"):
     import torch
     from catfuse_amd import snn
     g = torch.Generator().manual_seed(seed)
+    if workload == "spikformer_8_384":
+        # config C4: random init (seeded kaiming weights, config-0 BN statistics)
+        m = snn.spikformer_8_384(num_classes=num_classes, T=4)
+        snn.kaiming_init(m, g)
+        snn.randomize_bn(m, g)
+        return m.eval()
     m = snn.sew_resnet18(num_classes=num_classes, cnf="ADD", tau=2.0, v_threshold=1.0,
                          v_reset=0.0)
     snn.functional.set_step_mode(m, "m")
@@ -115,24 +121,24 @@ def measure_tails(dev, reps=20):
     return out
 
 
-def cpu_baseline(model, T, image, budget_s=12.0):
+def cpu_baseline(model, T, image, budget_s=12.0, forward=None):
     """Oracle forward (fp32 torch CPU conv + eval BN + C LIF, SpikingJelly
     multi-step semantics) on this host: 1 warm-up image, then batches of 2
     images until about budget_s seconds have been timed."""
     import torch
     import oracle
+    fwd = forward or oracle.sew_resnet_forward
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(1)
     x1 = torch.randn(1, 3, image, image, generator=g)
-    oracle.sew_resnet_forward(model, x1.unsqueeze(0).expand(T, 1, 3, image, image),
-                              conv_dtype=torch.float32)
+    fwd(model, x1.unsqueeze(0).expand(T, 1, 3, image, image), conv_dtype=torch.float32)
     x2 = torch.randn(2, 3, image, image, generator=g)
     xs = x2.unsqueeze(0).expand(T, 2, 3, image, image)
     imgs, t_total = 0, 0.0
     while t_total < budget_s:
         t0 = time.perf_counter()
-        oracle.sew_resnet_forward(model, xs, conv_dtype=torch.float32)
+        fwd(model, xs, conv_dtype=torch.float32)
         t_total += time.perf_counter() - t0
         imgs += 2
     return {"value": round(imgs / t_total, 3), "unit": "images/s", "cores": threads,
@@ -154,6 +160,10 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=12.0)
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of the captured HIP graph")
+    ap.add_argument("--workload", default="sew_resnet18",
+                    choices=["sew_resnet18", "spikformer_8_384"],
+                    help="sew_resnet18: the headline metric (config C3); spikformer_8_384: "
+                         "config C4 (spiking transformer), its own metric line")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: every GPU box in this setup has a single "
@@ -167,7 +177,8 @@ def main():
 
     dev = torch.device("cuda", 0)
     T, B, HW = args.T, args.batch, args.image
-    model = build_model()
+    spikformer = args.workload == "spikformer_8_384"
+    model = build_model(workload=args.workload)
     fused, stats = catfuse_amd.optimize(model, device=dev, T=T)
     fused.eval()
     g = torch.Generator(device=dev).manual_seed(0)
@@ -254,6 +265,26 @@ def main():
                       "ms_per_step": round(v["ms_total"] / args.steps, 4)}
                   for k, v in kern.items()}
 
+    if spikformer:
+        # the token linears (1x1 convs over each image's token grid) dominate
+        l_ms, l_fl, _, l_n = agg(["linear_tokens"])
+        lz_ms, _, _, lz_n = agg(["linear_tokens_staticzero"])
+        a_ms, a_fl, a_b, a_n = agg(["spike_attention"])
+        ach = l_fl / (l_ms * 1e-3) / 1e12 if l_ms else 0.0
+        roofline = {"kernel": "conv_halo_kernel 1x1 (cf_conv_mfma: fused Linear-BN1d-LIF over the "
+                              "token grid), launches that run the MFMA K loop",
+                    "bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP16_TFLOPS,
+                    "unit": "TFLOP/s", "frac": round(ach / PEAK_FP16_TFLOPS, 4), "traffic": None,
+                    "flops_per_launch_avg": l_fl // max(1, l_n),
+                    "us_per_launch_avg": round(l_ms * 1e3 / max(1, l_n), 2),
+                    "launches_per_step": l_n // args.steps,
+                    "staticzero_launches_per_step": lz_n // args.steps}
+        a_gbps = a_b / (a_ms * 1e-3) / 1e9 if a_ms else 0.0
+        staticzero = {"kernel": "spike_attention_kernel (cf_spike_attention_lif)",
+                      "launches_per_step": a_n // args.steps,
+                      "us_per_launch_avg": round(a_ms * 1e3 / max(1, a_n), 2),
+                      "achieved": round(a_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                      "frac": round(a_gbps / PEAK_HBM_GBPS, 4)}
     result = {
         "metric": METRIC, "value": round(ips, 2), "unit": "images/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
@@ -269,10 +300,24 @@ def main():
         "staticzero_convs": staticzero,
         "kernels": per_kernel,
     }
-    if not args.no_tails:
+    if spikformer:
+        result["metric"] = "Spikformer-8-384 T=4 images/s on 1 MI355X (config C4)"
+        result["config"] = {"workload": "spikformer_8_384_T4_B32_224", "T": T, "batch": B,
+                            "image": [3, HW, HW], "tokens": 196, "dim": 384, "heads": 12,
+                            "blocks": 8, "encoding": "direct (input repeated over T)",
+                            "fused_lif_nodes": stats["fused_lif_nodes"],
+                            "total_lif_nodes": stats["total_lif_nodes"]}
+        result["dtype"] = ("fp32 (linears/convs: fp16 hi/lo split weights x fp16-exact spikes on "
+                           "MFMA, fp32 acc; attention: exact integer Q(K^T V), one fp32 rounding)")
+        del result["staticzero_convs"]
+        result["attention"] = staticzero
+    if not args.no_tails and not spikformer:
         result["lif_tails"] = measure_tails(dev)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(model, T, HW, args.cpu_budget)
+        import oracle
+        result["cpu_baseline"] = cpu_baseline(
+            model, T, HW, args.cpu_budget,
+            forward=oracle.spikformer_forward if spikformer else None)
     print(json.dumps(result), flush=True)
 
 

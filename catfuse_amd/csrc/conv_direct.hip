@@ -26,7 +26,7 @@ struct DirectArgs {
   const float* beta;
   const float* v_in;
   float* v_out;
-  float* out;  // [T][B][Cout][Ho][Wo]
+  float* out;  // [T][B][Cout][Ho][Wo] or null (then out_nhwc is set)
   _Float16* out_nhwc;  // [T*B][Ho][Wo][cp_out] or null
   int cp_out;
   int T, B, Cin, Cout, H, W, Ho, Wo, KH, KW, stride, pad, x_img_tstride;
@@ -75,6 +75,8 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(DirectArgs a) {
   if (dedupe) conv_pixel<COB>(a, b, oh, ow, co0, acc);
   for (int t = 0; t < a.T; ++t) {
     if (!dedupe) conv_pixel<COB>(a, t * a.x_img_tstride + b, oh, ow, co0, acc);
+    typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+    h8v oh16[(COB + 7) / 8];
 #pragma unroll
     for (int j = 0; j < COB; ++j) {
       const int co = co0 + j;
@@ -88,8 +90,20 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(DirectArgs a) {
         ov = lif_fire_reset(vv, a.lif);
         v[j] = vv;
       }
-      a.out[o] = ov;
-      if (a.out_nhwc) store_nhwc(a.out_nhwc, a.cp_out, (size_t)t * a.B + b, HoWo, p, co, ov);
+      if (a.out) a.out[o] = ov;
+      oh16[j / 8][j % 8] = (_Float16)ov;
+    }
+    if (a.out_nhwc) {
+      _Float16* dst = a.out_nhwc + ((size_t)(t * a.B + b) * HoWo + p) * a.cp_out + co0;
+      if constexpr (COB % 8 == 0) {
+        // the pixel's COB channels as 16-byte chunks (co0 and cp_out are
+        // multiples of 8)
+#pragma unroll
+        for (int j = 0; j < COB; j += 8) *reinterpret_cast<h8v*>(dst + j) = oh16[j / 8];
+      } else {
+#pragma unroll
+        for (int j = 0; j < COB; ++j) dst[j] = oh16[j / 8][j % 8];
+      }
     }
     if (a.out_nhwc && co0 + COB == a.Cout)
       for (int co = a.Cout; co < a.cp_out; ++co)
@@ -118,7 +132,7 @@ CF_API int cf_conv_direct(const float* x, const float* w, const float* alpha, co
                           int64_t KH, int64_t KW, int64_t stride, int64_t pad,
                           int64_t x_img_tstride, int epilogue, double tau, double v_th,
                           double v_reset, int hard_reset, int decay_input, void* stream) {
-  if (!x || !w || !alpha || !beta || !out || T <= 0 || B <= 0 || Cin <= 0 || Cout <= 0 ||
+  if (!x || !w || !alpha || !beta || (!out && !out_nhwc) || T <= 0 || B <= 0 || Cin <= 0 || Cout <= 0 ||
       H <= 0 || W <= 0 || KH <= 0 || KW <= 0 || stride <= 0 || pad < 0 || x_img_tstride < 0 ||
       B > 65535)
     return (int)hipErrorInvalidValue;
@@ -129,7 +143,7 @@ CF_API int cf_conv_direct(const float* x, const float* w, const float* alpha, co
   DirectArgs a;
   a.x = x; a.w = w; a.alpha = alpha; a.beta = beta; a.v_in = v_in; a.v_out = v_out; a.out = out;
   a.out_nhwc = (_Float16*)out_nhwc; a.cp_out = (int)cp_out;
-  if (out_nhwc && cp_out < Cout) return (int)hipErrorInvalidValue;
+  if (out_nhwc && (cp_out < Cout || cp_out % 8 != 0)) return (int)hipErrorInvalidValue;
   a.T = (int)T; a.B = (int)B; a.Cin = (int)Cin; a.Cout = (int)Cout; a.H = (int)H; a.W = (int)W;
   a.Ho = (int)Ho; a.Wo = (int)Wo; a.KH = (int)KH; a.KW = (int)KW; a.stride = (int)stride;
   a.pad = (int)pad; a.x_img_tstride = (int)x_img_tstride;

@@ -315,7 +315,7 @@ void conv_halo_kernel(HaloArgs a) {
           const int c = tid + 256 * i;
           const int px = c / CH8Z, part = c % CH8Z;
           const int py = px / TW, pxx = px % TW;
-          const bool ok = (oh0 + py < a.Ho) & (ow0 + pxx < a.Wo);
+          const bool ok = (oh0 + py < a.Ho) & (ow0 + pxx < a.Wo) & (cout0 + part * 8 < a.Cout);
           const int pix = (oh0 + py) * a.Wo + ow0 + pxx;
           const h8 sp = *reinterpret_cast<const h8*>(&srow[t * BM + part * 8]);
           const h8 idv = __builtin_bit_cast(
@@ -340,8 +340,8 @@ void conv_halo_kernel(HaloArgs a) {
         for (int k = 0; k < VPT; ++k) {
           const int c = cg * VPT + k;
           __builtin_amdgcn_raw_buffer_store_b32(
-              __float_as_uint(vrow[c]), rv, ok ? (uint32_t)(((cout0 + c) * HoWo + pix) * 4) : HALO_OOB,
-              0, 0);
+              __float_as_uint(vrow[c]), rv,
+              (ok && cout0 + c < a.Cout) ? (uint32_t)(((cout0 + c) * HoWo + pix) * 4) : HALO_OOB, 0, 0);
         }
       }
       publish_count();
@@ -728,7 +728,7 @@ void conv_halo_kernel(HaloArgs a) {
             pk = idh + sph;
             if (a.nz_out) {
               const u32x2 pw = __builtin_bit_cast(u32x2, pk);
-              anyw |= n_ok[nt] ? (pw[0] | pw[1]) : 0u;
+              anyw |= (n_ok[nt] && col + 8 * r4 < a.Cout) ? (pw[0] | pw[1]) : 0u;
             }
           } else {
             const int ob = ((tt * a.B + b) * a.Cout + col) * HoWo;
@@ -773,8 +773,8 @@ void conv_halo_kernel(HaloArgs a) {
         const _Float16* ostage = obuf + (t % NOBUF) * OSTEP;
         _Float16* obase = a.out_nhwc + (size_t)((tb0 + t) * a.B + b) * HoWo * a.cp_out;
         if constexpr (LEAN) {
-          // every chunk index is below BN * CH8 and every channel real; the
-          // hardware drops pixels outside the output
+          // every chunk index is below BN * CH8; the hardware drops pixels
+          // outside the output and channels >= Cout
           static_assert(BN * CH8 % 256 == 0, "lean copy-out assumes whole passes");
           const __amdgpu_buffer_rsrc_t ro = halo_rsrc(obase, (uint32_t)(HoWo * a.cp_out * 2));
 #pragma unroll
@@ -782,7 +782,7 @@ void conv_halo_kernel(HaloArgs a) {
             const int c = opaque(tid) + 256 * i;
             const int px = c / CH8, part = c % CH8;
             const int py = px / TW, pxx = px % TW;
-            const bool ok = (oh0 + py < a.Ho) & (ow0 + pxx < a.Wo);
+            const bool ok = (oh0 + py < a.Ho) & (ow0 + pxx < a.Wo) & (cout0 + part * 8 < a.Cout);
             const uint32_t off =
                 ok ? (uint32_t)((((oh0 + py) * a.Wo + ow0 + pxx) * a.cp_out + cout0 + part * 8) * 2)
                    : HALO_OOB;
@@ -805,7 +805,7 @@ void conv_halo_kernel(HaloArgs a) {
     }
     // The block's final membrane potentials (the layer's state after the last block).
     if (LEAN && a.v_out) {
-      // every channel of a lean tile is real; pixels outside the output are dropped
+      // pixels outside the output and channels >= Cout are dropped
       const __amdgpu_buffer_rsrc_t rv =
           halo_rsrc(a.v_out + (size_t)b * a.Cout * HoWo, (uint32_t)(a.Cout * HoWo * 4));
 #pragma unroll
@@ -813,7 +813,8 @@ void conv_halo_kernel(HaloArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int dc = 8 * (r >> 2) + (r & 3);
-          const uint32_t off = n_ok[nt] ? (uint32_t)(((col + dc) * HoWo + e_off[nt]) * 4) : HALO_OOB;
+          const uint32_t off = (n_ok[nt] && col + dc < a.Cout)
+                                   ? (uint32_t)(((col + dc) * HoWo + e_off[nt]) * 4) : HALO_OOB;
           __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v[nt][r]), rv, off, 0, 0);
         }
     } else if (EPI == EPI_LIF && a.v_out) {
@@ -836,7 +837,9 @@ template <int TH, int TW, int S, int K = 3>
 hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
   dim3 grid((unsigned)(a.B * a.GH * a.GW * (a.Coutp / 64)));
   const dim3 block(256);
-  const bool lean = epi == EPI_LIF && !a.out && !a.identity && a.Cout % 64 == 0;
+  // lean: no fp32 output, no fp32 identity, whole 32-channel groups (the
+  // stores drop channels >= Cout of a partly real 64-channel tile)
+  const bool lean = epi == EPI_LIF && !a.out && !a.identity && a.Cout % 32 == 0;
   const bool oneb = a.T <= halo_tb<S, K>();
   if (epi == EPI_Z) {
     hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_Z, LM_GENERIC, false, false>), grid,

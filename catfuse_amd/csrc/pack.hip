@@ -247,6 +247,53 @@ __global__ __launch_bounds__(256) void tokens_to_f32_kernel(
   }
 }
 
+// Max pooling of an fp16 NHWC copy (the spikes a fused conv wrote):
+// out[n][oh][ow][c] = max over the k x k window (stride s, padding p; padded
+// positions ignored, as torch's max_pool2d) of xp[n][ih][iw][c].  The max of
+// spike values is exact in fp16.  One 8-channel chunk of one output pixel
+// per thread; the nonzero count of the output is published (count block).
+__global__ __launch_bounds__(256) void maxpool_nhwc_kernel(
+    const _Float16* __restrict__ xp, _Float16* __restrict__ out, int64_t NB, int H, int W,
+    int Ho, int Wo, int cp, int k, int s, int p, unsigned long long* __restrict__ nnz) {
+  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+  __shared__ unsigned any_sh[4];
+  const int nc8 = cp / 8;
+  const int64_t units = NB * Ho * Wo * nc8;
+  uint32_t anyw = 0u;
+  for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < units;
+       u += (int64_t)gridDim.x * 256) {
+    const int c8 = (int)(u % nc8);
+    const int64_t pix = u / nc8;
+    const int ow = (int)(pix % Wo), oh = (int)((pix / Wo) % Ho);
+    const int64_t n = pix / ((int64_t)Wo * Ho);
+    h8 m;
+    bool first = true;
+    for (int dy = 0; dy < k; ++dy) {
+      const int ih = oh * s - p + dy;
+      if (ih < 0 || ih >= H) continue;
+      for (int dx = 0; dx < k; ++dx) {
+        const int iw = ow * s - p + dx;
+        if (iw < 0 || iw >= W) continue;
+        const h8 v = *reinterpret_cast<const h8*>(xp + ((n * H + ih) * W + iw) * cp + c8 * 8);
+        if (first) {
+          m = v;
+          first = false;
+        } else {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) m[j] = v[j] > m[j] ? v[j] : m[j];
+        }
+      }
+    }
+    const uint4 w = __builtin_bit_cast(uint4, m);
+    anyw |= (w.x | w.y | w.z | w.w) & 0x7fff7fffu;
+    *reinterpret_cast<h8*>(out + pix * cp + c8 * 8) = m;
+  }
+  if (nnz) {
+    const bool any = cf_wg_any(anyw != 0u, any_sh);
+    if (threadIdx.x == 0) cf_count_publish(nnz, any ? 1ull : 0ull, blockIdx.x, gridDim.x);
+  }
+}
+
 __global__ void route_kernel(const unsigned long long* __restrict__ nnz, int64_t numel,
                              double sparse_threshold, int32_t* __restrict__ route) {
   if (threadIdx.x == 0 && blockIdx.x == 0) {
@@ -344,6 +391,24 @@ CF_API int cf_tokens_to_f32(const void* xp, float* out, int64_t rows, int64_t C,
   const unsigned grid = (unsigned)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
   hipLaunchKernelGGL(tokens_to_f32_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
                      (const _Float16*)xp, out, rows, (int)C, (int)cp);
+  return (int)hipGetLastError();
+}
+
+CF_API int cf_maxpool_nhwc(const void* xp, void* out, int64_t NB, int64_t H, int64_t W,
+                           int64_t cp, int64_t kernel_size, int64_t stride, int64_t padding,
+                           unsigned long long* nz_out, void* stream) {
+  if (!xp || !out || NB < 0 || H <= 0 || W <= 0 || cp <= 0 || cp % 8 != 0 || kernel_size <= 0 ||
+      stride <= 0 || padding < 0 || 2 * padding > kernel_size || NB * H * W * cp > ((int64_t)1 << 40))
+    return (int)hipErrorInvalidValue;
+  const int64_t Ho = (H + 2 * padding - kernel_size) / stride + 1;
+  const int64_t Wo = (W + 2 * padding - kernel_size) / stride + 1;
+  if (Ho <= 0 || Wo <= 0) return (int)hipErrorInvalidValue;
+  if (NB == 0) return 0;
+  const int64_t units = NB * Ho * Wo * (cp / 8);
+  const unsigned grid = (unsigned)((units + 255) / 256 < 4096 ? (units + 255) / 256 : 4096);
+  hipLaunchKernelGGL(maxpool_nhwc_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                     (const _Float16*)xp, (_Float16*)out, NB, (int)H, (int)W, (int)Ho, (int)Wo,
+                     (int)cp, (int)kernel_size, (int)stride, (int)padding, nz_out);
   return (int)hipGetLastError();
 }
 

@@ -57,7 +57,7 @@ class SparseFlow(HipConvImplementation):
         r = self.runner(spec, params, x.device)
         v_in = state.peek((B, spec.out_channels, Ho, Wo), x.device)
         if self.input_is_analog(x):
-            spikes, v_out = r.run_direct(x, v_in)
+            spikes, v_out = r.run_direct(x, v_in, emit_nhwc=True)
         else:
             sparse = self.route_geometry(spec, x.shape[3], x.shape[4])
             spikes, v_out = r.run_mfma(x.contiguous(), v_in, sparse=sparse,

@@ -59,7 +59,7 @@ class StreamFuse(HipConvImplementation):
         if self.input_is_analog(x):
             if identity is not None:
                 raise NotImplementedError("identity epilogue needs fp16-exact inputs")
-            spikes, v_out = r.run_direct(x, v_in)
+            spikes, v_out = r.run_direct(x, v_in, emit_nhwc=True)
         else:
             spikes, v_out = r.run_mfma(x.contiguous(), v_in, identity=identity,
                                        identity_mode=identity_mode, static_zero=True)

@@ -445,6 +445,32 @@ def global_avgpool_nhwc(xp: torch.Tensor, C: int, out: Optional[torch.Tensor] = 
     return y
 
 
+def maxpool_nhwc(x: torch.Tensor, kernel_size: int, stride: int, padding: int,
+                 gen_cell: Optional[list] = None, nz_out: Optional[torch.Tensor] = None):
+    """MaxPool2d of a fused layer's output x [T, B, C, H, W] read from its
+    fp16 NHWC copy; returns a lazy output carrying the pooled copy (and, with
+    nz_out and gen_cell, its count block), or None when x has no copy."""
+    T, B, C, H, W = x.shape
+    xp = shadow_of(x, (T * B, H, W, pad32(C)))
+    if xp is None:
+        return None
+    _require_block(nz_out)
+    Ho = (H + 2 * padding - kernel_size) // stride + 1
+    Wo = (W + 2 * padding - kernel_size) // stride + 1
+    cp = xp.shape[-1]
+    out = torch.empty((T * B, Ho, Wo, cp), dtype=torch.float16, device=x.device)
+    ev = _t0()
+    check(_hip.lib().cf_maxpool_nhwc(ptr(xp), ptr(out), T * B, H, W, cp, kernel_size, stride,
+                                     padding, ptr(nz_out), _hip.stream(x.device)),
+          "cf_maxpool_nhwc")
+    _t1("maxpool_nhwc", ev, nbytes=2 * T * B * (H * W + Ho * Wo) * cp)
+    y = lazy_output((T, B, C, Ho, Wo), out, x.device)
+    if nz_out is not None and gen_cell is not None:
+        gen_cell[0] += 1
+        attach_count(y, nz_out, gen_cell)
+    return y
+
+
 def spike_attention_lif(qkv: torch.Tensor, T: int, B: int, N: int, heads: int, offsets,
                         scale: float, tau=2.0, v_threshold=1.0, v_reset=0.0, decay_input=True,
                         v_in: Optional[torch.Tensor] = None, want_v_out=True,
@@ -802,7 +828,6 @@ class ConvLIFRunner:
         Ho, Wo = self.out_hw(H, W)
         if v_in is not None:
             require_gpu_tensor(v_in, "v_in")
-        out = torch.empty((T, B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
         # the halo kernel carries the membrane state between its time blocks
         # (2 or 4 steps) through v_out, so it gets one whenever T > 2
         v_out = (torch.empty((B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
@@ -810,17 +835,22 @@ class ConvLIFRunner:
         cp_out = pad32(self.Cout)
         nhwc = (torch.empty((T * B, Ho, Wo, cp_out), dtype=torch.float16, device=dev)
                 if (emit_nhwc and epilogue == EPI_LIF) else None)
+        if nhwc is not None:
+            # spikes written as the NHWC copy only, fp32 on first outside read
+            out = lazy_output((T, B, self.Cout, Ho, Wo), nhwc, dev)
+            out_ptr = None
+        else:
+            out = torch.empty((T, B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
+            out_ptr = ptr(out)
         ev = _t0()
         rc = _hip.lib().cf_conv_direct(
             ptr(xb), ptr(self._w_f32), ptr(self.alpha_direct), ptr(self.beta_direct), ptr(v_in),
-            ptr(v_out), ptr(out), ptr(nhwc), cp_out, T, B, C, self.Cout, H, W, Ho, Wo, self.KH,
+            ptr(v_out), out_ptr, ptr(nhwc), cp_out, T, B, C, self.Cout, H, W, Ho, Wo, self.KH,
             self.KW, self.stride, self.padding, tstride, int(epilogue), *self.lif,
             _hip.stream(dev))
         check(rc, "cf_conv_direct")
         _t1("conv_direct", ev, flops=2 * (1 if tstride == 0 else T) * B * Ho * Wo * self.Cout *
             C * self.KH * self.KW)
-        if nhwc is not None:
-            attach_shadow(out, nhwc)
         return out, v_out
 
     # -- fused stem: Conv -> BN -> LIF -> MaxPool(3, 2, 1) -------------------

@@ -22,8 +22,8 @@ import torch
 import torch.nn as nn
 
 from catfuse_amd.patterns import (CTFPattern, PartialFusionConvBNLIF, fold_bn, lif_params)
-from catfuse_amd.runtime import (ConvLIFRunner, count_of, lazy_tokens, pad32, shadow_of,
-                                 spike_attention_lif, token_shadow)
+from catfuse_amd.runtime import (ConvLIFRunner, count_block, count_of, lazy_tokens, maxpool_nhwc,
+                                 pad32, shadow_of, spike_attention_lif, token_shadow)
 from catfuse_amd.state import StateBuffer
 
 
@@ -217,16 +217,34 @@ class CTFSpikformerSPS(CTFPattern):
         self.pools = nn.ModuleList([p if p is not None else nn.Identity() for p in pools])
         self._pooled = [p is not None for p in pools]
         self.rpe = rpe
+        self._pool_gen = [[0] for _ in pools]   # calls that published each pool's count
+        self._pool_blocks = {}
+
+    def _pool_block(self, i, device):
+        blk = self._pool_blocks.get((i, device))
+        if blk is None:
+            blk = count_block(device)
+            self._pool_blocks[(i, device)] = blk
+        return blk
 
     def forward(self, x):
         T, B = x.shape[:2]
         y = x
-        for stage, pool, pooled in zip(self.stages, self.pools, self._pooled):
+        for i, (stage, pool, pooled) in enumerate(zip(self.stages, self.pools, self._pooled)):
             y = stage(y)
             if pooled:
-                p = nn.functional.max_pool2d(y.flatten(0, 1), pool.kernel_size, pool.stride,
-                                             pool.padding)
-                y = p.reshape(T, B, *p.shape[1:])
+                k, st, pd = (int(v if isinstance(v, int) else v[0])
+                             for v in (pool.kernel_size, pool.stride, pool.padding))
+                yp = None
+                if y.is_cuda and 2 * pd <= k:
+                    # pool the fp16 NHWC copy (exact for spikes), keep it as a copy
+                    yp = maxpool_nhwc(y, k, st, pd, self._pool_gen[i],
+                                      self._pool_block(i, y.device))
+                if yp is None:
+                    p = nn.functional.max_pool2d(y.flatten(0, 1), pool.kernel_size,
+                                                 pool.stride, pool.padding)
+                    yp = p.reshape(T, B, *p.shape[1:])
+                y = yp
         r = self.rpe(y, sew_identity=y)
         C, H, W = r.shape[2:]
         copy = shadow_of(r, (T * B, H, W, pad32(C)))

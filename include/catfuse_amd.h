@@ -156,6 +156,17 @@ int cf_spike_attention_lif(const void* q, const void* k, const void* v, int64_t 
                            double scale, double tau, double v_th, double v_reset, int hard_reset,
                            int decay_input, void* stream);
 
+/* MaxPool2d(kernel_size, stride, padding) of an fp16 NHWC copy xp
+ * [NB][H][W][cp] -> out [NB][Ho][Wo][cp] (padded positions ignored, as
+ * torch's max_pool2d; 2*padding <= kernel_size so every window has an input);
+ * nz_out (nullable) receives the output's count block.  Exact for spikes.
+ * Replaces the MaxPool2d between fused Conv-BN-LIF stages of
+ * models/spikformer_github.py:196-241 (SPS), which the reference runs in
+ * torch on the fp32 spikes. */
+int cf_maxpool_nhwc(const void* xp, void* out, int64_t NB, int64_t H, int64_t W, int64_t cp,
+                    int64_t kernel_size, int64_t stride, int64_t padding,
+                    unsigned long long* nz_out, void* stream);
+
 /* route = ZERO if the count block's published count k (nnz[1]) is 0, SPARSE
  * if 1 - k/numel > sparse_threshold (in double), else DENSE.  Replaces the host decision at
  * catfuse/sparseflow/ops/st_fusion_conv_bn_lif.py:510-524. */

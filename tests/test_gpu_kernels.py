@@ -244,6 +244,7 @@ OUTPUT_COUNT_CASES = [
     ("ds", 32, 64, 128, 3, 1, 2, 0, 16, 0),
     ("flat", 32, 64, 64, 5, 5, 1, 2, 12, 0),
     ("tile8x16", 32, 64, 64, 3, 3, 1, 1, 56, 16),
+    ("c96", 32, 96, 96, 3, 3, 1, 1, 16, 0),
 ]
 
 
@@ -296,6 +297,7 @@ STATICZERO_CASES = [
     ("s2", 64, 128, 3, 2, 1, 16, 4, 0),
     ("ds", 64, 128, 1, 2, 0, 16, 4, 0),
     ("tile8x16", 32, 64, 3, 1, 1, 56, 4, 16),
+    ("c96", 64, 96, 3, 1, 1, 12, 4, 0),
 ]
 
 

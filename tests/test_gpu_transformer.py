@@ -193,3 +193,28 @@ def test_spikformer_layers_and_logits(cuda):
     with torch.no_grad():
         y2 = fused(x.to(cuda))
     assert torch.equal(y, y2)
+
+
+@pytest.mark.parametrize("shape,k,s,p", [((3, 2, 40, 17, 23), 3, 2, 1), ((2, 2, 64, 8, 8), 2, 2, 0),
+                                         ((2, 1, 96, 9, 9), 3, 1, 1)])
+def test_maxpool_nhwc_bitwise(cuda, shape, k, s, p):
+    """The NHWC max pool of a fused output equals torch's max_pool2d of the
+    fp32 tensor, and publishes its output's count block."""
+    from catfuse_amd import runtime
+    T, B, C, H, W = shape
+    v = ((torch.rand(shape, generator=_gen(C)) < 0.2).float()
+         * torch.randint(1, 3, shape, generator=_gen(C + 1)).float())
+    cp = runtime.pad32(C)
+    nhwc = torch.zeros(T * B, H, W, cp, dtype=torch.float16)
+    nhwc[..., :C] = v.reshape(T * B, C, H, W).permute(0, 2, 3, 1).half()
+    x = runtime.lazy_output(shape, nhwc.to(cuda), cuda)
+    blk = runtime.count_block(cuda)
+    y = runtime.maxpool_nhwc(x, k, s, p, [0], blk)
+    ref = torch.nn.functional.max_pool2d(v.flatten(0, 1), k, s, p)
+    assert torch.equal(y.cpu(), ref.reshape(T, B, *ref.shape[1:]))
+    assert (int(blk[1].item()) == 0) == (not bool(ref.any()))
+    assert runtime.count_of(y) is blk
+    zero = runtime.lazy_output(shape, torch.zeros(T * B, H, W, cp, dtype=torch.float16,
+                                                  device=cuda), cuda)
+    runtime.maxpool_nhwc(zero, k, s, p, [0], blk)
+    assert int(blk[1].item()) == 0
