@@ -80,7 +80,7 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(DirectArgs a) {
 #pragma unroll
     for (int j = 0; j < COB; ++j) {
       const int co = co0 + j;
-      const float z = acc[j] * a.alpha[co] + a.beta[co];
+      const float z = fmaf(acc[j], a.alpha[co], a.beta[co]);
       const size_t o = ((size_t)(t * a.B + b) * a.Cout + co) * HoWo + p;
       float ov;
       if (EPI == EPI_Z) {
@@ -112,6 +112,150 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(DirectArgs a) {
   if (EPI == EPI_LIF && a.v_out) {
 #pragma unroll
     for (int j = 0; j < COB; ++j) a.v_out[((size_t)b * a.Cout + co0 + j) * HoWo + p] = v[j];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Conv(3 x 3, stride 1) -> BN -> LIF -> MaxPool2d(3, 2, 1) in one launch, for
+// the analog first stage of a spiking patch splitter (Spikformer SPS conv0,
+// models/spikformer_github.py:175-245: proj_conv -> proj_bn -> proj_lif ->
+// maxpool), which otherwise writes the full-resolution spike map and reads it
+// back for the pool.
+//
+// Workgroup: one PH x PW tile of pooled pixels of one image and COB output
+// channels.  Its pooling windows cover (2 PH + 1) x (2 PW + 1) = 255 conv
+// outputs, one per thread (the border row and column are recomputed by the
+// neighbouring tile).  The staged input tile sits in LDS; the weights are
+// read transposed ([Cin*9][Cout]) so each filter tap is one wave-uniform
+// read of COB consecutive floats.  z is the same fp32 fused multiply-add
+// chain as conv_direct_kernel's, so the spikes are bit-identical to
+// conv_direct_kernel followed by the pool.  Per step each thread stores the
+// COB spike bits of its conv output as one 64-bit word; a pooled output is
+// the OR of the nine words of its window (the max of {0, 1} values; the
+// pool's -inf padding never wins because every window holds a conv output).
+// v_out keeps the final membrane of the conv outputs the tile owns (local
+// rows and columns >= 1).
+constexpr int DP_PH = 7, DP_PW = 8;                  // pooled tile
+constexpr int DP_RH = 2 * DP_PH + 1, DP_RW = 2 * DP_PW + 1;   // 15 x 17 conv outputs
+constexpr int DP_NPIX = DP_RH * DP_RW;               // 255
+constexpr int DP_XH = DP_RH + 2, DP_XW = DP_RW + 2;  // staged input (3 x 3, stride 1)
+constexpr int DP_MAXCIN = 4;
+
+struct DirectPoolArgs {
+  const float* x;      // [img][Cin][H][W], img = t*x_img_tstride + b
+  const float* wt;     // [Cin*9][Cout]
+  const float* alpha;
+  const float* beta;
+  const float* v_in;   // [B][Cout][Ho][Wo] or null
+  float* v_out;        // [B][Cout][Ho][Wo] or null
+  _Float16* out_nhwc;  // [T*B][Hp][Wp][cp_out]
+  unsigned long long* nz_out;
+  int cp_out;
+  int T, B, Cin, Cout, H, W, Ho, Wo, pad, Hp, Wp, tiles_w, x_img_tstride;
+  LifParams lif;
+};
+
+template <int COB>
+__global__ __launch_bounds__(256) void conv_direct_pool_kernel(DirectPoolArgs a) {
+  static_assert(COB % 8 == 0 && COB <= 64, "COB spike bits per 64-bit word");
+  __shared__ float xs[DP_MAXCIN][DP_XH][DP_XW];
+  __shared__ unsigned long long spk[2][256];
+  __shared__ unsigned any_sh[4];
+  const int tid = threadIdx.x;
+  const int b = blockIdx.y, co0 = blockIdx.z * COB;
+  const int ph0 = (blockIdx.x / a.tiles_w) * DP_PH, pw0 = (blockIdx.x % a.tiles_w) * DP_PW;
+  const int cr0 = 2 * ph0 - 1, cc0 = 2 * pw0 - 1;    // conv output at local (0, 0)
+  const int lr = tid / DP_RW, lc = tid % DP_RW;
+  const int cr = cr0 + lr, cc = cc0 + lc;
+  const bool valid = tid < DP_NPIX && cr >= 0 && cr < a.Ho && cc >= 0 && cc < a.Wo;
+  const bool dedupe = a.x_img_tstride == 0;
+  const size_t HoWo = (size_t)a.Ho * a.Wo;
+  const int nch = (co0 + COB == a.Cout ? a.cp_out - co0 : COB) / 8;   // 16-byte chunks written
+  float z[COB], v[COB];
+#pragma unroll
+  for (int j = 0; j < COB; ++j)
+    v[j] = (a.v_in && valid) ? a.v_in[((size_t)b * a.Cout + co0 + j) * HoWo + (size_t)cr * a.Wo + cc]
+                             : lif_initial_v(a.lif);
+  uint32_t anyw = 0u;
+  for (int t = 0; t < a.T; ++t) {
+    if (t == 0 || !dedupe) {
+      const int img = t * a.x_img_tstride + b;
+      if (t > 0) __syncthreads();   // the previous step's reads of xs are complete
+      const float* xb = a.x + (size_t)img * a.Cin * a.H * a.W;
+      for (int u = tid; u < a.Cin * DP_XH * DP_XW; u += 256) {
+        const int ci = u / (DP_XH * DP_XW), rr = (u / DP_XW) % DP_XH, c = u % DP_XW;
+        const int ih = cr0 - a.pad + rr, iw = cc0 - a.pad + c;
+        xs[ci][rr][c] = (ih >= 0 && ih < a.H && iw >= 0 && iw < a.W)
+                            ? xb[((size_t)ci * a.H + ih) * a.W + iw] : 0.0f;
+      }
+      __syncthreads();
+      float acc[COB];
+#pragma unroll
+      for (int j = 0; j < COB; ++j) acc[j] = 0.0f;
+      if (tid < DP_NPIX) {
+        for (int ci = 0; ci < a.Cin; ++ci) {
+#pragma unroll
+          for (int kh = 0; kh < 3; ++kh) {
+#pragma unroll
+            for (int kw = 0; kw < 3; ++kw) {
+              const float xv = xs[ci][lr + kh][lc + kw];
+              const float* wk = a.wt + (size_t)((ci * 3 + kh) * 3 + kw) * a.Cout + co0;
+#pragma unroll
+              for (int j = 0; j < COB; ++j) acc[j] = fmaf(xv, wk[j], acc[j]);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < COB; ++j) z[j] = fmaf(acc[j], a.alpha[co0 + j], a.beta[co0 + j]);
+    }
+    unsigned long long m = 0ull;
+#pragma unroll
+    for (int j = 0; j < COB; ++j) {
+      float vv = lif_charge(v[j], z[j], a.lif);
+      const float f = lif_fire_reset(vv, a.lif);
+      v[j] = vv;
+      m |= (f != 0.0f ? 1ull : 0ull) << j;
+    }
+    spk[t & 1][tid] = valid ? m : 0ull;
+    __syncthreads();
+    // pooled outputs: unit = (pooled pixel of the tile, 16-byte chunk)
+    for (int u = tid; u < DP_PH * DP_PW * nch; u += 256) {
+      const int pp = u / nch, ch = u % nch;
+      const int py = pp / DP_PW, px = pp % DP_PW;
+      const int gy = ph0 + py, gx = pw0 + px;
+      if (gy >= a.Hp || gx >= a.Wp) continue;
+      uint32_t bits = 0u;
+      if (ch * 8 < COB) {
+        unsigned long long w = 0ull;
+#pragma unroll
+        for (int dy = 0; dy < 3; ++dy)
+#pragma unroll
+          for (int dx = 0; dx < 3; ++dx) w |= spk[t & 1][(2 * py + dy) * DP_RW + 2 * px + dx];
+        bits = (uint32_t)(w >> (ch * 8)) & 0xffu;
+      }
+      anyw |= bits;
+      uint4 o;
+      o.x = ((bits & 1u) ? 0x3c00u : 0u) | ((bits & 2u) ? 0x3c000000u : 0u);
+      o.y = ((bits & 4u) ? 0x3c00u : 0u) | ((bits & 8u) ? 0x3c000000u : 0u);
+      o.z = ((bits & 16u) ? 0x3c00u : 0u) | ((bits & 32u) ? 0x3c000000u : 0u);
+      o.w = ((bits & 64u) ? 0x3c00u : 0u) | ((bits & 128u) ? 0x3c000000u : 0u);
+      *reinterpret_cast<uint4*>(a.out_nhwc + (((size_t)t * a.B + b) * a.Hp + gy) * a.Wp * a.cp_out +
+                                (size_t)gx * a.cp_out + co0 + ch * 8) = o;
+    }
+  }
+  if (a.v_out && valid && lr >= 1 && lc >= 1) {
+#pragma unroll
+    for (int j = 0; j < COB; ++j)
+      a.v_out[((size_t)b * a.Cout + co0 + j) * HoWo + (size_t)cr * a.Wo + cc] = v[j];
+  }
+  if (a.nz_out) {
+    const bool any = cf_wg_any(anyw != 0u, any_sh);
+    if (tid == 0) {
+      const unsigned nwg = gridDim.x * gridDim.y * gridDim.z;
+      const unsigned wg = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+      cf_count_publish(a.nz_out, any ? 1ull : 0ull, wg, nwg);
+    }
   }
 }
 
@@ -152,4 +296,47 @@ CF_API int cf_conv_direct(const float* x, const float* w, const float* alpha, co
   if (Cout % 16 == 0) return (int)launch_direct<16>(a, epilogue, st);
   if (Cout % 4 == 0) return (int)launch_direct<4>(a, epilogue, st);
   return (int)launch_direct<1>(a, epilogue, st);
+}
+
+// Conv(3 x 3, stride 1, Cin <= 4) -> BN -> LIF -> MaxPool2d(3, 2, 1) of an
+// analog input; writes only the pooled fp16 NHWC copy (channels Cout ..
+// cp_out - 1 zero) and publishes its count block.
+CF_API int cf_conv_direct_lif_maxpool(const float* x, const float* wt, const float* alpha,
+                                      const float* beta, const float* v_in, float* v_out,
+                                      void* out_nhwc, int64_t cp_out,
+                                      unsigned long long* nz_out, int64_t T, int64_t B,
+                                      int64_t Cin, int64_t Cout, int64_t H, int64_t W,
+                                      int64_t pad, int64_t x_img_tstride, double tau,
+                                      double v_th, double v_reset, int hard_reset,
+                                      int decay_input, void* stream) {
+  if (!x || !wt || !alpha || !beta || !out_nhwc || T <= 0 || B <= 0 || B > 65535 || Cin <= 0 ||
+      Cin > DP_MAXCIN || Cout <= 0 || H <= 0 || W <= 0 || pad < 0 || pad > 2 ||
+      x_img_tstride < 0 || cp_out < Cout || cp_out % 8 != 0)
+    return (int)hipErrorInvalidValue;
+  const int64_t Ho = H + 2 * pad - 2, Wo = W + 2 * pad - 2;
+  if (Ho <= 0 || Wo <= 0) return (int)hipErrorInvalidValue;
+  const int64_t Hp = (Ho - 1) / 2 + 1, Wp = (Wo - 1) / 2 + 1;
+  const int64_t tiles_h = (Hp + DP_PH - 1) / DP_PH, tiles_w = (Wp + DP_PW - 1) / DP_PW;
+  int cob = 0;
+  for (int c : {64, 48, 32, 16})
+    if (Cout % c == 0) { cob = c; break; }
+  if (cob == 0 || tiles_h * tiles_w > 0x7fffffff) return (int)hipErrorInvalidValue;
+  const int64_t nwg = tiles_h * tiles_w * B * (Cout / cob);
+  if (nz_out && nwg >= (int64_t)CF_MAX_COUNT_WG) return (int)hipErrorInvalidValue;
+  DirectPoolArgs a;
+  a.x = x; a.wt = wt; a.alpha = alpha; a.beta = beta; a.v_in = v_in; a.v_out = v_out;
+  a.out_nhwc = (_Float16*)out_nhwc; a.nz_out = nz_out; a.cp_out = (int)cp_out;
+  a.T = (int)T; a.B = (int)B; a.Cin = (int)Cin; a.Cout = (int)Cout; a.H = (int)H; a.W = (int)W;
+  a.Ho = (int)Ho; a.Wo = (int)Wo; a.pad = (int)pad; a.Hp = (int)Hp; a.Wp = (int)Wp;
+  a.tiles_w = (int)tiles_w; a.x_img_tstride = (int)x_img_tstride;
+  a.lif = cf_make_lif_params(tau, v_th, v_reset, hard_reset, decay_input);
+  const dim3 grid((unsigned)(tiles_h * tiles_w), (unsigned)B, (unsigned)(Cout / cob));
+  hipStream_t st = (hipStream_t)stream;
+  switch (cob) {
+    case 64: hipLaunchKernelGGL(conv_direct_pool_kernel<64>, grid, dim3(256), 0, st, a); break;
+    case 48: hipLaunchKernelGGL(conv_direct_pool_kernel<48>, grid, dim3(256), 0, st, a); break;
+    case 32: hipLaunchKernelGGL(conv_direct_pool_kernel<32>, grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL(conv_direct_pool_kernel<16>, grid, dim3(256), 0, st, a); break;
+  }
+  return (int)hipGetLastError();
 }

@@ -611,6 +611,7 @@ class ConvLIFRunner:
                                               None, ptr(self.alpha_direct),
                                               ptr(self.beta_direct), st), "cf_pack_conv_weights")
         self._w_f32 = w
+        self._wt_f32 = w.reshape(self.Cout, -1).t().contiguous()   # [Cin*KH*KW][Cout]
         self._packed_key = key
 
     def out_hw(self, H, W):
@@ -851,6 +852,58 @@ class ConvLIFRunner:
         check(rc, "cf_conv_direct")
         _t1("conv_direct", ev, flops=2 * (1 if tstride == 0 else T) * B * Ho * Wo * self.Cout *
             C * self.KH * self.KW)
+        return out, v_out
+
+    # -- analog 3 x 3 conv -> BN -> LIF -> MaxPool(3, 2, 1) ------------------
+
+    def direct_pool_supported(self, x: torch.Tensor, pool) -> bool:
+        """cf_conv_direct_lif_maxpool covers a 3 x 3, stride-1 conv (padding
+        <= 2) over an fp32 input of at most 4 channels, Cout a multiple of 16,
+        followed by MaxPool2d(3, 2, 1)."""
+        return (x.dim() == 5 and x.dtype == torch.float32 and x.is_cuda and self.Cin <= 4
+                and self.KH == 3 and self.KW == 3 and self.stride == 1 and self.padding <= 2
+                and self.Cout % 16 == 0 and x.shape[1] <= 65535
+                and tuple(int(p) for p in pool) == (3, 2, 1))
+
+    def run_direct_pool(self, x: torch.Tensor, v_in=None, *, want_v_out=True, nz_out=None,
+                        gen_cell=None):
+        """x [T, B, Cin, H, W] (a stride-0 time axis evaluates the conv once).
+        Returns the pooled spikes [T, B, Cout, Hp, Wp] as a lazy output over
+        their fp16 NHWC copy (with nz_out and gen_cell, carrying its count
+        block) and the conv-resolution membrane [B, Cout, Ho, Wo]."""
+        if not self.direct_pool_supported(x, (3, 2, 1)):
+            raise ValueError("input/layer not covered by cf_conv_direct_lif_maxpool")
+        _require_block(nz_out)
+        T, B, C, H, W = x.shape
+        dev = x.device
+        self._ensure_packed(dev)
+        if x.stride(0) == 0 and x[0].is_contiguous():
+            tstride, xb = 0, x[0]
+        else:
+            x = x.contiguous()
+            tstride, xb = B, x
+        Ho, Wo = self.out_hw(H, W)
+        Hp, Wp = (Ho - 1) // 2 + 1, (Wo - 1) // 2 + 1
+        if v_in is not None:
+            require_gpu_tensor(v_in, "v_in")
+            if v_in.numel() != B * self.Cout * Ho * Wo:
+                raise ValueError("v_in has the wrong size")
+        v_out = (torch.empty((B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
+                 if want_v_out else None)
+        cp_out = pad32(self.Cout)
+        nhwc = torch.empty((T * B, Hp, Wp, cp_out), dtype=torch.float16, device=dev)
+        ev = _t0()
+        rc = _hip.lib().cf_conv_direct_lif_maxpool(
+            ptr(xb), ptr(self._wt_f32), ptr(self.alpha_direct), ptr(self.beta_direct),
+            ptr(v_in), ptr(v_out), ptr(nhwc), cp_out, ptr(nz_out), T, B, C, self.Cout, H, W,
+            self.padding, tstride, *self.lif, _hip.stream(dev))
+        check(rc, "cf_conv_direct_lif_maxpool")
+        _t1("conv_direct_pool", ev, flops=2 * (1 if tstride == 0 else T) * B * Ho * Wo *
+            self.Cout * C * 9)
+        out = lazy_output((T, B, self.Cout, Hp, Wp), nhwc, dev)
+        if nz_out is not None and gen_cell is not None:
+            gen_cell[0] += 1
+            attach_count(out, nz_out, gen_cell)
         return out, v_out
 
     # -- fused stem: Conv -> BN -> LIF -> MaxPool(3, 2, 1) -------------------

@@ -231,6 +231,10 @@ class CTFSpikformerSPS(CTFPattern):
         T, B = x.shape[:2]
         y = x
         for i, (stage, pool, pooled) in enumerate(zip(self.stages, self.pools, self._pooled)):
+            if pooled and self._direct_pool(stage, pool, y):
+                # analog input: conv, LIF and pool in one launch
+                y = self._run_direct_pool(i, stage, y)
+                continue
             y = stage(y)
             if pooled:
                 k, st, pd = (int(v if isinstance(v, int) else v[0])
@@ -255,6 +259,30 @@ class CTFSpikformerSPS(CTFPattern):
             # the same values: the rpe conv's count block describes the tokens
             tok._cf_count = r._cf_count[:3] + (tok._version,)
         return tok
+
+    @staticmethod
+    def _pool_geometry(pool):
+        return tuple(int(v if isinstance(v, int) else v[0])
+                     for v in (pool.kernel_size, pool.stride, pool.padding))
+
+    def _direct_pool(self, stage, pool, x) -> bool:
+        if not (x.is_cuda and x.dim() == 5 and stage._impl.input_is_analog(x)):
+            return False
+        if getattr(pool, "dilation", 1) not in (1, (1, 1)) or getattr(pool, "ceil_mode", False):
+            return False
+        r = stage._impl.runner(stage.spec, stage._ensure_params(), x.device)
+        return r.direct_pool_supported(x, self._pool_geometry(pool))
+
+    def _run_direct_pool(self, i, stage, x):
+        stage._impl.check_input(x, stage.spec)
+        r = stage._impl.runner(stage.spec, stage._ensure_params(), x.device)
+        B = x.shape[1]
+        Ho, Wo = r.out_hw(x.shape[3], x.shape[4])
+        v_in = stage.state.peek((B, stage.out_channels, Ho, Wo), x.device)
+        y, v = r.run_direct_pool(x, v_in, nz_out=self._pool_block(i, x.device),
+                                 gen_cell=self._pool_gen[i])
+        stage.state.set(v)
+        return y
 
     @classmethod
     def from_sj_module(cls, sps):

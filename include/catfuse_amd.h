@@ -273,6 +273,26 @@ int cf_conv_direct(const float* x, const float* w, const float* alpha, const flo
                    int epilogue, double tau, double v_th, double v_reset, int hard_reset,
                    int decay_input, void* stream);
 
+/* Conv(3 x 3, stride 1, Cin <= 4) -> BN -> LIF -> MaxPool2d(3, 2, 1) of an
+ * analog input x [T*x_img_tstride + B][Cin][H][W] in one launch (fp32 VALU,
+ * the same arithmetic as cf_conv_direct, so the pooled spikes equal
+ * cf_conv_direct's followed by the pool bit for bit).  wt is the transposed
+ * filter [Cin*9][Cout]; alpha/beta as cf_pack_conv_weights writes them.
+ * Writes the pooled fp16 NHWC copy [T*B][Hp][Wp][cp_out] (channels
+ * Cout .. cp_out-1 zero; cp_out a multiple of 8), the conv-resolution
+ * membrane v_out [B][Cout][Ho][Wo] (nullable), and publishes the output's
+ * count block nz_out (nullable; see the count-block convention above).
+ * Replaces the first stage of the reference's spiking patch splitter,
+ * models/spikformer_github.py:175-245 (proj_conv, proj_bn, proj_lif, maxpool),
+ * which runs the conv, the LIF and the pool as separate passes. */
+int cf_conv_direct_lif_maxpool(const float* x, const float* wt, const float* alpha,
+                               const float* beta, const float* v_in, float* v_out,
+                               void* out_nhwc, int64_t cp_out, unsigned long long* nz_out,
+                               int64_t T, int64_t B, int64_t Cin, int64_t Cout, int64_t H,
+                               int64_t W, int64_t pad, int64_t x_img_tstride, double tau,
+                               double v_th, double v_reset, int hard_reset, int decay_input,
+                               void* stream);
+
 /* Stem weight packing for cf_conv_stem_lif_maxpool: fp32 [Cout][Cin][KH][KW]
  * (Cin <= 4, KH <= 7, KW <= 8) -> fp16 hi/lo limbs [2][Coutp][KH][32] with
  * k = kw*4 + c, a per-channel power-of-two prescale, and the folded

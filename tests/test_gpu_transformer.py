@@ -218,3 +218,50 @@ def test_maxpool_nhwc_bitwise(cuda, shape, k, s, p):
                                                   device=cuda), cuda)
     runtime.maxpool_nhwc(zero, k, s, p, [0], blk)
     assert int(blk[1].item()) == 0
+
+
+DIRECT_POOL_CASES = [
+    # (T, B, Cin, Cout, H, W, pad, direct_encoded, with_v_in)
+    (4, 2, 3, 48, 32, 32, 1, True, False),
+    (3, 2, 3, 32, 29, 23, 1, True, True),
+    (2, 3, 4, 64, 17, 30, 2, False, False),
+    (5, 1, 1, 16, 15, 16, 0, True, True),
+]
+
+
+@pytest.mark.parametrize("case", DIRECT_POOL_CASES, ids=[f"c{c[3]}_{c[4]}x{c[5]}_p{c[6]}"
+                                                          for c in DIRECT_POOL_CASES])
+def test_conv_direct_lif_maxpool_bitwise(cuda, case):
+    """Analog 3x3 conv -> BN -> LIF -> MaxPool2d(3, 2, 1) in one launch equals
+    the direct conv's spikes pooled by torch (bit for bit), its membrane
+    equals the direct conv's, and its count block is published."""
+    from catfuse_amd import runtime
+    T, B, Cin, Cout, H, W, pad, direct, with_v = case
+    g = _gen(Cout + H)
+    w = torch.randn(Cout, Cin, 3, 3, generator=g) * 0.9
+    sc = torch.rand(Cout, generator=g) + 0.5
+    sh = torch.randn(Cout, generator=g) * 0.2
+    r = runtime.ConvLIFRunner(w.to(cuda), sc.to(cuda), sh.to(cuda), None, 1, pad, 2.0, 1.0,
+                              0.0, True)
+    img = torch.randn(B, Cin, H, W, generator=g).to(cuda)
+    x = (img.unsqueeze(0).expand(T, B, Cin, H, W) if direct
+         else torch.randn(T, B, Cin, H, W, generator=g).to(cuda))
+    Ho, Wo = r.out_hw(H, W)
+    v_in = (torch.rand(B, Cout, Ho, Wo, generator=g) * 0.8).to(cuda) if with_v else None
+    assert r.direct_pool_supported(x, (3, 2, 1))
+    ref_s, ref_v = r.run_direct(x, v_in)
+    ref = torch.nn.functional.max_pool2d(ref_s.flatten(0, 1), 3, 2, 1)
+    blk = runtime.count_block(cuda)
+    y, v = r.run_direct_pool(x, v_in, nz_out=blk, gen_cell=[0])
+    assert tuple(y.shape) == (T, B, Cout) + tuple(ref.shape[-2:])
+    assert torch.equal(y.reshape(T * B, *ref.shape[1:]), ref)
+    assert torch.equal(v, ref_v)
+    cp = runtime.pad32(Cout)
+    copy = runtime.shadow_of(y, (T * B,) + tuple(ref.shape[-2:]) + (cp,))
+    assert copy is not None and not bool(copy[..., Cout:].any())
+    assert (int(blk[1].item()) == 0) == (not bool(ref.any()))
+    assert runtime.count_of(y) is blk
+    # a second call on the same block (smaller batch) republishes
+    y2, _ = r.run_direct_pool(x[:, :1], None if v_in is None else v_in[:1], nz_out=blk,
+                              gen_cell=[0])
+    assert torch.equal(y2.reshape(T, *ref.shape[1:]), ref.reshape(T, B, *ref.shape[1:])[:, 0])
