@@ -155,28 +155,41 @@ struct DirectPoolArgs {
   LifParams lif;
 };
 
-template <int COB>
+template <int COB, int LM>
 __global__ __launch_bounds__(256) void conv_direct_pool_kernel(DirectPoolArgs a) {
   static_assert(COB % 8 == 0 && COB <= 64, "COB spike bits per 64-bit word");
   __shared__ float xs[DP_MAXCIN][DP_XH][DP_XW];
+  __shared__ __attribute__((aligned(16))) float wsm[DP_MAXCIN * 9][COB];   // [tap][channel]
   __shared__ unsigned long long spk[2][256];
   __shared__ unsigned any_sh[4];
   const int tid = threadIdx.x;
   const int b = blockIdx.y, co0 = blockIdx.z * COB;
   const int ph0 = (blockIdx.x / a.tiles_w) * DP_PH, pw0 = (blockIdx.x % a.tiles_w) * DP_PW;
   const int cr0 = 2 * ph0 - 1, cc0 = 2 * pw0 - 1;    // conv output at local (0, 0)
-  const int lr = tid / DP_RW, lc = tid % DP_RW;
+  // thread 255 has no conv output; it computes a clamped duplicate, so the
+  // conv loop has no divergent branch
+  const int lr = min(tid / DP_RW, DP_RH - 1), lc = tid % DP_RW;
   const int cr = cr0 + lr, cc = cc0 + lc;
   const bool valid = tid < DP_NPIX && cr >= 0 && cr < a.Ho && cc >= 0 && cc < a.Wo;
   const bool dedupe = a.x_img_tstride == 0;
   const size_t HoWo = (size_t)a.Ho * a.Wo;
   const int nch = (co0 + COB == a.Cout ? a.cp_out - co0 : COB) / 8;   // 16-byte chunks written
+  // membrane of this conv output, channel j at vbase + j * HoWo
+  const size_t vbase = ((size_t)b * a.Cout + co0) * HoWo + (valid ? (size_t)cr * a.Wo + cc : 0);
   float z[COB], v[COB];
+  if (a.v_in && valid) {
+    const float* vin = a.v_in + vbase;
 #pragma unroll
-  for (int j = 0; j < COB; ++j)
-    v[j] = (a.v_in && valid) ? a.v_in[((size_t)b * a.Cout + co0 + j) * HoWo + (size_t)cr * a.Wo + cc]
-                             : lif_initial_v(a.lif);
+    for (int j = 0; j < COB; ++j) v[j] = vin[(size_t)j * HoWo];
+  } else {
+#pragma unroll
+    for (int j = 0; j < COB; ++j) v[j] = lif_initial_v(a.lif);
+  }
   uint32_t anyw = 0u;
+  // this workgroup's filter slice; every lane reads the same weights, so
+  // the conv reads them as LDS broadcasts (16 bytes, four channels, a read)
+  for (int u = tid; u < a.Cin * 9 * COB; u += 256)
+    wsm[u / COB][u % COB] = a.wt[(size_t)(u / COB) * a.Cout + co0 + u % COB];
   for (int t = 0; t < a.T; ++t) {
     if (t == 0 || !dedupe) {
       const int img = t * a.x_img_tstride + b;
@@ -192,16 +205,20 @@ __global__ __launch_bounds__(256) void conv_direct_pool_kernel(DirectPoolArgs a)
       float acc[COB];
 #pragma unroll
       for (int j = 0; j < COB; ++j) acc[j] = 0.0f;
-      if (tid < DP_NPIX) {
-        for (int ci = 0; ci < a.Cin; ++ci) {
+      for (int ci = 0; ci < a.Cin; ++ci) {
 #pragma unroll
-          for (int kh = 0; kh < 3; ++kh) {
+        for (int kh = 0; kh < 3; ++kh) {
 #pragma unroll
-            for (int kw = 0; kw < 3; ++kw) {
-              const float xv = xs[ci][lr + kh][lc + kw];
-              const float* wk = a.wt + (size_t)((ci * 3 + kh) * 3 + kw) * a.Cout + co0;
+          for (int kw = 0; kw < 3; ++kw) {
+            const float xv = xs[ci][lr + kh][lc + kw];
+            const float4* wk = reinterpret_cast<const float4*>(wsm[(ci * 3 + kh) * 3 + kw]);
 #pragma unroll
-              for (int j = 0; j < COB; ++j) acc[j] = fmaf(xv, wk[j], acc[j]);
+            for (int j = 0; j < COB; j += 4) {
+              const float4 w4 = wk[j / 4];
+              acc[j] = fmaf(xv, w4.x, acc[j]);
+              acc[j + 1] = fmaf(xv, w4.y, acc[j + 1]);
+              acc[j + 2] = fmaf(xv, w4.z, acc[j + 2]);
+              acc[j + 3] = fmaf(xv, w4.w, acc[j + 3]);
             }
           }
         }
@@ -212,10 +229,10 @@ __global__ __launch_bounds__(256) void conv_direct_pool_kernel(DirectPoolArgs a)
     unsigned long long m = 0ull;
 #pragma unroll
     for (int j = 0; j < COB; ++j) {
-      float vv = lif_charge(v[j], z[j], a.lif);
-      const float f = lif_fire_reset(vv, a.lif);
+      float vv = lif_charge_m<LM>(v[j], z[j], a.lif);
+      const bool f = lif_fire_reset_bit<LM>(vv, a.lif);
       v[j] = vv;
-      m |= (f != 0.0f ? 1ull : 0ull) << j;
+      m |= (f ? 1ull : 0ull) << j;
     }
     spk[t & 1][tid] = valid ? m : 0ull;
     __syncthreads();
@@ -245,9 +262,9 @@ __global__ __launch_bounds__(256) void conv_direct_pool_kernel(DirectPoolArgs a)
     }
   }
   if (a.v_out && valid && lr >= 1 && lc >= 1) {
+    float* vout = a.v_out + vbase;
 #pragma unroll
-    for (int j = 0; j < COB; ++j)
-      a.v_out[((size_t)b * a.Cout + co0 + j) * HoWo + (size_t)cr * a.Wo + cc] = v[j];
+    for (int j = 0; j < COB; ++j) vout[(size_t)j * HoWo] = v[j];
   }
   if (a.nz_out) {
     const bool any = cf_wg_any(anyw != 0u, any_sh);
@@ -257,6 +274,17 @@ __global__ __launch_bounds__(256) void conv_direct_pool_kernel(DirectPoolArgs a)
       cf_count_publish(a.nz_out, any ? 1ull : 0ull, wg, nwg);
     }
   }
+}
+
+template <int LM>
+hipError_t launch_direct_pool(const DirectPoolArgs& a, int cob, dim3 grid, hipStream_t st) {
+  switch (cob) {
+    case 64: hipLaunchKernelGGL((conv_direct_pool_kernel<64, LM>), grid, dim3(256), 0, st, a); break;
+    case 48: hipLaunchKernelGGL((conv_direct_pool_kernel<48, LM>), grid, dim3(256), 0, st, a); break;
+    case 32: hipLaunchKernelGGL((conv_direct_pool_kernel<32, LM>), grid, dim3(256), 0, st, a); break;
+    default: hipLaunchKernelGGL((conv_direct_pool_kernel<16, LM>), grid, dim3(256), 0, st, a); break;
+  }
+  return hipGetLastError();
 }
 
 template <int COB>
@@ -317,9 +345,10 @@ CF_API int cf_conv_direct_lif_maxpool(const float* x, const float* wt, const flo
   if (Ho <= 0 || Wo <= 0) return (int)hipErrorInvalidValue;
   const int64_t Hp = (Ho - 1) / 2 + 1, Wp = (Wo - 1) / 2 + 1;
   const int64_t tiles_h = (Hp + DP_PH - 1) / DP_PH, tiles_w = (Wp + DP_PW - 1) / DP_PW;
-  int cob = 0;
-  for (int c : {64, 48, 32, 16})
-    if (Cout % c == 0) { cob = c; break; }
+  // 16 channels a workgroup: 87 VGPRs, five waves a SIMD to hide the
+  // per-step barriers (wider groups hold z and v for more channels and run
+  // two waves a SIMD)
+  const int cob = Cout % 16 == 0 ? 16 : 0;
   if (cob == 0 || tiles_h * tiles_w > 0x7fffffff) return (int)hipErrorInvalidValue;
   const int64_t nwg = tiles_h * tiles_w * B * (Cout / cob);
   if (nz_out && nwg >= (int64_t)CF_MAX_COUNT_WG) return (int)hipErrorInvalidValue;
@@ -331,12 +360,9 @@ CF_API int cf_conv_direct_lif_maxpool(const float* x, const float* wt, const flo
   a.tiles_w = (int)tiles_w; a.x_img_tstride = (int)x_img_tstride;
   a.lif = cf_make_lif_params(tau, v_th, v_reset, hard_reset, decay_input);
   const dim3 grid((unsigned)(tiles_h * tiles_w), (unsigned)B, (unsigned)(Cout / cob));
+  const int lm = cf_lif_mode(a.lif);
   hipStream_t st = (hipStream_t)stream;
-  switch (cob) {
-    case 64: hipLaunchKernelGGL(conv_direct_pool_kernel<64>, grid, dim3(256), 0, st, a); break;
-    case 48: hipLaunchKernelGGL(conv_direct_pool_kernel<48>, grid, dim3(256), 0, st, a); break;
-    case 32: hipLaunchKernelGGL(conv_direct_pool_kernel<32>, grid, dim3(256), 0, st, a); break;
-    default: hipLaunchKernelGGL(conv_direct_pool_kernel<16>, grid, dim3(256), 0, st, a); break;
-  }
-  return (int)hipGetLastError();
+  if (lm == LM_HARD0_DECAY_P2) return (int)launch_direct_pool<LM_HARD0_DECAY_P2>(a, cob, grid, st);
+  if (lm == LM_HARD_DECAY_P2) return (int)launch_direct_pool<LM_HARD_DECAY_P2>(a, cob, grid, st);
+  return (int)launch_direct_pool<LM_GENERIC>(a, cob, grid, st);
 }
