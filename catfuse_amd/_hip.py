@@ -82,8 +82,24 @@ def lib() -> _Lib:
             raise RuntimeError(
                 f"catfuse_amd HIP library not found at {_LIB_PATH}; build it with "
                 "`python -m catfuse_amd.build` (hipcc --offload-arch=gfx950)")
+        _check_fresh()
         _lib = _Lib(ctypes.CDLL(_LIB_PATH, mode=ctypes.RTLD_LOCAL))
     return _lib
+
+
+def _check_fresh() -> None:
+    """Refuse a library built from other sources than the ones in the tree:
+    its entry points may take other arguments than the signatures above."""
+    from catfuse_amd import build
+    try:
+        with open(build.stamp_path()) as fh:
+            built = fh.read().strip()
+    except OSError:
+        built = None
+    if built != build.source_digest():
+        raise RuntimeError(
+            f"catfuse_amd HIP library at {_LIB_PATH} was not built from the current "
+            "sources; rebuild it with `python -m catfuse_amd.build`")
 
 
 def check(rc: int, what: str = "") -> None:

@@ -17,6 +17,7 @@ Usage: ``python -m catfuse_amd.build`` (or ``catfuse_amd.build.build()``).
 from __future__ import annotations
 
 import concurrent.futures as _cf
+import hashlib
 import os
 import shutil
 import subprocess
@@ -55,6 +56,21 @@ def sources() -> list:
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
+def source_digest() -> str:
+    """SHA-256 over the HIP sources and headers the library is built from."""
+    h = hashlib.sha256()
+    for f in sorted(os.listdir(CSRC)):
+        if f.endswith((".hip", ".h")):
+            h.update(f.encode())
+            with open(os.path.join(CSRC, f), "rb") as fh:
+                h.update(fh.read())
+    return h.hexdigest()
+
+
+def stamp_path() -> str:
+    return os.path.join(LIB_DIR, LIB_NAME + ".sources")
+
+
 def _compile(src: str, hipcc: str) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src)[:-4] + ".o")
     cmd = [hipcc, *HIPCC_FLAGS, "-I", CSRC, "-c", src, "-o", obj]
@@ -70,6 +86,7 @@ def build(verbose: bool = True, jobs: int = 0) -> str:
     os.makedirs(BUILD_DIR, exist_ok=True)
     os.makedirs(LIB_DIR, exist_ok=True)
     srcs = sources()
+    digest = source_digest()
     jobs = jobs or min(len(srcs), max(1, (os.cpu_count() or 4) - 1), 8)
     with _cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         objs = list(ex.map(lambda s: _compile(s, hipcc), srcs))
@@ -80,6 +97,8 @@ def build(verbose: bool = True, jobs: int = 0) -> str:
     if r.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
     os.replace(tmp, out)
+    with open(stamp_path(), "w") as fh:   # the sources this library was built from
+        fh.write(digest + "\n")
     if verbose:
         print(f"[catfuse_amd.build] {len(srcs)} sources -> {out}")
     return out

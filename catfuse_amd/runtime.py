@@ -297,6 +297,23 @@ def lazy_tokens(shape, copy: torch.Tensor, device) -> NHWCSpikes:
     return NHWCSpikes(torch.empty(shape, dtype=torch.float32, device=device), copy, tokens=True)
 
 
+def token_view(B: int, N: int):
+    """(nimg, H, W): how a token layer's launch views the B * N tokens of a
+    step as images.  8 x 8 images of 64 consecutive tokens when 64 divides
+    B * N (the halo kernel's 8 x 8 pixel tile, no idle rows); else each
+    image's N tokens on a square grid (N a square of at least 16) or a
+    column (N, 1)."""
+    if (B * N) % 64 == 0:
+        return B * N // 64, 8, 8
+    r = int(round(N ** 0.5))
+    return (B, r, r) if (r * r == N and r >= 4) else (B, N, 1)
+
+
+def token_membrane(v: torch.Tensor, B: int, N: int) -> torch.Tensor:
+    """A token layer's state [nimg, C, H * W] (per view image) as [B, N, C]."""
+    return v.transpose(1, 2).reshape(B, N, v.shape[1])
+
+
 def token_shadow(x: torch.Tensor, cp: int) -> Optional[torch.Tensor]:
     """The current fp16 copy of a token-major x [..., N, C] as [rows, cp]
     (rows = x.numel() / C), or None."""
@@ -762,14 +779,16 @@ class ConvLIFRunner:
 
     def run_tokens(self, x: torch.Tensor, v_in=None, *, identity=None, want_v_out=True,
                    static_zero=True, grid=None):
-        """Linear -> (BN) -> LIF over token-major x [T, B, N, Cin] (a 1x1 conv
-        over each image's N tokens as a grid of pixels, grid = (H, W) with
-        H * W = N; default the square root when N is a square of at least 16,
-        else (N, 1)).  x's fp16 copy (a fused token layer's output) is read
-        directly, otherwise x is packed.  identity [T, B, N, Cout] is added to
-        the spikes (a residual), read from its fp16 copy (packed if it has
-        none; its values must be fp16-exact).  Returns (lazy fp32 tokens
-        [T, B, N, Cout], v_out [B, Cout, N] or None)."""
+        """Linear -> (BN) -> LIF over token-major x [T, B, N, Cin]: a 1x1 conv
+        over the token rows of each step, viewed as `nimg` images of H x W
+        tokens (token_view: 8 x 8 images of 64 consecutive tokens when 64
+        divides B * N, whole MFMA tiles; else each image's N tokens).  x's
+        fp16 copy (a fused token layer's output) is read directly, otherwise
+        x is packed.  identity [T, B, N, Cout] is added to the spikes (a
+        residual), read from its fp16 copy (packed if it has none; its values
+        must be fp16-exact).  The membrane state is per view image,
+        [nimg, Cout, H * W] (token_membrane gives it as [B, N, Cout]).
+        Returns (lazy fp32 tokens [T, B, N, Cout], v_out or None)."""
         require_gpu_tensor(x, "x")
         if self.KH != 1 or self.KW != 1 or self.stride != 1 or self.padding != 0:
             raise ValueError("run_tokens needs a 1x1 kernel with stride 1 and no padding")
@@ -779,10 +798,10 @@ class ConvLIFRunner:
         dev = x.device
         self._ensure_packed(dev)
         if grid is None:
-            r = int(round(N ** 0.5))
-            grid = (r, r) if (r * r == N and r >= 4) else (N, 1)
-        H, W = grid
-        if H * W != N:
+            nimg, H, W = token_view(B, N)
+        else:
+            (H, W), nimg = grid, B
+        if nimg * H * W != B * N:
             raise ValueError("token grid does not match N")
         xp = token_shadow(x, self.Cp)
         nnz = None
@@ -804,11 +823,11 @@ class ConvLIFRunner:
                                       out=self.workspace("idp", (T * B * N, id_cp),
                                                          torch.float16, dev))
         out, v_out = self._launch(
-            xp.view(T * B, H, W, self.Cp), T, B, H, W, H, W, x.numel(), nnz, None, 0, 0, 0,
-            v_in, EPI_LIF, want_v_out, None,
-            None if id_copy is None else id_copy.view(T * B, H, W, id_cp), ID_ADD_SPIKE, 2.0,
+            xp.view(T * nimg, H, W, self.Cp), T, nimg, H, W, H, W, x.numel(), nnz, None, 0, 0,
+            0, v_in, EPI_LIF, want_v_out, None,
+            None if id_copy is None else id_copy.view(T * nimg, H, W, id_cp), ID_ADD_SPIKE, 2.0,
             True, lambda nhwc: lazy_tokens((T, B, N, self.Cout), nhwc, dev), "linear_tokens")
-        return out, (None if v_out is None else v_out.view(B, self.Cout, N))
+        return out, (None if v_out is None else v_out.view(nimg, self.Cout, H * W))
 
     def run_direct(self, x: torch.Tensor, v_in=None, *, epilogue=EPI_LIF, want_v_out=True,
                    emit_nhwc=False):

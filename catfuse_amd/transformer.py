@@ -23,7 +23,8 @@ import torch.nn as nn
 
 from catfuse_amd.patterns import (CTFPattern, PartialFusionConvBNLIF, fold_bn, lif_params)
 from catfuse_amd.runtime import (ConvLIFRunner, count_block, count_of, lazy_tokens, maxpool_nhwc,
-                                 pad32, shadow_of, spike_attention_lif, token_shadow)
+                                 pad32, shadow_of, spike_attention_lif, token_membrane,
+                                 token_shadow, token_view)
 from catfuse_amd.state import StateBuffer
 
 
@@ -56,6 +57,7 @@ class FusedLinearBNLIF(CTFPattern):
             self.register_buffer("running_var", None)
         self.state = StateBuffer()
         self._register_state(self.state)
+        self._tokens = None   # (B, N) of the last call
         self._runner = None
         self._runner_key = None
 
@@ -86,10 +88,19 @@ class FusedLinearBNLIF(CTFPattern):
             x = x.unsqueeze(2)
             identity = None if identity is None else identity.unsqueeze(2)
         T, B, N, _ = x.shape
-        v_in = self.state.peek((B, self.out_features, N), x.device)
+        nimg, H, W = token_view(B, N)
+        v_in = self.state.peek((nimg, self.out_features, H * W), x.device)
         y, v = self.runner().run_tokens(x, v_in, identity=identity)
         self.state.set(v)
+        self._tokens = (B, N)
         return y.squeeze(2) if squeeze else y
+
+    def membrane(self):
+        """The LIF state after the last call as [B, N, out_features] (None
+        after a reset).  Held per launch view image ([nimg, out, H * W],
+        runtime.token_view), the layout the kernel reads and writes."""
+        v = self.state.tensor
+        return None if v is None else token_membrane(v, *self._tokens)
 
     @classmethod
     def from_sj_modules(cls, linear, bn, lif):

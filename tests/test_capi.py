@@ -81,3 +81,13 @@ def test_host_side_argument_validation():
     # pack: groups must fit 32 bits
     assert L.cf_pack_input(1, 1, 1024, 4, 4, 1024, None, 1, 16, 1e-6, None, None,
                            None) == INVALID
+
+
+def test_stale_library_refused(monkeypatch):
+    """A library whose recorded source digest differs from the tree's sources
+    is refused before any entry point is bound."""
+    from catfuse_amd import _hip, build
+    monkeypatch.setattr(build, "source_digest", lambda: "0" * 64)
+    monkeypatch.setattr(_hip, "_lib", None)
+    with pytest.raises(RuntimeError, match="not built from the current sources"):
+        _hip.lib()

@@ -56,7 +56,7 @@ def test_fused_linear_bn_lif_parity(cuda, case):
     y = f(x.to(cuda))
     xs = x if N else x.unsqueeze(2)
     s_ref, v_ref, h_ref = oracle.linear_bn_lif(xs, lin, bn, lif)
-    v = f.state.tensor.transpose(1, 2).cpu().numpy()   # state [B, O, N] -> [B, N, O]
+    v = f.membrane().cpu().numpy()   # [B, N, O]
     yo = y.cpu().numpy() if N else y.unsqueeze(2).cpu().numpy()
     lif_parity(yo, v, s_ref, v_ref, h_ref, what=name)
     # residual added in the epilogue (integer-valued, read from a packed copy)
