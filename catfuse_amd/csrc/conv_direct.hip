@@ -118,7 +118,7 @@ __global__ __launch_bounds__(256) void conv_direct_kernel(DirectArgs a) {
 // ---------------------------------------------------------------------------
 // Conv(3 x 3, stride 1) -> BN -> LIF -> MaxPool2d(3, 2, 1) in one launch, for
 // the analog first stage of a spiking patch splitter (Spikformer SPS conv0,
-// models/spikformer_github.py:175-245: proj_conv -> proj_bn -> proj_lif ->
+// models/spikformer_github.py:181-254: proj_conv -> proj_bn -> proj_lif ->
 // maxpool), which otherwise writes the full-resolution spike map and reads it
 // back for the pool.
 //

@@ -414,7 +414,7 @@ class SpikformerSPS(nn.Module):
     (the reference's CIFAR variant pools after stages 2 and 3; four pools
     give the 14 x 14 tokens of a 224 x 224 image), then the relative
     position Conv-BN-LIF added to its input, as tokens [T, B, N, C]
-    (models/spikformer_github.py:175-245)."""
+    (models/spikformer_github.py:181-254)."""
 
     def __init__(self, in_channels, embed_dim, v_threshold=1.0, pools=(2, 3)):
         super().__init__()
@@ -445,7 +445,7 @@ class SpikformerSPS(nn.Module):
 
 
 class Spikformer(nn.Module):
-    """models/spikformer_github.py:248-330: SPS, `depth` blocks, token
+    """models/spikformer_github.py:256-330: SPS, `depth` blocks, token
     average, pre-head LIF, linear head; x [T, B, C, H, W] (or [B, C, H, W],
     repeated over T) -> [T, B, num_classes]."""
 

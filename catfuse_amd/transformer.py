@@ -199,7 +199,7 @@ class CTFSpikformerMLP(CTFPattern):
 
 class CTFSpikformerBlock(CTFPattern):
     """x + SSA(x), then x + MLP(x), the adds in proj's and fc2's epilogues
-    (models/spikformer_github.py:163-173)."""
+    (models/spikformer_github.py:162-179)."""
 
     def __init__(self, attn: CTFSpikformerSSA, mlp: CTFSpikformerMLP):
         super().__init__()
@@ -220,7 +220,7 @@ class CTFSpikformerSPS(CTFPattern):
     after the pooled ones, on the materialised spikes), then the relative
     position Conv-BN-LIF with its input added in the epilogue; the result's
     NHWC copy is the token copy [T*B*N, C] of the output tokens [T, B, N, C]
-    (models/spikformer_github.py:175-245)."""
+    (models/spikformer_github.py:181-254)."""
 
     def __init__(self, stages, pools, rpe):
         super().__init__()

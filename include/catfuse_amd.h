@@ -161,7 +161,7 @@ int cf_spike_attention_lif(const void* q, const void* k, const void* v, int64_t 
  * torch's max_pool2d; 2*padding <= kernel_size so every window has an input);
  * nz_out (nullable) receives the output's count block.  Exact for spikes.
  * Replaces the MaxPool2d between fused Conv-BN-LIF stages of
- * models/spikformer_github.py:196-241 (SPS), which the reference runs in
+ * models/spikformer_github.py:181-254 (SPS), which the reference runs in
  * torch on the fp32 spikes. */
 int cf_maxpool_nhwc(const void* xp, void* out, int64_t NB, int64_t H, int64_t W, int64_t cp,
                     int64_t kernel_size, int64_t stride, int64_t padding,
@@ -283,7 +283,7 @@ int cf_conv_direct(const float* x, const float* w, const float* alpha, const flo
  * membrane v_out [B][Cout][Ho][Wo] (nullable), and publishes the output's
  * count block nz_out (nullable; see the count-block convention above).
  * Replaces the first stage of the reference's spiking patch splitter,
- * models/spikformer_github.py:175-245 (proj_conv, proj_bn, proj_lif, maxpool),
+ * models/spikformer_github.py:181-254 (proj_conv, proj_bn, proj_lif, maxpool),
  * which runs the conv, the LIF and the pool as separate passes. */
 int cf_conv_direct_lif_maxpool(const float* x, const float* wt, const float* alpha,
                                const float* beta, const float* v_in, float* v_out,

@@ -345,7 +345,7 @@ def spike_attention_bruteforce(q, k, v, heads, scale):
 
 def spikformer_forward(model, x_seq, conv_dtype=torch.float64, record=None):
     """Spikformer forward on CPU in SpikingJelly multi-step semantics
-    (models/spikformer_github.py:175-330 with every LIF over T): SPS stages
+    (models/spikformer_github.py:162-330 with every LIF over T): SPS stages
     Conv-BN-LIF (+ MaxPool), rpe Conv-BN-LIF + its input, tokens; blocks
     x + SSA(x), x + MLP(x); token mean, pre-head LIF, head (float64).
     `record`, if a dict, receives (input, spikes) per fused layer."""
