@@ -259,13 +259,16 @@ __global__ __launch_bounds__(256) void maxpool_nhwc_kernel(
   __shared__ unsigned any_sh[4];
   const int nc8 = cp / 8;
   const int64_t units = NB * Ho * Wo * nc8;
+  // unit decode in 32-bit arithmetic (the host keeps units below 2^31):
+  // 64-bit divisions by run-time values cost far more than the pool itself
+  const uint32_t HoWo = (uint32_t)(Ho * Wo);
   uint32_t anyw = 0u;
-  for (int64_t u = (int64_t)blockIdx.x * 256 + threadIdx.x; u < units;
-       u += (int64_t)gridDim.x * 256) {
-    const int c8 = (int)(u % nc8);
-    const int64_t pix = u / nc8;
-    const int ow = (int)(pix % Wo), oh = (int)((pix / Wo) % Ho);
-    const int64_t n = pix / ((int64_t)Wo * Ho);
+  for (uint32_t u = blockIdx.x * 256u + threadIdx.x; u < (uint32_t)units; u += gridDim.x * 256u) {
+    const uint32_t pix = u / (uint32_t)nc8;
+    const int c8 = (int)(u - pix * (uint32_t)nc8);
+    const uint32_t n32 = pix / HoWo, r = pix - n32 * HoWo;
+    const int oh = (int)(r / (uint32_t)Wo), ow = (int)(r - (uint32_t)oh * (uint32_t)Wo);
+    const int64_t n = n32;
     h8 m;
     bool first = true;
     for (int dy = 0; dy < k; ++dy) {
@@ -405,7 +408,9 @@ CF_API int cf_maxpool_nhwc(const void* xp, void* out, int64_t NB, int64_t H, int
   if (Ho <= 0 || Wo <= 0) return (int)hipErrorInvalidValue;
   if (NB == 0) return 0;
   const int64_t units = NB * Ho * Wo * (cp / 8);
-  const unsigned grid = (unsigned)((units + 255) / 256 < 4096 ? (units + 255) / 256 : 4096);
+  if (units >= ((int64_t)1 << 31)) return (int)hipErrorInvalidValue;   // 32-bit unit indices
+  // about one unit a thread (more loads in flight than a grid-stride loop)
+  const unsigned grid = (unsigned)((units + 255) / 256 < 65536 ? (units + 255) / 256 : 65536);
   hipLaunchKernelGGL(maxpool_nhwc_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
                      (const _Float16*)xp, (_Float16*)out, NB, (int)H, (int)W, (int)Ho, (int)Wo,
                      (int)cp, (int)kernel_size, (int)stride, (int)padding, nz_out);
