@@ -89,22 +89,46 @@ __global__ __launch_bounds__(256) void spike_attention_kernel(AttnArgs a) {
     const _Float16* qb = a.q + img * N * a.pitch + a.qoff + h * DH;
     const _Float16* kb = a.k + img * N * a.pitch + a.koff + h * DH;
     const _Float16* vb = a.v + img * N * a.pitch + a.voff + h * DH;
-    __syncthreads();  // the previous step's reads of kT / vT / kvT are complete
-    // stage K, V transposed: unit u = (token n, 8-channel part c)
-    for (int u = tid; u < NP * 4; u += 256) {
-      const int n = u >> 2, c = (u & 3) * 8;
-      h8 kx = {}, vx = {};
-      if (n < N) {
-        kx = *reinterpret_cast<const h8*>(kb + (size_t)n * a.pitch + c);
-        vx = *reinterpret_cast<const h8*>(vb + (size_t)n * a.pitch + c);
-      }
+    // this step's Q rows (A operand: row tile*32 + col, k 16 hi ..), issued
+    // first so their latency overlaps the K^T V phase; rows beyond N read
+    // zeros (out of the buffer's range)
+    const __amdgpu_buffer_rsrc_t rq = attn_rsrc(qb, (uint32_t)(((size_t)(N - 1) * a.pitch + DH) * 2));
+    h8 qr[MAXT][2];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        kT[c + j][n] = kx[j];
-        vT[c + j][n] = vx[j];
+    for (int i = 0; i < MAXT; ++i) {
+      const int n = (wave + 4 * i) * 32 + col;
+      const uint32_t qo = n < N ? (uint32_t)(((size_t)n * a.pitch) * 2) : 0x80000000u;
+      qr[i][0] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rq, qo + 16 * hi, 0, 0));
+      qr[i][1] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rq, qo + 32 + 16 * hi, 0, 0));
+    }
+    cf_barrier_lds();  // the previous step's reads of kT / vT / kvT are complete
+    // stage K, V transposed: unit u = tid + 256 i = (token u / 4, 8-channel
+    // part u % 4); every load of the thread is issued before the first LDS
+    // write, so the step waits for one load latency, not one per unit
+    constexpr int SU = NMAX * 4 / 256;
+    h8 kx[SU], vx[SU];
+#pragma unroll
+    for (int i = 0; i < SU; ++i) {
+      const int u = tid + 256 * i, n = u >> 2, c = (u & 3) * 8;
+      kx[i] = h8{};
+      vx[i] = h8{};
+      if (n < N) {
+        kx[i] = *reinterpret_cast<const h8*>(kb + (size_t)n * a.pitch + c);
+        vx[i] = *reinterpret_cast<const h8*>(vb + (size_t)n * a.pitch + c);
       }
     }
-    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < SU; ++i) {
+      const int u = tid + 256 * i, n = u >> 2, c = (u & 3) * 8;
+      if (n < NP) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          kT[c + j][n] = kx[i][j];
+          vT[c + j][n] = vx[i][j];
+        }
+      }
+    }
+    cf_barrier_lds();
     // K^T V: wave w accumulates the K steps w, w + 4, ...
     {
       f32x16 acc = {};
@@ -117,7 +141,7 @@ __global__ __launch_bounds__(256) void spike_attention_kernel(AttnArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) kvp[wave][8 * (r >> 2) + 4 * hi + (r & 3)][col] = acc[r];
     }
-    __syncthreads();
+    cf_barrier_lds();
     // sum the partials (integers: exact in any order) and keep (K^T V)^T in
     // fp16 (entries <= N, exact): kvT[j][i] = KV[i][j]
     for (int e = tid; e < DH * DH; e += 256) {
@@ -125,24 +149,18 @@ __global__ __launch_bounds__(256) void spike_attention_kernel(AttnArgs a) {
       const float s = kvp[0][i][j] + kvp[1][i][j] + kvp[2][i][j] + kvp[3][i][j];
       kvT[j][i] = (_Float16)s;
     }
-    __syncthreads();
+    cf_barrier_lds();
     // Y = Q KV per 32-token row tile; B operand: KV[i][j = col] for i in the step
     const h8 kv0 = *reinterpret_cast<const h8*>(&kvT[col][8 * hi]);
     const h8 kv1 = *reinterpret_cast<const h8*>(&kvT[col][16 + 8 * hi]);
-    const __amdgpu_buffer_rsrc_t rq = attn_rsrc(qb, (uint32_t)(((size_t)(N - 1) * a.pitch + DH) * 2));
     _Float16* ob = a.out + img * N * a.cp_out + h * DH;
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
       const int tile = wave + 4 * i;
       if (tile >= ntile) break;
-      const int n = tile * 32 + col;   // A row of this lane
-      // rows beyond N read zeros (out of the buffer's range)
-      const uint32_t qo = n < N ? (uint32_t)(((size_t)n * a.pitch) * 2) : 0x80000000u;
-      const h8 q0 = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rq, qo + 16 * hi, 0, 0));
-      const h8 q1 = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rq, qo + 32 + 16 * hi, 0, 0));
       f32x16 y = {};
-      y = __builtin_amdgcn_mfma_f32_32x32x16_f16(q0, kv0, y, 0, 0, 0);
-      y = __builtin_amdgcn_mfma_f32_32x32x16_f16(q1, kv1, y, 0, 0, 0);
+      y = __builtin_amdgcn_mfma_f32_32x32x16_f16(qr[i][0], kv0, y, 0, 0, 0);
+      y = __builtin_amdgcn_mfma_f32_32x32x16_f16(qr[i][1], kv1, y, 0, 0, 0);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int nr = tile * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
