@@ -101,7 +101,7 @@ __global__ __launch_bounds__(256) void spike_attention_kernel(AttnArgs a) {
       qr[i][0] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rq, qo + 16 * hi, 0, 0));
       qr[i][1] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(rq, qo + 32 + 16 * hi, 0, 0));
     }
-    cf_barrier_lds();  // the previous step's reads of kT / vT / kvT are complete
+    __syncthreads();  // the previous step's reads of kT / vT / kvT are complete
     // stage K, V transposed: unit u = tid + 256 i = (token u / 4, 8-channel
     // part u % 4); every load of the thread is issued before the first LDS
     // write, so the step waits for one load latency, not one per unit
@@ -128,7 +128,7 @@ __global__ __launch_bounds__(256) void spike_attention_kernel(AttnArgs a) {
         }
       }
     }
-    cf_barrier_lds();
+    __syncthreads();
     // K^T V: wave w accumulates the K steps w, w + 4, ...
     {
       f32x16 acc = {};
@@ -141,7 +141,7 @@ __global__ __launch_bounds__(256) void spike_attention_kernel(AttnArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) kvp[wave][8 * (r >> 2) + 4 * hi + (r & 3)][col] = acc[r];
     }
-    cf_barrier_lds();
+    __syncthreads();
     // sum the partials (integers: exact in any order) and keep (K^T V)^T in
     // fp16 (entries <= N, exact): kvT[j][i] = KV[i][j]
     for (int e = tid; e < DH * DH; e += 256) {
@@ -149,7 +149,7 @@ __global__ __launch_bounds__(256) void spike_attention_kernel(AttnArgs a) {
       const float s = kvp[0][i][j] + kvp[1][i][j] + kvp[2][i][j] + kvp[3][i][j];
       kvT[j][i] = (_Float16)s;
     }
-    cf_barrier_lds();
+    __syncthreads();
     // Y = Q KV per 32-token row tile; B operand: KV[i][j = col] for i in the step
     const h8 kv0 = *reinterpret_cast<const h8*>(&kvT[col][8 * hi]);
     const h8 kv1 = *reinterpret_cast<const h8*>(&kvT[col][16 + 8 * hi]);

@@ -117,17 +117,6 @@ __device__ __forceinline__ bool lif_fire_reset_bit(float& v, const LifParams& p)
   }
 }
 
-// Workgroup barrier that orders LDS accesses only: the release / acquire
-// fences are limited to the local address space, so a wave waits for its
-// own LDS operations (lgkmcnt) but not for its outstanding global loads and
-// stores, which __syncthreads()'s full workgroup fence drains at every
-// barrier.  For kernels whose waves exchange data through LDS only.
-__device__ __forceinline__ void cf_barrier_lds() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
-}
-
 __device__ __forceinline__ float lif_initial_v(const LifParams& p) {
   return p.hard ? p.v_reset : 0.0f;
 }
