@@ -91,3 +91,37 @@ def test_stale_library_refused(monkeypatch):
     monkeypatch.setattr(_hip, "_lib", None)
     with pytest.raises(RuntimeError, match="not built from the current sources"):
         _hip.lib()
+
+
+def test_token_and_pool_entry_points_validate_arguments():
+    """The Spikformer entry points reject shapes their kernels do not cover
+    on the host, before any launch (pointers are placeholders: nothing is
+    dereferenced)."""
+    from catfuse_amd import _hip
+    L = _hip.lib()
+    lif = (2.0, 1.0, 0.0, 1, 1)
+
+    def direct_pool(Cin=3, Cout=48, cp_out=64, pad=1, H=32, W=32):
+        return L.cf_conv_direct_lif_maxpool(1, 1, 1, 1, None, None, 1, cp_out, None, 4, 2, Cin,
+                                            Cout, H, W, pad, 0, *lif, None)
+    assert direct_pool(Cin=5) == INVALID            # more than 4 input channels
+    assert direct_pool(Cout=24, cp_out=32) == INVALID   # Cout not a multiple of 16
+    assert direct_pool(cp_out=52) == INVALID        # copy pitch not a multiple of 8
+    assert direct_pool(cp_out=32) == INVALID        # copy narrower than Cout
+    assert direct_pool(pad=3) == INVALID            # padding beyond 2
+    assert direct_pool(H=1, pad=0) == INVALID       # empty conv output
+
+    def attention(N=196, heads=2, head_dim=32, pitch=192, qoff=0, cp_out=64):
+        return L.cf_spike_attention_lif(1, 1, 1, qoff, 64, 128, pitch, 1, cp_out, None, None,
+                                        None, 4, 2, N, heads, head_dim, 0.125, *lif, None)
+    assert attention(head_dim=64) == INVALID        # one 32-wide MFMA tile per head
+    assert attention(N=300) == INVALID              # more tokens than the kernel stages
+    assert attention(qoff=160) == INVALID           # Q heads beyond the pitch
+    assert attention(cp_out=32) == INVALID          # output narrower than heads * 32
+    assert attention(pitch=196) == INVALID          # pitch not a multiple of 8
+
+    def pool(cp=64, k=3, s=2, p=1):
+        return L.cf_maxpool_nhwc(1, 1, 8, 16, 16, cp, k, s, p, None, None)
+    assert pool(cp=12) == INVALID                   # 16-byte channel chunks
+    assert pool(k=2, p=2) == INVALID                # padding beyond half the window
+    assert pool(s=0) == INVALID
