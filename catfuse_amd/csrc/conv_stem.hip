@@ -61,8 +61,8 @@ struct StemArgs {
   const _Float16* w;     // [2][Coutp][KH][32]
   const float* alpha;
   const float* beta;
-  const float* v_in;     // [B][Cout][Hc][Wc] or null
-  float* v_out;          // [B][Cout][Hc][Wc] or null
+  const float* v_in;     // [B][Hc][Wc][Cout] (channels-last) or null
+  float* v_out;          // [B][Hc][Wc][Cout] (channels-last) or null
   float* out;            // [T][B][Cout][Hp][Wp] or null
   _Float16* out_nhwc;    // [T*B][Hp][Wp][cp_out] or null
   int cp_out;
@@ -170,11 +170,13 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 2 : 1) void conv_stem_kernel
     alr[r] = a.alpha[co];
     ber[r] = a.beta[co];
   }
-  // Membrane-state planes of this image: a uniform 64-bit base and 32-bit
-  // per-element offsets.
+  // Membrane state of this image, channels-last ([Hc][Wc][Cout]: a conv
+  // output's channels are contiguous, so a lane's four consecutive channels
+  // are one 16-byte access): a uniform 64-bit base and 32-bit offsets.
   const float* vin_b = a.v_in ? a.v_in + (size_t)b * a.Cout * vplane : nullptr;
   float* vout_b = a.v_out ? a.v_out + (size_t)b * a.Cout * vplane : nullptr;
   const bool full_c = cout0 + BMS <= a.Cout;
+  const bool vec_v = full_c && a.Cout % 4 == 0;   // 16-byte state accesses
 
   // Epilogue of one column tile: BN, then the LIF over T with a constant z,
   // the 16 elements of the lane stepped together; spike trains -> LDS (four
@@ -186,7 +188,7 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 2 : 1) void conv_stem_kernel
     const int y = y0 + ly, x = x0 + lx;
     const bool valid = n < NPIX && y >= 0 && y < a.Hc && x >= 0 && x < a.Wc;
     const bool own = valid && ly >= 1 && lx >= 1;
-    const unsigned vo = (unsigned)(((cout0 + cl0) * a.Hc + y) * a.Wc + x);
+    const unsigned vo = (unsigned)((y * a.Wc + x) * a.Cout + cout0 + cl0);
     float zr[16], vr[16];
     uint32_t bits[16];
 #pragma unroll
@@ -196,10 +198,18 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 2 : 1) void conv_stem_kernel
       bits[r] = 0u;
     }
     if (vin_b && valid) {
+      if (vec_v) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int dc = 8 * (r >> 2) + (r & 3);
-        if (full_c || cout0 + cl0 + dc < a.Cout) vr[r] = vin_b[vo + dc * (unsigned)vplane];
+        for (int q = 0; q < 4; ++q) {
+          const float4 f = *reinterpret_cast<const float4*>(vin_b + vo + 8 * q);
+          vr[4 * q] = f.x; vr[4 * q + 1] = f.y; vr[4 * q + 2] = f.z; vr[4 * q + 3] = f.w;
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dc = 8 * (r >> 2) + (r & 3);
+          if (cout0 + cl0 + dc < a.Cout) vr[r] = vin_b[vo + dc];
+        }
       }
     }
     for (int t = 0; t < a.T; ++t) {
@@ -211,10 +221,17 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 2 : 1) void conv_stem_kernel
       }
     }
     if (vout_b && own) {
+      if (vec_v) {
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int dc = 8 * (r >> 2) + (r & 3);
-        if (full_c || cout0 + cl0 + dc < a.Cout) vout_b[vo + dc * (unsigned)vplane] = vr[r];
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<float4*>(vout_b + vo + 8 * q) =
+              make_float4(vr[4 * q], vr[4 * q + 1], vr[4 * q + 2], vr[4 * q + 3]);
+      } else {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dc = 8 * (r >> 2) + (r & 3);
+          if (cout0 + cl0 + dc < a.Cout) vout_b[vo + dc] = vr[r];
+        }
       }
     }
     if (n < NPIX) {

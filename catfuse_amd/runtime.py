@@ -961,7 +961,8 @@ class ConvLIFRunner:
     def run_stem_pool(self, x: torch.Tensor, v_in=None, *, want_v_out=True, emit_nhwc=True):
         """x [T, B, Cin, H, W] with a stride-0 time axis.  Returns the pooled
         spikes [T, B, Cout, Hp, Wp] (carrying the fp16 NHWC copy when
-        emit_nhwc) and the conv-resolution membrane [B, Cout, Hc, Wc]."""
+        emit_nhwc) and the conv-resolution membrane [B, Cout, Hc, Wc]
+        (channels_last memory format)."""
         if not self.stem_supported(x, (3, 2, 1)):
             raise ValueError("input/layer not covered by the fused stem kernel")
         T, B, C, H, W = x.shape
@@ -970,12 +971,14 @@ class ConvLIFRunner:
         self._ensure_stem_packed(dev)
         Hc, Wc = self.out_hw(H, W)
         Hp, Wp = (Hc - 1) // 2 + 1, (Wc - 1) // 2 + 1
+        # the membrane is kept channels-last (the kernel's state layout)
         if v_in is not None:
-            require_gpu_tensor(v_in, "v_in")
-            if v_in.numel() != B * self.Cout * Hc * Wc:
-                raise ValueError("v_in has the wrong size")
-        v_out = (torch.empty((B, self.Cout, Hc, Wc), dtype=torch.float32, device=dev)
-                 if want_v_out else None)
+            if not isinstance(v_in, torch.Tensor) or tuple(v_in.shape) != (B, self.Cout, Hc, Wc):
+                raise ValueError("v_in must be a [B, Cout, Hc, Wc] tensor")
+            v_in = v_in.contiguous(memory_format=torch.channels_last)
+            require_gpu_tensor(v_in.permute(0, 2, 3, 1), "v_in")   # its [B, Hc, Wc, Cout] storage
+        v_out = (torch.empty((B, self.Cout, Hc, Wc), dtype=torch.float32, device=dev,
+                             memory_format=torch.channels_last) if want_v_out else None)
         cp_out = pad32(self.Cout)
         if emit_nhwc:
             nhwc = torch.empty((T * B, Hp, Wp, cp_out), dtype=torch.float16, device=dev)

@@ -309,8 +309,10 @@ int cf_pack_stem_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
  * <= 32 steps: the conv runs once, its z feeds every LIF step).  The image
  * is split into fp16 hi/lo limbs; products wh*xh + wl*xh + wh*xl accumulate
  * in fp32.  Outputs the pooled spikes out [T][B][Cout][Hp][Wp] and/or their
- * fp16 NHWC copy [T*B][Hp][Wp][cp_out]; v_in/v_out [B][Cout][Hc][Wc] hold
- * the conv-resolution membrane.  status |= 2 if |x| > 65504 or not finite.
+ * fp16 NHWC copy [T*B][Hp][Wp][cp_out]; v_in/v_out hold the
+ * conv-resolution membrane channels-last, [B][Hc][Wc][Cout] (a conv output's
+ * channels contiguous: 16-byte state accesses; torch's channels_last format
+ * of a [B, Cout, Hc, Wc] tensor).  status |= 2 if |x| > 65504 or not finite.
  * Replaces catfuse/implementations/dense_keep.py:97-155 (conv1/bn1/sn1 via
  * catfuse/patterns.py:237-387) plus the unfused SpikingJelly MaxPool2d that
  * follows it in the ResNet stem. */
