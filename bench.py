@@ -57,11 +57,11 @@ def build_model(num_classes=1000, seed=0, workload="sew_resnet18"):
     return m.eval()
 
 
-def traffic_from_profiles():
+def traffic_from_profiles(name="conv_halo_sew_resnet18_traffic.json"):
     """HBM bytes per launch of the dominant kernel from the committed
-    rocprofv3 PMC summary (profiles/conv_halo_sew_resnet18_traffic.json), or
-    None when it has not been collected."""
-    p = os.path.join(ROOT, "profiles", "conv_halo_sew_resnet18_traffic.json")
+    rocprofv3 PMC summary profiles/<name>, or None when it has not been
+    collected."""
+    p = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(p):
         return None
     try:
@@ -266,25 +266,38 @@ def main():
                   for k, v in kern.items()}
 
     if spikformer:
-        # the token linears (1x1 convs over each image's token grid) dominate
+        # token linears (1x1 convs over the token rows) and the attention core
         l_ms, l_fl, _, l_n = agg(["linear_tokens"])
         lz_ms, _, _, lz_n = agg(["linear_tokens_staticzero"])
+        # route of each token-linear launch of one forward (D: MFMA K loop,
+        # Z: StaticZero), decided on the device and read back here
+        lin_recs = [r for r in timer.records if r[0].startswith("linear_tokens")]
+        per_fwd_l = len(lin_recs) // max(1, args.steps)
+        lin_seq = "".join("Z" if (r[5] is not None and r[5].is_zero()) else "D"
+                          for r in lin_recs[:per_fwd_l])
         a_ms, a_fl, a_b, a_n = agg(["spike_attention"])
+        # the dominant MFMA work is the patch splitter's 3x3 convs (the token
+        # linears take StaticZero when their input is all zero)
+        roofline["kernel"] = ("conv_halo_kernel 3x3 (cf_conv_mfma: the SPS Conv-BN-LIF stages), "
+                              "launches that run the MFMA K loop")
+        roofline["traffic"] = traffic_from_profiles("conv_halo_spikformer_8_384_traffic.json")
+        roofline["conv_route_sequence"] = route_seq
         ach = l_fl / (l_ms * 1e-3) / 1e12 if l_ms else 0.0
-        roofline = {"kernel": "conv_halo_kernel 1x1 (cf_conv_mfma: fused Linear-BN1d-LIF over the "
-                              "token grid), launches that run the MFMA K loop",
-                    "bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_FP16_TFLOPS,
-                    "unit": "TFLOP/s", "frac": round(ach / PEAK_FP16_TFLOPS, 4), "traffic": None,
-                    "flops_per_launch_avg": l_fl // max(1, l_n),
-                    "us_per_launch_avg": round(l_ms * 1e3 / max(1, l_n), 2),
-                    "launches_per_step": l_n // args.steps,
-                    "staticzero_launches_per_step": lz_n // args.steps}
+        linears = {"kernel": "conv_halo_kernel 1x1 (cf_conv_mfma: fused Linear-BN1d-LIF over the "
+                             "token rows)",
+                   "launches_per_step": (l_n + lz_n) // args.steps,
+                   "mfma_route": {"launches_per_step": l_n // args.steps,
+                                  "us_per_launch_avg": round(l_ms * 1e3 / max(1, l_n), 2),
+                                  "achieved": round(ach, 2), "unit": "TFLOP/s"},
+                   "staticzero_route": {"launches_per_step": lz_n // args.steps,
+                                        "us_per_launch_avg": round(lz_ms * 1e3 / max(1, lz_n), 2)},
+                   "linear_route_sequence": lin_seq}
         a_gbps = a_b / (a_ms * 1e-3) / 1e9 if a_ms else 0.0
-        staticzero = {"kernel": "spike_attention_kernel (cf_spike_attention_lif)",
-                      "launches_per_step": a_n // args.steps,
-                      "us_per_launch_avg": round(a_ms * 1e3 / max(1, a_n), 2),
-                      "achieved": round(a_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                      "frac": round(a_gbps / PEAK_HBM_GBPS, 4)}
+        attention = {"kernel": "spike_attention_kernel (cf_spike_attention_lif)",
+                     "launches_per_step": a_n // args.steps,
+                     "us_per_launch_avg": round(a_ms * 1e3 / max(1, a_n), 2),
+                     "achieved": round(a_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                     "frac": round(a_gbps / PEAK_HBM_GBPS, 4)}
     result = {
         "metric": METRIC, "value": round(ips, 2), "unit": "images/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
@@ -309,8 +322,8 @@ def main():
                             "total_lif_nodes": stats["total_lif_nodes"]}
         result["dtype"] = ("fp32 (linears/convs: fp16 hi/lo split weights x fp16-exact spikes on "
                            "MFMA, fp32 acc; attention: exact integer Q(K^T V), one fp32 rounding)")
-        del result["staticzero_convs"]
-        result["attention"] = staticzero
+        result["token_linears"] = linears
+        result["attention"] = attention
     if not args.no_tails and not spikformer:
         result["lif_tails"] = measure_tails(dev)
     if not args.no_cpu_baseline:

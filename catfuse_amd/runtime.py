@@ -491,12 +491,13 @@ def maxpool_nhwc(x: torch.Tensor, kernel_size: int, stride: int, padding: int,
 def spike_attention_lif(qkv: torch.Tensor, T: int, B: int, N: int, heads: int, offsets,
                         scale: float, tau=2.0, v_threshold=1.0, v_reset=0.0, decay_input=True,
                         v_in: Optional[torch.Tensor] = None, want_v_out=True,
-                        nz_out: Optional[torch.Tensor] = None):
+                        nz_out: Optional[torch.Tensor] = None, gen_cell: Optional[list] = None):
     """Spikformer's SSA core on the fp16 token copy qkv [T*B*N, pitch] that
     holds Q, K, V at channel offsets (qoff, koff, voff) (head h at
     off + 32h ..): LIF_T(((Q K^T) V) * scale) per head, evaluated as
     Q (K^T V) on the matrix cores.  Returns (TokenSpikes [T, B, N, heads*32],
-    v_out [B, N, heads*32] or None)."""
+    carrying the count block nz_out when it and gen_cell are given, so the
+    next fused linear routes on it; v_out [B, N, heads*32] or None)."""
     require_gpu_tensor(qkv, "qkv", dtype=torch.float16)
     _require_block(nz_out)
     dev = qkv.device
@@ -521,6 +522,9 @@ def spike_attention_lif(qkv: torch.Tensor, T: int, B: int, N: int, heads: int, o
     _t1("spike_attention", ev, flops=4 * T * B * heads * N * 32 * 32,
         nbytes=2 * T * B * N * 3 * C + 2 * T * B * N * cp)
     out = lazy_tokens((T, B, N, C), copy, dev)
+    if nz_out is not None and gen_cell is not None:
+        gen_cell[0] += 1
+        attach_count(out, nz_out, gen_cell)
     return out, v_out
 
 

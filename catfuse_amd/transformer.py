@@ -160,6 +160,8 @@ class CTFSpikformerSSA(CTFPattern):
         self.attn_lif = dict(attn_lif_params)
         self.attn_state = StateBuffer()
         self._register_state(self.attn_state)
+        self._attn_gen = [0]        # calls that published the core's count block
+        self._attn_blocks = {}
 
     def forward(self, x, residual=None):
         T, B, N, C = x.shape
@@ -170,9 +172,17 @@ class CTFSpikformerSSA(CTFPattern):
         a, v = spike_attention_lif(copy, T, B, N, self.num_heads, (0, C, 2 * C), self.scale,
                                    tau=lp["tau"], v_threshold=lp["v_threshold"],
                                    v_reset=lp["v_reset"], decay_input=lp["decay_input"],
-                                   v_in=v_in)
+                                   v_in=v_in, nz_out=self._attn_block(x.device),
+                                   gen_cell=self._attn_gen)
         self.attn_state.set(v)
         return self.proj(a, identity=residual)
+
+    def _attn_block(self, device):
+        blk = self._attn_blocks.get(device)
+        if blk is None:
+            blk = count_block(device)
+            self._attn_blocks[device] = blk
+        return blk
 
     @classmethod
     def from_sj_module(cls, ssa):

@@ -265,3 +265,23 @@ def test_conv_direct_lif_maxpool_bitwise(cuda, case):
     y2, _ = r.run_direct_pool(x[:, :1], None if v_in is None else v_in[:1], nz_out=blk,
                               gen_cell=[0])
     assert torch.equal(y2.reshape(T, *ref.shape[1:]), ref.reshape(T, B, *ref.shape[1:])[:, 0])
+
+
+def test_spike_attention_count_block(cuda):
+    """The attention core publishes its output's count block (zero iff no
+    spike) and attaches it to the output, so the proj linear can take the
+    StaticZero route on it."""
+    from catfuse_amd import runtime
+    T, B, N, heads = 4, 2, 64, 2
+    C = 32 * heads
+    blk = runtime.count_block(cuda)
+    for density, v_th in ((0.3, 0.5), (0.0, 1.0)):
+        qkv = (torch.rand(T * B * N, 3 * C, generator=_gen(7)) < density).half().to(cuda)
+        out, _ = runtime.spike_attention_lif(qkv, T, B, N, heads, (0, C, 2 * C), 0.125,
+                                             v_threshold=v_th, nz_out=blk, gen_cell=[0])
+        assert runtime.count_of(out) is blk
+        assert (int(blk[1].item()) == 0) == (not bool(out.any()))
+        if density == 0.0:
+            assert int(blk[1].item()) == 0
+        else:
+            assert bool(out.any())
