@@ -234,3 +234,23 @@ def test_fused_global_avgpool_fallback_cpu():
     ps = FusedGlobalAvgPool.from_sj_modules(snn.AdaptiveAvgPool2d((1, 1)))
     assert ps.step_mode == "s"
     assert torch.equal(ps(x[0]), torch.nn.functional.adaptive_avg_pool2d(x[0], 1))
+
+
+def test_token_view_and_membrane_layout():
+    """A token linear views the B*N tokens of a step as 8x8 images of 64
+    consecutive tokens when 64 divides B*N, else per image; its state is per
+    view image [nimg, C, H*W], and token_membrane returns it as [B, N, C]."""
+    import torch
+    from catfuse_amd.runtime import token_membrane, token_view
+    assert token_view(32, 196) == (98, 8, 8)
+    assert token_view(2, 64) == (2, 8, 8)
+    assert token_view(2, 196) == (2, 14, 14)
+    assert token_view(3, 10) == (3, 10, 1)
+    assert token_view(3, 1) == (3, 1, 1)
+    for B, N, C in ((32, 196, 5), (2, 196, 3), (3, 10, 4)):
+        nimg, H, W = token_view(B, N)
+        # natural state [B, N, C] -> the kernel's per-view-image layout
+        nat = torch.arange(B * N * C, dtype=torch.float32).view(B, N, C)
+        rows = nat.reshape(B * N, C)                       # token-major rows of one step
+        view = rows.view(nimg, H * W, C).transpose(1, 2)   # [nimg, C, H*W] (NCHW per image)
+        assert torch.equal(token_membrane(view.contiguous(), B, N), nat)
