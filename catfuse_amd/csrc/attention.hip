@@ -52,8 +52,12 @@ template <int LM>
 __global__ __launch_bounds__(256) void spike_attention_kernel(AttnArgs a) {
   // K and V of the current step, transposed ([d][n], n padded to a
   // multiple of 16 with zeros) so each MFMA operand is one 16-byte read.
-  __shared__ __attribute__((aligned(16))) _Float16 kT[DH][NMAX];
-  __shared__ __attribute__((aligned(16))) _Float16 vT[DH][NMAX];
+  // Rows are NMAX + 8 halves apart (528 bytes, 132 dwords: 4 banks on from
+  // the row above), so the 32 rows an operand read touches spread over all
+  // banks instead of sharing four.
+  constexpr int KLD = NMAX + 8;
+  __shared__ __attribute__((aligned(16))) _Float16 kT[DH][KLD];
+  __shared__ __attribute__((aligned(16))) _Float16 vT[DH][KLD];
   __shared__ __attribute__((aligned(16))) float kvp[4][DH][DH + 1];  // per-wave partial K^T V
   __shared__ __attribute__((aligned(16))) _Float16 kvT[DH][DH];      // (K^T V)^T as fp16
   __shared__ unsigned any_sh[4];
