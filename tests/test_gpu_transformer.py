@@ -195,7 +195,8 @@ def test_spikformer_layers_and_logits(cuda):
     assert torch.equal(y, y2)
 
 
-@pytest.mark.parametrize("shape,k,s,p", [((3, 2, 40, 17, 23), 3, 2, 1), ((2, 2, 64, 8, 8), 2, 2, 0),
+@pytest.mark.parametrize("shape,k,s,p", [((3, 2, 40, 17, 23), 3, 2, 1), ((2, 3, 96, 20, 15), 3, 2, 1),
+                                         ((1, 2, 200, 9, 33), 3, 2, 1), ((2, 2, 64, 8, 8), 2, 2, 0),
                                          ((2, 1, 96, 9, 9), 3, 1, 1)])
 def test_maxpool_nhwc_bitwise(cuda, shape, k, s, p):
     """The NHWC max pool of a fused output equals torch's max_pool2d of the
