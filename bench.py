@@ -1,32 +1,47 @@
-"""Benchmark: SEW-ResNet18 (ADD, LIF tau=2, v_th=1, hard reset) T=4, B=32,
-3x224x224 direct-encoded input, fused by catfuse_amd.optimize on one MI355X.
+"""Benchmark of the fused SNN inference path on one MI355X.
+
+Workloads (--workload):
+  sew_resnet18     the headline (config C3): SEW-ResNet18 (ADD, LIF tau=2,
+                   v_th=1, hard reset), T=4, B=32, 3x224x224 direct-encoded,
+                   random kaiming weights, config-0 BN statistics; plus its
+                   "live" companion: the same network with v_th = 0.1, the
+                   reference's own end-to-end setting
+                   (benchmarks/bench_sew_resnet18_e2e.py:101-115) under its
+                   liveness check (>= 80% of the SEW blocks with spike rate
+                   > 1e-4, :268-287), reported in its own keys;
+  spikformer_8_384 config C4 (spiking transformer), its own metric line;
+  vgg11_bn         config C2: spiking VGG-11-BN, T=4, B=64, 3x32x32;
+  sf_crossover     the SparseFlow / dense crossover sweep of one fused
+                   Conv3x3-BN-LIF layer (config C1 shapes) that sets the
+                   MI355X routing threshold; prints a markdown table.
 
 One step = one full forward of the fused network over the batch (all T
-steps, stem to logits) on synthetic inputs resident in HBM, with a
-functional.reset_net before it: by default a replay of the HIP graph that
-catfuse_amd.graph.capture records for reset_net + forward (the batch is
-copied into the graph's input first, inside the timed step; the replay's
-output is checked against the eager forward's); --eager times the eager
-launches instead.  Prints ONE JSON line (rank 0):
-  value      = images/s = B / (seconds per step)
-  roofline   = dominant kernel (the MFMA conv, conv_halo_kernel behind
-               cf_conv_mfma) achieved TFLOP/s over its launches that ran the
-               MFMA K loop (dense route) vs the 2.5 PFLOP/s fp16 dense MFMA
-               peak, timed with HIP events on the launch stream around every
-               launch of an eager pass over the same steps (the kernels the
-               graph replays); the launches that took the StaticZero route
-               (all-zero input: no K loop) are reported apart, as output
-               bytes written per second vs the 8 TB/s HBM peak
-  lif_tails  = standalone LIF-family kernels' achieved HBM GB/s vs 8 TB/s
-  cpu_baseline = the CPU oracle (SpikingJelly-equivalent PyTorch/C
-               multi-step path, fp32) on a bounded sample of the same
-               workload on this host's cores
+steps, stem to logits) on synthetic inputs resident in HBM, after a
+functional.reset_net: by default a replay of the HIP graph that
+catfuse_amd.capture records for reset_net + forward (the batch is copied
+into the graph's input first, inside the timed step; the replay's output is
+checked against the eager forward's); --eager times the eager launches.
+Prints ONE JSON line:
+  value        images/s = B / (seconds per step)
+  roofline     the dominant kernel (conv_halo_kernel behind cf_conv_mfma, the
+               fused Conv-BN-LIF) over its launches that ran the MFMA K loop:
+               dense-equivalent FLOPs / HIP-event time on the launch stream,
+               vs the 2.5 PFLOP/s dense fp16 MFMA peak
+  per_layer    every conv launch of one forward: layer, route, time, TFLOP/s
+  staticzero_convs  the conv launches that took StaticZero (all-zero input)
+  lif_tails    standalone LIF-family kernels' HBM GB/s vs 8 TB/s
+  cpu_baseline the CPU oracle's forward (fp32 torch conv + eval BN + C LIF,
+               SpikingJelly multi-step semantics) on this host's cores: 1
+               warm-up forward, then >= 3 timed forwards of a stated batch,
+               median; beside it the eager SpikingJelly-equivalent model
+               (catfuse_amd.snn, LIFNode's recurrence in torch), same protocol
 """
 from __future__ import annotations
 
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -37,30 +52,199 @@ if ROOT not in sys.path:
 METRIC = "SEW-ResNet18 T=4 images/s on 1 MI355X; fused-LIF HBM GB/s vs peak"
 PEAK_FP16_TFLOPS = 2500.0   # MI355X dense fp16 MFMA
 PEAK_HBM_GBPS = 8000.0
+LIVE_V_THRESHOLD = 0.1      # benchmarks/bench_sew_resnet18_e2e.py:101-115
+LIVE_RATE = 1e-4            # a block is alive above this spike rate (:268-287)
+LIVE_MIN_FRACTION = 0.8
+
+# images per CPU-baseline forward (a bounded sample: ~10-30 s of host work)
+CPU_BATCH = {"sew_resnet18": 8, "spikformer_8_384": 2, "vgg11_bn": 64}
+
+WORKLOADS = {
+    "sew_resnet18": dict(T=4, batch=32, image=224),
+    "spikformer_8_384": dict(T=4, batch=32, image=224),
+    "vgg11_bn": dict(T=4, batch=64, image=32),
+}
 
 
-def build_model(num_classes=1000, seed=0, workload="sew_resnet18"):
+# ---------------------------------------------------------------------------
+# models and timing
+# ---------------------------------------------------------------------------
+
+def build_model(workload="sew_resnet18", v_threshold=1.0, seed=0, num_classes=None):
+    """The unfused SpikingJelly-style model of a workload, seeded kaiming
+    weights and config-0 BN statistics."""
     import torch
     from catfuse_amd import snn
     g = torch.Generator().manual_seed(seed)
     if workload == "spikformer_8_384":
-        # config C4: random init (seeded kaiming weights, config-0 BN statistics)
-        m = snn.spikformer_8_384(num_classes=num_classes, T=4)
-        snn.kaiming_init(m, g)
-        snn.randomize_bn(m, g)
-        return m.eval()
-    m = snn.sew_resnet18(num_classes=num_classes, cnf="ADD", tau=2.0, v_threshold=1.0,
-                         v_reset=0.0)
+        m = snn.spikformer_8_384(num_classes=num_classes or 1000, T=4, v_threshold=v_threshold)
+    elif workload == "vgg11_bn":
+        m = snn.spiking_vgg11_bn(num_classes=num_classes or 10, v_threshold=v_threshold)
+    else:
+        m = snn.sew_resnet18(num_classes=num_classes or 1000, cnf="ADD", tau=2.0,
+                             v_threshold=v_threshold, v_reset=0.0)
     snn.functional.set_step_mode(m, "m")
     snn.kaiming_init(m, g)
     snn.randomize_bn(m, g)
     return m.eval()
 
 
+def _conv_patterns():
+    from catfuse_amd.patterns import PartialFusionConvBNLIF, PartialFusionConvLIF
+    from catfuse_amd.sparseflow.ops.st_fusion_conv_bn_lif import STFusionConvBNLIF
+    from catfuse_amd.patterns import FusedLinearLIF
+    from catfuse_amd.transformer import FusedLinearBNLIF
+    return (PartialFusionConvBNLIF, PartialFusionConvLIF, STFusionConvBNLIF, FusedLinearLIF,
+            FusedLinearBNLIF)
+
+
+def label_launches(model, timer):
+    """Forward hooks on every fused conv / linear layer that attribute the
+    timer records its call appended to the layer's module path.  Returns
+    (spans, handles); spans: [(name, first record, end record)]."""
+    spans, handles, stack = [], [], []
+    kinds = _conv_patterns()
+    for name, mod in model.named_modules():
+        if isinstance(mod, kinds):
+            handles.append(mod.register_forward_pre_hook(
+                lambda m, a: stack.append(len(timer.records))))
+            handles.append(mod.register_forward_hook(
+                lambda m, a, o, name=name: spans.append((name, stack.pop(),
+                                                         len(timer.records)))))
+    return spans, handles
+
+
+def time_forward(fused, x, img, steps, warmup, eager=False, label=False):
+    """Warm-up, an eager pass of `steps` forwards with HIP events around
+    every launch (per-kernel times; the same kernels the graph replays),
+    then (unless eager) `steps` replays of the captured graph.  Returns
+    dict(ms, ms_eager, mode, timer, spans)."""
+    import torch
+    import catfuse_amd
+    from catfuse_amd import graph as cf_graph
+    from catfuse_amd import runtime, snn
+    dev = x.device
+    with torch.no_grad():
+        for _ in range(warmup):
+            snn.functional.reset_net(fused)
+            fused(x)
+        torch.cuda.synchronize()
+        catfuse_amd.check_status(dev)
+        timer = runtime.KernelTimer()
+        spans, handles = label_launches(fused, timer) if label else ([], [])
+        runtime.set_timer(timer)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            snn.functional.reset_net(fused)
+            y = fused(x)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        runtime.set_timer(None)
+        for h in handles:
+            h.remove()
+        ms_eager = (t1 - t0) * 1e3 / steps
+        ms, mode = ms_eager, "eager"
+        if not eager:
+            graphed = cf_graph.capture(fused, x)
+            y_ref = y.clone()
+            for _ in range(warmup):
+                graphed(img)
+            torch.cuda.synchronize()
+            if not torch.equal(graphed(img), y_ref):
+                raise SystemExit("graph replay differs from the eager forward")
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                graphed(img)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            ms, mode = (t1 - t0) * 1e3 / steps, "hip_graph"
+            del graphed
+        catfuse_amd.check_status(dev)
+    return dict(ms=ms, ms_eager=ms_eager, mode=mode, timer=timer, spans=spans, steps=steps)
+
+
+def _agg(kern, names):
+    ds = [kern.get(n, {}) for n in names]
+    return (sum(d.get("ms_total", 0.0) for d in ds), sum(d.get("flops", 0) for d in ds),
+            sum(d.get("bytes", 0) for d in ds), sum(d.get("launches", 0) for d in ds))
+
+
+def conv_roofline(kern, steps, names=("conv_mfma", "conv_mfma_sparse"), traffic=None):
+    tot_ms, tot_fl, _, launches = _agg(kern, names)
+    achieved = tot_fl / (tot_ms * 1e-3) / 1e12 if tot_ms else 0.0
+    return {"kernel": "conv_halo_kernel (cf_conv_mfma fused Conv-BN-LIF), launches that run "
+                      "the MFMA K loop",
+            "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
+            "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
+            "traffic": traffic,
+            "flops_per_launch_avg": tot_fl // max(1, launches),
+            "us_per_launch_avg": round(tot_ms * 1e3 / max(1, launches), 2),
+            "launches_per_step": launches // max(1, steps)}
+
+
+def staticzero_summary(kern, steps, names=("conv_mfma_staticzero",
+                                          "conv_mfma_sparse_staticzero")):
+    z_ms, _, z_bytes, z_n = _agg(kern, names)
+    gbps = z_bytes / (z_ms * 1e-3) / 1e9 if z_ms else 0.0
+    return {"kernel": "conv_halo_kernel on the StaticZero route (all-zero input: BN bias -> "
+                      "LIF, no K loop)",
+            "bound": "hbm", "launches_per_step": z_n // max(1, steps),
+            "us_per_step": round(z_ms * 1e3 / max(1, steps), 2),
+            "us_per_launch_avg": round(z_ms * 1e3 / max(1, z_n), 2),
+            "bytes_per_launch_avg": z_bytes // max(1, z_n),
+            "achieved": round(gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+            "frac": round(gbps / PEAK_HBM_GBPS, 4)}
+
+
+def route_sequence(timer, prefix, steps):
+    """Route of each launch named prefix* in one forward, in launch order
+    (D: the MFMA K loop ran, Z: StaticZero), read back from the devices'
+    count blocks after the timed region."""
+    recs = [r for r in timer.records if r[0].startswith(prefix)]
+    per = len(recs) // max(1, steps)
+    return "".join("Z" if (r[5] is not None and r[5].is_zero()) else "D" for r in recs[:per])
+
+
+def per_layer_table(res, kernels=("conv_mfma", "conv_stem", "conv_direct", "linear_tokens")):
+    """One row per conv / linear launch of one forward (averaged over the
+    eager steps): layer path, kernel, route, us, dense-equivalent TFLOP/s and
+    fraction of the MFMA peak."""
+    timer, spans, steps = res["timer"], res["spans"], res["steps"]
+    label = {}
+    for name, a, b in spans:
+        for i in range(a, b):
+            label.setdefault(i, name)
+    rows = {}
+    order = []
+    for i, (kname, e0, e1, fl, nb, route) in enumerate(timer.records):
+        if not kname.startswith(kernels):
+            continue
+        key = (label.get(i, "?"), kname)
+        if key not in rows:
+            rows[key] = dict(layer=key[0], kernel=kname, n=0, ms=0.0, flops=0, zero=False)
+            order.append(key)
+        r = rows[key]
+        r["n"] += 1
+        r["ms"] += e0.elapsed_time(e1)
+        r["flops"] += fl
+        r["zero"] = bool(route is not None and route.is_zero())
+    out = []
+    for key in order:
+        r = rows[key]
+        us = r["ms"] * 1e3 / r["n"]
+        fl = r["flops"] / r["n"]
+        tf = 0.0 if r["zero"] else fl / (us * 1e-6) / 1e12
+        out.append({"layer": r["layer"], "kernel": r["kernel"], "route": "Z" if r["zero"] else "D",
+                    "us": round(us, 2), "gflop": round(fl / 1e9, 3),
+                    "TFLOP/s": round(tf, 1), "frac": round(tf / PEAK_FP16_TFLOPS, 4)})
+    return out
+
+
 def traffic_from_profiles(name="conv_halo_sew_resnet18_traffic.json"):
     """HBM bytes per launch of the dominant kernel from the committed
-    rocprofv3 PMC summary profiles/<name>, or None when it has not been
-    collected."""
+    rocprofv3 PMC summary profiles/<name>, or None when absent."""
     p = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(p):
         return None
@@ -68,6 +252,37 @@ def traffic_from_profiles(name="conv_halo_sew_resnet18_traffic.json"):
         return json.load(open(p)).get("hbm_bytes_per_launch")
     except Exception:
         return None
+
+
+def liveness(fused, x):
+    """Spike rate of every SEW block's output (CTFSEWBasicBlock), as the
+    reference's harness checks it: (alive fraction, {block: rate})."""
+    import torch
+    from catfuse_amd import snn
+    rates, hs = {}, []
+    for name, mod in fused.named_modules():
+        if type(mod).__name__ == "CTFSEWBasicBlock":
+            hs.append(mod.register_forward_hook(
+                lambda m, a, o, name=name: rates.__setitem__(name, float(o.float().mean()))))
+    with torch.no_grad():
+        snn.functional.reset_net(fused)
+        fused(x)
+    for h in hs:
+        h.remove()
+    alive = sum(1 for r in rates.values() if r > LIVE_RATE)
+    return alive / max(1, len(rates)), {k: round(v, 6) for k, v in rates.items()}
+
+
+# ---------------------------------------------------------------------------
+# LIF tails
+# ---------------------------------------------------------------------------
+
+def _tail_row(kernel, shape, timer):
+    s = next(iter(timer.summary().values()))
+    gbps = s["bytes"] / (s["ms_total"] * 1e-3) / 1e9
+    return {"kernel": kernel, "shape": list(shape), "bytes_per_launch": s["bytes"] // s["launches"],
+            "us_per_launch": round(s["ms_avg"] * 1e3, 2), "GB/s": round(gbps, 1),
+            "frac": round(gbps / PEAK_HBM_GBPS, 4)}
 
 
 def measure_tails(dev, reps=20):
@@ -91,20 +306,18 @@ def measure_tails(dev, reps=20):
         sh = torch.randn(C, device=dev, generator=g) * 0.1
         v0 = torch.zeros(B, C, H, W, device=dev)
         for _ in range(3):
-            runtime.lif_multistep(z, v0, mode=mode, z2=z2, scale=sc, shift=sh, channels=C, hw=H * W)
+            runtime.lif_multistep(z, v0, mode=mode, z2=z2, scale=sc, shift=sh, channels=C,
+                                  hw=H * W)
         timer = runtime.KernelTimer()
         runtime.set_timer(timer)
         for _ in range(reps):
-            runtime.lif_multistep(z, v0, mode=mode, z2=z2, scale=sc, shift=sh, channels=C, hw=H * W)
+            runtime.lif_multistep(z, v0, mode=mode, z2=z2, scale=sc, shift=sh, channels=C,
+                                  hw=H * W)
         runtime.set_timer(None)
-        s = next(iter(timer.summary().values()))
-        gbps = s["bytes"] / (s["ms_total"] * 1e-3) / 1e9
-        out.append({"kernel": f"cf_lif_multistep/{name}", "shape": list(shape),
-                    "bytes_per_launch": s["bytes"] // s["launches"],
-                    "us_per_launch": round(s["ms_avg"] * 1e3, 2), "GB/s": round(gbps, 1),
-                    "frac": round(gbps / PEAK_HBM_GBPS, 4)})
+        out.append(_tail_row(f"cf_lif_multistep/{name}", shape, timer))
         del z, z2
-    x = torch.rand((4, 32, 128, 32, 32), device=dev, generator=g)
+    shape = (4, 32, 128, 32, 32)
+    x = torch.rand(shape, device=dev, generator=g)
     for _ in range(3):
         runtime.avgpool2x2_lif(x)
     timer = runtime.KernelTimer()
@@ -112,225 +325,425 @@ def measure_tails(dev, reps=20):
     for _ in range(reps):
         runtime.avgpool2x2_lif(x)
     runtime.set_timer(None)
-    s = next(iter(timer.summary().values()))
-    gbps = s["bytes"] / (s["ms_total"] * 1e-3) / 1e9
-    out.append({"kernel": "cf_avgpool2x2_lif", "shape": [4, 32, 128, 32, 32],
-                "bytes_per_launch": s["bytes"] // s["launches"],
-                "us_per_launch": round(s["ms_avg"] * 1e3, 2), "GB/s": round(gbps, 1),
-                "frac": round(gbps / PEAK_HBM_GBPS, 4)})
+    out.append(_tail_row("cf_avgpool2x2_lif", shape, timer))
     return out
 
 
-def cpu_baseline(model, T, image, budget_s=12.0, forward=None):
-    """Oracle forward (fp32 torch CPU conv + eval BN + C LIF, SpikingJelly
-    multi-step semantics) on this host: 1 warm-up image, then batches of 2
-    images until about budget_s seconds have been timed."""
+# ---------------------------------------------------------------------------
+# CPU baseline
+# ---------------------------------------------------------------------------
+
+def cpu_model_name():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _median_forwards(fn, reps, budget_s):
+    """1 warm-up call, then `reps` timed calls (up to 9 while under
+    budget_s): (median seconds, all times)."""
+    fn()
+    times, spent = [], 0.0
+    while len(times) < reps or (spent < budget_s and len(times) < 9):
+        t0 = time.perf_counter()
+        fn()
+        dt = time.perf_counter() - t0
+        times.append(dt)
+        spent += dt
+    return statistics.median(times), times
+
+
+def cpu_baseline(model, workload, T, batch, image, reps=3, budget_s=10.0):
+    """The CPU oracle's network forward (oracle.sew_resnet_forward /
+    spikformer_forward / vgg_forward in fp32: torch CPU conv, eval BN, the C
+    LIF of SpikingJelly's multi-step recurrence) on this host's threads,
+    1 warm-up forward then >= `reps` timed forwards of `batch` images,
+    median.  Beside it, the same protocol for the eager SpikingJelly-
+    equivalent model (catfuse_amd.snn modules: LIFNode's recurrence in torch)."""
+    import copy
     import torch
     import oracle
-    fwd = forward or oracle.sew_resnet_forward
+    from catfuse_amd import snn
     threads = int(os.environ.get("OMP_NUM_THREADS", os.cpu_count() or 1))
     torch.set_num_threads(threads)
+    m = copy.deepcopy(model).cpu().eval()
     g = torch.Generator().manual_seed(1)
-    x1 = torch.randn(1, 3, image, image, generator=g)
-    fwd(model, x1.unsqueeze(0).expand(T, 1, 3, image, image), conv_dtype=torch.float32)
-    x2 = torch.randn(2, 3, image, image, generator=g)
-    xs = x2.unsqueeze(0).expand(T, 2, 3, image, image)
-    imgs, t_total = 0, 0.0
-    while t_total < budget_s:
-        t0 = time.perf_counter()
-        fwd(model, xs, conv_dtype=torch.float32)
-        t_total += time.perf_counter() - t0
-        imgs += 2
-    return {"value": round(imgs / t_total, 3), "unit": "images/s", "cores": threads,
-            "kind": "port",
-            "sample": f"{imgs} images of 3x{image}x{image}, T={T}, in batches of 2 "
-                      f"({t_total:.1f} s), after 1 warm-up image"}
+    img = torch.randn(batch, 3, image, image, generator=g)
+    x = img.unsqueeze(0).expand(T, batch, 3, image, image)
+    fwd = {"spikformer_8_384": oracle.spikformer_forward,
+           "vgg11_bn": oracle.vgg_forward}.get(workload, oracle.sew_resnet_forward)
+    with torch.no_grad():
+        med, times = _median_forwards(lambda: fwd(m, x, conv_dtype=torch.float32), reps,
+                                      budget_s)
+        xc = x.contiguous()
 
+        def eager():
+            snn.functional.reset_net(m)
+            m(xc)
+        emed, etimes = _median_forwards(eager, reps, budget_s)
+    sample = (f"batch {batch} of 3x{image}x{image} at T={T}: median of {{n}} forwards "
+              f"({{lo:.2f}}-{{hi:.2f}} s each) after 1 warm-up forward")
+    return {"value": round(batch / med, 3), "unit": "images/s", "cores": threads,
+            "kind": "port", "cpu": cpu_model_name(),
+            "sample": f"oracle {fwd.__name__} (fp32 torch CPU conv + eval BN + C LIF), "
+                      + sample.format(n=len(times), lo=min(times), hi=max(times)),
+            "eager_sj_equivalent": {
+                "value": round(batch / emed, 3), "unit": "images/s", "cores": threads,
+                "sample": "eager catfuse_amd.snn model (SpikingJelly-equivalent torch multi-step "
+                          "path, fp32), " + sample.format(n=len(etimes), lo=min(etimes),
+                                                          hi=max(etimes))}}
+
+
+# ---------------------------------------------------------------------------
+# workloads
+# ---------------------------------------------------------------------------
+
+def run_network(workload, args, dev, v_threshold=1.0, label=True):
+    """Optimize the workload's model, time it; returns (res, stats, model,
+    fused, x)."""
+    import torch
+    import catfuse_amd
+    T, B, HW = args.T, args.batch, args.image
+    model = build_model(workload, v_threshold=v_threshold)
+    fused, stats = catfuse_amd.optimize(model, device=dev, T=T)
+    fused.eval()
+    g = torch.Generator(device=dev).manual_seed(0)
+    img = torch.randn(B, 3, HW, HW, device=dev, generator=g)
+    x = img.unsqueeze(0).expand(T, B, 3, HW, HW)      # direct encoding, resident in HBM
+    res = time_forward(fused, x, img, args.steps, args.warmup, args.eager, label)
+    return res, stats, model, fused, x
+
+
+def sew_result(args, dev):
+    res, stats, model, fused, x = run_network("sew_resnet18", args, dev)
+    kern = res["timer"].summary()
+    roof = conv_roofline(kern, args.steps, traffic=traffic_from_profiles())
+    sz = staticzero_summary(kern, args.steps)
+    sz["conv_route_sequence"] = route_sequence(res["timer"], "conv_mfma", args.steps)
+    result = _base_result(args, res, stats, "sew_resnet18_adds_T4_B32_224")
+    result.update(roofline=roof, staticzero_convs=sz, per_layer=per_layer_table(res),
+                  kernels=_per_kernel(kern, args.steps))
+    if not args.no_live:
+        result["live"] = live_result(args, dev)
+    return result, model
+
+
+def live_result(args, dev):
+    """The headline network with v_th = 0.1 (every layer active): the dense
+    MFMA route at every layer's shape."""
+    res, stats, model, fused, x = run_network("sew_resnet18", args, dev,
+                                              v_threshold=LIVE_V_THRESHOLD)
+    frac, rates = liveness(fused, x)
+    kern = res["timer"].summary()
+    roof = conv_roofline(kern, args.steps)
+    rows = per_layer_table(res)
+    mfma3 = [r for r in rows if r["kernel"] == "conv_mfma" and r["route"] == "D"]
+    return {"v_threshold": LIVE_V_THRESHOLD,
+            "liveness": {"alive_fraction": round(frac, 4), "required": LIVE_MIN_FRACTION,
+                         "ok": frac >= LIVE_MIN_FRACTION, "block_spike_rates": rates},
+            "images_per_s": round(args.batch / (res["ms"] * 1e-3), 2),
+            "ms_per_step": round(res["ms"], 4), "mode": res["mode"],
+            "eager_ms_per_step": round(res["ms_eager"], 4),
+            "roofline": roof,
+            "conv_route_sequence": route_sequence(res["timer"], "conv_mfma", args.steps),
+            "min_conv_frac": min((r["frac"] for r in mfma3), default=None),
+            "per_layer": rows, "kernels": _per_kernel(kern, args.steps)}
+
+
+def spikformer_result(args, dev):
+    res, stats, model, fused, x = run_network("spikformer_8_384", args, dev)
+    timer, steps = res["timer"], args.steps
+    kern = timer.summary()
+    roof = conv_roofline(kern, steps,
+                         traffic=traffic_from_profiles("conv_halo_spikformer_8_384_traffic.json"))
+    roof["kernel"] = ("conv_halo_kernel 3x3 (cf_conv_mfma: the SPS Conv-BN-LIF stages), "
+                      "launches that run the MFMA K loop")
+    roof["conv_route_sequence"] = route_sequence(timer, "conv_mfma", steps)
+    l_ms, l_fl, _, l_n = _agg(kern, ["linear_tokens"])
+    lz_ms, _, _, lz_n = _agg(kern, ["linear_tokens_staticzero"])
+    a_ms, a_fl, a_b, a_n = _agg(kern, ["spike_attention"])
+    ach = l_fl / (l_ms * 1e-3) / 1e12 if l_ms else 0.0
+    a_gbps = a_b / (a_ms * 1e-3) / 1e9 if a_ms else 0.0
+    result = _base_result(args, res, stats, "spikformer_8_384_T4_B32_224")
+    result["metric"] = "Spikformer-8-384 T=4 images/s on 1 MI355X (config C4)"
+    result["config"].update(tokens=196, dim=384, heads=12, blocks=8)
+    result["dtype"] = ("fp32 (linears/convs: fp16 hi/lo split weights x fp16-exact spikes on "
+                       "MFMA, fp32 acc; attention: exact integer Q(K^T V), one fp32 rounding)")
+    result.update(roofline=roof, staticzero_convs=staticzero_summary(kern, steps),
+                  per_layer=per_layer_table(res), kernels=_per_kernel(kern, steps))
+    result["token_linears"] = {
+        "kernel": "conv_halo_kernel 1x1 (cf_conv_mfma: fused Linear-BN1d-LIF over the token rows)",
+        "launches_per_step": (l_n + lz_n) // steps,
+        "mfma_route": {"launches_per_step": l_n // steps,
+                       "us_per_launch_avg": round(l_ms * 1e3 / max(1, l_n), 2),
+                       "achieved": round(ach, 2), "unit": "TFLOP/s"},
+        "staticzero_route": {"launches_per_step": lz_n // steps,
+                             "us_per_launch_avg": round(lz_ms * 1e3 / max(1, lz_n), 2)},
+        "linear_route_sequence": route_sequence(timer, "linear_tokens", steps)}
+    result["attention"] = {"kernel": "spike_attention_kernel (cf_spike_attention_lif)",
+                           "launches_per_step": a_n // steps,
+                           "us_per_launch_avg": round(a_ms * 1e3 / max(1, a_n), 2),
+                           "achieved": round(a_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
+                           "frac": round(a_gbps / PEAK_HBM_GBPS, 4)}
+    return result, model
+
+
+def vgg_result(args, dev):
+    """Config C2 (reference: benchmarks/bench_vgg11_e2e.py:54-72,277-290):
+    the convs, the in-network AvgPool->LIF tails and the Linear->LIF head."""
+    res, stats, model, fused, x = run_network("vgg11_bn", args, dev)
+    timer, steps = res["timer"], args.steps
+    kern = timer.summary()
+    result = _base_result(args, res, stats, "spiking_vgg11_bn_T4_B64_32")
+    result["metric"] = "Spiking VGG-11-BN T=4 images/s on 1 MI355X (config C2)"
+    roof = conv_roofline(kern, steps)
+    pool_ms, _, pool_b, pool_n = _agg(kern, ["avgpool2x2_lif"])
+    result.update(roofline=roof, per_layer=per_layer_table(res),
+                  kernels=_per_kernel(kern, steps))
+    gb = pool_b / (pool_ms * 1e-3) / 1e9 if pool_ms else 0.0
+    result["avgpool_lif_tails"] = {"kernel": "avgpool2_lif_kernel (cf_avgpool2x2_lif)",
+                                   "launches_per_step": pool_n // steps,
+                                   "us_per_launch_avg": round(pool_ms * 1e3 / max(1, pool_n), 2),
+                                   "achieved": round(gb, 1), "peak": PEAK_HBM_GBPS,
+                                   "unit": "GB/s", "frac": round(gb / PEAK_HBM_GBPS, 4)}
+    return result, model
+
+
+def _per_kernel(kern, steps):
+    return {k: {"launches_per_step": v["launches"] // steps,
+                "ms_per_step": round(v["ms_total"] / steps, 4)} for k, v in kern.items()}
+
+
+def _base_result(args, res, stats, workload):
+    ips = args.batch / (res["ms"] * 1e-3)
+    return {
+        "metric": METRIC, "value": round(ips, 2), "unit": "images/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(res["ms"], 4),
+        "mode": res["mode"], "eager_ms_per_step": round(res["ms_eager"], 4),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32 (conv: fp16 hi/lo split weights x fp16-exact spikes on MFMA, fp32 acc)",
+        "data": "synthetic (seeded N(0,1) images, random kaiming weights, config BN stats)",
+        "config": {"workload": workload, "T": args.T, "batch": args.batch,
+                   "image": [3, args.image, args.image],
+                   "encoding": "direct (input repeated over T)",
+                   "fused_lif_nodes": stats["fused_lif_nodes"],
+                   "total_lif_nodes": stats["total_lif_nodes"]},
+    }
+
+
+# ---------------------------------------------------------------------------
+# SparseFlow / dense crossover (the MI355X routing threshold)
+# ---------------------------------------------------------------------------
+
+XO_RATES = (0.0, 0.001, 0.01, 0.05, 0.1, 0.2, 0.3, 0.5)
+XO_PATTERNS = ("iid", "block", "spatial")
+XO_ROUTES = ("SparseFlow", "StreamFuse", "DenseKeep", "auto")
+
+
+def xo_input(rate, pattern, shape=(4, 32, 256, 14, 14), seed=0, block=8, p_zero_block=0.7):
+    """fp32 CPU spikes [T, B, C, H, W] of one rate and spatial pattern:
+    iid Bernoulli(rate); block: per (t, b, c) and 8x8 block, zero with
+    probability 0.7, else Bernoulli(rate) (the granularity of the
+    reference's tests/test_70_oracle_gap.py:112-124); spatial: per (t, b)
+    and 8x8 block, zero in every channel with probability 0.7."""
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    T, B, C, H, W = shape
+    x = (torch.rand(shape, generator=g) < rate).float()
+    if pattern in ("block", "spatial"):
+        gh, gw = -(-H // block), -(-W // block)
+        kc = C if pattern == "block" else 1
+        keep = (torch.rand((T, B, kc, gh, gw), generator=g) >= p_zero_block).float()
+        keep = keep.repeat_interleave(block, 3).repeat_interleave(block, 4)[..., :H, :W]
+        x = x * keep
+    elif pattern != "iid":
+        raise ValueError(f"unknown pattern {pattern!r}")
+    return x
+
+
+def xo_as_fused_output(x):
+    """x (GPU fp32 spikes) as a fused conv's output: an NHWC-backed tensor
+    with the fp16 copy and a count block holding count_nonzero(x)."""
+    import torch
+    from catfuse_amd import runtime
+    T, B, C, H, W = x.shape
+    cp = runtime.pad32(C)
+    nhwc = torch.zeros((T * B, H, W, cp), dtype=torch.float16, device=x.device)
+    nhwc[..., :C] = x.reshape(T * B, C, H, W).permute(0, 2, 3, 1).half()
+    y = runtime.lazy_output(tuple(x.shape), nhwc, x.device)
+    blk = runtime.count_block(x.device)
+    blk[1] = int(torch.count_nonzero(x))
+    runtime.attach_count(y, blk, [0])
+    return y
+
+
+def _xo_layer(C_in, C_out, device, seed=0):
+    import torch
+    from catfuse_amd.implementations.base import ConvLIFParams, ConvLIFSpec
+    g = torch.Generator().manual_seed(seed)
+    w = torch.randn(C_out, C_in, 3, 3, generator=g) * (2.0 / (C_in * 9)) ** 0.5
+    mean = torch.randn(C_out, generator=g) * 0.1
+    var = torch.rand(C_out, generator=g) + 0.5
+    gamma = torch.rand(C_out, generator=g) * 0.4 + 0.8
+    beta = torch.randn(C_out, generator=g) * 0.1
+    scale = gamma / torch.sqrt(var + 1e-5)
+    shift = beta - mean * scale
+    spec = ConvLIFSpec(C_in, C_out, 3, 1, 1, has_conv_bias=False, has_bn=True, tau=2.0,
+                       v_threshold=1.0, v_reset=0.0, decay_input=True)
+    return spec, ConvLIFParams(w.to(device), None, scale.to(device), shift.to(device))
+
+
+def _xo_time_graph(fn, calls, reps, device):
+    """Median microseconds per call over `reps` replays of a graph of
+    `calls` calls."""
+    import torch
+    side = torch.cuda.Stream(device=device)
+    side.wait_stream(torch.cuda.current_stream(device))
+    with torch.cuda.stream(side):
+        fn()
+        fn()
+    torch.cuda.current_stream(device).wait_stream(side)
+    torch.cuda.synchronize(device)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for _ in range(calls):
+            fn()
+    graph.replay()
+    torch.cuda.synchronize(device)
+    times = []
+    for _ in range(reps):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        graph.replay()
+        e1.record()
+        torch.cuda.synchronize(device)
+        times.append(e0.elapsed_time(e1) * 1e3 / calls)
+    del graph
+    return statistics.median(times)
+
+
+def xo_sweep(device, rates=XO_RATES, patterns=XO_PATTERNS, shape=(4, 32, 256, 14, 14),
+             plain=False, calls=20, reps=5, seed=0):
+    """One row per (pattern, rate): the input density and the microseconds
+    per call of every route (each checked bitwise against the others)."""
+    import torch
+    from catfuse_amd.implementations.dense_keep import DenseKeep
+    from catfuse_amd.implementations.sparse_flow import SparseFlow
+    from catfuse_amd.implementations.stream_fuse import StreamFuse
+    from catfuse_amd.state import StateBuffer
+    T, B, C, H, W = shape
+    spec, params = _xo_layer(C, C, device, seed)
+    impls = {"SparseFlow": SparseFlow(sparsity_threshold=-1.0), "StreamFuse": StreamFuse(),
+             "DenseKeep": DenseKeep(), "auto": SparseFlow()}
+    rows = []
+    with torch.no_grad():
+        for pattern in patterns:
+            for rate in rates:
+                xc = xo_input(rate, pattern, shape, seed=seed + 1)
+                xd = xc.to(device)
+                x = xd if plain else xo_as_fused_output(xd)
+                row = {"pattern": pattern, "rate": rate,
+                       "density": float(torch.count_nonzero(xc)) / xc.numel()}
+                ref = None
+                for name in XO_ROUTES:
+                    impl = impls[name]
+
+                    def call(impl=impl):
+                        return impl.forward(x, spec, params, StateBuffer())
+                    y = call()
+                    if ref is None:
+                        ref = y.clone()
+                    elif not torch.equal(y, ref):
+                        raise RuntimeError(f"{name} differs from SparseFlow at {pattern} {rate}")
+                    row[name] = _xo_time_graph(call, calls, reps, device)
+                rows.append(row)
+                print(json.dumps(row), file=sys.stderr, flush=True)
+    return rows
+
+
+def xo_crossover(rows):
+    """Per pattern, the lowest input sparsity at which forced SparseFlow is
+    faster than the best dense route (None: at no measured nonzero rate)."""
+    out = {}
+    for pattern in sorted({r["pattern"] for r in rows}):
+        wins = [1.0 - r["density"] for r in rows
+                if r["pattern"] == pattern and r["density"] > 0.0
+                and r["SparseFlow"] < min(r["StreamFuse"], r["DenseKeep"])]
+        out[pattern] = min(wins) if wins else None
+    return out
+
+
+def xo_table(rows):
+    lines = ["| pattern | rate | density | " + " | ".join(f"{n} (us)" for n in XO_ROUTES) + " |",
+             "|---|---|---|" + "---|" * len(XO_ROUTES)]
+    for r in rows:
+        lines.append(f"| {r['pattern']} | {r['rate']:g} | {r['density']:.4f} | "
+                     + " | ".join(f"{r[n]:.1f}" for n in XO_ROUTES) + " |")
+    return "\n".join(lines)
+
+
+def sf_crossover_main(args):
+    import torch
+    dev = torch.device("cuda", 0)
+    shape = tuple(args.xo_shape)
+    rows = xo_sweep(dev, shape=shape, plain=args.xo_plain)
+    print(xo_table(rows))
+    print("crossover (lowest input sparsity where SparseFlow wins):", xo_crossover(rows))
+
+
+# ---------------------------------------------------------------------------
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--batch", type=int, default=32)
-    ap.add_argument("--image", type=int, default=224)
-    ap.add_argument("--T", type=int, default=4)
+    ap.add_argument("--batch", type=int, default=None)
+    ap.add_argument("--image", type=int, default=None)
+    ap.add_argument("--T", type=int, default=None)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-tails", action="store_true")
-    ap.add_argument("--cpu-budget", type=float, default=12.0)
+    ap.add_argument("--no-live", action="store_true")
+    ap.add_argument("--cpu-batch", type=int, default=None,
+                    help="images per CPU-baseline forward (default: CPU_BATCH[workload])")
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of the captured HIP graph")
     ap.add_argument("--workload", default="sew_resnet18",
-                    choices=["sew_resnet18", "spikformer_8_384"],
-                    help="sew_resnet18: the headline metric (config C3); spikformer_8_384: "
-                         "config C4 (spiking transformer), its own metric line")
+                    choices=list(WORKLOADS) + ["sf_crossover"])
+    ap.add_argument("--xo-shape", type=int, nargs=5, default=[4, 32, 256, 14, 14])
+    ap.add_argument("--xo-plain", action="store_true",
+                    help="crossover inputs as fp32 tensors (the layer packs them)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: every GPU box in this setup has a single "
               "MI355X; run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "sf_crossover":
+        sf_crossover_main(args)
+        return
+    for k, v in WORKLOADS[args.workload].items():
+        if getattr(args, k) is None:
+            setattr(args, k, v)
 
     import torch
-    import catfuse_amd
-    from catfuse_amd import graph as cf_graph
-    from catfuse_amd import runtime, snn
-
     dev = torch.device("cuda", 0)
-    T, B, HW = args.T, args.batch, args.image
-    spikformer = args.workload == "spikformer_8_384"
-    model = build_model(workload=args.workload)
-    fused, stats = catfuse_amd.optimize(model, device=dev, T=T)
-    fused.eval()
-    g = torch.Generator(device=dev).manual_seed(0)
-    img = torch.randn(B, 3, HW, HW, device=dev, generator=g)
-    x = img.unsqueeze(0).expand(T, B, 3, HW, HW)      # direct encoding, resident in HBM
-
-    with torch.no_grad():
-        for _ in range(args.warmup):
-            snn.functional.reset_net(fused)
-            fused(x)
-        torch.cuda.synchronize()
-        catfuse_amd.check_status(dev)
-
-        # Eager pass with HIP events around every launch (per-kernel times
-        # for the roofline; the same kernels the graph replays).
-        timer = runtime.KernelTimer()
-        runtime.set_timer(timer)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(args.steps):
-            snn.functional.reset_net(fused)
-            y = fused(x)
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        runtime.set_timer(None)
-        ms_eager = (t1 - t0) * 1e3 / args.steps
-        ms = ms_eager
-        mode = "eager"
-        if not args.eager:
-            # One step = copy the batch into the captured input + replay of
-            # reset_net + the whole fused forward (HIP graph).
-            graphed = cf_graph.capture(fused, x)
-            y_ref = y.clone()
-            for _ in range(args.warmup):
-                graphed(img)
-            torch.cuda.synchronize()
-            if not torch.equal(graphed(img), y_ref):
-                print("graph replay differs from the eager forward", file=sys.stderr)
-                sys.exit(1)
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            for _ in range(args.steps):
-                y = graphed(img)
-            torch.cuda.synchronize()
-            t1 = time.perf_counter()
-            ms = (t1 - t0) * 1e3 / args.steps
-            mode = "hip_graph"
-        catfuse_amd.check_status(dev)
-    kern = timer.summary()
-    ips = B / (ms * 1e-3)
-
-    def agg(names):
-        ds = [kern.get(n, {}) for n in names]
-        return (sum(d.get("ms_total", 0.0) for d in ds), sum(d.get("flops", 0) for d in ds),
-                sum(d.get("bytes", 0) for d in ds), sum(d.get("launches", 0) for d in ds))
-
-    tot_ms, tot_fl, _, launches = agg(["conv_mfma", "conv_mfma_sparse"])
-    z_ms, _, z_bytes, z_launches = agg(["conv_mfma_staticzero", "conv_mfma_sparse_staticzero"])
-    achieved = tot_fl / (tot_ms * 1e-3) / 1e12 if tot_ms else 0.0
-    roofline = {"kernel": "conv_halo_kernel (cf_conv_mfma fused Conv-BN-LIF), launches that run "
-                          "the MFMA K loop",
-                "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
-                "traffic": traffic_from_profiles(),
-                "flops_per_launch_avg": tot_fl // max(1, launches),
-                "us_per_launch_avg": round(tot_ms * 1e3 / max(1, launches), 2),
-                "launches_per_step": launches // args.steps}
-    z_gbps = z_bytes / (z_ms * 1e-3) / 1e9 if z_ms else 0.0
-    # route of each conv launch of one forward, in launch order (D: MFMA K
-    # loop, Z: StaticZero), decided on the device and read back here
-    conv_recs = [r for r in timer.records if r[0].startswith("conv_mfma")]
-    per_fwd = len(conv_recs) // max(1, args.steps)
-    route_seq = "".join("Z" if (r[5] is not None and r[5].is_zero()) else "D"
-                        for r in conv_recs[:per_fwd])
-    staticzero = {"kernel": "conv_halo_kernel on the StaticZero route (all-zero input: BN bias "
-                            "-> LIF, no K loop)",
-                  "bound": "hbm", "launches_per_step": z_launches // args.steps,
-                  "us_per_launch_avg": round(z_ms * 1e3 / max(1, z_launches), 2),
-                  "bytes_per_launch_avg": z_bytes // max(1, z_launches),
-                  "achieved": round(z_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                  "frac": round(z_gbps / PEAK_HBM_GBPS, 4),
-                  "conv_route_sequence": route_seq}
-    per_kernel = {k: {"launches_per_step": v["launches"] // args.steps,
-                      "ms_per_step": round(v["ms_total"] / args.steps, 4)}
-                  for k, v in kern.items()}
-
-    if spikformer:
-        # token linears (1x1 convs over the token rows) and the attention core
-        l_ms, l_fl, _, l_n = agg(["linear_tokens"])
-        lz_ms, _, _, lz_n = agg(["linear_tokens_staticzero"])
-        # route of each token-linear launch of one forward (D: MFMA K loop,
-        # Z: StaticZero), decided on the device and read back here
-        lin_recs = [r for r in timer.records if r[0].startswith("linear_tokens")]
-        per_fwd_l = len(lin_recs) // max(1, args.steps)
-        lin_seq = "".join("Z" if (r[5] is not None and r[5].is_zero()) else "D"
-                          for r in lin_recs[:per_fwd_l])
-        a_ms, a_fl, a_b, a_n = agg(["spike_attention"])
-        # the dominant MFMA work is the patch splitter's 3x3 convs (the token
-        # linears take StaticZero when their input is all zero)
-        roofline["kernel"] = ("conv_halo_kernel 3x3 (cf_conv_mfma: the SPS Conv-BN-LIF stages), "
-                              "launches that run the MFMA K loop")
-        roofline["traffic"] = traffic_from_profiles("conv_halo_spikformer_8_384_traffic.json")
-        roofline["conv_route_sequence"] = route_seq
-        ach = l_fl / (l_ms * 1e-3) / 1e12 if l_ms else 0.0
-        linears = {"kernel": "conv_halo_kernel 1x1 (cf_conv_mfma: fused Linear-BN1d-LIF over the "
-                             "token rows)",
-                   "launches_per_step": (l_n + lz_n) // args.steps,
-                   "mfma_route": {"launches_per_step": l_n // args.steps,
-                                  "us_per_launch_avg": round(l_ms * 1e3 / max(1, l_n), 2),
-                                  "achieved": round(ach, 2), "unit": "TFLOP/s"},
-                   "staticzero_route": {"launches_per_step": lz_n // args.steps,
-                                        "us_per_launch_avg": round(lz_ms * 1e3 / max(1, lz_n), 2)},
-                   "linear_route_sequence": lin_seq}
-        a_gbps = a_b / (a_ms * 1e-3) / 1e9 if a_ms else 0.0
-        attention = {"kernel": "spike_attention_kernel (cf_spike_attention_lif)",
-                     "launches_per_step": a_n // args.steps,
-                     "us_per_launch_avg": round(a_ms * 1e3 / max(1, a_n), 2),
-                     "achieved": round(a_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                     "frac": round(a_gbps / PEAK_HBM_GBPS, 4)}
-    result = {
-        "metric": METRIC, "value": round(ips, 2), "unit": "images/s", "n_gpus": 1,
-        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
-        "mode": mode, "eager_ms_per_step": round(ms_eager, 4),
-        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "fp32 (conv: fp16 hi/lo split weights x fp16-exact spikes on MFMA, fp32 acc)",
-        "data": "synthetic (seeded N(0,1) images, random kaiming weights, config BN stats)",
-        "config": {"workload": "sew_resnet18_adds_T4_B32_224", "T": T, "batch": B,
-                   "image": [3, HW, HW], "encoding": "direct (input repeated over T)",
-                   "fused_lif_nodes": stats["fused_lif_nodes"],
-                   "total_lif_nodes": stats["total_lif_nodes"]},
-        "roofline": roofline,
-        "staticzero_convs": staticzero,
-        "kernels": per_kernel,
-    }
-    if spikformer:
-        result["metric"] = "Spikformer-8-384 T=4 images/s on 1 MI355X (config C4)"
-        result["config"] = {"workload": "spikformer_8_384_T4_B32_224", "T": T, "batch": B,
-                            "image": [3, HW, HW], "tokens": 196, "dim": 384, "heads": 12,
-                            "blocks": 8, "encoding": "direct (input repeated over T)",
-                            "fused_lif_nodes": stats["fused_lif_nodes"],
-                            "total_lif_nodes": stats["total_lif_nodes"]}
-        result["dtype"] = ("fp32 (linears/convs: fp16 hi/lo split weights x fp16-exact spikes on "
-                           "MFMA, fp32 acc; attention: exact integer Q(K^T V), one fp32 rounding)")
-        result["token_linears"] = linears
-        result["attention"] = attention
-    if not args.no_tails and not spikformer:
+    if args.workload == "spikformer_8_384":
+        result, model = spikformer_result(args, dev)
+    elif args.workload == "vgg11_bn":
+        result, model = vgg_result(args, dev)
+    else:
+        result, model = sew_result(args, dev)
+    if not args.no_tails and args.workload == "sew_resnet18":
         result["lif_tails"] = measure_tails(dev)
     if not args.no_cpu_baseline:
-        import oracle
-        result["cpu_baseline"] = cpu_baseline(
-            model, T, HW, args.cpu_budget,
-            forward=oracle.spikformer_forward if spikformer else None)
+        result["cpu_baseline"] = cpu_baseline(model, args.workload, args.T,
+                                              args.cpu_batch or CPU_BATCH[args.workload],
+                                              args.image)
     print(json.dumps(result), flush=True)
 
 

@@ -289,7 +289,7 @@ __global__ __launch_bounds__(256) void maxpool_nhwc_kernel(
     }
     const uint4 w = __builtin_bit_cast(uint4, m);
     anyw |= (w.x | w.y | w.z | w.w) & 0x7fff7fffu;
-    *reinterpret_cast<h8*>(out + pix * cp + c8 * 8) = m;
+    *reinterpret_cast<h8*>(out + (size_t)pix * cp + c8 * 8) = m;
   }
   if (nnz) {
     const bool any = cf_wg_any(anyw != 0u, any_sh);

@@ -26,6 +26,7 @@ from typing import Optional
 import torch
 
 from . import snn
+from .runtime import NHWCSpikes
 
 
 def _base_of(x: torch.Tensor) -> torch.Tensor:
@@ -33,6 +34,19 @@ def _base_of(x: torch.Tensor) -> torch.Tensor:
     if x.dim() >= 1 and x.shape[0] > 1 and x.stride(0) == 0:
         return x[0]
     return x
+
+
+def _materialize_all(out) -> None:
+    """cf_materialize() every NHWC-backed tensor in a (nested) output."""
+    stack = [out]
+    while stack:
+        a = stack.pop()
+        if isinstance(a, NHWCSpikes):
+            a.cf_materialize()
+        elif isinstance(a, (list, tuple)):
+            stack.extend(a)
+        elif isinstance(a, dict):
+            stack.extend(a.values())
 
 
 class GraphedForward:
@@ -65,6 +79,11 @@ class GraphedForward:
             torch.cuda.synchronize(example.device)
             with torch.cuda.graph(self.graph):
                 self.static_out = self._run()
+                # a fused layer's output holds its values in its fp16 copy
+                # until first read; fill the fp32 form inside the graph so
+                # every replay refreshes it (outside, only the first read
+                # after capture would)
+                _materialize_all(self.static_out)
         torch.cuda.synchronize(example.device)
 
     def _run(self):

@@ -44,8 +44,48 @@ def _first(v):
     return v[0] if isinstance(v, (tuple, list)) else v
 
 
+def _pair(v):
+    return tuple(v) if isinstance(v, (tuple, list)) else (v, v)
+
+
+def conv_unsupported_reason(conv) -> Optional[str]:
+    """Why the fused conv kernels cannot compute this nn.Conv2d, or None.
+    They compute a dense (groups = 1), undilated, zero-padded convolution
+    with a square kernel, stride and padding; anything else is left to the
+    original module (the matchers refuse it)."""
+    groups = int(getattr(conv, "groups", 1))
+    if groups != 1:
+        return f"groups={groups}"
+    if isinstance(getattr(conv, "padding", 0), str):
+        return f"padding='{conv.padding}'"
+    if any(int(d) != 1 for d in _pair(getattr(conv, "dilation", 1))):
+        return f"dilation={tuple(_pair(conv.dilation))}"
+    mode = getattr(conv, "padding_mode", "zeros")
+    if mode != "zeros":
+        return f"padding_mode='{mode}'"
+    for name in ("kernel_size", "stride", "padding"):
+        a, b = _pair(getattr(conv, name))
+        if int(a) != int(b):
+            return f"non-square {name}=({a}, {b})"
+    return None
+
+
 def conv_geometry(conv):
+    """(kernel_size, stride, padding) of a conv the fused kernels compute;
+    ValueError for any other (conv_unsupported_reason)."""
+    why = conv_unsupported_reason(conv)
+    if why is not None:
+        raise ValueError(f"the fused conv kernels do not compute a Conv2d with {why}")
     return int(_first(conv.kernel_size)), int(_first(conv.stride)), int(_first(conv.padding))
+
+
+def is_lif_node(m) -> bool:
+    """SpikingJelly's LIFNode or the catfuse_amd.snn stand-in (duck-typed on
+    the class name and the neuron attributes the fused kernels read).  Other
+    neurons (IFNode, ParametricLIFNode, ...) are not LIF and stay unfused."""
+    if type(m).__name__ != "LIFNode":
+        return False
+    return all(hasattr(m, a) for a in ("v_threshold", "v_reset"))
 
 
 def lif_params(lif):
@@ -730,4 +770,5 @@ __all__ = ["CTFPattern", "PartialFusionConvLIF", "PartialFusionConvBNLIF",
            "FusedAddLIF", "FusedAddBNLIF", "FusedAvgPoolLIF", "FusedGlobalAvgPool",
            "CTFSEWBasicBlock",
            "CTFSpikingBasicBlock", "CTFSEWBottleneck", "CTFSpikingBottleneck",
-           "STFusionConvBNLIF", "PATTERN_REGISTRY", "fold_bn", "lif_params", "conv_geometry"]
+           "STFusionConvBNLIF", "PATTERN_REGISTRY", "fold_bn", "lif_params", "conv_geometry",
+           "conv_unsupported_reason", "is_lif_node"]

@@ -20,7 +20,7 @@ import torch.nn as nn
 
 from catfuse_amd.hardware import runtime_profile
 from catfuse_amd.implementations import ConvLIFParams, ConvLIFSpec, DenseKeep, SparseFlow, StreamFuse
-from catfuse_amd.patterns import CTFPattern, _first, lif_params
+from catfuse_amd.patterns import CTFPattern, conv_geometry, lif_params
 from catfuse_amd.runtime import ID_ADD_SPIKE
 from catfuse_amd.state import StateBuffer
 
@@ -148,11 +148,11 @@ class STFusionConvBNLIF(CTFPattern):
     def from_sj_modules(cls, conv: nn.Conv2d, bn: nn.BatchNorm2d, lif, K: int = 4,
                         threshold: float = 1e-6, routing: str = "device",
                         sparsity_threshold: Optional[float] = None):
+        k, s, p = conv_geometry(conv)
         bn.eval()
         scale, offset = _fold_bn_params(bn)
         lp = lif_params(lif)
-        m = cls(conv.in_channels, conv.out_channels, int(_first(conv.kernel_size)),
-                int(_first(conv.stride)), int(_first(conv.padding)), bias=conv.bias is not None,
+        m = cls(conv.in_channels, conv.out_channels, k, s, p, bias=conv.bias is not None,
                 bn_scale=scale, bn_bias=offset, K=K, threshold=threshold, routing=routing,
                 sparsity_threshold=sparsity_threshold, **lp)
         with torch.no_grad():

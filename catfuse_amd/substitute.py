@@ -33,12 +33,26 @@ from catfuse_amd.patterns import (CTFSEWBasicBlock, CTFSEWBottleneck, CTFSpiking
                                   FusedLinearLIF,
                                   PartialFusionConvBNAvgPoolLIF, PartialFusionConvBNLIF,
                                   PartialFusionConvBNLIFMaxPool, PartialFusionConvLIF,
-                                  STFusionConvBNLIF, conv_geometry)
+                                  STFusionConvBNLIF, conv_geometry, conv_unsupported_reason,
+                                  is_lif_node)
 from catfuse_amd.policy import SpatialBackend, get_policy
 
 
 def _is_sj_conv2d(m) -> bool:
-    return isinstance(m, nn.Conv2d)
+    """An nn.Conv2d the fused kernels compute (conv_unsupported_reason:
+    groups, dilation, padding mode and non-square geometry are refused)."""
+    return isinstance(m, nn.Conv2d) and conv_unsupported_reason(m) is None
+
+
+def _record_unsupported_convs(model, stats) -> None:
+    """List every nn.Conv2d left in the rewritten model that the fused
+    kernels cannot compute, with the reason, in stats['unsupported_structures']."""
+    lst = stats.setdefault("unsupported_structures", [])
+    for name, m in model.named_modules():
+        if isinstance(m, nn.Conv2d):
+            why = conv_unsupported_reason(m)
+            if why is not None:
+                lst.append(f"{_strip_root(name)}: Conv2d with {why} (left unfused)")
 
 
 def _is_sj_bn2d(m) -> bool:
@@ -78,25 +92,46 @@ def _is_resnet_stem_owner(m) -> bool:
 
 def _is_lif(m) -> bool:
     """SpikingJelly LIFNode or the catfuse_amd.snn stand-in (duck-typed)."""
-    if type(m).__name__ != "LIFNode":
-        return False
-    return all(hasattr(m, a) for a in ("v_threshold", "v_reset"))
+    return is_lif_node(m)
+
+
+def _block_fusable(m, n_convs: int, sew: bool) -> bool:
+    """Every conv{i} / bn{i} / sn{i} site of a ResNet block (and its
+    downsample) is a conv the fused kernels compute, a BatchNorm2d and an
+    LIF neuron, so the whole block can be replaced."""
+    for i in range(1, n_convs + 1):
+        if not (_is_sj_conv2d(getattr(m, f"conv{i}", None))
+                and _is_sj_bn2d(getattr(m, f"bn{i}", None))
+                and _is_lif(getattr(m, f"sn{i}", None))):
+            return False
+    ds = getattr(m, "downsample", None)
+    if ds is not None:
+        if not (isinstance(ds, nn.Sequential) and len(ds) >= 2 and _is_sj_conv2d(ds[0])
+                and _is_sj_bn2d(ds[1])):
+            return False
+        if sew and not _is_lif(getattr(m, "downsample_sn", None)):
+            return False
+    return True
 
 
 def _is_sew_basic_block(m) -> bool:
-    return type(m).__name__ == "BasicBlock" and getattr(m, "cnf", None) is not None
+    return (type(m).__name__ == "BasicBlock" and getattr(m, "cnf", None) is not None
+            and _block_fusable(m, 2, True))
 
 
 def _is_standard_spiking_basic_block(m) -> bool:
-    return type(m).__name__ == "BasicBlock" and not hasattr(m, "cnf")
+    return (type(m).__name__ == "BasicBlock" and not hasattr(m, "cnf")
+            and _block_fusable(m, 2, False))
 
 
 def _is_sew_bottleneck(m) -> bool:
-    return type(m).__name__ == "Bottleneck" and getattr(m, "cnf", None) is not None
+    return (type(m).__name__ == "Bottleneck" and getattr(m, "cnf", None) is not None
+            and _block_fusable(m, 3, True))
 
 
 def _is_standard_spiking_bottleneck(m) -> bool:
-    return type(m).__name__ == "Bottleneck" and not hasattr(m, "cnf")
+    return (type(m).__name__ == "Bottleneck" and not hasattr(m, "cnf")
+            and _block_fusable(m, 3, False))
 
 
 def _count_lif(model):
@@ -200,6 +235,7 @@ def substitute(sj_model: nn.Module, verbose: bool = False):
                     walk(child, raw)
 
     walk(model)
+    _record_unsupported_convs(model, stats)
     stats["coverage_pct"] = (100.0 * stats["fused_lif_nodes"] / stats["total_lif_nodes"]
                              if stats["total_lif_nodes"] else 0.0)
     return holder.root, stats
@@ -471,6 +507,7 @@ def substitute_sf(sj_model, T=16, verbose=False, force_sparse=False, fuse_sew_ad
                     setattr(pmod, name, FusedGlobalAvgPool.from_sj_modules(ch))
                     _bump(stats, "FusedGlobalAvgPool")
 
+    _record_unsupported_convs(model, stats)
     stats["coverage_pct"] = 100.0 * stats["fused_lif_nodes"] / max(stats["total_lif_nodes"], 1)
     return holder.root, stats
 
@@ -491,7 +528,7 @@ def _wrap_sew_blocks(model):
     CTFSEWBasicBlock (ADD in conv2's epilogue)."""
     for pname, pmod in list(model.named_modules()):
         for name, child in list(pmod.named_children()):
-            if not _is_sew_basic_block(child):
+            if not (type(child).__name__ == "BasicBlock" and getattr(child, "cnf", None)):
                 continue
             if not (_fused_conv(child.conv1) and _fused_conv(child.conv2)):
                 continue

@@ -21,8 +21,10 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
-from catfuse_amd.patterns import (CTFPattern, PartialFusionConvBNLIF, fold_bn, lif_params)
-from catfuse_amd.runtime import (ConvLIFRunner, count_block, count_of, lazy_tokens, maxpool_nhwc,
+from catfuse_amd.patterns import (CTFPattern, PartialFusionConvBNLIF, conv_unsupported_reason,
+                                  fold_bn, is_lif_node, lif_params)
+from catfuse_amd.runtime import (ConvLIFRunner, count_block, count_of, lazy_tokens, lif_multistep,
+                                 maxpool_nhwc,
                                  pad32, shadow_of, spike_attention_lif, token_membrane,
                                  token_shadow, token_view)
 from catfuse_amd.state import StateBuffer
@@ -147,14 +149,26 @@ class FusedLinearBNLIF(CTFPattern):
 class CTFSpikformerSSA(CTFPattern):
     """Spiking self-attention: fused QKV Linear-BN1d-LIF (one launch), the
     attention core with attn_lif (one launch), fused proj Linear-BN1d-LIF
-    (+ the block's residual)."""
+    (+ the block's residual).
+
+    The core kernel (cf_spike_attention_lif) covers a head dim of 32 and up
+    to ATTN_MAX_TOKENS tokens per image.  Other shapes (e.g. head dim 64, or
+    a 56 x 56 token grid) evaluate the same product, Q (K^T V), as two
+    library GEMMs in float64 on the GPU (exact: the operands are spikes and
+    every partial sum an integer), round once by the scale in fp32 and run
+    the LIF in cf_lif_multistep: the same values the kernel produces.  Such
+    calls are counted in `gemm_core_calls`."""
+
+    ATTN_HEAD_DIM = 32
+    ATTN_MAX_TOKENS = 256
 
     def __init__(self, dim, num_heads, scale, qkv: FusedLinearBNLIF, proj: FusedLinearBNLIF,
                  attn_lif_params: dict):
         super().__init__()
-        if dim != 32 * num_heads:
-            raise ValueError("the fused attention needs a head dim of 32")
+        if dim % num_heads:
+            raise ValueError("dim must be a multiple of num_heads")
         self.dim, self.num_heads, self.scale = int(dim), int(num_heads), float(scale)
+        self.head_dim = self.dim // self.num_heads
         self.qkv = qkv
         self.proj = proj
         self.attn_lif = dict(attn_lif_params)
@@ -162,20 +176,44 @@ class CTFSpikformerSSA(CTFPattern):
         self._register_state(self.attn_state)
         self._attn_gen = [0]        # calls that published the core's count block
         self._attn_blocks = {}
+        self.gemm_core_calls = 0
+
+    def kernel_covers(self, N: int) -> bool:
+        return self.head_dim == self.ATTN_HEAD_DIM and N <= self.ATTN_MAX_TOKENS
 
     def forward(self, x, residual=None):
         T, B, N, C = x.shape
         qkv = self.qkv(x)
-        copy = token_shadow(qkv, pad32(3 * C))
         lp = self.attn_lif
         v_in = self.attn_state.peek((B, N, C), x.device)
-        a, v = spike_attention_lif(copy, T, B, N, self.num_heads, (0, C, 2 * C), self.scale,
-                                   tau=lp["tau"], v_threshold=lp["v_threshold"],
-                                   v_reset=lp["v_reset"], decay_input=lp["decay_input"],
-                                   v_in=v_in, nz_out=self._attn_block(x.device),
-                                   gen_cell=self._attn_gen)
+        copy = token_shadow(qkv, pad32(3 * C)) if self.kernel_covers(N) else None
+        if copy is not None:
+            a, v = spike_attention_lif(copy, T, B, N, self.num_heads, (0, C, 2 * C), self.scale,
+                                       tau=lp["tau"], v_threshold=lp["v_threshold"],
+                                       v_reset=lp["v_reset"], decay_input=lp["decay_input"],
+                                       v_in=v_in, nz_out=self._attn_block(x.device),
+                                       gen_cell=self._attn_gen)
+        else:
+            a, v = self._gemm_core(qkv, v_in)
         self.attn_state.set(v)
         return self.proj(a, identity=residual)
+
+    def _gemm_core(self, qkv, v_in):
+        """LIF_T(Q (K^T V) * scale) for shapes the core kernel does not cover:
+        float64 GEMMs of the spike operands (exact integers), one fp32
+        rounding by the scale, cf_lif_multistep over T."""
+        T, B, N, C3 = qkv.shape
+        C, H, dh = C3 // 3, self.num_heads, self.head_dim
+        with torch.no_grad():
+            t = qkv.reshape(T, B, N, 3, H, dh).permute(3, 0, 1, 4, 2, 5).double()
+            q, k, v = t[0], t[1], t[2]                       # [T, B, H, N, dh]
+            kv = torch.matmul(k.transpose(-1, -2).contiguous(), v.contiguous())
+            y = torch.matmul(q.contiguous(), kv)             # integers, exact
+            z = y.permute(0, 1, 3, 2, 4).reshape(T, B, N, C).float() * self.scale
+        lp = self.attn_lif
+        self.gemm_core_calls += 1
+        return lif_multistep(z.contiguous(), v_in, tau=lp["tau"], v_threshold=lp["v_threshold"],
+                             v_reset=lp["v_reset"], decay_input=lp["decay_input"])
 
     def _attn_block(self, device):
         blk = self._attn_blocks.get(device)
@@ -258,10 +296,9 @@ class CTFSpikformerSPS(CTFPattern):
                 continue
             y = stage(y)
             if pooled:
-                k, st, pd = (int(v if isinstance(v, int) else v[0])
-                             for v in (pool.kernel_size, pool.stride, pool.padding))
+                k, st, pd = self._pool_geometry(pool)
                 yp = None
-                if y.is_cuda and 2 * pd <= k:
+                if y.is_cuda and 2 * pd <= k and self._plain_pool(pool):
                     # pool the fp16 NHWC copy (exact for spikes), keep it as a copy
                     yp = maxpool_nhwc(y, k, st, pd, self._pool_gen[i],
                                       self._pool_block(i, y.device))
@@ -283,13 +320,25 @@ class CTFSpikformerSPS(CTFPattern):
 
     @staticmethod
     def _pool_geometry(pool):
+        st = pool.stride if pool.stride is not None else pool.kernel_size
         return tuple(int(v if isinstance(v, int) else v[0])
-                     for v in (pool.kernel_size, pool.stride, pool.padding))
+                     for v in (pool.kernel_size, st, pool.padding))
+
+    @staticmethod
+    def _plain_pool(pool) -> bool:
+        """Square window, stride and padding, no dilation, floor mode: the
+        geometry the NHWC pool kernels compute; other pools run in torch."""
+        def sq(v):
+            return isinstance(v, int) or (len(v) == 2 and v[0] == v[1])
+        st = pool.stride if pool.stride is not None else pool.kernel_size
+        return (sq(pool.kernel_size) and sq(st) and sq(pool.padding)
+                and getattr(pool, "dilation", 1) in (1, (1, 1))
+                and not getattr(pool, "ceil_mode", False))
 
     def _direct_pool(self, stage, pool, x) -> bool:
         if not (x.is_cuda and x.dim() == 5 and stage._impl.input_is_analog(x)):
             return False
-        if getattr(pool, "dilation", 1) not in (1, (1, 1)) or getattr(pool, "ceil_mode", False):
+        if not self._plain_pool(pool):
             return False
         r = stage._impl.runner(stage.spec, stage._ensure_params(), x.device)
         return r.direct_pool_supported(x, self._pool_geometry(pool))
@@ -316,18 +365,58 @@ class CTFSpikformerSPS(CTFPattern):
         return cls(stages, pools, rpe)
 
 
+def _linear_bn_lif_site(owner, name) -> bool:
+    """owner.<name> is an nn.Linear, owner.<name>_bn a BatchNorm1d over its
+    outputs and owner.<name>_lif an LIF neuron."""
+    lin = getattr(owner, name, None)
+    bn = getattr(owner, name + "_bn", None)
+    return (isinstance(lin, nn.Linear) and isinstance(bn, nn.BatchNorm1d)
+            and bn.num_features == lin.out_features and is_lif_node(getattr(owner, name + "_lif", None)))
+
+
 def is_spikformer_block(m) -> bool:
+    """A Spikformer block (models/spikformer_github.py:162-179) whose every
+    neuron is LIF: attn with q/k/v/proj Linear-BN1d-LIF sites, attn_lif,
+    num_heads and scale; mlp with fc1/fc2 sites.  Blocks with other neurons
+    (IF, PLIF, ...) stay unfused."""
     attn, mlp = getattr(m, "attn", None), getattr(m, "mlp", None)
-    return (attn is not None and mlp is not None
-            and all(hasattr(attn, n) for n in ("q", "q_bn", "q_lif", "k", "v", "attn_lif",
-                                              "proj", "proj_bn", "proj_lif", "num_heads", "scale"))
-            and all(hasattr(mlp, n) for n in ("fc1", "fc1_bn", "fc1_lif", "fc2", "fc2_bn",
-                                             "fc2_lif")))
+    if attn is None or mlp is None:
+        return False
+    if not all(_linear_bn_lif_site(attn, n) for n in ("q", "k", "v", "proj")):
+        return False
+    if not (is_lif_node(getattr(attn, "attn_lif", None)) and hasattr(attn, "num_heads")
+            and hasattr(attn, "scale")):
+        return False
+    d = attn.q.in_features
+    heads = int(attn.num_heads)
+    if heads <= 0 or d % heads or any(getattr(attn, n).in_features != d or
+                                      getattr(attn, n).out_features != d
+                                      for n in ("q", "k", "v", "proj")):
+        return False
+    # Q, K and V share one launch: equal neuron parameters and BN eps
+    lps = [lif_params(getattr(attn, n + "_lif")) for n in ("q", "k", "v")]
+    if any(lp != lps[0] for lp in lps) or \
+            len({getattr(attn, n + "_bn").eps for n in ("q", "k", "v")}) != 1:
+        return False
+    return (_linear_bn_lif_site(mlp, "fc1") and _linear_bn_lif_site(mlp, "fc2")
+            and mlp.fc1.in_features == d and mlp.fc2.out_features == d)
 
 
 def is_spikformer_sps(m) -> bool:
-    return all(hasattr(m, n) for n in ("conv0", "bn0", "lif0", "conv3", "bn3", "lif3",
-                                       "rpe_conv", "rpe_bn", "rpe_lif"))
+    """A spiking patch splitter (models/spikformer_github.py:181-254) with
+    conv{0..3} / bn{0..3} / lif{0..3} and rpe_conv / rpe_bn / rpe_lif sites
+    the fused kernels compute (LIF neurons, supported convs) and pool{i}
+    either absent/None or a MaxPool2d."""
+    names = [f"{i}" for i in range(4)]
+    for conv, bn, lif in [(f"conv{i}", f"bn{i}", f"lif{i}") for i in names] + \
+            [("rpe_conv", "rpe_bn", "rpe_lif")]:
+        c = getattr(m, conv, None)
+        if not (isinstance(c, nn.Conv2d) and conv_unsupported_reason(c) is None
+                and isinstance(getattr(m, bn, None), nn.BatchNorm2d)
+                and is_lif_node(getattr(m, lif, None))):
+            return False
+    return all(getattr(m, f"pool{i}", None) is None or isinstance(getattr(m, f"pool{i}"),
+                                                                 nn.MaxPool2d) for i in names)
 
 
 __all__ = ["FusedLinearBNLIF", "CTFSpikformerSSA", "CTFSpikformerMLP", "CTFSpikformerBlock",

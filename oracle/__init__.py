@@ -255,14 +255,15 @@ def sew_resnet_forward(model, x_seq, conv_dtype=torch.float64, record=None):
     (out = sew(identity, sn2(bn2(conv2(sn1(bn1(conv1(x))))))), with
     identity = downsample_sn(downsample(x)) when present;
     catfuse/patterns.py:676-689).  `record`, if a dict, receives every LIF
-    layer's input spikes/outputs keyed by module path."""
+    layer's (input, spikes, charged potential h) keyed by the module path of
+    its conv ("conv1", "layer1.0.conv1", "layer2.0.downsample", ...)."""
     T, B = x_seq.shape[:2]
 
     def cbl(name, x, conv, bn, lif):
-        s, _, _ = conv_bn_lif(x, conv, bn, lif, conv_dtype=conv_dtype)
+        s, _, h = conv_bn_lif(x, conv, bn, lif, conv_dtype=conv_dtype)
         s = torch.from_numpy(s)
         if record is not None:
-            record[name] = (x, s)
+            record[name] = (x, s, h)
         return s
 
     x = cbl("conv1", x_seq, model.conv1, model.bn1, model.sn1)
@@ -289,6 +290,56 @@ def sew_resnet_forward(model, x_seq, conv_dtype=torch.float64, record=None):
     b = model.fc.bias.detach().cpu().double() if model.fc.bias is not None else None
     y = F.linear(x.double(), w, b)
     return y.float()
+
+
+def vgg_forward(model, x_seq, conv_dtype=torch.float64, record=None):
+    """Spiking VGG forward on CPU in SpikingJelly multi-step semantics.
+
+    x_seq: [T, B, 3, H, W].  `model.features` is read as runs of Conv2d ->
+    BatchNorm2d -> [AvgPool2d(2, 2)] -> LIFNode (the AvgPool -> LIF tail of
+    catfuse/kernels/avgpool_lif.py:193-206 when present); then flatten and
+    `model.classifier` as Linear -> LIFNode pairs and a final Linear (linears
+    in float64 rounded to fp32, as linear_bn_lif).  `record`, if a dict,
+    receives (input, spikes, h) per LIF layer keyed "features.<i>" (i the
+    conv's index) and "classifier.<j>" (j the linear's index)."""
+    T, B = x_seq.shape[:2]
+    x = torch.as_tensor(_f32(x_seq))
+    feats = list(model.features)
+    i = 0
+    while i < len(feats):
+        conv, bn = feats[i], feats[i + 1]
+        if not (isinstance(conv, torch.nn.Conv2d) and isinstance(bn, torch.nn.BatchNorm2d)):
+            raise ValueError(f"features.{i}: expected Conv2d -> BatchNorm2d")
+        j = i + 2
+        z = batch_norm(conv2d(x.flatten(0, 1), conv.weight, conv.bias, conv.stride[0],
+                              conv.padding[0], dtype=conv_dtype), bn)
+        if isinstance(feats[j], torch.nn.AvgPool2d):
+            z = F.avg_pool2d(z, feats[j].kernel_size, feats[j].stride)
+            j += 1
+        s, _, h = lif_multistep(z.reshape(T, B, *z.shape[1:]), None, **lif_params_of(feats[j]))
+        s = torch.from_numpy(s)
+        if record is not None:
+            record[f"features.{i}"] = (x, s, h)
+        x = s
+        i = j + 1
+    x = x.flatten(2)
+    cls = list(model.classifier)
+    j = 0
+    while j < len(cls):
+        lin = cls[j]
+        w = lin.weight.detach().cpu().double()
+        b = None if lin.bias is None else lin.bias.detach().cpu().double()
+        z = F.linear(x.double(), w, b).float()
+        if j + 1 < len(cls) and not isinstance(cls[j + 1], torch.nn.Linear):
+            s, _, h = lif_multistep(z, None, **lif_params_of(cls[j + 1]))
+            s = torch.from_numpy(s)
+            if record is not None:
+                record[f"classifier.{j}"] = (x, s, h)
+            x = s
+            j += 2
+        else:
+            return z
+    return x
 
 
 # ---------------------------------------------------------------------------
@@ -348,42 +399,48 @@ def spikformer_forward(model, x_seq, conv_dtype=torch.float64, record=None):
     (models/spikformer_github.py:162-330 with every LIF over T): SPS stages
     Conv-BN-LIF (+ MaxPool), rpe Conv-BN-LIF + its input, tokens; blocks
     x + SSA(x), x + MLP(x); token mean, pre-head LIF, head (float64).
-    `record`, if a dict, receives (input, spikes) per fused layer."""
+    `record`, if a dict, receives (input, LIF spikes, charged potential h)
+    per LIF layer (the rpe conv's and the residual layers' spikes before
+    their add; "attn.qkv" the three concatenated)."""
     T, B = x_seq.shape[:2]
     sps = model.patch_embed
 
-    def rec(name, x, s):
+    def rec(name, x, s, h):
+        """Record (input, the LIF's spikes, its charged potential h); return
+        the spikes as a tensor."""
+        s = torch.from_numpy(s) if isinstance(s, np.ndarray) else s
         if record is not None:
-            record[name] = (x, s)
+            record[name] = (x, s, h)
         return s
 
     y = torch.as_tensor(_f32(x_seq))
     for i in range(4):
-        s, _, _ = conv_bn_lif(y, getattr(sps, f"conv{i}"), getattr(sps, f"bn{i}"),
+        s, _, h = conv_bn_lif(y, getattr(sps, f"conv{i}"), getattr(sps, f"bn{i}"),
                               getattr(sps, f"lif{i}"), conv_dtype=conv_dtype)
-        s = rec(f"patch_embed.conv{i}", y, torch.from_numpy(s))
+        s = rec(f"patch_embed.conv{i}", y, s, h)
         pool = getattr(sps, f"pool{i}", None)
         if pool is not None:
             p = F.max_pool2d(s.flatten(0, 1), pool.kernel_size, pool.stride, pool.padding)
             s = p.reshape(T, B, *p.shape[1:])
         y = s
-    r, _, _ = conv_bn_lif(y, sps.rpe_conv, sps.rpe_bn, sps.rpe_lif, conv_dtype=conv_dtype)
-    r = rec("patch_embed.rpe_conv", y, torch.from_numpy(r) + y)
+    r, _, h = conv_bn_lif(y, sps.rpe_conv, sps.rpe_bn, sps.rpe_lif, conv_dtype=conv_dtype)
+    r = rec("patch_embed.rpe_conv", y, r, h) + y
     x = r.flatten(-2).transpose(-1, -2).contiguous()
     for bi, blk in enumerate(model.blocks):
         a, m = blk.attn, blk.mlp
         p = f"blocks.{bi}"
-        qkv = [torch.from_numpy(linear_bn_lif(x, getattr(a, n), getattr(a, n + "_bn"),
-                                              getattr(a, n + "_lif"))[0]) for n in ("q", "k", "v")]
-        rec(p + ".attn.qkv", x, torch.cat(qkv, -1))
-        att = torch.from_numpy(spike_attention_lif(*qkv, a.num_heads, a.scale, a.attn_lif)[0])
-        rec(p + ".attn.core", torch.cat(qkv, -1), att)
-        pr = torch.from_numpy(linear_bn_lif(att, a.proj, a.proj_bn, a.proj_lif)[0])
-        x = rec(p + ".attn.proj", att, x + pr)
-        h = torch.from_numpy(linear_bn_lif(x, m.fc1, m.fc1_bn, m.fc1_lif)[0])
-        rec(p + ".mlp.fc1", x, h)
-        o = torch.from_numpy(linear_bn_lif(h, m.fc2, m.fc2_bn, m.fc2_lif)[0])
-        x = rec(p + ".mlp.fc2", h, x + o)
+        outs = [linear_bn_lif(x, getattr(a, n), getattr(a, n + "_bn"), getattr(a, n + "_lif"))
+                for n in ("q", "k", "v")]
+        qkv = [torch.from_numpy(o[0]) for o in outs]
+        rec(p + ".attn.qkv", x, torch.cat(qkv, -1), np.concatenate([o[2] for o in outs], -1))
+        s, _, h = spike_attention_lif(*qkv, a.num_heads, a.scale, a.attn_lif)
+        att = rec(p + ".attn.core", torch.cat(qkv, -1), s, h)
+        s, _, h = linear_bn_lif(att, a.proj, a.proj_bn, a.proj_lif)
+        x = x + rec(p + ".attn.proj", att, s, h)
+        s, _, h = linear_bn_lif(x, m.fc1, m.fc1_bn, m.fc1_lif)
+        hid = rec(p + ".mlp.fc1", x, s, h)
+        s, _, h = linear_bn_lif(hid, m.fc2, m.fc2_bn, m.fc2_lif)
+        x = x + rec(p + ".mlp.fc2", hid, s, h)
     f = x.mean(dim=2)
     s = torch.from_numpy(lif_multistep(f, None, **lif_params_of(model.pre_head_lif))[0])
     w = model.head.weight.detach().cpu().double()

@@ -197,29 +197,30 @@ def test_substitute_sf_vgg11():
 
 
 def test_crossover_inputs_and_decision():
-    """The crossover sweep's input patterns and its decision rule (CPU)."""
-    from catfuse_amd.sparseflow import crossover as xo
+    """The crossover sweep's input patterns and its decision rule (bench.py
+    --workload sf_crossover; CPU parts)."""
+    import bench
     shape = (2, 3, 16, 14, 14)
-    x = xo.c1_input(0.5, "iid", shape, seed=1)
+    x = bench.xo_input(0.5, "iid", shape, seed=1)
     assert x.shape == shape and set(x.unique().tolist()) <= {0.0, 1.0}
     # spatial: a zeroed 8x8 block is zero in every channel
-    xs = xo.c1_input(1.0, "spatial", shape, seed=2)
+    xs = bench.xo_input(1.0, "spatial", shape, seed=2)
     blocks = xs[..., :8, :8].amax(dim=(3, 4))           # [T, B, C]
     assert torch.equal(blocks.amax(dim=2, keepdim=True).expand_as(blocks), blocks)
     # block: zeroed per channel, about 30% of the blocks survive
-    xb = xo.c1_input(1.0, "block", (4, 8, 64, 16, 16), seed=3)
+    xb = bench.xo_input(1.0, "block", (4, 8, 64, 16, 16), seed=3)
     frac = float(xb.mean())
     assert 0.2 < frac < 0.4
     with pytest.raises(ValueError):
-        xo.c1_input(0.1, "checker", shape)
+        bench.xo_input(0.1, "checker", shape)
     rows = [dict(pattern="iid", rate=r, density=r, SparseFlow=sf, StreamFuse=10.0,
                  DenseKeep=12.0, auto=10.0)
             for r, sf in ((0.0, 1.0), (0.01, 9.0), (0.1, 11.0), (0.5, 13.0))]
     # rate 0 (StaticZero) never counts as a SparseFlow win
-    assert xo.crossover(rows) == {"iid": pytest.approx(0.99)}
+    assert bench.xo_crossover(rows) == {"iid": pytest.approx(0.99)}
     rows[1]["SparseFlow"] = 10.5
-    assert xo.crossover(rows) == {"iid": None}
-    assert "| iid | 0.01 |" in xo.format_table(rows)
+    assert bench.xo_crossover(rows) == {"iid": None}
+    assert "| iid | 0.01 |" in bench.xo_table(rows)
 
 
 def test_fused_global_avgpool_fallback_cpu():
@@ -254,3 +255,113 @@ def test_token_view_and_membrane_layout():
         rows = nat.reshape(B * N, C)                       # token-major rows of one step
         view = rows.view(nimg, H * W, C).transpose(1, 2)   # [nimg, C, H*W] (NCHW per image)
         assert torch.equal(token_membrane(view.contiguous(), B, N), nat)
+
+
+# ---------------------------------------------------------------------------
+# structures the fused kernels do not compute stay unfused
+# ---------------------------------------------------------------------------
+
+def _seq(*mods):
+    m = torch.nn.Sequential(*mods)
+    snn.functional.set_step_mode(m, "m")
+    return m.eval()
+
+
+@pytest.mark.parametrize("conv_kw, reason", [
+    (dict(groups=8), "groups=8"),
+    (dict(groups=8, dilation=2, padding=2), "groups=8"),
+    (dict(dilation=2, padding=2), "dilation"),
+    (dict(padding_mode="reflect"), "padding_mode"),
+    (dict(kernel_size=(1, 3), padding=(0, 1)), "non-square kernel_size"),
+    (dict(stride=(1, 2)), "non-square stride"),
+    (dict(padding="same"), "padding='same'"),
+])
+def test_unsupported_conv_left_unfused(conv_kw, reason):
+    """Depthwise/grouped, dilated, reflect-padded and non-square convs are
+    not substituted (a dense fused kernel would compute something else);
+    optimize succeeds, the original module stays, and the reason is listed."""
+    import catfuse_amd
+    from catfuse_amd.patterns import conv_geometry, CTFPattern, PartialFusionConvBNLIF
+    kw = dict(kernel_size=3, stride=1, padding=1, bias=False)
+    kw.update(conv_kw)
+    ks = kw.pop("kernel_size")
+    conv = snn.Conv2d(8, 8, ks, **kw)
+    m = _seq(conv, snn.BatchNorm2d(8), snn.LIFNode(),
+             snn.Conv2d(8, 16, 3, 1, 1, bias=False), snn.BatchNorm2d(16), snn.LIFNode())
+    from catfuse_amd.substitute import substitute
+    for fn in (lambda mm: catfuse_amd.optimize(mm, T=4), substitute):
+        fused, stats = fn(m)
+        assert type(fused[0]).__name__ == "Conv2d" and not isinstance(fused[0], CTFPattern)
+        assert torch.equal(fused[0].weight, conv.weight)
+        assert stats["fused_lif_nodes"] == 1 and stats["total_lif_nodes"] == 2
+        assert any(reason in s and s.startswith("0:") for s in stats["unsupported_structures"]), \
+            stats["unsupported_structures"]
+        assert sum(isinstance(x, CTFPattern) for x in fused.modules()) == 1
+    with pytest.raises(ValueError):
+        conv_geometry(conv)
+    with pytest.raises(ValueError):
+        PartialFusionConvBNLIF.from_sj_modules(conv, snn.BatchNorm2d(8), snn.LIFNode())
+
+
+def test_sew_block_with_depthwise_conv_left_unfused():
+    """A SEW BasicBlock whose conv2 is depthwise is not replaced by the
+    fused block (conv1 and the downsample may still fuse one by one)."""
+    import catfuse_amd
+    from catfuse_amd.patterns import CTFSEWBasicBlock
+    net = snn.sew_resnet18(num_classes=10)
+    blk = net.layer1[1]
+    blk.conv2 = snn.Conv2d(64, 64, 3, 1, 1, groups=64, bias=False)
+    snn.functional.set_step_mode(net, "m")
+    from catfuse_amd.substitute import substitute
+    for fn in (lambda mm: catfuse_amd.optimize(mm, T=4), substitute):
+        fused, stats = fn(net.eval())
+        assert not isinstance(fused.layer1[1], CTFSEWBasicBlock)
+        assert type(fused.layer1[1].conv2).__name__ == "Conv2d"
+        assert fused.layer1[1].conv2.groups == 64
+        assert any(s.startswith("layer1.1.conv2:") and "groups=64" in s
+                   for s in stats["unsupported_structures"])
+        assert isinstance(fused.layer1[0], CTFSEWBasicBlock)
+
+
+class IFNode(torch.nn.Module):
+    """An integrate-and-fire neuron (SpikingJelly's IFNode has v_threshold,
+    v_reset but no leak): not an LIF neuron."""
+
+    def __init__(self, **kw):
+        super().__init__()
+        self.v_threshold, self.v_reset, self.step_mode = 1.0, 0.0, "m"
+
+    def forward(self, x):
+        return (x.cumsum(0) >= 1.0).float()
+
+
+def test_spikformer_block_with_if_neurons_left_unfused():
+    import catfuse_amd
+    from catfuse_amd.transformer import CTFSpikformerBlock, is_spikformer_block
+    net = snn.Spikformer(img_size=32, num_classes=10, embed_dim=64, num_heads=2, depth=2,
+                         pools=(0, 1))
+    net.blocks[1].attn.k_lif = IFNode()
+    assert not is_spikformer_block(net.blocks[1]) and is_spikformer_block(net.blocks[0])
+    fused, stats = catfuse_amd.optimize(net.eval(), T=4)
+    assert isinstance(fused.blocks[0], CTFSpikformerBlock)
+    assert not isinstance(fused.blocks[1], CTFSpikformerBlock)
+    assert stats["fused_lif_nodes"] <= stats["total_lif_nodes"]
+
+
+def test_spikformer_other_head_dims_fuse_with_gemm_core():
+    """head dim 64 (the reference's spikformer_cifar_tiny: dim 192, 3 heads)
+    is substituted; the attention core then runs as exact library GEMMs
+    (the MFMA core kernel covers head dim 32)."""
+    import catfuse_amd
+    from catfuse_amd.transformer import CTFSpikformerBlock
+    net = snn.Spikformer(img_size=32, num_classes=10, embed_dim=192, num_heads=3, depth=1,
+                         pools=(0, 1))
+    fused, stats = catfuse_amd.optimize(net.eval(), T=4)
+    blk = fused.blocks[0]
+    assert isinstance(blk, CTFSpikformerBlock)
+    assert blk.attn.head_dim == 64 and not blk.attn.kernel_covers(64)
+    assert stats["fused_lif_nodes"] == stats["total_lif_nodes"] - 1   # pre-head LIF
+    small = snn.spikformer_8_384(img_size=224)
+    f2, _ = catfuse_amd.optimize(small.eval(), T=4)
+    a = f2.blocks[0].attn
+    assert a.head_dim == 32 and a.kernel_covers(196) and not a.kernel_covers(3136)

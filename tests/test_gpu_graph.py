@@ -47,3 +47,35 @@ def test_graph_replays_match_eager(cuda, expanded):
                 assert torch.equal(z, eager[(i + 1) % 3])
         with pytest.raises(ValueError):
             graphed(torch.zeros(T, B + 1, 3, HW, HW, device=cuda))
+
+
+def test_graph_replays_of_a_model_ending_in_a_fused_conv(cuda):
+    """A captured forward whose output is a fused layer's NHWC-backed tensor
+    (a feature extractor): every replay's fp32 output holds that replay's
+    values (the fp16 -> fp32 fill is part of the graph)."""
+    import catfuse_amd
+    from catfuse_amd import graph, snn
+    g = torch.Generator().manual_seed(4)
+    m = torch.nn.Sequential(
+        snn.Conv2d(16, 32, 3, 1, 1, bias=False), snn.BatchNorm2d(32), snn.LIFNode(v_threshold=0.3),
+        snn.Conv2d(32, 32, 3, 1, 1, bias=False), snn.BatchNorm2d(32), snn.LIFNode(v_threshold=0.3))
+    snn.functional.set_step_mode(m, "m")
+    snn.kaiming_init(m, g)
+    snn.randomize_bn(m, g)
+    fused, _ = catfuse_amd.optimize(m.eval(), device=cuda, T=4)
+    T, B = 4, 2
+    xs = [(torch.rand(T, B, 16, 24, 24, generator=g) < 0.3).float().to(cuda) for _ in range(3)]
+    with torch.no_grad():
+        eager = []
+        for x in xs:
+            snn.functional.reset_net(fused)
+            eager.append(fused(x).clone())
+        assert not torch.equal(eager[0], eager[1])
+        graphed = graph.capture(fused, xs[0])
+        for rep in range(2):
+            for i, x in enumerate(xs):
+                y = graphed(x).clone()
+                torch.cuda.synchronize()
+                assert torch.equal(y, eager[i]), f"replay {rep}, input {i}"
+                snn.functional.reset_net(fused)
+                fused(xs[(i + 2) % 3])     # eager work between replays

@@ -289,3 +289,164 @@ def test_spike_attention_oracle_pins():
         np.testing.assert_array_equal(s, s_ref)
     qi, ki, vi = (a.reshape(T, B, N, heads, 32).permute(0, 1, 3, 2, 4).long() for a in (q, k, v))
     assert torch.equal((qi @ ki.transpose(-1, -2)) @ vi, qi @ (ki.transpose(-1, -2) @ vi))
+
+
+# ---------------------------------------------------------------------------
+# network-level forwards, pinned against the eager SpikingJelly-style models
+# (catfuse_amd.snn: the module formulation, nn.Conv2d / BatchNorm2d /
+# LIFNode.forward in torch fp32) layer by layer, with conv_dtype fp32 so the
+# conv is the same library routine on the same values
+# ---------------------------------------------------------------------------
+
+def _lif_outputs(model, names_of):
+    """Forward hooks on every LIFNode: {key: output spikes}."""
+    from catfuse_amd import snn
+    outs, hs = {}, []
+    for name, mod in model.named_modules():
+        if isinstance(mod, snn.LIFNode):
+            key = names_of(name)
+            hs.append(mod.register_forward_hook(
+                lambda m, a, o, key=key: outs.__setitem__(key, o.detach().clone())))
+    return outs, hs
+
+
+def _assert_spikes(got, ref, h, what):
+    from parity import lif_parity
+    lif_parity(got.numpy(), None, np.asarray(ref), None, h, what=what)
+
+
+def _sew_key(name):
+    if name == "sn1":
+        return "conv1"
+    base, leaf = name.rsplit(".", 1)
+    return {"sn1": base + ".conv1", "sn2": base + ".conv2",
+            "downsample_sn": base + ".downsample"}[leaf]
+
+
+@pytest.mark.parametrize("v_th", [1.0, 0.1])
+def test_sew_resnet_forward_pinned_by_eager_model(v_th):
+    """oracle.sew_resnet_forward (block order, downsample + its LIF, the
+    SEW ADD, the stem pool, the head) equals the eager SEW-ResNet18 built
+    from modules: every LIF layer's spikes and the logits.  v_th = 0.1 keeps
+    every layer active (checked), so no layer compares all-zero tensors."""
+    from catfuse_amd import snn
+    m = snn.sew_resnet18(num_classes=10, cnf="ADD", v_threshold=v_th)
+    snn.functional.set_step_mode(m, "m")
+    g = torch.Generator().manual_seed(5)
+    snn.kaiming_init(m, g)
+    snn.randomize_bn(m, g)
+    m.eval()
+    T, B = 2, 2
+    x = torch.randn(B, 3, 48, 48, generator=g).unsqueeze(0).expand(T, B, 3, 48, 48)
+    outs, hs = _lif_outputs(m, _sew_key)
+    with torch.no_grad():
+        y = m(x.contiguous())
+    for h in hs:
+        h.remove()
+    rec = {}
+    y_ref = oracle.sew_resnet_forward(m, x, conv_dtype=torch.float32, record=rec)
+    assert set(rec) == set(outs) and len(rec) == 20
+    for k, (xin, s, h) in rec.items():
+        # the stem's spikes before the pool, every other layer's before the add
+        _assert_spikes(outs[k], s, h, k)
+        if v_th < 1.0:
+            assert float(s.sum()) > 0, f"{k}: no spikes (the live variant must be active)"
+    np.testing.assert_allclose(y.numpy(), y_ref.numpy(), rtol=1e-5, atol=1e-5)
+    if v_th < 1.0:
+        # a plausible composition mistake fails on the live network: the
+        # wrong connect function in one block changes the logits
+        blk = m.layer1[0]
+        blk.cnf = "AND"
+        y_bad = oracle.sew_resnet_forward(m, x, conv_dtype=torch.float32)
+        blk.cnf = "ADD"
+        assert not torch.allclose(y_bad, y_ref)
+
+
+def test_vgg_forward_pinned_by_eager_model():
+    """oracle.vgg_forward (Conv-BN-[AvgPool]-LIF runs, flatten, Linear-LIF
+    head) equals the eager spiking VGG-11-BN layer by layer and in its
+    logits; v_th = 0.25 keeps every layer active (checked)."""
+    from catfuse_amd import snn
+    m = snn.spiking_vgg11_bn(num_classes=10, v_threshold=0.25)
+    snn.functional.set_step_mode(m, "m")
+    g = torch.Generator().manual_seed(6)
+    snn.kaiming_init(m, g)
+    snn.randomize_bn(m, g)
+    with torch.no_grad():   # fan-out init leaves the 4096-wide head silent
+        for mod in m.classifier:
+            if isinstance(mod, torch.nn.Linear):
+                mod.weight.mul_(8.0)
+    m.eval()
+    T, B = 2, 2
+    x = torch.randn(T, B, 3, 32, 32, generator=g)
+    keys = {}
+    feats = list(m.features)
+    conv_idx = [i for i, mod in enumerate(feats) if isinstance(mod, torch.nn.Conv2d)]
+    lif_idx = [i for i, mod in enumerate(feats) if isinstance(mod, snn.LIFNode)]
+    for ci, li in zip(conv_idx, lif_idx):
+        keys[f"features.{li}"] = f"features.{ci}"
+    keys["classifier.1"] = "classifier.0"
+    keys["classifier.3"] = "classifier.2"
+    outs, hs = _lif_outputs(m, lambda n: keys[n])
+    with torch.no_grad():
+        y = m(x)
+    for h in hs:
+        h.remove()
+    rec = {}
+    y_ref = oracle.vgg_forward(m, x, conv_dtype=torch.float32, record=rec)
+    assert set(rec) == set(outs) and len(rec) == 10
+    for k, (xin, s, h) in rec.items():
+        _assert_spikes(outs[k], s, h, k)
+        assert float(s.sum()) > 0, f"{k}: no spikes"
+    np.testing.assert_allclose(y.numpy(), y_ref.numpy(), rtol=1e-5, atol=1e-5)
+
+
+def test_spikformer_forward_pinned_by_eager_model():
+    """oracle.spikformer_forward (SPS stages and pools, rpe + its input,
+    token layout, q/k/v/attention/proj and MLP with their residuals, token
+    mean, pre-head LIF, head) equals the eager Spikformer layer by layer and
+    in its logits; weights scaled so every layer is active (checked)."""
+    from catfuse_amd import snn
+    m = snn.Spikformer(img_size=32, num_classes=10, embed_dim=64, num_heads=2, depth=2, T=2,
+                       pools=(2, 3), scale=0.125)
+    g = torch.Generator().manual_seed(7)
+    snn.kaiming_init(m, g)
+    snn.randomize_bn(m, g)
+    with torch.no_grad():
+        for mod in m.modules():
+            if isinstance(mod, (torch.nn.Linear, torch.nn.Conv2d)) and mod is not m.head:
+                mod.weight.mul_(3.0)
+    m.eval()
+    T, B = 2, 2
+    x = torch.randn(B, 3, 32, 32, generator=g).unsqueeze(0).expand(T, B, 3, 32, 32)
+
+    def key(n):
+        if n.startswith("patch_embed."):
+            leaf = n.split(".", 1)[1]
+            return "patch_embed." + ("rpe_conv" if leaf == "rpe_lif" else "conv" + leaf[3:])
+        if n == "pre_head_lif":
+            return n
+        blk, rest = n.split(".attn.") if ".attn." in n else n.split(".mlp.")
+        leaf = rest[:-4]
+        if ".attn." in n:
+            return f"{blk}.attn." + {"q": "q", "k": "k", "v": "v", "attn": "core",
+                                     "proj": "proj"}[leaf]
+        return f"{blk}.mlp.{leaf}"
+    outs, hs = _lif_outputs(m, key)
+    with torch.no_grad():
+        y = m(x)
+    for h in hs:
+        h.remove()
+    rec = {}
+    y_ref = oracle.spikformer_forward(m, x, conv_dtype=torch.float32, record=rec)
+    for k, (xin, s, h) in rec.items():
+        if k.endswith(".attn.qkv"):
+            b = k[:-len(".qkv")]
+            got = torch.cat([outs[b + ".q"], outs[b + ".k"], outs[b + ".v"]], -1)
+        else:
+            got = outs[k]
+        got = got.reshape(s.shape) if got.numel() == s.numel() else got
+        _assert_spikes(got, s, h, k)
+        assert float(s.sum()) > 0, f"{k}: no spikes"
+    assert len(rec) == 5 + 2 * 5
+    np.testing.assert_allclose(y.numpy(), y_ref.numpy(), rtol=1e-4, atol=1e-4)
