@@ -25,6 +25,7 @@ import sys
 
 PKG_DIR = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(PKG_DIR, "csrc")
+INCLUDE = os.path.join(os.path.dirname(PKG_DIR), "include")   # the C-ABI header
 LIB_DIR = os.path.join(PKG_DIR, "_lib")
 LIB_NAME = "libcatfuse_amd.so"
 BUILD_DIR = os.path.join(os.path.dirname(PKG_DIR), "_build", "catfuse_amd")
@@ -57,13 +58,15 @@ def sources() -> list:
 
 
 def source_digest() -> str:
-    """SHA-256 over the HIP sources and headers the library is built from."""
+    """SHA-256 over the HIP sources and headers (with the C-ABI header) the
+    library is built from."""
     h = hashlib.sha256()
-    for f in sorted(os.listdir(CSRC)):
-        if f.endswith((".hip", ".h")):
-            h.update(f.encode())
-            with open(os.path.join(CSRC, f), "rb") as fh:
-                h.update(fh.read())
+    files = [os.path.join(CSRC, f) for f in sorted(os.listdir(CSRC)) if f.endswith((".hip", ".h"))]
+    files.append(os.path.join(INCLUDE, "catfuse_amd.h"))
+    for path in files:
+        h.update(os.path.basename(path).encode())
+        with open(path, "rb") as fh:
+            h.update(fh.read())
     return h.hexdigest()
 
 
@@ -73,7 +76,7 @@ def stamp_path() -> str:
 
 def _compile(src: str, hipcc: str) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src)[:-4] + ".o")
-    cmd = [hipcc, *HIPCC_FLAGS, "-I", CSRC, "-c", src, "-o", obj]
+    cmd = [hipcc, *HIPCC_FLAGS, "-I", CSRC, "-I", INCLUDE, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n{' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

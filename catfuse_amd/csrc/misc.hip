@@ -1,5 +1,8 @@
 // Library metadata, error strings and the matrix-core operand layout probe.
+// cf_common.h first: the C-ABI header's constant macros must not rename its
+// enumerators
 #include "cf_common.h"
+#include "catfuse_amd.h"
 
 namespace {
 
@@ -28,7 +31,12 @@ __global__ void mfma_layout_probe(const _Float16* __restrict__ A, const _Float16
 
 CF_API int cf_version(void) { return 100; }
 
-CF_API const char* cf_error_string(int code) { return hipGetErrorString((hipError_t)code); }
+CF_API const char* cf_error_string(int code) {
+  if (code == CF_ERROR_NOALLOC_LIMIT)
+    return "input exceeds the no-allocation workspace (CF_NOALLOC_MAX_PIXELS / "
+           "CF_NOALLOC_MAX_TILES)";
+  return hipGetErrorString((hipError_t)code);
+}
 
 CF_API int cf_probe_mfma_layout(const void* A, const void* B, float* D, void* stream) {
   if (!A || !B || !D) return (int)hipErrorInvalidValue;

@@ -325,6 +325,47 @@ int cf_conv_stem_lif_maxpool(const float* x, const void* w_stem, const float* al
                              double v_th, double v_reset, int hard_reset, int decay_input,
                              void* stream);
 
+/* Library error code returned beside the hipError_t values: the input of
+ * cf_conv_sparse_noalloc needs more workspace than its static array holds. */
+#define CF_ERROR_NOALLOC_LIMIT 7001
+
+/* Workspace of cf_conv_sparse_noalloc, a static device array of
+ * CF_NOALLOC_SCRATCH_BYTES (about 9 MiB) on every GPU the library runs on:
+ * the input's count block, activity bits for up to CF_NOALLOC_MAX_PIXELS
+ * input pixels (T*B*H*W) and tile masks for up to CF_NOALLOC_MAX_TILES
+ * prescan tiles (T*B*ceil(Ho/tile_h)*ceil(Wo/tile_w)). */
+#define CF_NOALLOC_MAX_PIXELS (1 << 21)
+#define CF_NOALLOC_MAX_TILES (1 << 17)
+#define CF_NOALLOC_SCRATCH_BYTES (4096 + 4 * CF_NOALLOC_MAX_PIXELS + 8 * CF_NOALLOC_MAX_TILES)
+
+/* The SparseFlow-routed fused Conv -> BN -> LIF of cf_conv_mfma on an fp16
+ * NHWC input (x [T*B][H][W][Cp], channels >= Cin zero, e.g. a fused conv's
+ * output copy), with the routing workspace in the library instead of the
+ * caller's memory: no allocation at all.  No counterpart in the reference;
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  It runs
+ * cf_scan_nhwc (activity bits + nonzero count of x), cf_prescan_tiles (tile
+ * masks, tile_h x tile_w output tiles, group_size-channel groups) and
+ * cf_conv_mfma routed on them (StaticZero / SparseFlow above
+ * sparse_threshold / dense), with their workspace in a static device array
+ * (CF_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends); results
+ * are those of the same three calls with caller buffers, bit for bit.
+ * Square kernels (ksize x ksize); other arguments as cf_conv_mfma.  Returns
+ * CF_ERROR_NOALLOC_LIMIT, launching nothing, when T*B*H*W >
+ * CF_NOALLOC_MAX_PIXELS or the tile count > CF_NOALLOC_MAX_TILES.  Every
+ * call on one GPU uses that GPU's array: calls that overlap on one GPU (on
+ * streams not ordered against each other) race. */
+int cf_conv_sparse_noalloc(const void* x, int64_t Cin, const void* w_packed, const float* alpha,
+                           const float* beta, const float* v_in, float* v_out, float* out,
+                           void* out_nhwc, int64_t cp_out, const float* identity,
+                           const void* identity_nhwc, int64_t cp_id, int identity_mode,
+                           unsigned long long* nz_out, double sparse_threshold, int64_t T,
+                           int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
+                           int64_t W, int64_t Ho, int64_t Wo, int64_t ksize, int64_t stride,
+                           int64_t pad, int64_t tile_h, int64_t tile_w, int64_t group_size,
+                           int epilogue, double tau, double v_th, double v_reset, int hard_reset,
+                           int decay_input, void* stream);
+
 /* Diagnostic: one wave computes D(32x32 fp32) = A(32x16 fp16) * B(16x32
  * fp16) through the matrix-core lane mapping cf_conv_mfma relies on.
  * No reference counterpart (layout self-test). */
