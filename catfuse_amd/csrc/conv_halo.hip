@@ -177,9 +177,22 @@ constexpr int halo_min_blocks() {
 // output channel real (Cout a multiple of 64): no per-element branches.
 // ONEB: T fits one time block (T <= TB): the block loop runs once, so the
 // K-loop state is dead in the epilogue (fewer live registers).
+// One halo buffer (halves) of a configuration: whole 64-unit blocks of the
+// staged halo of a time block (16-byte units of TB steps x RH x RW pixels).
+template <int TH, int TW, int S, int K>
+constexpr int halo_buf_halves() {
+  using G = HaloGeom<S, K, TH, TW>;
+  return ((halo_tb<S, K>() * G::RH * G::RW * 4 + 63) / 64) * 64 * 8;
+}
+
+// The work of workgroup L of the nL that compute one conv: a device
+// function, so that one grid can run two convs of the same input side by
+// side (conv_halo_pair_kernel).  halo: 2 * halo_buf_halves() halves of LDS;
+// bn_s: the tile's BN coefficients; any_sh: the workgroup's vote words.
 template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB>
-__global__ __launch_bounds__(256, (halo_min_blocks<TH, TW>()))
-void conv_halo_kernel(HaloArgs a) {
+__device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const int nL,
+                                          _Float16* __restrict__ halo, float (*bn_s)[64],
+                                          unsigned* any_sh) {
   using G = HaloGeom<S, K, TH, TW>;
   constexpr int BM = 64;
   constexpr int BN = TH * TW;
@@ -201,9 +214,7 @@ void conv_halo_kernel(HaloArgs a) {
   constexpr int NOBUF = 2 * OSTEP <= HB ? 2 : 1;
   static_assert(OSTEP <= HB, "output staging exceeds a halo buffer");
   static_assert(NT >= 1, "tile too small");
-  __shared__ __attribute__((aligned(16))) _Float16 halo[2 * HB];
-  __shared__ __attribute__((aligned(16))) float bn_s[2][BM];  // alpha, beta of the tile
-  __shared__ unsigned any_sh[4];  // per-wave votes of the output count
+  static_assert(HB == halo_buf_halves<TH, TW, S, K>(), "halo buffer size");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar registers
@@ -216,7 +227,7 @@ void conv_halo_kernel(HaloArgs a) {
   // neighbouring tiles (whose halos overlap) then run together on one XCD and
   // share its L2.
   const int nwork = a.B * a.GH * a.GW * (a.Coutp / BM);
-  const int L = blockIdx.x, xcd = L & 7, j = L >> 3;
+  const int xcd = L & 7, j = L >> 3;
   const int work = xcd * (nwork >> 3) + min(xcd, nwork & 7) + j;
   const int ncb = a.Coutp / BM;
   const int tile = work / ncb;
@@ -272,7 +283,7 @@ void conv_halo_kernel(HaloArgs a) {
       // lean path, one fp32 value otherwise
       const uint32_t mag = LEAN ? 0x7fff7fffu : 0x7fffffffu;
       const bool any = cf_wg_any((anyw & mag) != 0u, any_sh);
-      if (threadIdx.x == 0) cf_count_publish(a.nz_out, any ? 1ull : 0ull, blockIdx.x, gridDim.x);
+      if (threadIdx.x == 0) cf_count_publish(a.nz_out, any ? 1ull : 0ull, (unsigned)L, (unsigned)nL);
     }
   };
 
@@ -831,6 +842,16 @@ void conv_halo_kernel(HaloArgs a) {
     }
   }
   publish_count();
+}
+
+template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB>
+__global__ __launch_bounds__(256, (halo_min_blocks<TH, TW>()))
+void conv_halo_kernel(HaloArgs a) {
+  __shared__ __attribute__((aligned(16))) _Float16 halo[2 * halo_buf_halves<TH, TW, S, K>()];
+  __shared__ __attribute__((aligned(16))) float bn_s[2][64];  // alpha, beta of the tile
+  __shared__ unsigned any_sh[4];  // per-wave votes of the output count
+  halo_body<TH, TW, S, K, EPI, LM, LEAN, ONEB>(a, (int)blockIdx.x, (int)gridDim.x, halo, bn_s,
+                                               any_sh);
 }
 
 template <int TH, int TW, int S, int K = 3>

@@ -26,8 +26,9 @@ import torch.nn as nn
 
 from catfuse_amd.hardware import runtime_profile
 from catfuse_amd.implementations import ConvLIFParams, ConvLIFSpec, DenseKeep, StreamFuse
-from catfuse_amd.runtime import (EPI_Z, ID_ADD_SPIKE, ID_ADD_Z, ConvLIFRunner, avgpool2x2_lif,
-                                 global_avgpool_nhwc, lif_multistep, pad32, shadow_of)
+from catfuse_amd.runtime import (EPI_Z, ID_ADD_SPIKE, ID_ADD_Z, ConvLIFRunner,
+                                 GroupedConvLIFRunner, avgpool2x2_lif, global_avgpool_nhwc,
+                                 lif_multistep, pad32, shadow_of)
 from catfuse_amd.state import StateBuffer
 
 try:  # SpikingJelly's MemoryModule when available, so reset_net recognises us
@@ -68,6 +69,23 @@ def conv_unsupported_reason(conv) -> Optional[str]:
         if int(a) != int(b):
             return f"non-square {name}=({a}, {b})"
     return None
+
+
+def grouped_conv_supported(conv) -> bool:
+    """A grouped convolution (groups > 1, depthwise included) that the fused
+    grouped kernel computes: undilated, zero padding, square kernel, stride
+    and padding, channels divisible by groups."""
+    groups = int(getattr(conv, "groups", 1))
+    if groups <= 1 or isinstance(getattr(conv, "padding", 0), str):
+        return False
+    if any(int(d) != 1 for d in _pair(getattr(conv, "dilation", 1))):
+        return False
+    if getattr(conv, "padding_mode", "zeros") != "zeros":
+        return False
+    if conv.in_channels % groups or conv.out_channels % groups:
+        return False
+    return all(int(_pair(getattr(conv, n))[0]) == int(_pair(getattr(conv, n))[1])
+               for n in ("kernel_size", "stride", "padding"))
 
 
 def conv_geometry(conv):
@@ -390,6 +408,109 @@ class PartialFusionConvBNLIFMaxPool(PartialFusionConvBNLIF):
                 inst.conv_bias.copy_(sj_conv.bias)
         inst._copy_bn(sj_bn)
         return inst.to(sj_conv.weight.device)
+
+
+class PartialFusionGroupedConvBNLIF(CTFPattern):
+    """Grouped Conv (groups > 1; depthwise when groups == in_channels) ->
+    BN (eval, folded) -> LIF in one launch over all T steps
+    (cf_conv_grouped_lif).  The reference runs a grouped conv as `groups`
+    independent sparse sub-convs with the LIF separate
+    (catfuse/sparseflow/sparse_grouped_conv2d_kernel.py:93-364); a grouped
+    conv is HBM-bound (Cin/groups * k^2 products per output), so here it is
+    one streaming kernel on the fp16 NHWC copies, StaticZero on an all-zero
+    input.  The membrane state is channels-last ([B, Cout, Ho, Wo] in
+    torch's channels_last format).  Analog inputs are read in fp32."""
+
+    policy_row = "GroupedConvBNLIF"
+
+    def __init__(self, in_channels, out_channels, kernel_size, stride=1, padding=0, groups=1,
+                 tau=2.0, v_threshold=1.0, v_reset=0.0, bn_eps=1e-5, decay_input=True,
+                 bias=False, has_bn=True):
+        super().__init__()
+        if in_channels % groups or out_channels % groups:
+            raise ValueError("channels must be divisible by groups")
+        self.in_channels, self.out_channels = int(in_channels), int(out_channels)
+        self.kernel_size, self.stride, self.padding = int(kernel_size), int(stride), int(padding)
+        self.groups = int(groups)
+        self.tau, self.v_threshold = float(tau), float(v_threshold)
+        self.v_reset = None if v_reset is None else float(v_reset)
+        self.decay_input = bool(decay_input)
+        self.bn_eps = float(bn_eps)
+        self.weight = nn.Parameter(torch.empty(out_channels, in_channels // groups, kernel_size,
+                                               kernel_size))
+        nn.init.kaiming_normal_(self.weight)
+        self.conv_bias = nn.Parameter(torch.zeros(out_channels)) if bias else None
+        if has_bn:
+            self.bn_weight = nn.Parameter(torch.ones(out_channels))
+            self.bn_bias = nn.Parameter(torch.zeros(out_channels))
+            self.register_buffer("running_mean", torch.zeros(out_channels))
+            self.register_buffer("running_var", torch.ones(out_channels))
+        else:
+            self.bn_weight = self.bn_bias = None
+            self.register_buffer("running_mean", None)
+            self.register_buffer("running_var", None)
+        self.state = StateBuffer()
+        self._register_state(self.state)
+        self._runner = None
+        self._runner_key = None
+        self._exact_input = None
+
+    def runner(self) -> GroupedConvLIFRunner:
+        ts = [t for t in (self.weight, self.conv_bias, self.bn_weight, self.bn_bias,
+                          self.running_mean, self.running_var) if t is not None]
+        key = tuple((id(t), t._version, t.device) for t in ts)
+        if key != self._runner_key:
+            scale = shift = None
+            if self.bn_weight is not None:
+                scale, shift = fold_bn(self.bn_weight, self.bn_bias, self.running_mean,
+                                       self.running_var, self.bn_eps)
+            self._runner = GroupedConvLIFRunner(
+                self.weight.detach(), self.groups, scale, shift,
+                None if self.conv_bias is None else self.conv_bias.detach(), self.stride,
+                self.padding, self.tau, self.v_threshold, self.v_reset, self.decay_input)
+            self._runner_key = key
+        return self._runner
+
+    def forward(self, x):
+        squeeze = x.ndim == 4
+        if squeeze:
+            x = x.unsqueeze(0)
+        if x.dim() != 5 or not x.is_cuda or x.dtype != torch.float32:
+            raise RuntimeError("catfuse_amd fused patterns take float32 GPU [T, B, C, H, W] "
+                               "tensors (there is no CPU path)")
+        if self._exact_input is None:   # one host check per layer: spikes or analog values
+            self._exact_input = bool((x.half().float() == x).all().item())
+        r = self.runner()
+        B = x.shape[1]
+        Ho, Wo = r.out_hw(x.shape[3], x.shape[4])
+        v_in = self.state.peek((B, self.out_channels, Ho, Wo), x.device)
+        s, v = r.run(x, v_in, analog=not self._exact_input)
+        self.state.set(v)
+        return s.squeeze(0) if squeeze else s
+
+    @classmethod
+    def from_sj_modules(cls, sj_conv, sj_bn, sj_lif):
+        if not grouped_conv_supported(sj_conv):
+            raise ValueError("not a grouped conv the fused grouped kernel computes")
+        k, s, p = (int(_first(getattr(sj_conv, n))) for n in ("kernel_size", "stride", "padding"))
+        inst = cls(sj_conv.in_channels, sj_conv.out_channels, k, s, p, sj_conv.groups,
+                   bn_eps=sj_bn.eps if sj_bn is not None else 1e-5,
+                   bias=sj_conv.bias is not None, has_bn=sj_bn is not None, **lif_params(sj_lif))
+        with torch.no_grad():
+            inst.weight.copy_(sj_conv.weight)
+            if sj_conv.bias is not None:
+                inst.conv_bias.copy_(sj_conv.bias)
+            if sj_bn is not None:
+                inst.bn_weight.copy_(sj_bn.weight)
+                inst.bn_bias.copy_(sj_bn.bias)
+                inst.running_mean.copy_(sj_bn.running_mean)
+                inst.running_var.copy_(sj_bn.running_var)
+        return inst.to(sj_conv.weight.device)
+
+    def extra_repr(self):
+        return (f"{self.in_channels}, {self.out_channels}, kernel_size={self.kernel_size}, "
+                f"stride={self.stride}, padding={self.padding}, groups={self.groups}, "
+                f"tau={self.tau}, v_th={self.v_threshold}, v_reset={self.v_reset}")
 
 
 # ---------------------------------------------------------------------------
@@ -750,6 +871,7 @@ PATTERN_REGISTRY = {
     "PartialFusionConvBNAddLIF": PartialFusionConvBNAddLIF,
     "PartialFusionConvBNAvgPoolLIF": PartialFusionConvBNAvgPoolLIF,
     "PartialFusionConvBNLIFMaxPool": PartialFusionConvBNLIFMaxPool,
+    "PartialFusionGroupedConvBNLIF": PartialFusionGroupedConvBNLIF,
     "FusedLinearLIF": FusedLinearLIF,
     "FusedAddLIF": FusedAddLIF,
     "FusedAddBNLIF": FusedAddBNLIF,
@@ -766,9 +888,9 @@ PATTERN_REGISTRY["STFusionConvBNLIF"] = STFusionConvBNLIF
 
 __all__ = ["CTFPattern", "PartialFusionConvLIF", "PartialFusionConvBNLIF",
            "PartialFusionConvBNAddLIF", "PartialFusionConvBNAvgPoolLIF",
-           "PartialFusionConvBNLIFMaxPool", "FusedLinearLIF",
+           "PartialFusionConvBNLIFMaxPool", "PartialFusionGroupedConvBNLIF", "FusedLinearLIF",
            "FusedAddLIF", "FusedAddBNLIF", "FusedAvgPoolLIF", "FusedGlobalAvgPool",
            "CTFSEWBasicBlock",
            "CTFSpikingBasicBlock", "CTFSEWBottleneck", "CTFSpikingBottleneck",
            "STFusionConvBNLIF", "PATTERN_REGISTRY", "fold_bn", "lif_params", "conv_geometry",
-           "conv_unsupported_reason", "is_lif_node"]
+           "conv_unsupported_reason", "grouped_conv_supported", "is_lif_node"]

@@ -1001,3 +1001,112 @@ class ConvLIFRunner:
         check(rc, "cf_conv_stem_lif_maxpool")
         _t1("conv_stem", ev, flops=2 * B * Hc * Wc * self.Cout * C * self.KH * self.KW)
         return out, v_out
+
+
+class GroupedConvLIFRunner:
+    """Device state + launch of one fused grouped Conv -> (BN) -> LIF layer
+    (groups > 1; depthwise when groups == Cin): cf_conv_grouped_lif.
+
+    weight [Cout, Cin/groups, K, K] fp32; bn_scale/bn_shift [Cout] (folded
+    eval BN, optional); bias [Cout] (optional).  The membrane state is kept
+    channels-last: a [B, Cout, Ho, Wo] tensor in torch's channels_last
+    memory format (the kernel's lanes run along channels)."""
+
+    def __init__(self, weight, groups, bn_scale, bn_shift, bias, stride, padding, tau,
+                 v_threshold, v_reset, decay_input):
+        self.weight, self.groups = weight, int(groups)
+        self.bn_scale, self.bn_shift, self.bias = bn_scale, bn_shift, bias
+        self.stride, self.padding = int(stride), int(padding)
+        self.lif = _lif_args(tau, v_threshold, v_reset, decay_input)
+        self.Cout, self.Cg, self.KH, self.KW = (int(s) for s in weight.shape)
+        self.Cin = self.Cg * self.groups
+        self.Cp = pad32(self.Cin)
+        self.Coutp = ((self.Cout + 63) // 64) * 64
+        self._key = None
+        self._gen = [0]
+        self._blocks = {}
+
+    def _ensure(self, device):
+        key = (device, self.weight.data_ptr(), self.weight._version,
+               *(None if t is None else (t.data_ptr(), t._version)
+                 for t in (self.bn_scale, self.bn_shift, self.bias)))
+        if key == self._key:
+            return
+        w = self.weight.detach().float().contiguous()
+        ts = [None if t is None else t.detach().float().contiguous()
+              for t in (self.bn_scale, self.bn_shift, self.bias)]
+        for name, t in zip(("weight", "bn_scale", "bn_shift", "bias"), [w] + ts):
+            if t is not None:
+                require_gpu_tensor(t, name)
+        self.alpha = torch.empty(self.Coutp, dtype=torch.float32, device=device)
+        self.beta = torch.empty(self.Coutp, dtype=torch.float32, device=device)
+        check(_hip.lib().cf_pack_conv_weights(ptr(w), self.Cout, self.Cg, self.KH, self.KW,
+                                              self.Coutp, self.Cp, ptr(ts[0]), ptr(ts[1]),
+                                              ptr(ts[2]), None, ptr(self.alpha), ptr(self.beta),
+                                              _hip.stream(device)), "cf_pack_conv_weights")
+        self._w = w
+        self._key = key
+
+    def out_hw(self, H, W):
+        return ((H + 2 * self.padding - self.KH) // self.stride + 1,
+                (W + 2 * self.padding - self.KW) // self.stride + 1)
+
+    def _out_block(self, device):
+        blk = self._blocks.get(device)
+        if blk is None:
+            blk = count_block(device)
+            self._blocks[device] = blk
+        return blk
+
+    def run(self, x: torch.Tensor, v_in=None, *, analog=False, want_v_out=True):
+        """x [T, B, Cin, H, W] -> (spikes [T, B, Cout, Ho, Wo] held as their
+        fp16 NHWC copy with the output's count block attached, v_out
+        [B, Cout, Ho, Wo] channels-last).  A spike-valued input is read from
+        its fp16 NHWC copy (packed first when it has none); analog=True reads
+        the fp32 tensor (a stride-0 time axis reads one image for all T)."""
+        if x.dim() != 5 or x.shape[2] != self.Cin:
+            raise ValueError(f"expected [T, B, {self.Cin}, H, W], got {tuple(x.shape)}")
+        T, B, C, H, W = x.shape
+        dev = x.device
+        self._ensure(dev)
+        Ho, Wo = self.out_hw(H, W)
+        xp = x32 = nnz = None
+        tstride = 0
+        if analog:
+            if x.stride(0) == 0 and x[0].is_contiguous():
+                x32, tstride = x[0], 0
+            else:
+                x32, tstride = x.contiguous(), B
+            require_gpu_tensor(x32, "x")
+        else:
+            require_gpu_tensor(x if x.is_contiguous() else x.contiguous(), "x")
+            xp = shadow_of(x, (T * B, H, W, self.Cp))
+            if xp is not None:
+                nnz = count_of(x)
+            else:
+                xp, _ = pack_input(x.contiguous().reshape(T * B, C, H, W), cp=self.Cp,
+                                   status=status_word(dev))
+        if v_in is not None:
+            if tuple(v_in.shape) != (B, self.Cout, Ho, Wo):
+                raise ValueError("v_in must be [B, Cout, Ho, Wo]")
+            v_in = v_in.contiguous(memory_format=torch.channels_last)
+            require_gpu_tensor(v_in.permute(0, 2, 3, 1), "v_in")
+        v_out = (torch.empty((B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev,
+                             memory_format=torch.channels_last) if want_v_out else None)
+        cp_out = pad32(self.Cout)
+        nhwc = torch.empty((T * B, Ho, Wo, cp_out), dtype=torch.float16, device=dev)
+        nz_out = self._out_block(dev)
+        ev = _t0()
+        check(_hip.lib().cf_conv_grouped_lif(
+            ptr(xp), ptr(x32), tstride, ptr(self._w), ptr(self.alpha), ptr(self.beta),
+            ptr(v_in), ptr(v_out), ptr(nhwc), cp_out, ptr(nnz), ptr(nz_out), T, B, self.Cin,
+            self.Cp, self.Cout, self.groups, H, W, Ho, Wo, self.KH, self.stride, self.padding,
+            *self.lif, _hip.stream(dev)), "cf_conv_grouped_lif")
+        _t1("conv_grouped", ev,
+            flops=2 * T * B * Ho * Wo * self.Cout * self.Cg * self.KH * self.KW,
+            nbytes=(4 * T * B * H * W * self.Cin if analog else 2 * T * B * H * W * self.Cp)
+            + 2 * T * B * Ho * Wo * cp_out + 4 * B * self.Cout * Ho * Wo * (1 + (v_in is not None)))
+        out = lazy_output((T, B, self.Cout, Ho, Wo), nhwc, dev)
+        self._gen[0] += 1
+        attach_count(out, nz_out, self._gen)
+        return out, v_out

@@ -33,8 +33,8 @@ from catfuse_amd.patterns import (CTFSEWBasicBlock, CTFSEWBottleneck, CTFSpiking
                                   FusedLinearLIF,
                                   PartialFusionConvBNAvgPoolLIF, PartialFusionConvBNLIF,
                                   PartialFusionConvBNLIFMaxPool, PartialFusionConvLIF,
-                                  STFusionConvBNLIF, conv_geometry, conv_unsupported_reason,
-                                  is_lif_node)
+                                  PartialFusionGroupedConvBNLIF, STFusionConvBNLIF, conv_geometry,
+                                  conv_unsupported_reason, grouped_conv_supported, is_lif_node)
 from catfuse_amd.policy import SpatialBackend, get_policy
 
 
@@ -42,6 +42,16 @@ def _is_sj_conv2d(m) -> bool:
     """An nn.Conv2d the fused kernels compute (conv_unsupported_reason:
     groups, dilation, padding mode and non-square geometry are refused)."""
     return isinstance(m, nn.Conv2d) and conv_unsupported_reason(m) is None
+
+
+def _is_grouped_conv(m) -> bool:
+    """A grouped / depthwise nn.Conv2d the fused grouped kernel computes."""
+    return isinstance(m, nn.Conv2d) and grouped_conv_supported(m)
+
+
+def _is_fusable_conv(m) -> bool:
+    """The conv of a Conv -> BN -> LIF triple: dense or grouped."""
+    return _is_sj_conv2d(m) or _is_grouped_conv(m)
 
 
 def _record_unsupported_convs(model, stats) -> None:
@@ -164,9 +174,11 @@ def _rewrite_sequential(seq: nn.Sequential):
             result.replacements.append(("PartialFusionConvBNAvgPoolLIF", tuple(range(i, i + 4))))
             i += 4
             continue
-        if i + 2 < n and _is_sj_conv2d(ch[i]) and _is_sj_bn2d(ch[i + 1]) and _is_lif(ch[i + 2]):
-            out.append(PartialFusionConvBNLIF.from_sj_modules(*ch[i:i + 3]))
-            result.replacements.append(("PartialFusionConvBNLIF", (i, i + 1, i + 2)))
+        if i + 2 < n and _is_fusable_conv(ch[i]) and _is_sj_bn2d(ch[i + 1]) and _is_lif(ch[i + 2]):
+            cls = (PartialFusionGroupedConvBNLIF if _is_grouped_conv(ch[i])
+                   else PartialFusionConvBNLIF)
+            out.append(cls.from_sj_modules(*ch[i:i + 3]))
+            result.replacements.append((cls.__name__, (i, i + 1, i + 2)))
             i += 3
             continue
         if i + 1 < n and _is_sj_conv2d(ch[i]) and _is_lif(ch[i + 1]):
@@ -269,6 +281,12 @@ def _estimate_h(cin):
 
 def _build_conv_bn_lif(c, b, l, T, force_sparse, hwprof):
     cin, cout = c.in_channels, c.out_channels
+    if _is_grouped_conv(c):
+        fused = PartialFusionGroupedConvBNLIF.from_sj_modules(c, b, l)
+        return fused, {"pattern": "PartialFusionGroupedConvBNLIF",
+                       "shape": f"{cin}->{cout}, k={fused.kernel_size}, s={fused.stride}, "
+                                f"groups={fused.groups}",
+                       "backend": SpatialBackend.DENSE_KEEP, "K": T}
     k, s, _ = conv_geometry(c)
     h = _estimate_h(cin)
     row = get_policy("Conv3x3_BN_LIF", C_in=cin, C_out=cout, H=h, W=h, kernel_size=k, T=T,
@@ -381,7 +399,7 @@ def substitute_sf(sj_model, T=16, verbose=False, force_sparse=False, fuse_sew_ad
             c = getattr(pmod, f"conv{idx}", None)
             b = getattr(pmod, f"bn{idx}", None)
             l = getattr(pmod, f"sn{idx}", None)
-            if not (_is_sj_conv2d(c) and _is_sj_bn2d(b) and _is_lif(l)) or id(l) in done:
+            if not (_is_fusable_conv(c) and _is_sj_bn2d(b) and _is_lif(l)) or id(l) in done:
                 continue
             fused, entry = _build_conv_bn_lif(c, b, l, T, force_sparse, hwprof)
             setattr(pmod, f"conv{idx}", fused)
@@ -428,7 +446,7 @@ def substitute_sf(sj_model, T=16, verbose=False, force_sparse=False, fuse_sew_ad
             if c is None or b is None or not _is_lif(l) or id(l) in done:
                 continue
             full = f"{pname}.{ca}" if pname else ca
-            if _is_sj_conv2d(c) and _is_sj_bn2d(b):
+            if _is_fusable_conv(c) and _is_sj_bn2d(b):
                 fused, entry = _build_conv_bn_lif(c, b, l, T, force_sparse, hwprof)
                 setattr(pmod, ca, fused)
                 setattr(pmod, ba, nn.Identity())
@@ -460,7 +478,7 @@ def substitute_sf(sj_model, T=16, verbose=False, force_sparse=False, fuse_sew_ad
                     i += 4
                     changed = True
                     continue
-                if (i + 2 < n and _is_sj_conv2d(ch[i]) and _is_sj_bn2d(ch[i + 1])
+                if (i + 2 < n and _is_fusable_conv(ch[i]) and _is_sj_bn2d(ch[i + 1])
                         and _is_lif(ch[i + 2]) and id(ch[i + 2]) not in done):
                     fused, entry = _build_conv_bn_lif(ch[i], ch[i + 1], ch[i + 2], T,
                                                       force_sparse, hwprof)

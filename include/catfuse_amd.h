@@ -325,6 +325,29 @@ int cf_conv_stem_lif_maxpool(const float* x, const void* w_stem, const float* al
                              double v_th, double v_reset, int hard_reset, int decay_input,
                              void* stream);
 
+/* Fused grouped Conv -> BN -> LIF (groups > 1; depthwise when groups == Cin)
+ * over T steps, one streaming launch (a grouped conv is HBM-bound).  Input:
+ * exactly one of x, fp16 NHWC [T*B][H][W][Cp] (channels >= Cin zero; Cp a
+ * multiple of 8), or x32, fp32 NCHW [T*x_img_tstride + B][Cin][H][W]
+ * (x_img_tstride 0: the same image at every step).  w fp32
+ * [Cout][Cin/groups][ksize][ksize]; alpha/beta [Cout] as cf_pack_conv_weights
+ * writes them with w_packed NULL; v_in/v_out channels-last [B][Ho][Wo][Cout]
+ * (nullable); out_nhwc fp16 [T*B][Ho][Wo][cp_out] (channels >= Cout zero);
+ * nnz (nullable): the input's count block, zero -> StaticZero (no input
+ * reads); nz_out (nullable): the output's count block.  Each output sums
+ * its group's products in fp32 in the order kh, kw, input channel.
+ * Replaces catfuse/sparseflow/sparse_grouped_conv2d_kernel.py:93-364
+ * (sparse_grouped_conv2d_forward: groups as independent sparse conv
+ * sub-problems), with BN and the LIF of the layer fused. */
+int cf_conv_grouped_lif(const void* x, const float* x32, int64_t x_img_tstride, const float* w,
+                        const float* alpha, const float* beta, const float* v_in, float* v_out,
+                        void* out_nhwc, int64_t cp_out, const unsigned long long* nnz,
+                        unsigned long long* nz_out, int64_t T, int64_t B, int64_t Cin, int64_t Cp,
+                        int64_t Cout, int64_t groups, int64_t H, int64_t W, int64_t Ho,
+                        int64_t Wo, int64_t ksize, int64_t stride, int64_t pad, double tau,
+                        double v_th, double v_reset, int hard_reset, int decay_input,
+                        void* stream);
+
 /* Library error code returned beside the hipError_t values: the input of
  * cf_conv_sparse_noalloc needs more workspace than its static array holds. */
 #define CF_ERROR_NOALLOC_LIMIT 7001

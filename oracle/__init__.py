@@ -16,7 +16,9 @@ What it restates (reference = hpcyhr/CATFuse, SpikingJelly 0.0.0.0.14):
   (catfuse/sparseflow/prescan.py:32-189) in torch CPU; each pins the other,
   plus the all-zero / all-one / single-spike closed forms.
 * ``conv2d`` — torch CPU convolution in float64 (library routine), pinned on
-  tiny shapes against the double-precision brute force ``conv2d_bruteforce``.
+  tiny shapes against the double-precision brute force ``conv2d_bruteforce``;
+  grouped convolutions (groups > 1) pinned against ``conv2d_grouped_by_parts``
+  (per-group dense convolutions) and the brute force per group.
 * ``bn_fold`` / ``batch_norm`` — eval-mode BatchNorm (closed form, and
   torch's F.batch_norm, the routine SpikingJelly's BatchNorm2d calls).
 * ``route`` — StaticZero/SparseFlow/DenseKeep decision
@@ -183,12 +185,31 @@ def route(x, sparse_threshold=0.7):
 # Conv / BN
 # ---------------------------------------------------------------------------
 
-def conv2d(x, w, bias=None, stride=1, padding=0, dtype=torch.float64):
-    """torch CPU convolution in `dtype` (default float64), result as fp32."""
+def conv2d(x, w, bias=None, stride=1, padding=0, dtype=torch.float64, groups=1):
+    """torch CPU convolution in `dtype` (default float64), result as fp32;
+    groups > 1 is a grouped convolution (weight [Cout, Cin/groups, k, k])."""
     xt = torch.as_tensor(_f32(x)).to(dtype)
     wt = torch.as_tensor(_f32(w)).to(dtype)
     bt = None if bias is None else torch.as_tensor(_f32(bias)).to(dtype)
-    return F.conv2d(xt, wt, bt, stride=stride, padding=padding).to(torch.float32)
+    return F.conv2d(xt, wt, bt, stride=stride, padding=padding,
+                    groups=groups).to(torch.float32)
+
+
+def conv2d_grouped_by_parts(x, w, bias=None, stride=1, padding=0, groups=1):
+    """A grouped convolution as `groups` independent dense convolutions (the
+    reference's formulation, catfuse/sparseflow/sparse_grouped_conv2d_kernel.py:
+    251-288), each through conv2d with groups = 1, concatenated over the
+    output channels."""
+    xt = torch.as_tensor(_f32(x))
+    wt = torch.as_tensor(_f32(w))
+    cin_g = xt.shape[1] // groups
+    cout_g = wt.shape[0] // groups
+    parts = []
+    for g in range(groups):
+        b = None if bias is None else torch.as_tensor(_f32(bias))[g * cout_g:(g + 1) * cout_g]
+        parts.append(conv2d(xt[:, g * cin_g:(g + 1) * cin_g], wt[g * cout_g:(g + 1) * cout_g], b,
+                            stride, padding))
+    return torch.cat(parts, 1)
 
 
 def conv2d_bruteforce(x, w, stride=1, padding=0):
@@ -236,7 +257,7 @@ def conv_bn_lif(x_seq, conv, bn, lif, v_in=None, conv_dtype=torch.float64):
     x_seq = torch.as_tensor(_f32(x_seq))
     T, B = x_seq.shape[:2]
     z = conv2d(x_seq.flatten(0, 1), conv.weight, conv.bias, conv.stride[0], conv.padding[0],
-               dtype=conv_dtype)
+               dtype=conv_dtype, groups=getattr(conv, "groups", 1))
     if bn is not None:
         z = batch_norm(z, bn)
     z = z.reshape(T, B, *z.shape[1:])

@@ -268,8 +268,8 @@ def _seq(*mods):
 
 
 @pytest.mark.parametrize("conv_kw, reason", [
-    (dict(groups=8), "groups=8"),
     (dict(groups=8, dilation=2, padding=2), "groups=8"),
+    (dict(groups=4, padding_mode="reflect"), "groups=4"),
     (dict(dilation=2, padding=2), "dilation"),
     (dict(padding_mode="reflect"), "padding_mode"),
     (dict(kernel_size=(1, 3), padding=(0, 1)), "non-square kernel_size"),
@@ -303,24 +303,51 @@ def test_unsupported_conv_left_unfused(conv_kw, reason):
         PartialFusionConvBNLIF.from_sj_modules(conv, snn.BatchNorm2d(8), snn.LIFNode())
 
 
-def test_sew_block_with_depthwise_conv_left_unfused():
-    """A SEW BasicBlock whose conv2 is depthwise is not replaced by the
-    fused block (conv1 and the downsample may still fuse one by one)."""
+@pytest.mark.parametrize("groups, cin, cout, k, s, p", [
+    (8, 8, 8, 3, 1, 1), (8, 8, 16, 3, 2, 1), (2, 8, 16, 1, 1, 0), (4, 8, 8, 5, 1, 2)])
+def test_grouped_conv_fused(groups, cin, cout, k, s, p):
+    """Grouped and depthwise Conv -> BN -> LIF triples become the fused
+    grouped pattern (Sequential, conv{i}/bn{i}/sn{i} attributes), with the
+    weights, BN statistics and geometry of the original modules."""
     import catfuse_amd
-    from catfuse_amd.patterns import CTFSEWBasicBlock
+    from catfuse_amd.patterns import PartialFusionGroupedConvBNLIF
+    from catfuse_amd.substitute import substitute
+    conv = snn.Conv2d(cin, cout, k, s, p, groups=groups, bias=True)
+    bn = snn.BatchNorm2d(cout)
+    m = _seq(conv, bn, snn.LIFNode(v_threshold=0.5))
+    for fn in (lambda mm: catfuse_amd.optimize(mm, T=4), substitute):
+        fused, stats = fn(m)
+        f = fused[0]
+        assert isinstance(f, PartialFusionGroupedConvBNLIF)
+        assert (f.groups, f.kernel_size, f.stride, f.padding) == (groups, k, s, p)
+        assert torch.equal(f.weight, conv.weight) and torch.equal(f.conv_bias, conv.bias)
+        assert torch.equal(f.running_var, bn.running_var) and f.v_threshold == 0.5
+        assert stats["fused_lif_nodes"] == 1 and not stats.get("unsupported_structures")
+
+
+def test_sew_block_with_depthwise_conv():
+    """A SEW BasicBlock whose conv2 is depthwise is not replaced by the
+    fused block (its ADD stays the block's own): optimize fuses its convs
+    one by one, the depthwise one as the grouped pattern; the block-level
+    substitute leaves that block unfused and lists the conv."""
+    import catfuse_amd
+    from catfuse_amd.patterns import CTFSEWBasicBlock, PartialFusionGroupedConvBNLIF
+    from catfuse_amd.substitute import substitute
     net = snn.sew_resnet18(num_classes=10)
     blk = net.layer1[1]
     blk.conv2 = snn.Conv2d(64, 64, 3, 1, 1, groups=64, bias=False)
     snn.functional.set_step_mode(net, "m")
-    from catfuse_amd.substitute import substitute
-    for fn in (lambda mm: catfuse_amd.optimize(mm, T=4), substitute):
-        fused, stats = fn(net.eval())
-        assert not isinstance(fused.layer1[1], CTFSEWBasicBlock)
-        assert type(fused.layer1[1].conv2).__name__ == "Conv2d"
-        assert fused.layer1[1].conv2.groups == 64
-        assert any(s.startswith("layer1.1.conv2:") and "groups=64" in s
-                   for s in stats["unsupported_structures"])
-        assert isinstance(fused.layer1[0], CTFSEWBasicBlock)
+    fused, stats = catfuse_amd.optimize(net.eval(), T=4)
+    assert not isinstance(fused.layer1[1], CTFSEWBasicBlock)
+    assert isinstance(fused.layer1[1].conv2, PartialFusionGroupedConvBNLIF)
+    assert isinstance(fused.layer1[0], CTFSEWBasicBlock)
+    assert stats["fused_lif_nodes"] == stats["total_lif_nodes"]
+    fused, stats = substitute(net.eval())
+    assert not isinstance(fused.layer1[1], CTFSEWBasicBlock)
+    assert type(fused.layer1[1].conv2).__name__ == "Conv2d"
+    assert any(s.startswith("layer1.1.conv2:") and "groups=64" in s
+               for s in stats["unsupported_structures"])
+    assert isinstance(fused.layer1[0], CTFSEWBasicBlock)
 
 
 class IFNode(torch.nn.Module):

@@ -450,3 +450,23 @@ def test_spikformer_forward_pinned_by_eager_model():
         assert float(s.sum()) > 0, f"{k}: no spikes"
     assert len(rec) == 5 + 2 * 5
     np.testing.assert_allclose(y.numpy(), y_ref.numpy(), rtol=1e-4, atol=1e-4)
+
+
+@pytest.mark.parametrize("groups, cin, cout, k, s, p", [
+    (4, 8, 8, 3, 1, 1), (8, 8, 16, 3, 2, 1), (2, 6, 4, 1, 1, 0), (3, 6, 9, 5, 1, 2)])
+def test_grouped_conv_oracle_pins(groups, cin, cout, k, s, p):
+    """The oracle's grouped conv equals the per-group dense convolutions
+    concatenated, and each group equals the C brute force; a plausible
+    mistake (groups taken in the wrong order) fails."""
+    g = torch.Generator().manual_seed(groups * 10 + k)
+    x = (torch.rand(3, cin, 9, 7, generator=g) < 0.4).float()
+    w = torch.randn(cout, cin // groups, k, k, generator=g)
+    y = oracle.conv2d(x, w, None, s, p, groups=groups)
+    np.testing.assert_array_equal(y.numpy(),
+                                  oracle.conv2d_grouped_by_parts(x, w, None, s, p, groups).numpy())
+    cg, og = cin // groups, cout // groups
+    for gi in range(groups):
+        bf = oracle.conv2d_bruteforce(x[:, gi * cg:(gi + 1) * cg], w[gi * og:(gi + 1) * og], s, p)
+        np.testing.assert_allclose(y[:, gi * og:(gi + 1) * og].numpy(), bf, rtol=1e-6, atol=1e-6)
+    w_swapped = torch.cat([w[og:], w[:og]]) if groups > 1 else w
+    assert not torch.equal(oracle.conv2d(x, w_swapped, None, s, p, groups=groups), y)
