@@ -541,8 +541,8 @@ def _base_result(args, res, stats, workload):
 # ---------------------------------------------------------------------------
 
 XO_RATES = (0.0, 0.001, 0.01, 0.05, 0.1, 0.2, 0.3, 0.5)
-XO_PATTERNS = ("iid", "block", "spatial")
-XO_ROUTES = ("SparseFlow", "StreamFuse", "DenseKeep", "auto")
+XO_PATTERNS = ("iid", "block", "spatial", "chgroup", "region")
+XO_ROUTES = ("SparseFlow", "SparseFlow-linear", "SF+EGD", "StreamFuse", "DenseKeep", "auto")
 
 
 def xo_input(rate, pattern, shape=(4, 32, 256, 14, 14), seed=0, block=8, p_zero_block=0.7):
@@ -550,7 +550,11 @@ def xo_input(rate, pattern, shape=(4, 32, 256, 14, 14), seed=0, block=8, p_zero_
     iid Bernoulli(rate); block: per (t, b, c) and 8x8 block, zero with
     probability 0.7, else Bernoulli(rate) (the granularity of the
     reference's tests/test_70_oracle_gap.py:112-124); spatial: per (t, b)
-    and 8x8 block, zero in every channel with probability 0.7."""
+    and 8x8 block, zero in every channel with probability 0.7; chgroup:
+    per image and 16-channel group, silent at every step and pixel with
+    probability 0.7 (dead channel groups); region: per image, activity only
+    inside one random window of half the height and width (a quarter of the
+    area), at every step."""
     import torch
     g = torch.Generator().manual_seed(seed)
     T, B, C, H, W = shape
@@ -560,6 +564,18 @@ def xo_input(rate, pattern, shape=(4, 32, 256, 14, 14), seed=0, block=8, p_zero_
         kc = C if pattern == "block" else 1
         keep = (torch.rand((T, B, kc, gh, gw), generator=g) >= p_zero_block).float()
         keep = keep.repeat_interleave(block, 3).repeat_interleave(block, 4)[..., :H, :W]
+        x = x * keep
+    elif pattern == "chgroup":
+        ng = -(-C // 16)
+        keep = (torch.rand((1, B, ng, 1, 1), generator=g) >= p_zero_block).float()
+        x = x * keep.repeat_interleave(16, 2)[:, :, :C]
+    elif pattern == "region":
+        keep = torch.zeros((1, B, 1, H, W))
+        hh, hw = max(1, H // 2), max(1, W // 2)
+        for b in range(B):
+            r0 = int(torch.randint(0, H - hh + 1, (1,), generator=g))
+            c0 = int(torch.randint(0, W - hw + 1, (1,), generator=g))
+            keep[0, b, 0, r0:r0 + hh, c0:c0 + hw] = 1.0
         x = x * keep
     elif pattern != "iid":
         raise ValueError(f"unknown pattern {pattern!r}")
@@ -638,8 +654,11 @@ def xo_sweep(device, rates=XO_RATES, patterns=XO_PATTERNS, shape=(4, 32, 256, 14
     from catfuse_amd.state import StateBuffer
     T, B, C, H, W = shape
     spec, params = _xo_layer(C, C, device, seed)
-    impls = {"SparseFlow": SparseFlow(sparsity_threshold=-1.0), "StreamFuse": StreamFuse(),
-             "DenseKeep": DenseKeep(), "auto": SparseFlow()}
+    impls = {"SparseFlow": SparseFlow(sparsity_threshold=-1.0, egd=False),
+             "SparseFlow-linear": SparseFlow(sparsity_threshold=-1.0, compact_tiles=False,
+                                             egd=False),
+             "SF+EGD": SparseFlow(sparsity_threshold=-1.0),
+             "StreamFuse": StreamFuse(), "DenseKeep": DenseKeep(), "auto": SparseFlow()}
     rows = []
     with torch.no_grad():
         for pattern in patterns:
@@ -656,6 +675,8 @@ def xo_sweep(device, rates=XO_RATES, patterns=XO_PATTERNS, shape=(4, 32, 256, 14
                     def call(impl=impl):
                         return impl.forward(x, spec, params, StateBuffer())
                     y = call()
+                    if name == "SparseFlow":
+                        row.update(xo_score(impl, spec, T, H, W))
                     if ref is None:
                         ref = y.clone()
                     elif not torch.equal(y, ref):
@@ -666,9 +687,78 @@ def xo_sweep(device, rates=XO_RATES, patterns=XO_PATTERNS, shape=(4, 32, 256, 14
     return rows
 
 
+_POPCOUNT8 = None
+
+
+def xo_score(impl, spec, T, H, W):
+    """Dispatch score of the SparseFlow launch just run, as cf_compact_tiles
+    computes it (the reference's catfuse/sparseflow/dispatch.py:868-935 over
+    the tile's time steps): R = 1 - AGR of the tile masks OR-ed over the
+    steps, I = dense MACs per image / tiles per image, S = R * I."""
+    import torch
+    global _POPCOUNT8
+    _tc, ag = impl.last_tiles()
+    if _POPCOUNT8 is None or _POPCOUNT8.device != ag.device:
+        _POPCOUNT8 = torch.tensor([bin(i).count("1") for i in range(256)], dtype=torch.int64,
+                                  device=ag.device)
+    geo = impl.geometry(spec, H, W)
+    G = -(-spec.in_channels // geo["group_size"])
+    Ho, Wo = spec.output_hw(H, W)
+    GH, GW = -(-Ho // geo["block_h"]), -(-Wo // geo["block_w"])
+    steps = ag.view(T, -1)
+    m = steps[0].clone()
+    for t in range(1, T):
+        m |= steps[t]
+    pop = int(_POPCOUNT8[m.contiguous().view(torch.uint8).long()].sum())
+    R = 1.0 - pop / (m.numel() * G)
+    I = Ho * Wo * spec.out_channels * spec.in_channels * spec.kernel_size ** 2 / (GH * GW)
+    return {"R": R, "I": I, "S": R * I}
+
+
+def xo_egd_fit(rows):
+    """The dispatch-score threshold tau that best separates the measured
+    rows (nonzero inputs) where forced SparseFlow beat the best dense route
+    from those where it did not: tau minimising the misclassified rows
+    (SparseFlow iff S > tau, R >= r_min), with the misclassification count;
+    tau is the midpoint between the scores on either side of it."""
+    pts = sorted((r["S"], r["SparseFlow"] < min(r["StreamFuse"], r["DenseKeep"]))
+                 for r in rows if r["density"] > 0.0 and "S" in r)
+    if not pts:
+        return None, 0
+    best = (len(pts) + 1, None)
+    cands = [pts[0][0] - 1.0] + [(a[0] + b[0]) / 2 for a, b in zip(pts, pts[1:])] + [pts[-1][0]]
+    for tau in cands:
+        err = sum((s > tau) != win for s, win in pts)
+        if err < best[0]:
+            best = (err, tau)
+    return best[1], best[0]
+
+
+def xo_rmin_fit(rows):
+    """The silent-group fraction R_min that best separates the measured rows
+    (nonzero inputs) where forced SparseFlow beat the best dense route from
+    those where it did not (SparseFlow iff R >= R_min): the midpoint of the
+    widest interval of thresholds with the fewest misclassified rows, and
+    that count."""
+    pts = sorted((r["R"], r["SparseFlow"] < min(r["StreamFuse"], r["DenseKeep"]))
+                 for r in rows if r["density"] > 0.0 and "R" in r)
+    if not pts:
+        return None, 0
+    edges = [0.0] + sorted({p[0] for p in pts}) + [1.0 + 1e-9]
+    best = None
+    for lo, hi in zip(edges, edges[1:]):
+        thr = (lo + hi) / 2 if lo < hi else lo
+        err = sum((R >= thr) != win for R, win in pts)
+        key = (err, -(hi - lo))
+        if best is None or key < best[0]:
+            best = (key, thr)
+    return best[1], best[0][0]
+
+
 def xo_crossover(rows):
-    """Per pattern, the lowest input sparsity at which forced SparseFlow is
-    faster than the best dense route (None: at no measured nonzero rate)."""
+    """Per pattern, the lowest input sparsity at which forced SparseFlow
+    (compacted tile order) is faster than the best dense route (None: at no
+    measured nonzero rate)."""
     out = {}
     for pattern in sorted({r["pattern"] for r in rows}):
         wins = [1.0 - r["density"] for r in rows
@@ -679,10 +769,12 @@ def xo_crossover(rows):
 
 
 def xo_table(rows):
-    lines = ["| pattern | rate | density | " + " | ".join(f"{n} (us)" for n in XO_ROUTES) + " |",
-             "|---|---|---|" + "---|" * len(XO_ROUTES)]
+    lines = ["| pattern | rate | density | R | S | "
+             + " | ".join(f"{n} (us)" for n in XO_ROUTES) + " |",
+             "|---|---|---|---|---|" + "---|" * len(XO_ROUTES)]
     for r in rows:
         lines.append(f"| {r['pattern']} | {r['rate']:g} | {r['density']:.4f} | "
+                     f"{r.get('R', float('nan')):.3f} | {r.get('S', float('nan')):.3g} | "
                      + " | ".join(f"{r[n]:.1f}" for n in XO_ROUTES) + " |")
     return "\n".join(lines)
 
@@ -694,6 +786,14 @@ def sf_crossover_main(args):
     rows = xo_sweep(dev, shape=shape, plain=args.xo_plain)
     print(xo_table(rows))
     print("crossover (lowest input sparsity where SparseFlow wins):", xo_crossover(rows))
+    n = sum(r["density"] > 0 for r in rows)
+    tau, err = xo_egd_fit(rows)
+    print(f"dispatch score fit: tau = {tau:.4g} ({err} misclassified of {n})"
+          if tau is not None else "no score")
+    r_min, err = xo_rmin_fit(rows)
+    print(f"silent-group fraction fit: R_min = {r_min:.3f} ({err} misclassified of {n})"
+          if r_min is not None else "no score")
+    print("rows:", json.dumps(rows))
 
 
 # ---------------------------------------------------------------------------

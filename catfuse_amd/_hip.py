@@ -40,10 +40,13 @@ _SIGNATURES = {
     "cf_zero_counter": [_P, _P],
     "cf_prescan_tiles": [_P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P],
     "cf_pack_conv_weights": [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P],
-    "cf_conv_mfma": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, c_int, _P, _P, _P, _I, c_double,
+    "cf_compact_tiles": [_P, _I, _I, _I, c_double, c_double, c_double, _P, _P],
+    "cf_conv_mfma": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, c_int, _P, _P, _P, _P, _I,
+                     c_double,
                      _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                      c_int, c_double, c_double, c_double, c_int, c_int, _P],
-    "cf_conv_halo": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, c_int, _P, _P, _P, _I, c_double,
+    "cf_conv_halo": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, c_int, _P, _P, _P, _P, _I,
+                     c_double,
                      _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                      c_int, c_double, c_double, c_double, c_int, c_int, _P],
     "cf_pack_stem_weights": [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P],

@@ -142,6 +142,8 @@ struct HaloArgs {
   int cp_id;
   int identity_mode;
   const int32_t* ag_mask;   // [T][B*GH*GW]
+  const int32_t* order;     // [1 + B*GH*GW]: active tile count, then every tile, the
+                            // active ones first (cf_compact_tiles), or null
   const unsigned long long* nnz;  // count block of the input (cf_count_read), or null
   unsigned long long* nz_out;     // count block of the output: workgroups that wrote a
                                   // nonzero value (cf_count_publish), or null
@@ -177,6 +179,9 @@ constexpr int halo_min_blocks() {
 // output channel real (Cout a multiple of 64): no per-element branches.
 // ONEB: T fits one time block (T <= TB): the block loop runs once, so the
 // K-loop state is dead in the epilogue (fewer live registers).
+// HS: the SparseFlow route skips the MFMAs of a silent 16-channel chunk half
+// (prescan groups narrower than a chunk); off, the K loop has no per-half
+// branches (the instantiations a dense-only launch uses).
 // One halo buffer (halves) of a configuration: whole 64-unit blocks of the
 // staged halo of a time block (16-byte units of TB steps x RH x RW pixels).
 template <int TH, int TW, int S, int K>
@@ -189,7 +194,7 @@ constexpr int halo_buf_halves() {
 // function, so that one grid can run two convs of the same input side by
 // side (conv_halo_pair_kernel).  halo: 2 * halo_buf_halves() halves of LDS;
 // bn_s: the tile's BN coefficients; any_sh: the workgroup's vote words.
-template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB>
+template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB, bool HS>
 __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const int nL,
                                           _Float16* __restrict__ halo, float (*bn_s)[64],
                                           unsigned* any_sh) {
@@ -226,18 +231,39 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   // adjacent.  The blocks of a tile (which stage the same input halo) and
   // neighbouring tiles (whose halos overlap) then run together on one XCD and
   // share its L2.
-  const int nwork = a.B * a.GH * a.GW * (a.Coutp / BM);
-  const int xcd = L & 7, j = L >> 3;
-  const int work = xcd * (nwork >> 3) + min(xcd, nwork & 7) + j;
+  //
+  // On the SparseFlow route with a compacted tile order, the XCD's range
+  // holds its equal share of the active work items (tiles active at some
+  // step, in the order's sequence) first, then its share of the inactive
+  // ones (epilogue only): the long workgroups start first on every XCD.
+  // A tile order whose count is negative (cf_compact_tiles' dispatch score
+  // rejected SparseFlow) turns the sparse route into the dense one.
+  int route = halo_route(a.nnz, a.numel, a.sparse_thr);
+  if (route == CF_ROUTE_SPARSE && a.order != nullptr && a.order[0] < 0) route = CF_ROUTE_DENSE;
   const int ncb = a.Coutp / BM;
-  const int tile = work / ncb;
+  const int ntiles = a.B * a.GH * a.GW;
+  const int nwork = ntiles * ncb;
+  const int xcd = L & 7, j = L >> 3;
+  const int xstart = xcd * (nwork >> 3) + min(xcd, nwork & 7);   // the XCD's first work item
+  int tile, cb;
+  if (a.order != nullptr && route == CF_ROUTE_SPARSE) {
+    const int na = min(a.order[0], ntiles) * ncb;                    // active work items
+    const int ax = (na >> 3) + (xcd < (na & 7) ? 1 : 0);             // the XCD's share of them
+    const int sa = xcd * (na >> 3) + min(xcd, na & 7);
+    const int pos = j < ax ? sa + j : na + (xstart - sa) + (j - ax);
+    tile = min(max(a.order[1 + pos / ncb], 0), ntiles - 1);
+    cb = pos % ncb;
+  } else {
+    const int work = xstart + j;
+    tile = work / ncb;
+    cb = work - tile * ncb;
+  }
   const int gw = tile % a.GW, gh = (tile / a.GW) % a.GH, b = tile / (a.GW * a.GH);
   const int oh0 = gh * TH, ow0 = gw * TW;
   const int ih0 = oh0 * S - a.pad, iw0 = ow0 * S - a.pad;
-  const int cout0 = (work - tile * ncb) * BM;
+  const int cout0 = cb * BM;
   const int HoWo = a.Ho * a.Wo;
   const int nch = a.Cp / KC;
-  const int ntiles = a.B * a.GH * a.GW;
   if (tid < BM) {  // alpha/beta hold Coutp entries
     bn_s[0][tid] = a.alpha[cout0 + tid];
     bn_s[1][tid] = a.beta[cout0 + tid];
@@ -274,7 +300,6 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   const int co_lane = cout0 + wm * WM + 4 * hi;
   const bool full_c = cout0 + BM <= a.Cout;  // every channel of the tile is real
 
-  const int route = halo_route(a.nnz, a.numel, a.sparse_thr);
   uint32_t anyw = 0u;  // OR of the bits of the output values this thread stores
   // The output's count block: workgroups that stored a nonzero value.
   auto publish_count = [&]() {
@@ -365,19 +390,39 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     if (route == CF_ROUTE_DENSE) return 0xffffffffu;
     return (uint32_t)a.ag_mask[(size_t)tt * ntiles + tile];
   };
-  // Group bits of chunk ch: groups g0 .. g1 its 32 channels fall in.
-  auto chunk_bits = [&](int ch) -> uint32_t {
+  // Group bits of channels c0 .. c0 + n - 1: groups g0 .. g1 they fall in.
+  auto range_bits = [&](int c0, int n) -> uint32_t {
     int g0, g1;
     if (a.gs_shift >= 0) {
-      g0 = (ch * KC) >> a.gs_shift;
-      g1 = (ch * KC + KC - 1) >> a.gs_shift;
+      g0 = c0 >> a.gs_shift;
+      g1 = (c0 + n - 1) >> a.gs_shift;
     } else {
-      g0 = (ch * KC) / a.gs;
-      g1 = (ch * KC + KC - 1) / a.gs;
+      g0 = c0 / a.gs;
+      g1 = (c0 + n - 1) / a.gs;
     }
     if (g0 > 31) return 0u;
     const uint32_t hi = g1 >= 31 ? 0xffffffffu : ((2u << g1) - 1u);
     return hi & ~((1u << g0) - 1u);
+  };
+  // Group bits of chunk ch (its 32 channels).
+  auto chunk_bits = [&](int ch) -> uint32_t { return range_bits(ch * KC, KC); };
+  // With groups narrower than a chunk, the 16-channel halves of a chunk can
+  // be silent on their own: bit ks * TB + t of half_act is set when half ks
+  // of chunk ch is active at step tbs + t.  The MFMAs of a half that is
+  // silent at every step of a batch of B-fragment reads are skipped: its
+  // products are exact zeros, so the accumulators' bits are those of the
+  // dense evaluation.
+  const bool half_skip = HS && route == CF_ROUTE_SPARSE && a.gs < KC;
+  auto half_act = [&](int tbs, int ch) -> uint32_t {
+    const uint32_t g0 = range_bits(ch * KC, KC / 2), g1 = range_bits(ch * KC + KC / 2, KC / 2);
+    uint32_t m = 0u;
+#pragma unroll
+    for (int t = 0; t < TB; ++t) {
+      const uint32_t sm = step_mask(tbs + t);
+      m |= ((sm & g0) != 0u ? 1u : 0u) << t;
+      m |= ((sm & g1) != 0u ? 1u : 0u) << (TB + t);
+    }
+    return m;
   };
   // Steps (bit t) of the block starting at tbs (< T) that chunk ch is
   // active at: every step on the dense route, none on the zero route.
@@ -529,8 +574,11 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   // per-step branches: a step the chunk is inactive at was staged as zeros,
   // and adding the exact zero products leaves the accumulator's bits
   // unchanged (it starts at +0 and is never -0), so this equals skipping it.
-  auto run_taps = [&](const _Float16* __restrict__ hb, _Float16* __restrict__ hb_next, int ch,
-                      int ntb, int nc, uint32_t nact, int wblk) {
+  // SKIP: skip the MFMAs of a silent chunk half (hm: half_act of the step).
+  auto run_taps = [&](auto skip_c, const _Float16* __restrict__ hb,
+                      _Float16* __restrict__ hb_next, int ch, int ntb, int nc, uint32_t nact,
+                      int wblk, uint32_t hm) {
+    constexpr bool SKIP = decltype(skip_c)::value;
     const int stb = ntb == wblk ? ntb : a.T;  // a.T: stage zeros
 #pragma unroll
     for (int tap = 0; tap < KK; ++tap) {
@@ -565,7 +613,10 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
         // so none waits for the previous one's result; each accumulator
         // still sums ks 0 hi, ks 0 lo, ks 1 hi, ks 1 lo in that order.
 #pragma unroll
-        for (int ks = 0; ks < 2; ++ks)
+        for (int ks = 0; ks < 2; ++ks) {
+          if constexpr (SKIP) {
+            if (((hm >> (ks * TB + th)) & ((1u << TBR) - 1u)) == 0u) continue;
+          }
 #pragma unroll
           for (int limb = 0; limb < 2; ++limb)
 #pragma unroll
@@ -574,6 +625,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
               for (int nt = 0; nt < NT; ++nt)
                 acc[th + tr][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
                     limb ? al[cur][ks] : ah[cur][ks], bb[tr][ks][nt], acc[th + tr][nt], 0, 0, 0);
+        }
         // Later reads stay below these MFMAs (register budget).
         __builtin_amdgcn_sched_barrier(0);
       }
@@ -620,7 +672,8 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
       // the other buffer, which the taps below refill.
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      run_taps(halo + buf * HB, halo + (buf ^ 1) * HB, s_ch, ntb, nc, nact, tb0);
+      run_taps(std::integral_constant<bool, HS>{}, halo + buf * HB, halo + (buf ^ 1) * HB, s_ch,
+               ntb, nc, nact, tb0, half_skip ? half_act(s_tb, s_ch) : 0xffffffffu);
       buf ^= 1;
       s_tb = ntb;
       s_ch = nc;
@@ -844,14 +897,14 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   publish_count();
 }
 
-template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB>
+template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB, bool HS = false>
 __global__ __launch_bounds__(256, (halo_min_blocks<TH, TW>()))
 void conv_halo_kernel(HaloArgs a) {
   __shared__ __attribute__((aligned(16))) _Float16 halo[2 * halo_buf_halves<TH, TW, S, K>()];
   __shared__ __attribute__((aligned(16))) float bn_s[2][64];  // alpha, beta of the tile
   __shared__ unsigned any_sh[4];  // per-wave votes of the output count
-  halo_body<TH, TW, S, K, EPI, LM, LEAN, ONEB>(a, (int)blockIdx.x, (int)gridDim.x, halo, bn_s,
-                                               any_sh);
+  halo_body<TH, TW, S, K, EPI, LM, LEAN, ONEB, HS>(a, (int)blockIdx.x, (int)gridDim.x, halo,
+                                                   bn_s, any_sh);
 }
 
 template <int TH, int TW, int S, int K = 3>
@@ -870,9 +923,18 @@ hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
                        block, 0, st, a);
   } else {
     const int lm = cf_lif_mode(a.lif);
-#define CF_HALO_LEAN(LMV, OB)                                                                   \
-  hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LMV, true, OB>), grid, block, 0, st, \
-                     a)
+    // SparseFlow-capable with groups narrower than a chunk: the K loop that
+    // skips silent chunk halves
+    const bool hs = a.ag_mask != nullptr && a.gs < KC;
+#define CF_HALO_LEAN(LMV, OB)                                                                     \
+  do {                                                                                            \
+    if (hs)                                                                                       \
+      hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LMV, true, OB, true>), grid,    \
+                         block, 0, st, a);                                                        \
+    else                                                                                          \
+      hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LMV, true, OB, false>), grid,   \
+                         block, 0, st, a);                                                        \
+  } while (0)
     if (lm == LM_HARD0_DECAY_P2) {
       if (oneb) CF_HALO_LEAN(LM_HARD0_DECAY_P2, true);
       else CF_HALO_LEAN(LM_HARD0_DECAY_P2, false);
@@ -896,7 +958,7 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
                         const float* beta, const float* v_in, float* v_out, float* out,
                         void* out_nhwc, int64_t cp_out,
                         const float* identity, const void* identity_nhwc, int64_t cp_id,
-                        int identity_mode, const int32_t* ag_mask,
+                        int identity_mode, const int32_t* ag_mask, const int32_t* tile_order,
                         const unsigned long long* nnz, unsigned long long* nz_out,
                         int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
@@ -923,6 +985,7 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
     return (int)hipErrorInvalidValue;
   if (ag_mask && (group_size <= 0 || (Cp + group_size - 1) / group_size > 32))
     return (int)hipErrorInvalidValue;
+  if (tile_order && !ag_mask) return (int)hipErrorInvalidValue;
   // 32-bit element indices of the outputs, and 32-bit offsets of a tile's
   // input within one time block (4 steps)
   if (T * B * Cout * Ho * Wo > INT32_MAX || T * B * H * W > ((int64_t)1 << 40) ||
@@ -938,7 +1001,7 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
   a.v_in = v_in; a.v_out = v_out; a.out = out; a.identity = identity;
   a.identity_nhwc = (const _Float16*)identity_nhwc; a.cp_id = (int)cp_id;
   a.out_nhwc = (_Float16*)out_nhwc; a.cp_out = (int)cp_out;
-  a.identity_mode = identity_mode; a.ag_mask = ag_mask;
+  a.identity_mode = identity_mode; a.ag_mask = ag_mask; a.order = tile_order;
   // Without masks the SparseFlow route cannot be taken: pass the count only
   // when masks exist (StaticZero is still detected through nnz == 0 below).
   a.nnz = nnz; a.nz_out = nz_out; a.numel = numel;

@@ -432,7 +432,7 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
                         const float* beta, const float* v_in, float* v_out, float* out,
                         void* out_nhwc, int64_t cp_out,
                         const float* identity, const void* identity_nhwc, int64_t cp_id,
-                        int identity_mode, const int32_t* ag_mask,
+                        int identity_mode, const int32_t* ag_mask, const int32_t* tile_order,
                         const unsigned long long* nnz, unsigned long long* nz_out,
                         int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
@@ -445,7 +445,7 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
                         const float* beta, const float* v_in, float* v_out, float* out,
                         void* out_nhwc, int64_t cp_out,
                         const float* identity, const void* identity_nhwc, int64_t cp_id,
-                        int identity_mode, const int32_t* ag_mask,
+                        int identity_mode, const int32_t* ag_mask, const int32_t* tile_order,
                         const unsigned long long* nnz, unsigned long long* nz_out,
                         int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
@@ -481,7 +481,8 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
     const int64_t th = 8, tw = rect ? tile_w : 8;
     return cf_conv_halo(x, w_packed, alpha, beta, v_in, v_out, out, out_nhwc, cp_out, identity,
                         identity_nhwc, cp_id, identity_mode,
-                        rect ? ag_mask : nullptr, nnz, nz_out, numel, sparse_threshold, T, B, Cp, Cout,
+                        rect ? ag_mask : nullptr, rect ? tile_order : nullptr, nnz, nz_out,
+                        numel, sparse_threshold, T, B, Cp, Cout,
                         Coutp, H, W, Ho, Wo, KH, stride, pad, th, tw, rect ? group_size : 0,
                         epilogue, tau, v_th, v_reset, hard_reset, decay_input, stream);
   }
@@ -491,6 +492,7 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
       return (int)hipErrorInvalidValue;
     if (nnz && !ag_mask) return (int)hipErrorInvalidValue;
   }
+  if (tile_order && !(rect && ag_mask)) return (int)hipErrorInvalidValue;
   // 32-bit index ranges used inside the kernel
   if (B * Ho * Wo > INT32_MAX || T * B > INT32_MAX || (T * x_img_tstride + B) * H * W > ((int64_t)1 << 40))
     return (int)hipErrorInvalidValue;

@@ -2,10 +2,11 @@
 // that cannot allocate device memory (code under HIP graph capture, tight
 // serving loops, harnesses that forbid hipMalloc).
 //
-// cf_conv_mfma's SparseFlow route needs three device buffers beside its
+// cf_conv_mfma's SparseFlow route needs four device buffers beside its
 // inputs and outputs: the input's per-pixel channel-group activity bits
-// (cf_scan_nhwc), its nonzero-count block, and the prescan tile masks
-// (cf_prescan_tiles).  Here they live in one file-scope device array,
+// (cf_scan_nhwc), its nonzero-count block, the prescan tile masks
+// (cf_prescan_tiles) and the compacted tile order (cf_compact_tiles).  Here
+// they live in one file-scope device array,
 // `scratch`, of CF_NOALLOC_SCRATCH_BYTES per GPU: the runtime places a copy
 // of it on every device the library runs on, and it stays until the process
 // ends.  Its device address is looked up once per device with
@@ -13,8 +14,8 @@
 // array's name, which on the host is a stand-in symbol).  Every call on one
 // GPU shares that GPU's array: calls that overlap on one GPU (streams not
 // ordered against each other) race.  The count block is cleared by a kernel
-// at the start of every call; the activity bits and tile masks are fully
-// rewritten by every call before they are read.
+// at the start of every call; the activity bits, tile masks and tile order
+// are fully rewritten by every call before they are read.
 #include <mutex>
 
 // cf_common.h first: the C-ABI header's constant macros must not rename its
@@ -27,8 +28,10 @@ namespace {
 constexpr size_t NA_COUNT_BYTES = 4096;   // count block (CF_COUNT_BLOCK_WORDS u64) + pad
 constexpr size_t NA_ACT_BYTES = (size_t)CF_NOALLOC_MAX_PIXELS * 4;
 constexpr size_t NA_TILE_BYTES = (size_t)CF_NOALLOC_MAX_TILES * 4;
+constexpr size_t NA_ORDER_BYTES = (size_t)CF_NOALLOC_MAX_TILES * 4 + 256;   // count + tiles
 static_assert(CF_COUNT_BLOCK_WORDS * 8 <= NA_COUNT_BYTES, "count block exceeds its slot");
-static_assert(NA_COUNT_BYTES + NA_ACT_BYTES + 2 * NA_TILE_BYTES == CF_NOALLOC_SCRATCH_BYTES,
+static_assert(NA_COUNT_BYTES + NA_ACT_BYTES + 2 * NA_TILE_BYTES + NA_ORDER_BYTES ==
+                  CF_NOALLOC_SCRATCH_BYTES,
               "scratch layout does not add up to CF_NOALLOC_SCRATCH_BYTES");
 
 __device__ __align__(256) unsigned char scratch[CF_NOALLOC_SCRATCH_BYTES];
@@ -86,6 +89,7 @@ CF_API int cf_conv_sparse_noalloc(
   uint32_t* act = (uint32_t*)(s + NA_COUNT_BYTES);
   int32_t* ag = (int32_t*)(s + NA_COUNT_BYTES + NA_ACT_BYTES);
   int32_t* tc = (int32_t*)(s + NA_COUNT_BYTES + NA_ACT_BYTES + NA_TILE_BYTES);
+  int32_t* order = (int32_t*)(s + NA_COUNT_BYTES + NA_ACT_BYTES + 2 * NA_TILE_BYTES);
   hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(na_clear_block, dim3(1), dim3(256), 0, st, blk);
   rc = (int)hipGetLastError();
@@ -96,8 +100,12 @@ CF_API int cf_conv_sparse_noalloc(
   rc = cf_prescan_tiles(act, NB, H, W, Ho, Wo, ksize, stride, pad, tile_h, tile_w, groups, ag,
                         tc, stream);
   if (rc) return rc;
+  // tile masks are per (step, image, tile); the conv's tiles are (image, tile)
+  rc = cf_compact_tiles(ag, T, B * GH * GW, groups, 0.0, -1.0, 0.0, order, stream);
+  if (rc) return rc;
   return cf_conv_mfma(x, w_packed, alpha, beta, v_in, v_out, out, out_nhwc, cp_out, identity,
-                      identity_nhwc, cp_id, identity_mode, ag, blk, nz_out, NB * Cin * H * W,
+                      identity_nhwc, cp_id, identity_mode, ag, order, blk, nz_out,
+                      NB * Cin * H * W,
                       sparse_threshold, T, B, Cp, Cout, Coutp, H, W, Ho, Wo, ksize, ksize,
                       stride, pad, B, tile_h, tile_w, group_size, epilogue, tau, v_th, v_reset,
                       hard_reset, decay_input, stream);

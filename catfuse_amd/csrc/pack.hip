@@ -96,37 +96,59 @@ __global__ __launch_bounds__(256) void pack_kernel(
 // channels of a chunk share one group, and the pixel's bits are OR-reduced
 // over its 16 lanes.  Grid-stride over pixels; the count is published with
 // one atomic per block.
+// Activity bits and nonzero count of an fp16 NHWC copy.  LP lanes share a
+// pixel (LP = Cp/8 capped at 16, a power of two: every lane of a wave busy),
+// each reading 16-byte chunks of 8 channels; a thread takes two pixels per
+// iteration (two loads in flight).  The tests work on the halves' bits: a
+// half is nonzero iff its magnitude bits are (so -0 counts as zero, as
+// v != 0.0f), and |v| > thr iff its magnitude bits exceed thr_mag (the bits
+// of the largest fp16 magnitude <= thr; -1 when thr < 0) and are not a NaN
+// (<= 0x7c00), the order of non-negative fp16 values being that of their
+// bits.  Each chunk lies in one channel group (gs is a multiple of 8).
+template <int LP>
 __global__ __launch_bounds__(256) void scan_nhwc_kernel(
     const _Float16* __restrict__ xp, int64_t npix, int Cp, int C, uint32_t* __restrict__ act,
-    int gs, float thr, unsigned long long* __restrict__ nnz) {
-  typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+    int gs, int thr_mag, unsigned long long* __restrict__ nnz) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  constexpr int PPB = 256 / LP;   // pixels of a block per half-iteration
   __shared__ unsigned int cnt_sh;
-  const int tid = threadIdx.x, sub = tid & 15;
+  const int tid = threadIdx.x, sub = tid % LP;
   if (tid == 0) cnt_sh = 0;
   __syncthreads();
   unsigned int cnt = 0;
   const int nc8 = Cp / 8;
-  for (int64_t p0 = (int64_t)blockIdx.x * 16; p0 < npix; p0 += (int64_t)gridDim.x * 16) {
-    const int64_t p = p0 + (tid >> 4);
-    uint32_t bits = 0;
-    if (p < npix) {
-      const _Float16* src = xp + p * Cp;
-      for (int c8 = sub; c8 < nc8; c8 += 16) {
-        const h8 hv = *reinterpret_cast<const h8*>(src + c8 * 8);
+  for (int64_t p0 = (int64_t)blockIdx.x * 2 * PPB; p0 < npix; p0 += (int64_t)gridDim.x * 2 * PPB) {
+    int64_t pp[2];
+    uint32_t bits[2] = {0u, 0u};
+#pragma unroll
+    for (int u = 0; u < 2; ++u) pp[u] = p0 + u * PPB + tid / LP;
+    for (int c8 = sub; c8 < nc8; c8 += LP) {
+      u32x4 v[2];
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        v[u] = pp[u] < npix ? *reinterpret_cast<const u32x4*>(xp + pp[u] * Cp + c8 * 8)
+                            : u32x4{0u, 0u, 0u, 0u};
+      const int nreal = C - c8 * 8;   // real channels in the chunk (may be <= 0 or >= 8)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
         bool any = false;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float v = (float)hv[j];
-          cnt += (v != 0.0f) ? 1u : 0u;
-          any |= fabsf(v) > thr && c8 * 8 + j < C;
+        for (int k = 0; k < 4; ++k) {
+          const int lo = (int)(v[u][k] & 0x7fffu), hi = (int)((v[u][k] >> 16) & 0x7fffu);
+          cnt += (lo != 0 ? 1u : 0u) + (hi != 0 ? 1u : 0u);
+          any |= (lo > thr_mag && lo <= 0x7c00 && 2 * k < nreal) ||
+                 (hi > thr_mag && hi <= 0x7c00 && 2 * k + 1 < nreal);
         }
-        if (any) bits |= 1u << (unsigned)((c8 * 8) / gs);
+        if (any) bits[u] |= 1u << (unsigned)((c8 * 8) / gs);
       }
     }
-    // the 16 lanes of a pixel share p, so this reduction stays in bounds
+    // the LP lanes of a pixel share it, so this reduction stays in bounds
 #pragma unroll
-    for (int off = 8; off > 0; off >>= 1) bits |= __shfl_xor(bits, off, 16);
-    if (act && p < npix && sub == 0) act[p] = bits;
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int off = LP / 2; off > 0; off >>= 1) bits[u] |= __shfl_xor(bits[u], off, LP);
+      if (act && pp[u] < npix && sub == 0) act[pp[u]] = bits[u];
+    }
   }
   if (nnz) {
     for (int off = 32; off > 0; off >>= 1) cnt += __shfl_xor(cnt, off, 64);
@@ -339,12 +361,45 @@ CF_API int cf_scan_nhwc(const void* xp, int64_t NB, int64_t H, int64_t W, int64_
   if (act && (group_size <= 0 || group_size % 8 != 0 || (C + group_size - 1) / group_size > 32))
     return (int)hipErrorInvalidValue;
   if (group_size <= 0) group_size = 32;
+  if (threshold != threshold) return (int)hipErrorInvalidValue;   // NaN
   const int64_t npix = NB * H * W;
   if (npix == 0) return 0;
-  const int64_t nblk = (npix + 15) / 16;
-  hipLaunchKernelGGL(scan_nhwc_kernel, dim3((unsigned)(nblk < 512 ? nblk : 512)), dim3(256), 0,
-                     (hipStream_t)stream, (const _Float16*)xp, npix, (int)Cp, (int)C, act,
-                     group_size, threshold, nnz);
+  // bits of the largest fp16 magnitude <= threshold (-1: every value exceeds it)
+  int thr_mag = -1;
+  if (threshold > 65504.0f) {
+    thr_mag = 0x7c00;   // only a larger infinity would exceed it: none
+    if (threshold < __builtin_huge_valf()) thr_mag = 0x7bff;
+  } else if (threshold == 65504.0f) {
+    thr_mag = 0x7bff;
+  } else if (threshold >= 0.0f) {
+    const _Float16 h = (_Float16)threshold;
+    unsigned short b;
+    __builtin_memcpy(&b, &h, 2);
+    thr_mag = (int)(b & 0x7fffu);
+    if ((float)h > threshold) --thr_mag;   // rounded up: the next smaller magnitude
+  }
+  const int nc8 = (int)(Cp / 8);
+  const int lp = nc8 >= 16 ? 16 : (nc8 >= 8 ? 8 : (nc8 >= 4 ? 4 : (nc8 >= 2 ? 2 : 1)));
+  const int64_t per_blk = 2 * (256 / lp);
+  const int64_t nblk = (npix + per_blk - 1) / per_blk;
+  const dim3 grid((unsigned)(nblk < 2048 ? nblk : 2048)), block(256);
+  hipStream_t st = (hipStream_t)stream;
+  const _Float16* x = (const _Float16*)xp;
+  if (lp == 16)
+    hipLaunchKernelGGL(scan_nhwc_kernel<16>, grid, block, 0, st, x, npix, (int)Cp, (int)C, act,
+                       group_size, thr_mag, nnz);
+  else if (lp == 8)
+    hipLaunchKernelGGL(scan_nhwc_kernel<8>, grid, block, 0, st, x, npix, (int)Cp, (int)C, act,
+                       group_size, thr_mag, nnz);
+  else if (lp == 4)
+    hipLaunchKernelGGL(scan_nhwc_kernel<4>, grid, block, 0, st, x, npix, (int)Cp, (int)C, act,
+                       group_size, thr_mag, nnz);
+  else if (lp == 2)
+    hipLaunchKernelGGL(scan_nhwc_kernel<2>, grid, block, 0, st, x, npix, (int)Cp, (int)C, act,
+                       group_size, thr_mag, nnz);
+  else
+    hipLaunchKernelGGL(scan_nhwc_kernel<1>, grid, block, 0, st, x, npix, (int)Cp, (int)C, act,
+                       group_size, thr_mag, nnz);
   return (int)hipGetLastError();
 }
 

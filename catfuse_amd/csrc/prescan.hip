@@ -67,3 +67,106 @@ CF_API int cf_prescan_tiles(const uint32_t* act, int64_t NB, int64_t H, int64_t 
                      (int)GH, (int)GW, all_ones, ag_mask, tile_class);
   return (int)hipGetLastError();
 }
+
+namespace {
+
+// One workgroup: tiles active at some step (any bit of ag_mask[t][tile] for
+// t < T) in ascending order, then the inactive ones in ascending order.
+// Scanned in passes of 1024 tiles: per-wave ballots and popcounts give each
+// tile its rank among the active (or inactive) tiles of the pass, offset by
+// the counts of the earlier passes.  The first pass also sums the group
+// bits active at some step of every tile for the dispatch score.
+__global__ __launch_bounds__(1024) void compact_tiles_kernel(const int32_t* __restrict__ ag_mask,
+                                                             int T, int ntiles, int num_groups,
+                                                             double macs_per_tile, double tau,
+                                                             double r_min,
+                                                             int32_t* __restrict__ n_active,
+                                                             int32_t* __restrict__ order) {
+  __shared__ int wave_act[16];
+  __shared__ unsigned long long wave_pop[16];
+  __shared__ int base_sh;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // total active tiles first (the inactive ones go after them)
+  int cnt = 0;
+  unsigned long long pop = 0ull;
+  for (int i = tid; i < ntiles; i += 1024) {
+    uint32_t m = 0u;
+    for (int t = 0; t < T; ++t) m |= (uint32_t)ag_mask[(size_t)t * ntiles + i];
+    pop += (unsigned long long)__popc(m);
+    cnt += m != 0u;
+  }
+  for (int off = 32; off > 0; off >>= 1) {
+    cnt += __shfl_xor(cnt, off, 64);
+    pop += __shfl_xor(pop, off, 64);
+  }
+  if (lane == 0) {
+    wave_act[wave] = cnt;
+    wave_pop[wave] = pop;
+  }
+  __syncthreads();
+  if (tid == 0) {
+    int s = 0;
+    unsigned long long ps = 0ull;
+    for (int w = 0; w < 16; ++w) {
+      s += wave_act[w];
+      ps += wave_pop[w];
+    }
+    base_sh = s;
+    // Dispatch score (catfuse/sparseflow/dispatch.py:868-1000): R = 1 - AGR,
+    // S = R * macs_per_tile; SparseFlow iff R >= 0.99, or R >= r_min and
+    // S > tau; else the conv takes the dense route (n_active = -1).  The
+    // conv stages the steps of a tile together and skips a group's products
+    // only where it is silent at all of them, so R here is the fraction of
+    // (tile, group) pairs silent at every step (the reference counts
+    // (image, tile, group) triples, its kernel running one image per tile).
+    bool keep = true;
+    if (tau >= 0.0) {
+      const double total = (double)ntiles * (double)num_groups;
+      const double R = 1.0 - (double)ps / total;
+      keep = R >= 0.99 || (R >= r_min && R * macs_per_tile > tau);
+    }
+    *n_active = keep ? s : -1;
+  }
+  __syncthreads();
+  const int total_active = base_sh;
+  int act_before = 0;   // active tiles of earlier passes
+  for (int p0 = 0; p0 < ntiles; p0 += 1024) {
+    const int i = p0 + tid;
+    uint32_t m = 0u;
+    if (i < ntiles)
+      for (int t = 0; t < T; ++t) m |= (uint32_t)ag_mask[(size_t)t * ntiles + i];
+    const bool act = i < ntiles && m != 0u;
+    const unsigned long long bal = __ballot(act ? 1 : 0);
+    const int rank_w = __popcll(bal & ((1ull << lane) - 1ull));
+    __syncthreads();   // wave_act of the previous pass has been read
+    if (lane == 0) wave_act[wave] = __popcll(bal);
+    __syncthreads();
+    int before_w = 0, pass_act = 0;
+    for (int w = 0; w < 16; ++w) {
+      before_w += w < wave ? wave_act[w] : 0;
+      pass_act += wave_act[w];
+    }
+    if (i < ntiles) {
+      const int ra = act_before + before_w + rank_w;   // rank among active tiles
+      order[act ? ra : total_active + (i - ra)] = i;
+    }
+    act_before += pass_act;
+  }
+}
+
+}  // namespace
+
+// Reference: catfuse/sparseflow/sparse_conv2d_kernel.py:113-123 (the
+// active tiles of tile_class, host-synchronising torch.nonzero there).
+CF_API int cf_compact_tiles(const int32_t* ag_mask, int64_t T, int64_t ntiles,
+                            int64_t num_groups, double macs_per_tile, double tau, double r_min,
+                            int32_t* order, void* stream) {
+  if (!ag_mask || !order || T <= 0 || ntiles <= 0 || ntiles >= ((int64_t)1 << 30) ||
+      T * ntiles >= ((int64_t)1 << 40) || num_groups <= 0 || num_groups > 32 ||
+      !(macs_per_tile >= 0.0) || tau != tau || !(r_min <= 1.0))
+    return (int)hipErrorInvalidValue;
+  hipLaunchKernelGGL(compact_tiles_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, ag_mask,
+                     (int)T, (int)ntiles, (int)num_groups, macs_per_tile, tau, r_min, order,
+                     order + 1);
+  return (int)hipGetLastError();
+}

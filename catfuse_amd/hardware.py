@@ -11,7 +11,13 @@ default_K_compute_bound, notes.
 Fields (added): gcn_arch, peak_fp16_tflops, sf_sparsity_threshold (input
 sparsity above which STFusionConvBNLIF takes the SparseFlow route),
 dense_impl ("StreamFuse": fused Conv->BN->LIF with z on chip; "DenseKeep":
-z through HBM as the reference's schedule).
+z through HBM as the reference's schedule), sf_tile (output tile of the
+SparseFlow prescan and conv; None: the reference's _select_tile_sizes rule),
+sf_egd_tau_3x3 / sf_egd_tau_1x1 / sf_egd_r_min (the execution-grounded
+dispatch score gate of a SparseFlow launch, scored on the device by
+cf_compact_tiles: SparseFlow iff R >= 0.99 or R >= r_min and R * MACs per
+tile > tau; tau < 0: no score; the reference's sparseflow/config.py:48-61
+DISPATCH_TAU_3X3 / _1X1 / DISPATCH_R_MIN).
 """
 from __future__ import annotations
 
@@ -35,6 +41,10 @@ class HardwareProfile:
     peak_fp16_tflops: float = 0.0
     sf_sparsity_threshold: float = 0.7
     dense_impl: str = "DenseKeep"
+    sf_tile: tuple = None
+    sf_egd_tau_3x3: float = -1.0
+    sf_egd_tau_1x1: float = -1.0
+    sf_egd_r_min: float = 0.15
 
     @property
     def sm_capability(self) -> int:
@@ -58,20 +68,36 @@ A100_80GB = replace(A100_40GB, arch_name="A100 80GB", hbm_bandwidth_gbps=2039.0)
 
 # AMD Instinct MI355X (CDNA4, gfx950): 256 CUs in 8 XCDs, 288 GB HBM3E at
 # ~8 TB/s, 256 MB Infinity Cache, ~2.5 PFLOP/s dense fp16 MFMA.  The
-# SparseFlow route threshold is the measured crossover of the gfx950 kernels
-# (catfuse_amd.sparseflow.crossover): at every measured input sparsity of
-# config C1 (i.i.d., per-channel and all-channel 8x8 block patterns, rates
-# 0.001-0.5) the fused dense conv beat the forced SparseFlow route (scan +
-# prescan + chunk skipping), so the threshold is 1.0 (never taken); all-zero
-# inputs take StaticZero on every route.  The static regime thresholds keep
-# the reference's table shape.
+# SparseFlow thresholds come from the measured crossover of the gfx950
+# kernels (bench.py --workload sf_crossover at 3x3 layers 256ch 14x14,
+# 128ch 28x28, 64ch 56x56, 512ch 7x7; T=4, B=32): with i.i.d., per-channel
+# 8x8 block and all-channel 8x8 block patterns at rates 0.001-0.5 the fused
+# dense conv beats the forced SparseFlow route (activity scan + tile
+# prescan + tile compaction + chunk skipping) at every sparsity; with dead
+# 16-channel groups per image, or activity confined to a quarter of the
+# image, SparseFlow wins at 82-99% input sparsity depending on the shape.
+# The nonzero count does not tell these apart at equal sparsity, so the
+# density threshold is 1.0: SparseFlow is never taken by default
+# (CATFUSE_SF_SPARSITY_THRESHOLD enables it).  When enabled, the launch is
+# gated on the device by the dispatch score over its tile masks: across the
+# 140 measured rows the fraction R of (tile, group) pairs silent at every
+# step separates wins from losses best with R_min = 0.4 (7 rows
+# misclassified, each within 4% of break-even), while S = R * MACs-per-tile
+# against any single tau misclassifies 24, so the 3x3 gate is R >= 0.4 with
+# tau = 0 (the reference's V100 values, sparseflow/config.py:48-61, are
+# tau_3x3 = 1e5 and R_min = 0.15); 1x1 layers were not swept (no score).
+# All-zero inputs take StaticZero on every route.  SparseFlow tiles are 8x8
+# at every size: the 8x16 tile of the reference's rule (>= 3136 output
+# pixels) needs the kernel's full register file (one workgroup per CU).  The
+# static regime thresholds keep the reference's table shape.
 MI355X = HardwareProfile(
     arch_name="AMD Instinct MI355X", sm_version=(9, 5), hbm_bandwidth_gbps=8000.0,
     l2_size_mb=32.0, sm_count=256, sf_threshold_C=256, sf_threshold_H=14,
     default_K_memory_bound=8, default_K_compute_bound=4,
     notes="gfx950; fused StreamFuse conv as the dense path, device-side routing.",
     gcn_arch="gfx950", peak_fp16_tflops=2500.0, sf_sparsity_threshold=1.0,
-    dense_impl="StreamFuse")
+    dense_impl="StreamFuse", sf_tile=(8, 8), sf_egd_tau_3x3=0.0, sf_egd_tau_1x1=-1.0,
+    sf_egd_r_min=0.4)
 
 DEFAULT = V100_PCIE_32GB
 

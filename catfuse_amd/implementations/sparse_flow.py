@@ -6,20 +6,27 @@ Realises TimeBlock(K) ∘ StreamFuse(Conv, LIF) ∘ StateCarry(LIF)
 1. cf_pack_input stages x as fp16 NHWC, ORs channel-group activity bits per
    pixel and counts nonzeros (one pass over x);
 2. cf_prescan_tiles reduces the bits over each output tile's receptive
-   field (tile geometry and group size exactly as the reference's
-   _select_tile_sizes / choose_group_size);
-3. cf_conv_mfma in rectangular-tile mode reads the nonzero count and
+   field (group size as the reference's choose_group_size; 8x8 tiles, the
+   MI355X profile's sf_tile, where the reference's _select_tile_sizes picks
+   8x16 for large maps);
+3. cf_compact_tiles orders the tiles on the device, those active at some
+   step first (the reference's host-side _build_active_tile_ids,
+   catfuse/sparseflow/sparse_conv2d_kernel.py:113-123, without its sync);
+4. cf_conv_mfma in rectangular-tile mode reads the nonzero count and
    decides the route itself — nnz == 0: StaticZero (no K loop, z = bias);
-   sparsity > threshold: skip every 32-channel K chunk whose group bits are
-   clear for the tile; otherwise dense — then applies BN and the LIF in its
-   epilogue.  No host synchronisation; every route gives bit-identical
-   results (skipped chunks contribute exact zeros).
+   sparsity > threshold: the tiles in the compacted order, skipping every
+   32-channel K chunk whose group bits are clear for the tile (and the
+   MFMAs of a silent 16-channel half when the groups are 16 channels
+   wide); otherwise dense — then applies BN and the LIF in its epilogue.
+   No host synchronisation; every route gives bit-identical results
+   (skipped chunks contribute exact zeros).
 
-Steps 1-2 and the sparse route run only when the threshold is below 1.  The
-MI355X profile's threshold is 1.0: on gfx950 no measured input sparsity made
-the SparseFlow route faster than the fused dense conv (the sweep of
-catfuse_amd.sparseflow.crossover), so the layer then runs the dense fused
-conv, with StaticZero decided from the input's count block.
+Steps 1-3 and the sparse route run only when the threshold is below 1.  The
+MI355X profile's threshold is 1.0: on gfx950 the SparseFlow route beats the
+fused dense conv only on channel-group sparse inputs, which the nonzero
+count cannot tell from i.i.d. ones (bench.py --workload sf_crossover), so
+the layer runs the dense fused conv, with StaticZero decided from the
+input's count block.
 """
 from __future__ import annotations
 
@@ -34,15 +41,31 @@ from catfuse_amd.sparseflow.sparse_helpers import _select_tile_sizes, choose_gro
 class SparseFlow(HipConvImplementation):
     name = "SparseFlow"
 
-    def __init__(self, sparsity_threshold: float = None):
+    def __init__(self, sparsity_threshold: float = None, compact_tiles: bool = True,
+                 egd: bool = True):
+        """egd: gate the SparseFlow route with the profile's dispatch score
+        (tau per kernel size; no gate when the profile's tau is negative)."""
         super().__init__()
-        self.sparsity_threshold = (runtime_profile().sf_sparsity_threshold
+        prof = runtime_profile()
+        self.sparsity_threshold = (prof.sf_sparsity_threshold
                                    if sparsity_threshold is None else float(sparsity_threshold))
+        self.compact_tiles = bool(compact_tiles)
+        self.tile = prof.sf_tile
+        self.egd = None
+        if egd:
+            self.egd = {1: (prof.sf_egd_tau_1x1, prof.sf_egd_r_min),
+                        3: (prof.sf_egd_tau_3x3, prof.sf_egd_r_min)}
 
     def geometry(self, spec, H_in, W_in):
         Ho, Wo = spec.output_hw(H_in, W_in)
-        bh, bw = _select_tile_sizes(Ho, Wo)
-        return dict(block_h=bh, block_w=bw, group_size=choose_group_size(spec.in_channels))
+        bh, bw = self.tile if self.tile is not None else _select_tile_sizes(Ho, Wo)
+        gate = None
+        if self.egd is not None:
+            gate = self.egd.get(spec.kernel_size, self.egd[3])
+            if gate[0] < 0:
+                gate = None
+        return dict(block_h=bh, block_w=bw, group_size=choose_group_size(spec.in_channels),
+                    compact=self.compact_tiles, egd=gate)
 
     def route_geometry(self, spec, H_in, W_in):
         """Prescan geometry for the conv, or None when the threshold (>= 1)

@@ -549,6 +549,27 @@ def prescan_tiles(act: torch.Tensor, H: int, W: int, H_out: int, W_out: int, ker
     return tc[:n], ag[:n]
 
 
+def compact_tiles(ag_mask: torch.Tensor, T: int, ntiles: int, num_groups: int = 32,
+                  order_out=None, *, macs_per_tile: float = 0.0, tau: float = -1.0,
+                  r_min: float = 0.0) -> torch.Tensor:
+    """Device-side active-tile order (cf_compact_tiles) of tile masks
+    [T][ntiles]: int32 [1 + ntiles], the number of tiles active at some step
+    (-1 when tau >= 0 and the dispatch score R * macs_per_tile rejects
+    SparseFlow), then the tile indices, active ones first."""
+    if ag_mask.numel() < T * ntiles:
+        raise ValueError("tile masks are smaller than T * ntiles")
+    order = order_out if order_out is not None else torch.empty(
+        ntiles + 1, dtype=torch.int32, device=ag_mask.device)
+    if order.numel() < ntiles + 1:
+        raise ValueError("tile order buffer is too small")
+    ev = _t0()
+    check(_hip.lib().cf_compact_tiles(ptr(ag_mask), T, ntiles, int(num_groups),
+                                      float(macs_per_tile), float(tau), float(r_min), ptr(order),
+                                      _hip.stream(ag_mask.device)), "cf_compact_tiles")
+    _t1("compact_tiles", ev, nbytes=8 * T * ntiles + 4 * ntiles)
+    return order[:ntiles + 1]
+
+
 def zero_counter(c: torch.Tensor) -> None:
     check(_hip.lib().cf_zero_counter(ptr(c), _hip.stream(c.device)), "cf_zero_counter")
 
@@ -669,8 +690,9 @@ class ConvLIFRunner:
                  identity=None, identity_mode=ID_ADD_SPIKE, sparse=None, sparse_threshold=0.7,
                  static_zero=True, emit_nhwc=True):
         """x [T, B, Cin, H, W] fp32 (values exact in fp16).  sparse: None for
-        the dense route only, or a dict with block_h, block_w, group_size to
-        run the prescan and SparseFlow chunk skipping.  If x carries a current
+        the dense route only, or a dict with block_h, block_w, group_size
+        (and optionally compact: True / "always" / False, the active-tile
+        order) to run the prescan and SparseFlow chunk skipping.  If x carries a current
         fp16 NHWC copy (written by the producing fused conv) the pack pass is
         skipped: a SparseFlow layer scans the copy for its activity bits and
         count, a dense one takes the dense route; with emit_nhwc the output
@@ -706,7 +728,7 @@ class ConvLIFRunner:
                    else None)
             pack_input(x.reshape(T * B, C, H, W), cp=self.Cp, group_size=gs, nnz=nnz,
                        act_out=act, xp_out=xp, status=st)
-        ag = None
+        ag = order = None
         th = tw = 0
         if sparse is not None:
             th, tw = sparse["block_h"], sparse["block_w"]
@@ -718,6 +740,20 @@ class ConvLIFRunner:
             prescan_tiles(act, H, W, Ho, Wo, self.KH, self.stride, self.padding, th, tw, G,
                           ag_buf, tc_buf)
             ag = ag_buf
+            # compact: True orders the tiles when the grid does not fit one
+            # dispatch wave (256 CUs x 3 workgroups of the 8x8 halo kernel;
+            # within one wave the order cannot matter), "always" at any size.
+            # egd: (tau, r_min) of the dispatch score, computed by the same
+            # launch (so it runs whenever a score is asked for).
+            cmode = sparse.get("compact", True)
+            egd = sparse.get("egd")
+            if (egd is not None or cmode == "always"
+                    or (cmode and B * GH * GW * (self.Coutp // 64) > 768)):
+                tau, r_min = egd if egd is not None else (-1.0, 0.0)
+                macs_tile = Ho * Wo * self.Cout * self.Cin * self.KH * self.KW / (GH * GW)
+                order = compact_tiles(ag, T, B * GH * GW, G, self.workspace(
+                    "order", (B * GH * GW + 1,), torch.int32, dev), macs_per_tile=macs_tile,
+                    tau=tau, r_min=r_min)
         id_nhwc = None
         if identity is not None:
             require_gpu_tensor(identity, "identity")
@@ -727,14 +763,16 @@ class ConvLIFRunner:
                 # spike-valued identity: read its fp16 NHWC copy when current
                 id_nhwc = shadow_of(identity, (T * B, Ho, Wo, pad32(self.Cout)))
         out, v_out = self._launch(
-            xp, T, B, H, W, Ho, Wo, x.numel(), nnz, ag, th, tw, gs, v_in, epilogue, want_v_out,
+            xp, T, B, H, W, Ho, Wo, x.numel(), nnz, ag, order, th, tw, gs, v_in, epilogue,
+            want_v_out,
             None if id_nhwc is not None else identity, id_nhwc, identity_mode, sparse_threshold,
             emit_nhwc, lambda nhwc: lazy_output((T, B, self.Cout, Ho, Wo), nhwc, dev),
             "conv_mfma" + ("_sparse" if sparse is not None else ""))
         self.last_tiles = None if ag is None else (tc_buf, ag)
+        self.last_order = order
         return out, v_out
 
-    def _launch(self, xp, T, B, H, W, Ho, Wo, numel, nnz, ag, th, tw, gs, v_in, epilogue,
+    def _launch(self, xp, T, B, H, W, Ho, Wo, numel, nnz, ag, order, th, tw, gs, v_in, epilogue,
                 want_v_out, identity, id_nhwc, identity_mode, sparse_threshold, emit_nhwc,
                 make_lazy, timer_name):
         """One cf_conv_mfma launch on the staged fp16 NHWC input xp; the
@@ -767,7 +805,7 @@ class ConvLIFRunner:
         rc = _hip.lib().cf_conv_mfma(
             ptr(xp), ptr(self.w_packed), ptr(self.alpha), ptr(self.beta), ptr(v_in), ptr(v_out),
             out_ptr, ptr(nhwc), cp_out, ptr(identity), ptr(id_nhwc), pad32(self.Cout),
-            int(identity_mode), ptr(ag), ptr(nnz), ptr(nz_out), numel,
+            int(identity_mode), ptr(ag), ptr(order), ptr(nnz), ptr(nz_out), numel,
             float(sparse_threshold), T, B, self.Cp, self.Cout, self.Coutp, H, W, Ho, Wo, self.KH,
             self.KW, self.stride, self.padding, B, th, tw, gs, int(epilogue), *self.lif,
             _hip.stream(dev))
@@ -827,8 +865,8 @@ class ConvLIFRunner:
                                       out=self.workspace("idp", (T * B * N, id_cp),
                                                          torch.float16, dev))
         out, v_out = self._launch(
-            xp.view(T * nimg, H, W, self.Cp), T, nimg, H, W, H, W, x.numel(), nnz, None, 0, 0,
-            0, v_in, EPI_LIF, want_v_out, None,
+            xp.view(T * nimg, H, W, self.Cp), T, nimg, H, W, H, W, x.numel(), nnz, None, None,
+            0, 0, 0, v_in, EPI_LIF, want_v_out, None,
             None if id_copy is None else id_copy.view(T * nimg, H, W, id_cp), ID_ADD_SPIKE, 2.0,
             True, lambda nhwc: lazy_tokens((T, B, N, self.Cout), nhwc, dev), "linear_tokens")
         return out, (None if v_out is None else v_out.view(nimg, self.Cout, H * W))

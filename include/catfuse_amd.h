@@ -186,6 +186,31 @@ int cf_prescan_tiles(const uint32_t* act, int64_t NB, int64_t H, int64_t W, int6
                      int64_t block_h, int64_t block_w, int64_t num_groups, int32_t* ag_mask,
                      int32_t* tile_class, void* stream);
 
+/* Active-tile compaction and dispatch score on the device: from ag_mask
+ * [T][ntiles] (cf_prescan_tiles, ntiles = B*GH*GW, num_groups groups),
+ * order[0] = the number of tiles active at some step (any bit of
+ * ag_mask[t][tile] set for some t < T), order[1 ..] = the tile indices,
+ * active tiles first, each part ascending.  With tau >= 0 the launch also
+ * scores the layer as the reference's execution-grounded dispatch does,
+ * over the tile's time steps (the conv skips a group only where it is
+ * silent at all of them): R = 1 - (set bits of the OR over t of
+ * ag_mask[t][tile]) / (ntiles * num_groups), S = R * macs_per_tile (dense
+ * MACs per image / tiles per image); unless R >= 0.99,
+ * or R >= r_min and S > tau, order[0] is -1 and cf_conv_mfma then takes the
+ * dense route (same results).  tau < 0: no score.  order holds 1 + ntiles
+ * int32; ntiles < 2^30.  One workgroup, no host synchronisation, graph-
+ * capture safe.  Replaces the host-synchronising
+ * catfuse/sparseflow/sparse_conv2d_kernel.py:113-123 _build_active_tile_ids
+ * (torch.nonzero over tile_class != TILE_ZERO) feeding the active-tile
+ * launch at :1102-1163, and the host-side decision of
+ * catfuse/sparseflow/dispatch.py:860-1000 (make_dispatch_decision, R_l,
+ * S_l, tau, R_min); here every tile keeps its workgroup (inactive ones run
+ * the LIF epilogue on the bias drive) and the order makes the active ones
+ * run first (cf_conv_mfma tile_order). */
+int cf_compact_tiles(const int32_t* ag_mask, int64_t T, int64_t ntiles, int64_t num_groups,
+                     double macs_per_tile, double tau, double r_min, int32_t* order,
+                     void* stream);
+
 /* Conv weight staging for cf_conv_mfma: fp32 w [Cout][Cin][KH][KW] ->
  * fp16 hi/lo limbs with a per-channel power-of-two prescale (2*Coutp*KH*KW*Cp
  * halves, fragment-major: per limb, 32-channel tile, tap and 16-channel K
@@ -220,7 +245,14 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
  *   tile_h/tile_w > 0 selects rectangular pixel tiles aligned with the
  *   prescan tiles (tile_h*tile_w in {64,128}) and enables SparseFlow chunk
  *   skipping from ag_mask ([T][B*GH*GW]) when nnz is non-NULL; tile_h = 0
- *   selects flat pixel tiles (dense).  nnz (nullable, read only) is the
+ *   selects flat pixel tiles (dense).  With prescan groups narrower than 32
+ *   channels, a silent 16-channel half of a chunk also skips its MFMAs.
+ *   tile_order (nullable, needs ag_mask; [1 + B*GH*GW] as cf_compact_tiles
+ *   writes it): on the SparseFlow route the halo kernel gives each XCD an
+ *   equal share of the tiles active at some step, dispatched before the
+ *   inactive ones (which only run the epilogue), and takes the dense route
+ *   instead when tile_order[0] < 0 (the dispatch score rejected SparseFlow);
+ *   ignored by the flat-tile kernel and by the other routes.  nnz (nullable, read only) is the
  *   count block of the input: its published count k (exact, from
  *   cf_pack_input / cf_scan_nhwc, or the producing conv's nz_out) routes
  *   the launch: k == 0 StaticZero (no K loop), SparseFlow when ag_mask is
@@ -236,7 +268,8 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
 int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha, const float* beta,
                  const float* v_in, float* v_out, float* out, void* out_nhwc, int64_t cp_out,
                  const float* identity, const void* identity_nhwc, int64_t cp_id,
-                 int identity_mode, const int32_t* ag_mask, const unsigned long long* nnz,
+                 int identity_mode, const int32_t* ag_mask, const int32_t* tile_order,
+                 const unsigned long long* nnz,
                  unsigned long long* nz_out, int64_t numel, double sparse_threshold, int64_t T,
                  int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo, int64_t KH,
                  int64_t KW, int64_t stride, int64_t pad, int64_t x_img_tstride, int64_t tile_h,
@@ -254,7 +287,8 @@ int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha, const 
 int cf_conv_halo(const void* x, const void* w_packed, const float* alpha, const float* beta,
                  const float* v_in, float* v_out, float* out, void* out_nhwc, int64_t cp_out,
                  const float* identity, const void* identity_nhwc, int64_t cp_id,
-                 int identity_mode, const int32_t* ag_mask, const unsigned long long* nnz,
+                 int identity_mode, const int32_t* ag_mask, const int32_t* tile_order,
+                 const unsigned long long* nnz,
                  unsigned long long* nz_out, int64_t numel, double sparse_threshold, int64_t T,
                  int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
                  int64_t ksize, int64_t stride, int64_t pad, int64_t tile_h, int64_t tile_w,
@@ -353,13 +387,14 @@ int cf_conv_grouped_lif(const void* x, const float* x32, int64_t x_img_tstride, 
 #define CF_ERROR_NOALLOC_LIMIT 7001
 
 /* Workspace of cf_conv_sparse_noalloc, a static device array of
- * CF_NOALLOC_SCRATCH_BYTES (about 9 MiB) on every GPU the library runs on:
+ * CF_NOALLOC_SCRATCH_BYTES (about 9.5 MiB) on every GPU the library runs on:
  * the input's count block, activity bits for up to CF_NOALLOC_MAX_PIXELS
- * input pixels (T*B*H*W) and tile masks for up to CF_NOALLOC_MAX_TILES
- * prescan tiles (T*B*ceil(Ho/tile_h)*ceil(Wo/tile_w)). */
+ * input pixels (T*B*H*W), tile masks for up to CF_NOALLOC_MAX_TILES
+ * prescan tiles (T*B*ceil(Ho/tile_h)*ceil(Wo/tile_w)) and their compacted
+ * order. */
 #define CF_NOALLOC_MAX_PIXELS (1 << 21)
 #define CF_NOALLOC_MAX_TILES (1 << 17)
-#define CF_NOALLOC_SCRATCH_BYTES (4096 + 4 * CF_NOALLOC_MAX_PIXELS + 8 * CF_NOALLOC_MAX_TILES)
+#define CF_NOALLOC_SCRATCH_BYTES (4096 + 4 * CF_NOALLOC_MAX_PIXELS + 12 * CF_NOALLOC_MAX_TILES + 256)
 
 /* The SparseFlow-routed fused Conv -> BN -> LIF of cf_conv_mfma on an fp16
  * NHWC input (x [T*B][H][W][Cp], channels >= Cin zero, e.g. a fused conv's
@@ -368,11 +403,11 @@ int cf_conv_grouped_lif(const void* x, const float* x32, int64_t x_img_tstride, 
  * it is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  It runs
  * cf_scan_nhwc (activity bits + nonzero count of x), cf_prescan_tiles (tile
- * masks, tile_h x tile_w output tiles, group_size-channel groups) and
- * cf_conv_mfma routed on them (StaticZero / SparseFlow above
+ * masks, tile_h x tile_w output tiles, group_size-channel groups),
+ * cf_compact_tiles and cf_conv_mfma routed on them (StaticZero / SparseFlow above
  * sparse_threshold / dense), with their workspace in a static device array
  * (CF_NOALLOC_SCRATCH_BYTES per GPU, held until the process ends); results
- * are those of the same three calls with caller buffers, bit for bit.
+ * are those of the same calls with caller buffers, bit for bit.
  * Square kernels (ksize x ksize); other arguments as cf_conv_mfma.  Returns
  * CF_ERROR_NOALLOC_LIMIT, launching nothing, when T*B*H*W >
  * CF_NOALLOC_MAX_PIXELS or the tile count > CF_NOALLOC_MAX_TILES.  Every

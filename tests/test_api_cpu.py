@@ -211,16 +211,38 @@ def test_crossover_inputs_and_decision():
     xb = bench.xo_input(1.0, "block", (4, 8, 64, 16, 16), seed=3)
     frac = float(xb.mean())
     assert 0.2 < frac < 0.4
+    # chgroup: a 16-channel group of an image is silent everywhere or active
+    xg = bench.xo_input(1.0, "chgroup", (3, 8, 64, 6, 6), seed=4)
+    per_group = xg.reshape(3, 8, 4, 16 * 36).amax(-1)     # [T, B, group]
+    assert torch.equal(xg.reshape(3, 8, 4, 16 * 36).amin(-1), per_group)
+    assert torch.equal(per_group, per_group[:1].expand_as(per_group))
+    assert 0.1 < float(per_group.mean()) < 0.5
+    # region: activity of an image only inside one H/2 x W/2 window
+    xr = bench.xo_input(1.0, "region", (2, 5, 4, 12, 10), seed=5)
+    for b in range(5):
+        m = xr[:, b].amax(dim=(0, 1))
+        rows_on, cols_on = m.amax(1).nonzero().flatten(), m.amax(0).nonzero().flatten()
+        assert len(rows_on) == 6 and len(cols_on) == 5 and int(m.sum()) == 30
     with pytest.raises(ValueError):
         bench.xo_input(0.1, "checker", shape)
     rows = [dict(pattern="iid", rate=r, density=r, SparseFlow=sf, StreamFuse=10.0,
-                 DenseKeep=12.0, auto=10.0)
+                 DenseKeep=12.0, auto=10.0, **{"SparseFlow-linear": 20.0, "SF+EGD": 10.0})
             for r, sf in ((0.0, 1.0), (0.01, 9.0), (0.1, 11.0), (0.5, 13.0))]
     # rate 0 (StaticZero) never counts as a SparseFlow win
     assert bench.xo_crossover(rows) == {"iid": pytest.approx(0.99)}
     rows[1]["SparseFlow"] = 10.5
     assert bench.xo_crossover(rows) == {"iid": None}
     assert "| iid | 0.01 |" in bench.xo_table(rows)
+    # dispatch-score fit: SparseFlow wins above S = 5, loses below
+    fit = [dict(density=0.1, S=s, SparseFlow=9.0 if s > 5 else 11.0, StreamFuse=10.0,
+                DenseKeep=12.0) for s in (1.0, 2.0, 4.0, 6.0, 8.0)]
+    assert bench.xo_egd_fit(fit) == (5.0, 0)
+    fit[0]["SparseFlow"] = 9.0            # one win below the others: one misclassified
+    assert bench.xo_egd_fit(fit) == (5.0, 1)
+    # R_min fit: wins at R 0.6 and 0.8, losses at 0.1 and 0.3 -> midpoint 0.45
+    rfit = [dict(density=0.1, R=R, SparseFlow=9.0 if R > 0.5 else 11.0, StreamFuse=10.0,
+                 DenseKeep=12.0) for R in (0.1, 0.3, 0.6, 0.8)]
+    assert bench.xo_rmin_fit(rfit) == (pytest.approx(0.45), 0)
 
 
 def test_fused_global_avgpool_fallback_cpu():

@@ -65,17 +65,26 @@ def test_host_side_argument_validation():
     assert L.cf_lif_multistep(1, None, None, None, 1, None, 1, 0, None, 4, 16, 1, 1,
                               2.0, 1.0, 0.0, 1, 1, None) == INVALID
     # conv: Cp not a multiple of 32
-    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, None, 0, 0.7,
+    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, None, None, 0, 0.7,
                           4, 2, 48, 64, 64, 8, 8, 8, 8, 3, 3, 1, 1, 2, 0, 0, 0,
                           0, 2.0, 1.0, 0.0, 1, 1, None) == INVALID
     # conv: inconsistent output size
-    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, None, 0, 0.7,
+    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, None, None, 0, 0.7,
                           4, 2, 64, 64, 64, 8, 8, 7, 8, 3, 3, 1, 1, 2, 0, 0, 0,
                           0, 2.0, 1.0, 0.0, 1, 1, None) == INVALID
     # conv: rect tile must hold 64 or 128 pixels
-    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, None, 0, 0.7,
+    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, None, None, 0, 0.7,
                           4, 2, 64, 64, 64, 8, 8, 8, 8, 3, 3, 1, 1, 2, 4, 4, 16,
                           0, 2.0, 1.0, 0.0, 1, 1, None) == INVALID
+    # conv: a tile order needs tile masks
+    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, 1, None, None,
+                          0, 0.7, 4, 2, 64, 64, 64, 8, 8, 8, 8, 3, 3, 1, 1, 2, 8, 8, 16,
+                          0, 2.0, 1.0, 0.0, 1, 1, None) == INVALID
+    # compaction: no tiles / no mask
+    assert L.cf_compact_tiles(1, 4, 0, 8, 0.0, -1.0, 0.0, 1, None) == INVALID
+    assert L.cf_compact_tiles(None, 4, 8, 8, 0.0, -1.0, 0.0, 1, None) == INVALID
+    assert L.cf_compact_tiles(1, 4, 8, 33, 0.0, -1.0, 0.0, 1, None) == INVALID   # > 32 groups
+    assert L.cf_compact_tiles(1, 4, 8, 8, float("nan"), -1.0, 0.0, 1, None) == INVALID
     # prescan: more than 32 groups
     assert L.cf_prescan_tiles(1, 1, 8, 8, 8, 8, 3, 1, 1, 8, 8, 33, 1, 1, None) == INVALID
     # pack: groups must fit 32 bits

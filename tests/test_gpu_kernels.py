@@ -406,6 +406,113 @@ def test_sparse_route_multiblock_bitwise(cuda, stride, T):
                what=f"multiblock s{stride} T{T}")
 
 
+@pytest.mark.parametrize("ntiles,T,frac", [(1, 1, 1.0), (7, 4, 0.3), (1024, 4, 0.05),
+                                             (1025, 2, 0.5), (3000, 4, 0.0), (3000, 3, 1.0)])
+def test_compact_tiles_order(cuda, ntiles, T, frac):
+    """cf_compact_tiles: order[0] = tiles active at some step, then the
+    active tiles ascending, then the inactive ones ascending (numpy)."""
+    from catfuse_amd import runtime
+    g = _gen(ntiles + T)
+    act = torch.rand(T, ntiles, generator=g) < frac
+    bits = torch.randint(1, 1 << 20, (T, ntiles), generator=g, dtype=torch.int32)
+    ag = torch.where(act, bits, torch.zeros_like(bits))
+    order = runtime.compact_tiles(ag.reshape(-1).to(cuda), T, ntiles).cpu().numpy()
+    any_act = (ag.numpy() != 0).any(axis=0)
+    expect = np.concatenate([np.flatnonzero(any_act), np.flatnonzero(~any_act)])
+    assert order[0] == int(any_act.sum())
+    assert np.array_equal(order[1:], expect)
+
+
+@pytest.mark.parametrize("frac,groups", [(0.02, 8), (0.3, 16), (0.9, 32)])
+def test_compact_tiles_dispatch_score(cuda, frac, groups):
+    """The dispatch score of cf_compact_tiles: R = 1 - group bits set at some
+    step / (ntiles * groups) (numpy), S = R * macs_per_tile; order[0] stays the
+    active-tile count when R >= 0.99 or (R >= r_min and S > tau), else -1;
+    the permutation is written either way."""
+    from catfuse_amd import runtime
+    T, ntiles = 4, 700
+    g = _gen(groups)
+    bits = (torch.rand(T, ntiles, groups, generator=g) < frac).int()
+    ag = (bits << torch.arange(groups, dtype=torch.int32)).sum(-1).int()
+    R = 1.0 - float(bits.any(0).sum()) / (ntiles * groups)
+    n_act = int((ag != 0).any(0).sum())
+    macs = 1.0e6
+    for tau, r_min in ((-1.0, 0.0), (0.0, 0.0), (R * macs * 0.99, 0.0), (R * macs * 1.01, 0.0),
+                       (0.0, min(R + 0.01, 1.0)), (0.0, max(R - 0.01, 0.0))):
+        order = runtime.compact_tiles(ag.reshape(-1).to(cuda), T, ntiles, groups,
+                                      macs_per_tile=macs, tau=tau, r_min=r_min).cpu()
+        keep = tau < 0 or R >= 0.99 or (R >= r_min and R * macs > tau)
+        assert int(order[0]) == (n_act if keep else -1), (tau, r_min, R)
+        assert sorted(order[1:].tolist()) == list(range(ntiles))
+
+
+def test_sparse_route_dispatch_score_gate_bitwise(cuda):
+    """A SparseFlow launch the dispatch score rejects (tau above S) takes the
+    dense route inside the conv; one it accepts runs SparseFlow: both equal
+    the dense evaluation bit for bit."""
+    T, B, C, H = 4, 3, 64, 20
+    conv, bn, lif = _layer(C, 64, 3, 1, 1, seed=91)
+    x = _half_silent_input(T, B, C, H, H, seed=92)
+    r = _runner(conv, bn, lif, cuda)
+    xd = x.to(cuda)
+    s_dense, v_dense = r.run_mfma(xd, static_zero=False)
+    geo = dict(block_h=8, block_w=8, group_size=16)
+    for egd in ((1e30, 0.15), (0.0, 0.0)):
+        s2, v2 = r.run_mfma(xd, sparse=dict(geo, egd=egd), sparse_threshold=-1.0)
+        assert torch.equal(s2, s_dense) and torch.equal(v2, v_dense)
+        if egd[0] > 1e20:
+            assert int(r.last_order[0]) == -1             # rejected: dense route
+    assert int(r.last_order[0]) > 0                       # accepted: active tiles
+
+
+def _half_silent_input(T, B, C, H, W, seed, rate=0.08):
+    """Spikes where whole 16-channel groups, half of some 32-channel chunks,
+    are silent (only the group's other half active), activity concentrated
+    in a corner of some images and whole (t, b) images silent."""
+    g = _gen(seed)
+    x = (torch.rand(T, B, C, H, W, generator=g) < rate).float()
+    for c0 in range(0, C, 64):
+        x[:, :, c0 + 16:c0 + 32] = 0.0          # second half of every other chunk
+    x[:, 0, :, H // 2:, :] = 0.0                 # image 0: top half only
+    x[:, 0, :, :, W // 2:] = 0.0
+    x[1, -1] = 0.0                               # a silent (t, b) image
+    return x
+
+
+@pytest.mark.parametrize("k,stride,T,tile,C", [(3, 1, 4, (8, 8), 128), (3, 2, 5, (8, 8), 96),
+                                               (1, 1, 4, (8, 8), 64), (3, 1, 7, (8, 16), 64),
+                                               (3, 1, 4, (8, 8), 256)])
+def test_sparse_compaction_and_half_skip_bitwise(cuda, k, stride, T, tile, C):
+    """The SparseFlow route with the compacted tile order and (16-channel
+    groups) the skipped silent chunk halves equals the route without the
+    order and the dense route bit for bit, and the oracle."""
+    from catfuse_amd.sparseflow.sparse_helpers import choose_group_size
+    B, H = 3, 28 if tile[1] == 16 else 20
+    p = 1 if k == 3 else 0
+    conv, bn, lif = _layer(C, 64, k, stride, p, seed=70 + C + k, lif=None)
+    x = _half_silent_input(T, B, C, H, H, seed=C + T)
+    r = _runner(conv, bn, lif, cuda)
+    xd = x.to(cuda)
+    Ho = (H + 2 * p - k) // stride + 1
+    v0 = (torch.rand(B, 64, Ho, Ho, generator=_gen(5)) * 0.5).to(cuda)
+    gs = choose_group_size(C)
+    geo = dict(block_h=tile[0], block_w=tile[1], group_size=gs)
+    s_dense, v_dense = r.run_mfma(xd, v0, static_zero=False)
+    s_ord, v_ord = r.run_mfma(xd, v0, sparse=dict(geo, compact="always"))
+    s_lin, v_lin = r.run_mfma(xd, v0, sparse=dict(geo, compact=False))
+    for s2, v2 in ((s_ord, v_ord), (s_lin, v_lin)):
+        assert torch.equal(s2, s_dense) and torch.equal(v2, v_dense)
+    from catfuse_amd import runtime
+    assert runtime.route_from_nnz(r.last_nnz, r.last_numel, 0.7).item() == 1   # SPARSE
+    tc, ag = r.last_tiles
+    GH, GW = -(-Ho // tile[0]), -(-Ho // tile[1])
+    active = (ag.view(T, B * GH * GW) != 0).any(0)
+    assert 0 < int(active.sum()) < B * GH * GW            # some tiles run the epilogue only
+    s_ref, v_ref, h_ref = oracle.conv_bn_lif(x, conv, bn, lif, v_in=v0.cpu())
+    lif_parity(s_dense.cpu().numpy(), v_dense.cpu().numpy(), s_ref, v_ref, h_ref,
+               what=f"compact k{k} s{stride} T{T} C{C}")
+
+
 def test_static_zero_route_equals_bias_only(cuda):
     T, B, C, H, W = 4, 2, 64, 8, 8
     conv, bn, lif = _layer(C, C, 3, 1, 1, seed=8)
@@ -539,6 +646,37 @@ def test_scan_nhwc_matches_pack(cuda, C, gs):
         assert int(n1[1].item()) == int(n2[1].item()) == int((x != 0).sum())
         assert not bool(n1[0].item()) and not bool(n1[16::16].any())
         assert not bool(n2[0].item()) and not bool(n2[16::16].any())
+
+
+@pytest.mark.parametrize("NB,H,W,C,cp,gs,thr", [(128, 56, 56, 64, 64, 16, 1e-6),
+                                                  (16, 14, 14, 250, 256, 32, 0.5),
+                                                  (3, 5, 7, 12, 16, 8, 1e-6),
+                                                  (5, 9, 9, 96, 96, 16, -1.0),
+                                                  (7, 6, 6, 40, 64, 16, 3.0e-5)])
+def test_scan_nhwc_thresholds_and_sizes(cuda, NB, H, W, C, cp, gs, thr):
+    """cf_scan_nhwc against torch on fp16 copies holding signed values, -0,
+    subnormals and values at the threshold: bit g of a pixel iff some
+    channel c < C of group g has |x| > thr; the count is that of nonzero
+    halves (channels >= C included, -0 not); sizes from a few pixels to a
+    grid-stride pass over 400k pixels."""
+    from catfuse_amd import runtime
+    g = _gen(NB + C)
+    vals = torch.tensor([0.0, -0.0, 1.0, -1.0, 2.0, 2.0 ** -24, -(2.0 ** -20), 0.5, 3.0e-5, 1e-6],
+                        dtype=torch.float16)
+    idx = torch.randint(0, len(vals), (NB, H, W, cp), generator=g)
+    keep = torch.rand(NB, H, W, cp, generator=g) < 0.1
+    xp = torch.where(keep, vals[idx], torch.zeros((), dtype=torch.float16))
+    blk = runtime.count_block(cuda)
+    act = runtime.scan_nhwc(xp.to(cuda), C, group_size=gs, threshold=thr, nnz=blk).cpu()
+    mag = xp.float().abs()[..., :C]
+    hit = mag > thr
+    ng = -(-C // gs)
+    pad = ng * gs - C
+    hit = torch.nn.functional.pad(hit, (0, pad)).reshape(NB, H, W, ng, gs).any(-1)
+    expect = (hit.int() << torch.arange(ng, dtype=torch.int32)).sum(-1).int()
+    assert torch.equal(act.view(NB, H, W), expect)
+    nz = int(((xp.view(torch.int16) & 0x7fff) != 0).sum())
+    assert int(blk[1].item()) == nz
 
 
 def test_sparseflow_on_nhwc_copy_bitwise(cuda):
