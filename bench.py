@@ -277,56 +277,78 @@ def liveness(fused, x):
 # LIF tails
 # ---------------------------------------------------------------------------
 
-def _tail_row(kernel, shape, timer):
-    s = next(iter(timer.summary().values()))
-    gbps = s["bytes"] / (s["ms_total"] * 1e-3) / 1e9
-    return {"kernel": kernel, "shape": list(shape), "bytes_per_launch": s["bytes"] // s["launches"],
-            "us_per_launch": round(s["ms_avg"] * 1e3, 2), "GB/s": round(gbps, 1),
+def _tail_row(kernel, shape, nbytes, us):
+    gbps = nbytes / (us * 1e-6) / 1e9
+    return {"kernel": kernel, "shape": list(shape), "bytes_per_launch": int(nbytes),
+            "us_per_launch": round(us, 2), "GB/s": round(gbps, 1),
             "frac": round(gbps / PEAK_HBM_GBPS, 4)}
 
 
-def measure_tails(dev, reps=20):
-    """Standalone LIF-family kernels at SEW-RN18 / C1 shapes; GB/s from the
-    algorithmic bytes of each launch and its HIP-event duration."""
+def _time_launches(fn, reps, dev):
+    """Microseconds per call: `reps` calls captured in one HIP graph, the
+    median over 5 replays of the replay time / reps (graph replay keeps the
+    host's launch gaps out; each call still includes its dispatch)."""
+    return _xo_time_graph(fn, reps, 5, dev)
+
+
+TAIL_CASES = [
+    # name, kernel shape [T, B, C, H, W], cf_lif_multistep mode (None: AvgPool2x2-LIF)
+    ("lif", (4, 32, 64, 56, 56), 0),        # C3 layer1 tail: (8T+8)N bytes
+    ("bn_lif", (4, 32, 64, 56, 56), 1),
+    ("add_lif", (4, 32, 64, 56, 56), 3),    # (12T+8)N
+    ("lif", (4, 32, 256, 14, 14), 0),       # C1 tail
+    ("avgpool2x2_lif", (4, 32, 128, 32, 32), None),   # 20T+8 bytes per output neuron
+]
+
+
+def measure_tails(dev, reps=50):
+    """Standalone LIF-family kernels at SEW-RN18 / C1 / VGG shapes: GB/s from
+    the algorithmic bytes of a launch and the average duration of `reps`
+    back-to-back launches."""
     import torch
     from catfuse_amd import runtime
     out = []
     g = torch.Generator(device=dev).manual_seed(0)
-    cases = [
-        ("lif", (4, 32, 64, 56, 56), 0),        # C3 layer1 tail: (8T+8)N
-        ("bn_lif", (4, 32, 64, 56, 56), 1),
-        ("add_lif", (4, 32, 64, 56, 56), 3),    # (12T+8)N
-        ("lif", (4, 32, 256, 14, 14), 0),       # C1 tail
-    ]
-    for name, shape, mode in cases:
+    for name, shape, mode in TAIL_CASES:
         T, B, C, H, W = shape
+        if mode is None:
+            x = torch.rand(shape, device=dev, generator=g)
+            n_out = B * C * (H // 2) * (W // 2)
+            nbytes = T * n_out * 20 + 4 * n_out
+            us = _time_launches(lambda: runtime.avgpool2x2_lif(x), reps, dev)
+            out.append(_tail_row("cf_avgpool2x2_lif", shape, nbytes, us))
+            del x
+            continue
         z = torch.randn(shape, device=dev, generator=g)
         z2 = torch.randn(shape, device=dev, generator=g) if mode in (2, 3, 4) else None
         sc = torch.rand(C, device=dev, generator=g) + 0.5
         sh = torch.randn(C, device=dev, generator=g) * 0.1
         v0 = torch.zeros(B, C, H, W, device=dev)
-        for _ in range(3):
-            runtime.lif_multistep(z, v0, mode=mode, z2=z2, scale=sc, shift=sh, channels=C,
-                                  hw=H * W)
-        timer = runtime.KernelTimer()
-        runtime.set_timer(timer)
-        for _ in range(reps):
-            runtime.lif_multistep(z, v0, mode=mode, z2=z2, scale=sc, shift=sh, channels=C,
-                                  hw=H * W)
-        runtime.set_timer(None)
-        out.append(_tail_row(f"cf_lif_multistep/{name}", shape, timer))
+        N = B * C * H * W
+        nbytes = (8 * T + 8) * N + (4 * T * N if z2 is not None else 0)
+        us = _time_launches(lambda: runtime.lif_multistep(z, v0, mode=mode, z2=z2, scale=sc,
+                                                          shift=sh, channels=C, hw=H * W),
+                            reps, dev)
+        out.append(_tail_row(f"cf_lif_multistep/{name}", shape, nbytes, us))
         del z, z2
-    shape = (4, 32, 128, 32, 32)
-    x = torch.rand(shape, device=dev, generator=g)
-    for _ in range(3):
-        runtime.avgpool2x2_lif(x)
-    timer = runtime.KernelTimer()
-    runtime.set_timer(timer)
-    for _ in range(reps):
-        runtime.avgpool2x2_lif(x)
-    runtime.set_timer(None)
-    out.append(_tail_row("cf_avgpool2x2_lif", shape, timer))
     return out
+
+
+def tails_main(args):
+    """--workload lif_tails: the LIF-family tails alone (one JSON line per
+    kernel), the command the tails' rocprofv3 summaries are taken from."""
+    import torch
+    dev = torch.device("cuda", 0)
+    for row in measure_tails(dev, reps=args.steps * 10):
+        print(json.dumps(row), flush=True)
+    # a plain copy of known size in the same process: the scale of the HBM
+    # traffic counters (FETCH_SIZE / WRITE_SIZE) for the tails' summaries
+    x = torch.ones(64 * 1024 * 1024, device=dev)
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize(dev)
+    print(json.dumps({"calibration_copy_bytes": x.numel() * 4}), flush=True)
 
 
 # ---------------------------------------------------------------------------
@@ -814,7 +836,7 @@ def main():
     ap.add_argument("--eager", action="store_true",
                     help="time eager launches instead of the captured HIP graph")
     ap.add_argument("--workload", default="sew_resnet18",
-                    choices=list(WORKLOADS) + ["sf_crossover"])
+                    choices=list(WORKLOADS) + ["sf_crossover", "lif_tails"])
     ap.add_argument("--xo-shape", type=int, nargs=5, default=[4, 32, 256, 14, 14])
     ap.add_argument("--xo-plain", action="store_true",
                     help="crossover inputs as fp32 tensors (the layer packs them)")
@@ -823,6 +845,9 @@ def main():
         print("bench.py measures one GPU only: every GPU box in this setup has a single "
               "MI355X; run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "lif_tails":
+        tails_main(args)
+        return
     if args.workload == "sf_crossover":
         sf_crossover_main(args)
         return

@@ -17,6 +17,9 @@
 // (off = qoff, koff, voff; one concatenated QKV tensor or three tensors);
 // out is fp16 [T*B][N][cp_out] with head h at channels h*dh ..; v_in / v_out
 // fp32 [B][N][heads*dh].  One workgroup per (b, head), all T steps; dh = 32.
+// An input whose count block (nnz) publishes zero takes the zero route: no
+// operand reads and no MFMAs, z = 0 (the bits Q (K^T V) * scale has for zero
+// operands) into the LIF.
 #include "cf_common.h"
 
 namespace {
@@ -37,6 +40,7 @@ struct AttnArgs {
   int cp_out;
   const float* v_in;
   float* v_out;
+  const unsigned long long* nnz;   // count block of Q, K, V (one tensor), or null
   unsigned long long* nz_out;
   int T, B, N, heads;
   float scale;
@@ -74,6 +78,7 @@ __global__ __launch_bounds__(256) void spike_attention_kernel(AttnArgs a) {
   constexpr int MAXT = NMAX / 32 / 4;       // row tiles per wave at most
   float v[MAXT][16];
   uint32_t anyw = 0u;
+  const bool zero_in = a.nnz != nullptr && cf_count_read(a.nnz) == 0ull;   // uniform
 
   // initial membrane potentials
 #pragma unroll
@@ -98,6 +103,8 @@ __global__ __launch_bounds__(256) void spike_attention_kernel(AttnArgs a) {
     // zeros (out of the buffer's range)
     const __amdgpu_buffer_rsrc_t rq = attn_rsrc(qb, (uint32_t)(((size_t)(N - 1) * a.pitch + DH) * 2));
     h8 qr[MAXT][2];
+    h8 kv0 = {}, kv1 = {};
+    if (!zero_in) {
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
       const int n = (wave + 4 * i) * 32 + col;
@@ -155,16 +162,19 @@ __global__ __launch_bounds__(256) void spike_attention_kernel(AttnArgs a) {
     }
     __syncthreads();
     // Y = Q KV per 32-token row tile; B operand: KV[i][j = col] for i in the step
-    const h8 kv0 = *reinterpret_cast<const h8*>(&kvT[col][8 * hi]);
-    const h8 kv1 = *reinterpret_cast<const h8*>(&kvT[col][16 + 8 * hi]);
+    kv0 = *reinterpret_cast<const h8*>(&kvT[col][8 * hi]);
+    kv1 = *reinterpret_cast<const h8*>(&kvT[col][16 + 8 * hi]);
+    }  // !zero_in
     _Float16* ob = a.out + img * N * a.cp_out + h * DH;
 #pragma unroll
     for (int i = 0; i < MAXT; ++i) {
       const int tile = wave + 4 * i;
       if (tile >= ntile) break;
       f32x16 y = {};
-      y = __builtin_amdgcn_mfma_f32_32x32x16_f16(qr[i][0], kv0, y, 0, 0, 0);
-      y = __builtin_amdgcn_mfma_f32_32x32x16_f16(qr[i][1], kv1, y, 0, 0, 0);
+      if (!zero_in) {
+        y = __builtin_amdgcn_mfma_f32_32x32x16_f16(qr[i][0], kv0, y, 0, 0, 0);
+        y = __builtin_amdgcn_mfma_f32_32x32x16_f16(qr[i][1], kv1, y, 0, 0, 0);
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int nr = tile * 32 + 8 * (r >> 2) + 4 * hi + (r & 3);
@@ -202,7 +212,8 @@ __global__ __launch_bounds__(256) void spike_attention_kernel(AttnArgs a) {
 CF_API int cf_spike_attention_lif(const void* q, const void* k, const void* v, int64_t qoff,
                                   int64_t koff, int64_t voff, int64_t pitch, void* out,
                                   int64_t cp_out, const float* v_in, float* v_out,
-                                  unsigned long long* nz_out, int64_t T, int64_t B, int64_t N,
+                                  const unsigned long long* nnz, unsigned long long* nz_out,
+                                  int64_t T, int64_t B, int64_t N,
                                   int64_t heads, int64_t head_dim, double scale, double tau,
                                   double v_th, double v_reset, int hard_reset, int decay_input,
                                   void* stream) {
@@ -218,7 +229,7 @@ CF_API int cf_spike_attention_lif(const void* q, const void* k, const void* v, i
   a.q = (const _Float16*)q; a.k = (const _Float16*)k; a.v = (const _Float16*)v;
   a.qoff = (int)qoff; a.koff = (int)koff; a.voff = (int)voff; a.pitch = (int)pitch;
   a.out = (_Float16*)out; a.cp_out = (int)cp_out; a.v_in = v_in; a.v_out = v_out;
-  a.nz_out = nz_out; a.T = (int)T; a.B = (int)B; a.N = (int)N; a.heads = (int)heads;
+  a.nnz = nnz; a.nz_out = nz_out; a.T = (int)T; a.B = (int)B; a.N = (int)N; a.heads = (int)heads;
   a.scale = (float)scale;
   a.lif = cf_make_lif_params(tau, v_th, v_reset, hard_reset, decay_input);
   const dim3 grid((unsigned)(B * heads)), block(256);

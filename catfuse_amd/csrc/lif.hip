@@ -3,7 +3,9 @@
 // One thread owns 4 consecutive neurons for all T steps: the membrane
 // potential v stays in VGPRs across the time loop (TimeBlock(K=T) with
 // StateCarry through v_in/v_out), z is read once per step with dwordx4
-// loads, spikes are written once per step.  Algorithmic bytes per neuron:
+// loads, spikes are written once per step.  The loads of up to four steps
+// are issued before the first of them is used, so a thread waits for one
+// memory latency per four steps, not one per step.  Algorithmic bytes per neuron:
 //   mode 0/1 : (8T + 8)  (z, spike, v_in, v_out)
 //   mode 2-4 : (12T + 8) (z, z2, spike, v_in, v_out)
 //
@@ -36,6 +38,30 @@ template <typename S> __device__ __forceinline__ S to_spike(float s);
 template <> __device__ __forceinline__ float to_spike<float>(float s) { return s; }
 template <> __device__ __forceinline__ uint8_t to_spike<uint8_t>(float s) { return (uint8_t)s; }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Streamed operands (read or written once per launch).  NT: non-temporal
+// accesses, which measured faster for the two-input modes (three streams)
+// and slower for the one-input modes on gfx950.
+template <bool NT>
+__device__ __forceinline__ float4 load_stream(const float* p) {
+  if constexpr (NT) {
+    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p));
+    return make_float4(v[0], v[1], v[2], v[3]);
+  } else {
+    return *reinterpret_cast<const float4*>(p);
+  }
+}
+template <bool NT>
+__device__ __forceinline__ void store_stream(float* p, float a, float b, float c, float d) {
+  if constexpr (NT) {
+    const f32x4 v = {a, b, c, d};
+    __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
+  } else {
+    *reinterpret_cast<float4*>(p) = make_float4(a, b, c, d);
+  }
+}
+
 template <int MODE, typename S, int LM>
 __global__ __launch_bounds__(256) void lif_stream_vec4(
     const float* __restrict__ z, const float* __restrict__ z2,
@@ -65,27 +91,40 @@ __global__ __launch_bounds__(256) void lif_stream_vec4(
     const float v0 = lif_initial_v(p);
     v[0] = v[1] = v[2] = v[3] = v0;
   }
-  for (int t = 0; t < T; ++t) {
-    const int64_t off = (int64_t)t * N + n0;
-    const float4 zz = *reinterpret_cast<const float4*>(z + off);
-    float4 z2v = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (MODE == M_BN_ADD || MODE == M_ADD || MODE == M_ADD_BN)
-      z2v = *reinterpret_cast<const float4*>(z2 + off);
-    const float zi[4] = {zz.x, zz.y, zz.z, zz.w};
-    const float z2i[4] = {z2v.x, z2v.y, z2v.z, z2v.w};
-    float s[4];
+  constexpr bool TWO = MODE == M_BN_ADD || MODE == M_ADD || MODE == M_ADD_BN;
+  constexpr int TC = 4;   // steps whose loads are in flight together
+  for (int t0 = 0; t0 < T; t0 += TC) {
+    float4 zz[TC], z2v[TC];
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const float x = input_current<MODE>(zi[j], z2i[j], sc[j], sh[j]);
-      v[j] = lif_charge_m<LM>(v[j], x, p);
-      s[j] = lif_fire_reset_bit<LM>(v[j], p) ? 1.0f : 0.0f;
+    for (int u = 0; u < TC; ++u) {
+      zz[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      z2v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
+      if (t0 + u < T) {
+        const int64_t off = (int64_t)(t0 + u) * N + n0;
+        zz[u] = load_stream<TWO>(z + off);
+        if (TWO) z2v[u] = load_stream<TWO>(z2 + off);
+      }
     }
-    if constexpr (sizeof(S) == 4) {
-      *reinterpret_cast<float4*>(spike + off) = make_float4(s[0], s[1], s[2], s[3]);
-    } else {
-      uchar4 o;
-      o.x = (uint8_t)s[0]; o.y = (uint8_t)s[1]; o.z = (uint8_t)s[2]; o.w = (uint8_t)s[3];
-      *reinterpret_cast<uchar4*>(spike + off) = o;
+#pragma unroll
+    for (int u = 0; u < TC; ++u) {
+      if (t0 + u >= T) break;
+      const int64_t off = (int64_t)(t0 + u) * N + n0;
+      const float zi[4] = {zz[u].x, zz[u].y, zz[u].z, zz[u].w};
+      const float z2i[4] = {z2v[u].x, z2v[u].y, z2v[u].z, z2v[u].w};
+      float s[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float x = input_current<MODE>(zi[j], z2i[j], sc[j], sh[j]);
+        v[j] = lif_charge_m<LM>(v[j], x, p);
+        s[j] = lif_fire_reset_bit<LM>(v[j], p) ? 1.0f : 0.0f;
+      }
+      if constexpr (sizeof(S) == 4) {
+        store_stream<TWO>(spike + off, s[0], s[1], s[2], s[3]);
+      } else {
+        uchar4 o;
+        o.x = (uint8_t)s[0]; o.y = (uint8_t)s[1]; o.z = (uint8_t)s[2]; o.w = (uint8_t)s[3];
+        *reinterpret_cast<uchar4*>(spike + off) = o;
+      }
     }
   }
   if (v_out) *reinterpret_cast<float4*>(v_out + n0) = make_float4(v[0], v[1], v[2], v[3]);

@@ -491,15 +491,18 @@ def maxpool_nhwc(x: torch.Tensor, kernel_size: int, stride: int, padding: int,
 def spike_attention_lif(qkv: torch.Tensor, T: int, B: int, N: int, heads: int, offsets,
                         scale: float, tau=2.0, v_threshold=1.0, v_reset=0.0, decay_input=True,
                         v_in: Optional[torch.Tensor] = None, want_v_out=True,
-                        nz_out: Optional[torch.Tensor] = None, gen_cell: Optional[list] = None):
+                        nz_out: Optional[torch.Tensor] = None, gen_cell: Optional[list] = None,
+                        nnz: Optional[torch.Tensor] = None):
     """Spikformer's SSA core on the fp16 token copy qkv [T*B*N, pitch] that
     holds Q, K, V at channel offsets (qoff, koff, voff) (head h at
     off + 32h ..): LIF_T(((Q K^T) V) * scale) per head, evaluated as
-    Q (K^T V) on the matrix cores.  Returns (TokenSpikes [T, B, N, heads*32],
+    Q (K^T V) on the matrix cores; nnz: the copy's count block (a zero count
+    skips the products: z = 0).  Returns (TokenSpikes [T, B, N, heads*32],
     carrying the count block nz_out when it and gen_cell are given, so the
     next fused linear routes on it; v_out [B, N, heads*32] or None)."""
     require_gpu_tensor(qkv, "qkv", dtype=torch.float16)
     _require_block(nz_out)
+    _require_block(nnz)
     dev = qkv.device
     pitch = qkv.shape[-1]
     C = heads * 32
@@ -516,7 +519,7 @@ def spike_attention_lif(qkv: torch.Tensor, T: int, B: int, N: int, heads: int, o
     ev = _t0()
     check(_hip.lib().cf_spike_attention_lif(
         ptr(qkv), ptr(qkv), ptr(qkv), qoff, koff, voff, pitch, ptr(copy), cp, ptr(v_in),
-        ptr(v_out), ptr(nz_out), T, B, N, heads, 32, float(scale),
+        ptr(v_out), ptr(nnz), ptr(nz_out), T, B, N, heads, 32, float(scale),
         *_lif_args(tau, v_threshold, v_reset, decay_input), _hip.stream(dev)),
         "cf_spike_attention_lif")
     _t1("spike_attention", ev, flops=4 * T * B * heads * N * 32 * 32,

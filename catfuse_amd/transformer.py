@@ -192,7 +192,7 @@ class CTFSpikformerSSA(CTFPattern):
                                        tau=lp["tau"], v_threshold=lp["v_threshold"],
                                        v_reset=lp["v_reset"], decay_input=lp["decay_input"],
                                        v_in=v_in, nz_out=self._attn_block(x.device),
-                                       gen_cell=self._attn_gen)
+                                       gen_cell=self._attn_gen, nnz=count_of(qkv))
         else:
             a, v = self._gemm_core(qkv, v_in)
         self.attn_state.set(v)

@@ -144,14 +144,17 @@ int cf_tokens_to_f32(const void* xp, float* out, int64_t rows, int64_t C, int64_
  * are fp16 token copies [T*B][N][pitch] with head h at channel
  * off + 32h (off = qoff / koff / voff; q, k, v may be one concatenated QKV
  * tensor); out fp16 [T*B][N][cp_out] (head h at channel 32h); v_in / v_out
- * fp32 [B][N][heads*32] (nullable); nz_out (nullable): count block of the
- * output (workgroups with a spike).  N <= 256.  Replaces the SSA core of
+ * fp32 [B][N][heads*32] (nullable); nnz (nullable): count block of the Q, K,
+ * V tensor (one concatenated tensor): a published count of zero takes the
+ * zero route (no operand reads, no MFMAs, z = 0); nz_out (nullable): count
+ * block of the output (workgroups with a spike).  N <= 256.  Replaces the SSA core of
  * models/spikformer_github.py:139-160 (q @ k^T * scale, @ v, attn_lif) and
  * the reference's spike-matmul kernels (sparseflow/sparse_bmm_kernel.py:40-358,
  * sparse_attention_kernel.py:24-118). */
 int cf_spike_attention_lif(const void* q, const void* k, const void* v, int64_t qoff,
                            int64_t koff, int64_t voff, int64_t pitch, void* out, int64_t cp_out,
-                           const float* v_in, float* v_out, unsigned long long* nz_out,
+                           const float* v_in, float* v_out, const unsigned long long* nnz,
+                           unsigned long long* nz_out,
                            int64_t T, int64_t B, int64_t N, int64_t heads, int64_t head_dim,
                            double scale, double tau, double v_th, double v_reset, int hard_reset,
                            int decay_input, void* stream);

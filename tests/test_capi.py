@@ -122,7 +122,7 @@ def test_token_and_pool_entry_points_validate_arguments():
 
     def attention(N=196, heads=2, head_dim=32, pitch=192, qoff=0, cp_out=64):
         return L.cf_spike_attention_lif(1, 1, 1, qoff, 64, 128, pitch, 1, cp_out, None, None,
-                                        None, 4, 2, N, heads, head_dim, 0.125, *lif, None)
+                                        None, None, 4, 2, N, heads, head_dim, 0.125, *lif, None)
     assert attention(head_dim=64) == INVALID        # one 32-wide MFMA tile per head
     assert attention(N=300) == INVALID              # more tokens than the kernel stages
     assert attention(qoff=160) == INVALID           # Q heads beyond the pitch

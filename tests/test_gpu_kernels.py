@@ -52,7 +52,7 @@ LIF_VARIANTS = [
 
 @pytest.mark.parametrize("variant", range(len(LIF_VARIANTS)))
 @pytest.mark.parametrize("mode", [0, 1, 2, 3, 4])
-@pytest.mark.parametrize("shape", [(4, 2, 16, 7, 9), (4, 3, 8, 8, 8)])
+@pytest.mark.parametrize("shape", [(4, 2, 16, 7, 9), (4, 3, 8, 8, 8), (7, 2, 4, 5, 8)])
 def test_lif_multistep_bit_exact(cuda, variant, mode, shape):
     from catfuse_amd import runtime
     p = LIF_VARIANTS[variant]
@@ -91,18 +91,27 @@ def test_lif_sequential_api(cuda):
     np.testing.assert_array_equal(v.cpu().numpy(), v_ref)
 
 
-@pytest.mark.parametrize("shape", [(4, 2, 8, 16, 16), (3, 1, 5, 7, 9)])
-def test_avgpool2x2_lif_bit_exact(cuda, shape):
+@pytest.mark.parametrize("shape", [(4, 2, 8, 16, 16), (3, 1, 5, 7, 9), (5, 2, 3, 9, 12),
+                                   (9, 1, 4, 8, 20)])
+@pytest.mark.parametrize("variant", [0, 2, 5])
+def test_avgpool2x2_lif_bit_exact(cuda, shape, variant):
+    """Both kernels (two outputs per thread when W is a multiple of 4, else
+    one), steps beyond a 4-step load chunk, odd heights, every LIF
+    specialisation, a carried membrane and uint8 spikes."""
     from catfuse_amd import runtime
-    g = _gen(11)
+    p = LIF_VARIANTS[variant]
+    g = _gen(11 + variant)
     x = torch.rand(shape, generator=g) * 3
     T, B, C, H, W = shape
     z = torch.nn.functional.avg_pool2d(x.flatten(0, 1), 2, 2)
     z = z.reshape(T, B, C, H // 2, W // 2)
-    s_ref, v_ref, _ = oracle.lif_multistep(z)
-    s, v = runtime.avgpool2x2_lif(x.to(cuda))
+    v0 = torch.rand(B, C, H // 2, W // 2, generator=g) * 0.5
+    s_ref, v_ref, _ = oracle.lif_multistep(z, v0, **p)
+    s, v = runtime.avgpool2x2_lif(x.to(cuda), v0.to(cuda), **p)
     np.testing.assert_array_equal(s.cpu().numpy(), s_ref)
     np.testing.assert_array_equal(v.cpu().numpy(), v_ref)
+    s8, v8 = runtime.avgpool2x2_lif(x.to(cuda), v0.to(cuda), spike_dtype=torch.uint8, **p)
+    assert torch.equal(s8.float(), s) and torch.equal(v8, v)
 
 
 # ---------------------------------------------------------------------------

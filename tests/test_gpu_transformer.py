@@ -116,6 +116,27 @@ def test_spike_attention_parity(cuda, N, heads, T, scale):
     assert torch.equal(torch.cat([out1, out2]).cpu(), out.cpu())
 
 
+def test_spike_attention_zero_route_bitwise(cuda):
+    """A Q, K, V copy whose count block publishes zero takes the zero route
+    (no operand reads, z = 0); with a carried membrane (so the LIF still
+    spikes) it equals the full evaluation of the same zero input bit for
+    bit, and a nonzero published count takes the full evaluation."""
+    from catfuse_amd import runtime
+    T, B, N, heads = 4, 3, 100, 2
+    C = heads * 32
+    copy = torch.zeros((T * B * N, 3 * C), dtype=torch.float16, device=cuda)
+    v_in = (torch.rand(B, N, C, generator=_gen(3)) * 4.0).to(cuda)   # half charges past 1
+    ref, v_ref = runtime.spike_attention_lif(copy, T, B, N, heads, (0, C, 2 * C), 0.125,
+                                             v_in=v_in)
+    for count in (0, 7):
+        blk = runtime.count_block(cuda)
+        blk[1] = count
+        out, v_out = runtime.spike_attention_lif(copy, T, B, N, heads, (0, C, 2 * C), 0.125,
+                                                 v_in=v_in, nnz=blk)
+        assert torch.equal(out, ref) and torch.equal(v_out, v_ref)
+    assert bool(ref.any()) and not bool(ref.all())
+
+
 def _small_spikformer(seed=41):
     from catfuse_amd import snn
     m = snn.Spikformer(img_size=32, num_classes=10, embed_dim=64, num_heads=2, depth=2, T=4,
