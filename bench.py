@@ -171,11 +171,12 @@ def _agg(kern, names):
             sum(d.get("bytes", 0) for d in ds), sum(d.get("launches", 0) for d in ds))
 
 
-def conv_roofline(kern, steps, names=("conv_mfma", "conv_mfma_sparse"), traffic=None):
+def conv_roofline(kern, steps, names=("conv_mfma", "conv_mfma_sparse", "conv_pair"),
+                  traffic=None):
     tot_ms, tot_fl, _, launches = _agg(kern, names)
     achieved = tot_fl / (tot_ms * 1e-3) / 1e12 if tot_ms else 0.0
-    return {"kernel": "conv_halo_kernel (cf_conv_mfma fused Conv-BN-LIF), launches that run "
-                      "the MFMA K loop",
+    return {"kernel": "conv_halo_kernel and conv_halo_pair_kernel (cf_conv_mfma / "
+                      "cf_conv_halo_pair fused Conv-BN-LIF), launches that run the MFMA K loop",
             "bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_FP16_TFLOPS,
             "unit": "TFLOP/s", "frac": round(achieved / PEAK_FP16_TFLOPS, 4),
             "traffic": traffic,
@@ -185,7 +186,8 @@ def conv_roofline(kern, steps, names=("conv_mfma", "conv_mfma_sparse"), traffic=
 
 
 def staticzero_summary(kern, steps, names=("conv_mfma_staticzero",
-                                          "conv_mfma_sparse_staticzero")):
+                                          "conv_mfma_sparse_staticzero",
+                                          "conv_pair_staticzero")):
     z_ms, _, z_bytes, z_n = _agg(kern, names)
     gbps = z_bytes / (z_ms * 1e-3) / 1e9 if z_ms else 0.0
     return {"kernel": "conv_halo_kernel on the StaticZero route (all-zero input: BN bias -> "
@@ -198,6 +200,9 @@ def staticzero_summary(kern, steps, names=("conv_mfma_staticzero",
             "frac": round(gbps / PEAK_HBM_GBPS, 4)}
 
 
+CONV_LAUNCHES = ("conv_mfma", "conv_pair")   # timer names of the halo-kernel conv launches
+
+
 def route_sequence(timer, prefix, steps):
     """Route of each launch named prefix* in one forward, in launch order
     (D: the MFMA K loop ran, Z: StaticZero), read back from the devices'
@@ -207,7 +212,8 @@ def route_sequence(timer, prefix, steps):
     return "".join("Z" if (r[5] is not None and r[5].is_zero()) else "D" for r in recs[:per])
 
 
-def per_layer_table(res, kernels=("conv_mfma", "conv_stem", "conv_direct", "linear_tokens")):
+def per_layer_table(res, kernels=("conv_mfma", "conv_pair", "conv_stem", "conv_direct",
+                                  "linear_tokens")):
     """One row per conv / linear launch of one forward (averaged over the
     eager steps): layer path, kernel, route, us, dense-equivalent TFLOP/s and
     fraction of the MFMA peak."""
@@ -446,7 +452,7 @@ def sew_result(args, dev):
     kern = res["timer"].summary()
     roof = conv_roofline(kern, args.steps, traffic=traffic_from_profiles())
     sz = staticzero_summary(kern, args.steps)
-    sz["conv_route_sequence"] = route_sequence(res["timer"], "conv_mfma", args.steps)
+    sz["conv_route_sequence"] = route_sequence(res["timer"], CONV_LAUNCHES, args.steps)
     result = _base_result(args, res, stats, "sew_resnet18_adds_T4_B32_224")
     result.update(roofline=roof, staticzero_convs=sz, per_layer=per_layer_table(res),
                   kernels=_per_kernel(kern, args.steps))
@@ -464,7 +470,7 @@ def live_result(args, dev):
     kern = res["timer"].summary()
     roof = conv_roofline(kern, args.steps)
     rows = per_layer_table(res)
-    mfma3 = [r for r in rows if r["kernel"] == "conv_mfma" and r["route"] == "D"]
+    mfma3 = [r for r in rows if r["kernel"] in CONV_LAUNCHES and r["route"] == "D"]
     return {"v_threshold": LIVE_V_THRESHOLD,
             "liveness": {"alive_fraction": round(frac, 4), "required": LIVE_MIN_FRACTION,
                          "ok": frac >= LIVE_MIN_FRACTION, "block_spike_rates": rates},
@@ -472,7 +478,7 @@ def live_result(args, dev):
             "ms_per_step": round(res["ms"], 4), "mode": res["mode"],
             "eager_ms_per_step": round(res["ms_eager"], 4),
             "roofline": roof,
-            "conv_route_sequence": route_sequence(res["timer"], "conv_mfma", args.steps),
+            "conv_route_sequence": route_sequence(res["timer"], CONV_LAUNCHES, args.steps),
             "min_conv_frac": min((r["frac"] for r in mfma3), default=None),
             "per_layer": rows, "kernels": _per_kernel(kern, args.steps)}
 

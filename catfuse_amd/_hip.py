@@ -49,6 +49,10 @@ _SIGNATURES = {
                      c_double,
                      _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                      c_int, c_double, c_double, c_double, c_int, c_int, _P],
+    "cf_conv_halo_pair": [_P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
+                          _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I,
+                          _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I,
+                          c_double, c_double, c_double, c_int, c_int, _P],
     "cf_pack_stem_weights": [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P],
     "cf_conv_stem_lif_maxpool": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I,
                                  _I, _I, _I, _I, _I, _I, _I, _I, c_double, c_double, c_double,

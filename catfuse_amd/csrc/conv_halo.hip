@@ -951,21 +951,21 @@ hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
 
 }  // namespace
 
-// 3x3 convolutions (stride 1 or 2, any padding) with halo staging; the
-// caller picks the tile (tile_h x tile_w in {8x8, 8x16}; 8x16 only with
-// stride 1).  Arguments as cf_conv_mfma.
-CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
-                        const float* beta, const float* v_in, float* v_out, float* out,
-                        void* out_nhwc, int64_t cp_out,
-                        const float* identity, const void* identity_nhwc, int64_t cp_id,
-                        int identity_mode, const int32_t* ag_mask, const int32_t* tile_order,
-                        const unsigned long long* nnz, unsigned long long* nz_out,
-                        int64_t numel, double sparse_threshold,
-                        int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
-                        int64_t W, int64_t Ho, int64_t Wo, int64_t ksize, int64_t stride,
-                        int64_t pad, int64_t tile_h, int64_t tile_w, int64_t group_size,
-                        int epilogue, double tau, double v_th, double v_reset, int hard_reset,
-                        int decay_input, void* stream) {
+namespace {
+
+// Checks the arguments of one halo conv and fills its HaloArgs; 0 or a
+// hipError_t (as int).
+int make_halo_args(HaloArgs& a, const void* x, const void* w_packed, const float* alpha,
+                   const float* beta, const float* v_in, float* v_out, float* out,
+                   void* out_nhwc, int64_t cp_out, const float* identity,
+                   const void* identity_nhwc, int64_t cp_id, int identity_mode,
+                   const int32_t* ag_mask, const int32_t* tile_order,
+                   const unsigned long long* nnz, unsigned long long* nz_out, int64_t numel,
+                   double sparse_threshold, int64_t T, int64_t B, int64_t Cp, int64_t Cout,
+                   int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo, int64_t ksize,
+                   int64_t stride, int64_t pad, int64_t tile_h, int64_t tile_w,
+                   int64_t group_size, int epilogue, double tau, double v_th, double v_reset,
+                   int hard_reset, int decay_input) {
   if (!x || !w_packed || !alpha || !beta || (!out && !out_nhwc)) return (int)hipErrorInvalidValue;
   if (ksize != 1 && ksize != 3) return (int)hipErrorInvalidValue;
   if (out_nhwc && (cp_out < Cout || cp_out > Coutp)) return (int)hipErrorInvalidValue;
@@ -996,7 +996,6 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
   // The membrane state passes from one time block to the next through v_out.
   const int tb = (stride == 2 && ksize == 3) ? halo_tb<2, 3>() : halo_tb<1, 3>();
   if (epilogue == EPI_LIF && !v_out && T > tb) return (int)hipErrorInvalidValue;
-  HaloArgs a;
   a.x = (const _Float16*)x; a.w = (const _Float16*)w_packed; a.alpha = alpha; a.beta = beta;
   a.v_in = v_in; a.v_out = v_out; a.out = out; a.identity = identity;
   a.identity_nhwc = (const _Float16*)identity_nhwc; a.cp_id = (int)cp_id;
@@ -1013,6 +1012,55 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
   a.gs = group_size > 0 ? (int)group_size : 32;
   a.gs_shift = (a.gs & (a.gs - 1)) == 0 ? __builtin_ctz((unsigned)a.gs) : -1;
   a.lif = cf_make_lif_params(tau, v_th, v_reset, hard_reset, decay_input);
+  return 0;
+}
+
+// A stride-2 3x3 conv and a stride-2 1x1 conv of the same input (a
+// ResNet block's conv1 and its downsample) in one grid: workgroups
+// 0 .. nLa-1 run the 3x3 conv's tiles, the rest the 1x1 conv's (whose input
+// pixels are the 3x3 conv's centre taps), each as its own launch would (same
+// accumulation order, so the same bits), sharing the input through the L2.
+// Lean LIF epilogues only (fp16 NHWC outputs, no identity).
+template <int LM, bool OBA, bool OBB>
+__global__ __launch_bounds__(256, (halo_min_blocks<8, 8>()))
+void conv_halo_pair_kernel(HaloArgs a, HaloArgs b, int nLa) {
+  constexpr int HA = halo_buf_halves<8, 8, 2, 3>(), HBB = halo_buf_halves<8, 8, 2, 1>();
+  __shared__ __attribute__((aligned(16))) _Float16 halo[2 * (HA > HBB ? HA : HBB)];
+  __shared__ __attribute__((aligned(16))) float bn_s[2][64];
+  __shared__ unsigned any_sh[4];
+  const int L = (int)blockIdx.x;
+  if (L < nLa)
+    halo_body<8, 8, 2, 3, EPI_LIF, LM, true, OBA, false>(a, L, nLa, halo, bn_s, any_sh);
+  else
+    halo_body<8, 8, 2, 1, EPI_LIF, LM, true, OBB, false>(b, L - nLa, (int)gridDim.x - nLa, halo,
+                                                         bn_s, any_sh);
+}
+
+}  // namespace
+
+// 3x3 convolutions (stride 1 or 2, any padding) with halo staging; the
+// caller picks the tile (tile_h x tile_w in {8x8, 8x16}; 8x16 only with
+// stride 1).  Arguments as cf_conv_mfma.
+CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
+                        const float* beta, const float* v_in, float* v_out, float* out,
+                        void* out_nhwc, int64_t cp_out,
+                        const float* identity, const void* identity_nhwc, int64_t cp_id,
+                        int identity_mode, const int32_t* ag_mask, const int32_t* tile_order,
+                        const unsigned long long* nnz, unsigned long long* nz_out,
+                        int64_t numel, double sparse_threshold,
+                        int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
+                        int64_t W, int64_t Ho, int64_t Wo, int64_t ksize, int64_t stride,
+                        int64_t pad, int64_t tile_h, int64_t tile_w, int64_t group_size,
+                        int epilogue, double tau, double v_th, double v_reset, int hard_reset,
+                        int decay_input, void* stream) {
+  HaloArgs a;
+  const int rc = make_halo_args(a, x, w_packed, alpha, beta, v_in, v_out, out, out_nhwc, cp_out,
+                                identity, identity_nhwc, cp_id, identity_mode, ag_mask,
+                                tile_order, nnz, nz_out, numel, sparse_threshold, T, B, Cp, Cout,
+                                Coutp, H, W, Ho, Wo, ksize, stride, pad, tile_h, tile_w,
+                                group_size, epilogue, tau, v_th, v_reset, hard_reset,
+                                decay_input);
+  if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
   hipError_t e;
   if (ksize == 1)
@@ -1024,4 +1072,52 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
   else
     e = launch_halo<8, 8, 2>(a, epilogue, st);
   return (int)e;
+}
+
+CF_API int cf_conv_halo_pair(
+    const void* x, const unsigned long long* nnz, int64_t numel, int64_t T, int64_t B,
+    int64_t Cp, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
+    const void* w_a, const float* alpha_a, const float* beta_a, const float* v_in_a,
+    float* v_out_a, void* out_a, int64_t cp_out_a, unsigned long long* nz_a, int64_t Cout_a,
+    int64_t Coutp_a, int64_t pad_a,
+    const void* w_b, const float* alpha_b, const float* beta_b, const float* v_in_b,
+    float* v_out_b, void* out_b, int64_t cp_out_b, unsigned long long* nz_b, int64_t Cout_b,
+    int64_t Coutp_b, int64_t pad_b,
+    double tau, double v_th, double v_reset, int hard_reset, int decay_input, void* stream) {
+  if (!out_a || !out_b || Cout_a % 32 != 0 || Cout_b % 32 != 0) return (int)hipErrorInvalidValue;
+  HaloArgs a, b;
+  int rc = make_halo_args(a, x, w_a, alpha_a, beta_a, v_in_a, v_out_a, nullptr, out_a, cp_out_a,
+                          nullptr, nullptr, 0, 0, nullptr, nullptr, nnz, nz_a, numel, 2.0, T, B,
+                          Cp, Cout_a, Coutp_a, H, W, Ho, Wo, 3, 2, pad_a, 8, 8, 0, EPI_LIF, tau,
+                          v_th, v_reset, hard_reset, decay_input);
+  if (rc) return rc;
+  rc = make_halo_args(b, x, w_b, alpha_b, beta_b, v_in_b, v_out_b, nullptr, out_b, cp_out_b,
+                      nullptr, nullptr, 0, 0, nullptr, nullptr, nnz, nz_b, numel, 2.0, T, B, Cp,
+                      Cout_b, Coutp_b, H, W, Ho, Wo, 1, 2, pad_b, 8, 8, 0, EPI_LIF, tau, v_th,
+                      v_reset, hard_reset, decay_input);
+  if (rc) return rc;
+  // each part's workgroup count as its own launch (below 2^23 together)
+  const int64_t nLa = B * a.GH * a.GW * (Coutp_a / 64), nLb = B * b.GH * b.GW * (Coutp_b / 64);
+  if (nLa + nLb >= ((int64_t)1 << 23)) return (int)hipErrorInvalidValue;
+  const dim3 grid((unsigned)(nLa + nLb)), block(256);
+  hipStream_t st = (hipStream_t)stream;
+  const int lm = cf_lif_mode(a.lif);
+  const int ob = T <= halo_tb<2, 3>() ? 2 : (T <= halo_tb<2, 1>() ? 1 : 0);
+#define CF_PAIR(LMV)                                                                          \
+  do {                                                                                        \
+    if (ob == 2)                                                                              \
+      hipLaunchKernelGGL((conv_halo_pair_kernel<LMV, true, true>), grid, block, 0, st, a, b,   \
+                         (int)nLa);                                                           \
+    else if (ob == 1)                                                                         \
+      hipLaunchKernelGGL((conv_halo_pair_kernel<LMV, false, true>), grid, block, 0, st, a, b,  \
+                         (int)nLa);                                                           \
+    else                                                                                      \
+      hipLaunchKernelGGL((conv_halo_pair_kernel<LMV, false, false>), grid, block, 0, st, a, b, \
+                         (int)nLa);                                                           \
+  } while (0)
+  if (lm == LM_HARD0_DECAY_P2) CF_PAIR(LM_HARD0_DECAY_P2);
+  else if (lm == LM_HARD_DECAY_P2) CF_PAIR(LM_HARD_DECAY_P2);
+  else CF_PAIR(LM_GENERIC);
+#undef CF_PAIR
+  return (int)hipGetLastError();
 }

@@ -24,6 +24,7 @@ from typing import Optional
 import torch
 import torch.nn as nn
 
+from catfuse_amd import runtime
 from catfuse_amd.hardware import runtime_profile
 from catfuse_amd.implementations import ConvLIFParams, ConvLIFSpec, DenseKeep, StreamFuse
 from catfuse_amd.runtime import (EPI_Z, ID_ADD_SPIKE, ID_ADD_Z, ConvLIFRunner,
@@ -197,6 +198,11 @@ class _ConvPattern(CTFPattern):
                                 decay_input=self.decay_input, bn_eps=self.bn_eps)
         self._params = None
         self._params_key = None
+        # a paired launch with a downsample of the same input (CTFSEWBasicBlock):
+        # _pair_with = (partner, x) for the next call, _pair_result = (x, out)
+        # left for the partner's call
+        self._pair_with = None
+        self._pair_result = None
 
     def _bn_tensors(self):
         return None
@@ -276,6 +282,15 @@ class PartialFusionConvBNLIF(_ConvPattern):
         return (self.bn_weight, self.bn_bias, self.running_mean, self.running_var)
 
     def forward(self, x, sew_identity=None):
+        pr, self._pair_result = self._pair_result, None
+        if pr is not None and pr[0] is x and sew_identity is None:
+            return pr[1]                   # computed by the partner's paired launch
+        pw, self._pair_with = self._pair_with, None
+        if pw is not None and pw[1] is x and sew_identity is None:
+            res = _paired_forward(self, pw[0], x)
+            if res is not None:
+                pw[0]._pair_result = (x, res[1])
+                return res[0]
         if sew_identity is not None:
             return self._run(self._impl, x, identity=sew_identity, identity_mode=ID_ADD_SPIKE)
         return self._run(self._impl, x)
@@ -715,10 +730,39 @@ def _conv_bn_lif_from(conv, bn, lif, K=None):
     return PartialFusionConvBNLIF.from_sj_modules(conv, bn, lif)
 
 
+def _paired_forward(fa, fb, x):
+    """fa (3x3, stride 2) and fb (1x1, stride 2) of the same input in one
+    cf_conv_halo_pair launch when both run the fused dense conv on a spike
+    input the pair kernel covers: (out_a, out_b), each module's state set as
+    its own call would; None otherwise."""
+    ia, ib = fa._impl, fb._impl
+    if type(ia) is not StreamFuse or type(ib) is not StreamFuse or x.ndim != 5:
+        return None
+    ia.check_input(x, fa.spec)
+    ib.check_input(x, fb.spec)
+    if ia.input_is_analog(x) or ib.input_is_analog(x):
+        return None
+    ra = ia.runner(fa.spec, fa._ensure_params(), x.device)
+    rb = ib.runner(fb.spec, fb._ensure_params(), x.device)
+    if not runtime.halo_pair_supported(ra, rb, x):
+        return None
+    B = x.shape[1]
+    Ho, Wo = fa.spec.output_hw(x.shape[3], x.shape[4])
+    va = fa.state.peek((B, fa.out_channels, Ho, Wo), x.device)
+    vb = fb.state.peek((B, fb.out_channels, Ho, Wo), x.device)
+    out_a, v_a, out_b, v_b = runtime.run_halo_pair(ra, rb, x.contiguous(), va, vb)
+    fa.state.set(v_a)
+    fb.state.set(v_b)
+    return out_a, out_b
+
+
 class CTFSEWBasicBlock(CTFPattern):
     """SEW-ResNet BasicBlock: out = sew(identity, LIF(BN(conv2(LIF(BN(conv1 x))))))
     with identity = downsample_sn(downsample(x)) or x; for cnf='ADD' the add
-    is done in conv2's epilogue."""
+    is done in conv2's epilogue.  A stride-2 conv1 and its 1x1 downsample
+    run as one paired launch (cf_conv_halo_pair): conv1's call computes
+    both, the downsample's call returns its half (each module is still
+    called, so its hooks run)."""
 
     def __init__(self, fused_first, fused_second, fused_downsample, cnf):
         super().__init__()
@@ -728,8 +772,13 @@ class CTFSEWBasicBlock(CTFPattern):
         self.cnf = cnf
 
     def forward(self, x):
-        out = self.fused_first(x)
-        identity = self.fused_downsample(x) if self.fused_downsample is not None else x
+        first, ds = self.fused_first, self.fused_downsample
+        if (ds is not None and isinstance(first, PartialFusionConvBNLIF)
+                and isinstance(ds, PartialFusionConvBNLIF) and first.stride == 2):
+            first._pair_with = (ds, x)
+        out = first(x)
+        first._pair_with = None
+        identity = ds(x) if ds is not None else x
         second = self.fused_second
         if (self.cnf == "ADD" and getattr(second, "supports_sew_identity", lambda: False)()
                 and identity.shape[:2] == out.shape[:2]):

@@ -1044,6 +1044,81 @@ class ConvLIFRunner:
         return out, v_out
 
 
+def halo_pair_supported(ra: "ConvLIFRunner", rb: "ConvLIFRunner", x: torch.Tensor) -> bool:
+    """Whether cf_conv_halo_pair computes ra (3x3, stride 2) and rb (1x1,
+    stride 2) of x [T, B, Cin, H, W] in one launch: same input channels,
+    output size and LIF parameters, whole 32-channel outputs, the shapes
+    the halo kernel covers."""
+    if x.dim() != 5 or not x.is_cuda or x.dtype != torch.float32:
+        return False
+    T, B, C, H, W = x.shape
+    if (ra.KH, ra.KW, rb.KH, rb.KW) != (3, 3, 1, 1) or ra.stride != 2 or rb.stride != 2:
+        return False
+    if ra.Cin != C or rb.Cin != C or ra.lif != rb.lif or ra.Cout % 32 or rb.Cout % 32:
+        return False
+    if ra.padding > 2 or rb.padding > 2 or ra.Cp // 32 > 64:
+        return False
+    Ho, Wo = ra.out_hw(H, W)
+    if rb.out_hw(H, W) != (Ho, Wo) or Ho < 4 or Wo < 4:
+        return False
+    return T * B * max(ra.Cout, rb.Cout) * Ho * Wo <= 2 ** 31 - 1 and 4 * B * H * W * ra.Cp < 2 ** 31
+
+
+def run_halo_pair(ra: "ConvLIFRunner", rb: "ConvLIFRunner", x: torch.Tensor, v_in_a=None,
+                  v_in_b=None):
+    """A ResNet block's stride-2 3x3 conv1 (ra) and 1x1 downsample (rb) of
+    the same input in one cf_conv_halo_pair launch, each output exactly
+    what run_mfma would return (an NHWC-backed spike tensor with its count
+    block).  x: [T, B, Cin, H, W] (its fp16 NHWC copy when it carries one,
+    else packed here).  Returns (out_a, v_out_a, out_b, v_out_b)."""
+    if not halo_pair_supported(ra, rb, x):
+        raise ValueError("cf_conv_halo_pair does not cover these convolutions")
+    T, B, C, H, W = x.shape
+    dev = x.device
+    ra._ensure_packed(dev)
+    rb._ensure_packed(dev)
+    Ho, Wo = ra.out_hw(H, W)
+    xp = shadow_of(x, (T * B, H, W, ra.Cp))
+    if xp is not None:
+        nnz = count_of(x)
+    else:
+        nnz = ra.counter(dev)
+        xp = ra.workspace("xp", (T * B, H, W, ra.Cp), torch.float16, dev)
+        pack_input(x.reshape(T * B, C, H, W), cp=ra.Cp, group_size=0, nnz=nnz, xp_out=xp,
+                   status=status_word(dev))
+    outs = []
+    for r, v_in, tb in ((ra, v_in_a, 2), (rb, v_in_b, 4)):
+        if v_in is not None:
+            require_gpu_tensor(v_in, "v_in")
+            if v_in.numel() != B * r.Cout * Ho * Wo:
+                raise ValueError("v_in has the wrong size")
+        v_out = torch.empty((B, r.Cout, Ho, Wo), dtype=torch.float32, device=dev)
+        cp = pad32(r.Cout)
+        nhwc = torch.empty((T * B, Ho, Wo, cp), dtype=torch.float16, device=dev)
+        out = lazy_output((T, B, r.Cout, Ho, Wo), nhwc, dev)
+        nz = r.out_counter(dev)
+        r._gen[0] += 1
+        attach_count(out, nz, r._gen)
+        outs.append((r, v_in, v_out, nhwc, cp, nz, out))
+    (_, va, voa, na, cpa, nza, oa), (_, vb, vob, nb, cpb, nzb, ob) = outs
+    ev = _t0()
+    check(_hip.lib().cf_conv_halo_pair(
+        ptr(xp), ptr(nnz), x.numel(), T, B, ra.Cp, H, W, Ho, Wo,
+        ptr(ra.w_packed), ptr(ra.alpha), ptr(ra.beta), ptr(va), ptr(voa), ptr(na), cpa, ptr(nza),
+        ra.Cout, ra.Coutp, ra.padding,
+        ptr(rb.w_packed), ptr(rb.alpha), ptr(rb.beta), ptr(vb), ptr(vob), ptr(nb), cpb, ptr(nzb),
+        rb.Cout, rb.Coutp, rb.padding, *ra.lif, _hip.stream(dev)), "cf_conv_halo_pair")
+    flops = 2 * T * B * Ho * Wo * C * (ra.Cout * 9 + rb.Cout)
+    nbytes = sum(2 * T * B * Ho * Wo * cp + 4 * B * Ho * Wo * r.Cout
+                 for r, cp in ((ra, cpa), (rb, cpb)))
+    _t1("conv_pair", ev, flops=flops,
+        route=None if nnz is None else _RouteProbe(nnz, nbytes))
+    for r in (ra, rb):
+        r.last_nnz = nnz
+        r.last_numel = x.numel()
+    return oa, voa, ob, vob
+
+
 class GroupedConvLIFRunner:
     """Device state + launch of one fused grouped Conv -> (BN) -> LIF layer
     (groups > 1; depthwise when groups == Cin): cf_conv_grouped_lif.

@@ -298,6 +298,29 @@ int cf_conv_halo(const void* x, const void* w_packed, const float* alpha, const 
                  int64_t group_size, int epilogue, double tau, double v_th, double v_reset,
                  int hard_reset, int decay_input, void* stream);
 
+/* A ResNet block's stride-2 3x3 conv1 (conv a, pad_a) and its stride-2 1x1
+ * downsample (conv b, pad_b) of the same fp16 NHWC input x in one launch:
+ * the workgroups of conv a's tiles, then conv b's, each computing exactly
+ * what its own cf_conv_halo launch computes (same results, bit for bit),
+ * reading x through the L2 once.  Both with the lean LIF epilogue: fp16
+ * NHWC outputs out_a / out_b only (Cout a multiple of 32, no fp32 output,
+ * no identity), v_in / v_out as cf_conv_mfma, their own count blocks nz_a /
+ * nz_b; the input's count block nnz (nullable) routes both (StaticZero on
+ * a zero count); one set of LIF parameters for both.  w/alpha/beta from
+ * cf_pack_conv_weights.  Replaces the two launches of
+ * catfuse/patterns.py:672-737 (SEWBasicBlock: conv1-bn1-sn1 and
+ * downsample-downsample_sn of the same input). */
+int cf_conv_halo_pair(const void* x, const unsigned long long* nnz, int64_t numel, int64_t T,
+                      int64_t B, int64_t Cp, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
+                      const void* w_a, const float* alpha_a, const float* beta_a,
+                      const float* v_in_a, float* v_out_a, void* out_a, int64_t cp_out_a,
+                      unsigned long long* nz_a, int64_t Cout_a, int64_t Coutp_a, int64_t pad_a,
+                      const void* w_b, const float* alpha_b, const float* beta_b,
+                      const float* v_in_b, float* v_out_b, void* out_b, int64_t cp_out_b,
+                      unsigned long long* nz_b, int64_t Cout_b, int64_t Coutp_b, int64_t pad_b,
+                      double tau, double v_th, double v_reset, int hard_reset, int decay_input,
+                      void* stream);
+
 /* Fused Conv -> BN -> LIF / z in fp32 (VALU) for analog inputs
  * x [T*x_img_tstride + B][Cin][H][W]; x_img_tstride == 0 evaluates the
  * convolution once for a time-repeated (direct-encoded) input.  Replaces

@@ -85,6 +85,16 @@ def test_host_side_argument_validation():
     assert L.cf_compact_tiles(None, 4, 8, 8, 0.0, -1.0, 0.0, 1, None) == INVALID
     assert L.cf_compact_tiles(1, 4, 8, 33, 0.0, -1.0, 0.0, 1, None) == INVALID   # > 32 groups
     assert L.cf_compact_tiles(1, 4, 8, 8, float("nan"), -1.0, 0.0, 1, None) == INVALID
+    # paired conv: the 1x1 conv's output size differs from the 3x3 conv's
+    def pair(Ho=8, Cout_a=64, pad_b=0, out_a=1):
+        return L.cf_conv_halo_pair(1, None, 0, 4, 2, 64, 16, 16, Ho, Ho,
+                                   1, 1, 1, None, 1, out_a, 64, None, Cout_a, 64, 1,
+                                   1, 1, 1, None, 1, 1, 64, None, 64, 64, pad_b,
+                                   2.0, 1.0, 0.0, 1, 1, None)
+    assert pair(pad_b=1) == INVALID                 # 1x1/s2 with padding 1: 9x9 output
+    assert pair(Ho=7) == INVALID                    # inconsistent output size
+    assert pair(Cout_a=48) == INVALID               # outputs in whole 32-channel groups
+    assert pair(out_a=None) == INVALID              # NHWC outputs required
     # prescan: more than 32 groups
     assert L.cf_prescan_tiles(1, 1, 8, 8, 8, 8, 3, 1, 1, 8, 8, 33, 1, 1, None) == INVALID
     # pack: groups must fit 32 bits

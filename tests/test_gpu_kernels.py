@@ -522,6 +522,86 @@ def test_sparse_compaction_and_half_skip_bitwise(cuda, k, stride, T, tile, C):
                what=f"compact k{k} s{stride} T{T} C{C}")
 
 
+@pytest.mark.parametrize("T,variant,zero", [(4, 0, False), (2, 0, False), (5, 5, False),
+                                             (4, 2, False), (4, 0, True)])
+def test_conv_halo_pair_bitwise(cuda, T, variant, zero):
+    """cf_conv_halo_pair (a stride-2 3x3 conv and a stride-2 1x1 conv of the
+    same input in one launch) equals the two convs' own launches bit for
+    bit: spikes, membranes, published counts; with a carried membrane, T
+    below, at and above the time blocks, every LIF specialisation and the
+    StaticZero route."""
+    from catfuse_amd import runtime, snn
+    p = LIF_VARIANTS[variant]
+    B, C, Cout, H = 3, 64, 128, 19
+    lif = snn.LIFNode(tau=p["tau"], v_threshold=p["v_threshold"], v_reset=p["v_reset"],
+                      decay_input=p["decay_input"])
+    conv_a, bn_a, _ = _layer(C, Cout, 3, 2, 1, seed=81)
+    conv_b, bn_b, _ = _layer(C, Cout, 1, 2, 0, seed=82)
+    ra, rb = _runner(conv_a, bn_a, lif, cuda), _runner(conv_b, bn_b, lif, cuda)
+    x = (torch.rand(T, B, C, H, H, generator=_gen(T + variant)) < 0.2).float()
+    if zero:
+        x.zero_()
+    xd = x.to(cuda)
+    Ho = (H + 2 - 3) // 2 + 1
+    g = _gen(7)
+    va = (torch.rand(B, Cout, Ho, Ho, generator=g) * 0.5).to(cuda)
+    vb = (torch.rand(B, Cout, Ho, Ho, generator=g) * 0.5).to(cuda)
+    for v_a, v_b in ((None, None), (va, vb)):
+        sa, wa = ra.run_mfma(xd, v_a)
+        sb, wb = rb.run_mfma(xd, v_b)
+        ca, cb = int(runtime.count_of(sa)[1]), int(runtime.count_of(sb)[1])
+        pa, qa, pb, qb = runtime.run_halo_pair(ra, rb, xd, v_a, v_b)
+        torch.cuda.synchronize()
+        assert torch.equal(pa, sa) and torch.equal(qa, wa)
+        assert torch.equal(pb, sb) and torch.equal(qb, wb)
+        assert int(runtime.count_of(pa)[1]) == ca and int(runtime.count_of(pb)[1]) == cb
+        if not zero:
+            assert bool(sa.any()) and bool(sb.any())
+    s_ref, v_ref, h_ref = oracle.conv_bn_lif(x, conv_a, bn_a, lif, v_in=va.cpu())
+    lif_parity(pa.cpu().numpy(), qa.cpu().numpy(), s_ref, v_ref, h_ref,
+               v_th=p["v_threshold"], what="pair 3x3")
+
+
+def test_sew_block_downsample_pair_matches_separate(cuda):
+    """A SEW block with a stride-2 downsample runs conv1 and the downsample
+    as one paired launch; its output and every state equal the block run
+    with the pair disabled (separate launches), and the downsample
+    module's hooks still see its output."""
+    import copy
+    from catfuse_amd import snn
+    from catfuse_amd.patterns import CTFSEWBasicBlock
+    import catfuse_amd
+    g = _gen(5)
+    ds = torch.nn.Sequential(snn.Conv2d(64, 128, 1, 2, bias=False), snn.BatchNorm2d(128))
+    blk = snn.BasicBlock(64, 128, stride=2, downsample=ds, cnf="ADD", v_threshold=0.5)
+    snn.kaiming_init(blk, g)
+    snn.randomize_bn(blk, g)
+    snn.functional.set_step_mode(blk, "m")
+    fused = CTFSEWBasicBlock.from_sj_block(blk.eval()).to(cuda)
+    plain = copy.deepcopy(fused)
+    seen = []
+    fused.fused_downsample.register_forward_hook(lambda m, a, o: seen.append(o))
+    x = (torch.rand(4, 2, 64, 16, 16, generator=g) < 0.3).float().to(cuda)
+    y = fused(x)
+    calls = []
+    orig = plain.fused_first.__class__.forward
+
+    def no_pair(self, x, sew_identity=None):
+        self._pair_with = None
+        calls.append(1)
+        return orig(self, x, sew_identity)
+    plain.fused_first.forward = no_pair.__get__(plain.fused_first)
+    y2 = plain(x)
+    torch.cuda.synchronize()
+    catfuse_amd.check_status()
+    assert calls and torch.equal(y, y2) and bool(y.any())
+    for a, b in ((fused.fused_first, plain.fused_first),
+                 (fused.fused_downsample, plain.fused_downsample),
+                 (fused.fused_second, plain.fused_second)):
+        assert torch.equal(a.state.tensor, b.state.tensor)
+    assert len(seen) == 1 and seen[0].shape == (4, 2, 128, 8, 8)
+
+
 def test_static_zero_route_equals_bias_only(cuda):
     T, B, C, H, W = 4, 2, 64, 8, 8
     conv, bn, lif = _layer(C, C, 3, 1, 1, seed=8)
