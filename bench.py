@@ -837,6 +837,9 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-tails", action="store_true")
     ap.add_argument("--no-live", action="store_true")
+    ap.add_argument("--live-only", action="store_true",
+                    help="only the live SEW line (v_th = 0.1), printed as its own JSON line "
+                         "(the command of its rocprofv3 summary)")
     ap.add_argument("--cpu-batch", type=int, default=None,
                     help="images per CPU-baseline forward (default: CPU_BATCH[workload])")
     ap.add_argument("--eager", action="store_true",
@@ -863,6 +866,9 @@ def main():
 
     import torch
     dev = torch.device("cuda", 0)
+    if args.live_only:
+        print(json.dumps(live_result(args, dev)), flush=True)
+        return
     if args.workload == "spikformer_8_384":
         result, model = spikformer_result(args, dev)
     elif args.workload == "vgg11_bn":
