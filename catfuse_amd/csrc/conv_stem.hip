@@ -16,7 +16,8 @@
 // is below 2^-22 |w x| per product.
 //
 // Workgroup: one 8 x 7 tile of pooled pixels of one image and 64 output
-// channels.  It computes the 17 x 15 conv outputs under the tile's pooling
+// channels; the filter rows' weight fragments stream from L2 one row ahead
+// (141 VGPRs: three workgroups per CU).  It computes the 17 x 15 conv outputs under the tile's pooling
 // windows (the border row/column is recomputed by the neighbouring tile),
 // runs the LIF over T for each, keeps the spike train of each conv output as
 // a T-bit word in LDS, ORs the words over each 3 x 3 window and writes the
@@ -72,7 +73,7 @@ struct StemArgs {
 };
 
 template <typename SW, int LM>
-__global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 2 : 1) void conv_stem_kernel(StemArgs a) {
+__global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel(StemArgs a) {
   constexpr int SLD = spike_ld<SW>();
   __shared__ __attribute__((aligned(16))) _Float16 xs[2][RH * RW * 4];
   __shared__ __attribute__((aligned(16))) SW spk[NPIX * SLD];
@@ -95,25 +96,18 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 2 : 1) void conv_stem_kernel
   const int y0 = 2 * ph0 - 1, x0 = 2 * pw0 - 1;  // conv output at local (0, 0)
   const int cout0 = (work - tile * ncb) * BMS;
 
-  // Weight fragments of this wave's 32 output channels, all filter rows.
-  h8 wh[MAXKH][2], wl[MAXKH][2];
-  {
-    const int co = cout0 + mt * 32 + (lane & 31);
-    const _Float16* p0 = a.w + (size_t)co * a.KH * KROW + 8 * (lane >> 5);
-    const size_t limb = (size_t)a.Coutp * a.KH * KROW;
+  // Weight fragments of this wave's 32 output channels, one filter row at a
+  // time from L2 (the next row's loaded while the current row's MFMAs run).
+  const int wco = cout0 + mt * 32 + (lane & 31);
+  const _Float16* wp0 = a.w + (size_t)wco * a.KH * KROW + 8 * (lane >> 5);
+  const size_t wlimb = (size_t)a.Coutp * a.KH * KROW;
+  auto load_w = [&](int kh, h8* dh, h8* dl) {
 #pragma unroll
-    for (int kh = 0; kh < MAXKH; ++kh)
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        if (kh < a.KH) {
-          wh[kh][ks] = *reinterpret_cast<const h8*>(p0 + kh * KROW + ks * 16);
-          wl[kh][ks] = *reinterpret_cast<const h8*>(p0 + limb + kh * KROW + ks * 16);
-        } else {
-          wh[kh][ks] = (h8)(_Float16)0.0f;
-          wl[kh][ks] = (h8)(_Float16)0.0f;
-        }
-      }
-  }
+    for (int ks = 0; ks < 2; ++ks) {
+      dh[ks] = *reinterpret_cast<const h8*>(wp0 + kh * KROW + ks * 16);
+      dl[ks] = *reinterpret_cast<const h8*>(wp0 + wlimb + kh * KROW + ks * 16);
+    }
+  };
 
   // Stage the input rows/columns under the tile, split into fp16 limbs.
   // All loads of the thread are issued before the first conversion.
@@ -278,9 +272,13 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 2 : 1) void conv_stem_kernel
       acc0[r] = 0.0f;
       acc1[r] = 0.0f;
     }
+    h8 wh[2][2], wl[2][2];   // [row parity][ks]
+    load_w(0, wh[0], wl[0]);
 #pragma unroll
     for (int kh = 0; kh < MAXKH; ++kh) {
       if (kh >= a.KH) break;
+      const int cb = kh & 1;
+      if (kh + 1 < a.KH) load_w(kh + 1, wh[cb ^ 1], wl[cb ^ 1]);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const int o = (kh * RW + 4 * ks) * 4;
@@ -288,12 +286,12 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 2 : 1) void conv_stem_kernel
         const h8 xl0 = *reinterpret_cast<const h8*>(&xs[1][base0 + o]);
         const h8 xh1 = *reinterpret_cast<const h8*>(&xs[0][base1 + o]);
         const h8 xl1 = *reinterpret_cast<const h8*>(&xs[1][base1 + o]);
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wh[kh][ks], xh0, acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wh[kh][ks], xh1, acc1, 0, 0, 0);
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wl[kh][ks], xh0, acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wl[kh][ks], xh1, acc1, 0, 0, 0);
-        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wh[kh][ks], xl0, acc0, 0, 0, 0);
-        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wh[kh][ks], xl1, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wh[cb][ks], xh0, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wh[cb][ks], xh1, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wl[cb][ks], xh0, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wl[cb][ks], xh1, acc1, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wh[cb][ks], xl0, acc0, 0, 0, 0);
+        acc1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(wh[cb][ks], xl1, acc1, 0, 0, 0);
       }
     }
     epilogue(nt, acc0);
