@@ -30,7 +30,10 @@ _SIGNATURES = {
     "cf_pack_input": [_P, _I, _I, _I, _I, _I, _P, _P, c_int, c_float, _P, _P, _P],
     "cf_scan_nhwc": [_P, _I, _I, _I, _I, _I, _P, c_int, c_float, _P, _P],
     "cf_nhwc_to_nchw": [_P, _P, _I, _I, _I, _I, _I, _P],
-    "cf_global_avgpool_nhwc": [_P, _P, _I, _I, _I, _I, _P],
+    "cf_global_avgpool_nhwc": [_P, _P, _P, _I, _I, _I, _I, _P],
+    "cf_resolve_copy": [_P, _I, _P, _P],
+    "cf_bias_response": [_P, _P, _I, _I, c_double, c_double, c_double, c_int, c_int, _P, _P, _P],
+    "cf_expand_state": [_P, _P, _P, _I, _I, _I, _P],
     "cf_pack_tokens": [_P, _I, _I, _I, _P, _P, _P, _P],
     "cf_tokens_to_f32": [_P, _P, _I, _I, _I, _P],
     "cf_maxpool_nhwc": [_P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P],
@@ -41,17 +44,19 @@ _SIGNATURES = {
     "cf_prescan_tiles": [_P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P],
     "cf_pack_conv_weights": [_P, _I, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P],
     "cf_compact_tiles": [_P, _I, _I, _I, c_double, c_double, c_double, _P, _P],
-    "cf_conv_mfma": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, c_int, _P, _P, _P, _P, _I,
+    "cf_conv_mfma": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, c_int, _P, _P, _P, _P,
+                     _P, _P, _P, c_int, _P, _I,
                      c_double,
                      _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                      c_int, c_double, c_double, c_double, c_int, c_int, _P],
-    "cf_conv_halo": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, c_int, _P, _P, _P, _P, _I,
+    "cf_conv_halo": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, c_int, _P, _P, _P, _P,
+                     _P, _P, _P, c_int, _P, _I,
                      c_double,
                      _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                      c_int, c_double, c_double, c_double, c_int, c_int, _P],
-    "cf_conv_halo_pair": [_P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
-                          _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I,
-                          _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I,
+    "cf_conv_halo_pair": [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
+                          _P, _P, _P, _P, _P, _P, _I, _P, _P, c_int, _I, _I, _I,
+                          _P, _P, _P, _P, _P, _P, _I, _P, _P, c_int, _I, _I, _I,
                           c_double, c_double, c_double, c_int, c_int, _P],
     "cf_pack_stem_weights": [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P],
     "cf_conv_stem_lif_maxpool": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I,

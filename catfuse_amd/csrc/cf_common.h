@@ -180,6 +180,43 @@ __device__ __forceinline__ unsigned long long cf_count_read(const unsigned long 
   return blk[1];
 }
 
+// Descriptor of a fused conv's output (16 bytes of device memory, written by
+// the launch that is given one, read by later launches in stream order):
+//   copy:   CF_COPY_WRITTEN  the fp16 NHWC copy buffer holds the values;
+//           CF_COPY_ZERO     every value is zero and the buffer was not
+//                            written;
+//           CF_COPY_ALIAS    the values are those of the copy at `alias` (the
+//                            layer's identity, same shape and pitch) and the
+//                            buffer was not written;
+//   vstate: 0 v_out holds the membrane state; 1 every pixel of channel c
+//           holds v_chan[c] (the launch's per-channel buffer) and v_out was
+//           not written.
+enum { CF_COPY_WRITTEN = 0, CF_COPY_ZERO = 1, CF_COPY_ALIAS = 2 };
+struct CfOutDesc {
+  uint32_t copy;
+  uint32_t vstate;
+  const void* alias;
+};
+static_assert(sizeof(CfOutDesc) == 16, "descriptor layout");
+
+// What a caller knows of a layer's response to its BN bias alone (the
+// StaticZero drive: z = 0 * alpha + beta at every pixel, from the initial
+// state), from cf_bias_response: CF_BIAS_SILENT no channel fires at any of
+// the T steps; CF_BIAS_VCHAN the caller holds the per-channel final
+// potentials (so a StaticZero launch need not write v_out).
+enum { CF_BIAS_SILENT = 1, CF_BIAS_VCHAN = 2 };
+
+// Where a copy's values are, given its descriptor (nullable): the buffer
+// itself, the aliased copy, or nullptr for an all-zero copy.
+template <typename T>
+__device__ __forceinline__ const T* cf_copy_source(const CfOutDesc* d, const T* own) {
+  if (d == nullptr) return own;
+  const uint32_t st = d->copy;
+  if (st == CF_COPY_ZERO) return nullptr;
+  if (st == CF_COPY_ALIAS) return reinterpret_cast<const T*>(d->alias);
+  return own;
+}
+
 // Host: LIF parameter block from SpikingJelly-level (double) parameters.
 LifParams cf_make_lif_params(double tau, double v_th, double v_reset, int hard, int decay_input);
 

@@ -147,6 +147,16 @@ struct HaloArgs {
   const unsigned long long* nnz;  // count block of the input (cf_count_read), or null
   unsigned long long* nz_out;     // count block of the output: workgroups that wrote a
                                   // nonzero value (cf_count_publish), or null
+  // Descriptors (CfOutDesc, nullable) of the input's and the identity's
+  // copies as their producers left them, and of this launch's output; what
+  // the caller knows of the layer's response to its bias alone (bias_info:
+  // CF_BIAS_SILENT, CF_BIAS_VCHAN; needs out_desc); the identity's count
+  // block (for an output that aliases it), nullable.
+  const CfOutDesc* x_desc;
+  const CfOutDesc* id_desc;
+  CfOutDesc* out_desc;
+  int bias_info;
+  const unsigned long long* id_nnz;
   int64_t numel;
   double sparse_thr;
   int T, B, Cp, Cout, Coutp, H, W, Ho, Wo, pad;
@@ -240,6 +250,54 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   // rejected SparseFlow) turns the sparse route into the dense one.
   int route = halo_route(a.nnz, a.numel, a.sparse_thr);
   if (route == CF_ROUTE_SPARSE && a.order != nullptr && a.order[0] < 0) route = CF_ROUTE_DENSE;
+  // The input and identity copies where their producers left the values:
+  // an all-zero input takes StaticZero (its buffer is not read), an
+  // all-zero identity is read as zeros, aliased ones where they point.
+  const _Float16* const xsrc = cf_copy_source(a.x_desc, a.x);
+  if (xsrc == nullptr) route = CF_ROUTE_ZERO;
+  const _Float16* const id_nhwc =
+      a.identity_nhwc != nullptr ? cf_copy_source(a.id_desc, a.identity_nhwc) : nullptr;
+  auto set_out_desc = [&](uint32_t copy, const void* alias, bool vchan) {
+    if (a.out_desc != nullptr && tid == 0 && L == 0) {
+      a.out_desc->copy = copy;
+      a.out_desc->vstate = vchan ? 1u : 0u;
+      a.out_desc->alias = alias;
+    }
+  };
+  // StaticZero with no initial state and the layer's bias response known
+  // to the caller (cf_bias_response, computed once per layer with the lean
+  // path's operations): when no channel fires on its bias alone the output
+  // is the identity (all zero without one), and its copy is not written:
+  // the descriptor marks it all zero, or an alias of the identity's copy
+  // when that is a fused layer's copy of the same pitch (identity + 0 is
+  // the identity, bit for bit: spike counts hold no -0).  When the caller
+  // also holds the per-channel final potentials, v_out is not written
+  // either; then workgroup 0 alone records the descriptor and the count,
+  // and every workgroup returns here, before any other memory access.
+  const bool zlean = LEAN && EPI == EPI_LIF && route == CF_ROUTE_ZERO && a.v_in == nullptr &&
+                     (a.T + 2) * BM <= 2 * HB;
+  const bool zvchan = zlean && a.out_desc != nullptr && (a.bias_info & CF_BIAS_VCHAN) != 0;
+  uint32_t zcopy = CF_COPY_WRITTEN;
+  const void* zalias = nullptr;
+  bool id_live = false;   // an aliased identity has a nonzero value
+  if (zlean && a.out_desc != nullptr && (a.bias_info & CF_BIAS_SILENT) != 0) {
+    if (id_nhwc == nullptr) {
+      zcopy = CF_COPY_ZERO;
+    } else if (a.id_desc != nullptr && a.cp_id == a.cp_out) {
+      zcopy = CF_COPY_ALIAS;
+      zalias = id_nhwc;
+      id_live = a.id_nnz == nullptr || cf_count_read(a.id_nnz) != 0ull;   // unknown: nonzero
+    }
+    if (zcopy != CF_COPY_WRITTEN && (zvchan || a.v_out == nullptr)) {
+      if (L == 0 && tid == 0) {
+        if (a.nz_out != nullptr) a.nz_out[1] = id_live ? 1ull : 0ull;
+        a.out_desc->copy = zcopy;
+        a.out_desc->vstate = zvchan ? 1u : 0u;
+        a.out_desc->alias = zalias;
+      }
+      return;
+    }
+  }
   const int ncb = a.Coutp / BM;
   const int ntiles = a.B * a.GH * a.GW;
   const int nwork = ntiles * ncb;
@@ -320,8 +378,17 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   // halves in LDS, and writes the tile from the rows: identity + spikes per
   // 16-byte chunk (packed fp16 adds, as below), then the final potential at
   // every pixel.  No K loop, no per-element LIF.
+  //
+  // The copy and state decisions were made above (zcopy, zvchan): a copy
+  // recorded as all zero or as an alias is not written, nor is v_out when
+  // the caller holds the per-channel potentials.
   if constexpr (LEAN && EPI == EPI_LIF) {
-    if (route == CF_ROUTE_ZERO && a.v_in == nullptr && (a.T + 2) * BM <= 2 * HB) {
+    if (zlean) {
+      const uint32_t cst = zcopy;
+      const void* alias = zalias;
+      const bool vchan = zvchan;
+      if (id_live) anyw = 1u;   // the published count is the identity's
+      const bool elide = cst != CF_COPY_WRITTEN;
       _Float16* srow = halo;                                       // [T][BM] spikes
       float* vrow = reinterpret_cast<float*>(halo + a.T * BM);     // [BM] final v
       if (tid < BM) {  // the thread that loaded this channel's alpha/beta
@@ -338,13 +405,13 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
       constexpr int CH8Z = BM / 8;                       // 16-byte chunks per pixel
       constexpr int CPIZ = BN * CH8Z / 256;              // chunks per thread per step
       static_assert(BN * CH8Z % 256 == 0, "whole copy-out passes");
-      const bool have_id = a.identity_nhwc != nullptr;
-      for (int t = 0; t < a.T; ++t) {
+      const bool have_id = id_nhwc != nullptr;
+      for (int t = 0; t < (elide ? 0 : a.T); ++t) {
         const size_t img = (size_t)t * a.B + b;
         const __amdgpu_buffer_rsrc_t ro =
             halo_rsrc(a.out_nhwc + img * HoWo * a.cp_out, (uint32_t)(HoWo * a.cp_out * 2));
         const __amdgpu_buffer_rsrc_t ri =
-            halo_rsrc(have_id ? a.identity_nhwc + img * HoWo * a.cp_id : a.identity_nhwc,
+            halo_rsrc(have_id ? id_nhwc + img * HoWo * a.cp_id : a.identity_nhwc,
                       have_id ? (uint32_t)(HoWo * a.cp_id * 2) : 0u);
 #pragma unroll
         for (int i = 0; i < CPIZ; ++i) {
@@ -363,7 +430,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
               sum, ro, ok ? (uint32_t)((pix * a.cp_out + cout0 + part * 8) * 2) : HALO_OOB, 0, 0);
         }
       }
-      if (a.v_out) {
+      if (a.v_out && !vchan) {
         // pixel p of the tile, channels cg * VPT .. + VPT - 1 of the block
         constexpr int VPT = BM * BN / 256;
         const int p = tid % BN, cg = tid / BN;
@@ -381,6 +448,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
         }
       }
       publish_count();
+      set_out_desc(cst, alias, vchan);
       return;
     }
   }
@@ -475,7 +543,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   // pixel lies inside the image (bit i of cp_inb) and its time step within
   // the block (bits 2i.. of cp_t).  Per K step only the block, the chunk and
   // the step activity change.
-  const _Float16* xtile = a.x + (ptrdiff_t)((ptrdiff_t)ih0 * a.W + iw0) * a.Cp;
+  const _Float16* xtile = xsrc + (ptrdiff_t)((ptrdiff_t)ih0 * a.W + iw0) * a.Cp;
   // Unit of direct load i of this thread: 64-unit block 4 i + w of wave w
   // (wrapped into 0 .. NB-1: a wrapped load repeats another one, writing
   // the same bytes), lane l unit 64 * block + l.  Its source offset (halves,
@@ -737,9 +805,9 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     // identity or beyond the block: an empty range).
     h4 idq[LEAN ? 2 : 1][NT][4];
     auto id_load = [&](int t) {
-      const bool have = a.identity_nhwc && t < nsteps;
+      const bool have = id_nhwc && t < nsteps;
       const _Float16* base =
-          have ? a.identity_nhwc + (size_t)((tb0 + t) * a.B + b) * HoWo * a.cp_id : a.identity_nhwc;
+          have ? id_nhwc + (size_t)((tb0 + t) * a.B + b) * HoWo * a.cp_id : a.identity_nhwc;
       const __amdgpu_buffer_rsrc_t rid = halo_rsrc(base, have ? (uint32_t)(HoWo * a.cp_id * 2) : 0u);
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4)
@@ -754,7 +822,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
       const int tt = tb0 + t;
       const int img = tt * a.B + b;
       _Float16* ostage = obuf + (t % NOBUF) * OSTEP;
-      const _Float16* idn = a.identity_nhwc;
+      const _Float16* idn = id_nhwc;
       const _Float16* idbase = idn ? idn + (size_t)img * HoWo * a.cp_id : nullptr;
       if constexpr (LEAN) {
         if (t + 1 < TB) id_load(t + 1);
@@ -895,6 +963,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     }
   }
   publish_count();
+  set_out_desc(CF_COPY_WRITTEN, nullptr, false);
 }
 
 template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB, bool HS = false>
@@ -960,8 +1029,9 @@ int make_halo_args(HaloArgs& a, const void* x, const void* w_packed, const float
                    void* out_nhwc, int64_t cp_out, const float* identity,
                    const void* identity_nhwc, int64_t cp_id, int identity_mode,
                    const int32_t* ag_mask, const int32_t* tile_order,
-                   const unsigned long long* nnz, unsigned long long* nz_out, int64_t numel,
-                   double sparse_threshold, int64_t T, int64_t B, int64_t Cp, int64_t Cout,
+                   const unsigned long long* nnz, unsigned long long* nz_out,
+                   const void* x_desc, const void* id_desc, void* out_desc, int bias_info,
+                   const unsigned long long* id_nnz, int64_t numel, double sparse_threshold, int64_t T, int64_t B, int64_t Cp, int64_t Cout,
                    int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo, int64_t ksize,
                    int64_t stride, int64_t pad, int64_t tile_h, int64_t tile_w,
                    int64_t group_size, int epilogue, double tau, double v_th, double v_reset,
@@ -986,6 +1056,8 @@ int make_halo_args(HaloArgs& a, const void* x, const void* w_packed, const float
   if (ag_mask && (group_size <= 0 || (Cp + group_size - 1) / group_size > 32))
     return (int)hipErrorInvalidValue;
   if (tile_order && !ag_mask) return (int)hipErrorInvalidValue;
+  if ((bias_info & ~(CF_BIAS_SILENT | CF_BIAS_VCHAN)) != 0 || (bias_info && !out_desc))
+    return (int)hipErrorInvalidValue;
   // 32-bit element indices of the outputs, and 32-bit offsets of a tile's
   // input within one time block (4 steps)
   if (T * B * Cout * Ho * Wo > INT32_MAX || T * B * H * W > ((int64_t)1 << 40) ||
@@ -1004,6 +1076,8 @@ int make_halo_args(HaloArgs& a, const void* x, const void* w_packed, const float
   // Without masks the SparseFlow route cannot be taken: pass the count only
   // when masks exist (StaticZero is still detected through nnz == 0 below).
   a.nnz = nnz; a.nz_out = nz_out; a.numel = numel;
+  a.x_desc = (const CfOutDesc*)x_desc; a.id_desc = (const CfOutDesc*)id_desc;
+  a.out_desc = (CfOutDesc*)out_desc; a.bias_info = bias_info; a.id_nnz = id_nnz;
   a.sparse_thr = ag_mask ? sparse_threshold : 2.0;  // 2.0: sparsity never exceeds it
   a.T = (int)T; a.B = (int)B; a.Cp = (int)Cp; a.Cout = (int)Cout; a.Coutp = (int)Coutp;
   a.H = (int)H; a.W = (int)W; a.Ho = (int)Ho; a.Wo = (int)Wo; a.pad = (int)pad;
@@ -1036,7 +1110,55 @@ void conv_halo_pair_kernel(HaloArgs a, HaloArgs b, int nLa) {
                                                          bn_s, any_sh);
 }
 
+// The StaticZero drive of each channel (z = 0 * alpha + beta, from the
+// initial state, T steps) with the lean path's operations: its final
+// potential and whether it fires at some step.
+template <int LM>
+__global__ __launch_bounds__(256) void bias_response_kernel(const float* __restrict__ alpha,
+                                                            const float* __restrict__ beta,
+                                                            int Cout, int T, LifParams lif,
+                                                            float* __restrict__ v_final,
+                                                            uint32_t* __restrict__ fires) {
+  const int c = (int)blockIdx.x * 256 + (int)threadIdx.x;
+  if (c >= Cout) return;
+  const float z = __builtin_fmaf(0.0f, alpha[c], beta[c]);
+  float v = lif_initial_v(lif);
+  bool f = false;
+  for (int t = 0; t < T; ++t) {
+    float vv = lif_charge_m<LM>(v, z, lif);
+    f |= lif_fire_reset_bit<LM>(vv, lif);
+    v = vv;
+  }
+  v_final[c] = v;
+  fires[c] = f ? 1u : 0u;
+}
+
 }  // namespace
+
+CF_API int cf_bias_response(const float* alpha, const float* beta, int64_t Cout, int64_t T,
+                            double tau, double v_th, double v_reset, int hard_reset,
+                            int decay_input, float* v_final, uint32_t* fires, void* stream) {
+  if (!alpha || !beta || !v_final || !fires || Cout <= 0 || Cout > INT32_MAX || T <= 0 ||
+      T > INT32_MAX)
+    return (int)hipErrorInvalidValue;
+  const LifParams lif = cf_make_lif_params(tau, v_th, v_reset, hard_reset, decay_input);
+  const dim3 grid(cf_blocks(Cout, 256)), block(256);
+  hipStream_t st = (hipStream_t)stream;
+  switch (cf_lif_mode(lif)) {
+    case LM_HARD0_DECAY_P2:
+      hipLaunchKernelGGL(bias_response_kernel<LM_HARD0_DECAY_P2>, grid, block, 0, st, alpha, beta,
+                         (int)Cout, (int)T, lif, v_final, fires);
+      break;
+    case LM_HARD_DECAY_P2:
+      hipLaunchKernelGGL(bias_response_kernel<LM_HARD_DECAY_P2>, grid, block, 0, st, alpha, beta,
+                         (int)Cout, (int)T, lif, v_final, fires);
+      break;
+    default:
+      hipLaunchKernelGGL(bias_response_kernel<LM_GENERIC>, grid, block, 0, st, alpha, beta,
+                         (int)Cout, (int)T, lif, v_final, fires);
+  }
+  return (int)hipGetLastError();
+}
 
 // 3x3 convolutions (stride 1 or 2, any padding) with halo staging; the
 // caller picks the tile (tile_h x tile_w in {8x8, 8x16}; 8x16 only with
@@ -1047,6 +1169,8 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
                         const float* identity, const void* identity_nhwc, int64_t cp_id,
                         int identity_mode, const int32_t* ag_mask, const int32_t* tile_order,
                         const unsigned long long* nnz, unsigned long long* nz_out,
+                        const void* x_desc, const void* id_desc, void* out_desc,
+                        int bias_info, const unsigned long long* id_nnz,
                         int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
                         int64_t W, int64_t Ho, int64_t Wo, int64_t ksize, int64_t stride,
@@ -1056,7 +1180,9 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
   HaloArgs a;
   const int rc = make_halo_args(a, x, w_packed, alpha, beta, v_in, v_out, out, out_nhwc, cp_out,
                                 identity, identity_nhwc, cp_id, identity_mode, ag_mask,
-                                tile_order, nnz, nz_out, numel, sparse_threshold, T, B, Cp, Cout,
+                                tile_order, nnz, nz_out, x_desc, id_desc, out_desc, bias_info,
+                                id_nnz, numel,
+                                sparse_threshold, T, B, Cp, Cout,
                                 Coutp, H, W, Ho, Wo, ksize, stride, pad, tile_h, tile_w,
                                 group_size, epilogue, tau, v_th, v_reset, hard_reset,
                                 decay_input);
@@ -1075,24 +1201,26 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
 }
 
 CF_API int cf_conv_halo_pair(
-    const void* x, const unsigned long long* nnz, int64_t numel, int64_t T, int64_t B,
-    int64_t Cp, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
+    const void* x, const unsigned long long* nnz, const void* x_desc, int64_t numel,
+    int64_t T, int64_t B, int64_t Cp, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
     const void* w_a, const float* alpha_a, const float* beta_a, const float* v_in_a,
-    float* v_out_a, void* out_a, int64_t cp_out_a, unsigned long long* nz_a, int64_t Cout_a,
-    int64_t Coutp_a, int64_t pad_a,
+    float* v_out_a, void* out_a, int64_t cp_out_a, unsigned long long* nz_a, void* desc_a, int bias_info_a,
+    int64_t Cout_a, int64_t Coutp_a, int64_t pad_a,
     const void* w_b, const float* alpha_b, const float* beta_b, const float* v_in_b,
-    float* v_out_b, void* out_b, int64_t cp_out_b, unsigned long long* nz_b, int64_t Cout_b,
-    int64_t Coutp_b, int64_t pad_b,
+    float* v_out_b, void* out_b, int64_t cp_out_b, unsigned long long* nz_b, void* desc_b, int bias_info_b,
+    int64_t Cout_b, int64_t Coutp_b, int64_t pad_b,
     double tau, double v_th, double v_reset, int hard_reset, int decay_input, void* stream) {
   if (!out_a || !out_b || Cout_a % 32 != 0 || Cout_b % 32 != 0) return (int)hipErrorInvalidValue;
   HaloArgs a, b;
   int rc = make_halo_args(a, x, w_a, alpha_a, beta_a, v_in_a, v_out_a, nullptr, out_a, cp_out_a,
-                          nullptr, nullptr, 0, 0, nullptr, nullptr, nnz, nz_a, numel, 2.0, T, B,
+                          nullptr, nullptr, 0, 0, nullptr, nullptr, nnz, nz_a, x_desc, nullptr,
+                          desc_a, bias_info_a, nullptr, numel, 2.0, T, B,
                           Cp, Cout_a, Coutp_a, H, W, Ho, Wo, 3, 2, pad_a, 8, 8, 0, EPI_LIF, tau,
                           v_th, v_reset, hard_reset, decay_input);
   if (rc) return rc;
   rc = make_halo_args(b, x, w_b, alpha_b, beta_b, v_in_b, v_out_b, nullptr, out_b, cp_out_b,
-                      nullptr, nullptr, 0, 0, nullptr, nullptr, nnz, nz_b, numel, 2.0, T, B, Cp,
+                      nullptr, nullptr, 0, 0, nullptr, nullptr, nnz, nz_b, x_desc, nullptr,
+                      desc_b, bias_info_b, nullptr, numel, 2.0, T, B, Cp,
                       Cout_b, Coutp_b, H, W, Ho, Wo, 1, 2, pad_b, 8, 8, 0, EPI_LIF, tau, v_th,
                       v_reset, hard_reset, decay_input);
   if (rc) return rc;

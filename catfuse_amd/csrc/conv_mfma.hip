@@ -64,6 +64,9 @@ struct ConvArgs {
   const unsigned long long* nnz;  // count block of the input (cf_count_read), or null
   unsigned long long* nz_out;     // count block of the output: workgroups that wrote a
                                   // nonzero value (cf_count_publish), or null
+  const CfOutDesc* x_desc;        // descriptors of the input's and the identity's copies
+  const CfOutDesc* id_desc;       // (nullable); the output's is set to "written" (this
+  CfOutDesc* out_desc;            // kernel always writes its outputs)
   int64_t numel;
   double sparse_thr;
   int T, B, Cp, Cout, Coutp, H, W, Ho, Wo, KH, KW, stride, pad;
@@ -147,6 +150,8 @@ __global__ __launch_bounds__(256, (conv_min_blocks<BM, BN, EPI>())) void conv_mf
     e_off[nb] = oh * a.Wo + ow;
   }
 
+  // the input where its producer left the values (nullptr: all zero)
+  const _Float16* const xsrc = cf_copy_source(a.x_desc, a.x);
   auto gload = [&](int t, int tap, int chunk, u32x4 (&ar)[AU], u32x4 (&br)[BU]) {
     const int kh = tap / a.KW, kw = tap - (tap / a.KW) * a.KW;
     const int c0 = chunk * KC;
@@ -165,7 +170,7 @@ __global__ __launch_bounds__(256, (conv_min_blocks<BM, BN, EPI>())) void conv_mf
       const bool ok = b_img[i] >= 0 && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W;
       const size_t off =
           ok ? ((((size_t)(img_base + b_img[i]) * a.H + ih) * a.W + iw) * a.Cp + c0 + part * 8) : 0;
-      const u32x4 val = *reinterpret_cast<const u32x4*>(a.x + off);
+      const u32x4 val = *reinterpret_cast<const u32x4*>(xsrc + off);
       br[i] = ok ? val : (u32x4)(0u);
     }
   };
@@ -224,7 +229,14 @@ __global__ __launch_bounds__(256, (conv_min_blocks<BM, BN, EPI>())) void conv_mf
         }
   }
 
-  const int route = device_route(a.nnz, a.numel, a.sparse_thr);
+  const int route = xsrc == nullptr ? CF_ROUTE_ZERO : device_route(a.nnz, a.numel, a.sparse_thr);
+  const _Float16* const id_nhwc =
+      a.identity_nhwc != nullptr ? cf_copy_source(a.id_desc, a.identity_nhwc) : nullptr;
+  if (a.out_desc && tid == 0 && blockIdx.x == 0 && blockIdx.y == 0) {
+    a.out_desc->copy = CF_COPY_WRITTEN;
+    a.out_desc->vstate = 0u;
+    a.out_desc->alias = nullptr;
+  }
   const int ntiles_t = a.n_ptiles;
   uint32_t anyw = 0u;  // OR of the bits of every output value this thread writes
 
@@ -306,9 +318,11 @@ __global__ __launch_bounds__(256, (conv_min_blocks<BM, BN, EPI>())) void conv_mf
             float vv = lif_charge(v[mb][nb][r], z, a.lif);
             float sp = lif_fire_reset(vv, a.lif);
             v[mb][nb][r] = vv;
-            if (a.identity_nhwc)
-              ov = (float)a.identity_nhwc[((size_t)t * a.B + e_img[nb]) * HoWo * a.cp_id +
-                                          (size_t)e_off[nb] * a.cp_id + co] + sp;
+            if (id_nhwc)
+              ov = (float)id_nhwc[((size_t)t * a.B + e_img[nb]) * HoWo * a.cp_id +
+                                  (size_t)e_off[nb] * a.cp_id + co] + sp;
+            else if (a.identity_nhwc)
+              ov = sp;   // elided identity: all zero
             else
               ov = (a.identity && a.identity_mode == ID_ADD_SPIKE) ? a.identity[o] + sp : sp;
           }
@@ -434,6 +448,8 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
                         const float* identity, const void* identity_nhwc, int64_t cp_id,
                         int identity_mode, const int32_t* ag_mask, const int32_t* tile_order,
                         const unsigned long long* nnz, unsigned long long* nz_out,
+                        const void* x_desc, const void* id_desc, void* out_desc,
+                        int bias_info, const unsigned long long* id_nnz,
                         int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
                         int64_t W, int64_t Ho, int64_t Wo, int64_t ksize, int64_t stride,
@@ -447,6 +463,8 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
                         const float* identity, const void* identity_nhwc, int64_t cp_id,
                         int identity_mode, const int32_t* ag_mask, const int32_t* tile_order,
                         const unsigned long long* nnz, unsigned long long* nz_out,
+                        const void* x_desc, const void* id_desc, void* out_desc,
+                        int bias_info, const unsigned long long* id_nnz,
                         int64_t numel, double sparse_threshold,
                         int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
                         int64_t W, int64_t Ho, int64_t Wo, int64_t KH, int64_t KW, int64_t stride,
@@ -466,6 +484,8 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
   if (out_nhwc && (cp_out < Cout || cp_out > Coutp)) return (int)hipErrorInvalidValue;
   if (Ho != (H + 2 * pad - KH) / stride + 1 || Wo != (W + 2 * pad - KW) / stride + 1)
     return (int)hipErrorInvalidValue;
+  if ((bias_info & ~(CF_BIAS_SILENT | CF_BIAS_VCHAN)) != 0 || (bias_info && !out_desc))
+    return (int)hipErrorInvalidValue;
   const bool rect = tile_h > 0 && tile_w > 0;
   // 3x3 convolutions and 1x1 convolutions over feature maps of at least
   // 4x4 (stride 1/2, pad <= 2, one time-major input) always take the
@@ -482,7 +502,7 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
     return cf_conv_halo(x, w_packed, alpha, beta, v_in, v_out, out, out_nhwc, cp_out, identity,
                         identity_nhwc, cp_id, identity_mode,
                         rect ? ag_mask : nullptr, rect ? tile_order : nullptr, nnz, nz_out,
-                        numel, sparse_threshold, T, B, Cp, Cout,
+                        x_desc, id_desc, out_desc, bias_info, id_nnz, numel, sparse_threshold, T, B, Cp, Cout,
                         Coutp, H, W, Ho, Wo, KH, stride, pad, th, tw, rect ? group_size : 0,
                         epilogue, tau, v_th, v_reset, hard_reset, decay_input, stream);
   }
@@ -502,6 +522,8 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
   a.alpha = alpha; a.beta = beta; a.v_in = v_in; a.v_out = v_out; a.out = out;
   a.out_nhwc = (_Float16*)out_nhwc; a.cp_out = (int)cp_out;
   a.identity = identity; a.identity_mode = identity_mode; a.ag_mask = ag_mask; a.nnz = nnz; a.nz_out = nz_out; a.numel = numel;
+  a.x_desc = (const CfOutDesc*)x_desc; a.id_desc = (const CfOutDesc*)id_desc;
+  a.out_desc = (CfOutDesc*)out_desc;
   a.identity_nhwc = (const _Float16*)identity_nhwc; a.cp_id = (int)cp_id;
   a.sparse_thr = sparse_threshold;
   a.T = (int)T; a.B = (int)B; a.Cp = (int)Cp; a.Cout = (int)Cout; a.Coutp = (int)Coutp;

@@ -105,7 +105,7 @@ CF_API int cf_conv_sparse_noalloc(
   if (rc) return rc;
   return cf_conv_mfma(x, w_packed, alpha, beta, v_in, v_out, out, out_nhwc, cp_out, identity,
                       identity_nhwc, cp_id, identity_mode, ag, order, blk, nz_out,
-                      NB * Cin * H * W,
+                      nullptr, nullptr, nullptr, 0, nullptr, NB * Cin * H * W,
                       sparse_threshold, T, B, Cp, Cout, Coutp, H, W, Ho, Wo, ksize, ksize,
                       stride, pad, B, tile_h, tile_w, group_size, epilogue, tau, v_th, v_reset,
                       hard_reset, decay_input, stream);

@@ -197,16 +197,17 @@ __global__ __launch_bounds__(256) void nhwc_to_nchw_kernel(
 // exact in any order.  Block (n, 512-channel slice); a thread sums two
 // adjacent channels (one 4-byte load per pixel, 1 KB per pixel per block).
 __global__ __launch_bounds__(256) void global_avgpool_nhwc_kernel(
-    const _Float16* __restrict__ xp, float* __restrict__ out, int64_t HW, int C, int cp,
-    float factor) {
+    const _Float16* __restrict__ xp, const CfOutDesc* desc, float* __restrict__ out, int64_t HW,
+    int C, int cp, float factor) {
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
   const int64_t n = blockIdx.x;
   const int c = (int)blockIdx.y * 512 + 2 * (int)threadIdx.x;
   if (c >= C) return;
-  const _Float16* src = xp + n * HW * cp + c;
+  const _Float16* base = cf_copy_source(desc, xp);   // nullptr: all zero
+  const _Float16* src = base + n * HW * cp + c;
   float s0 = 0.0f, s1 = 0.0f;
 #pragma unroll 7
-  for (int64_t p = 0; p < HW; ++p) {
+  for (int64_t p = 0; p < (base != nullptr ? HW : 0); ++p) {
     const h2 v = *reinterpret_cast<const h2*>(src + p * cp);
     s0 += (float)v[0];
     s1 += (float)v[1];
@@ -415,16 +416,16 @@ CF_API int cf_nhwc_to_nchw(const void* xp, float* out, int64_t NB, int64_t C, in
   return (int)hipGetLastError();
 }
 
-CF_API int cf_global_avgpool_nhwc(const void* xp, float* out, int64_t NB, int64_t HW, int64_t C,
-                                  int64_t cp, void* stream) {
+CF_API int cf_global_avgpool_nhwc(const void* xp, const void* desc, float* out, int64_t NB,
+                                  int64_t HW, int64_t C, int64_t cp, void* stream) {
   if (!xp || !out || NB < 0 || HW <= 0 || C <= 0 || cp < C || cp % 8 != 0 || NB > INT32_MAX ||
       NB * HW * cp > ((int64_t)1 << 40))
     return (int)hipErrorInvalidValue;
   if (NB == 0) return 0;
   const float factor = 1.0f / (float)HW;
   hipLaunchKernelGGL(global_avgpool_nhwc_kernel, dim3((unsigned)NB, (unsigned)((C + 511) / 512)),
-                     dim3(256), 0, (hipStream_t)stream, (const _Float16*)xp, out, HW, (int)C,
-                     (int)cp, factor);
+                     dim3(256), 0, (hipStream_t)stream, (const _Float16*)xp,
+                     (const CfOutDesc*)desc, out, HW, (int)C, (int)cp, factor);
   return (int)hipGetLastError();
 }
 
@@ -486,5 +487,57 @@ CF_API int cf_route_from_nnz(const unsigned long long* nnz, int64_t numel,
 CF_API int cf_zero_counter(unsigned long long* p, void* stream) {
   if (!p) return (int)hipErrorInvalidValue;
   hipLaunchKernelGGL(zero_u64, dim3(1), dim3(1), 0, (hipStream_t)stream, p);
+  return (int)hipGetLastError();
+}
+
+namespace {
+
+// Fills a copy buffer its producer did not write (descriptor ZERO: zeros;
+// ALIAS: the aliased copy's bytes); a written copy is left alone.  16-byte
+// units, grid-stride.
+__global__ __launch_bounds__(256) void resolve_copy_kernel(uint4* __restrict__ buf, int64_t n16,
+                                                           const CfOutDesc* desc) {
+  const uint32_t st = desc->copy;
+  if (st != CF_COPY_ZERO && st != CF_COPY_ALIAS) return;
+  const uint4* src = reinterpret_cast<const uint4*>(desc->alias);
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16;
+       i += (int64_t)gridDim.x * 256)
+    buf[i] = st == CF_COPY_ALIAS ? src[i] : make_uint4(0u, 0u, 0u, 0u);
+}
+
+// v [B][C][HW] from the per-channel potentials when the descriptor says the
+// producer kept the state per channel (vstate 1); otherwise v is left alone.
+__global__ __launch_bounds__(256) void expand_state_kernel(float* __restrict__ v,
+                                                           const float* __restrict__ v_chan,
+                                                           const CfOutDesc* desc, int64_t n,
+                                                           int C, int64_t HW) {
+  if (desc->vstate != 1u) return;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * 256)
+    v[i] = v_chan[(int)((i / HW) % C)];
+}
+
+}  // namespace
+
+CF_API int cf_resolve_copy(void* buf, int64_t bytes, const void* desc, void* stream) {
+  if (!buf || !desc || bytes < 0 || bytes % 16 != 0 || ((uintptr_t)buf & 15) != 0)
+    return (int)hipErrorInvalidValue;
+  if (bytes == 0) return 0;
+  const int64_t n16 = bytes / 16;
+  const unsigned nb = cf_blocks(n16, 256), grid = nb < 2048u ? nb : 2048u;
+  hipLaunchKernelGGL(resolve_copy_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                     (uint4*)buf, n16, (const CfOutDesc*)desc);
+  return (int)hipGetLastError();
+}
+
+CF_API int cf_expand_state(float* v, const float* v_chan, const void* desc, int64_t B, int64_t C,
+                           int64_t HW, void* stream) {
+  if (!v || !v_chan || !desc || B < 0 || C <= 0 || HW <= 0 || C > INT32_MAX)
+    return (int)hipErrorInvalidValue;
+  const int64_t n = B * C * HW;
+  if (n == 0) return 0;
+  const unsigned nb = cf_blocks(n, 256), grid = nb < 2048u ? nb : 2048u;
+  hipLaunchKernelGGL(expand_state_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream, v,
+                     v_chan, (const CfOutDesc*)desc, n, (int)C, HW);
   return (int)hipGetLastError();
 }

@@ -28,8 +28,8 @@ from catfuse_amd import runtime
 from catfuse_amd.hardware import runtime_profile
 from catfuse_amd.implementations import ConvLIFParams, ConvLIFSpec, DenseKeep, StreamFuse
 from catfuse_amd.runtime import (EPI_Z, ID_ADD_SPIKE, ID_ADD_Z, ConvLIFRunner,
-                                 GroupedConvLIFRunner, avgpool2x2_lif, global_avgpool_nhwc,
-                                 lif_multistep, pad32, shadow_of)
+                                 GroupedConvLIFRunner, avgpool2x2_lif, desc_of,
+                                 global_avgpool_nhwc, lif_multistep, pad32, shadow_of)
 from catfuse_amd.state import StateBuffer
 
 try:  # SpikingJelly's MemoryModule when available, so reset_net recognises us
@@ -708,9 +708,9 @@ class FusedGlobalAvgPool(nn.Module):
         nb = 1
         for d in lead:
             nb *= int(d)
-        xp = shadow_of(x, (nb, H, W, pad32(C))) if x.is_cuda else None
+        xp = shadow_of(x, (nb, H, W, pad32(C)), resolve=False) if x.is_cuda else None
         if xp is not None:
-            return global_avgpool_nhwc(xp, C).view(*lead, C, 1, 1)
+            return global_avgpool_nhwc(xp, C, desc=desc_of(x)).view(*lead, C, 1, 1)
         self.fallback_calls += 1
         y = nn.functional.adaptive_avg_pool2d(x.reshape(nb, C, H, W), 1)
         return y.view(*lead, C, 1, 1)

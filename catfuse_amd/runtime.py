@@ -31,12 +31,21 @@ class KernelTimer:
     """Optional live timing of kernel launches with HIP events recorded on
     the launch stream (torch's current stream, which every wrapper here
     launches on).  Each record carries the launch's algorithmic work (FLOPs
-    and/or bytes) so callers can report achieved rates per kernel."""
+    and/or bytes) so callers can report achieved rates per kernel.
 
-    def __init__(self):
+    settle_cycles > 0 queues a bounded spin kernel (torch.cuda._sleep) ahead
+    of each start event, so the GPU is still busy while the host prepares
+    and issues the launch: start event, kernel and end event then run back
+    to back and the interval is the kernel's own duration, also for launches
+    shorter than the host's per-launch overhead."""
+
+    def __init__(self, settle_cycles: int = 0):
         self.records = []   # (name, start_event, end_event, flops, bytes, route probe)
+        self.settle_cycles = int(settle_cycles)
 
     def start(self):
+        if self.settle_cycles > 0:
+            torch.cuda._sleep(self.settle_cycles)
         ev = torch.cuda.Event(enable_timing=True)
         ev.record()
         return ev
@@ -50,17 +59,22 @@ class KernelTimer:
         """{name: dict(launches, ms_total, ms_avg, flops, bytes)} (synchronises).
         A conv launch that took the StaticZero route (read from its input's
         count block when the summary is made) is listed under
-        name + "_staticzero" with no FLOPs and its output bytes."""
+        name + "_staticzero" with no FLOPs and the output bytes it stored
+        ("elided": launches that stored none, their descriptor recording the
+        outputs)."""
         torch.cuda.synchronize()
         out = {}
         for name, e0, e1, fl, nb, route in self.records:
+            el = 0
             if route is not None and route.is_zero():
-                name, fl, nb = name + "_staticzero", 0, route.zero_bytes
-            d = out.setdefault(name, dict(launches=0, ms_total=0.0, flops=0, bytes=0))
+                name, fl, nb = name + "_staticzero", 0, route.bytes_stored()
+                el = int(nb == 0)
+            d = out.setdefault(name, dict(launches=0, ms_total=0.0, flops=0, bytes=0, elided=0))
             d["launches"] += 1
             d["ms_total"] += e0.elapsed_time(e1)
             d["flops"] += fl
             d["bytes"] += nb
+            d["elided"] += el
         for d in out.values():
             d["ms_avg"] = d["ms_total"] / max(1, d["launches"])
         return out
@@ -86,15 +100,26 @@ def _t1(name, ev0, flops=0, nbytes=0, route=None):
 
 class _RouteProbe:
     """The StaticZero decision of a conv launch, read back from the input's
-    count block (published count zero) after the launches complete."""
-    __slots__ = ("blk", "zero_bytes")
+    count block (published count zero) after the launches complete, and
+    the output bytes it stored on that route.  parts: one (output
+    descriptor or None, copy bytes, state bytes) per output; a descriptor
+    that records the copy / the state as unwritten removes those bytes."""
+    __slots__ = ("blk", "parts")
 
-    def __init__(self, blk, zero_bytes):
+    def __init__(self, blk, parts):
         self.blk = blk
-        self.zero_bytes = int(zero_bytes)
+        self.parts = tuple(parts)
 
     def is_zero(self) -> bool:
         return int(self.blk[1].item()) == 0
+
+    def bytes_stored(self) -> int:
+        b = 0
+        for d, copy_bytes, state_bytes in self.parts:
+            w = 0 if d is None else int(d[0].item())
+            copy, vstate = w & 0xffffffff, (w >> 32) & 0xffffffff
+            b += (copy_bytes if copy == 0 else 0) + (state_bytes if vstate == 0 else 0)
+        return b
 
 
 def status_word(device) -> torch.Tensor:
@@ -222,14 +247,39 @@ def _metadata_functions():
 _METADATA = None
 
 
-class NHWCSpikes(torch.Tensor):
+class _LazyTensor(torch.Tensor):
+    """Base of the tensors whose values a fused launch left elsewhere (a
+    copy, a per-channel buffer): cf_materialize() fills the storage, which
+    happens the first time anything other than a metadata query touches
+    the tensor.  Results of torch operations are plain tensors."""
+
+    def cf_materialize(self) -> None:  # pragma: no cover - overridden
+        raise NotImplementedError
+
+    @classmethod
+    def __torch_function__(cls, func, types, args=(), kwargs=None):
+        global _METADATA
+        if _METADATA is None:
+            _METADATA = _metadata_functions()
+        kwargs = kwargs or {}
+        self_ok = func is torch.Tensor.contiguous and args and args[0].is_contiguous()
+        if not self_ok and func not in _METADATA:
+            for a in _tensors_in(args, kwargs):
+                if isinstance(a, _LazyTensor):
+                    a.cf_materialize()
+        with torch._C.DisableTorchFunctionSubclass():
+            return func(*args, **kwargs)
+
+
+class NHWCSpikes(_LazyTensor):
     """An fp32 NCHW [T, B, C, H, W] output of a fused layer whose values were
     written only as the fp16 NHWC copy the next fused layer reads.  The fp32
     storage is filled (cf_nhwc_to_nchw) the first time anything other than a
     metadata query touches the tensor, so code outside the fused chain sees
     an ordinary tensor with the right values; fused layers that take the copy
-    never pay for the fp32 form.  Results of torch operations are plain
-    tensors."""
+    never pay for the fp32 form.  A copy its producer did not write (output
+    descriptor: all zero, or an alias of the identity's copy) is resolved
+    first (cf_resolve_copy)."""
 
     @staticmethod
     def __new__(cls, base: torch.Tensor, nhwc: torch.Tensor, tokens: bool = False):
@@ -245,6 +295,7 @@ class NHWCSpikes(torch.Tensor):
         self._cf_pending = False
         with torch._C.DisableTorchFunctionSubclass():
             nhwc = self._cf_nhwc[0]
+            _resolve(self, nhwc)
             cp = nhwc.shape[-1]
             if self.__dict__.get("_cf_tokens", False):
                 # token-major [..., N, C]: a cast of the copy, dropping padding
@@ -258,19 +309,37 @@ class NHWCSpikes(torch.Tensor):
                                              cp, _hip.stream(self.device)),
                   "cf_nhwc_to_nchw")
 
-    @classmethod
-    def __torch_function__(cls, func, types, args=(), kwargs=None):
-        global _METADATA
-        if _METADATA is None:
-            _METADATA = _metadata_functions()
-        kwargs = kwargs or {}
-        self_ok = func is torch.Tensor.contiguous and args and args[0].is_contiguous()
-        if not self_ok and func not in _METADATA:
-            for a in _tensors_in(args, kwargs):
-                if isinstance(a, NHWCSpikes):
-                    a.cf_materialize()
+
+class ChannelState(_LazyTensor):
+    """A fused layer's membrane state [B, C, H, W] that its launch may have
+    kept as one potential per channel (on the StaticZero route with no
+    initial state every pixel of a channel ends at the same value; the
+    output descriptor says whether it did).  Expanded into the storage
+    (cf_expand_state) on first use.  A state made inside a HIP graph
+    capture is expanded again on every use until it is changed in place,
+    since each replay rewrites the per-channel values."""
+
+    @staticmethod
+    def __new__(cls, base: torch.Tensor, v_chan: torch.Tensor, desc: torch.Tensor):
+        t = base.as_subclass(cls)
+        t._cf_pending = True
+        t._cf_state = (v_chan, desc, base._version)
+        t._cf_sticky = torch.cuda.is_current_stream_capturing()
+        return t
+
+    def cf_materialize(self) -> None:
+        if not self.__dict__.get("_cf_pending", False):
+            return
         with torch._C.DisableTorchFunctionSubclass():
-            return func(*args, **kwargs)
+            v_chan, desc, ver = self._cf_state
+            if not (self.__dict__.get("_cf_sticky", False) and self._version == ver):
+                self._cf_pending = False
+            if self._version != ver:
+                return   # changed in place after an earlier expansion
+            B, C = self.shape[0], self.shape[1]
+            check(_hip.lib().cf_expand_state(self.data_ptr(), v_chan.data_ptr(), desc.data_ptr(),
+                                             B, C, self.numel() // (B * C),
+                                             _hip.stream(self.device)), "cf_expand_state")
 
 
 def _tensors_in(args, kwargs):
@@ -325,6 +394,7 @@ def token_shadow(x: torch.Tensor, cp: int) -> Optional[torch.Tensor]:
     if (ver != x._version or t.device != x.device or t.shape[-1] != cp
             or t.numel() != rows * cp):
         return None
+    _resolve(x, t)
     return t.reshape(rows, cp)
 
 
@@ -352,15 +422,75 @@ def attach_shadow(out: torch.Tensor, nhwc: torch.Tensor) -> None:
     out._cf_nhwc = (nhwc, out._version)
 
 
-def shadow_of(x: torch.Tensor, shape) -> Optional[torch.Tensor]:
-    """The current fp16 NHWC copy of x with the given shape, or None."""
+def shadow_of(x: torch.Tensor, shape, resolve: bool = True) -> Optional[torch.Tensor]:
+    """The current fp16 NHWC copy of x with the given shape, or None.  With
+    resolve (the default) a copy its producer did not write (output
+    descriptor: all zero, or an alias) is filled first; a caller that reads
+    the copy through its descriptor (desc_of) passes resolve=False."""
     sh = getattr(x, "_cf_nhwc", None)
     if sh is None:
         return None
     t, ver = sh
     if ver != x._version or tuple(t.shape) != tuple(shape) or t.device != x.device:
         return None
+    if resolve:
+        _resolve(x, t)
     return t
+
+
+# Output descriptors (16 bytes each: uint32 copy state, uint32 state kind,
+# alias pointer) let a StaticZero launch leave its outputs unwritten; off
+# for comparisons against the always-writing path.
+COPY_ELISION = True
+
+
+def new_out_desc(device) -> torch.Tensor:
+    """One output's descriptor (16 bytes), written by the launch that
+    receives it before any reader runs."""
+    return torch.empty(2, dtype=torch.int64, device=device)
+
+
+_WRITTEN_DESC = {}
+
+
+def written_desc(device) -> torch.Tensor:
+    """A read-only descriptor that says "written", for a fused layer's copy
+    whose producer keeps no descriptor (an identity copy may then be
+    aliased: it holds spike counts)."""
+    d = _WRITTEN_DESC.get(device)
+    if d is None:
+        d = _WRITTEN_DESC[device] = torch.zeros(2, dtype=torch.int64, device=device)
+    return d
+
+
+def attach_desc(out: torch.Tensor, desc: torch.Tensor, keep=()) -> None:
+    """Record the output descriptor of out's copy; keep: the copies its
+    values may alias (held alive with it)."""
+    out._cf_desc = (desc, out._version, tuple(keep))
+
+
+def desc_of(x: torch.Tensor) -> Optional[torch.Tensor]:
+    """The descriptor of x's current copy (None: the copy is written)."""
+    d = getattr(x, "_cf_desc", None)
+    if d is None or d[1] != x._version:
+        return None
+    return d[0]
+
+
+def keep_of(x: torch.Tensor) -> tuple:
+    """The copies x's copy may alias (see attach_desc)."""
+    d = getattr(x, "_cf_desc", None)
+    return () if d is None else d[2]
+
+
+def _resolve(x: torch.Tensor, t: torch.Tensor) -> None:
+    """Make x's copy t hold its values if its producer left it unwritten."""
+    d = x.__dict__.get("_cf_desc")
+    if d is None:
+        return
+    x._cf_desc = None
+    check(_hip.lib().cf_resolve_copy(t.data_ptr(), t.numel() * t.element_size(),
+                                     d[0].data_ptr(), _hip.stream(t.device)), "cf_resolve_copy")
 
 
 COUNT_BLOCK_WORDS = 272  # CF_COUNT_BLOCK_WORDS of the C-ABI
@@ -449,14 +579,16 @@ def scan_nhwc(xp: torch.Tensor, C: int, *, group_size: int, threshold=1e-6,
     return act
 
 
-def global_avgpool_nhwc(xp: torch.Tensor, C: int, out: Optional[torch.Tensor] = None):
+def global_avgpool_nhwc(xp: torch.Tensor, C: int, out: Optional[torch.Tensor] = None,
+                        desc: Optional[torch.Tensor] = None):
     """xp fp16 NHWC [NB, H, W, cp] -> fp32 [NB, C]: the mean over H, W
-    (AdaptiveAvgPool2d((1, 1)) of the fp32 tensor the copy stands for)."""
+    (AdaptiveAvgPool2d((1, 1)) of the fp32 tensor the copy stands for);
+    desc: the copy's output descriptor when its producer kept one."""
     require_gpu_tensor(xp, "xp", dtype=torch.float16)
     NB, H, W, cp = xp.shape
     y = out if out is not None else torch.empty((NB, C), dtype=torch.float32, device=xp.device)
     ev = _t0()
-    check(_hip.lib().cf_global_avgpool_nhwc(ptr(xp), ptr(y), NB, H * W, C, cp,
+    check(_hip.lib().cf_global_avgpool_nhwc(ptr(xp), ptr(desc), ptr(y), NB, H * W, C, cp,
                                             _hip.stream(xp.device)), "cf_global_avgpool_nhwc")
     _t1("global_avgpool_nhwc", ev, nbytes=2 * NB * H * W * C + 4 * NB * C)
     return y
@@ -657,7 +789,39 @@ class ConvLIFRunner:
                                               ptr(self.beta_direct), st), "cf_pack_conv_weights")
         self._w_f32 = w
         self._wt_f32 = w.reshape(self.Cout, -1).t().contiguous()   # [Cin*KH*KW][Cout]
+        self._bias_resp = {}
         self._packed_key = key
+
+    def bias_response(self, device, T: int):
+        """(v_final [Cout] fp32, silent) of the layer's bias drive alone over
+        T steps (cf_bias_response): each channel's final potential on the
+        StaticZero route, and whether no channel fires there.  Computed once
+        per T (a host read); None while a graph is being captured and the
+        value is not yet known."""
+        r = self._bias_resp.get(T)
+        if r is None:
+            if torch.cuda.is_current_stream_capturing():
+                return None
+            v = torch.empty(self.Cout, dtype=torch.float32, device=device)
+            f = torch.empty(self.Cout, dtype=torch.int32, device=device)
+            check(_hip.lib().cf_bias_response(ptr(self.alpha), ptr(self.beta), self.Cout, T,
+                                              *self.lif, ptr(v), ptr(f), _hip.stream(device)),
+                  "cf_bias_response")
+            r = self._bias_resp[T] = (v, not bool(f.any().item()))
+        return r
+
+    def zero_route_info(self, device, T: int, desc, v_out, v_in):
+        """(bias_info, v_final or None) for a launch with output descriptor
+        desc: the bias_info bits of cf_conv_mfma and the per-channel
+        potentials that stand for v_out when the launch leaves it unwritten."""
+        if desc is None:
+            return 0, None
+        r = self.bias_response(device, T)
+        if r is None:
+            return 0, None
+        v_final, silent = r
+        hold = v_out is not None and v_in is None
+        return (1 if silent else 0) | (2 if hold else 0), (v_final if hold else None)
 
     def out_hw(self, H, W):
         return ((H + 2 * self.padding - self.KH) // self.stride + 1,
@@ -710,7 +874,10 @@ class ConvLIFRunner:
         self._ensure_packed(dev)
         Ho, Wo = self.out_hw(H, W)
         gs = sparse["group_size"] if sparse is not None else 0
-        xp = shadow_of(x, (T * B, H, W, self.Cp))
+        # the dense route reads the copy through its descriptor; SparseFlow
+        # scans it, so an unwritten copy is filled first
+        xp = shadow_of(x, (T * B, H, W, self.Cp), resolve=sparse is not None)
+        x_desc = desc_of(x) if (xp is not None and sparse is None) else None
         nnz = act = None
         if xp is not None and sparse is not None:
             # SparseFlow on an input that carries its fp16 NHWC copy: the
@@ -757,30 +924,45 @@ class ConvLIFRunner:
                 order = compact_tiles(ag, T, B * GH * GW, G, self.workspace(
                     "order", (B * GH * GW + 1,), torch.int32, dev), macs_per_tile=macs_tile,
                     tau=tau, r_min=r_min)
-        id_nhwc = None
+        id_nhwc = id_desc = id_nnz = None
+        id_keep = ()
         if identity is not None:
             require_gpu_tensor(identity, "identity")
             if identity.shape != (T, B, self.Cout, Ho, Wo):
                 raise ValueError("identity shape mismatch")
             if identity_mode == ID_ADD_SPIKE:
                 # spike-valued identity: read its fp16 NHWC copy when current
-                id_nhwc = shadow_of(identity, (T * B, Ho, Wo, pad32(self.Cout)))
+                # (through its descriptor: a fused layer's copy, which an
+                # output equal to it may alias)
+                id_nhwc = shadow_of(identity, (T * B, Ho, Wo, pad32(self.Cout)), resolve=False)
+                if id_nhwc is not None:
+                    id_desc = desc_of(identity)
+                    if id_desc is None:
+                        id_desc = written_desc(dev)
+                    id_nnz = count_of(identity)
+                    id_keep = (id_nhwc,) + keep_of(identity)
         out, v_out = self._launch(
             xp, T, B, H, W, Ho, Wo, x.numel(), nnz, ag, order, th, tw, gs, v_in, epilogue,
             want_v_out,
             None if id_nhwc is not None else identity, id_nhwc, identity_mode, sparse_threshold,
             emit_nhwc, lambda nhwc: lazy_output((T, B, self.Cout, Ho, Wo), nhwc, dev),
-            "conv_mfma" + ("_sparse" if sparse is not None else ""))
+            "conv_mfma" + ("_sparse" if sparse is not None else ""),
+            x_desc=x_desc, id_desc=id_desc, id_nnz=id_nnz, id_keep=id_keep)
         self.last_tiles = None if ag is None else (tc_buf, ag)
         self.last_order = order
         return out, v_out
 
     def _launch(self, xp, T, B, H, W, Ho, Wo, numel, nnz, ag, order, th, tw, gs, v_in, epilogue,
                 want_v_out, identity, id_nhwc, identity_mode, sparse_threshold, emit_nhwc,
-                make_lazy, timer_name):
+                make_lazy, timer_name, x_desc=None, id_desc=None, id_nnz=None, id_keep=()):
         """One cf_conv_mfma launch on the staged fp16 NHWC input xp; the
         output is make_lazy(nhwc copy) when emitting the copy (with its count
-        block attached), else an fp32 NCHW tensor.  Returns (out, v_out)."""
+        block attached), else an fp32 NCHW tensor.  x_desc / id_desc: output
+        descriptors of the input's / identity's copies (see cf_conv_mfma).
+        When the launch may take StaticZero it gets an output descriptor of
+        its own (attached to the output, with id_keep: the copies the output
+        may alias) and, with no initial state, a per-channel state buffer
+        (v_out is then a ChannelState).  Returns (out, v_out)."""
         dev = xp.device
         if v_in is not None:
             require_gpu_tensor(v_in, "v_in")
@@ -804,23 +986,32 @@ class ConvLIFRunner:
         else:
             out = torch.empty((T, B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
             out_ptr = ptr(out)
+        desc = None
+        if (COPY_ELISION and nhwc is not None and epilogue == EPI_LIF
+                and (nnz is not None or x_desc is not None)):
+            desc = new_out_desc(dev)
+            attach_desc(out, desc, id_keep)
+        bias_info, v_chan = self.zero_route_info(dev, T, desc, v_out, v_in)
         ev = _t0()
         rc = _hip.lib().cf_conv_mfma(
             ptr(xp), ptr(self.w_packed), ptr(self.alpha), ptr(self.beta), ptr(v_in), ptr(v_out),
             out_ptr, ptr(nhwc), cp_out, ptr(identity), ptr(id_nhwc), pad32(self.Cout),
-            int(identity_mode), ptr(ag), ptr(order), ptr(nnz), ptr(nz_out), numel,
+            int(identity_mode), ptr(ag), ptr(order), ptr(nnz), ptr(nz_out),
+            ptr(x_desc), ptr(id_desc), ptr(desc), bias_info, ptr(id_nnz), numel,
             float(sparse_threshold), T, B, self.Cp, self.Cout, self.Coutp, H, W, Ho, Wo, self.KH,
             self.KW, self.stride, self.padding, B, th, tw, gs, int(epilogue), *self.lif,
             _hip.stream(dev))
         check(rc, "cf_conv_mfma")
-        out_bytes = (2 * T * B * Ho * Wo * cp_out if nhwc is not None else 0) \
-            + (4 * T * B * Ho * Wo * self.Cout if out_ptr is not None else 0) \
-            + (4 * B * Ho * Wo * self.Cout if v_out is not None else 0)
+        copy_bytes = (2 * T * B * Ho * Wo * cp_out if nhwc is not None else 0) \
+            + (4 * T * B * Ho * Wo * self.Cout if out_ptr is not None else 0)
+        state_bytes = 4 * B * Ho * Wo * self.Cout if v_out is not None else 0
         _t1(timer_name, ev, flops=2 * T * B * Ho * Wo * self.Cout * self.Cin * self.KH * self.KW,
-            route=None if nnz is None else _RouteProbe(nnz, out_bytes))
+            route=None if nnz is None else _RouteProbe(nnz, [(desc, copy_bytes, state_bytes)]))
         self.last_nnz = nnz  # count block of this input (None: not counted)
         self.last_numel = numel
-        return out, (v_out if want_v_out else None)
+        if not want_v_out:
+            return out, None
+        return out, (ChannelState(v_out, v_chan, desc) if v_chan is not None else v_out)
 
     def run_tokens(self, x: torch.Tensor, v_in=None, *, identity=None, want_v_out=True,
                    static_zero=True, grid=None):
@@ -1078,9 +1269,11 @@ def run_halo_pair(ra: "ConvLIFRunner", rb: "ConvLIFRunner", x: torch.Tensor, v_i
     ra._ensure_packed(dev)
     rb._ensure_packed(dev)
     Ho, Wo = ra.out_hw(H, W)
-    xp = shadow_of(x, (T * B, H, W, ra.Cp))
+    xp = shadow_of(x, (T * B, H, W, ra.Cp), resolve=False)
+    x_desc = None
     if xp is not None:
         nnz = count_of(x)
+        x_desc = desc_of(x)
     else:
         nnz = ra.counter(dev)
         xp = ra.workspace("xp", (T * B, H, W, ra.Cp), torch.float16, dev)
@@ -1099,23 +1292,34 @@ def run_halo_pair(ra: "ConvLIFRunner", rb: "ConvLIFRunner", x: torch.Tensor, v_i
         nz = r.out_counter(dev)
         r._gen[0] += 1
         attach_count(out, nz, r._gen)
-        outs.append((r, v_in, v_out, nhwc, cp, nz, out))
-    (_, va, voa, na, cpa, nza, oa), (_, vb, vob, nb, cpb, nzb, ob) = outs
+        desc = None
+        if COPY_ELISION and (nnz is not None or x_desc is not None):
+            # StaticZero may leave the outputs unwritten (no identity here)
+            desc = new_out_desc(dev)
+            attach_desc(out, desc)
+        info, v_chan = r.zero_route_info(dev, T, desc, v_out, v_in)
+        outs.append((r, v_in, v_out, nhwc, cp, nz, out, desc, info, v_chan))
+    ((_, va, voa, na, cpa, nza, oa, da, ia, ca),
+     (_, vb, vob, nb, cpb, nzb, ob, db, ib, cb)) = outs
     ev = _t0()
     check(_hip.lib().cf_conv_halo_pair(
-        ptr(xp), ptr(nnz), x.numel(), T, B, ra.Cp, H, W, Ho, Wo,
+        ptr(xp), ptr(nnz), ptr(x_desc), x.numel(), T, B, ra.Cp, H, W, Ho, Wo,
         ptr(ra.w_packed), ptr(ra.alpha), ptr(ra.beta), ptr(va), ptr(voa), ptr(na), cpa, ptr(nza),
-        ra.Cout, ra.Coutp, ra.padding,
+        ptr(da), ia, ra.Cout, ra.Coutp, ra.padding,
         ptr(rb.w_packed), ptr(rb.alpha), ptr(rb.beta), ptr(vb), ptr(vob), ptr(nb), cpb, ptr(nzb),
-        rb.Cout, rb.Coutp, rb.padding, *ra.lif, _hip.stream(dev)), "cf_conv_halo_pair")
+        ptr(db), ib, rb.Cout, rb.Coutp, rb.padding, *ra.lif, _hip.stream(dev)),
+        "cf_conv_halo_pair")
     flops = 2 * T * B * Ho * Wo * C * (ra.Cout * 9 + rb.Cout)
-    nbytes = sum(2 * T * B * Ho * Wo * cp + 4 * B * Ho * Wo * r.Cout
-                 for r, cp in ((ra, cpa), (rb, cpb)))
-    _t1("conv_pair", ev, flops=flops,
-        route=None if nnz is None else _RouteProbe(nnz, nbytes))
+    parts = [(d, 2 * T * B * Ho * Wo * cp, 4 * B * Ho * Wo * r.Cout)
+             for d, cp, r in ((da, cpa, ra), (db, cpb, rb))]
+    _t1("conv_pair", ev, flops=flops, route=None if nnz is None else _RouteProbe(nnz, parts))
     for r in (ra, rb):
         r.last_nnz = nnz
         r.last_numel = x.numel()
+    if ca is not None:
+        voa = ChannelState(voa, ca, da)
+    if cb is not None:
+        vob = ChannelState(vob, cb, db)
     return oa, voa, ob, vob
 
 

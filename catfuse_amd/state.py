@@ -36,7 +36,12 @@ class StateBuffer:
         return v
 
     def set(self, v: torch.Tensor) -> None:
-        self._v = v.detach()
+        # a fused launch's lazily filled state (no autograd history) is kept
+        # as it is: detach() would fill it now
+        if hasattr(v, "cf_materialize") and not v.requires_grad:
+            self._v = v
+        else:
+            self._v = v.detach()
 
     def reset(self) -> None:
         self._v = None

@@ -118,9 +118,25 @@ int cf_nhwc_to_nchw(const void* xp, float* out, int64_t NB, int64_t C, int64_t H
  * for the integer values a fused conv's copy holds.  No counterpart in the
  * reference (the network head after the fused layers is SpikingJelly's
  * layer.AdaptiveAvgPool2d); it reads the copy instead of materialising the
- * fp32 feature map. */
-int cf_global_avgpool_nhwc(const void* xp, float* out, int64_t NB, int64_t HW, int64_t C,
-                           int64_t cp, void* stream);
+ * fp32 feature map.  desc (nullable): the copy's output descriptor (see
+ * cf_conv_mfma): an all-zero copy pools to zeros, an aliased one is read
+ * where it points. */
+int cf_global_avgpool_nhwc(const void* xp, const void* desc, float* out, int64_t NB, int64_t HW,
+                           int64_t C, int64_t cp, void* stream);
+
+/* Output descriptors.  A fused conv given an output descriptor (16 bytes of
+ * device memory: uint32 copy, uint32 vstate, pointer alias) records there
+ * how it left its outputs: copy 0 written, 1 all zero and the fp16 copy not
+ * written, 2 equal to the copy at alias (its identity) and not written;
+ * vstate 1: every pixel of channel c holds v_chan[c] and v_out was not
+ * written.  cf_resolve_copy makes the buffer xp (bytes, a multiple of 16,
+ * 16-byte aligned) hold the values when it was not written (zeros, or the
+ * aliased bytes); cf_expand_state fills v [B][C][HW] from v_chan when
+ * vstate is 1.  Both leave written outputs alone.  No counterpart in the
+ * reference (its fused layers always write their outputs). */
+int cf_resolve_copy(void* xp, int64_t bytes, const void* desc, void* stream);
+int cf_expand_state(float* v, const float* v_chan, const void* desc, int64_t B, int64_t C,
+                    int64_t HW, void* stream);
 
 /* Token-major fp32 x [rows][C] (a transformer's [T, B, N, C] activations)
  * -> its fp16 copy xp [rows][cp] (cp >= C, cp % 8 == 0, channels >= C zero),
@@ -264,6 +280,24 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
  *   number of workgroups that stored a nonzero value (0 iff the output is
  *   all zero), so the next fused conv can route on it without a counting
  *   pass.  All routes give bit-identical results.
+ *   Output descriptors (each nullable, see cf_resolve_copy): x_desc /
+ *   id_desc are those of the input's / identity's copies as their producers
+ *   left them: an all-zero input takes StaticZero without reading x, an
+ *   all-zero identity is read as zeros, aliased ones where they point.
+ *   out_desc receives this launch's.  bias_info (needs out_desc) is what
+ *   the caller knows from cf_bias_response for this layer and T: bit 0, no
+ *   channel fires on its bias drive alone; bit 1, the caller holds the
+ *   per-channel final potentials.  A halo launch on StaticZero with the
+ *   lean epilogue (out_nhwc only), no v_in and bit 0 writes no out_nhwc and
+ *   records it as all zero (no identity, or an all-zero one; nz_out
+ *   publishes 0) or as an alias of the identity's copy (id_desc given, the
+ *   identity a fused layer's copy of spike counts, and cp_id == cp_out;
+ *   nz_out publishes nonzero unless id_nnz, the identity's count block,
+ *   says zero); with bit 1 such a launch also leaves v_out unwritten
+ *   (vstate 1: every pixel of channel c holds v_final[c]).  Every other
+ *   launch writes its outputs and records so.  A caller that passes
+ *   out_desc reads the outputs through it (or hands it on as x_desc /
+ *   id_desc).
  * Replaces catfuse/implementations/dense_keep.py:97-155 (DenseKeep.forward),
  * catfuse/implementations/sparse_flow.py:186-270 (SparseFlow.forward ->
  * catfuse/sparseflow/streamfuse_kernel.py:32-187), and
@@ -272,8 +306,10 @@ int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha, const 
                  const float* v_in, float* v_out, float* out, void* out_nhwc, int64_t cp_out,
                  const float* identity, const void* identity_nhwc, int64_t cp_id,
                  int identity_mode, const int32_t* ag_mask, const int32_t* tile_order,
-                 const unsigned long long* nnz,
-                 unsigned long long* nz_out, int64_t numel, double sparse_threshold, int64_t T,
+                 const unsigned long long* nnz, unsigned long long* nz_out,
+                 const void* x_desc, const void* id_desc, void* out_desc, int bias_info,
+                 const unsigned long long* id_nnz, int64_t numel, double sparse_threshold,
+                 int64_t T,
                  int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo, int64_t KH,
                  int64_t KW, int64_t stride, int64_t pad, int64_t x_img_tstride, int64_t tile_h,
                  int64_t tile_w, int64_t group_size, int epilogue, double tau, double v_th,
@@ -291,8 +327,10 @@ int cf_conv_halo(const void* x, const void* w_packed, const float* alpha, const 
                  const float* v_in, float* v_out, float* out, void* out_nhwc, int64_t cp_out,
                  const float* identity, const void* identity_nhwc, int64_t cp_id,
                  int identity_mode, const int32_t* ag_mask, const int32_t* tile_order,
-                 const unsigned long long* nnz,
-                 unsigned long long* nz_out, int64_t numel, double sparse_threshold, int64_t T,
+                 const unsigned long long* nnz, unsigned long long* nz_out,
+                 const void* x_desc, const void* id_desc, void* out_desc, int bias_info,
+                 const unsigned long long* id_nnz, int64_t numel, double sparse_threshold,
+                 int64_t T,
                  int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
                  int64_t ksize, int64_t stride, int64_t pad, int64_t tile_h, int64_t tile_w,
                  int64_t group_size, int epilogue, double tau, double v_th, double v_reset,
@@ -305,21 +343,40 @@ int cf_conv_halo(const void* x, const void* w_packed, const float* alpha, const 
  * reading x through the L2 once.  Both with the lean LIF epilogue: fp16
  * NHWC outputs out_a / out_b only (Cout a multiple of 32, no fp32 output,
  * no identity), v_in / v_out as cf_conv_mfma, their own count blocks nz_a /
- * nz_b; the input's count block nnz (nullable) routes both (StaticZero on
- * a zero count); one set of LIF parameters for both.  w/alpha/beta from
+ * nz_b, output descriptors desc_a / desc_b and bias knowledge
+ * bias_info_a / bias_info_b (as out_desc / bias_info of cf_conv_mfma); the
+ * input's count block nnz and descriptor x_desc (both nullable) route both
+ * (StaticZero on a zero count or an all-zero copy); one set of LIF
+ * parameters for both.  w/alpha/beta from
  * cf_pack_conv_weights.  Replaces the two launches of
  * catfuse/patterns.py:672-737 (SEWBasicBlock: conv1-bn1-sn1 and
  * downsample-downsample_sn of the same input). */
-int cf_conv_halo_pair(const void* x, const unsigned long long* nnz, int64_t numel, int64_t T,
-                      int64_t B, int64_t Cp, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
+int cf_conv_halo_pair(const void* x, const unsigned long long* nnz, const void* x_desc,
+                      int64_t numel, int64_t T, int64_t B, int64_t Cp, int64_t H, int64_t W,
+                      int64_t Ho, int64_t Wo,
                       const void* w_a, const float* alpha_a, const float* beta_a,
                       const float* v_in_a, float* v_out_a, void* out_a, int64_t cp_out_a,
-                      unsigned long long* nz_a, int64_t Cout_a, int64_t Coutp_a, int64_t pad_a,
+                      unsigned long long* nz_a, void* desc_a, int bias_info_a, int64_t Cout_a,
+                      int64_t Coutp_a, int64_t pad_a,
                       const void* w_b, const float* alpha_b, const float* beta_b,
                       const float* v_in_b, float* v_out_b, void* out_b, int64_t cp_out_b,
-                      unsigned long long* nz_b, int64_t Cout_b, int64_t Coutp_b, int64_t pad_b,
+                      unsigned long long* nz_b, void* desc_b, int bias_info_b, int64_t Cout_b,
+                      int64_t Coutp_b, int64_t pad_b,
                       double tau, double v_th, double v_reset, int hard_reset, int decay_input,
                       void* stream);
+
+/* A layer's response to its BN bias alone (the StaticZero drive z =
+ * 0 * alpha + beta, alpha/beta from cf_pack_conv_weights, Cout entries),
+ * from the initial state over T steps, with the halo kernel's operations:
+ * v_final [Cout] the final potential and fires [Cout] 1 where the channel
+ * fires at some step.  Computed once per layer and T; the bias_info of
+ * cf_conv_mfma states it.  No counterpart in the reference (its StaticZero
+ * short-circuit, catfuse/implementations/base.py:250-308
+ * static_zero_forward, broadcasts the bias and runs the LIF on every
+ * call). */
+int cf_bias_response(const float* alpha, const float* beta, int64_t Cout, int64_t T, double tau,
+                     double v_th, double v_reset, int hard_reset, int decay_input,
+                     float* v_final, uint32_t* fires, void* stream);
 
 /* Fused Conv -> BN -> LIF / z in fp32 (VALU) for analog inputs
  * x [T*x_img_tstride + B][Cin][H][W]; x_img_tstride == 0 evaluates the

@@ -65,21 +65,43 @@ def test_host_side_argument_validation():
     assert L.cf_lif_multistep(1, None, None, None, 1, None, 1, 0, None, 4, 16, 1, 1,
                               2.0, 1.0, 0.0, 1, 1, None) == INVALID
     # conv: Cp not a multiple of 32
-    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, None, None, 0, 0.7,
+    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, None, None,
+                          None, None, None, 0, None, 0, 0.7,
                           4, 2, 48, 64, 64, 8, 8, 8, 8, 3, 3, 1, 1, 2, 0, 0, 0,
                           0, 2.0, 1.0, 0.0, 1, 1, None) == INVALID
     # conv: inconsistent output size
-    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, None, None, 0, 0.7,
+    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, None, None,
+                          None, None, None, 0, None, 0, 0.7,
                           4, 2, 64, 64, 64, 8, 8, 7, 8, 3, 3, 1, 1, 2, 0, 0, 0,
                           0, 2.0, 1.0, 0.0, 1, 1, None) == INVALID
     # conv: rect tile must hold 64 or 128 pixels
-    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, None, None, 0, 0.7,
+    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, None, None, None,
+                          None, None, None, 0, None, 0, 0.7,
                           4, 2, 64, 64, 64, 8, 8, 8, 8, 3, 3, 1, 1, 2, 4, 4, 16,
                           0, 2.0, 1.0, 0.0, 1, 1, None) == INVALID
     # conv: a tile order needs tile masks
     assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, None, 0, None, None, 0, 0, None, 1, None, None,
+                          None, None, None, 0, None,
                           0, 0.7, 4, 2, 64, 64, 64, 8, 8, 8, 8, 3, 3, 1, 1, 2, 8, 8, 16,
                           0, 2.0, 1.0, 0.0, 1, 1, None) == INVALID
+    # conv: bias knowledge needs an output descriptor; unknown bits
+    for x_desc, out_desc, info in ((None, None, 1), (None, None, 2), (None, 1, 4)):
+        assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, 1, 64, None, None, 0, 0, None, None, None,
+                              None, x_desc, None, out_desc, info, None,
+                              0, 0.7, 4, 2, 64, 64, 64, 8, 8, 8, 8, 3, 3, 1, 1, 2, 0, 0, 0,
+                              0, 2.0, 1.0, 0.0, 1, 1, None) == INVALID
+    assert L.cf_bias_response(1, 1, 0, 4, 2.0, 1.0, 0.0, 1, 1, 1, 1, None) == INVALID
+    assert L.cf_bias_response(1, None, 8, 4, 2.0, 1.0, 0.0, 1, 1, 1, 1, None) == INVALID
+    assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, 1, 64, None, None, 0, 0, None, None, None, None,
+                          None, None, None, 1, None,
+                          0, 0.7, 4, 2, 64, 64, 64, 8, 8, 8, 8, 3, 3, 1, 1, 2, 0, 0, 0,
+                          0, 2.0, 1.0, 0.0, 1, 1, None) == INVALID
+    # descriptor resolution / state expansion: misaligned or partial units
+    assert L.cf_resolve_copy(1, 24, 16, None) == INVALID
+    assert L.cf_resolve_copy(8, 32, 16, None) == INVALID
+    assert L.cf_resolve_copy(16, 32, None, None) == INVALID
+    assert L.cf_expand_state(16, 16, None, 2, 4, 4, None) == INVALID
+    assert L.cf_expand_state(16, 16, 16, 2, 0, 4, None) == INVALID
     # compaction: no tiles / no mask
     assert L.cf_compact_tiles(1, 4, 0, 8, 0.0, -1.0, 0.0, 1, None) == INVALID
     assert L.cf_compact_tiles(None, 4, 8, 8, 0.0, -1.0, 0.0, 1, None) == INVALID
@@ -87,9 +109,9 @@ def test_host_side_argument_validation():
     assert L.cf_compact_tiles(1, 4, 8, 8, float("nan"), -1.0, 0.0, 1, None) == INVALID
     # paired conv: the 1x1 conv's output size differs from the 3x3 conv's
     def pair(Ho=8, Cout_a=64, pad_b=0, out_a=1):
-        return L.cf_conv_halo_pair(1, None, 0, 4, 2, 64, 16, 16, Ho, Ho,
-                                   1, 1, 1, None, 1, out_a, 64, None, Cout_a, 64, 1,
-                                   1, 1, 1, None, 1, 1, 64, None, 64, 64, pad_b,
+        return L.cf_conv_halo_pair(1, None, None, 0, 4, 2, 64, 16, 16, Ho, Ho,
+                                   1, 1, 1, None, 1, out_a, 64, None, None, 0, Cout_a, 64, 1,
+                                   1, 1, 1, None, 1, 1, 64, None, None, 0, 64, 64, pad_b,
                                    2.0, 1.0, 0.0, 1, 1, None)
     assert pair(pad_b=1) == INVALID                 # 1x1/s2 with padding 1: 9x9 output
     assert pair(Ho=7) == INVALID                    # inconsistent output size

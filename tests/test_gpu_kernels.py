@@ -602,6 +602,93 @@ def test_sew_block_downsample_pair_matches_separate(cuda):
     assert len(seen) == 1 and seen[0].shape == (4, 2, 128, 8, 8)
 
 
+def _elision_chain(cuda, elide):
+    """A chain of fused convs over all-zero and live inputs, each layer's
+    output and state materialised at the end; with elide the StaticZero
+    launches may leave their outputs unwritten (output descriptors)."""
+    from catfuse_amd import runtime, snn
+    runtime.COPY_ELISION = elide
+    try:
+        T, B, C, H = 4, 2, 64, 16
+        lif = snn.LIFNode(tau=2.0, v_threshold=0.5, v_reset=0.0)
+
+        def layer(seed, k=3, s=1, p=1, bias_fill=None, cout=C):
+            conv, bn, _ = _layer(C, cout, k, s, p, seed=seed)
+            if bias_fill is not None:
+                with torch.no_grad():
+                    bn.bias.copy_(bias_fill(bn.bias))
+            return _runner(conv, bn, lif, cuda)
+
+        quiet = lambda b: torch.full_like(b, -0.2)   # no channel fires on its bias
+        r0 = layer(31)
+        r_kill = layer(32, bias_fill=lambda b: torch.full_like(b, -8.0))
+        r1, r2, r3 = layer(33, bias_fill=quiet), layer(34, bias_fill=quiet), layer(35)
+
+        def one_hot_bias(b):
+            b = b.clone()
+            b[5] = 4.0   # channel 5 fires on its bias alone
+            return b
+        r4 = layer(36, bias_fill=one_hot_bias)
+        ra = layer(37, 3, 2, 1, bias_fill=quiet, cout=128)
+        rb = layer(38, 1, 2, 0, bias_fill=quiet, cout=128)
+        x0 = (torch.rand(T, B, C, H, H, generator=_gen(40)) < 0.3).float().to(cuda)
+        s0, v0 = r0.run_mfma(x0)                       # live
+        z1, v1 = r_kill.run_mfma(s0)                   # dense route, all-zero output
+        z2, v2 = r1.run_mfma(z1)                       # StaticZero, no identity
+        a3, v3 = r2.run_mfma(z2, identity=s0)          # StaticZero, equal to its identity
+        d4, v4 = r3.run_mfma(a3)                       # dense route over a3
+        f5, v5 = r4.run_mfma(z2)                       # StaticZero, one channel fires
+        e6, v6 = r2.run_mfma(z2, identity=z2)          # StaticZero, all-zero identity
+        pa, qa, pb, qb = runtime.run_halo_pair(ra, rb, z2)
+        pc, qc, pd, qd = runtime.run_halo_pair(ra, rb, a3)
+        states = {}
+        for name, t in (("z2", z2), ("a3", a3), ("f5", f5), ("e6", e6), ("pa", pa), ("pb", pb)):
+            d = runtime.desc_of(t)
+            states[name] = None if d is None else d.clone()
+        pools = []
+        for t in (z2, a3, f5):
+            xp = runtime.shadow_of(t, (T * B, H, H, C), resolve=False)
+            pools.append(runtime.global_avgpool_nhwc(xp, C, desc=runtime.desc_of(t)))
+        mp = runtime.maxpool_nhwc(a3, 3, 2, 1)
+        outs = [s0, z1, z2, a3, d4, f5, e6, pa, pb, pc, pd, mp] + pools
+        vs = [v0, v1, v2, v3, v4, v5, v6, qa, qb, qc, qd]
+        # (a runner called twice republishes its block: the later outputs')
+        counts = [int(runtime.count_of(t)[1]) != 0 for t in (z1, z2, d4, f5, e6, pc, pd)]
+        res = ([o.clone() for o in outs], [v.clone() for v in vs], counts, states,
+               runtime.shadow_of(s0, (T * B, H, H, C)).data_ptr())
+        torch.cuda.synchronize()
+        return res
+    finally:
+        runtime.COPY_ELISION = True
+
+
+def test_static_zero_output_elision_bitwise(cuda):
+    """StaticZero launches that provably output nothing new leave their
+    copies unwritten (all zero, or an alias of the identity's copy) and
+    their state per channel; every output, state and count-block verdict of
+    a chain that reads such outputs (convs through the descriptors, the
+    paired launch, the global average pool, the max pool and
+    materialisation through a fill) equals the always-writing path's."""
+    outs_e, vs_e, counts_e, st, s0_ptr = _elision_chain(cuda, True)
+    outs_w, vs_w, counts_w, st_w, _ = _elision_chain(cuda, False)
+    assert all(v is None for v in st_w.values())
+    names = ["s0", "z1", "z2", "a3", "d4", "f5", "e6", "pa", "pb", "pc", "pd", "mp",
+             "pool_z2", "pool_a3", "pool_f5"]
+    for n, a, b in zip(names, outs_e, outs_w):
+        assert torch.equal(a, b), n
+    for i, (a, b) in enumerate(zip(vs_e, vs_w)):
+        assert torch.equal(a, b), f"state {i}"
+    assert counts_e == counts_w
+    # the chain exercised what it names: live data, a zero copy, an alias
+    assert bool(outs_w[0].any()) and not bool(outs_w[2].any()) and bool(outs_w[5].any())
+    assert bool(outs_w[4].any()) and torch.equal(outs_w[3], outs_w[0])
+    copy = {k: int(v[0].item() & 0xffffffff) for k, v in st.items()}
+    vstate = {k: int(v[0].item() >> 32) for k, v in st.items()}
+    assert copy == {"z2": 1, "a3": 2, "f5": 0, "e6": 1, "pa": 1, "pb": 1}
+    assert vstate == {"z2": 1, "a3": 1, "f5": 1, "e6": 1, "pa": 1, "pb": 1}
+    assert int(st["a3"][1].item()) == s0_ptr
+
+
 def test_static_zero_route_equals_bias_only(cuda):
     T, B, C, H, W = 4, 2, 64, 8, 8
     conv, bn, lif = _layer(C, C, 3, 1, 1, seed=8)

@@ -66,7 +66,7 @@ def _existing(r, xp, T, B, C, H, W, tile, gs, thr, dev):
     cp = nhwc.shape[-1]
     assert L.cf_conv_mfma(ptr(xp), ptr(r.w_packed), ptr(r.alpha), ptr(r.beta), None, ptr(v_out),
                           ptr(out), ptr(nhwc), cp, None, None, cp, 1, ptr(ag), None, ptr(blk), ptr(nz),
-                          NB * C * H * W, thr, T, B, r.Cp, r.Cout, r.Coutp, H, W, H, W, 3, 3, 1,
+                          None, None, None, 0, None, NB * C * H * W, thr, T, B, r.Cp, r.Cout, r.Coutp, H, W, H, W, 3, 3, 1,
                           1, B, tile[0], tile[1], gs, 0, *_lif(), st) == 0
     return out, nhwc, v_out, nz, blk
 
