@@ -88,10 +88,19 @@ __device__ __forceinline__ unsigned lds_addr(const void* p) {
   return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
 
-// Time steps per block: 4, or 2 for stride-2 3x3 tiles (17 x 17 input halo).
+// Time steps per block: 4.
 template <int S, int K>
 constexpr int halo_tb() {
-  return (S == 2 && K == 3) ? 2 : 4;
+  return 4;
+}
+
+// Halo buffers: two (the next K step is staged while the current one is
+// computed), or one for stride-2 3x3 tiles, whose 17 x 17 input halo of
+// four steps (74 KB) would not fit twice next to a second workgroup: their
+// K steps stage after the taps, and the CU's other workgroup fills the gap.
+template <int S, int K>
+constexpr int halo_nbuf() {
+  return (S == 2 && K == 3) ? 1 : 2;
 }
 
 // Staged halo geometry and LDS layout: [t][RH][RW] pixels of 64 bytes (32
@@ -176,10 +185,11 @@ __device__ __forceinline__ int halo_route(const unsigned long long* nnz, int64_t
 
 // Workgroups per CU the kernel is sized for: 64 x 64 tiles fit in 168
 // registers (three per CU); 64 x 128 tiles keep twice the accumulators and
-// get the full register budget.
-template <int TH, int TW>
+// get the full register budget; stride-2 3x3 tiles, whose halo buffer
+// leaves room for two workgroups per CU, get two workgroups' budget.
+template <int TH, int TW, int S = 1, int K = 3>
 constexpr int halo_min_blocks() {
-  return TH * TW >= 128 ? 1 : 3;
+  return TH * TW >= 128 ? 1 : ((S == 2 && K == 3) ? 2 : 3);
 }
 
 // K: filter size (3, or 1 for pointwise convolutions, whose strided input
@@ -202,7 +212,7 @@ constexpr int halo_buf_halves() {
 
 // The work of workgroup L of the nL that compute one conv: a device
 // function, so that one grid can run two convs of the same input side by
-// side (conv_halo_pair_kernel).  halo: 2 * halo_buf_halves() halves of LDS;
+// side (conv_halo_pair_kernel).  halo: halo_nbuf() * halo_buf_halves() halves of LDS;
 // bn_s: the tile's BN coefficients; any_sh: the workgroup's vote words.
 template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB, bool HS>
 __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const int nL,
@@ -215,6 +225,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   constexpr int RH = G::RH, RW = G::RW, SS = G::SS;
   constexpr int KK = K * K;
   constexpr int TB = halo_tb<S, K>();
+  constexpr int NBUF = halo_nbuf<S, K>();
   constexpr int TSTR = RH * RW * KC;           // staged time step (halves)
   constexpr int NU = TB * RH * RW * 4;         // 16-byte units per staged chunk
   constexpr int NB = (NU + 63) / 64;           // 64-unit blocks (one direct load each)
@@ -569,7 +580,11 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   // keeps them in registers for its taps (cp_off, bit i of cp_inb, bits
   // 2i.. of cp_t), so a K step's loads cost a few instructions each.
   int cp_off[NPF];
-  uint32_t cp_inb = 0u, cp_t = 0u;
+  // (two bits of cp_t per load: 64 of them once a thread has more than 16)
+  using StepBits = std::conditional_t<(2 * NPF > 32), uint64_t, uint32_t>;
+  static_assert(NPF <= 32, "one bit of cp_inb per direct load");
+  uint32_t cp_inb = 0u;
+  StepBits cp_t = 0u;
   auto units_precompute = [&]() {
     cp_inb = 0u;
     cp_t = 0u;
@@ -579,7 +594,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
       int t;
       unit_of(i, cp_off[i], inb, t);
       cp_inb |= (inb ? 1u : 0u) << i;
-      cp_t |= (uint32_t)t << (2 * i);
+      cp_t |= (StepBits)t << (2 * i);
     }
   };
   // Direct loads i0 .. i1-1 (of NPF) of this thread for K step (tbs, ch)
@@ -601,7 +616,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
         if (4 * NPF > NB && blk >= NB) blk -= NB;
         off = cp_off[i];
         inb = ((cp_inb >> i) & 1u) != 0u;
-        t = (cp_t >> (2 * i)) & 3u;
+        t = (int)((cp_t >> (2 * i)) & 3u);
       } else {
         blk = unit_of(i, off, inb, t);
       }
@@ -668,7 +683,9 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
         if (th == 0) {
           if (tap + 1 < KK) load_w(cur ^ 1, tap + 1, ch);
           else load_w(cur ^ 1, 0, nc);
-          if (KK == 1) {
+          if (NBUF == 1) {
+            // one buffer: the next K step stages after the taps
+          } else if (KK == 1) {
             stage_loads(std::true_type{}, stb, nc, nact, hb_next, 0, NPF);
           } else if (tap + 1 < KK) {
             const int i0 = (tap * NPF) / (KK - 1), i1 = ((tap + 1) * NPF) / (KK - 1);
@@ -740,9 +757,19 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
       // the other buffer, which the taps below refill.
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
-      run_taps(std::integral_constant<bool, HS>{}, halo + buf * HB, halo + (buf ^ 1) * HB, s_ch,
-               ntb, nc, nact, tb0, half_skip ? half_act(s_tb, s_ch) : 0xffffffffu);
-      buf ^= 1;
+      run_taps(std::integral_constant<bool, HS>{}, halo + buf * HB,
+               halo + (NBUF == 2 ? (buf ^ 1) * HB : 0), s_ch, ntb, nc, nact, tb0,
+               half_skip ? half_act(s_tb, s_ch) : 0xffffffffu);
+      if constexpr (NBUF == 1) {
+        // the next K step of this block into the buffer, once every wave
+        // has finished reading it
+        if (ntb == tb0) {
+          __syncthreads();
+          stage_loads(std::true_type{}, ntb, nc, nact, halo, 0, NPF);
+        }
+      } else {
+        buf ^= 1;
+      }
       s_tb = ntb;
       s_ch = nc;
       s_act = nact;
@@ -767,12 +794,14 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     // reuse the units computed for this block: they are the same for every
     // block.  Four-step blocks compute them here, which keeps the units out of
     // the registers live across their K loop.)
-    if (s_tb < a.T && s_tb != pf_tb) {
+    if (NBUF == 2 && s_tb < a.T && s_tb != pf_tb) {
       load_w(0, 0, s_ch);
       stage_loads(std::integral_constant<bool, (TB == 2)>{}, s_tb, s_ch, s_act, halo, 0, NPF);
       pf_tb = s_tb;
     }
-    _Float16* obuf = halo + HB;
+    // (with one halo buffer the output is staged in it, and the next block's
+    // first K step is staged after the epilogue)
+    _Float16* obuf = halo + (NBUF - 1) * HB;
     // Addresses below are a workgroup-uniform 64-bit base (scalar registers)
     // plus a 32-bit per-lane offset.  Lane-constant parts: its channel
     // column (col), its pixel (e_off, 0 for pixels outside the output).
@@ -961,15 +990,25 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
         }
       }
     }
+    // One halo buffer: the next block's first K step, once every wave has
+    // copied its output out of the buffer.
+    if constexpr (NBUF == 1) {
+      if (s_tb < a.T && s_tb != pf_tb) {
+        __syncthreads();
+        load_w(0, 0, s_ch);
+        stage_loads(std::false_type{}, s_tb, s_ch, s_act, halo, 0, NPF);
+        pf_tb = s_tb;
+      }
+    }
   }
   publish_count();
   set_out_desc(CF_COPY_WRITTEN, nullptr, false);
 }
 
 template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB, bool HS = false>
-__global__ __launch_bounds__(256, (halo_min_blocks<TH, TW>()))
+__global__ __launch_bounds__(256, (halo_min_blocks<TH, TW, S, K>()))
 void conv_halo_kernel(HaloArgs a) {
-  __shared__ __attribute__((aligned(16))) _Float16 halo[2 * halo_buf_halves<TH, TW, S, K>()];
+  __shared__ __attribute__((aligned(16))) _Float16 halo[halo_nbuf<S, K>() * halo_buf_halves<TH, TW, S, K>()];
   __shared__ __attribute__((aligned(16))) float bn_s[2][64];  // alpha, beta of the tile
   __shared__ unsigned any_sh[4];  // per-wave votes of the output count
   halo_body<TH, TW, S, K, EPI, LM, LEAN, ONEB, HS>(a, (int)blockIdx.x, (int)gridDim.x, halo,
@@ -1096,10 +1135,11 @@ int make_halo_args(HaloArgs& a, const void* x, const void* w_packed, const float
 // accumulation order, so the same bits), sharing the input through the L2.
 // Lean LIF epilogues only (fp16 NHWC outputs, no identity).
 template <int LM, bool OBA, bool OBB>
-__global__ __launch_bounds__(256, (halo_min_blocks<8, 8>()))
+__global__ __launch_bounds__(256, (halo_min_blocks<8, 8, 2, 3>()))
 void conv_halo_pair_kernel(HaloArgs a, HaloArgs b, int nLa) {
-  constexpr int HA = halo_buf_halves<8, 8, 2, 3>(), HBB = halo_buf_halves<8, 8, 2, 1>();
-  __shared__ __attribute__((aligned(16))) _Float16 halo[2 * (HA > HBB ? HA : HBB)];
+  constexpr int HA = halo_nbuf<2, 3>() * halo_buf_halves<8, 8, 2, 3>();
+  constexpr int HBB = halo_nbuf<2, 1>() * halo_buf_halves<8, 8, 2, 1>();
+  __shared__ __attribute__((aligned(16))) _Float16 halo[HA > HBB ? HA : HBB];
   __shared__ __attribute__((aligned(16))) float bn_s[2][64];
   __shared__ unsigned any_sh[4];
   const int L = (int)blockIdx.x;
