@@ -342,6 +342,19 @@ class ChannelState(_LazyTensor):
                                              _hip.stream(self.device)), "cf_expand_state")
 
 
+def lazy_view(t: torch.Tensor, *shape) -> torch.Tensor:
+    """t.view(*shape), keeping a ChannelState lazy (the view expands itself
+    on first use, from the same per-channel values)."""
+    if isinstance(t, ChannelState):
+        v_chan, desc, _ = t._cf_state
+        with torch._C.DisableTorchFunctionSubclass():
+            base = torch.Tensor.view(t, *shape)
+        v = ChannelState(base, v_chan, desc)
+        v._cf_sticky = t.__dict__.get("_cf_sticky", False)
+        return v
+    return t.view(*shape)
+
+
 def _tensors_in(args, kwargs):
     stack = list(args) + list(kwargs.values())
     while stack:
@@ -383,9 +396,9 @@ def token_membrane(v: torch.Tensor, B: int, N: int) -> torch.Tensor:
     return v.transpose(1, 2).reshape(B, N, v.shape[1])
 
 
-def token_shadow(x: torch.Tensor, cp: int) -> Optional[torch.Tensor]:
+def token_shadow(x: torch.Tensor, cp: int, resolve: bool = True) -> Optional[torch.Tensor]:
     """The current fp16 copy of a token-major x [..., N, C] as [rows, cp]
-    (rows = x.numel() / C), or None."""
+    (rows = x.numel() / C), or None; resolve as shadow_of."""
     sh = getattr(x, "_cf_nhwc", None)
     if sh is None:
         return None
@@ -394,7 +407,8 @@ def token_shadow(x: torch.Tensor, cp: int) -> Optional[torch.Tensor]:
     if (ver != x._version or t.device != x.device or t.shape[-1] != cp
             or t.numel() != rows * cp):
         return None
-    _resolve(x, t)
+    if resolve:
+        _resolve(x, t)
     return t.reshape(rows, cp)
 
 
@@ -990,8 +1004,11 @@ class ConvLIFRunner:
         if (COPY_ELISION and nhwc is not None and epilogue == EPI_LIF
                 and (nnz is not None or x_desc is not None)):
             desc = new_out_desc(dev)
-            attach_desc(out, desc, id_keep)
         bias_info, v_chan = self.zero_route_info(dev, T, desc, v_out, v_in)
+        if bias_info & 1:
+            # the launch may leave the copy unwritten: readers go through
+            # the descriptor (otherwise it always writes the copy)
+            attach_desc(out, desc, id_keep)
         ev = _t0()
         rc = _hip.lib().cf_conv_mfma(
             ptr(xp), ptr(self.w_packed), ptr(self.alpha), ptr(self.beta), ptr(v_in), ptr(v_out),
@@ -1039,22 +1056,31 @@ class ConvLIFRunner:
             (H, W), nimg = grid, B
         if nimg * H * W != B * N:
             raise ValueError("token grid does not match N")
-        xp = token_shadow(x, self.Cp)
-        nnz = None
+        xp = token_shadow(x, self.Cp, resolve=False)
+        nnz = x_desc = None
         if xp is not None:
             nnz = count_of(x) if static_zero else None
+            x_desc = desc_of(x)
         else:
             nnz = self.counter(dev) if static_zero else None
             xp = pack_tokens(x, self.Cp, nnz=nnz, status=status_word(dev),
                              out=self.workspace("xp", (T * B * N, self.Cp), torch.float16, dev))
         id_cp = pad32(self.Cout)
-        id_copy = None
+        id_copy = id_desc = id_nnz = None
+        id_keep = ()
         if identity is not None:
             require_gpu_tensor(identity, "identity")
             if tuple(identity.shape) != (T, B, N, self.Cout):
                 raise ValueError("identity shape mismatch")
-            id_copy = token_shadow(identity, id_cp)
-            if id_copy is None:
+            id_copy = token_shadow(identity, id_cp, resolve=False)
+            if id_copy is not None:
+                # a fused layer's copy, read through its descriptor
+                id_desc = desc_of(identity)
+                if id_desc is None:
+                    id_desc = written_desc(dev)
+                id_nnz = count_of(identity)
+                id_keep = (id_copy,) + keep_of(identity)
+            else:
                 id_copy = pack_tokens(identity, id_cp, status=status_word(dev),
                                       out=self.workspace("idp", (T * B * N, id_cp),
                                                          torch.float16, dev))
@@ -1062,8 +1088,9 @@ class ConvLIFRunner:
             xp.view(T * nimg, H, W, self.Cp), T, nimg, H, W, H, W, x.numel(), nnz, None, None,
             0, 0, 0, v_in, EPI_LIF, want_v_out, None,
             None if id_copy is None else id_copy.view(T * nimg, H, W, id_cp), ID_ADD_SPIKE, 2.0,
-            True, lambda nhwc: lazy_tokens((T, B, N, self.Cout), nhwc, dev), "linear_tokens")
-        return out, (None if v_out is None else v_out.view(nimg, self.Cout, H * W))
+            True, lambda nhwc: lazy_tokens((T, B, N, self.Cout), nhwc, dev), "linear_tokens",
+            x_desc=x_desc, id_desc=id_desc, id_nnz=id_nnz, id_keep=id_keep)
+        return out, (None if v_out is None else lazy_view(v_out, nimg, self.Cout, H * W))
 
     def run_direct(self, x: torch.Tensor, v_in=None, *, epilogue=EPI_LIF, want_v_out=True,
                    emit_nhwc=False):
@@ -1294,10 +1321,11 @@ def run_halo_pair(ra: "ConvLIFRunner", rb: "ConvLIFRunner", x: torch.Tensor, v_i
         attach_count(out, nz, r._gen)
         desc = None
         if COPY_ELISION and (nnz is not None or x_desc is not None):
-            # StaticZero may leave the outputs unwritten (no identity here)
             desc = new_out_desc(dev)
-            attach_desc(out, desc)
         info, v_chan = r.zero_route_info(dev, T, desc, v_out, v_in)
+        if info & 1:
+            # StaticZero may leave the copy unwritten (no identity here)
+            attach_desc(out, desc)
         outs.append((r, v_in, v_out, nhwc, cp, nz, out, desc, info, v_chan))
     ((_, va, voa, na, cpa, nza, oa, da, ia, ca),
      (_, vb, vob, nb, cpb, nzb, ob, db, ib, cb)) = outs

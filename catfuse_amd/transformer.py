@@ -23,7 +23,8 @@ import torch.nn as nn
 
 from catfuse_amd.patterns import (CTFPattern, PartialFusionConvBNLIF, conv_unsupported_reason,
                                   fold_bn, is_lif_node, lif_params)
-from catfuse_amd.runtime import (ConvLIFRunner, count_block, count_of, lazy_tokens, lif_multistep,
+from catfuse_amd.runtime import (ConvLIFRunner, attach_desc, count_block, count_of, desc_of,
+                                 keep_of, lazy_tokens, lif_multistep,
                                  maxpool_nhwc,
                                  pad32, shadow_of, spike_attention_lif, token_membrane,
                                  token_shadow, token_view)
@@ -186,13 +187,19 @@ class CTFSpikformerSSA(CTFPattern):
         qkv = self.qkv(x)
         lp = self.attn_lif
         v_in = self.attn_state.peek((B, N, C), x.device)
-        copy = token_shadow(qkv, pad32(3 * C)) if self.kernel_covers(N) else None
+        nnz = count_of(qkv)
+        # With a current count block the kernel takes its zero route on an
+        # all-zero copy and reads nothing, so a copy its producer left
+        # unwritten (all zero) need not be filled; one that may alias
+        # another copy is.
+        copy = (token_shadow(qkv, pad32(3 * C), resolve=nnz is None or bool(keep_of(qkv)))
+                if self.kernel_covers(N) else None)
         if copy is not None:
             a, v = spike_attention_lif(copy, T, B, N, self.num_heads, (0, C, 2 * C), self.scale,
                                        tau=lp["tau"], v_threshold=lp["v_threshold"],
                                        v_reset=lp["v_reset"], decay_input=lp["decay_input"],
                                        v_in=v_in, nz_out=self._attn_block(x.device),
-                                       gen_cell=self._attn_gen, nnz=count_of(qkv))
+                                       gen_cell=self._attn_gen, nnz=nnz)
         else:
             a, v = self._gemm_core(qkv, v_in)
         self.attn_state.set(v)
@@ -309,10 +316,13 @@ class CTFSpikformerSPS(CTFPattern):
                 y = yp
         r = self.rpe(y, sew_identity=y)
         C, H, W = r.shape[2:]
-        copy = shadow_of(r, (T * B, H, W, pad32(C)))
+        copy = shadow_of(r, (T * B, H, W, pad32(C)), resolve=False)
         if copy is None:
             return r.flatten(-2).transpose(-1, -2).contiguous()
         tok = lazy_tokens((T, B, H * W, C), copy, r.device)
+        if desc_of(r) is not None:
+            # the same copy, as its producer left it
+            attach_desc(tok, desc_of(r), keep_of(r))
         if count_of(r) is not None:
             # the same values: the rpe conv's count block describes the tokens
             tok._cf_count = r._cf_count[:3] + (tok._version,)

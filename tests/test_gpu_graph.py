@@ -79,3 +79,51 @@ def test_graph_replays_of_a_model_ending_in_a_fused_conv(cuda):
                 assert torch.equal(y, eager[i]), f"replay {rep}, input {i}"
                 snn.functional.reset_net(fused)
                 fused(xs[(i + 2) % 3])     # eager work between replays
+
+
+def test_graph_replays_keep_elided_outputs_and_states_current(cuda):
+    """Replays alternating between an all-zero input (every fused conv takes
+    StaticZero: its output recorded in a descriptor, its state kept per
+    channel) and live ones: after every replay the output and every fused
+    layer's membrane state equal the eager forward's, bit for bit."""
+    import catfuse_amd
+    from catfuse_amd import graph, snn
+    from catfuse_amd.state import StateBuffer
+    g = torch.Generator().manual_seed(5)
+    m = torch.nn.Sequential(
+        snn.Conv2d(16, 32, 3, 1, 1, bias=False), snn.BatchNorm2d(32), snn.LIFNode(v_threshold=0.3),
+        snn.Conv2d(32, 32, 3, 1, 1, bias=False), snn.BatchNorm2d(32), snn.LIFNode(v_threshold=0.3),
+        snn.Conv2d(32, 32, 3, 1, 1, bias=False), snn.BatchNorm2d(32), snn.LIFNode(v_threshold=0.3))
+    snn.functional.set_step_mode(m, "m")
+    snn.kaiming_init(m, g)
+    snn.randomize_bn(m, g)
+    with torch.no_grad():
+        for mod in m.modules():
+            if isinstance(mod, torch.nn.BatchNorm2d):
+                mod.bias.fill_(-0.2)     # no channel fires on its bias alone
+    fused, _ = catfuse_amd.optimize(m.eval(), device=cuda, T=4)
+    bufs = [mod.state for mod in fused.modules() if isinstance(getattr(mod, "state", None), StateBuffer)]
+    assert len(bufs) == 3
+    T, B = 4, 2
+    live = [(torch.rand(T, B, 16, 24, 24, generator=g) < 0.3).float().to(cuda) for _ in range(2)]
+    xs = [torch.zeros_like(live[0]), live[0], torch.zeros_like(live[0]), live[1]]
+
+    def states():
+        return [b.tensor.clone() for b in bufs]
+
+    with torch.no_grad():
+        eager = []
+        for x in xs:
+            snn.functional.reset_net(fused)
+            y = fused(x).clone()
+            eager.append((y, states()))
+        assert bool(eager[1][0].any()) and not bool(eager[0][0].any())
+        graphed = graph.capture(fused, xs[1])
+        for rep in range(2):
+            for i, x in enumerate(xs):
+                y = graphed(x).clone()
+                got = states()
+                torch.cuda.synchronize()
+                assert torch.equal(y, eager[i][0]), f"replay {rep}, input {i}: output"
+                for k, (a, b) in enumerate(zip(got, eager[i][1])):
+                    assert torch.equal(a, b), f"replay {rep}, input {i}: state of layer {k}"
