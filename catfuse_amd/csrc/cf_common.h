@@ -121,6 +121,10 @@ __device__ __forceinline__ float lif_initial_v(const LifParams& p) {
   return p.hard ? p.v_reset : 0.0f;
 }
 
+// Cache-policy operand of the raw buffer store builtins: the non-temporal
+// (streaming) hint.
+constexpr int CF_CPOL_NT = 2;
+
 // Count block of a producer pass (cf_pack_input, cf_scan_nhwc, a fused conv
 // writing its output): CF_COUNT_BLOCK_WORDS u64,
 //   [0] the pass accumulator, (sum of counts) << CF_TALLY_BITS | completed

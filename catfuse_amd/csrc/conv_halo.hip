@@ -947,8 +947,11 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
             const uint32_t off =
                 ok ? (uint32_t)((((oh0 + py) * a.Wo + ow0 + pxx) * a.cp_out + cout0 + part * 8) * 2)
                    : HALO_OOB;
+            // streaming (non-temporal) stores: the copy is read back by the
+            // next layer only after the whole output is written
             __builtin_amdgcn_raw_buffer_store_b128(
-                *reinterpret_cast<const u32x4*>(&ostage[px * OLD + part * 8]), ro, off, 0, 0);
+                *reinterpret_cast<const u32x4*>(&ostage[px * OLD + part * 8]), ro, off, 0,
+                CF_CPOL_NT);
           }
         } else {
 #pragma unroll
