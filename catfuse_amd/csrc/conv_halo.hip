@@ -175,14 +175,6 @@ struct HaloArgs {
   LifParams lif;
 };
 
-__device__ __forceinline__ int halo_route(const unsigned long long* nnz, int64_t numel,
-                                          double thr) {
-  if (!nnz) return CF_ROUTE_DENSE;
-  const unsigned long long k = cf_count_read(nnz);
-  if (k == 0) return CF_ROUTE_ZERO;
-  return (1.0 - (double)k / (double)numel > thr) ? CF_ROUTE_SPARSE : CF_ROUTE_DENSE;
-}
-
 // Workgroups per CU the kernel is sized for: 64 x 64 tiles fit in 168
 // registers (three per CU); 64 x 128 tiles keep twice the accumulators and
 // get the full register budget; stride-2 3x3 tiles, whose halo buffer
@@ -259,15 +251,32 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   // ones (epilogue only): the long workgroups start first on every XCD.
   // A tile order whose count is negative (cf_compact_tiles' dispatch score
   // rejected SparseFlow) turns the sparse route into the dense one.
-  int route = halo_route(a.nnz, a.numel, a.sparse_thr);
+  // The words that decide the route and where the input and identity are
+  // (the input's count, the copies' descriptors, the identity's count),
+  // loaded together: an absent one reads the zero page instead (a written
+  // copy, a zero count), its absence kept apart.
+  const unsigned long long* const zp = reinterpret_cast<const unsigned long long*>(&g_halo_zero);
+  const CfOutDesc* const zdesc = reinterpret_cast<const CfOutDesc*>(&g_halo_zero);
+  const unsigned long long in_count = *(a.nnz != nullptr ? a.nnz + 1 : zp);
+  const unsigned long long id_count = *(a.id_nnz != nullptr ? a.id_nnz + 1 : zp);
+  const CfOutDesc xd = *(a.x_desc != nullptr ? a.x_desc : zdesc);
+  const CfOutDesc idd = *(a.id_desc != nullptr ? a.id_desc : zdesc);
+  int route = a.nnz == nullptr ? CF_ROUTE_DENSE
+              : in_count == 0ull ? CF_ROUTE_ZERO
+              : ((1.0 - (double)in_count / (double)a.numel > a.sparse_thr) ? CF_ROUTE_SPARSE
+                                                                          : CF_ROUTE_DENSE);
   if (route == CF_ROUTE_SPARSE && a.order != nullptr && a.order[0] < 0) route = CF_ROUTE_DENSE;
   // The input and identity copies where their producers left the values:
   // an all-zero input takes StaticZero (its buffer is not read), an
   // all-zero identity is read as zeros, aliased ones where they point.
-  const _Float16* const xsrc = cf_copy_source(a.x_desc, a.x);
+  const _Float16* const xsrc = xd.copy == CF_COPY_ZERO    ? nullptr
+                               : xd.copy == CF_COPY_ALIAS ? (const _Float16*)xd.alias
+                                                          : a.x;
   if (xsrc == nullptr) route = CF_ROUTE_ZERO;
-  const _Float16* const id_nhwc =
-      a.identity_nhwc != nullptr ? cf_copy_source(a.id_desc, a.identity_nhwc) : nullptr;
+  const _Float16* const id_nhwc = a.identity_nhwc == nullptr   ? nullptr
+                                  : idd.copy == CF_COPY_ZERO  ? nullptr
+                                  : idd.copy == CF_COPY_ALIAS ? (const _Float16*)idd.alias
+                                                              : a.identity_nhwc;
   auto set_out_desc = [&](uint32_t copy, const void* alias, bool vchan) {
     if (a.out_desc != nullptr && tid == 0 && L == 0) {
       a.out_desc->copy = copy;
@@ -297,7 +306,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     } else if (a.id_desc != nullptr && a.cp_id == a.cp_out) {
       zcopy = CF_COPY_ALIAS;
       zalias = id_nhwc;
-      id_live = a.id_nnz == nullptr || cf_count_read(a.id_nnz) != 0ull;   // unknown: nonzero
+      id_live = a.id_nnz == nullptr || id_count != 0ull;   // unknown: nonzero
     }
     if (zcopy != CF_COPY_WRITTEN && (zvchan || a.v_out == nullptr)) {
       if (L == 0 && tid == 0) {
