@@ -199,21 +199,37 @@ __global__ __launch_bounds__(256) void nhwc_to_nchw_kernel(
 __global__ __launch_bounds__(256) void global_avgpool_nhwc_kernel(
     const _Float16* __restrict__ xp, const CfOutDesc* desc, float* __restrict__ out, int64_t HW,
     int C, int cp, float factor) {
+  // Workgroup: image n, 64 channels; thread (g, j) sums channels c, c + 1
+  // (c = 64 * blockIdx.y + 2 j) over pixels g, g + 8, ...; the eight
+  // partial sums meet in LDS.  The copy's values are small integers, so
+  // every partial sum is exact and the order of the additions does not
+  // change the result.
   typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  __shared__ float red[8][64];
   const int64_t n = blockIdx.x;
-  const int c = (int)blockIdx.y * 512 + 2 * (int)threadIdx.x;
-  if (c >= C) return;
+  const int g = (int)threadIdx.x >> 5, j = (int)threadIdx.x & 31;
+  const int c = (int)blockIdx.y * 64 + 2 * j;
   const _Float16* base = cf_copy_source(desc, xp);   // nullptr: all zero
-  const _Float16* src = base + n * HW * cp + c;
   float s0 = 0.0f, s1 = 0.0f;
-#pragma unroll 7
-  for (int64_t p = 0; p < (base != nullptr ? HW : 0); ++p) {
-    const h2 v = *reinterpret_cast<const h2*>(src + p * cp);
-    s0 += (float)v[0];
-    s1 += (float)v[1];
+  if (base != nullptr && c < C) {
+    const _Float16* src = base + n * HW * cp + c;
+#pragma unroll 4
+    for (int64_t p = g; p < HW; p += 8) {
+      const h2 v = *reinterpret_cast<const h2*>(src + p * cp);
+      s0 += (float)v[0];
+      s1 += (float)v[1];
+    }
   }
-  out[n * C + c] = s0 * factor;
-  if (c + 1 < C) out[n * C + c + 1] = s1 * factor;
+  red[g][2 * j] = s0;
+  red[g][2 * j + 1] = s1;
+  __syncthreads();
+  if (threadIdx.x < 64) {
+    const int cc = (int)blockIdx.y * 64 + (int)threadIdx.x;
+    float s = 0.0f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) s += red[k][threadIdx.x];
+    if (cc < C) out[n * C + cc] = s * factor;
+  }
 }
 
 // Token-major fp32 [NB][P][C] (a transformer's [T, B, N, C] activations)
@@ -423,7 +439,7 @@ CF_API int cf_global_avgpool_nhwc(const void* xp, const void* desc, float* out, 
     return (int)hipErrorInvalidValue;
   if (NB == 0) return 0;
   const float factor = 1.0f / (float)HW;
-  hipLaunchKernelGGL(global_avgpool_nhwc_kernel, dim3((unsigned)NB, (unsigned)((C + 511) / 512)),
+  hipLaunchKernelGGL(global_avgpool_nhwc_kernel, dim3((unsigned)NB, (unsigned)((C + 63) / 64)),
                      dim3(256), 0, (hipStream_t)stream, (const _Float16*)xp,
                      (const CfOutDesc*)desc, out, HW, (int)C, (int)cp, factor);
   return (int)hipGetLastError();

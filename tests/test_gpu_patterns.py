@@ -370,19 +370,19 @@ def test_fused_global_avgpool_nhwc_bitwise(cuda):
     bit for bit, without materialising it."""
     from catfuse_amd import runtime
     from catfuse_amd.patterns import FusedGlobalAvgPool
-    T, B, C, H, W = 4, 3, 80, 7, 9
     g = _gen(31)
-    v = ((torch.rand(T, B, C, H, W, generator=g) < 0.4).float()
-         * torch.randint(1, 4, (T, B, C, H, W), generator=g).float())
-    cp = runtime.pad32(C)
-    nhwc = torch.zeros(T * B, H, W, cp, dtype=torch.float16)
-    nhwc[..., :C] = v.reshape(T * B, C, H, W).permute(0, 2, 3, 1).half()
-    x = runtime.lazy_output((T, B, C, H, W), nhwc.to(cuda), cuda)
-    pool = FusedGlobalAvgPool("m")
-    y = pool(x)
-    assert pool.fallback_calls == 0 and x.__dict__.get("_cf_pending", False)  # not materialised
-    ref = torch.nn.functional.adaptive_avg_pool2d(v.to(cuda).flatten(0, 1), 1).view(T, B, C, 1, 1)
-    assert torch.equal(y, ref)
+    for T, B, C, H, W in ((4, 3, 80, 7, 9), (2, 2, 512, 7, 7), (1, 2, 64, 56, 56)):
+        v = ((torch.rand(T, B, C, H, W, generator=g) < 0.4).float()
+             * torch.randint(1, 4, (T, B, C, H, W), generator=g).float())
+        cp = runtime.pad32(C)
+        nhwc = torch.zeros(T * B, H, W, cp, dtype=torch.float16)
+        nhwc[..., :C] = v.reshape(T * B, C, H, W).permute(0, 2, 3, 1).half()
+        x = runtime.lazy_output((T, B, C, H, W), nhwc.to(cuda), cuda)
+        pool = FusedGlobalAvgPool("m")
+        y = pool(x)
+        assert pool.fallback_calls == 0 and x.__dict__.get("_cf_pending", False)  # not materialised
+        ref = torch.nn.functional.adaptive_avg_pool2d(v.to(cuda).flatten(0, 1), 1).view(T, B, C, 1, 1)
+        assert torch.equal(y, ref), (T, B, C, H, W)
 
 
 def test_vgg11_per_layer(cuda):
