@@ -926,3 +926,34 @@ def test_nhwc_shadow_handoff_bitwise_and_invalidated(cuda):
     sh = runtime.shadow_of(y3, (8, 8, 8, 64))
     assert sh is not None and not sh[..., 40:].any()
     assert torch.equal(sh[..., :40], y3.reshape(8, 40, 8, 8).permute(0, 2, 3, 1).half())
+
+
+def test_resolve_copy_and_expand_state_descriptors(cuda):
+    """cf_resolve_copy fills a copy its descriptor records as all zero or as
+    an alias (and leaves a written one alone); cf_expand_state broadcasts the
+    per-channel potentials when the descriptor says so (and leaves v alone
+    otherwise)."""
+    from catfuse_amd import _hip
+    L, st = _hip.lib(), _hip.stream(cuda)
+    n = 3 * 1024 + 48                       # halves: a multiple of 8 (16-byte units)
+    src = torch.arange(n, dtype=torch.float16, device=cuda) % 7
+    for state, expect in ((0, "keep"), (1, "zero"), (2, "alias")):
+        buf = torch.full((n,), 5.0, dtype=torch.float16, device=cuda)
+        desc = torch.zeros(2, dtype=torch.int64, device=cuda)
+        desc[0] = state                     # copy state (low word), vstate 0
+        desc[1] = src.data_ptr() if state == 2 else 0
+        assert L.cf_resolve_copy(buf.data_ptr(), n * 2, desc.data_ptr(), st) == 0
+        torch.cuda.synchronize()
+        ref = {"keep": torch.full_like(buf, 5.0), "zero": torch.zeros_like(buf), "alias": src}[expect]
+        assert torch.equal(buf, ref), expect
+    B, C, HW = 3, 40, 49
+    v_chan = torch.randn(C, device=cuda)
+    for vstate in (0, 1):
+        v = torch.full((B, C, HW), -3.0, device=cuda)
+        desc = torch.zeros(2, dtype=torch.int64, device=cuda)
+        desc[0] = vstate << 32
+        assert L.cf_expand_state(v.data_ptr(), v_chan.data_ptr(), desc.data_ptr(), B, C, HW,
+                                 st) == 0
+        torch.cuda.synchronize()
+        ref = v_chan.view(1, C, 1).expand(B, C, HW) if vstate else torch.full_like(v, -3.0)
+        assert torch.equal(v, ref), vstate
