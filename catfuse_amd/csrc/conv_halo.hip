@@ -149,6 +149,7 @@ struct HaloArgs {
   const float* identity;
   const _Float16* identity_nhwc;  // [T*B][Ho][Wo][cp_id] spike-valued identity, or null
   int cp_id;
+  int cin_real;             // real input channels (<= Cp): K halves beyond are zero padding
   int identity_mode;
   const int32_t* ag_mask;   // [T][B*GH*GW]
   const int32_t* order;     // [1 + B*GH*GW]: active tile count, then every tile, the
@@ -667,9 +668,21 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   // and adding the exact zero products leaves the accumulator's bits
   // unchanged (it starts at +0 and is never -0), so this equals skipping it.
   // SKIP: skip the MFMAs of a silent chunk half (hm: half_act of the step).
+  // 16-channel halves of chunk ch whose MFMAs run (bit ks): none for a
+  // wave whose 32 output channels are all padding (Cout not a multiple of
+  // 64), the lower one only where the upper 16 input channels are padding
+  // (Cin not a multiple of 32).  The skipped products are exact zeros
+  // (zero weights and zero input channels), so the accumulators' bits are
+  // those of the full evaluation.
+  const bool wave_idle = cout0 + wm * WM >= a.Cout;
+  auto ks_run = [&](int ch) -> uint32_t {
+    if (wave_idle) return 0u;
+    return ch * KC + KC / 2 < a.cin_real ? 3u : 1u;
+  };
   auto run_taps = [&](auto skip_c, const _Float16* __restrict__ hb,
                       _Float16* __restrict__ hb_next, int ch, int ntb, int nc, uint32_t nact,
                       int wblk, uint32_t hm) {
+    const uint32_t kr = ks_run(ch);
     constexpr bool SKIP = decltype(skip_c)::value;
     const int stb = ntb == wblk ? ntb : a.T;  // a.T: stage zeros
 #pragma unroll
@@ -708,6 +721,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
         // still sums ks 0 hi, ks 0 lo, ks 1 hi, ks 1 lo in that order.
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
+          if (((kr >> ks) & 1u) == 0u) continue;
           if constexpr (SKIP) {
             if (((hm >> (ks * TB + th)) & ((1u << TBR) - 1u)) == 0u) continue;
           }
@@ -1130,6 +1144,11 @@ int make_halo_args(HaloArgs& a, const void* x, const void* w_packed, const float
   a.x_desc = (const CfOutDesc*)x_desc; a.id_desc = (const CfOutDesc*)id_desc;
   a.out_desc = (CfOutDesc*)out_desc; a.bias_info = bias_info; a.id_nnz = id_nnz;
   a.sparse_thr = ag_mask ? sparse_threshold : 2.0;  // 2.0: sparsity never exceeds it
+  // the input's real channel count, numel / (T*B*H*W) when that divides and
+  // is at most Cp (else every chunk runs whole)
+  a.cin_real = (int)Cp;
+  if (numel > 0 && numel % (T * B * H * W) == 0 && numel / (T * B * H * W) <= Cp)
+    a.cin_real = (int)(numel / (T * B * H * W));
   a.T = (int)T; a.B = (int)B; a.Cp = (int)Cp; a.Cout = (int)Cout; a.Coutp = (int)Coutp;
   a.H = (int)H; a.W = (int)W; a.Ho = (int)Ho; a.Wo = (int)Wo; a.pad = (int)pad;
   a.GH = (int)((Ho + tile_h - 1) / tile_h);

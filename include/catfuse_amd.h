@@ -275,7 +275,12 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
  *   count block of the input: its published count k (exact, from
  *   cf_pack_input / cf_scan_nhwc, or the producing conv's nz_out) routes
  *   the launch: k == 0 StaticZero (no K loop), SparseFlow when ag_mask is
- *   given and 1 - k/numel > sparse_threshold, dense otherwise.  nz_out
+ *   given and 1 - k/numel > sparse_threshold, dense otherwise.  numel is the
+ *   input's element count T*B*Cin*H*W; the halo kernel takes its real
+ *   channel count Cin = numel/(T*B*H*W) (when that divides and is at most
+ *   Cp) and skips the products of zero-padded 16-channel input halves, and
+ *   of output waves whose 32 channels all lie beyond Cout (exact zeros or
+ *   discarded outputs: the results are those of the full evaluation).  nz_out
  *   (nullable) is the count block the launch publishes for its output: the
  *   number of workgroups that stored a nonzero value (0 iff the output is
  *   all zero), so the next fused conv can route on it without a counting
