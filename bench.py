@@ -526,6 +526,8 @@ def spikformer_result(args, dev):
     l_ms, l_fl, _, l_n = _agg(kern, ["linear_tokens"])
     lz_ms, _, _, lz_n = _agg(kern, ["linear_tokens_staticzero"])
     a_ms, a_fl, a_b, a_n = _agg(kern, ["spike_attention"])
+    az_ms, _, az_b, az_n = _agg(kern, ["spike_attention_staticzero"])
+    az_el = kern.get("spike_attention_staticzero", {}).get("elided", 0)
     ach = l_fl / (l_ms * 1e-3) / 1e12 if l_ms else 0.0
     a_gbps = a_b / (a_ms * 1e-3) / 1e9 if a_ms else 0.0
     result = _base_result(args, res, stats, "spikformer_8_384_T4_B32_224")
@@ -545,10 +547,16 @@ def spikformer_result(args, dev):
                              "us_per_launch_avg": round(lz_ms * 1e3 / max(1, lz_n), 2)},
         "linear_route_sequence": route_sequence(timer, "linear_tokens", steps)}
     result["attention"] = {"kernel": "spike_attention_kernel (cf_spike_attention_lif)",
-                           "launches_per_step": a_n // steps,
-                           "us_per_launch_avg": round(a_ms * 1e3 / max(1, a_n), 2),
-                           "achieved": round(a_gbps, 1), "peak": PEAK_HBM_GBPS, "unit": "GB/s",
-                           "frac": round(a_gbps / PEAK_HBM_GBPS, 4)}
+                           "launches_per_step": (a_n + az_n) // steps,
+                           "full_route": {"launches_per_step": a_n // steps,
+                                          "us_per_launch_avg": round(a_ms * 1e3 / max(1, a_n), 2),
+                                          "achieved": round(a_gbps, 1), "peak": PEAK_HBM_GBPS,
+                                          "unit": "GB/s",
+                                          "frac": round(a_gbps / PEAK_HBM_GBPS, 4)},
+                           "zero_route": {"launches_per_step": az_n // steps,
+                                          "elided_per_step": az_el // steps,
+                                          "bytes_per_step": az_b // steps,
+                                          "us_per_launch_avg": round(az_ms * 1e3 / max(1, az_n), 2)}}
     return result, model
 
 

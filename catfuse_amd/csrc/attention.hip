@@ -42,6 +42,8 @@ struct AttnArgs {
   float* v_out;
   const unsigned long long* nnz;   // count block of Q, K, V (one tensor), or null
   unsigned long long* nz_out;
+  CfOutDesc* out_desc;             // output descriptor (CfOutDesc), or null
+  int zero_info;                   // CF_BIAS_* for the LIF on z = 0 (needs out_desc)
   int T, B, N, heads;
   float scale;
   LifParams lif;
@@ -79,6 +81,26 @@ __global__ __launch_bounds__(256) void spike_attention_kernel(AttnArgs a) {
   float v[MAXT][16];
   uint32_t anyw = 0u;
   const bool zero_in = a.nnz != nullptr && cf_count_read(a.nnz) == 0ull;   // uniform
+  // An all-zero Q/K/V from the initial state drives every neuron with z = 0:
+  // when the caller knows that the LIF never fires on it and holds the
+  // final potential, the output is all zero and the state uniform, so
+  // workgroup 0 records that in the descriptor and the count, and no
+  // workgroup stores anything else.
+  if (zero_in && a.v_in == nullptr && a.out_desc != nullptr && (a.zero_info & CF_BIAS_SILENT) &&
+      ((a.zero_info & CF_BIAS_VCHAN) || a.v_out == nullptr)) {
+    if (blockIdx.x == 0 && tid == 0) {
+      if (a.nz_out != nullptr) a.nz_out[1] = 0ull;
+      a.out_desc->copy = CF_COPY_ZERO;
+      a.out_desc->vstate = (a.zero_info & CF_BIAS_VCHAN) ? 1u : 0u;
+      a.out_desc->alias = nullptr;
+    }
+    return;
+  }
+  if (a.out_desc != nullptr && blockIdx.x == 0 && tid == 0) {
+    a.out_desc->copy = CF_COPY_WRITTEN;
+    a.out_desc->vstate = 0u;
+    a.out_desc->alias = nullptr;
+  }
 
   // initial membrane potentials
 #pragma unroll
@@ -213,6 +235,7 @@ CF_API int cf_spike_attention_lif(const void* q, const void* k, const void* v, i
                                   int64_t koff, int64_t voff, int64_t pitch, void* out,
                                   int64_t cp_out, const float* v_in, float* v_out,
                                   const unsigned long long* nnz, unsigned long long* nz_out,
+                                  void* out_desc, int zero_info,
                                   int64_t T, int64_t B, int64_t N,
                                   int64_t heads, int64_t head_dim, double scale, double tau,
                                   double v_th, double v_reset, int hard_reset, int decay_input,
@@ -225,11 +248,14 @@ CF_API int cf_spike_attention_lif(const void* q, const void* k, const void* v, i
       cp_out < C || T * B * N * pitch > ((int64_t)1 << 40) || B * heads >= (int64_t)CF_MAX_COUNT_WG ||
       (int64_t)(N - 1) * pitch * 2 + 64 > INT32_MAX)
     return (int)hipErrorInvalidValue;
+  if ((zero_info & ~(CF_BIAS_SILENT | CF_BIAS_VCHAN)) != 0 || (zero_info && !out_desc))
+    return (int)hipErrorInvalidValue;
   AttnArgs a;
   a.q = (const _Float16*)q; a.k = (const _Float16*)k; a.v = (const _Float16*)v;
   a.qoff = (int)qoff; a.koff = (int)koff; a.voff = (int)voff; a.pitch = (int)pitch;
   a.out = (_Float16*)out; a.cp_out = (int)cp_out; a.v_in = v_in; a.v_out = v_out;
-  a.nnz = nnz; a.nz_out = nz_out; a.T = (int)T; a.B = (int)B; a.N = (int)N; a.heads = (int)heads;
+  a.nnz = nnz; a.nz_out = nz_out; a.T = (int)T;
+  a.out_desc = (CfOutDesc*)out_desc; a.zero_info = zero_info; a.B = (int)B; a.N = (int)N; a.heads = (int)heads;
   a.scale = (float)scale;
   a.lif = cf_make_lif_params(tau, v_th, v_reset, hard_reset, decay_input);
   const dim3 grid((unsigned)(B * heads)), block(256);

@@ -320,11 +320,13 @@ class ChannelState(_LazyTensor):
     since each replay rewrites the per-channel values."""
 
     @staticmethod
-    def __new__(cls, base: torch.Tensor, v_chan: torch.Tensor, desc: torch.Tensor):
+    def __new__(cls, base: torch.Tensor, v_chan: torch.Tensor, desc: torch.Tensor,
+                uniform: bool = False):
         t = base.as_subclass(cls)
         t._cf_pending = True
         t._cf_state = (v_chan, desc, base._version)
         t._cf_sticky = torch.cuda.is_current_stream_capturing()
+        t._cf_uniform = uniform      # one value (v_chan[0]) for every element
         return t
 
     def cf_materialize(self) -> None:
@@ -336,7 +338,10 @@ class ChannelState(_LazyTensor):
                 self._cf_pending = False
             if self._version != ver:
                 return   # changed in place after an earlier expansion
-            B, C = self.shape[0], self.shape[1]
+            if self.__dict__.get("_cf_uniform", False):
+                B, C = 1, 1
+            else:
+                B, C = self.shape[0], self.shape[1]
             check(_hip.lib().cf_expand_state(self.data_ptr(), v_chan.data_ptr(), desc.data_ptr(),
                                              B, C, self.numel() // (B * C),
                                              _hip.stream(self.device)), "cf_expand_state")
@@ -349,7 +354,7 @@ def lazy_view(t: torch.Tensor, *shape) -> torch.Tensor:
         v_chan, desc, _ = t._cf_state
         with torch._C.DisableTorchFunctionSubclass():
             base = torch.Tensor.view(t, *shape)
-        v = ChannelState(base, v_chan, desc)
+        v = ChannelState(base, v_chan, desc, uniform=t.__dict__.get("_cf_uniform", False))
         v._cf_sticky = t.__dict__.get("_cf_sticky", False)
         return v
     return t.view(*shape)
@@ -662,19 +667,58 @@ def spike_attention_lif(qkv: torch.Tensor, T: int, B: int, N: int, heads: int, o
     copy = torch.empty((T * B * N, cp), dtype=torch.float16, device=dev)
     v_out = torch.empty((B, N, C), dtype=torch.float32, device=dev) if want_v_out else None
     qoff, koff, voff = (int(o) for o in offsets)
+    lif = _lif_args(tau, v_threshold, v_reset, decay_input)
+    # on the zero route from the initial state the output may be left
+    # unwritten (all zero) and the state uniform: the LIF's response to z = 0
+    desc = v_uniform = None
+    zero_info = 0
+    if COPY_ELISION and nnz is not None and v_in is None:
+        r = zero_drive_response(dev, T, lif)
+        if r is not None and r[1]:
+            desc = new_out_desc(dev)
+            v_uniform = r[0] if v_out is not None else None
+            zero_info = 1 | (2 if v_uniform is not None else 0)
     ev = _t0()
     check(_hip.lib().cf_spike_attention_lif(
         ptr(qkv), ptr(qkv), ptr(qkv), qoff, koff, voff, pitch, ptr(copy), cp, ptr(v_in),
-        ptr(v_out), ptr(nnz), ptr(nz_out), T, B, N, heads, 32, float(scale),
-        *_lif_args(tau, v_threshold, v_reset, decay_input), _hip.stream(dev)),
-        "cf_spike_attention_lif")
+        ptr(v_out), ptr(nnz), ptr(nz_out), ptr(desc), zero_info, T, B, N, heads, 32,
+        float(scale), *lif, _hip.stream(dev)), "cf_spike_attention_lif")
     _t1("spike_attention", ev, flops=4 * T * B * heads * N * 32 * 32,
-        nbytes=2 * T * B * N * 3 * C + 2 * T * B * N * cp)
+        nbytes=2 * T * B * N * 3 * C + 2 * T * B * N * cp,
+        route=None if nnz is None else _RouteProbe(
+            nnz, [(desc, 2 * T * B * N * cp, 4 * B * N * C if v_out is not None else 0)]))
     out = lazy_tokens((T, B, N, C), copy, dev)
+    if desc is not None:
+        attach_desc(out, desc)
     if nz_out is not None and gen_cell is not None:
         gen_cell[0] += 1
         attach_count(out, nz_out, gen_cell)
+    if v_uniform is not None:
+        v_out = ChannelState(v_out, v_uniform, desc, uniform=True)
     return out, v_out
+
+
+_ZERO_DRIVE = {}
+
+
+def zero_drive_response(device, T: int, lif) -> Optional[tuple]:
+    """(v_final [1] fp32, silent) of a LIF with parameters lif (the C-ABI's
+    tau, v_th, v_reset, hard, decay_input) driven by z = 0 for T steps from
+    its initial state (cf_bias_response of a zero affine), computed once per
+    device, T and parameters; None while a graph is being captured and the
+    value is not yet known."""
+    key = (str(device), int(T), tuple(lif))
+    r = _ZERO_DRIVE.get(key)
+    if r is None:
+        if torch.cuda.is_current_stream_capturing():
+            return None
+        z = torch.zeros(1, dtype=torch.float32, device=device)
+        v = torch.empty(1, dtype=torch.float32, device=device)
+        f = torch.empty(1, dtype=torch.int32, device=device)
+        check(_hip.lib().cf_bias_response(ptr(z), ptr(z), 1, T, *lif, ptr(v), ptr(f),
+                                          _hip.stream(device)), "cf_bias_response")
+        r = _ZERO_DRIVE[key] = (v, not bool(f.item()))
+    return r
 
 
 def prescan_tiles(act: torch.Tensor, H: int, W: int, H_out: int, W_out: int, kernel_size: int,

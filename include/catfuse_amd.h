@@ -163,14 +163,20 @@ int cf_tokens_to_f32(const void* xp, float* out, int64_t rows, int64_t C, int64_
  * fp32 [B][N][heads*32] (nullable); nnz (nullable): count block of the Q, K,
  * V tensor (one concatenated tensor): a published count of zero takes the
  * zero route (no operand reads, no MFMAs, z = 0); nz_out (nullable): count
- * block of the output (workgroups with a spike).  N <= 256.  Replaces the SSA core of
+ * block of the output (workgroups with a spike).  out_desc (nullable): the
+ * output's descriptor (see cf_conv_mfma), with zero_info the caller's
+ * knowledge of the LIF on z = 0 (cf_bias_response of a zero affine: bit 0,
+ * it never fires over T; bit 1, the caller holds its final potential, the
+ * same for every neuron): on the zero route from the initial state with
+ * bit 0 the launch stores no spikes (copy recorded all zero), and with bit
+ * 1 no state either (vstate 1).  N <= 256.  Replaces the SSA core of
  * models/spikformer_github.py:139-160 (q @ k^T * scale, @ v, attn_lif) and
  * the reference's spike-matmul kernels (sparseflow/sparse_bmm_kernel.py:40-358,
  * sparse_attention_kernel.py:24-118). */
 int cf_spike_attention_lif(const void* q, const void* k, const void* v, int64_t qoff,
                            int64_t koff, int64_t voff, int64_t pitch, void* out, int64_t cp_out,
                            const float* v_in, float* v_out, const unsigned long long* nnz,
-                           unsigned long long* nz_out,
+                           unsigned long long* nz_out, void* out_desc, int zero_info,
                            int64_t T, int64_t B, int64_t N, int64_t heads, int64_t head_dim,
                            double scale, double tau, double v_th, double v_reset, int hard_reset,
                            int decay_input, void* stream);

@@ -154,12 +154,16 @@ def test_token_and_pool_entry_points_validate_arguments():
 
     def attention(N=196, heads=2, head_dim=32, pitch=192, qoff=0, cp_out=64):
         return L.cf_spike_attention_lif(1, 1, 1, qoff, 64, 128, pitch, 1, cp_out, None, None,
-                                        None, None, 4, 2, N, heads, head_dim, 0.125, *lif, None)
+                                        None, None, None, 0, 4, 2, N, heads, head_dim, 0.125,
+                                        *lif, None)
     assert attention(head_dim=64) == INVALID        # one 32-wide MFMA tile per head
     assert attention(N=300) == INVALID              # more tokens than the kernel stages
     assert attention(qoff=160) == INVALID           # Q heads beyond the pitch
     assert attention(cp_out=32) == INVALID          # output narrower than heads * 32
     assert attention(pitch=196) == INVALID          # pitch not a multiple of 8
+    assert L.cf_spike_attention_lif(1, 1, 1, 0, 64, 128, 192, 1, 64, None, None, None, None,
+                                    None, 1, 4, 2, 196, 2, 32, 0.125, *lif,
+                                    None) == INVALID    # zero-drive knowledge without a descriptor
 
     def pool(cp=64, k=3, s=2, p=1):
         return L.cf_maxpool_nhwc(1, 1, 8, 16, 16, cp, k, s, p, None, None)

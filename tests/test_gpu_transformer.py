@@ -137,6 +137,43 @@ def test_spike_attention_zero_route_bitwise(cuda):
     assert bool(ref.any()) and not bool(ref.all())
 
 
+def test_spike_attention_zero_route_elision_bitwise(cuda):
+    """From the initial state, a zero count drives every neuron with z = 0:
+    a LIF that never fires on it leaves the output unwritten (descriptor:
+    all zero, count zero) and the state uniform; the next token linear reads
+    it through the descriptor; outputs, states and counts equal the
+    always-writing path bit for bit."""
+    from catfuse_amd import runtime
+    T, B, N, heads = 4, 3, 100, 2
+    C = heads * 32
+    copy = torch.zeros((T * B * N, 3 * C), dtype=torch.float16, device=cuda)
+    w = (torch.randn(64, C, 1, 1, generator=_gen(8)) * 0.2).to(cuda)
+    proj = runtime.ConvLIFRunner(w, torch.ones(64, device=cuda),
+                                 torch.full((64,), -0.2, device=cuda), None, 1, 0, 2.0, 1.0,
+                                 0.0, True)
+
+    def run(elide):
+        runtime.COPY_ELISION = elide
+        try:
+            blk = runtime.count_block(cuda)
+            nz = runtime.count_block(cuda)
+            out, v = runtime.spike_attention_lif(copy, T, B, N, heads, (0, C, 2 * C), 0.125,
+                                                 nnz=blk, nz_out=nz, gen_cell=[0])
+            d = runtime.desc_of(out)
+            st = None if d is None else int(d[0].item())
+            y, vy = proj.run_tokens(out)
+            return (out.clone(), v.clone(), y.clone(), vy.clone(), int(nz[1].item()), st)
+        finally:
+            runtime.COPY_ELISION = True
+
+    e, w_ = run(True), run(False)
+    for a, b in zip(e[:4], w_[:4]):
+        assert torch.equal(a, b)
+    assert e[4] == w_[4] == 0
+    assert e[5] == (1 | (1 << 32)) and w_[5] is None    # all zero, state uniform
+    assert not bool(e[0].any())
+
+
 def _small_spikformer(seed=41):
     from catfuse_amd import snn
     m = snn.Spikformer(img_size=32, num_classes=10, embed_dim=64, num_heads=2, depth=2, T=4,
