@@ -133,7 +133,9 @@ struct HaloGeom {
   }
 };
 
-enum { EPI_LIF = 0, EPI_Z = 1 };
+// EPI_POOL: BN -> AvgPool2d(2, 2) -> LIF, the pooled spikes as the fp16
+// NHWC copy, the pooled membrane state (8x8 tiles of stride-1 3x3 convs).
+enum { EPI_LIF = 0, EPI_Z = 1, EPI_POOL = 2 };
 enum { ID_ADD_SPIKE = 1, ID_ADD_Z = 2 };
 
 struct HaloArgs {
@@ -832,6 +834,92 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     int epix[NT];
 #pragma unroll
     for (int nt = 0; nt < NT; ++nt) epix[nt] = n_ok[nt] ? e_off[nt] : 0;
+    // BN -> AvgPool2d(2, 2) -> LIF: a 2x2 window of the tile is lanes l,
+    // l + 1, l + 8, l + 9 of a 32-lane half (pixel column l % 8 of row
+    // l / 8); the lane of its top-left pixel sums the four BN outputs in the
+    // order of cf_avgpool2x2_lif (((z00 + z01) + z10) + z11) * 0.25 and runs
+    // the pooled neuron's LIF, whose potential it keeps across the steps.
+    // Stores go through buffer descriptors: out-of-range offsets drop.
+    if constexpr (EPI == EPI_POOL) {
+      static_assert(NBUF == 2 && TH == 8 && TW == 8, "pooled epilogue: 8x8 tiles");
+      const int Hp = a.Ho / 2, Wp = a.Wo / 2, HpWp = Hp * Wp;
+      const int l = lane & 31;
+      bool pok[NT];
+      int pofs[NT];
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt) {
+        const int p = wn * WN + nt * 32 + l;
+        const int ppy = (oh0 + p / TW) / 2, ppx = (ow0 + p % TW) / 2;
+        pok[nt] = (l & 9) == 0 && ppy < Hp && ppx < Wp;
+        pofs[nt] = pok[nt] ? ppy * Wp + ppx : 0;
+      }
+      float vp[NT][16];
+      const float* vsrc = tb0 == 0 ? a.v_in : a.v_out;
+      const __amdgpu_buffer_rsrc_t rvin =
+          halo_rsrc(vsrc ? vsrc + (size_t)b * a.Cout * HpWp : a.v_out,
+                    vsrc ? (uint32_t)(a.Cout * HpWp * 4) : 0u);
+#pragma unroll
+      for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dc = 8 * (r >> 2) + (r & 3);
+          const uint32_t off = (pok[nt] && col + dc < a.Cout)
+                                   ? (uint32_t)(((col + dc) * HpWp + pofs[nt]) * 4) : HALO_OOB;
+          vp[nt][r] = vsrc ? __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rvin, off, 0, 0))
+                           : lif_initial_v(a.lif);
+        }
+#pragma unroll
+      for (int t = 0; t < TB; ++t) {
+        if (t > 0 && t >= nsteps) break;  // (unrolled: acc stays in registers)
+        const size_t img = (size_t)(tb0 + t) * a.B + b;
+        const __amdgpu_buffer_rsrc_t ro =
+            halo_rsrc(a.out_nhwc + img * HpWp * a.cp_out, (uint32_t)(HpWp * a.cp_out * 2));
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const int colb = wm * WM + 8 * r4 + 4 * hi;
+          const float4 al4 = *reinterpret_cast<const float4*>(&bn_s[0][colb]);
+          const float4 be4 = *reinterpret_cast<const float4*>(&bn_s[1][colb]);
+          const float alv[4] = {al4.x, al4.y, al4.z, al4.w};
+          const float bev[4] = {be4.x, be4.y, be4.z, be4.w};
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt) {
+            h4 sph;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const int r = 4 * r4 + j;
+              const float z = __builtin_fmaf(acc[t][nt][r], alv[j], bev[j]);
+              const float z01 = __shfl_down(z, 1, 64);
+              const float z10 = __shfl_down(z, 8, 64);
+              const float z11 = __shfl_down(z, 9, 64);
+              const float zp = (((z + z01) + z10) + z11) * 0.25f;
+              float vv = lif_charge_m<LM>(vp[nt][r], zp, a.lif);
+              sph[j] = lif_fire_reset_bit<LM>(vv, a.lif) ? (_Float16)1.0f : (_Float16)0.0f;
+              vp[nt][r] = vv;
+            }
+            const bool ok = pok[nt] && col + 8 * r4 < a.Cout;
+            const u32x2 pw = __builtin_bit_cast(u32x2, sph);
+            anyw |= ok ? (pw[0] | pw[1]) : 0u;
+            __builtin_amdgcn_raw_buffer_store_b64(
+                pw, ro, ok ? (uint32_t)((pofs[nt] * a.cp_out + col + 8 * r4) * 2) : HALO_OOB, 0,
+                0);
+          }
+        }
+      }
+      if (a.v_out) {
+        const __amdgpu_buffer_rsrc_t rv =
+            halo_rsrc(a.v_out + (size_t)b * a.Cout * HpWp, (uint32_t)(a.Cout * HpWp * 4));
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int dc = 8 * (r >> 2) + (r & 3);
+            const uint32_t off = (pok[nt] && col + dc < a.Cout)
+                                     ? (uint32_t)(((col + dc) * HpWp + pofs[nt]) * 4) : HALO_OOB;
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(vp[nt][r]), rv, off, 0, 0);
+          }
+      }
+      continue;
+    }
     // Membrane potentials of this lane's elements live in registers during
     // the epilogue only: from v_in (or the initial value) for the first time
     // block, from v_out (written at the end of the previous block's epilogue
@@ -1049,6 +1137,27 @@ hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
   // stores drop channels >= Cout of a partly real 64-channel tile)
   const bool lean = epi == EPI_LIF && !a.out && !a.identity && a.Cout % 32 == 0;
   const bool oneb = a.T <= halo_tb<S, K>();
+  if (epi == EPI_POOL) {
+    // (the host admits it for stride-1 3x3 convs on 8x8 tiles only)
+    if constexpr (TH == 8 && TW == 8 && S == 1 && K == 3) {
+      const int lm = cf_lif_mode(a.lif);
+#define CF_HALO_POOL(LMV)                                                                         \
+  do {                                                                                            \
+    if (oneb)                                                                                     \
+      hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_POOL, LMV, false, true>), grid,      \
+                         block, 0, st, a);                                                        \
+    else                                                                                          \
+      hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_POOL, LMV, false, false>), grid,     \
+                         block, 0, st, a);                                                        \
+  } while (0)
+      if (lm == LM_HARD0_DECAY_P2) CF_HALO_POOL(LM_HARD0_DECAY_P2);
+      else if (lm == LM_HARD_DECAY_P2) CF_HALO_POOL(LM_HARD_DECAY_P2);
+      else CF_HALO_POOL(LM_GENERIC);
+#undef CF_HALO_POOL
+      return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
+  }
   if (epi == EPI_Z) {
     hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_Z, LM_GENERIC, false, false>), grid,
                        block, 0, st, a);
@@ -1111,10 +1220,19 @@ int make_halo_args(HaloArgs& a, const void* x, const void* w_packed, const float
   if (Ho != (H + 2 * pad - ksize) / stride + 1 || Wo != (W + 2 * pad - ksize) / stride + 1 || Ho <= 0 ||
       Wo <= 0)
     return (int)hipErrorInvalidValue;
-  if (epilogue != EPI_LIF && epilogue != EPI_Z) return (int)hipErrorInvalidValue;
+  if (epilogue != EPI_LIF && epilogue != EPI_Z && epilogue != EPI_POOL)
+    return (int)hipErrorInvalidValue;
   if (identity && identity_mode != ID_ADD_SPIKE && identity_mode != ID_ADD_Z)
     return (int)hipErrorInvalidValue;
   if (identity_nhwc && (identity_mode != ID_ADD_SPIKE || cp_id < Cout || cp_id % 4 != 0))
+    return (int)hipErrorInvalidValue;
+  // BN -> AvgPool2d(2, 2) -> LIF: stride-1 3x3 convs on 8x8 tiles, the
+  // pooled spikes as the fp16 NHWC copy only (pitch a multiple of 4), whole
+  // 32-channel groups, no identity, no StaticZero elision (the pooled bias
+  // response is not the layer's)
+  if (epilogue == EPI_POOL &&
+      (ksize != 3 || stride != 1 || tile_w != 8 || out || !out_nhwc || cp_out % 4 != 0 ||
+       Cout % 32 != 0 || identity || identity_nhwc || bias_info != 0 || Ho < 2 || Wo < 2))
     return (int)hipErrorInvalidValue;
   if (!((tile_h == 8 && tile_w == 8) || (tile_h == 8 && tile_w == 16 && stride == 1 && ksize == 3)))
     return (int)hipErrorInvalidValue;
@@ -1132,7 +1250,7 @@ int make_halo_args(HaloArgs& a, const void* x, const void* w_packed, const float
   // (the grid is below 2^23 workgroups, within a count block's tally)
   // The membrane state passes from one time block to the next through v_out.
   const int tb = (stride == 2 && ksize == 3) ? halo_tb<2, 3>() : halo_tb<1, 3>();
-  if (epilogue == EPI_LIF && !v_out && T > tb) return (int)hipErrorInvalidValue;
+  if (epilogue != EPI_Z && !v_out && T > tb) return (int)hipErrorInvalidValue;
   a.x = (const _Float16*)x; a.w = (const _Float16*)w_packed; a.alpha = alpha; a.beta = beta;
   a.v_in = v_in; a.v_out = v_out; a.out = out; a.identity = identity;
   a.identity_nhwc = (const _Float16*)identity_nhwc; a.cp_id = (int)cp_id;

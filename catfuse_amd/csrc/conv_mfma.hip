@@ -40,7 +40,7 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 constexpr int KC = 32;        // channels per K step
 constexpr int LDK = KC + 8;   // padded LDS row (halves)
 
-enum { EPI_LIF = 0, EPI_Z = 1 };
+enum { EPI_LIF = 0, EPI_Z = 1, EPI_POOL = 2 };
 // identity_mode: where a non-NULL identity tensor enters the epilogue.
 //   ID_ADD_SPIKE: out = identity + spike   (SEW ADD after the LIF)
 //   ID_ADD_Z    : z = BN(conv) + identity  (spiking ResNet: BN -> Add -> LIF)
@@ -476,7 +476,9 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
       Coutp % 64 != 0 || H <= 0 || W <= 0 || Ho <= 0 || Wo <= 0 || KH <= 0 || KW <= 0 ||
       stride <= 0 || pad < 0 || x_img_tstride < 0)
     return (int)hipErrorInvalidValue;
-  if (epilogue != EPI_LIF && epilogue != EPI_Z) return (int)hipErrorInvalidValue;
+  // EPI_POOL (BN -> AvgPool2d(2, 2) -> LIF) runs in the halo kernel only
+  if (epilogue != EPI_LIF && epilogue != EPI_Z && epilogue != EPI_POOL)
+    return (int)hipErrorInvalidValue;
   if (identity && identity_mode != ID_ADD_SPIKE && identity_mode != ID_ADD_Z)
     return (int)hipErrorInvalidValue;
   if (identity_nhwc && (identity_mode != ID_ADD_SPIKE || cp_id < Cout || cp_id % 4 != 0))
@@ -497,6 +499,7 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
                        x_img_tstride == B && T * B * Cout * Ho * Wo <= INT32_MAX &&
                        (!rect || (tile_h == 8 && (tile_w == 8 ||
                                                   (tile_w == 16 && stride == 1 && KH == 3))));
+  if (epilogue == EPI_POOL && !halo_ok) return (int)hipErrorInvalidValue;
   if (halo_ok) {
     const int64_t th = 8, tw = rect ? tile_w : 8;
     return cf_conv_halo(x, w_packed, alpha, beta, v_in, v_out, out, out_nhwc, cp_out, identity,

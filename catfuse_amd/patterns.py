@@ -27,7 +27,7 @@ import torch.nn as nn
 from catfuse_amd import runtime
 from catfuse_amd.hardware import runtime_profile
 from catfuse_amd.implementations import ConvLIFParams, ConvLIFSpec, DenseKeep, StreamFuse
-from catfuse_amd.runtime import (EPI_Z, ID_ADD_SPIKE, ID_ADD_Z, ConvLIFRunner,
+from catfuse_amd.runtime import (EPI_POOL, EPI_Z, ID_ADD_SPIKE, ID_ADD_Z, ConvLIFRunner,
                                  GroupedConvLIFRunner, avgpool2x2_lif, desc_of,
                                  global_avgpool_nhwc, lif_multistep, pad32, shadow_of)
 from catfuse_amd.state import StateBuffer
@@ -335,10 +335,22 @@ class PartialFusionConvBNAddLIF(PartialFusionConvBNLIF):
 
 
 class PartialFusionConvBNAvgPoolLIF(PartialFusionConvBNLIF):
-    """Conv -> BN -> AvgPool2d(2, 2) -> LIF: the conv writes z (MFMA, BN in
-    the epilogue), the pooled LIF runs in one streaming kernel."""
+    """Conv -> BN -> AvgPool2d(2, 2) -> LIF.  A spike input to a stride-1
+    3x3 conv with whole 32-channel groups runs the whole chain in the conv
+    kernel (cf_conv_mfma's pooled epilogue: BN, the 2x2 average of the z
+    tile in registers, the pooled LIF; only the pooled spikes and state are
+    written).  Otherwise the conv writes z (BN in its epilogue) and the
+    pooled LIF runs in one streaming kernel; both give the same bits (the
+    reference's F8, catfuse/kernels/conv_pool_lif.py:94-178: the 2x2 average
+    (z00 + z01 + z10 + z11) * 0.25 in that order, line 162, then the LIF
+    with v in registers across the steps)."""
 
     policy_row = "ConvBNAvgPoolLIF"
+
+    def _pool_in_epilogue(self, H, W) -> bool:
+        k, p = self.kernel_size, self.padding
+        return (k == 3 and self.stride == 1 and self.out_channels % 32 == 0
+                and H + 2 * p - k + 1 >= 2 and W + 2 * p - k + 1 >= 2)
 
     def forward(self, x):
         squeeze = x.ndim == 4
@@ -347,6 +359,13 @@ class PartialFusionConvBNAvgPoolLIF(PartialFusionConvBNLIF):
         params = self._ensure_params()
         impl = self._impl
         r = impl.runner(self.spec, params, x.device)
+        T, B, _, H, W = x.shape
+        if not impl.input_is_analog(x) and self._pool_in_epilogue(H, W):
+            Ho, Wo = r.out_hw(H, W)
+            v_in = self.state.peek((B, self.out_channels, Ho // 2, Wo // 2), x.device)
+            s, v = r.run_mfma(x.contiguous(), v_in, epilogue=EPI_POOL, static_zero=True)
+            self.state.set(v)
+            return s.squeeze(0) if squeeze else s
         if impl.input_is_analog(x):
             z, _ = r.run_direct(x, epilogue=EPI_Z)
         else:

@@ -18,7 +18,7 @@ import torch
 from catfuse_amd import _hip
 from catfuse_amd._hip import check, ptr, require_gpu_tensor
 
-EPI_LIF, EPI_Z = 0, 1
+EPI_LIF, EPI_Z, EPI_POOL = 0, 1, 2
 ID_ADD_SPIKE, ID_ADD_Z = 1, 2
 ROUTE_ZERO, ROUTE_SPARSE, ROUTE_DENSE = 0, 1, 2
 STATUS_INEXACT_FP16 = 1
@@ -923,7 +923,11 @@ class ConvLIFRunner:
         count, a dense one takes the dense route; with emit_nhwc the output
         carries its own copy for the next layer, and the count block of its
         output (attach_count): a dense layer whose input carries one takes
-        the StaticZero route on an all-zero input.  Returns (out, v_out)."""
+        the StaticZero route on an all-zero input.  epilogue=EPI_POOL (a
+        stride-1 3x3 conv): BN -> AvgPool2d(2, 2) -> LIF in the conv's
+        epilogue; out is then the pooled spikes [T, B, Cout, Ho//2, Wo//2]
+        (written as the fp16 NHWC copy) and v_out the pooled membrane state.
+        Returns (out, v_out)."""
         require_gpu_tensor(x, "x")
         T, B, C, H, W = x.shape
         if C != self.Cin:
@@ -931,6 +935,14 @@ class ConvLIFRunner:
         dev = x.device
         self._ensure_packed(dev)
         Ho, Wo = self.out_hw(H, W)
+        if epilogue == EPI_POOL:
+            if (self.KH, self.KW, self.stride) != (3, 3, 1) or self.Cout % 32 or Ho < 2 or Wo < 2:
+                raise ValueError("the pooled epilogue needs a stride-1 3x3 conv, Cout a "
+                                 "multiple of 32 and an output of at least 2x2")
+            if identity is not None or not emit_nhwc:
+                raise ValueError("the pooled epilogue writes the fp16 copy only, no identity")
+            if sparse is not None and (sparse["block_h"], sparse["block_w"]) != (8, 8):
+                raise ValueError("the pooled epilogue runs on 8x8 tiles")
         gs = sparse["group_size"] if sparse is not None else 0
         # the dense route reads the copy through its descriptor; SparseFlow
         # scans it, so an unwritten copy is filled first
@@ -1003,7 +1015,8 @@ class ConvLIFRunner:
             xp, T, B, H, W, Ho, Wo, x.numel(), nnz, ag, order, th, tw, gs, v_in, epilogue,
             want_v_out,
             None if id_nhwc is not None else identity, id_nhwc, identity_mode, sparse_threshold,
-            emit_nhwc, lambda nhwc: lazy_output((T, B, self.Cout, Ho, Wo), nhwc, dev),
+            emit_nhwc,
+            lambda nhwc: lazy_output((T, B, self.Cout) + tuple(nhwc.shape[1:3]), nhwc, dev),
             "conv_mfma" + ("_sparse" if sparse is not None else ""),
             x_desc=x_desc, id_desc=id_desc, id_nnz=id_nnz, id_keep=id_keep)
         self.last_tiles = None if ag is None else (tc_buf, ag)
@@ -1022,17 +1035,19 @@ class ConvLIFRunner:
         may alias) and, with no initial state, a per-channel state buffer
         (v_out is then a ChannelState).  Returns (out, v_out)."""
         dev = xp.device
+        # the pooled epilogue's output and state are at the pooled size
+        Hs, Ws = (Ho // 2, Wo // 2) if epilogue == EPI_POOL else (Ho, Wo)
         if v_in is not None:
             require_gpu_tensor(v_in, "v_in")
-            if v_in.numel() != B * self.Cout * Ho * Wo:
+            if v_in.numel() != B * self.Cout * Hs * Ws:
                 raise ValueError("v_in has the wrong size")
         # the halo kernel carries the membrane state between its time blocks
         # (2 or 4 steps) through v_out, so it gets one whenever T > 2
-        v_out = (torch.empty((B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
-                 if (epilogue == EPI_LIF and (want_v_out or T > 2)) else None)
+        v_out = (torch.empty((B, self.Cout, Hs, Ws), dtype=torch.float32, device=dev)
+                 if (epilogue != EPI_Z and (want_v_out or T > 2)) else None)
         cp_out = pad32(self.Cout)
-        nhwc = (torch.empty((T * B, Ho, Wo, cp_out), dtype=torch.float16, device=dev)
-                if (emit_nhwc and epilogue == EPI_LIF) else None)
+        nhwc = (torch.empty((T * B, Hs, Ws, cp_out), dtype=torch.float16, device=dev)
+                if (emit_nhwc and epilogue != EPI_Z) else None)
         nz_out = None
         if nhwc is not None:
             # spikes: written as the NHWC copy only; fp32 on first outside read
@@ -1063,9 +1078,9 @@ class ConvLIFRunner:
             self.KW, self.stride, self.padding, B, th, tw, gs, int(epilogue), *self.lif,
             _hip.stream(dev))
         check(rc, "cf_conv_mfma")
-        copy_bytes = (2 * T * B * Ho * Wo * cp_out if nhwc is not None else 0) \
+        copy_bytes = (2 * T * B * Hs * Ws * cp_out if nhwc is not None else 0) \
             + (4 * T * B * Ho * Wo * self.Cout if out_ptr is not None else 0)
-        state_bytes = 4 * B * Ho * Wo * self.Cout if v_out is not None else 0
+        state_bytes = 4 * B * Hs * Ws * self.Cout if v_out is not None else 0
         _t1(timer_name, ev, flops=2 * T * B * Ho * Wo * self.Cout * self.Cin * self.KH * self.KW,
             route=None if nnz is None else _RouteProbe(nnz, [(desc, copy_bytes, state_bytes)]))
         self.last_nnz = nnz  # count block of this input (None: not counted)

@@ -90,6 +90,25 @@ def test_host_side_argument_validation():
                               None, x_desc, None, out_desc, info, None,
                               0, 0.7, 4, 2, 64, 64, 64, 8, 8, 8, 8, 3, 3, 1, 1, 2, 0, 0, 0,
                               0, 2.0, 1.0, 0.0, 1, 1, None) == INVALID
+    # pooled epilogue (2): stride-1 3x3 convs on 8x8 tiles writing the fp16
+    # copy only, whole 32-channel groups, no identity, no bias knowledge
+    def pooled(out=None, identity=None, out_desc=None, info=0, Cout=64, cp_out=64, H=8, Ho=8,
+               k=3, stride=1, pad=1, tiles=(0, 0, 0), ag=None, T=4, v_out=1, epi=2):
+        return L.cf_conv_mfma(1, 1, 1, 1, None, v_out, out, 1, cp_out, identity, None, 64,
+                              1, ag, None, None, None, None, None, out_desc, info, None, 0, 0.7,
+                              T, 2, 64, Cout, 64, H, H, Ho, Ho, k, k, stride, pad, 2, *tiles,
+                              epi, 2.0, 1.0, 0.0, 1, 1, None)
+    assert pooled(out=1) == INVALID                          # fp32 output
+    assert pooled(identity=1) == INVALID                     # identity
+    assert pooled(out_desc=1, info=1) == INVALID             # StaticZero elision
+    assert pooled(Cout=48, cp_out=48) == INVALID             # partial 32-channel group
+    assert pooled(Cout=32, cp_out=34) == INVALID             # copy pitch not a multiple of 4
+    assert pooled(H=16, stride=2) == INVALID                 # stride 2
+    assert pooled(k=1, pad=0) == INVALID                     # 1x1 kernel
+    assert pooled(tiles=(8, 16, 16), ag=1) == INVALID        # 8x16 tiles
+    assert pooled(H=1, Ho=1) == INVALID                      # no whole 2x2 window
+    assert pooled(T=9, v_out=None) == INVALID                # state across time blocks
+    assert pooled(epi=3) == INVALID                          # unknown epilogue
     assert L.cf_bias_response(1, 1, 0, 4, 2.0, 1.0, 0.0, 1, 1, 1, 1, None) == INVALID
     assert L.cf_bias_response(1, None, 8, 4, 2.0, 1.0, 0.0, 1, 1, 1, 1, None) == INVALID
     assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, 1, 64, None, None, 0, 0, None, None, None, None,

@@ -246,6 +246,66 @@ def test_conv_bn_lif_mfma_parity(cuda, case):
                                atol=2e-5)
 
 
+POOL_EPI_CASES = [
+    # name, T, B, Cin, Cout, H, W, padding, LIF variant, rate, v_in, SparseFlow
+    ("vgg", 4, 2, 64, 128, 16, 16, 1, 0, 0.2, False, False),
+    ("odd", 3, 2, 40, 96, 15, 13, 1, 0, 0.4, True, False),
+    ("t9", 9, 1, 32, 64, 12, 12, 1, 2, 0.3, True, False),
+    ("t6_generic", 6, 2, 64, 64, 10, 18, 1, 3, 0.3, False, False),
+    ("pad0", 2, 3, 64, 32, 6, 7, 0, 5, 0.5, True, False),
+    ("sparse", 4, 2, 64, 64, 16, 16, 1, 1, 0.05, False, True),
+]
+
+
+@pytest.mark.parametrize("case", POOL_EPI_CASES, ids=[c[0] for c in POOL_EPI_CASES])
+def test_conv_bn_avgpool_lif_epilogue_bitwise(cuda, case):
+    """The pooled epilogue (BN -> AvgPool2d(2, 2) -> LIF inside the conv)
+    equals the conv's z (EPI_Z) followed by cf_avgpool2x2_lif bit for bit:
+    same accumulation, the same four-term sum, the same LIF.  Covers odd
+    sizes (the floor of AvgPool2d, partial tiles), Cout not a multiple of 64,
+    time blocks carried through v_out (T > 4), an initial state, generic LIF
+    forms and the SparseFlow route."""
+    from catfuse_amd import runtime, snn
+    name, T, B, Cin, Cout, H, W, p, variant, rate, with_v, sparse = case
+    lif = snn.LIFNode(**LIF_VARIANTS[variant])
+    conv, bn, lif = _layer(Cin, Cout, 3, 1, p, seed=len(name) * 31 + T, lif=lif)
+    r = _runner(conv, bn, lif, cuda)
+    g = _gen(T * 7 + Cout)
+    x = (torch.rand(T, B, Cin, H, W, generator=g) < rate).float()
+    Ho, Wo = H + 2 * p - 2, W + 2 * p - 2
+    v0 = (torch.randn(B, Cout, Ho // 2, Wo // 2, generator=g) * 0.4).to(cuda) if with_v else None
+    sp = dict(block_h=8, block_w=8, group_size=16) if sparse else None
+    s, v = r.run_mfma(x.to(cuda), v0, epilogue=runtime.EPI_POOL, sparse=sp)
+    z, _ = r.run_mfma(x.to(cuda), epilogue=runtime.EPI_Z, sparse=sp)
+    s_ref, v_ref = runtime.avgpool2x2_lif(z, v0, **LIF_VARIANTS[variant])
+    torch.cuda.synchronize()
+    # the output count block: zero iff every pooled spike is zero
+    nz = runtime.count_of(s)
+    assert nz is not None and (int(nz[1].item()) != 0) == bool(s_ref.any()), name
+    assert s.shape == (T, B, Cout, Ho // 2, Wo // 2) and v.shape == (B, Cout, Ho // 2, Wo // 2)
+    assert torch.equal(s.cpu(), s_ref.cpu()), name
+    assert torch.equal(v.cpu(), v_ref.cpu()), name
+    # the pooled spikes feed the next fused conv through their fp16 copy
+    conv2, bn2, lif2 = _layer(Cout, 32, 3, 1, 1, seed=5)
+    r2 = _runner(conv2, bn2, lif2, cuda)
+    s2, _ = r2.run_mfma(s)
+    s2_ref, _ = r2.run_mfma(s_ref.clone())
+    assert torch.equal(s2.cpu(), s2_ref.cpu()), name
+
+
+def test_pooled_epilogue_all_zero_input(cuda):
+    """An all-zero input (StaticZero route, no K loop): z is the BN bias at
+    every pixel, the pooled LIF as the two-kernel path computes it."""
+    from catfuse_amd import runtime
+    conv, bn, lif = _layer(64, 64, 3, 1, 1, seed=77)
+    r = _runner(conv, bn, lif, cuda)
+    x = torch.zeros(4, 2, 64, 8, 8, device=cuda)
+    s, v = r.run_mfma(x, epilogue=runtime.EPI_POOL)
+    z, _ = r.run_mfma(x, epilogue=runtime.EPI_Z)
+    s_ref, v_ref = runtime.avgpool2x2_lif(z, None)
+    assert torch.equal(s.cpu(), s_ref.cpu()) and torch.equal(v.cpu(), v_ref.cpu())
+
+
 OUTPUT_COUNT_CASES = [
     # name, Cin, Cmid, Cout, k1, k2, s2, p2, H, producer SparseFlow tile width
     ("halo", 64, 64, 64, 3, 3, 1, 1, 16, 0),
