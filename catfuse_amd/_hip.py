@@ -65,6 +65,8 @@ _SIGNATURES = {
                                  c_int, c_int, _P],
     "cf_conv_direct_lif_maxpool": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I,
                                    _I, _I, c_double, c_double, c_double, c_int, c_int, _P],
+    "cf_conv_direct_avgpool_lif": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I,
+                                   _I, _I, c_double, c_double, c_double, c_int, c_int, _P],
     "cf_conv_sparse_noalloc": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, c_int, _P,
                                c_double, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                                _I, _I, c_int, c_double, c_double, c_double, c_int, c_int, _P],

@@ -276,6 +276,180 @@ __global__ __launch_bounds__(256) void conv_direct_pool_kernel(DirectPoolArgs a)
   }
 }
 
+// ---------------------------------------------------------------------------
+// Conv(3 x 3, stride 1) -> BN -> AvgPool2d(2, 2) -> LIF in one launch, for
+// an analog input (the first layer of a spiking VGG, whose conv is followed
+// by a pool): the conv output is never written, the pooled spikes go out as
+// the fp16 NHWC copy the next fused conv reads.
+//
+// Workgroup: one DA_P x DA_P tile of pooled pixels of one image and COB
+// output channels, one pooled pixel a thread.  A thread computes the four
+// conv outputs of its window with the fp32 fused multiply-add chain of
+// conv_direct_kernel (taps in the order ci, kh, kw; then alpha, beta), sums
+// them as ((z00 + z01) + z10) + z11 and scales by 0.25, the order of
+// cf_avgpool2x2_lif, and runs the pooled neuron's LIF: the spikes equal
+// cf_conv_direct (EPI_Z) followed by cf_avgpool2x2_lif bit for bit.  With a
+// stride-0 time axis (direct encoding) the pooled input is computed once and
+// feeds every step.  Input tile and filter slice sit in LDS (the filter
+// transposed, [Cin*9][Cout]: one broadcast read per tap and four channels).
+constexpr int DA_P = 16;                  // pooled tile
+constexpr int DA_X = 2 * DA_P + 2;        // staged input rows / columns (34)
+
+struct DirectAvgArgs {
+  const float* x;      // [img][Cin][H][W], img = t*x_img_tstride + b
+  const float* wt;     // [Cin*9][Cout]
+  const float* alpha;
+  const float* beta;
+  const float* v_in;   // [B][Cout][Hp][Wp] or null
+  float* v_out;        // [B][Cout][Hp][Wp] or null
+  _Float16* out_nhwc;  // [T*B][Hp][Wp][cp_out]
+  unsigned long long* nz_out;
+  int cp_out;
+  int T, B, Cin, Cout, H, W, pad, Hp, Wp, tiles_w, x_img_tstride;
+  LifParams lif;
+};
+
+template <int COB, int LM>
+__global__ __launch_bounds__(256) void conv_direct_avgpool_kernel(DirectAvgArgs a) {
+  static_assert(COB % 8 == 0, "whole 16-byte chunks of spikes");
+  __shared__ float xs[DP_MAXCIN][DA_X][DA_X];
+  __shared__ __attribute__((aligned(16))) float wsm[DP_MAXCIN * 9][COB];   // [tap][channel]
+  __shared__ unsigned any_sh[4];
+  const int tid = threadIdx.x;
+  const int b = blockIdx.y, co0 = blockIdx.z * COB;
+  const int ph0 = (blockIdx.x / a.tiles_w) * DA_P, pw0 = (blockIdx.x % a.tiles_w) * DA_P;
+  const int py = tid / DA_P, px = tid % DA_P;
+  const int gy = ph0 + py, gx = pw0 + px;
+  const bool valid = gy < a.Hp && gx < a.Wp;
+  const bool dedupe = a.x_img_tstride == 0;
+  const size_t HpWp = (size_t)a.Hp * a.Wp;
+  // pooled membrane of this thread, channel j at vbase + j * HpWp
+  const size_t vbase = ((size_t)b * a.Cout + co0) * HpWp + (valid ? (size_t)gy * a.Wp + gx : 0);
+  float zp[COB], v[COB];
+  if (a.v_in && valid) {
+    const float* vin = a.v_in + vbase;
+#pragma unroll
+    for (int j = 0; j < COB; ++j) v[j] = vin[(size_t)j * HpWp];
+  } else {
+#pragma unroll
+    for (int j = 0; j < COB; ++j) v[j] = lif_initial_v(a.lif);
+  }
+  // the copy's padding channels (Cout .. cp_out - 1) are written by the
+  // workgroups of the last channel block
+  const int nch = (co0 + COB == a.Cout ? a.cp_out - co0 : COB) / 8;
+  uint32_t anyw = 0u;
+  // this workgroup's filter slice (published by the staging barrier below)
+  for (int u = tid; u < a.Cin * 9 * COB; u += 256)
+    wsm[u / COB][u % COB] = a.wt[(size_t)(u / COB) * a.Cout + co0 + u % COB];
+  const int r0 = 2 * ph0 - a.pad, c0 = 2 * pw0 - a.pad;   // input pixel at staged (0, 0)
+  for (int t = 0; t < a.T; ++t) {
+    if (t == 0 || !dedupe) {
+      const int img = t * a.x_img_tstride + b;
+      if (t > 0) __syncthreads();   // the previous step's reads of xs are complete
+      const float* xb = a.x + (size_t)img * a.Cin * a.H * a.W;
+      // every load of the tile in flight at once, then the LDS writes
+      constexpr int NU = (DP_MAXCIN * DA_X * DA_X + 255) / 256;
+      const int nst = a.Cin * DA_X * DA_X;
+      float xv[NU];
+#pragma unroll
+      for (int i = 0; i < NU; ++i) {
+        const int u = tid + 256 * i;
+        const int ci = u / (DA_X * DA_X), rr = (u / DA_X) % DA_X, c = u % DA_X;
+        const int ih = r0 + rr, iw = c0 + c;
+        xv[i] = (u < nst && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W)
+                    ? xb[((size_t)ci * a.H + ih) * a.W + iw] : 0.0f;
+      }
+#pragma unroll
+      for (int i = 0; i < NU; ++i) {
+        const int u = tid + 256 * i;
+        if (u < nst) (&xs[0][0][0])[u] = xv[i];
+      }
+      __syncthreads();
+      // the four conv outputs of the window together: the 4 x 4 input patch
+      // of each channel in registers, each tap's COB weights read once (LDS
+      // broadcasts) for all four; every output keeps its own chain
+      // (ci, kh, kw)
+      float acc[4][COB];
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int j = 0; j < COB; ++j) acc[q][j] = 0.0f;
+      for (int ci = 0; ci < a.Cin; ++ci) {
+        float pt[4][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+          for (int c = 0; c < 4; ++c) pt[r][c] = xs[ci][2 * py + r][2 * px + c];
+#pragma unroll
+        for (int kh = 0; kh < 3; ++kh) {
+#pragma unroll
+          for (int kw = 0; kw < 3; ++kw) {
+            const float4* wk = reinterpret_cast<const float4*>(wsm[(ci * 3 + kh) * 3 + kw]);
+            float wv[COB];
+#pragma unroll
+            for (int j = 0; j < COB; j += 4) {
+              const float4 w4 = wk[j / 4];
+              wv[j] = w4.x;
+              wv[j + 1] = w4.y;
+              wv[j + 2] = w4.z;
+              wv[j + 3] = w4.w;
+            }
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+              const float xv = pt[(q >> 1) + kh][(q & 1) + kw];
+#pragma unroll
+              for (int j = 0; j < COB; ++j) acc[q][j] = fmaf(xv, wv[j], acc[q][j]);
+            }
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < COB; ++j) {
+        const float al = a.alpha[co0 + j], be = a.beta[co0 + j];
+        zp[j] = fmaf(acc[0][j], al, be);
+#pragma unroll
+        for (int q = 1; q < 4; ++q) zp[j] = zp[j] + fmaf(acc[q][j], al, be);
+      }
+#pragma unroll
+      for (int j = 0; j < COB; ++j) zp[j] = zp[j] * 0.25f;
+    }
+    uint32_t o[COB / 2];
+#pragma unroll
+    for (int j = 0; j < COB; ++j) {
+      float vv = lif_charge_m<LM>(v[j], zp[j], a.lif);
+      const bool f = lif_fire_reset_bit<LM>(vv, a.lif);
+      v[j] = vv;
+      const uint32_t h = f ? 0x3c00u : 0u;   // fp16 1.0
+      if (j & 1) o[j / 2] |= h << 16;
+      else o[j / 2] = h;
+      anyw |= valid ? h : 0u;
+    }
+    if (valid) {
+      _Float16* dst = a.out_nhwc + ((((size_t)t * a.B + b) * a.Hp + gy) * a.Wp + gx) * a.cp_out + co0;
+      for (int ch = 0; ch < nch; ++ch) {
+        uint4 w4 = make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+        for (int k = 0; k < COB / 8; ++k)
+          if (ch == k) w4 = make_uint4(o[4 * k], o[4 * k + 1], o[4 * k + 2], o[4 * k + 3]);
+        *reinterpret_cast<uint4*>(dst + ch * 8) = w4;
+      }
+    }
+  }
+  if (a.v_out && valid) {
+    float* vout = a.v_out + vbase;
+#pragma unroll
+    for (int j = 0; j < COB; ++j) vout[(size_t)j * HpWp] = v[j];
+  }
+  if (a.nz_out) {
+    const bool any = cf_wg_any(anyw != 0u, any_sh);
+    if (tid == 0) {
+      const unsigned nwg = gridDim.x * gridDim.y * gridDim.z;
+      const unsigned wg = (blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+      cf_count_publish(a.nz_out, any ? 1ull : 0ull, wg, nwg);
+    }
+  }
+}
+
 template <int LM>
 hipError_t launch_direct_pool(const DirectPoolArgs& a, int cob, dim3 grid, hipStream_t st) {
   switch (cob) {
@@ -365,4 +539,50 @@ CF_API int cf_conv_direct_lif_maxpool(const float* x, const float* wt, const flo
   if (lm == LM_HARD0_DECAY_P2) return (int)launch_direct_pool<LM_HARD0_DECAY_P2>(a, cob, grid, st);
   if (lm == LM_HARD_DECAY_P2) return (int)launch_direct_pool<LM_HARD_DECAY_P2>(a, cob, grid, st);
   return (int)launch_direct_pool<LM_GENERIC>(a, cob, grid, st);
+}
+
+// Conv(3 x 3, stride 1, Cin <= 4) -> BN -> AvgPool2d(2, 2) -> LIF of an
+// analog input; writes the pooled fp16 NHWC copy (channels Cout .. cp_out - 1
+// zero) and the pooled membrane, and publishes the output's count block.
+CF_API int cf_conv_direct_avgpool_lif(const float* x, const float* wt, const float* alpha,
+                                      const float* beta, const float* v_in, float* v_out,
+                                      void* out_nhwc, int64_t cp_out,
+                                      unsigned long long* nz_out, int64_t T, int64_t B,
+                                      int64_t Cin, int64_t Cout, int64_t H, int64_t W,
+                                      int64_t pad, int64_t x_img_tstride, double tau,
+                                      double v_th, double v_reset, int hard_reset,
+                                      int decay_input, void* stream) {
+  if (!x || !wt || !alpha || !beta || !out_nhwc || T <= 0 || B <= 0 || B > 65535 || Cin <= 0 ||
+      Cin > DP_MAXCIN || Cout <= 0 || Cout % 16 != 0 || H <= 0 || W <= 0 || pad < 0 ||
+      pad > 2 || x_img_tstride < 0 || cp_out < Cout || cp_out % 8 != 0)
+    return (int)hipErrorInvalidValue;
+  const int64_t Ho = H + 2 * pad - 2, Wo = W + 2 * pad - 2;
+  const int64_t Hp = Ho / 2, Wp = Wo / 2;
+  if (Hp <= 0 || Wp <= 0) return (int)hipErrorInvalidValue;
+  const int64_t tiles_h = (Hp + DA_P - 1) / DA_P, tiles_w = (Wp + DA_P - 1) / DA_P;
+  // eight channels a workgroup: two waves a SIMD on a 32 x 32 image batch
+  constexpr int cob = 8;
+  if (tiles_h * tiles_w > 0x7fffffff) return (int)hipErrorInvalidValue;
+  const int64_t nwg = tiles_h * tiles_w * B * (Cout / cob);
+  if (nz_out && nwg >= (int64_t)CF_MAX_COUNT_WG) return (int)hipErrorInvalidValue;
+  // 32-bit spatial indices; the copy's element offsets are 64-bit
+  if (T * B * Cout * Hp * Wp > ((int64_t)1 << 40) || (int64_t)Cin * H * W > INT32_MAX)
+    return (int)hipErrorInvalidValue;
+  DirectAvgArgs a;
+  a.x = x; a.wt = wt; a.alpha = alpha; a.beta = beta; a.v_in = v_in; a.v_out = v_out;
+  a.out_nhwc = (_Float16*)out_nhwc; a.nz_out = nz_out; a.cp_out = (int)cp_out;
+  a.T = (int)T; a.B = (int)B; a.Cin = (int)Cin; a.Cout = (int)Cout; a.H = (int)H; a.W = (int)W;
+  a.pad = (int)pad; a.Hp = (int)Hp; a.Wp = (int)Wp;
+  a.tiles_w = (int)tiles_w; a.x_img_tstride = (int)x_img_tstride;
+  a.lif = cf_make_lif_params(tau, v_th, v_reset, hard_reset, decay_input);
+  const dim3 grid((unsigned)(tiles_h * tiles_w), (unsigned)B, (unsigned)(Cout / cob));
+  const int lm = cf_lif_mode(a.lif);
+  hipStream_t st = (hipStream_t)stream;
+  if (lm == LM_HARD0_DECAY_P2)
+    hipLaunchKernelGGL((conv_direct_avgpool_kernel<cob, LM_HARD0_DECAY_P2>), grid, dim3(256), 0, st, a);
+  else if (lm == LM_HARD_DECAY_P2)
+    hipLaunchKernelGGL((conv_direct_avgpool_kernel<cob, LM_HARD_DECAY_P2>), grid, dim3(256), 0, st, a);
+  else
+    hipLaunchKernelGGL((conv_direct_avgpool_kernel<cob, LM_GENERIC>), grid, dim3(256), 0, st, a);
+  return (int)hipGetLastError();
 }

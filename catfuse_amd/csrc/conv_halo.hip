@@ -1213,7 +1213,7 @@ int make_halo_args(HaloArgs& a, const void* x, const void* w_packed, const float
   if (!x || !w_packed || !alpha || !beta || (!out && !out_nhwc)) return (int)hipErrorInvalidValue;
   if (ksize != 1 && ksize != 3) return (int)hipErrorInvalidValue;
   if (out_nhwc && (cp_out < Cout || cp_out > Coutp)) return (int)hipErrorInvalidValue;
-  if (T <= 0 || B <= 0 || Cp <= 0 || Cp % KC != 0 || Cp / KC > 64 || Cout <= 0 ||
+  if (T <= 0 || B <= 0 || Cp <= 0 || Cp % KC != 0 || Cout <= 0 ||
       Coutp < Cout || Coutp % 64 != 0 || H <= 0 || W <= 0 || pad < 0 || pad > 2)
     return (int)hipErrorInvalidValue;
   if (stride != 1 && stride != 2) return (int)hipErrorInvalidValue;

@@ -495,7 +495,7 @@ CF_API int cf_conv_mfma(const void* x, const void* w_packed, const float* alpha,
   // implementation of a layer accumulates in the same order.  The choice
   // depends on the layer shape only.
   const bool k_ok = (KH == 3 && KW == 3) || (KH == 1 && KW == 1 && Ho >= 4 && Wo >= 4);
-  const bool halo_ok = k_ok && (stride == 1 || stride == 2) && pad <= 2 && Cp / KC <= 64 &&
+  const bool halo_ok = k_ok && (stride == 1 || stride == 2) && pad <= 2 &&
                        x_img_tstride == B && T * B * Cout * Ho * Wo <= INT32_MAX &&
                        (!rect || (tile_h == 8 && (tile_w == 8 ||
                                                   (tile_w == 16 && stride == 1 && KH == 3))));

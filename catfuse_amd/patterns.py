@@ -339,8 +339,10 @@ class PartialFusionConvBNAvgPoolLIF(PartialFusionConvBNLIF):
     3x3 conv with whole 32-channel groups runs the whole chain in the conv
     kernel (cf_conv_mfma's pooled epilogue: BN, the 2x2 average of the z
     tile in registers, the pooled LIF; only the pooled spikes and state are
-    written).  Otherwise the conv writes z (BN in its epilogue) and the
-    pooled LIF runs in one streaming kernel; both give the same bits (the
+    written), and so does an analog input of at most 4 channels
+    (cf_conv_direct_avgpool_lif, fp32 VALU: VGG's first layer).  Otherwise
+    the conv writes z (BN in its epilogue) and the pooled LIF runs in one
+    streaming kernel; every path gives the same bits (the
     reference's F8, catfuse/kernels/conv_pool_lif.py:94-178: the 2x2 average
     (z00 + z01 + z10 + z11) * 0.25 in that order, line 162, then the LIF
     with v in registers across the steps)."""
@@ -360,13 +362,18 @@ class PartialFusionConvBNAvgPoolLIF(PartialFusionConvBNLIF):
         impl = self._impl
         r = impl.runner(self.spec, params, x.device)
         T, B, _, H, W = x.shape
-        if not impl.input_is_analog(x) and self._pool_in_epilogue(H, W):
+        analog = impl.input_is_analog(x)
+        if (self._pool_in_epilogue(H, W) if not analog else r.direct_avgpool_supported(x)):
             Ho, Wo = r.out_hw(H, W)
             v_in = self.state.peek((B, self.out_channels, Ho // 2, Wo // 2), x.device)
-            s, v = r.run_mfma(x.contiguous(), v_in, epilogue=EPI_POOL, static_zero=True)
+            if analog:
+                s, v = r.run_direct_avgpool(x, v_in, nz_out=r.out_counter(x.device),
+                                            gen_cell=r._gen)
+            else:
+                s, v = r.run_mfma(x.contiguous(), v_in, epilogue=EPI_POOL, static_zero=True)
             self.state.set(v)
             return s.squeeze(0) if squeeze else s
-        if impl.input_is_analog(x):
+        if analog:
             z, _ = r.run_direct(x, epilogue=EPI_Z)
         else:
             z, _ = r.run_mfma(x.contiguous(), epilogue=EPI_Z, static_zero=True)
@@ -552,9 +559,15 @@ class PartialFusionGroupedConvBNLIF(CTFPattern):
 # ---------------------------------------------------------------------------
 
 class FusedLinearLIF(CTFPattern):
-    """Linear (+bias) -> LIF on [T, B, I]; the linear runs on the matrix
-    cores as a 1x1 convolution over B one-pixel images, the LIF in its
-    epilogue."""
+    """Linear (+bias) -> LIF on [T, B, I] (catfuse/patterns.py:533-571: the
+    linear over the T * B rows, then the LIF over T with the state
+    [B, out]).  Spike inputs run on the matrix cores as a 1x1 convolution
+    over the B samples of each step viewed as token images
+    (ConvLIFRunner.run_tokens: 8 x 8 images of 64 samples when 64 divides
+    B), the LIF in its epilogue; the output is the fp16 copy the next fused
+    layer reads.  The state is kept in that launch view, [nimg, out, H * W];
+    membrane() gives it as [B, out].  Analog inputs take the fp32 direct
+    path, state [B, out, 1, 1]."""
 
     policy_row = 4
 
@@ -577,6 +590,7 @@ class FusedLinearLIF(CTFPattern):
         self._impl = StreamFuse()
         self._params = None
         self._params_key = None
+        self._batch = None   # B of the last spike-input call (the state's view)
 
     def _ensure_params(self):
         key = (id(self.weight_io), self.weight_io._version,
@@ -592,10 +606,30 @@ class FusedLinearLIF(CTFPattern):
         if squeeze:
             x = x.unsqueeze(0)
         T, B, I = x.shape
-        y = self._impl.forward(x.reshape(T, B, I, 1, 1), self.spec, self._ensure_params(),
-                               self.state)
-        y = y.reshape(T, B, self.out_features)
+        impl = self._impl
+        params = self._ensure_params()
+        if not isinstance(x, runtime.NHWCSpikes) and impl.input_is_analog(x):
+            y = impl.forward(x.reshape(T, B, I, 1, 1), self.spec, params, self.state)
+            y = y.reshape(T, B, self.out_features)
+            self._batch = None
+            return y.squeeze(0) if squeeze else y
+        r = impl.runner(self.spec, params, x.device)
+        nimg, H, W = runtime.token_view(B, 1)
+        v_in = self.state.peek((nimg, self.out_features, H * W), x.device)
+        y, v = r.run_tokens(x, v_in)
+        self.state.set(v)
+        self._batch = B
         return y.squeeze(0) if squeeze else y
+
+    def membrane(self):
+        """The LIF state after the last call as [B, out_features] (None after
+        a reset)."""
+        v = self.state.tensor
+        if v is None:
+            return None
+        if self.__dict__.get("_batch") is None:
+            return v.reshape(v.shape[0], self.out_features)
+        return runtime.token_membrane(v, self._batch, 1).reshape(self._batch, self.out_features)
 
     @classmethod
     def from_sj_modules(cls, sj_linear, sj_lif):
@@ -737,6 +771,36 @@ class FusedGlobalAvgPool(nn.Module):
     @classmethod
     def from_sj_modules(cls, pool):
         return cls(getattr(pool, "step_mode", "s"))
+
+
+class FusedFlatten(nn.Module):
+    """Flatten of a network head in multi-step mode ([T, B, C, H, W] ->
+    [T, B, C * H * W], SpikingJelly's layer.Flatten with step_mode 'm').  A
+    fused layer's one-pixel output (H = W = 1, e.g. the last VGG pool) stays
+    in its fp16 copy (runtime.pixel_tokens): the fused linear layer that
+    follows reads the copy instead of a packed fp32 tensor.  No counterpart
+    in the reference.  Anything else is torch.flatten (counted in
+    `fallback_calls`)."""
+
+    def __init__(self):
+        super().__init__()
+        self.step_mode = "m"
+        self.fallback_calls = 0
+
+    def forward(self, x):
+        if x.dim() == 5:
+            y = runtime.pixel_tokens(x)
+            if y is not None:
+                return y
+        self.fallback_calls += 1
+        return torch.flatten(x, 2)
+
+    @classmethod
+    def from_sj_modules(cls, flat):
+        if (getattr(flat, "step_mode", "s") != "m" or flat.start_dim != 1
+                or flat.end_dim != -1):
+            raise ValueError("only the multi-step Flatten(start_dim=1) is fused")
+        return cls()
 
 
 # ---------------------------------------------------------------------------
@@ -958,7 +1022,7 @@ __all__ = ["CTFPattern", "PartialFusionConvLIF", "PartialFusionConvBNLIF",
            "PartialFusionConvBNAddLIF", "PartialFusionConvBNAvgPoolLIF",
            "PartialFusionConvBNLIFMaxPool", "PartialFusionGroupedConvBNLIF", "FusedLinearLIF",
            "FusedAddLIF", "FusedAddBNLIF", "FusedAvgPoolLIF", "FusedGlobalAvgPool",
-           "CTFSEWBasicBlock",
+           "FusedFlatten", "CTFSEWBasicBlock",
            "CTFSpikingBasicBlock", "CTFSEWBottleneck", "CTFSpikingBottleneck",
            "STFusionConvBNLIF", "PATTERN_REGISTRY", "fold_bn", "lif_params", "conv_geometry",
            "conv_unsupported_reason", "grouped_conv_supported", "is_lif_node"]

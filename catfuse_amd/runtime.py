@@ -396,6 +396,29 @@ def token_view(B: int, N: int):
     return (B, r, r) if (r * r == N and r >= 4) else (B, N, 1)
 
 
+def pixel_tokens(x: torch.Tensor) -> Optional[torch.Tensor]:
+    """A fused layer's output x [T, B, C, 1, 1] whose values are still only
+    in its fp16 NHWC copy, as token-major [T, B, C] over the same copy (for
+    one-pixel images the NHWC and NCHW orders agree): the flatten of a
+    network head that a fused linear layer reads without a pack.  Carries
+    x's count block and copy descriptor.  None for any other x."""
+    if (not isinstance(x, NHWCSpikes) or not x.__dict__.get("_cf_pending", False)
+            or x.__dict__.get("_cf_tokens", False) or x.dim() != 5
+            or x.shape[3] != 1 or x.shape[4] != 1):
+        return None
+    nhwc, ver = x._cf_nhwc
+    if ver != x._version:
+        return None
+    T, B, C = x.shape[:3]
+    with torch._C.DisableTorchFunctionSubclass():
+        base = torch.Tensor.view(x, T, B, C)
+    y = NHWCSpikes(base, nhwc, tokens=True)
+    for a in ("_cf_count", "_cf_desc"):
+        if a in x.__dict__:
+            setattr(y, a, x.__dict__[a])
+    return y
+
+
 def token_membrane(v: torch.Tensor, B: int, N: int) -> torch.Tensor:
     """A token layer's state [nimg, C, H * W] (per view image) as [B, N, C]."""
     return v.transpose(1, 2).reshape(B, N, v.shape[1])
@@ -1100,11 +1123,17 @@ class ConvLIFRunner:
         residual), read from its fp16 copy (packed if it has none; its values
         must be fp16-exact).  The membrane state is per view image,
         [nimg, Cout, H * W] (token_membrane gives it as [B, N, Cout]).
+        x may also be [T, B, Cin] (one token per sample, N = 1; identity and
+        output are then [T, B, Cout]).
         Returns (lazy fp32 tokens [T, B, N, Cout], v_out or None)."""
         require_gpu_tensor(x, "x")
         if self.KH != 1 or self.KW != 1 or self.stride != 1 or self.padding != 0:
             raise ValueError("run_tokens needs a 1x1 kernel with stride 1 and no padding")
-        T, B, N, C = x.shape
+        if x.dim() == 3:
+            (T, B, C), N = x.shape, 1
+        else:
+            T, B, N, C = x.shape
+        out_shape = tuple(x.shape[:-1]) + (self.Cout,)
         if C != self.Cin:
             raise ValueError(f"expected {self.Cin} input channels, got {C}")
         dev = x.device
@@ -1129,7 +1158,7 @@ class ConvLIFRunner:
         id_keep = ()
         if identity is not None:
             require_gpu_tensor(identity, "identity")
-            if tuple(identity.shape) != (T, B, N, self.Cout):
+            if tuple(identity.shape) != out_shape:
                 raise ValueError("identity shape mismatch")
             id_copy = token_shadow(identity, id_cp, resolve=False)
             if id_copy is not None:
@@ -1147,7 +1176,7 @@ class ConvLIFRunner:
             xp.view(T * nimg, H, W, self.Cp), T, nimg, H, W, H, W, x.numel(), nnz, None, None,
             0, 0, 0, v_in, EPI_LIF, want_v_out, None,
             None if id_copy is None else id_copy.view(T * nimg, H, W, id_cp), ID_ADD_SPIKE, 2.0,
-            True, lambda nhwc: lazy_tokens((T, B, N, self.Cout), nhwc, dev), "linear_tokens",
+            True, lambda nhwc: lazy_tokens(out_shape, nhwc, dev), "linear_tokens",
             x_desc=x_desc, id_desc=id_desc, id_nnz=id_nnz, id_keep=id_keep)
         return out, (None if v_out is None else lazy_view(v_out, nimg, self.Cout, H * W))
 
@@ -1240,6 +1269,60 @@ class ConvLIFRunner:
             self.padding, tstride, *self.lif, _hip.stream(dev))
         check(rc, "cf_conv_direct_lif_maxpool")
         _t1("conv_direct_pool", ev, flops=2 * (1 if tstride == 0 else T) * B * Ho * Wo *
+            self.Cout * C * 9)
+        out = lazy_output((T, B, self.Cout, Hp, Wp), nhwc, dev)
+        if nz_out is not None and gen_cell is not None:
+            gen_cell[0] += 1
+            attach_count(out, nz_out, gen_cell)
+        return out, v_out
+
+    # -- analog 3 x 3 conv -> BN -> AvgPool(2, 2) -> LIF ---------------------
+
+    def direct_avgpool_supported(self, x: torch.Tensor) -> bool:
+        """cf_conv_direct_avgpool_lif covers a 3 x 3, stride-1 conv (padding
+        <= 2) over an fp32 input of at most 4 channels, Cout a multiple of 16,
+        with a conv output of at least 2 x 2."""
+        if not (x.dim() == 5 and x.dtype == torch.float32 and x.is_cuda and self.Cin <= 4
+                and self.KH == 3 and self.KW == 3 and self.stride == 1 and self.padding <= 2
+                and self.Cout % 16 == 0 and x.shape[1] <= 65535):
+            return False
+        Ho, Wo = self.out_hw(x.shape[3], x.shape[4])
+        return Ho >= 2 and Wo >= 2
+
+    def run_direct_avgpool(self, x: torch.Tensor, v_in=None, *, want_v_out=True, nz_out=None,
+                           gen_cell=None):
+        """x [T, B, Cin, H, W] analog (a stride-0 time axis evaluates the conv
+        once) -> (pooled spikes [T, B, Cout, Ho//2, Wo//2] as a lazy output
+        over their fp16 NHWC copy, carrying its count block with nz_out and
+        gen_cell; pooled membrane [B, Cout, Ho//2, Wo//2])."""
+        if not self.direct_avgpool_supported(x):
+            raise ValueError("input/layer not covered by cf_conv_direct_avgpool_lif")
+        _require_block(nz_out)
+        T, B, C, H, W = x.shape
+        dev = x.device
+        self._ensure_packed(dev)
+        if x.stride(0) == 0 and x[0].is_contiguous():
+            tstride, xb = 0, x[0]
+        else:
+            x = x.contiguous()
+            tstride, xb = B, x
+        Ho, Wo = self.out_hw(H, W)
+        Hp, Wp = Ho // 2, Wo // 2
+        if v_in is not None:
+            require_gpu_tensor(v_in, "v_in")
+            if v_in.numel() != B * self.Cout * Hp * Wp:
+                raise ValueError("v_in has the wrong size")
+        v_out = (torch.empty((B, self.Cout, Hp, Wp), dtype=torch.float32, device=dev)
+                 if want_v_out else None)
+        cp_out = pad32(self.Cout)
+        nhwc = torch.empty((T * B, Hp, Wp, cp_out), dtype=torch.float16, device=dev)
+        ev = _t0()
+        rc = _hip.lib().cf_conv_direct_avgpool_lif(
+            ptr(xb), ptr(self._wt_f32), ptr(self.alpha_direct), ptr(self.beta_direct),
+            ptr(v_in), ptr(v_out), ptr(nhwc), cp_out, ptr(nz_out), T, B, C, self.Cout, H, W,
+            self.padding, tstride, *self.lif, _hip.stream(dev))
+        check(rc, "cf_conv_direct_avgpool_lif")
+        _t1("conv_direct_avgpool", ev, flops=2 * (1 if tstride == 0 else T) * B * Ho * Wo *
             self.Cout * C * 9)
         out = lazy_output((T, B, self.Cout, Hp, Wp), nhwc, dev)
         if nz_out is not None and gen_cell is not None:

@@ -29,8 +29,8 @@ import torch.nn as nn
 from catfuse_amd.transformer import (CTFSpikformerBlock, CTFSpikformerSPS, is_spikformer_block,
                                      is_spikformer_sps)
 from catfuse_amd.patterns import (CTFSEWBasicBlock, CTFSEWBottleneck, CTFSpikingBasicBlock,
-                                  CTFSpikingBottleneck, FusedAvgPoolLIF, FusedGlobalAvgPool,
-                                  FusedLinearLIF,
+                                  CTFSpikingBottleneck, FusedAvgPoolLIF, FusedFlatten,
+                                  FusedGlobalAvgPool, FusedLinearLIF,
                                   PartialFusionConvBNAvgPoolLIF, PartialFusionConvBNLIF,
                                   PartialFusionConvBNLIFMaxPool, PartialFusionConvLIF,
                                   PartialFusionGroupedConvBNLIF, STFusionConvBNLIF, conv_geometry,
@@ -516,18 +516,27 @@ def substitute_sf(sj_model, T=16, verbose=False, force_sparse=False, fuse_sew_ad
         _wrap_sew_blocks(model)
 
     # Phase 3: a global average pool in the head reads the last fused conv's
-    # fp16 NHWC copy (no counterpart in the reference, which leaves the head
-    # to SpikingJelly).
+    # fp16 NHWC copy, and a multi-step flatten passes a one-pixel fused
+    # output on as tokens over that copy (no counterpart in the reference,
+    # which leaves the head to SpikingJelly).
     if fuse_head:
         for pname, pmod in list(model.named_modules()):
             for name, ch in list(pmod.named_children()):
                 if _is_global_avgpool(ch):
                     setattr(pmod, name, FusedGlobalAvgPool.from_sj_modules(ch))
                     _bump(stats, "FusedGlobalAvgPool")
+                elif _is_multistep_flatten(ch):
+                    setattr(pmod, name, FusedFlatten.from_sj_modules(ch))
+                    _bump(stats, "FusedFlatten")
 
     _record_unsupported_convs(model, stats)
     stats["coverage_pct"] = 100.0 * stats["fused_lif_nodes"] / max(stats["total_lif_nodes"], 1)
     return holder.root, stats
+
+
+def _is_multistep_flatten(m) -> bool:
+    return (isinstance(m, nn.Flatten) and getattr(m, "step_mode", "s") == "m"
+            and m.start_dim == 1 and m.end_dim == -1)
 
 
 def _is_global_avgpool(m) -> bool:

@@ -250,8 +250,9 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
                          const float* bias, void* w_packed, float* alpha, float* beta,
                          void* stream);
 
-/* Fused Conv -> BN -> LIF (epilogue 0) or Conv -> BN -> z (epilogue 1) on
- * the matrix cores, all T steps in one launch.
+/* Fused Conv -> BN -> LIF (epilogue 0), Conv -> BN -> z (epilogue 1) or
+ * Conv -> BN -> AvgPool2d(2, 2) -> LIF (epilogue 2) on the matrix cores, all
+ * T steps in one launch.
  *   x: NHWC16 [T*x_img_tstride + B][H][W][Cp] from cf_pack_input;
  *   out: NCHW [T][B][Cout][Ho][Wo] spikes or z;
  *   out_nhwc (nullable): the same values as fp16 NHWC [T*B][Ho][Wo][cp_out]
@@ -309,6 +310,16 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
  *   launch writes its outputs and records so.  A caller that passes
  *   out_desc reads the outputs through it (or hands it on as x_desc /
  *   id_desc).
+ *   Epilogue 2 (stride-1 3x3 convs on 8x8 tiles, the halo kernel): each 2x2
+ *   window of BN outputs is summed as ((z00 + z01) + z10) + z11, times
+ *   0.25 (the order of cf_avgpool2x2_lif, so the spikes equal epilogue 1
+ *   followed by cf_avgpool2x2_lif bit for bit), and drives the pooled
+ *   neuron's LIF; out_nhwc (required, out must be NULL) then holds the
+ *   pooled spikes [T*B][Ho/2][Wo/2][cp_out] (cp_out a multiple of 4),
+ *   v_in/v_out the pooled state [B][Cout][Ho/2][Wo/2]; Cout a multiple of
+ *   32, no identity, bias_info 0 (reference: the F8 chain of
+ *   catfuse/kernels/conv_pool_lif.py:94-178, whose z makes a round trip
+ *   through HBM).
  * Replaces catfuse/implementations/dense_keep.py:97-155 (DenseKeep.forward),
  * catfuse/implementations/sparse_flow.py:186-270 (SparseFlow.forward ->
  * catfuse/sparseflow/streamfuse_kernel.py:32-187), and
@@ -414,6 +425,28 @@ int cf_conv_direct(const float* x, const float* w, const float* alpha, const flo
  * models/spikformer_github.py:181-254 (proj_conv, proj_bn, proj_lif, maxpool),
  * which runs the conv, the LIF and the pool as separate passes. */
 int cf_conv_direct_lif_maxpool(const float* x, const float* wt, const float* alpha,
+                               const float* beta, const float* v_in, float* v_out,
+                               void* out_nhwc, int64_t cp_out, unsigned long long* nz_out,
+                               int64_t T, int64_t B, int64_t Cin, int64_t Cout, int64_t H,
+                               int64_t W, int64_t pad, int64_t x_img_tstride, double tau,
+                               double v_th, double v_reset, int hard_reset, int decay_input,
+                               void* stream);
+
+/* Conv(3 x 3, stride 1, Cin <= 4) -> BN -> AvgPool2d(2, 2) -> LIF of an
+ * analog input x [T*x_img_tstride + B][Cin][H][W] in one launch (fp32 VALU,
+ * the arithmetic of cf_conv_direct, then the pool sum
+ * ((z00 + z01) + z10) + z11 times 0.25 and the LIF of cf_avgpool2x2_lif, so
+ * the spikes equal cf_conv_direct (epilogue 1) followed by
+ * cf_avgpool2x2_lif bit for bit; a stride-0 time axis evaluates the conv
+ * once).  wt is the transposed filter [Cin*9][Cout]; alpha/beta as for
+ * cf_conv_direct; Cout a multiple of 16.  Writes the pooled fp16 NHWC copy
+ * [T*B][Hp][Wp][cp_out] (Hp = Ho / 2, Wp = Wo / 2; channels Cout ..
+ * cp_out-1 zero; cp_out a multiple of 8) and the pooled membrane v_out
+ * [B][Cout][Hp][Wp] (nullable; v_in likewise), and publishes the output's
+ * count block nz_out (nullable).  Replaces the reference's F8
+ * (catfuse/kernels/conv_pool_lif.py:94-178: the conv's z written to HBM, then
+ * the pool and the LIF) for the first layer of a spiking VGG. */
+int cf_conv_direct_avgpool_lif(const float* x, const float* wt, const float* alpha,
                                const float* beta, const float* v_in, float* v_out,
                                void* out_nhwc, int64_t cp_out, unsigned long long* nz_out,
                                int64_t T, int64_t B, int64_t Cin, int64_t Cout, int64_t H,

@@ -194,6 +194,12 @@ def test_substitute_sf_vgg11():
     assert pm["FusedLinearLIF"] == 2
     assert pm.get("PartialFusionConvBNLIF", 0) + pm.get("STFusionConvBNLIF", 0) == 3
     assert stats["fused_lif_nodes"] == stats["total_lif_nodes"] == 10
+    # the head's multi-step flatten passes the last pool's copy on as tokens
+    from catfuse_amd.patterns import FusedFlatten
+    assert pm["FusedFlatten"] == 1 and isinstance(fused.flatten, FusedFlatten)
+    x = torch.arange(2 * 3 * 4 * 2 * 2, dtype=torch.float32).view(2, 3, 4, 2, 2)
+    assert torch.equal(fused.flatten(x), torch.flatten(x, 2))   # not a fused output
+    assert fused.flatten.fallback_calls == 1
 
 
 def test_crossover_inputs_and_decision():

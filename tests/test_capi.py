@@ -171,6 +171,16 @@ def test_token_and_pool_entry_points_validate_arguments():
     assert direct_pool(pad=3) == INVALID            # padding beyond 2
     assert direct_pool(H=1, pad=0) == INVALID       # empty conv output
 
+    def direct_avg(Cin=3, Cout=64, cp_out=64, pad=1, H=32, W=32):
+        return L.cf_conv_direct_avgpool_lif(1, 1, 1, 1, None, None, 1, cp_out, None, 4, 2, Cin,
+                                            Cout, H, W, pad, 0, 2.0, 1.0, 0.0, 1, 1, None)
+    assert direct_avg(Cin=5) == INVALID             # more than 4 input channels
+    assert direct_avg(Cout=24, cp_out=32) == INVALID    # Cout not a multiple of 16
+    assert direct_avg(cp_out=68) == INVALID         # copy pitch not a multiple of 8
+    assert direct_avg(cp_out=32) == INVALID         # copy narrower than Cout
+    assert direct_avg(pad=3) == INVALID             # padding beyond 2
+    assert direct_avg(H=3, pad=0) == INVALID        # 1-row conv output: no 2x2 window
+
     def attention(N=196, heads=2, head_dim=32, pitch=192, qoff=0, cp_out=64):
         return L.cf_spike_attention_lif(1, 1, 1, qoff, 64, 128, pitch, 1, cp_out, None, None,
                                         None, None, None, 0, 4, 2, N, heads, head_dim, 0.125,

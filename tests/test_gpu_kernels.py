@@ -804,6 +804,45 @@ def test_conv_direct_stem_parity(cuda, dedupe):
     lif_parity(spk.cpu().numpy(), v.cpu().numpy(), s_ref, v_ref, h_ref, what="stem")
 
 
+DIRECT_AVG_CASES = [
+    # name, T, B, Cin, Cout, H, W, pad, LIF variant, direct encoding, v_in
+    ("vgg0", 4, 2, 3, 64, 32, 32, 1, 0, True, False),
+    ("odd_steps", 3, 3, 3, 32, 37, 35, 1, 2, False, True),
+    ("c1_pad0", 5, 2, 1, 16, 6, 7, 0, 5, True, True),
+    ("t9_c4", 9, 1, 4, 48, 20, 18, 2, 3, False, False),
+]
+
+
+@pytest.mark.parametrize("case", DIRECT_AVG_CASES, ids=[c[0] for c in DIRECT_AVG_CASES])
+def test_conv_direct_avgpool_lif_bitwise(cuda, case):
+    """cf_conv_direct_avgpool_lif (analog Conv 3x3 -> BN -> AvgPool 2x2 ->
+    LIF) equals cf_conv_direct's z followed by cf_avgpool2x2_lif bit for
+    bit: odd sizes (the pool's floor, partial 16 x 16 tiles), a stride-0
+    time axis and a time-varying input, an initial state, generic LIF forms;
+    its count block says whether any pooled spike fired."""
+    from catfuse_amd import runtime, snn
+    name, T, B, Cin, Cout, H, W, p, variant, direct, with_v = case
+    lif = snn.LIFNode(**LIF_VARIANTS[variant])
+    conv, bn, lif = _layer(Cin, Cout, 3, 1, p, seed=len(name) + 7 * T, bias=True, lif=lif)
+    r = _runner(conv, bn, lif, cuda)
+    g = _gen(T + 3 * Cout)
+    if direct:
+        img = torch.randn(B, Cin, H, W, generator=g).to(cuda)
+        x = img.unsqueeze(0).expand(T, B, Cin, H, W)
+    else:
+        x = torch.randn(T, B, Cin, H, W, generator=g).to(cuda)
+    Ho, Wo = H + 2 * p - 2, W + 2 * p - 2
+    v0 = (torch.randn(B, Cout, Ho // 2, Wo // 2, generator=g) * 0.4).to(cuda) if with_v else None
+    nz = runtime.count_block(cuda)
+    s, v = r.run_direct_avgpool(x, v0, nz_out=nz, gen_cell=[0])
+    z, _ = r.run_direct(x, epilogue=runtime.EPI_Z)
+    s_ref, v_ref = runtime.avgpool2x2_lif(z, v0, **LIF_VARIANTS[variant])
+    torch.cuda.synchronize()
+    assert (int(runtime.count_of(s)[1].item()) != 0) == bool(s_ref.any()), name
+    assert s.shape == s_ref.shape and torch.equal(s.cpu(), s_ref.cpu()), name
+    assert torch.equal(v.cpu(), v_ref.cpu()), name
+
+
 STEM_CASES = [
     # name, T, B, H, W, Cout, lif, continue_state
     ("rn_stem", 4, 2, 64, 64, 64, None, False),

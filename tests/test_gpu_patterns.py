@@ -186,8 +186,79 @@ def test_fused_linear_lif(cuda):
     out = pat(x.to(cuda))
     z = F.linear(x.double(), lin.weight.double(), lin.bias.double()).float()
     s_ref, v_ref, h_ref = oracle.lif_multistep(z)
-    lif_parity(out.cpu().numpy(), pat.state.tensor.cpu().numpy(), s_ref, v_ref, h_ref,
+    lif_parity(out.cpu().numpy(), pat.membrane().cpu().numpy(), s_ref, v_ref, h_ref,
                what="linear")
+
+
+@pytest.mark.parametrize("cin,cout,rate", [(512, 4096, 0.3), (4096, 256, 0.2), (4096, 4096, 0.0)])
+def test_fused_linear_lif_token_view(cuda, cin, cout, rate):
+    """B = 64 samples per step: the linear runs as the halo 1x1 kernel over
+    one 8 x 8 token image per step (4096 inputs: 128 K chunks), against the
+    fp64 linear + the LIF oracle; a second call continues from the state
+    (held in the launch view; membrane() gives [B, out])."""
+    from catfuse_amd import runtime, snn
+    from catfuse_amd.patterns import FusedLinearLIF
+    T, B = 4, 64
+    lin, lif = snn.Linear(cin, cout), snn.LIFNode()
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(cout, cin, generator=_gen(cin)) * (2 / cin) ** 0.5 * 2)
+        lin.bias.copy_(torch.randn(cout, generator=_gen(cout)) * 0.5)
+    pat = FusedLinearLIF.from_sj_modules(lin, lif).to(cuda)
+    x1 = (torch.rand(T, B, cin, generator=_gen(5)) < rate).float()
+    x2 = (torch.rand(T, B, cin, generator=_gen(6)) < rate).float()
+    y1 = pat(x1.to(cuda))
+    assert isinstance(y1, runtime.NHWCSpikes) and y1.shape == (T, B, cout)
+    assert pat.state.tensor.shape == (1, cout, 64)
+    y2 = pat(x2.to(cuda))
+    x = torch.cat([x1, x2])
+    z = F.linear(x.double(), lin.weight.double(), lin.bias.double()).float()
+    s_ref, v_ref, h_ref = oracle.lif_multistep(z)
+    out = torch.cat([y1.cpu(), y2.cpu()]).numpy()
+    lif_parity(out, pat.membrane().cpu().numpy(), s_ref, v_ref, h_ref, what=f"linear{cin}")
+
+
+def test_vgg_head_reads_pool_copy(cuda):
+    """Conv-BN-AvgPool-LIF to a 1 x 1 map, FusedFlatten, two FusedLinearLIF:
+    the flatten stays lazy over the pool's fp16 copy, the linears read it
+    (no pack), and every output equals the same chain on materialised fp32
+    tensors bit for bit."""
+    from catfuse_amd import runtime, snn
+    from catfuse_amd.patterns import (FusedFlatten, FusedLinearLIF,
+                                      PartialFusionConvBNAvgPoolLIF)
+    T, B = 4, 64
+    g = _gen(31)
+    conv = snn.Conv2d(128, 128, 3, 1, 1, bias=False)
+    bn = snn.BatchNorm2d(128)
+    with torch.no_grad():
+        conv.weight.copy_(torch.randn(conv.weight.shape, generator=g) * (2 / 1152) ** 0.5 * 3)
+        bn.running_mean.copy_(torch.randn(128, generator=g) * 0.1)
+        bn.bias.copy_(torch.randn(128, generator=g) * 0.3 + 0.3)
+    blk = PartialFusionConvBNAvgPoolLIF.from_sj_modules(conv, bn.eval(), snn.AvgPool2d(2, 2),
+                                                        snn.LIFNode()).to(cuda)
+    l1, l2 = snn.Linear(128, 512), snn.Linear(512, 256)
+    with torch.no_grad():
+        for lin in (l1, l2):
+            lin.weight.copy_(torch.randn(lin.weight.shape, generator=g) *
+                             (2 / lin.in_features) ** 0.5 * 3)
+            lin.bias.copy_(torch.randn(lin.out_features, generator=g) * 0.3)
+    f1 = FusedLinearLIF.from_sj_modules(l1, snn.LIFNode()).to(cuda)
+    f2 = FusedLinearLIF.from_sj_modules(l2, snn.LIFNode()).to(cuda)
+    flat = FusedFlatten()
+    x = (torch.rand(T, B, 128, 2, 2, generator=g) < 0.4).float().to(cuda)
+    p = blk(x)
+    t = flat(p)
+    assert flat.fallback_calls == 0 and isinstance(t, runtime.NHWCSpikes)
+    assert t.__dict__.get("_cf_pending") and p.__dict__.get("_cf_pending")
+    y1 = f1(t)
+    y2 = f2(y1)
+    assert t.__dict__.get("_cf_pending"), "the flatten was materialised"
+    # the same chain on plain fp32 tensors
+    for m in (f1, f2):
+        m.reset()
+    r1 = f1(torch.flatten(p.clone(), 2))
+    r2 = f2(r1.clone())
+    assert torch.equal(y1.cpu(), r1.cpu()) and torch.equal(y2.cpu(), r2.cpu())
+    assert bool(p.clone().any()), "the test input should make the pool fire"
 
 
 def test_tail_patterns_bit_exact(cuda):
