@@ -32,7 +32,8 @@ _SIGNATURES = {
     "cf_nhwc_to_nchw": [_P, _P, _I, _I, _I, _I, _I, _P],
     "cf_global_avgpool_nhwc": [_P, _P, _P, _I, _I, _I, _I, _P],
     "cf_resolve_copy": [_P, _I, _P, _P],
-    "cf_bias_response": [_P, _P, _I, _I, c_double, c_double, c_double, c_int, c_int, _P, _P, _P],
+    "cf_bias_response": [_P, _P, _I, _I, c_int, c_double, c_double, c_double, c_int, c_int, _P,
+                         _P, _P],
     "cf_expand_state": [_P, _P, _P, _I, _I, _I, _P],
     "cf_pack_tokens": [_P, _I, _I, _I, _P, _P, _P, _P],
     "cf_tokens_to_f32": [_P, _P, _I, _I, _I, _P],

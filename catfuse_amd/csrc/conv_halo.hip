@@ -297,6 +297,24 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   // also holds the per-channel final potentials, v_out is not written
   // either; then workgroup 0 alone records the descriptor and the count,
   // and every workgroup returns here, before any other memory access.
+  // The pooled epilogue likewise, when the pooled bias response
+  // (cf_bias_response with pool = 1) is silent: the copy is recorded as all
+  // zero and not written, v_out left to the caller's per-channel potentials
+  // (or not asked for); otherwise a pooled StaticZero launch runs the
+  // epilogue on z = beta below.
+  if constexpr (EPI == EPI_POOL) {
+    if (route == CF_ROUTE_ZERO && a.v_in == nullptr && a.out_desc != nullptr &&
+        (a.bias_info & CF_BIAS_SILENT) != 0 &&
+        ((a.bias_info & CF_BIAS_VCHAN) != 0 || a.v_out == nullptr)) {
+      if (L == 0 && tid == 0) {
+        if (a.nz_out != nullptr) a.nz_out[1] = 0ull;
+        a.out_desc->copy = CF_COPY_ZERO;
+        a.out_desc->vstate = (a.bias_info & CF_BIAS_VCHAN) != 0 ? 1u : 0u;
+        a.out_desc->alias = nullptr;
+      }
+      return;
+    }
+  }
   const bool zlean = LEAN && EPI == EPI_LIF && route == CF_ROUTE_ZERO && a.v_in == nullptr &&
                      (a.T + 2) * BM <= 2 * HB;
   const bool zvchan = zlean && a.out_desc != nullptr && (a.bias_info & CF_BIAS_VCHAN) != 0;
@@ -1228,11 +1246,10 @@ int make_halo_args(HaloArgs& a, const void* x, const void* w_packed, const float
     return (int)hipErrorInvalidValue;
   // BN -> AvgPool2d(2, 2) -> LIF: stride-1 3x3 convs on 8x8 tiles, the
   // pooled spikes as the fp16 NHWC copy only (pitch a multiple of 4), whole
-  // 32-channel groups, no identity, no StaticZero elision (the pooled bias
-  // response is not the layer's)
+  // 32-channel groups, no identity (bias_info: the pooled bias response)
   if (epilogue == EPI_POOL &&
       (ksize != 3 || stride != 1 || tile_w != 8 || out || !out_nhwc || cp_out % 4 != 0 ||
-       Cout % 32 != 0 || identity || identity_nhwc || bias_info != 0 || Ho < 2 || Wo < 2))
+       Cout % 32 != 0 || identity || identity_nhwc || Ho < 2 || Wo < 2))
     return (int)hipErrorInvalidValue;
   if (!((tile_h == 8 && tile_w == 8) || (tile_h == 8 && tile_w == 16 && stride == 1 && ksize == 3)))
     return (int)hipErrorInvalidValue;
@@ -1300,17 +1317,20 @@ void conv_halo_pair_kernel(HaloArgs a, HaloArgs b, int nLa) {
 }
 
 // The StaticZero drive of each channel (z = 0 * alpha + beta, from the
-// initial state, T steps) with the lean path's operations: its final
+// initial state, T steps; pool: the pooled epilogue's average of four equal
+// z, summed in its order) with the epilogues' operations: its final
 // potential and whether it fires at some step.
 template <int LM>
 __global__ __launch_bounds__(256) void bias_response_kernel(const float* __restrict__ alpha,
                                                             const float* __restrict__ beta,
-                                                            int Cout, int T, LifParams lif,
+                                                            int Cout, int T, int pool,
+                                                            LifParams lif,
                                                             float* __restrict__ v_final,
                                                             uint32_t* __restrict__ fires) {
   const int c = (int)blockIdx.x * 256 + (int)threadIdx.x;
   if (c >= Cout) return;
-  const float z = __builtin_fmaf(0.0f, alpha[c], beta[c]);
+  const float z1 = __builtin_fmaf(0.0f, alpha[c], beta[c]);
+  const float z = pool ? (((z1 + z1) + z1) + z1) * 0.25f : z1;
   float v = lif_initial_v(lif);
   bool f = false;
   for (int t = 0; t < T; ++t) {
@@ -1325,10 +1345,10 @@ __global__ __launch_bounds__(256) void bias_response_kernel(const float* __restr
 }  // namespace
 
 CF_API int cf_bias_response(const float* alpha, const float* beta, int64_t Cout, int64_t T,
-                            double tau, double v_th, double v_reset, int hard_reset,
+                            int pool, double tau, double v_th, double v_reset, int hard_reset,
                             int decay_input, float* v_final, uint32_t* fires, void* stream) {
   if (!alpha || !beta || !v_final || !fires || Cout <= 0 || Cout > INT32_MAX || T <= 0 ||
-      T > INT32_MAX)
+      T > INT32_MAX || (pool != 0 && pool != 1))
     return (int)hipErrorInvalidValue;
   const LifParams lif = cf_make_lif_params(tau, v_th, v_reset, hard_reset, decay_input);
   const dim3 grid(cf_blocks(Cout, 256)), block(256);
@@ -1336,15 +1356,15 @@ CF_API int cf_bias_response(const float* alpha, const float* beta, int64_t Cout,
   switch (cf_lif_mode(lif)) {
     case LM_HARD0_DECAY_P2:
       hipLaunchKernelGGL(bias_response_kernel<LM_HARD0_DECAY_P2>, grid, block, 0, st, alpha, beta,
-                         (int)Cout, (int)T, lif, v_final, fires);
+                         (int)Cout, (int)T, pool, lif, v_final, fires);
       break;
     case LM_HARD_DECAY_P2:
       hipLaunchKernelGGL(bias_response_kernel<LM_HARD_DECAY_P2>, grid, block, 0, st, alpha, beta,
-                         (int)Cout, (int)T, lif, v_final, fires);
+                         (int)Cout, (int)T, pool, lif, v_final, fires);
       break;
     default:
       hipLaunchKernelGGL(bias_response_kernel<LM_GENERIC>, grid, block, 0, st, alpha, beta,
-                         (int)Cout, (int)T, lif, v_final, fires);
+                         (int)Cout, (int)T, pool, lif, v_final, fires);
   }
   return (int)hipGetLastError();
 }

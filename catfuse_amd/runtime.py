@@ -738,7 +738,7 @@ def zero_drive_response(device, T: int, lif) -> Optional[tuple]:
         z = torch.zeros(1, dtype=torch.float32, device=device)
         v = torch.empty(1, dtype=torch.float32, device=device)
         f = torch.empty(1, dtype=torch.int32, device=device)
-        check(_hip.lib().cf_bias_response(ptr(z), ptr(z), 1, T, *lif, ptr(v), ptr(f),
+        check(_hip.lib().cf_bias_response(ptr(z), ptr(z), 1, T, 0, *lif, ptr(v), ptr(f),
                                           _hip.stream(device)), "cf_bias_response")
         r = _ZERO_DRIVE[key] = (v, not bool(f.item()))
     return r
@@ -873,31 +873,34 @@ class ConvLIFRunner:
         self._bias_resp = {}
         self._packed_key = key
 
-    def bias_response(self, device, T: int):
+    def bias_response(self, device, T: int, pool: bool = False):
         """(v_final [Cout] fp32, silent) of the layer's bias drive alone over
-        T steps (cf_bias_response): each channel's final potential on the
-        StaticZero route, and whether no channel fires there.  Computed once
-        per T (a host read); None while a graph is being captured and the
-        value is not yet known."""
-        r = self._bias_resp.get(T)
+        T steps (cf_bias_response; pool: the pooled epilogue's drive): each
+        channel's final potential on the StaticZero route, and whether no
+        channel fires there.  Computed once per (T, pool) (a host read); None
+        while a graph is being captured and the value is not yet known."""
+        key = (T, bool(pool))
+        r = self._bias_resp.get(key)
         if r is None:
             if torch.cuda.is_current_stream_capturing():
                 return None
             v = torch.empty(self.Cout, dtype=torch.float32, device=device)
             f = torch.empty(self.Cout, dtype=torch.int32, device=device)
             check(_hip.lib().cf_bias_response(ptr(self.alpha), ptr(self.beta), self.Cout, T,
-                                              *self.lif, ptr(v), ptr(f), _hip.stream(device)),
+                                              int(bool(pool)), *self.lif, ptr(v), ptr(f),
+                                              _hip.stream(device)),
                   "cf_bias_response")
-            r = self._bias_resp[T] = (v, not bool(f.any().item()))
+            r = self._bias_resp[key] = (v, not bool(f.any().item()))
         return r
 
-    def zero_route_info(self, device, T: int, desc, v_out, v_in):
+    def zero_route_info(self, device, T: int, desc, v_out, v_in, pool: bool = False):
         """(bias_info, v_final or None) for a launch with output descriptor
         desc: the bias_info bits of cf_conv_mfma and the per-channel
-        potentials that stand for v_out when the launch leaves it unwritten."""
+        potentials that stand for v_out when the launch leaves it unwritten
+        (pool: a launch with the pooled epilogue)."""
         if desc is None:
             return 0, None
-        r = self.bias_response(device, T)
+        r = self.bias_response(device, T, pool)
         if r is None:
             return 0, None
         v_final, silent = r
@@ -1083,10 +1086,11 @@ class ConvLIFRunner:
             out = torch.empty((T, B, self.Cout, Ho, Wo), dtype=torch.float32, device=dev)
             out_ptr = ptr(out)
         desc = None
-        if (COPY_ELISION and nhwc is not None and epilogue == EPI_LIF
+        if (COPY_ELISION and nhwc is not None and epilogue != EPI_Z
                 and (nnz is not None or x_desc is not None)):
             desc = new_out_desc(dev)
-        bias_info, v_chan = self.zero_route_info(dev, T, desc, v_out, v_in)
+        bias_info, v_chan = self.zero_route_info(dev, T, desc, v_out, v_in,
+                                                 pool=epilogue == EPI_POOL)
         if bias_info & 1:
             # the launch may leave the copy unwritten: readers go through
             # the descriptor (otherwise it always writes the copy)

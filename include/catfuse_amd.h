@@ -317,7 +317,10 @@ int cf_pack_conv_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
  *   neuron's LIF; out_nhwc (required, out must be NULL) then holds the
  *   pooled spikes [T*B][Ho/2][Wo/2][cp_out] (cp_out a multiple of 4),
  *   v_in/v_out the pooled state [B][Cout][Ho/2][Wo/2]; Cout a multiple of
- *   32, no identity, bias_info 0 (reference: the F8 chain of
+ *   32, no identity; bias_info from cf_bias_response with pool = 1 (a
+ *   StaticZero launch with no v_in and bit 0 writes no copy, records it as
+ *   all zero, and with bit 1 leaves v_out to the per-channel potentials;
+ *   every other pooled launch writes its outputs) (reference: the F8 chain of
  *   catfuse/kernels/conv_pool_lif.py:94-178, whose z makes a round trip
  *   through HBM).
  * Replaces catfuse/implementations/dense_keep.py:97-155 (DenseKeep.forward),
@@ -388,16 +391,18 @@ int cf_conv_halo_pair(const void* x, const unsigned long long* nnz, const void* 
                       void* stream);
 
 /* A layer's response to its BN bias alone (the StaticZero drive z =
- * 0 * alpha + beta, alpha/beta from cf_pack_conv_weights, Cout entries),
- * from the initial state over T steps, with the halo kernel's operations:
+ * 0 * alpha + beta, alpha/beta from cf_pack_conv_weights, Cout entries;
+ * pool = 1: the drive of cf_conv_mfma's pooled epilogue, the 2x2 average
+ * (((z + z) + z) + z) * 0.25 of that z), from the initial state over T
+ * steps, with the halo kernel's operations:
  * v_final [Cout] the final potential and fires [Cout] 1 where the channel
  * fires at some step.  Computed once per layer and T; the bias_info of
  * cf_conv_mfma states it.  No counterpart in the reference (its StaticZero
  * short-circuit, catfuse/implementations/base.py:250-308
  * static_zero_forward, broadcasts the bias and runs the LIF on every
  * call). */
-int cf_bias_response(const float* alpha, const float* beta, int64_t Cout, int64_t T, double tau,
-                     double v_th, double v_reset, int hard_reset, int decay_input,
+int cf_bias_response(const float* alpha, const float* beta, int64_t Cout, int64_t T, int pool,
+                     double tau, double v_th, double v_reset, int hard_reset, int decay_input,
                      float* v_final, uint32_t* fires, void* stream);
 
 /* Fused Conv -> BN -> LIF / z in fp32 (VALU) for analog inputs

@@ -100,7 +100,6 @@ def test_host_side_argument_validation():
                               epi, 2.0, 1.0, 0.0, 1, 1, None)
     assert pooled(out=1) == INVALID                          # fp32 output
     assert pooled(identity=1) == INVALID                     # identity
-    assert pooled(out_desc=1, info=1) == INVALID             # StaticZero elision
     assert pooled(Cout=48, cp_out=48) == INVALID             # partial 32-channel group
     assert pooled(Cout=32, cp_out=34) == INVALID             # copy pitch not a multiple of 4
     assert pooled(H=16, stride=2) == INVALID                 # stride 2
@@ -109,8 +108,9 @@ def test_host_side_argument_validation():
     assert pooled(H=1, Ho=1) == INVALID                      # no whole 2x2 window
     assert pooled(T=9, v_out=None) == INVALID                # state across time blocks
     assert pooled(epi=3) == INVALID                          # unknown epilogue
-    assert L.cf_bias_response(1, 1, 0, 4, 2.0, 1.0, 0.0, 1, 1, 1, 1, None) == INVALID
-    assert L.cf_bias_response(1, None, 8, 4, 2.0, 1.0, 0.0, 1, 1, 1, 1, None) == INVALID
+    assert L.cf_bias_response(1, 1, 0, 4, 0, 2.0, 1.0, 0.0, 1, 1, 1, 1, None) == INVALID
+    assert L.cf_bias_response(1, None, 8, 4, 0, 2.0, 1.0, 0.0, 1, 1, 1, 1, None) == INVALID
+    assert L.cf_bias_response(1, 1, 8, 4, 2, 2.0, 1.0, 0.0, 1, 1, 1, 1, None) == INVALID
     assert L.cf_conv_mfma(1, 1, 1, 1, None, None, 1, 1, 64, None, None, 0, 0, None, None, None, None,
                           None, None, None, 1, None,
                           0, 0.7, 4, 2, 64, 64, 64, 8, 8, 8, 8, 3, 3, 1, 1, 2, 0, 0, 0,

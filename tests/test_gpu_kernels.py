@@ -306,6 +306,58 @@ def test_pooled_epilogue_all_zero_input(cuda):
     assert torch.equal(s.cpu(), s_ref.cpu()) and torch.equal(v.cpu(), v_ref.cpu())
 
 
+@pytest.mark.parametrize("bias", ["quiet", "fires"])
+def test_pooled_static_zero_elision(cuda, bias):
+    """The pooled epilogue on an all-zero input (a fused layer's silent
+    output): with a silent pooled bias response (cf_bias_response, pool = 1)
+    the copy is left unwritten (descriptor: all zero) and the state kept
+    per channel; with a channel that fires on its bias the launch writes.
+    Outputs, states, the count-block verdict and a next conv reading the
+    output through its descriptor equal the always-writing path's."""
+    from catfuse_amd import runtime, snn
+    T, B, C, H = 4, 2, 64, 16
+    lif = snn.LIFNode(tau=2.0, v_threshold=0.5, v_reset=0.0)
+
+    def run(elide):
+        runtime.COPY_ELISION = elide
+        try:
+            conv0, bn0, _ = _layer(C, C, 3, 1, 1, seed=51)
+            conv1, bn1, _ = _layer(C, C, 3, 1, 1, seed=52)
+            conv2, bn2, _ = _layer(C, C, 3, 1, 1, seed=53)
+            with torch.no_grad():
+                bn0.bias.fill_(-8.0)          # silences every output
+                bn1.bias.fill_(-0.2)
+                if bias == "fires":
+                    bn1.bias[7] = 4.0         # channel 7 fires on its bias alone
+            r0, r1, r2 = (_runner(c, b, lif, cuda) for c, b in ((conv0, bn0), (conv1, bn1),
+                                                                  (conv2, bn2)))
+            x = (torch.rand(T, B, C, H, H, generator=_gen(54)) < 0.3).float().to(cuda)
+            z, _ = r0.run_mfma(x)                              # all zero, counted
+            s, v = r1.run_mfma(z, epilogue=runtime.EPI_POOL)   # StaticZero, pooled
+            d = runtime.desc_of(s)
+            d = None if d is None else d.clone()
+            nz = int(runtime.count_of(s)[1].item())
+            s2, v2 = r2.run_mfma(s)                            # reads s through d
+            res = (s.clone(), v.clone(), s2.clone(), v2.clone(), nz, d)
+            torch.cuda.synchronize()
+            return res
+        finally:
+            runtime.COPY_ELISION = True
+
+    se, ve, s2e, v2e, nze, de = run(True)
+    sw, vw, s2w, v2w, nzw, dw = run(False)
+    assert dw is None
+    for a, b, n in ((se, sw, "s"), (ve, vw, "v"), (s2e, s2w, "s2"), (v2e, v2w, "v2")):
+        assert torch.equal(a, b), n
+    assert (nze != 0) == (nzw != 0) == bool(sw.any())
+    if bias == "quiet":
+        assert not bool(sw.any())
+        assert de is not None and int(de[0].item() & 0xffffffff) == 1    # all zero
+        assert int(de[0].item() >> 32) == 1                               # per-channel state
+    else:
+        assert bool(sw.any()) and de is None    # written; no descriptor attached
+
+
 OUTPUT_COUNT_CASES = [
     # name, Cin, Cmid, Cout, k1, k2, s2, p2, H, producer SparseFlow tile width
     ("halo", 64, 64, 64, 3, 3, 1, 1, 16, 0),
