@@ -375,20 +375,27 @@ __global__ __launch_bounds__(256) void conv_direct_avgpool_kernel(DirectAvgArgs 
 #pragma unroll
         for (int j = 0; j < COB; ++j) acc[q][j] = 0.0f;
       for (int ci = 0; ci < a.Cin; ++ci) {
+        // the channel's patch and all nine taps' weights requested together,
+        // before the first product (one wait instead of one per tap)
         float pt[4][4];
+        float4 wr[9][COB / 4];
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
           for (int c = 0; c < 4; ++c) pt[r][c] = xs[ci][2 * py + r][2 * px + c];
 #pragma unroll
+        for (int k = 0; k < 9; ++k)
+#pragma unroll
+          for (int j = 0; j < COB / 4; ++j)
+            wr[k][j] = reinterpret_cast<const float4*>(wsm[ci * 9 + k])[j];
+#pragma unroll
         for (int kh = 0; kh < 3; ++kh) {
 #pragma unroll
           for (int kw = 0; kw < 3; ++kw) {
-            const float4* wk = reinterpret_cast<const float4*>(wsm[(ci * 3 + kh) * 3 + kw]);
             float wv[COB];
 #pragma unroll
             for (int j = 0; j < COB; j += 4) {
-              const float4 w4 = wk[j / 4];
+              const float4 w4 = wr[kh * 3 + kw][j / 4];
               wv[j] = w4.x;
               wv[j + 1] = w4.y;
               wv[j + 2] = w4.z;
