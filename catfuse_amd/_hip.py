@@ -61,9 +61,9 @@ _SIGNATURES = {
                           _P, _P, _P, _P, _P, _P, _I, _P, _P, c_int, _I, _I, _I,
                           c_double, c_double, c_double, c_int, c_int, _P],
     "cf_pack_stem_weights": [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P],
-    "cf_conv_stem_lif_maxpool": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I,
-                                 _I, _I, _I, _I, _I, _I, _I, _I, c_double, c_double, c_double,
-                                 c_int, c_int, _P],
+    "cf_conv_stem_lif_maxpool": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I,
+                                 _I, _I, _I, _I, _I, _I, _I, _I, _I, c_double, c_double,
+                                 c_double, c_int, c_int, _P],
     "cf_conv_direct_lif_maxpool": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I,
                                    _I, _I, c_double, c_double, c_double, c_int, c_int, _P],
     "cf_conv_direct_avgpool_lif": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I,

@@ -1,7 +1,9 @@
-// Fused network stem: Conv(KH x KW, stride 2) -> BN -> LIF -> MaxPool(3, 2, 1)
-// on the matrix cores, for an analog image that is repeated over T (direct
-// encoding: the convolution is evaluated once per image and its z feeds all
-// T LIF steps, which is exact because z is the same at every step).
+// Fused network stem: Conv(KH x KW, stride 2 or 1) -> BN -> LIF ->
+// MaxPool(3, 2, 1) on the matrix cores, for an analog image that is repeated
+// over T (direct encoding: the convolution is evaluated once per image and
+// its z feeds all T LIF steps, which is exact because z is the same at every
+// step).  Stride 2: the SEW/Spiking-ResNet 7x7 stem; stride 1: the first
+// stage of a Spikformer patch splitter (3x3 conv, then the pool).
 //
 // Replaces, for the SEW/Spiking-ResNet stem, the reference's DenseKeep
 // conv1 -> bn1 -> sn1 (catfuse/implementations/dense_keep.py:97-155 through
@@ -22,7 +24,10 @@
 // runs the LIF over T for each, keeps the spike train of each conv output as
 // a T-bit word in LDS, ORs the words over each 3 x 3 window and writes the
 // pooled spikes (fp32 NCHW and/or the fp16 NHWC copy the next fused conv
-// reads).  v_out holds the final membrane of the conv outputs each tile owns.
+// reads), and publishes the output's count block when asked.  v_out holds
+// the final membrane of the conv outputs each tile owns.  For the patch
+// splitter's first stage it replaces models/spikformer_github.py:181-254
+// (proj_conv, proj_bn, proj_lif, maxpool: four passes there).
 //
 // K layout: for filter row kh the 32 k-values are kw * 4 + c (kw < 8,
 // c < 4), so one 16-byte LDS read gives a lane two neighbouring input pixels
@@ -43,11 +48,12 @@ constexpr int PRH = 2 * PTH + 1;           // conv output rows under the tile (1
 constexpr int PRW = 2 * PTW + 1;           // conv output columns (15)
 constexpr int NPIX = PRH * PRW;            // 255
 constexpr int NTILE = (NPIX + 31) / 32;    // 8 MFMA column tiles
-constexpr int CS = 2;                      // conv stride
 constexpr int MAXKH = 7;
 constexpr int KROW = 32;                   // k-values per filter row
-constexpr int RH = (PRH - 1) * CS + MAXKH; // 39 staged input rows
-constexpr int RW = (PRW - 1) * CS + 8;     // 36 staged input columns
+// Staged input rows / columns under a tile for conv stride S (1 or 2):
+// 23 x 22 or 39 x 36.
+template <int S> constexpr int stem_rh() { return (PRH - 1) * S + MAXKH; }
+template <int S> constexpr int stem_rw() { return (PRW - 1) * S + 8; }
 constexpr int BMS = 64;                    // output channels per workgroup
 
 // Spike-word row stride (in words) per conv output: an odd number of dwords,
@@ -68,14 +74,17 @@ struct StemArgs {
   _Float16* out_nhwc;    // [T*B][Hp][Wp][cp_out] or null
   int cp_out;
   uint32_t* status;
+  unsigned long long* nz_out;   // count block of the pooled output, or null
   int T, B, Cin, Cout, Coutp, H, W, KH, pad, Hc, Wc, Hp, Wp, GHp, GWp;
   LifParams lif;
 };
 
-template <typename SW, int LM>
+template <typename SW, int LM, int S>
 __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel(StemArgs a) {
   constexpr int SLD = spike_ld<SW>();
+  constexpr int RH = stem_rh<S>(), RW = stem_rw<S>();
   __shared__ __attribute__((aligned(16))) _Float16 xs[2][RH * RW * 4];
+  __shared__ unsigned any_sh[4];
   __shared__ __attribute__((aligned(16))) SW spk[NPIX * SLD];
   __shared__ __attribute__((aligned(16))) SW pooled[PTH * PTW * SLD];
 
@@ -113,7 +122,7 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
   // All loads of the thread are issued before the first conversion.
   {
     constexpr int NP = (RH * RW + 255) / 256;  // positions per thread
-    const int ih0 = y0 * CS - a.pad, iw0 = x0 * CS - a.pad;
+    const int ih0 = y0 * S - a.pad, iw0 = x0 * S - a.pad;
     const size_t plane = (size_t)a.H * a.W;
     const float* xb = a.x + (size_t)b * a.Cin * plane;
     float xv[NP][4];
@@ -257,7 +266,7 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
   auto tile_base = [&](int nt) {
     const int n = nt * 32 + (lane & 31);
     const int nc = n < NPIX ? n : NPIX - 1;  // keeps dead lanes' reads inside the tile
-    return ((CS * (nc / PRW)) * RW + CS * (nc % PRW) + kof2) * 4;
+    return ((S * (nc / PRW)) * RW + S * (nc % PRW) + kof2) * 4;
   };
 
   // Column tiles nsel, nsel + 2, ... of this wave, two at a time so that two
@@ -333,6 +342,7 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
   __syncthreads();
 
   const int HpWp = a.Hp * a.Wp;
+  uint32_t anyw = 0u;   // OR of the spike words this thread writes out
   if (a.out) {
     // fp32 NCHW: consecutive threads write consecutive pooled pixels of a row.
     for (int i = tid; i < BMS * NPOOL; i += 256) {
@@ -341,6 +351,7 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
       const int co = cout0 + cl, oh = ph0 + py, ow = pw0 + px;
       if (co >= a.Cout || oh >= a.Hp || ow >= a.Wp) continue;
       const uint32_t wd = pooled[pp * SLD + cl];
+      anyw |= wd;
       float* dst = a.out + ((size_t)b * a.Cout + co) * HpWp + (size_t)oh * a.Wp + ow;
       const size_t tstep = (size_t)a.B * a.Cout * HpWp;
       for (int t = 0; t < a.T; ++t) dst[t * tstep] = (float)((wd >> t) & 1u);
@@ -355,7 +366,10 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
       if (oh >= a.Hp || ow >= a.Wp || co8 >= a.cp_out) continue;
       uint32_t wd[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) wd[j] = pooled[pp * SLD + 8 * c8 + j];
+      for (int j = 0; j < 8; ++j) {
+        wd[j] = pooled[pp * SLD + 8 * c8 + j];
+        anyw |= wd[j];   // channels >= Cout hold zero words
+      }
       for (int t = 0; t < a.T; ++t) {
         h8 hv;
 #pragma unroll
@@ -365,6 +379,11 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
                                co8) = hv;
       }
     }
+  }
+  // the output's count block: workgroups that wrote a spike
+  if (a.nz_out) {
+    const bool any = cf_wg_any(anyw != 0u, any_sh);
+    if (tid == 0) cf_count_publish(a.nz_out, any ? 1ull : 0ull, (unsigned)L, gridDim.x);
   }
 }
 
@@ -419,14 +438,21 @@ __global__ __launch_bounds__(256) void pack_stem_weights_kernel(
   }
 }
 
-template <typename SW>
+template <typename SW, int S>
 void launch_stem(const StemArgs& a, int lm, dim3 grid, hipStream_t st) {
   if (lm == LM_HARD0_DECAY_P2)
-    hipLaunchKernelGGL((conv_stem_kernel<SW, LM_HARD0_DECAY_P2>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((conv_stem_kernel<SW, LM_HARD0_DECAY_P2, S>), grid, dim3(256), 0, st, a);
   else if (lm == LM_HARD_DECAY_P2)
-    hipLaunchKernelGGL((conv_stem_kernel<SW, LM_HARD_DECAY_P2>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((conv_stem_kernel<SW, LM_HARD_DECAY_P2, S>), grid, dim3(256), 0, st, a);
   else
-    hipLaunchKernelGGL((conv_stem_kernel<SW, LM_GENERIC>), grid, dim3(256), 0, st, a);
+    hipLaunchKernelGGL((conv_stem_kernel<SW, LM_GENERIC, S>), grid, dim3(256), 0, st, a);
+}
+
+template <int S>
+void launch_stem_s(const StemArgs& a, int lm, dim3 grid, hipStream_t st) {
+  if (a.T <= 8) launch_stem<uint8_t, S>(a, lm, grid, st);
+  else if (a.T <= 16) launch_stem<uint16_t, S>(a, lm, grid, st);
+  else launch_stem<uint32_t, S>(a, lm, grid, st);
 }
 
 }  // namespace
@@ -447,6 +473,7 @@ CF_API int cf_pack_stem_weights(const float* w, int64_t Cout, int64_t Cin, int64
 CF_API int cf_conv_stem_lif_maxpool(const float* x, const void* w_stem, const float* alpha,
                                     const float* beta, const float* v_in, float* v_out,
                                     float* out, void* out_nhwc, int64_t cp_out, uint32_t* status,
+                                    unsigned long long* nz_out,
                                     int64_t T, int64_t B, int64_t Cin, int64_t Cout, int64_t Coutp,
                                     int64_t H, int64_t W, int64_t KH, int64_t KW, int64_t stride,
                                     int64_t pad, int64_t pool_k, int64_t pool_stride,
@@ -455,21 +482,23 @@ CF_API int cf_conv_stem_lif_maxpool(const float* x, const void* w_stem, const fl
   if (!x || !w_stem || !alpha || !beta || (!out && !out_nhwc)) return (int)hipErrorInvalidValue;
   if (T <= 0 || T > 32 || B <= 0 || Cin <= 0 || Cin > 4 || Cout <= 0 || Coutp < Cout ||
       Coutp % BMS != 0 || H <= 0 || W <= 0 || KH <= 0 || KH > MAXKH || KW <= 0 || KW > 8 ||
-      stride != CS || pad < 0)
+      (stride != 1 && stride != 2) || pad < 0)
     return (int)hipErrorInvalidValue;
   if (pool_k != 3 || pool_stride != 2 || pool_pad != 1) return (int)hipErrorInvalidValue;
   if (out_nhwc && (cp_out < Cout || cp_out > Coutp || cp_out % 8 != 0))
     return (int)hipErrorInvalidValue;
-  const int64_t Hc = (H + 2 * pad - KH) / CS + 1, Wc = (W + 2 * pad - KW) / CS + 1;
+  const int64_t Hc = (H + 2 * pad - KH) / stride + 1, Wc = (W + 2 * pad - KW) / stride + 1;
   if (Hc <= 0 || Wc <= 0) return (int)hipErrorInvalidValue;
   const int64_t Hp = (Hc + 2 - 3) / 2 + 1, Wp = (Wc + 2 - 3) / 2 + 1;
   const int64_t GHp = (Hp + PTH - 1) / PTH, GWp = (Wp + PTW - 1) / PTW;
   if (B * GHp * GWp > INT32_MAX || T * B * Cout * Hp * Wp > ((int64_t)1 << 40))
     return (int)hipErrorInvalidValue;
+  if (nz_out && B * GHp * GWp * (Coutp / BMS) >= (int64_t)CF_MAX_COUNT_WG)
+    return (int)hipErrorInvalidValue;
   StemArgs a;
   a.x = x; a.w = (const _Float16*)w_stem; a.alpha = alpha; a.beta = beta;
   a.v_in = v_in; a.v_out = v_out; a.out = out; a.out_nhwc = (_Float16*)out_nhwc;
-  a.cp_out = (int)cp_out; a.status = status;
+  a.cp_out = (int)cp_out; a.status = status; a.nz_out = nz_out;
   a.T = (int)T; a.B = (int)B; a.Cin = (int)Cin; a.Cout = (int)Cout; a.Coutp = (int)Coutp;
   a.H = (int)H; a.W = (int)W; a.KH = (int)KH; a.pad = (int)pad;
   a.Hc = (int)Hc; a.Wc = (int)Wc; a.Hp = (int)Hp; a.Wp = (int)Wp;
@@ -478,8 +507,7 @@ CF_API int cf_conv_stem_lif_maxpool(const float* x, const void* w_stem, const fl
   dim3 grid((unsigned)(B * GHp * GWp * (Coutp / BMS)));
   hipStream_t st = (hipStream_t)stream;
   const int lm = cf_lif_mode(a.lif);
-  if (T <= 8) launch_stem<uint8_t>(a, lm, grid, st);
-  else if (T <= 16) launch_stem<uint16_t>(a, lm, grid, st);
-  else launch_stem<uint32_t>(a, lm, grid, st);
+  if (stride == 2) launch_stem_s<2>(a, lm, grid, st);
+  else launch_stem_s<1>(a, lm, grid, st);
   return (int)hipGetLastError();
 }

@@ -1259,6 +1259,7 @@ class ConvLIFRunner:
         Ho, Wo = self.out_hw(H, W)
         Hp, Wp = (Ho - 1) // 2 + 1, (Wo - 1) // 2 + 1
         if v_in is not None:
+            v_in = v_in.contiguous()   # (a state the stem kernel left is channels-last)
             require_gpu_tensor(v_in, "v_in")
             if v_in.numel() != B * self.Cout * Ho * Wo:
                 raise ValueError("v_in has the wrong size")
@@ -1339,10 +1340,10 @@ class ConvLIFRunner:
     def stem_supported(self, x: torch.Tensor, pool) -> bool:
         """cf_conv_stem_lif_maxpool covers a direct-encoded image (stride-0
         time axis, or T = 1), at most 4 input channels, filters up to 7 x 8, conv
-        stride 2, T <= 32 and MaxPool2d(3, 2, 1)."""
+        stride 2 or 1, T <= 32 and MaxPool2d(3, 2, 1)."""
         return (x.dim() == 5 and (x.stride(0) == 0 or x.shape[0] == 1) and x[0].is_contiguous()
                 and x.dtype == torch.float32 and self.Cin <= 4 and self.KH <= 7
-                and self.KW <= 8 and self.stride == 2 and 1 <= x.shape[0] <= 32
+                and self.KW <= 8 and self.stride in (1, 2) and 1 <= x.shape[0] <= 32
                 and tuple(int(p) for p in pool) == (3, 2, 1))
 
     def _ensure_stem_packed(self, device):
@@ -1367,17 +1368,20 @@ class ConvLIFRunner:
               "cf_pack_stem_weights")
         self._stem_key = key
 
-    def run_stem_pool(self, x: torch.Tensor, v_in=None, *, want_v_out=True, emit_nhwc=True):
+    def run_stem_pool(self, x: torch.Tensor, v_in=None, *, want_v_out=True, emit_nhwc=True,
+                      nz_out=None, gen_cell=None):
         """x [T, B, Cin, H, W] with a stride-0 time axis.  Returns the pooled
         spikes [T, B, Cout, Hp, Wp] (carrying the fp16 NHWC copy when
-        emit_nhwc) and the conv-resolution membrane [B, Cout, Hc, Wc]
-        (channels_last memory format)."""
+        emit_nhwc, and with nz_out and gen_cell its count block) and the
+        conv-resolution membrane [B, Cout, Hc, Wc] (channels_last memory
+        format)."""
         if not self.stem_supported(x, (3, 2, 1)):
             raise ValueError("input/layer not covered by the fused stem kernel")
         T, B, C, H, W = x.shape
         dev = x.device
         require_gpu_tensor(x[0], "x")
         self._ensure_stem_packed(dev)
+        _require_block(nz_out)
         Hc, Wc = self.out_hw(H, W)
         Hp, Wp = (Hc - 1) // 2 + 1, (Wc - 1) // 2 + 1
         # the membrane is kept channels-last (the kernel's state layout)
@@ -1400,11 +1404,14 @@ class ConvLIFRunner:
         ev = _t0()
         rc = _hip.lib().cf_conv_stem_lif_maxpool(
             ptr(x[0]), ptr(self.w_stem), ptr(self.alpha_stem), ptr(self.beta_stem), ptr(v_in),
-            ptr(v_out), out_ptr, ptr(nhwc), cp_out, ptr(status_word(dev)), T, B, C, self.Cout,
-            self.Coutp, H, W, self.KH, self.KW, self.stride, self.padding, 3, 2, 1, *self.lif,
-            _hip.stream(dev))
+            ptr(v_out), out_ptr, ptr(nhwc), cp_out, ptr(status_word(dev)), ptr(nz_out), T, B, C,
+            self.Cout, self.Coutp, H, W, self.KH, self.KW, self.stride, self.padding, 3, 2, 1,
+            *self.lif, _hip.stream(dev))
         check(rc, "cf_conv_stem_lif_maxpool")
         _t1("conv_stem", ev, flops=2 * B * Hc * Wc * self.Cout * C * self.KH * self.KW)
+        if nz_out is not None and gen_cell is not None:
+            gen_cell[0] += 1
+            attach_count(out, nz_out, gen_cell)
         return out, v_out
 
 

@@ -354,6 +354,12 @@ class CTFSpikformerSPS(CTFPattern):
         return r.direct_pool_supported(x, self._pool_geometry(pool))
 
     def _run_direct_pool(self, i, stage, x):
+        """The analog first stage in one launch, fp32 on the VALU
+        (cf_conv_direct_lif_maxpool).  (cf_conv_stem_lif_maxpool also takes
+        this stride-1 3x3 stage on the matrix cores, but measured slower on
+        Spikformer-8-384's 224 x 224 x 48 stage: 315 against 278 us per
+        step, its LIF over 64 padded channels and recomputed border outputs
+        outweighing the cheaper conv.)"""
         stage._impl.check_input(x, stage.spec)
         r = stage._impl.runner(stage.spec, stage._ensure_params(), x.device)
         B = x.shape[1]

@@ -470,8 +470,8 @@ int cf_pack_stem_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
                          const float* bias, void* w_stem, float* alpha, float* beta,
                          void* stream);
 
-/* Fused stem Conv(stride 2) -> BN -> LIF -> MaxPool2d(3, 2, 1) on the matrix
- * cores for a direct-encoded image x [B][Cin][H][W] (the same frame at all T
+/* Fused stem Conv(stride 2 or 1) -> BN -> LIF -> MaxPool2d(3, 2, 1) on the
+ * matrix cores for a direct-encoded image x [B][Cin][H][W] (the same frame at all T
  * <= 32 steps: the conv runs once, its z feeds every LIF step).  The image
  * is split into fp16 hi/lo limbs; products wh*xh + wl*xh + wh*xl accumulate
  * in fp32.  Outputs the pooled spikes out [T][B][Cout][Hp][Wp] and/or their
@@ -479,12 +479,16 @@ int cf_pack_stem_weights(const float* w, int64_t Cout, int64_t Cin, int64_t KH, 
  * conv-resolution membrane channels-last, [B][Hc][Wc][Cout] (a conv output's
  * channels contiguous: 16-byte state accesses; torch's channels_last format
  * of a [B, Cout, Hc, Wc] tensor).  status |= 2 if |x| > 65504 or not finite.
- * Replaces catfuse/implementations/dense_keep.py:97-155 (conv1/bn1/sn1 via
- * catfuse/patterns.py:237-387) plus the unfused SpikingJelly MaxPool2d that
- * follows it in the ResNet stem. */
+ * nz_out (nullable): the pooled output's count block (see the count-block
+ * convention above).  Replaces catfuse/implementations/dense_keep.py:97-155
+ * (conv1/bn1/sn1 via catfuse/patterns.py:237-387) plus the unfused
+ * SpikingJelly MaxPool2d that follows it in the ResNet stem (stride 2), and
+ * the first stage of the Spikformer patch splitter,
+ * models/spikformer_github.py:181-254 (stride 1). */
 int cf_conv_stem_lif_maxpool(const float* x, const void* w_stem, const float* alpha,
                              const float* beta, const float* v_in, float* v_out, float* out,
-                             void* out_nhwc, int64_t cp_out, uint32_t* status, int64_t T,
+                             void* out_nhwc, int64_t cp_out, uint32_t* status,
+                             unsigned long long* nz_out, int64_t T,
                              int64_t B, int64_t Cin, int64_t Cout, int64_t Coutp, int64_t H,
                              int64_t W, int64_t KH, int64_t KW, int64_t stride, int64_t pad,
                              int64_t pool_k, int64_t pool_stride, int64_t pool_pad, double tau,

@@ -171,6 +171,17 @@ def test_token_and_pool_entry_points_validate_arguments():
     assert direct_pool(pad=3) == INVALID            # padding beyond 2
     assert direct_pool(H=1, pad=0) == INVALID       # empty conv output
 
+    def stem(Cin=3, KH=7, KW=7, stride=2, pad=3, T=4, pool=(3, 2, 1), cp_out=64):
+        return L.cf_conv_stem_lif_maxpool(1, 1, 1, 1, None, None, None, 1, cp_out, None, None,
+                                          T, 2, Cin, 64, 64, 64, 64, KH, KW, stride, pad,
+                                          *pool, 2.0, 1.0, 0.0, 1, 1, None)
+    assert stem(stride=3) == INVALID                # conv stride 1 or 2 only
+    assert stem(T=33) == INVALID                    # spike trains up to 32 steps
+    assert stem(Cin=5) == INVALID                   # at most 4 input channels
+    assert stem(KH=8) == INVALID                    # filter rows up to 7
+    assert stem(pool=(2, 2, 0)) == INVALID          # MaxPool2d(3, 2, 1) only
+    assert stem(cp_out=60) == INVALID               # copy pitch a multiple of 8
+
     def direct_avg(Cin=3, Cout=64, cp_out=64, pad=1, H=32, W=32):
         return L.cf_conv_direct_avgpool_lif(1, 1, 1, 1, None, None, 1, cp_out, None, 4, 2, Cin,
                                             Cout, H, W, pad, 0, 2.0, 1.0, 0.0, 1, 1, None)

@@ -910,15 +910,30 @@ STEM_CASES = [
 ]
 
 
-@pytest.mark.parametrize("case", STEM_CASES, ids=[c[0] for c in STEM_CASES])
+# the patch splitter's first stage: Conv 3x3/1 (name, T, B, H, W, Cout, lif,
+# continue_state, padding)
+STEM_S1_CASES = [
+    ("sps0", 4, 2, 32, 32, 48, None, False, 1),
+    ("sps0_odd", 3, 2, 29, 23, 32, None, True, 1),
+    ("sps0_t12", 12, 1, 24, 24, 64, dict(tau=4.0, v_threshold=0.8, v_reset=0.0,
+                                         decay_input=True), False, 2),
+    ("sps0_soft", 5, 2, 20, 18, 16, dict(tau=1.7, v_threshold=0.6, v_reset=None,
+                                         decay_input=False), True, 0),
+]
+
+
+@pytest.mark.parametrize("case", STEM_CASES + STEM_S1_CASES,
+                         ids=[c[0] for c in STEM_CASES + STEM_S1_CASES])
 def test_conv_stem_lif_maxpool_parity(cuda, case):
-    """Fused stem (Conv 7x7/2 -> BN -> LIF -> MaxPool 3/2/1, direct encoding)
-    against the oracle's conv (fp64) -> BN -> LIF, max-pooled on the CPU;
-    the fp16 NHWC copy equals the fp32 output; channels past Cout are zero."""
+    """Fused stem (Conv 7x7/2 or 3x3/1 -> BN -> LIF -> MaxPool 3/2/1, direct
+    encoding) against the oracle's conv (fp64) -> BN -> LIF, max-pooled on
+    the CPU; the fp16 NHWC copy equals the fp32 output; channels past Cout
+    are zero; the count block says whether any pooled spike fired."""
     from catfuse_amd import runtime, snn
-    name, T, B, H, W, Cout, lifp, cont = case
+    name, T, B, H, W, Cout, lifp, cont = case[:8]
+    k, s_, p_ = (3, 1, case[8]) if len(case) > 8 else (7, 2, 3)
     lif = snn.LIFNode(**lifp) if lifp else None
-    conv, bn, lif = _layer(3, Cout, 7, 2, 3, seed=61, lif=lif)
+    conv, bn, lif = _layer(3, Cout, k, s_, p_, seed=61, lif=lif)
     img = torch.randn(B, 3, H, W, generator=_gen(62))
     r = _runner(conv, bn, lif, cuda)
     x = img.to(cuda).unsqueeze(0).expand(T, B, 3, H, W)
@@ -928,9 +943,12 @@ def test_conv_stem_lif_maxpool_parity(cuda, case):
         _, v_in = r.run_stem_pool(x)
     v_in_ref = None if v_in is None else v_in.cpu()
     runtime.clear_status(cuda)
-    out, v = r.run_stem_pool(x, v_in)
+    blk = runtime.count_block(cuda)
+    out, v = r.run_stem_pool(x, v_in, nz_out=blk, gen_cell=[0])
     torch.cuda.synchronize()
     assert runtime.read_status(cuda) == 0
+    assert runtime.count_of(out) is blk
+    assert (int(blk[1].item()) == 0) == (not bool(out.any())), name
     s_ref, v_ref, h_ref = oracle.conv_bn_lif(x.cpu().contiguous(), conv, bn, lif,
                                               v_in=v_in_ref)
     vth = lif.v_threshold
