@@ -66,6 +66,7 @@ _SIGNATURES = {
                                  c_double, c_int, c_int, _P],
     "cf_conv_direct_lif_maxpool": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I,
                                    _I, _I, c_double, c_double, c_double, c_int, c_int, _P],
+    "cf_linear_tokens": [_P, _P, _P, _P, _P, _I, _I, _I, _I, _P],
     "cf_conv_direct_avgpool_lif": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I, _I,
                                    _I, _I, c_double, c_double, c_double, c_int, c_int, _P],
     "cf_conv_sparse_noalloc": [_P, _I, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, c_int, _P,

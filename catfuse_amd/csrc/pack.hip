@@ -286,6 +286,54 @@ __global__ __launch_bounds__(256) void tokens_to_f32_kernel(
   }
 }
 
+// A plain Linear (no neuron) over a token-major fused output kept only as
+// its fp16 copy (a network's last classifier layer after a fused
+// Linear-LIF): out[m][o] = bias[o] + sum_k x[m][k] * w[o][k] in fp32, x read
+// through the copy's output descriptor (an all-zero copy gives the bias).
+// One workgroup per row: its 256 threads take every 256th k (coalesced
+// weight rows), LT_OB outputs a pass; the partial sums are reduced in a
+// fixed tree (lanes, then waves in order), so the result is deterministic.
+// Spike values are small integers; a zero skips its products (exact).
+constexpr int LT_OB = 16;
+__global__ __launch_bounds__(256) void linear_tokens_kernel(
+    const _Float16* __restrict__ xp, const CfOutDesc* __restrict__ desc,
+    const float* __restrict__ w, const float* __restrict__ bias, float* __restrict__ out,
+    int K, int cp, int O) {
+  __shared__ float red[4][LT_OB];
+  const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const _Float16* xs = cf_copy_source(desc, xp);
+  const _Float16* xr = xs != nullptr ? xs + (size_t)m * cp : nullptr;
+  for (int o0 = 0; o0 < O; o0 += LT_OB) {
+    float acc[LT_OB];
+#pragma unroll
+    for (int j = 0; j < LT_OB; ++j) acc[j] = 0.0f;
+    if (xr != nullptr) {
+      for (int k = tid; k < K; k += 256) {
+        const float xv = (float)xr[k];
+        if (xv != 0.0f) {
+#pragma unroll
+          for (int j = 0; j < LT_OB; ++j)
+            if (o0 + j < O) acc[j] = fmaf(xv, w[(size_t)(o0 + j) * K + k], acc[j]);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < LT_OB; ++j)
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) acc[j] += __shfl_xor(acc[j], off, 64);
+    if (lane == 0) {
+#pragma unroll
+      for (int j = 0; j < LT_OB; ++j) red[wave][j] = acc[j];
+    }
+    __syncthreads();
+    if (tid < LT_OB && o0 + tid < O) {
+      const float s = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+      out[(size_t)m * O + o0 + tid] = bias != nullptr ? bias[o0 + tid] + s : s;
+    }
+    __syncthreads();   // red is rewritten by the next pass
+  }
+}
+
 // Max pooling of an fp16 NHWC copy (the spikes a fused conv wrote):
 // out[n][oh][ow][c] = max over the k x k window (stride s, padding p; padded
 // positions ignored, as torch's max_pool2d) of xp[n][ih][iw][c].  The max of
@@ -466,6 +514,19 @@ CF_API int cf_tokens_to_f32(const void* xp, float* out, int64_t rows, int64_t C,
   const unsigned grid = (unsigned)((n + 255) / 256 < 4096 ? (n + 255) / 256 : 4096);
   hipLaunchKernelGGL(tokens_to_f32_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
                      (const _Float16*)xp, out, rows, (int)C, (int)cp);
+  return (int)hipGetLastError();
+}
+
+CF_API int cf_linear_tokens(const void* xp, const void* desc, const float* w, const float* bias,
+                            float* out, int64_t M, int64_t K, int64_t cp, int64_t O,
+                            void* stream) {
+  if (!xp || !w || !out || M < 0 || M > INT32_MAX || K <= 0 || cp < K || O <= 0 ||
+      O > 4096 || K * O > INT32_MAX || (int64_t)M * cp > ((int64_t)1 << 40))
+    return (int)hipErrorInvalidValue;
+  if (M == 0) return 0;
+  hipLaunchKernelGGL(linear_tokens_kernel, dim3((unsigned)M), dim3(256), 0, (hipStream_t)stream,
+                     (const _Float16*)xp, (const CfOutDesc*)desc, w, bias, out, (int)K, (int)cp,
+                     (int)O);
   return (int)hipGetLastError();
 }
 

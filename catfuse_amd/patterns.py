@@ -773,6 +773,41 @@ class FusedGlobalAvgPool(nn.Module):
         return cls(getattr(pool, "step_mode", "s"))
 
 
+class FusedLinear(nn.Module):
+    """A network's last Linear (no neuron) after a fused Linear-LIF: reads
+    the spikes from the fp16 copy the fused layer wrote (through its
+    descriptor, cf_linear_tokens) instead of their fp32 form.  No
+    counterpart in the reference (SpikingJelly's layer.Linear).  fp32
+    accumulation in a fixed order: equal to F.linear within fp32 rounding.
+    Inputs without a current copy go through F.linear (counted in
+    `fallback_calls`)."""
+
+    def __init__(self, in_features, out_features, bias=True):
+        super().__init__()
+        self.in_features, self.out_features = int(in_features), int(out_features)
+        self.weight = nn.Parameter(torch.empty(out_features, in_features))
+        self.bias = nn.Parameter(torch.zeros(out_features)) if bias else None
+        self.fallback_calls = 0
+
+    def forward(self, x):
+        if x.is_cuda and x.shape[-1] == self.in_features:
+            y = runtime.linear_tokens(x, self.weight.detach(),
+                                      None if self.bias is None else self.bias.detach())
+            if y is not None:
+                return y
+        self.fallback_calls += 1
+        return nn.functional.linear(x, self.weight, self.bias)
+
+    @classmethod
+    def from_sj_modules(cls, linear):
+        inst = cls(linear.in_features, linear.out_features, bias=linear.bias is not None)
+        with torch.no_grad():
+            inst.weight.copy_(linear.weight)
+            if linear.bias is not None:
+                inst.bias.copy_(linear.bias)
+        return inst.to(linear.weight.device)
+
+
 class FusedFlatten(nn.Module):
     """Flatten of a network head in multi-step mode ([T, B, C, H, W] ->
     [T, B, C * H * W], SpikingJelly's layer.Flatten with step_mode 'm').  A
@@ -1022,7 +1057,7 @@ __all__ = ["CTFPattern", "PartialFusionConvLIF", "PartialFusionConvBNLIF",
            "PartialFusionConvBNAddLIF", "PartialFusionConvBNAvgPoolLIF",
            "PartialFusionConvBNLIFMaxPool", "PartialFusionGroupedConvBNLIF", "FusedLinearLIF",
            "FusedAddLIF", "FusedAddBNLIF", "FusedAvgPoolLIF", "FusedGlobalAvgPool",
-           "FusedFlatten", "CTFSEWBasicBlock",
+           "FusedFlatten", "FusedLinear", "CTFSEWBasicBlock",
            "CTFSpikingBasicBlock", "CTFSEWBottleneck", "CTFSpikingBottleneck",
            "STFusionConvBNLIF", "PATTERN_REGISTRY", "fold_bn", "lif_params", "conv_geometry",
            "conv_unsupported_reason", "grouped_conv_supported", "is_lif_node"]

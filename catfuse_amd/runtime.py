@@ -636,6 +636,31 @@ def global_avgpool_nhwc(xp: torch.Tensor, C: int, out: Optional[torch.Tensor] = 
     return y
 
 
+def linear_tokens(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None
+                  ) -> Optional[torch.Tensor]:
+    """x @ weight.T + bias for a token-major fused output x [..., K] read from
+    its fp16 copy through its descriptor (cf_linear_tokens), fp32 [..., O];
+    None when x carries no current copy (the caller then runs F.linear)."""
+    K = x.shape[-1]
+    O = weight.shape[0]
+    if weight.dim() != 2 or weight.shape[1] != K or O > 4096:
+        return None
+    copy = token_shadow(x, pad32(K), resolve=False)
+    if copy is None:
+        return None
+    require_gpu_tensor(weight, "weight")
+    if bias is not None:
+        require_gpu_tensor(bias, "bias")
+    rows = copy.shape[0]
+    out = torch.empty(tuple(x.shape[:-1]) + (O,), dtype=torch.float32, device=x.device)
+    ev = _t0()
+    check(_hip.lib().cf_linear_tokens(ptr(copy), ptr(desc_of(x)), ptr(weight), ptr(bias),
+                                      ptr(out), rows, K, copy.shape[1], O,
+                                      _hip.stream(x.device)), "cf_linear_tokens")
+    _t1("linear_tokens_head", ev, nbytes=2 * rows * K + 4 * O * K + 4 * rows * O)
+    return out
+
+
 def maxpool_nhwc(x: torch.Tensor, kernel_size: int, stride: int, padding: int,
                  gen_cell: Optional[list] = None, nz_out: Optional[torch.Tensor] = None):
     """MaxPool2d of a fused layer's output x [T, B, C, H, W] read from its

@@ -30,7 +30,7 @@ from catfuse_amd.transformer import (CTFSpikformerBlock, CTFSpikformerSPS, is_sp
                                      is_spikformer_sps)
 from catfuse_amd.patterns import (CTFSEWBasicBlock, CTFSEWBottleneck, CTFSpikingBasicBlock,
                                   CTFSpikingBottleneck, FusedAvgPoolLIF, FusedFlatten,
-                                  FusedGlobalAvgPool, FusedLinearLIF,
+                                  FusedGlobalAvgPool, FusedLinear, FusedLinearLIF,
                                   PartialFusionConvBNAvgPoolLIF, PartialFusionConvBNLIF,
                                   PartialFusionConvBNLIFMaxPool, PartialFusionConvLIF,
                                   PartialFusionGroupedConvBNLIF, STFusionConvBNLIF, conv_geometry,
@@ -195,6 +195,11 @@ def _rewrite_sequential(seq: nn.Sequential):
             out.append(FusedAvgPoolLIF.from_sj_modules(ch[i], ch[i + 1]))
             result.replacements.append(("FusedAvgPoolLIF", (i, i + 1)))
             i += 2
+            continue
+        if _head_linear(ch, i, out):
+            out.append(FusedLinear.from_sj_modules(ch[i]))
+            result.replacements.append(("FusedLinear", (i,)))
+            i += 1
             continue
         out.append(ch[i])
         result.skipped_indices.append(i)
@@ -507,6 +512,12 @@ def substitute_sf(sj_model, T=16, verbose=False, force_sparse=False, fuse_sew_ad
                     i += 2
                     changed = True
                     continue
+                if _head_linear(ch, i, out):
+                    out.append(FusedLinear.from_sj_modules(ch[i]))
+                    _bump(stats, "FusedLinear")
+                    i += 1
+                    changed = True
+                    continue
                 out.append(ch[i])
                 i += 1
             if changed:
@@ -532,6 +543,15 @@ def substitute_sf(sj_model, T=16, verbose=False, force_sparse=False, fuse_sew_ad
     _record_unsupported_convs(model, stats)
     stats["coverage_pct"] = 100.0 * stats["fused_lif_nodes"] / max(stats["total_lif_nodes"], 1)
     return holder.root, stats
+
+
+def _head_linear(ch, i, out) -> bool:
+    """ch[i] is a plain Linear (no neuron after it) whose input is the
+    output of the fused Linear-LIF just rewritten (out[-1]): it can read that
+    layer's fp16 copy (FusedLinear)."""
+    return (_is_sj_linear(ch[i]) and not (i + 1 < len(ch) and _is_lif(ch[i + 1]))
+            and bool(out) and isinstance(out[-1], FusedLinearLIF)
+            and ch[i].out_features <= 4096)
 
 
 def _is_multistep_flatten(m) -> bool:

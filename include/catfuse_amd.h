@@ -181,6 +181,17 @@ int cf_spike_attention_lif(const void* q, const void* k, const void* v, int64_t 
                            double scale, double tau, double v_th, double v_reset, int hard_reset,
                            int decay_input, void* stream);
 
+/* A plain Linear (no neuron) over a token-major fused output kept as its
+ * fp16 copy xp [M][cp] (cp >= K; a fused Linear-LIF's output, read through
+ * its output descriptor desc, nullable): out [M][O] fp32 = x w^T + bias
+ * (w [O][K] fp32, bias [O] nullable; O <= 4096), accumulated in fp32 in a
+ * fixed order (deterministic; not torch's order, so equal to torch's
+ * F.linear within fp32 rounding).  For a network's last classifier layer
+ * after fused Linear-LIF layers, which otherwise needs the fp32 form of its
+ * input first.  No counterpart in the reference (nn.Linear there). */
+int cf_linear_tokens(const void* xp, const void* desc, const float* w, const float* bias,
+                     float* out, int64_t M, int64_t K, int64_t cp, int64_t O, void* stream);
+
 /* MaxPool2d(kernel_size, stride, padding) of an fp16 NHWC copy xp
  * [NB][H][W][cp] -> out [NB][Ho][Wo][cp] (padded positions ignored, as
  * torch's max_pool2d; 2*padding <= kernel_size so every window has an input);

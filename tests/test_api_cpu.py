@@ -200,6 +200,11 @@ def test_substitute_sf_vgg11():
     x = torch.arange(2 * 3 * 4 * 2 * 2, dtype=torch.float32).view(2, 3, 4, 2, 2)
     assert torch.equal(fused.flatten(x), torch.flatten(x, 2))   # not a fused output
     assert fused.flatten.fallback_calls == 1
+    # the last Linear reads the second Linear-LIF's copy
+    from catfuse_amd.patterns import FusedLinear
+    assert pm["FusedLinear"] == 1 and isinstance(fused.classifier[-1], FusedLinear)
+    y = torch.randn(2, 3, 4096)
+    assert torch.allclose(fused.classifier[-1](y), m.classifier[-1](y))   # fallback on CPU
 
 
 def test_crossover_inputs_and_decision():

@@ -182,6 +182,12 @@ def test_token_and_pool_entry_points_validate_arguments():
     assert stem(pool=(2, 2, 0)) == INVALID          # MaxPool2d(3, 2, 1) only
     assert stem(cp_out=60) == INVALID               # copy pitch a multiple of 8
 
+    # head linear over a token copy: pitch below K, no outputs, too many outputs
+    assert L.cf_linear_tokens(1, None, 1, None, 1, 4, 64, 32, 10, None) == INVALID
+    assert L.cf_linear_tokens(1, None, 1, None, 1, 4, 64, 64, 0, None) == INVALID
+    assert L.cf_linear_tokens(1, None, 1, None, 1, 4, 64, 64, 5000, None) == INVALID
+    assert L.cf_linear_tokens(None, None, 1, None, 1, 4, 64, 64, 10, None) == INVALID
+
     def direct_avg(Cin=3, Cout=64, cp_out=64, pad=1, H=32, W=32):
         return L.cf_conv_direct_avgpool_lif(1, 1, 1, 1, None, None, 1, cp_out, None, 4, 2, Cin,
                                             Cout, H, W, pad, 0, 2.0, 1.0, 0.0, 1, 1, None)

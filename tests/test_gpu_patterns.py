@@ -223,7 +223,7 @@ def test_vgg_head_reads_pool_copy(cuda):
     (no pack), and every output equals the same chain on materialised fp32
     tensors bit for bit."""
     from catfuse_amd import runtime, snn
-    from catfuse_amd.patterns import (FusedFlatten, FusedLinearLIF,
+    from catfuse_amd.patterns import (FusedFlatten, FusedLinear, FusedLinearLIF,
                                       PartialFusionConvBNAvgPoolLIF)
     T, B = 4, 64
     g = _gen(31)
@@ -252,6 +252,10 @@ def test_vgg_head_reads_pool_copy(cuda):
     y1 = f1(t)
     y2 = f2(y1)
     assert t.__dict__.get("_cf_pending"), "the flatten was materialised"
+    # the last Linear reads y2's copy (fp32 accumulation in its own order)
+    head = FusedLinear.from_sj_modules(snn.Linear(256, 10)).to(cuda)
+    logits = head(y2)
+    assert head.fallback_calls == 0 and y2.__dict__.get("_cf_pending")
     # the same chain on plain fp32 tensors
     for m in (f1, f2):
         m.reset()
@@ -259,6 +263,41 @@ def test_vgg_head_reads_pool_copy(cuda):
     r2 = f2(r1.clone())
     assert torch.equal(y1.cpu(), r1.cpu()) and torch.equal(y2.cpu(), r2.cpu())
     assert bool(p.clone().any()), "the test input should make the pool fire"
+    ref = F.linear(r2.clone().double(), head.weight.double(), head.bias.double()).float()
+    torch.testing.assert_close(logits, ref, rtol=1e-5, atol=1e-5)
+
+
+@pytest.mark.parametrize("elide", [True, False])
+def test_fused_linear_head_silent_input(cuda, elide):
+    """A silent fused Linear-LIF output (StaticZero, its copy elided or
+    written as zeros) gives the head's bias exactly, and a live one the fp64
+    reference within fp32 rounding."""
+    from catfuse_amd import runtime, snn
+    from catfuse_amd.patterns import FusedLinear, FusedLinearLIF
+    runtime.COPY_ELISION = elide
+    try:
+        T, B = 4, 64
+        lin = snn.Linear(512, 256)
+        with torch.no_grad():
+            lin.bias.fill_(-0.5)              # no channel fires on its bias
+        f = FusedLinearLIF.from_sj_modules(lin, snn.LIFNode()).to(cuda)
+        head = FusedLinear.from_sj_modules(snn.Linear(256, 100)).to(cuda)
+        x = torch.zeros(T, B, 512, device=cuda)
+        y = f(x)
+        out = head(y)
+        assert head.fallback_calls == 0
+        assert torch.equal(out, head.bias.detach().expand(T, B, 100))
+        assert (runtime.desc_of(y) is not None) == elide
+        xl = (torch.rand(T, B, 512, generator=_gen(81)) < 0.3).float().to(cuda)
+        with torch.no_grad():
+            f.bias.fill_(0.3)
+        f.reset()
+        y = f(xl)
+        out = head(y)
+        ref = F.linear(y.clone().double(), head.weight.double(), head.bias.double()).float()
+        torch.testing.assert_close(out, ref, rtol=1e-5, atol=1e-5)
+    finally:
+        runtime.COPY_ELISION = True
 
 
 def test_tail_patterns_bit_exact(cuda):
