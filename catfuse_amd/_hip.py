@@ -37,7 +37,7 @@ _SIGNATURES = {
     "cf_expand_state": [_P, _P, _P, _I, _I, _I, _P],
     "cf_pack_tokens": [_P, _I, _I, _I, _P, _P, _P, _P],
     "cf_tokens_to_f32": [_P, _P, _I, _I, _I, _P],
-    "cf_maxpool_nhwc": [_P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P],
+    "cf_maxpool_nhwc": [_P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _P, _P],
     "cf_spike_attention_lif": [_P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, c_int,
                                _I, _I, _I, _I,
                                _I, c_double, c_double, c_double, c_double, c_int, c_int, _P],

@@ -340,10 +340,28 @@ __global__ __launch_bounds__(256) void linear_tokens_kernel(
 // spike values is exact in fp16.  One 8-channel chunk of one output pixel
 // per thread; the nonzero count of the output is published (count block).
 __global__ __launch_bounds__(256) void maxpool_nhwc_kernel(
-    const _Float16* __restrict__ xp, _Float16* __restrict__ out, int64_t NB, int H, int W,
+    const _Float16* __restrict__ xp_own, const CfOutDesc* __restrict__ in_desc,
+    _Float16* __restrict__ out, CfOutDesc* __restrict__ out_desc, int64_t NB, int H, int W,
     int Ho, int Wo, int cp, int k, int s, int p, unsigned long long* __restrict__ nnz) {
   typedef _Float16 h8 __attribute__((ext_vector_type(8)));
   __shared__ unsigned any_sh[4];
+  // the input where its producer left it; an all-zero input pools to an
+  // all-zero output, which is then recorded in out_desc instead of written
+  const _Float16* const xp = cf_copy_source(in_desc, xp_own);
+  if (xp == nullptr && out_desc != nullptr) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
+      if (nnz) nnz[1] = 0ull;
+      out_desc->copy = CF_COPY_ZERO;
+      out_desc->vstate = 0u;
+      out_desc->alias = nullptr;
+    }
+    return;
+  }
+  if (out_desc != nullptr && blockIdx.x == 0 && threadIdx.x == 0) {
+    out_desc->copy = CF_COPY_WRITTEN;
+    out_desc->vstate = 0u;
+    out_desc->alias = nullptr;
+  }
   const int nc8 = cp / 8;
   const int64_t units = NB * Ho * Wo * nc8;
   // unit decode in 32-bit arithmetic (the host keeps units below 2^31):
@@ -364,7 +382,9 @@ __global__ __launch_bounds__(256) void maxpool_nhwc_kernel(
       for (int dx = 0; dx < k; ++dx) {
         const int iw = ow * s - p + dx;
         if (iw < 0 || iw >= W) continue;
-        const h8 v = *reinterpret_cast<const h8*>(xp + ((n * H + ih) * W + iw) * cp + c8 * 8);
+        const h8 v = xp != nullptr
+                         ? *reinterpret_cast<const h8*>(xp + ((n * H + ih) * W + iw) * cp + c8 * 8)
+                         : h8{};
         if (first) {
           m = v;
           first = false;
@@ -530,7 +550,8 @@ CF_API int cf_linear_tokens(const void* xp, const void* desc, const float* w, co
   return (int)hipGetLastError();
 }
 
-CF_API int cf_maxpool_nhwc(const void* xp, void* out, int64_t NB, int64_t H, int64_t W,
+CF_API int cf_maxpool_nhwc(const void* xp, const void* in_desc, void* out, void* out_desc,
+                           int64_t NB, int64_t H, int64_t W,
                            int64_t cp, int64_t kernel_size, int64_t stride, int64_t padding,
                            unsigned long long* nz_out, void* stream) {
   if (!xp || !out || NB < 0 || H <= 0 || W <= 0 || cp <= 0 || cp % 8 != 0 || kernel_size <= 0 ||
@@ -545,7 +566,8 @@ CF_API int cf_maxpool_nhwc(const void* xp, void* out, int64_t NB, int64_t H, int
   // about one unit a thread (more loads in flight than a grid-stride loop)
   const unsigned grid = (unsigned)((units + 255) / 256 < 65536 ? (units + 255) / 256 : 65536);
   hipLaunchKernelGGL(maxpool_nhwc_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
-                     (const _Float16*)xp, (_Float16*)out, NB, (int)H, (int)W, (int)Ho, (int)Wo,
+                     (const _Float16*)xp, (const CfOutDesc*)in_desc, (_Float16*)out,
+                     (CfOutDesc*)out_desc, NB, (int)H, (int)W, (int)Ho, (int)Wo,
                      (int)cp, (int)kernel_size, (int)stride, (int)padding, nz_out);
   return (int)hipGetLastError();
 }

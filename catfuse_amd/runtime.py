@@ -664,23 +664,30 @@ def linear_tokens(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Te
 def maxpool_nhwc(x: torch.Tensor, kernel_size: int, stride: int, padding: int,
                  gen_cell: Optional[list] = None, nz_out: Optional[torch.Tensor] = None):
     """MaxPool2d of a fused layer's output x [T, B, C, H, W] read from its
-    fp16 NHWC copy; returns a lazy output carrying the pooled copy (and, with
-    nz_out and gen_cell, its count block), or None when x has no copy."""
+    fp16 NHWC copy (through its descriptor when the producer kept one);
+    returns a lazy output carrying the pooled copy (and, with nz_out and
+    gen_cell, its count block), or None when x has no copy.  The pool of an
+    elided all-zero copy is itself recorded as all zero, not written."""
     T, B, C, H, W = x.shape
-    xp = shadow_of(x, (T * B, H, W, pad32(C)))
+    xp = shadow_of(x, (T * B, H, W, pad32(C)), resolve=False)
     if xp is None:
         return None
     _require_block(nz_out)
+    in_desc = desc_of(x)
     Ho = (H + 2 * padding - kernel_size) // stride + 1
     Wo = (W + 2 * padding - kernel_size) // stride + 1
     cp = xp.shape[-1]
     out = torch.empty((T * B, Ho, Wo, cp), dtype=torch.float16, device=x.device)
+    out_desc = new_out_desc(x.device) if (COPY_ELISION and in_desc is not None) else None
     ev = _t0()
-    check(_hip.lib().cf_maxpool_nhwc(ptr(xp), ptr(out), T * B, H, W, cp, kernel_size, stride,
-                                     padding, ptr(nz_out), _hip.stream(x.device)),
+    check(_hip.lib().cf_maxpool_nhwc(ptr(xp), ptr(in_desc), ptr(out), ptr(out_desc), T * B, H,
+                                     W, cp, kernel_size, stride, padding, ptr(nz_out),
+                                     _hip.stream(x.device)),
           "cf_maxpool_nhwc")
     _t1("maxpool_nhwc", ev, nbytes=2 * T * B * (H * W + Ho * Wo) * cp)
     y = lazy_output((T, B, C, Ho, Wo), out, x.device)
+    if out_desc is not None:
+        attach_desc(y, out_desc)   # all zero or written: it aliases nothing
     if nz_out is not None and gen_cell is not None:
         gen_cell[0] += 1
         attach_count(y, nz_out, gen_cell)

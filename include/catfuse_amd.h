@@ -196,12 +196,15 @@ int cf_linear_tokens(const void* xp, const void* desc, const float* w, const flo
  * [NB][H][W][cp] -> out [NB][Ho][Wo][cp] (padded positions ignored, as
  * torch's max_pool2d; 2*padding <= kernel_size so every window has an input);
  * nz_out (nullable) receives the output's count block.  Exact for spikes.
- * Replaces the MaxPool2d between fused Conv-BN-LIF stages of
- * models/spikformer_github.py:181-254 (SPS), which the reference runs in
- * torch on the fp32 spikes. */
-int cf_maxpool_nhwc(const void* xp, void* out, int64_t NB, int64_t H, int64_t W, int64_t cp,
-                    int64_t kernel_size, int64_t stride, int64_t padding,
-                    unsigned long long* nz_out, void* stream);
+ * in_desc (nullable): the input copy's output descriptor (read where its
+ * producer left the values); out_desc (nullable) receives the output's: an
+ * all-zero input (in_desc ZERO) with out_desc given writes no output, only
+ * the descriptor (all zero) and a zero count.  Replaces the MaxPool2d
+ * between fused Conv-BN-LIF stages of models/spikformer_github.py:181-254
+ * (SPS), which the reference runs in torch on the fp32 spikes. */
+int cf_maxpool_nhwc(const void* xp, const void* in_desc, void* out, void* out_desc, int64_t NB,
+                    int64_t H, int64_t W, int64_t cp, int64_t kernel_size, int64_t stride,
+                    int64_t padding, unsigned long long* nz_out, void* stream);
 
 /* route = ZERO if the count block's published count k (nnz[1]) is 0, SPARSE
  * if 1 - k/numel > sparse_threshold (in double), else DENSE.  Replaces the host decision at

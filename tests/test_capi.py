@@ -212,7 +212,7 @@ def test_token_and_pool_entry_points_validate_arguments():
                                     None) == INVALID    # zero-drive knowledge without a descriptor
 
     def pool(cp=64, k=3, s=2, p=1):
-        return L.cf_maxpool_nhwc(1, 1, 8, 16, 16, cp, k, s, p, None, None)
+        return L.cf_maxpool_nhwc(1, None, 1, None, 8, 16, 16, cp, k, s, p, None, None)
     assert pool(cp=12) == INVALID                   # 16-byte channel chunks
     assert pool(k=2, p=2) == INVALID                # padding beyond half the window
     assert pool(s=0) == INVALID

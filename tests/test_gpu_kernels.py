@@ -761,8 +761,10 @@ def _elision_chain(cuda, elide):
         for t in (z2, a3, f5):
             xp = runtime.shadow_of(t, (T * B, H, H, C), resolve=False)
             pools.append(runtime.global_avgpool_nhwc(xp, C, desc=runtime.desc_of(t)))
-        mp = runtime.maxpool_nhwc(a3, 3, 2, 1)
-        outs = [s0, z1, z2, a3, d4, f5, e6, pa, pb, pc, pd, mp] + pools
+        mp = runtime.maxpool_nhwc(a3, 3, 2, 1)     # through the alias
+        mz = runtime.maxpool_nhwc(z2, 3, 2, 1)     # of an all-zero copy: elided
+        states["mz"] = None if runtime.desc_of(mz) is None else runtime.desc_of(mz).clone()
+        outs = [s0, z1, z2, a3, d4, f5, e6, pa, pb, pc, pd, mp, mz] + pools
         vs = [v0, v1, v2, v3, v4, v5, v6, qa, qb, qc, qd]
         # (a runner called twice republishes its block: the later outputs')
         counts = [int(runtime.count_of(t)[1]) != 0 for t in (z1, z2, d4, f5, e6, pc, pd)]
@@ -784,7 +786,7 @@ def test_static_zero_output_elision_bitwise(cuda):
     outs_e, vs_e, counts_e, st, s0_ptr = _elision_chain(cuda, True)
     outs_w, vs_w, counts_w, st_w, _ = _elision_chain(cuda, False)
     assert all(v is None for v in st_w.values())
-    names = ["s0", "z1", "z2", "a3", "d4", "f5", "e6", "pa", "pb", "pc", "pd", "mp",
+    names = ["s0", "z1", "z2", "a3", "d4", "f5", "e6", "pa", "pb", "pc", "pd", "mp", "mz",
              "pool_z2", "pool_a3", "pool_f5"]
     for n, a, b in zip(names, outs_e, outs_w):
         assert torch.equal(a, b), n
@@ -799,8 +801,8 @@ def test_static_zero_output_elision_bitwise(cuda):
     assert st.pop("f5") is None
     copy = {k: int(v[0].item() & 0xffffffff) for k, v in st.items()}
     vstate = {k: int(v[0].item() >> 32) for k, v in st.items()}
-    assert copy == {"z2": 1, "a3": 2, "e6": 1, "pa": 1, "pb": 1}
-    assert vstate == {"z2": 1, "a3": 1, "e6": 1, "pa": 1, "pb": 1}
+    assert copy == {"z2": 1, "a3": 2, "e6": 1, "pa": 1, "pb": 1, "mz": 1}
+    assert vstate == {"z2": 1, "a3": 1, "e6": 1, "pa": 1, "pb": 1, "mz": 0}
     assert int(st["a3"][1].item()) == s0_ptr
 
 
