@@ -662,6 +662,29 @@ class _TailPattern(CTFPattern):
         return s
 
 
+class FusedLIF(_TailPattern):
+    """A multi-step LIF node that no fused pattern absorbed (e.g. the
+    pre-head LIF of a spiking transformer), as one streaming kernel:
+    cf_lif_multistep over x [T, ...] with v in registers across T
+    (catfuse/sparseflow/lif_seq_kernel.py:51-90 `lif_sequential`, the
+    kernel the reference's patterns call; bit-exact against the LIF oracle).
+    The state is [...] of one step, as SpikingJelly's node keeps it."""
+
+    policy_row = "LIF"
+
+    def __init__(self, tau=2.0, v_threshold=1.0, v_reset=0.0, decay_input=True):
+        super().__init__()
+        self._lif_setup(tau, v_threshold, v_reset, decay_input)
+        self.step_mode = "m"
+
+    def forward(self, x):
+        return self._lif(x.contiguous())
+
+    @classmethod
+    def from_sj_modules(cls, sj_lif):
+        return cls(**lif_params(sj_lif))
+
+
 class FusedAddLIF(_TailPattern):
     """a + x -> LIF (catfuse/kernels/add_lif.py:63-151)."""
 
@@ -1057,7 +1080,7 @@ __all__ = ["CTFPattern", "PartialFusionConvLIF", "PartialFusionConvBNLIF",
            "PartialFusionConvBNAddLIF", "PartialFusionConvBNAvgPoolLIF",
            "PartialFusionConvBNLIFMaxPool", "PartialFusionGroupedConvBNLIF", "FusedLinearLIF",
            "FusedAddLIF", "FusedAddBNLIF", "FusedAvgPoolLIF", "FusedGlobalAvgPool",
-           "FusedFlatten", "FusedLinear", "CTFSEWBasicBlock",
+           "FusedFlatten", "FusedLinear", "FusedLIF", "CTFSEWBasicBlock",
            "CTFSpikingBasicBlock", "CTFSEWBottleneck", "CTFSpikingBottleneck",
            "STFusionConvBNLIF", "PATTERN_REGISTRY", "fold_bn", "lif_params", "conv_geometry",
            "conv_unsupported_reason", "grouped_conv_supported", "is_lif_node"]

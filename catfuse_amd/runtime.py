@@ -262,6 +262,10 @@ class _LazyTensor(torch.Tensor):
         if _METADATA is None:
             _METADATA = _metadata_functions()
         kwargs = kwargs or {}
+        if func is torch.mean or func is torch.Tensor.mean:
+            y = _token_mean(args, kwargs)
+            if y is not None:
+                return y
         self_ok = func is torch.Tensor.contiguous and args and args[0].is_contiguous()
         if not self_ok and func not in _METADATA:
             for a in _tensors_in(args, kwargs):
@@ -269,6 +273,34 @@ class _LazyTensor(torch.Tensor):
                     a.cf_materialize()
         with torch._C.DisableTorchFunctionSubclass():
             return func(*args, **kwargs)
+
+
+def _token_mean(args, kwargs) -> Optional[torch.Tensor]:
+    """x.mean(dim=-2) of a token-major fused output x [..., N, C] (the token
+    average of a spiking transformer's head) from x's fp16 copy, read
+    through its descriptor, without the fp32 form: cf_global_avgpool_nhwc
+    over the N tokens of each row (an exact integer sum times float(1/N),
+    the value torch's mean computes).  None for any other call."""
+    if not args or len(args) > 2 or set(kwargs) - {"dim"}:
+        return None
+    x = args[0]
+    dim = args[1] if len(args) > 1 else kwargs.get("dim")
+    if not (isinstance(x, NHWCSpikes) and x.__dict__.get("_cf_pending", False)
+            and x.__dict__.get("_cf_tokens", False) and x.dim() >= 3):
+        return None
+    if isinstance(dim, (tuple, list)):
+        if len(dim) != 1:
+            return None
+        dim = dim[0]
+    if not isinstance(dim, int) or dim % x.dim() != x.dim() - 2:
+        return None
+    N, C = int(x.shape[-2]), int(x.shape[-1])
+    copy = token_shadow(x, pad32(C), resolve=False)
+    if copy is None or copy.shape[0] % N:
+        return None
+    y = global_avgpool_nhwc(copy.view(copy.shape[0] // N, N, 1, copy.shape[1]), C,
+                            desc=desc_of(x))
+    return y.view(*x.shape[:-2], C)
 
 
 class NHWCSpikes(_LazyTensor):

@@ -30,7 +30,7 @@ from catfuse_amd.transformer import (CTFSpikformerBlock, CTFSpikformerSPS, is_sp
                                      is_spikformer_sps)
 from catfuse_amd.patterns import (CTFSEWBasicBlock, CTFSEWBottleneck, CTFSpikingBasicBlock,
                                   CTFSpikingBottleneck, FusedAvgPoolLIF, FusedFlatten,
-                                  FusedGlobalAvgPool, FusedLinear, FusedLinearLIF,
+                                  FusedGlobalAvgPool, FusedLIF, FusedLinear, FusedLinearLIF,
                                   PartialFusionConvBNAvgPoolLIF, PartialFusionConvBNLIF,
                                   PartialFusionConvBNLIFMaxPool, PartialFusionConvLIF,
                                   PartialFusionGroupedConvBNLIF, STFusionConvBNLIF, conv_geometry,
@@ -527,9 +527,10 @@ def substitute_sf(sj_model, T=16, verbose=False, force_sparse=False, fuse_sew_ad
         _wrap_sew_blocks(model)
 
     # Phase 3: a global average pool in the head reads the last fused conv's
-    # fp16 NHWC copy, and a multi-step flatten passes a one-pixel fused
-    # output on as tokens over that copy (no counterpart in the reference,
-    # which leaves the head to SpikingJelly).
+    # fp16 NHWC copy, a multi-step flatten passes a one-pixel fused output on
+    # as tokens over that copy, and a multi-step LIF no pattern absorbed runs
+    # as the streaming LIF kernel (no counterpart in the reference, which
+    # leaves the head to SpikingJelly).
     if fuse_head:
         for pname, pmod in list(model.named_modules()):
             for name, ch in list(pmod.named_children()):
@@ -539,6 +540,14 @@ def substitute_sf(sj_model, T=16, verbose=False, force_sparse=False, fuse_sew_ad
                 elif _is_multistep_flatten(ch):
                     setattr(pmod, name, FusedFlatten.from_sj_modules(ch))
                     _bump(stats, "FusedFlatten")
+                elif (_is_lif(ch) and id(ch) not in done
+                      and getattr(ch, "step_mode", "s") == "m"):
+                    # a multi-step LIF no pattern absorbed: the streaming kernel
+                    fused = FusedLIF.from_sj_modules(ch)
+                    setattr(pmod, name, fused)
+                    full = f"{pname}.{name}" if pname else name
+                    record(full, fused, {"pattern": "FusedLIF", "shape": "standalone",
+                                         "backend": SpatialBackend.DENSE_KEEP, "K": T}, ch)
 
     _record_unsupported_convs(model, stats)
     stats["coverage_pct"] = 100.0 * stats["fused_lif_nodes"] / max(stats["total_lif_nodes"], 1)

@@ -321,15 +321,19 @@ def test_unsupported_conv_left_unfused(conv_kw, reason):
     conv = snn.Conv2d(8, 8, ks, **kw)
     m = _seq(conv, snn.BatchNorm2d(8), snn.LIFNode(),
              snn.Conv2d(8, 16, 3, 1, 1, bias=False), snn.BatchNorm2d(16), snn.LIFNode())
+    from catfuse_amd.patterns import FusedLIF
     from catfuse_amd.substitute import substitute
-    for fn in (lambda mm: catfuse_amd.optimize(mm, T=4), substitute):
+    # optimize runs the unfused conv's LIF as the standalone LIF kernel;
+    # the block-level substitute leaves it to SpikingJelly
+    for fn, nfused in ((lambda mm: catfuse_amd.optimize(mm, T=4), 2), (substitute, 1)):
         fused, stats = fn(m)
         assert type(fused[0]).__name__ == "Conv2d" and not isinstance(fused[0], CTFPattern)
         assert torch.equal(fused[0].weight, conv.weight)
-        assert stats["fused_lif_nodes"] == 1 and stats["total_lif_nodes"] == 2
+        assert stats["fused_lif_nodes"] == nfused and stats["total_lif_nodes"] == 2
         assert any(reason in s and s.startswith("0:") for s in stats["unsupported_structures"]), \
             stats["unsupported_structures"]
-        assert sum(isinstance(x, CTFPattern) for x in fused.modules()) == 1
+        assert sum(isinstance(x, CTFPattern) for x in fused.modules()) == nfused
+        assert isinstance(fused[2], FusedLIF) == (nfused == 2)
     with pytest.raises(ValueError):
         conv_geometry(conv)
     with pytest.raises(ValueError):
@@ -420,7 +424,9 @@ def test_spikformer_other_head_dims_fuse_with_gemm_core():
     blk = fused.blocks[0]
     assert isinstance(blk, CTFSpikformerBlock)
     assert blk.attn.head_dim == 64 and not blk.attn.kernel_covers(64)
-    assert stats["fused_lif_nodes"] == stats["total_lif_nodes"] - 1   # pre-head LIF
+    assert stats["fused_lif_nodes"] == stats["total_lif_nodes"]   # pre-head LIF: FusedLIF
+    from catfuse_amd.patterns import FusedLIF
+    assert isinstance(fused.pre_head_lif, FusedLIF) and stats["patterns_matched"]["FusedLIF"] == 1
     small = snn.spikformer_8_384(img_size=224)
     f2, _ = catfuse_amd.optimize(small.eval(), T=4)
     a = f2.blocks[0].attn

@@ -204,7 +204,7 @@ def _spikformer_parity(cuda, m, x, live):
     from catfuse_amd.transformer import FusedLinearBNLIF
     T = x.shape[0]
     fused, stats = catfuse_amd.optimize(m, T=T)
-    assert stats["fused_lif_nodes"] == stats["total_lif_nodes"] - 1   # pre_head_lif
+    assert stats["fused_lif_nodes"] == stats["total_lif_nodes"]   # pre_head_lif: FusedLIF
     recs = []
     origs = {}
     for bi, (fb, ob) in enumerate(zip(fused.blocks, m.blocks)):
@@ -479,6 +479,33 @@ def test_conv_direct_lif_maxpool_bitwise(cuda, case):
     y2, _ = r.run_direct_pool(x[:, :1], None if v_in is None else v_in[:1], nz_out=blk,
                               gen_cell=[0])
     assert torch.equal(y2.reshape(T, *ref.shape[1:]), ref.reshape(T, B, *ref.shape[1:])[:, 0])
+
+
+@pytest.mark.parametrize("B,N,C,silent", [(4, 196, 384, False), (2, 64, 96, False),
+                                          (3, 50, 40, False), (4, 196, 384, True)])
+def test_token_mean_reads_copy(cuda, B, N, C, silent):
+    """x.mean(dim=2) of a token layer's lazy output [T, B, N, C] is computed
+    from its fp16 copy (through its descriptor; an elided all-zero copy gives
+    zeros) without materialising x, bit-identical to torch's mean of the
+    fp32 values."""
+    from catfuse_amd import runtime
+    T, Cin = 4, 64
+    g = _gen(B * N + C)
+    w = torch.randn(C, Cin, 1, 1, generator=g) * 0.4
+    sh = torch.full((C,), -0.5) if silent else torch.randn(C, generator=g) * 0.5
+    r = runtime.ConvLIFRunner(w.to(cuda), torch.ones(C, device=cuda), sh.to(cuda), None, 1, 0,
+                              2.0, 1.0, 0.0, True)
+    x = (torch.rand(T, B, N, Cin, generator=g) < (0.0 if silent else 0.3)).float().to(cuda)
+    y, _ = r.run_tokens(x)
+    if silent:   # StaticZero with a silent bias response: the copy is elided
+        d = runtime.desc_of(y)
+        assert d is not None and int(d[0].item() & 0xffffffff) == 1
+    m = y.mean(dim=2)
+    m2 = y.mean(-2)
+    assert y.__dict__.get("_cf_pending"), "the mean materialised the tokens"
+    ref = y.clone().mean(dim=2)
+    assert m.shape == (T, B, C) and torch.equal(m, ref) and torch.equal(m2, ref)
+    assert bool(ref.any()) != silent
 
 
 def test_spike_attention_count_block(cuda):
