@@ -93,10 +93,14 @@ __host__ __device__ inline int cf_lif_mode(const LifParams& p) {
   return __builtin_bit_cast(uint32_t, p.v_reset) == 0u ? LM_HARD0_DECAY_P2 : LM_HARD_DECAY_P2;
 }
 
+// In the P2 forms the product d * inv_tau is exact (a power of two; unless
+// it falls below the normal range, where |v| would be below 2^-125 too), so
+// one fused multiply-add rounds exactly as the separate multiply and add.
 template <int LM>
 __device__ __forceinline__ float lif_charge_m(float v, float x, const LifParams& p) {
-  if constexpr (LM == LM_HARD0_DECAY_P2) return v + (x - v) * p.inv_tau;
-  else if constexpr (LM == LM_HARD_DECAY_P2) return v + (x - (v - p.v_reset)) * p.inv_tau;
+  if constexpr (LM == LM_HARD0_DECAY_P2) return __builtin_fmaf(x - v, p.inv_tau, v);
+  else if constexpr (LM == LM_HARD_DECAY_P2)
+    return __builtin_fmaf(x - (v - p.v_reset), p.inv_tau, v);
   else return lif_charge(v, x, p);
 }
 
