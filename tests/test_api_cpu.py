@@ -431,3 +431,15 @@ def test_spikformer_other_head_dims_fuse_with_gemm_core():
     f2, _ = catfuse_amd.optimize(small.eval(), T=4)
     a = f2.blocks[0].attn
     assert a.head_dim == 32 and a.kernel_covers(196) and not a.kernel_covers(3136)
+
+
+def test_lazy_head_helpers_decline_plain_tensors():
+    """The copy-reading head helpers take only pending fused outputs: a plain
+    tensor, a wrong axis or extra arguments go through torch (None)."""
+    from catfuse_amd import runtime
+    x = torch.randn(2, 3, 5, 4)
+    assert runtime._token_mean((x, 2), {}) is None
+    assert runtime._token_mean((x,), {"dim": 2, "keepdim": True}) is None
+    assert torch.equal(x.mean(dim=2), x.mean(2))
+    assert runtime.pixel_tokens(torch.randn(2, 3, 4, 1, 1)) is None
+    assert runtime.linear_tokens(torch.randn(2, 3, 8), torch.randn(4, 8)) is None
