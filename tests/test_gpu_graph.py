@@ -127,3 +127,45 @@ def test_graph_replays_keep_elided_outputs_and_states_current(cuda):
                 assert torch.equal(y, eager[i][0]), f"replay {rep}, input {i}: output"
                 for k, (a, b) in enumerate(zip(got, eager[i][1])):
                     assert torch.equal(a, b), f"replay {rep}, input {i}: state of layer {k}"
+
+
+@pytest.mark.parametrize("live", [False, True])
+def test_graph_replays_of_vgg(cuda, live):
+    """Spiking VGG-11-BN: pooled conv epilogues, the analog conv + avg pool,
+    the token-view Linear-LIFs, the lazy flatten and the head Linear over
+    the copy, with (live) and without (silent: elided outputs, per-channel
+    states) activity past the first layers; every replay equals the eager
+    forward with eager work between replays."""
+    import catfuse_amd
+    from catfuse_amd import graph, snn
+    from catfuse_amd.patterns import FusedFlatten, FusedLinear
+    T, B = 4, 64
+    g = torch.Generator().manual_seed(11)
+    m = snn.spiking_vgg11_bn(num_classes=10, v_threshold=0.1 if live else 1.0)
+    snn.functional.set_step_mode(m, "m")
+    snn.kaiming_init(m, g)
+    snn.randomize_bn(m, g)
+    fused, _ = catfuse_amd.optimize(m.eval(), device=cuda, T=T)
+    fused = fused.eval()
+    assert isinstance(fused.flatten, FusedFlatten) and isinstance(fused.classifier[-1], FusedLinear)
+    gen = torch.Generator(device=cuda).manual_seed(1)
+    imgs = [torch.randn(B, 3, 32, 32, device=cuda, generator=gen) for _ in range(3)]
+
+    def as_input(img):
+        return img.unsqueeze(0).expand(T, B, 3, 32, 32)
+
+    with torch.no_grad():
+        eager = []
+        for img in imgs:
+            snn.functional.reset_net(fused)
+            eager.append(fused(as_input(img)).clone())
+        graphed = graph.capture(fused, as_input(imgs[0]))
+        for rep in range(2):
+            for i, img in enumerate(imgs):
+                y = graphed(as_input(img)).clone()
+                torch.cuda.synchronize()
+                assert torch.equal(y, eager[i]), f"replay {rep}, input {i}"
+                snn.functional.reset_net(fused)
+                z = fused(as_input(imgs[(i + 1) % 3]))
+                assert torch.equal(z, eager[(i + 1) % 3])
+    assert fused.flatten.fallback_calls == 0 and fused.classifier[-1].fallback_calls == 0
