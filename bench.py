@@ -162,9 +162,12 @@ def time_forward(fused, x, img, steps, warmup, eager=False, label=False):
             if not torch.equal(graphed(img), y_ref):
                 raise SystemExit("graph replay differs from the eager forward")
             torch.cuda.synchronize()
+            # the batch is resident in the captured graph's input buffer (the
+            # check above copied it there): each timed step replays the whole
+            # forward on it, without re-copying the same 3xHxW images
             t0 = time.perf_counter()
             for _ in range(steps):
-                graphed(img)
+                graphed()
             torch.cuda.synchronize()
             t1 = time.perf_counter()
             ms, mode = (t1 - t0) * 1e3 / steps, "hip_graph"
@@ -594,7 +597,7 @@ def _base_result(args, res, stats, workload):
         "mode": res["mode"], "eager_ms_per_step": round(res["ms_eager"], 4),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "fp32 (conv: fp16 hi/lo split weights x fp16-exact spikes on MFMA, fp32 acc)",
-        "data": "synthetic (seeded N(0,1) images, random kaiming weights, config BN stats)",
+        "data": "synthetic (seeded N(0,1) images, resident in HBM, random kaiming weights, config BN stats)",
         "config": {"workload": workload, "T": args.T, "batch": args.batch,
                    "image": [3, args.image, args.image],
                    "encoding": "direct (input repeated over T)",
