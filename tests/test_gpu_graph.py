@@ -169,3 +169,43 @@ def test_graph_replays_of_vgg(cuda, live):
                 z = fused(as_input(imgs[(i + 1) % 3]))
                 assert torch.equal(z, eager[(i + 1) % 3])
     assert fused.flatten.fallback_calls == 0 and fused.classifier[-1].fallback_calls == 0
+
+
+@pytest.mark.parametrize("v_th", [1.0, 0.2])
+def test_graph_replays_of_spikformer(cuda, v_th):
+    """A small Spikformer (patch splitter, two blocks, the pre-head LIF as
+    FusedLIF, the token mean read from the last copy): every replay equals
+    the eager forward, with eager work between replays."""
+    import catfuse_amd
+    from catfuse_amd import graph, snn
+    from catfuse_amd.patterns import FusedLIF
+    T, B = 4, 2
+    g = torch.Generator().manual_seed(5)
+    net = snn.Spikformer(img_size=32, num_classes=10, embed_dim=64, num_heads=2, depth=2,
+                         pools=(0, 1), v_threshold=v_th)
+    snn.kaiming_init(net, g)
+    snn.randomize_bn(net, g)
+    fused, stats = catfuse_amd.optimize(net.eval(), device=cuda, T=T)
+    fused = fused.eval()
+    assert isinstance(fused.pre_head_lif, FusedLIF)
+    assert stats["fused_lif_nodes"] == stats["total_lif_nodes"]
+    gen = torch.Generator(device=cuda).manual_seed(2)
+    imgs = [torch.randn(B, 3, 32, 32, device=cuda, generator=gen) for _ in range(3)]
+
+    def as_input(img):
+        return img.unsqueeze(0).expand(T, B, 3, 32, 32)
+
+    with torch.no_grad():
+        eager = []
+        for img in imgs:
+            snn.functional.reset_net(fused)
+            eager.append(fused(as_input(img)).clone())
+        graphed = graph.capture(fused, as_input(imgs[0]))
+        for rep in range(2):
+            for i, img in enumerate(imgs):
+                y = graphed(as_input(img)).clone()
+                torch.cuda.synchronize()
+                assert torch.equal(y, eager[i]), f"replay {rep}, input {i}"
+                snn.functional.reset_net(fused)
+                z = fused(as_input(imgs[(i + 1) % 3]))
+                assert torch.equal(z, eager[(i + 1) % 3])
