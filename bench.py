@@ -18,9 +18,11 @@ Workloads (--workload):
 One step = one full forward of the fused network over the batch (all T
 steps, stem to logits) on synthetic inputs resident in HBM, after a
 functional.reset_net: by default a replay of the HIP graph that
-catfuse_amd.capture records for reset_net + forward (the batch is copied
-into the graph's input first, inside the timed step; the replay's output is
-checked against the eager forward's); --eager times the eager launches.
+catfuse_amd.capture records for reset_net + forward, on the batch resident
+in the graph's input buffer (copied there once, before timing, by the
+replay whose output is checked against the eager forward's; each timed step
+replays the whole forward on it, with no copy); --eager times the eager
+launches.
 Prints ONE JSON line:
   value        images/s = B / (seconds per step)
   roofline     the dominant kernel (conv_halo_kernel behind cf_conv_mfma, the

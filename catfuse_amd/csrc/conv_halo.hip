@@ -316,7 +316,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     }
   }
   const bool zlean = LEAN && EPI == EPI_LIF && route == CF_ROUTE_ZERO && a.v_in == nullptr &&
-                     (a.T + 2) * BM <= 2 * HB;
+                     (a.T + 2) * BM <= NBUF * HB;   // [T][BM] spike rows + BM floats
   const bool zvchan = zlean && a.out_desc != nullptr && (a.bias_info & CF_BIAS_VCHAN) != 0;
   uint32_t zcopy = CF_COPY_WRITTEN;
   const void* zalias = nullptr;

@@ -416,6 +416,11 @@ STATICZERO_CASES = [
     ("s1", 64, 64, 3, 1, 1, 12, 4, 0),
     ("s1_T6", 64, 64, 3, 1, 1, 12, 6, 0),
     ("s2", 64, 128, 3, 2, 1, 16, 4, 0),
+    # stride-2 3x3 tiles hold one halo buffer: the lean epilogue's T spike
+    # rows + final potentials fit it up to T = 582, longer runs take the
+    # per-element epilogue
+    ("s2_T580", 64, 64, 3, 2, 1, 16, 580, 0),
+    ("s2_T600", 64, 64, 3, 2, 1, 16, 600, 0),
     ("ds", 64, 128, 1, 2, 0, 16, 4, 0),
     ("tile8x16", 32, 64, 3, 1, 1, 56, 4, 16),
     ("c96", 64, 96, 3, 1, 1, 12, 4, 0),
