@@ -10,7 +10,11 @@ Workloads (--workload):
                    liveness check (>= 80% of the SEW blocks with spike rate
                    > 1e-4, :268-287), reported in its own keys;
   spikformer_8_384 config C4 (spiking transformer), its own metric line;
-  vgg11_bn         config C2: spiking VGG-11-BN, T=4, B=64, 3x32x32;
+  vgg11_bn         config C2: spiking VGG-11-BN, T=4, B=64, 3x32x32; plus
+                   its live companion at v_th = 0.1 (the reference's VGG
+                   setting, benchmarks/bench_vgg11_e2e.py:74-80) under that
+                   harness's liveness check (>= 80% of the fused conv and
+                   Linear-LIF layers with spike rate > 1e-4, :205-241);
   sf_crossover     the SparseFlow / dense crossover sweep of one fused
                    Conv3x3-BN-LIF layer (config C1 shapes) that sets the
                    MI355X routing threshold; prints a markdown table.
@@ -296,14 +300,24 @@ def traffic_from_profiles(name="conv_halo_sew_resnet18_traffic.json"):
         return None
 
 
-def liveness(fused, x):
-    """Spike rate of every SEW block's output (CTFSEWBasicBlock), as the
-    reference's harness checks it: (alive fraction, {block: rate})."""
+# modules whose outputs the reference's harnesses check for liveness:
+# SEW blocks (benchmarks/bench_sew_resnet18_e2e.py:268-287); every fused
+# conv and Linear-LIF (benchmarks/bench_vgg11_e2e.py:205-241)
+LIVENESS_MODULES = {
+    "sew_resnet18": ("CTFSEWBasicBlock",),
+    "vgg11_bn": ("PartialFusionConvBNLIF", "PartialFusionConvBNAvgPoolLIF", "FusedLinearLIF"),
+}
+
+
+def liveness(fused, x, workload="sew_resnet18"):
+    """Spike rate of every module the reference's harness checks (SEW blocks,
+    or VGG's fused layers): (alive fraction, {module: rate})."""
     import torch
     from catfuse_amd import snn
     rates, hs = {}, []
+    kinds = LIVENESS_MODULES[workload]
     for name, mod in fused.named_modules():
-        if type(mod).__name__ == "CTFSEWBasicBlock":
+        if type(mod).__name__ in kinds:
             hs.append(mod.register_forward_hook(
                 lambda m, a, o, name=name: rates.__setitem__(name, float(o.float().mean()))))
     with torch.no_grad():
@@ -343,36 +357,80 @@ TAIL_CASES = [
 ]
 
 
+# buffer sets a cold tail measurement rotates through: together above 1 GiB
+# and at least 4, so no launch finds its inputs in the 256 MB Infinity Cache
+# (every set is evicted by the others before it is reused)
+COLD_BYTES = 3 << 29
+COLD_MIN_SETS = 4
+
+
 def measure_tails(dev, reps=50):
     """Standalone LIF-family kernels at SEW-RN18 / C1 / VGG shapes: GB/s from
     the algorithmic bytes of a launch and the average duration of `reps`
-    back-to-back launches."""
+    launches captured back to back in one graph.  Cold (the row's main
+    figures, HBM): the launches rotate through buffer sets (inputs, states
+    and outputs) totalling more than 1 GiB.  Resident (`resident`): every
+    launch on one buffer set, which for the smaller shapes stays in the
+    Infinity Cache between launches."""
     import torch
-    from catfuse_amd import runtime
+    from catfuse_amd import _hip
+    from catfuse_amd.runtime import _lif_args, check, ptr
+    L = _hip.lib()
+    lif = _lif_args(2.0, 1.0, 0.0, True)
     out = []
     g = torch.Generator(device=dev).manual_seed(0)
     for name, shape, mode in TAIL_CASES:
         T, B, C, H, W = shape
         if mode is None:
-            x = torch.rand(shape, device=dev, generator=g)
             n_out = B * C * (H // 2) * (W // 2)
             nbytes = T * n_out * 20 + 4 * n_out
-            us = _time_launches(lambda: runtime.avgpool2x2_lif(x), reps, dev)
-            out.append(_tail_row("cf_avgpool2x2_lif", shape, nbytes, us))
-            del x
-            continue
-        z = torch.randn(shape, device=dev, generator=g)
-        z2 = torch.randn(shape, device=dev, generator=g) if mode in (2, 3, 4) else None
-        sc = torch.rand(C, device=dev, generator=g) + 0.5
-        sh = torch.randn(C, device=dev, generator=g) * 0.1
-        v0 = torch.zeros(B, C, H, W, device=dev)
-        N = B * C * H * W
-        nbytes = (8 * T + 8) * N + (4 * T * N if z2 is not None else 0)
-        us = _time_launches(lambda: runtime.lif_multistep(z, v0, mode=mode, z2=z2, scale=sc,
-                                                          shift=sh, channels=C, hw=H * W),
-                            reps, dev)
-        out.append(_tail_row(f"cf_lif_multistep/{name}", shape, nbytes, us))
-        del z, z2
+
+            def make():
+                return dict(x=torch.rand(shape, device=dev, generator=g),
+                            s=torch.empty((T, B, C, H // 2, W // 2), device=dev),
+                            v=torch.empty((B, C, H // 2, W // 2), device=dev))
+
+            def launch(b):
+                # (the stream current at the call: the capture stream inside
+                # the timed graph)
+                check(L.cf_avgpool2x2_lif(ptr(b["x"]), None, ptr(b["s"]), 0, ptr(b["v"]), T,
+                                          B * C, H, W, *lif, _hip.stream(dev)),
+                      "cf_avgpool2x2_lif")
+            kernel = "cf_avgpool2x2_lif"
+        else:
+            N = B * C * H * W
+            two = mode in (2, 3, 4)
+            nbytes = (8 * T + 8) * N + (4 * T * N if two else 0)
+            sc = torch.rand(C, device=dev, generator=g) + 0.5
+            sh = torch.randn(C, device=dev, generator=g) * 0.1
+
+            def make():
+                return dict(z=torch.randn(shape, device=dev, generator=g),
+                            z2=torch.randn(shape, device=dev, generator=g) if two else None,
+                            v0=torch.zeros(B, C, H, W, device=dev),
+                            s=torch.empty(shape, device=dev),
+                            v=torch.empty(B, C, H, W, device=dev))
+
+            def launch(b, mode=mode, N=N, sc=sc, sh=sh):
+                check(L.cf_lif_multistep(ptr(b["z"]), ptr(b["z2"]), ptr(sc), ptr(sh), mode,
+                                         ptr(b["v0"]), ptr(b["s"]), 0, ptr(b["v"]), T, N, C,
+                                         H * W, *lif, _hip.stream(dev)), "cf_lif_multistep")
+            kernel = f"cf_lif_multistep/{name}"
+        nsets = max(COLD_MIN_SETS, -(-COLD_BYTES // nbytes))
+        sets = [make() for _ in range(nsets)]
+        cnt = [0]
+
+        def rotate():
+            launch(sets[cnt[0] % nsets])
+            cnt[0] += 1
+        us_cold = _time_launches(rotate, max(reps, 2 * nsets), dev)
+        us_res = _time_launches(lambda: launch(sets[0]), reps, dev)
+        row = _tail_row(kernel, shape, nbytes, us_cold)
+        row["buffers"] = {"sets": nsets, "bytes_total": int(nsets * nbytes)}
+        res = _tail_row(kernel, shape, nbytes, us_res)
+        row["resident"] = {k: res[k] for k in ("us_per_launch", "GB/s", "frac")}
+        out.append(row)
+        del sets
     return out
 
 
@@ -497,19 +555,20 @@ def sew_result(args, dev):
     return result, model
 
 
-def live_result(args, dev):
-    """The headline network with v_th = 0.1 (every layer active): the dense
-    MFMA route at every layer's shape."""
-    res, stats, model, fused, x = run_network("sew_resnet18", args, dev,
+def live_result(args, dev, workload="sew_resnet18"):
+    """The workload's network with v_th = 0.1 (every layer active, the
+    reference's end-to-end setting): the dense MFMA route at every layer's
+    shape."""
+    res, stats, model, fused, x = run_network(workload, args, dev,
                                               v_threshold=LIVE_V_THRESHOLD)
-    frac, rates = liveness(fused, x)
+    frac, rates = liveness(fused, x, workload)
     kern = res["timer"].summary()
     roof = conv_roofline(kern, args.steps)
     rows = per_layer_table(res)
     mfma3 = [r for r in rows if r["kernel"] in CONV_LAUNCHES and r["route"] == "D"]
     return {"v_threshold": LIVE_V_THRESHOLD,
             "liveness": {"alive_fraction": round(frac, 4), "required": LIVE_MIN_FRACTION,
-                         "ok": frac >= LIVE_MIN_FRACTION, "block_spike_rates": rates},
+                         "ok": frac >= LIVE_MIN_FRACTION, "module_spike_rates": rates},
             "images_per_s": round(args.batch / (res["ms"] * 1e-3), 2),
             "ms_per_step": round(res["ms"], 4), "mode": res["mode"],
             "eager_ms_per_step": round(res["ms_eager"], 4),
@@ -583,6 +642,8 @@ def vgg_result(args, dev):
                                    "us_per_launch_avg": round(pool_ms * 1e3 / max(1, pool_n), 2),
                                    "achieved": round(gb, 1), "peak": PEAK_HBM_GBPS,
                                    "unit": "GB/s", "frac": round(gb / PEAK_HBM_GBPS, 4)}
+    if not args.no_live:
+        result["live"] = live_result(args, dev, "vgg11_bn")
     return result, model
 
 
@@ -911,7 +972,7 @@ def main():
     import torch
     dev = torch.device("cuda", 0)
     if args.live_only:
-        print(json.dumps(live_result(args, dev)), flush=True)
+        print(json.dumps(live_result(args, dev, args.workload)), flush=True)
         return
     if args.workload == "spikformer_8_384":
         result, model = spikformer_result(args, dev)

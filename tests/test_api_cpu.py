@@ -443,3 +443,36 @@ def test_lazy_head_helpers_decline_plain_tensors():
     assert torch.equal(x.mean(dim=2), x.mean(2))
     assert runtime.pixel_tokens(torch.randn(2, 3, 4, 1, 1)) is None
     assert runtime.linear_tokens(torch.randn(2, 3, 8), torch.randn(4, 8)) is None
+
+
+@pytest.mark.parametrize("downsample", [False, True])
+def test_substitute_bottlenecks(downsample):
+    """SEW and spiking-ResNet Bottlenecks become CTFSEWBottleneck /
+    CTFSpikingBottleneck (catfuse/substitute.py matches "Bottleneck" blocks,
+    with and without `cnf`), every LIF of the block counted as fused."""
+    from catfuse_amd.substitute import substitute
+    from catfuse_amd.patterns import (CTFSEWBottleneck, CTFSpikingBottleneck,
+                                      PartialFusionConvBNAddLIF, PartialFusionConvBNLIF)
+    from blocks import SEWBottleneck, SpikingBottleneck
+    stride = 2 if downsample else 1
+    inp = 64 if downsample else 128
+    sew = torch.nn.Sequential(SEWBottleneck(inp, 32, stride, "ADD", downsample))
+    snn.functional.set_step_mode(sew, "m")
+    fused, stats = substitute(sew)
+    blk = fused[0]
+    assert isinstance(blk, CTFSEWBottleneck) and blk.cnf == "ADD"
+    assert stats["patterns_matched"].get("CTFSEWBottleneck") == 1
+    assert stats["fused_lif_nodes"] == stats["total_lif_nodes"] == (4 if downsample else 3)
+    for part in (blk.fused_first, blk.fused_middle, blk.fused_last):
+        assert isinstance(part, PartialFusionConvBNLIF)
+    assert (blk.fused_downsample is not None) == downsample
+    assert blk.fused_middle.stride == stride
+    spk = torch.nn.Sequential(SpikingBottleneck(inp, 32, stride, downsample))
+    snn.functional.set_step_mode(spk, "m")
+    fused, stats = substitute(spk)
+    blk = fused[0]
+    assert isinstance(blk, CTFSpikingBottleneck)
+    assert isinstance(blk.fused_last_add, PartialFusionConvBNAddLIF)
+    assert stats["patterns_matched"].get("CTFSpikingBottleneck") == 1
+    assert stats["fused_lif_nodes"] == stats["total_lif_nodes"] == 3
+    assert blk.has_downsample == downsample
