@@ -663,6 +663,7 @@ def _base_result(args, res, stats, workload):
         "data": "synthetic (seeded N(0,1) images, resident in HBM, random kaiming weights, config BN stats)",
         "config": {"workload": workload, "T": args.T, "batch": args.batch,
                    "image": [3, args.image, args.image],
+                   "spike_copy": getattr(args, "spike_copy", "f16"),
                    "encoding": "direct (input repeated over T)",
                    "fused_lif_nodes": stats["fused_lif_nodes"],
                    "total_lif_nodes": stats["total_lif_nodes"]},
@@ -951,6 +952,9 @@ def main():
                     help="time eager launches instead of the captured HIP graph")
     ap.add_argument("--workload", default="sew_resnet18",
                     choices=list(WORKLOADS) + ["sf_crossover", "lif_tails"])
+    ap.add_argument("--spike-copy", default="f16", choices=["f16", "u8"],
+                    help="element of the NHWC spike copies between fused layers (one byte "
+                         "per channel with u8; results are the same bit for bit)")
     ap.add_argument("--xo-shape", type=int, nargs=5, default=[4, 32, 256, 14, 14])
     ap.add_argument("--xo-plain", action="store_true",
                     help="crossover inputs as fp32 tensors (the layer packs them)")
@@ -970,9 +974,13 @@ def main():
             setattr(args, k, v)
 
     import torch
+    import catfuse_amd
+    catfuse_amd.set_spike_copy(args.spike_copy)
     dev = torch.device("cuda", 0)
     if args.live_only:
-        print(json.dumps(live_result(args, dev, args.workload)), flush=True)
+        line = live_result(args, dev, args.workload)
+        line["spike_copy"] = args.spike_copy
+        print(json.dumps(line), flush=True)
         return
     if args.workload == "spikformer_8_384":
         result, model = spikformer_result(args, dev)

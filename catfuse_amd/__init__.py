@@ -46,6 +46,15 @@ def check_status(device=None) -> None:
                            "fp16 range (|x| > 65504 or not finite)")
 
 
+def set_spike_copy(fmt: str) -> None:
+    """Element of the NHWC spike copies the fused layers exchange: "f16"
+    (two bytes per channel) or "u8" (one byte: the values are integers
+    0..255).  Layers launched afterwards produce copies in that format;
+    results are bit for bit the same in both."""
+    from catfuse_amd import runtime
+    runtime.set_spike_copy(fmt)
+
+
 def capture(model, example, reset=True, warmup=2):
     """HIP-graph replay of ``reset_net(model); model(example)`` (see
     catfuse_amd.graph): returns a callable that copies its input into the
@@ -54,4 +63,4 @@ def capture(model, example, reset=True, warmup=2):
     return graph.capture(model, example, reset=reset, warmup=warmup)
 
 
-__all__ = ["optimize", "check_status", "capture", "__version__"]
+__all__ = ["optimize", "check_status", "capture", "set_spike_copy", "__version__"]

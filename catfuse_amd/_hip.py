@@ -60,6 +60,19 @@ _SIGNATURES = {
                           _P, _P, _P, _P, _P, _P, _I, _P, _P, c_int, _I, _I, _I,
                           _P, _P, _P, _P, _P, _P, _I, _P, _P, c_int, _I, _I, _I,
                           c_double, c_double, c_double, c_int, c_int, _P],
+    "cf_conv_halo_u8": [_P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _P, _P, _P, _P, _P, _P, _P,
+                        c_int, _P, _I, c_double, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
+                        _I, _I, c_double, c_double, c_double, c_int, c_int, _P],
+    "cf_conv_halo_pair_u8": [_P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I,
+                             _P, _P, _P, _P, _P, _P, _I, _P, _P, c_int, _I, _I, _I,
+                             _P, _P, _P, _P, _P, _P, _I, _P, _P, c_int, _I, _I, _I,
+                             c_double, c_double, c_double, c_int, c_int, _P],
+    "cf_conv_stem_lif_maxpool_u8": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I,
+                                    _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, c_double, c_double,
+                                    c_double, c_int, c_int, _P],
+    "cf_nhwc_to_nchw_u8": [_P, _P, _I, _I, _I, _I, _I, _P],
+    "cf_global_avgpool_nhwc_u8": [_P, _P, _P, _I, _I, _I, _I, _P],
+    "cf_copy_u8_to_f16": [_P, _P, _I, _P],
     "cf_pack_stem_weights": [_P, _I, _I, _I, _I, _I, _P, _P, _P, _P, _P, _P, _P],
     "cf_conv_stem_lif_maxpool": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I,
                                  _I, _I, _I, _I, _I, _I, _I, _I, _I, c_double, c_double,

@@ -36,6 +36,33 @@ typedef _Float16 h4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
+// One-byte spike copies.  A spike value n (0/1, a SEW sum, any integer
+// 0..255) becomes the fp16 value n exactly: v_perm places the byte under a
+// 0x64 high byte, i.e. the half 1024 + n (fp16 holds every integer below
+// 2048), and subtracting 1024 is exact.  The reverse adds 1024 to a half
+// holding an integer 0..255 and keeps its low byte.
+__device__ __forceinline__ h8 u8x8_to_h8(u32x2 r) {
+  u32x4 w;
+  w[0] = __builtin_amdgcn_perm(0x64646464u, r[0], 0x04010400u);   // b0, b1
+  w[1] = __builtin_amdgcn_perm(0x64646464u, r[0], 0x04030402u);   // b2, b3
+  w[2] = __builtin_amdgcn_perm(0x64646464u, r[1], 0x04010400u);
+  w[3] = __builtin_amdgcn_perm(0x64646464u, r[1], 0x04030402u);
+  return __builtin_bit_cast(h8, w) - (h8)(_Float16)1024.0f;
+}
+__device__ __forceinline__ h4 u8x4_to_h4(uint32_t r) {
+  u32x2 w;
+  w[0] = __builtin_amdgcn_perm(0x64646464u, r, 0x04010400u);
+  w[1] = __builtin_amdgcn_perm(0x64646464u, r, 0x04030402u);
+  return __builtin_bit_cast(h4, w) - (h4)(_Float16)1024.0f;
+}
+__device__ __forceinline__ u32x2 h8_to_u8x8(h8 h) {
+  const u32x4 w = __builtin_bit_cast(u32x4, h + (h8)(_Float16)1024.0f);
+  u32x2 r;
+  r[0] = __builtin_amdgcn_perm(w[1], w[0], 0x06040200u);   // low bytes of halves 0..3
+  r[1] = __builtin_amdgcn_perm(w[3], w[2], 0x06040200u);
+  return r;
+}
+
 // Raw buffer resource over [base, base + bytes) (gfx9 word 3).  Buffer
 // loads outside the range return zeros and buffer stores outside it are
 // dropped by the hardware, so the lean epilogue issues every load and store
@@ -175,6 +202,8 @@ struct HaloArgs {
   int GH, GW;
   int gs;
   int gs_shift;             // log2(gs) when gs is a power of two, else -1
+  int u8;                   // the input, identity and output copies hold one byte per
+                            // channel (the U8 instantiations), else fp16
   LifParams lif;
 };
 
@@ -209,10 +238,17 @@ constexpr int halo_buf_halves() {
 // function, so that one grid can run two convs of the same input side by
 // side (conv_halo_pair_kernel).  halo: halo_nbuf() * halo_buf_halves() halves of LDS;
 // bn_s: the tile's BN coefficients; any_sh: the workgroup's vote words.
-template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB, bool HS>
+template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB, bool HS, bool U8>
 __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const int nL,
                                           _Float16* __restrict__ halo, float (*bn_s)[64],
                                           unsigned* any_sh) {
+  static_assert(!U8 || (LEAN && EPI == EPI_LIF), "one-byte copies: the lean LIF epilogue only");
+  // Element of the input, identity and output copies: one byte (U8) or one
+  // half per channel.  Element offsets are the same in both layouts
+  // ([T*B][H][W][cp]); the halo in LDS is fp16 either way (a U8 K step's
+  // bytes are widened on their way into it), so the K loop is the same.
+  using XT = std::conditional_t<U8, uint8_t, _Float16>;
+  constexpr int XB = (int)sizeof(XT);
   using G = HaloGeom<S, K, TH, TW>;
   constexpr int BM = 64;
   constexpr int BN = TH * TW;
@@ -272,14 +308,15 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   // The input and identity copies where their producers left the values:
   // an all-zero input takes StaticZero (its buffer is not read), an
   // all-zero identity is read as zeros, aliased ones where they point.
-  const _Float16* const xsrc = xd.copy == CF_COPY_ZERO    ? nullptr
-                               : xd.copy == CF_COPY_ALIAS ? (const _Float16*)xd.alias
-                                                          : a.x;
+  const XT* const xsrc = xd.copy == CF_COPY_ZERO    ? nullptr
+                         : xd.copy == CF_COPY_ALIAS ? (const XT*)xd.alias
+                                                    : (const XT*)(const void*)a.x;
   if (xsrc == nullptr) route = CF_ROUTE_ZERO;
-  const _Float16* const id_nhwc = a.identity_nhwc == nullptr   ? nullptr
-                                  : idd.copy == CF_COPY_ZERO  ? nullptr
-                                  : idd.copy == CF_COPY_ALIAS ? (const _Float16*)idd.alias
-                                                              : a.identity_nhwc;
+  const XT* const id_nhwc = a.identity_nhwc == nullptr   ? nullptr
+                            : idd.copy == CF_COPY_ZERO  ? nullptr
+                            : idd.copy == CF_COPY_ALIAS ? (const XT*)idd.alias
+                                                        : (const XT*)(const void*)a.identity_nhwc;
+  XT* const out_copy = (XT*)(void*)a.out_nhwc;
   auto set_out_desc = [&](uint32_t copy, const void* alias, bool vchan) {
     if (a.out_desc != nullptr && tid == 0 && L == 0) {
       a.out_desc->copy = copy;
@@ -450,10 +487,10 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
       for (int t = 0; t < (elide ? 0 : a.T); ++t) {
         const size_t img = (size_t)t * a.B + b;
         const __amdgpu_buffer_rsrc_t ro =
-            halo_rsrc(a.out_nhwc + img * HoWo * a.cp_out, (uint32_t)(HoWo * a.cp_out * 2));
+            halo_rsrc(out_copy + img * HoWo * a.cp_out, (uint32_t)(HoWo * a.cp_out * XB));
         const __amdgpu_buffer_rsrc_t ri =
-            halo_rsrc(have_id ? id_nhwc + img * HoWo * a.cp_id : a.identity_nhwc,
-                      have_id ? (uint32_t)(HoWo * a.cp_id * 2) : 0u);
+            halo_rsrc(have_id ? id_nhwc + img * HoWo * a.cp_id : (const XT*)a.identity_nhwc,
+                      have_id ? (uint32_t)(HoWo * a.cp_id * XB) : 0u);
 #pragma unroll
         for (int i = 0; i < CPIZ; ++i) {
           const int c = tid + 256 * i;
@@ -462,13 +499,20 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
           const bool ok = (oh0 + py < a.Ho) & (ow0 + pxx < a.Wo) & (cout0 + part * 8 < a.Cout);
           const int pix = (oh0 + py) * a.Wo + ow0 + pxx;
           const h8 sp = *reinterpret_cast<const h8*>(&srow[t * BM + part * 8]);
-          const h8 idv = __builtin_bit_cast(
-              h8, __builtin_amdgcn_raw_buffer_load_b128(
-                      ri, ok ? (uint32_t)((pix * a.cp_id + cout0 + part * 8) * 2) : HALO_OOB, 0, 0));
-          const u32x4 sum = __builtin_bit_cast(u32x4, idv + sp);
+          const uint32_t ioff = ok ? (uint32_t)((pix * a.cp_id + cout0 + part * 8) * XB) : HALO_OOB;
+          h8 idv;
+          if constexpr (U8)
+            idv = u8x8_to_h8(__builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(ri, ioff, 0, 0)));
+          else
+            idv = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(ri, ioff, 0, 0));
+          const h8 sumh = idv + sp;
+          const u32x4 sum = __builtin_bit_cast(u32x4, sumh);
           anyw |= ok ? (sum[0] | sum[1] | sum[2] | sum[3]) : 0u;
-          __builtin_amdgcn_raw_buffer_store_b128(
-              sum, ro, ok ? (uint32_t)((pix * a.cp_out + cout0 + part * 8) * 2) : HALO_OOB, 0, 0);
+          const uint32_t ooff = ok ? (uint32_t)((pix * a.cp_out + cout0 + part * 8) * XB) : HALO_OOB;
+          if constexpr (U8)
+            __builtin_amdgcn_raw_buffer_store_b64(h8_to_u8x8(sumh), ro, ooff, 0, 0);
+          else
+            __builtin_amdgcn_raw_buffer_store_b128(sum, ro, ooff, 0, 0);
         }
       }
       if (a.v_out && !vchan) {
@@ -577,14 +621,14 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     nact = 0u;
   };
   const size_t img_stride = (size_t)a.H * a.W * a.Cp;  // halves per staged image
-  const _Float16* zero_page = opaque_ptr(reinterpret_cast<const _Float16*>(&g_halo_zero));
+  const XT* zero_page = opaque_ptr(reinterpret_cast<const XT*>(&g_halo_zero));
   // This thread's unit of direct load i is the same for every K step of the
   // tile: its source offset (halves, from the tile's top-left input pixel of
   // time step 0 of the block; 32-bit, checked on the host), whether the
   // pixel lies inside the image (bit i of cp_inb) and its time step within
   // the block (bits 2i.. of cp_t).  Per K step only the block, the chunk and
   // the step activity change.
-  const _Float16* xtile = xsrc + (ptrdiff_t)((ptrdiff_t)ih0 * a.W + iw0) * a.Cp;
+  const XT* xtile = xsrc + (ptrdiff_t)((ptrdiff_t)ih0 * a.W + iw0) * a.Cp;
   // Unit of direct load i of this thread: 64-unit block 4 i + w of wave w
   // (wrapped into 0 .. NB-1: a wrapped load repeats another one, writing
   // the same bytes), lane l unit 64 * block + l.  Its source offset (halves,
@@ -636,7 +680,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     constexpr bool PRE = decltype(pre_c)::value;
     const int nst = tbs < a.T ? min(TB, a.T - tbs) : 0;  // 0: every unit loads zeros
     const uint32_t live = act & ((1u << nst) - 1u);    // steps to load, bit t
-    const _Float16* xb = xtile + (size_t)(tbs * a.B + b) * img_stride + ch * KC;
+    const XT* xb = xtile + (size_t)(tbs * a.B + b) * img_stride + ch * KC;
 #pragma unroll
     for (int i = i0; i < i1; ++i) {
       int off, t, blk;
@@ -651,8 +695,51 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
         blk = unit_of(i, off, inb, t);
       }
       const bool ok = inb & (((live >> t) & 1u) != 0u);
-      lds_copy16(ok ? xb + off : zero_page,
-                 __builtin_amdgcn_readfirstlane(lds_addr(hb + blk * 512)));
+      if constexpr (U8) {
+        // eight channels (bytes) of the unit, widened to its 16 LDS bytes;
+        // a buffer load (an out-of-range offset reads zeros)
+        const u32x2 r = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(halo_rsrc(xb, 0x7fffffffu),
+                                                        ok ? (uint32_t)off : HALO_OOB, 0, 0));
+        *reinterpret_cast<h8*>(hb + blk * 512 + opaque(lane) * 8) = u8x8_to_h8(r);
+      } else {
+        lds_copy16(ok ? xb + off : zero_page,
+                   __builtin_amdgcn_readfirstlane(lds_addr(hb + blk * 512)));
+      }
+    }
+  };
+  // One-byte copies inside the K loop: a K step's loads are issued into
+  // registers, spread over the taps of the step before (stage_defer), and
+  // widened into their halo buffer once those taps are done
+  // (stage_commit), so their latency is hidden as the direct loads' is.
+  u32x2 raw[U8 ? NPF : 1];
+  auto stage_defer = [&](int tbs, int ch, uint32_t act, int i0, int i1) {
+    if constexpr (U8) {
+      const int nst = tbs < a.T ? min(TB, a.T - tbs) : 0;
+      const uint32_t live = act & ((1u << nst) - 1u);
+      const XT* xb = xtile + (size_t)(tbs * a.B + b) * img_stride + ch * KC;
+      // buffer loads from the K step's base (offsets below 2^31, checked
+      // on the host; units outside the image or the live steps read zeros)
+      const __amdgpu_buffer_rsrc_t rx = halo_rsrc(xb, 0x7fffffffu);
+#pragma unroll
+      for (int i = i0; i < i1; ++i) {
+        const bool inb = ((cp_inb >> i) & 1u) != 0u;
+        const int t = (int)((cp_t >> (2 * i)) & 3u);
+        const bool ok = inb & (((live >> t) & 1u) != 0u);
+        raw[i] = __builtin_bit_cast(
+            u32x2, __builtin_amdgcn_raw_buffer_load_b64(rx, ok ? (uint32_t)cp_off[i] : HALO_OOB,
+                                                        0, 0));
+      }
+    }
+  };
+  auto stage_commit = [&](_Float16* hb) {
+    if constexpr (U8) {
+#pragma unroll
+      for (int i = 0; i < NPF; ++i) {
+        int blk = 4 * i + wave;
+        if (4 * NPF > NB && blk >= NB) blk -= NB;
+        *reinterpret_cast<h8*>(hb + blk * 512 + opaque(lane) * 8) = u8x8_to_h8(raw[i]);
+      }
     }
   };
 
@@ -725,7 +812,15 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
         if (th == 0) {
           if (tap + 1 < KK) load_w(cur ^ 1, tap + 1, ch);
           else load_w(cur ^ 1, 0, nc);
-          if (NBUF == 1) {
+          if constexpr (U8) {
+            // both buffer counts: loads now, widened after the taps
+            if (KK == 1) {
+              stage_defer(stb, nc, nact, 0, NPF);
+            } else if (tap + 1 < KK) {
+              const int i0 = (tap * NPF) / (KK - 1), i1 = ((tap + 1) * NPF) / (KK - 1);
+              if (i1 > i0) stage_defer(stb, nc, nact, i0, i1);
+            }
+          } else if (NBUF == 1) {
             // one buffer: the next K step stages after the taps
           } else if (KK == 1) {
             stage_loads(std::true_type{}, stb, nc, nact, hb_next, 0, NPF);
@@ -808,9 +903,11 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
         // has finished reading it
         if (ntb == tb0) {
           __syncthreads();
-          stage_loads(std::true_type{}, ntb, nc, nact, halo, 0, NPF);
+          if constexpr (U8) stage_commit(halo);
+          else stage_loads(std::true_type{}, ntb, nc, nact, halo, 0, NPF);
         }
       } else {
+        if constexpr (U8) stage_commit(halo + (buf ^ 1) * HB);
         buf ^= 1;
       }
       s_tb = ntb;
@@ -961,27 +1058,34 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     // Lean path: the identity of step t is loaded into idq[t & 1] while step
     // t - 1 is computed, before that step's stores (zeros without an
     // identity or beyond the block: an empty range).
-    h4 idq[LEAN ? 2 : 1][NT][4];
+    // (one-byte copies: the four channels' bytes, widened when used)
+    h4 idq[LEAN && !U8 ? 2 : 1][NT][4];
+    uint32_t idr[U8 ? 2 : 1][NT][4];
     auto id_load = [&](int t) {
       const bool have = id_nhwc && t < nsteps;
-      const _Float16* base =
-          have ? id_nhwc + (size_t)((tb0 + t) * a.B + b) * HoWo * a.cp_id : a.identity_nhwc;
-      const __amdgpu_buffer_rsrc_t rid = halo_rsrc(base, have ? (uint32_t)(HoWo * a.cp_id * 2) : 0u);
+      const XT* base = have ? id_nhwc + (size_t)((tb0 + t) * a.B + b) * HoWo * a.cp_id
+                            : (const XT*)a.identity_nhwc;
+      const __amdgpu_buffer_rsrc_t rid =
+          halo_rsrc(base, have ? (uint32_t)(HoWo * a.cp_id * XB) : 0u);
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt)
-          idq[t & 1][nt][r4] = __builtin_bit_cast(
-              h4, __builtin_amdgcn_raw_buffer_load_b64(
-                      rid, (unsigned)((epix[nt] * a.cp_id + col + 8 * r4) * 2), 0, 0));
+        for (int nt = 0; nt < NT; ++nt) {
+          const unsigned off = (unsigned)((epix[nt] * a.cp_id + col + 8 * r4) * XB);
+          if constexpr (U8)
+            idr[t & 1][nt][r4] = __builtin_amdgcn_raw_buffer_load_b32(rid, off, 0, 0);
+          else
+            idq[t & 1][nt][r4] =
+                __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rid, off, 0, 0));
+        }
     };
     if constexpr (LEAN) id_load(0);
     auto epi_step = [&](int t) {
       const int tt = tb0 + t;
       const int img = tt * a.B + b;
       _Float16* ostage = obuf + (t % NOBUF) * OSTEP;
-      const _Float16* idn = id_nhwc;
-      const _Float16* idbase = idn ? idn + (size_t)img * HoWo * a.cp_id : nullptr;
+      const XT* idn = id_nhwc;
+      const XT* idbase = idn ? idn + (size_t)img * HoWo * a.cp_id : nullptr;
       if constexpr (LEAN) {
         if (t + 1 < TB) id_load(t + 1);
       }
@@ -996,7 +1100,9 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           h4 idh = {};
-          if constexpr (LEAN) {
+          if constexpr (U8) {
+            idh = u8x4_to_h4(idr[t & 1][nt][r4]);
+          } else if constexpr (LEAN) {
             idh = idq[t & 1][nt][r4];
           } else {
             if (idbase)
@@ -1066,7 +1172,9 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
           // every chunk index is below BN * CH8; the hardware drops pixels
           // outside the output and channels >= Cout
           static_assert(BN * CH8 % 256 == 0, "lean copy-out assumes whole passes");
-          const __amdgpu_buffer_rsrc_t ro = halo_rsrc(obase, (uint32_t)(HoWo * a.cp_out * 2));
+          const __amdgpu_buffer_rsrc_t ro =
+              halo_rsrc(out_copy + (size_t)((tb0 + t) * a.B + b) * HoWo * a.cp_out,
+                        (uint32_t)(HoWo * a.cp_out * XB));
 #pragma unroll
           for (int i = 0; i < CPI; ++i) {
             const int c = opaque(tid) + 256 * i;
@@ -1074,13 +1182,16 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
             const int py = px / TW, pxx = px % TW;
             const bool ok = (oh0 + py < a.Ho) & (ow0 + pxx < a.Wo) & (cout0 + part * 8 < a.Cout);
             const uint32_t off =
-                ok ? (uint32_t)((((oh0 + py) * a.Wo + ow0 + pxx) * a.cp_out + cout0 + part * 8) * 2)
+                ok ? (uint32_t)((((oh0 + py) * a.Wo + ow0 + pxx) * a.cp_out + cout0 + part * 8) * XB)
                    : HALO_OOB;
             // streaming (non-temporal) stores: the copy is read back by the
             // next layer only after the whole output is written
-            __builtin_amdgcn_raw_buffer_store_b128(
-                *reinterpret_cast<const u32x4*>(&ostage[px * OLD + part * 8]), ro, off, 0,
-                CF_CPOL_NT);
+            const u32x4 chunk = *reinterpret_cast<const u32x4*>(&ostage[px * OLD + part * 8]);
+            if constexpr (U8)
+              __builtin_amdgcn_raw_buffer_store_b64(h8_to_u8x8(__builtin_bit_cast(h8, chunk)), ro,
+                                                    off, 0, CF_CPOL_NT);
+            else
+              __builtin_amdgcn_raw_buffer_store_b128(chunk, ro, off, 0, CF_CPOL_NT);
           }
         } else {
 #pragma unroll
@@ -1137,14 +1248,15 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   set_out_desc(CF_COPY_WRITTEN, nullptr, false);
 }
 
-template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB, bool HS = false>
+template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB, bool HS = false,
+          bool U8 = false>
 __global__ __launch_bounds__(256, (halo_min_blocks<TH, TW, S, K>()))
 void conv_halo_kernel(HaloArgs a) {
   __shared__ __attribute__((aligned(16))) _Float16 halo[halo_nbuf<S, K>() * halo_buf_halves<TH, TW, S, K>()];
   __shared__ __attribute__((aligned(16))) float bn_s[2][64];  // alpha, beta of the tile
   __shared__ unsigned any_sh[4];  // per-wave votes of the output count
-  halo_body<TH, TW, S, K, EPI, LM, LEAN, ONEB, HS>(a, (int)blockIdx.x, (int)gridDim.x, halo,
-                                                   bn_s, any_sh);
+  halo_body<TH, TW, S, K, EPI, LM, LEAN, ONEB, HS, U8>(a, (int)blockIdx.x, (int)gridDim.x, halo,
+                                                       bn_s, any_sh);
 }
 
 template <int TH, int TW, int S, int K = 3>
@@ -1155,6 +1267,29 @@ hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
   // stores drop channels >= Cout of a partly real 64-channel tile)
   const bool lean = epi == EPI_LIF && !a.out && !a.identity && a.Cout % 32 == 0;
   const bool oneb = a.T <= halo_tb<S, K>();
+  if (a.u8) {
+    // one-byte copies: the lean LIF epilogue on 8x8 tiles only (the SparseFlow
+    // route without the half skip: the skipped products are zeros either way)
+    if constexpr (TH == 8 && TW == 8) {
+      if (!lean) return hipErrorInvalidValue;
+      const int lm = cf_lif_mode(a.lif);
+#define CF_HALO_U8(LMV)                                                                          \
+  do {                                                                                           \
+    if (oneb)                                                                                    \
+      hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LMV, true, true, false, true>), \
+                         grid, block, 0, st, a);                                                 \
+    else                                                                                         \
+      hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LMV, true, false, false, true>), \
+                         grid, block, 0, st, a);                                                 \
+  } while (0)
+      if (lm == LM_HARD0_DECAY_P2) CF_HALO_U8(LM_HARD0_DECAY_P2);
+      else if (lm == LM_HARD_DECAY_P2) CF_HALO_U8(LM_HARD_DECAY_P2);
+      else CF_HALO_U8(LM_GENERIC);
+#undef CF_HALO_U8
+      return hipGetLastError();
+    }
+    return hipErrorInvalidValue;
+  }
   if (epi == EPI_POOL) {
     // (the host admits it for stride-1 3x3 convs on 8x8 tiles only)
     if constexpr (TH == 8 && TW == 8 && S == 1 && K == 3) {
@@ -1291,6 +1426,7 @@ int make_halo_args(HaloArgs& a, const void* x, const void* w_packed, const float
   a.gs = group_size > 0 ? (int)group_size : 32;
   a.gs_shift = (a.gs & (a.gs - 1)) == 0 ? __builtin_ctz((unsigned)a.gs) : -1;
   a.lif = cf_make_lif_params(tau, v_th, v_reset, hard_reset, decay_input);
+  a.u8 = 0;
   return 0;
 }
 
@@ -1300,7 +1436,7 @@ int make_halo_args(HaloArgs& a, const void* x, const void* w_packed, const float
 // pixels are the 3x3 conv's centre taps), each as its own launch would (same
 // accumulation order, so the same bits), sharing the input through the L2.
 // Lean LIF epilogues only (fp16 NHWC outputs, no identity).
-template <int LM, bool OBA, bool OBB>
+template <int LM, bool OBA, bool OBB, bool U8 = false>
 __global__ __launch_bounds__(256, (halo_min_blocks<8, 8, 2, 3>()))
 void conv_halo_pair_kernel(HaloArgs a, HaloArgs b, int nLa) {
   constexpr int HA = halo_nbuf<2, 3>() * halo_buf_halves<8, 8, 2, 3>();
@@ -1310,9 +1446,9 @@ void conv_halo_pair_kernel(HaloArgs a, HaloArgs b, int nLa) {
   __shared__ unsigned any_sh[4];
   const int L = (int)blockIdx.x;
   if (L < nLa)
-    halo_body<8, 8, 2, 3, EPI_LIF, LM, true, OBA, false>(a, L, nLa, halo, bn_s, any_sh);
+    halo_body<8, 8, 2, 3, EPI_LIF, LM, true, OBA, false, U8>(a, L, nLa, halo, bn_s, any_sh);
   else
-    halo_body<8, 8, 2, 1, EPI_LIF, LM, true, OBB, false>(b, L - nLa, (int)gridDim.x - nLa, halo,
+    halo_body<8, 8, 2, 1, EPI_LIF, LM, true, OBB, false, U8>(b, L - nLa, (int)gridDim.x - nLa, halo,
                                                          bn_s, any_sh);
 }
 
@@ -1371,7 +1507,49 @@ CF_API int cf_bias_response(const float* alpha, const float* beta, int64_t Cout,
 
 // 3x3 convolutions (stride 1 or 2, any padding) with halo staging; the
 // caller picks the tile (tile_h x tile_w in {8x8, 8x16}; 8x16 only with
-// stride 1).  Arguments as cf_conv_mfma.
+// stride 1).  u8: the copies (x, identity_nhwc, out_nhwc) hold one byte per
+// channel (8x8 tiles, lean LIF epilogue).
+static int conv_halo(const void* x, const void* w_packed, const float* alpha,
+                     const float* beta, const float* v_in, float* v_out, float* out,
+                     void* out_nhwc, int64_t cp_out,
+                     const float* identity, const void* identity_nhwc, int64_t cp_id,
+                     int identity_mode, const int32_t* ag_mask, const int32_t* tile_order,
+                     const unsigned long long* nnz, unsigned long long* nz_out,
+                     const void* x_desc, const void* id_desc, void* out_desc,
+                     int bias_info, const unsigned long long* id_nnz,
+                     int64_t numel, double sparse_threshold,
+                     int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp, int64_t H,
+                     int64_t W, int64_t Ho, int64_t Wo, int64_t ksize, int64_t stride,
+                     int64_t pad, int64_t tile_h, int64_t tile_w, int64_t group_size,
+                     int epilogue, double tau, double v_th, double v_reset, int hard_reset,
+                     int decay_input, int u8, void* stream) {
+  HaloArgs a;
+  const int rc = make_halo_args(a, x, w_packed, alpha, beta, v_in, v_out, out, out_nhwc, cp_out,
+                                identity, identity_nhwc, cp_id, identity_mode, ag_mask,
+                                tile_order, nnz, nz_out, x_desc, id_desc, out_desc, bias_info,
+                                id_nnz, numel,
+                                sparse_threshold, T, B, Cp, Cout,
+                                Coutp, H, W, Ho, Wo, ksize, stride, pad, tile_h, tile_w,
+                                group_size, epilogue, tau, v_th, v_reset, hard_reset,
+                                decay_input);
+  if (rc) return rc;
+  if (u8 && (tile_w != 8 || epilogue != EPI_LIF || out || identity || !out_nhwc ||
+             Cout % 32 != 0 || cp_out % 8 != 0 || Cp % 32 != 0))
+    return (int)hipErrorInvalidValue;
+  a.u8 = u8 ? 1 : 0;
+  hipStream_t st = (hipStream_t)stream;
+  hipError_t e;
+  if (ksize == 1)
+    e = stride == 1 ? launch_halo<8, 8, 1, 1>(a, epilogue, st) : launch_halo<8, 8, 2, 1>(a, epilogue, st);
+  else if (stride == 1 && tile_w == 16)
+    e = launch_halo<8, 16, 1>(a, epilogue, st);
+  else if (stride == 1)
+    e = launch_halo<8, 8, 1>(a, epilogue, st);
+  else
+    e = launch_halo<8, 8, 2>(a, epilogue, st);
+  return (int)e;
+}
+
 CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
                         const float* beta, const float* v_in, float* v_out, float* out,
                         void* out_nhwc, int64_t cp_out,
@@ -1386,30 +1564,35 @@ CF_API int cf_conv_halo(const void* x, const void* w_packed, const float* alpha,
                         int64_t pad, int64_t tile_h, int64_t tile_w, int64_t group_size,
                         int epilogue, double tau, double v_th, double v_reset, int hard_reset,
                         int decay_input, void* stream) {
-  HaloArgs a;
-  const int rc = make_halo_args(a, x, w_packed, alpha, beta, v_in, v_out, out, out_nhwc, cp_out,
-                                identity, identity_nhwc, cp_id, identity_mode, ag_mask,
-                                tile_order, nnz, nz_out, x_desc, id_desc, out_desc, bias_info,
-                                id_nnz, numel,
-                                sparse_threshold, T, B, Cp, Cout,
-                                Coutp, H, W, Ho, Wo, ksize, stride, pad, tile_h, tile_w,
-                                group_size, epilogue, tau, v_th, v_reset, hard_reset,
-                                decay_input);
-  if (rc) return rc;
-  hipStream_t st = (hipStream_t)stream;
-  hipError_t e;
-  if (ksize == 1)
-    e = stride == 1 ? launch_halo<8, 8, 1, 1>(a, epilogue, st) : launch_halo<8, 8, 2, 1>(a, epilogue, st);
-  else if (stride == 1 && tile_w == 16)
-    e = launch_halo<8, 16, 1>(a, epilogue, st);
-  else if (stride == 1)
-    e = launch_halo<8, 8, 1>(a, epilogue, st);
-  else
-    e = launch_halo<8, 8, 2>(a, epilogue, st);
-  return (int)e;
+  return conv_halo(x, w_packed, alpha, beta, v_in, v_out, out, out_nhwc, cp_out, identity,
+                   identity_nhwc, cp_id, identity_mode, ag_mask, tile_order, nnz, nz_out, x_desc,
+                   id_desc, out_desc, bias_info, id_nnz, numel, sparse_threshold, T, B, Cp, Cout,
+                   Coutp, H, W, Ho, Wo, ksize, stride, pad, tile_h, tile_w, group_size, epilogue,
+                   tau, v_th, v_reset, hard_reset, decay_input, 0, stream);
 }
 
-CF_API int cf_conv_halo_pair(
+CF_API int cf_conv_halo_u8(const void* x, const void* w_packed, const float* alpha,
+                           const float* beta, const float* v_in, float* v_out,
+                           void* out_copy, int64_t cp_out, const void* identity_copy,
+                           int64_t cp_id, const int32_t* ag_mask, const int32_t* tile_order,
+                           const unsigned long long* nnz, unsigned long long* nz_out,
+                           const void* x_desc, const void* id_desc, void* out_desc,
+                           int bias_info, const unsigned long long* id_nnz,
+                           int64_t numel, double sparse_threshold,
+                           int64_t T, int64_t B, int64_t Cp, int64_t Cout, int64_t Coutp,
+                           int64_t H, int64_t W, int64_t Ho, int64_t Wo, int64_t ksize,
+                           int64_t stride, int64_t pad, int64_t group_size, double tau,
+                           double v_th, double v_reset, int hard_reset, int decay_input,
+                           void* stream) {
+  return conv_halo(x, w_packed, alpha, beta, v_in, v_out, nullptr, out_copy, cp_out, nullptr,
+                   identity_copy, cp_id, identity_copy ? ID_ADD_SPIKE : 0, ag_mask, tile_order,
+                   nnz, nz_out, x_desc, id_desc, out_desc, bias_info, id_nnz, numel,
+                   sparse_threshold, T, B, Cp, Cout, Coutp, H, W, Ho, Wo, ksize, stride, pad, 8,
+                   8, group_size, EPI_LIF, tau, v_th, v_reset, hard_reset, decay_input, 1,
+                   stream);
+}
+
+static int conv_halo_pair(
     const void* x, const unsigned long long* nnz, const void* x_desc, int64_t numel,
     int64_t T, int64_t B, int64_t Cp, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
     const void* w_a, const float* alpha_a, const float* beta_a, const float* v_in_a,
@@ -1418,8 +1601,11 @@ CF_API int cf_conv_halo_pair(
     const void* w_b, const float* alpha_b, const float* beta_b, const float* v_in_b,
     float* v_out_b, void* out_b, int64_t cp_out_b, unsigned long long* nz_b, void* desc_b, int bias_info_b,
     int64_t Cout_b, int64_t Coutp_b, int64_t pad_b,
-    double tau, double v_th, double v_reset, int hard_reset, int decay_input, void* stream) {
+    double tau, double v_th, double v_reset, int hard_reset, int decay_input, int u8,
+    void* stream) {
   if (!out_a || !out_b || Cout_a % 32 != 0 || Cout_b % 32 != 0) return (int)hipErrorInvalidValue;
+  if (u8 && (cp_out_a % 8 != 0 || cp_out_b % 8 != 0 || Cp % 32 != 0))
+    return (int)hipErrorInvalidValue;
   HaloArgs a, b;
   int rc = make_halo_args(a, x, w_a, alpha_a, beta_a, v_in_a, v_out_a, nullptr, out_a, cp_out_a,
                           nullptr, nullptr, 0, 0, nullptr, nullptr, nnz, nz_a, x_desc, nullptr,
@@ -1433,6 +1619,7 @@ CF_API int cf_conv_halo_pair(
                       Cout_b, Coutp_b, H, W, Ho, Wo, 1, 2, pad_b, 8, 8, 0, EPI_LIF, tau, v_th,
                       v_reset, hard_reset, decay_input);
   if (rc) return rc;
+  a.u8 = b.u8 = u8 ? 1 : 0;
   // each part's workgroup count as its own launch (below 2^23 together)
   const int64_t nLa = B * a.GH * a.GW * (Coutp_a / 64), nLb = B * b.GH * b.GW * (Coutp_b / 64);
   if (nLa + nLb >= ((int64_t)1 << 23)) return (int)hipErrorInvalidValue;
@@ -1442,7 +1629,17 @@ CF_API int cf_conv_halo_pair(
   const int ob = T <= halo_tb<2, 3>() ? 2 : (T <= halo_tb<2, 1>() ? 1 : 0);
 #define CF_PAIR(LMV)                                                                          \
   do {                                                                                        \
-    if (ob == 2)                                                                              \
+    if (u8) {                                                                                 \
+      if (ob == 2)                                                                            \
+        hipLaunchKernelGGL((conv_halo_pair_kernel<LMV, true, true, true>), grid, block, 0, st, \
+                           a, b, (int)nLa);                                                   \
+      else if (ob == 1)                                                                       \
+        hipLaunchKernelGGL((conv_halo_pair_kernel<LMV, false, true, true>), grid, block, 0, st, \
+                           a, b, (int)nLa);                                                   \
+      else                                                                                    \
+        hipLaunchKernelGGL((conv_halo_pair_kernel<LMV, false, false, true>), grid, block, 0,  \
+                           st, a, b, (int)nLa);                                               \
+    } else if (ob == 2)                                                                       \
       hipLaunchKernelGGL((conv_halo_pair_kernel<LMV, true, true>), grid, block, 0, st, a, b,   \
                          (int)nLa);                                                           \
     else if (ob == 1)                                                                         \
@@ -1457,4 +1654,38 @@ CF_API int cf_conv_halo_pair(
   else CF_PAIR(LM_GENERIC);
 #undef CF_PAIR
   return (int)hipGetLastError();
+}
+
+CF_API int cf_conv_halo_pair(
+    const void* x, const unsigned long long* nnz, const void* x_desc, int64_t numel,
+    int64_t T, int64_t B, int64_t Cp, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
+    const void* w_a, const float* alpha_a, const float* beta_a, const float* v_in_a,
+    float* v_out_a, void* out_a, int64_t cp_out_a, unsigned long long* nz_a, void* desc_a,
+    int bias_info_a, int64_t Cout_a, int64_t Coutp_a, int64_t pad_a,
+    const void* w_b, const float* alpha_b, const float* beta_b, const float* v_in_b,
+    float* v_out_b, void* out_b, int64_t cp_out_b, unsigned long long* nz_b, void* desc_b,
+    int bias_info_b, int64_t Cout_b, int64_t Coutp_b, int64_t pad_b,
+    double tau, double v_th, double v_reset, int hard_reset, int decay_input, void* stream) {
+  return conv_halo_pair(x, nnz, x_desc, numel, T, B, Cp, H, W, Ho, Wo, w_a, alpha_a, beta_a,
+                        v_in_a, v_out_a, out_a, cp_out_a, nz_a, desc_a, bias_info_a, Cout_a,
+                        Coutp_a, pad_a, w_b, alpha_b, beta_b, v_in_b, v_out_b, out_b, cp_out_b,
+                        nz_b, desc_b, bias_info_b, Cout_b, Coutp_b, pad_b, tau, v_th, v_reset,
+                        hard_reset, decay_input, 0, stream);
+}
+
+CF_API int cf_conv_halo_pair_u8(
+    const void* x, const unsigned long long* nnz, const void* x_desc, int64_t numel,
+    int64_t T, int64_t B, int64_t Cp, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
+    const void* w_a, const float* alpha_a, const float* beta_a, const float* v_in_a,
+    float* v_out_a, void* out_a, int64_t cp_out_a, unsigned long long* nz_a, void* desc_a,
+    int bias_info_a, int64_t Cout_a, int64_t Coutp_a, int64_t pad_a,
+    const void* w_b, const float* alpha_b, const float* beta_b, const float* v_in_b,
+    float* v_out_b, void* out_b, int64_t cp_out_b, unsigned long long* nz_b, void* desc_b,
+    int bias_info_b, int64_t Cout_b, int64_t Coutp_b, int64_t pad_b,
+    double tau, double v_th, double v_reset, int hard_reset, int decay_input, void* stream) {
+  return conv_halo_pair(x, nnz, x_desc, numel, T, B, Cp, H, W, Ho, Wo, w_a, alpha_a, beta_a,
+                        v_in_a, v_out_a, out_a, cp_out_a, nz_a, desc_a, bias_info_a, Cout_a,
+                        Coutp_a, pad_a, w_b, alpha_b, beta_b, v_in_b, v_out_b, out_b, cp_out_b,
+                        nz_b, desc_b, bias_info_b, Cout_b, Coutp_b, pad_b, tau, v_th, v_reset,
+                        hard_reset, decay_input, 1, stream);
 }

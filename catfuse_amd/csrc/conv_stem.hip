@@ -73,6 +73,7 @@ struct StemArgs {
   float* out;            // [T][B][Cout][Hp][Wp] or null
   _Float16* out_nhwc;    // [T*B][Hp][Wp][cp_out] or null
   int cp_out;
+  int u8;                // out_nhwc holds one byte per channel
   uint32_t* status;
   unsigned long long* nz_out;   // count block of the pooled output, or null
   int T, B, Cin, Cout, Coutp, H, W, KH, pad, Hc, Wc, Hp, Wp, GHp, GWp;
@@ -371,12 +372,22 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
         anyw |= wd[j];   // channels >= Cout hold zero words
       }
       for (int t = 0; t < a.T; ++t) {
-        h8 hv;
+        const size_t e = (((size_t)t * a.B + b) * HpWp + (size_t)oh * a.Wp + ow) * a.cp_out + co8;
+        if (a.u8) {
+          // one byte per channel: 8 bytes
+          uint32_t lo = 0u, hi = 0u;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) hv[j] = ((wd[j] >> t) & 1u) ? (_Float16)1.0f : (_Float16)0.0f;
-        *reinterpret_cast<h8*>(a.out_nhwc +
-                               (((size_t)t * a.B + b) * HpWp + (size_t)oh * a.Wp + ow) * a.cp_out +
-                               co8) = hv;
+          for (int j = 0; j < 4; ++j) {
+            lo |= ((wd[j] >> t) & 1u) << (8 * j);
+            hi |= ((wd[4 + j] >> t) & 1u) << (8 * j);
+          }
+          *reinterpret_cast<uint2*>(reinterpret_cast<uint8_t*>(a.out_nhwc) + e) = make_uint2(lo, hi);
+        } else {
+          h8 hv;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) hv[j] = ((wd[j] >> t) & 1u) ? (_Float16)1.0f : (_Float16)0.0f;
+          *reinterpret_cast<h8*>(a.out_nhwc + e) = hv;
+        }
       }
     }
   }
@@ -470,15 +481,15 @@ CF_API int cf_pack_stem_weights(const float* w, int64_t Cout, int64_t Cin, int64
   return (int)hipGetLastError();
 }
 
-CF_API int cf_conv_stem_lif_maxpool(const float* x, const void* w_stem, const float* alpha,
-                                    const float* beta, const float* v_in, float* v_out,
-                                    float* out, void* out_nhwc, int64_t cp_out, uint32_t* status,
-                                    unsigned long long* nz_out,
-                                    int64_t T, int64_t B, int64_t Cin, int64_t Cout, int64_t Coutp,
-                                    int64_t H, int64_t W, int64_t KH, int64_t KW, int64_t stride,
-                                    int64_t pad, int64_t pool_k, int64_t pool_stride,
-                                    int64_t pool_pad, double tau, double v_th, double v_reset,
-                                    int hard_reset, int decay_input, void* stream) {
+static int conv_stem(const float* x, const void* w_stem, const float* alpha,
+                     const float* beta, const float* v_in, float* v_out,
+                     float* out, void* out_nhwc, int64_t cp_out, uint32_t* status,
+                     unsigned long long* nz_out,
+                     int64_t T, int64_t B, int64_t Cin, int64_t Cout, int64_t Coutp,
+                     int64_t H, int64_t W, int64_t KH, int64_t KW, int64_t stride,
+                     int64_t pad, int64_t pool_k, int64_t pool_stride,
+                     int64_t pool_pad, double tau, double v_th, double v_reset,
+                     int hard_reset, int decay_input, int u8, void* stream) {
   if (!x || !w_stem || !alpha || !beta || (!out && !out_nhwc)) return (int)hipErrorInvalidValue;
   if (T <= 0 || T > 32 || B <= 0 || Cin <= 0 || Cin > 4 || Cout <= 0 || Coutp < Cout ||
       Coutp % BMS != 0 || H <= 0 || W <= 0 || KH <= 0 || KH > MAXKH || KW <= 0 || KW > 8 ||
@@ -498,7 +509,7 @@ CF_API int cf_conv_stem_lif_maxpool(const float* x, const void* w_stem, const fl
   StemArgs a;
   a.x = x; a.w = (const _Float16*)w_stem; a.alpha = alpha; a.beta = beta;
   a.v_in = v_in; a.v_out = v_out; a.out = out; a.out_nhwc = (_Float16*)out_nhwc;
-  a.cp_out = (int)cp_out; a.status = status; a.nz_out = nz_out;
+  a.cp_out = (int)cp_out; a.status = status; a.nz_out = nz_out; a.u8 = u8 ? 1 : 0;
   a.T = (int)T; a.B = (int)B; a.Cin = (int)Cin; a.Cout = (int)Cout; a.Coutp = (int)Coutp;
   a.H = (int)H; a.W = (int)W; a.KH = (int)KH; a.pad = (int)pad;
   a.Hc = (int)Hc; a.Wc = (int)Wc; a.Hp = (int)Hp; a.Wp = (int)Wp;
@@ -510,4 +521,33 @@ CF_API int cf_conv_stem_lif_maxpool(const float* x, const void* w_stem, const fl
   if (stride == 2) launch_stem_s<2>(a, lm, grid, st);
   else launch_stem_s<1>(a, lm, grid, st);
   return (int)hipGetLastError();
+}
+
+CF_API int cf_conv_stem_lif_maxpool(const float* x, const void* w_stem, const float* alpha,
+                                    const float* beta, const float* v_in, float* v_out,
+                                    float* out, void* out_nhwc, int64_t cp_out, uint32_t* status,
+                                    unsigned long long* nz_out,
+                                    int64_t T, int64_t B, int64_t Cin, int64_t Cout, int64_t Coutp,
+                                    int64_t H, int64_t W, int64_t KH, int64_t KW, int64_t stride,
+                                    int64_t pad, int64_t pool_k, int64_t pool_stride,
+                                    int64_t pool_pad, double tau, double v_th, double v_reset,
+                                    int hard_reset, int decay_input, void* stream) {
+  return conv_stem(x, w_stem, alpha, beta, v_in, v_out, out, out_nhwc, cp_out, status, nz_out, T,
+                   B, Cin, Cout, Coutp, H, W, KH, KW, stride, pad, pool_k, pool_stride, pool_pad,
+                   tau, v_th, v_reset, hard_reset, decay_input, 0, stream);
+}
+
+CF_API int cf_conv_stem_lif_maxpool_u8(const float* x, const void* w_stem, const float* alpha,
+                                       const float* beta, const float* v_in, float* v_out,
+                                       float* out, void* out_copy, int64_t cp_out,
+                                       uint32_t* status, unsigned long long* nz_out, int64_t T,
+                                       int64_t B, int64_t Cin, int64_t Cout, int64_t Coutp,
+                                       int64_t H, int64_t W, int64_t KH, int64_t KW,
+                                       int64_t stride, int64_t pad, int64_t pool_k,
+                                       int64_t pool_stride, int64_t pool_pad, double tau,
+                                       double v_th, double v_reset, int hard_reset,
+                                       int decay_input, void* stream) {
+  return conv_stem(x, w_stem, alpha, beta, v_in, v_out, out, out_copy, cp_out, status, nz_out, T,
+                   B, Cin, Cout, Coutp, H, W, KH, KW, stride, pad, pool_k, pool_stride, pool_pad,
+                   tau, v_th, v_reset, hard_reset, decay_input, 1, stream);
 }

@@ -162,20 +162,22 @@ __global__ __launch_bounds__(256) void scan_nhwc_kernel(
 // view of a fused conv output that was kept only as its NHWC copy.  A block
 // moves 64 pixels x 32 channels through LDS (reads: 64-byte runs per pixel;
 // writes: 256-byte runs per channel).
+// XT: the copy's element, fp16 or one byte per channel (uint8_t).
+template <typename XT>
 __global__ __launch_bounds__(256) void nhwc_to_nchw_kernel(
-    const _Float16* __restrict__ xp, float* __restrict__ out, int64_t C, int64_t HW, int64_t cp) {
+    const XT* __restrict__ xp, float* __restrict__ out, int64_t C, int64_t HW, int64_t cp) {
   __shared__ float tile[CC][PX + 1];
   const int tid = threadIdx.x;
   const int64_t n = blockIdx.z;
   const int64_t hw0 = (int64_t)blockIdx.x * PX;
   const int64_t c0 = (int64_t)blockIdx.y * CC;
   {
-    // read: 4 threads per pixel, 8 channels (16 bytes) each
+    // read: 4 threads per pixel, 8 channels (16 or 8 bytes) each
     const int px = tid / 4, part = tid % 4;
-    typedef _Float16 h8 __attribute__((ext_vector_type(8)));
-    h8 v = {};
+    typedef XT x8 __attribute__((ext_vector_type(8)));
+    x8 v = {};
     if (hw0 + px < HW && c0 + part * 8 < cp)
-      v = *reinterpret_cast<const h8*>(xp + ((n * HW + hw0 + px) * cp + c0 + part * 8));
+      v = *reinterpret_cast<const x8*>(xp + ((n * HW + hw0 + px) * cp + c0 + part * 8));
 #pragma unroll
     for (int j = 0; j < 8; ++j) tile[part * 8 + j][px] = (float)v[j];
   }
@@ -196,23 +198,24 @@ __global__ __launch_bounds__(256) void nhwc_to_nchw_kernel(
 // The copies this reads hold integers (spikes, SEW sums), whose fp32 sum is
 // exact in any order.  Block (n, 512-channel slice); a thread sums two
 // adjacent channels (one 4-byte load per pixel, 1 KB per pixel per block).
+template <typename XT>
 __global__ __launch_bounds__(256) void global_avgpool_nhwc_kernel(
-    const _Float16* __restrict__ xp, const CfOutDesc* desc, float* __restrict__ out, int64_t HW,
+    const XT* __restrict__ xp, const CfOutDesc* desc, float* __restrict__ out, int64_t HW,
     int C, int cp, float factor) {
   // Workgroup: image n, 64 channels; thread (g, j) sums channels c, c + 1
   // (c = 64 * blockIdx.y + 2 j) over pixels g, g + 8, ...; the eight
   // partial sums meet in LDS.  The copy's values are small integers, so
   // every partial sum is exact and the order of the additions does not
   // change the result.
-  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  typedef XT h2 __attribute__((ext_vector_type(2)));
   __shared__ float red[8][64];
   const int64_t n = blockIdx.x;
   const int g = (int)threadIdx.x >> 5, j = (int)threadIdx.x & 31;
   const int c = (int)blockIdx.y * 64 + 2 * j;
-  const _Float16* base = cf_copy_source(desc, xp);   // nullptr: all zero
+  const XT* base = cf_copy_source(desc, xp);   // nullptr: all zero
   float s0 = 0.0f, s1 = 0.0f;
   if (base != nullptr && c < C) {
-    const _Float16* src = base + n * HW * cp + c;
+    const XT* src = base + n * HW * cp + c;
 #pragma unroll 4
     for (int64_t p = g; p < HW; p += 8) {
       const h2 v = *reinterpret_cast<const h2*>(src + p * cp);
@@ -488,28 +491,79 @@ CF_API int cf_scan_nhwc(const void* xp, int64_t NB, int64_t H, int64_t W, int64_
   return (int)hipGetLastError();
 }
 
-CF_API int cf_nhwc_to_nchw(const void* xp, float* out, int64_t NB, int64_t C, int64_t H,
-                           int64_t W, int64_t cp, void* stream) {
+template <typename XT>
+static int nhwc_to_nchw(const void* xp, float* out, int64_t NB, int64_t C, int64_t H, int64_t W,
+                        int64_t cp, void* stream) {
   if (!xp || !out || NB < 0 || C <= 0 || H <= 0 || W <= 0 || cp < C || cp % 8 != 0 || NB > 65535)
     return (int)hipErrorInvalidValue;
   if (NB == 0) return 0;
   const int64_t HW = H * W;
   dim3 grid(cf_blocks(HW, PX), (unsigned)((C + CC - 1) / CC), (unsigned)NB);
-  hipLaunchKernelGGL(nhwc_to_nchw_kernel, grid, dim3(256), 0, (hipStream_t)stream,
-                     (const _Float16*)xp, out, C, HW, cp);
+  hipLaunchKernelGGL(nhwc_to_nchw_kernel<XT>, grid, dim3(256), 0, (hipStream_t)stream,
+                     (const XT*)xp, out, C, HW, cp);
   return (int)hipGetLastError();
 }
 
-CF_API int cf_global_avgpool_nhwc(const void* xp, const void* desc, float* out, int64_t NB,
-                                  int64_t HW, int64_t C, int64_t cp, void* stream) {
+CF_API int cf_nhwc_to_nchw(const void* xp, float* out, int64_t NB, int64_t C, int64_t H,
+                           int64_t W, int64_t cp, void* stream) {
+  return nhwc_to_nchw<_Float16>(xp, out, NB, C, H, W, cp, stream);
+}
+
+CF_API int cf_nhwc_to_nchw_u8(const void* xp, float* out, int64_t NB, int64_t C, int64_t H,
+                              int64_t W, int64_t cp, void* stream) {
+  return nhwc_to_nchw<uint8_t>(xp, out, NB, C, H, W, cp, stream);
+}
+
+template <typename XT>
+static int global_avgpool_nhwc(const void* xp, const void* desc, float* out, int64_t NB,
+                               int64_t HW, int64_t C, int64_t cp, void* stream) {
   if (!xp || !out || NB < 0 || HW <= 0 || C <= 0 || cp < C || cp % 8 != 0 || NB > INT32_MAX ||
       NB * HW * cp > ((int64_t)1 << 40))
     return (int)hipErrorInvalidValue;
   if (NB == 0) return 0;
   const float factor = 1.0f / (float)HW;
-  hipLaunchKernelGGL(global_avgpool_nhwc_kernel, dim3((unsigned)NB, (unsigned)((C + 63) / 64)),
-                     dim3(256), 0, (hipStream_t)stream, (const _Float16*)xp,
-                     (const CfOutDesc*)desc, out, HW, (int)C, (int)cp, factor);
+  hipLaunchKernelGGL(global_avgpool_nhwc_kernel<XT>,
+                     dim3((unsigned)NB, (unsigned)((C + 63) / 64)), dim3(256), 0,
+                     (hipStream_t)stream, (const XT*)xp, (const CfOutDesc*)desc, out, HW, (int)C,
+                     (int)cp, factor);
+  return (int)hipGetLastError();
+}
+
+CF_API int cf_global_avgpool_nhwc(const void* xp, const void* desc, float* out, int64_t NB,
+                                  int64_t HW, int64_t C, int64_t cp, void* stream) {
+  return global_avgpool_nhwc<_Float16>(xp, desc, out, NB, HW, C, cp, stream);
+}
+
+CF_API int cf_global_avgpool_nhwc_u8(const void* xp, const void* desc, float* out, int64_t NB,
+                                     int64_t HW, int64_t C, int64_t cp, void* stream) {
+  return global_avgpool_nhwc<uint8_t>(xp, desc, out, NB, HW, C, cp, stream);
+}
+
+// One-byte copy -> fp16 copy of the same layout (n elements, a multiple of
+// 8): for the readers that take fp16 copies only.  Every byte value is exact
+// in fp16.
+__global__ __launch_bounds__(256) void copy_u8_to_f16_kernel(const uint8_t* __restrict__ src,
+                                                             _Float16* __restrict__ dst,
+                                                             int64_t n8) {
+  typedef uint8_t u8v8 __attribute__((ext_vector_type(8)));
+  typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n8;
+       i += (int64_t)gridDim.x * 256) {
+    const u8v8 v = *reinterpret_cast<const u8v8*>(src + 8 * i);
+    h8v h;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) h[j] = (_Float16)(float)v[j];
+    *reinterpret_cast<h8v*>(dst + 8 * i) = h;
+  }
+}
+
+CF_API int cf_copy_u8_to_f16(const void* src, void* dst, int64_t n, void* stream) {
+  if (!src || !dst || n < 0 || n % 8 != 0) return (int)hipErrorInvalidValue;
+  if (n == 0) return 0;
+  const int64_t n8 = n / 8;
+  const unsigned grid = (unsigned)((n8 + 255) / 256 < 8192 ? (n8 + 255) / 256 : 8192);
+  hipLaunchKernelGGL(copy_u8_to_f16_kernel, dim3(grid), dim3(256), 0, (hipStream_t)stream,
+                     (const uint8_t*)src, (_Float16*)dst, n8);
   return (int)hipGetLastError();
 }
 

@@ -784,7 +784,7 @@ class FusedGlobalAvgPool(nn.Module):
         nb = 1
         for d in lead:
             nb *= int(d)
-        xp = shadow_of(x, (nb, H, W, pad32(C)), resolve=False) if x.is_cuda else None
+        xp = shadow_of(x, (nb, H, W, pad32(C)), resolve=False, u8_ok=True) if x.is_cuda else None
         if xp is not None:
             return global_avgpool_nhwc(xp, C, desc=desc_of(x)).view(*lead, C, 1, 1)
         self.fallback_calls += 1

@@ -11,6 +11,7 @@ buffer, prescan buffers and the nonzero counter.
 """
 from __future__ import annotations
 
+import os
 from typing import Optional
 
 import torch
@@ -226,6 +227,40 @@ def avgpool2x2_lif(x: torch.Tensor, v_in: Optional[torch.Tensor] = None, *, tau=
 # Prescan
 # ---------------------------------------------------------------------------
 
+# Element of the NHWC spike copies fused layers exchange: "f16" (two bytes
+# per channel) or "u8" (one byte; the copies hold integers 0..255: spikes,
+# SEW sums).  The halo convolutions (single and paired), the stem, the head
+# average pool and materialisation read and write byte copies natively;
+# every other reader gets the copy widened to fp16 (cf_copy_u8_to_f16,
+# counted in U8_WIDENED).  Results are the same bit for bit in both formats.
+SPIKE_COPY = os.environ.get("CATFUSE_SPIKE_COPY", "f16")
+U8_WIDENED = [0]
+
+
+def set_spike_copy(fmt: str) -> None:
+    """Select the spike-copy format of the fused layers that produce copies
+    from now on: "f16" or "u8"."""
+    global SPIKE_COPY
+    if fmt not in ("f16", "u8"):
+        raise ValueError("spike copy format must be 'f16' or 'u8'")
+    SPIKE_COPY = fmt
+
+
+def spike_copy() -> str:
+    return SPIKE_COPY
+
+
+def _widen(x: torch.Tensor, t: torch.Tensor) -> torch.Tensor:
+    """x's byte copy t (resolved first) as a new fp16 copy of the same
+    layout, for a reader that takes fp16 copies only."""
+    _resolve(x, t)
+    w = torch.empty(t.shape, dtype=torch.float16, device=t.device)
+    check(_hip.lib().cf_copy_u8_to_f16(ptr(t), ptr(w), t.numel(), _hip.stream(t.device)),
+          "cf_copy_u8_to_f16")
+    U8_WIDENED[0] += 1
+    return w
+
+
 def pad32(c: int) -> int:
     return ((c + 31) // 32) * 32
 
@@ -329,6 +364,8 @@ class NHWCSpikes(_LazyTensor):
             nhwc = self._cf_nhwc[0]
             _resolve(self, nhwc)
             cp = nhwc.shape[-1]
+            if nhwc.dtype == torch.uint8 and self.__dict__.get("_cf_tokens", False):
+                nhwc = _widen(self, nhwc)
             if self.__dict__.get("_cf_tokens", False):
                 # token-major [..., N, C]: a cast of the copy, dropping padding
                 C = self.shape[-1]
@@ -337,9 +374,10 @@ class NHWCSpikes(_LazyTensor):
                                                   _hip.stream(self.device)), "cf_tokens_to_f32")
                 return
             T, B, C, H, W = self.shape
-            check(_hip.lib().cf_nhwc_to_nchw(nhwc.data_ptr(), self.data_ptr(), T * B, C, H, W,
-                                             cp, _hip.stream(self.device)),
-                  "cf_nhwc_to_nchw")
+            fn = (_hip.lib().cf_nhwc_to_nchw_u8 if nhwc.dtype == torch.uint8
+                  else _hip.lib().cf_nhwc_to_nchw)
+            check(fn(nhwc.data_ptr(), self.data_ptr(), T * B, C, H, W, cp,
+                     _hip.stream(self.device)), "cf_nhwc_to_nchw")
 
 
 class ChannelState(_LazyTensor):
@@ -467,6 +505,8 @@ def token_shadow(x: torch.Tensor, cp: int, resolve: bool = True) -> Optional[tor
     if (ver != x._version or t.device != x.device or t.shape[-1] != cp
             or t.numel() != rows * cp):
         return None
+    if t.dtype == torch.uint8:
+        return _widen(x, t).reshape(rows, cp)
     if resolve:
         _resolve(x, t)
     return t.reshape(rows, cp)
@@ -496,17 +536,23 @@ def attach_shadow(out: torch.Tensor, nhwc: torch.Tensor) -> None:
     out._cf_nhwc = (nhwc, out._version)
 
 
-def shadow_of(x: torch.Tensor, shape, resolve: bool = True) -> Optional[torch.Tensor]:
-    """The current fp16 NHWC copy of x with the given shape, or None.  With
+def shadow_of(x: torch.Tensor, shape, resolve: bool = True,
+              u8_ok: bool = False) -> Optional[torch.Tensor]:
+    """The current NHWC copy of x with the given shape, or None.  With
     resolve (the default) a copy its producer did not write (output
     descriptor: all zero, or an alias) is filled first; a caller that reads
-    the copy through its descriptor (desc_of) passes resolve=False."""
+    the copy through its descriptor (desc_of) passes resolve=False.  A byte
+    copy is returned as it is to a caller that reads byte copies (u8_ok),
+    else widened to a new fp16 copy (resolved first: x then has no
+    descriptor)."""
     sh = getattr(x, "_cf_nhwc", None)
     if sh is None:
         return None
     t, ver = sh
     if ver != x._version or tuple(t.shape) != tuple(shape) or t.device != x.device:
         return None
+    if t.dtype == torch.uint8 and not u8_ok:
+        return _widen(x, t)
     if resolve:
         _resolve(x, t)
     return t
@@ -655,16 +701,19 @@ def scan_nhwc(xp: torch.Tensor, C: int, *, group_size: int, threshold=1e-6,
 
 def global_avgpool_nhwc(xp: torch.Tensor, C: int, out: Optional[torch.Tensor] = None,
                         desc: Optional[torch.Tensor] = None):
-    """xp fp16 NHWC [NB, H, W, cp] -> fp32 [NB, C]: the mean over H, W
-    (AdaptiveAvgPool2d((1, 1)) of the fp32 tensor the copy stands for);
-    desc: the copy's output descriptor when its producer kept one."""
-    require_gpu_tensor(xp, "xp", dtype=torch.float16)
+    """xp NHWC copy [NB, H, W, cp] (fp16 or one byte per channel) -> fp32
+    [NB, C]: the mean over H, W (AdaptiveAvgPool2d((1, 1)) of the fp32
+    tensor the copy stands for); desc: the copy's output descriptor when its
+    producer kept one."""
+    u8 = xp.dtype == torch.uint8
+    require_gpu_tensor(xp, "xp", dtype=torch.uint8 if u8 else torch.float16)
     NB, H, W, cp = xp.shape
     y = out if out is not None else torch.empty((NB, C), dtype=torch.float32, device=xp.device)
     ev = _t0()
-    check(_hip.lib().cf_global_avgpool_nhwc(ptr(xp), ptr(desc), ptr(y), NB, H * W, C, cp,
-                                            _hip.stream(xp.device)), "cf_global_avgpool_nhwc")
-    _t1("global_avgpool_nhwc", ev, nbytes=2 * NB * H * W * C + 4 * NB * C)
+    fn = _hip.lib().cf_global_avgpool_nhwc_u8 if u8 else _hip.lib().cf_global_avgpool_nhwc
+    check(fn(ptr(xp), ptr(desc), ptr(y), NB, H * W, C, cp, _hip.stream(xp.device)),
+          "cf_global_avgpool_nhwc")
+    _t1("global_avgpool_nhwc", ev, nbytes=xp.element_size() * NB * H * W * C + 4 * NB * C)
     return y
 
 
@@ -971,6 +1020,15 @@ class ConvLIFRunner:
         hold = v_out is not None and v_in is None
         return (1 if silent else 0) | (2 if hold else 0), (v_final if hold else None)
 
+    def halo_lean_ok(self, T, B, Ho, Wo) -> bool:
+        """Whether a launch of this layer at output size Ho x Wo runs the
+        halo kernel (3x3, or 1x1 over maps of at least 4x4; stride 1 or 2),
+        which the byte-copy path needs."""
+        k_ok = ((self.KH, self.KW) == (3, 3)
+                or ((self.KH, self.KW) == (1, 1) and Ho >= 4 and Wo >= 4))
+        return (k_ok and self.stride in (1, 2) and self.padding <= 2
+                and T * B * self.Cout * Ho * Wo <= 2 ** 31 - 1)
+
     def out_hw(self, H, W):
         return ((H + 2 * self.padding - self.KH) // self.stride + 1,
                 (W + 2 * self.padding - self.KW) // self.stride + 1)
@@ -1034,9 +1092,21 @@ class ConvLIFRunner:
             if sparse is not None and (sparse["block_h"], sparse["block_w"]) != (8, 8):
                 raise ValueError("the pooled epilogue runs on 8x8 tiles")
         gs = sparse["group_size"] if sparse is not None else 0
+        # One-byte copies: a dense-route launch of the halo kernel with the
+        # lean LIF epilogue whose input (and SEW identity) arrive as byte
+        # copies reads them as they are and writes a byte copy.
+        u8 = False
+        if (SPIKE_COPY == "u8" and sparse is None and epilogue == EPI_LIF and emit_nhwc
+                and self.Cout % 32 == 0 and self.halo_lean_ok(T, B, Ho, Wo)):
+            cand = shadow_of(x, (T * B, H, W, self.Cp), resolve=False, u8_ok=True)
+            u8 = cand is not None and cand.dtype == torch.uint8
+            if u8 and identity is not None:
+                ic = (shadow_of(identity, (T * B, Ho, Wo, pad32(self.Cout)), resolve=False,
+                                u8_ok=True) if identity_mode == ID_ADD_SPIKE else None)
+                u8 = ic is not None and ic.dtype == torch.uint8
         # the dense route reads the copy through its descriptor; SparseFlow
         # scans it, so an unwritten copy is filled first
-        xp = shadow_of(x, (T * B, H, W, self.Cp), resolve=sparse is not None)
+        xp = shadow_of(x, (T * B, H, W, self.Cp), resolve=sparse is not None, u8_ok=u8)
         x_desc = desc_of(x) if (xp is not None and sparse is None) else None
         nnz = act = None
         if xp is not None and sparse is not None:
@@ -1094,7 +1164,8 @@ class ConvLIFRunner:
                 # spike-valued identity: read its fp16 NHWC copy when current
                 # (through its descriptor: a fused layer's copy, which an
                 # output equal to it may alias)
-                id_nhwc = shadow_of(identity, (T * B, Ho, Wo, pad32(self.Cout)), resolve=False)
+                id_nhwc = shadow_of(identity, (T * B, Ho, Wo, pad32(self.Cout)), resolve=False,
+                                    u8_ok=u8)
                 if id_nhwc is not None:
                     id_desc = desc_of(identity)
                     if id_desc is None:
@@ -1108,17 +1179,19 @@ class ConvLIFRunner:
             emit_nhwc,
             lambda nhwc: lazy_output((T, B, self.Cout) + tuple(nhwc.shape[1:3]), nhwc, dev),
             "conv_mfma" + ("_sparse" if sparse is not None else ""),
-            x_desc=x_desc, id_desc=id_desc, id_nnz=id_nnz, id_keep=id_keep)
+            x_desc=x_desc, id_desc=id_desc, id_nnz=id_nnz, id_keep=id_keep, u8=u8)
         self.last_tiles = None if ag is None else (tc_buf, ag)
         self.last_order = order
         return out, v_out
 
     def _launch(self, xp, T, B, H, W, Ho, Wo, numel, nnz, ag, order, th, tw, gs, v_in, epilogue,
                 want_v_out, identity, id_nhwc, identity_mode, sparse_threshold, emit_nhwc,
-                make_lazy, timer_name, x_desc=None, id_desc=None, id_nnz=None, id_keep=()):
-        """One cf_conv_mfma launch on the staged fp16 NHWC input xp; the
-        output is make_lazy(nhwc copy) when emitting the copy (with its count
-        block attached), else an fp32 NCHW tensor.  x_desc / id_desc: output
+                make_lazy, timer_name, x_desc=None, id_desc=None, id_nnz=None, id_keep=(),
+                u8=False):
+        """One cf_conv_mfma launch on the staged fp16 NHWC input xp (u8: one
+        cf_conv_halo_u8 launch, xp, id_nhwc and the output copy one byte per
+        channel); the output is make_lazy(nhwc copy) when emitting the copy
+        (with its count block attached), else an fp32 NCHW tensor.  x_desc / id_desc: output
         descriptors of the input's / identity's copies (see cf_conv_mfma).
         When the launch may take StaticZero it gets an output descriptor of
         its own (attached to the output, with id_keep: the copies the output
@@ -1136,7 +1209,8 @@ class ConvLIFRunner:
         v_out = (torch.empty((B, self.Cout, Hs, Ws), dtype=torch.float32, device=dev)
                  if (epilogue != EPI_Z and (want_v_out or T > 2)) else None)
         cp_out = pad32(self.Cout)
-        nhwc = (torch.empty((T * B, Hs, Ws, cp_out), dtype=torch.float16, device=dev)
+        nhwc = (torch.empty((T * B, Hs, Ws, cp_out), dtype=torch.uint8 if u8 else torch.float16,
+                            device=dev)
                 if (emit_nhwc and epilogue != EPI_Z) else None)
         nz_out = None
         if nhwc is not None:
@@ -1160,16 +1234,26 @@ class ConvLIFRunner:
             # the descriptor (otherwise it always writes the copy)
             attach_desc(out, desc, id_keep)
         ev = _t0()
-        rc = _hip.lib().cf_conv_mfma(
-            ptr(xp), ptr(self.w_packed), ptr(self.alpha), ptr(self.beta), ptr(v_in), ptr(v_out),
-            out_ptr, ptr(nhwc), cp_out, ptr(identity), ptr(id_nhwc), pad32(self.Cout),
-            int(identity_mode), ptr(ag), ptr(order), ptr(nnz), ptr(nz_out),
-            ptr(x_desc), ptr(id_desc), ptr(desc), bias_info, ptr(id_nnz), numel,
-            float(sparse_threshold), T, B, self.Cp, self.Cout, self.Coutp, H, W, Ho, Wo, self.KH,
-            self.KW, self.stride, self.padding, B, th, tw, gs, int(epilogue), *self.lif,
-            _hip.stream(dev))
-        check(rc, "cf_conv_mfma")
-        copy_bytes = (2 * T * B * Hs * Ws * cp_out if nhwc is not None else 0) \
+        if u8:
+            rc = _hip.lib().cf_conv_halo_u8(
+                ptr(xp), ptr(self.w_packed), ptr(self.alpha), ptr(self.beta), ptr(v_in),
+                ptr(v_out), ptr(nhwc), cp_out, ptr(id_nhwc), pad32(self.Cout), ptr(ag),
+                ptr(order), ptr(nnz), ptr(nz_out), ptr(x_desc), ptr(id_desc), ptr(desc),
+                bias_info, ptr(id_nnz), numel, float(sparse_threshold), T, B, self.Cp, self.Cout,
+                self.Coutp, H, W, Ho, Wo, self.KH, self.stride, self.padding, gs, *self.lif,
+                _hip.stream(dev))
+            check(rc, "cf_conv_halo_u8")
+        else:
+            rc = _hip.lib().cf_conv_mfma(
+                ptr(xp), ptr(self.w_packed), ptr(self.alpha), ptr(self.beta), ptr(v_in),
+                ptr(v_out), out_ptr, ptr(nhwc), cp_out, ptr(identity), ptr(id_nhwc),
+                pad32(self.Cout), int(identity_mode), ptr(ag), ptr(order), ptr(nnz), ptr(nz_out),
+                ptr(x_desc), ptr(id_desc), ptr(desc), bias_info, ptr(id_nnz), numel,
+                float(sparse_threshold), T, B, self.Cp, self.Cout, self.Coutp, H, W, Ho, Wo,
+                self.KH, self.KW, self.stride, self.padding, B, th, tw, gs, int(epilogue),
+                *self.lif, _hip.stream(dev))
+            check(rc, "cf_conv_mfma")
+        copy_bytes = (nhwc.element_size() * T * B * Hs * Ws * cp_out if nhwc is not None else 0) \
             + (4 * T * B * Ho * Wo * self.Cout if out_ptr is not None else 0)
         state_bytes = 4 * B * Hs * Ws * self.Cout if v_out is not None else 0
         _t1(timer_name, ev, flops=2 * T * B * Ho * Wo * self.Cout * self.Cin * self.KH * self.KW,
@@ -1457,8 +1541,10 @@ class ConvLIFRunner:
         v_out = (torch.empty((B, self.Cout, Hc, Wc), dtype=torch.float32, device=dev,
                              memory_format=torch.channels_last) if want_v_out else None)
         cp_out = pad32(self.Cout)
+        u8 = emit_nhwc and SPIKE_COPY == "u8"
         if emit_nhwc:
-            nhwc = torch.empty((T * B, Hp, Wp, cp_out), dtype=torch.float16, device=dev)
+            nhwc = torch.empty((T * B, Hp, Wp, cp_out), dtype=torch.uint8 if u8 else torch.float16,
+                               device=dev)
             out = lazy_output((T, B, self.Cout, Hp, Wp), nhwc, dev)
             out_ptr = None
         else:
@@ -1466,7 +1552,9 @@ class ConvLIFRunner:
             out = torch.empty((T, B, self.Cout, Hp, Wp), dtype=torch.float32, device=dev)
             out_ptr = ptr(out)
         ev = _t0()
-        rc = _hip.lib().cf_conv_stem_lif_maxpool(
+        stem = (_hip.lib().cf_conv_stem_lif_maxpool_u8 if u8
+                else _hip.lib().cf_conv_stem_lif_maxpool)
+        rc = stem(
             ptr(x[0]), ptr(self.w_stem), ptr(self.alpha_stem), ptr(self.beta_stem), ptr(v_in),
             ptr(v_out), out_ptr, ptr(nhwc), cp_out, ptr(status_word(dev)), ptr(nz_out), T, B, C,
             self.Cout, self.Coutp, H, W, self.KH, self.KW, self.stride, self.padding, 3, 2, 1,
@@ -1513,7 +1601,11 @@ def run_halo_pair(ra: "ConvLIFRunner", rb: "ConvLIFRunner", x: torch.Tensor, v_i
     ra._ensure_packed(dev)
     rb._ensure_packed(dev)
     Ho, Wo = ra.out_hw(H, W)
-    xp = shadow_of(x, (T * B, H, W, ra.Cp), resolve=False)
+    # byte copies in, byte copies out (cf_conv_halo_pair_u8)
+    cand = (shadow_of(x, (T * B, H, W, ra.Cp), resolve=False, u8_ok=True)
+            if SPIKE_COPY == "u8" else None)
+    u8 = cand is not None and cand.dtype == torch.uint8
+    xp = shadow_of(x, (T * B, H, W, ra.Cp), resolve=False, u8_ok=u8)
     x_desc = None
     if xp is not None:
         nnz = count_of(x)
@@ -1531,7 +1623,8 @@ def run_halo_pair(ra: "ConvLIFRunner", rb: "ConvLIFRunner", x: torch.Tensor, v_i
                 raise ValueError("v_in has the wrong size")
         v_out = torch.empty((B, r.Cout, Ho, Wo), dtype=torch.float32, device=dev)
         cp = pad32(r.Cout)
-        nhwc = torch.empty((T * B, Ho, Wo, cp), dtype=torch.float16, device=dev)
+        nhwc = torch.empty((T * B, Ho, Wo, cp), dtype=torch.uint8 if u8 else torch.float16,
+                           device=dev)
         out = lazy_output((T, B, r.Cout, Ho, Wo), nhwc, dev)
         nz = r.out_counter(dev)
         r._gen[0] += 1
@@ -1547,7 +1640,8 @@ def run_halo_pair(ra: "ConvLIFRunner", rb: "ConvLIFRunner", x: torch.Tensor, v_i
     ((_, va, voa, na, cpa, nza, oa, da, ia, ca),
      (_, vb, vob, nb, cpb, nzb, ob, db, ib, cb)) = outs
     ev = _t0()
-    check(_hip.lib().cf_conv_halo_pair(
+    pair = _hip.lib().cf_conv_halo_pair_u8 if u8 else _hip.lib().cf_conv_halo_pair
+    check(pair(
         ptr(xp), ptr(nnz), ptr(x_desc), x.numel(), T, B, ra.Cp, H, W, Ho, Wo,
         ptr(ra.w_packed), ptr(ra.alpha), ptr(ra.beta), ptr(va), ptr(voa), ptr(na), cpa, ptr(nza),
         ptr(da), ia, ra.Cout, ra.Coutp, ra.padding,
@@ -1555,7 +1649,7 @@ def run_halo_pair(ra: "ConvLIFRunner", rb: "ConvLIFRunner", x: torch.Tensor, v_i
         ptr(db), ib, rb.Cout, rb.Coutp, rb.padding, *ra.lif, _hip.stream(dev)),
         "cf_conv_halo_pair")
     flops = 2 * T * B * Ho * Wo * C * (ra.Cout * 9 + rb.Cout)
-    parts = [(d, 2 * T * B * Ho * Wo * cp, 4 * B * Ho * Wo * r.Cout)
+    parts = [(d, (1 if u8 else 2) * T * B * Ho * Wo * cp, 4 * B * Ho * Wo * r.Cout)
              for d, cp, r in ((da, cpa, ra), (db, cpb, rb))]
     _t1("conv_pair", ev, flops=flops, route=None if nnz is None else _RouteProbe(nnz, parts))
     for r in (ra, rb):

@@ -404,6 +404,64 @@ int cf_conv_halo_pair(const void* x, const unsigned long long* nnz, const void* 
                       double tau, double v_th, double v_reset, int hard_reset, int decay_input,
                       void* stream);
 
+/* One-byte spike copies between fused layers.  The _u8 entry points take
+ * and write NHWC copies of one byte per channel ([T*B][H][W][cp] uint8, the
+ * same element layout as the fp16 copies, channels >= C zero): the spike
+ * values the fused layers exchange (0/1, SEW sums, any integer 0..255) are
+ * exact in a byte, and the byte copies halve the copies' HBM traffic.  The
+ * conv entry points widen each staged byte to fp16 in LDS, so their K loop,
+ * accumulation order and results are those of the fp16-copy entry points
+ * bit for bit.  Replaces the fp32 -> uint8 spike exchange motivated by
+ * tests/test_32_spike_uint8.py:16-104 (which casts fp32 spikes to uint8
+ * between layers).
+ *
+ * cf_conv_halo_u8: cf_conv_halo with the lean LIF epilogue (no fp32 output,
+ * identity only as a copy: identity_copy nullable, added to the spikes),
+ * 8x8 tiles, Cout a multiple of 32, cp_out a multiple of 8, Cp of 32;
+ * x / identity_copy / out_copy one byte per channel; other arguments as
+ * cf_conv_halo.  cf_conv_halo_pair_u8: cf_conv_halo_pair on byte copies.
+ * cf_conv_stem_lif_maxpool_u8: the stem writing its pooled output as a byte
+ * copy (out_copy).  cf_nhwc_to_nchw_u8 / cf_global_avgpool_nhwc_u8: as the
+ * fp16 forms, reading a byte copy.  cf_copy_u8_to_f16: a byte copy of n
+ * elements (a multiple of 8) widened to an fp16 copy, for readers that take
+ * fp16 copies only.  No other counterpart in the reference. */
+int cf_conv_halo_u8(const void* x, const void* w_packed, const float* alpha, const float* beta,
+                    const float* v_in, float* v_out, void* out_copy, int64_t cp_out,
+                    const void* identity_copy, int64_t cp_id, const int32_t* ag_mask,
+                    const int32_t* tile_order, const unsigned long long* nnz,
+                    unsigned long long* nz_out, const void* x_desc, const void* id_desc,
+                    void* out_desc, int bias_info, const unsigned long long* id_nnz,
+                    int64_t numel, double sparse_threshold, int64_t T, int64_t B, int64_t Cp,
+                    int64_t Cout, int64_t Coutp, int64_t H, int64_t W, int64_t Ho, int64_t Wo,
+                    int64_t ksize, int64_t stride, int64_t pad, int64_t group_size, double tau,
+                    double v_th, double v_reset, int hard_reset, int decay_input, void* stream);
+int cf_conv_halo_pair_u8(const void* x, const unsigned long long* nnz, const void* x_desc,
+                         int64_t numel, int64_t T, int64_t B, int64_t Cp, int64_t H, int64_t W,
+                         int64_t Ho, int64_t Wo,
+                         const void* w_a, const float* alpha_a, const float* beta_a,
+                         const float* v_in_a, float* v_out_a, void* out_a, int64_t cp_out_a,
+                         unsigned long long* nz_a, void* desc_a, int bias_info_a, int64_t Cout_a,
+                         int64_t Coutp_a, int64_t pad_a,
+                         const void* w_b, const float* alpha_b, const float* beta_b,
+                         const float* v_in_b, float* v_out_b, void* out_b, int64_t cp_out_b,
+                         unsigned long long* nz_b, void* desc_b, int bias_info_b, int64_t Cout_b,
+                         int64_t Coutp_b, int64_t pad_b,
+                         double tau, double v_th, double v_reset, int hard_reset,
+                         int decay_input, void* stream);
+int cf_conv_stem_lif_maxpool_u8(const float* x, const void* w_stem, const float* alpha,
+                                const float* beta, const float* v_in, float* v_out, float* out,
+                                void* out_copy, int64_t cp_out, uint32_t* status,
+                                unsigned long long* nz_out, int64_t T, int64_t B, int64_t Cin,
+                                int64_t Cout, int64_t Coutp, int64_t H, int64_t W, int64_t KH,
+                                int64_t KW, int64_t stride, int64_t pad, int64_t pool_k,
+                                int64_t pool_stride, int64_t pool_pad, double tau, double v_th,
+                                double v_reset, int hard_reset, int decay_input, void* stream);
+int cf_nhwc_to_nchw_u8(const void* xp, float* out, int64_t NB, int64_t C, int64_t H, int64_t W,
+                       int64_t cp, void* stream);
+int cf_global_avgpool_nhwc_u8(const void* xp, const void* desc, float* out, int64_t NB,
+                              int64_t HW, int64_t C, int64_t cp, void* stream);
+int cf_copy_u8_to_f16(const void* src, void* dst, int64_t n, void* stream);
+
 /* A layer's response to its BN bias alone (the StaticZero drive z =
  * 0 * alpha + beta, alpha/beta from cf_pack_conv_weights, Cout entries;
  * pool = 1: the drive of cf_conv_mfma's pooled epilogue, the 2x2 average
