@@ -732,18 +732,18 @@ def xo_as_fused_output(x):
     return y
 
 
-def _xo_layer(C_in, C_out, device, seed=0):
+def _xo_layer(C_in, C_out, device, seed=0, k=3, stride=1):
     import torch
     from catfuse_amd.implementations.base import ConvLIFParams, ConvLIFSpec
     g = torch.Generator().manual_seed(seed)
-    w = torch.randn(C_out, C_in, 3, 3, generator=g) * (2.0 / (C_in * 9)) ** 0.5
+    w = torch.randn(C_out, C_in, k, k, generator=g) * (2.0 / (C_in * k * k)) ** 0.5
     mean = torch.randn(C_out, generator=g) * 0.1
     var = torch.rand(C_out, generator=g) + 0.5
     gamma = torch.rand(C_out, generator=g) * 0.4 + 0.8
     beta = torch.randn(C_out, generator=g) * 0.1
     scale = gamma / torch.sqrt(var + 1e-5)
     shift = beta - mean * scale
-    spec = ConvLIFSpec(C_in, C_out, 3, 1, 1, has_conv_bias=False, has_bn=True, tau=2.0,
+    spec = ConvLIFSpec(C_in, C_out, k, stride, k // 2, has_conv_bias=False, has_bn=True, tau=2.0,
                        v_threshold=1.0, v_reset=0.0, decay_input=True)
     return spec, ConvLIFParams(w.to(device), None, scale.to(device), shift.to(device))
 
@@ -778,16 +778,18 @@ def _xo_time_graph(fn, calls, reps, device):
 
 
 def xo_sweep(device, rates=XO_RATES, patterns=XO_PATTERNS, shape=(4, 32, 256, 14, 14),
-             plain=False, calls=20, reps=5, seed=0):
+             plain=False, calls=20, reps=5, seed=0, k=3, stride=1, c_out=None):
     """One row per (pattern, rate): the input density and the microseconds
-    per call of every route (each checked bitwise against the others)."""
+    per call of every route (each checked bitwise against the others) of a
+    k x k / stride conv of shape's input (c_out output channels, default
+    the input's)."""
     import torch
     from catfuse_amd.implementations.dense_keep import DenseKeep
     from catfuse_amd.implementations.sparse_flow import SparseFlow
     from catfuse_amd.implementations.stream_fuse import StreamFuse
     from catfuse_amd.state import StateBuffer
     T, B, C, H, W = shape
-    spec, params = _xo_layer(C, C, device, seed)
+    spec, params = _xo_layer(C, c_out or C, device, seed, k=k, stride=stride)
     impls = {"SparseFlow": SparseFlow(sparsity_threshold=-1.0, egd=False),
              "SparseFlow-linear": SparseFlow(sparsity_threshold=-1.0, compact_tiles=False,
                                              egd=False),
@@ -800,7 +802,8 @@ def xo_sweep(device, rates=XO_RATES, patterns=XO_PATTERNS, shape=(4, 32, 256, 14
                 xc = xo_input(rate, pattern, shape, seed=seed + 1)
                 xd = xc.to(device)
                 x = xd if plain else xo_as_fused_output(xd)
-                row = {"pattern": pattern, "rate": rate,
+                row = {"pattern": pattern, "rate": rate, "k": k, "stride": stride,
+                       "shape": list(shape), "c_out": spec.out_channels,
                        "density": float(torch.count_nonzero(xc)) / xc.numel()}
                 ref = None
                 for name in XO_ROUTES:
@@ -917,7 +920,9 @@ def sf_crossover_main(args):
     import torch
     dev = torch.device("cuda", 0)
     shape = tuple(args.xo_shape)
-    rows = xo_sweep(dev, shape=shape, plain=args.xo_plain)
+    rows = xo_sweep(dev, shape=shape, plain=args.xo_plain, k=args.xo_kernel,
+                    stride=args.xo_stride, c_out=args.xo_cout,
+                    patterns=tuple(args.xo_patterns.split(",")))
     print(xo_table(rows))
     print("crossover (lowest input sparsity where SparseFlow wins):", xo_crossover(rows))
     n = sum(r["density"] > 0 for r in rows)
@@ -956,6 +961,10 @@ def main():
                     help="element of the NHWC spike copies between fused layers (one byte "
                          "per channel with u8; results are the same bit for bit)")
     ap.add_argument("--xo-shape", type=int, nargs=5, default=[4, 32, 256, 14, 14])
+    ap.add_argument("--xo-kernel", type=int, default=3, choices=[1, 3])
+    ap.add_argument("--xo-stride", type=int, default=1, choices=[1, 2])
+    ap.add_argument("--xo-cout", type=int, default=None)
+    ap.add_argument("--xo-patterns", default=",".join(XO_PATTERNS))
     ap.add_argument("--xo-plain", action="store_true",
                     help="crossover inputs as fp32 tensors (the layer packs them)")
     args = ap.parse_args()

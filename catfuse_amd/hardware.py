@@ -16,11 +16,13 @@ SparseFlow prescan and conv; None: the reference's _select_tile_sizes rule),
 sf_egd_tau_3x3 / sf_egd_tau_1x1 / sf_egd_r_min (the execution-grounded
 dispatch score gate of a SparseFlow launch, scored on the device by
 cf_compact_tiles: SparseFlow iff R >= 0.99 or R >= r_min and R * MACs per
-tile > tau; tau < 0: no score; the reference's sparseflow/config.py:48-61
+tile > tau; tau < 0: no score; tau = inf: SparseFlow refused for that kernel
+size, no scan or prescan; the reference's sparseflow/config.py:48-61
 DISPATCH_TAU_3X3 / _1X1 / DISPATCH_R_MIN).
 """
 from __future__ import annotations
 
+import math
 import os
 from dataclasses import dataclass, replace
 
@@ -85,7 +87,14 @@ A100_80GB = replace(A100_40GB, arch_name="A100 80GB", hbm_bandwidth_gbps=2039.0)
 # misclassified, each within 4% of break-even), while S = R * MACs-per-tile
 # against any single tau misclassifies 24, so the 3x3 gate is R >= 0.4 with
 # tau = 0 (the reference's V100 values, sparseflow/config.py:48-61, are
-# tau_3x3 = 1e5 and R_min = 0.15); 1x1 layers were not swept (no score).
+# tau_3x3 = 1e5 and R_min = 0.15).  1x1 layers (bench.py --workload
+# sf_crossover --xo-kernel 1: the SEW downsamples 64->128 at 56x56, 128->256
+# at 28x28, 256->512 at 14x14, stride 2, and a stride-1 256->256 pointwise
+# conv at 14x14; same patterns, rates 0.001-0.5, 140 rows): forced SparseFlow
+# takes 1.42-2.11x the dense route's time in every row (one tap leaves little
+# MFMA work to skip, against the same activity scan, prescan and compaction),
+# so the MI355X profile refuses SparseFlow for 1x1 convs (tau_1x1 = inf: no
+# scan, no prescan; the reference's V100 tau_1x1 is 1e4, config.py:51-54).
 # All-zero inputs take StaticZero on every route.  SparseFlow tiles are 8x8
 # at every size: the 8x16 tile of the reference's rule (>= 3136 output
 # pixels) needs the kernel's full register file (one workgroup per CU).  The
@@ -96,7 +105,7 @@ MI355X = HardwareProfile(
     default_K_memory_bound=8, default_K_compute_bound=4,
     notes="gfx950; fused StreamFuse conv as the dense path, device-side routing.",
     gcn_arch="gfx950", peak_fp16_tflops=2500.0, sf_sparsity_threshold=1.0,
-    dense_impl="StreamFuse", sf_tile=(8, 8), sf_egd_tau_3x3=0.0, sf_egd_tau_1x1=-1.0,
+    dense_impl="StreamFuse", sf_tile=(8, 8), sf_egd_tau_3x3=0.0, sf_egd_tau_1x1=math.inf,
     sf_egd_r_min=0.4)
 
 DEFAULT = V100_PCIE_32GB

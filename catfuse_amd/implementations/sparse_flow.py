@@ -30,6 +30,8 @@ input's count block.
 """
 from __future__ import annotations
 
+import math
+
 import torch
 
 from catfuse_amd.hardware import runtime_profile
@@ -44,7 +46,9 @@ class SparseFlow(HipConvImplementation):
     def __init__(self, sparsity_threshold: float = None, compact_tiles: bool = True,
                  egd: bool = True):
         """egd: gate the SparseFlow route with the profile's dispatch score
-        (tau per kernel size; no gate when the profile's tau is negative)."""
+        (tau per kernel size; no gate when the profile's tau is negative; an
+        infinite tau refuses SparseFlow for that kernel size outright, so
+        its layers run no activity scan or prescan)."""
         super().__init__()
         prof = runtime_profile()
         self.sparsity_threshold = (prof.sf_sparsity_threshold
@@ -67,11 +71,20 @@ class SparseFlow(HipConvImplementation):
         return dict(block_h=bh, block_w=bw, group_size=choose_group_size(spec.in_channels),
                     compact=self.compact_tiles, egd=gate)
 
+    def refused(self, spec) -> bool:
+        """Whether the profile refuses SparseFlow for this kernel size."""
+        if self.egd is None:
+            return False
+        return math.isinf(self.egd.get(spec.kernel_size, self.egd[3])[0])
+
     def route_geometry(self, spec, H_in, W_in):
         """Prescan geometry for the conv, or None when the threshold (>= 1)
-        can never select the SparseFlow route: no activity scan or prescan
-        then, only the StaticZero check."""
-        return self.geometry(spec, H_in, W_in) if self.sparsity_threshold < 1.0 else None
+        or the profile's refusal for the kernel size can never select the
+        SparseFlow route: no activity scan or prescan then, only the
+        StaticZero check."""
+        if self.sparsity_threshold >= 1.0 or self.refused(spec):
+            return None
+        return self.geometry(spec, H_in, W_in)
 
     def forward(self, x, spec, params, state):
         self.check_input(x, spec)

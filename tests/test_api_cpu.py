@@ -476,3 +476,19 @@ def test_substitute_bottlenecks(downsample):
     assert stats["patterns_matched"].get("CTFSpikingBottleneck") == 1
     assert stats["fused_lif_nodes"] == stats["total_lif_nodes"] == 3
     assert blk.has_downsample == downsample
+
+
+def test_mi355x_profile_refuses_sparseflow_for_1x1(monkeypatch):
+    """The measured gfx950 crossover (SparseFlow 1.42-2.11x slower than the
+    dense route on every 1x1 row) makes the MI355X profile refuse
+    SparseFlow for 1x1 convs: no scan/prescan geometry even with the
+    sparsity threshold lowered; 3x3 layers keep their gate (tau 0, R_min 0.4)."""
+    monkeypatch.setenv("CATFUSE_SF_SPARSITY_THRESHOLD", "0.7")
+    sf = SparseFlow()
+    assert math.isinf(hardware.MI355X.sf_egd_tau_1x1)
+    kw = dict(has_conv_bias=False, has_bn=True, tau=2.0, v_threshold=1.0, v_reset=0.0,
+              decay_input=True)
+    assert sf.route_geometry(ConvLIFSpec(64, 128, 1, 2, 0, **kw), 56, 56) is None
+    assert sf.route_geometry(ConvLIFSpec(256, 256, 1, 1, 0, **kw), 14, 14) is None
+    g = sf.route_geometry(ConvLIFSpec(64, 64, 3, 1, 1, **kw), 56, 56)
+    assert g is not None and g["egd"] == (0.0, 0.4) and (g["block_h"], g["block_w"]) == (8, 8)
