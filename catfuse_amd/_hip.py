@@ -41,6 +41,9 @@ _SIGNATURES = {
     "cf_spike_attention_lif": [_P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, c_int,
                                _I, _I, _I, _I,
                                _I, c_double, c_double, c_double, c_double, c_int, c_int, _P],
+    "cf_spike_attention_kv_lif": [_P, _P, _P, _I, _I, _I, _I, _P, _I, _P, _P, _P, _P, _P, _P,
+                                  c_int, _I, _I, _I, _I, _I, c_double, c_double, c_double,
+                                  c_double, c_int, c_int, _P],
     "cf_route_from_nnz": [_P, _I, c_double, _P, _P],
     "cf_zero_counter": [_P, _P],
     "cf_prescan_tiles": [_P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _P, _P, _P],

@@ -775,24 +775,46 @@ def maxpool_nhwc(x: torch.Tensor, kernel_size: int, stride: int, padding: int,
     return y
 
 
+# The single-pass attention kernel's shapes (one workgroup per image and
+# head holds every token): head dim 32, at most 256 tokens.  Other shapes
+# (head dim 64, longer token rows) take the two-pass kernels.
+ATTN_ONE_PASS_DIM = 32
+ATTN_ONE_PASS_TOKENS = 256
+
+
+def attention_covers(head_dim: int, N: int) -> bool:
+    """Whether the hand-written attention kernels cover the shape."""
+    return head_dim in (32, 64) and N < 65536 and head_dim * N < 2 ** 24
+
+
 def spike_attention_lif(qkv: torch.Tensor, T: int, B: int, N: int, heads: int, offsets,
                         scale: float, tau=2.0, v_threshold=1.0, v_reset=0.0, decay_input=True,
                         v_in: Optional[torch.Tensor] = None, want_v_out=True,
                         nz_out: Optional[torch.Tensor] = None, gen_cell: Optional[list] = None,
-                        nnz: Optional[torch.Tensor] = None):
+                        nnz: Optional[torch.Tensor] = None, head_dim: int = 32,
+                        two_pass: Optional[bool] = None):
     """Spikformer's SSA core on the fp16 token copy qkv [T*B*N, pitch] that
     holds Q, K, V at channel offsets (qoff, koff, voff) (head h at
-    off + 32h ..): LIF_T(((Q K^T) V) * scale) per head, evaluated as
+    off + head_dim h ..): LIF_T(((Q K^T) V) * scale) per head, evaluated as
     Q (K^T V) on the matrix cores; nnz: the copy's count block (a zero count
-    skips the products: z = 0).  Returns (TokenSpikes [T, B, N, heads*32],
-    carrying the count block nz_out when it and gen_cell are given, so the
-    next fused linear routes on it; v_out [B, N, heads*32] or None)."""
+    skips the products: z = 0).  Head dim 32 with at most 256 tokens runs the
+    single-pass kernel, other shapes (head dim 64, longer rows) the two-pass
+    one (two_pass forces the choice; both give the same values).  Returns
+    (TokenSpikes [T, B, N, heads*head_dim], carrying the count block nz_out
+    when it and gen_cell are given, so the next fused linear routes on it;
+    v_out [B, N, heads*head_dim] or None)."""
     require_gpu_tensor(qkv, "qkv", dtype=torch.float16)
     _require_block(nz_out)
     _require_block(nnz)
+    if not attention_covers(head_dim, N):
+        raise ValueError(f"no attention kernel for head dim {head_dim} and {N} tokens")
+    if two_pass is None:
+        two_pass = head_dim != ATTN_ONE_PASS_DIM or N > ATTN_ONE_PASS_TOKENS
+    elif not two_pass and (head_dim != ATTN_ONE_PASS_DIM or N > ATTN_ONE_PASS_TOKENS):
+        raise ValueError("the single-pass attention kernel needs head dim 32, N <= 256")
     dev = qkv.device
     pitch = qkv.shape[-1]
-    C = heads * 32
+    C = heads * head_dim
     cp = pad32(C)
     if qkv.numel() != T * B * N * pitch:
         raise ValueError("qkv does not hold T * B * N tokens")
@@ -815,11 +837,18 @@ def spike_attention_lif(qkv: torch.Tensor, T: int, B: int, N: int, heads: int, o
             v_uniform = r[0] if v_out is not None else None
             zero_info = 1 | (2 if v_uniform is not None else 0)
     ev = _t0()
-    check(_hip.lib().cf_spike_attention_lif(
-        ptr(qkv), ptr(qkv), ptr(qkv), qoff, koff, voff, pitch, ptr(copy), cp, ptr(v_in),
-        ptr(v_out), ptr(nnz), ptr(nz_out), ptr(desc), zero_info, T, B, N, heads, 32,
-        float(scale), *lif, _hip.stream(dev)), "cf_spike_attention_lif")
-    _t1("spike_attention", ev, flops=4 * T * B * heads * N * 32 * 32,
+    if two_pass:
+        kv_ws = torch.empty((T * B * heads, head_dim, head_dim), dtype=torch.float32, device=dev)
+        check(_hip.lib().cf_spike_attention_kv_lif(
+            ptr(qkv), ptr(qkv), ptr(qkv), qoff, koff, voff, pitch, ptr(copy), cp, ptr(v_in),
+            ptr(v_out), ptr(kv_ws), ptr(nnz), ptr(nz_out), ptr(desc), zero_info, T, B, N, heads,
+            head_dim, float(scale), *lif, _hip.stream(dev)), "cf_spike_attention_kv_lif")
+    else:
+        check(_hip.lib().cf_spike_attention_lif(
+            ptr(qkv), ptr(qkv), ptr(qkv), qoff, koff, voff, pitch, ptr(copy), cp, ptr(v_in),
+            ptr(v_out), ptr(nnz), ptr(nz_out), ptr(desc), zero_info, T, B, N, heads, 32,
+            float(scale), *lif, _hip.stream(dev)), "cf_spike_attention_lif")
+    _t1("spike_attention", ev, flops=4 * T * B * heads * N * head_dim * head_dim,
         nbytes=2 * T * B * N * 3 * C + 2 * T * B * N * cp,
         route=None if nnz is None else _RouteProbe(
             nnz, [(desc, 2 * T * B * N * cp, 4 * B * N * C if v_out is not None else 0)]))

@@ -27,6 +27,7 @@ from catfuse_amd.runtime import (ConvLIFRunner, attach_desc, count_block, count_
                                  keep_of, lazy_tokens, lif_multistep,
                                  maxpool_nhwc,
                                  pad32, shadow_of, spike_attention_lif, token_membrane,
+                                 attention_covers,
                                  token_shadow, token_view)
 from catfuse_amd.state import StateBuffer
 
@@ -152,16 +153,15 @@ class CTFSpikformerSSA(CTFPattern):
     attention core with attn_lif (one launch), fused proj Linear-BN1d-LIF
     (+ the block's residual).
 
-    The core kernel (cf_spike_attention_lif) covers a head dim of 32 and up
-    to ATTN_MAX_TOKENS tokens per image.  Other shapes (e.g. head dim 64, or
-    a 56 x 56 token grid) evaluate the same product, Q (K^T V), as two
-    library GEMMs in float64 on the GPU (exact: the operands are spikes and
-    every partial sum an integer), round once by the scale in fp32 and run
-    the LIF in cf_lif_multistep: the same values the kernel produces.  Such
-    calls are counted in `gemm_core_calls`."""
-
-    ATTN_HEAD_DIM = 32
-    ATTN_MAX_TOKENS = 256
+    The core kernels cover head dims 32 and 64 at any token count below
+    65,536 (cf_spike_attention_lif: head dim 32, up to 256 tokens, one
+    launch; cf_spike_attention_kv_lif: the others, K^T V then Q (K^T V), e.g.
+    spikformer_cifar_tiny's head dim 64 or a 56 x 56 token grid).  Other
+    head dims evaluate the same product as two library GEMMs in float64 on
+    the GPU (exact: the operands are spikes and every partial sum an
+    integer), round once by the scale in fp32 and run the LIF in
+    cf_lif_multistep: the same values the kernels produce.  Such calls are
+    counted in `gemm_core_calls`."""
 
     def __init__(self, dim, num_heads, scale, qkv: FusedLinearBNLIF, proj: FusedLinearBNLIF,
                  attn_lif_params: dict):
@@ -180,7 +180,7 @@ class CTFSpikformerSSA(CTFPattern):
         self.gemm_core_calls = 0
 
     def kernel_covers(self, N: int) -> bool:
-        return self.head_dim == self.ATTN_HEAD_DIM and N <= self.ATTN_MAX_TOKENS
+        return attention_covers(self.head_dim, N)
 
     def forward(self, x, residual=None):
         T, B, N, C = x.shape
@@ -199,7 +199,8 @@ class CTFSpikformerSSA(CTFPattern):
                                        tau=lp["tau"], v_threshold=lp["v_threshold"],
                                        v_reset=lp["v_reset"], decay_input=lp["decay_input"],
                                        v_in=v_in, nz_out=self._attn_block(x.device),
-                                       gen_cell=self._attn_gen, nnz=nnz)
+                                       gen_cell=self._attn_gen, nnz=nnz,
+                                       head_dim=self.head_dim)
         else:
             a, v = self._gemm_core(qkv, v_in)
         self.attn_state.set(v)

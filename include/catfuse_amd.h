@@ -181,6 +181,27 @@ int cf_spike_attention_lif(const void* q, const void* k, const void* v, int64_t 
                            double scale, double tau, double v_th, double v_reset, int hard_reset,
                            int decay_input, void* stream);
 
+/* The same core for any token count (N < 65536, head_dim * N < 2^24) and
+ * head_dim 32 or 64, in two launches: K^T V of every (t, b, head) reduced
+ * over all N tokens into the caller's workspace kv_ws (fp32
+ * [T*B*heads][head_dim][head_dim], exact integers), then per (b, head,
+ * 128-token block) Y = Q (K^T V) on the matrix cores with K^T V as two exact
+ * fp16 limbs, z = Y * scale (one rounding), the LIF over T.  Same values as
+ * cf_spike_attention_lif where both apply (the exact Y, the same rounding);
+ * other arguments, layouts (head h at channels off + h*head_dim), routes
+ * and descriptors as cf_spike_attention_lif.  Replaces the same reference
+ * interfaces, for the shapes of models/spikformer_github.py:332-350
+ * (head_dim 64) and its two-pool patch splitter (:240-242, 3,136 tokens at
+ * 224 x 224). */
+int cf_spike_attention_kv_lif(const void* q, const void* k, const void* v, int64_t qoff,
+                              int64_t koff, int64_t voff, int64_t pitch, void* out,
+                              int64_t cp_out, const float* v_in, float* v_out, float* kv_ws,
+                              const unsigned long long* nnz, unsigned long long* nz_out,
+                              void* out_desc, int zero_info, int64_t T, int64_t B, int64_t N,
+                              int64_t heads, int64_t head_dim, double scale, double tau,
+                              double v_th, double v_reset, int hard_reset, int decay_input,
+                              void* stream);
+
 /* A plain Linear (no neuron) over a token-major fused output kept as its
  * fp16 copy xp [M][cp] (cp >= K; a fused Linear-LIF's output, read through
  * its output descriptor desc, nullable): out [M][O] fp32 = x w^T + bias

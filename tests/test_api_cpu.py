@@ -412,10 +412,12 @@ def test_spikformer_block_with_if_neurons_left_unfused():
     assert stats["fused_lif_nodes"] <= stats["total_lif_nodes"]
 
 
-def test_spikformer_other_head_dims_fuse_with_gemm_core():
+def test_spikformer_attention_kernel_coverage():
     """head dim 64 (the reference's spikformer_cifar_tiny: dim 192, 3 heads)
-    is substituted; the attention core then runs as exact library GEMMs
-    (the MFMA core kernel covers head dim 32)."""
+    is substituted and its attention core is covered by the hand-written
+    kernels, as are long token rows (56 x 56 = 3,136 tokens, the two-pool
+    patch splitter at 224 x 224); a head dim the kernels do not take (48)
+    runs the exact library-GEMM core."""
     import catfuse_amd
     from catfuse_amd.transformer import CTFSpikformerBlock
     net = snn.Spikformer(img_size=32, num_classes=10, embed_dim=192, num_heads=3, depth=1,
@@ -423,14 +425,18 @@ def test_spikformer_other_head_dims_fuse_with_gemm_core():
     fused, stats = catfuse_amd.optimize(net.eval(), T=4)
     blk = fused.blocks[0]
     assert isinstance(blk, CTFSpikformerBlock)
-    assert blk.attn.head_dim == 64 and not blk.attn.kernel_covers(64)
+    assert blk.attn.head_dim == 64 and blk.attn.kernel_covers(64) and blk.attn.kernel_covers(3136)
     assert stats["fused_lif_nodes"] == stats["total_lif_nodes"]   # pre-head LIF: FusedLIF
     from catfuse_amd.patterns import FusedLIF
     assert isinstance(fused.pre_head_lif, FusedLIF) and stats["patterns_matched"]["FusedLIF"] == 1
     small = snn.spikformer_8_384(img_size=224)
     f2, _ = catfuse_amd.optimize(small.eval(), T=4)
     a = f2.blocks[0].attn
-    assert a.head_dim == 32 and a.kernel_covers(196) and not a.kernel_covers(3136)
+    assert a.head_dim == 32 and a.kernel_covers(196) and a.kernel_covers(3136)
+    odd = snn.Spikformer(img_size=32, num_classes=10, embed_dim=96, num_heads=2, depth=1,
+                         pools=(0, 1))
+    f3, _ = catfuse_amd.optimize(odd.eval(), T=4)
+    assert f3.blocks[0].attn.head_dim == 48 and not f3.blocks[0].attn.kernel_covers(64)
 
 
 def test_lazy_head_helpers_decline_plain_tensors():

@@ -384,8 +384,10 @@ def test_spikformer_8_384_c4_size(cuda, v_th):
 
 
 def test_spikformer_gemm_core_for_other_shapes(cuda):
-    """Head dim 64 (the reference's spikformer_cifar_tiny layout) and more
-    than 256 tokens per image take the exact library-GEMM attention core;
+    """Head dim 64 (the reference's spikformer_cifar_tiny layout), more than
+    256 tokens per image and the two-pool patch splitter's 56 x 56 = 3,136
+    tokens at 224 x 224 run the two-pass attention kernels
+    (cf_spike_attention_kv_lif): no call reaches the library-GEMM core, and
     the network stays at oracle parity."""
     from catfuse_amd import snn
     m = snn.Spikformer(img_size=32, num_classes=10, embed_dim=128, num_heads=2, depth=1, T=4,
@@ -396,7 +398,7 @@ def test_spikformer_gemm_core_for_other_shapes(cuda):
     m.eval()
     img = torch.randn(2, 3, 32, 32, generator=g)
     _, fused = _spikformer_parity(cuda, m, img.unsqueeze(0).expand(4, 2, 3, 32, 32), live=True)
-    assert fused.blocks[0].attn.gemm_core_calls > 0
+    assert fused.blocks[0].attn.gemm_core_calls == 0
     m2 = snn.Spikformer(img_size=40, num_classes=10, embed_dim=64, num_heads=2, depth=1, T=2,
                         pools=(0,), v_threshold=0.1)   # head dim 32, 20x20 = 400 tokens
     g = _gen(45)
@@ -405,7 +407,75 @@ def test_spikformer_gemm_core_for_other_shapes(cuda):
     m2.eval()
     img = torch.randn(1, 3, 40, 40, generator=g)
     _, fused = _spikformer_parity(cuda, m2, img.unsqueeze(0).expand(2, 1, 3, 40, 40), live=True)
-    assert fused.blocks[0].attn.gemm_core_calls > 0
+    assert fused.blocks[0].attn.gemm_core_calls == 0
+    m3 = snn.Spikformer(img_size=224, num_classes=10, embed_dim=128, num_heads=2, depth=1, T=2,
+                        pools=(2, 3), v_threshold=0.1)   # head dim 64, 56x56 = 3,136 tokens
+    g = _gen(46)
+    snn.kaiming_init(m3, g)
+    snn.randomize_bn(m3, g)
+    m3.eval()
+    img = torch.randn(1, 3, 224, 224, generator=g)
+    _, fused = _spikformer_parity(cuda, m3, img.unsqueeze(0).expand(2, 1, 3, 224, 224),
+                                  live=True)
+    assert fused.blocks[0].attn.gemm_core_calls == 0
+
+
+def _qkv_copy(T, B, N, C, rate, seed, dev):
+    g = _gen(seed)
+    qkv = torch.zeros(T * B * N, 3 * C + 32, dtype=torch.float16)   # pitch beyond 3C
+    qkv[:, :3 * C] = (torch.rand(T * B * N, 3 * C, generator=g) < rate).half()
+    return qkv.to(dev)
+
+
+@pytest.mark.parametrize("N,heads,dh", [(196, 12, 32), (256, 4, 32), (400, 2, 32), (64, 3, 64),
+                                        (256, 2, 64), (3136, 2, 64), (1000, 3, 32)])
+def test_attention_two_pass_bitwise(cuda, N, heads, dh):
+    """cf_spike_attention_kv_lif: equal to the single-pass kernel bit for bit
+    where both apply (head dim 32, N <= 256), and to the exact float64
+    evaluation + one rounding + the oracle LIF everywhere (spikes and final
+    potentials bit for bit: the products are exact and the LIF tails are
+    bit-exact)."""
+    from catfuse_amd import runtime
+    T, B, scale = 4, 2, 0.125
+    lif = dict(tau=2.0, v_threshold=0.5, v_reset=0.0, decay_input=True)
+    C = heads * dh
+    qkv = _qkv_copy(T, B, N, C, 0.3, seed=N + dh, dev=cuda)
+    v0 = (torch.rand(B, N, C, generator=_gen(7)) * 0.3).to(cuda)
+    a2, v2 = runtime.spike_attention_lif(qkv, T, B, N, heads, (0, C, 2 * C), scale, v_in=v0,
+                                         head_dim=dh, two_pass=True, **lif)
+    if dh == 32 and N <= 256:
+        a1, v1 = runtime.spike_attention_lif(qkv, T, B, N, heads, (0, C, 2 * C), scale, v_in=v0,
+                                             head_dim=dh, two_pass=False, **lif)
+        assert torch.equal(a1.cpu(), a2.cpu()) and torch.equal(v1.cpu(), v2.cpu())
+    # with the initial state: the oracle's v_in
+    s_ref, v_ref, _ = oracle.lif_multistep(
+        _attn_z(qkv, T, B, N, heads, dh, scale), v0.cpu(), **lif)
+    np.testing.assert_array_equal(a2.cpu().numpy(), s_ref)
+    np.testing.assert_array_equal(v2.cpu().numpy(), v_ref)
+
+
+def _attn_z(qkv, T, B, N, heads, dh, scale):
+    C = heads * dh
+    t = qkv[:, :3 * C].cpu().double().view(T, B, N, 3, heads, dh).permute(3, 0, 1, 4, 2, 5)
+    y = t[0] @ (t[1].transpose(-1, -2) @ t[2])
+    return y.permute(0, 1, 3, 2, 4).reshape(T, B, N, C).float() * scale
+
+
+def test_attention_two_pass_zero_route(cuda):
+    """An all-zero Q/K/V copy with its count block publishing zero: the
+    two-pass kernels read nothing, z = 0 into the LIF (the initial state
+    given, so the output is written), the same as the single-pass kernel."""
+    from catfuse_amd import runtime
+    T, B, N, heads, dh = 4, 2, 196, 6, 32
+    C = heads * dh
+    qkv = torch.zeros(T * B * N, 3 * C, dtype=torch.float16, device=cuda)
+    nnz = runtime.count_block(cuda)
+    v0 = (1.0 + torch.rand(B, N, C, generator=_gen(8)) * 2.0).to(cuda)   # z = 0 halves v
+    outs = [runtime.spike_attention_lif(qkv, T, B, N, heads, (0, C, 2 * C), 0.125, v_in=v0,
+                                        nnz=nnz, two_pass=tp) for tp in (False, True)]
+    assert torch.equal(outs[0][0].cpu(), outs[1][0].cpu())
+    assert torch.equal(outs[0][1].cpu(), outs[1][1].cpu())
+    assert bool(outs[0][0].cpu().any())          # v0 >= 2 fires at the first step
 
 
 @pytest.mark.parametrize("shape,k,s,p", [((3, 2, 40, 17, 23), 3, 2, 1), ((2, 3, 96, 20, 15), 3, 2, 1),
