@@ -159,8 +159,15 @@ def ptr(t) -> int | None:
     return t.data_ptr()
 
 
+_RAW_STREAM = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream(device=None) -> int:
-    """hipStream_t of torch's current stream on the tensor's device."""
+    """hipStream_t of torch's current stream on the tensor's device (the raw
+    handle straight from torch's stream registry when it exposes one: no
+    Stream object per launch)."""
+    if _RAW_STREAM is not None and isinstance(device, torch.device) and device.index is not None:
+        return _RAW_STREAM(device.index)
     return torch.cuda.current_stream(device).cuda_stream
 
 

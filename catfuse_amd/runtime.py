@@ -282,6 +282,11 @@ def _metadata_functions():
 _METADATA = None
 
 
+def _meta_of(base: torch.Tensor) -> tuple:
+    """(shape, dtype, device, numel, contiguous) of a plain tensor."""
+    return (base.shape, base.dtype, base.device, base.numel(), base.is_contiguous())
+
+
 class _LazyTensor(torch.Tensor):
     """Base of the tensors whose values a fused launch left elsewhere (a
     copy, a per-channel buffer): cf_materialize() fills the storage, which
@@ -290,6 +295,62 @@ class _LazyTensor(torch.Tensor):
 
     def cf_materialize(self) -> None:  # pragma: no cover - overridden
         raise NotImplementedError
+
+    # Metadata recorded when the tensor is made (_cf_meta: shape, dtype,
+    # device, numel, contiguous), served while it is pending without the
+    # torch-function dispatch a tensor subclass otherwise pays for every
+    # query (the fused layers ask several per launch).  Nothing but
+    # metadata queries has touched a pending tensor (any other operation
+    # materialises it first), so the record is current; afterwards the
+    # queries take the ordinary path.
+    def _cf_meta_now(self):
+        d = self.__dict__
+        return d.get("_cf_meta") if d.get("_cf_pending", False) else None
+
+    @property
+    def shape(self):
+        m = self._cf_meta_now()
+        return m[0] if m is not None else super().shape
+
+    @property
+    def dtype(self):
+        m = self._cf_meta_now()
+        return m[1] if m is not None else super().dtype
+
+    @property
+    def device(self):
+        m = self._cf_meta_now()
+        return m[2] if m is not None else super().device
+
+    @property
+    def is_cuda(self):
+        m = self._cf_meta_now()
+        return m[2].type == "cuda" if m is not None else super().is_cuda
+
+    @property
+    def ndim(self):
+        m = self._cf_meta_now()
+        return len(m[0]) if m is not None else super().ndim
+
+    def dim(self):
+        m = self._cf_meta_now()
+        return len(m[0]) if m is not None else super().dim()
+
+    def numel(self):
+        m = self._cf_meta_now()
+        return m[3] if m is not None else super().numel()
+
+    def is_contiguous(self, memory_format=torch.contiguous_format):
+        m = self._cf_meta_now()
+        if m is not None and memory_format is torch.contiguous_format:
+            return m[4]
+        return super().is_contiguous(memory_format=memory_format)
+
+    def contiguous(self, memory_format=torch.contiguous_format):
+        m = self._cf_meta_now()
+        if m is not None and memory_format is torch.contiguous_format and m[4]:
+            return self
+        return super().contiguous(memory_format=memory_format)
 
     @classmethod
     def __torch_function__(cls, func, types, args=(), kwargs=None):
@@ -351,6 +412,7 @@ class NHWCSpikes(_LazyTensor):
     @staticmethod
     def __new__(cls, base: torch.Tensor, nhwc: torch.Tensor, tokens: bool = False):
         t = base.as_subclass(cls)
+        t._cf_meta = _meta_of(base)
         t._cf_pending = True
         t._cf_tokens = tokens
         t._cf_nhwc = (nhwc, base._version)
@@ -393,6 +455,7 @@ class ChannelState(_LazyTensor):
     def __new__(cls, base: torch.Tensor, v_chan: torch.Tensor, desc: torch.Tensor,
                 uniform: bool = False):
         t = base.as_subclass(cls)
+        t._cf_meta = _meta_of(base)
         t._cf_pending = True
         t._cf_state = (v_chan, desc, base._version)
         t._cf_sticky = torch.cuda.is_current_stream_capturing()

@@ -498,3 +498,21 @@ def test_mi355x_profile_refuses_sparseflow_for_1x1(monkeypatch):
     assert sf.route_geometry(ConvLIFSpec(256, 256, 1, 1, 0, **kw), 14, 14) is None
     g = sf.route_geometry(ConvLIFSpec(64, 64, 3, 1, 1, **kw), 56, 56)
     assert g is not None and g["egd"] == (0.0, 0.4) and (g["block_h"], g["block_w"]) == (8, 8)
+
+
+def test_lazy_output_metadata_without_materialising():
+    """A fused layer's pending output answers metadata queries (shape,
+    dtype, device, dim, numel, contiguity, contiguous()) from the record
+    made at creation, without materialising (on the CPU any
+    materialisation would call the HIP library and fail)."""
+    from catfuse_amd import runtime
+    base = torch.empty(4, 2, 8, 5, 5)
+    nhwc = torch.zeros(8, 5, 5, 32, dtype=torch.float16)
+    x = runtime.NHWCSpikes(base, nhwc)
+    assert x.shape == (4, 2, 8, 5, 5) and x.dtype == torch.float32
+    assert x.device == torch.device("cpu") and not x.is_cuda
+    assert x.ndim == x.dim() == 5 and x.numel() == 1600 and x.size(2) == 8
+    assert x.is_contiguous() and x.contiguous() is x
+    assert x.__dict__["_cf_pending"]
+    x._cf_pending = False          # materialised: the ordinary path
+    assert x.shape == (4, 2, 8, 5, 5) and x.dim() == 5 and x.is_contiguous()

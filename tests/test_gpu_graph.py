@@ -209,3 +209,21 @@ def test_graph_replays_of_spikformer(cuda, v_th):
                 snn.functional.reset_net(fused)
                 z = fused(as_input(imgs[(i + 1) % 3]))
                 assert torch.equal(z, eager[(i + 1) % 3])
+
+
+def test_launch_stream_is_torch_current_stream(cuda):
+    """The handle the launches use is torch's current stream: the default
+    stream, a side stream selected with torch.cuda.stream, and the capture
+    stream of a graph being recorded."""
+    from catfuse_amd import _hip
+    assert _hip.stream(cuda) == torch.cuda.current_stream(cuda).cuda_stream
+    side = torch.cuda.Stream(device=cuda)
+    with torch.cuda.stream(side):
+        assert _hip.stream(cuda) == side.cuda_stream
+    g = torch.cuda.CUDAGraph()
+    x = torch.zeros(8, device=cuda)
+    seen = []
+    with torch.cuda.graph(g):
+        seen.append((_hip.stream(cuda), torch.cuda.current_stream(cuda).cuda_stream))
+        x.add_(1.0)
+    assert seen[0][0] == seen[0][1]
