@@ -226,6 +226,10 @@ constexpr int halo_min_blocks() {
 // HS: the SparseFlow route skips the MFMAs of a silent 16-channel chunk half
 // (prescan groups narrower than a chunk); off, the K loop has no per-half
 // branches (the instantiations a dense-only launch uses).
+// DEEP: launches of at most one workgroup per CU (one wave per SIMD, nothing
+// else to switch to while a wave waits): the register budget of one
+// workgroup per CU, and stride-1 3x3 K loops load each tap's weight
+// fragments two taps ahead (three register buffers) instead of one.
 // One halo buffer (halves) of a configuration: whole 64-unit blocks of the
 // staged halo of a time block (16-byte units of TB steps x RH x RW pixels).
 template <int TH, int TW, int S, int K>
@@ -238,7 +242,8 @@ constexpr int halo_buf_halves() {
 // function, so that one grid can run two convs of the same input side by
 // side (conv_halo_pair_kernel).  halo: halo_nbuf() * halo_buf_halves() halves of LDS;
 // bn_s: the tile's BN coefficients; any_sh: the workgroup's vote words.
-template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB, bool HS, bool U8>
+template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB, bool HS, bool U8,
+          bool DEEP = false>
 __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const int nL,
                                           _Float16* __restrict__ halo, float (*bn_s)[64],
                                           unsigned* any_sh) {
@@ -747,11 +752,15 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   // fragment (tap, 16-channel step k16) of its 32-channel M tile are at
   // wbase + (tap * Cp/16 + k16) * 512 halves; the lo limb follows the hi limb
   // at limb_stride.  Two register buffers, alternating with a running tap
-  // count that continues across K steps.
+  // count that continues across K steps; three (W2: tap j in buffer j % 3,
+  // loaded at tap j - 2) in the DEEP stride-1 3x3 K loop, whose nine taps
+  // per K step keep that assignment the same in every K step.
   const int k16s = a.Cp / 16;
   const _Float16* wbase = a.w + (size_t)((cout0 + wm * WM) / 32) * KK * k16s * 512 + lane * 8;
   const size_t limb_stride = (size_t)a.Coutp * KK * a.Cp;
-  h8 ah[2][2], al[2][2];
+  constexpr bool W2 = DEEP && KK == 9 && NBUF == 2;
+  constexpr int NWB = W2 ? 3 : 2;
+  h8 ah[NWB][2], al[NWB][2];
   auto load_w = [&](int buf, int tap, int ch) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
@@ -764,7 +773,9 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   f16v acc[TB][NT];
   // The taps of K step ch from halo buffer hb: tap j uses weight buffer
   // j & 1 and loads the weights of the next tap (at the last tap: the next
-  // K step's tap 0, moved to buffer 0 after the taps), then the direct loads
+  // K step's tap 0, moved to buffer 0 after the taps; W2: buffer j % 3, and
+  // the weights of tap j + 2, the next K step's taps 0 and 1 at the last
+  // two taps), then the direct loads
   // of the next K step (ntb, nc) into the other halo buffer hb_next, spread
   // over taps 0 .. KK-2.  Every load is issued unconditionally (a next step
   // in a later time block stages zeros here, its weights are reloaded
@@ -794,7 +805,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     const int stb = ntb == wblk ? ntb : a.T;  // a.T: stage zeros
 #pragma unroll
     for (int tap = 0; tap < KK; ++tap) {
-      const int cur = tap & 1;
+      const int cur = W2 ? tap % 3 : (tap & 1);
       const int kh = tap / K, kw = tap % K;
       // B fragments are read TBR steps at a time, unconditionally (reads of
       // steps this chunk skips hold zeros), each batch before its MFMAs.
@@ -810,8 +821,13 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
               bb[tr][ks][nt] = *reinterpret_cast<const h8*>(
                   &hb[(th + tr) * TSTR + kh * RW * KC + rd_addr(nt, kw, ks)]);
         if (th == 0) {
-          if (tap + 1 < KK) load_w(cur ^ 1, tap + 1, ch);
-          else load_w(cur ^ 1, 0, nc);
+          if constexpr (W2) {
+            if (tap + 2 < KK) load_w((tap + 2) % 3, tap + 2, ch);
+            else load_w((tap + 2) % 3, tap + 2 - KK, nc);
+          } else {
+            if (tap + 1 < KK) load_w(cur ^ 1, tap + 1, ch);
+            else load_w(cur ^ 1, 0, nc);
+          }
           if constexpr (U8) {
             // both buffer counts: loads now, widened after the taps
             if (KK == 1) {
@@ -853,7 +869,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
         __builtin_amdgcn_sched_barrier(0);
       }
     }
-    if (KK & 1) {
+    if (!W2 && (KK & 1)) {
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         ah[0][ks] = ah[1][ks];
@@ -862,13 +878,15 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     }
   };
 
-  // First K step: staged and its tap-0 weights loaded before the loop.
+  // First K step: staged and its tap-0 (W2: and tap-1) weights loaded
+  // before the loop.
   int s_tb, s_ch;
   uint32_t s_act;
   next_step(0, -1, s_tb, s_ch, s_act);
   int pf_tb = s_tb;  // block of the K step already staged into buffer 0
   if (s_tb < a.T) {
     load_w(0, 0, s_ch);
+    if constexpr (W2) load_w(1, 1, s_ch);
     stage_loads(std::false_type{}, s_tb, s_ch, s_act, halo, 0, NPF);
   }
 
@@ -936,6 +954,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     // the registers live across their K loop.)
     if (NBUF == 2 && s_tb < a.T && s_tb != pf_tb) {
       load_w(0, 0, s_ch);
+      if constexpr (W2) load_w(1, 1, s_ch);
       stage_loads(std::integral_constant<bool, (TB == 2)>{}, s_tb, s_ch, s_act, halo, 0, NPF);
       pf_tb = s_tb;
     }
@@ -1249,20 +1268,52 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
 }
 
 template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB, bool HS = false,
-          bool U8 = false>
-__global__ __launch_bounds__(256, (halo_min_blocks<TH, TW, S, K>()))
+          bool U8 = false, bool DEEP = false>
+__global__ __launch_bounds__(256, (DEEP ? 1 : halo_min_blocks<TH, TW, S, K>()))
 void conv_halo_kernel(HaloArgs a) {
   __shared__ __attribute__((aligned(16))) _Float16 halo[halo_nbuf<S, K>() * halo_buf_halves<TH, TW, S, K>()];
   __shared__ __attribute__((aligned(16))) float bn_s[2][64];  // alpha, beta of the tile
   __shared__ unsigned any_sh[4];  // per-wave votes of the output count
-  halo_body<TH, TW, S, K, EPI, LM, LEAN, ONEB, HS, U8>(a, (int)blockIdx.x, (int)gridDim.x, halo,
-                                                       bn_s, any_sh);
+  halo_body<TH, TW, S, K, EPI, LM, LEAN, ONEB, HS, U8, DEEP>(a, (int)blockIdx.x, (int)gridDim.x,
+                                                             halo, bn_s, any_sh);
+}
+
+// Compute units of the current device (cached per device), or 0 when the
+// runtime does not say.
+int halo_cu_count() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (cache[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) n = 0;
+    cache[dev] = n > 0 ? n : -1;
+  }
+  return cache[dev] > 0 ? cache[dev] : 0;
+}
+
+// A lean EPI_LIF launch: the DEEP instantiation when deep (stride-1 3x3 8x8
+// tiles without the half skip), else the ordinary one.
+template <int TH, int TW, int S, int K, int LM, bool OB, bool HS, bool U8>
+void launch_lean(bool deep, dim3 grid, dim3 block, hipStream_t st, const HaloArgs& a) {
+  if constexpr (TH == 8 && TW == 8 && S == 1 && K == 3 && !HS) {
+    if (deep) {
+      hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LM, true, OB, HS, U8, true>), grid,
+                         block, 0, st, a);
+      return;
+    }
+  }
+  hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LM, true, OB, HS, U8>), grid, block, 0,
+                     st, a);
 }
 
 template <int TH, int TW, int S, int K = 3>
 hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
   dim3 grid((unsigned)(a.B * a.GH * a.GW * (a.Coutp / 64)));
   const dim3 block(256);
+  // at most one workgroup per CU: the DEEP K loop (used where it exists)
+  const int cus = halo_cu_count();
+  const bool deep = cus > 0 && grid.x <= (unsigned)cus;
   // lean: no fp32 output, no fp32 identity, whole 32-channel groups (the
   // stores drop channels >= Cout of a partly real 64-channel tile)
   const bool lean = epi == EPI_LIF && !a.out && !a.identity && a.Cout % 32 == 0;
@@ -1273,14 +1324,12 @@ hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
     if constexpr (TH == 8 && TW == 8) {
       if (!lean) return hipErrorInvalidValue;
       const int lm = cf_lif_mode(a.lif);
-#define CF_HALO_U8(LMV)                                                                          \
-  do {                                                                                           \
-    if (oneb)                                                                                    \
-      hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LMV, true, true, false, true>), \
-                         grid, block, 0, st, a);                                                 \
-    else                                                                                         \
-      hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LMV, true, false, false, true>), \
-                         grid, block, 0, st, a);                                                 \
+#define CF_HALO_U8(LMV)                                                                  \
+  do {                                                                                   \
+    if (oneb)                                                                            \
+      launch_lean<TH, TW, S, K, LMV, true, false, true>(deep, grid, block, st, a);       \
+    else                                                                                 \
+      launch_lean<TH, TW, S, K, LMV, false, false, true>(deep, grid, block, st, a);      \
   } while (0)
       if (lm == LM_HARD0_DECAY_P2) CF_HALO_U8(LM_HARD0_DECAY_P2);
       else if (lm == LM_HARD_DECAY_P2) CF_HALO_U8(LM_HARD_DECAY_P2);
@@ -1322,14 +1371,12 @@ hipError_t launch_halo(const HaloArgs& a, int epi, hipStream_t st) {
     // SparseFlow-capable with groups narrower than a chunk: the K loop that
     // skips silent chunk halves
     const bool hs = a.ag_mask != nullptr && a.gs < KC;
-#define CF_HALO_LEAN(LMV, OB)                                                                     \
-  do {                                                                                            \
-    if (hs)                                                                                       \
-      hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LMV, true, OB, true>), grid,    \
-                         block, 0, st, a);                                                        \
-    else                                                                                          \
-      hipLaunchKernelGGL((conv_halo_kernel<TH, TW, S, K, EPI_LIF, LMV, true, OB, false>), grid,   \
-                         block, 0, st, a);                                                        \
+#define CF_HALO_LEAN(LMV, OB)                                                            \
+  do {                                                                                   \
+    if (hs)                                                                              \
+      launch_lean<TH, TW, S, K, LMV, OB, true, false>(false, grid, block, st, a);        \
+    else                                                                                 \
+      launch_lean<TH, TW, S, K, LMV, OB, false, false>(deep, grid, block, st, a);        \
   } while (0)
     if (lm == LM_HARD0_DECAY_P2) {
       if (oneb) CF_HALO_LEAN(LM_HARD0_DECAY_P2, true);
