@@ -640,19 +640,27 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   // from the tile's top-left input pixel of time step 0 of the block;
   // 32-bit, checked on the host), whether the pixel lies inside the image,
   // and its time step within the block.
+  // (Unsigned in-tile arithmetic: divisions by the constant halo sizes are
+  // a multiply-high and a shift; the pixel offset is a 24-bit product, exact
+  // since the host bounds 4 * B * H * W * Cp below 2^31; the time step's
+  // stride is two selects of workgroup-uniform multiples.)
+  const int tstr1 = a.B * (int)img_stride;
   auto unit_of = [&](int i, int& off, bool& inb, int& t) {
     int blk = 4 * i + wave;
     if (4 * NPF > NB && blk >= NB) blk -= NB;
-    const int l = opaque(lane);
-    const int U = blk * 64 + l;
-    const int slot = l & 3, pix = blk * 16 + (l >> 2);
-    const int c = pix % RW, ry = (pix / RW) % RH;
-    t = min(pix / (RW * RH), TB - 1);
-    const int rx = G::inv_col(c);
-    const int part = slot ^ G::swz(ry, c);
-    const int ih = ih0 + ry * SS, iw = iw0 + rx * SS;
-    inb = (U < NU) & (ih >= 0) & (ih < a.H) & (iw >= 0) & (iw < a.W);
-    off = t * a.B * (int)img_stride + ((ry * SS) * a.W + rx * SS) * a.Cp + part * 8;
+    const unsigned l = (unsigned)opaque(lane);
+    const unsigned U = (unsigned)blk * 64u + l;
+    const unsigned slot = l & 3u, pix = (unsigned)blk * 16u + (l >> 2);
+    const unsigned c = pix % (unsigned)RW, ry = (pix / (unsigned)RW) % (unsigned)RH;
+    const unsigned tu = min(pix / (unsigned)(RW * RH), (unsigned)(TB - 1));
+    t = (int)tu;
+    const int rx = G::inv_col((int)c);
+    const unsigned part = slot ^ (unsigned)G::swz((int)ry, (int)c);
+    const int ih = ih0 + (int)ry * SS, iw = iw0 + rx * SS;
+    inb = (U < (unsigned)NU) & (ih >= 0) & (ih < a.H) & (iw >= 0) & (iw < a.W);
+    const unsigned sp = __umul24((unsigned)((int)ry * SS), (unsigned)a.W) + (unsigned)(rx * SS);
+    off = (int)(__umul24(sp, (unsigned)a.Cp) + part * 8u) + ((tu & 1u) ? tstr1 : 0) +
+          ((tu & 2u) ? 2 * tstr1 : 0);
     return blk;
   };
   // The units are the same for every K step of the tile; each time block
@@ -1062,15 +1070,19 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     if (EPI == EPI_LIF) {
       const float* vsrc = tb0 == 0 ? a.v_in : a.v_out;
       const float* vbase = vsrc ? vsrc + (size_t)b * a.Cout * HoWo : nullptr;
+      const float v0 = lif_initial_v(a.lif);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int dc = 8 * (r >> 2) + (r & 3);
+      for (int r = 0; r < 16; ++r)
 #pragma unroll
-        for (int nt = 0; nt < NT; ++nt) {
-          float v0 = lif_initial_v(a.lif);
-          if (vbase && (full_c || col + dc < a.Cout) && n_ok[nt])
-            v0 = vbase[(unsigned)((col + dc) * HoWo + e_off[nt])];
-          v[nt][r] = v0;
+        for (int nt = 0; nt < NT; ++nt) v[nt][r] = v0;
+      if (vbase) {  // (workgroup-uniform: no per-element branches without a state)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dc = 8 * (r >> 2) + (r & 3);
+#pragma unroll
+          for (int nt = 0; nt < NT; ++nt)
+            if ((full_c || col + dc < a.Cout) && n_ok[nt])
+              v[nt][r] = vbase[(unsigned)((col + dc) * HoWo + e_off[nt])];
         }
       }
     }
@@ -1178,6 +1190,22 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     // Copy-out of a staged step: BN * BM/8 sixteen-byte chunks, CPI per thread.
     constexpr int CH8 = BM / 8;  // 16-byte chunks per pixel
     constexpr int CPI = (BN * CH8 + 255) / 256;
+    // Lean path: this thread's chunks are the same at every step (their
+    // store offsets within a step's image and their LDS staging offsets),
+    // computed once per block.
+    uint32_t lo_off[LEAN ? CPI : 1], lo_lds[LEAN ? CPI : 1];
+    if constexpr (LEAN) {
+#pragma unroll
+      for (int i = 0; i < CPI; ++i) {
+        const int c = tid + 256 * i;
+        const int px = c / CH8, part = c % CH8;
+        const int py = px / TW, pxx = px % TW;
+        const bool ok = (oh0 + py < a.Ho) & (ow0 + pxx < a.Wo) & (cout0 + part * 8 < a.Cout);
+        lo_off[i] = ok ? (uint32_t)((((oh0 + py) * a.Wo + ow0 + pxx) * a.cp_out + cout0 + part * 8) * XB)
+                       : HALO_OOB;
+        lo_lds[i] = (uint32_t)(px * OLD + part * 8);
+      }
+    }
 #pragma unroll
     for (int t = 0; t < TB; ++t) {
       if (t > 0 && t >= nsteps) break;  // every block has a first step
@@ -1196,16 +1224,10 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
                         (uint32_t)(HoWo * a.cp_out * XB));
 #pragma unroll
           for (int i = 0; i < CPI; ++i) {
-            const int c = opaque(tid) + 256 * i;
-            const int px = c / CH8, part = c % CH8;
-            const int py = px / TW, pxx = px % TW;
-            const bool ok = (oh0 + py < a.Ho) & (ow0 + pxx < a.Wo) & (cout0 + part * 8 < a.Cout);
-            const uint32_t off =
-                ok ? (uint32_t)((((oh0 + py) * a.Wo + ow0 + pxx) * a.cp_out + cout0 + part * 8) * XB)
-                   : HALO_OOB;
+            const uint32_t off = lo_off[i];
             // streaming (non-temporal) stores: the copy is read back by the
             // next layer only after the whole output is written
-            const u32x4 chunk = *reinterpret_cast<const u32x4*>(&ostage[px * OLD + part * 8]);
+            const u32x4 chunk = *reinterpret_cast<const u32x4*>(&ostage[lo_lds[i]]);
             if constexpr (U8)
               __builtin_amdgcn_raw_buffer_store_b64(h8_to_u8x8(__builtin_bit_cast(h8, chunk)), ro,
                                                     off, 0, CF_CPOL_NT);

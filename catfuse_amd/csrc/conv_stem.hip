@@ -18,7 +18,7 @@
 // is below 2^-22 |w x| per product.
 //
 // Workgroup: one 8 x 7 tile of pooled pixels of one image and 64 output
-// channels; the filter rows' weight fragments stream from L2 one row ahead
+// channels; the filter rows' weight fragments stream from L2 two rows ahead
 // (141 VGPRs: three workgroups per CU).  It computes the 17 x 15 conv outputs under the tile's pooling
 // windows (the border row/column is recomputed by the neighbouring tile),
 // runs the LIF over T for each, keeps the spike train of each conv output as
@@ -216,12 +216,35 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
         }
       }
     }
-    for (int t = 0; t < a.T; ++t) {
-      const uint32_t tbit = 1u << t;
+    constexpr bool HARD = LM == LM_HARD0_DECAY_P2 || LM == LM_HARD_DECAY_P2;
+    if (HARD && !vin_b && a.T == 4) {
+      // Hard reset from the initial state with a constant z: a reset puts v
+      // back to the initial value bit for bit (+0 or v_reset; no state is
+      // ever -0), so the trajectory restarts, and the spike train follows
+      // from the reset-free charges u_1 .. u_4 (the same operations on the
+      // same values as the stepped form): with k the first step where
+      // u_k >= v_th, the neuron fires at steps k, 2k, ... and ends at
+      // u_(4 mod k) (the initial value when that is 0).
+      const float v0 = lif_initial_v(a.lif);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        vr[r] = lif_charge_m<LM>(vr[r], zr[r], a.lif);
-        bits[r] |= lif_fire_reset_bit<LM>(vr[r], a.lif) ? tbit : 0u;
+        const float u1 = lif_charge_m<LM>(v0, zr[r], a.lif);
+        const float u2 = lif_charge_m<LM>(u1, zr[r], a.lif);
+        const float u3 = lif_charge_m<LM>(u2, zr[r], a.lif);
+        const float u4 = lif_charge_m<LM>(u3, zr[r], a.lif);
+        const bool f1 = u1 >= a.lif.v_th, f2 = u2 >= a.lif.v_th, f3 = u3 >= a.lif.v_th,
+                   f4 = u4 >= a.lif.v_th;
+        bits[r] = f1 ? 15u : f2 ? 10u : f3 ? 4u : f4 ? 8u : 0u;
+        vr[r] = (f1 || f2) ? v0 : f3 ? u1 : f4 ? v0 : u4;
+      }
+    } else {
+      for (int t = 0; t < a.T; ++t) {
+        const uint32_t tbit = 1u << t;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          vr[r] = lif_charge_m<LM>(vr[r], zr[r], a.lif);
+          bits[r] |= lif_fire_reset_bit<LM>(vr[r], a.lif) ? tbit : 0u;
+        }
       }
     }
     if (vout_b && own) {
@@ -282,13 +305,15 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
       acc0[r] = 0.0f;
       acc1[r] = 0.0f;
     }
-    h8 wh[2][2], wl[2][2];   // [row parity][ks]
+    // filter row kh's fragments in buffer kh % 3, loaded two rows ahead
+    h8 wh[3][2], wl[3][2];   // [row % 3][ks]
     load_w(0, wh[0], wl[0]);
+    if (a.KH > 1) load_w(1, wh[1], wl[1]);
 #pragma unroll
     for (int kh = 0; kh < MAXKH; ++kh) {
       if (kh >= a.KH) break;
-      const int cb = kh & 1;
-      if (kh + 1 < a.KH) load_w(kh + 1, wh[cb ^ 1], wl[cb ^ 1]);
+      const int cb = kh % 3;
+      if (kh + 2 < a.KH) load_w(kh + 2, wh[(kh + 2) % 3], wl[(kh + 2) % 3]);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const int o = (kh * RW + 4 * ks) * 4;
