@@ -193,9 +193,28 @@ class Flatten(nn.Flatten):
 
 
 def _reset_net(net: nn.Module):
-    for m in net.modules():
-        if hasattr(m, "reset") and callable(m.reset):
-            m.reset()
+    # Every module of net in net.modules() order (pre-order, each once),
+    # walked over the _modules dicts directly; a module's reset is found as
+    # attribute lookup would find it (instance attribute, class attribute,
+    # then a submodule of that name), without nn.Module.__getattr__'s
+    # failing lookup for the modules that have none.
+    seen = set()
+    stack = [net]
+    while stack:
+        m = stack.pop()
+        if id(m) in seen:
+            continue
+        seen.add(id(m))
+        r = m.__dict__.get("reset")
+        if r is None and getattr(type(m), "reset", None) is not None:
+            r = m.reset
+        if r is None:
+            r = m._modules.get("reset")
+        if r is not None and callable(r):
+            r()
+        kids = [c for c in m._modules.values() if c is not None]
+        kids.reverse()
+        stack.extend(kids)
 
 
 def _set_step_mode(net: nn.Module, step_mode: str):
