@@ -1345,11 +1345,12 @@ class ConvLIFRunner:
                 self.KH, self.KW, self.stride, self.padding, B, th, tw, gs, int(epilogue),
                 *self.lif, _hip.stream(dev))
             check(rc, "cf_conv_mfma")
-        copy_bytes = (nhwc.element_size() * T * B * Hs * Ws * cp_out if nhwc is not None else 0) \
-            + (4 * T * B * Ho * Wo * self.Cout if out_ptr is not None else 0)
-        state_bytes = 4 * B * Hs * Ws * self.Cout if v_out is not None else 0
-        _t1(timer_name, ev, flops=2 * T * B * Ho * Wo * self.Cout * self.Cin * self.KH * self.KW,
-            route=None if nnz is None else _RouteProbe(nnz, [(desc, copy_bytes, state_bytes)]))
+        if ev is not None:
+            copy_bytes = (nhwc.element_size() * T * B * Hs * Ws * cp_out if nhwc is not None
+                          else 0) + (4 * T * B * Ho * Wo * self.Cout if out_ptr is not None else 0)
+            state_bytes = 4 * B * Hs * Ws * self.Cout if v_out is not None else 0
+            _t1(timer_name, ev, flops=2 * T * B * Ho * Wo * self.Cout * self.Cin * self.KH * self.KW,
+                route=None if nnz is None else _RouteProbe(nnz, [(desc, copy_bytes, state_bytes)]))
         self.last_nnz = nnz  # count block of this input (None: not counted)
         self.last_numel = numel
         if not want_v_out:
@@ -1740,10 +1741,11 @@ def run_halo_pair(ra: "ConvLIFRunner", rb: "ConvLIFRunner", x: torch.Tensor, v_i
         ptr(rb.w_packed), ptr(rb.alpha), ptr(rb.beta), ptr(vb), ptr(vob), ptr(nb), cpb, ptr(nzb),
         ptr(db), ib, rb.Cout, rb.Coutp, rb.padding, *ra.lif, _hip.stream(dev)),
         "cf_conv_halo_pair")
-    flops = 2 * T * B * Ho * Wo * C * (ra.Cout * 9 + rb.Cout)
-    parts = [(d, (1 if u8 else 2) * T * B * Ho * Wo * cp, 4 * B * Ho * Wo * r.Cout)
-             for d, cp, r in ((da, cpa, ra), (db, cpb, rb))]
-    _t1("conv_pair", ev, flops=flops, route=None if nnz is None else _RouteProbe(nnz, parts))
+    if ev is not None:
+        flops = 2 * T * B * Ho * Wo * C * (ra.Cout * 9 + rb.Cout)
+        parts = [(d, (1 if u8 else 2) * T * B * Ho * Wo * cp, 4 * B * Ho * Wo * r.Cout)
+                 for d, cp, r in ((da, cpa, ra), (db, cpb, rb))]
+        _t1("conv_pair", ev, flops=flops, route=None if nnz is None else _RouteProbe(nnz, parts))
     for r in (ra, rb):
         r.last_nnz = nnz
         r.last_numel = x.numel()
