@@ -811,23 +811,34 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     const uint32_t kr = ks_run(ch);
     constexpr bool SKIP = decltype(skip_c)::value;
     const int stb = ntb == wblk ? ntb : a.T;  // a.T: stage zeros
+    // B fragments are read TBR steps at a time (a batch), unconditionally
+    // (reads of steps this chunk skips hold zeros), one 16-channel half
+    // (ks) at a time: half ks of the next batch (the next TBR steps, or the
+    // next tap's first ones) is read as soon as the MFMAs of this batch's
+    // half ks are issued, into the registers they read, so its LDS latency
+    // passes under the other half's MFMAs.  The first batch of the K step is
+    // read before its taps.
+    h8 bb[TBR][2][NT];
+    auto read_half = [&](int tap, int th, int ks) {
+      const int kh = tap / K, kw = tap % K;
+#pragma unroll
+      for (int tr = 0; tr < TBR; ++tr)
+#pragma unroll
+        for (int nt = 0; nt < NT; ++nt)
+          bb[tr][ks][nt] = *reinterpret_cast<const h8*>(
+              &hb[(th + tr) * TSTR + kh * RW * KC + rd_addr(nt, kw, ks)]);
+    };
+    read_half(0, 0, 0);
+    read_half(0, 0, 1);
+    // Every 16-channel half runs (the common case: all channels real, no
+    // half skip): the K loop without per-half branches.
+    auto taps = [&](auto full_c) {
+      constexpr bool FULL = decltype(full_c)::value;
 #pragma unroll
     for (int tap = 0; tap < KK; ++tap) {
       const int cur = W2 ? tap % 3 : (tap & 1);
-      const int kh = tap / K, kw = tap % K;
-      // B fragments are read TBR steps at a time, unconditionally (reads of
-      // steps this chunk skips hold zeros), each batch before its MFMAs.
 #pragma unroll
       for (int th = 0; th < TB; th += TBR) {
-        h8 bb[TBR][2][NT];
-#pragma unroll
-        for (int tr = 0; tr < TBR; ++tr)
-#pragma unroll
-          for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-            for (int nt = 0; nt < NT; ++nt)
-              bb[tr][ks][nt] = *reinterpret_cast<const h8*>(
-                  &hb[(th + tr) * TSTR + kh * RW * KC + rd_addr(nt, kw, ks)]);
         if (th == 0) {
           if constexpr (W2) {
             if (tap + 2 < KK) load_w((tap + 2) % 3, tap + 2, ch);
@@ -855,28 +866,40 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
         }
         // Issue the loads before these MFMAs.
         __builtin_amdgcn_sched_barrier(0);
+        // The batch after this one within the K step (none after the last
+        // tap's last batch: the next K step's halo is not published yet).
+        const int ntap = th + TBR < TB ? tap : tap + 1;
+        const int nth = th + TBR < TB ? th + TBR : 0;
         // Consecutive MFMAs go to different accumulators (time steps, tiles)
         // so none waits for the previous one's result; each accumulator
         // still sums ks 0 hi, ks 0 lo, ks 1 hi, ks 1 lo in that order.
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          if (((kr >> ks) & 1u) == 0u) continue;
-          if constexpr (SKIP) {
-            if (((hm >> (ks * TB + th)) & ((1u << TBR) - 1u)) == 0u) continue;
+          bool run = true;
+          if constexpr (!FULL) {
+            run = ((kr >> ks) & 1u) != 0u;
+            if constexpr (SKIP) run = run && ((hm >> (ks * TB + th)) & ((1u << TBR) - 1u)) != 0u;
           }
+          if (run) {
 #pragma unroll
-          for (int limb = 0; limb < 2; ++limb)
+            for (int limb = 0; limb < 2; ++limb)
 #pragma unroll
-            for (int tr = 0; tr < TBR; ++tr)
+              for (int tr = 0; tr < TBR; ++tr)
 #pragma unroll
-              for (int nt = 0; nt < NT; ++nt)
-                acc[th + tr][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
-                    limb ? al[cur][ks] : ah[cur][ks], bb[tr][ks][nt], acc[th + tr][nt], 0, 0, 0);
+                for (int nt = 0; nt < NT; ++nt)
+                  acc[th + tr][nt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(
+                      limb ? al[cur][ks] : ah[cur][ks], bb[tr][ks][nt], acc[th + tr][nt], 0, 0,
+                      0);
+          }
+          // The next batch's half ks into the registers these MFMAs read.
+          __builtin_amdgcn_sched_barrier(0);
+          if (ntap < KK) read_half(ntap, nth, ks);
+          __builtin_amdgcn_sched_barrier(0);
         }
-        // Later reads stay below these MFMAs (register budget).
-        __builtin_amdgcn_sched_barrier(0);
       }
     }
+    };
+    taps(std::false_type{});
     if (!W2 && (KK & 1)) {
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
