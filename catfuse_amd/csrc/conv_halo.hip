@@ -74,9 +74,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t halo_rsrc(const void* base, ui
 }
 constexpr uint32_t HALO_OOB = 0x80000000u;  // an offset beyond every range used here
 
-// Sixteen zero bytes in device memory: out-of-range halo units load from
-// here, so a loaded register never needs a select that would force the
-// wave to wait for the load before the taps run.
+// Sixteen zero bytes in device memory: absent route words (counts,
+// descriptors) are read from here.
 __device__ __attribute__((aligned(16))) u32x4 g_halo_zero;
 
 // Returns x unchanged, hidden from the optimiser: per-element addresses
@@ -87,29 +86,38 @@ __device__ __forceinline__ int opaque(int x) {
   return x;
 }
 
-template <typename P>
-__device__ __forceinline__ P* opaque_ptr(P* p) {
-  asm volatile("" : "+s"(p));
-  return p;
-}
-
 constexpr int KC = 32;  // channels per chunk: four 16-byte parts per staged pixel
 
-// One direct global -> LDS load (global_load_lds_dwordx4): lane l copies
-// 16 bytes from its src to LDS byte address lds + 16 l (lds wave-uniform).
+// One direct global -> LDS load (buffer_load_dwordx4 ... lds): lane l
+// copies the 16 bytes at byte offset voff of the buffer rsrc (zeros when
+// voff is beyond its range) to LDS byte address lds + 16 l (lds
+// wave-uniform); the buffer's base is in scalar registers, so a copy takes
+// no vector address arithmetic.
 // Issued through inline assembly so that the compiler does not track it:
 // its own load counting then never waits for these copies (it only waits
 // for loads it issued, which in-order completion makes safe: a copy issued
 // after a load never delays the wait for that load).  The kernel waits for
 // the copies itself (s_waitcnt vmcnt(0) and a barrier) before reading them.
-__device__ __forceinline__ void lds_copy16(const void* src, unsigned lds) {
+typedef int cf_v4i __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ void lds_buf_copy16(cf_v4i rsrc, unsigned voff, unsigned lds) {
   asm volatile(
-      "s_mov_b32 m0, %1\n\t"
+      "s_mov_b32 m0, %2\n\t"
       "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %0, off"
+      "buffer_load_dwordx4 %0, %1, 0 offen lds"
       :
-      : "v"(src), "s"(lds)
+      : "v"(voff), "s"(rsrc), "s"(lds)
       : "memory", "m0");
+}
+// Raw buffer resource words (as halo_rsrc) in scalar registers, for inline
+// assembly.
+__device__ __forceinline__ cf_v4i halo_rsrc_v4(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)(uintptr_t)base;
+  cf_v4i r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)p);
+  r[1] = __builtin_amdgcn_readfirstlane((int)((uint32_t)(p >> 32) & 0xffffu));
+  r[2] = (int)bytes;
+  r[3] = 0x00020000;
+  return r;
 }
 __device__ __forceinline__ unsigned lds_addr(const void* p) {
   return (unsigned)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
@@ -626,7 +634,6 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     nact = 0u;
   };
   const size_t img_stride = (size_t)a.H * a.W * a.Cp;  // halves per staged image
-  const XT* zero_page = opaque_ptr(reinterpret_cast<const XT*>(&g_halo_zero));
   // This thread's unit of direct load i is the same for every K step of the
   // tile: its source offset (halves, from the tile's top-left input pixel of
   // time step 0 of the block; 32-bit, checked on the host), whether the
@@ -694,6 +701,9 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     const int nst = tbs < a.T ? min(TB, a.T - tbs) : 0;  // 0: every unit loads zeros
     const uint32_t live = act & ((1u << nst) - 1u);    // steps to load, bit t
     const XT* xb = xtile + (size_t)(tbs * a.B + b) * img_stride + ch * KC;
+    // (offsets in bytes below 2^31, checked on the host; a unit not loaded
+    // takes an offset beyond the range and copies zeros)
+    const cf_v4i xr = halo_rsrc_v4(xb, 0x7fffffffu);
 #pragma unroll
     for (int i = i0; i < i1; ++i) {
       int off, t, blk;
@@ -716,8 +726,8 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
                                                         ok ? (uint32_t)off : HALO_OOB, 0, 0));
         *reinterpret_cast<h8*>(hb + blk * 512 + opaque(lane) * 8) = u8x8_to_h8(r);
       } else {
-        lds_copy16(ok ? xb + off : zero_page,
-                   __builtin_amdgcn_readfirstlane(lds_addr(hb + blk * 512)));
+        lds_buf_copy16(xr, ok ? (uint32_t)off * 2u : HALO_OOB,
+                       __builtin_amdgcn_readfirstlane(lds_addr(hb + blk * 512)));
       }
     }
   };
@@ -764,17 +774,24 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   // loaded at tap j - 2) in the DEEP stride-1 3x3 K loop, whose nine taps
   // per K step keep that assignment the same in every K step.
   const int k16s = a.Cp / 16;
-  const _Float16* wbase = a.w + (size_t)((cout0 + wm * WM) / 32) * KK * k16s * 512 + lane * 8;
-  const size_t limb_stride = (size_t)a.Coutp * KK * a.Cp;
+  // Buffer loads from the wave's first fragment: the lane's 16 bytes at a
+  // constant per-lane offset, the fragment's offset (and the lo limb's) in a
+  // scalar register, so a load takes no vector address arithmetic.  (The
+  // host bounds both limbs' bytes below 2^31.)
+  const _Float16* wbase = a.w + (size_t)((cout0 + wm * WM) / 32) * KK * k16s * 512;
+  const __amdgpu_buffer_rsrc_t wrsrc = halo_rsrc(wbase, 0x7fffffffu);
+  const uint32_t w_lane = (uint32_t)opaque(lane) * 16u;
+  const uint32_t limb_bytes = (uint32_t)a.Coutp * KK * (uint32_t)a.Cp * 2u;
   constexpr bool W2 = DEEP && KK == 9 && NBUF == 2;
   constexpr int NWB = W2 ? 3 : 2;
   h8 ah[NWB][2], al[NWB][2];
   auto load_w = [&](int buf, int tap, int ch) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const _Float16* p = wbase + (size_t)(tap * k16s + ch * 2 + ks) * 512;
-      ah[buf][ks] = *reinterpret_cast<const h8*>(p);
-      al[buf][ks] = *reinterpret_cast<const h8*>(p + limb_stride);
+      const uint32_t so = (uint32_t)((tap * k16s + ch * 2 + ks) * 1024);
+      ah[buf][ks] = __builtin_bit_cast(h8, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, w_lane, so, 0));
+      al[buf][ks] = __builtin_bit_cast(
+          h8, __builtin_amdgcn_raw_buffer_load_b128(wrsrc, w_lane, so + limb_bytes, 0));
     }
   };
 
@@ -811,6 +828,11 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     const uint32_t kr = ks_run(ch);
     constexpr bool SKIP = decltype(skip_c)::value;
     const int stb = ntb == wblk ? ntb : a.T;  // a.T: stage zeros
+    // Taps the next K step's direct loads are spread over: all but the last
+    // (the barrier that publishes them follows the last tap); the first
+    // three in a launch of one workgroup per CU, whose one wave per SIMD
+    // would otherwise wait at that barrier for the latest ones.
+    constexpr int SPAN = DEEP ? (KK - 1 < 3 ? KK - 1 : 3) : KK - 1;
     // B fragments are read TBR steps at a time (a batch), unconditionally
     // (reads of steps this chunk skips hold zeros), one 16-channel half
     // (ks) at a time: half ks of the next batch (the next TBR steps, or the
@@ -859,8 +881,8 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
             // one buffer: the next K step stages after the taps
           } else if (KK == 1) {
             stage_loads(std::true_type{}, stb, nc, nact, hb_next, 0, NPF);
-          } else if (tap + 1 < KK) {
-            const int i0 = (tap * NPF) / (KK - 1), i1 = ((tap + 1) * NPF) / (KK - 1);
+          } else if (tap < SPAN) {
+            const int i0 = (tap * NPF) / SPAN, i1 = ((tap + 1) * NPF) / SPAN;
             if (i1 > i0) stage_loads(std::true_type{}, stb, nc, nact, hb_next, i0, i1);
           }
         }
@@ -1485,10 +1507,11 @@ int make_halo_args(HaloArgs& a, const void* x, const void* w_packed, const float
   if (tile_order && !ag_mask) return (int)hipErrorInvalidValue;
   if ((bias_info & ~(CF_BIAS_SILENT | CF_BIAS_VCHAN)) != 0 || (bias_info && !out_desc))
     return (int)hipErrorInvalidValue;
-  // 32-bit element indices of the outputs, and 32-bit offsets of a tile's
-  // input within one time block (4 steps)
+  // 32-bit element indices of the outputs, 32-bit offsets of a tile's
+  // input within one time block (4 steps) and of the packed weights (both
+  // limbs)
   if (T * B * Cout * Ho * Wo > INT32_MAX || T * B * H * W > ((int64_t)1 << 40) ||
-      4 * B * H * W * Cp > INT32_MAX ||
+      8 * B * H * W * Cp > INT32_MAX || 4 * Coutp * ksize * ksize * Cp > INT32_MAX ||
       B * ((Ho + tile_h - 1) / tile_h) * ((Wo + tile_w - 1) / tile_w) * (Coutp / 64) * 256 > INT32_MAX)
     return (int)hipErrorInvalidValue;
   // (the grid is below 2^23 workgroups, within a count block's tally)
