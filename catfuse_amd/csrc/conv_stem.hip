@@ -80,8 +80,23 @@ struct StemArgs {
   LifParams lif;
 };
 
-template <typename SW, int LM, int S>
+// Raw buffer resource over [base, base + bytes): loads beyond the range
+// return zeros (gfx9 word 3).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t stem_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+constexpr uint32_t STEM_OOB = 0x80000000u;  // beyond every range used here
+
+// LEAN: the SEW / Spiking-ResNet stem as the fused network runs it: a hard
+// reset neuron from its initial state (no v_in) over T = 4 steps, a 7-row
+// filter, every output channel real (Cout = Coutp), the NHWC copy as the
+// only output (no fp32 spikes); the same operations on the same values as
+// the general instantiation, without its run-time branches.
+template <typename SW, int LM, int S, bool LEAN = false>
 __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel(StemArgs a) {
+  static_assert(!LEAN || (sizeof(SW) == 1 && (LM == LM_HARD0_DECAY_P2 || LM == LM_HARD_DECAY_P2)),
+                "lean stem: one-byte spike words, hard reset");
   constexpr int SLD = spike_ld<SW>();
   constexpr int RH = stem_rh<S>(), RW = stem_rw<S>();
   __shared__ __attribute__((aligned(16))) _Float16 xs[2][RH * RW * 4];
@@ -127,15 +142,34 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
     const size_t plane = (size_t)a.H * a.W;
     const float* xb = a.x + (size_t)b * a.Cin * plane;
     float xv[NP][4];
+    if constexpr (LEAN) {
+      // buffer loads over the image's planes: positions outside the image
+      // and channels >= Cin read zeros (the host bounds the image's bytes
+      // below 2^31)
+      const __amdgpu_buffer_rsrc_t xr = stem_rsrc(xb, (uint32_t)(a.Cin * plane * 4));
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      const int p = tid + 256 * i;
-      const int ry = p / RW, rx = p % RW;
-      const int ih = ih0 + ry, iw = iw0 + rx;
-      const bool in = p < RH * RW && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W;
-      const float* src = xb + (size_t)ih * a.W + iw;
+      for (int i = 0; i < NP; ++i) {
+        const int p = tid + 256 * i;
+        const int ry = p / RW, rx = p % RW;
+        const int ih = ih0 + ry, iw = iw0 + rx;
+        const bool in = p < RH * RW && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W;
+        const uint32_t o = in ? (uint32_t)((ih * a.W + iw) * 4) : STEM_OOB;
 #pragma unroll
-      for (int c = 0; c < 4; ++c) xv[i][c] = (in && c < a.Cin) ? src[c * plane] : 0.0f;
+        for (int c = 0; c < 4; ++c)
+          xv[i][c] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+              xr, c < a.Cin ? o + (uint32_t)(c * plane * 4) : STEM_OOB, 0, 0));
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < NP; ++i) {
+        const int p = tid + 256 * i;
+        const int ry = p / RW, rx = p % RW;
+        const int ih = ih0 + ry, iw = iw0 + rx;
+        const bool in = p < RH * RW && ih >= 0 && ih < a.H && iw >= 0 && iw < a.W;
+        const float* src = xb + (size_t)ih * a.W + iw;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) xv[i][c] = (in && c < a.Cin) ? src[c * plane] : 0.0f;
+      }
     }
     bool overflow = false;
 #pragma unroll
@@ -177,10 +211,10 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
   // Membrane state of this image, channels-last ([Hc][Wc][Cout]: a conv
   // output's channels are contiguous, so a lane's four consecutive channels
   // are one 16-byte access): a uniform 64-bit base and 32-bit offsets.
-  const float* vin_b = a.v_in ? a.v_in + (size_t)b * a.Cout * vplane : nullptr;
+  const float* vin_b = (!LEAN && a.v_in) ? a.v_in + (size_t)b * a.Cout * vplane : nullptr;
   float* vout_b = a.v_out ? a.v_out + (size_t)b * a.Cout * vplane : nullptr;
-  const bool full_c = cout0 + BMS <= a.Cout;
-  const bool vec_v = full_c && a.Cout % 4 == 0;   // 16-byte state accesses
+  const bool full_c = LEAN || cout0 + BMS <= a.Cout;
+  const bool vec_v = LEAN || (full_c && a.Cout % 4 == 0);   // 16-byte state accesses
 
   // Epilogue of one column tile: BN, then the LIF over T with a constant z,
   // the 16 elements of the lane stepped together; spike trains -> LDS (four
@@ -201,7 +235,7 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
       vr[r] = lif_initial_v(a.lif);
       bits[r] = 0u;
     }
-    if (vin_b && valid) {
+    if (!LEAN && vin_b && valid) {
       if (vec_v) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -217,7 +251,7 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
       }
     }
     constexpr bool HARD = LM == LM_HARD0_DECAY_P2 || LM == LM_HARD_DECAY_P2;
-    if (HARD && !vin_b && a.T == 4) {
+    if (LEAN || (HARD && !vin_b && a.T == 4)) {
       // Hard reset from the initial state with a constant z: a reset puts v
       // back to the initial value bit for bit (+0 or v_reset; no state is
       // ever -0), so the trajectory restarts, and the spike train follows
@@ -236,6 +270,10 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
                    f4 = u4 >= a.lif.v_th;
         bits[r] = f1 ? 15u : f2 ? 10u : f3 ? 4u : f4 ? 8u : 0u;
         vr[r] = (f1 || f2) ? v0 : f3 ? u1 : f4 ? v0 : u4;
+        // the selects are made here, each element's compare masks dead
+        // right after (left to the uses, sixteen elements' masks would be
+        // live together and spill from the scalar registers)
+        asm volatile("" : "+v"(bits[r]), "+v"(vr[r]));
       }
     } else {
       for (int t = 0; t < a.T; ++t) {
@@ -261,7 +299,18 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
         }
       }
     }
-    if (n < NPIX) {
+    if constexpr (LEAN) {
+      // four channels' words (bytes) per 32-bit LDS store, all channels
+      // real; invalid outputs hold zero words
+      if (n < NPIX) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t w = bits[4 * q] | (bits[4 * q + 1] << 8) | (bits[4 * q + 2] << 16) |
+                             (bits[4 * q + 3] << 24);
+          *reinterpret_cast<uint32_t*>(&spk[n * SLD + cl0 + 8 * q]) = valid ? w : 0u;
+        }
+      }
+    } else if (n < NPIX) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         // channels cl0 + 8q .. + 3; channels >= Cout and invalid outputs
@@ -308,12 +357,12 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
     // filter row kh's fragments in buffer kh % 3, loaded two rows ahead
     h8 wh[3][2], wl[3][2];   // [row % 3][ks]
     load_w(0, wh[0], wl[0]);
-    if (a.KH > 1) load_w(1, wh[1], wl[1]);
+    if (LEAN || a.KH > 1) load_w(1, wh[1], wl[1]);
 #pragma unroll
     for (int kh = 0; kh < MAXKH; ++kh) {
-      if (kh >= a.KH) break;
+      if (!LEAN && kh >= a.KH) break;
       const int cb = kh % 3;
-      if (kh + 2 < a.KH) load_w(kh + 2, wh[(kh + 2) % 3], wl[(kh + 2) % 3]);
+      if (kh + 2 < (LEAN ? MAXKH : a.KH)) load_w(kh + 2, wh[(kh + 2) % 3], wl[(kh + 2) % 3]);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         const int o = (kh * RW + 4 * ks) * 4;
@@ -369,7 +418,7 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
 
   const int HpWp = a.Hp * a.Wp;
   uint32_t anyw = 0u;   // OR of the spike words this thread writes out
-  if (a.out) {
+  if (!LEAN && a.out) {
     // fp32 NCHW: consecutive threads write consecutive pooled pixels of a row.
     for (int i = tid; i < BMS * NPOOL; i += 256) {
       const int pp = i % NPOOL, cl = i / NPOOL;
@@ -383,7 +432,37 @@ __global__ __launch_bounds__(256, sizeof(SW) <= 2 ? 3 : 1) void conv_stem_kernel
       for (int t = 0; t < a.T; ++t) dst[t * tstep] = (float)((wd >> t) & 1u);
     }
   }
-  if (a.out_nhwc) {
+  if constexpr (LEAN) {
+    // NHWC copy, 8 channels of one pooled pixel per store: the pixel's two
+    // words of four channels' spike bytes; at step t, m = (w >> t) &
+    // 0x01010101 holds the four spikes as bytes (the one-byte copy as it
+    // is), and each pair of them spread to the low bytes of two halves
+    // (v_perm) times 0x3c00 is the pair of fp16 spikes.
+    for (int i = tid; i < NPOOL * (BMS / 8); i += 256) {
+      const int c8 = i % (BMS / 8), pp = i / (BMS / 8);
+      const int py = pp / PTW, px = pp % PTW;
+      const int oh = ph0 + py, ow = pw0 + px, co8 = cout0 + 8 * c8;
+      if (oh >= a.Hp || ow >= a.Wp || co8 >= a.cp_out) continue;
+      const uint32_t w0 = *reinterpret_cast<const uint32_t*>(&pooled[pp * SLD + 8 * c8]);
+      const uint32_t w1 = *reinterpret_cast<const uint32_t*>(&pooled[pp * SLD + 8 * c8 + 4]);
+      anyw |= w0 | w1;
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const size_t e = (((size_t)t * a.B + b) * HpWp + (size_t)oh * a.Wp + ow) * a.cp_out + co8;
+        const uint32_t m0 = (w0 >> t) & 0x01010101u, m1 = (w1 >> t) & 0x01010101u;
+        if (a.u8) {
+          *reinterpret_cast<uint2*>(reinterpret_cast<uint8_t*>(a.out_nhwc) + e) = make_uint2(m0, m1);
+        } else {
+          uint4 hv;
+          hv.x = __builtin_amdgcn_perm(0u, m0, 0x0c010c00u) * 0x3c00u;
+          hv.y = __builtin_amdgcn_perm(0u, m0, 0x0c030c02u) * 0x3c00u;
+          hv.z = __builtin_amdgcn_perm(0u, m1, 0x0c010c00u) * 0x3c00u;
+          hv.w = __builtin_amdgcn_perm(0u, m1, 0x0c030c02u) * 0x3c00u;
+          *reinterpret_cast<uint4*>(a.out_nhwc + e) = hv;
+        }
+      }
+    }
+  } else if (a.out_nhwc) {
     // fp16 NHWC: 16 bytes = 8 channels of one pooled pixel per store.
     for (int i = tid; i < NPOOL * (BMS / 8); i += 256) {
       const int c8 = i % (BMS / 8), pp = i / (BMS / 8);
@@ -476,6 +555,20 @@ __global__ __launch_bounds__(256) void pack_stem_weights_kernel(
 
 template <typename SW, int S>
 void launch_stem(const StemArgs& a, int lm, dim3 grid, hipStream_t st) {
+  if constexpr (sizeof(SW) == 1) {
+    const bool lean = !a.v_in && !a.out && a.out_nhwc && a.Cout == a.Coutp && a.T == 4 &&
+                      a.KH == MAXKH && (lm == LM_HARD0_DECAY_P2 || lm == LM_HARD_DECAY_P2) &&
+                      (int64_t)a.Cin * a.H * a.W * 4 <= INT32_MAX;
+    if (lean) {
+      if (lm == LM_HARD0_DECAY_P2)
+        hipLaunchKernelGGL((conv_stem_kernel<SW, LM_HARD0_DECAY_P2, S, true>), grid, dim3(256), 0,
+                           st, a);
+      else
+        hipLaunchKernelGGL((conv_stem_kernel<SW, LM_HARD_DECAY_P2, S, true>), grid, dim3(256), 0,
+                           st, a);
+      return;
+    }
+  }
   if (lm == LM_HARD0_DECAY_P2)
     hipLaunchKernelGGL((conv_stem_kernel<SW, LM_HARD0_DECAY_P2, S>), grid, dim3(256), 0, st, a);
   else if (lm == LM_HARD_DECAY_P2)

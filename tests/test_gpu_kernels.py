@@ -968,6 +968,39 @@ def test_conv_stem_lif_maxpool_parity(cuda, case):
     assert torch.equal(sh[..., :Cout].float(), out.reshape(T * B, Cout, Hp, Wp).permute(0, 2, 3, 1))
 
 
+@pytest.mark.parametrize("v_reset,copy", [(0.0, "f16"), (-0.2, "f16"), (0.0, "u8")])
+def test_conv_stem_lean_matches_general(cuda, v_reset, copy):
+    """The lean stem instantiation (no initial state passed, T = 4, hard
+    reset, a 7-row filter, every channel real, the NHWC copy only) equals the
+    general one bit for bit: the same call with the initial state passed
+    explicitly (v_in = v_reset everywhere) takes the general kernel's
+    stepped LIF; spikes (the copy), final potentials and the count agree."""
+    from catfuse_amd import runtime, snn
+    lif = snn.LIFNode(tau=2.0, v_threshold=0.7, v_reset=v_reset, decay_input=True)
+    conv, bn, lif = _layer(3, 64, 7, 2, 3, seed=64, lif=lif)
+    img = torch.randn(3, 3, 61, 77, generator=_gen(65)) * 1.5
+    r = _runner(conv, bn, lif, cuda)
+    x = img.to(cuda).unsqueeze(0).expand(4, 3, 3, 61, 77)
+    prev = runtime.SPIKE_COPY
+    runtime.set_spike_copy(copy)
+    try:
+        blk_a, blk_b = runtime.count_block(cuda), runtime.count_block(cuda)
+        out_a, v_a = r.run_stem_pool(x, nz_out=blk_a, gen_cell=[0])
+        v0 = torch.full_like(v_a, v_reset)
+        out_b, v_b = r.run_stem_pool(x, v0, nz_out=blk_b, gen_cell=[0])
+        torch.cuda.synchronize()
+        Hp, Wp = out_a.shape[3], out_a.shape[4]
+        sh_a = runtime.shadow_of(out_a, (12, Hp, Wp, 64), u8_ok=True)
+        sh_b = runtime.shadow_of(out_b, (12, Hp, Wp, 64), u8_ok=True)
+        assert sh_a.dtype == sh_b.dtype == (torch.uint8 if copy == "u8" else torch.float16)
+        assert bool(sh_a.any())
+        assert torch.equal(sh_a, sh_b)
+        assert torch.equal(v_a.view(torch.int32), v_b.view(torch.int32))
+        assert int(blk_a[1].item()) == int(blk_b[1].item())
+    finally:
+        runtime.set_spike_copy(prev)
+
+
 def test_conv_stem_range_flag(cuda):
     """An image value outside fp16's range raises the sticky status bit."""
     from catfuse_amd import runtime
