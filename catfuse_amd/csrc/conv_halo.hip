@@ -832,7 +832,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     // (the barrier that publishes them follows the last tap); the first
     // three in a launch of one workgroup per CU, whose one wave per SIMD
     // would otherwise wait at that barrier for the latest ones.
-    constexpr int SPAN = DEEP ? (KK - 1 < 3 ? KK - 1 : 3) : KK - 1;
+    constexpr int SPAN = KK - 1 < 3 ? KK - 1 : 3;
     // B fragments are read TBR steps at a time (a batch), unconditionally
     // (reads of steps this chunk skips hold zeros), one 16-channel half
     // (ks) at a time: half ks of the next batch (the next TBR steps, or the
@@ -1131,11 +1131,11 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
         }
       }
     }
-    // Lean path: the identity of step t is loaded into idq[t & 1] while step
-    // t - 1 is computed, before that step's stores (zeros without an
-    // identity or beyond the block: an empty range).
-    // (one-byte copies: the four channels' bytes, widened when used)
-    h4 idq[LEAN && !U8 ? 2 : 1][NT][4];
+    // One-byte copies: the identity of step t is loaded into idr[t & 1]
+    // while step t - 1 is computed, before that step's stores (zeros without
+    // an identity or beyond the block: an empty range): the four channels'
+    // bytes, widened when used.  (The lean fp16 path adds the identity to
+    // the staged tile at copy-out instead, below.)
     uint32_t idr[U8 ? 2 : 1][NT][4];
     auto id_load = [&](int t) {
       const bool have = id_nhwc && t < nsteps;
@@ -1148,21 +1148,17 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
 #pragma unroll
         for (int nt = 0; nt < NT; ++nt) {
           const unsigned off = (unsigned)((epix[nt] * a.cp_id + col + 8 * r4) * XB);
-          if constexpr (U8)
-            idr[t & 1][nt][r4] = __builtin_amdgcn_raw_buffer_load_b32(rid, off, 0, 0);
-          else
-            idq[t & 1][nt][r4] =
-                __builtin_bit_cast(h4, __builtin_amdgcn_raw_buffer_load_b64(rid, off, 0, 0));
+          idr[t & 1][nt][r4] = __builtin_amdgcn_raw_buffer_load_b32(rid, off, 0, 0);
         }
     };
-    if constexpr (LEAN) id_load(0);
+    if constexpr (U8) id_load(0);
     auto epi_step = [&](int t) {
       const int tt = tb0 + t;
       const int img = tt * a.B + b;
       _Float16* ostage = obuf + (t % NOBUF) * OSTEP;
       const XT* idn = id_nhwc;
       const XT* idbase = idn ? idn + (size_t)img * HoWo * a.cp_id : nullptr;
-      if constexpr (LEAN) {
+      if constexpr (U8) {
         if (t + 1 < TB) id_load(t + 1);
       }
 #pragma unroll
@@ -1179,7 +1175,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
           if constexpr (U8) {
             idh = u8x4_to_h4(idr[t & 1][nt][r4]);
           } else if constexpr (LEAN) {
-            idh = idq[t & 1][nt][r4];
+            // (added at copy-out)
           } else {
             if (idbase)
               idh = *reinterpret_cast<const h4*>(idbase + (unsigned)(epix[nt] * a.cp_id + col + 8 * r4));
@@ -1198,7 +1194,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
               v[nt][r] = vv;
             }
             pk = idh + sph;
-            if (a.nz_out) {
+            if (U8 && a.nz_out) {
               const u32x2 pw = __builtin_bit_cast(u32x2, pk);
               anyw |= (n_ok[nt] && col + 8 * r4 < a.Cout) ? (pw[0] | pw[1]) : 0u;
             }
@@ -1238,7 +1234,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     // Lean path: this thread's chunks are the same at every step (their
     // store offsets within a step's image and their LDS staging offsets),
     // computed once per block.
-    uint32_t lo_off[LEAN ? CPI : 1], lo_lds[LEAN ? CPI : 1];
+    uint32_t lo_off[LEAN ? CPI : 1], lo_lds[LEAN ? CPI : 1], lo_id[LEAN && !U8 ? CPI : 1];
     if constexpr (LEAN) {
 #pragma unroll
       for (int i = 0; i < CPI; ++i) {
@@ -1246,15 +1242,34 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
         const int px = c / CH8, part = c % CH8;
         const int py = px / TW, pxx = px % TW;
         const bool ok = (oh0 + py < a.Ho) & (ow0 + pxx < a.Wo) & (cout0 + part * 8 < a.Cout);
-        lo_off[i] = ok ? (uint32_t)((((oh0 + py) * a.Wo + ow0 + pxx) * a.cp_out + cout0 + part * 8) * XB)
-                       : HALO_OOB;
+        const int pix = (oh0 + py) * a.Wo + ow0 + pxx;
+        lo_off[i] = ok ? (uint32_t)((pix * a.cp_out + cout0 + part * 8) * XB) : HALO_OOB;
         lo_lds[i] = (uint32_t)(px * OLD + part * 8);
+        if constexpr (!U8) lo_id[i] = ok ? (uint32_t)((pix * a.cp_id + cout0 + part * 8) * 2) : HALO_OOB;
       }
     }
+    // Lean fp16 path: the SEW identity is added to the staged tile at
+    // copy-out, one 16-byte chunk (8 channels of a pixel, the copy-out's own
+    // chunk) per load, issued before the step's LIF so it lands under it;
+    // packed fp16 adds of small integers are exact.  Zeros without an
+    // identity (an empty range).
+    u32x4 idc[LEAN && !U8 ? CPI : 1];
+    auto idc_load = [&](int t) {
+      if constexpr (LEAN && !U8) {
+        const bool have = id_nhwc && t < nsteps;
+        const __amdgpu_buffer_rsrc_t rid =
+            halo_rsrc(have ? (const void*)(id_nhwc + (size_t)((tb0 + t) * a.B + b) * HoWo * a.cp_id)
+                           : (const void*)a.identity_nhwc,
+                      have ? (uint32_t)(HoWo * a.cp_id * 2) : 0u);
+#pragma unroll
+        for (int i = 0; i < CPI; ++i) idc[i] = __builtin_amdgcn_raw_buffer_load_b128(rid, lo_id[i], 0, 0);
+      }
+    };
 #pragma unroll
     for (int t = 0; t < TB; ++t) {
       if (t > 0 && t >= nsteps) break;  // every block has a first step
       if (NOBUF == 1 && t > 0) __syncthreads();  // the previous step's copy-out is complete
+      idc_load(t);
       epi_step(t);
       if (a.out_nhwc) {
         __syncthreads();  // the step's tile is staged
@@ -1272,7 +1287,13 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
             const uint32_t off = lo_off[i];
             // streaming (non-temporal) stores: the copy is read back by the
             // next layer only after the whole output is written
-            const u32x4 chunk = *reinterpret_cast<const u32x4*>(&ostage[lo_lds[i]]);
+            u32x4 chunk = *reinterpret_cast<const u32x4*>(&ostage[lo_lds[i]]);
+            if constexpr (!U8) {
+              chunk = __builtin_bit_cast(u32x4, __builtin_bit_cast(h8, chunk) +
+                                                    __builtin_bit_cast(h8, idc[i]));
+              if (a.nz_out)
+                anyw |= off != HALO_OOB ? (chunk[0] | chunk[1] | chunk[2] | chunk[3]) : 0u;
+            }
             if constexpr (U8)
               __builtin_amdgcn_raw_buffer_store_b64(h8_to_u8x8(__builtin_bit_cast(h8, chunk)), ro,
                                                     off, 0, CF_CPOL_NT);
