@@ -937,10 +937,13 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   uint32_t s_act;
   next_step(0, -1, s_tb, s_ch, s_act);
   int pf_tb = s_tb;  // block of the K step already staged into buffer 0
+  // (A single time block computes its units once, here, and stages its
+  // first K step from them.)
+  if constexpr (ONEB) units_precompute();
   if (s_tb < a.T) {
     load_w(0, 0, s_ch);
     if constexpr (W2) load_w(1, 1, s_ch);
-    stage_loads(std::false_type{}, s_tb, s_ch, s_act, halo, 0, NPF);
+    stage_loads(std::integral_constant<bool, ONEB>{}, s_tb, s_ch, s_act, halo, 0, NPF);
   }
 
   for (int tb0 = 0; tb0 < (ONEB ? 1 : a.T); tb0 += TB) {
@@ -955,7 +958,7 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     // The block's K steps alternate halo buffers, starting with buffer 0.
     // (The units are recomputed per block, unconditionally, so that they are
     // not live across the epilogue.)
-    units_precompute();
+    if constexpr (!ONEB) units_precompute();
     int buf = 0;
     while (s_tb == tb0) {
       int ntb, nc;
