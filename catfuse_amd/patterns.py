@@ -208,10 +208,13 @@ class _ConvPattern(CTFPattern):
         return None
 
     def _ensure_params(self) -> ConvLIFParams:
+        # parameters read from the module's own dict (attribute lookup goes
+        # through nn.Module.__getattr__ on every call)
+        P = self._parameters
+        w, cb = P["weight"], P.get("conv_bias")
         bn = self._bn_tensors()
-        key = (id(self.weight), self.weight._version,
-               None if self.conv_bias is None else (id(self.conv_bias), self.conv_bias._version),
-               None if bn is None else tuple((id(t), t._version) for t in bn if t is not None))
+        key = (id(w), w._version, None if cb is None else (id(cb), cb._version),
+               None if bn is None else tuple([(id(t), t._version) for t in bn if t is not None]))
         if self._params_key == key and self._params is not None:
             return self._params
         with torch.no_grad():
@@ -279,7 +282,8 @@ class PartialFusionConvBNLIF(_ConvPattern):
         self._impl = _dense_impl()
 
     def _bn_tensors(self):
-        return (self.bn_weight, self.bn_bias, self.running_mean, self.running_var)
+        P, B = self._parameters, self._buffers
+        return (P["bn_weight"], P["bn_bias"], B["running_mean"], B["running_var"])
 
     def forward(self, x, sew_identity=None):
         pr, self._pair_result = self._pair_result, None
@@ -883,15 +887,21 @@ def _paired_forward(fa, fb, x):
     ib.check_input(x, fb.spec)
     if ia.input_is_analog(x) or ib.input_is_analog(x):
         return None
-    ra = ia.runner(fa.spec, fa._ensure_params(), x.device)
-    rb = ib.runner(fb.spec, fb._ensure_params(), x.device)
-    if not runtime.halo_pair_supported(ra, rb, x):
-        return None
+    dev = x.device
+    ra = ia.runner(fa.spec, fa._ensure_params(), dev)
+    rb = ib.runner(fb.spec, fb._ensure_params(), dev)
     B = x.shape[1]
     Ho, Wo = fa.spec.output_hw(x.shape[3], x.shape[4])
-    va = fa.state.peek((B, fa.out_channels, Ho, Wo), x.device)
-    vb = fb.state.peek((B, fb.out_channels, Ho, Wo), x.device)
-    out_a, v_a, out_b, v_b = runtime.run_halo_pair(ra, rb, x.contiguous(), va, vb)
+    va = fa.state.peek((B, fa.out_channels, Ho, Wo), dev)
+    vb = fb.state.peek((B, fb.out_channels, Ho, Wo), dev)
+    # no initial states: the launch plan cached for x's signature, when
+    # there is one (it was made by the same support checks)
+    res = runtime.halo_pair_repeat(ra, rb, x) if va is None and vb is None else None
+    if res is None:
+        if not runtime.halo_pair_supported(ra, rb, x):
+            return None
+        res = runtime.run_halo_pair(ra, rb, x.contiguous(), va, vb)
+    out_a, v_a, out_b, v_b = res
     fa.state.set(v_a)
     fb.state.set(v_b)
     return out_a, out_b

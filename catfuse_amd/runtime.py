@@ -282,6 +282,12 @@ def _metadata_functions():
 _METADATA = None
 
 
+def _ver(x: torch.Tensor) -> int:
+    """x._version, read from the plain tensor a lazy output was made from
+    (it shares x's version counter) so no torch-function dispatch runs."""
+    return x.__dict__.get("_cf_base", x)._version
+
+
 def _meta_of(base: torch.Tensor) -> tuple:
     """(shape, dtype, device, numel, contiguous) of a plain tensor."""
     return (base.shape, base.dtype, base.device, base.numel(), base.is_contiguous())
@@ -410,9 +416,11 @@ class NHWCSpikes(_LazyTensor):
     first (cf_resolve_copy)."""
 
     @staticmethod
-    def __new__(cls, base: torch.Tensor, nhwc: torch.Tensor, tokens: bool = False):
+    def __new__(cls, base: torch.Tensor, nhwc: torch.Tensor, tokens: bool = False, meta=None):
+        # meta: base's _meta_of record when the caller already holds it
         t = base.as_subclass(cls)
-        t._cf_meta = _meta_of(base)
+        t._cf_meta = _meta_of(base) if meta is None else meta
+        t._cf_base = base
         t._cf_pending = True
         t._cf_tokens = tokens
         t._cf_nhwc = (nhwc, base._version)
@@ -456,6 +464,7 @@ class ChannelState(_LazyTensor):
                 uniform: bool = False):
         t = base.as_subclass(cls)
         t._cf_meta = _meta_of(base)
+        t._cf_base = base
         t._cf_pending = True
         t._cf_state = (v_chan, desc, base._version)
         t._cf_sticky = torch.cuda.is_current_stream_capturing()
@@ -540,7 +549,7 @@ def pixel_tokens(x: torch.Tensor) -> Optional[torch.Tensor]:
             or x.shape[3] != 1 or x.shape[4] != 1):
         return None
     nhwc, ver = x._cf_nhwc
-    if ver != x._version:
+    if ver != _ver(x):
         return None
     T, B, C = x.shape[:3]
     with torch._C.DisableTorchFunctionSubclass():
@@ -565,7 +574,7 @@ def token_shadow(x: torch.Tensor, cp: int, resolve: bool = True) -> Optional[tor
         return None
     t, ver = sh
     rows = x.numel() // x.shape[-1]
-    if (ver != x._version or t.device != x.device or t.shape[-1] != cp
+    if (ver != _ver(x) or t.device != x.device or t.shape[-1] != cp
             or t.numel() != rows * cp):
         return None
     if t.dtype == torch.uint8:
@@ -596,7 +605,7 @@ def attach_shadow(out: torch.Tensor, nhwc: torch.Tensor) -> None:
     """Record the fp16 NHWC copy a fused conv wrote next to its fp32 output,
     tagged with the output's version counter (any in-place change of `out`
     invalidates it)."""
-    out._cf_nhwc = (nhwc, out._version)
+    out._cf_nhwc = (nhwc, _ver(out))
 
 
 def shadow_of(x: torch.Tensor, shape, resolve: bool = True,
@@ -612,7 +621,7 @@ def shadow_of(x: torch.Tensor, shape, resolve: bool = True,
     if sh is None:
         return None
     t, ver = sh
-    if ver != x._version or tuple(t.shape) != tuple(shape) or t.device != x.device:
+    if ver != _ver(x) or tuple(t.shape) != tuple(shape) or t.device != x.device:
         return None
     if t.dtype == torch.uint8 and not u8_ok:
         return _widen(x, t)
@@ -625,6 +634,11 @@ def shadow_of(x: torch.Tensor, shape, resolve: bool = True,
 # alias pointer) let a StaticZero launch leave its outputs unwritten; off
 # for comparisons against the always-writing path.
 COPY_ELISION = True
+
+# Launch plans cached per input signature for the common fused-conv launches
+# (ConvLIFRunner._dense_repeat, halo_pair_repeat); off for comparisons
+# against the general path.
+REPEAT_PLANS = True
 
 
 def new_out_desc(device) -> torch.Tensor:
@@ -649,13 +663,13 @@ def written_desc(device) -> torch.Tensor:
 def attach_desc(out: torch.Tensor, desc: torch.Tensor, keep=()) -> None:
     """Record the output descriptor of out's copy; keep: the copies its
     values may alias (held alive with it)."""
-    out._cf_desc = (desc, out._version, tuple(keep))
+    out._cf_desc = (desc, _ver(out), tuple(keep))
 
 
 def desc_of(x: torch.Tensor) -> Optional[torch.Tensor]:
     """The descriptor of x's current copy (None: the copy is written)."""
     d = getattr(x, "_cf_desc", None)
-    if d is None or d[1] != x._version:
+    if d is None or d[1] != _ver(x):
         return None
     return d[0]
 
@@ -702,7 +716,7 @@ def attach_count(out: torch.Tensor, blk: torch.Tensor, gen_cell: list) -> None:
     is all zero).  gen_cell is the producing layer's call counter: a later
     call of the same layer republishes the block, which then no longer
     describes this output."""
-    out._cf_count = (blk, gen_cell, gen_cell[0], out._version)
+    out._cf_count = (blk, gen_cell, gen_cell[0], _ver(out))
 
 
 def count_of(x: torch.Tensor) -> Optional[torch.Tensor]:
@@ -711,7 +725,7 @@ def count_of(x: torch.Tensor) -> Optional[torch.Tensor]:
     if c is None:
         return None
     blk, cell, gen, ver = c
-    if ver != x._version or cell[0] != gen or blk.device != x.device:
+    if ver != _ver(x) or cell[0] != gen or blk.device != x.device:
         return None
     return blk
 
@@ -1009,6 +1023,14 @@ def route_from_nnz(nnz: torch.Tensor, numel: int, sparse_threshold: float,
 # Conv -> BN -> LIF
 # ---------------------------------------------------------------------------
 
+class _DensePlan:
+    """What run_mfma's dense route decides from an input signature alone
+    (ConvLIFRunner._dense_plan): the copy format, the output shapes, the
+    static launch arguments and the layer's bias response."""
+    __slots__ = ("u8", "need_v", "vshape", "cshape", "cdtype", "oshape", "ometa", "nz_out",
+                 "nz_ptr", "weights", "numel", "T", "cp_out", "bias", "fn", "tail")
+
+
 class ConvLIFRunner:
     """Device state + launches for one fused Conv -> (BN) -> LIF layer.
 
@@ -1033,6 +1055,7 @@ class ConvLIFRunner:
         self.w_packed = self.alpha = self.beta = None
         self.alpha_direct = self.beta_direct = None
         self._ws = {}
+        self._plans = {}  # input signature -> _DensePlan (or False: not covered)
         self._gen = [0]  # calls that published the output count block
 
     def refresh(self):
@@ -1076,6 +1099,7 @@ class ConvLIFRunner:
         self._w_f32 = w
         self._wt_f32 = w.reshape(self.Cout, -1).t().contiguous()   # [Cin*KH*KW][Cout]
         self._bias_resp = {}
+        self._plans = {}
         self._packed_key = key
 
     def bias_response(self, device, T: int, pool: bool = False):
@@ -1151,6 +1175,168 @@ class ConvLIFRunner:
             self._ws["nz_out"] = t
         return t
 
+    def _dense_plan(self, key, x, xp, identity, ish, xshape, dev):
+        """The _DensePlan of one input signature (see _dense_repeat), made
+        with the checks and choices of run_mfma's general path; False when
+        that path would do anything else than one dense launch on the
+        copies as they are (repack, widen a byte copy, an fp32 identity, an
+        error)."""
+        if len(xshape) != 5:
+            return False
+        T, B, C, H, W = xshape
+        Ho, Wo = self.out_hw(H, W)
+        cp_out = pad32(self.Cout)
+        meta = key[0]     # x: fp32, contiguous, on the GPU (require_gpu_tensor)
+        ok = (C == self.Cin and Ho >= 1 and Wo >= 1 and meta[1] == torch.float32 and meta[4]
+              and dev.type == "cuda" and xp.device == dev
+              and tuple(xp.shape) == (T * B, H, W, self.Cp)
+              and xp.dtype in (torch.float16, torch.uint8))
+        id_u8 = False
+        if ok and identity is not None:
+            ic = ish[0]
+            ok = (tuple(key[3]) == (T, B, self.Cout, Ho, Wo)
+                  and key[7] == (torch.float32, dev) and key[8]
+                  and ic.device == dev and tuple(ic.shape) == (T * B, Ho, Wo, cp_out)
+                  and ic.dtype in (torch.float16, torch.uint8))
+            id_u8 = ok and ic.dtype == torch.uint8
+        if not ok:
+            return False
+        u8 = (SPIKE_COPY == "u8" and self.Cout % 32 == 0 and self.halo_lean_ok(T, B, Ho, Wo)
+              and xp.dtype == torch.uint8 and (identity is None or id_u8))
+        if (xp.dtype == torch.uint8 or id_u8) and not u8:
+            return False      # the general path widens the byte copy first
+        p = _DensePlan()
+        p.u8 = u8
+        p.need_v = key[6] or T > 2
+        p.vshape = (B, self.Cout, Ho, Wo)
+        p.cshape = (T * B, Ho, Wo, cp_out)
+        p.cdtype = torch.uint8 if u8 else torch.float16
+        p.oshape = (T, B, self.Cout, Ho, Wo)
+        p.ometa = (torch.Size(p.oshape), torch.float32, dev, T * B * self.Cout * Ho * Wo, True)
+        p.nz_out = self.out_counter(dev)
+        p.nz_ptr = p.nz_out.data_ptr()
+        p.weights = (self.w_packed.data_ptr(), self.alpha.data_ptr(), self.beta.data_ptr())
+        p.numel = T * B * C * H * W
+        p.T = T
+        p.cp_out = cp_out
+        p.bias = None
+        if u8:
+            p.fn = _hip.lib().cf_conv_halo_u8
+            p.tail = (T, B, self.Cp, self.Cout, self.Coutp, H, W, Ho, Wo, self.KH, self.stride,
+                      self.padding, 0) + tuple(self.lif)
+        else:
+            p.fn = _hip.lib().cf_conv_mfma
+            p.tail = (T, B, self.Cp, self.Cout, self.Coutp, H, W, Ho, Wo, self.KH, self.KW,
+                      self.stride, self.padding, B, 0, 0, 0, EPI_LIF) + tuple(self.lif)
+        return p
+
+    def _dense_repeat(self, x, identity, want_v_out, sparse_threshold):
+        """run_mfma's launch for its common case from a plan cached per input
+        signature: a dense-route LIF launch with no initial state whose
+        input (and spike identity) carry a current NHWC copy, writing the
+        output's copy, with no kernel timer.  The checks and choices that
+        depend only on the signature (shapes, copy formats, device, whether
+        the state is wanted, the copy settings) ran once when the plan was
+        made; each call reads the copies' descriptors and count blocks,
+        allocates the outputs and launches with the arguments the general
+        path passes.  None when the case is not covered (run_mfma then takes
+        its general path)."""
+        d = x.__dict__
+        sh = d.get("_cf_nhwc")
+        if sh is None:
+            return None
+        xp, ver = sh
+        if ver != d.get("_cf_base", x)._version:
+            return None
+        meta = d.get("_cf_meta") if d.get("_cf_pending", False) else None
+        if meta is None:
+            meta = _meta_of(x)
+        xshape, dev = meta[0], meta[2]
+        ish = None
+        if identity is not None:
+            idd = identity.__dict__
+            ish = idd.get("_cf_nhwc")
+            if ish is None or ish[1] != idd.get("_cf_base", identity)._version:
+                return None
+            ic = ish[0]
+            im = idd.get("_cf_meta") if idd.get("_cf_pending", False) else None
+            if im is None:
+                im = _meta_of(identity)
+            key = (meta, xp.shape, xp.dtype, im[0], ic.shape, ic.dtype, want_v_out, im[1:3],
+                   im[4], SPIKE_COPY, COPY_ELISION)
+        else:
+            key = (meta, xp.shape, xp.dtype, None, None, None, want_v_out, None, None,
+                   SPIKE_COPY, COPY_ELISION)
+        self._ensure_packed(dev)
+        p = self._plans.get(key)
+        if p is None:
+            p = self._plans[key] = self._dense_plan(key, x, xp, identity, ish, xshape, dev)
+        if p is False:
+            return None
+        # the input's descriptor and count block (as desc_of / count_of)
+        dd = d.get("_cf_desc")
+        x_desc = dd[0] if dd is not None and dd[1] == ver else None
+        c = d.get("_cf_count")
+        nnz = c[0] if c is not None and c[3] == ver and c[1][0] == c[2] else None
+        id_ptr = id_desc = id_nnz = 0
+        id_keep = ()
+        if identity is not None:
+            iver = ish[1]
+            ic = ish[0]
+            id_ptr = ic.data_ptr()
+            dd = idd.get("_cf_desc")
+            idesc = dd[0] if dd is not None and dd[1] == iver else written_desc(dev)
+            id_desc = idesc.data_ptr()
+            c = idd.get("_cf_count")
+            if c is not None and c[3] == iver and c[1][0] == c[2]:
+                id_nnz = c[0].data_ptr()
+            id_keep = (ic,) + (() if dd is None else dd[2])
+        v_out = torch.empty(p.vshape, dtype=torch.float32, device=dev) if p.need_v else None
+        nhwc = torch.empty(p.cshape, dtype=p.cdtype, device=dev)
+        base = torch.empty(p.oshape, dtype=torch.float32, device=dev)
+        out = NHWCSpikes(base, nhwc, meta=p.ometa)
+        gen = self._gen
+        gen[0] += 1
+        out._cf_count = (p.nz_out, gen, gen[0], base._version)
+        desc = None
+        info = 0
+        v_chan = None
+        if COPY_ELISION and (nnz is not None or x_desc is not None):
+            desc = torch.empty(2, dtype=torch.int64, device=dev)
+            r = p.bias
+            if r is None:
+                r = p.bias = self.bias_response(dev, p.T)
+            if r is not None:
+                info = (1 if r[1] else 0) | (2 if v_out is not None else 0)
+                if v_out is not None:
+                    v_chan = r[0]
+            if info & 1:
+                out._cf_desc = (desc, base._version, id_keep)
+        w, al, be = p.weights
+        vo = v_out.data_ptr() if v_out is not None else None
+        dp = desc.data_ptr() if desc is not None else None
+        stream = _hip.stream(dev)
+        if p.u8:
+            rc = p.fn(xp.data_ptr(), w, al, be, None, vo, nhwc.data_ptr(), p.cp_out, id_ptr or None,
+                      p.cp_out, None, None, nnz.data_ptr() if nnz is not None else None, p.nz_ptr,
+                      x_desc.data_ptr() if x_desc is not None else None, id_desc or None, dp,
+                      info, id_nnz or None, p.numel, float(sparse_threshold), *p.tail, stream)
+            check(rc, "cf_conv_halo_u8")
+        else:
+            rc = p.fn(xp.data_ptr(), w, al, be, None, vo, None, nhwc.data_ptr(), p.cp_out, None,
+                      id_ptr or None, p.cp_out, ID_ADD_SPIKE, None, None,
+                      nnz.data_ptr() if nnz is not None else None, p.nz_ptr,
+                      x_desc.data_ptr() if x_desc is not None else None, id_desc or None, dp,
+                      info, id_nnz or None, p.numel, float(sparse_threshold), *p.tail, stream)
+            check(rc, "cf_conv_mfma")
+        self.last_nnz = nnz
+        self.last_numel = p.numel
+        self.last_tiles = None
+        self.last_order = None
+        if not want_v_out:
+            return out, None
+        return out, (ChannelState(v_out, v_chan, desc) if v_chan is not None else v_out)
+
     def run_mfma(self, x: torch.Tensor, v_in=None, *, epilogue=EPI_LIF, want_v_out=True,
                  identity=None, identity_mode=ID_ADD_SPIKE, sparse=None, sparse_threshold=0.7,
                  static_zero=True, emit_nhwc=True):
@@ -1168,6 +1354,12 @@ class ConvLIFRunner:
         epilogue; out is then the pooled spikes [T, B, Cout, Ho//2, Wo//2]
         (written as the fp16 NHWC copy) and v_out the pooled membrane state.
         Returns (out, v_out)."""
+        if (sparse is None and epilogue == EPI_LIF and emit_nhwc and static_zero
+                and v_in is None and identity_mode == ID_ADD_SPIKE and _timer is None
+                and REPEAT_PLANS):
+            r = self._dense_repeat(x, identity, want_v_out, sparse_threshold)
+            if r is not None:
+                return r
         require_gpu_tensor(x, "x")
         T, B, C, H, W = x.shape
         if C != self.Cin:
@@ -1680,6 +1872,123 @@ def halo_pair_supported(ra: "ConvLIFRunner", rb: "ConvLIFRunner", x: torch.Tenso
     return T * B * max(ra.Cout, rb.Cout) * Ho * Wo <= 2 ** 31 - 1 and 4 * B * H * W * ra.Cp < 2 ** 31
 
 
+class _PairPlan:
+    """What run_halo_pair decides from an input signature alone
+    (halo_pair_repeat): the copy format, the output shapes, the partner and
+    the static launch arguments."""
+    __slots__ = ("rb", "rb_key", "u8", "fn", "numel", "T", "head", "halves")
+
+
+def _halo_pair_plan(ra, rb, x, xp, meta):
+    """The _PairPlan of one input signature, made with run_halo_pair's
+    checks; False when run_halo_pair would do anything else than one paired
+    launch on x's copy as it is (pack the input, widen a byte copy, an
+    error)."""
+    if len(meta[0]) != 5 or meta[1] != torch.float32 or not meta[4]:
+        return False
+    T, B, C, H, W = meta[0]
+    dev = meta[2]
+    if not halo_pair_supported(ra, rb, x):
+        return False
+    if xp.device != dev or tuple(xp.shape) != (T * B, H, W, ra.Cp):
+        return False
+    u8 = SPIKE_COPY == "u8" and xp.dtype == torch.uint8
+    if xp.dtype != (torch.uint8 if u8 else torch.float16):
+        return False
+    Ho, Wo = ra.out_hw(H, W)
+    p = _PairPlan()
+    p.rb, p.rb_key = rb, rb._packed_key
+    p.u8 = u8
+    p.fn = _hip.lib().cf_conv_halo_pair_u8 if u8 else _hip.lib().cf_conv_halo_pair
+    p.numel = T * B * C * H * W
+    p.T = T
+    p.head = (p.numel, T, B, ra.Cp, H, W, Ho, Wo)
+    halves = []
+    for r in (ra, rb):
+        cp = pad32(r.Cout)
+        nz = r.out_counter(dev)
+        halves.append((
+            r, (B, r.Cout, Ho, Wo), (T * B, Ho, Wo, cp), (T, B, r.Cout, Ho, Wo),
+            (torch.Size((T, B, r.Cout, Ho, Wo)), torch.float32, dev, T * B * r.Cout * Ho * Wo,
+             True),
+            nz, (r.w_packed.data_ptr(), r.alpha.data_ptr(), r.beta.data_ptr()), cp,
+            nz.data_ptr(), (r.Cout, r.Coutp, r.padding)))
+    p.halves = tuple(halves)
+    return p
+
+
+def halo_pair_repeat(ra, rb, x):
+    """run_halo_pair's launch for its common case from a plan cached per
+    input signature: no initial states, x carrying a current NHWC copy, no
+    kernel timer.  The checks that depend only on the signature ran when
+    the plan was made; each call reads the copy's descriptor and count
+    block, allocates the outputs and launches with the arguments the
+    general path passes.  None when the case is not covered."""
+    if _timer is not None or not REPEAT_PLANS:
+        return None
+    d = x.__dict__
+    sh = d.get("_cf_nhwc")
+    if sh is None:
+        return None
+    xp, ver = sh
+    if ver != d.get("_cf_base", x)._version:
+        return None
+    meta = d.get("_cf_meta") if d.get("_cf_pending", False) else None
+    if meta is None:
+        meta = _meta_of(x)
+    dev = meta[2]
+    ra._ensure_packed(dev)
+    rb._ensure_packed(dev)
+    key = ("pair", meta, xp.shape, xp.dtype, SPIKE_COPY, COPY_ELISION)
+    p = ra._plans.get(key)
+    if p is None or (p is not False and (p.rb is not rb or p.rb_key is not rb._packed_key)):
+        p = ra._plans[key] = _halo_pair_plan(ra, rb, x, xp, meta)
+    if p is False:
+        return None
+    dd = d.get("_cf_desc")
+    x_desc = dd[0] if dd is not None and dd[1] == ver else None
+    c = d.get("_cf_count")
+    nnz = c[0] if c is not None and c[3] == ver and c[1][0] == c[2] else None
+    elide = COPY_ELISION and (nnz is not None or x_desc is not None)
+    res = []
+    args = []
+    cdtype = torch.uint8 if p.u8 else torch.float16
+    for r, vshape, cshape, oshape, ometa, nz, wts, cp, nz_ptr, geo in p.halves:
+        v_out = torch.empty(vshape, dtype=torch.float32, device=dev)
+        nhwc = torch.empty(cshape, dtype=cdtype, device=dev)
+        base = torch.empty(oshape, dtype=torch.float32, device=dev)
+        out = NHWCSpikes(base, nhwc, meta=ometa)
+        gen = r._gen
+        gen[0] += 1
+        out._cf_count = (nz, gen, gen[0], base._version)
+        desc = None
+        info = 0
+        v_chan = None
+        if elide:
+            desc = torch.empty(2, dtype=torch.int64, device=dev)
+            rr = r.bias_response(dev, p.T)
+            if rr is not None:
+                info = (1 if rr[1] else 0) | 2
+                v_chan = rr[0]
+            if info & 1:
+                out._cf_desc = (desc, base._version, ())
+        res.append((out, v_out, v_chan, desc))
+        args += [*wts, None, v_out.data_ptr(), nhwc.data_ptr(), cp, nz_ptr,
+                 desc.data_ptr() if desc is not None else None, info, *geo]
+    check(p.fn(xp.data_ptr(), nnz.data_ptr() if nnz is not None else None,
+               x_desc.data_ptr() if x_desc is not None else None, *p.head, *args, *ra.lif,
+               _hip.stream(dev)), "cf_conv_halo_pair")
+    for r in (ra, rb):
+        r.last_nnz = nnz
+        r.last_numel = p.numel
+    (oa, voa, ca, da), (ob, vob, cb, db) = res
+    if ca is not None:
+        voa = ChannelState(voa, ca, da)
+    if cb is not None:
+        vob = ChannelState(vob, cb, db)
+    return oa, voa, ob, vob
+
+
 def run_halo_pair(ra: "ConvLIFRunner", rb: "ConvLIFRunner", x: torch.Tensor, v_in_a=None,
                   v_in_b=None):
     """A ResNet block's stride-2 3x3 conv1 (ra) and 1x1 downsample (rb) of
@@ -1687,6 +1996,10 @@ def run_halo_pair(ra: "ConvLIFRunner", rb: "ConvLIFRunner", x: torch.Tensor, v_i
     what run_mfma would return (an NHWC-backed spike tensor with its count
     block).  x: [T, B, Cin, H, W] (its fp16 NHWC copy when it carries one,
     else packed here).  Returns (out_a, v_out_a, out_b, v_out_b)."""
+    if v_in_a is None and v_in_b is None:
+        r = halo_pair_repeat(ra, rb, x)
+        if r is not None:
+            return r
     if not halo_pair_supported(ra, rb, x):
         raise ValueError("cf_conv_halo_pair does not cover these convolutions")
     T, B, C, H, W = x.shape

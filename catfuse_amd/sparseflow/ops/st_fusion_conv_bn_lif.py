@@ -82,7 +82,9 @@ class STFusionConvBNLIF(CTFPattern):
         self.route_counts = {"StaticZero": 0, "SparseFlow": 0, "DenseKeep": 0}
 
     def _ensure_params(self) -> ConvLIFParams:
-        key = (id(self.weight), id(self.bias), id(self.bn_scale), id(self.bn_bias_folded))
+        P, B = self._parameters, self._buffers
+        key = (id(P["weight"]), id(P.get("bias")), id(B.get("bn_scale")),
+               id(B.get("bn_bias_folded")))
         if self._params_key != key or self._params is None:
             self._params = ConvLIFParams(self.weight, self.bias, self.bn_scale,
                                          self.bn_bias_folded)

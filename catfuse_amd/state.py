@@ -37,11 +37,15 @@ class StateBuffer:
 
     def set(self, v: torch.Tensor) -> None:
         # a fused launch's lazily filled state (no autograd history) is kept
-        # as it is: detach() would fill it now
-        if hasattr(v, "cf_materialize") and not v.requires_grad:
-            self._v = v
-        else:
-            self._v = v.detach()
+        # as it is: detach() would fill it now.  Its requires_grad is read
+        # with the subclass's torch-function dispatch off (a plain read).
+        if hasattr(v, "cf_materialize"):
+            with torch._C.DisableTorchFunctionSubclass():
+                keep = not v.requires_grad
+            if keep:
+                self._v = v
+                return
+        self._v = v.detach()
 
     def reset(self) -> None:
         self._v = None
