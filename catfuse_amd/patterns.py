@@ -286,18 +286,24 @@ class PartialFusionConvBNLIF(_ConvPattern):
         return (P["bn_weight"], P["bn_bias"], B["running_mean"], B["running_var"])
 
     def forward(self, x, sew_identity=None):
-        pr, self._pair_result = self._pair_result, None
+        # the hand-over slots are plain instance attributes, written through
+        # __dict__ (nn.Module.__setattr__ costs a microsecond per write)
+        d = self.__dict__
+        pr = d["_pair_result"]
+        d["_pair_result"] = None
         if pr is not None and pr[0] is x and sew_identity is None:
             return pr[1]                   # computed by the partner's paired launch
-        pw, self._pair_with = self._pair_with, None
+        pw = d["_pair_with"]
+        d["_pair_with"] = None
+        impl = self._modules["_impl"]
         if pw is not None and pw[1] is x and sew_identity is None:
             res = _paired_forward(self, pw[0], x)
             if res is not None:
-                pw[0]._pair_result = (x, res[1])
+                pw[0].__dict__["_pair_result"] = (x, res[1])
                 return res[0]
         if sew_identity is not None:
-            return self._run(self._impl, x, identity=sew_identity, identity_mode=ID_ADD_SPIKE)
-        return self._run(self._impl, x)
+            return self._run(impl, x, identity=sew_identity, identity_mode=ID_ADD_SPIKE)
+        return self._run(impl, x)
 
     def supports_sew_identity(self):
         return isinstance(self._impl, StreamFuse)
@@ -923,14 +929,17 @@ class CTFSEWBasicBlock(CTFPattern):
         self.cnf = cnf
 
     def forward(self, x):
-        first, ds = self.fused_first, self.fused_downsample
-        if (ds is not None and isinstance(first, PartialFusionConvBNLIF)
-                and isinstance(ds, PartialFusionConvBNLIF) and first.stride == 2):
-            first._pair_with = (ds, x)
+        mods = self._modules
+        first, ds = mods["fused_first"], mods.get("fused_downsample")
+        paired = (ds is not None and isinstance(first, PartialFusionConvBNLIF)
+                  and isinstance(ds, PartialFusionConvBNLIF) and first.stride == 2)
+        if paired:
+            first.__dict__["_pair_with"] = (ds, x)
         out = first(x)
-        first._pair_with = None
+        if paired:
+            first.__dict__["_pair_with"] = None
         identity = ds(x) if ds is not None else x
-        second = self.fused_second
+        second = mods["fused_second"]
         if (self.cnf == "ADD" and getattr(second, "supports_sew_identity", lambda: False)()
                 and identity.shape[:2] == out.shape[:2]):
             return second(out, sew_identity=identity.contiguous())

@@ -461,9 +461,10 @@ class ChannelState(_LazyTensor):
 
     @staticmethod
     def __new__(cls, base: torch.Tensor, v_chan: torch.Tensor, desc: torch.Tensor,
-                uniform: bool = False):
+                uniform: bool = False, meta=None):
+        # meta: base's _meta_of record when the caller already holds it
         t = base.as_subclass(cls)
-        t._cf_meta = _meta_of(base)
+        t._cf_meta = _meta_of(base) if meta is None else meta
         t._cf_base = base
         t._cf_pending = True
         t._cf_state = (v_chan, desc, base._version)
@@ -1027,8 +1028,8 @@ class _DensePlan:
     """What run_mfma's dense route decides from an input signature alone
     (ConvLIFRunner._dense_plan): the copy format, the output shapes, the
     static launch arguments and the layer's bias response."""
-    __slots__ = ("u8", "need_v", "vshape", "cshape", "cdtype", "oshape", "ometa", "nz_out",
-                 "nz_ptr", "weights", "numel", "T", "cp_out", "bias", "fn", "tail")
+    __slots__ = ("u8", "need_v", "vshape", "vmeta", "cshape", "cdtype", "oshape", "ometa",
+                 "nz_out", "nz_ptr", "weights", "numel", "T", "cp_out", "bias", "fn", "tail")
 
 
 class ConvLIFRunner:
@@ -1209,6 +1210,7 @@ class ConvLIFRunner:
         p.u8 = u8
         p.need_v = key[6] or T > 2
         p.vshape = (B, self.Cout, Ho, Wo)
+        p.vmeta = (torch.Size(p.vshape), torch.float32, dev, B * self.Cout * Ho * Wo, True)
         p.cshape = (T * B, Ho, Wo, cp_out)
         p.cdtype = torch.uint8 if u8 else torch.float16
         p.oshape = (T, B, self.Cout, Ho, Wo)
@@ -1335,7 +1337,8 @@ class ConvLIFRunner:
         self.last_order = None
         if not want_v_out:
             return out, None
-        return out, (ChannelState(v_out, v_chan, desc) if v_chan is not None else v_out)
+        return out, (ChannelState(v_out, v_chan, desc, meta=p.vmeta) if v_chan is not None
+                     else v_out)
 
     def run_mfma(self, x: torch.Tensor, v_in=None, *, epilogue=EPI_LIF, want_v_out=True,
                  identity=None, identity_mode=ID_ADD_SPIKE, sparse=None, sparse_threshold=0.7,
@@ -1912,7 +1915,8 @@ def _halo_pair_plan(ra, rb, x, xp, meta):
             (torch.Size((T, B, r.Cout, Ho, Wo)), torch.float32, dev, T * B * r.Cout * Ho * Wo,
              True),
             nz, (r.w_packed.data_ptr(), r.alpha.data_ptr(), r.beta.data_ptr()), cp,
-            nz.data_ptr(), (r.Cout, r.Coutp, r.padding)))
+            nz.data_ptr(), (r.Cout, r.Coutp, r.padding),
+            (torch.Size((B, r.Cout, Ho, Wo)), torch.float32, dev, B * r.Cout * Ho * Wo, True)))
     p.halves = tuple(halves)
     return p
 
@@ -1953,7 +1957,7 @@ def halo_pair_repeat(ra, rb, x):
     res = []
     args = []
     cdtype = torch.uint8 if p.u8 else torch.float16
-    for r, vshape, cshape, oshape, ometa, nz, wts, cp, nz_ptr, geo in p.halves:
+    for r, vshape, cshape, oshape, ometa, nz, wts, cp, nz_ptr, geo, vmeta in p.halves:
         v_out = torch.empty(vshape, dtype=torch.float32, device=dev)
         nhwc = torch.empty(cshape, dtype=cdtype, device=dev)
         base = torch.empty(oshape, dtype=torch.float32, device=dev)
@@ -1972,7 +1976,7 @@ def halo_pair_repeat(ra, rb, x):
                 v_chan = rr[0]
             if info & 1:
                 out._cf_desc = (desc, base._version, ())
-        res.append((out, v_out, v_chan, desc))
+        res.append((out, v_out, v_chan, desc, vmeta))
         args += [*wts, None, v_out.data_ptr(), nhwc.data_ptr(), cp, nz_ptr,
                  desc.data_ptr() if desc is not None else None, info, *geo]
     check(p.fn(xp.data_ptr(), nnz.data_ptr() if nnz is not None else None,
@@ -1981,11 +1985,11 @@ def halo_pair_repeat(ra, rb, x):
     for r in (ra, rb):
         r.last_nnz = nnz
         r.last_numel = p.numel
-    (oa, voa, ca, da), (ob, vob, cb, db) = res
+    (oa, voa, ca, da, ma), (ob, vob, cb, db, mb) = res
     if ca is not None:
-        voa = ChannelState(voa, ca, da)
+        voa = ChannelState(voa, ca, da, meta=ma)
     if cb is not None:
-        vob = ChannelState(vob, cb, db)
+        vob = ChannelState(vob, cb, db, meta=mb)
     return oa, voa, ob, vob
 
 
