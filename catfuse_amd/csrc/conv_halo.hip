@@ -828,10 +828,11 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
     const uint32_t kr = ks_run(ch);
     constexpr bool SKIP = decltype(skip_c)::value;
     const int stb = ntb == wblk ? ntb : a.T;  // a.T: stage zeros
-    // Taps the next K step's direct loads are spread over: all but the last
-    // (the barrier that publishes them follows the last tap); the first
-    // three in a launch of one workgroup per CU, whose one wave per SIMD
-    // would otherwise wait at that barrier for the latest ones.
+    // Taps the next K step's staging loads are spread over: the first three
+    // (at most all but the last, after which the barrier publishes them).
+    // Issued early, they have landed before the later taps wait for their
+    // weight fragments, a wait the in-order load counter would otherwise
+    // extend to every staging load issued before them.
     constexpr int SPAN = KK - 1 < 3 ? KK - 1 : 3;
     // B fragments are read TBR steps at a time (a batch), unconditionally
     // (reads of steps this chunk skips hold zeros), one 16-channel half
@@ -870,11 +871,12 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
             else load_w(cur ^ 1, 0, nc);
           }
           if constexpr (U8) {
-            // both buffer counts: loads now, widened after the taps
+            // both buffer counts: loads now (on the first SPAN taps, as the
+            // direct loads), widened after the taps
             if (KK == 1) {
               stage_defer(stb, nc, nact, 0, NPF);
-            } else if (tap + 1 < KK) {
-              const int i0 = (tap * NPF) / (KK - 1), i1 = ((tap + 1) * NPF) / (KK - 1);
+            } else if (tap < SPAN) {
+              const int i0 = (tap * NPF) / SPAN, i1 = ((tap + 1) * NPF) / SPAN;
               if (i1 > i0) stage_defer(stb, nc, nact, i0, i1);
             }
           } else if (NBUF == 1) {
