@@ -1360,9 +1360,18 @@ __device__ __forceinline__ void halo_body(const HaloArgs a, const int L, const i
   set_out_desc(CF_COPY_WRITTEN, nullptr, false);
 }
 
+// The one-byte stride-1 3x3 instantiations hold the next K step's staged
+// bytes in registers across the taps: the register budget of two workgroups
+// per CU (at three they spill).
+template <int TH, int TW, int S, int K, bool U8, bool DEEP>
+constexpr int halo_kernel_min_blocks() {
+  return DEEP ? 1 : ((U8 && S == 1 && K == 3 && halo_min_blocks<TH, TW, S, K>() > 2)
+                         ? 2 : halo_min_blocks<TH, TW, S, K>());
+}
+
 template <int TH, int TW, int S, int K, int EPI, int LM, bool LEAN, bool ONEB, bool HS = false,
           bool U8 = false, bool DEEP = false>
-__global__ __launch_bounds__(256, (DEEP ? 1 : halo_min_blocks<TH, TW, S, K>()))
+__global__ __launch_bounds__(256, (halo_kernel_min_blocks<TH, TW, S, K, U8, DEEP>()))
 void conv_halo_kernel(HaloArgs a) {
   __shared__ __attribute__((aligned(16))) _Float16 halo[halo_nbuf<S, K>() * halo_buf_halves<TH, TW, S, K>()];
   __shared__ __attribute__((aligned(16))) float bn_s[2][64];  // alpha, beta of the tile
