@@ -1029,7 +1029,8 @@ class _DensePlan:
     (ConvLIFRunner._dense_plan): the copy format, the output shapes, the
     static launch arguments and the layer's bias response."""
     __slots__ = ("u8", "need_v", "vshape", "vmeta", "cshape", "cdtype", "oshape", "ometa",
-                 "nz_out", "nz_ptr", "weights", "numel", "T", "cp_out", "bias", "fn", "tail")
+                 "nz_out", "nz_ptr", "weights", "numel", "T", "cp_out", "bias", "pool", "fn",
+                 "tail")
 
 
 class ConvLIFRunner:
@@ -1176,7 +1177,7 @@ class ConvLIFRunner:
             self._ws["nz_out"] = t
         return t
 
-    def _dense_plan(self, key, x, xp, identity, ish, xshape, dev):
+    def _dense_plan(self, key, x, xp, identity, ish, xshape, dev, epilogue=EPI_LIF):
         """The _DensePlan of one input signature (see _dense_repeat), made
         with the checks and choices of run_mfma's general path; False when
         that path would do anything else than one dense launch on the
@@ -1187,11 +1188,16 @@ class ConvLIFRunner:
         T, B, C, H, W = xshape
         Ho, Wo = self.out_hw(H, W)
         cp_out = pad32(self.Cout)
+        pool = epilogue == EPI_POOL
         meta = key[0]     # x: fp32, contiguous, on the GPU (require_gpu_tensor)
         ok = (C == self.Cin and Ho >= 1 and Wo >= 1 and meta[1] == torch.float32 and meta[4]
               and dev.type == "cuda" and xp.device == dev
               and tuple(xp.shape) == (T * B, H, W, self.Cp)
               and xp.dtype in (torch.float16, torch.uint8))
+        if pool:
+            # the pooled epilogue's own conditions (run_mfma raises on them)
+            ok = (ok and (self.KH, self.KW, self.stride) == (3, 3, 1) and self.Cout % 32 == 0
+                  and Ho >= 2 and Wo >= 2 and identity is None)
         id_u8 = False
         if ok and identity is not None:
             ic = ish[0]
@@ -1202,19 +1208,23 @@ class ConvLIFRunner:
             id_u8 = ok and ic.dtype == torch.uint8
         if not ok:
             return False
-        u8 = (SPIKE_COPY == "u8" and self.Cout % 32 == 0 and self.halo_lean_ok(T, B, Ho, Wo)
+        u8 = (not pool and SPIKE_COPY == "u8" and self.Cout % 32 == 0
+              and self.halo_lean_ok(T, B, Ho, Wo)
               and xp.dtype == torch.uint8 and (identity is None or id_u8))
         if (xp.dtype == torch.uint8 or id_u8) and not u8:
             return False      # the general path widens the byte copy first
+        # output and state at the pooled size with the pooled epilogue
+        Hs, Ws = (Ho // 2, Wo // 2) if pool else (Ho, Wo)
         p = _DensePlan()
         p.u8 = u8
+        p.pool = pool
         p.need_v = key[6] or T > 2
-        p.vshape = (B, self.Cout, Ho, Wo)
-        p.vmeta = (torch.Size(p.vshape), torch.float32, dev, B * self.Cout * Ho * Wo, True)
-        p.cshape = (T * B, Ho, Wo, cp_out)
+        p.vshape = (B, self.Cout, Hs, Ws)
+        p.vmeta = (torch.Size(p.vshape), torch.float32, dev, B * self.Cout * Hs * Ws, True)
+        p.cshape = (T * B, Hs, Ws, cp_out)
         p.cdtype = torch.uint8 if u8 else torch.float16
-        p.oshape = (T, B, self.Cout, Ho, Wo)
-        p.ometa = (torch.Size(p.oshape), torch.float32, dev, T * B * self.Cout * Ho * Wo, True)
+        p.oshape = (T, B, self.Cout, Hs, Ws)
+        p.ometa = (torch.Size(p.oshape), torch.float32, dev, T * B * self.Cout * Hs * Ws, True)
         p.nz_out = self.out_counter(dev)
         p.nz_ptr = p.nz_out.data_ptr()
         p.weights = (self.w_packed.data_ptr(), self.alpha.data_ptr(), self.beta.data_ptr())
@@ -1229,14 +1239,14 @@ class ConvLIFRunner:
         else:
             p.fn = _hip.lib().cf_conv_mfma
             p.tail = (T, B, self.Cp, self.Cout, self.Coutp, H, W, Ho, Wo, self.KH, self.KW,
-                      self.stride, self.padding, B, 0, 0, 0, EPI_LIF) + tuple(self.lif)
+                      self.stride, self.padding, B, 0, 0, 0, epilogue) + tuple(self.lif)
         return p
 
-    def _dense_repeat(self, x, identity, want_v_out, sparse_threshold):
+    def _dense_repeat(self, x, identity, want_v_out, sparse_threshold, epilogue=EPI_LIF):
         """run_mfma's launch for its common case from a plan cached per input
-        signature: a dense-route LIF launch with no initial state whose
-        input (and spike identity) carry a current NHWC copy, writing the
-        output's copy, with no kernel timer.  The checks and choices that
+        signature: a dense-route LIF (or pooled LIF) launch with no initial
+        state whose input (and spike identity) carry a current NHWC copy,
+        writing the output's copy, with no kernel timer.  The checks and choices that
         depend only on the signature (shapes, copy formats, device, whether
         the state is wanted, the copy settings) ran once when the plan was
         made; each call reads the copies' descriptors and count blocks,
@@ -1265,14 +1275,15 @@ class ConvLIFRunner:
             if im is None:
                 im = _meta_of(identity)
             key = (meta, xp.shape, xp.dtype, im[0], ic.shape, ic.dtype, want_v_out, im[1:3],
-                   im[4], SPIKE_COPY, COPY_ELISION)
+                   im[4], SPIKE_COPY, COPY_ELISION, epilogue)
         else:
             key = (meta, xp.shape, xp.dtype, None, None, None, want_v_out, None, None,
-                   SPIKE_COPY, COPY_ELISION)
+                   SPIKE_COPY, COPY_ELISION, epilogue)
         self._ensure_packed(dev)
         p = self._plans.get(key)
         if p is None:
-            p = self._plans[key] = self._dense_plan(key, x, xp, identity, ish, xshape, dev)
+            p = self._plans[key] = self._dense_plan(key, x, xp, identity, ish, xshape, dev,
+                                                    epilogue)
         if p is False:
             return None
         # the input's descriptor and count block (as desc_of / count_of)
@@ -1307,7 +1318,7 @@ class ConvLIFRunner:
             desc = torch.empty(2, dtype=torch.int64, device=dev)
             r = p.bias
             if r is None:
-                r = p.bias = self.bias_response(dev, p.T)
+                r = p.bias = self.bias_response(dev, p.T, p.pool)
             if r is not None:
                 info = (1 if r[1] else 0) | (2 if v_out is not None else 0)
                 if v_out is not None:
@@ -1357,10 +1368,10 @@ class ConvLIFRunner:
         epilogue; out is then the pooled spikes [T, B, Cout, Ho//2, Wo//2]
         (written as the fp16 NHWC copy) and v_out the pooled membrane state.
         Returns (out, v_out)."""
-        if (sparse is None and epilogue == EPI_LIF and emit_nhwc and static_zero
-                and v_in is None and identity_mode == ID_ADD_SPIKE and _timer is None
-                and REPEAT_PLANS):
-            r = self._dense_repeat(x, identity, want_v_out, sparse_threshold)
+        if (sparse is None and (epilogue == EPI_LIF or epilogue == EPI_POOL) and emit_nhwc
+                and static_zero and v_in is None and identity_mode == ID_ADD_SPIKE
+                and _timer is None and REPEAT_PLANS):
+            r = self._dense_repeat(x, identity, want_v_out, sparse_threshold, epilogue)
             if r is not None:
                 return r
         require_gpu_tensor(x, "x")

@@ -118,3 +118,47 @@ def test_repeat_plans_follow_in_place_parameter_changes(cuda):
     assert torch.equal(fast[0][0], general[0][0])
     for a, b in zip(fast[0][1], general[0][1]):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("v_th", [1.0, 0.1])
+def test_repeat_path_matches_general_path_vgg(cuda, monkeypatch, v_th):
+    """Spiking VGG-11-BN (the pooled epilogue's Conv-BN-AvgPool-LIF layers,
+    Conv-BN-LIF layers, the Linear-LIF classifier) at T=4 on live and
+    all-zero inputs: logits and every fused layer's state equal the general
+    path's bit for bit, with the repeat path taken by the pooled layers."""
+    import catfuse_amd
+    from catfuse_amd import runtime, snn
+    g = torch.Generator().manual_seed(12)
+    m = snn.spiking_vgg11_bn(num_classes=10, v_threshold=v_th)
+    snn.functional.set_step_mode(m, "m")
+    snn.kaiming_init(m, g)
+    snn.randomize_bn(m, g)
+    fused, _ = catfuse_amd.optimize(m.eval(), device=cuda, T=4)
+    fused.eval()
+    T, B = 4, 8
+    gen = torch.Generator(device=cuda).manual_seed(3)
+    x0 = torch.randn(B, 3, 32, 32, device=cuda, generator=gen).unsqueeze(0).expand(T, B, 3, 32, 32)
+    xs = [x0, torch.zeros_like(x0), x0]
+    pooled = {"n": 0}
+    dense = runtime.ConvLIFRunner._dense_repeat
+
+    def count(self, *a, **k):
+        r = dense(self, *a, **k)
+        if r is not None and len(a) > 4 and a[4] == runtime.EPI_POOL:
+            pooled["n"] += 1
+        return r
+
+    monkeypatch.setattr(runtime.ConvLIFRunner, "_dense_repeat", count)
+    with torch.no_grad():
+        fast = _run(fused, xs)
+        runtime.REPEAT_PLANS = False
+        try:
+            general = _run(fused, xs)
+        finally:
+            runtime.REPEAT_PLANS = True
+    assert pooled["n"] >= len(xs), pooled
+    for i, ((yf, sf), (yg, sg)) in enumerate(zip(fast, general)):
+        assert torch.equal(yf, yg), f"input {i}: logits"
+        assert len(sf) == len(sg)
+        for k, (a, b) in enumerate(zip(sf, sg)):
+            assert torch.equal(a, b), f"input {i}: state of layer {k}"
