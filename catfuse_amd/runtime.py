@@ -1563,6 +1563,157 @@ class ConvLIFRunner:
             return out, None
         return out, (ChannelState(v_out, v_chan, desc) if v_chan is not None else v_out)
 
+    def _tokens_plan(self, xp, identity, ish, meta, im, want_v_out, grid):
+        """The _DensePlan of one token-layer input signature (see
+        _tokens_repeat), made with run_tokens' checks; False when run_tokens
+        would do anything else than one launch on the copies as they are
+        (pack an input, widen a byte copy, an error)."""
+        shape, dtype, dev = meta[0], meta[1], meta[2]
+        if ((self.KH, self.KW, self.stride, self.padding) != (1, 1, 1, 0)
+                or len(shape) not in (3, 4) or dtype != torch.float32 or not meta[4]
+                or dev.type != "cuda"):
+            return False
+        if len(shape) == 3:
+            (T, B, C), N = shape, 1
+        else:
+            T, B, N, C = shape
+        if C != self.Cin:
+            return False
+        nimg, H, W = token_view(B, N) if grid is None else (B,) + tuple(grid)
+        if nimg * H * W != B * N:
+            return False
+        rows = T * B * N
+        # the input's copy as token_shadow takes it
+        if (xp.device != dev or xp.dtype != torch.float16 or xp.shape[-1] != self.Cp
+                or xp.numel() != rows * self.Cp or not xp.is_contiguous()):
+            return False
+        out_shape = tuple(shape[:-1]) + (self.Cout,)
+        cp_out = pad32(self.Cout)
+        if identity is not None:
+            # identity: fp32, contiguous, the output's shape (require_gpu_tensor)
+            ic = ish[0]
+            if (tuple(im[0]) != out_shape or im[1:3] != (torch.float32, dev) or not im[4]
+                    or ic.device != dev or ic.dtype != torch.float16 or ic.shape[-1] != cp_out
+                    or ic.numel() != rows * cp_out or not ic.is_contiguous()):
+                return False
+        p = _DensePlan()
+        p.u8 = False
+        p.pool = False
+        p.need_v = want_v_out or T > 2
+        p.vshape = (nimg, self.Cout, H, W)
+        p.vmeta = (torch.Size((nimg, self.Cout, H * W)), torch.float32, dev,
+                   nimg * self.Cout * H * W, True)    # the state as run_tokens returns it
+        p.cshape = (T * nimg, H, W, cp_out)
+        p.cdtype = torch.float16
+        p.oshape = out_shape
+        p.ometa = (torch.Size(out_shape), torch.float32, dev, rows * self.Cout, True)
+        p.nz_out = self.out_counter(dev)
+        p.nz_ptr = p.nz_out.data_ptr()
+        p.weights = (self.w_packed.data_ptr(), self.alpha.data_ptr(), self.beta.data_ptr())
+        p.numel = rows * C
+        p.T = T
+        p.cp_out = cp_out
+        p.bias = None
+        p.fn = _hip.lib().cf_conv_mfma
+        p.tail = (T, nimg, self.Cp, self.Cout, self.Coutp, H, W, H, W, 1, 1, 1, 0, nimg, 0, 0, 0,
+                  EPI_LIF) + tuple(self.lif)
+        return p
+
+    def _tokens_repeat(self, x, identity, want_v_out, grid):
+        """run_tokens' launch for its common case from a plan cached per input
+        signature: no initial state, the input (and the identity, if any)
+        carrying a current fp16 copy, no kernel timer.  The checks that
+        depend only on the signature ran when the plan was made; a call
+        reads the copies' descriptors and count blocks, allocates the
+        outputs and launches with the arguments run_tokens passes.  None
+        when the case is not covered."""
+        d = x.__dict__
+        sh = d.get("_cf_nhwc")
+        if sh is None:
+            return None
+        xp, ver = sh
+        if ver != d.get("_cf_base", x)._version:
+            return None
+        meta = d.get("_cf_meta") if d.get("_cf_pending", False) else None
+        if meta is None:
+            meta = _meta_of(x)
+        dev = meta[2]
+        ish = im = None
+        if identity is not None:
+            idd = identity.__dict__
+            ish = idd.get("_cf_nhwc")
+            if ish is None or ish[1] != idd.get("_cf_base", identity)._version:
+                return None
+            ic = ish[0]
+            im = idd.get("_cf_meta") if idd.get("_cf_pending", False) else None
+            if im is None:
+                im = _meta_of(identity)
+            key = ("tokens", meta, xp.shape, xp.dtype, want_v_out, im, ic.shape, ic.dtype, grid,
+                   COPY_ELISION)
+        else:
+            key = ("tokens", meta, xp.shape, xp.dtype, want_v_out, None, None, None, grid,
+                   COPY_ELISION)
+        self._ensure_packed(dev)
+        p = self._plans.get(key)
+        if p is None:
+            p = self._plans[key] = self._tokens_plan(xp, identity, ish, meta, im, want_v_out,
+                                                     grid)
+        if p is False:
+            return None
+        dd = d.get("_cf_desc")
+        x_desc = dd[0] if dd is not None and dd[1] == ver else None
+        c = d.get("_cf_count")
+        nnz = c[0] if c is not None and c[3] == ver and c[1][0] == c[2] else None
+        id_ptr = id_desc = id_nnz = 0
+        id_keep = ()
+        if identity is not None:
+            iver = ish[1]
+            ic = ish[0]
+            id_ptr = ic.data_ptr()
+            dd = idd.get("_cf_desc")
+            idesc = dd[0] if dd is not None and dd[1] == iver else written_desc(dev)
+            id_desc = idesc.data_ptr()
+            c = idd.get("_cf_count")
+            if c is not None and c[3] == iver and c[1][0] == c[2]:
+                id_nnz = c[0].data_ptr()
+            id_keep = (ic,) + (() if dd is None else dd[2])
+        v_out = torch.empty(p.vshape, dtype=torch.float32, device=dev) if p.need_v else None
+        nhwc = torch.empty(p.cshape, dtype=torch.float16, device=dev)
+        base = torch.empty(p.oshape, dtype=torch.float32, device=dev)
+        out = NHWCSpikes(base, nhwc, tokens=True, meta=p.ometa)
+        gen = self._gen
+        gen[0] += 1
+        out._cf_count = (p.nz_out, gen, gen[0], base._version)
+        desc = None
+        info = 0
+        v_chan = None
+        if COPY_ELISION and (nnz is not None or x_desc is not None):
+            desc = torch.empty(2, dtype=torch.int64, device=dev)
+            r = p.bias
+            if r is None:
+                r = p.bias = self.bias_response(dev, p.T)
+            if r is not None:
+                info = (1 if r[1] else 0) | (2 if v_out is not None else 0)
+                if v_out is not None:
+                    v_chan = r[0]
+            if info & 1:
+                out._cf_desc = (desc, base._version, id_keep)
+        w, al, be = p.weights
+        check(p.fn(xp.data_ptr(), w, al, be, None,
+                   v_out.data_ptr() if v_out is not None else None, None, nhwc.data_ptr(),
+                   p.cp_out, None, id_ptr or None, p.cp_out, ID_ADD_SPIKE, None, None,
+                   nnz.data_ptr() if nnz is not None else None, p.nz_ptr,
+                   x_desc.data_ptr() if x_desc is not None else None, id_desc or None,
+                   desc.data_ptr() if desc is not None else None, info, id_nnz or None,
+                   p.numel, 2.0, *p.tail, _hip.stream(dev)), "cf_conv_mfma")
+        self.last_nnz = nnz
+        self.last_numel = p.numel
+        if not want_v_out:
+            return out, None
+        nimg, Cout, H, W = p.vshape
+        vv = v_out.view(nimg, Cout, H * W)
+        return out, (ChannelState(vv, v_chan, desc, meta=p.vmeta) if v_chan is not None else vv)
+
     def run_tokens(self, x: torch.Tensor, v_in=None, *, identity=None, want_v_out=True,
                    static_zero=True, grid=None):
         """Linear -> (BN) -> LIF over token-major x [T, B, N, Cin]: a 1x1 conv
@@ -1577,6 +1728,11 @@ class ConvLIFRunner:
         x may also be [T, B, Cin] (one token per sample, N = 1; identity and
         output are then [T, B, Cout]).
         Returns (lazy fp32 tokens [T, B, N, Cout], v_out or None)."""
+        if v_in is None and static_zero and _timer is None and REPEAT_PLANS:
+            r = self._tokens_repeat(x, identity, want_v_out,
+                                    None if grid is None else tuple(grid))
+            if r is not None:
+                return r
         require_gpu_tensor(x, "x")
         if self.KH != 1 or self.KW != 1 or self.stride != 1 or self.padding != 0:
             raise ValueError("run_tokens needs a 1x1 kernel with stride 1 and no padding")

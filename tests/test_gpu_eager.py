@@ -162,3 +162,47 @@ def test_repeat_path_matches_general_path_vgg(cuda, monkeypatch, v_th):
         assert len(sf) == len(sg)
         for k, (a, b) in enumerate(zip(sf, sg)):
             assert torch.equal(a, b), f"input {i}: state of layer {k}"
+
+
+@pytest.mark.parametrize("v_th", [1.0, 0.2])
+def test_repeat_path_matches_general_path_spikformer(cuda, monkeypatch, v_th):
+    """A small Spikformer (token Linear-BN-LIF layers with and without the
+    residual identity, attention between them): logits and every fused
+    layer's state equal the general path's bit for bit on live and
+    all-zero inputs, with the token layers' repeat path taken."""
+    import catfuse_amd
+    from catfuse_amd import runtime, snn
+    T, B = 4, 2
+    g = torch.Generator().manual_seed(5)
+    net = snn.Spikformer(img_size=32, num_classes=10, embed_dim=64, num_heads=2, depth=2,
+                         pools=(0, 1), v_threshold=v_th)
+    snn.kaiming_init(net, g)
+    snn.randomize_bn(net, g)
+    fused, _ = catfuse_amd.optimize(net.eval(), device=cuda, T=T)
+    fused = fused.eval()
+    gen = torch.Generator(device=cuda).manual_seed(2)
+    x0 = torch.randn(B, 3, 32, 32, device=cuda, generator=gen).unsqueeze(0).expand(T, B, 3, 32, 32)
+    x1 = torch.randn(B, 3, 32, 32, device=cuda, generator=gen).unsqueeze(0).expand(T, B, 3, 32, 32)
+    xs = [x0, torch.zeros_like(x0), x1, x0]
+    taken = {"n": 0}
+    tokens = runtime.ConvLIFRunner._tokens_repeat
+
+    def count(self, *a, **k):
+        r = tokens(self, *a, **k)
+        taken["n"] += r is not None
+        return r
+
+    monkeypatch.setattr(runtime.ConvLIFRunner, "_tokens_repeat", count)
+    with torch.no_grad():
+        fast = _run(fused, xs)
+        runtime.REPEAT_PLANS = False
+        try:
+            general = _run(fused, xs)
+        finally:
+            runtime.REPEAT_PLANS = True
+    assert taken["n"] >= 4 * len(xs), taken
+    for i, ((yf, sf), (yg, sg)) in enumerate(zip(fast, general)):
+        assert torch.equal(yf, yg), f"input {i}: logits"
+        assert len(sf) == len(sg)
+        for k, (a, b) in enumerate(zip(sf, sg)):
+            assert torch.equal(a, b), f"input {i}: state of layer {k}"
