@@ -628,7 +628,7 @@ class FusedLinearLIF(CTFPattern):
         v_in = self.state.peek((nimg, self.out_features, H * W), x.device)
         y, v = r.run_tokens(x, v_in)
         self.state.set(v)
-        self._batch = B
+        self.__dict__["_batch"] = B   # a plain attribute (no nn.Module hook)
         return y.squeeze(0) if squeeze else y
 
     def membrane(self):

@@ -66,11 +66,14 @@ class FusedLinearBNLIF(CTFPattern):
         self._runner_key = None
 
     def _param_tensors(self):
-        return [t for t in (self.weight, self.bias, self.bn_weight, self.bn_bias,
-                            self.running_mean, self.running_var) if t is not None]
+        # read from the module's own dicts (attribute lookup of a parameter
+        # goes through nn.Module.__getattr__ on every call)
+        P, Bf = self._parameters, self._buffers
+        return [t for t in (P.get("weight"), P.get("bias"), P.get("bn_weight"), P.get("bn_bias"),
+                            Bf.get("running_mean"), Bf.get("running_var")) if t is not None]
 
     def runner(self) -> ConvLIFRunner:
-        key = tuple((id(t), t._version, t.device) for t in self._param_tensors())
+        key = tuple([(id(t), t._version, t.device) for t in self._param_tensors()])
         if key != self._runner_key:
             with torch.no_grad():
                 scale = shift = None
@@ -96,7 +99,7 @@ class FusedLinearBNLIF(CTFPattern):
         v_in = self.state.peek((nimg, self.out_features, H * W), x.device)
         y, v = self.runner().run_tokens(x, v_in, identity=identity)
         self.state.set(v)
-        self._tokens = (B, N)
+        self.__dict__["_tokens"] = (B, N)   # a plain attribute (no nn.Module hook)
         return y.squeeze(2) if squeeze else y
 
     def membrane(self):
