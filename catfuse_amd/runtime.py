@@ -636,9 +636,10 @@ def shadow_of(x: torch.Tensor, shape, resolve: bool = True,
 # for comparisons against the always-writing path.
 COPY_ELISION = True
 
-# Launch plans cached per input signature for the common fused-conv launches
-# (ConvLIFRunner._dense_repeat, halo_pair_repeat); off for comparisons
-# against the general path.
+# Launch plans cached per input signature for the common fused-conv and
+# token-layer launches (ConvLIFRunner._dense_repeat, ConvLIFRunner.
+# _tokens_repeat, halo_pair_repeat); off for comparisons against the general
+# path.
 REPEAT_PLANS = True
 
 
