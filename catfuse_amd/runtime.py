@@ -1025,6 +1025,43 @@ def route_from_nnz(nnz: torch.Tensor, numel: int, sparse_threshold: float,
 # Conv -> BN -> LIF
 # ---------------------------------------------------------------------------
 
+def _copy_record(x):
+    """(record dict, copy, version, metadata) of x's current NHWC copy -- its
+    producer's copy at x's present version, as shadow_of accepts it -- or
+    None: the launch plans' reading of x."""
+    d = x.__dict__
+    sh = d.get("_cf_nhwc")
+    if sh is None:
+        return None
+    xp, ver = sh
+    if ver != d.get("_cf_base", x)._version:
+        return None
+    meta = d.get("_cf_meta") if d.get("_cf_pending", False) else None
+    return d, xp, ver, (_meta_of(x) if meta is None else meta)
+
+
+def _desc_count(d, ver):
+    """(descriptor, count block) of a copy record at version ver, as desc_of
+    and count_of return them (None: absent or stale)."""
+    dd = d.get("_cf_desc")
+    c = d.get("_cf_count")
+    return ((dd[0] if dd is not None and dd[1] == ver else None),
+            (c[0] if c is not None and c[3] == ver and c[1][0] == c[2] else None))
+
+
+def _identity_args(idd, ic, iver, dev):
+    """The general path's arguments for a spike identity with current copy
+    ic (record idd at version iver): the pointers of the copy, of its
+    descriptor (written_desc when it keeps none) and of its count block (0
+    when absent), and the copies an output aliasing it keeps alive."""
+    idesc, inz = _desc_count(idd, iver)
+    if idesc is None:
+        idesc = written_desc(dev)
+    dd = idd.get("_cf_desc")
+    return (ic.data_ptr(), idesc.data_ptr(), 0 if inz is None else inz.data_ptr(),
+            (ic,) + (() if dd is None else dd[2]))
+
+
 class _DensePlan:
     """What run_mfma's dense route decides from an input signature alone
     (ConvLIFRunner._dense_plan): the copy format, the output shapes, the
@@ -1243,38 +1280,58 @@ class ConvLIFRunner:
                       self.stride, self.padding, B, 0, 0, 0, epilogue) + tuple(self.lif)
         return p
 
+    def _plan_outputs(self, p, dev, elide, keep=(), tokens=False):
+        """The outputs of a launch from plan p, as _launch makes them: the
+        state (when the plan keeps one), the copy and the lazy output with
+        its count block; with elide (the input has a count block or a
+        descriptor) the output descriptor and the StaticZero bits of the
+        layer's bias response (keep: the copies an aliasing output holds).
+        Returns (out, v_out, nhwc, desc, info, v_chan)."""
+        v_out = torch.empty(p.vshape, dtype=torch.float32, device=dev) if p.need_v else None
+        nhwc = torch.empty(p.cshape, dtype=p.cdtype, device=dev)
+        base = torch.empty(p.oshape, dtype=torch.float32, device=dev)
+        out = NHWCSpikes(base, nhwc, tokens=tokens, meta=p.ometa)
+        gen = self._gen
+        gen[0] += 1
+        out._cf_count = (p.nz_out, gen, gen[0], base._version)
+        desc = v_chan = None
+        info = 0
+        if elide:
+            desc = torch.empty(2, dtype=torch.int64, device=dev)
+            r = p.bias
+            if r is None:
+                r = p.bias = self.bias_response(dev, p.T, p.pool)
+            if r is not None:
+                info = (1 if r[1] else 0) | (2 if v_out is not None else 0)
+                if v_out is not None:
+                    v_chan = r[0]
+            if info & 1:
+                out._cf_desc = (desc, base._version, keep)
+        return out, v_out, nhwc, desc, info, v_chan
+
     def _dense_repeat(self, x, identity, want_v_out, sparse_threshold, epilogue=EPI_LIF):
         """run_mfma's launch for its common case from a plan cached per input
         signature: a dense-route LIF (or pooled LIF) launch with no initial
         state whose input (and spike identity) carry a current NHWC copy,
-        writing the output's copy, with no kernel timer.  The checks and choices that
-        depend only on the signature (shapes, copy formats, device, whether
-        the state is wanted, the copy settings) ran once when the plan was
-        made; each call reads the copies' descriptors and count blocks,
-        allocates the outputs and launches with the arguments the general
-        path passes.  None when the case is not covered (run_mfma then takes
-        its general path)."""
-        d = x.__dict__
-        sh = d.get("_cf_nhwc")
-        if sh is None:
+        writing the output's copy, with no kernel timer.  The checks and
+        choices that depend only on the signature (shapes, copy formats,
+        device, whether the state is wanted, the copy settings) ran once when
+        the plan was made; each call reads the copies' descriptors and count
+        blocks, allocates the outputs and launches with the arguments the
+        general path passes.  None when the case is not covered (run_mfma
+        then takes its general path)."""
+        rec = _copy_record(x)
+        if rec is None:
             return None
-        xp, ver = sh
-        if ver != d.get("_cf_base", x)._version:
-            return None
-        meta = d.get("_cf_meta") if d.get("_cf_pending", False) else None
-        if meta is None:
-            meta = _meta_of(x)
+        d, xp, ver, meta = rec
         xshape, dev = meta[0], meta[2]
         ish = None
         if identity is not None:
-            idd = identity.__dict__
-            ish = idd.get("_cf_nhwc")
-            if ish is None or ish[1] != idd.get("_cf_base", identity)._version:
+            irec = _copy_record(identity)
+            if irec is None:
                 return None
-            ic = ish[0]
-            im = idd.get("_cf_meta") if idd.get("_cf_pending", False) else None
-            if im is None:
-                im = _meta_of(identity)
+            idd, ic, iver, im = irec
+            ish = (ic, iver)
             key = (meta, xp.shape, xp.dtype, im[0], ic.shape, ic.dtype, want_v_out, im[1:3],
                    im[4], SPIKE_COPY, COPY_ELISION, epilogue)
         else:
@@ -1287,45 +1344,13 @@ class ConvLIFRunner:
                                                     epilogue)
         if p is False:
             return None
-        # the input's descriptor and count block (as desc_of / count_of)
-        dd = d.get("_cf_desc")
-        x_desc = dd[0] if dd is not None and dd[1] == ver else None
-        c = d.get("_cf_count")
-        nnz = c[0] if c is not None and c[3] == ver and c[1][0] == c[2] else None
+        x_desc, nnz = _desc_count(d, ver)
         id_ptr = id_desc = id_nnz = 0
         id_keep = ()
         if identity is not None:
-            iver = ish[1]
-            ic = ish[0]
-            id_ptr = ic.data_ptr()
-            dd = idd.get("_cf_desc")
-            idesc = dd[0] if dd is not None and dd[1] == iver else written_desc(dev)
-            id_desc = idesc.data_ptr()
-            c = idd.get("_cf_count")
-            if c is not None and c[3] == iver and c[1][0] == c[2]:
-                id_nnz = c[0].data_ptr()
-            id_keep = (ic,) + (() if dd is None else dd[2])
-        v_out = torch.empty(p.vshape, dtype=torch.float32, device=dev) if p.need_v else None
-        nhwc = torch.empty(p.cshape, dtype=p.cdtype, device=dev)
-        base = torch.empty(p.oshape, dtype=torch.float32, device=dev)
-        out = NHWCSpikes(base, nhwc, meta=p.ometa)
-        gen = self._gen
-        gen[0] += 1
-        out._cf_count = (p.nz_out, gen, gen[0], base._version)
-        desc = None
-        info = 0
-        v_chan = None
-        if COPY_ELISION and (nnz is not None or x_desc is not None):
-            desc = torch.empty(2, dtype=torch.int64, device=dev)
-            r = p.bias
-            if r is None:
-                r = p.bias = self.bias_response(dev, p.T, p.pool)
-            if r is not None:
-                info = (1 if r[1] else 0) | (2 if v_out is not None else 0)
-                if v_out is not None:
-                    v_chan = r[0]
-            if info & 1:
-                out._cf_desc = (desc, base._version, id_keep)
+            id_ptr, id_desc, id_nnz, id_keep = _identity_args(idd, ic, iver, dev)
+        out, v_out, nhwc, desc, info, v_chan = self._plan_outputs(
+            p, dev, COPY_ELISION and (nnz is not None or x_desc is not None), id_keep)
         w, al, be = p.weights
         vo = v_out.data_ptr() if v_out is not None else None
         dp = desc.data_ptr() if desc is not None else None
@@ -1628,27 +1653,18 @@ class ConvLIFRunner:
         reads the copies' descriptors and count blocks, allocates the
         outputs and launches with the arguments run_tokens passes.  None
         when the case is not covered."""
-        d = x.__dict__
-        sh = d.get("_cf_nhwc")
-        if sh is None:
+        rec = _copy_record(x)
+        if rec is None:
             return None
-        xp, ver = sh
-        if ver != d.get("_cf_base", x)._version:
-            return None
-        meta = d.get("_cf_meta") if d.get("_cf_pending", False) else None
-        if meta is None:
-            meta = _meta_of(x)
+        d, xp, ver, meta = rec
         dev = meta[2]
         ish = im = None
         if identity is not None:
-            idd = identity.__dict__
-            ish = idd.get("_cf_nhwc")
-            if ish is None or ish[1] != idd.get("_cf_base", identity)._version:
+            irec = _copy_record(identity)
+            if irec is None:
                 return None
-            ic = ish[0]
-            im = idd.get("_cf_meta") if idd.get("_cf_pending", False) else None
-            if im is None:
-                im = _meta_of(identity)
+            idd, ic, iver, im = irec
+            ish = (ic, iver)
             key = ("tokens", meta, xp.shape, xp.dtype, want_v_out, im, ic.shape, ic.dtype, grid,
                    COPY_ELISION)
         else:
@@ -1661,44 +1677,14 @@ class ConvLIFRunner:
                                                      grid)
         if p is False:
             return None
-        dd = d.get("_cf_desc")
-        x_desc = dd[0] if dd is not None and dd[1] == ver else None
-        c = d.get("_cf_count")
-        nnz = c[0] if c is not None and c[3] == ver and c[1][0] == c[2] else None
+        x_desc, nnz = _desc_count(d, ver)
         id_ptr = id_desc = id_nnz = 0
         id_keep = ()
         if identity is not None:
-            iver = ish[1]
-            ic = ish[0]
-            id_ptr = ic.data_ptr()
-            dd = idd.get("_cf_desc")
-            idesc = dd[0] if dd is not None and dd[1] == iver else written_desc(dev)
-            id_desc = idesc.data_ptr()
-            c = idd.get("_cf_count")
-            if c is not None and c[3] == iver and c[1][0] == c[2]:
-                id_nnz = c[0].data_ptr()
-            id_keep = (ic,) + (() if dd is None else dd[2])
-        v_out = torch.empty(p.vshape, dtype=torch.float32, device=dev) if p.need_v else None
-        nhwc = torch.empty(p.cshape, dtype=torch.float16, device=dev)
-        base = torch.empty(p.oshape, dtype=torch.float32, device=dev)
-        out = NHWCSpikes(base, nhwc, tokens=True, meta=p.ometa)
-        gen = self._gen
-        gen[0] += 1
-        out._cf_count = (p.nz_out, gen, gen[0], base._version)
-        desc = None
-        info = 0
-        v_chan = None
-        if COPY_ELISION and (nnz is not None or x_desc is not None):
-            desc = torch.empty(2, dtype=torch.int64, device=dev)
-            r = p.bias
-            if r is None:
-                r = p.bias = self.bias_response(dev, p.T)
-            if r is not None:
-                info = (1 if r[1] else 0) | (2 if v_out is not None else 0)
-                if v_out is not None:
-                    v_chan = r[0]
-            if info & 1:
-                out._cf_desc = (desc, base._version, id_keep)
+            id_ptr, id_desc, id_nnz, id_keep = _identity_args(idd, ic, iver, dev)
+        out, v_out, nhwc, desc, info, v_chan = self._plan_outputs(
+            p, dev, COPY_ELISION and (nnz is not None or x_desc is not None), id_keep,
+            tokens=True)
         w, al, be = p.weights
         check(p.fn(xp.data_ptr(), w, al, be, None,
                    v_out.data_ptr() if v_out is not None else None, None, nhwc.data_ptr(),
@@ -2045,9 +2031,9 @@ def halo_pair_supported(ra: "ConvLIFRunner", rb: "ConvLIFRunner", x: torch.Tenso
 
 class _PairPlan:
     """What run_halo_pair decides from an input signature alone
-    (halo_pair_repeat): the copy format, the output shapes, the partner and
-    the static launch arguments."""
-    __slots__ = ("rb", "rb_key", "u8", "fn", "numel", "T", "head", "halves")
+    (halo_pair_repeat): the copy format, the partner, the static launch
+    arguments and, per conv, a _DensePlan of its outputs."""
+    __slots__ = ("rb", "rb_key", "u8", "fn", "numel", "head", "halves")
 
 
 def _halo_pair_plan(ra, rb, x, xp, meta):
@@ -2072,19 +2058,25 @@ def _halo_pair_plan(ra, rb, x, xp, meta):
     p.u8 = u8
     p.fn = _hip.lib().cf_conv_halo_pair_u8 if u8 else _hip.lib().cf_conv_halo_pair
     p.numel = T * B * C * H * W
-    p.T = T
     p.head = (p.numel, T, B, ra.Cp, H, W, Ho, Wo)
     halves = []
     for r in (ra, rb):
-        cp = pad32(r.Cout)
-        nz = r.out_counter(dev)
-        halves.append((
-            r, (B, r.Cout, Ho, Wo), (T * B, Ho, Wo, cp), (T, B, r.Cout, Ho, Wo),
-            (torch.Size((T, B, r.Cout, Ho, Wo)), torch.float32, dev, T * B * r.Cout * Ho * Wo,
-             True),
-            nz, (r.w_packed.data_ptr(), r.alpha.data_ptr(), r.beta.data_ptr()), cp,
-            nz.data_ptr(), (r.Cout, r.Coutp, r.padding),
-            (torch.Size((B, r.Cout, Ho, Wo)), torch.float32, dev, B * r.Cout * Ho * Wo, True)))
+        h = _DensePlan()
+        h.u8, h.pool, h.need_v, h.T, h.bias = u8, False, True, T, None
+        h.cp_out = pad32(r.Cout)
+        h.vshape = (B, r.Cout, Ho, Wo)
+        h.vmeta = (torch.Size(h.vshape), torch.float32, dev, B * r.Cout * Ho * Wo, True)
+        h.cshape = (T * B, Ho, Wo, h.cp_out)
+        h.cdtype = torch.uint8 if u8 else torch.float16
+        h.oshape = (T, B, r.Cout, Ho, Wo)
+        h.ometa = (torch.Size(h.oshape), torch.float32, dev, T * B * r.Cout * Ho * Wo, True)
+        h.nz_out = r.out_counter(dev)
+        h.nz_ptr = h.nz_out.data_ptr()
+        h.weights = (r.w_packed.data_ptr(), r.alpha.data_ptr(), r.beta.data_ptr())
+        h.numel = p.numel
+        h.fn = None
+        h.tail = (r.Cout, r.Coutp, r.padding)
+        halves.append((r, h))
     p.halves = tuple(halves)
     return p
 
@@ -2098,16 +2090,10 @@ def halo_pair_repeat(ra, rb, x):
     general path passes.  None when the case is not covered."""
     if _timer is not None or not REPEAT_PLANS:
         return None
-    d = x.__dict__
-    sh = d.get("_cf_nhwc")
-    if sh is None:
+    rec = _copy_record(x)
+    if rec is None:
         return None
-    xp, ver = sh
-    if ver != d.get("_cf_base", x)._version:
-        return None
-    meta = d.get("_cf_meta") if d.get("_cf_pending", False) else None
-    if meta is None:
-        meta = _meta_of(x)
+    d, xp, ver, meta = rec
     dev = meta[2]
     ra._ensure_packed(dev)
     rb._ensure_packed(dev)
@@ -2117,36 +2103,15 @@ def halo_pair_repeat(ra, rb, x):
         p = ra._plans[key] = _halo_pair_plan(ra, rb, x, xp, meta)
     if p is False:
         return None
-    dd = d.get("_cf_desc")
-    x_desc = dd[0] if dd is not None and dd[1] == ver else None
-    c = d.get("_cf_count")
-    nnz = c[0] if c is not None and c[3] == ver and c[1][0] == c[2] else None
+    x_desc, nnz = _desc_count(d, ver)
     elide = COPY_ELISION and (nnz is not None or x_desc is not None)
     res = []
     args = []
-    cdtype = torch.uint8 if p.u8 else torch.float16
-    for r, vshape, cshape, oshape, ometa, nz, wts, cp, nz_ptr, geo, vmeta in p.halves:
-        v_out = torch.empty(vshape, dtype=torch.float32, device=dev)
-        nhwc = torch.empty(cshape, dtype=cdtype, device=dev)
-        base = torch.empty(oshape, dtype=torch.float32, device=dev)
-        out = NHWCSpikes(base, nhwc, meta=ometa)
-        gen = r._gen
-        gen[0] += 1
-        out._cf_count = (nz, gen, gen[0], base._version)
-        desc = None
-        info = 0
-        v_chan = None
-        if elide:
-            desc = torch.empty(2, dtype=torch.int64, device=dev)
-            rr = r.bias_response(dev, p.T)
-            if rr is not None:
-                info = (1 if rr[1] else 0) | 2
-                v_chan = rr[0]
-            if info & 1:
-                out._cf_desc = (desc, base._version, ())
-        res.append((out, v_out, v_chan, desc, vmeta))
-        args += [*wts, None, v_out.data_ptr(), nhwc.data_ptr(), cp, nz_ptr,
-                 desc.data_ptr() if desc is not None else None, info, *geo]
+    for r, h in p.halves:
+        out, v_out, nhwc, desc, info, v_chan = r._plan_outputs(h, dev, elide)
+        res.append((out, v_out, v_chan, desc, h.vmeta))
+        args += [*h.weights, None, v_out.data_ptr(), nhwc.data_ptr(), h.cp_out, h.nz_ptr,
+                 desc.data_ptr() if desc is not None else None, info, *h.tail]
     check(p.fn(xp.data_ptr(), nnz.data_ptr() if nnz is not None else None,
                x_desc.data_ptr() if x_desc is not None else None, *p.head, *args, *ra.lif,
                _hip.stream(dev)), "cf_conv_halo_pair")
