@@ -93,7 +93,43 @@ _SIGNATURES = {
                             c_int, _P],
     "cf_conv_direct": [_P, _P, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I, _I,
                        _I, _I, _I, c_int, c_double, c_double, c_double, c_int, c_int, _P],
+    # argument blocks (ConvMfmaArgs / ConvHaloPairArgs below), by address
+    "cf_conv_mfma_args": [_P],
+    "cf_conv_halo_pair_args": [_P],
+    "cf_conv_args_sizes": [_P],
 }
+
+_D = c_double
+# The argument blocks of cf_conv_mfma_args / cf_conv_halo_pair_args
+# (include/catfuse_amd.h: CfConvMfmaArgs, CfConvHaloPairArgs): every field
+# 8 bytes, in the order of the entry points' parameters.
+_CONV_MFMA_FIELDS = [
+    ("x", _P), ("w_packed", _P), ("alpha", _P), ("beta", _P), ("v_in", _P), ("v_out", _P),
+    ("out", _P), ("out_nhwc", _P), ("cp_out", _I), ("identity", _P), ("identity_nhwc", _P),
+    ("cp_id", _I), ("identity_mode", _I), ("ag_mask", _P), ("tile_order", _P), ("nnz", _P),
+    ("nz_out", _P), ("x_desc", _P), ("id_desc", _P), ("out_desc", _P), ("bias_info", _I),
+    ("id_nnz", _P), ("numel", _I), ("sparse_threshold", _D), ("T", _I), ("B", _I), ("Cp", _I),
+    ("Cout", _I), ("Coutp", _I), ("H", _I), ("W", _I), ("Ho", _I), ("Wo", _I), ("KH", _I),
+    ("KW", _I), ("stride", _I), ("pad", _I), ("x_img_tstride", _I), ("tile_h", _I),
+    ("tile_w", _I), ("group_size", _I), ("epilogue", _I), ("tau", _D), ("v_th", _D),
+    ("v_reset", _D), ("hard_reset", _I), ("decay_input", _I), ("stream", _P)]
+_PAIR_HALF = [("w", _P), ("alpha", _P), ("beta", _P), ("v_in", _P), ("v_out", _P), ("out", _P),
+              ("cp_out", _I), ("nz", _P), ("desc", _P), ("bias_info", _I), ("Cout", _I),
+              ("Coutp", _I), ("pad", _I)]
+_CONV_HALO_PAIR_FIELDS = (
+    [("x", _P), ("nnz", _P), ("x_desc", _P), ("numel", _I), ("T", _I), ("B", _I), ("Cp", _I),
+     ("H", _I), ("W", _I), ("Ho", _I), ("Wo", _I)]
+    + [(f + "_a", t) for f, t in _PAIR_HALF] + [(f + "_b", t) for f, t in _PAIR_HALF]
+    + [("tau", _D), ("v_th", _D), ("v_reset", _D), ("hard_reset", _I), ("decay_input", _I),
+       ("stream", _P)])
+
+
+class ConvMfmaArgs(ctypes.Structure):
+    _fields_ = _CONV_MFMA_FIELDS
+
+
+class ConvHaloPairArgs(ctypes.Structure):
+    _fields_ = _CONV_HALO_PAIR_FIELDS
 _RESTYPES = {"cf_error_string": c_char_p}
 
 _lib = None

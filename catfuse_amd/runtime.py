@@ -11,6 +11,7 @@ buffer, prescan buffers and the nonzero counter.
 """
 from __future__ import annotations
 
+import ctypes
 import os
 from typing import Optional
 
@@ -1062,13 +1063,32 @@ def _identity_args(idd, ic, iver, dev):
             (ic,) + (() if dd is None else dd[2]))
 
 
+def _conv_args_block(p):
+    """The cf_conv_mfma_args block of plan p with its static fields filled
+    (weights, sizes, epilogue, LIF parameters from p.tail, as the positional
+    call passes them); a launch fills the per-call ones.  Kept on the plan
+    with its address."""
+    a = _hip.ConvMfmaArgs()
+    a.w_packed, a.alpha, a.beta = p.weights
+    a.v_in = a.out = a.identity = a.ag_mask = a.tile_order = None
+    a.cp_out = a.cp_id = p.cp_out
+    a.identity_mode = ID_ADD_SPIKE
+    a.nz_out = p.nz_ptr
+    a.numel = p.numel
+    (a.T, a.B, a.Cp, a.Cout, a.Coutp, a.H, a.W, a.Ho, a.Wo, a.KH, a.KW, a.stride, a.pad,
+     a.x_img_tstride, a.tile_h, a.tile_w, a.group_size, a.epilogue, a.tau, a.v_th, a.v_reset,
+     a.hard_reset, a.decay_input) = p.tail
+    p.args = a
+    p.args_addr = ctypes.addressof(a)
+
+
 class _DensePlan:
     """What run_mfma's dense route decides from an input signature alone
     (ConvLIFRunner._dense_plan): the copy format, the output shapes, the
     static launch arguments and the layer's bias response."""
     __slots__ = ("u8", "need_v", "vshape", "vmeta", "cshape", "cdtype", "oshape", "ometa",
                  "nz_out", "nz_ptr", "weights", "numel", "T", "cp_out", "bias", "pool", "fn",
-                 "tail")
+                 "tail", "args", "args_addr")
 
 
 class ConvLIFRunner:
@@ -1275,9 +1295,10 @@ class ConvLIFRunner:
             p.tail = (T, B, self.Cp, self.Cout, self.Coutp, H, W, Ho, Wo, self.KH, self.stride,
                       self.padding, 0) + tuple(self.lif)
         else:
-            p.fn = _hip.lib().cf_conv_mfma
+            p.fn = _hip.lib().cf_conv_mfma_args
             p.tail = (T, B, self.Cp, self.Cout, self.Coutp, H, W, Ho, Wo, self.KH, self.KW,
                       self.stride, self.padding, B, 0, 0, 0, epilogue) + tuple(self.lif)
+            _conv_args_block(p)
         return p
 
     def _plan_outputs(self, p, dev, elide, keep=(), tokens=False):
@@ -1362,12 +1383,20 @@ class ConvLIFRunner:
                       info, id_nnz or None, p.numel, float(sparse_threshold), *p.tail, stream)
             check(rc, "cf_conv_halo_u8")
         else:
-            rc = p.fn(xp.data_ptr(), w, al, be, None, vo, None, nhwc.data_ptr(), p.cp_out, None,
-                      id_ptr or None, p.cp_out, ID_ADD_SPIKE, None, None,
-                      nnz.data_ptr() if nnz is not None else None, p.nz_ptr,
-                      x_desc.data_ptr() if x_desc is not None else None, id_desc or None, dp,
-                      info, id_nnz or None, p.numel, float(sparse_threshold), *p.tail, stream)
-            check(rc, "cf_conv_mfma")
+            a = p.args
+            a.x = xp.data_ptr()
+            a.v_out = vo
+            a.out_nhwc = nhwc.data_ptr()
+            a.identity_nhwc = id_ptr or None
+            a.nnz = nnz.data_ptr() if nnz is not None else None
+            a.x_desc = x_desc.data_ptr() if x_desc is not None else None
+            a.id_desc = id_desc or None
+            a.out_desc = dp
+            a.bias_info = info
+            a.id_nnz = id_nnz or None
+            a.sparse_threshold = float(sparse_threshold)
+            a.stream = stream
+            check(p.fn(p.args_addr), "cf_conv_mfma")
         self.last_nnz = nnz
         self.last_numel = p.numel
         self.last_tiles = None
@@ -1640,9 +1669,11 @@ class ConvLIFRunner:
         p.T = T
         p.cp_out = cp_out
         p.bias = None
-        p.fn = _hip.lib().cf_conv_mfma
+        p.fn = _hip.lib().cf_conv_mfma_args
         p.tail = (T, nimg, self.Cp, self.Cout, self.Coutp, H, W, H, W, 1, 1, 1, 0, nimg, 0, 0, 0,
                   EPI_LIF) + tuple(self.lif)
+        _conv_args_block(p)
+        p.args.sparse_threshold = 2.0
         return p
 
     def _tokens_repeat(self, x, identity, want_v_out, grid):
@@ -1685,14 +1716,19 @@ class ConvLIFRunner:
         out, v_out, nhwc, desc, info, v_chan = self._plan_outputs(
             p, dev, COPY_ELISION and (nnz is not None or x_desc is not None), id_keep,
             tokens=True)
-        w, al, be = p.weights
-        check(p.fn(xp.data_ptr(), w, al, be, None,
-                   v_out.data_ptr() if v_out is not None else None, None, nhwc.data_ptr(),
-                   p.cp_out, None, id_ptr or None, p.cp_out, ID_ADD_SPIKE, None, None,
-                   nnz.data_ptr() if nnz is not None else None, p.nz_ptr,
-                   x_desc.data_ptr() if x_desc is not None else None, id_desc or None,
-                   desc.data_ptr() if desc is not None else None, info, id_nnz or None,
-                   p.numel, 2.0, *p.tail, _hip.stream(dev)), "cf_conv_mfma")
+        a = p.args
+        a.x = xp.data_ptr()
+        a.v_out = v_out.data_ptr() if v_out is not None else None
+        a.out_nhwc = nhwc.data_ptr()
+        a.identity_nhwc = id_ptr or None
+        a.nnz = nnz.data_ptr() if nnz is not None else None
+        a.x_desc = x_desc.data_ptr() if x_desc is not None else None
+        a.id_desc = id_desc or None
+        a.out_desc = desc.data_ptr() if desc is not None else None
+        a.bias_info = info
+        a.id_nnz = id_nnz or None
+        a.stream = _hip.stream(dev)
+        check(p.fn(p.args_addr), "cf_conv_mfma")
         self.last_nnz = nnz
         self.last_numel = p.numel
         if not want_v_out:
@@ -2033,7 +2069,7 @@ class _PairPlan:
     """What run_halo_pair decides from an input signature alone
     (halo_pair_repeat): the copy format, the partner, the static launch
     arguments and, per conv, a _DensePlan of its outputs."""
-    __slots__ = ("rb", "rb_key", "u8", "fn", "numel", "head", "halves")
+    __slots__ = ("rb", "rb_key", "u8", "fn", "numel", "head", "halves", "args", "args_addr")
 
 
 def _halo_pair_plan(ra, rb, x, xp, meta):
@@ -2078,6 +2114,23 @@ def _halo_pair_plan(ra, rb, x, xp, meta):
         h.tail = (r.Cout, r.Coutp, r.padding)
         halves.append((r, h))
     p.halves = tuple(halves)
+    p.args = p.args_addr = None
+    if not u8:
+        # the cf_conv_halo_pair_args block, static fields filled
+        p.fn = _hip.lib().cf_conv_halo_pair_args
+        a = _hip.ConvHaloPairArgs()
+        a.numel, a.T, a.B, a.Cp, a.H, a.W, a.Ho, a.Wo = p.head
+        for sfx, (r, h) in zip(("_a", "_b"), halves):
+            for f, v in zip(("w", "alpha", "beta"), h.weights):
+                setattr(a, f + sfx, v)
+            setattr(a, "v_in" + sfx, None)
+            setattr(a, "cp_out" + sfx, h.cp_out)
+            setattr(a, "nz" + sfx, h.nz_ptr)
+            for f, v in zip(("Cout", "Coutp", "pad"), h.tail):
+                setattr(a, f + sfx, v)
+        a.tau, a.v_th, a.v_reset, a.hard_reset, a.decay_input = ra.lif
+        p.args = a
+        p.args_addr = ctypes.addressof(a)
     return p
 
 
@@ -2107,14 +2160,27 @@ def halo_pair_repeat(ra, rb, x):
     elide = COPY_ELISION and (nnz is not None or x_desc is not None)
     res = []
     args = []
-    for r, h in p.halves:
+    a = p.args
+    for sfx, (r, h) in zip(("_a", "_b"), p.halves):
         out, v_out, nhwc, desc, info, v_chan = r._plan_outputs(h, dev, elide)
         res.append((out, v_out, v_chan, desc, h.vmeta))
-        args += [*h.weights, None, v_out.data_ptr(), nhwc.data_ptr(), h.cp_out, h.nz_ptr,
-                 desc.data_ptr() if desc is not None else None, info, *h.tail]
-    check(p.fn(xp.data_ptr(), nnz.data_ptr() if nnz is not None else None,
-               x_desc.data_ptr() if x_desc is not None else None, *p.head, *args, *ra.lif,
-               _hip.stream(dev)), "cf_conv_halo_pair")
+        dp = desc.data_ptr() if desc is not None else None
+        if a is not None:
+            setattr(a, "v_out" + sfx, v_out.data_ptr())
+            setattr(a, "out" + sfx, nhwc.data_ptr())
+            setattr(a, "desc" + sfx, dp)
+            setattr(a, "bias_info" + sfx, info)
+        else:
+            args += [*h.weights, None, v_out.data_ptr(), nhwc.data_ptr(), h.cp_out, h.nz_ptr, dp,
+                     info, *h.tail]
+    xd = x_desc.data_ptr() if x_desc is not None else None
+    nn = nnz.data_ptr() if nnz is not None else None
+    if a is not None:
+        a.x, a.nnz, a.x_desc, a.stream = xp.data_ptr(), nn, xd, _hip.stream(dev)
+        check(p.fn(p.args_addr), "cf_conv_halo_pair")
+    else:
+        check(p.fn(xp.data_ptr(), nn, xd, *p.head, *args, *ra.lif, _hip.stream(dev)),
+              "cf_conv_halo_pair")
     for r in (ra, rb):
         r.last_nnz = nnz
         r.last_numel = p.numel

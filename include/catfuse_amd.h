@@ -425,6 +425,115 @@ int cf_conv_halo_pair(const void* x, const unsigned long long* nnz, const void* 
                       double tau, double v_th, double v_reset, int hard_reset, int decay_input,
                       void* stream);
 
+/* cf_conv_mfma's and cf_conv_halo_pair's arguments as one block each, in
+ * the order of their parameters, every field 8 bytes (the int parameters
+ * as int64_t): the same launches for a caller whose per-call conversion of
+ * 48 separate arguments costs more than the launch itself (a Python ctypes
+ * binding re-filling a few fields of a block it keeps per layer).  No
+ * counterpart in the reference (its Triton launches take Python arguments).
+ * cf_conv_args_sizes writes sizeof of both blocks (sizes[0], sizes[1]) for
+ * a binding to check its mirror of the layout. */
+typedef struct CfConvMfmaArgs {
+  const void* x;
+  const void* w_packed;
+  const float* alpha;
+  const float* beta;
+  const float* v_in;
+  float* v_out;
+  float* out;
+  void* out_nhwc;
+  int64_t cp_out;
+  const float* identity;
+  const void* identity_nhwc;
+  int64_t cp_id;
+  int64_t identity_mode;
+  const int32_t* ag_mask;
+  const int32_t* tile_order;
+  const unsigned long long* nnz;
+  unsigned long long* nz_out;
+  const void* x_desc;
+  const void* id_desc;
+  void* out_desc;
+  int64_t bias_info;
+  const unsigned long long* id_nnz;
+  int64_t numel;
+  double sparse_threshold;
+  int64_t T;
+  int64_t B;
+  int64_t Cp;
+  int64_t Cout;
+  int64_t Coutp;
+  int64_t H;
+  int64_t W;
+  int64_t Ho;
+  int64_t Wo;
+  int64_t KH;
+  int64_t KW;
+  int64_t stride;
+  int64_t pad;
+  int64_t x_img_tstride;
+  int64_t tile_h;
+  int64_t tile_w;
+  int64_t group_size;
+  int64_t epilogue;
+  double tau;
+  double v_th;
+  double v_reset;
+  int64_t hard_reset;
+  int64_t decay_input;
+  void* stream;
+} CfConvMfmaArgs;
+
+typedef struct CfConvHaloPairArgs {
+  const void* x;
+  const unsigned long long* nnz;
+  const void* x_desc;
+  int64_t numel;
+  int64_t T;
+  int64_t B;
+  int64_t Cp;
+  int64_t H;
+  int64_t W;
+  int64_t Ho;
+  int64_t Wo;
+  const void* w_a;
+  const float* alpha_a;
+  const float* beta_a;
+  const float* v_in_a;
+  float* v_out_a;
+  void* out_a;
+  int64_t cp_out_a;
+  unsigned long long* nz_a;
+  void* desc_a;
+  int64_t bias_info_a;
+  int64_t Cout_a;
+  int64_t Coutp_a;
+  int64_t pad_a;
+  const void* w_b;
+  const float* alpha_b;
+  const float* beta_b;
+  const float* v_in_b;
+  float* v_out_b;
+  void* out_b;
+  int64_t cp_out_b;
+  unsigned long long* nz_b;
+  void* desc_b;
+  int64_t bias_info_b;
+  int64_t Cout_b;
+  int64_t Coutp_b;
+  int64_t pad_b;
+  double tau;
+  double v_th;
+  double v_reset;
+  int64_t hard_reset;
+  int64_t decay_input;
+  void* stream;
+} CfConvHaloPairArgs;
+
+int cf_conv_mfma_args(const CfConvMfmaArgs* args);
+int cf_conv_halo_pair_args(const CfConvHaloPairArgs* args);
+int cf_conv_args_sizes(int64_t* sizes);
+
 /* One-byte spike copies between fused layers.  The _u8 entry points take
  * and write NHWC copies of one byte per channel ([T*B][H][W][cp] uint8, the
  * same element layout as the fp16 copies, channels >= C zero): the spike

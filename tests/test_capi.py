@@ -216,3 +216,33 @@ def test_token_and_pool_entry_points_validate_arguments():
     assert pool(cp=12) == INVALID                   # 16-byte channel chunks
     assert pool(k=2, p=2) == INVALID                # padding beyond half the window
     assert pool(s=0) == INVALID
+
+
+def _header_struct_fields(name):
+    text = open(HEADER).read()
+    m = re.search(r"typedef struct " + name + r" \{(.*?)\} " + name + ";", text, re.S)
+    assert m, name
+    return [re.findall(r"(\w+);", line)[0] for line in m.group(1).strip().splitlines()
+            if line.strip()]
+
+
+@pytest.mark.parametrize("cname, pyname", [("CfConvMfmaArgs", "ConvMfmaArgs"),
+                                           ("CfConvHaloPairArgs", "ConvHaloPairArgs")])
+def test_argument_blocks_mirror_the_header(cname, pyname):
+    """The ctypes mirrors of the argument blocks have the header's fields in
+    the header's order, every one 8 bytes, and the library's sizeof."""
+    from catfuse_amd import _hip
+    st = getattr(_hip, pyname)
+    assert [f for f, _ in st._fields_] == _header_struct_fields(cname)
+    assert all(ctypes.sizeof(t) == 8 for _, t in st._fields_)
+    sizes = (ctypes.c_int64 * 2)()
+    assert _hip.lib().cf_conv_args_sizes(ctypes.addressof(sizes)) == 0
+    assert ctypes.sizeof(st) == sizes[0 if cname == "CfConvMfmaArgs" else 1]
+    assert ctypes.sizeof(st) == 8 * len(st._fields_)
+
+
+def test_argument_block_entry_points_reject_null():
+    from catfuse_amd import _hip
+    assert _hip.lib().cf_conv_mfma_args(None) == INVALID
+    assert _hip.lib().cf_conv_halo_pair_args(None) == INVALID
+    assert _hip.lib().cf_conv_args_sizes(None) == INVALID
