@@ -124,10 +124,11 @@ def label_launches(model, timer):
 
 
 def time_forward(fused, x, img, steps, warmup, eager=False, label=False):
-    """Warm-up, an eager pass of `steps` forwards with HIP events around
-    every launch (per-kernel times; the same kernels the graph replays),
-    then (unless eager) `steps` replays of the captured graph.  Returns
-    dict(ms, ms_eager, mode, timer, spans)."""
+    """Warm-up, three timed eager passes of `steps` forwards (their median is
+    ms_eager), an eager pass with HIP events around every launch (per-kernel
+    times; the same kernels the graph replays), then (unless eager) `steps`
+    replays of the captured graph.  Returns dict(ms, ms_eager, mode, timer,
+    spans)."""
     import torch
     import catfuse_amd
     from catfuse_amd import graph as cf_graph
@@ -139,13 +140,19 @@ def time_forward(fused, x, img, steps, warmup, eager=False, label=False):
             fused(x)
         torch.cuda.synchronize()
         catfuse_amd.check_status(dev)
-        t0 = time.perf_counter()
-        for _ in range(steps):
-            snn.functional.reset_net(fused)
-            y = fused(x)
-        torch.cuda.synchronize()
-        t1 = time.perf_counter()
-        ms_eager = (t1 - t0) * 1e3 / steps
+        # eager: the median of three passes of `steps` forwards (the host
+        # launches them, so a pass also measures the host's other load)
+        passes = []
+        for _ in range(3):
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                snn.functional.reset_net(fused)
+                y = fused(x)
+            torch.cuda.synchronize()
+            t1 = time.perf_counter()
+            passes.append((t1 - t0) * 1e3 / steps)
+        ms_eager = sorted(passes)[1]
         # per-launch times: a second eager pass with the GPU kept busy ahead
         # of every launch, so each event pair brackets the kernel alone
         timer = runtime.KernelTimer(settle_cycles=SETTLE_CYCLES)
