@@ -30,7 +30,7 @@ class HipConvImplementation(Implementation):
 
     def runner(self, spec, params, device) -> ConvLIFRunner:
         key = (id(params.weight), id(params.bias), id(params.bn_scale), id(params.bn_bias),
-               torch.device(device))
+               device if type(device) is torch.device else torch.device(device))
         if self._runner_key != key:
             self._runner = ConvLIFRunner(
                 params.weight,

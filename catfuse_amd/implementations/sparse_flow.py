@@ -88,14 +88,15 @@ class SparseFlow(HipConvImplementation):
 
     def forward(self, x, spec, params, state):
         self.check_input(x, spec)
-        B = x.shape[1]
-        Ho, Wo = spec.output_hw(x.shape[3], x.shape[4])
-        r = self.runner(spec, params, x.device)
-        v_in = state.peek((B, spec.out_channels, Ho, Wo), x.device)
+        _, B, _, H, W = x.shape
+        dev = x.device
+        Ho, Wo = spec.output_hw(H, W)
+        r = self.runner(spec, params, dev)
+        v_in = state.peek((B, spec.out_channels, Ho, Wo), dev)
         if self.input_is_analog(x):
             spikes, v_out = r.run_direct(x, v_in, emit_nhwc=True)
         else:
-            sparse = self.route_geometry(spec, x.shape[3], x.shape[4])
+            sparse = self.route_geometry(spec, H, W)
             spikes, v_out = r.run_mfma(x.contiguous(), v_in, sparse=sparse,
                                        sparse_threshold=self.sparsity_threshold)
         state.set(v_out)

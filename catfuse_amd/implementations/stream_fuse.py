@@ -52,10 +52,11 @@ class StreamFuse(HipConvImplementation):
 
     def forward(self, x, spec, params, state, identity=None, identity_mode=ID_ADD_SPIKE):
         self.check_input(x, spec)
-        B = x.shape[1]
-        Ho, Wo = spec.output_hw(x.shape[3], x.shape[4])
-        r = self.runner(spec, params, x.device)
-        v_in = state.peek((B, spec.out_channels, Ho, Wo), x.device)
+        _, B, _, H, W = x.shape
+        dev = x.device
+        Ho, Wo = spec.output_hw(H, W)
+        r = self.runner(spec, params, dev)
+        v_in = state.peek((B, spec.out_channels, Ho, Wo), dev)
         if self.input_is_analog(x):
             if identity is not None:
                 raise NotImplementedError("identity epilogue needs fp16-exact inputs")

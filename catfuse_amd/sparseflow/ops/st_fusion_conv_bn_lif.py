@@ -121,15 +121,16 @@ class STFusionConvBNLIF(CTFPattern):
 
     def _forward_identity(self, impl, x, params, identity):
         if isinstance(impl, SparseFlow):
-            B = x.shape[1]
-            Ho, Wo = self.spec.output_hw(x.shape[3], x.shape[4])
-            r = impl.runner(self.spec, params, x.device)
-            v_in = self.state.peek((B, self.out_channels, Ho, Wo), x.device)
+            _, B, _, H, W = x.shape
+            dev = x.device
+            Ho, Wo = self.spec.output_hw(H, W)
+            r = impl.runner(self.spec, params, dev)
+            v_in = self.state.peek((B, self.out_channels, Ho, Wo), dev)
             if impl.input_is_analog(x):
                 spikes, v_out = r.run_direct(x, v_in)
                 spikes = identity + spikes
             else:
-                sparse = impl.route_geometry(self.spec, x.shape[3], x.shape[4])
+                sparse = impl.route_geometry(self.spec, H, W)
                 spikes, v_out = r.run_mfma(x.contiguous(), v_in, identity=identity.contiguous(),
                                            identity_mode=ID_ADD_SPIKE, sparse=sparse,
                                            sparse_threshold=impl.sparsity_threshold)
